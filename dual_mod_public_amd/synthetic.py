@@ -1,0 +1,64 @@
+"""Seeded synthetic weights and inputs for the benchmark configurations.
+
+Weights use the reference's parameter names (models/dualmod/attention.py:100-202,
+models/dualmod/model.py:118-121) so a state dict made here loads into either
+implementation. Every draw comes from ``numpy.random.default_rng(seed)`` in the
+fixed order of ``param_specs`` — platform-independent, so the CPU oracle, the
+golden-vector script and the GPU run all see identical numbers.
+
+Distribution (all configs): every matrix N(0, std=0.02), including w_kctx,
+w_vctx and v_map so the mult_res branch is live; gate biases and the v_gate
+bias N(0, 0.02) (gates open, sigma ~ 0.5); RMSNorm weights 1; per-head gains 1.
+"""
+
+from collections import OrderedDict
+
+import numpy as np
+import torch
+
+
+def param_specs(cfg, with_attn_norm=True):
+    """Ordered (name, shape, kind) of one DM attention layer's parameters."""
+    d = cfg.d_model
+    h = cfg.n_heads
+    mod = getattr(cfg, "ctx_mod", "linear")
+    specs = [("wq.weight", (d, d), "w"), ("wk.weight", (d, d), "w"),
+             ("wv.weight", (d, d), "w"), ("wo.weight", (d, d), "w")]
+    if getattr(cfg, "v_norm", "none") == "rms":
+        specs.append(("v_gain", (h,), "one"))
+    if cfg.enable_key_mod:
+        specs += [("w_kctx.weight", (d, d), "w"), ("w_gk.weight", (d, 2 * d), "w"),
+                  ("w_gk.bias", (d,), "b")]
+        if getattr(cfg, "k_ctx_norm", "none") == "rms":
+            specs.append(("k_gain", (h,), "one"))
+    if cfg.enable_value_mod:
+        specs += [("w_vctx.weight", (d, d), "w"), ("w_gv.weight", (d, 2 * d), "w"),
+                  ("w_gv.bias", (d,), "b")]
+        if getattr(cfg, "v_ctx_norm", "none") == "rms":
+            specs.append(("ctx_gain", (h,), "one"))
+    if mod in ("mult", "mult_res"):
+        specs += [("v_gate.weight", (d, d), "w"), ("v_gate.bias", (d,), "b"),
+                  ("v_map.weight", (d, d), "w")]
+    if cfg.enable_key_mod or cfg.enable_value_mod:
+        specs.append(("norm_ctx.weight", (d,), "one"))
+    if with_attn_norm:
+        specs.append(("attn_norm.weight", (d,), "one"))
+    return specs
+
+
+def make_state_dict(cfg, seed=0, std=0.02, dtype=torch.float32, with_attn_norm=True):
+    rng = np.random.default_rng(seed)
+    sd = OrderedDict()
+    for name, shape, kind in param_specs(cfg, with_attn_norm):
+        if kind == "one":
+            a = np.ones(shape, dtype=np.float64)
+        else:
+            a = rng.normal(0.0, std, size=shape)
+        sd[name] = torch.from_numpy(a).to(dtype)
+    return sd
+
+
+def make_input(shape, seed=1, dtype=torch.float32, scale=1.0):
+    """x ~ N(0, scale^2) of the given shape (float64 draw, cast)."""
+    rng = np.random.default_rng(seed)
+    return torch.from_numpy(rng.normal(0.0, scale, size=shape)).to(dtype)

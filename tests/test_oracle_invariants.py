@@ -1,0 +1,199 @@
+"""Invariants that pin the oracle independently of the golden vectors.
+
+Re-states the reference's relational tests on the CPU restatement:
+T1/T2 (tests/test_dualmod_equivalence.py:57-93) reduce to torch's SDPA,
+T3 decode == teacher forcing (:98-112), T5 causality (:153-164),
+T-K2 chunked == exact for K=c (engines/wavescan/tests/test_k1_k9.py:87-109),
+T-K3 nilpotency + frontier (:114-137), T-K9 RoPE pairing (:142-152), and the
+special case v_map = 0, lambda = 1 (mult_res reduces to linear).
+"""
+
+import pytest
+import torch
+
+import oracle as O
+from dual_mod_public_amd.config import DualModConfig
+from dual_mod_public_amd.synthetic import make_input, make_state_dict
+from tests.conftest import relerr
+
+D = torch.float64
+TOL = 1e-10       # fp64: relations hold to rounding
+
+
+def _cfg(**kw):
+    base = dict(d_model=64, n_layers=1, n_heads=4, max_seq_len=48, checkpoint_chunk=0,
+                dtype="fp32", ctx_mod="mult_res")
+    base.update(kw)
+    return DualModConfig(**base)
+
+
+def _setup(cfg, B=2, T=24, seed=5):
+    sd = {k: v.to(D) for k, v in make_state_dict(cfg, seed=seed, std=0.05).items()}
+    cos, sin = O.build_rope_cache(cfg.max_seq_len, cfg.head_dim, cfg.rope_theta, dtype=D)
+    x = make_input((B, T, cfg.d_model), seed=seed + 1, dtype=D)
+    return sd, cos[:T], sin[:T], x
+
+
+def test_t1_mods_off_is_vanilla():
+    cfg = _cfg(enable_key_mod=False, enable_value_mod=False)
+    sd, cos, sin, x = _setup(cfg)
+    with torch.no_grad():
+        a = O.sequential_scan(cfg, sd, x, cos, sin)
+        b = O.vanilla_attention(cfg, sd, x, cos, sin)
+    assert relerr(a, b) < TOL
+
+
+@pytest.mark.parametrize("mod", ["linear", "mult_res"])
+def test_t2_gates_closed_is_vanilla(mod):
+    cfg = _cfg(ctx_mod=mod)
+    sd, cos, sin, x = _setup(cfg)
+    for g in ("w_gk", "w_gv"):
+        sd[g + ".bias"].fill_(40.0)
+        sd[g + ".weight"].zero_()
+    sd["w_kctx.weight"].normal_(0, 0.5)
+    sd["w_vctx.weight"].normal_(0, 0.5)
+    with torch.no_grad():
+        a = O.sequential_scan(cfg, sd, x, cos, sin)
+        b = O.vanilla_attention(cfg, sd, x, cos, sin)
+    assert relerr(a, b) < TOL
+
+
+def test_t2_gates_open_is_not_vanilla():
+    cfg = _cfg()
+    sd, cos, sin, x = _setup(cfg)
+    with torch.no_grad():
+        a = O.sequential_scan(cfg, sd, x, cos, sin)
+        b = O.vanilla_attention(cfg, sd, x, cos, sin)
+    assert relerr(a, b) > 1e-3
+
+
+@pytest.mark.parametrize("mod", ["linear", "mult_res"])
+def test_t3_decode_is_teacher_forced(mod):
+    cfg = _cfg(ctx_mod=mod)
+    sd, cos, sin, x = _setup(cfg)
+    T = x.shape[1]
+    with torch.no_grad():
+        o_tf, K_tf, V_tf = O.sequential_scan(cfg, sd, x, cos, sin, return_cache=True)
+        cache = {"K": None, "V": None}
+        o_dec = torch.cat([O.decode_step(cfg, sd, x[:, t:t + 1], t, cache, cos, sin)[0]
+                           for t in range(T)], 1)
+        Kb = torch.zeros(x.shape[0], cfg.n_heads, T, cfg.head_dim, dtype=D)
+        Vb = torch.zeros_like(Kb)
+        o_st = torch.cat([O.static_decode_step(cfg, sd, x[:, t:t + 1], t, Kb, Vb, cos, sin)
+                          for t in range(T)], 1)
+    assert relerr(o_dec, o_tf) < TOL
+    assert relerr(cache["K"], K_tf) < TOL and relerr(cache["V"], V_tf) < TOL
+    assert relerr(o_st, o_tf) < TOL
+    assert relerr(Kb, K_tf) < TOL and relerr(Vb, V_tf) < TOL
+
+
+def test_t5_causality():
+    cfg = _cfg()
+    sd, cos, sin, x = _setup(cfg, T=16)
+    x = x.clone().requires_grad_(True)
+    t = 7
+    y = O.dm_layer(cfg, sd, x, cos, sin)
+    (g,) = torch.autograd.grad(y[:, t].sum(), x)
+    assert g[:, t + 1:].abs().max().item() == 0.0
+    assert g[:, :t + 1].abs().max().item() > 0.0
+
+
+@pytest.mark.parametrize("sched_fn", [
+    lambda T: O.exact_sequential(T),
+    lambda T: O.uniform_chunks(T, 4),
+    lambda T: O.uniform_chunks(T, 8),
+    lambda T: [(0, 3, 3)] + [(p + 3, c, c) for p, c, _ in O.uniform_chunks(T - 3, 8)],
+])
+def test_k2_chunked_exact_equals_scan(sched_fn):
+    cfg = _cfg()
+    sd, cos, sin, x = _setup(cfg, T=40)
+    sched = sched_fn(40)
+    assert sum(c for _, c, _ in sched) == 40
+    with torch.no_grad():
+        o, K, V = O.layer_forward(cfg, sd, x, cos, sin, sched)
+        o_ref, K_ref, V_ref = O.sequential_scan(cfg, sd, x, cos, sin, return_cache=True)
+    assert relerr(o, o_ref) < TOL
+    assert relerr(K, K_ref) < TOL and relerr(V, V_ref) < TOL
+
+
+@pytest.mark.parametrize("c", [4, 8, 16])
+def test_k3_nilpotency_and_frontier(c):
+    cfg = _cfg()
+    a = 12
+    sd, cos, sin, x = _setup(cfg, T=a + c, seed=9)
+    with torch.no_grad():
+        _, K_all, V_all = O.sequential_scan(cfg, sd, x, cos, sin, return_cache=True)
+        o_all = O.sequential_scan(cfg, sd, x, cos, sin)
+        K_comm, V_comm = K_all[:, :, :a], V_all[:, :, :a]
+        for s in range(1, c + 1):
+            o_s, K_s, V_s = O.chunk_cell_forward(cfg, sd, x[:, a:], cos[a:], sin[a:],
+                                                 K_comm, V_comm, s)
+            assert relerr(o_s[:, :s], o_all[:, a:a + s]) < TOL
+            assert relerr(K_s[:, :, :s], K_all[:, :, a:a + s]) < TOL
+            if s <= c // 4:   # rows beyond the early frontier are still approximate
+                assert relerr(o_s[:, s:], o_all[:, a + s:]) > 1e-12
+    assert relerr(o_s, o_all[:, a:]) < TOL
+    assert relerr(V_s, V_all[:, :, a:]) < TOL
+
+
+def test_k9_rope_pairing():
+    dh = 16
+    cos, sin = O.build_rope_cache(8, dh, 10000.0)
+    for i in range(dh // 2):
+        e = torch.zeros(1, 1, 1, dh)
+        e[..., i] = 1.0
+        r = O.apply_rope(e, cos[3:4], sin[3:4])
+        moved = set((r[0, 0, 0] != 0).nonzero().flatten().tolist())
+        assert moved <= {i, i + dh // 2}
+        # rotation preserves the norm
+        assert abs(r.norm().item() - 1.0) < 1e-6
+
+
+def test_rope_closed_form():
+    # position p, pair i: angle p * theta^(-2i/dh)
+    cos, sin = O.build_rope_cache(10, 8, 10000.0, dtype=D)
+    for p in (0, 1, 9):
+        for i in range(4):
+            ang = p * 10000.0 ** (-2 * i / 8)
+            assert abs(cos[p, i].item() - torch.cos(torch.tensor(ang, dtype=D)).item()) < 1e-12
+            assert abs(sin[p, i].item() - torch.sin(torch.tensor(ang, dtype=D)).item()) < 1e-12
+
+
+def test_rms_norm_closed_form():
+    x = torch.tensor([[3.0, 4.0]], dtype=D)
+    w = torch.tensor([1.0, 2.0], dtype=D)
+    y = O.rms_norm(x, w, eps=0.0)
+    r = (12.5) ** -0.5
+    assert torch.allclose(y, torch.tensor([[3 * r, 8 * r]], dtype=D))
+
+
+def test_mult_res_with_zero_map_is_linear():
+    """v_map = 0 => tanh(0) = 0 => v_in = lambda*u; lambda = 1 => linear."""
+    cfg_m = _cfg(ctx_mod="mult_res")
+    cfg_l = _cfg(ctx_mod="linear")
+    sd, cos, sin, x = _setup(cfg_m)
+    sd["v_map.weight"].zero_()
+    sd_l = {k: v for k, v in sd.items() if not k.startswith(("v_map", "v_gate"))}
+    with torch.no_grad():
+        a = O.sequential_scan(cfg_m, sd, x, cos, sin)
+        b = O.sequential_scan(cfg_l, sd_l, x, cos, sin)
+    assert relerr(a, b) < TOL
+
+
+def test_attend_one_brute_force():
+    """attend_one against a scalar softmax written out per key (tiny)."""
+    cfg = _cfg()
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, 1, 1, 4, generator=g, dtype=D)
+    ks = torch.randn(1, 1, 1, 4, generator=g, dtype=D)
+    vs = torch.randn(1, 1, 1, 4, generator=g, dtype=D)
+    K = torch.randn(1, 1, 3, 4, generator=g, dtype=D)
+    V = torch.randn(1, 1, 3, 4, generator=g, dtype=D)
+    o = O.attend_one(cfg, q, ks, vs, K, V)[0, 0, 0]
+    keys = [K[0, 0, i] for i in range(3)] + [ks[0, 0, 0]]
+    vals = [V[0, 0, i] for i in range(3)] + [vs[0, 0, 0]]
+    sc = [float((q[0, 0, 0] * k).sum()) / 2.0 for k in keys]
+    import math
+    e = [math.exp(s - max(sc)) for s in sc]
+    ref = sum(ei * v for ei, v in zip(e, vals)) / sum(e)
+    assert torch.allclose(o, ref, atol=1e-12)
