@@ -1,0 +1,160 @@
+"""ctypes binding of libdm_hip.so (the C ABI in include/dm_abi.h).
+
+The library is loaded from the package directory. There is no fallback:
+if it is missing or fails to load, every compute entry point raises.
+Tensors cross the boundary as raw device pointers; the stream is torch's
+current HIP stream.
+"""
+
+import ctypes
+import os
+
+import torch
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libdm_hip.so")
+
+DM_F32, DM_BF16 = 0, 1
+CTX_MOD = {"linear": 0, "mult_res": 1, "mult": 2}
+
+c_i32 = ctypes.c_int32
+c_vp = ctypes.c_void_p
+c_fp = ctypes.c_void_p
+
+
+class dm_config(ctypes.Structure):
+    _fields_ = [("dtype", c_i32), ("B", c_i32), ("d", c_i32), ("h", c_i32), ("dh", c_i32),
+                ("ctx_mod", c_i32), ("mult_res_lambda", ctypes.c_float), ("rms_eps", ctypes.c_float),
+                ("local_window", c_i32), ("reserved", c_i32 * 7)]
+
+
+class dm_params(ctypes.Structure):
+    _fields_ = [(n, c_vp) for n in ("wq", "wk", "wv", "wo", "w_kctx", "w_vctx", "w_gk", "w_gv",
+                                    "b_gk", "b_gv", "v_gate", "b_vgate", "v_map", "norm_ctx_w",
+                                    "attn_norm_w")]
+
+
+class dm_packed(ctypes.Structure):
+    _fields_ = [(n, c_vp) for n in ("w_proj", "b_proj", "w_sweep", "w_vctx", "norm_ctx_w",
+                                    "attn_norm_w", "wo")]
+
+
+class dm_layer_bufs(ctypes.Structure):
+    _fields_ = [("T", c_i32), ("xhat", c_vp), ("qr", c_vp), ("kraw", c_vp), ("kself", c_vp),
+                ("vraw", c_vp), ("glogx", c_vp), ("sig", c_vp)]
+
+
+class dm_cell_args(ctypes.Structure):
+    _fields_ = [("pos0", c_i32), ("c", c_i32), ("n_sweeps", c_i32), ("cache_T", c_i32),
+                ("K_cache", c_vp), ("V_cache", c_vp), ("ocat", c_vp), ("o_last", c_vp),
+                ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t)]
+
+
+class dm_decode_args(ctypes.Structure):
+    _fields_ = [("pos", c_i32), ("tape_T", c_i32), ("xhat", c_vp), ("K_tape", c_vp),
+                ("V_tape", c_vp), ("o_cat", c_vp), ("y", c_vp), ("workspace", c_vp),
+                ("workspace_bytes", ctypes.c_size_t)]
+
+
+P = ctypes.POINTER
+
+# name -> (restype, argtypes); every symbol include/dm_abi.h declares
+SIGNATURES = {
+    "dm_abi_version": (ctypes.c_int, []),
+    "dm_last_error": (ctypes.c_char_p, []),
+    "dm_pack_weights": (ctypes.c_int, [P(dm_config), P(dm_params), P(dm_packed), c_vp]),
+    "dm_layer_proj": (ctypes.c_int, [P(dm_config), P(dm_packed), c_vp, c_fp, c_fp,
+                                     P(dm_layer_bufs), c_vp]),
+    "dm_cell_workspace_bytes": (ctypes.c_size_t, [P(dm_config), c_i32]),
+    "dm_cell_fwd": (ctypes.c_int, [P(dm_config), P(dm_packed), P(dm_layer_bufs), c_fp, c_fp,
+                                   P(dm_cell_args), c_vp]),
+    "dm_layer_fwd": (ctypes.c_int, [P(dm_config), P(dm_packed), c_vp, c_vp, c_fp, c_fp,
+                                    P(dm_layer_bufs), P(c_i32), c_i32, c_vp, c_vp, c_i32, c_vp,
+                                    c_vp, ctypes.c_size_t, c_vp]),
+    "dm_decode_workspace_bytes": (ctypes.c_size_t, [P(dm_config), c_i32]),
+    "dm_decode_step": (ctypes.c_int, [P(dm_config), P(dm_packed), c_fp, c_fp,
+                                      P(dm_decode_args), c_vp]),
+    "dm_linear": (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp]),
+    "dm_gemm_nt": (ctypes.c_int, [c_i32, c_vp, c_vp, c_fp, c_i32, c_i32, c_i32, c_vp]),
+}
+
+_lib = None
+_lib_err = None
+
+
+def load(path=LIB_PATH):
+    """Load libdm_hip.so and bind every declared symbol (no GPU needed)."""
+    global _lib, _lib_err
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        _lib_err = f"{path} not built (run dual_mod_public_amd._build.build())"
+        raise RuntimeError(_lib_err)
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def lib():
+    return _lib if _lib is not None else load()
+
+
+class DMError(RuntimeError):
+    pass
+
+
+def check(rc):
+    if rc != 0:
+        msg = lib().dm_last_error().decode(errors="replace")
+        raise DMError(f"libdm_hip error {rc}: {msg}")
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream_ptr():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def dtype_code(dt):
+    if dt == torch.float32:
+        return DM_F32
+    if dt == torch.bfloat16:
+        return DM_BF16
+    raise NotImplementedError(f"storage dtype {dt} (fp32 or bf16)")
+
+
+def linear(x, W, residual=None, out=None):
+    """y = x W^T (+ residual) through dm_linear; x [..., K], W [N, K]."""
+    K = x.shape[-1]
+    N = W.shape[0]
+    x2 = x.reshape(-1, K).contiguous()
+    W = W.to(dtype=x.dtype).contiguous()
+    y = out if out is not None else torch.empty(*x.shape[:-1], N, device=x.device, dtype=x.dtype)
+    r = residual.reshape(-1, N).contiguous() if residual is not None else None
+    check(lib().dm_linear(dtype_code(x.dtype), ptr(x2), ptr(W), ptr(r), ptr(y), x2.shape[0], N, K,
+                          stream_ptr()))
+    return y
+
+
+def make_config(cfg, B, dtype):
+    """dm_config from a DualModConfig (the knob subset the ABI carries)."""
+    c = dm_config()
+    c.dtype = dtype_code(dtype)
+    c.B = B
+    c.d = cfg.d_model
+    c.h = cfg.n_heads
+    c.dh = cfg.head_dim
+    c.ctx_mod = CTX_MOD[cfg.ctx_mod]
+    c.mult_res_lambda = float(getattr(cfg, "mult_res_lambda", 1.0))
+    c.rms_eps = 1e-5
+    c.local_window = int(getattr(cfg, "local_window", 0) or 0)
+    return c

@@ -1,0 +1,114 @@
+"""DualModAttention on the HIP path — same parameters and call signatures as
+models/dualmod/attention.py:86-588, so reference state dicts load unchanged.
+
+``forward`` runs the exact chunked scan (K = c per chunk, equal to the
+sequential scan by nilpotency, scan_cell_fwd.py:1-10) in libdm_hip.so;
+``decode_step`` runs the static-tape decode kernels. Knobs outside the HIP
+path's set raise NotImplementedError at construction (engine.check_supported).
+"""
+
+import math
+
+import torch
+import torch.nn as nn
+
+from . import _lib as L
+from .config import DualModConfig
+from .engine import HipSweepCell, check_supported, uniform_chunks
+
+
+class RMSNorm(nn.Module):
+    """attention.py:74-83 (parameter container; the kernels apply it)."""
+
+    def __init__(self, d, eps=1e-5):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(d))
+        self.eps = eps
+
+
+class DualModAttention(nn.Module):
+    CHUNK = 64   # chunk length of the exact forward (cells of K = c sweeps)
+
+    def __init__(self, cfg: DualModConfig):
+        super().__init__()
+        check_supported(cfg)
+        self.cfg = cfg
+        d = cfg.d_model
+        self.n_heads = cfg.n_heads
+        self.head_dim = cfg.head_dim
+        self.scale = 1.0 / math.sqrt(cfg.head_dim)
+        self.wq = nn.Linear(d, d, bias=False)
+        self.wk = nn.Linear(d, d, bias=False)
+        self.wv = nn.Linear(d, d, bias=False)
+        self.wo = nn.Linear(d, d, bias=False)
+        self.w_kctx = nn.Linear(d, d, bias=False)
+        self.w_gk = nn.Linear(2 * d, d, bias=True)
+        self.w_vctx = nn.Linear(d, d, bias=False)
+        self.w_gv = nn.Linear(2 * d, d, bias=True)
+        if cfg.ctx_mod in ("mult", "mult_res"):
+            self.v_gate = nn.Linear(d, d, bias=True)
+            self.v_map = nn.Linear(d, d, bias=False)
+        self.norm_ctx = RMSNorm(d)
+        self._cells = {}
+        self._packed_version = None
+
+    # ---- HIP cell cache --------------------------------------------------------
+    def _param_version(self):
+        return tuple((p.data_ptr(), p._version) for p in self.parameters())
+
+    def _hip_cell(self, B, cache_T, dtype):
+        key = (B, cache_T, dtype)
+        cell = self._cells.get(key)
+        ver = self._param_version()
+        if cell is None:
+            dev = self.wq.weight.device
+            cell = HipSweepCell(self.cfg, B, cache_T, device=dev, dtype=dtype)
+            self._cells[key] = cell
+            cell._ver = None
+        if cell._ver != ver:
+            cell.pack(dict(self.named_parameters()))
+            cell._ver = ver
+        return cell
+
+    # ---- full-sequence forward (attention.py:438-447, mode "sequential") --------
+    @torch.no_grad()
+    def forward(self, xhat, cos, sin, collect=None):
+        """xhat [B,T,d] pre-normed; cos/sin rows 0..T-1. Returns W_O o_cat [B,T,d]."""
+        if collect is not None:
+            raise NotImplementedError("telemetry collection is not supported on the HIP path")
+        B, T, d = xhat.shape
+        xhat = xhat.contiguous()
+        cell = self._hip_cell(B, T, xhat.dtype)
+        bufs = cell.new_bufs(T)
+        cell.layer_proj(xhat, bufs, cos[:T], sin[:T], normalize=False)
+        K = torch.empty(B, self.n_heads, T, self.head_dim, device=xhat.device, dtype=xhat.dtype)
+        V = torch.empty_like(K)
+        ocat = torch.empty(B, T, d, device=xhat.device, dtype=xhat.dtype)
+        for pos0, c, k in uniform_chunks(T, self.CHUNK):
+            cell.cell_forward(bufs, cos[:T], sin[:T], K, V, pos0, c, k, ocat=ocat)
+        return L.linear(ocat, self.wo.weight)
+
+    # ---- incremental decode (attention.py:564-588) ------------------------------
+    @torch.no_grad()
+    def decode_step(self, xhat_j, pos, cache, cos, sin):
+        """One token at absolute position ``pos``; xhat_j [B,1,d] pre-normed.
+
+        cache: the reference's {"K", "V"} dict. On first use a static tape of
+        cfg.max_seq_len rows is attached as cache["tape"]; cache["K"]/["V"] are
+        then views of its first pos+1 rows (refined, pre-rotated keys / values),
+        the same tensors the reference's cat-append would hold.
+        """
+        from .decode import StaticTape
+        B = xhat_j.shape[0]
+        tape = cache.get("tape")
+        if tape is None:
+            tape = StaticTape(self, B, self.cfg.max_seq_len, xhat_j.device, xhat_j.dtype)
+            if cache.get("K") is not None:
+                P = cache["K"].shape[2]
+                tape.K[:, :, :P] = cache["K"]
+                tape.V[:, :, :P] = cache["V"]
+            cache["tape"] = tape
+        o_cat, y = tape.step(xhat_j.reshape(B, -1), pos, cos, sin, with_wo=True)
+        cache["K"] = tape.K[:, :, :pos + 1]
+        cache["V"] = tape.V[:, :, :pos + 1]
+        return y.reshape(B, 1, -1).clone()   # the tape's output buffer is reused per step

@@ -1,0 +1,142 @@
+// Flash-style attention tiles on MFMA for the DM cell.
+//
+// One workgroup = 4 waves = 64 query rows of one (batch, head); wave w owns
+// rows 16w..16w+15. Keys stream through LDS in tiles of 64: K row-major
+// (B-operand of S = Q K^T), V transposed (B-operand of O += P V), P staged
+// per wave (A-operand). Row max / row sum reductions run inside the 16-lane
+// groups that hold one output row (shuffle xor 1..8); the per-lane partial
+// row sums are combined only once, at the end.
+//
+// Lane layout of every 16x16 fp32 tile: lane l holds rows 4*(l>>4)+r (r=0..3)
+// of column (l & 15).
+#pragma once
+
+#include "dm_common.h"
+
+namespace dm {
+
+constexpr float NEG_INF = -__builtin_huge_valf();
+
+template <typename T, int DH> struct AttnCfg {
+  using MF = Mfma<T>;
+  static constexpr int KT = 64;                     // keys per tile
+  static constexpr int PAD = 16 / (int)sizeof(T);
+  static constexpr int LDK = DH + PAD;              // Ks row stride
+  static constexpr int LDV = KT + PAD;              // Vt row stride (keys)
+  static constexpr int LDP = KT + PAD;              // Ps row stride (keys)
+  static constexpr int NDT = DH / 16;               // 16-wide output column tiles
+  static constexpr int NKS = DH / MF::KSTEP;        // k-steps over head_dim
+  static constexpr int NPS = KT / MF::KSTEP;        // k-steps over keys
+  static constexpr int VEC = 16 / (int)sizeof(T);   // elements per 16-byte load
+  static constexpr int LDS_ELEMS = KT * LDK + DH * LDV + 4 * 16 * LDP;
+};
+
+template <typename T, int DH> struct FlashState {
+  floatx4 O[DH / 16];   // O[dt][r]: row 4g+r, col (lane&15)+16dt
+  float m[4];           // running row max (uniform across the 16-lane group)
+  float z[4];           // per-lane partial row sum
+};
+
+template <typename T, int DH>
+DM_DEV void flash_init(FlashState<T, DH>& st) {
+#pragma unroll
+  for (int dt = 0; dt < DH / 16; ++dt) st.O[dt] = zero4();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) { st.m[r] = NEG_INF; st.z[r] = 0.f; }
+}
+
+// Query fragments for rows qrow = 16*wave + (lane&15): A-operand of S = Q K^T.
+template <typename T, int DH>
+DM_DEV void load_q_frags(const T* qrow_ptr, bool valid, typename Mfma<T>::frag* qf) {
+  using C = AttnCfg<T, DH>;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int ks = 0; ks < C::NKS; ++ks) {
+    if (valid) {
+      qf[ks] = Mfma<T>::load(qrow_ptr + ks * Mfma<T>::KSTEP + (lane >> 4) * Mfma<T>::KPL);
+    } else {
+      float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      qf[ks] = Mfma<T>::from_floats(z);
+    }
+  }
+}
+
+// Stage keys [0, nvalid) of a tile: K rows -> Ks, V rows transposed -> Vt.
+// Rows >= nvalid are zero-filled (so 0-probability columns multiply zeros).
+template <typename T, int DH>
+DM_DEV void stage_kv(const T* __restrict__ Kg, const T* __restrict__ Vg, long row_stride,
+                     int nvalid, T* Ks, T* Vt) {
+  using C = AttnCfg<T, DH>;
+  constexpr int VPR = DH / C::VEC;            // 16-byte vectors per row
+  for (int v = threadIdx.x; v < C::KT * VPR; v += 256) {
+    int k = v / VPR, c0 = (v % VPR) * C::VEC;
+    uint4 kr = uint4{0u, 0u, 0u, 0u}, vr = uint4{0u, 0u, 0u, 0u};
+    if (k < nvalid) {
+      kr = *reinterpret_cast<const uint4*>(Kg + (long)k * row_stride + c0);
+      vr = *reinterpret_cast<const uint4*>(Vg + (long)k * row_stride + c0);
+    }
+    *reinterpret_cast<uint4*>(Ks + k * C::LDK + c0) = kr;
+    const T* ve = reinterpret_cast<const T*>(&vr);
+#pragma unroll
+    for (int j = 0; j < C::VEC; ++j) Vt[(c0 + j) * C::LDV + k] = ve[j];
+  }
+}
+
+// One 64-key tile: S = Q K^T * scale, mask, online softmax update, O += P V.
+// mask(q, key) -> true if the score is kept; q is the wave-relative row + 16*wave.
+template <typename T, int DH, class MASK>
+DM_DEV void flash_tile(const typename Mfma<T>::frag* qf, const T* Ks, const T* Vt, T* Pw,
+                       float scale, const MASK& keep, FlashState<T, DH>& st) {
+  using C = AttnCfg<T, DH>;
+  using MF = Mfma<T>;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, col = lane & 15;
+
+  floatx4 S[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    S[t] = zero4();
+#pragma unroll
+    for (int ks = 0; ks < C::NKS; ++ks) {
+      typename MF::frag kf = MF::load(Ks + (col + 16 * t) * C::LDK + ks * MF::KSTEP + g * MF::KPL);
+      S[t] = MF::mma(qf[ks], kf, S[t]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int q = 16 * wave + 4 * g + r;
+    float mx = NEG_INF;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float s = S[t][r] * scale;
+      if (!keep(q, col + 16 * t)) s = NEG_INF;
+      S[t][r] = s;
+      mx = fmaxf(mx, s);
+    }
+    mx = group16_max(mx);
+    const float mnew = fmaxf(st.m[r], mx);
+    const float alpha = (st.m[r] == NEG_INF) ? 0.f : __expf(st.m[r] - mnew);
+    st.m[r] = mnew;
+    st.z[r] *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < C::NDT; ++dt) st.O[dt][r] *= alpha;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float p = (S[t][r] == NEG_INF) ? 0.f : __expf(S[t][r] - mnew);
+      st.z[r] += p;
+      Pw[(4 * g + r) * C::LDP + col + 16 * t] = from_f<T>(p);
+    }
+  }
+  __syncthreads();   // P visible to the whole wave (all waves run in lockstep)
+#pragma unroll
+  for (int kb = 0; kb < C::NPS; ++kb) {
+    typename MF::frag pf = MF::load(Pw + col * C::LDP + kb * MF::KSTEP + g * MF::KPL);
+#pragma unroll
+    for (int dt = 0; dt < C::NDT; ++dt) {
+      typename MF::frag vf = MF::load(Vt + (col + 16 * dt) * C::LDV + kb * MF::KSTEP + g * MF::KPL);
+      st.O[dt] = MF::mma(pf, vf, st.O[dt]);
+    }
+  }
+}
+
+}  // namespace dm

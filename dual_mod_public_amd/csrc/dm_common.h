@@ -1,0 +1,160 @@
+// Common device helpers for the Dual-Mod CDNA4 kernels (gfx950, wave64).
+//
+// Storage types: float (fp32 parity runs) and __bf16 (production). All
+// arithmetic that the reference keeps in fp32 islands (softmax, sigmoid,
+// RMS, RoPE, blends) is fp32 here as well.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define DM_DEV __device__ __forceinline__
+
+typedef __bf16 bf16;
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+namespace dm {
+
+constexpr int WAVE = 64;
+
+DM_DEV float to_f(float x) { return x; }
+DM_DEV float to_f(bf16 x) { return (float)x; }
+template <typename T> DM_DEV T from_f(float x);
+template <> DM_DEV float from_f<float>(float x) { return x; }
+template <> DM_DEV bf16 from_f<bf16>(float x) { return (bf16)x; }
+
+// 16-byte vector of storage elements: 8 bf16 or 4 fp32.
+template <typename T> struct Vec16;
+template <> struct Vec16<bf16> {
+  static constexpr int N = 8;
+  typedef uint4 raw;
+};
+template <> struct Vec16<float> {
+  static constexpr int N = 4;
+  typedef uint4 raw;
+};
+
+template <typename T>
+DM_DEV void unpack16(const uint4& r, float* out) {
+  if constexpr (sizeof(T) == 2) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = __uint_as_float(w[i] << 16);
+      out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else {
+    out[0] = __uint_as_float(r.x);
+    out[1] = __uint_as_float(r.y);
+    out[2] = __uint_as_float(r.z);
+    out[3] = __uint_as_float(r.w);
+  }
+}
+
+template <typename T>
+DM_DEV uint4 pack16(const float* in) {
+  uint4 r;
+  if constexpr (sizeof(T) == 2) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      bf16 lo = (bf16)in[2 * i];
+      bf16 hi = (bf16)in[2 * i + 1];
+      w[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+    r.x = w[0]; r.y = w[1]; r.z = w[2]; r.w = w[3];
+  } else {
+    r.x = __float_as_uint(in[0]);
+    r.y = __float_as_uint(in[1]);
+    r.z = __float_as_uint(in[2]);
+    r.w = __float_as_uint(in[3]);
+  }
+  return r;
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+// streaming 16-byte load (non-temporal hint: the data is read once)
+template <typename T>
+DM_DEV uint4 ld_nt(const T* p) {
+  u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return uint4{v.x, v.y, v.z, v.w};
+}
+
+DM_DEV float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// tanh from the exponential: tanh(x) = sign(x) * (1 - e) / (1 + e), e = exp(-2|x|).
+// Accurate to a few fp32 ulp away from 0; near 0 the odd Taylor series
+// x - x^3/3 + 2x^5/15 is used (its error is below fp32 resolution for |x| < 2^-4).
+DM_DEV float tanhf_(float x) {
+  float ax = fabsf(x);
+  if (ax < 0.0625f) {
+    float x2 = x * x;
+    return x * (1.0f + x2 * (-1.0f / 3.0f + x2 * (2.0f / 15.0f)));
+  }
+  float e = __expf(-2.0f * ax);
+  float t = (1.0f - e) / (1.0f + e);
+  return copysignf(t, x);
+}
+
+// ---- wave reductions (full 64-lane and within 16-lane groups) ----------------
+DM_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+DM_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+// reduce across the 16 lanes that share lane>>4 (xor over the low 4 bits)
+DM_DEV float group16_max(float v) {
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+DM_DEV float group16_sum(float v) {
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// ---- MFMA traits -------------------------------------------------------------
+// 16x16 output tile; lane l holds D[4*(l>>4) + r][l & 15], r = 0..3.
+// A fragment: row (l & 15), k-group (l >> 4); B fragment: col (l & 15), same k-group.
+// bf16: v_mfma_f32_16x16x32_bf16, 8 consecutive k per lane (k = 8*(l>>4) + j).
+// fp32: v_mfma_f32_16x16x4_f32, 1 k per lane (k = l >> 4).
+template <typename T> struct Mfma;
+template <> struct Mfma<bf16> {
+  static constexpr int KSTEP = 32;   // k consumed per instruction
+  static constexpr int KPL = 8;      // k elements held per lane
+  typedef bf16x8 frag;
+  static DM_DEV floatx4 mma(const frag& a, const frag& b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  // load KPL consecutive elements starting at p (16-byte aligned)
+  static DM_DEV frag load(const bf16* p) { return *reinterpret_cast<const frag*>(p); }
+  static DM_DEV frag from_floats(const float* f) {
+    frag r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (bf16)f[i];
+    return r;
+  }
+};
+template <> struct Mfma<float> {
+  static constexpr int KSTEP = 4;
+  static constexpr int KPL = 1;
+  typedef float frag;
+  static DM_DEV floatx4 mma(const frag& a, const frag& b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  static DM_DEV frag load(const float* p) { return *p; }
+  static DM_DEV frag from_floats(const float* f) { return f[0]; }
+};
+
+DM_DEV floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
+
+}  // namespace dm

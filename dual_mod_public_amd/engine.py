@@ -1,0 +1,265 @@
+"""Host orchestration of the HIP cell: packed weights, layer buffers, cells.
+
+Mirrors the reference engine's cell entry points:
+  * ``HipSweepCell.pack / layer_proj / cell_forward`` — FusedSweepCell
+    (engines/wavescan/cells/fused_sweep.py:1218-1553)
+  * ``layer_forward`` — engines/wavescan/engine/forward.py:95-113
+  * ``chunk_cell_forward`` — engines/wavescan/cells/scan_cell_fwd.py:88-116
+  * ``uniform_chunks / exact_sequential`` — engines/wavescan/engine/schedule.py:58-69
+
+All compute runs in libdm_hip.so; torch provides device memory and the stream.
+"""
+
+import ctypes
+
+import torch
+
+from . import _lib as L
+
+
+def uniform_chunks(T, c, n_sweeps=None):
+    """schedule.py:63-69 — fixed-size chunks; n_sweeps=None means K=c (exact)."""
+    cells = []
+    for pos in range(0, T, c):
+        cc = min(c, T - pos)
+        cells.append((pos, cc, cc if n_sweeps is None else min(n_sweeps, cc)))
+    return cells
+
+
+def exact_sequential(T):
+    """schedule.py:58-60 — every position its own exact cell."""
+    return [(j, 1, 1) for j in range(T)]
+
+
+def check_supported(cfg):
+    """The knob set the HIP path implements; anything else raises (no fallback).
+    Mirrors FusedSweepCell.__init__'s asserts (fused_sweep.py:1219-1225)."""
+    bad = []
+    if cfg.gate_type != "convex_sigmoid":
+        bad.append(f"gate_type={cfg.gate_type}")
+    if getattr(cfg, "gate_type_v", "convex") != "convex":
+        bad.append(f"gate_type_v={cfg.gate_type_v}")
+    if cfg.gate_input != "xu":
+        bad.append(f"gate_input={cfg.gate_input}")
+    if not (cfg.enable_key_mod and cfg.enable_value_mod):
+        bad.append("enable_key_mod/enable_value_mod must both be True")
+    if not cfg.rmsnorm_on_o:
+        bad.append("rmsnorm_on_o=False")
+    if cfg.ctx_mod not in L.CTX_MOD:
+        bad.append(f"ctx_mod={cfg.ctx_mod}")
+    for knob, off in (("k_ctx_norm", "none"), ("v_ctx_norm", "none"), ("v_norm", "none")):
+        if getattr(cfg, knob, off) != off:
+            bad.append(f"{knob}={getattr(cfg, knob)}")
+    for knob in ("kmod_vraw_heads", "gate_rank", "ctx_rank", "attn_logn_ref"):
+        if getattr(cfg, knob, 0):
+            bad.append(f"{knob}={getattr(cfg, knob)}")
+    if getattr(cfg, "v_clamp_tau", 0.0):
+        bad.append(f"v_clamp_tau={cfg.v_clamp_tau}")
+    if cfg.head_dim not in (64, 128):
+        bad.append(f"head_dim={cfg.head_dim} (64 or 128)")
+    if cfg.d_model % 128:
+        bad.append(f"d_model={cfg.d_model} (multiple of 128)")
+    if bad:
+        raise NotImplementedError("HIP DM path does not implement: " + ", ".join(bad))
+
+
+class PackedWeights:
+    """Device-side packed weights of one layer (dm_packed)."""
+
+    def __init__(self, cfg, device, dtype):
+        check_supported(cfg)
+        d = cfg.d_model
+        self.cfg, self.device, self.dtype = cfg, device, dtype
+        mult = cfg.ctx_mod != "linear"
+        kw = dict(device=device, dtype=dtype)
+        self.w_proj = torch.empty((6 if mult else 5) * d, d, **kw)
+        self.b_proj = torch.zeros(3 * d, device=device, dtype=torch.float32)
+        self.w_sweep = torch.empty(4 * d, d, **kw)
+        self.w_vctx = torch.empty(d, d, **kw) if mult else None
+        self.norm_ctx_w = torch.empty(d, **kw)
+        self.attn_norm_w = torch.empty(d, **kw)
+        self.wo = torch.empty(d, d, **kw)
+        self.has_attn_norm = False
+
+    def struct(self, with_attn_norm=None):
+        s = L.dm_packed()
+        s.w_proj, s.b_proj, s.w_sweep = L.ptr(self.w_proj), L.ptr(self.b_proj), L.ptr(self.w_sweep)
+        s.w_vctx, s.norm_ctx_w, s.wo = L.ptr(self.w_vctx), L.ptr(self.norm_ctx_w), L.ptr(self.wo)
+        use = self.has_attn_norm if with_attn_norm is None else with_attn_norm
+        s.attn_norm_w = L.ptr(self.attn_norm_w) if use else None
+        return s
+
+    @torch.no_grad()
+    def pack(self, sd, attn_norm_w=None):
+        """sd: mapping with the reference parameter names (attention.py:100-202) —
+        a state dict or a DualModAttention's named parameters."""
+        cfg = self.cfg
+        keep = []
+
+        def t(name):
+            x = sd[name].detach().to(device=self.device, dtype=self.dtype).contiguous()
+            keep.append(x)
+            return L.ptr(x)
+
+        p = L.dm_params()
+        for f, n in (("wq", "wq.weight"), ("wk", "wk.weight"), ("wv", "wv.weight"),
+                     ("wo", "wo.weight"), ("w_kctx", "w_kctx.weight"), ("w_vctx", "w_vctx.weight"),
+                     ("w_gk", "w_gk.weight"), ("w_gv", "w_gv.weight"), ("b_gk", "w_gk.bias"),
+                     ("b_gv", "w_gv.bias"), ("norm_ctx_w", "norm_ctx.weight")):
+            setattr(p, f, t(n))
+        if cfg.ctx_mod != "linear":
+            p.v_gate, p.b_vgate, p.v_map = t("v_gate.weight"), t("v_gate.bias"), t("v_map.weight")
+        if attn_norm_w is None and "attn_norm.weight" in sd:
+            attn_norm_w = sd["attn_norm.weight"]
+        if attn_norm_w is not None:
+            a = attn_norm_w.detach().to(device=self.device, dtype=self.dtype).contiguous()
+            keep.append(a)
+            p.attn_norm_w = L.ptr(a)
+            self.has_attn_norm = True
+        out = self.struct(with_attn_norm=attn_norm_w is not None)
+        c = L.make_config(cfg, 1, self.dtype)
+        L.check(L.lib().dm_pack_weights(ctypes.byref(c), ctypes.byref(p), ctypes.byref(out),
+                                        L.stream_ptr()))
+        # sources must outlive the async copies: wait on this stream before releasing them
+        torch.cuda.current_stream().synchronize()
+        return self
+
+
+class LayerBufs:
+    """Per-layer projection buffers (dm_layer_bufs) for batch B, length T."""
+
+    def __init__(self, cfg, B, T, device, dtype):
+        d, h, dh = cfg.d_model, cfg.n_heads, cfg.head_dim
+        kw = dict(device=device, dtype=dtype)
+        self.B, self.T = B, T
+        self.xhat = torch.empty(B, T, d, **kw)
+        self.qr = torch.empty(B, h, T, dh, **kw)
+        self.kraw = torch.empty(B, h, T, dh, **kw)
+        self.kself = torch.empty(B, h, T, dh, **kw)
+        self.vraw = torch.empty(B, h, T, dh, **kw)
+        self.glogx = torch.empty(B, T, 2 * d, device=device, dtype=torch.float32)
+        self.sig = (torch.empty(B, T, d, device=device, dtype=torch.float32)
+                    if cfg.ctx_mod != "linear" else None)
+
+    def struct(self):
+        s = L.dm_layer_bufs()
+        s.T = self.T
+        for n in ("xhat", "qr", "kraw", "kself", "vraw", "glogx", "sig"):
+            setattr(s, n, L.ptr(getattr(self, n)))
+        return s
+
+
+def _f32(t, device):
+    return t.to(device=device, dtype=torch.float32).contiguous()
+
+
+class HipSweepCell:
+    """FusedSweepCell analogue for one DM layer on one GPU (fused_sweep.py:1218).
+
+    Owns the packed weights and the cell workspace; callers own the layer
+    buffers, K/V caches (append-only, rows [0, pos0) committed) and outputs.
+    """
+
+    def __init__(self, cfg, B, cache_T, device="cuda", dtype=torch.bfloat16):
+        check_supported(cfg)
+        self.cfg, self.B, self.cache_T = cfg, B, cache_T
+        self.device, self.dtype = torch.device(device), dtype
+        self.w = PackedWeights(cfg, self.device, dtype)
+        self.conf = L.make_config(cfg, B, dtype)
+        nbytes = L.lib().dm_cell_workspace_bytes(ctypes.byref(self.conf), cache_T)
+        if nbytes == 0:
+            raise L.DMError("dm_cell_workspace_bytes rejected the configuration")
+        self.workspace = torch.empty(nbytes, device=self.device, dtype=torch.uint8)
+
+    def pack(self, sd, attn_norm_w=None):
+        self.w.pack(sd, attn_norm_w)
+        return self
+
+    def new_bufs(self, T):
+        return LayerBufs(self.cfg, self.B, T, self.device, self.dtype)
+
+    def layer_proj(self, x, bufs, cos, sin, normalize=True):
+        """fused_sweep.py:1403-1436 — projections for the whole layer.
+        normalize=True applies attn_norm (Block input x); False takes x as xhat."""
+        assert x.is_contiguous() and x.dtype == self.dtype
+        cos, sin = _f32(cos, self.device), _f32(sin, self.device)
+        ws = self.w.struct(with_attn_norm=normalize)
+        b = bufs.struct()
+        L.check(L.lib().dm_layer_proj(ctypes.byref(self.conf), ctypes.byref(ws), L.ptr(x),
+                                      L.ptr(cos), L.ptr(sin), ctypes.byref(b), L.stream_ptr()))
+        return bufs
+
+    def cell_forward(self, bufs, cos, sin, K_cache, V_cache, pos0, c, n_sweeps, ocat=None,
+                     o_last=None):
+        """fused_sweep.py:1455-1553 — one chunk [pos0, pos0+c), n_sweeps Jacobi sweeps.
+        Writes the chunk's final rows into K_cache/V_cache and (optionally) its
+        o_cat rows into ocat [B, T, d] / the fp32 o_last [B*c, d]."""
+        cos, sin = _f32(cos, self.device), _f32(sin, self.device)
+        a = L.dm_cell_args()
+        a.pos0, a.c, a.n_sweeps, a.cache_T = pos0, c, n_sweeps, K_cache.shape[2]
+        a.K_cache, a.V_cache = L.ptr(K_cache), L.ptr(V_cache)
+        a.ocat, a.o_last = L.ptr(ocat), L.ptr(o_last)
+        a.workspace, a.workspace_bytes = L.ptr(self.workspace), self.workspace.numel()
+        ws = self.w.struct()
+        b = bufs.struct()
+        L.check(L.lib().dm_cell_fwd(ctypes.byref(self.conf), ctypes.byref(ws), ctypes.byref(b),
+                                    L.ptr(cos), L.ptr(sin), ctypes.byref(a), L.stream_ptr()))
+
+    def layer_forward(self, x, y, cos, sin, schedule, K_cache, V_cache, ocat, bufs):
+        """Attention sublayer y = x + W_O DM(attn_norm(x)) over ``schedule``
+        (model.py:123-124 with forward.py:95-113's chunk loop), one C call."""
+        sched = (ctypes.c_int32 * (3 * len(schedule)))(*[v for cell in schedule for v in cell])
+        cos, sin = _f32(cos, self.device), _f32(sin, self.device)
+        ws = self.w.struct(with_attn_norm=True)
+        b = bufs.struct()
+        L.check(L.lib().dm_layer_fwd(
+            ctypes.byref(self.conf), ctypes.byref(ws), L.ptr(x), L.ptr(y), L.ptr(cos), L.ptr(sin),
+            ctypes.byref(b), sched, len(schedule), L.ptr(K_cache), L.ptr(V_cache),
+            K_cache.shape[2], L.ptr(ocat), L.ptr(self.workspace), self.workspace.numel(),
+            L.stream_ptr()))
+        return y
+
+
+def chunk_cell_forward(attn, xhat_c, cos_c, sin_c, K_comm, V_comm, n_sweeps, intra_mask=None):
+    """scan_cell_fwd.py:88-116 signature: one chunk against a committed prefix.
+
+    attn: a dual_mod_public_amd.attention.DualModAttention. xhat_c [B,c,d];
+    cos_c/sin_c: RoPE rows of the chunk's positions; K_comm/V_comm [B,h,a,dh]
+    (None or 0-length for the first chunk). Returns (o_cat [B,c,d],
+    K_rows [B,h,c,dh] rotated, V_rows [B,h,c,dh]). ``intra_mask`` is accepted
+    for signature compatibility; the kernels apply the strict-lower mask.
+    """
+    B, c, d = xhat_c.shape
+    a = 0 if K_comm is None else K_comm.shape[2]
+    cell = attn._hip_cell(B, a + c, xhat_c.dtype)
+    dev, dt = xhat_c.device, xhat_c.dtype
+    h, dh = attn.n_heads, attn.head_dim
+    T = a + c
+    x = torch.zeros(B, T, d, device=dev, dtype=dt)
+    x[:, a:] = xhat_c
+    cos = torch.zeros(T, dh // 2, device=dev, dtype=torch.float32)
+    sin = torch.zeros_like(cos)
+    cos[a:], sin[a:] = cos_c.float(), sin_c.float()
+    Kc = torch.zeros(B, h, T, dh, device=dev, dtype=dt)
+    Vc = torch.zeros_like(Kc)
+    if a:
+        Kc[:, :, :a], Vc[:, :, :a] = K_comm, V_comm
+    bufs = cell.new_bufs(T)
+    cell.layer_proj(x, bufs, cos, sin, normalize=False)
+    ocat = torch.empty(B, T, d, device=dev, dtype=dt)
+    cell.cell_forward(bufs, cos, sin, Kc, Vc, a, c, n_sweeps, ocat=ocat)
+    return ocat[:, a:], Kc[:, :, a:], Vc[:, :, a:]
+
+
+def layer_forward(attn, xhat, cos, sin, schedule, K_cache, V_cache, masks=None, o_out=None):
+    """forward.py:95-113 signature: one layer's chunked scan over ``schedule``.
+    K_cache/V_cache [B,h,T_max,dh] are written append-only. Returns o_cat [B,T,d]."""
+    B, T, d = xhat.shape
+    cell = attn._hip_cell(B, K_cache.shape[2], xhat.dtype)
+    bufs = cell.new_bufs(T)
+    cell.layer_proj(xhat.contiguous(), bufs, cos, sin, normalize=False)
+    if o_out is None:
+        o_out = torch.empty(B, T, d, device=xhat.device, dtype=xhat.dtype)
+    for pos0, c, k in schedule:
+        cell.cell_forward(bufs, cos, sin, K_cache, V_cache, pos0, c, k, ocat=o_out)
+    return o_out

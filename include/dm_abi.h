@@ -1,0 +1,180 @@
+/* dm_abi.h — C ABI of libdm_hip.so, the MI355X (gfx950) Dual-Mod attention hot path.
+ *
+ * Plain C: device pointers, sizes, enums. No torch, no HIP types in the
+ * signatures (streams are passed as `void*` holding a hipStream_t; NULL =
+ * the null stream). Every call validates its arguments, launches asynchronously
+ * on the given stream, never allocates device memory, never synchronizes,
+ * and returns 0 (DM_OK) or a negative dm_status; dm_last_error() then holds a
+ * message (thread-local).
+ *
+ * Layouts (all contiguous, row-major):
+ *   x, y        [B, T, d]        storage dtype
+ *   head bufs   [B, h, T, dh]    storage dtype (qr, kraw, kself, vraw)
+ *   K/V cache   [B, h, Tc, dh]   storage dtype, rows [0, pos0) committed
+ *   glogx       [B, T, 2d] fp32  x-half of the key|value gate logits + bias
+ *   sig         [B, T, d]  fp32  sigmoid(v_gate(xhat)) (ctx_mod mult/mult_res)
+ *   cos, sin    [Tc, dh/2] fp32  RoPE tables (models/dualmod/rope.py:13-19)
+ *
+ * Reference interface each entry point replaces (paths in Atom-101/dual_mod_public):
+ *   dm_pack_weights  engines/wavescan/cells/fused_sweep.py:1266-1291 (FusedSweepCell.pack)
+ *   dm_layer_proj    engines/wavescan/cells/fused_sweep.py:1403-1436 (FusedSweepCell.layer_proj)
+ *   dm_cell_fwd      engines/wavescan/cells/fused_sweep.py:1455-1553 (FusedSweepCell.cell_forward)
+ *                    == engines/wavescan/cells/scan_cell_fwd.py:88-116 (chunk_cell_forward)
+ *   dm_layer_fwd     engines/wavescan/engine/forward.py:95-113 (layer_forward) + W_O,
+ *                    models/dualmod/model.py:123-124 (Block attention sublayer)
+ *   dm_decode_step   models/dualmod/attention.py:564-588 (DualModAttention.decode_step),
+ *                    lm/eval/graph_decode.py:33-51 (GraphDecoder._attn)
+ */
+#ifndef DM_ABI_H
+#define DM_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DM_ABI_VERSION 1
+
+typedef enum dm_status {
+  DM_OK = 0,
+  DM_ERR_INVALID = -1,      /* bad shape / pointer / alignment */
+  DM_ERR_UNSUPPORTED = -2,  /* knob or shape the HIP path does not implement */
+  DM_ERR_WORKSPACE = -3,    /* workspace too small */
+  DM_ERR_HIP = -4           /* a HIP runtime call failed */
+} dm_status;
+
+typedef enum dm_dtype { DM_F32 = 0, DM_BF16 = 1 } dm_dtype;
+
+/* ctx_mod values (models/dualmod/config.py:61, attention.py:338-360) */
+typedef enum dm_ctx_mod { DM_CTX_LINEAR = 0, DM_CTX_MULT_RES = 1, DM_CTX_MULT = 2 } dm_ctx_mod;
+
+/* Shape + knob set shared by every call (DualModConfig subset). */
+typedef struct dm_config {
+  int32_t dtype;            /* dm_dtype of activations, weights and caches */
+  int32_t B, d, h, dh;      /* batch, d_model, heads, head_dim (d == h*dh) */
+  int32_t ctx_mod;          /* dm_ctx_mod */
+  float mult_res_lambda;    /* config.py:126 */
+  float rms_eps;            /* RMSNorm eps of attn_norm / norm_ctx: 1e-5 */
+  int32_t local_window;     /* decode only: W tokens incl. self, 0 = full */
+  int32_t reserved[7];
+} dm_config;
+
+/* The reference parameters of one DualModAttention layer (attention.py:100-202),
+ * each as stored by torch (nn.Linear weight = [out, in]). Storage dtype unless noted. */
+typedef struct dm_params {
+  const void* wq; const void* wk; const void* wv; const void* wo;   /* [d, d] */
+  const void* w_kctx; const void* w_vctx;                            /* [d, d] */
+  const void* w_gk; const void* w_gv;                                /* [d, 2d] */
+  const void* b_gk; const void* b_gv;                                /* [d] */
+  const void* v_gate; const void* b_vgate; const void* v_map;        /* [d,d],[d],[d,d]; mult family */
+  const void* norm_ctx_w;                                            /* [d] */
+  const void* attn_norm_w;                                           /* [d] (layer entry points) */
+} dm_params;
+
+/* Packed weights (written by dm_pack_weights, read by every compute call).
+ *   w_proj  [6d, d]  rows: wq | wk | wv | w_gk[:, :d] | w_gv[:, :d] | v_gate   (linear: 5d rows)
+ *   b_proj  [3d] fp32: b_gk | b_gv | b_vgate
+ *   w_sweep [4d, d]  per head g: [w_kctx rows of g ; w_gk[:, d:] rows of g] (2*dh rows each),
+ *                    then mult family: v_map (d rows), w_gv[:, d:] (d rows);
+ *                    linear: per head g: [w_vctx rows of g ; w_gv[:, d:] rows of g]
+ *   w_vctx  [d, d]   (mult family), norm_ctx_w [d], attn_norm_w [d], wo [d, d]: copies */
+typedef struct dm_packed {
+  void* w_proj; float* b_proj; void* w_sweep; void* w_vctx;
+  void* norm_ctx_w; void* attn_norm_w; void* wo;
+} dm_packed;
+
+/* Per-layer projection buffers (fused_sweep.py:1179-1215 LayerBufs, own layout). */
+typedef struct dm_layer_bufs {
+  int32_t T;                /* sequence length of these buffers */
+  void* xhat;               /* [B, T, d] attn_norm(x) (kept for the backward) */
+  void* qr;                 /* [B, h, T, dh] rotated query */
+  void* kraw;               /* [B, h, T, dh] unrotated raw key (blend space) */
+  void* kself;              /* [B, h, T, dh] rotated raw key (self column) */
+  void* vraw;               /* [B, h, T, dh] raw value */
+  float* glogx;             /* [B, T, 2d] */
+  float* sig;               /* [B, T, d] or NULL (linear) */
+} dm_layer_bufs;
+
+/* ---- version / errors ------------------------------------------------------ */
+int dm_abi_version(void);
+const char* dm_last_error(void);
+
+/* ---- weights ----------------------------------------------------------------
+ * Replaces FusedSweepCell.pack (engines/wavescan/cells/fused_sweep.py:1266-1291). */
+int dm_pack_weights(const dm_config* cfg, const dm_params* p, const dm_packed* out, void* stream);
+
+/* ---- layer projection pass --------------------------------------------------
+ * Replaces FusedSweepCell.layer_proj (fused_sweep.py:1403-1436): xhat = RMSNorm(x),
+ * q/k/v projections + RoPE, x-half gate logits (+bias), sigmoid(v_gate(xhat)).
+ * x: [B, T, d]; cos/sin: [>=T, dh/2] fp32 tables, row t = position t.
+ * With w->attn_norm_w == NULL, x is taken as already normalised (xhat) and
+ * bufs->xhat is not written (DualModAttention.forward takes xhat, attention.py:438). */
+int dm_layer_proj(const dm_config* cfg, const dm_packed* w, const void* x, const float* cos,
+                  const float* sin, const dm_layer_bufs* bufs, void* stream);
+
+/* ---- one forward cell ---------------------------------------------------------
+ * Replaces FusedSweepCell.cell_forward (fused_sweep.py:1455-1553) and
+ * chunk_cell_forward (scan_cell_fwd.py:88-116): chunk [pos0, pos0+c) of the
+ * layer, n_sweeps Jacobi sweeps against the committed rows [0, pos0) of K/V
+ * cache, writing the chunk's final refined rows into the cache (append-only)
+ * and the last sweep's o_cat into ocat[:, pos0:pos0+c] (storage dtype, [B,T,d]).
+ * Requires 1 <= c <= 64, pos0 + c <= bufs->T <= cache_T. */
+typedef struct dm_cell_args {
+  int32_t pos0, c, n_sweeps, cache_T;
+  void* K_cache; void* V_cache;        /* [B, h, cache_T, dh] */
+  void* ocat;                          /* [B, bufs->T, d] or NULL */
+  float* o_last;                       /* [B*c, d] fp32 copy of the last sweep's o, or NULL */
+  void* workspace; size_t workspace_bytes;
+} dm_cell_args;
+size_t dm_cell_workspace_bytes(const dm_config* cfg, int32_t cache_T);
+int dm_cell_fwd(const dm_config* cfg, const dm_packed* w, const dm_layer_bufs* bufs,
+                const float* cos, const float* sin, const dm_cell_args* a, void* stream);
+
+/* ---- whole layer forward ------------------------------------------------------
+ * Block attention sublayer (models/dualmod/model.py:123-124) run through the
+ * chunk schedule (engines/wavescan/engine/forward.py:95-113, schedule.py:63-69):
+ *   y = x + W_O . DM(RMSNorm(x)).  sched = n_cells triples (pos0, c, n_sweeps)
+ * that tile [0, T) in order. Fills bufs, the caches and ocat [B, T, d]. */
+int dm_layer_fwd(const dm_config* cfg, const dm_packed* w, const void* x, void* y,
+                 const float* cos, const float* sin, const dm_layer_bufs* bufs,
+                 const int32_t* sched, int32_t n_cells, void* K_cache, void* V_cache,
+                 int32_t cache_T, void* ocat, void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+/* ---- decode ------------------------------------------------------------------
+ * Replaces DualModAttention.decode_step (attention.py:564-588) on a static tape
+ * (lm/eval/graph_decode.py:33-51): one token per batch row at position pos.
+ * Reads tape rows [max(0, pos-W+1), pos) + the raw self pair, refines, and
+ * writes the refined rotated key / refined value into tape slot pos.
+ * xhat: [B, d] pre-normed input. o_cat: [B, d] storage dtype output (pre-W_O).
+ * y: [B, d] = W_O o_cat, or NULL to skip. */
+typedef struct dm_decode_args {
+  int32_t pos, tape_T;
+  const void* xhat;
+  void* K_tape; void* V_tape;          /* [B, h, tape_T, dh] */
+  void* o_cat; void* y;
+  void* workspace; size_t workspace_bytes;
+} dm_decode_args;
+size_t dm_decode_workspace_bytes(const dm_config* cfg, int32_t tape_T);
+int dm_decode_step(const dm_config* cfg, const dm_packed* w, const float* cos, const float* sin,
+                   const dm_decode_args* a, void* stream);
+
+/* ---- linear layer -------------------------------------------------------------
+ * y[M, N] = x[M, K] . W[N, K]^T (+ r[M, N] when r != NULL): nn.Linear without
+ * bias (the W_O projection, attention.py:103), storage dtype, fp32 accumulate.
+ * N multiple of 128, K multiple of 64, any M. */
+int dm_linear(int32_t dtype, const void* x, const void* W, const void* r, void* y, int32_t M,
+              int32_t N, int32_t K, void* stream);
+
+/* ---- plain GEMM (test / utility) --------------------------------------------
+ * C[M, N] (fp32) = A[M, K] . B[N, K]^T in the storage dtype with fp32 accumulate.
+ * M, N, K multiples of 64. */
+int dm_gemm_nt(int32_t dtype, const void* A, const void* Bm, float* C, int32_t M, int32_t N,
+               int32_t K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DM_ABI_H */

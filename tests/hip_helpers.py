@@ -1,0 +1,40 @@
+"""Shared helpers for the GPU parity tests (HIP path vs the CPU oracle)."""
+
+import sys
+
+import torch
+
+import oracle as O
+from dual_mod_public_amd.config import DualModConfig
+from dual_mod_public_amd.synthetic import make_input, make_state_dict
+
+DEV = "cuda"
+
+
+def say(msg):
+    print(f"[gpu-test] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def cfg_of(d=256, h=4, ctx_mod="mult_res", T=64, **kw):
+    return DualModConfig(d_model=d, n_heads=h, n_layers=1, max_seq_len=T, checkpoint_chunk=0,
+                         ctx_mod=ctx_mod, dtype="fp32", **kw)
+
+
+def setup(cfg, B, T, wseed=11, xseed=12, std=0.02):
+    """(sd fp64 CPU, x fp64 CPU, cos/sin fp64 CPU, cos/sin fp32 CPU)."""
+    sd = {k: v.double() for k, v in make_state_dict(cfg, seed=wseed, std=std).items()}
+    x = make_input((B, T, cfg.d_model), seed=xseed, dtype=torch.float64)
+    cos64, sin64 = O.build_rope_cache(T, cfg.head_dim, cfg.rope_theta, dtype=torch.float64)
+    cos32, sin32 = O.build_rope_cache(T, cfg.head_dim, cfg.rope_theta, dtype=torch.float32)
+    return sd, x, (cos64, sin64), (cos32, sin32)
+
+
+def to_dev(sd, dtype):
+    return {k: v.to(device=DEV, dtype=dtype) for k, v in sd.items()}
+
+
+def relerr(a, b):
+    a = a.double().cpu()
+    b = b.double().cpu()
+    return ((a - b).norm() / (b.norm() + 1e-30)).item()

@@ -1,0 +1,82 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol declared in
+include/dm_abi.h, and rejects bad arguments before touching a device."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from dual_mod_public_amd import _lib as L
+from dual_mod_public_amd.config import DualModConfig
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    src = open(os.path.join(REPO, "include", "dm_abi.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(dm_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = L.load()
+    names = declared_symbols()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in L.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(L.SIGNATURES) == set(names)
+
+
+def test_abi_version():
+    assert L.load().dm_abi_version() == 1
+
+
+def _conf(**kw):
+    cfg = DualModConfig(d_model=256, n_heads=4, ctx_mod="mult_res")
+    import torch
+    c = L.make_config(cfg, 2, torch.float32)
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+def test_rejects_bad_config_without_device():
+    lib = L.load()
+    c = _conf(dh=32, h=8)           # d == h*dh but head_dim 32 unsupported
+    assert lib.dm_cell_workspace_bytes(ctypes.byref(c), 64) == 0
+    c = _conf(d=250)
+    rc = lib.dm_layer_proj(ctypes.byref(c), None, None, None, None, None, None)
+    assert rc == -1
+    assert b"d=250" in lib.dm_last_error()
+
+
+def test_rejects_null_and_bad_shapes():
+    lib = L.load()
+    c = _conf()
+    a = L.dm_cell_args()
+    a.c = 65
+    rc = lib.dm_cell_fwd(ctypes.byref(c), None, None, None, None, ctypes.byref(a), None)
+    assert rc == -1 and b"null packed" in lib.dm_last_error()
+    assert lib.dm_gemm_nt(0, None, None, None, 64, 64, 64, None) == -1
+    assert lib.dm_linear(0, 1, 1, None, 1, 64, 100, 64, None) == -1
+
+
+def test_workspace_query():
+    lib = L.load()
+    c = _conf()
+    n1 = lib.dm_cell_workspace_bytes(ctypes.byref(c), 64)
+    n2 = lib.dm_cell_workspace_bytes(ctypes.byref(c), 4096)
+    assert 0 < n1 < n2
+    assert lib.dm_decode_workspace_bytes(ctypes.byref(c), 32768) > 0
+
+
+def test_unsupported_knobs_raise():
+    from dual_mod_public_amd.engine import check_supported
+    for kw in (dict(k_ctx_norm="rms"), dict(v_clamp_tau=1.0), dict(kmod_vraw_heads=1),
+               dict(gate_type_v="independent"), dict(ctx_mod="fusion"), dict(attn_logn_ref=64)):
+        cfg = DualModConfig(d_model=256, n_heads=4, **kw)
+        with pytest.raises(NotImplementedError):
+            check_supported(cfg)
+    check_supported(DualModConfig(d_model=256, n_heads=4, ctx_mod="mult_res"))

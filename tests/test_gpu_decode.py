@@ -1,0 +1,106 @@
+"""GPU parity of the HIP decode step (dm_decode_step) against the CPU oracle.
+
+T3 analogue (tests/test_dualmod_equivalence.py:98-112): decoding token by token
+through the static tape reproduces the teacher-forced sequential scan; plus a
+pre-written random bf16 tape (BASELINE config 5 shape, scaled down) checked
+against the oracle's static-tape decode (lm/eval/graph_decode.py:33-51).
+"""
+
+import pytest
+import torch
+
+import oracle as O
+from dual_mod_public_amd import _lib as L
+from dual_mod_public_amd.decode import StaticTape
+from tests.hip_helpers import DEV, cfg_of, relerr, say, setup, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    L.load()
+
+
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear"])
+def test_decode_equals_teacher_forced_fp32(ctx_mod):
+    say(f"decode fp32 teacher-forced ctx_mod={ctx_mod}")
+    cfg = cfg_of(ctx_mod=ctx_mod)
+    B, T = 2, 64
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    tape = StaticTape(cfg, B, T, DEV, torch.float32, sd=to_dev(sd, torch.float32))
+    xd = x.float().to(DEV)
+    outs = []
+    for t in range(T):
+        o, _ = tape.step(xd[:, t].contiguous(), t, c32, s32)
+        outs.append(o.clone())
+    torch.cuda.synchronize()
+    o_ref, K_ref, V_ref = O.sequential_scan(cfg, sd, x, c64, s64, return_cache=True)
+    assert relerr(torch.stack(outs, 1), o_ref) < 1e-5
+    assert relerr(tape.K, K_ref) < 1e-5
+    assert relerr(tape.V, V_ref) < 1e-5
+
+
+def test_decode_local_window_fp32():
+    say("decode fp32 local_window=8")
+    cfg = cfg_of(local_window=8, T=24)
+    B, T = 2, 24
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    tape = StaticTape(cfg, B, T, DEV, torch.float32, sd=to_dev(sd, torch.float32))
+    xd = x.float().to(DEV)
+    cache = {"K": None, "V": None}
+    for t in range(T):
+        o, _ = tape.step(xd[:, t].contiguous(), t, c32, s32)
+        o_ref, _ = O.decode_step(cfg, sd, x[:, t:t + 1], t, cache, c64, s64)
+        assert relerr(o, o_ref[:, 0]) < 1e-5, t
+    assert relerr(tape.K, cache["K"]) < 1e-5
+
+
+@pytest.mark.parametrize("P0", [0, 1, 511, 1500])
+def test_decode_on_random_bf16_tape(P0):
+    """Pre-written N(0,1) bf16 tape of P0 rows (multi-split when P0 > 512), d=1024
+    16x64, 4 steps; vs the oracle static-tape decode in fp32 on the same tape."""
+    say(f"decode bf16 random tape P0={P0}")
+    cfg = cfg_of(d=1024, h=16, T=P0 + 8)
+    B, steps = 4, 4
+    P = P0 + steps
+    sd, x, _, (c32, s32) = setup(cfg, B, P)
+    g = torch.Generator().manual_seed(5)
+    K0 = torch.randn(B, 16, P, 64, generator=g).bfloat16()
+    V0 = torch.randn(B, 16, P, 64, generator=g).bfloat16()
+    tape = StaticTape(cfg, B, P, DEV, torch.bfloat16, sd=to_dev(sd, torch.bfloat16))
+    tape.K.copy_(K0.to(DEV))
+    tape.V.copy_(V0.to(DEV))
+    Kb, Vb = K0.float(), V0.float()
+    sdf = {k: v.float() for k, v in sd.items()}
+    xb = x.bfloat16()
+    for t in range(P0, P):
+        o, _ = tape.step(xb[:, t].to(DEV).contiguous(), t, c32, s32)
+        o_ref = O.static_decode_step(cfg, sdf, xb[:, t:t + 1].float(), t, Kb, Vb, c32, s32)
+        torch.cuda.synchronize()
+        e = relerr(o, o_ref[:, 0])
+        say(f"  step {t}: relerr o={e:.2e}")
+        assert e < 2e-2
+    assert relerr(tape.K[:, :, P0:P], Kb[:, :, P0:P]) < 2e-2
+    assert relerr(tape.V[:, :, P0:P], Vb[:, :, P0:P]) < 2e-2
+    assert torch.equal(tape.K[:, :, :P0].cpu(), K0[:, :, :P0])   # append-only
+
+
+def test_attention_module_decode_matches_scan():
+    from dual_mod_public_amd.attention import DualModAttention
+    say("DualModAttention.decode_step fp32")
+    cfg = cfg_of(T=32)
+    B, T = 2, 32
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    attn = DualModAttention(cfg).to(DEV)
+    attn.load_state_dict({k: v.float() for k, v in sd.items() if k != "attn_norm.weight"})
+    cache = {"K": None, "V": None}
+    xd = x.float().to(DEV)
+    ys = [attn.decode_step(xd[:, t:t + 1], t, cache, c32.to(DEV), s32.to(DEV)) for t in range(T)]
+    torch.cuda.synchronize()
+    o_ref, K_ref, _ = O.sequential_scan(cfg, sd, x, c64, s64, return_cache=True)
+    y_ref = O.dm_oracle._lin(o_ref, sd, "wo")
+    assert relerr(torch.cat(ys, 1), y_ref) < 1e-5
+    assert relerr(cache["K"], K_ref) < 1e-5
