@@ -1,0 +1,232 @@
+"""Benchmark of the Dual-Mod attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-decode]
+
+One step = one DM attention layer of the 340M shape (B=8, T=2048, d=1024,
+16 heads x 64, c=64, K=4 Jacobi sweeps chained over 32 chunks, bf16 storage /
+fp32 accumulate) through libdm_hip.so: attn_norm + projections, the 32 chunk
+cells (committed accumulator + 4 sweeps each) and W_O with the residual.
+Inputs (x, weights, RoPE tables) are resident in HBM before timing starts.
+
+Prints ONE JSON line (rank 0): the headline sweep throughput in tokens/s, the
+roofline of the dominant kernel timed with HIP events inside the timed region,
+the path-level roofline, the CPU baseline (the oracle's chunked-Jacobi layer
+forward timed on this host's cores on a bounded sample) and the decode
+sub-benchmark (batch 64, bf16 tape of 32768 positions, HBM GB/s).
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+from dual_mod_public_amd import _lib as L  # noqa: E402
+from dual_mod_public_amd.config import DualModConfig  # noqa: E402
+from dual_mod_public_amd.decode import StaticTape  # noqa: E402
+from dual_mod_public_amd.engine import HipSweepCell, uniform_chunks  # noqa: E402
+from dual_mod_public_amd.rope import build_rope_cache  # noqa: E402
+from dual_mod_public_amd.synthetic import make_input, make_state_dict  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+# BASELINE config 2 (forward) — the 340M-shape DM layer
+C2 = dict(B=8, T=2048, d=1024, h=16, c=64, K=4, wseed=1, xseed=2)
+# BASELINE config 5 — incremental decode
+C5 = dict(B=64, d=1024, h=16, P0=32768, steps=256, wseed=3, xseed=4, tseed=5)
+
+
+def fwd_flops_per_token(d, T, c, K, ctx_mod="mult_res"):
+    """Algorithmic forward FLOPs per token of one DM layer (recompute excluded):
+    projections q,k,v,W_O + gate x-halves + v_gate (14 d^2), per sweep the packed
+    ctx/gate GEMM (8 d^2) and w_vctx (2 d^2), committed attention averaged over
+    chunks 2d(T-c), causal intra pairs 2d(c-1) and the raw-self column 4d per sweep."""
+    proj = 14 if ctx_mod != "linear" else 12
+    per_sweep = 10 if ctx_mod != "linear" else 8
+    return (proj + per_sweep * K) * d * d + 2 * d * (T - c) + 2 * K * d * (c - 1) + 4 * K * d
+
+
+def sweep1_flops(N, d):
+    """Useful FLOPs of one sweep GEMM 1 launch: N rows x (w_kctx, g_k u-half, v_map,
+    g_v u-half) = 4 d x d products."""
+    return 2.0 * N * d * 4 * d
+
+
+def build_layer(cfg, B, T, dev):
+    sd = make_state_dict(cfg, seed=C2["wseed"])
+    cell = HipSweepCell(cfg, B, T, device=dev, dtype=torch.bfloat16)
+    cell.pack({k: v.to(dev) for k, v in sd.items()})
+    x = make_input((B, T, cfg.d_model), seed=C2["xseed"]).to(dev, torch.bfloat16)
+    cos, sin = build_rope_cache(T, cfg.head_dim, cfg.rope_theta, device=dev)
+    bufs = cell.new_bufs(T)
+    K = torch.zeros(B, cfg.n_heads, T, cfg.head_dim, device=dev, dtype=torch.bfloat16)
+    V = torch.zeros_like(K)
+    ocat = torch.empty_like(x)
+    y = torch.empty_like(x)
+    return sd, cell, x, cos.contiguous(), sin.contiguous(), bufs, K, V, ocat, y
+
+
+def time_steps(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def cpu_baseline_fwd(cfg, sd, T, B):
+    """The oracle's chunked-Jacobi layer forward (same schedule, fp32) on the host."""
+    import oracle as O
+    nthr = os.cpu_count() or 1
+    nthr = min(nthr, 16)
+    torch.set_num_threads(nthr)
+    x = make_input((B, T, cfg.d_model), seed=C2["xseed"])
+    cos, sin = O.build_rope_cache(T, cfg.head_dim, cfg.rope_theta)
+    sched = O.uniform_chunks(T, C2["c"], C2["K"])
+    sdf = {k: v.float() for k, v in sd.items()}
+    with torch.no_grad():
+        t0 = time.perf_counter()
+        O.dm_layer(cfg, sdf, x, cos, sin, schedule=sched)
+        dt = time.perf_counter() - t0
+    return dict(value=B * T / dt, unit="tokens/s", cores=nthr, kind="port",
+                sample=f"one full layer forward at B={B}, T={T} (c=64, K=4), fp32 torch CPU, "
+                       f"{dt:.2f} s wall")
+
+
+def bench_decode(dev, steps_override=None):
+    cfg = DualModConfig(d_model=C5["d"], n_heads=C5["h"], ctx_mod="mult_res", max_seq_len=8,
+                        dtype="bf16")
+    B, P0 = C5["B"], C5["P0"]
+    steps = steps_override or C5["steps"]
+    P = P0 + steps
+    sd = make_state_dict(cfg, seed=C5["wseed"], with_attn_norm=False)
+    tape = StaticTape(cfg, B, P, dev, torch.bfloat16,
+                      sd={k: v.to(dev) for k, v in sd.items()})
+    g = torch.Generator(device=dev).manual_seed(C5["tseed"])
+    tape.K.normal_(generator=g)
+    tape.V.normal_(generator=g)
+    x = torch.randn(steps, B, cfg.d_model, generator=g, device=dev).to(torch.bfloat16)
+    cos, sin = build_rope_cache(P, cfg.head_dim, cfg.rope_theta, device=dev)
+    cos, sin = cos.contiguous(), sin.contiguous()
+    dh, h, d = cfg.head_dim, cfg.n_heads, cfg.d_model
+
+    def run_all():
+        for t in range(steps):
+            tape.step(x[t], P0 + t, cos, sin, with_wo=True)
+
+    # warm-up pass over the first few slots, then restore nothing (slots are rewritten)
+    for t in range(4):
+        tape.step(x[t], P0 + t, cos, sin, with_wo=True)
+    torch.cuda.synchronize()
+    with L.KernelTimer("dec_read", max_launches=steps + 8) as kt:
+        t0 = time.perf_counter()
+        run_all()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    tape_bytes = sum(2.0 * B * h * (P0 + t) * dh * 2 for t in range(steps))
+    weight_bytes = steps * 12.0 * d * d * 2
+    write_bytes = steps * 2.0 * B * d * 2
+    total = tape_bytes + weight_bytes + write_bytes
+    read_avg_s = kt.avg_ms / 1e3
+    read_bytes_per_launch = tape_bytes / steps
+    return {
+        "metric": "decode HBM GB/s (attend_one+refine_kv over the tape, append)",
+        "value": total / wall / 1e9, "unit": "GB/s", "steps": steps, "ms_per_step": wall / steps * 1e3,
+        "tokens_per_s": B * steps / wall,
+        "config": {"workload": "C5 decode: B=64, bf16 tape 32768..33023 positions, d=1024, 16x64",
+                   "algorithmic_bytes": total},
+        "roofline": {"bound": "hbm", "achieved": read_bytes_per_launch / read_avg_s / 1e9,
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": read_bytes_per_launch / read_avg_s / 1e9 / PEAK_HBM_GBS,
+                     "traffic": None, "kernel": "k_decode_partial",
+                     "avg_launch_ms": kt.avg_ms, "launches": kt.n},
+        "path_frac_of_hbm_peak": total / wall / 1e9 / PEAK_HBM_GBS,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-steps", type=int, default=0)
+    ap.add_argument("--kernel", default="sweep1", help="kernel class timed for the roofline")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the DM hot path is measured "
+                                   "on one MI355X (see the sharding notes); --gpus must be 1"}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    L.load()
+
+    B, T, d, h, c, K = C2["B"], C2["T"], C2["d"], C2["h"], C2["c"], C2["K"]
+    cfg = DualModConfig(d_model=d, n_heads=h, ctx_mod="mult_res", max_seq_len=T, dtype="bf16")
+    sd, cell, x, cos, sin, bufs, Kc, Vc, ocat, y = build_layer(cfg, B, T, dev)
+    sched = uniform_chunks(T, c, K)
+
+    def step():
+        cell.layer_forward(x, y, cos, sin, sched, Kc, Vc, ocat, bufs)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    sweeps = sum(k for _, _, k in sched)
+    with L.KernelTimer(args.kernel, max_launches=args.steps * sweeps * 2 + 64) as kt:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / args.steps
+    tokens = B * T
+    fpt = fwd_flops_per_token(d, T, c, K)
+    if args.kernel == "sweep1":
+        per_launch = sweep1_flops(B * c, d)
+        kname = "k_gemm_rs<EpiSweep1> (sweep GEMM 1: u . [w_kctx|g_k|v_map|g_v]^T)"
+    elif args.kernel == "layer":
+        per_launch = fpt * tokens
+        kname = "whole dm_layer_fwd call"
+    else:
+        per_launch = float("nan")
+        kname = args.kernel
+    achieved = per_launch / (kt.avg_ms / 1e3) / 1e12 if kt.n else None
+    out = {
+        "metric": "DM sweep tokens/s/GPU (c=64, K=4) — forward",
+        "value": tokens / dt, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": dt * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) x, N(0,0.02) weights)",
+        "config": {"workload": "C2: 340M-shape DM layer forward, B=8 T=2048 d=1024 16x64 c=64 K=4, "
+                               "32 chunks Gauss-Seidel",
+                   "global_batch": B, "seq_len": T, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": (achieved / PEAK_BF16_TFLOPS) if achieved else None,
+                     "traffic": None, "kernel": kname, "flops_per_launch": per_launch,
+                     "avg_launch_ms": kt.avg_ms, "launches": kt.n},
+        "path_roofline": {"flops_per_token": fpt, "achieved_tflops": fpt * tokens / dt / 1e12,
+                          "frac": fpt * tokens / dt / 1e12 / PEAK_BF16_TFLOPS},
+    }
+    if not args.no_decode:
+        del cell, bufs, Kc, Vc, ocat, y, x
+        torch.cuda.empty_cache()
+        out["decode"] = bench_decode(dev, args.decode_steps or None)
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_fwd(cfg, sd, T, B)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -76,7 +76,36 @@ SIGNATURES = {
                                       P(dm_decode_args), c_vp]),
     "dm_linear": (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp]),
     "dm_gemm_nt": (ctypes.c_int, [c_i32, c_vp, c_vp, c_fp, c_i32, c_i32, c_i32, c_vp]),
+    "dm_prof_start": (ctypes.c_int, [c_i32, c_i32]),
+    "dm_prof_stop": (ctypes.c_int, [P(ctypes.c_float), P(c_i32)]),
 }
+
+# kernel classes of dm_prof_start (include/dm_abi.h)
+PROF = {"proj": 1, "comm": 2, "attend": 3, "sweep1": 4, "sweep2": 5, "wo": 6, "dec_read": 7,
+        "dec_merge": 8, "dec_refine": 9, "bwd": 10, "layer": 11}
+
+
+class KernelTimer:
+    """Times every launch of one kernel class with HIP events (dm_prof_*)."""
+
+    def __init__(self, kernel_class, max_launches=8192):
+        self.cls = PROF[kernel_class] if isinstance(kernel_class, str) else int(kernel_class)
+        self.cap = max_launches
+        self.total_ms, self.n = 0.0, 0
+
+    def __enter__(self):
+        check(lib().dm_prof_start(self.cls, self.cap))
+        return self
+
+    def __exit__(self, *exc):
+        ms, n = ctypes.c_float(), c_i32()
+        check(lib().dm_prof_stop(ctypes.byref(ms), ctypes.byref(n)))
+        self.total_ms, self.n = float(ms.value), int(n.value)
+        return False
+
+    @property
+    def avg_ms(self):
+        return self.total_ms / max(self.n, 1)
 
 _lib = None
 _lib_err = None

@@ -9,6 +9,7 @@
 
 #include "../../include/dm_abi.h"
 #include "dm_kernels.h"
+#include "dm_prof.h"
 
 using namespace dm;
 
@@ -118,6 +119,7 @@ int run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int T
   EpiProj<T> epi{M, 64, c->d, c->h, c->dh, Tl, Tbuf, buf_t0, rope_t0, cos, sin, w->b_proj,
                  qr, kraw, kself, vraw, glogx, sig};
   ALoadPlain<T> al{xhat, c->d, M};
+  ProfScope ps(PROF_PROJ, s);
   launch_gemm<T, 64, 128, 2, 2>(al, (const T*)w->w_proj, c->d, M, nseg * c->d, c->d, epi, s);
   return DM_OK;
 }
@@ -144,6 +146,7 @@ int run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, con
     int split_len = cdiv(cdiv(pos0, nsplit), 64) * 64;
     nsplit = cdiv(pos0, split_len);
     CommArgs<T> ca{g, qr, Kc, Vc, split_len, scale, ws.Ap, ws.Zp, ws.Mp};
+    ProfScope ps(PROF_COMM, s);
     if (nsplit == 1) { ca.A = ws.A; ca.Z = ws.Z; ca.Mx = ws.M; }
     hipLaunchKernelGGL((k_comm_partial<T, DH>), dim3(nsplit, BH), dim3(256), 0, s, ca);
     if (nsplit > 1)
@@ -157,15 +160,22 @@ int run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, con
     const bool last = sw == n_sweeps - 1;
     AttendArgs<T> aa{g, qr, kself, vraw, Kc, Vc, A, Z, Mx, scale, ws.o, ws.ssq,
                      last ? ocat : nullptr, last ? o_last : nullptr};
-    hipLaunchKernelGGL((k_attend<T, DH>), dim3(BH), dim3(256), 0, s, aa);
+    {
+      ProfScope ps(PROF_ATTEND, s);
+      hipLaunchKernelGGL((k_attend<T, DH>), dim3(BH), dim3(256), 0, s, aa);
+    }
 
     ALoadRms<T, 64> al{ws.o, c->d, ws.ssq, c->h, (const T*)w->norm_ctx_w, N, c->d, c->rms_eps};
     EpiSweep1<T> e1{g, N, 64, c->ctx_mod, c->mult_res_lambda, kraw, vraw, L->glogx, L->sig, cos, sin,
                     ws.o, (const T*)w->norm_ctx_w, Kc, Vc, (T*)ws.vin, ws.gvu};
-    launch_gemm_rs<T, 64, 2 * DH, 2, 2>(al, (const T*)w->w_sweep, c->d, N, 4 * c->d, c->d, e1, s);
+    {
+      ProfScope ps(PROF_SWEEP1, s);
+      launch_gemm_rs<T, 64, 2 * DH, 2, 2>(al, (const T*)w->w_sweep, c->d, N, 4 * c->d, c->d, e1, s);
+    }
     if (!lin) {
       ALoadPlain<T> av{(const T*)ws.vin, c->d, N};
       EpiSweep2<T> e2{g, N, 64, vraw, L->glogx, ws.gvu, Vc};
+      ProfScope ps(PROF_SWEEP2, s);
       launch_gemm_rs<T, 64, DH, 2, 2>(av, (const T*)w->w_vctx, c->d, N, c->d, c->d, e2, s);
     }
   }
@@ -376,6 +386,7 @@ int dm_layer_fwd(const dm_config* c, const dm_packed* w, const void* x, void* y,
   }
   DM_REQUIRE(expect == L->T, DM_ERR_INVALID, "schedule covers %d positions, T=%d", expect, L->T);
   DM_REQUIRE(L->T <= cache_T, DM_ERR_INVALID, "T=%d > cache_T=%d", L->T, cache_T);
+  ProfScope whole(PROF_LAYER, S(stream));
   if ((rc = dm_layer_proj(c, w, x, cos, sin, L, stream))) return rc;
   for (int i = 0; i < n_cells; ++i) {
     dm_cell_args a{sched[3 * i], sched[3 * i + 1], sched[3 * i + 2], cache_T, K_cache, V_cache, ocat,
@@ -384,6 +395,7 @@ int dm_layer_fwd(const dm_config* c, const dm_packed* w, const void* x, void* y,
   }
   const int M = c->B * L->T;
   hipStream_t s = S(stream);
+  ProfScope ps(PROF_WO, s);
   if (c->dtype == DM_BF16) {
     ALoadPlain<bf16> al{(const bf16*)ocat, c->d, M};
     EpiResidual<bf16> ep{M, c->d, 64, (const bf16*)x, (bf16*)y};
@@ -443,9 +455,15 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
   DecodeArgs<T> da{B, h, d, a->tape_T, pos, lo, DEC_SPLIT, nsplit, 1.0f / sqrtf((float)DH),
                    (const T*)ws.q, (const T*)ws.kself, (const T*)ws.vraw, (const T*)a->K_tape,
                    (const T*)a->V_tape, ws.part, ws.o, ws.ssq, (T*)a->o_cat};
-  if (nsplit > 0)
+  if (nsplit > 0) {
+    ProfScope ps(PROF_DEC_READ, s);
     hipLaunchKernelGGL((k_decode_partial<T, DH, DEC_SPLIT>), dim3(nsplit, B * h), dim3(256), 0, s, da);
-  hipLaunchKernelGGL((k_decode_merge<T, DH>), dim3(B * h), dim3(64), 0, s, da);
+  }
+  {
+    ProfScope ps(PROF_DEC_MERGE, s);
+    hipLaunchKernelGGL((k_decode_merge<T, DH>), dim3(B * h), dim3(64), 0, s, da);
+  }
+  ProfScope ps(PROF_DEC_REFINE, s);
 
   // refine_kv for the B rows (c = 1, position pos), write slot pos of the tape
   CellGeom g{B, 1, d, h, DH, pos, 0, 1, a->tape_T};
@@ -492,6 +510,7 @@ int dm_decode_step(const dm_config* c, const dm_packed* w, const float* cos, con
              a->workspace_bytes, need.bytes);
   const DecWs ws = carve_dec(c, a->tape_T, a->workspace);
   hipStream_t s = S(stream);
+  ProfScope whole(PROF_LAYER, s);
   if (c->dtype == DM_BF16)
     rc = c->dh == 64 ? run_decode<bf16, 64>(c, w, cos, sin, a, ws, s) : run_decode<bf16, 128>(c, w, cos, sin, a, ws, s);
   else
@@ -540,6 +559,44 @@ int dm_gemm_nt(int32_t dtype, const void* A, const void* Bm, float* C, int32_t M
     return fail(DM_ERR_INVALID, "dtype %d", dtype);
   }
   DM_HIP(hipGetLastError());
+  return DM_OK;
+}
+
+}  // extern "C"
+
+// ---- optional per-kernel-class timing --------------------------------------------
+extern "C" {
+
+int dm_prof_start(int32_t kernel_class, int32_t max_launches) {
+  ProfState& p = prof();
+  DM_REQUIRE(p.armed == PROF_NONE, DM_ERR_INVALID, "timing already armed for class %d", p.armed);
+  DM_REQUIRE(kernel_class > PROF_NONE && kernel_class < PROF_NCLASS, DM_ERR_INVALID, "kernel class %d",
+             kernel_class);
+  DM_REQUIRE(max_launches > 0 && max_launches <= (1 << 16), DM_ERR_INVALID, "max_launches %d", max_launches);
+  if ((int)p.ev.size() < 2 * max_launches) {
+    const size_t have = p.ev.size();
+    p.ev.resize(2 * (size_t)max_launches);
+    for (size_t i = have; i < p.ev.size(); ++i) DM_HIP(hipEventCreate(&p.ev[i]));
+  }
+  p.cap = max_launches;
+  p.n = 0;
+  p.armed = kernel_class;
+  return DM_OK;
+}
+
+int dm_prof_stop(float* total_ms, int32_t* n_launches) {
+  ProfState& p = prof();
+  DM_REQUIRE(p.armed != PROF_NONE, DM_ERR_INVALID, "timing not armed");
+  p.armed = PROF_NONE;
+  float tot = 0.f;
+  for (int i = 0; i < p.n; ++i) {
+    DM_HIP(hipEventSynchronize(p.ev[2 * i + 1]));
+    float ms = 0.f;
+    DM_HIP(hipEventElapsedTime(&ms, p.ev[2 * i], p.ev[2 * i + 1]));
+    tot += ms;
+  }
+  if (total_ms) *total_ms = tot;
+  if (n_launches) *n_launches = p.n;
   return DM_OK;
 }
 

@@ -174,6 +174,17 @@ int dm_linear(int32_t dtype, const void* x, const void* W, const void* r, void* 
 int dm_gemm_nt(int32_t dtype, const void* A, const void* Bm, float* C, int32_t M, int32_t N,
                int32_t K, void* stream);
 
+/* ---- optional kernel timing (benchmarks) -------------------------------------
+ * No reference counterpart (the reference times with ad-hoc torch events,
+ * engines/wave3d/wave3d_x.py:28-33). Arms one kernel class; every later launch of
+ * that class (up to max_launches) is bracketed by HIP events on its own stream.
+ * dm_prof_stop waits for the recorded events and returns their summed duration.
+ * Classes: 1 projection, 2 committed accumulator, 3 sweep attention, 4 sweep GEMM 1,
+ * 5 sweep GEMM 2, 6 W_O, 7 decode tape read, 8 decode merge, 9 decode refine,
+ * 10 backward, 11 whole entry-point call. */
+int dm_prof_start(int32_t kernel_class, int32_t max_launches);
+int dm_prof_stop(float* total_ms, int32_t* n_launches);
+
 #ifdef __cplusplus
 }
 #endif
