@@ -36,7 +36,8 @@ class dm_params(ctypes.Structure):
 
 class dm_packed(ctypes.Structure):
     _fields_ = [(n, c_vp) for n in ("w_proj", "b_proj", "w_sweep", "w_vctx", "norm_ctx_w",
-                                    "attn_norm_w", "wo")]
+                                    "attn_norm_w", "wo", "w_proj_t", "w_sweep_t", "w_vctx_t",
+                                    "wo_t")]
 
 
 class dm_layer_bufs(ctypes.Structure):
@@ -75,7 +76,9 @@ SIGNATURES = {
     "dm_decode_step": (ctypes.c_int, [P(dm_config), P(dm_packed), c_fp, c_fp,
                                       P(dm_decode_args), c_vp]),
     "dm_linear": (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp]),
-    "dm_gemm_nt": (ctypes.c_int, [c_i32, c_vp, c_vp, c_fp, c_i32, c_i32, c_i32, c_vp]),
+    "dm_gemm": (ctypes.c_int, [c_i32, c_i32, c_i32, c_vp, c_vp, c_fp, c_i32, c_i32, c_i32, c_i32,
+                               c_vp]),
+    "dm_check_schedule": (ctypes.c_int, [P(c_i32), c_i32, c_i32]),
     "dm_prof_start": (ctypes.c_int, [c_i32, c_i32]),
     "dm_prof_stop": (ctypes.c_int, [P(ctypes.c_float), P(c_i32)]),
 }

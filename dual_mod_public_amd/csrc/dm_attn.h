@@ -61,22 +61,44 @@ DM_DEV void load_q_frags(const T* qrow_ptr, bool valid, typename Mfma<T>::frag* 
   }
 }
 
-// Stage keys [0, nvalid) of a tile: K rows -> Ks, V rows transposed -> Vt.
-// Rows >= nvalid are zero-filled (so 0-probability columns multiply zeros).
+// One key tile held in registers (global -> registers -> LDS, so the next tile's
+// loads can be in flight while the current tile is used).
+template <typename T, int DH> struct KVRegs {
+  static constexpr int VPR = DH / AttnCfg<T, DH>::VEC;             // 16-byte vectors per row
+  static constexpr int NV = AttnCfg<T, DH>::KT * VPR / 256;        // vectors per thread
+  uint4 k[NV], v[NV];
+};
+
+// Load keys [0, nvalid) of a tile; rows >= nvalid become zeros (so 0-probability
+// columns multiply zeros).
 template <typename T, int DH>
-DM_DEV void stage_kv(const T* __restrict__ Kg, const T* __restrict__ Vg, long row_stride,
-                     int nvalid, T* Ks, T* Vt) {
-  using C = AttnCfg<T, DH>;
-  constexpr int VPR = DH / C::VEC;            // 16-byte vectors per row
-  for (int v = threadIdx.x; v < C::KT * VPR; v += 256) {
-    int k = v / VPR, c0 = (v % VPR) * C::VEC;
-    uint4 kr = uint4{0u, 0u, 0u, 0u}, vr = uint4{0u, 0u, 0u, 0u};
+DM_DEV void load_kv(const T* __restrict__ Kg, const T* __restrict__ Vg, long row_stride, int nvalid,
+                    KVRegs<T, DH>& r) {
+  using R = KVRegs<T, DH>;
+#pragma unroll
+  for (int i = 0; i < R::NV; ++i) {
+    const int v = threadIdx.x + 256 * i;
+    const int k = v / R::VPR, c0 = (v % R::VPR) * AttnCfg<T, DH>::VEC;
+    r.k[i] = uint4{0u, 0u, 0u, 0u};
+    r.v[i] = uint4{0u, 0u, 0u, 0u};
     if (k < nvalid) {
-      kr = *reinterpret_cast<const uint4*>(Kg + (long)k * row_stride + c0);
-      vr = *reinterpret_cast<const uint4*>(Vg + (long)k * row_stride + c0);
+      r.k[i] = *reinterpret_cast<const uint4*>(Kg + (long)k * row_stride + c0);
+      r.v[i] = *reinterpret_cast<const uint4*>(Vg + (long)k * row_stride + c0);
     }
-    *reinterpret_cast<uint4*>(Ks + k * C::LDK + c0) = kr;
-    const T* ve = reinterpret_cast<const T*>(&vr);
+  }
+}
+
+// K rows -> Ks [key][dh], V rows transposed -> Vt [dh][key].
+template <typename T, int DH>
+DM_DEV void store_kv(const KVRegs<T, DH>& r, T* Ks, T* Vt) {
+  using C = AttnCfg<T, DH>;
+  using R = KVRegs<T, DH>;
+#pragma unroll
+  for (int i = 0; i < R::NV; ++i) {
+    const int v = threadIdx.x + 256 * i;
+    const int k = v / R::VPR, c0 = (v % R::VPR) * C::VEC;
+    *reinterpret_cast<uint4*>(Ks + k * C::LDK + c0) = r.k[i];
+    const T* ve = reinterpret_cast<const T*>(&r.v[i]);
 #pragma unroll
     for (int j = 0; j < C::VEC; ++j) Vt[(c0 + j) * C::LDV + k] = ve[j];
   }

@@ -1,0 +1,204 @@
+// Host-side launch sequences of the forward: layer projections and one chunk
+// cell (committed accumulator + n_sweeps Jacobi sweeps). Shared by the forward
+// entry points and by the backward's exact recompute (which keeps every sweep's
+// state in a CellSave instead of overwriting it in place).
+#pragma once
+
+#include "dm_host.h"
+
+namespace dm {
+
+// cell workspace (forward): per-sweep scratch reused across sweeps
+struct CellWs {
+  void* o; float* ssq;
+  float* Ap; float* Zp; float* Mp;   // committed split partials
+  float* A; float* Z; float* M;      // merged committed accumulator
+  void* vin; float* gvu;
+  size_t bytes;
+};
+
+inline CellWs carve_cell(const dm_config* c, int cache_T, void* base) {
+  CellWs w{};
+  const size_t N = (size_t)c->B * CMAX, BH = (size_t)c->B * c->h;
+  const size_t ns = comm_splits_max(cache_T);
+  Carver cv(base);
+  w.o = cv.take<void>(N * c->d * esz(c->dtype));
+  w.ssq = cv.take<float>(N * c->h * 4);
+  w.Ap = cv.take<float>(ns * BH * CMAX * c->dh * 4);
+  w.Zp = cv.take<float>(ns * BH * CMAX * 4);
+  w.Mp = cv.take<float>(ns * BH * CMAX * 4);
+  w.A = cv.take<float>(BH * CMAX * c->dh * 4);
+  w.Z = cv.take<float>(BH * CMAX * 4);
+  w.M = cv.take<float>(BH * CMAX * 4);
+  w.vin = cv.take<void>(N * c->d * esz(c->dtype));
+  w.gvu = cv.take<float>(N * c->d * 4);
+  w.bytes = cv.off;
+  return w;
+}
+
+// Every sweep's state of one cell, kept for the backward (strides are per sweep,
+// sized for N = B*CMAX rows and B*h*CMAX attention rows).
+template <typename T> struct CellSave {
+  T* o;              // [K][N, d]      o of sweep s (storage dtype, as stored by the attention)
+  float* ssq;        // [K][N, h]      per-head sums of squares of o
+  float* stat_m;     // [K][BH, CMAX]  final row max of sweep s
+  float* stat_z;     // [K][BH, CMAX]  final row sum of sweep s
+  float* save1;      // [K][N, 4d]     raw sweep GEMM 1 outputs
+  float* save2;      // [K][N, d]      raw v_ctx (mult family)
+  T* vin;            // [K][N, d]      v_in (mult family)
+  T* u;              // [K][N, d]      u = RMSNorm_ctx(o)
+  T* Kin; T* Vin;    // [K+1][BH, CMAX, DH]  intra rows read by sweep s (slot 0 unused: raw rows)
+};
+
+template <typename T, int DH>
+void run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int Tl, int Tbuf, int buf_t0,
+              int rope_t0, const float* cos, const float* sin, T* qr, T* kraw, T* kself, T* vraw,
+              float* glogx, float* sig, hipStream_t s) {
+  const int nseg = (c->ctx_mod == DM_CTX_LINEAR) ? 5 : 6;
+  EpiProj<T, DH> epi{M, c->d, c->h, Tl, Tbuf, buf_t0, rope_t0, cos, sin, w->b_proj,
+                     qr, kraw, kself, vraw, glogx, sig};
+  SrcRows<T> sa{xhat, c->d, M};
+  SrcRows<T> sb{(const T*)w->w_proj, c->d, nseg * c->d};
+  ProfScope ps(PROF_PROJ, s);
+  if constexpr (DH == 64)
+    launch_gemm<T, 128, 128, 2, 2, 4>(sa, sb, M, nseg * c->d, c->d, epi, s);
+  else
+    launch_gemm<T, 128, 128, 4, 1, 4>(sa, sb, M, nseg * c->d, c->d, epi, s);
+}
+
+template <typename T>
+void run_proj_dispatch(const dm_config* c, const dm_packed* w, const T* xhat, int M, int Tl, int Tbuf,
+                       int buf_t0, int rope_t0, const float* cos, const float* sin, T* qr, T* kraw, T* kself,
+                       T* vraw, float* glogx, float* sig, hipStream_t s) {
+  if (c->dh == 64)
+    run_proj<T, 64>(c, w, xhat, M, Tl, Tbuf, buf_t0, rope_t0, cos, sin, qr, kraw, kself, vraw, glogx, sig, s);
+  else
+    run_proj<T, 128>(c, w, xhat, M, Tl, Tbuf, buf_t0, rope_t0, cos, sin, qr, kraw, kself, vraw, glogx, sig, s);
+}
+
+// One sweep's refine: sweep GEMM 1 (+ GEMM 2 for the mult family) with the blend
+// epilogues, writing the refined rows to (Kout, Vout).
+template <typename T, int DH>
+void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N, const T* o, const float* ssq,
+                const T* kraw, const T* vraw, const float* glogx, const float* sig, const float* cos,
+                const float* sin, T* Kout, T* Vout, long out_stride, int out_row0, T* vin, float* gvu,
+                float* save1, float* save2, T* uout, hipStream_t s) {
+  const T* normw = (const T*)w->norm_ctx_w;
+  SrcRms<T> sa{o, c->d, N, ssq, c->h, normw, 1.0f / (float)c->d, c->rms_eps, uout};
+  SrcRows<T> sb{(const T*)w->w_sweep, c->d, 4 * c->d};
+  EpiSweep1<T, DH> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
+                      Kout, Vout, out_stride, out_row0, vin, gvu, save1};
+  {
+    ProfScope ps(PROF_SWEEP1, s);
+    launch_gemm<T, 64, 64, 4, 1, 4>(sa, sb, N, 4 * c->d, c->d, e1, s);
+  }
+  if (c->ctx_mod != DM_CTX_LINEAR) {
+    SrcRows<T> av{vin, c->d, N};
+    SrcRows<T> bv{(const T*)w->w_vctx, c->d, c->d};
+    EpiSweep2<T, DH> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2};
+    ProfScope ps(PROF_SWEEP2, s);
+    launch_gemm<T, 64, 64, 2, 2, 4>(av, bv, N, c->d, c->d, e2, s);
+  }
+}
+
+// Committed accumulator of a cell: split partials (merged by the first sweep's
+// attention) or, with one split, the merged state directly.
+template <typename T, int DH>
+int run_comm(const CellGeom& g, const T* qr, const T* Kc, const T* Vc, float scale, const CellWs& ws,
+             hipStream_t s) {
+  const CommPlan cp = comm_plan(g.pos0);
+  if (cp.nsplit == 0) return 0;
+  const int BH = g.B * g.h;
+  CommArgs<T> ca{g, qr, Kc, Vc, cp.split_len, scale, ws.Ap, ws.Zp, ws.Mp};
+  if (cp.nsplit == 1) { ca.A = ws.A; ca.Z = ws.Z; ca.Mx = ws.M; }
+  ProfScope ps(PROF_COMM, s);
+  hipLaunchKernelGGL((k_comm_partial<T, DH>), dim3(cp.nsplit, BH), dim3(256), 0, s, ca);
+  return cp.nsplit;
+}
+
+// One chunk cell [pos0, pos0+cc) of the layer: n_sweeps Jacobi sweeps against the
+// committed rows [0, pos0) of the cache. Without `sv` the sweeps refine the
+// chunk's cache rows in place and the last sweep leaves the final rows there;
+// with `sv` every sweep's rows and state are kept in sv (cache rows untouched).
+template <typename T, int DH>
+void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const float* cos,
+              const float* sin, int pos0, int cc, int n_sweeps, int buf_t0, int Tbuf, T* Kc, T* Vc,
+              int cache_T, T* ocat, float* o_last, const CellWs& ws, const CellSave<T>* sv, hipStream_t s) {
+  CellGeom g{c->B, cc, c->d, c->h, DH, pos0, buf_t0, Tbuf, cache_T};
+  const int BH = c->B * c->h;
+  const int N = c->B * cc;
+  const size_t Nmax = (size_t)c->B * CMAX, d = c->d;
+  const float scale = 1.0f / sqrtf((float)DH);
+  const T* qr = (const T*)L->qr;
+  const T* kself = (const T*)L->kself;
+  const T* vraw = (const T*)L->vraw;
+  const T* kraw = (const T*)L->kraw;
+  const int nsplit = run_comm<T, DH>(g, qr, Kc, Vc, scale, ws, s);
+  const long cache_stride = (long)cache_T * DH, ws_stride = (long)CMAX * DH;
+  const size_t slot = (size_t)BH * CMAX * DH;
+
+  for (int sw = 0; sw < n_sweeps; ++sw) {
+    const bool last = sw == n_sweeps - 1;
+    // intra rows read by this sweep
+    const T* Kin; const T* Vin; long in_stride; int in_row0;
+    if (sw == 0) { Kin = kself; Vin = vraw; in_stride = (long)Tbuf * DH; in_row0 = buf_t0; }
+    else if (sv) { Kin = sv->Kin + sw * slot; Vin = sv->Vin + sw * slot; in_stride = ws_stride; in_row0 = 0; }
+    else { Kin = Kc; Vin = Vc; in_stride = cache_stride; in_row0 = pos0; }
+    // rows written by this sweep's refine
+    T* Kout; T* Vout; long out_stride; int out_row0;
+    if (sv) { Kout = sv->Kin + (sw + 1) * slot; Vout = sv->Vin + (sw + 1) * slot; out_stride = ws_stride; out_row0 = 0; }
+    else { Kout = Kc; Vout = Vc; out_stride = cache_stride; out_row0 = pos0; }
+
+    T* o = sv ? sv->o + sw * Nmax * d : (T*)ws.o;
+    float* ssq = sv ? sv->ssq + sw * Nmax * c->h : ws.ssq;
+    AttendArgs<T> aa{g, qr, kself, vraw, Kin, Vin, in_stride, in_row0,
+                     sw == 0 ? nsplit : (nsplit > 0 ? 1 : 0), ws.Ap, ws.Zp, ws.Mp, ws.A, ws.Z, ws.M,
+                     scale, o, ssq, last ? ocat : nullptr, last ? o_last : nullptr,
+                     sv ? sv->stat_m + sw * (size_t)BH * CMAX : nullptr,
+                     sv ? sv->stat_z + sw * (size_t)BH * CMAX : nullptr};
+    {
+      ProfScope ps(PROF_ATTEND, s);
+      hipLaunchKernelGGL((k_attend<T, DH>), dim3(BH), dim3(256), 0, s, aa);
+    }
+    T* vin = sv ? sv->vin + sw * Nmax * d : (T*)ws.vin;
+    run_refine<T, DH>(c, w, g, N, o, ssq, kraw, vraw, L->glogx, L->sig, cos, sin, Kout, Vout, out_stride,
+                      out_row0, vin, ws.gvu, sv ? sv->save1 + sw * Nmax * 4 * d : nullptr,
+                      sv ? sv->save2 + sw * Nmax * d : nullptr, sv ? sv->u + sw * Nmax * d : nullptr, s);
+  }
+}
+
+template <typename T>
+void run_cell_dispatch(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const float* cos,
+                       const float* sin, int pos0, int cc, int n_sweeps, int buf_t0, int Tbuf, void* Kc,
+                       void* Vc, int cache_T, void* ocat, float* o_last, const CellWs& ws,
+                       const CellSave<T>* sv, hipStream_t s) {
+  if (c->dh == 64)
+    run_cell<T, 64>(c, w, L, cos, sin, pos0, cc, n_sweeps, buf_t0, Tbuf, (T*)Kc, (T*)Vc, cache_T, (T*)ocat,
+                    o_last, ws, sv, s);
+  else
+    run_cell<T, 128>(c, w, L, cos, sin, pos0, cc, n_sweeps, buf_t0, Tbuf, (T*)Kc, (T*)Vc, cache_T, (T*)ocat,
+                     o_last, ws, sv, s);
+}
+
+inline int check_bufs(const dm_config* c, const dm_layer_bufs* L) {
+  DM_REQUIRE(L != nullptr, DM_ERR_INVALID, "null layer buffers");
+  DM_REQUIRE(L->T > 0, DM_ERR_INVALID, "layer buffer T=%d", L->T);
+  DM_REQUIRE(L->qr && L->kraw && L->kself && L->vraw && L->glogx, DM_ERR_INVALID, "null layer buffer");
+  DM_REQUIRE(aligned16(L->qr) && aligned16(L->kraw) && aligned16(L->kself) && aligned16(L->vraw),
+             DM_ERR_INVALID, "layer buffers must be 16-byte aligned");
+  DM_REQUIRE(c->ctx_mod == DM_CTX_LINEAR || L->sig != nullptr, DM_ERR_INVALID,
+             "ctx_mod mult/mult_res needs the sig buffer");
+  return DM_OK;
+}
+
+inline int check_packed(const dm_config* c, const dm_packed* w) {
+  DM_REQUIRE(w != nullptr, DM_ERR_INVALID, "null packed weights");
+  DM_REQUIRE(w->w_proj && w->b_proj && w->w_sweep && w->norm_ctx_w, DM_ERR_INVALID, "null packed weight");
+  DM_REQUIRE(c->ctx_mod == DM_CTX_LINEAR || w->w_vctx, DM_ERR_INVALID, "mult family needs w_vctx");
+  DM_REQUIRE(aligned16(w->w_proj) && aligned16(w->w_sweep) && aligned16(w->norm_ctx_w) &&
+                 (w->w_vctx == nullptr || aligned16(w->w_vctx)),
+             DM_ERR_INVALID, "packed weights must be 16-byte aligned");
+  return DM_OK;
+}
+
+}  // namespace dm

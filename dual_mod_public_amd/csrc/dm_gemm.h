@@ -1,11 +1,21 @@
-// MFMA GEMM mainloop: C[BM x BN] = A[BM x K] . B[BN x K]^T  (both K-contiguous).
+// MFMA GEMM core: C[BM x BN] = A[BM x K] . B[BN x K]^T with fp32 accumulation.
 //
 // 256 threads = 4 waves arranged WM x WN; each wave owns a (BM/WM) x (BN/WN)
-// sub-tile made of 16x16 MFMA tiles. A and B k-tiles are staged through LDS
-// (one buffer, next tile prefetched into registers while the current one
-// feeds the MFMAs). After the k-loop the fp32 accumulators are written to an
-// LDS tile so the epilogue can read any (row, col) pattern it needs (RoPE
-// pairs, gate/candidate column pairs, per-head reductions).
+// sub-tile of 16x16 MFMA tiles, kept in registers. Operands are staged through
+// two LDS buffers (one barrier per k-tile) and fed from a ring of D register
+// stages, so the global loads of k-tile kt+D are in flight while tiles
+// kt..kt+D-1 are consumed: the small-M sweep GEMMs (M = B*c rows) have little
+// compute per k-tile and are otherwise bound by load latency.
+//
+// Operand sources describe a logical row-major [rows x K] operand:
+//   SrcRows   element (r, k) at p[r*ld + k]   (K contiguous; 16-byte vector loads along k)
+//   SrcRms    SrcRows scaled on the way into LDS: u = o * rs[r] * w[k]  (RMSNorm of o)
+//   SrcKMajor element (r, k) at p[k*ld + r]   (rows contiguous; vectors along r,
+//                                              transposed on the way into LDS)
+// After the k-loop the epilogue functor receives the wave's accumulators:
+// lane l holds rows 16i + 4(l>>4) + q (q = 0..3) of column 16j + (l & 15) of the
+// wave tile, so head-aligned wave tiles keep RoPE pairs and gate/candidate
+// columns in one lane.
 #pragma once
 
 #include "dm_common.h"
@@ -15,144 +25,180 @@ namespace dm {
 template <typename T> struct GemmTraits {
   static constexpr int BK = (sizeof(T) == 2) ? 64 : 32;   // k per LDS tile
   static constexpr int PAD = 16 / (int)sizeof(T);          // 16-byte row pad
-  static constexpr int VEC = 16 / (int)sizeof(T);          // elems per 16 B
+  static constexpr int VEC = 16 / (int)sizeof(T);          // elements per 16 B
   static constexpr int LDK = BK + PAD;
 };
 
-// ---- A-operand loaders: 16 bytes of row m, columns [k, k+VEC) -------------
-template <typename T> struct ALoadPlain {
-  const T* A;
-  long lda;
-  int M;
-  DM_DEV void prepare(int, float*) const {}
-  DM_DEV uint4 load(int m, int k, const float*) const {
-    if (m >= M) return uint4{0u, 0u, 0u, 0u};
-    return *reinterpret_cast<const uint4*>(A + (long)m * lda + k);
+DM_DEV uint4 zero_u4() { return uint4{0u, 0u, 0u, 0u}; }
+
+template <typename T> struct SrcRows {
+  static constexpr bool KMAJOR = false;
+  const T* __restrict__ p;
+  long ld;
+  int rows;   // valid rows (global index bound)
+  DM_DEV uint4 load(int r, int k) const {
+    return r < rows ? *reinterpret_cast<const uint4*>(p + (long)r * ld + k) : zero_u4();
   }
+  DM_DEV uint4 xform(uint4 v, int, int, const float*, int) const { return v; }
 };
 
-// u = o * rs[m] * w[k]: RMSNorm applied on the fly to an fp32 row-major
-// matrix o [M, ldo]; rs is computed per tile row from per-head partial sums
-// of squares ssq [M, nparts] (rs = rsqrt(sum/d + eps)).
-template <typename T, int BM> struct ALoadRms {
-  const float* o;
-  long ldo;
-  const float* ssq;
+constexpr int RMS_MAXR = 128;     // row-scale slots in LDS (>= BM of any RMS-sourced GEMM)
+constexpr int RMS_MAXK = 4096;    // norm-weight elements staged in LDS (>= K of any RMS-sourced GEMM)
+
+// u[r, k] = o[r, k] * rs[r] * w[k], rs = rsqrt(sum_p ssq[r, p] / d + eps); o in storage dtype.
+template <typename T> struct SrcRms {
+  static constexpr bool KMAJOR = false;
+  const T* __restrict__ p;           // o [rows, ld]
+  long ld;
+  int rows;
+  const float* __restrict__ ssq;     // [rows, nparts] partial sums of squares
   int nparts;
-  const T* w;
-  int M;
-  int d;
-  float eps;
-  DM_DEV void prepare(int m0, float* rs_lds) const {
-    for (int i = threadIdx.x; i < BM; i += blockDim.x) {
-      int m = m0 + i;
+  const T* __restrict__ w;           // norm weight [K]
+  float inv_d, eps;
+  T* __restrict__ uout;              // optional: u rows [rows, ld] written by the blocks of column 0
+  // per-row scales of the tile's rows into rs_lds[0..R), the norm weight into w_lds[0..K)
+  template <int R> DM_DEV void prepare_rows(int r0, float* rs_lds, T* w_lds, int K) const {
+    for (int i = threadIdx.x; i < R; i += 256) {
+      const int r = r0 + i;
       float s = 0.f;
-      if (m < M)
-        for (int p = 0; p < nparts; ++p) s += ssq[(long)m * nparts + p];
-      rs_lds[i] = rsqrtf(s / (float)d + eps);
+      if (r < rows)
+        for (int q = 0; q < nparts; ++q) s += ssq[(long)r * nparts + q];
+      rs_lds[i] = rsqrtf(s * inv_d + eps);
     }
-  }
-  DM_DEV uint4 load(int m, int k, const float* rs_lds_rel) const {
     constexpr int V = GemmTraits<T>::VEC;
-    float f[V];
-    if (m >= M) {
+    for (int i = threadIdx.x * V; i < K; i += 256 * V)
+      *reinterpret_cast<uint4*>(w_lds + i) = *reinterpret_cast<const uint4*>(w + i);
+  }
+  DM_DEV uint4 load(int r, int k) const {
+    return r < rows ? *reinterpret_cast<const uint4*>(p + (long)r * ld + k) : zero_u4();
+  }
+  DM_DEV uint4 xform(uint4 v, int rloc, int k, const float* rs_lds, int r0) const {
+    constexpr int V = GemmTraits<T>::VEC;
+    float f[V], wf[V];
+    unpack16<T>(v, f);
+    const T* w_lds = reinterpret_cast<const T*>(rs_lds + RMS_MAXR);
+    unpack16<T>(*reinterpret_cast<const uint4*>(w_lds + k), wf);
+    const float r = rs_lds[rloc];
 #pragma unroll
-      for (int j = 0; j < V; ++j) f[j] = 0.f;
-    } else {
-      const float r = rs_lds_rel[0];
-      const float* src = o + (long)m * ldo + k;
-      float wf[V];
-      unpack16<T>(*reinterpret_cast<const uint4*>(w + k), wf);
-#pragma unroll
-      for (int j = 0; j < V; j += 4) {
-        float4 v = *reinterpret_cast<const float4*>(src + j);
-        f[j] = v.x * r * wf[j];
-        f[j + 1] = v.y * r * wf[j + 1];
-        f[j + 2] = v.z * r * wf[j + 2];
-        f[j + 3] = v.w * r * wf[j + 3];
-      }
-    }
-    return pack16<T>(f);
+    for (int j = 0; j < V; ++j) f[j] = f[j] * r * wf[j];
+    const uint4 u = pack16<T>(f);
+    if (uout != nullptr && blockIdx.x == 0 && r0 + rloc < rows)
+      *reinterpret_cast<uint4*>(uout + (long)(r0 + rloc) * ld + k) = u;
+    return u;
   }
 };
 
-template <typename T, int BM, int BN>
+template <typename T> struct SrcKMajor {
+  static constexpr bool KMAJOR = true;
+  const T* __restrict__ p;   // element (r, k) at p[k*ld + r]
+  long ld;
+  int rows;
+  DM_DEV uint4 load(int r, int k) const {   // VEC consecutive rows r.. at column k
+    return r < rows ? *reinterpret_cast<const uint4*>(p + (long)k * ld + r) : zero_u4();
+  }
+  DM_DEV uint4 xform(uint4 v, int, int, const float*, int) const { return v; }
+};
+
+template <class S> struct requires_prepare { static constexpr bool value = false; };
+template <typename T> struct requires_prepare<SrcRms<T>> { static constexpr bool value = true; };
+
+// 2 operand stages + (RMS sources) row scales and the norm weight
+template <typename T, int BM, int BN, bool RMS>
 constexpr int gemm_lds_bytes() {
-  constexpr int ab = (BM + BN) * GemmTraits<T>::LDK * (int)sizeof(T);
-  constexpr int c = BM * (BN + 4) * 4;
-  constexpr int body = ab > c ? ab : c;
-  return body + BM * 4;   // + per-row scale scratch
+  return 2 * (BM + BN) * GemmTraits<T>::LDK * (int)sizeof(T) +
+         (RMS ? RMS_MAXR * 4 + RMS_MAXK * (int)sizeof(T) : BM * 4);
 }
 
-// Runs the k-loop for the tile at (m0, n0) and leaves the fp32 result in
-// Cs[BM][BN+4] (LDS). Must be called by all 256 threads.
-template <typename T, int BM, int BN, int WM, int WN, class AL>
-DM_DEV void gemm_tile(const AL& al, const T* __restrict__ Bw, long ldb, int K, int m0,
-                      int n0, char* smem, float*& Cs_out) {
+// Wave tile geometry of a (BM, BN, WM, WN) block.
+template <int BM, int BN, int WM, int WN> struct WaveTile {
+  static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
+  static_assert(WM * WN == 4, "4 waves per block");
+  static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be whole 16x16 MFMA tiles");
+};
+
+// The k-loop. acc must be zero-initialised by the caller (or hold a C to add to).
+template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB>
+DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, char* smem,
+                          floatx4 (&acc)[WaveTile<BM, BN, WM, WN>::FM][WaveTile<BM, BN, WM, WN>::FN]) {
   using Tr = GemmTraits<T>;
   using MF = Mfma<T>;
+  using WT = WaveTile<BM, BN, WM, WN>;
   constexpr int BK = Tr::BK, LDK = Tr::LDK, VEC = Tr::VEC;
-  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
-  constexpr int VPR = BK / VEC;                 // 16-byte vectors per tile row
-  constexpr int NA = BM * VPR / 256, NB = BN * VPR / 256;
-  static_assert(WM * WN == 4, "4 waves");
-  static_assert(BM * VPR % 256 == 0 && BN * VPR % 256 == 0, "tile/threads");
-  static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile");
+  constexpr int FM = WT::FM, FN = WT::FN, TM = WT::TM, TN = WT::TN;
+  constexpr int NA = BM * BK / VEC / 256, NB = BN * BK / VEC / 256;
+  static_assert(BM * BK / VEC % 256 == 0 && BN * BK / VEC % 256 == 0, "tile/threads");
 
-  T* As = reinterpret_cast<T*>(smem);
-  T* Bs = As + BM * LDK;
-  float* Cs = reinterpret_cast<float*>(smem);
-  float* rs = reinterpret_cast<float*>(smem + (gemm_lds_bytes<T, BM, BN>() - BM * 4));
+  T* buf[2];
+  buf[0] = reinterpret_cast<T*>(smem);
+  buf[1] = buf[0] + (BM + BN) * LDK;
+  float* rs_lds = reinterpret_cast<float*>(smem + 2 * (BM + BN) * LDK * sizeof(T));
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  al.prepare(m0, rs);
-  __syncthreads();
+  // per-operand vector coordinates (fixed over k-tiles)
+  auto coordA = [&](int i, int& r, int& kc) {
+    const int v = tid + i * 256;
+    if constexpr (SA::KMAJOR) { r = (v % (BM / VEC)) * VEC; kc = v / (BM / VEC); }
+    else { r = v / (BK / VEC); kc = (v % (BK / VEC)) * VEC; }
+  };
+  auto coordB = [&](int i, int& r, int& kc) {
+    const int v = tid + i * 256;
+    if constexpr (SB::KMAJOR) { r = (v % (BN / VEC)) * VEC; kc = v / (BN / VEC); }
+    else { r = v / (BK / VEC); kc = (v % (BK / VEC)) * VEC; }
+  };
 
-  floatx4 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = zero4();
-
-  uint4 ra[NA], rb[NB];
-  auto gload = [&](int k0) {
+  uint4 ra[D][NA], rb[D][NB];
+  auto gload = [&](int kt, uint4 (&xa)[NA], uint4 (&xb)[NB]) {
+    const int k0 = kt * BK;
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
-      int v = tid + i * 256;
-      int r = v / VPR, kc = (v % VPR) * VEC;
-      ra[i] = al.load(m0 + r, k0 + kc, rs + r);
+      int r, kc;
+      coordA(i, r, kc);
+      xa[i] = sa.load(m0 + r, k0 + kc);
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      int v = tid + i * 256;
-      int r = v / VPR, kc = (v % VPR) * VEC;
-      rb[i] = *reinterpret_cast<const uint4*>(Bw + (long)(n0 + r) * ldb + k0 + kc);
+      int r, kc;
+      coordB(i, r, kc);
+      xb[i] = sb.load(n0 + r, k0 + kc);
     }
   };
-  auto sstore = [&]() {
+  auto sstore = [&](int kt, T* dst, const uint4 (&xa)[NA], const uint4 (&xb)[NB]) {
+    const int k0 = kt * BK;
+    T* As = dst;
+    T* Bs = dst + BM * LDK;
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
-      int v = tid + i * 256;
-      int r = v / VPR, kc = (v % VPR) * VEC;
-      *reinterpret_cast<uint4*>(As + r * LDK + kc) = ra[i];
+      int r, kc;
+      coordA(i, r, kc);
+      const uint4 v = sa.xform(xa[i], r, k0 + kc, rs_lds, m0);
+      if constexpr (SA::KMAJOR) {
+        const T* e = reinterpret_cast<const T*>(&v);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) As[(r + j) * LDK + kc] = e[j];
+      } else {
+        *reinterpret_cast<uint4*>(As + r * LDK + kc) = v;
+      }
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      int v = tid + i * 256;
-      int r = v / VPR, kc = (v % VPR) * VEC;
-      *reinterpret_cast<uint4*>(Bs + r * LDK + kc) = rb[i];
+      int r, kc;
+      coordB(i, r, kc);
+      const uint4 v = xb[i];
+      if constexpr (SB::KMAJOR) {
+        const T* e = reinterpret_cast<const T*>(&v);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) Bs[(r + j) * LDK + kc] = e[j];
+      } else {
+        *reinterpret_cast<uint4*>(Bs + r * LDK + kc) = v;
+      }
     }
   };
-
-  const int nk = K / BK;
-  gload(0);
-  sstore();
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) gload((kt + 1) * BK);
+  auto compute = [&](const T* src) {
+    const T* As = src;
+    const T* Bs = src + BM * LDK;
 #pragma unroll
     for (int kk = 0; kk < BK; kk += MF::KSTEP) {
       typename MF::frag af[FM], bfr[FN];
@@ -167,35 +213,53 @@ DM_DEV void gemm_tile(const AL& al, const T* __restrict__ Bw, long ldb, int K, i
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = MF::mma(af[i], bfr[j], acc[i][j]);
     }
-    __syncthreads();
-    if (kt + 1 < nk) {
-      sstore();
-      __syncthreads();
+  };
+
+  const int nk = K / BK;
+#pragma unroll
+  for (int s = 0; s < D; ++s)
+    if (s < nk) gload(s, ra[s], rb[s]);
+  sstore(0, buf[0], ra[0], rb[0]);
+  __syncthreads();
+  for (int kt0 = 0; kt0 < nk; kt0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int kt = kt0 + j;
+      if (kt < nk) {
+        // slot j (tile kt) is already in LDS: refill it with tile kt + D
+        if (kt + D < nk) gload(kt + D, ra[j], rb[j]);
+        compute(buf[kt & 1]);
+        if (kt + 1 < nk) sstore(kt + 1, buf[(kt + 1) & 1], ra[(j + 1) % D], rb[(j + 1) % D]);
+        __syncthreads();
+      }
     }
   }
-  // accumulators -> LDS tile (aliases As/Bs; the loop ended on a barrier)
-  constexpr int LDC = BN + 4;
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        Cs[(wm * TM + i * 16 + 4 * (lane >> 4) + r) * LDC + wn * TN + j * 16 + (lane & 15)] =
-            acc[i][j][r];
-  __syncthreads();
-  Cs_out = Cs;
 }
 
-// Generic kernel: tile -> epilogue functor epi(Cs, LDC, m0, n0).
-template <typename T, int BM, int BN, int WM, int WN, class AL, class EPI>
-__global__ __launch_bounds__(256) void k_gemm(AL al, const T* __restrict__ Bw, long ldb, int K,
-                                              EPI epi) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];
+// Generic kernel: zero accumulators, k-loop, epilogue on the wave's registers.
+// epi(acc, row0, col0) with row0/col0 the global origin of the wave tile.
+template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
+__global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi) {
+  using WT = WaveTile<BM, BN, WM, WN>;
+  constexpr bool RMS = requires_prepare<SA>::value;
+  __shared__ __attribute__((aligned(16))) char smem[gemm_lds_bytes<T, BM, BN, RMS>()];
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  float* Cs;
-  gemm_tile<T, BM, BN, WM, WN, AL>(al, Bw, ldb, K, m0, n0, smem, Cs);
-  epi(Cs, BN + 4, m0, n0);
+  if constexpr (RMS) {
+    static_assert(BM <= RMS_MAXR, "row-scale slots");
+    float* rs = reinterpret_cast<float*>(smem + 2 * (BM + BN) * GemmTraits<T>::LDK * sizeof(T));
+    sa.template prepare_rows<BM>(m0, rs, reinterpret_cast<T*>(rs + RMS_MAXR), K);
+    __syncthreads();
+  }
+  floatx4 acc[WT::FM][WT::FN];
+#pragma unroll
+  for (int i = 0; i < WT::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < WT::FN; ++j) acc[i][j] = zero4();
+  gemm_mainloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc);
+  const int wave = threadIdx.x >> 6;
+  epi(acc, m0 + (wave / WN) * WT::TM, n0 + (wave % WN) * WT::TN,
+      reinterpret_cast<const float*>(smem + 2 * (BM + BN) * GemmTraits<T>::LDK * sizeof(T)) +
+          (wave / WN) * WT::TM);
 }
 
 }  // namespace dm

@@ -1,0 +1,103 @@
+// Host-side helpers shared by the translation units of libdm_hip.so:
+// error reporting, argument checks, launch helpers, workspace carving.
+#pragma once
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/dm_abi.h"
+#include "dm_kernels.h"
+#include "dm_prof.h"
+
+namespace dm {
+
+inline std::string& last_error() {
+  static thread_local std::string e;
+  return e;
+}
+
+inline int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+inline int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  last_error() = buf;
+  return code;
+}
+
+#define DM_REQUIRE(cond, code, ...)                  \
+  do {                                               \
+    if (!(cond)) return ::dm::fail(code, __VA_ARGS__); \
+  } while (0)
+
+#define DM_HIP(call)                                                                             \
+  do {                                                                                           \
+    hipError_t e_ = (call);                                                                      \
+    if (e_ != hipSuccess) return ::dm::fail(DM_ERR_HIP, "%s: %s", #call, hipGetErrorString(e_)); \
+  } while (0)
+
+inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+inline size_t esz(int dtype) { return dtype == DM_BF16 ? 2 : 4; }
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+inline int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+constexpr int CMAX = 64;              // max chunk length of one cell
+constexpr int COMM_SPLIT_MIN = 256;   // committed keys per split (lower bound)
+constexpr int COMM_MAX_SPLITS = 16;
+constexpr int DEC_SPLIT = 512;        // tape keys per decode split
+
+inline int check_cfg(const dm_config* c) {
+  DM_REQUIRE(c != nullptr, DM_ERR_INVALID, "null config");
+  DM_REQUIRE(c->dtype == DM_F32 || c->dtype == DM_BF16, DM_ERR_INVALID, "dtype %d", c->dtype);
+  DM_REQUIRE(c->B > 0 && c->d > 0 && c->h > 0 && c->dh > 0, DM_ERR_INVALID, "non-positive dims");
+  DM_REQUIRE(c->d == c->h * c->dh, DM_ERR_INVALID, "d=%d != h*dh=%d", c->d, c->h * c->dh);
+  DM_REQUIRE(c->dh == 64 || c->dh == 128, DM_ERR_UNSUPPORTED, "head_dim %d (64 or 128)", c->dh);
+  DM_REQUIRE(c->d % (2 * c->dh) == 0 && c->d % 128 == 0, DM_ERR_UNSUPPORTED,
+             "d_model %d must be a multiple of 128 and of 2*head_dim", c->d);
+  DM_REQUIRE(c->d <= RMS_MAXK, DM_ERR_UNSUPPORTED, "d_model %d > %d", c->d, RMS_MAXK);
+  DM_REQUIRE(c->ctx_mod >= 0 && c->ctx_mod <= 2, DM_ERR_UNSUPPORTED, "ctx_mod %d", c->ctx_mod);
+  DM_REQUIRE(c->local_window >= 0, DM_ERR_INVALID, "local_window %d", c->local_window);
+  return DM_OK;
+}
+
+// committed-prefix split plan for a cell at pos0
+struct CommPlan {
+  int nsplit, split_len;
+};
+inline CommPlan comm_plan(int pos0) {
+  if (pos0 <= 0) return CommPlan{0, 0};
+  int nsplit = cdiv(pos0, COMM_SPLIT_MIN);
+  if (nsplit > COMM_MAX_SPLITS) nsplit = COMM_MAX_SPLITS;
+  const int split_len = cdiv(cdiv(pos0, nsplit), 64) * 64;
+  return CommPlan{cdiv(pos0, split_len), split_len};
+}
+inline int comm_splits_max(int cache_T) {
+  int n = cdiv(cache_T, COMM_SPLIT_MIN);
+  return n < 1 ? 1 : (n > COMM_MAX_SPLITS ? COMM_MAX_SPLITS : n);
+}
+
+// bump allocator over a caller-provided workspace (base == nullptr: size query)
+struct Carver {
+  char* base;
+  size_t off = 0;
+  explicit Carver(void* b) : base(reinterpret_cast<char*>(b)) {}
+  template <typename P> P* take(size_t bytes) {
+    char* r = base ? base + off : nullptr;
+    off += align256(bytes);
+    return reinterpret_cast<P*>(r);
+  }
+};
+
+// GEMM launch: grid (N/BN, ceil(M/BM)), 256 threads
+template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
+void launch_gemm(const SA& sa, const SB& sb, int M, int N, int K, const EPI& epi, hipStream_t s) {
+  dim3 grid(N / BN, cdiv(M, BM));
+  hipLaunchKernelGGL((k_gemm<T, BM, BN, WM, WN, D, SA, SB, EPI>), grid, dim3(256), 0, s, sa, sb, K, epi);
+}
+
+}  // namespace dm

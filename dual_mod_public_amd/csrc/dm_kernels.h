@@ -1,4 +1,4 @@
-// Kernels of the DM forward cell, layer projection and decode step.
+// Kernels of the DM forward cell and the layer projection pass.
 #pragma once
 
 #include "dm_attn.h"
@@ -45,6 +45,23 @@ __global__ void k_to_f32(const T* __restrict__ src, float* __restrict__ dst, int
   if (i < n) dst[i] = to_f(src[i]);
 }
 
+// out [cols, rows] = in [rows, cols]^T, 64x64 tiles through LDS
+template <typename T>
+__global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ in, T* __restrict__ out, int rows,
+                                                   int cols) {
+  __shared__ T tile[64][65];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int r = i / 64, cc = i % 64;
+    if (r0 + r < rows && c0 + cc < cols) tile[r][cc] = in[(long)(r0 + r) * cols + c0 + cc];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int cc = i / 64, r = i % 64;
+    if (r0 + r < rows && c0 + cc < cols) out[(long)(c0 + cc) * rows + r0 + r] = tile[r][cc];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // row RMSNorm (attn_norm, models/dualmod/attention.py:74-83): one wave per row
 // ---------------------------------------------------------------------------
@@ -68,71 +85,72 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const T* __restrict__ x, c
 
 // ---------------------------------------------------------------------------
 // projection epilogue: xhat . [wq | wk | wv | w_gk_x | w_gv_x | v_gate]^T
+// (fused_sweep.py:1403-1436 hoists; rope.py:22-33 on q and the raw key).
+// Wave tiles are one head wide (TN == DH) so RoPE pairs (j, j + DH/2) sit in
+// accumulator tiles j and j + FN/2 of the same lane.
 // ---------------------------------------------------------------------------
-template <typename T> struct EpiProj {
-  int M, bm, d, h, dh;
+template <typename T, int DH> struct EpiProj {
+  int M, d, h;
   int Tl;        // rows per batch element in this call
   int Tbuf;      // T of the destination head buffers
   int buf_t0;    // buffer row of local row 0
   int rope_t0;   // RoPE position of local row 0
-  const float* cos;
-  const float* sin;
-  const float* bias;   // [3d] fp32
-  T* qr; T* kraw; T* kself; T* vraw;
-  float* glogx; float* sig;
-  DM_DEV void operator()(const float* Cs, int ldc, int m0, int n0) const {
-    const int bn = ldc - 4;
-    const int seg = n0 / d, j0 = n0 - seg * d;
-    const int half = dh / 2;
-    if (seg <= 1) {
-      const int nh = bn / dh;
-      for (int it = threadIdx.x; it < bm * nh * half; it += 256) {
-        const int r = it / (nh * half), rem = it - r * nh * half;
-        const int hi = rem / half, jj = rem - hi * half;
-        const int m = m0 + r;
+  const float* __restrict__ cos;
+  const float* __restrict__ sin;
+  const float* __restrict__ bias;   // [3d] fp32
+  T* __restrict__ qr; T* __restrict__ kraw; T* __restrict__ kself; T* __restrict__ vraw;
+  float* __restrict__ glogx; float* __restrict__ sig;
+
+  template <int FM, int FN>
+  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
+    static_assert(FN * 16 == DH, "projection wave tile must be one head wide");
+    constexpr int HF = FN / 2;
+    const int lane = threadIdx.x & 63, lc = lane & 15;
+    const int seg = col0 / d, c0 = col0 - seg * d;
+    const int hh = c0 / DH;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
         if (m >= M) continue;
         const int b = m / Tl, tl = m - b * Tl;
-        const int hh = j0 / dh + hi;
-        const float a = Cs[r * ldc + hi * dh + jj], bb = Cs[r * ldc + hi * dh + jj + half];
-        const float c = cos[(long)(rope_t0 + tl) * half + jj], s = sin[(long)(rope_t0 + tl) * half + jj];
-        const long off = (((long)b * h + hh) * Tbuf + buf_t0 + tl) * dh;
-        if (seg == 0) {
-          qr[off + jj] = from_f<T>(a * c - bb * s);
-          qr[off + jj + half] = from_f<T>(bb * c + a * s);
+        const long hrow = (((long)b * h + hh) * Tbuf + buf_t0 + tl) * DH;
+        const long xrow = (long)b * Tbuf + buf_t0 + tl;
+        if (seg <= 1) {
+          const long rrow = (long)(rope_t0 + tl) * (DH / 2);
+#pragma unroll
+          for (int j = 0; j < HF; ++j) {
+            const int jj = 16 * j + lc;
+            const float a = acc[i][j][q], bb = acc[i][j + HF][q];
+            const float cs = cos[rrow + jj], sn = sin[rrow + jj];
+            if (seg == 0) {
+              qr[hrow + jj] = from_f<T>(a * cs - bb * sn);
+              qr[hrow + jj + DH / 2] = from_f<T>(bb * cs + a * sn);
+            } else {
+              kraw[hrow + jj] = from_f<T>(a);
+              kraw[hrow + jj + DH / 2] = from_f<T>(bb);
+              kself[hrow + jj] = from_f<T>(a * cs - bb * sn);
+              kself[hrow + jj + DH / 2] = from_f<T>(bb * cs + a * sn);
+            }
+          }
+        } else if (seg == 2) {
+#pragma unroll
+          for (int j = 0; j < FN; ++j) vraw[hrow + 16 * j + lc] = from_f<T>(acc[i][j][q]);
+        } else if (seg <= 4) {
+          const int gs = seg - 3;
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            const int col = c0 + 16 * j + lc;
+            glogx[xrow * 2 * d + gs * d + col] = acc[i][j][q] + bias[gs * d + col];
+          }
         } else {
-          kraw[off + jj] = from_f<T>(a);
-          kraw[off + jj + half] = from_f<T>(bb);
-          kself[off + jj] = from_f<T>(a * c - bb * s);
-          kself[off + jj + half] = from_f<T>(bb * c + a * s);
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            const int col = c0 + 16 * j + lc;
+            sig[xrow * d + col] = sigmoidf_(acc[i][j][q] + bias[2 * d + col]);
+          }
         }
-      }
-    } else if (seg == 2) {
-      for (int it = threadIdx.x; it < bm * bn; it += 256) {
-        const int r = it / bn, jj = it - r * bn;
-        const int m = m0 + r;
-        if (m >= M) continue;
-        const int b = m / Tl, tl = m - b * Tl;
-        const int j = j0 + jj, hh = j / dh, e = j - hh * dh;
-        vraw[(((long)b * h + hh) * Tbuf + buf_t0 + tl) * dh + e] = from_f<T>(Cs[r * ldc + jj]);
-      }
-    } else if (seg <= 4) {
-      const int gs = seg - 3;
-      for (int it = threadIdx.x; it < bm * bn; it += 256) {
-        const int r = it / bn, jj = it - r * bn;
-        const int m = m0 + r;
-        if (m >= M) continue;
-        const int b = m / Tl, tl = m - b * Tl;
-        const int j = j0 + jj;
-        glogx[((long)b * Tbuf + buf_t0 + tl) * 2 * d + gs * d + j] = Cs[r * ldc + jj] + bias[gs * d + j];
-      }
-    } else {
-      for (int it = threadIdx.x; it < bm * bn; it += 256) {
-        const int r = it / bn, jj = it - r * bn;
-        const int m = m0 + r;
-        if (m >= M) continue;
-        const int b = m / Tl, tl = m - b * Tl;
-        const int j = j0 + jj;
-        sig[((long)b * Tbuf + buf_t0 + tl) * d + j] = sigmoidf_(Cs[r * ldc + jj] + bias[2 * d + j]);
       }
     }
   }
@@ -149,26 +167,10 @@ struct CellGeom {
   int cache_T;     // T of the K/V cache
 };
 
-// rows [pos0, pos0+c) of the cache := raw rows (sweep 0 reads raw intra rows)
-template <typename T>
-__global__ void k_init_rows(CellGeom g, const T* __restrict__ kself, const T* __restrict__ vraw,
-                            T* __restrict__ Kc, T* __restrict__ Vc) {
-  const long n = (long)g.B * g.h * g.c * g.dh;
-  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
-    const int e = i % g.dh;
-    const long r = i / g.dh;
-    const int p = r % g.c;
-    const long bh = r / g.c;
-    const long src = (bh * g.Tbuf + g.buf_t0 + p) * g.dh + e;
-    const long dst = (bh * g.cache_T + g.pos0 + p) * g.dh + e;
-    Kc[dst] = kself[src];
-    Vc[dst] = vraw[src];
-  }
-}
-
 // ---------------------------------------------------------------------------
 // committed-prefix accumulator (scan_cell_fwd.py:119-129): per (split, b, h),
-// keys [s*L, min((s+1)*L, pos0)) -> unnormalised A [c, dh], Z [c], m [c]
+// keys [s*L, min((s+1)*L, pos0)) -> unnormalised A [c, dh], Z [c], m [c].
+// The next key tile is loaded into registers while the current one is used.
 // ---------------------------------------------------------------------------
 template <typename T> struct CommArgs {
   CellGeom g;
@@ -205,17 +207,22 @@ __global__ __launch_bounds__(256) void k_comm_partial(CommArgs<T> a) {
   const int k_end = min(k_begin + a.split_len, g.pos0);
   const int qrow = 16 * wave + (lane & 15);
 
+  const T* Kb = a.Kc + (long)bh * g.cache_T * DH;
+  const T* Vb = a.Vc + (long)bh * g.cache_T * DH;
+  KVRegs<T, DH> kv;
+  if (k_begin < k_end) load_kv<T, DH>(Kb + (long)k_begin * DH, Vb + (long)k_begin * DH, DH,
+                                      min(C::KT, k_end - k_begin), kv);
   typename Mfma<T>::frag qf[C::NKS];
   load_q_frags<T, DH>(a.qr + ((long)bh * g.Tbuf + g.buf_t0 + qrow) * DH, qrow < g.c, qf);
   FlashState<T, DH> st;
   flash_init(st);
-  const T* Kb = a.Kc + (long)bh * g.cache_T * DH;
-  const T* Vb = a.Vc + (long)bh * g.cache_T * DH;
   for (int k0 = k_begin; k0 < k_end; k0 += C::KT) {
     const int nv = min(C::KT, k_end - k0);
     __syncthreads();
-    stage_kv<T, DH>(Kb + (long)k0 * DH, Vb + (long)k0 * DH, DH, nv, Ks, Vt);
+    store_kv<T, DH>(kv, Ks, Vt);
     __syncthreads();
+    const int k1 = k0 + C::KT;
+    if (k1 < k_end) load_kv<T, DH>(Kb + (long)k1 * DH, Vb + (long)k1 * DH, DH, min(C::KT, k_end - k1), kv);
     flash_tile<T, DH>(qf, Ks, Vt, Ps + wave * 16 * C::LDP, a.scale, KeyBound{nv}, st);
   }
   const int g4 = lane >> 4, col = lane & 15;
@@ -235,48 +242,29 @@ __global__ __launch_bounds__(256) void k_comm_partial(CommArgs<T> a) {
   }
 }
 
-// merge the split partials into split 0's slots' twin buffers (A, Z, m)
-__global__ __launch_bounds__(256) void k_comm_merge(int nsplit, int BH, int c, int dh,
-                                                    const float* __restrict__ Ap,
-                                                    const float* __restrict__ Zp,
-                                                    const float* __restrict__ Mp, float* __restrict__ A,
-                                                    float* __restrict__ Z, float* __restrict__ Mx) {
-  const int bh = blockIdx.x;
-  for (int i = threadIdx.x; i < c * dh; i += 256) {
-    const int q = i / dh, e = i - q * dh;
-    float M = NEG_INF;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, Mp[((long)s * BH + bh) * c + q]);
-    float acc = 0.f, z = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-      const long b = ((long)s * BH + bh) * c + q;
-      const float w = (Mp[b] == NEG_INF) ? 0.f : __expf(Mp[b] - M);
-      acc += w * Ap[b * dh + e];
-      z += w * Zp[b];
-    }
-    const long o = (long)bh * c + q;
-    A[o * dh + e] = acc;
-    if (e == 0) {
-      Z[o] = z;
-      Mx[o] = M;
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // one sweep's read (scan_cell_fwd.py:63-85 / :132-149): intra rows (strict
-// lower) + raw self column, merged with the committed accumulator.
-// writes o [B*c, d] fp32, per-head sums of squares ssq [B*c, h]
+// lower) + raw self column, merged with the committed accumulator. The first
+// sweep of a cell merges the committed split partials (flash-decoding style)
+// and writes the merged (A, Z, m) for the later sweeps.
+// Writes o [B*c, d] in the storage dtype and per-head sums of squares of the
+// stored values, ssq [B*c, h] (the norm_ctx RMS of the next GEMM).
 // ---------------------------------------------------------------------------
 template <typename T> struct AttendArgs {
   CellGeom g;
   const T* qr; const T* kself; const T* vraw;   // layer buffers
-  const T* Kc; const T* Vc;                     // cache (intra rows at pos0)
-  const float* A; const float* Z; const float* Mx;   // committed (nullptr if pos0 == 0)
+  const T* Kin; const T* Vin;                   // intra rows of this sweep: (b,h) at bh*in_stride,
+  long in_stride; int in_row0;                  //   chunk row p at row in_row0 + p
+  int nsplit;                                   // committed partials to merge (0: none, 1: merged)
+  const float* Ap; const float* Zp; const float* Mp;   // partials [nsplit, B*h, c, ...] when nsplit > 1
+  float* A; float* Z; float* Mx;                // merged committed state [B*h, c, ...]
   float scale;
-  float* o;     // [B*c, d]
+  T* o;         // [B*c, d]
   float* ssq;   // [B*c, h]
   T* ocat;      // [B, Tbuf, d] or nullptr (buffer rows buf_t0 + p)
-  float* o_last;   // [B*c, d] or nullptr
+  float* o_last;    // [B*c, d] or nullptr
+  float* stat_m;    // [B*h, c] final row max (or nullptr)
+  float* stat_z;    // [B*h, c] final row sum (or nullptr)
 };
 
 template <typename T, int DH>
@@ -293,12 +281,16 @@ __global__ __launch_bounds__(256) void k_attend(AttendArgs<T> a) {
   const int g4 = lane >> 4, col = lane & 15;
   const int qrow = 16 * wave + col;
   const long lrow0 = (long)bh * g.Tbuf + g.buf_t0;   // layer-buffer row of chunk row 0
+  const int BH = g.B * g.h;
 
+  KVRegs<T, DH> kv;
+  load_kv<T, DH>(a.Kin + (long)bh * a.in_stride + (long)a.in_row0 * DH,
+                 a.Vin + (long)bh * a.in_stride + (long)a.in_row0 * DH, DH, g.c, kv);
   typename Mfma<T>::frag qf[C::NKS];
   load_q_frags<T, DH>(a.qr + (lrow0 + qrow) * DH, qrow < g.c, qf);
   FlashState<T, DH> st;
   flash_init(st);
-  if (a.A != nullptr) {
+  if (a.nsplit == 1) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int q = 16 * wave + 4 * g4 + r;
@@ -310,50 +302,91 @@ __global__ __launch_bounds__(256) void k_attend(AttendArgs<T> a) {
         for (int dt = 0; dt < C::NDT; ++dt) st.O[dt][r] = a.A[o * DH + col + 16 * dt];
       }
     }
+  } else if (a.nsplit > 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int q = 16 * wave + 4 * g4 + r;
+      if (q < g.c) {
+        float M = NEG_INF;
+        for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.Mp[((long)s * BH + bh) * g.c + q]);
+        float z = 0.f;
+        float acc[C::NDT];
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; ++dt) acc[dt] = 0.f;
+        for (int s = 0; s < a.nsplit; ++s) {
+          const long base = ((long)s * BH + bh) * g.c + q;
+          const float ms = a.Mp[base];
+          const float w = (ms == NEG_INF) ? 0.f : __expf(ms - M);
+          z += w * a.Zp[base];
+#pragma unroll
+          for (int dt = 0; dt < C::NDT; ++dt) acc[dt] += w * a.Ap[base * DH + col + 16 * dt];
+        }
+        const long o = (long)bh * g.c + q;
+        st.m[r] = M;
+        st.z[r] = (col == 0) ? z : 0.f;
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; ++dt) {
+          st.O[dt][r] = acc[dt];
+          a.A[o * DH + col + 16 * dt] = acc[dt];
+        }
+        if (col == 0) {
+          a.Z[o] = z;
+          a.Mx[o] = M;
+        }
+      }
+    }
   }
-  stage_kv<T, DH>(a.Kc + ((long)bh * g.cache_T + g.pos0) * DH, a.Vc + ((long)bh * g.cache_T + g.pos0) * DH,
-                  DH, g.c, Ks, Vt);
-  __syncthreads();
-  flash_tile<T, DH>(qf, Ks, Vt, Ps + wave * 16 * C::LDP, a.scale, KeyStrictLower{}, st);
-
-  // raw self column: s_self = scale * <q_r, k_self_r> (fp32), value v_raw
+  // raw self column inputs, loaded before the barriers below: partial <q_r, k_self_r>
+  // over this lane's PER elements, and v_raw at the lane's output columns
   constexpr int PER = DH / 16;
+  float sdot[4], vself[4][C::NDT];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int q = 16 * wave + 4 * g4 + r;
-    const int qc = min(q, g.c - 1);
+    const int qc = min(16 * wave + 4 * g4 + r, g.c - 1);
     const T* qp = a.qr + (lrow0 + qc) * DH + col * PER;
     const T* kp = a.kself + (lrow0 + qc) * DH + col * PER;
     float dot = 0.f;
 #pragma unroll
     for (int e = 0; e < PER; ++e) dot += to_f(qp[e]) * to_f(kp[e]);
-    const float ss = group16_sum(dot) * a.scale;
+    sdot[r] = dot;
+    const T* vp = a.vraw + (lrow0 + qc) * DH;
+#pragma unroll
+    for (int dt = 0; dt < C::NDT; ++dt) vself[r][dt] = to_f(vp[col + 16 * dt]);
+  }
+  store_kv<T, DH>(kv, Ks, Vt);
+  __syncthreads();
+  flash_tile<T, DH>(qf, Ks, Vt, Ps + wave * 16 * C::LDP, a.scale, KeyStrictLower{}, st);
+
+  // raw self column: s_self = scale * <q_r, k_self_r> (fp32), value v_raw
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float ss = group16_sum(sdot[r]) * a.scale;
     const float mnew = fmaxf(st.m[r], ss);
     const float alpha = (st.m[r] == NEG_INF) ? 0.f : __expf(st.m[r] - mnew);
     const float es = __expf(ss - mnew);
-    const T* vp = a.vraw + (lrow0 + qc) * DH;
 #pragma unroll
-    for (int dt = 0; dt < C::NDT; ++dt) st.O[dt][r] = st.O[dt][r] * alpha + es * to_f(vp[col + 16 * dt]);
+    for (int dt = 0; dt < C::NDT; ++dt) st.O[dt][r] = st.O[dt][r] * alpha + es * vself[r][dt];
     st.z[r] = st.z[r] * alpha + (col == 0 ? es : 0.f);
     st.m[r] = mnew;
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int q = 16 * wave + 4 * g4 + r;
-    const float inv = 1.0f / group16_sum(st.z[r]);
+    const float zt = group16_sum(st.z[r]);
+    const float inv = 1.0f / zt;
     float sq = 0.f;
     float ov[C::NDT];
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt) {
-      ov[dt] = st.O[dt][r] * inv;
+      ov[dt] = to_f(from_f<T>(st.O[dt][r] * inv));   // the stored (rounded) value
       sq += ov[dt] * ov[dt];
     }
     sq = group16_sum(sq);
     if (q < g.c) {
       const long n = (long)b * g.c + q;
-      float* orow = a.o + n * g.d + hh * DH;
+      T* orow = a.o + n * g.d + hh * DH;
 #pragma unroll
-      for (int dt = 0; dt < C::NDT; ++dt) orow[col + 16 * dt] = ov[dt];
+      for (int dt = 0; dt < C::NDT; ++dt) orow[col + 16 * dt] = from_f<T>(ov[dt]);
       if (a.o_last != nullptr) {
         float* lrow = a.o_last + n * g.d + hh * DH;
 #pragma unroll
@@ -364,305 +397,254 @@ __global__ __launch_bounds__(256) void k_attend(AttendArgs<T> a) {
 #pragma unroll
         for (int dt = 0; dt < C::NDT; ++dt) crow[col + 16 * dt] = from_f<T>(ov[dt]);
       }
-      if (col == 0) a.ssq[n * g.h + hh] = sq;
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// sweep GEMM 1 epilogue: u . W_sweep^T, one (2*dh)-wide column group per tile
-//   groups [0, h)        : k_ctx | g_k(u) of head g -> blend, RoPE, write K rows
-//   linear   [h, 2h)     : v_ctx | g_v(u) of head g -> blend, write V rows
-//   mult fam [h, h+G)    : v_map(u) -> v_in = lam*u + sig * tanh(.)   (G = d/(2dh))
-//            [h+G, h+2G) : g_v(u) -> fp32 scratch for GEMM 2
-// (attention.py:314-387; fused_sweep.py:514-611, :1064-1089)
-// ---------------------------------------------------------------------------
-template <typename T> struct EpiSweep1 {
-  CellGeom g;
-  int M, bm, ctx_mod;
-  float lam;
-  const T* kraw; const T* vraw;
-  const float* glogx; const float* sig;
-  const float* cos; const float* sin;
-  const float* o; const T* normw;   // for u = o * rs * w (v_in's lam*u term)
-  T* Kc; T* Vc;
-  T* vin; float* gvu;
-  DM_DEV void operator()(const float* Cs, int ldc, int m0, int n0, const float* rs) const {
-    const int dh = g.dh, half = dh / 2, d = g.d;
-    const int grp = n0 / (2 * dh);
-    if (grp < g.h || ctx_mod == 0) {
-      const bool is_k = grp < g.h;
-      const int hd = is_k ? grp : grp - g.h;
-      for (int it = threadIdx.x; it < bm * half; it += 256) {
-        const int r = it / half, jj = it - r * half;
-        const int m = m0 + r;
-        if (m >= M) continue;
-        const int b = m / g.c, p = m - b * g.c;
-        const long lrow = ((long)b * g.h + hd) * g.Tbuf + g.buf_t0 + p;
-        const long crow = ((long)b * g.h + hd) * g.cache_T + g.pos0 + p;
-        const float* gx = glogx + ((long)b * g.Tbuf + g.buf_t0 + p) * 2 * d + (is_k ? 0 : d) + hd * dh;
-        const float ca = Cs[r * ldc + jj], cb = Cs[r * ldc + jj + half];
-        const float ga = sigmoidf_(gx[jj] + Cs[r * ldc + dh + jj]);
-        const float gb = sigmoidf_(gx[jj + half] + Cs[r * ldc + dh + jj + half]);
-        if (is_k) {
-          const float ka = ga * to_f(kraw[lrow * dh + jj]) + (1.f - ga) * ca;
-          const float kb = gb * to_f(kraw[lrow * dh + jj + half]) + (1.f - gb) * cb;
-          const long t = g.pos0 + p;
-          const float cs = cos[t * half + jj], sn = sin[t * half + jj];
-          Kc[crow * dh + jj] = from_f<T>(ka * cs - kb * sn);
-          Kc[crow * dh + jj + half] = from_f<T>(kb * cs + ka * sn);
-        } else {
-          Vc[crow * dh + jj] = from_f<T>(ga * to_f(vraw[lrow * dh + jj]) + (1.f - ga) * ca);
-          Vc[crow * dh + jj + half] =
-              from_f<T>(gb * to_f(vraw[lrow * dh + jj + half]) + (1.f - gb) * cb);
+      if (col == 0) {
+        a.ssq[n * g.h + hh] = sq;
+        if (a.stat_m != nullptr) {
+          a.stat_m[(long)bh * g.c + q] = st.m[r];
+          a.stat_z[(long)bh * g.c + q] = zt;
         }
       }
-      return;
     }
-    const int bn = 2 * dh;
-    const int j0 = (grp - g.h) * bn;   // column in [0, 2d)
-    if (j0 < d) {
-      for (int it = threadIdx.x; it < bm * bn; it += 256) {
-        const int r = it / bn, jj = it - r * bn;
-        const int m = m0 + r;
-        if (m >= M) continue;
-        const int b = m / g.c, p = m - b * g.c;
-        const int col = j0 + jj;
-        const float sg = sig[((long)b * g.Tbuf + g.buf_t0 + p) * d + col];
-        float v = sg * tanhf_(Cs[r * ldc + jj]);
-        if (ctx_mod == 1) v += lam * (o[(long)m * d + col] * rs[r] * to_f(normw[col]));
-        vin[(long)m * d + col] = from_f<T>(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// sweep GEMM 1: u . W_sweep^T (u = RMSNorm_ctx(o) on the A load)
+// (attention.py:314-387; fused_sweep.py:514-611, :1064-1089). W_sweep rows are
+// packed in 64-row groups so that one wave's 16 x 64 tile is self-contained:
+//   [0, 2d)  per head g, group q < DH/32:  k_ctx cols 16q.., k_ctx cols DH/2+16q..,
+//            g_k(u) cols 16q.., g_k(u) cols DH/2+16q..  -> blend, RoPE, K rows
+//   linear [2d, 4d) per head g, group q < DH/32: v_ctx cols 32q.. | g_v(u) cols 32q..
+//            -> blend, V rows
+//   mult   [2d, 3d) v_map(u) -> v_in = lam*u + sig * tanh(.)
+//          [3d, 4d) g_v(u)   -> fp32 scratch for GEMM 2
+// save != nullptr stores the raw GEMM outputs [rows, 4d] in this packed order.
+// ---------------------------------------------------------------------------
+template <typename T, int DH> struct EpiSweep1 {
+  CellGeom g;
+  int M, ctx_mod;
+  float lam;
+  const T* __restrict__ kraw; const T* __restrict__ vraw;
+  const float* __restrict__ glogx; const float* __restrict__ sig;
+  const float* __restrict__ cos; const float* __restrict__ sin;
+  const T* __restrict__ o; const T* __restrict__ normw;   // u = o * rs * w for v_in's lam*u term
+  T* __restrict__ Kout; T* __restrict__ Vout;             // refined rows: (b,h) at bh*out_stride,
+  long out_stride; int out_row0;                          //   chunk row p at row out_row0 + p
+  T* __restrict__ vin; float* __restrict__ gvu;
+  float* __restrict__ save;
+
+  // All global loads of the lane are issued before any store (gather, then
+  // compute + scatter): the outputs may alias nothing, but the compiler cannot
+  // know that, and interleaving would serialise a memory latency per element.
+  template <int FM, int FN>
+  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float* rs) const {
+    static_assert(FM == 1 && FN == 4, "sweep GEMM 1 wave tile is 16 x 64");
+    const int lane = threadIdx.x & 63, lc = lane & 15;
+    const int d = g.d, h = g.h;
+    const int mq0 = row0 + 4 * (lane >> 4);
+    int bq[4], pq[4];
+    bool ok[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int m = mq0 + q;
+      ok[q] = m < M;
+      bq[q] = ok[q] ? m / g.c : 0;
+      pq[q] = ok[q] ? m - bq[q] * g.c : 0;
+    }
+    if (save != nullptr) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (ok[q])
+#pragma unroll
+          for (int j = 0; j < FN; ++j) save[(long)(mq0 + q) * 4 * d + col0 + 16 * j + lc] = acc[0][j][q];
+    }
+    if (col0 < 2 * d) {
+      const int hd = col0 / (2 * DH), jj = 16 * ((col0 % (2 * DH)) / 64) + lc;
+      float gxa[4], gxb[4], kra[4], krb[4], cs[4], sn[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t = g.buf_t0 + pq[q], pos = g.pos0 + pq[q];
+        const float* gx = glogx + ((long)bq[q] * g.Tbuf + t) * 2 * d + hd * DH;
+        const long lrow = (((long)bq[q] * h + hd) * g.Tbuf + t) * DH;
+        gxa[q] = gx[jj];
+        gxb[q] = gx[jj + DH / 2];
+        kra[q] = to_f(kraw[lrow + jj]);
+        krb[q] = to_f(kraw[lrow + jj + DH / 2]);
+        cs[q] = cos[(long)pos * (DH / 2) + jj];
+        sn[q] = sin[(long)pos * (DH / 2) + jj];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (!ok[q]) continue;
+        const float ga = sigmoidf_(gxa[q] + acc[0][2][q]);
+        const float gb = sigmoidf_(gxb[q] + acc[0][3][q]);
+        const float k1 = ga * kra[q] + (1.f - ga) * acc[0][0][q];
+        const float k2 = gb * krb[q] + (1.f - gb) * acc[0][1][q];
+        const long crow = ((long)bq[q] * h + hd) * out_stride + (long)(out_row0 + pq[q]) * DH;
+        Kout[crow + jj] = from_f<T>(k1 * cs[q] - k2 * sn[q]);
+        Kout[crow + jj + DH / 2] = from_f<T>(k2 * cs[q] + k1 * sn[q]);
+      }
+    } else if (ctx_mod == 0) {
+      const int cl = col0 - 2 * d;
+      const int hd = cl / (2 * DH), e0 = 32 * ((cl % (2 * DH)) / 64);
+      float gxv[4][2], vr[4][2];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t = g.buf_t0 + pq[q];
+        const float* gx = glogx + ((long)bq[q] * g.Tbuf + t) * 2 * d + d + hd * DH;
+        const long lrow = (((long)bq[q] * h + hd) * g.Tbuf + t) * DH;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          gxv[q][j] = gx[e0 + 16 * j + lc];
+          vr[q][j] = to_f(vraw[lrow + e0 + 16 * j + lc]);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (!ok[q]) continue;
+        const long crow = ((long)bq[q] * h + hd) * out_stride + (long)(out_row0 + pq[q]) * DH;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float gv = sigmoidf_(gxv[q][j] + acc[0][j + 2][q]);
+          Vout[crow + e0 + 16 * j + lc] = from_f<T>(gv * vr[q][j] + (1.f - gv) * acc[0][j][q]);
+        }
       }
     } else {
-      for (int it = threadIdx.x; it < bm * bn; it += 256) {
-        const int r = it / bn, jj = it - r * bn;
-        const int m = m0 + r;
-        if (m >= M) continue;
-        gvu[(long)m * d + j0 - d + jj] = Cs[r * ldc + jj];
+      const int c0 = col0 - 2 * d;   // column in [0, 2d)
+      if (c0 < d) {
+        float sg[4][FN], ov[4][FN], nw[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) nw[j] = to_f(normw[c0 + 16 * j + lc]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const long xrow = (long)bq[q] * g.Tbuf + g.buf_t0 + pq[q];
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            const int col = c0 + 16 * j + lc;
+            sg[q][j] = sig[xrow * d + col];
+            ov[q][j] = ctx_mod == 1 ? to_f(o[(long)(ok[q] ? mq0 + q : 0) * d + col]) : 0.f;
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (!ok[q]) continue;
+          const float r = rs[4 * (lane >> 4) + q];
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            float v = sg[q][j] * tanhf_(acc[0][j][q]);
+            if (ctx_mod == 1) v += lam * (ov[q][j] * r * nw[j]);
+            vin[(long)(mq0 + q) * d + c0 + 16 * j + lc] = from_f<T>(v);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (ok[q])
+#pragma unroll
+            for (int j = 0; j < FN; ++j) gvu[(long)(mq0 + q) * d + c0 - d + 16 * j + lc] = acc[0][j][q];
       }
     }
   }
 };
 
-// sweep GEMM 2 epilogue (mult family): v_ctx = v_in . w_vctx^T, one head per
-// tile -> v'' = g_v v_raw + (1 - g_v) v_ctx -> V rows
-template <typename T> struct EpiSweep2 {
+// sweep GEMM 2 (mult family): v_ctx = v_in . w_vctx^T ->
+// v'' = g_v v_raw + (1 - g_v) v_ctx -> V rows. save2 stores raw v_ctx [rows, d].
+template <typename T, int DH> struct EpiSweep2 {
   CellGeom g;
-  int M, bm;
-  const T* vraw;
-  const float* glogx;
-  const float* gvu;
-  T* Vc;
-  DM_DEV void operator()(const float* Cs, int ldc, int m0, int n0, const float*) const {
-    const int dh = g.dh, d = g.d;
-    const int hd = n0 / dh;
-    for (int it = threadIdx.x; it < bm * dh; it += 256) {
-      const int r = it / dh, jj = it - r * dh;
-      const int m = m0 + r;
-      if (m >= M) continue;
-      const int b = m / g.c, p = m - b * g.c;
-      const long lrow = ((long)b * g.h + hd) * g.Tbuf + g.buf_t0 + p;
-      const long crow = ((long)b * g.h + hd) * g.cache_T + g.pos0 + p;
-      const int col = hd * dh + jj;
-      const float gv = sigmoidf_(glogx[((long)b * g.Tbuf + g.buf_t0 + p) * 2 * d + d + col] +
-                                 gvu[(long)m * d + col]);
-      Vc[crow * dh + jj] = from_f<T>(gv * to_f(vraw[lrow * dh + jj]) + (1.f - gv) * Cs[r * ldc + jj]);
-    }
+  int M;
+  const T* __restrict__ vraw;
+  const float* __restrict__ glogx;
+  const float* __restrict__ gvu;
+  T* __restrict__ Vout;
+  long out_stride; int out_row0;
+  float* __restrict__ save2;
+
+  template <int FM, int FN>
+  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
+    const int lane = threadIdx.x & 63, lc = lane & 15;
+    const int d = g.d;
+    float gx[FM][4][FN], gu[FM][4][FN], vr[FM][4][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int m = row0 + 16 * i + 4 * (lane >> 4) + q;
+        m = m < M ? m : 0;
+        const int b = m / g.c, t = g.buf_t0 + m - b * g.c;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int col = col0 + 16 * j + lc;
+          const int hd = col / DH, e = col - hd * DH;
+          gx[i][q][j] = glogx[((long)b * g.Tbuf + t) * 2 * d + d + col];
+          gu[i][q][j] = gvu[(long)m * d + col];
+          vr[i][q][j] = to_f(vraw[(((long)b * g.h + hd) * g.Tbuf + t) * DH + e]);
+        }
+      }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
+        if (m >= M) continue;
+        const int b = m / g.c, p = m - b * g.c;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int col = col0 + 16 * j + lc;
+          const int hd = col / DH, e = col - hd * DH;
+          const float gv = sigmoidf_(gx[i][q][j] + gu[i][q][j]);
+          Vout[((long)b * g.h + hd) * out_stride + (long)(out_row0 + p) * DH + e] =
+              from_f<T>(gv * vr[i][q][j] + (1.f - gv) * acc[i][j][q]);
+          if (save2 != nullptr) save2[(long)m * d + col] = acc[i][j][q];
+        }
+      }
   }
 };
 
-// y = x + C (W_O projection with the block residual), or y = C when x == nullptr
+// y = acc (+ x): the W_O projection with the block residual, or plain nn.Linear
 template <typename T> struct EpiResidual {
-  int M, N, bm;
-  const T* x;
-  T* y;
-  DM_DEV void operator()(const float* Cs, int ldc, int m0, int n0) const {
-    const int bn = ldc - 4;
-    for (int it = threadIdx.x; it < bm * bn; it += 256) {
-      const int r = it / bn, jj = it - r * bn;
-      const int m = m0 + r;
-      if (m >= M) continue;
-      const long idx = (long)m * N + n0 + jj;
-      float v = Cs[r * ldc + jj];
-      if (x != nullptr) v += to_f(x[idx]);
-      y[idx] = from_f<T>(v);
-    }
+  int M, N;
+  const T* __restrict__ x;
+  T* __restrict__ y;
+  template <int FM, int FN>
+  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
+    const int lane = threadIdx.x & 63, lc = lane & 15;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const long idx = (long)m * N + col0 + 16 * j + lc;
+          float v = acc[i][j][q];
+          if (x != nullptr) v += to_f(x[idx]);
+          y[idx] = from_f<T>(v);
+        }
+      }
   }
 };
 
+// C (fp32) = acc, or C += acc when accumulate != 0
 struct EpiStoreF32 {
-  int M, N, bm;
-  float* C;
-  DM_DEV void operator()(const float* Cs, int ldc, int m0, int n0) const {
-    const int bn = ldc - 4;
-    for (int it = threadIdx.x; it < bm * bn; it += 256) {
-      const int r = it / bn, jj = it - r * bn;
-      const int m = m0 + r;
-      if (m < M) C[(long)m * N + n0 + jj] = Cs[r * ldc + jj];
-    }
+  int M, N, accumulate;
+  float* __restrict__ C;
+  template <int FM, int FN>
+  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
+    const int lane = threadIdx.x & 63, lc = lane & 15;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const long idx = (long)m * N + col0 + 16 * j + lc;
+          C[idx] = accumulate ? C[idx] + acc[i][j][q] : acc[i][j][q];
+        }
+      }
   }
 };
-
-// GEMM kernel whose epilogue also sees the per-row scale scratch of the A loader
-template <typename T, int BM, int BN, int WM, int WN, class AL, class EPI>
-__global__ __launch_bounds__(256) void k_gemm_rs(AL al, const T* __restrict__ Bw, long ldb, int K,
-                                                 EPI epi) {
-  __shared__ __attribute__((aligned(16))) char smem[gemm_lds_bytes<T, BM, BN>()];
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  float* Cs;
-  gemm_tile<T, BM, BN, WM, WN, AL>(al, Bw, ldb, K, m0, n0, smem, Cs);
-  const float* rs = reinterpret_cast<const float*>(smem + (gemm_lds_bytes<T, BM, BN>() - BM * 4));
-  epi(Cs, BN + 4, m0, n0, rs);
-}
-
-template <typename T, int BM, int BN, int WM, int WN, class AL, class EPI>
-__global__ __launch_bounds__(256) void k_gemm_plain(AL al, const T* __restrict__ Bw, long ldb, int K,
-                                                    EPI epi) {
-  __shared__ __attribute__((aligned(16))) char smem[gemm_lds_bytes<T, BM, BN>()];
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  float* Cs;
-  gemm_tile<T, BM, BN, WM, WN, AL>(al, Bw, ldb, K, m0, n0, smem, Cs);
-  epi(Cs, BN + 4, m0, n0);
-}
-
-// ---------------------------------------------------------------------------
-// decode: split-P read of the tape (attention.py:283-312 over a static tape)
-// grid (nsplit, B*h); keys [lo + s*L, min(lo + (s+1)*L, pos))
-// ---------------------------------------------------------------------------
-template <typename T> struct DecodeArgs {
-  int B, h, d, tape_T, pos, lo, split_len, nsplit;
-  float scale;
-  const T* q;        // [B, h, 1, dh] rotated query of this step
-  const T* kself;    // [B, h, 1, dh]
-  const T* vself;    // [B, h, 1, dh]
-  const T* Kt; const T* Vt;   // tape [B, h, tape_T, dh]
-  float* part;       // [nsplit, B*h, dh + 2]: A[dh], Z, m
-  float* o;          // [B, d] fp32
-  float* ssq;        // [B, h]
-  T* o_cat;          // [B, d] storage dtype
-};
-
-template <typename T, int DH, int L>
-__global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs<T> a) {
-  constexpr int VEC = 16 / (int)sizeof(T);
-  constexpr int LPK = DH / VEC;          // lanes per key row
-  constexpr int KPP = 256 / LPK;         // keys per pass
-  constexpr int NP = L / KPP;            // passes
-  static_assert(L % KPP == 0, "split length");
-  __shared__ float red[4][DH + 2];
-  const int s = blockIdx.x, bh = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int kslot = tid / LPK, part = tid - kslot * LPK;
-  const int k_begin = a.lo + s * a.split_len;
-  const int k_end = min(k_begin + a.split_len, a.pos);
-
-  float qv[VEC];
-  unpack16<T>(*reinterpret_cast<const uint4*>(a.q + (long)bh * DH + part * VEC), qv);
-  const T* Kb = a.Kt + (long)bh * a.tape_T * DH + part * VEC;
-  const T* Vb = a.Vt + (long)bh * a.tape_T * DH + part * VEC;
-
-  uint4 raw[NP];
-#pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    const int key = k_begin + i * KPP + kslot;
-    raw[i] = (key < k_end) ? ld_nt(Kb + (long)key * DH) : uint4{0u, 0u, 0u, 0u};
-  }
-  float sc[NP];
-  float mx = NEG_INF;
-#pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    float kv[VEC];
-    unpack16<T>(raw[i], kv);
-    float dot = 0.f;
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) dot += qv[j] * kv[j];
-#pragma unroll
-    for (int o = 1; o < LPK; o <<= 1) dot += __shfl_xor(dot, o, 64);
-    const int key = k_begin + i * KPP + kslot;
-    sc[i] = (key < k_end) ? dot * a.scale : NEG_INF;
-    mx = fmaxf(mx, sc[i]);
-  }
-#pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    const int key = k_begin + i * KPP + kslot;
-    raw[i] = (key < k_end) ? ld_nt(Vb + (long)key * DH) : uint4{0u, 0u, 0u, 0u};
-  }
-  // block max
-#pragma unroll
-  for (int o = LPK; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-  if (lane == 0) red[wave][0] = mx;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0]));
-  __syncthreads();
-  float acc[VEC];
-#pragma unroll
-  for (int j = 0; j < VEC; ++j) acc[j] = 0.f;
-  float z = 0.f;
-#pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    const float p = (sc[i] == NEG_INF) ? 0.f : __expf(sc[i] - M);
-    z += p;
-    float vv[VEC];
-    unpack16<T>(raw[i], vv);
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) acc[j] += p * vv[j];
-  }
-  // reduce over key slots: lanes with equal `part` inside the wave, then waves
-#pragma unroll
-  for (int o = LPK; o < 64; o <<= 1) {
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) acc[j] += __shfl_xor(acc[j], o, 64);
-  }
-  // z counted once per key (all LPK lanes of a key hold the same p): use part 0
-  float zz = (part == 0) ? z : 0.f;
-  zz = wave_sum(zz);
-  if (lane < LPK) {
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) red[wave][lane * VEC + j] = acc[j];
-  }
-  if (lane == 0) red[wave][DH] = zz;
-  __syncthreads();
-  float* out = a.part + ((long)s * (a.B * a.h) + bh) * (DH + 2);
-  for (int i = tid; i < DH + 1; i += 256) out[i] = red[0][i] + red[1][i] + red[2][i] + red[3][i];
-  if (tid == 0) out[DH + 1] = M;
-}
-
-// merge split partials + raw self column -> o, ssq, o_cat (one wave per (b, h))
-template <typename T, int DH>
-__global__ __launch_bounds__(64) void k_decode_merge(DecodeArgs<T> a) {
-  constexpr int PER = DH / 64;
-  const int bh = blockIdx.x, lane = threadIdx.x;
-  const int b = bh / a.h, hh = bh - b * a.h;
-  float qk = 0.f;
-#pragma unroll
-  for (int e = 0; e < PER; ++e)
-    qk += to_f(a.q[(long)bh * DH + lane * PER + e]) * to_f(a.kself[(long)bh * DH + lane * PER + e]);
-  const float ss = wave_sum(qk) * a.scale;
-  float M = ss;
-  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part[((long)s * (a.B * a.h) + bh) * (DH + 2) + DH + 1]);
-  const float es = __expf(ss - M);
-  float z = es;
-  float acc[PER];
-#pragma unroll
-  for (int e = 0; e < PER; ++e) acc[e] = es * to_f(a.vself[(long)bh * DH + lane * PER + e]);
-  for (int s = 0; s < a.nsplit; ++s) {
-    const float* pp = a.part + ((long)s * (a.B * a.h) + bh) * (DH + 2);
-    const float w = (pp[DH + 1] == NEG_INF) ? 0.f : __expf(pp[DH + 1] - M);
-    z += w * pp[DH];
-#pragma unroll
-    for (int e = 0; e < PER; ++e) acc[e] += w * pp[lane * PER + e];
-  }
-  const float inv = 1.0f / z;
-  float sq = 0.f;
-#pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const float v = acc[e] * inv;
-    sq += v * v;
-    a.o[(long)b * a.d + hh * DH + lane * PER + e] = v;
-    a.o_cat[(long)b * a.d + hh * DH + lane * PER + e] = from_f<T>(v);
-  }
-  sq = wave_sum(sq);
-  if (lane == 0) a.ssq[(long)b * a.h + hh] = sq;
-}
 
 }  // namespace dm

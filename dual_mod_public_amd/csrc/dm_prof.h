@@ -48,12 +48,12 @@ struct ProfScope {
   ProfScope(int cls, hipStream_t s) : s_(s) {
     ProfState& p = prof();
     if (p.armed != cls || p.n >= p.cap) return;
-    hipEventRecord(p.ev[2 * p.n], s);
+    (void)hipEventRecord(p.ev[2 * p.n], s);
     stop_ = p.ev[2 * p.n + 1];
     ++p.n;
   }
   ~ProfScope() {
-    if (stop_ != nullptr) hipEventRecord(stop_, s_);
+    if (stop_ != nullptr) (void)hipEventRecord(stop_, s_);
   }
 };
 

@@ -30,7 +30,7 @@ class StaticTape:
         self.workspace = torch.empty(nbytes, device=self.device, dtype=torch.uint8)
         self.o_cat = torch.empty(B, cfg.d_model, device=self.device, dtype=dtype)
         self.y = torch.empty(B, cfg.d_model, device=self.device, dtype=dtype)
-        self.w = PackedWeights(cfg, self.device, dtype)
+        self.w = PackedWeights(cfg, self.device, dtype, with_transposes=False)
         self._attn = attn_or_cfg if hasattr(attn_or_cfg, "named_parameters") else None
         self._ver = None
         if sd is not None:

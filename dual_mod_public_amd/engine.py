@@ -66,25 +66,33 @@ def check_supported(cfg):
 class PackedWeights:
     """Device-side packed weights of one layer (dm_packed)."""
 
-    def __init__(self, cfg, device, dtype):
+    def __init__(self, cfg, device, dtype, with_transposes=True):
         check_supported(cfg)
         d = cfg.d_model
         self.cfg, self.device, self.dtype = cfg, device, dtype
         mult = cfg.ctx_mod != "linear"
         kw = dict(device=device, dtype=dtype)
-        self.w_proj = torch.empty((6 if mult else 5) * d, d, **kw)
+        nproj = 6 if mult else 5
+        self.w_proj = torch.empty(nproj * d, d, **kw)
         self.b_proj = torch.zeros(3 * d, device=device, dtype=torch.float32)
         self.w_sweep = torch.empty(4 * d, d, **kw)
         self.w_vctx = torch.empty(d, d, **kw) if mult else None
         self.norm_ctx_w = torch.empty(d, **kw)
         self.attn_norm_w = torch.empty(d, **kw)
         self.wo = torch.empty(d, d, **kw)
+        # transposed copies for the backward
+        self.w_proj_t = torch.empty(d, nproj * d, **kw) if with_transposes else None
+        self.w_sweep_t = torch.empty(d, 4 * d, **kw) if with_transposes else None
+        self.w_vctx_t = torch.empty(d, d, **kw) if (with_transposes and mult) else None
+        self.wo_t = torch.empty(d, d, **kw) if with_transposes else None
         self.has_attn_norm = False
 
     def struct(self, with_attn_norm=None):
         s = L.dm_packed()
         s.w_proj, s.b_proj, s.w_sweep = L.ptr(self.w_proj), L.ptr(self.b_proj), L.ptr(self.w_sweep)
         s.w_vctx, s.norm_ctx_w, s.wo = L.ptr(self.w_vctx), L.ptr(self.norm_ctx_w), L.ptr(self.wo)
+        s.w_proj_t, s.w_sweep_t = L.ptr(self.w_proj_t), L.ptr(self.w_sweep_t)
+        s.w_vctx_t, s.wo_t = L.ptr(self.w_vctx_t), L.ptr(self.wo_t)
         use = self.has_attn_norm if with_attn_norm is None else with_attn_norm
         s.attn_norm_w = L.ptr(self.attn_norm_w) if use else None
         return s

@@ -74,6 +74,8 @@ typedef struct dm_params {
 } dm_params;
 
 /* Packed weights (written by dm_pack_weights, read by every compute call).
+ * The *_t fields are transposed copies used by the backward (may be NULL for
+ * forward-only use; dm_layer_bwd requires them).
  *   w_proj  [6d, d]  rows: wq | wk | wv | w_gk[:, :d] | w_gv[:, :d] | v_gate   (linear: 5d rows)
  *   b_proj  [3d] fp32: b_gk | b_gv | b_vgate
  *   w_sweep [4d, d]  per head g: [w_kctx rows of g ; w_gk[:, d:] rows of g] (2*dh rows each),
@@ -83,6 +85,10 @@ typedef struct dm_params {
 typedef struct dm_packed {
   void* w_proj; float* b_proj; void* w_sweep; void* w_vctx;
   void* norm_ctx_w; void* attn_norm_w; void* wo;
+  void* w_proj_t;   /* [d, 6d] (linear: [d, 5d]) */
+  void* w_sweep_t;  /* [d, 4d] */
+  void* w_vctx_t;   /* [d, d]  (mult family) */
+  void* wo_t;       /* [d, d]  */
 } dm_packed;
 
 /* Per-layer projection buffers (fused_sweep.py:1179-1215 LayerBufs, own layout). */
@@ -169,10 +175,17 @@ int dm_linear(int32_t dtype, const void* x, const void* W, const void* r, void* 
               int32_t N, int32_t K, void* stream);
 
 /* ---- plain GEMM (test / utility) --------------------------------------------
- * C[M, N] (fp32) = A[M, K] . B[N, K]^T in the storage dtype with fp32 accumulate.
- * M, N, K multiples of 64. */
-int dm_gemm_nt(int32_t dtype, const void* A, const void* Bm, float* C, int32_t M, int32_t N,
-               int32_t K, void* stream);
+ * C[M, N] (fp32) = op(A) . op(B)^T (+ C when accumulate != 0), storage dtype inputs,
+ * fp32 accumulate. op(A) = A [M, K] (trans_a = 0) or A^T with A stored [K, M];
+ * op(B) = B [N, K] (trans_b = 0) or B^T with B stored [K, N].
+ * M, N multiples of 128, K multiple of 64. */
+int dm_gemm(int32_t dtype, int32_t trans_a, int32_t trans_b, const void* A, const void* Bm, float* C,
+            int32_t M, int32_t N, int32_t K, int32_t accumulate, void* stream);
+
+/* ---- schedule check ------------------------------------------------------------
+ * Validates a chunk schedule (engines/wavescan/engine/schedule.py:63-69 format):
+ * n_cells triples (pos0, c, n_sweeps) tiling [0, T) in order, 1 <= c <= 64. */
+int dm_check_schedule(const int32_t* sched, int32_t n_cells, int32_t T);
 
 /* ---- optional kernel timing (benchmarks) -------------------------------------
  * No reference counterpart (the reference times with ad-hoc torch events,

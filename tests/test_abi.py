@@ -59,7 +59,7 @@ def test_rejects_null_and_bad_shapes():
     a.c = 65
     rc = lib.dm_cell_fwd(ctypes.byref(c), None, None, None, None, ctypes.byref(a), None)
     assert rc == -1 and b"null packed" in lib.dm_last_error()
-    assert lib.dm_gemm_nt(0, None, None, None, 64, 64, 64, None) == -1
+    assert lib.dm_gemm(0, 0, 0, None, None, None, 128, 128, 64, 0, None) == -1
     assert lib.dm_linear(0, 1, 1, None, 1, 64, 100, 64, None) == -1
 
 

@@ -28,17 +28,22 @@ def _gpu():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (128, 192, 256), (256, 128, 1024)])
-def test_gemm_nt_matches_torch(dtype, M, N, K):
-    say(f"gemm_nt dtype={dtype} M={M} N={N} K={K}")
-    g = torch.Generator().manual_seed(M + N + K)
-    A = torch.randn(M, K, generator=g).to(DEV, dtype)
-    B = torch.randn(N, K, generator=g).to(DEV, dtype)
-    C = torch.empty(M, N, device=DEV, dtype=torch.float32)
-    L.check(L.lib().dm_gemm_nt(L.dtype_code(dtype), A.data_ptr(), B.data_ptr(), C.data_ptr(),
-                               M, N, K, L.stream_ptr()))
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (256, 384, 320), (128, 256, 1024)])
+def test_gemm_matches_fp64(dtype, ta, tb, M, N, K):
+    """dm_gemm: C = op(A) op(B)^T (+C) for the four operand layouts the backward uses."""
+    say(f"gemm dtype={dtype} ta={ta} tb={tb} M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(M + N + K + 7 * ta + 3 * tb)
+    A = torch.randn(M, K, generator=g).to(dtype)
+    B = torch.randn(N, K, generator=g).to(dtype)
+    C0 = torch.randn(M, N, generator=g)
+    Ad = (A.T if ta else A).contiguous().to(DEV)
+    Bd = (B.T if tb else B).contiguous().to(DEV)
+    C = C0.clone().to(DEV)
+    L.check(L.lib().dm_gemm(L.dtype_code(dtype), ta, tb, Ad.data_ptr(), Bd.data_ptr(), C.data_ptr(),
+                            M, N, K, 1, L.stream_ptr()))
     torch.cuda.synchronize()
-    ref = A.double().cpu() @ B.double().cpu().T
+    ref = A.double() @ B.double().T + C0.double()
     assert relerr(C, ref) < (1e-6 if dtype == torch.float32 else 1e-5)
 
 
