@@ -1,12 +1,16 @@
 """Benchmark of the Dual-Mod attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-decode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload fwdbwd|fwd]
+                    [--no-cpu-baseline] [--no-decode]
 
 One step = one DM attention layer of the 340M shape (B=8, T=2048, d=1024,
 16 heads x 64, c=64, K=4 Jacobi sweeps chained over 32 chunks, bf16 storage /
-fp32 accumulate) through libdm_hip.so: attn_norm + projections, the 32 chunk
-cells (committed accumulator + 4 sweeps each) and W_O with the residual.
-Inputs (x, weights, RoPE tables) are resident in HBM before timing starts.
+fp32 accumulate) through libdm_hip.so: the forward (attn_norm + projections,
+the 32 chunk cells = committed accumulator + 4 sweeps each, W_O with the
+residual) and, for the default fwdbwd workload, the
+reverse-scan backward with exact recompute producing dx and every parameter
+gradient for an upstream dy ~ N(0,1). Inputs (x, dy, weights, RoPE tables) are
+resident in HBM before timing starts.
 
 Prints ONE JSON line (rank 0): the headline sweep throughput in tokens/s, the
 roofline of the dominant kernel timed with HIP events inside the timed region,
@@ -52,6 +56,13 @@ def fwd_flops_per_token(d, T, c, K, ctx_mod="mult_res"):
     return (proj + per_sweep * K) * d * d + 2 * d * (T - c) + 2 * K * d * (c - 1) + 4 * K * d
 
 
+def fwdbwd_flops_per_token(d, T, c, K, ctx_mod="mult_res"):
+    """Algorithmic forward + backward FLOPs per token: the backward of every product
+    is two products of the same size, so 3x the forward; the backward's exact
+    recompute of the forward is not useful work and is not counted."""
+    return 3 * fwd_flops_per_token(d, T, c, K, ctx_mod)
+
+
 def sweep1_flops(N, d):
     """Useful FLOPs of one sweep GEMM 1 launch: N rows x (w_kctx, g_k u-half, v_map,
     g_v u-half) = 4 d x d products."""
@@ -72,34 +83,35 @@ def build_layer(cfg, B, T, dev):
     return sd, cell, x, cos.contiguous(), sin.contiguous(), bufs, K, V, ocat, y
 
 
-def time_steps(fn, steps, warmup):
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        fn()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) / steps
-
-
-def cpu_baseline_fwd(cfg, sd, T, B):
-    """The oracle's chunked-Jacobi layer forward (same schedule, fp32) on the host."""
+def cpu_baseline(cfg, sd, T, B, fwdbwd):
+    """The oracle's chunked-Jacobi layer (same schedule, fp32 torch) on this host's cores:
+    forward only, or forward + autograd backward over a T-prefix sample (the same
+    per-token work at a shorter committed prefix: 512 positions = 8 chunks)."""
     import oracle as O
-    nthr = os.cpu_count() or 1
-    nthr = min(nthr, 16)
+    nthr = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(nthr)
-    x = make_input((B, T, cfg.d_model), seed=C2["xseed"])
-    cos, sin = O.build_rope_cache(T, cfg.head_dim, cfg.rope_theta)
-    sched = O.uniform_chunks(T, C2["c"], C2["K"])
-    sdf = {k: v.float() for k, v in sd.items()}
-    with torch.no_grad():
+    Ts = T if not fwdbwd else min(T, 512)
+    x = make_input((B, Ts, cfg.d_model), seed=C2["xseed"])
+    cos, sin = O.build_rope_cache(Ts, cfg.head_dim, cfg.rope_theta)
+    sched = O.uniform_chunks(Ts, C2["c"], C2["K"])
+    if fwdbwd:
+        sdf = {k: v.float().clone().requires_grad_(True) for k, v in sd.items()}
+        x.requires_grad_(True)
+        dy = make_input((B, Ts, cfg.d_model), seed=C2["xseed"] + 100)
         t0 = time.perf_counter()
-        O.dm_layer(cfg, sdf, x, cos, sin, schedule=sched)
+        y = O.dm_layer(cfg, sdf, x, cos, sin, schedule=sched)
+        (y * dy).sum().backward()
         dt = time.perf_counter() - t0
-    return dict(value=B * T / dt, unit="tokens/s", cores=nthr, kind="port",
-                sample=f"one full layer forward at B={B}, T={T} (c=64, K=4), fp32 torch CPU, "
-                       f"{dt:.2f} s wall")
+        what = f"layer forward + autograd backward at B={B}, T={Ts} (T-prefix of 2048; c=64, K=4)"
+    else:
+        sdf = {k: v.float() for k, v in sd.items()}
+        with torch.no_grad():
+            t0 = time.perf_counter()
+            O.dm_layer(cfg, sdf, x, cos, sin, schedule=sched)
+            dt = time.perf_counter() - t0
+        what = f"layer forward at B={B}, T={Ts} (c=64, K=4)"
+    return dict(value=B * Ts / dt, unit="tokens/s", cores=nthr, kind="port",
+                sample=f"{what}, fp32 torch CPU oracle, {dt:.2f} s wall")
 
 
 def bench_decode(dev, steps_override=None):
@@ -162,6 +174,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=0)
     ap.add_argument("--kernel", default="sweep1", help="kernel class timed for the roofline")
+    ap.add_argument("--workload", default="fwdbwd", choices=["fwdbwd", "fwd"])
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -179,38 +192,58 @@ def main():
     sd, cell, x, cos, sin, bufs, Kc, Vc, ocat, y = build_layer(cfg, B, T, dev)
     sched = uniform_chunks(T, c, K)
 
+    from dual_mod_public_amd.engine import LayerGrads
+    grads = LayerGrads(cfg, dev)
+    dy = make_input((B, T, d), seed=C2["xseed"] + 100).to(dev, torch.bfloat16)
+    dx = torch.empty_like(x)
+    fwdbwd = args.workload == "fwdbwd"
+
+    def step_fwd():
+        cell.layer_forward(x, y, cos, sin, sched, Kc, Vc, ocat, bufs)
+
     def step():
         cell.layer_forward(x, y, cos, sin, sched, Kc, Vc, ocat, bufs)
+        if fwdbwd:
+            cell.layer_backward(x, dy, dx, cos, sin, sched, Kc, Vc, ocat, bufs, grads)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     sweeps = sum(k for _, _, k in sched)
-    with L.KernelTimer(args.kernel, max_launches=args.steps * sweeps * 2 + 64) as kt:
+    per_step_launches = sweeps * (2 if fwdbwd else 1)
+    with L.KernelTimer(args.kernel, max_launches=args.steps * per_step_launches * 2 + 64) as kt:
         t0 = time.perf_counter()
         for _ in range(args.steps):
             step()
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / args.steps
+    # forward alone (reported beside the headline)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step_fwd()
+    torch.cuda.synchronize()
+    dt_fwd = (time.perf_counter() - t0) / args.steps
     tokens = B * T
-    fpt = fwd_flops_per_token(d, T, c, K)
+    fpt = fwdbwd_flops_per_token(d, T, c, K) if fwdbwd else fwd_flops_per_token(d, T, c, K)
     if args.kernel == "sweep1":
         per_launch = sweep1_flops(B * c, d)
-        kname = "k_gemm_rs<EpiSweep1> (sweep GEMM 1: u . [w_kctx|g_k|v_map|g_v]^T)"
+        kname = "k_gemm<SrcRms, EpiSweep1> (sweep GEMM 1: u . [w_kctx|g_k|v_map|g_v]^T)"
     elif args.kernel == "layer":
-        per_launch = fpt * tokens
+        per_launch = fwd_flops_per_token(d, T, c, K) * tokens
         kname = "whole dm_layer_fwd call"
     else:
         per_launch = float("nan")
         kname = args.kernel
     achieved = per_launch / (kt.avg_ms / 1e3) / 1e12 if kt.n else None
+    wl = ("C3: 340M-shape DM layer forward + reverse-scan backward (exact recompute)" if fwdbwd
+          else "C2: 340M-shape DM layer forward")
     out = {
-        "metric": "DM sweep tokens/s/GPU (c=64, K=4) — forward",
+        "metric": "DM sweep tokens/s/GPU (fwd+bwd, c=64, K=4)" if fwdbwd else
+                  "DM sweep tokens/s/GPU (forward, c=64, K=4)",
         "value": tokens / dt, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": dt * 1e3, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) x, N(0,0.02) weights)",
-        "config": {"workload": "C2: 340M-shape DM layer forward, B=8 T=2048 d=1024 16x64 c=64 K=4, "
-                               "32 chunks Gauss-Seidel",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) x and dy, N(0,0.02) weights)",
+        "config": {"workload": wl + ", B=8 T=2048 d=1024 16x64 c=64 K=4, 32 chunks Gauss-Seidel",
                    "global_batch": B, "seq_len": T, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": (achieved / PEAK_BF16_TFLOPS) if achieved else None,
@@ -218,13 +251,15 @@ def main():
                      "avg_launch_ms": kt.avg_ms, "launches": kt.n},
         "path_roofline": {"flops_per_token": fpt, "achieved_tflops": fpt * tokens / dt / 1e12,
                           "frac": fpt * tokens / dt / 1e12 / PEAK_BF16_TFLOPS},
+        "forward_only": {"ms_per_step": dt_fwd * 1e3, "tokens_per_s": tokens / dt_fwd,
+                         "frac": fwd_flops_per_token(d, T, c, K) * tokens / dt_fwd / 1e12 / PEAK_BF16_TFLOPS},
     }
     if not args.no_decode:
-        del cell, bufs, Kc, Vc, ocat, y, x
+        del cell, bufs, Kc, Vc, ocat, y, x, dx, dy, grads
         torch.cuda.empty_cache()
         out["decode"] = bench_decode(dev, args.decode_steps or None)
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline_fwd(cfg, sd, T, B)
+        out["cpu_baseline"] = cpu_baseline(cfg, sd, T, B, fwdbwd)
     print(json.dumps(out), flush=True)
 
 

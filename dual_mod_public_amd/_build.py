@@ -14,8 +14,9 @@ import sys
 PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libdm_hip.so")
-SOURCES = ["dm_lib.hip"]
-HEADERS = ["dm_common.h", "dm_gemm.h", "dm_attn.h", "dm_kernels.h", "../../include/dm_abi.h"]
+SOURCES = ["dm_lib.hip", "dm_bwd.hip"]
+HEADERS = ["dm_common.h", "dm_gemm.h", "dm_attn.h", "dm_kernels.h", "dm_decode.h", "dm_bwd.h", "dm_host.h",
+           "dm_fwd_host.h", "dm_prof.h", "../../include/dm_abi.h"]
 
 
 def hipcc():

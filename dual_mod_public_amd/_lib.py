@@ -25,7 +25,21 @@ c_fp = ctypes.c_void_p
 class dm_config(ctypes.Structure):
     _fields_ = [("dtype", c_i32), ("B", c_i32), ("d", c_i32), ("h", c_i32), ("dh", c_i32),
                 ("ctx_mod", c_i32), ("mult_res_lambda", ctypes.c_float), ("rms_eps", ctypes.c_float),
-                ("local_window", c_i32), ("reserved", c_i32 * 7)]
+                ("local_window", c_i32), ("flags", c_i32), ("reserved", c_i32 * 6)]
+
+
+DM_FLAG_NO_RESIDUAL = 1
+
+# dm_grads fields and the reference parameter each one accumulates
+GRAD_FIELDS = (("wq", "wq.weight"), ("wk", "wk.weight"), ("wv", "wv.weight"), ("wo", "wo.weight"),
+               ("w_kctx", "w_kctx.weight"), ("w_vctx", "w_vctx.weight"), ("w_gk", "w_gk.weight"),
+               ("w_gv", "w_gv.weight"), ("b_gk", "w_gk.bias"), ("b_gv", "w_gv.bias"),
+               ("v_gate", "v_gate.weight"), ("b_vgate", "v_gate.bias"), ("v_map", "v_map.weight"),
+               ("norm_ctx_w", "norm_ctx.weight"), ("attn_norm_w", "attn_norm.weight"))
+
+
+class dm_grads(ctypes.Structure):
+    _fields_ = [(f, c_vp) for f, _ in GRAD_FIELDS]
 
 
 class dm_params(ctypes.Structure):
@@ -72,6 +86,10 @@ SIGNATURES = {
     "dm_layer_fwd": (ctypes.c_int, [P(dm_config), P(dm_packed), c_vp, c_vp, c_fp, c_fp,
                                     P(dm_layer_bufs), P(c_i32), c_i32, c_vp, c_vp, c_i32, c_vp,
                                     c_vp, ctypes.c_size_t, c_vp]),
+    "dm_layer_bwd_workspace_bytes": (ctypes.c_size_t, [P(dm_config), c_i32, c_i32, c_i32]),
+    "dm_layer_bwd": (ctypes.c_int, [P(dm_config), P(dm_packed), c_vp, c_vp, c_vp, c_fp, c_fp,
+                                    P(dm_layer_bufs), P(c_i32), c_i32, c_vp, c_vp, c_i32, c_vp,
+                                    P(dm_grads), c_vp, ctypes.c_size_t, c_vp]),
     "dm_decode_workspace_bytes": (ctypes.c_size_t, [P(dm_config), c_i32]),
     "dm_decode_step": (ctypes.c_int, [P(dm_config), P(dm_packed), c_fp, c_fp,
                                       P(dm_decode_args), c_vp]),

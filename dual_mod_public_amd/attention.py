@@ -71,22 +71,21 @@ class DualModAttention(nn.Module):
         return cell
 
     # ---- full-sequence forward (attention.py:438-447, mode "sequential") --------
-    @torch.no_grad()
-    def forward(self, xhat, cos, sin, collect=None):
-        """xhat [B,T,d] pre-normed; cos/sin rows 0..T-1. Returns W_O o_cat [B,T,d]."""
+    def forward(self, xhat, cos, sin, collect=None, n_sweeps=None):
+        """xhat [B,T,d] pre-normed; cos/sin rows 0..T-1. Returns W_O o_cat [B,T,d].
+
+        Runs the chunked scan with chunks of CHUNK rows: n_sweeps=None gives K = c
+        sweeps per chunk, equal to the exact sequential scan (nilpotency,
+        scan_cell_fwd.py:1-10); n_sweeps < c gives the chunked Jacobi result at that
+        K. Differentiable: the backward is the HIP reverse scan with exact recompute."""
         if collect is not None:
             raise NotImplementedError("telemetry collection is not supported on the HIP path")
+        from .autograd import dm_layer
         B, T, d = xhat.shape
-        xhat = xhat.contiguous()
         cell = self._hip_cell(B, T, xhat.dtype)
-        bufs = cell.new_bufs(T)
-        cell.layer_proj(xhat, bufs, cos[:T], sin[:T], normalize=False)
-        K = torch.empty(B, self.n_heads, T, self.head_dim, device=xhat.device, dtype=xhat.dtype)
-        V = torch.empty_like(K)
-        ocat = torch.empty(B, T, d, device=xhat.device, dtype=xhat.dtype)
-        for pos0, c, k in uniform_chunks(T, self.CHUNK):
-            cell.cell_forward(bufs, cos[:T], sin[:T], K, V, pos0, c, k, ocat=ocat)
-        return L.linear(ocat, self.wo.weight)
+        params = dict(self.named_parameters())
+        return dm_layer(xhat, cell, params, cos[:T], sin[:T], uniform_chunks(T, self.CHUNK, n_sweeps),
+                        normalize=False, residual=False)
 
     # ---- incremental decode (attention.py:564-588) ------------------------------
     @torch.no_grad()

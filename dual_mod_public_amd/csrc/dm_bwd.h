@@ -1,0 +1,819 @@
+// Kernels of the reverse-scan backward with exact recompute
+// (engines/wavescan/cells/fused_sweep.py:1557-1850 semantics, own design).
+//
+// Per cell, sweeps run in reverse. For sweep s with recomputed state:
+//   k_refine_bwd  VJP of the blend/gate/RoPE epilogue of the sweep-s refine:
+//                 grads of the refined rows -> dctx (packed GEMM-1 column order),
+//                 dv_ctx, and the layer accumulators dglogx / dkraw / dvraw
+//   EpiVinBwd     epilogue of dv_in = dv_ctx . W_vctx: tanh / sigmoid VJP of v_in
+//   EpiDuBwd      epilogue of du = dctx . W_sweep (+ lam dv_in): g = du * w_ctx,
+//                 per-row partial <g, o> for the RMS VJP, norm_ctx weight partials
+//   k_attn_bwd    attention VJP of sweep s per (b, h): intra rows (strict lower)
+//                 + raw self column; accumulates the committed part's G, Dbar
+// After the sweeps, k_comm_bwd runs the committed-prefix VJP once per cell:
+//   sum_s dS_comm^s = E o (G V^T - Dbar),  E = exp(S - m_comm),
+//   G = sum_s alpha_s dO_s, Dbar = sum_s alpha_s D_s, alpha_s = exp(m_comm - M_s) / Z_s,
+// which is exact because the committed scores are the same in every sweep.
+#pragma once
+
+#include "dm_kernels.h"
+
+namespace dm {
+
+// ---------------------------------------------------------------------------
+// small helpers
+// ---------------------------------------------------------------------------
+static __global__ __launch_bounds__(256) void k_fill(float* __restrict__ p, long n, float v) {
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) p[i] = v;
+}
+
+// C-layout MFMA product for one wave: acc[t] += X[16 rows, KD] . Y[16 t + (0..15), KD]^T,
+// X and Y row-major in LDS with leading dimensions ldx / ldy (K contiguous).
+template <typename T, int KD, int NT>
+DM_DEV void wave_mma(const T* X, int ldx, const T* Y, int ldy, floatx4 (&acc)[NT]) {
+  using MF = Mfma<T>;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 0; k < KD; k += MF::KSTEP) {
+    const typename MF::frag a = MF::load(X + (lane & 15) * ldx + k + (lane >> 4) * MF::KPL);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const typename MF::frag b = MF::load(Y + (16 * t + (lane & 15)) * ldy + k + (lane >> 4) * MF::KPL);
+      acc[t] = MF::mma(a, b, acc[t]);
+    }
+  }
+}
+
+// packed GEMM-1 column of the k_ctx / g_k(u) quads (see EpiSweep1)
+template <int DH> DM_DEV int col_k(int hd, int jj, int part) {
+  return hd * 2 * DH + 64 * (jj / 16) + 16 * part + (jj % 16);
+}
+// linear ctx_mod: packed column of v_ctx element e of head hd (g_v(u) at +32)
+template <int DH> DM_DEV int col_vlin(int d, int hd, int e) {
+  return 2 * d + hd * 2 * DH + 64 * (e / 32) + (e % 32);
+}
+
+// ---------------------------------------------------------------------------
+// refine VJP of one sweep (attention.py:314-387 backward), one thread per
+// (row m, head hd, pair jj < DH/2): K pair (jj, jj + DH/2), V elements jj, jj + DH/2.
+// ---------------------------------------------------------------------------
+template <typename T> struct RefineBwdArgs {
+  CellGeom g;
+  int N, ctx_mod;
+  const float* dK; const float* dV;    // grads of the refined rows (rotated K, V)
+  long dk_stride; int dk_row0;         //   (b,h) at bh*dk_stride, chunk row p at row dk_row0 + p
+  const float* save1;                  // [N, 4d] raw GEMM-1 outputs of this sweep
+  const float* save2;                  // [N, d] raw v_ctx (mult family)
+  const float* glogx; const T* kraw; const T* vraw;
+  const float* cos; const float* sin;
+  T* dctx;                             // [N, 4d] (packed columns; v_map columns written by EpiVinBwd)
+  T* dvc;                              // [N, d] dv_ctx (mult family)
+  float* dglogx; float* dkraw; float* dvraw;   // layer accumulators (+=)
+};
+
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
+  const CellGeom& g = a.g;
+  const int d = g.d, h = g.h;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  const int per_row = d / 2;
+  if (idx >= a.N * per_row) return;
+  const int m = idx / per_row, rem = idx - m * per_row;
+  const int hd = rem / (DH / 2), jj = rem - hd * (DH / 2);
+  const int b = m / g.c, p = m - b * g.c;
+  const int t = g.buf_t0 + p, pos = g.pos0 + p;
+  const long bh = (long)b * h + hd;
+  const long drow = bh * a.dk_stride + (long)(a.dk_row0 + p) * DH;
+  const long lrow = (bh * g.Tbuf + t) * DH;
+  const long xrow = (long)b * g.Tbuf + t;
+  const float* S1 = a.save1 + (long)m * 4 * d;
+  const float* gx = a.glogx + xrow * 2 * d;
+  // ---- gather
+  const float da = a.dK[drow + jj], db = a.dK[drow + jj + DH / 2];
+  const float cs = a.cos[(long)pos * (DH / 2) + jj], sn = a.sin[(long)pos * (DH / 2) + jj];
+  const float kc1 = S1[col_k<DH>(hd, jj, 0)], kc2 = S1[col_k<DH>(hd, jj, 1)];
+  const float gu1 = S1[col_k<DH>(hd, jj, 2)], gu2 = S1[col_k<DH>(hd, jj, 3)];
+  const float gx1 = gx[hd * DH + jj], gx2 = gx[hd * DH + jj + DH / 2];
+  const float kr1 = to_f(a.kraw[lrow + jj]), kr2 = to_f(a.kraw[lrow + jj + DH / 2]);
+  const float dv1 = a.dV[drow + jj], dv2 = a.dV[drow + jj + DH / 2];
+  const float vr1 = to_f(a.vraw[lrow + jj]), vr2 = to_f(a.vraw[lrow + jj + DH / 2]);
+  const float gxv1 = gx[d + hd * DH + jj], gxv2 = gx[d + hd * DH + jj + DH / 2];
+  const int c1 = hd * DH + jj, c2 = c1 + DH / 2;
+  float vc1, vc2, gvu1, gvu2;
+  int cv1 = 0, cv2 = 0;
+  if (a.ctx_mod == 0) {
+    cv1 = col_vlin<DH>(d, hd, jj);
+    cv2 = col_vlin<DH>(d, hd, jj + DH / 2);
+    vc1 = S1[cv1]; vc2 = S1[cv2];
+    gvu1 = S1[cv1 + 32]; gvu2 = S1[cv2 + 32];
+  } else {
+    vc1 = a.save2[(long)m * d + c1]; vc2 = a.save2[(long)m * d + c2];
+    gvu1 = S1[3 * d + c1]; gvu2 = S1[3 * d + c2];
+  }
+  // ---- key: unrotate, then the convex blend k'' = g k_raw + (1 - g) k_ctx
+  const float dk1 = da * cs + db * sn, dk2 = -da * sn + db * cs;
+  const float g1 = sigmoidf_(gx1 + gu1), g2 = sigmoidf_(gx2 + gu2);
+  const float dl1 = dk1 * (kr1 - kc1) * g1 * (1.f - g1);
+  const float dl2 = dk2 * (kr2 - kc2) * g2 * (1.f - g2);
+  T* D = a.dctx + (long)m * 4 * d;
+  D[col_k<DH>(hd, jj, 0)] = from_f<T>(dk1 * (1.f - g1));
+  D[col_k<DH>(hd, jj, 1)] = from_f<T>(dk2 * (1.f - g2));
+  D[col_k<DH>(hd, jj, 2)] = from_f<T>(dl1);
+  D[col_k<DH>(hd, jj, 3)] = from_f<T>(dl2);
+  float* dgx = a.dglogx + xrow * 2 * d;
+  dgx[c1] += dl1;
+  dgx[c2] += dl2;
+  a.dkraw[lrow + jj] += dk1 * g1;
+  a.dkraw[lrow + jj + DH / 2] += dk2 * g2;
+  // ---- value: v'' = g_v v_raw + (1 - g_v) v_ctx
+  const float gv1 = sigmoidf_(gxv1 + gvu1), gv2 = sigmoidf_(gxv2 + gvu2);
+  const float dlv1 = dv1 * (vr1 - vc1) * gv1 * (1.f - gv1);
+  const float dlv2 = dv2 * (vr2 - vc2) * gv2 * (1.f - gv2);
+  if (a.ctx_mod == 0) {
+    D[cv1] = from_f<T>(dv1 * (1.f - gv1));
+    D[cv2] = from_f<T>(dv2 * (1.f - gv2));
+    D[cv1 + 32] = from_f<T>(dlv1);
+    D[cv2 + 32] = from_f<T>(dlv2);
+  } else {
+    a.dvc[(long)m * d + c1] = from_f<T>(dv1 * (1.f - gv1));
+    a.dvc[(long)m * d + c2] = from_f<T>(dv2 * (1.f - gv2));
+    D[3 * d + c1] = from_f<T>(dlv1);
+    D[3 * d + c2] = from_f<T>(dlv2);
+  }
+  dgx[d + c1] += dlv1;
+  dgx[d + c2] += dlv2;
+  a.dvraw[lrow + jj] += dv1 * gv1;
+  a.dvraw[lrow + jj + DH / 2] += dv2 * gv2;
+}
+
+// ---------------------------------------------------------------------------
+// dv_in = dv_ctx . W_vctx epilogue (mult family): v_in = lam u + sig tanh(vm)
+//   dsig += dv_in tanh(vm); dctx[:, 2d + j] = dv_in sig (1 - tanh^2); lamdv = lam dv_in
+// ---------------------------------------------------------------------------
+template <typename T> struct EpiVinBwd {
+  CellGeom g;
+  int M, ctx_mod;
+  float lam;
+  const float* __restrict__ save1;   // [N, 4d]
+  const float* __restrict__ sig;     // [B, Tbuf, d]
+  T* __restrict__ dctx;              // [N, 4d]
+  float* __restrict__ dsig;          // layer accumulator [B, Tbuf, d]
+  float* __restrict__ lamdv;         // [N, d]
+  template <int FM, int FN>
+  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
+    const int lane = threadIdx.x & 63, lc = lane & 15;
+    const int d = g.d;
+    float vm[FM][4][FN], sg[FM][4][FN], ds[FM][4][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int m = row0 + 16 * i + 4 * (lane >> 4) + q;
+        m = m < M ? m : 0;
+        const int b = m / g.c;
+        const long xrow = (long)b * g.Tbuf + g.buf_t0 + m - b * g.c;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int col = col0 + 16 * j + lc;
+          vm[i][q][j] = save1[(long)m * 4 * d + 2 * d + col];
+          sg[i][q][j] = sig[xrow * d + col];
+          ds[i][q][j] = dsig[xrow * d + col];
+        }
+      }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
+        if (m >= M) continue;
+        const int b = m / g.c;
+        const long xrow = (long)b * g.Tbuf + g.buf_t0 + m - b * g.c;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int col = col0 + 16 * j + lc;
+          const float dvi = acc[i][j][q];
+          const float th = tanhf_(vm[i][q][j]);
+          dsig[xrow * d + col] = ds[i][q][j] + dvi * th;
+          dctx[(long)m * 4 * d + 2 * d + col] = from_f<T>(dvi * sg[i][q][j] * (1.f - th * th));
+          lamdv[(long)m * d + col] = ctx_mod == 1 ? lam * dvi : 0.f;
+        }
+      }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// du = dctx . W_sweep (+ lam dv_in) epilogue: RMS VJP inputs
+//   gw = du * w (fp32), rowdot[m, col0 / TN] = sum over the wave's columns of gw * o,
+//   dnw[row0 / TM][col] += sum over the wave's rows of du * o * r   (norm_ctx.weight)
+// ---------------------------------------------------------------------------
+template <typename T> struct EpiDuBwd {
+  int M, d, h, nrd;
+  float inv_d, eps;
+  const float* __restrict__ lamdv;   // [M, d] or nullptr
+  const T* __restrict__ o;           // [M, d] this sweep's o
+  const float* __restrict__ ssq;     // [M, h]
+  const T* __restrict__ normw;       // [d]
+  float* __restrict__ gw;            // [M, d]
+  float* __restrict__ rowdot;        // [M, nrd]
+  float* __restrict__ dnw;           // [ceil(Mmax/TM), d] partials (+=)
+  template <int FM, int FN>
+  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
+    const int lane = threadIdx.x & 63, lc = lane & 15;
+    float ov[FM][4][FN], ld[FM][4][FN], rr[FM][4], wv[FN], dn[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      wv[j] = to_f(normw[col0 + 16 * j + lc]);
+      dn[j] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int m = row0 + 16 * i + 4 * (lane >> 4) + q;
+        m = m < M ? m : 0;
+        float s = 0.f;
+        for (int p = 0; p < h; ++p) s += ssq[(long)m * h + p];
+        rr[i][q] = rsqrtf(s * inv_d + eps);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int col = col0 + 16 * j + lc;
+          ov[i][q][j] = to_f(o[(long)m * d + col]);
+          ld[i][q][j] = lamdv != nullptr ? lamdv[(long)m * d + col] : 0.f;
+        }
+      }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
+        const bool ok = m < M;
+        float dot = 0.f;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const float du = ok ? acc[i][j][q] + ld[i][q][j] : 0.f;
+          const float gv = du * wv[j];
+          dot += gv * ov[i][q][j];
+          dn[j] += du * ov[i][q][j] * rr[i][q];
+          if (ok) gw[(long)m * d + col0 + 16 * j + lc] = gv;
+        }
+        dot = group16_sum(dot);
+        if (ok && lc == 0) rowdot[(long)m * nrd + col0 / (FN * 16)] = dot;
+      }
+    // column sums over the wave's rows: lanes l, l^16, l^32, l^48 share a column
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      float v = dn[j];
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      if (lane < 16) dnw[(long)(row0 / (FM * 16)) * d + col0 + 16 * j + lc] += v;
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// attention VJP of one sweep, one block per (b, h), 4 waves x 16 rows
+// ---------------------------------------------------------------------------
+template <typename T> struct AttnBwdArgs {
+  CellGeom g;
+  const T* qr; const T* kself; const T* vraw;          // layer buffers
+  const T* Kin; const T* Vin; long in_stride; int in_row0;   // intra rows read by this sweep
+  const T* o; const float* ssq;                        // this sweep's o [N, d], ssq [N, h]
+  const float* gw; const float* rowdot; int nrd;       // RMS VJP inputs (EpiDuBwd)
+  const float* docat;                                  // [B, Tbuf, d] upstream grad of o_cat, or nullptr
+  const float* stat_m; const float* stat_z;            // [B*h, c] final row max / sum of the sweep
+  const float* Mx;                                     // committed row max [B*h, c] or nullptr
+  float* G; float* Dbar;                               // committed grads [B*h, CMAX, DH], [B*h, CMAX]
+  int first;                                           // first reverse sweep: G / Dbar are written, else +=
+  float scale, inv_d, eps;
+  float* dKout; float* dVout;                          // [B*h, CMAX, DH] grads of the intra rows (sweep >= 1)
+  float* dkself; float* dvraw; float* dq;              // layer accumulators [B, h, Tbuf, DH] (+=)
+};
+
+template <typename T, int DH> struct AttnBwdCfg {
+  static constexpr int PAD = 16 / (int)sizeof(T);
+  static constexpr int LDE = DH + PAD;     // rows over head_dim
+  static constexpr int LDI = 64 + PAD;     // rows over the 64 queries / keys
+  // Qs, Ks, Vs, dOs [64][LDE]; Qt, Kt, dOt [DH][LDI]; per-wave stage [4][16][LDI]
+  static constexpr int LDS_ELEMS = 4 * 64 * LDE + 3 * DH * LDI + 4 * 16 * LDI;
+};
+
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
+  using C = AttnBwdCfg<T, DH>;
+  constexpr int LDE = C::LDE, LDI = C::LDI, NDT = DH / 16;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  T* Qs = reinterpret_cast<T*>(smem_raw);
+  T* Ks = Qs + 64 * LDE;
+  T* Vs = Ks + 64 * LDE;
+  T* dOs = Vs + 64 * LDE;
+  T* Qt = dOs + 64 * LDE;
+  T* Kt = Qt + DH * LDI;
+  T* dOt = Kt + DH * LDI;
+  T* Wst = dOt + DH * LDI;
+  __shared__ float sM[64], sZ[64], sD[64];
+
+  const CellGeom& g = a.g;
+  const int bh = blockIdx.x, b = bh / g.h, hh = bh - b * g.h;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g4 = lane >> 4, lc = lane & 15;
+  const int d = g.d, c = g.c;
+  const long lrow0 = (long)bh * g.Tbuf + g.buf_t0;
+  T* W = Wst + wave * 16 * LDI;
+
+  // ---- phase 1: 4 threads per row i build dO, D, stage Q / K / V / dO, self column
+  {
+    constexpr int EPT = DH / 4;          // elements per thread
+    const int i = tid >> 2, part = tid & 3, e0 = part * EPT;
+    const bool ok = i < c;
+    const int ic = ok ? i : 0;
+    const long n = (long)b * c + ic;                      // row of the sweep arrays
+    float q[EPT], kv[EPT], vv[EPT], ks[EPT], vr[EPT], ov[EPT], gwv[EPT], dc[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      q[e] = to_f(a.qr[(lrow0 + ic) * DH + e0 + e]);
+      kv[e] = to_f(a.Kin[(long)bh * a.in_stride + (long)(a.in_row0 + ic) * DH + e0 + e]);
+      vv[e] = to_f(a.Vin[(long)bh * a.in_stride + (long)(a.in_row0 + ic) * DH + e0 + e]);
+      ks[e] = to_f(a.kself[(lrow0 + ic) * DH + e0 + e]);
+      vr[e] = to_f(a.vraw[(lrow0 + ic) * DH + e0 + e]);
+      ov[e] = to_f(a.o[n * d + hh * DH + e0 + e]);
+      gwv[e] = a.gw[n * d + hh * DH + e0 + e];
+      dc[e] = a.docat != nullptr ? a.docat[((long)b * g.Tbuf + g.buf_t0 + ic) * d + hh * DH + e0 + e] : 0.f;
+    }
+    float ss = 0.f, dot = 0.f;
+    for (int p = part; p < g.h; p += 4) ss += a.ssq[n * g.h + p];
+    for (int p = part; p < a.nrd; p += 4) dot += a.rowdot[n * a.nrd + p];
+    ss += __shfl_xor(ss, 1, 64); ss += __shfl_xor(ss, 2, 64);
+    dot += __shfl_xor(dot, 1, 64); dot += __shfl_xor(dot, 2, 64);
+    const float r = rsqrtf(ss * a.inv_d + a.eps);
+    const float c3 = r * r * r * a.inv_d * dot;
+    const float Mi = ok ? a.stat_m[(long)bh * c + i] : 0.f;
+    const float Zi = ok ? a.stat_z[(long)bh * c + i] : 1.f;
+    float dO[EPT], Dp = 0.f, sq = 0.f, dov = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      dO[e] = ok ? r * gwv[e] - ov[e] * c3 + dc[e] : 0.f;
+      dO[e] = to_f(from_f<T>(dO[e]));    // the value the MFMA products use
+      Dp += dO[e] * ov[e];
+      sq += q[e] * ks[e];
+      dov += dO[e] * vr[e];
+    }
+    Dp += __shfl_xor(Dp, 1, 64); Dp += __shfl_xor(Dp, 2, 64);
+    sq += __shfl_xor(sq, 1, 64); sq += __shfl_xor(sq, 2, 64);
+    dov += __shfl_xor(dov, 1, 64); dov += __shfl_xor(dov, 2, 64);
+    // raw self column: p_self = exp(s_self - M) / Z, dS_self = p_self (dO.v_raw - D)
+    const float ps = ok ? __expf(sq * a.scale - Mi) / Zi : 0.f;
+    const float dss = ps * (dov - Dp);
+    if (part == 0) { sM[i] = Mi; sZ[i] = Zi; sD[i] = Dp; }
+    // committed part: alpha = exp(m_comm - M) / Z
+    if (a.Mx != nullptr && ok) {
+      const float alpha = __expf(a.Mx[(long)bh * c + i] - Mi) / Zi;
+      float* Gr = a.G + ((long)bh * CMAX + i) * DH + e0;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) Gr[e] = (a.first ? 0.f : Gr[e]) + alpha * dO[e];
+      if (part == 0) a.Dbar[(long)bh * CMAX + i] = (a.first ? 0.f : a.Dbar[(long)bh * CMAX + i]) + alpha * Dp;
+    }
+    if (ok) {
+      const long lr = (lrow0 + i) * DH + e0;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        a.dkself[lr + e] += a.scale * dss * q[e];
+        a.dvraw[lr + e] += ps * dO[e];
+        a.dq[lr + e] += a.scale * dss * ks[e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int col = e0 + e;
+      Qs[i * LDE + col] = from_f<T>(ok ? q[e] : 0.f);
+      Ks[i * LDE + col] = from_f<T>(ok ? kv[e] : 0.f);
+      Vs[i * LDE + col] = from_f<T>(ok ? vv[e] : 0.f);
+      dOs[i * LDE + col] = from_f<T>(dO[e]);
+      Qt[col * LDI + i] = from_f<T>(ok ? q[e] : 0.f);
+      Kt[col * LDI + i] = from_f<T>(ok ? kv[e] : 0.f);
+      dOt[col * LDI + i] = from_f<T>(dO[e]);
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2: query-major (rows i = 16 wave + ..): dS, then dQ = dS . K
+  {
+    floatx4 S[4], dP[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) { S[t] = zero4(); dP[t] = zero4(); }
+    wave_mma<T, DH, 4>(Qs + 16 * wave * LDE, LDE, Ks, LDE, S);
+    wave_mma<T, DH, 4>(dOs + 16 * wave * LDE, LDE, Vs, LDE, dP);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int il = 4 * g4 + r, i = 16 * wave + il;
+      const float Mi = sM[i], Zi = sZ[i], Di = sD[i];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int j = 16 * t + lc;
+        const float p = (j < i && i < c) ? __expf(S[t][r] * a.scale - Mi) / Zi : 0.f;
+        W[il * LDI + j] = from_f<T>(p * (dP[t][r] - Di));
+      }
+    }
+    __syncthreads();
+    floatx4 dQ[NDT];
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) dQ[t] = zero4();
+    wave_mma<T, 64, NDT>(W, LDI, Kt, LDI, dQ);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * wave + 4 * g4 + r;
+      if (i >= c) continue;
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) a.dq[(lrow0 + i) * DH + 16 * t + lc] += a.scale * dQ[t][r];
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 3: key-major (rows j = 16 wave + ..): P^T, dS^T -> dV = P^T dO, dK = dS^T Q
+  {
+    floatx4 St[4], dPt[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) { St[t] = zero4(); dPt[t] = zero4(); }
+    wave_mma<T, DH, 4>(Ks + 16 * wave * LDE, LDE, Qs, LDE, St);
+    wave_mma<T, DH, 4>(Vs + 16 * wave * LDE, LDE, dOs, LDE, dPt);
+    float Pt[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int i = 16 * t + lc;
+      const float Mi = sM[i], Zi = sZ[i];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * wave + 4 * g4 + r;
+        Pt[t][r] = (j < i && i < c) ? __expf(St[t][r] * a.scale - Mi) / Zi : 0.f;
+        W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r]);
+      }
+    }
+    __syncthreads();
+    floatx4 dV[NDT], dK[NDT];
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) { dV[t] = zero4(); dK[t] = zero4(); }
+    wave_mma<T, 64, NDT>(W, LDI, dOt, LDI, dV);
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int i = 16 * t + lc;
+      const float Di = sD[i];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r] * (dPt[t][r] - Di));
+    }
+    __syncthreads();
+    wave_mma<T, 64, NDT>(W, LDI, Qt, LDI, dK);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int j = 16 * wave + 4 * g4 + r;
+      if (j >= c) continue;
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        const int e = 16 * t + lc;
+        if (a.dKout != nullptr) {
+          a.dKout[((long)bh * CMAX + j) * DH + e] = a.scale * dK[t][r];
+          a.dVout[((long)bh * CMAX + j) * DH + e] = dV[t][r];
+        } else {
+          a.dkself[(lrow0 + j) * DH + e] += a.scale * dK[t][r];
+          a.dvraw[(lrow0 + j) * DH + e] += dV[t][r];
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// committed-prefix VJP of a cell, one block per (split, b, h) over the split's
+// key tiles: dq partials, dK / dV of the committed rows into the grad cache.
+// ---------------------------------------------------------------------------
+template <typename T> struct CommBwdArgs {
+  CellGeom g;
+  int split_len;
+  const T* qr; const T* Kc; const T* Vc;   // layer buffer q_r; cache rows [0, pos0)
+  const float* Mx;                         // [B*h, c] committed row max (forward layout)
+  const float* G; const float* Dbar;       // [B*h, CMAX, DH], [B*h, CMAX]
+  float scale;
+  float* dKgc; float* dVgc;                // grad cache [B, h, cache_T, DH] (+=)
+  float* dq_part;                          // [nsplit, B*h, CMAX, DH]
+};
+
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_comm_bwd(CommBwdArgs<T> a) {
+  using C = AttnBwdCfg<T, DH>;
+  constexpr int LDE = C::LDE, LDI = C::LDI, NDT = DH / 16;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  T* Qs = reinterpret_cast<T*>(smem_raw);
+  T* Ks = Qs + 64 * LDE;
+  T* Vs = Ks + 64 * LDE;
+  T* Gs = Vs + 64 * LDE;
+  T* Qt = Gs + 64 * LDE;
+  T* Kt = Qt + DH * LDI;
+  T* Gt = Kt + DH * LDI;
+  T* Wst = Gt + DH * LDI;
+  __shared__ float sM[64], sD[64];
+
+  const CellGeom& g = a.g;
+  const int s = blockIdx.x, bh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g4 = lane >> 4, lc = lane & 15;
+  const int c = g.c;
+  const int k_begin = s * a.split_len, k_end = min(k_begin + a.split_len, g.pos0);
+  T* W = Wst + wave * 16 * LDI;
+  const long lrow0 = (long)bh * g.Tbuf + g.buf_t0;
+  const T* Kb = a.Kc + (long)bh * g.cache_T * DH;
+  const T* Vb = a.Vc + (long)bh * g.cache_T * DH;
+
+  // queries and committed grads of the block's 64 rows
+  {
+    constexpr int EPT = DH / 4;
+    const int i = tid >> 2, e0 = (tid & 3) * EPT;
+    const bool ok = i < c;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const float q = ok ? to_f(a.qr[(lrow0 + i) * DH + e0 + e]) : 0.f;
+      const float gg = ok ? a.G[((long)bh * CMAX + i) * DH + e0 + e] : 0.f;
+      Qs[i * LDE + e0 + e] = from_f<T>(q);
+      Qt[(e0 + e) * LDI + i] = from_f<T>(q);
+      Gs[i * LDE + e0 + e] = from_f<T>(gg);
+      Gt[(e0 + e) * LDI + i] = from_f<T>(gg);
+    }
+    if ((tid & 3) == 0) {
+      sM[i] = ok ? a.Mx[(long)bh * c + i] : 0.f;
+      sD[i] = ok ? a.Dbar[(long)bh * CMAX + i] : 0.f;
+    }
+  }
+  floatx4 dQ[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) dQ[t] = zero4();
+
+  for (int k0 = k_begin; k0 < k_end; k0 += 64) {
+    const int nv = min(64, k_end - k0);
+    __syncthreads();
+    {
+      constexpr int EPT = DH / 4;
+      const int j = tid >> 2, e0 = (tid & 3) * EPT;
+      const bool ok = j < nv;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const float kk = ok ? to_f(Kb[(long)(k0 + j) * DH + e0 + e]) : 0.f;
+        const float vv = ok ? to_f(Vb[(long)(k0 + j) * DH + e0 + e]) : 0.f;
+        Ks[j * LDE + e0 + e] = from_f<T>(kk);
+        Kt[(e0 + e) * LDI + j] = from_f<T>(kk);
+        Vs[j * LDE + e0 + e] = from_f<T>(vv);
+      }
+    }
+    __syncthreads();
+    // query-major: dS = E (G V^T - Dbar), dQ += dS K
+    {
+      floatx4 S[4], dP[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) { S[t] = zero4(); dP[t] = zero4(); }
+      wave_mma<T, DH, 4>(Qs + 16 * wave * LDE, LDE, Ks, LDE, S);
+      wave_mma<T, DH, 4>(Gs + 16 * wave * LDE, LDE, Vs, LDE, dP);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int il = 4 * g4 + r, i = 16 * wave + il;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int j = 16 * t + lc;
+          const float e = (j < nv && i < c) ? __expf(S[t][r] * a.scale - sM[i]) : 0.f;
+          W[il * LDI + j] = from_f<T>(e * (dP[t][r] - sD[i]));
+        }
+      }
+      __syncthreads();
+      wave_mma<T, 64, NDT>(W, LDI, Kt, LDI, dQ);
+    }
+    __syncthreads();
+    // key-major: E^T, dS^T -> dV = E^T G, dK = dS^T Q (rows j = 16 wave + ..)
+    {
+      floatx4 St[4], dPt[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) { St[t] = zero4(); dPt[t] = zero4(); }
+      wave_mma<T, DH, 4>(Ks + 16 * wave * LDE, LDE, Qs, LDE, St);
+      wave_mma<T, DH, 4>(Vs + 16 * wave * LDE, LDE, Gs, LDE, dPt);
+      float Et[4][4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int i = 16 * t + lc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * wave + 4 * g4 + r;
+          Et[t][r] = (j < nv && i < c) ? __expf(St[t][r] * a.scale - sM[i]) : 0.f;
+          W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[t][r]);
+        }
+      }
+      __syncthreads();
+      floatx4 dV[NDT], dK[NDT];
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) { dV[t] = zero4(); dK[t] = zero4(); }
+      wave_mma<T, 64, NDT>(W, LDI, Gt, LDI, dV);
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int i = 16 * t + lc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[t][r] * (dPt[t][r] - sD[i]));
+      }
+      __syncthreads();
+      wave_mma<T, 64, NDT>(W, LDI, Qt, LDI, dK);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * wave + 4 * g4 + r;
+        if (j >= nv) continue;
+        const long row = ((long)bh * g.cache_T + k0 + j) * DH;
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) {
+          a.dKgc[row + 16 * t + lc] += a.scale * dK[t][r];
+          a.dVgc[row + 16 * t + lc] += dV[t][r];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = 16 * wave + 4 * g4 + r;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+      a.dq_part[(((long)s * g.B * g.h + bh) * CMAX + i) * DH + 16 * t + lc] = a.scale * dQ[t][r];
+  }
+}
+
+// dq[b, h, buf_t0 + i] += sum_s dq_part[s, bh, i]
+static __global__ __launch_bounds__(256) void k_dq_reduce(CellGeom g, int nsplit, const float* __restrict__ dq_part,
+                                                   float* __restrict__ dq) {
+  const long BH = (long)g.B * g.h;
+  const long n = BH * g.c * g.dh;
+  for (long idx = blockIdx.x * 256L + threadIdx.x; idx < n; idx += (long)gridDim.x * 256) {
+    const int e = idx % g.dh;
+    const long r = idx / g.dh;
+    const int i = r % g.c;
+    const long bh = r / g.c;
+    float s = 0.f;
+    for (int sp = 0; sp < nsplit; ++sp) s += dq_part[((sp * BH + bh) * CMAX + i) * g.dh + e];
+    dq[(bh * g.Tbuf + g.buf_t0 + i) * g.dh + e] += s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// projection VJP inputs: d_proj [B*T, nproj*d] in the w_proj row order
+//   q: unrotate dq_r; k: dkraw + unrotate(dkself); v: dvraw; gate x-halves: dglogx;
+//   v_gate: dsig * sig * (1 - sig)
+// ---------------------------------------------------------------------------
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, int h, int nproj,
+                                                  const float* __restrict__ dq, const float* __restrict__ dkraw,
+                                                  const float* __restrict__ dkself, const float* __restrict__ dvraw,
+                                                  const float* __restrict__ dglogx, const float* __restrict__ dsig,
+                                                  const float* __restrict__ sig, const float* __restrict__ cos,
+                                                  const float* __restrict__ sin, T* __restrict__ dproj) {
+  const long idx = blockIdx.x * 256L + threadIdx.x;
+  const int per_row = d / 2;
+  if (idx >= (long)M * per_row) return;
+  const int m = idx / per_row, rem = idx - (long)m * per_row;
+  const int hd = rem / (DH / 2), jj = rem - hd * (DH / 2);
+  const int b = m / T_, t = m - b * T_;
+  const long hr = (((long)b * h + hd) * T_ + t) * DH;
+  const float cs = cos[(long)t * (DH / 2) + jj], sn = sin[(long)t * (DH / 2) + jj];
+  const int c1 = hd * DH + jj, c2 = c1 + DH / 2;
+  T* D = dproj + (long)m * nproj * d;
+  // q
+  {
+    const float a1 = dq[hr + jj], a2 = dq[hr + jj + DH / 2];
+    D[c1] = from_f<T>(a1 * cs + a2 * sn);
+    D[c2] = from_f<T>(-a1 * sn + a2 * cs);
+  }
+  // k
+  {
+    const float a1 = dkself[hr + jj], a2 = dkself[hr + jj + DH / 2];
+    D[d + c1] = from_f<T>(dkraw[hr + jj] + a1 * cs + a2 * sn);
+    D[d + c2] = from_f<T>(dkraw[hr + jj + DH / 2] - a1 * sn + a2 * cs);
+  }
+  // v
+  D[2 * d + c1] = from_f<T>(dvraw[hr + jj]);
+  D[2 * d + c2] = from_f<T>(dvraw[hr + jj + DH / 2]);
+  // gate x-halves
+  const float* dg = dglogx + (long)m * 2 * d;
+  D[3 * d + c1] = from_f<T>(dg[c1]);
+  D[3 * d + c2] = from_f<T>(dg[c2]);
+  D[4 * d + c1] = from_f<T>(dg[d + c1]);
+  D[4 * d + c2] = from_f<T>(dg[d + c2]);
+  if (nproj == 6) {
+    const float s1 = sig[(long)m * d + c1], s2 = sig[(long)m * d + c2];
+    D[5 * d + c1] = from_f<T>(dsig[(long)m * d + c1] * s1 * (1.f - s1));
+    D[5 * d + c2] = from_f<T>(dsig[(long)m * d + c2] * s2 * (1.f - s2));
+  }
+}
+
+// Column sums of the bias gradients over the M rows, stage 1: part[chunk][col]
+//   cols [0, 2d): dglogx; cols [2d, 3d): dsig * sig * (1 - sig)
+static __global__ __launch_bounds__(256) void k_bias_partial(int M, int d, int ncols, int rows_per_chunk,
+                                                      const float* __restrict__ dglogx,
+                                                      const float* __restrict__ dsig,
+                                                      const float* __restrict__ sig, float* __restrict__ part) {
+  const int col = blockIdx.x * 256 + threadIdx.x;
+  if (col >= ncols) return;
+  const int r0 = blockIdx.y * rows_per_chunk, r1 = min(r0 + rows_per_chunk, M);
+  float s = 0.f;
+  for (int m = r0; m < r1; ++m) {
+    if (col < 2 * d) {
+      s += dglogx[(long)m * 2 * d + col];
+    } else {
+      const float sg = sig[(long)m * d + col - 2 * d];
+      s += dsig[(long)m * d + col - 2 * d] * sg * (1.f - sg);
+    }
+  }
+  part[(long)blockIdx.y * ncols + col] = s;
+}
+
+// Column sums of a row-major fp32 matrix [M, ncols], stage 1: part[chunk][col]
+static __global__ __launch_bounds__(256) void k_colsum_partial(int M, int ncols, int rows_per_chunk,
+                                                        const float* __restrict__ src, float* __restrict__ part) {
+  const int col = blockIdx.x * 256 + threadIdx.x;
+  if (col >= ncols) return;
+  const int r0 = blockIdx.y * rows_per_chunk, r1 = min(r0 + rows_per_chunk, M);
+  float s = 0.f;
+  for (int m = r0; m < r1; ++m) s += src[(long)m * ncols + col];
+  part[(long)blockIdx.y * ncols + col] = s;
+}
+
+// out[col] += sum_chunk part[chunk * ld + col], col < ncols
+static __global__ __launch_bounds__(256) void k_sum_rows_add(int nchunk, int ncols, int ld, const float* __restrict__ part,
+                                                      float* __restrict__ out) {
+  const int col = blockIdx.x * 256 + threadIdx.x;
+  if (col >= ncols) return;
+  float s = 0.f;
+  for (int k = 0; k < nchunk; ++k) s += part[(long)k * ld + col];
+  out[col] += s;
+}
+
+// ---------------------------------------------------------------------------
+// attn_norm VJP (attention.py:74-83) with the block residual, one wave per row:
+//   dx = dy + r w dxhat - x r^3 / d <w dxhat, x>; dwa_part[row / 4 group] over rows
+// ---------------------------------------------------------------------------
+template <typename T>
+static __global__ __launch_bounds__(256) void k_rmsnorm_bwd(int M, int d, float eps, int residual,
+                                                     const T* __restrict__ x, const T* __restrict__ w,
+                                                     const float* __restrict__ dxhat, const T* __restrict__ dy,
+                                                     T* __restrict__ dx, float* __restrict__ dwa_part) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const T* xr = x + (long)m * d;
+  const float* gr = dxhat + (long)m * d;
+  float ss = 0.f, dot = 0.f;
+  for (int j = lane; j < d; j += 64) {
+    const float xv = to_f(xr[j]);
+    ss += xv * xv;
+    dot += to_f(w[j]) * gr[j] * xv;
+  }
+  ss = wave_sum(ss);
+  dot = wave_sum(dot);
+  const float r = rsqrtf(ss / (float)d + eps);
+  const float c3 = r * r * r / (float)d * dot;
+  for (int j = lane; j < d; j += 64) {
+    const float xv = to_f(xr[j]);
+    float v = r * to_f(w[j]) * gr[j] - xv * c3;
+    if (residual) v += to_f(dy[(long)m * d + j]);
+    dx[(long)m * d + j] = from_f<T>(v);
+    dwa_part[(long)m * d + j] = gr[j] * xv * r;   // summed over rows afterwards
+  }
+}
+
+// dx = dy + dxhat (no attn_norm) or dx = dxhat (no residual either)
+template <typename T>
+static __global__ __launch_bounds__(256) void k_dx_plain(long n, int residual, const float* __restrict__ dxhat,
+                                                  const T* __restrict__ dy, T* __restrict__ dx) {
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256)
+    dx[i] = from_f<T>(dxhat[i] + (residual ? to_f(dy[i]) : 0.f));
+}
+
+// ---------------------------------------------------------------------------
+// unpack: ref[dst rows] (+)= packed[src rows] (fp32), the inverse of k_pack
+// ---------------------------------------------------------------------------
+struct UnpackSeg {
+  float* dst;
+  long dst_ld;     // elements between destination rows
+  int dst_col;     // first destination column
+  int nrows;
+  int src_row;     // first packed row
+  int pad_;
+};
+constexpr int UNPACK_MAX_SEG = 48;
+struct UnpackArgs {
+  UnpackSeg seg[UNPACK_MAX_SEG];
+  int nseg;
+  int ncols;
+  const float* src;
+};
+
+static __global__ __launch_bounds__(256) void k_unpack_add(UnpackArgs a) {
+  const int row = blockIdx.x;
+  int s = 0, acc = 0;
+  while (s < a.nseg && row >= acc + a.seg[s].nrows) { acc += a.seg[s].nrows; ++s; }
+  const UnpackSeg& sg = a.seg[s];
+  const int r = row - acc;
+  const float* src = a.src + (long)(sg.src_row + r) * a.ncols;
+  float* dst = sg.dst + (long)r * sg.dst_ld + sg.dst_col;
+  for (int j = threadIdx.x; j < a.ncols; j += 256) dst[j] += src[j];
+}
+
+}  // namespace dm

@@ -1,0 +1,371 @@
+// libdm_hip.so — the backward entry points of the C ABI (include/dm_abi.h):
+// reverse-scan layer backward with exact per-cell recompute.
+//
+// Never allocates device memory and never synchronizes: every buffer is carved
+// from the caller's workspace; all launches go to the caller's stream.
+#include <vector>
+
+#include "dm_bwd.h"
+#include "dm_fwd_host.h"
+
+namespace dm {
+
+template <typename T> struct BwdWs {
+  // layer accumulators (fp32)
+  float *dq, *dkraw, *dkself, *dvraw;   // [B, h, T, dh]
+  float *dKgc, *dVgc;                   // [B, h, cache_T, dh] grad cache of the refined rows
+  float *dglogx;                        // [B, T, 2d]
+  float *dsig;                          // [B, T, d]
+  float *docat;                         // [B, T, d] = dy . W_O
+  float *dnw;                           // [NSLOT, d] norm_ctx.weight partials
+  // one cell
+  CellWs fws;                           // forward scratch of the recompute
+  CellSave<T> sv;                       // every sweep's state
+  T *dctx, *dvc;                        // [K][N, 4d], [K][N, d]
+  float *dKa, *dVa, *dKb, *dVb;         // [B*h, CMAX, dh] grads of the intra rows (ping-pong)
+  float *lamdv, *gw, *rowdot;           // [N, d], [N, d], [N, NRD]
+  float *G, *Dbar;                      // [B*h, CMAX, dh], [B*h, CMAX]
+  float *dq_part;                       // [nsplit, B*h, CMAX, dh]
+  // layer close
+  T* dproj;                             // [B*T, nproj*d]
+  float* dxhat;                         // [B*T, d]
+  float *dWp, *dWs;                     // packed weight-grad staging [nproj*d, d], [4d, d]
+  float* colpart;                       // [NCHUNK, 3d]
+  size_t bytes;
+};
+
+constexpr int NSLOT_TM = 32;      // rows per norm_ctx-weight partial slot (du GEMM wave tile)
+constexpr int DU_TN = 32;         // columns per row-dot partial (du GEMM wave tile)
+constexpr int NCHUNK = 64;        // row chunks of the column sums
+
+template <typename T>
+BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base) {
+  BwdWs<T> w{};
+  const size_t B = c->B, d = c->d, h = c->h, dh = c->dh, e = sizeof(T);
+  const size_t BT = B * T_, BH = B * h, N = B * CMAX;
+  const size_t nproj = c->ctx_mod == DM_CTX_LINEAR ? 5 : 6;
+  Carver cv(base);
+  w.dq = cv.take<float>(BT * d * 4);
+  w.dkraw = cv.take<float>(BT * d * 4);
+  w.dkself = cv.take<float>(BT * d * 4);
+  w.dvraw = cv.take<float>(BT * d * 4);
+  w.dKgc = cv.take<float>(B * cache_T * d * 4);
+  w.dVgc = cv.take<float>(B * cache_T * d * 4);
+  w.dglogx = cv.take<float>(BT * 2 * d * 4);
+  w.dsig = cv.take<float>(BT * d * 4);
+  w.docat = cv.take<float>(BT * d * 4);
+  w.dnw = cv.take<float>(cdiv(N, NSLOT_TM) * d * 4);
+  w.fws = carve_cell(c, cache_T, cv.base ? cv.base + cv.off : nullptr);
+  cv.off += align256(w.fws.bytes);
+  w.sv.o = cv.take<T>(kmax * N * d * e);
+  w.sv.ssq = cv.take<float>(kmax * N * h * 4);
+  w.sv.stat_m = cv.take<float>(kmax * BH * CMAX * 4);
+  w.sv.stat_z = cv.take<float>(kmax * BH * CMAX * 4);
+  w.sv.save1 = cv.take<float>(kmax * N * 4 * d * 4);
+  w.sv.save2 = cv.take<float>(kmax * N * d * 4);
+  w.sv.vin = cv.take<T>(kmax * N * d * e);
+  w.sv.u = cv.take<T>(kmax * N * d * e);
+  w.sv.Kin = cv.take<T>((kmax + 1) * BH * CMAX * dh * e);
+  w.sv.Vin = cv.take<T>((kmax + 1) * BH * CMAX * dh * e);
+  w.dctx = cv.take<T>(kmax * N * 4 * d * e);
+  w.dvc = cv.take<T>(kmax * N * d * e);
+  w.dKa = cv.take<float>(BH * CMAX * dh * 4);
+  w.dVa = cv.take<float>(BH * CMAX * dh * 4);
+  w.dKb = cv.take<float>(BH * CMAX * dh * 4);
+  w.dVb = cv.take<float>(BH * CMAX * dh * 4);
+  w.lamdv = cv.take<float>(N * d * 4);
+  w.gw = cv.take<float>(N * d * 4);
+  w.rowdot = cv.take<float>(N * (d / DU_TN) * 4);
+  w.G = cv.take<float>(BH * CMAX * dh * 4);
+  w.Dbar = cv.take<float>(BH * CMAX * 4);
+  w.dq_part = cv.take<float>(comm_splits_max(cache_T) * BH * CMAX * dh * 4);
+  // the attn_norm weight partials [B*T, d] fp32 reuse dproj once it is consumed
+  w.dproj = cv.take<T>(std::max(BT * nproj * d * e, BT * d * 4));
+  w.dxhat = cv.take<float>(BT * d * 4);
+  w.dWp = cv.take<float>(nproj * d * d * 4);
+  w.dWs = cv.take<float>(4 * d * d * 4);
+  w.colpart = cv.take<float>(NCHUNK * 3 * d * 4);
+  w.bytes = cv.off;
+  return w;
+}
+
+inline void fill0(float* p, size_t n, hipStream_t s) {
+  const int blocks = (int)std::min<size_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(k_fill, dim3(blocks), dim3(256), 0, s, p, (long)n, 0.f);
+}
+
+// out[chunk] column sums of a [M, ncols] fp32 matrix, added into dst[0..ncols)
+inline void colsum_add(const float* src, int M, int ncols, float* part, float* dst, hipStream_t s) {
+  const int rpc = cdiv(M, NCHUNK);
+  hipLaunchKernelGGL(k_colsum_partial, dim3(cdiv(ncols, 256), NCHUNK), dim3(256), 0, s, M, ncols, rpc, src, part);
+  hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(ncols, 256)), dim3(256), 0, s, NCHUNK, ncols, ncols, part, dst);
+}
+
+inline void unpack(const std::vector<UnpackSeg>& segs, int ncols, const float* src, hipStream_t s) {
+  for (size_t i0 = 0; i0 < segs.size(); i0 += UNPACK_MAX_SEG) {
+    UnpackArgs a{};
+    a.nseg = (int)std::min<size_t>(UNPACK_MAX_SEG, segs.size() - i0);
+    int rows = 0;
+    for (int i = 0; i < a.nseg; ++i) { a.seg[i] = segs[i0 + i]; rows += a.seg[i].nrows; }
+    a.ncols = ncols;
+    a.src = src;
+    hipLaunchKernelGGL(k_unpack_add, dim3(rows), dim3(256), 0, s, a);
+  }
+}
+
+// fp32 staging C [M, N] (+)= op(A) . op(B)^T with K-major (transposed) operands
+template <typename T>
+void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N, int K, int accumulate,
+             hipStream_t s) {
+  EpiStoreF32 ep{M, N, accumulate, C};
+  SrcKMajor<T> sa{A, lda, M, K};
+  SrcKMajor<T> sb{Bm, ldb, N, K};
+  launch_gemm<T, 128, 128, 2, 2, 4>(sa, sb, M, N, K, ep, s);
+}
+
+template <typename T, int DH>
+int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T* dx, const float* cos,
+                  const float* sin, const dm_layer_bufs* L, const int32_t* sched, int n_cells, const T* Kc,
+                  const T* Vc, int cache_T, const T* ocat, const dm_grads* gr, const BwdWs<T>& ws, hipStream_t s) {
+  const int B = c->B, d = c->d, h = c->h, T_ = L->T, BT = B * T_, BH = B * h;
+  const bool mult = c->ctx_mod != DM_CTX_LINEAR;
+  const int nproj = mult ? 6 : 5;
+  const bool norm = w->attn_norm_w != nullptr;
+  const bool residual = !(c->flags & DM_FLAG_NO_RESIDUAL);
+  const float scale = 1.0f / sqrtf((float)DH);
+  const float inv_d = 1.0f / (float)d;
+  ProfScope whole(PROF_BWD, s);
+
+  // ---- zero the accumulators
+  fill0(ws.dq, (size_t)BT * d, s);
+  fill0(ws.dkraw, (size_t)BT * d, s);
+  fill0(ws.dkself, (size_t)BT * d, s);
+  fill0(ws.dvraw, (size_t)BT * d, s);
+  fill0(ws.dKgc, (size_t)B * cache_T * d, s);
+  fill0(ws.dVgc, (size_t)B * cache_T * d, s);
+  fill0(ws.dglogx, (size_t)BT * 2 * d, s);
+  fill0(ws.dsig, (size_t)BT * d, s);
+  fill0(ws.dnw, (size_t)cdiv(B * CMAX, NSLOT_TM) * d, s);
+  fill0(ws.dWs, (size_t)4 * d * d, s);
+
+  // ---- W_O: do_cat = dy . W_O ; dW_O += dy^T . ocat
+  {
+    EpiStoreF32 ep{BT, d, 0, ws.docat};
+    launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{dy, d, BT}, SrcRows<T>{(const T*)w->wo_t, d, d}, BT, d, d, ep, s);
+    gemm_tn<T>(dy, d, ocat, d, gr->wo, d, d, BT, 1, s);
+  }
+
+  const T* qr = (const T*)L->qr;
+  const T* kself = (const T*)L->kself;
+  const T* vraw = (const T*)L->vraw;
+  const T* kraw = (const T*)L->kraw;
+  const size_t slot = (size_t)BH * CMAX * DH;
+
+  for (int ci = n_cells - 1; ci >= 0; --ci) {
+    const int pos0 = sched[3 * ci], cc = sched[3 * ci + 1], K = sched[3 * ci + 2];
+    const int N = B * cc;
+    const size_t NS = (size_t)N;
+    CellGeom g{B, cc, d, h, DH, pos0, pos0, T_, cache_T};
+    // exact recompute of the cell, keeping every sweep's state
+    run_cell<T, DH>(c, w, L, cos, sin, pos0, cc, K, pos0, T_, (T*)Kc, (T*)Vc, cache_T, nullptr, nullptr, ws.fws,
+                    &ws.sv, s);
+    const float* Mx = pos0 > 0 ? ws.fws.M : nullptr;
+    const float* dKn = ws.dKgc;
+    const float* dVn = ws.dVgc;
+    long dn_stride = (long)cache_T * DH;
+    int dn_row0 = pos0;
+    for (int sw = K - 1; sw >= 0; --sw) {
+      // refine VJP of sweep sw
+      RefineBwdArgs<T> ra{g, N, c->ctx_mod, dKn, dVn, dn_stride, dn_row0, ws.sv.save1 + sw * NS * 4 * d,
+                          ws.sv.save2 + sw * NS * d, L->glogx, kraw, vraw, cos, sin, ws.dctx + sw * NS * 4 * d,
+                          ws.dvc + sw * NS * d, ws.dglogx, ws.dkraw, ws.dvraw};
+      hipLaunchKernelGGL((k_refine_bwd<T, DH>), dim3(cdiv((long)N * d / 2, 256)), dim3(256), 0, s, ra);
+      // dv_in = dv_ctx . W_vctx (mult family)
+      if (mult) {
+        EpiVinBwd<T> ev{g, N, c->ctx_mod, c->mult_res_lambda, ws.sv.save1 + sw * NS * 4 * d, L->sig,
+                        ws.dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
+        launch_gemm<T, 64, 64, 2, 2, 4>(SrcRows<T>{ws.dvc + sw * NS * d, d, N},
+                                        SrcRows<T>{(const T*)w->w_vctx_t, d, d}, N, d, d, ev, s);
+      }
+      // du = dctx . W_sweep (+ lam dv_in) -> RMS VJP inputs
+      {
+        EpiDuBwd<T> eu{N, d, h, d / DU_TN, inv_d, c->rms_eps, mult ? ws.lamdv : nullptr, ws.sv.o + sw * NS * d,
+                       ws.sv.ssq + sw * NS * h, (const T*)w->norm_ctx_w, ws.gw, ws.rowdot, ws.dnw};
+        launch_gemm<T, 64, 64, 2, 2, 4>(SrcRows<T>{ws.dctx + sw * NS * 4 * d, 4 * d, N},
+                                        SrcRows<T>{(const T*)w->w_sweep_t, 4 * d, d}, N, d, 4 * d, eu, s);
+      }
+      // attention VJP of sweep sw
+      {
+        const T* Kin; const T* Vin; long in_stride; int in_row0;
+        if (sw == 0) { Kin = kself; Vin = vraw; in_stride = (long)T_ * DH; in_row0 = pos0; }
+        else { Kin = ws.sv.Kin + sw * slot; Vin = ws.sv.Vin + sw * slot; in_stride = (long)CMAX * DH; in_row0 = 0; }
+        float* dKo = sw == 0 ? nullptr : ((K - 1 - sw) % 2 == 0 ? ws.dKa : ws.dKb);
+        float* dVo = sw == 0 ? nullptr : ((K - 1 - sw) % 2 == 0 ? ws.dVa : ws.dVb);
+        AttnBwdArgs<T> aa{g, qr, kself, vraw, Kin, Vin, in_stride, in_row0, ws.sv.o + sw * NS * d,
+                          ws.sv.ssq + sw * NS * h, ws.gw, ws.rowdot, d / DU_TN,
+                          sw == K - 1 ? ws.docat : nullptr, ws.sv.stat_m + sw * (size_t)BH * CMAX,
+                          ws.sv.stat_z + sw * (size_t)BH * CMAX, Mx, ws.G, ws.Dbar, sw == K - 1 ? 1 : 0,
+                          scale, inv_d, c->rms_eps, dKo, dVo, ws.dkself, ws.dvraw, ws.dq};
+        const size_t lds = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
+        hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(BH), dim3(256), lds, s, aa);
+        dKn = dKo; dVn = dVo;
+        dn_stride = (long)CMAX * DH;
+        dn_row0 = 0;
+      }
+    }
+    // committed-prefix VJP (once per cell) into the grad cache and dq
+    if (pos0 > 0) {
+      const CommPlan cp = comm_plan(pos0);
+      CommBwdArgs<T> ca{g, cp.split_len, qr, Kc, Vc, Mx, ws.G, ws.Dbar, scale, ws.dKgc, ws.dVgc, ws.dq_part};
+      const size_t lds = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
+      hipLaunchKernelGGL((k_comm_bwd<T, DH>), dim3(cp.nsplit, BH), dim3(256), lds, s, ca);
+      hipLaunchKernelGGL(k_dq_reduce, dim3(cdiv((long)BH * cc * DH, 256)), dim3(256), 0, s, g, cp.nsplit,
+                         (const float*)ws.dq_part, ws.dq);
+    }
+    // weight grads of the cell's sweeps: dW_sweep += dctx^T u ; dW_vctx += dv_ctx^T v_in
+    gemm_tn<T>(ws.dctx, 4 * d, ws.sv.u, d, ws.dWs, 4 * d, d, K * N, 1, s);
+    if (mult) gemm_tn<T>(ws.dvc, d, ws.sv.vin, d, gr->w_vctx, d, d, K * N, 1, s);
+  }
+
+  // ---- projection VJP
+  hipLaunchKernelGGL((k_proj_bwd<T, DH>), dim3(cdiv((long)BT * d / 2, 256)), dim3(256), 0, s, BT, T_, d, h,
+                     nproj, (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself,
+                     (const float*)ws.dvraw, (const float*)ws.dglogx, (const float*)ws.dsig, (const float*)L->sig,
+                     cos, sin, ws.dproj);
+  {   // bias grads: column sums of dglogx (b_gk | b_gv) and of dsig sig (1 - sig) (b_vgate)
+    const int ncols = mult ? 3 * d : 2 * d;
+    const int rpc = cdiv(BT, NCHUNK);
+    hipLaunchKernelGGL(k_bias_partial, dim3(cdiv(ncols, 256), NCHUNK), dim3(256), 0, s, BT, d, ncols, rpc,
+                       (const float*)ws.dglogx, (const float*)ws.dsig, (const float*)L->sig, ws.colpart);
+    float* dst[3] = {gr->b_gk, gr->b_gv, mult ? gr->b_vgate : nullptr};
+    for (int i = 0; i < 3; ++i)
+      if (dst[i])
+        hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(d, 256)), dim3(256), 0, s, NCHUNK, d, ncols,
+                           (const float*)(ws.colpart + i * d), dst[i]);
+  }
+  const T* xhat = norm ? (const T*)L->xhat : x;
+  // dW_proj = d_proj^T . xhat (packed rows), dxhat = d_proj . W_proj
+  gemm_tn<T>(ws.dproj, (long)nproj * d, xhat, d, ws.dWp, nproj * d, d, BT, 0, s);
+  {
+    EpiStoreF32 ep{BT, d, 0, ws.dxhat};
+    launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{ws.dproj, (long)nproj * d, BT},
+                                      SrcRows<T>{(const T*)w->w_proj_t, (long)nproj * d, d}, BT, d, nproj * d, ep, s);
+  }
+  // unpack the packed weight grads into the reference layout
+  {
+    std::vector<UnpackSeg> u;
+    u.push_back(UnpackSeg{gr->wq, d, 0, d, 0, 0});
+    u.push_back(UnpackSeg{gr->wk, d, 0, d, d, 0});
+    u.push_back(UnpackSeg{gr->wv, d, 0, d, 2 * d, 0});
+    u.push_back(UnpackSeg{gr->w_gk, 2 * d, 0, d, 3 * d, 0});
+    u.push_back(UnpackSeg{gr->w_gv, 2 * d, 0, d, 4 * d, 0});
+    if (mult) u.push_back(UnpackSeg{gr->v_gate, d, 0, d, 5 * d, 0});
+    unpack(u, d, ws.dWp, s);
+    u.clear();
+    for (int hd = 0; hd < h; ++hd)
+      for (int q = 0; q < DH / 32; ++q) {
+        const int base = 2 * DH * hd + 64 * q, r0 = hd * DH + 16 * q, r1 = r0 + DH / 2;
+        u.push_back(UnpackSeg{gr->w_kctx + (size_t)r0 * d, d, 0, 16, base, 0});
+        u.push_back(UnpackSeg{gr->w_kctx + (size_t)r1 * d, d, 0, 16, base + 16, 0});
+        u.push_back(UnpackSeg{gr->w_gk + (size_t)r0 * 2 * d, 2 * d, d, 16, base + 32, 0});
+        u.push_back(UnpackSeg{gr->w_gk + (size_t)r1 * 2 * d, 2 * d, d, 16, base + 48, 0});
+      }
+    if (mult) {
+      u.push_back(UnpackSeg{gr->v_map, d, 0, d, 2 * d, 0});
+      u.push_back(UnpackSeg{gr->w_gv, 2 * d, d, d, 3 * d, 0});
+    } else {
+      for (int hd = 0; hd < h; ++hd)
+        for (int q = 0; q < DH / 32; ++q) {
+          const int base = 2 * d + 2 * DH * hd + 64 * q, r0 = hd * DH + 32 * q;
+          u.push_back(UnpackSeg{gr->w_vctx + (size_t)r0 * d, d, 0, 32, base, 0});
+          u.push_back(UnpackSeg{gr->w_gv + (size_t)r0 * 2 * d, 2 * d, d, 32, base + 32, 0});
+        }
+    }
+    unpack(u, d, ws.dWs, s);
+  }
+  // norm_ctx.weight
+  colsum_add(ws.dnw, cdiv(B * CMAX, NSLOT_TM), d, ws.colpart, gr->norm_ctx_w, s);
+  // attn_norm VJP + residual
+  if (norm) {
+    float* dwa_part = reinterpret_cast<float*>(ws.dproj);
+    hipLaunchKernelGGL(k_rmsnorm_bwd<T>, dim3(cdiv(BT, 4)), dim3(256), 0, s, BT, d, c->rms_eps, residual ? 1 : 0,
+                       x, (const T*)w->attn_norm_w, (const float*)ws.dxhat, dy, dx, dwa_part);
+    colsum_add(dwa_part, BT, d, ws.colpart, gr->attn_norm_w, s);
+  } else {
+    hipLaunchKernelGGL(k_dx_plain<T>, dim3(std::min(cdiv((long)BT * d, 256), 4096)), dim3(256), 0, s,
+                       (long)BT * d, residual ? 1 : 0, (const float*)ws.dxhat, dy, dx);
+  }
+  return DM_OK;
+}
+
+}  // namespace dm
+
+using namespace dm;
+
+extern "C" {
+
+size_t dm_layer_bwd_workspace_bytes(const dm_config* c, int32_t T, int32_t cache_T, int32_t max_sweeps) {
+  if (check_cfg(c) != DM_OK || T <= 0 || cache_T < T || max_sweeps <= 0) return 0;
+  return c->dtype == DM_BF16 ? carve_bwd<bf16>(c, T, cache_T, max_sweeps, nullptr).bytes
+                             : carve_bwd<float>(c, T, cache_T, max_sweeps, nullptr).bytes;
+}
+
+int dm_layer_bwd(const dm_config* c, const dm_packed* w, const void* x, const void* dy, void* dx,
+                 const float* cos, const float* sin, const dm_layer_bufs* L, const int32_t* sched,
+                 int32_t n_cells, const void* K_cache, const void* V_cache, int32_t cache_T, const void* ocat,
+                 const dm_grads* g, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_cfg(c);
+  if (rc) return rc;
+  if ((rc = check_packed(c, w)) || (rc = check_bufs(c, L))) return rc;
+  const bool mult = c->ctx_mod != DM_CTX_LINEAR;
+  DM_REQUIRE(x && dy && dx && cos && sin && K_cache && V_cache && ocat && g, DM_ERR_INVALID,
+             "null backward argument");
+  DM_REQUIRE(w->w_proj_t && w->w_sweep_t && w->wo_t && (!mult || w->w_vctx_t), DM_ERR_INVALID,
+             "dm_layer_bwd needs the transposed packed weights");
+  DM_REQUIRE(g->wq && g->wk && g->wv && g->wo && g->w_kctx && g->w_vctx && g->w_gk && g->w_gv && g->b_gk &&
+                 g->b_gv && g->norm_ctx_w,
+             DM_ERR_INVALID, "null gradient buffer");
+  DM_REQUIRE(!mult || (g->v_gate && g->b_vgate && g->v_map), DM_ERR_INVALID, "mult family needs v_gate/v_map grads");
+  DM_REQUIRE(w->attn_norm_w == nullptr || (g->attn_norm_w && L->xhat), DM_ERR_INVALID,
+             "attn_norm needs its gradient buffer and bufs->xhat");
+  if ((rc = dm_check_schedule(sched, n_cells, L->T))) return rc;
+  DM_REQUIRE(L->T <= cache_T, DM_ERR_INVALID, "T=%d > cache_T=%d", L->T, cache_T);
+  {   // the attention VJP keeps Q, K, V, dO and their transposes of a 64-row block in LDS
+    const size_t lds = c->dtype == DM_BF16
+                           ? (c->dh == 64 ? AttnBwdCfg<bf16, 64>::LDS_ELEMS : AttnBwdCfg<bf16, 128>::LDS_ELEMS) * 2
+                           : (c->dh == 64 ? AttnBwdCfg<float, 64>::LDS_ELEMS : AttnBwdCfg<float, 128>::LDS_ELEMS) * 4;
+    int dev = 0, lim = 0;
+    DM_HIP(hipGetDevice(&dev));
+    DM_HIP(hipDeviceGetAttribute(&lim, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+    DM_REQUIRE(lds + 1024 <= (size_t)lim, DM_ERR_UNSUPPORTED,
+               "backward attention block needs %zu bytes of LDS, device allows %d (fp32 head_dim 128)", lds, lim);
+  }
+  int kmax = 0;
+  for (int i = 0; i < n_cells; ++i) kmax = std::max(kmax, (int)sched[3 * i + 2]);
+  const size_t need = dm_layer_bwd_workspace_bytes(c, L->T, cache_T, kmax);
+  DM_REQUIRE(workspace && workspace_bytes >= need, DM_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes,
+             need);
+  hipStream_t s = S(stream);
+  if (c->dtype == DM_BF16) {
+    const BwdWs<bf16> ws = carve_bwd<bf16>(c, L->T, cache_T, kmax, workspace);
+    rc = c->dh == 64 ? run_layer_bwd<bf16, 64>(c, w, (const bf16*)x, (const bf16*)dy, (bf16*)dx, cos, sin, L, sched,
+                                               n_cells, (const bf16*)K_cache, (const bf16*)V_cache, cache_T,
+                                               (const bf16*)ocat, g, ws, s)
+                     : run_layer_bwd<bf16, 128>(c, w, (const bf16*)x, (const bf16*)dy, (bf16*)dx, cos, sin, L, sched,
+                                                n_cells, (const bf16*)K_cache, (const bf16*)V_cache, cache_T,
+                                                (const bf16*)ocat, g, ws, s);
+  } else {
+    const BwdWs<float> ws = carve_bwd<float>(c, L->T, cache_T, kmax, workspace);
+    rc = c->dh == 64 ? run_layer_bwd<float, 64>(c, w, (const float*)x, (const float*)dy, (float*)dx, cos, sin, L,
+                                                sched, n_cells, (const float*)K_cache, (const float*)V_cache, cache_T,
+                                                (const float*)ocat, g, ws, s)
+                     : run_layer_bwd<float, 128>(c, w, (const float*)x, (const float*)dy, (float*)dx, cos, sin, L,
+                                                 sched, n_cells, (const float*)K_cache, (const float*)V_cache,
+                                                 cache_T, (const float*)ocat, g, ws, s);
+  }
+  if (rc) return rc;
+  DM_HIP(hipGetLastError());
+  return DM_OK;
+}
+
+}  // extern "C"

@@ -18,6 +18,7 @@ typedef float floatx2 __attribute__((ext_vector_type(2)));
 namespace dm {
 
 constexpr int WAVE = 64;
+constexpr int CMAX = 64;   // max chunk length of one cell (rows of one attention block)
 
 DM_DEV float to_f(float x) { return x; }
 DM_DEV float to_f(bf16 x) { return (float)x; }

@@ -36,8 +36,9 @@ inline CellWs carve_cell(const dm_config* c, int cache_T, void* base) {
   return w;
 }
 
-// Every sweep's state of one cell, kept for the backward (strides are per sweep,
-// sized for N = B*CMAX rows and B*h*CMAX attention rows).
+// Every sweep's state of one cell, kept for the backward. Per-sweep arrays are
+// stacked with the cell's own row count N = B*c (so the K sweeps of a [N, x]
+// array form one [K*N, x] matrix); attention rows use B*h*CMAX slots.
 template <typename T> struct CellSave {
   T* o;              // [K][N, d]      o of sweep s (storage dtype, as stored by the attention)
   float* ssq;        // [K][N, h]      per-head sums of squares of o
@@ -127,7 +128,7 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
   CellGeom g{c->B, cc, c->d, c->h, DH, pos0, buf_t0, Tbuf, cache_T};
   const int BH = c->B * c->h;
   const int N = c->B * cc;
-  const size_t Nmax = (size_t)c->B * CMAX, d = c->d;
+  const size_t NS = (size_t)N, d = c->d;   // per-sweep row stride of the saved arrays
   const float scale = 1.0f / sqrtf((float)DH);
   const T* qr = (const T*)L->qr;
   const T* kself = (const T*)L->kself;
@@ -149,8 +150,8 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
     if (sv) { Kout = sv->Kin + (sw + 1) * slot; Vout = sv->Vin + (sw + 1) * slot; out_stride = ws_stride; out_row0 = 0; }
     else { Kout = Kc; Vout = Vc; out_stride = cache_stride; out_row0 = pos0; }
 
-    T* o = sv ? sv->o + sw * Nmax * d : (T*)ws.o;
-    float* ssq = sv ? sv->ssq + sw * Nmax * c->h : ws.ssq;
+    T* o = sv ? sv->o + sw * NS * d : (T*)ws.o;
+    float* ssq = sv ? sv->ssq + sw * NS * c->h : ws.ssq;
     AttendArgs<T> aa{g, qr, kself, vraw, Kin, Vin, in_stride, in_row0,
                      sw == 0 ? nsplit : (nsplit > 0 ? 1 : 0), ws.Ap, ws.Zp, ws.Mp, ws.A, ws.Z, ws.M,
                      scale, o, ssq, last ? ocat : nullptr, last ? o_last : nullptr,
@@ -160,10 +161,10 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
       ProfScope ps(PROF_ATTEND, s);
       hipLaunchKernelGGL((k_attend<T, DH>), dim3(BH), dim3(256), 0, s, aa);
     }
-    T* vin = sv ? sv->vin + sw * Nmax * d : (T*)ws.vin;
+    T* vin = sv ? sv->vin + sw * NS * d : (T*)ws.vin;
     run_refine<T, DH>(c, w, g, N, o, ssq, kraw, vraw, L->glogx, L->sig, cos, sin, Kout, Vout, out_stride,
-                      out_row0, vin, ws.gvu, sv ? sv->save1 + sw * Nmax * 4 * d : nullptr,
-                      sv ? sv->save2 + sw * Nmax * d : nullptr, sv ? sv->u + sw * Nmax * d : nullptr, s);
+                      out_row0, vin, ws.gvu, sv ? sv->save1 + sw * NS * 4 * d : nullptr,
+                      sv ? sv->save2 + sw * NS * d : nullptr, sv ? sv->u + sw * NS * d : nullptr, s);
   }
 }
 

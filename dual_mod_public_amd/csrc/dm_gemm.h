@@ -93,8 +93,9 @@ template <typename T> struct SrcKMajor {
   const T* __restrict__ p;   // element (r, k) at p[k*ld + r]
   long ld;
   int rows;
+  int kmax = 0x7fffffff;     // k >= kmax reads as zero (K not a multiple of the k-tile)
   DM_DEV uint4 load(int r, int k) const {   // VEC consecutive rows r.. at column k
-    return r < rows ? *reinterpret_cast<const uint4*>(p + (long)k * ld + r) : zero_u4();
+    return (r < rows && k < kmax) ? *reinterpret_cast<const uint4*>(p + (long)k * ld + r) : zero_u4();
   }
   DM_DEV uint4 xform(uint4 v, int, int, const float*, int) const { return v; }
 };
@@ -215,7 +216,7 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
     }
   };
 
-  const int nk = K / BK;
+  const int nk = (K + BK - 1) / BK;   // a partial last tile needs k-bounded sources
 #pragma unroll
   for (int s = 0; s < D; ++s)
     if (s < nk) gload(s, ra[s], rb[s]);

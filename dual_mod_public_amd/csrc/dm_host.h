@@ -46,7 +46,6 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 inline int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-constexpr int CMAX = 64;              // max chunk length of one cell
 constexpr int COMM_SPLIT_MIN = 256;   // committed keys per split (lower bound)
 constexpr int COMM_MAX_SPLITS = 16;
 constexpr int DEC_SPLIT = 512;        // tape keys per decode split

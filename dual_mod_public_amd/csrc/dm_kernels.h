@@ -26,7 +26,7 @@ struct PackArgs {
   void* dst;       // rows of ncols elements
 };
 
-__global__ __launch_bounds__(256) void k_pack(PackArgs a) {
+static __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
   int row = blockIdx.x;   // row index within this launch's segments (concatenated)
   int s = 0, acc = 0;
   while (s < a.nseg && row >= acc + a.seg[s].nrows) { acc += a.seg[s].nrows; ++s; }
@@ -47,7 +47,7 @@ __global__ void k_to_f32(const T* __restrict__ src, float* __restrict__ dst, int
 
 // out [cols, rows] = in [rows, cols]^T, 64x64 tiles through LDS
 template <typename T>
-__global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ in, T* __restrict__ out, int rows,
+static __global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ in, T* __restrict__ out, int rows,
                                                    int cols) {
   __shared__ T tile[64][65];
   const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
@@ -66,7 +66,7 @@ __global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ in, T* 
 // row RMSNorm (attn_norm, models/dualmod/attention.py:74-83): one wave per row
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(256) void k_rmsnorm_rows(const T* __restrict__ x, const T* __restrict__ w,
+static __global__ __launch_bounds__(256) void k_rmsnorm_rows(const T* __restrict__ x, const T* __restrict__ w,
                                                       T* __restrict__ y, int M, int d, float eps) {
   const int lane = threadIdx.x & 63;
   const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -193,7 +193,7 @@ struct KeyStrictLower {
 };
 
 template <typename T, int DH>
-__global__ __launch_bounds__(256) void k_comm_partial(CommArgs<T> a) {
+static __global__ __launch_bounds__(256) void k_comm_partial(CommArgs<T> a) {
   using C = AttnCfg<T, DH>;
   __shared__ __attribute__((aligned(16))) T lds[C::LDS_ELEMS];
   T* Ks = lds;
@@ -268,7 +268,7 @@ template <typename T> struct AttendArgs {
 };
 
 template <typename T, int DH>
-__global__ __launch_bounds__(256) void k_attend(AttendArgs<T> a) {
+static __global__ __launch_bounds__(256) void k_attend(AttendArgs<T> a) {
   using C = AttnCfg<T, DH>;
   __shared__ __attribute__((aligned(16))) T lds[C::LDS_ELEMS];
   T* Ks = lds;

@@ -211,7 +211,8 @@ int dm_layer_fwd(const dm_config* c, const dm_packed* w, const void* x, void* y,
                    nullptr, workspace, workspace_bytes};
     if ((rc = dm_cell_fwd(c, w, L, cos, sin, &a, stream))) return rc;
   }
-  return dm_linear(c->dtype, ocat, w->wo, x, y, c->B * L->T, c->d, c->d, stream);
+  return dm_linear(c->dtype, ocat, w->wo, (c->flags & DM_FLAG_NO_RESIDUAL) ? nullptr : x, y, c->B * L->T,
+                   c->d, c->d, stream);
 }
 
 }  // extern "C"

@@ -161,6 +161,42 @@ def _f32(t, device):
     return t.to(device=device, dtype=torch.float32).contiguous()
 
 
+def _sched(schedule):
+    return (ctypes.c_int32 * (3 * len(schedule)))(*[v for cell in schedule for v in cell])
+
+
+class LayerGrads:
+    """fp32 gradient buffers of one layer in the reference parameter layout (dm_grads).
+    The backward ADDS into them (like .grad accumulation); ``zero_()`` clears."""
+
+    def __init__(self, cfg, device):
+        d = cfg.d_model
+        mult = cfg.ctx_mod != "linear"
+        shapes = {"wq.weight": (d, d), "wk.weight": (d, d), "wv.weight": (d, d), "wo.weight": (d, d),
+                  "w_kctx.weight": (d, d), "w_vctx.weight": (d, d), "w_gk.weight": (d, 2 * d),
+                  "w_gv.weight": (d, 2 * d), "w_gk.bias": (d,), "w_gv.bias": (d,),
+                  "norm_ctx.weight": (d,), "attn_norm.weight": (d,)}
+        if mult:
+            shapes.update({"v_gate.weight": (d, d), "v_gate.bias": (d,), "v_map.weight": (d, d)})
+        self.t = {k: torch.zeros(v, device=device, dtype=torch.float32) for k, v in shapes.items()}
+
+    def zero_(self):
+        for v in self.t.values():
+            v.zero_()
+        return self
+
+    def struct(self, with_attn_norm=True):
+        g = L.dm_grads()
+        for f, name in L.GRAD_FIELDS:
+            if name == "attn_norm.weight" and not with_attn_norm:
+                continue
+            setattr(g, f, L.ptr(self.t.get(name)))
+        return g
+
+    def __getitem__(self, name):
+        return self.t[name]
+
+
 class HipSweepCell:
     """FusedSweepCell analogue for one DM layer on one GPU (fused_sweep.py:1218).
 
@@ -213,19 +249,58 @@ class HipSweepCell:
         L.check(L.lib().dm_cell_fwd(ctypes.byref(self.conf), ctypes.byref(ws), ctypes.byref(b),
                                     L.ptr(cos), L.ptr(sin), ctypes.byref(a), L.stream_ptr()))
 
-    def layer_forward(self, x, y, cos, sin, schedule, K_cache, V_cache, ocat, bufs):
+    def _conf(self, residual):
+        c = L.make_config(self.cfg, self.B, self.dtype)
+        c.flags = 0 if residual else L.DM_FLAG_NO_RESIDUAL
+        return c
+
+    def layer_forward(self, x, y, cos, sin, schedule, K_cache, V_cache, ocat, bufs, normalize=True,
+                      residual=True):
         """Attention sublayer y = x + W_O DM(attn_norm(x)) over ``schedule``
-        (model.py:123-124 with forward.py:95-113's chunk loop), one C call."""
-        sched = (ctypes.c_int32 * (3 * len(schedule)))(*[v for cell in schedule for v in cell])
+        (model.py:123-124 with forward.py:95-113's chunk loop), one C call.
+        normalize=False takes x as xhat (no attn_norm); residual=False drops the +x
+        (DualModAttention.forward, attention.py:438-447)."""
+        sched = _sched(schedule)
         cos, sin = _f32(cos, self.device), _f32(sin, self.device)
-        ws = self.w.struct(with_attn_norm=True)
+        ws = self.w.struct(with_attn_norm=normalize)
         b = bufs.struct()
+        conf = self._conf(residual)
         L.check(L.lib().dm_layer_fwd(
-            ctypes.byref(self.conf), ctypes.byref(ws), L.ptr(x), L.ptr(y), L.ptr(cos), L.ptr(sin),
+            ctypes.byref(conf), ctypes.byref(ws), L.ptr(x), L.ptr(y), L.ptr(cos), L.ptr(sin),
             ctypes.byref(b), sched, len(schedule), L.ptr(K_cache), L.ptr(V_cache),
             K_cache.shape[2], L.ptr(ocat), L.ptr(self.workspace), self.workspace.numel(),
             L.stream_ptr()))
         return y
+
+    def _bwd_workspace(self, T, cache_T, kmax):
+        key = (T, cache_T, kmax)
+        if getattr(self, "_bwd_key", None) != key:
+            n = L.lib().dm_layer_bwd_workspace_bytes(ctypes.byref(self.conf), T, cache_T, kmax)
+            if n == 0:
+                raise L.DMError("dm_layer_bwd_workspace_bytes rejected the configuration")
+            self._bwd_ws = torch.empty(n, device=self.device, dtype=torch.uint8)
+            self._bwd_key = key
+        return self._bwd_ws
+
+    def layer_backward(self, x, dy, dx, cos, sin, schedule, K_cache, V_cache, ocat, bufs, grads,
+                       normalize=True, residual=True):
+        """Reverse-scan backward of ``layer_forward`` with exact recompute
+        (engines/wavescan/engine/backward.py:92-123, fused_sweep.py:1557-1959):
+        writes dx and ADDS the parameter grads into ``grads`` (LayerGrads)."""
+        sched = _sched(schedule)
+        cos, sin = _f32(cos, self.device), _f32(sin, self.device)
+        ws = self.w.struct(with_attn_norm=normalize)
+        b = bufs.struct()
+        conf = self._conf(residual)
+        kmax = max(k for _, _, k in schedule)
+        work = self._bwd_workspace(bufs.T, K_cache.shape[2], kmax)
+        g = grads.struct(with_attn_norm=normalize)
+        L.check(L.lib().dm_layer_bwd(
+            ctypes.byref(conf), ctypes.byref(ws), L.ptr(x), L.ptr(dy), L.ptr(dx), L.ptr(cos),
+            L.ptr(sin), ctypes.byref(b), sched, len(schedule), L.ptr(K_cache), L.ptr(V_cache),
+            K_cache.shape[2], L.ptr(ocat), ctypes.byref(g), L.ptr(work), work.numel(),
+            L.stream_ptr()))
+        return dx
 
 
 def chunk_cell_forward(attn, xhat_c, cos_c, sin_c, K_comm, V_comm, n_sweeps, intra_mask=None):

@@ -58,8 +58,14 @@ typedef struct dm_config {
   float mult_res_lambda;    /* config.py:126 */
   float rms_eps;            /* RMSNorm eps of attn_norm / norm_ctx: 1e-5 */
   int32_t local_window;     /* decode only: W tokens incl. self, 0 = full */
-  int32_t reserved[7];
+  int32_t flags;            /* DM_FLAG_* */
+  int32_t reserved[6];
 } dm_config;
+
+/* dm_layer_fwd / dm_layer_bwd: without this flag y = x + W_O . DM(norm(x)) (the Block
+ * attention sublayer, models/dualmod/model.py:123-124); with it y = W_O . DM(norm(x))
+ * (DualModAttention.forward, attention.py:438-447). */
+#define DM_FLAG_NO_RESIDUAL 1
 
 /* The reference parameters of one DualModAttention layer (attention.py:100-202),
  * each as stored by torch (nn.Linear weight = [out, in]). Storage dtype unless noted. */
@@ -147,6 +153,32 @@ int dm_layer_fwd(const dm_config* cfg, const dm_packed* w, const void* x, void* 
                  const float* cos, const float* sin, const dm_layer_bufs* bufs,
                  const int32_t* sched, int32_t n_cells, void* K_cache, void* V_cache,
                  int32_t cache_T, void* ocat, void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+/* ---- whole layer backward ---------------------------------------------------------
+ * Reverse-scan backward with exact recompute of the layer forward above
+ * (engines/wavescan/engine/backward.py:92-123, FusedSweepCell.cell_backward
+ * fused_sweep.py:1557-1850, layer_close :1873-1959): cells in reverse order; each
+ * cell recomputes its n_sweeps sweeps from the forward's projections (bufs) and
+ * final cache rows, then runs the sweeps backward; grads of the committed rows
+ * it read accumulate in an fp32 grad cache consumed by the earlier cells.
+ * Inputs are exactly what dm_layer_fwd produced / consumed (x, bufs, caches, ocat)
+ * plus dy [B, T, d]. Writes dx [B, T, d] (storage dtype) and ADDS the parameter
+ * gradients into g (fp32, reference layout). Needs the *_t fields of w. */
+typedef struct dm_grads {
+  float* wq; float* wk; float* wv; float* wo;        /* [d, d] */
+  float* w_kctx; float* w_vctx;                      /* [d, d] */
+  float* w_gk; float* w_gv;                          /* [d, 2d] */
+  float* b_gk; float* b_gv;                          /* [d] */
+  float* v_gate; float* b_vgate; float* v_map;       /* [d, d], [d], [d, d] (mult family) */
+  float* norm_ctx_w;                                 /* [d] */
+  float* attn_norm_w;                                /* [d] (when w->attn_norm_w != NULL) */
+} dm_grads;
+size_t dm_layer_bwd_workspace_bytes(const dm_config* cfg, int32_t T, int32_t cache_T, int32_t max_sweeps);
+int dm_layer_bwd(const dm_config* cfg, const dm_packed* w, const void* x, const void* dy, void* dx,
+                 const float* cos, const float* sin, const dm_layer_bufs* bufs, const int32_t* sched,
+                 int32_t n_cells, const void* K_cache, const void* V_cache, int32_t cache_T,
+                 const void* ocat, const dm_grads* g, void* workspace, size_t workspace_bytes,
                  void* stream);
 
 /* ---- decode ------------------------------------------------------------------

@@ -1,0 +1,187 @@
+"""GPU parity of the HIP reverse-scan backward (dm_layer_bwd) against autograd
+through the CPU oracle.
+
+The oracle's layer forward is written functionally (cat-grown caches), so torch
+autograd through it is the reference's own gradient oracle for K < c
+(engines/wavescan/tests/test_k1_k9.py:240-281) and, at K = c, autograd through the
+sequential scan (the oracle's scan grads are pinned to the reference's golden
+gradients in tests/test_oracle_golden.py). Tolerances: fp32 grads within 1e-4
+relative (the reference's T-K6 bar, test_k1_k9.py:212-237) — in practice ~1e-6;
+bf16 within 5e-2 relative of the fp32 oracle.
+"""
+
+import pytest
+import torch
+
+import oracle as O
+from dual_mod_public_amd import _lib as L
+from dual_mod_public_amd.autograd import dm_layer
+from dual_mod_public_amd.engine import HipSweepCell, LayerGrads, uniform_chunks
+from tests.hip_helpers import DEV, cfg_of, relerr, say, setup
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-4
+BF16_TOL = 5e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    L.load()
+
+
+def oracle_grads(cfg, sd, x, dy, cos, sin, sched, dtype=torch.float64, normalize=True, residual=True):
+    """dx and parameter grads of y = [x +] W_O DM([attn_norm](x)) by autograd through the oracle."""
+    sdg = {k: v.to(dtype).clone().requires_grad_(True) for k, v in sd.items()}
+    xg = x.to(dtype).clone().requires_grad_(True)
+    with torch.enable_grad():
+        if normalize:
+            xh = O.rms_norm(xg, sdg["attn_norm.weight"], 1e-5)
+        else:
+            xh = xg
+        o = O.layer_forward(cfg, sdg, xh, cos.to(dtype), sin.to(dtype), sched)[0]
+        y = O.dm_oracle._lin(o, sdg, "wo")
+        if residual:
+            y = y + xg
+        (y * dy.to(dtype)).sum().backward()
+    g = {k: v.grad for k, v in sdg.items() if v.grad is not None}
+    return xg.grad, g
+
+
+def hip_grads(cfg, sd, x, dy, cos, sin, sched, dtype, normalize=True, residual=True):
+    B, T, d = x.shape
+    cell = HipSweepCell(cfg, B, T, device=DEV, dtype=dtype)
+    cell.pack({k: v.to(DEV, dtype) for k, v in sd.items()})
+    bufs = cell.new_bufs(T)
+    xd = x.to(DEV, dtype).contiguous()
+    y = torch.empty_like(xd)
+    K = torch.empty(B, cfg.n_heads, T, cfg.head_dim, device=DEV, dtype=dtype)
+    V = torch.empty_like(K)
+    ocat = torch.empty_like(xd)
+    cell.layer_forward(xd, y, cos, sin, sched, K, V, ocat, bufs, normalize=normalize, residual=residual)
+    grads = LayerGrads(cfg, DEV)
+    dx = torch.empty_like(xd)
+    cell.layer_backward(xd, dy.to(DEV, dtype).contiguous(), dx, cos, sin, sched, K, V, ocat, bufs, grads,
+                        normalize=normalize, residual=residual)
+    torch.cuda.synchronize()
+    return y, dx, grads
+
+
+def compare(name, dx, g, dx_ref, g_ref, tol, skip=()):
+    errs = {"x": relerr(dx, dx_ref)}
+    for k, v in g_ref.items():
+        if k in skip:
+            continue
+        errs[k] = relerr(g[k], v)
+    worst = max(errs, key=errs.get)
+    say(f"  {name}: worst {worst} {errs[worst]:.2e}; " +
+        " ".join(f"{k.split('.')[0]}={v:.1e}" for k, v in errs.items()))
+    for k, v in errs.items():
+        assert v < tol, f"{k}: relerr {v:.3e} >= {tol}"
+
+
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "mult"])
+@pytest.mark.parametrize("c,k", [(16, 16), (16, 4), (64, 4), (8, 3)])
+def test_layer_grads_fp32(ctx_mod, c, k):
+    """dm_layer_bwd vs autograd through the oracle (fp64), config-1 shape, fp32 storage."""
+    say(f"bwd fp32 ctx_mod={ctx_mod} c={c} K={k}")
+    cfg = cfg_of(ctx_mod=ctx_mod)
+    B, T = 2, 64
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(99), dtype=torch.float64)
+    sched = uniform_chunks(T, c, k)
+    _, dx, g = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.float32)
+    dx_ref, g_ref = oracle_grads(cfg, sd, x, dy, c64, s64, sched)
+    compare("fp32", dx, g, dx_ref, g_ref, FP32_TOL)
+
+
+def test_layer_grads_no_norm_no_residual_fp32():
+    """DualModAttention.forward's form: y = W_O DM(xhat)."""
+    say("bwd fp32 no attn_norm, no residual")
+    cfg = cfg_of()
+    B, T = 2, 48
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(7), dtype=torch.float64)
+    sched = uniform_chunks(T, 16, 5)
+    _, dx, g = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.float32, normalize=False, residual=False)
+    dx_ref, g_ref = oracle_grads(cfg, sd, x, dy, c64, s64, sched, normalize=False, residual=False)
+    compare("fp32 plain", dx, g, dx_ref, g_ref, FP32_TOL, skip=("attn_norm.weight",))
+
+
+def test_grads_accumulate():
+    """Two backward calls into the same LayerGrads add up (``.grad`` semantics)."""
+    say("bwd accumulation")
+    cfg = cfg_of()
+    B, T = 2, 32
+    sd, x, _, (c32, s32) = setup(cfg, B, T)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(3), dtype=torch.float64)
+    sched = uniform_chunks(T, 16, 4)
+    cell = HipSweepCell(cfg, B, T, device=DEV, dtype=torch.float32)
+    cell.pack({k: v.to(DEV, torch.float32) for k, v in sd.items()})
+    bufs = cell.new_bufs(T)
+    xd = x.float().to(DEV)
+    y = torch.empty_like(xd)
+    K = torch.empty(B, cfg.n_heads, T, cfg.head_dim, device=DEV)
+    V = torch.empty_like(K)
+    ocat = torch.empty_like(xd)
+    cell.layer_forward(xd, y, c32, s32, sched, K, V, ocat, bufs)
+    g1, g2 = LayerGrads(cfg, DEV), LayerGrads(cfg, DEV)
+    dx = torch.empty_like(xd)
+    dyd = dy.float().to(DEV)
+    cell.layer_backward(xd, dyd, dx, c32, s32, sched, K, V, ocat, bufs, g1)
+    cell.layer_backward(xd, dyd, dx, c32, s32, sched, K, V, ocat, bufs, g2)
+    cell.layer_backward(xd, dyd, dx, c32, s32, sched, K, V, ocat, bufs, g2)
+    torch.cuda.synchronize()
+    for name, t in g1.t.items():
+        assert relerr(g2[name], 2 * t) < 1e-6, name
+
+
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear"])
+def test_layer_grads_340m_shape_fp32(ctx_mod):
+    """340M layer shape (d=1024, 16x64), c=64, K=4, T=256, fp32 storage (
+    fp32 leg) vs autograd through the oracle in fp64."""
+    say(f"bwd fp32 d=1024 T=256 c=64 K=4 ctx_mod={ctx_mod}")
+    cfg = cfg_of(d=1024, h=16, T=256, ctx_mod=ctx_mod)
+    B, T = 2, 256
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(11), dtype=torch.float64)
+    sched = uniform_chunks(T, 64, 4)
+    _, dx, g = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.float32)
+    dx_ref, g_ref = oracle_grads(cfg, sd, x, dy, c64, s64, sched)
+    compare("fp32 340m", dx, g, dx_ref, g_ref, FP32_TOL)
+
+
+def test_layer_grads_340m_shape_bf16():
+    """bf16 storage / fp32 accumulate at the 340M layer shape, T=256, vs the fp32 oracle."""
+    say("bwd bf16 d=1024 T=256 c=64 K=4")
+    cfg = cfg_of(d=1024, h=16, T=256)
+    B, T = 2, 256
+    sd, x, _, (c32, s32) = setup(cfg, B, T)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(11), dtype=torch.float64)
+    sched = uniform_chunks(T, 64, 4)
+    _, dx, g = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.bfloat16)
+    dx_ref, g_ref = oracle_grads(cfg, {k: v.float() for k, v in sd.items()}, x.float(), dy.float(),
+                                 c32, s32, sched, dtype=torch.float32)
+    compare("bf16 340m", dx, g, dx_ref, g_ref, BF16_TOL)
+
+
+def test_module_autograd_matches_oracle():
+    """DualModAttention (reference signature) forward + loss.backward() through the HIP path."""
+    from dual_mod_public_amd.attention import DualModAttention
+    say("DualModAttention autograd fp32")
+    cfg = cfg_of(T=64)
+    B, T = 2, 64
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    attn = DualModAttention(cfg).to(DEV)
+    attn.load_state_dict({k: v.float() for k, v in sd.items() if k != "attn_norm.weight"})
+    xd = x.float().to(DEV).requires_grad_(True)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(5), dtype=torch.float64)
+    y = attn(xd, c32.to(DEV), s32.to(DEV), n_sweeps=4)
+    (y * dy.float().to(DEV)).sum().backward()
+    torch.cuda.synchronize()
+    sched = uniform_chunks(T, attn.CHUNK, 4)
+    dx_ref, g_ref = oracle_grads(cfg, sd, x, dy, c64, s64, sched, normalize=False, residual=False)
+    got = {n: p.grad for n, p in attn.named_parameters()}
+    compare("module", xd.grad, got, dx_ref, g_ref, FP32_TOL, skip=("attn_norm.weight",))
