@@ -62,7 +62,9 @@ DM_DEV void load_q_frags(const T* qrow_ptr, bool valid, typename Mfma<T>::frag* 
 }
 
 // One key tile held in registers (global -> registers -> LDS, so the next tile's
-// loads can be in flight while the current tile is used).
+// loads can be in flight while the current tile is used). Consecutive lanes take
+// consecutive keys of one 16-byte column chunk, so the transposed V stores of a
+// wave land in one LDS row (no bank conflicts).
 template <typename T, int DH> struct KVRegs {
   static constexpr int VPR = DH / AttnCfg<T, DH>::VEC;             // 16-byte vectors per row
   static constexpr int NV = AttnCfg<T, DH>::KT * VPR / 256;        // vectors per thread
@@ -78,13 +80,11 @@ DM_DEV void load_kv(const T* __restrict__ Kg, const T* __restrict__ Vg, long row
 #pragma unroll
   for (int i = 0; i < R::NV; ++i) {
     const int v = threadIdx.x + 256 * i;
-    const int k = v / R::VPR, c0 = (v % R::VPR) * AttnCfg<T, DH>::VEC;
-    r.k[i] = uint4{0u, 0u, 0u, 0u};
-    r.v[i] = uint4{0u, 0u, 0u, 0u};
-    if (k < nvalid) {
-      r.k[i] = *reinterpret_cast<const uint4*>(Kg + (long)k * row_stride + c0);
-      r.v[i] = *reinterpret_cast<const uint4*>(Vg + (long)k * row_stride + c0);
-    }
+    const int k = v % AttnCfg<T, DH>::KT, c0 = (v / AttnCfg<T, DH>::KT) * AttnCfg<T, DH>::VEC;
+    const bool ok = k < nvalid;
+    const long off = (long)(ok ? k : 0) * row_stride + c0;
+    r.k[i] = keep_if(*reinterpret_cast<const uint4*>(Kg + off), ok);
+    r.v[i] = keep_if(*reinterpret_cast<const uint4*>(Vg + off), ok);
   }
 }
 
@@ -96,7 +96,7 @@ DM_DEV void store_kv(const KVRegs<T, DH>& r, T* Ks, T* Vt) {
 #pragma unroll
   for (int i = 0; i < R::NV; ++i) {
     const int v = threadIdx.x + 256 * i;
-    const int k = v / R::VPR, c0 = (v % R::VPR) * C::VEC;
+    const int k = v % C::KT, c0 = (v / C::KT) * C::VEC;
     *reinterpret_cast<uint4*>(Ks + k * C::LDK + c0) = r.k[i];
     const T* ve = reinterpret_cast<const T*>(&r.v[i]);
 #pragma unroll

@@ -328,16 +328,18 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
     const int ic = ok ? i : 0;
     const long n = (long)b * c + ic;                      // row of the sweep arrays
     float q[EPT], kv[EPT], vv[EPT], ks[EPT], vr[EPT], ov[EPT], gwv[EPT], dc[EPT];
+    load_vec<T, EPT>(a.qr + (lrow0 + ic) * DH + e0, q);
+    load_vec<T, EPT>(a.Kin + (long)bh * a.in_stride + (long)(a.in_row0 + ic) * DH + e0, kv);
+    load_vec<T, EPT>(a.Vin + (long)bh * a.in_stride + (long)(a.in_row0 + ic) * DH + e0, vv);
+    load_vec<T, EPT>(a.kself + (lrow0 + ic) * DH + e0, ks);
+    load_vec<T, EPT>(a.vraw + (lrow0 + ic) * DH + e0, vr);
+    load_vec<T, EPT>(a.o + n * d + hh * DH + e0, ov);
+    load_vec<float, EPT>(a.gw + n * d + hh * DH + e0, gwv);
+    if (a.docat != nullptr) {
+      load_vec<float, EPT>(a.docat + ((long)b * g.Tbuf + g.buf_t0 + ic) * d + hh * DH + e0, dc);
+    } else {
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      q[e] = to_f(a.qr[(lrow0 + ic) * DH + e0 + e]);
-      kv[e] = to_f(a.Kin[(long)bh * a.in_stride + (long)(a.in_row0 + ic) * DH + e0 + e]);
-      vv[e] = to_f(a.Vin[(long)bh * a.in_stride + (long)(a.in_row0 + ic) * DH + e0 + e]);
-      ks[e] = to_f(a.kself[(lrow0 + ic) * DH + e0 + e]);
-      vr[e] = to_f(a.vraw[(lrow0 + ic) * DH + e0 + e]);
-      ov[e] = to_f(a.o[n * d + hh * DH + e0 + e]);
-      gwv[e] = a.gw[n * d + hh * DH + e0 + e];
-      dc[e] = a.docat != nullptr ? a.docat[((long)b * g.Tbuf + g.buf_t0 + ic) * d + hh * DH + e0 + e] : 0.f;
+      for (int e = 0; e < EPT; ++e) dc[e] = 0.f;
     }
     float ss = 0.f, dot = 0.f;
     for (int p = part; p < g.h; p += 4) ss += a.ssq[n * g.h + p];
@@ -374,22 +376,32 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
     }
     if (ok) {
       const long lr = (lrow0 + i) * DH + e0;
+      float a0[EPT], a1[EPT], a2[EPT];
+      load_vec<float, EPT>(a.dkself + lr, a0);
+      load_vec<float, EPT>(a.dvraw + lr, a1);
+      load_vec<float, EPT>(a.dq + lr, a2);
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
-        a.dkself[lr + e] += a.scale * dss * q[e];
-        a.dvraw[lr + e] += ps * dO[e];
-        a.dq[lr + e] += a.scale * dss * ks[e];
+        a0[e] += a.scale * dss * q[e];
+        a1[e] += ps * dO[e];
+        a2[e] += a.scale * dss * ks[e];
       }
+      store_vec<float, EPT>(a.dkself + lr, a0);
+      store_vec<float, EPT>(a.dvraw + lr, a1);
+      store_vec<float, EPT>(a.dq + lr, a2);
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) { q[e] = 0.f; kv[e] = 0.f; vv[e] = 0.f; }
     }
+    store_vec<T, EPT>(Qs + i * LDE + e0, q);
+    store_vec<T, EPT>(Ks + i * LDE + e0, kv);
+    store_vec<T, EPT>(Vs + i * LDE + e0, vv);
+    store_vec<T, EPT>(dOs + i * LDE + e0, dO);
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       const int col = e0 + e;
-      Qs[i * LDE + col] = from_f<T>(ok ? q[e] : 0.f);
-      Ks[i * LDE + col] = from_f<T>(ok ? kv[e] : 0.f);
-      Vs[i * LDE + col] = from_f<T>(ok ? vv[e] : 0.f);
-      dOs[i * LDE + col] = from_f<T>(dO[e]);
-      Qt[col * LDI + i] = from_f<T>(ok ? q[e] : 0.f);
-      Kt[col * LDI + i] = from_f<T>(ok ? kv[e] : 0.f);
+      Qt[col * LDI + i] = from_f<T>(q[e]);
+      Kt[col * LDI + i] = from_f<T>(kv[e]);
       dOt[col * LDI + i] = from_f<T>(dO[e]);
     }
   }
@@ -522,46 +534,70 @@ static __global__ __launch_bounds__(256) void k_comm_bwd(CommBwdArgs<T> a) {
   const T* Kb = a.Kc + (long)bh * g.cache_T * DH;
   const T* Vb = a.Vc + (long)bh * g.cache_T * DH;
 
+  constexpr int EPT = DH / 4;            // elements per thread in the row-wise staging
+  const int ri = tid >> 2, re0 = (tid & 3) * EPT;
   // queries and committed grads of the block's 64 rows
   {
-    constexpr int EPT = DH / 4;
-    const int i = tid >> 2, e0 = (tid & 3) * EPT;
-    const bool ok = i < c;
+    const bool ok = ri < c;
+    float q[EPT], gg[EPT];
+    load_vec<T, EPT>(a.qr + (lrow0 + (ok ? ri : 0)) * DH + re0, q);
+    load_vec<float, EPT>(a.G + ((long)bh * CMAX + (ok ? ri : 0)) * DH + re0, gg);
+    if (!ok) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) { q[e] = 0.f; gg[e] = 0.f; }
+    }
+    store_vec<T, EPT>(Qs + ri * LDE + re0, q);
+    store_vec<T, EPT>(Gs + ri * LDE + re0, gg);
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-      const float q = ok ? to_f(a.qr[(lrow0 + i) * DH + e0 + e]) : 0.f;
-      const float gg = ok ? a.G[((long)bh * CMAX + i) * DH + e0 + e] : 0.f;
-      Qs[i * LDE + e0 + e] = from_f<T>(q);
-      Qt[(e0 + e) * LDI + i] = from_f<T>(q);
-      Gs[i * LDE + e0 + e] = from_f<T>(gg);
-      Gt[(e0 + e) * LDI + i] = from_f<T>(gg);
+      Qt[(re0 + e) * LDI + ri] = from_f<T>(q[e]);
+      Gt[(re0 + e) * LDI + ri] = from_f<T>(gg[e]);
     }
     if ((tid & 3) == 0) {
-      sM[i] = ok ? a.Mx[(long)bh * c + i] : 0.f;
-      sD[i] = ok ? a.Dbar[(long)bh * CMAX + i] : 0.f;
+      sM[ri] = ok ? a.Mx[(long)bh * c + ri] : 0.f;
+      sD[ri] = ok ? a.Dbar[(long)bh * CMAX + ri] : 0.f;
     }
   }
   floatx4 dQ[NDT];
 #pragma unroll
   for (int t = 0; t < NDT; ++t) dQ[t] = zero4();
 
+  // key tiles: K / V of the next tile are loaded into registers while the current
+  // tile is used; the grad-cache rows a tile adds into are read at its start
+  float kreg[EPT], vreg[EPT];
+  auto load_tile = [&](int k0) {
+    const int j = min(ri, k_end - k0 - 1);
+    load_vec<T, EPT>(Kb + (long)(k0 + j) * DH + re0, kreg);
+    load_vec<T, EPT>(Vb + (long)(k0 + j) * DH + re0, vreg);
+  };
+  if (k_begin < k_end) load_tile(k_begin);
   for (int k0 = k_begin; k0 < k_end; k0 += 64) {
     const int nv = min(64, k_end - k0);
-    __syncthreads();
-    {
-      constexpr int EPT = DH / 4;
-      const int j = tid >> 2, e0 = (tid & 3) * EPT;
-      const bool ok = j < nv;
+    // old grad-cache values of this tile's rows, in the C layout of dK / dV
+    float oldK[4][NDT], oldV[4][NDT];
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        const float kk = ok ? to_f(Kb[(long)(k0 + j) * DH + e0 + e]) : 0.f;
-        const float vv = ok ? to_f(Vb[(long)(k0 + j) * DH + e0 + e]) : 0.f;
-        Ks[j * LDE + e0 + e] = from_f<T>(kk);
-        Kt[(e0 + e) * LDI + j] = from_f<T>(kk);
-        Vs[j * LDE + e0 + e] = from_f<T>(vv);
+    for (int r = 0; r < 4; ++r) {
+      const int j = min(16 * wave + 4 * g4 + r, nv - 1);
+      const long row = ((long)bh * g.cache_T + k0 + j) * DH;
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        oldK[r][t] = a.dKgc[row + 16 * t + lc];
+        oldV[r][t] = a.dVgc[row + 16 * t + lc];
       }
     }
     __syncthreads();
+    {
+      const bool ok = ri < nv;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        if (!ok) { kreg[e] = 0.f; vreg[e] = 0.f; }
+        Kt[(re0 + e) * LDI + ri] = from_f<T>(kreg[e]);
+      }
+      store_vec<T, EPT>(Ks + ri * LDE + re0, kreg);
+      store_vec<T, EPT>(Vs + ri * LDE + re0, vreg);
+    }
+    __syncthreads();
+    if (k0 + 64 < k_end) load_tile(k0 + 64);
     // query-major: dS = E (G V^T - Dbar), dQ += dS K
     {
       floatx4 S[4], dP[4];
@@ -622,8 +658,8 @@ static __global__ __launch_bounds__(256) void k_comm_bwd(CommBwdArgs<T> a) {
         const long row = ((long)bh * g.cache_T + k0 + j) * DH;
 #pragma unroll
         for (int t = 0; t < NDT; ++t) {
-          a.dKgc[row + 16 * t + lc] += a.scale * dK[t][r];
-          a.dVgc[row + 16 * t + lc] += dV[t][r];
+          a.dKgc[row + 16 * t + lc] = oldK[r][t] + a.scale * dK[t][r];
+          a.dVgc[row + 16 * t + lc] = oldV[r][t] + dV[t][r];
         }
       }
     }

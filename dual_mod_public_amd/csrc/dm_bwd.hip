@@ -27,14 +27,16 @@ template <typename T> struct BwdWs {
   float *G, *Dbar;                      // [B*h, CMAX, dh], [B*h, CMAX]
   float *dq_part;                       // [nsplit, B*h, CMAX, dh]
   // layer close
+  T *dctxT, *uT, *dvcT, *vinT;          // per-cell transposes [4d | d, K*N] for the weight-grad GEMMs
   T* dproj;                             // [B*T, nproj*d]
+  T *tA, *tB;                           // layer-level transposes [max(nproj*d, d), B*T] and [d, B*T]
   float* dxhat;                         // [B*T, d]
   float *dWp, *dWs;                     // packed weight-grad staging [nproj*d, d], [4d, d]
   float* colpart;                       // [NCHUNK, 3d]
   size_t bytes;
 };
 
-constexpr int NSLOT_TM = 32;      // rows per norm_ctx-weight partial slot (du GEMM wave tile)
+constexpr int NSLOT_TM = 16;      // rows per norm_ctx-weight partial slot (du GEMM wave tile)
 constexpr int DU_TN = 32;         // columns per row-dot partial (du GEMM wave tile)
 constexpr int NCHUNK = 64;        // row chunks of the column sums
 
@@ -78,9 +80,15 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.rowdot = cv.take<float>(N * (d / DU_TN) * 4);
   w.G = cv.take<float>(BH * CMAX * dh * 4);
   w.Dbar = cv.take<float>(BH * CMAX * 4);
-  w.dq_part = cv.take<float>(comm_splits_max(cache_T) * BH * CMAX * dh * 4);
+  w.dq_part = cv.take<float>(comm_splits_max_bwd(cache_T) * BH * CMAX * dh * 4);
+  w.dctxT = cv.take<T>((kmax * N + 64) * 4 * d * e);
+  w.uT = cv.take<T>((kmax * N + 64) * d * e);
+  w.dvcT = cv.take<T>((kmax * N + 64) * d * e);
+  w.vinT = cv.take<T>((kmax * N + 64) * d * e);
   // the attn_norm weight partials [B*T, d] fp32 reuse dproj once it is consumed
   w.dproj = cv.take<T>(std::max(BT * nproj * d * e, BT * d * 4));
+  w.tA = cv.take<T>((BT + 64) * nproj * d * e);
+  w.tB = cv.take<T>((BT + 64) * d * e);
   w.dxhat = cv.take<float>(BT * d * 4);
   w.dWp = cv.take<float>(nproj * d * d * 4);
   w.dWs = cv.take<float>(4 * d * d * 4);
@@ -113,14 +121,26 @@ inline void unpack(const std::vector<UnpackSeg>& segs, int ncols, const float* s
   }
 }
 
-// fp32 staging C [M, N] (+)= op(A) . op(B)^T with K-major (transposed) operands
+// out [cols, ld_out] (columns col0_out..) = in [rows, cols]^T
 template <typename T>
-void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N, int K, int accumulate,
-             hipStream_t s) {
+void transpose(const T* in, long ld_in, int rows, int cols, int rows_pad, T* out, long ld_out, long col0_out,
+               hipStream_t s) {
+  dim3 grid(cdiv(cols, 64), cdiv(rows_pad, 64));
+  hipLaunchKernelGGL(k_transpose16<T>, grid, dim3(256), 0, s, in, ld_in, rows, cols, rows_pad, out, ld_out,
+                     col0_out);
+}
+
+// C [M, N] (+)= A^T . B for row-major A [K, M], B [K, N] (the weight-grad products
+// sum over rows): both operands are transposed into scratch first so the GEMM runs
+// with K-contiguous operands (16-byte LDS stores).
+template <typename T>
+void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N, int K, int accumulate, T* At,
+             T* Bt, hipStream_t s) {
+  const int Kp = cdiv(K, 64) * 64;   // zero-padded to whole k-tiles
+  transpose<T>(A, lda, K, M, Kp, At, Kp, 0, s);
+  transpose<T>(Bm, ldb, K, N, Kp, Bt, Kp, 0, s);
   EpiStoreF32 ep{M, N, accumulate, C};
-  SrcKMajor<T> sa{A, lda, M, K};
-  SrcKMajor<T> sb{Bm, ldb, N, K};
-  launch_gemm<T, 128, 128, 2, 2, 4>(sa, sb, M, N, K, ep, s);
+  launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{At, Kp, M}, SrcRows<T>{Bt, Kp, N}, M, N, Kp, ep, s);
 }
 
 template <typename T, int DH>
@@ -152,7 +172,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   {
     EpiStoreF32 ep{BT, d, 0, ws.docat};
     launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{dy, d, BT}, SrcRows<T>{(const T*)w->wo_t, d, d}, BT, d, d, ep, s);
-    gemm_tn<T>(dy, d, ocat, d, gr->wo, d, d, BT, 1, s);
+    gemm_tn<T>(dy, d, ocat, d, gr->wo, d, d, BT, 1, ws.tA, ws.tB, s);
   }
 
   const T* qr = (const T*)L->qr;
@@ -184,14 +204,14 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
       if (mult) {
         EpiVinBwd<T> ev{g, N, c->ctx_mod, c->mult_res_lambda, ws.sv.save1 + sw * NS * 4 * d, L->sig,
                         ws.dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
-        launch_gemm<T, 64, 64, 2, 2, 4>(SrcRows<T>{ws.dvc + sw * NS * d, d, N},
+        launch_gemm<T, 64, 32, 4, 1, 8>(SrcRows<T>{ws.dvc + sw * NS * d, d, N},
                                         SrcRows<T>{(const T*)w->w_vctx_t, d, d}, N, d, d, ev, s);
       }
       // du = dctx . W_sweep (+ lam dv_in) -> RMS VJP inputs
       {
         EpiDuBwd<T> eu{N, d, h, d / DU_TN, inv_d, c->rms_eps, mult ? ws.lamdv : nullptr, ws.sv.o + sw * NS * d,
                        ws.sv.ssq + sw * NS * h, (const T*)w->norm_ctx_w, ws.gw, ws.rowdot, ws.dnw};
-        launch_gemm<T, 64, 64, 2, 2, 4>(SrcRows<T>{ws.dctx + sw * NS * 4 * d, 4 * d, N},
+        launch_gemm<T, 64, 32, 4, 1, 8>(SrcRows<T>{ws.dctx + sw * NS * 4 * d, 4 * d, N},
                                         SrcRows<T>{(const T*)w->w_sweep_t, 4 * d, d}, N, d, 4 * d, eu, s);
       }
       // attention VJP of sweep sw
@@ -215,7 +235,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
     }
     // committed-prefix VJP (once per cell) into the grad cache and dq
     if (pos0 > 0) {
-      const CommPlan cp = comm_plan(pos0);
+      const CommPlan cp = comm_plan_bwd(pos0);
       CommBwdArgs<T> ca{g, cp.split_len, qr, Kc, Vc, Mx, ws.G, ws.Dbar, scale, ws.dKgc, ws.dVgc, ws.dq_part};
       const size_t lds = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
       hipLaunchKernelGGL((k_comm_bwd<T, DH>), dim3(cp.nsplit, BH), dim3(256), lds, s, ca);
@@ -223,8 +243,8 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
                          (const float*)ws.dq_part, ws.dq);
     }
     // weight grads of the cell's sweeps: dW_sweep += dctx^T u ; dW_vctx += dv_ctx^T v_in
-    gemm_tn<T>(ws.dctx, 4 * d, ws.sv.u, d, ws.dWs, 4 * d, d, K * N, 1, s);
-    if (mult) gemm_tn<T>(ws.dvc, d, ws.sv.vin, d, gr->w_vctx, d, d, K * N, 1, s);
+    gemm_tn<T>(ws.dctx, 4 * d, ws.sv.u, d, ws.dWs, 4 * d, d, K * N, 1, ws.dctxT, ws.uT, s);
+    if (mult) gemm_tn<T>(ws.dvc, d, ws.sv.vin, d, gr->w_vctx, d, d, K * N, 1, ws.dvcT, ws.vinT, s);
   }
 
   // ---- projection VJP
@@ -245,7 +265,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   }
   const T* xhat = norm ? (const T*)L->xhat : x;
   // dW_proj = d_proj^T . xhat (packed rows), dxhat = d_proj . W_proj
-  gemm_tn<T>(ws.dproj, (long)nproj * d, xhat, d, ws.dWp, nproj * d, d, BT, 0, s);
+  gemm_tn<T>(ws.dproj, (long)nproj * d, xhat, d, ws.dWp, nproj * d, d, BT, 0, ws.tA, ws.tB, s);
   {
     EpiStoreF32 ep{BT, d, 0, ws.dxhat};
     launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{ws.dproj, (long)nproj * d, BT},

@@ -76,6 +76,30 @@ DM_DEV uint4 pack16(const float* in) {
   return r;
 }
 
+// N consecutive elements (16-byte aligned, N a multiple of 16 / sizeof(T)) -> floats
+template <typename T, int N>
+DM_DEV void load_vec(const T* p, float* out) {
+  constexpr int V = 16 / (int)sizeof(T);
+#pragma unroll
+  for (int i = 0; i < N / V; ++i) unpack16<T>(*reinterpret_cast<const uint4*>(p + i * V), out + i * V);
+}
+template <typename T, int N>
+DM_DEV void store_vec(T* p, const float* in) {
+  constexpr int V = 16 / (int)sizeof(T);
+#pragma unroll
+  for (int i = 0; i < N / V; ++i) *reinterpret_cast<uint4*>(p + i * V) = pack16<T>(in + i * V);
+}
+
+// v if ok else 0, without a branch: the mask is made opaque to the optimizer so the
+// (unconditional) load that produced v is not sunk into a divergent branch (the
+// compiler then has to drain all outstanding loads at the join).
+DM_DEV uint4 keep_if(uint4 v, bool ok) {
+  unsigned m = ok ? 0xffffffffu : 0u;
+  asm volatile("" : "+v"(m));
+  v.x &= m; v.y &= m; v.z &= m; v.w &= m;
+  return v;
+}
+
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // streaming 16-byte load (non-temporal hint: the data is read once)
 template <typename T>

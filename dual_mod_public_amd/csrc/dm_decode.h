@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs<T> a) {
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     const int key = k_begin + i * KPP + kslot;
-    raw[i] = (key < k_end) ? ld_nt(Kb + (long)key * DH) : uint4{0u, 0u, 0u, 0u};
+    raw[i] = keep_if(ld_nt(Kb + (long)(key < k_end ? key : k_begin) * DH), key < k_end);
   }
   float sc[NP];
   float mx = NEG_INF;
@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs<T> a) {
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     const int key = k_begin + i * KPP + kslot;
-    raw[i] = (key < k_end) ? ld_nt(Vb + (long)key * DH) : uint4{0u, 0u, 0u, 0u};
+    raw[i] = keep_if(ld_nt(Vb + (long)(key < k_end ? key : k_begin) * DH), key < k_end);
   }
   // block max
 #pragma unroll

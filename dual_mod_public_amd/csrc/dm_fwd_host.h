@@ -98,7 +98,7 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
     SrcRows<T> bv{(const T*)w->w_vctx, c->d, c->d};
     EpiSweep2<T, DH> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2};
     ProfScope ps(PROF_SWEEP2, s);
-    launch_gemm<T, 64, 64, 2, 2, 4>(av, bv, N, c->d, c->d, e2, s);
+    launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, c->d, c->d, e2, s);
   }
 }
 

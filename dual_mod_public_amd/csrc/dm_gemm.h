@@ -31,13 +31,19 @@ template <typename T> struct GemmTraits {
 
 DM_DEV uint4 zero_u4() { return uint4{0u, 0u, 0u, 0u}; }
 
+// Row-major operand loads clamp the row instead of branching: a load under a
+// divergent branch makes the compiler wait for every outstanding load at the join,
+// which would drain the prefetch ring each k-tile. Rows past the end (a partial
+// last tile) then repeat the last row; they only feed output rows >= M, which no
+// epilogue stores.
+
 template <typename T> struct SrcRows {
   static constexpr bool KMAJOR = false;
   const T* __restrict__ p;
   long ld;
   int rows;   // valid rows (global index bound)
   DM_DEV uint4 load(int r, int k) const {
-    return r < rows ? *reinterpret_cast<const uint4*>(p + (long)r * ld + k) : zero_u4();
+    return *reinterpret_cast<const uint4*>(p + (long)min(r, rows - 1) * ld + k);
   }
   DM_DEV uint4 xform(uint4 v, int, int, const float*, int) const { return v; }
 };
@@ -70,7 +76,7 @@ template <typename T> struct SrcRms {
       *reinterpret_cast<uint4*>(w_lds + i) = *reinterpret_cast<const uint4*>(w + i);
   }
   DM_DEV uint4 load(int r, int k) const {
-    return r < rows ? *reinterpret_cast<const uint4*>(p + (long)r * ld + k) : zero_u4();
+    return *reinterpret_cast<const uint4*>(p + (long)min(r, rows - 1) * ld + k);
   }
   DM_DEV uint4 xform(uint4 v, int rloc, int k, const float* rs_lds, int r0) const {
     constexpr int V = GemmTraits<T>::VEC;
@@ -217,22 +223,40 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
   };
 
   const int nk = (K + BK - 1) / BK;   // a partial last tile needs k-bounded sources
+  if (nk >= D && nk % D == 0) {
+    // Software pipeline with no data-dependent branches around the loads: the
+    // steady state always prefetches tile kt + D (it exists), the last D tiles run
+    // unrolled without prefetch. The waitcnt before each LDS store then only waits
+    // for the oldest ring slot.
 #pragma unroll
-  for (int s = 0; s < D; ++s)
-    if (s < nk) gload(s, ra[s], rb[s]);
-  sstore(0, buf[0], ra[0], rb[0]);
-  __syncthreads();
-  for (int kt0 = 0; kt0 < nk; kt0 += D) {
+    for (int s = 0; s < D; ++s) gload(s, ra[s], rb[s]);
+    sstore(0, buf[0], ra[0], rb[0]);
+    __syncthreads();
+    for (int kt0 = 0; kt0 < nk - D; kt0 += D) {
 #pragma unroll
-    for (int j = 0; j < D; ++j) {
-      const int kt = kt0 + j;
-      if (kt < nk) {
-        // slot j (tile kt) is already in LDS: refill it with tile kt + D
-        if (kt + D < nk) gload(kt + D, ra[j], rb[j]);
-        compute(buf[kt & 1]);
-        if (kt + 1 < nk) sstore(kt + 1, buf[(kt + 1) & 1], ra[(j + 1) % D], rb[(j + 1) % D]);
+      for (int j = 0; j < D; ++j) {
+        const int kt = kt0 + j;
+        gload(kt + D, ra[j], rb[j]);
+        compute(buf[j & 1]);
+        sstore(kt + 1, buf[(j + 1) & 1], ra[(j + 1) % D], rb[(j + 1) % D]);
         __syncthreads();
       }
+    }
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int kt = nk - D + j;
+      compute(buf[j & 1]);
+      if (j + 1 < D) sstore(kt + 1, buf[(j + 1) & 1], ra[(j + 1) % D], rb[(j + 1) % D]);
+      __syncthreads();
+    }
+  } else {
+    // short or ragged K: one tile at a time
+    for (int kt = 0; kt < nk; ++kt) {
+      gload(kt, ra[0], rb[0]);
+      sstore(kt, buf[0], ra[0], rb[0]);
+      __syncthreads();
+      compute(buf[0]);
+      __syncthreads();
     }
   }
 }

@@ -62,6 +62,39 @@ static __global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ 
   }
 }
 
+// out[c, col0_out + r] = in[r, c] for a [rows, cols] row-major matrix (ld_in) into a
+// [cols, ld_out] matrix, with output columns [rows, rows_pad) zero-filled: 64x64 tiles
+// through LDS, 16-byte loads and stores. cols, rows_pad, ld_out and col0_out must be
+// multiples of 16 / sizeof(T).
+template <typename T>
+static __global__ __launch_bounds__(256) void k_transpose16(const T* __restrict__ in, long ld_in, int rows, int cols,
+                                                            int rows_pad, T* __restrict__ out, long ld_out,
+                                                            long col0_out) {
+  constexpr int V = 16 / (int)sizeof(T);
+  __shared__ T tile[64][64 + 1];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  for (int v = threadIdx.x; v < 64 * 64 / V; v += 256) {
+    const int r = v / (64 / V), cc = (v % (64 / V)) * V;
+    if (r0 + r < rows && c0 + cc < cols) {
+      const uint4 x = *reinterpret_cast<const uint4*>(in + (long)(r0 + r) * ld_in + c0 + cc);
+      const T* e = reinterpret_cast<const T*>(&x);
+#pragma unroll
+      for (int j = 0; j < V; ++j) tile[r][cc + j] = e[j];
+    }
+  }
+  __syncthreads();
+  for (int v = threadIdx.x; v < 64 * 64 / V; v += 256) {
+    const int cc = v / (64 / V), r = (v % (64 / V)) * V;
+    if (r0 + r < rows_pad && c0 + cc < cols) {
+      uint4 x;
+      T* e = reinterpret_cast<T*>(&x);
+#pragma unroll
+      for (int j = 0; j < V; ++j) e[j] = (r0 + r + j < rows) ? tile[r + j][cc] : from_f<T>(0.f);
+      *reinterpret_cast<uint4*>(out + (long)(c0 + cc) * ld_out + col0_out + r0 + r) = x;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // row RMSNorm (attn_norm, models/dualmod/attention.py:74-83): one wave per row
 // ---------------------------------------------------------------------------
