@@ -8,8 +8,11 @@ One step = one DM attention layer of the 340M shape (B=8, T=2048, d=1024,
 fp32 accumulate) through libdm_hip.so: the forward (attn_norm + projections,
 the 32 chunk cells = committed accumulator + 4 sweeps each, W_O with the
 residual) and, for the default fwdbwd workload, the
-reverse-scan backward with exact recompute producing dx and every parameter
-gradient for an upstream dy ~ N(0,1). Inputs (x, dy, weights, RoPE tables) are
+reverse-scan backward producing dx and every parameter gradient for an upstream
+dy ~ N(0,1). The forward keeps every cell's sweep states in an HBM tape (1.9 GB
+for this layer) that the backward reads instead of recomputing them; the
+reference's exact-recompute mode (same values bit for bit) is timed beside it
+(--recompute makes it the headline). Inputs (x, dy, weights, RoPE tables) are
 resident in HBM before timing starts.
 
 Prints ONE JSON line (rank 0): the headline sweep throughput in tokens/s, the
@@ -39,6 +42,9 @@ from dual_mod_public_amd.synthetic import make_input, make_state_dict  # noqa: E
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+TIMING_NOTE = ("avg_launch_ms: per-dispatch span from the device clock (s_memrealtime, first block "
+               "start to last block end), recorded by the kernel itself in the timed region; "
+               "avg_launch_ms_events: HIP event pair around each launch on its stream (adds queue time)")
 
 # BASELINE config 2 (forward) — the 340M-shape DM layer
 C2 = dict(B=8, T=2048, d=1024, h=16, c=64, K=4, wseed=1, xseed=2)
@@ -148,7 +154,8 @@ def bench_decode(dev, steps_override=None):
     weight_bytes = steps * 12.0 * d * d * 2
     write_bytes = steps * 2.0 * B * d * 2
     total = tape_bytes + weight_bytes + write_bytes
-    read_avg_s = kt.avg_ms / 1e3
+    read_avg_ms = kt.device_avg_ms if kt.device_avg_ms is not None else kt.avg_ms
+    read_avg_s = read_avg_ms / 1e3
     read_bytes_per_launch = tape_bytes / steps
     return {
         "metric": "decode HBM GB/s (attend_one+refine_kv over the tape, append)",
@@ -160,7 +167,8 @@ def bench_decode(dev, steps_override=None):
                      "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": read_bytes_per_launch / read_avg_s / 1e9 / PEAK_HBM_GBS,
                      "traffic": None, "kernel": "k_decode_partial",
-                     "avg_launch_ms": kt.avg_ms, "launches": kt.n},
+                     "avg_launch_ms": read_avg_ms, "avg_launch_ms_events": kt.avg_ms,
+                     "timing": TIMING_NOTE, "launches": kt.n},
         "path_frac_of_hbm_peak": total / wall / 1e9 / PEAK_HBM_GBS,
     }
 
@@ -175,6 +183,8 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=0)
     ap.add_argument("--kernel", default="sweep1", help="kernel class timed for the roofline")
     ap.add_argument("--workload", default="fwdbwd", choices=["fwdbwd", "fwd"])
+    ap.add_argument("--recompute", action="store_true",
+                    help="headline without the forward tape (backward recomputes every cell)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -198,45 +208,61 @@ def main():
     dx = torch.empty_like(x)
     fwdbwd = args.workload == "fwdbwd"
 
+    use_tape = fwdbwd and not args.recompute
+    tape = cell.new_tape(sched) if fwdbwd else None
+
     def step_fwd():
         cell.layer_forward(x, y, cos, sin, sched, Kc, Vc, ocat, bufs)
 
-    def step():
-        cell.layer_forward(x, y, cos, sin, sched, Kc, Vc, ocat, bufs)
-        if fwdbwd:
-            cell.layer_backward(x, dy, dx, cos, sin, sched, Kc, Vc, ocat, bufs, grads)
+    def make_step(taped):
+        tp = tape if taped else None
 
+        def step():
+            cell.layer_forward(x, y, cos, sin, sched, Kc, Vc, ocat, bufs, tape=tp)
+            if fwdbwd:
+                cell.layer_backward(x, dy, dx, cos, sin, sched, Kc, Vc, ocat, bufs, grads, tape=tp)
+        return step
+
+    def timed(fn, steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    step = make_step(use_tape)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     sweeps = sum(k for _, _, k in sched)
     per_step_launches = sweeps * (2 if fwdbwd else 1)
     with L.KernelTimer(args.kernel, max_launches=args.steps * per_step_launches * 2 + 64) as kt:
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        dt = (time.perf_counter() - t0) / args.steps
-    # forward alone (reported beside the headline)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step_fwd()
-    torch.cuda.synchronize()
-    dt_fwd = (time.perf_counter() - t0) / args.steps
+        dt = timed(step, args.steps)
+    # forward alone, and the other backward mode (reported beside the headline)
+    dt_fwd = timed(step_fwd, args.steps)
+    dt_other = None
+    if fwdbwd:
+        other = make_step(not use_tape)
+        other()
+        dt_other = timed(other, args.steps)
     tokens = B * T
     fpt = fwdbwd_flops_per_token(d, T, c, K) if fwdbwd else fwd_flops_per_token(d, T, c, K)
     if args.kernel == "sweep1":
         per_launch = sweep1_flops(B * c, d)
-        kname = "k_gemm<SrcRms, EpiSweep1> (sweep GEMM 1: u . [w_kctx|g_k|v_map|g_v]^T)"
+        kname = ("k_gemm<SrcRowsRs, EpiSweep1> (sweep GEMM 1: RMSNorm(o) . [w_kctx|g_k|v_map|g_v]^T, "
+                 "norm weight folded into W, row scale in the epilogue)")
     elif args.kernel == "layer":
         per_launch = fwd_flops_per_token(d, T, c, K) * tokens
         kname = "whole dm_layer_fwd call"
     else:
         per_launch = float("nan")
         kname = args.kernel
-    achieved = per_launch / (kt.avg_ms / 1e3) / 1e12 if kt.n else None
-    wl = ("C3: 340M-shape DM layer forward + reverse-scan backward (exact recompute)" if fwdbwd
-          else "C2: 340M-shape DM layer forward")
+    avg_ms = kt.device_avg_ms if kt.device_avg_ms is not None else kt.avg_ms
+    achieved = per_launch / (avg_ms / 1e3) / 1e12 if kt.n else None
+    wl = ("C3: 340M-shape DM layer forward + reverse-scan backward (" +
+          ("exact recompute" if not use_tape else "sweep states from the forward's HBM tape") + ")"
+          if fwdbwd else "C2: 340M-shape DM layer forward")
     out = {
         "metric": "DM sweep tokens/s/GPU (fwd+bwd, c=64, K=4)" if fwdbwd else
                   "DM sweep tokens/s/GPU (forward, c=64, K=4)",
@@ -248,14 +274,20 @@ def main():
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": (achieved / PEAK_BF16_TFLOPS) if achieved else None,
                      "traffic": None, "kernel": kname, "flops_per_launch": per_launch,
-                     "avg_launch_ms": kt.avg_ms, "launches": kt.n},
+                     "avg_launch_ms": avg_ms, "avg_launch_ms_events": kt.avg_ms,
+                     "timing": TIMING_NOTE if kt.device_avg_ms is not None else "HIP event pairs",
+                     "launches": kt.n},
         "path_roofline": {"flops_per_token": fpt, "achieved_tflops": fpt * tokens / dt / 1e12,
                           "frac": fpt * tokens / dt / 1e12 / PEAK_BF16_TFLOPS},
         "forward_only": {"ms_per_step": dt_fwd * 1e3, "tokens_per_s": tokens / dt_fwd,
                          "frac": fwd_flops_per_token(d, T, c, K) * tokens / dt_fwd / 1e12 / PEAK_BF16_TFLOPS},
     }
+    if fwdbwd:
+        out["tape_bytes"] = tape.numel()
+        out["recompute" if use_tape else "tape"] = {"ms_per_step": dt_other * 1e3,
+                                                    "tokens_per_s": tokens / dt_other}
     if not args.no_decode:
-        del cell, bufs, Kc, Vc, ocat, y, x, dx, dy, grads
+        del cell, bufs, Kc, Vc, ocat, y, x, dx, dy, grads, tape
         torch.cuda.empty_cache()
         out["decode"] = bench_decode(dev, args.decode_steps or None)
     if not args.no_cpu_baseline:

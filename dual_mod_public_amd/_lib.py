@@ -83,13 +83,15 @@ SIGNATURES = {
     "dm_cell_workspace_bytes": (ctypes.c_size_t, [P(dm_config), c_i32]),
     "dm_cell_fwd": (ctypes.c_int, [P(dm_config), P(dm_packed), P(dm_layer_bufs), c_fp, c_fp,
                                    P(dm_cell_args), c_vp]),
+    "dm_layer_tape_bytes": (ctypes.c_size_t, [P(dm_config), P(c_i32), c_i32]),
     "dm_layer_fwd": (ctypes.c_int, [P(dm_config), P(dm_packed), c_vp, c_vp, c_fp, c_fp,
                                     P(dm_layer_bufs), P(c_i32), c_i32, c_vp, c_vp, c_i32, c_vp,
-                                    c_vp, ctypes.c_size_t, c_vp]),
+                                    c_vp, ctypes.c_size_t, c_vp, ctypes.c_size_t, c_vp]),
     "dm_layer_bwd_workspace_bytes": (ctypes.c_size_t, [P(dm_config), c_i32, c_i32, c_i32]),
     "dm_layer_bwd": (ctypes.c_int, [P(dm_config), P(dm_packed), c_vp, c_vp, c_vp, c_fp, c_fp,
                                     P(dm_layer_bufs), P(c_i32), c_i32, c_vp, c_vp, c_i32, c_vp,
-                                    P(dm_grads), c_vp, ctypes.c_size_t, c_vp]),
+                                    c_vp, ctypes.c_size_t, P(dm_grads), c_vp, ctypes.c_size_t,
+                                    c_vp]),
     "dm_decode_workspace_bytes": (ctypes.c_size_t, [P(dm_config), c_i32]),
     "dm_decode_step": (ctypes.c_int, [P(dm_config), P(dm_packed), c_fp, c_fp,
                                       P(dm_decode_args), c_vp]),
@@ -98,6 +100,7 @@ SIGNATURES = {
                                c_vp]),
     "dm_check_schedule": (ctypes.c_int, [P(c_i32), c_i32, c_i32]),
     "dm_prof_start": (ctypes.c_int, [c_i32, c_i32]),
+    "dm_prof_stop2": (ctypes.c_int, [P(ctypes.c_float), P(ctypes.c_float), P(c_i32)]),
     "dm_prof_stop": (ctypes.c_int, [P(ctypes.c_float), P(c_i32)]),
 }
 
@@ -112,21 +115,30 @@ class KernelTimer:
     def __init__(self, kernel_class, max_launches=8192):
         self.cls = PROF[kernel_class] if isinstance(kernel_class, str) else int(kernel_class)
         self.cap = max_launches
-        self.total_ms, self.n = 0.0, 0
+        self.total_ms, self.n, self.device_total_ms = 0.0, 0, None
 
     def __enter__(self):
         check(lib().dm_prof_start(self.cls, self.cap))
         return self
 
     def __exit__(self, *exc):
-        ms, n = ctypes.c_float(), c_i32()
-        check(lib().dm_prof_stop(ctypes.byref(ms), ctypes.byref(n)))
+        ms, dms, n = ctypes.c_float(), ctypes.c_float(), c_i32()
+        check(lib().dm_prof_stop2(ctypes.byref(ms), ctypes.byref(dms), ctypes.byref(n)))
         self.total_ms, self.n = float(ms.value), int(n.value)
+        self.device_total_ms = float(dms.value) if dms.value >= 0 else None
         return False
 
     @property
     def avg_ms(self):
+        """Mean per-launch time from the HIP event pairs (includes queue overheads)."""
         return self.total_ms / max(self.n, 1)
+
+    @property
+    def device_avg_ms(self):
+        """Mean per-dispatch span from the device clock (None for classes without it)."""
+        if self.device_total_ms is None:
+            return None
+        return self.device_total_ms / max(self.n, 1)
 
 _lib = None
 _lib_err = None

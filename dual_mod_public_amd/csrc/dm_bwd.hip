@@ -1,5 +1,6 @@
 // libdm_hip.so — the backward entry points of the C ABI (include/dm_abi.h):
-// reverse-scan layer backward with exact per-cell recompute.
+// reverse-scan layer backward, reading every cell's sweep states from the
+// forward's tape or rebuilding them by exact per-cell recompute.
 //
 // Never allocates device memory and never synchronizes: every buffer is carved
 // from the caller's workspace; all launches go to the caller's stream.
@@ -59,16 +60,7 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.dnw = cv.take<float>(cdiv(N, NSLOT_TM) * d * 4);
   w.fws = carve_cell(c, cache_T, cv.base ? cv.base + cv.off : nullptr);
   cv.off += align256(w.fws.bytes);
-  w.sv.o = cv.take<T>(kmax * N * d * e);
-  w.sv.ssq = cv.take<float>(kmax * N * h * 4);
-  w.sv.stat_m = cv.take<float>(kmax * BH * CMAX * 4);
-  w.sv.stat_z = cv.take<float>(kmax * BH * CMAX * 4);
-  w.sv.save1 = cv.take<float>(kmax * N * 4 * d * 4);
-  w.sv.save2 = cv.take<float>(kmax * N * d * 4);
-  w.sv.vin = cv.take<T>(kmax * N * d * e);
-  w.sv.u = cv.take<T>(kmax * N * d * e);
-  w.sv.Kin = cv.take<T>((kmax + 1) * BH * CMAX * dh * e);
-  w.sv.Vin = cv.take<T>((kmax + 1) * BH * CMAX * dh * e);
+  w.sv = carve_save<T>(c, N, kmax, false, false, cv);
   w.dctx = cv.take<T>(kmax * N * 4 * d * e);
   w.dvc = cv.take<T>(kmax * N * d * e);
   w.dKa = cv.take<float>(BH * CMAX * dh * 4);
@@ -143,10 +135,24 @@ void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N
   launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{At, Kp, M}, SrcRows<T>{Bt, Kp, N}, M, N, Kp, ep, s);
 }
 
+// C [M, N] (+)= A^T . u for u = RMSNorm(o) [K, N] with the norm weight w: u^T is
+// formed from o, its partial sums of squares and w in the transpose pass.
+template <typename T>
+void gemm_tn_rms(const T* A, long lda, const T* o, const float* ssq, int nparts, const T* w, float inv_d, float eps,
+                 float* C, int M, int N, int K, int accumulate, T* At, T* Bt, hipStream_t s) {
+  const int Kp = cdiv(K, 64) * 64;
+  transpose<T>(A, lda, K, M, Kp, At, Kp, 0, s);
+  hipLaunchKernelGGL(k_transpose_rms16<T>, dim3(cdiv(N, 64), cdiv(Kp, 64)), dim3(256), 0, s, o, (long)N, K, N, Kp,
+                     ssq, nparts, w, inv_d, eps, Bt, (long)Kp);
+  EpiStoreF32 ep{M, N, accumulate, C};
+  launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{At, Kp, M}, SrcRows<T>{Bt, Kp, N}, M, N, Kp, ep, s);
+}
+
 template <typename T, int DH>
 int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T* dx, const float* cos,
                   const float* sin, const dm_layer_bufs* L, const int32_t* sched, int n_cells, const T* Kc,
-                  const T* Vc, int cache_T, const T* ocat, const dm_grads* gr, const BwdWs<T>& ws, hipStream_t s) {
+                  const T* Vc, int cache_T, const T* ocat, const char* tape, const size_t* tape_off,
+                  const dm_grads* gr, const BwdWs<T>& ws, hipStream_t s) {
   const int B = c->B, d = c->d, h = c->h, T_ = L->T, BT = B * T_, BH = B * h;
   const bool mult = c->ctx_mod != DM_CTX_LINEAR;
   const int nproj = mult ? 6 : 5;
@@ -186,31 +192,39 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
     const int N = B * cc;
     const size_t NS = (size_t)N;
     CellGeom g{B, cc, d, h, DH, pos0, pos0, T_, cache_T};
-    // exact recompute of the cell, keeping every sweep's state
-    run_cell<T, DH>(c, w, L, cos, sin, pos0, cc, K, pos0, T_, (T*)Kc, (T*)Vc, cache_T, nullptr, nullptr, ws.fws,
-                    &ws.sv, s);
-    const float* Mx = pos0 > 0 ? ws.fws.M : nullptr;
+    // every sweep's state of the cell: saved by the forward, or an exact recompute
+    CellSave<T> sv = ws.sv;
+    const float* Mx;
+    if (tape != nullptr) {
+      Carver cv(const_cast<char*>(tape) + tape_off[ci]);
+      sv = carve_save<T>(c, NS, K, true, pos0 > 0, cv);
+      Mx = sv.Mx;
+    } else {
+      run_cell<T, DH>(c, w, L, cos, sin, pos0, cc, K, pos0, T_, (T*)Kc, (T*)Vc, cache_T, nullptr, nullptr, ws.fws,
+                      &ws.sv, s);
+      Mx = pos0 > 0 ? ws.fws.M : nullptr;
+    }
     const float* dKn = ws.dKgc;
     const float* dVn = ws.dVgc;
     long dn_stride = (long)cache_T * DH;
     int dn_row0 = pos0;
     for (int sw = K - 1; sw >= 0; --sw) {
       // refine VJP of sweep sw
-      RefineBwdArgs<T> ra{g, N, c->ctx_mod, dKn, dVn, dn_stride, dn_row0, ws.sv.save1 + sw * NS * 4 * d,
-                          ws.sv.save2 + sw * NS * d, L->glogx, kraw, vraw, cos, sin, ws.dctx + sw * NS * 4 * d,
+      RefineBwdArgs<T> ra{g, N, c->ctx_mod, dKn, dVn, dn_stride, dn_row0, sv.save1 + sw * NS * 4 * d,
+                          mult ? sv.save2 + sw * NS * d : nullptr, L->glogx, kraw, vraw, cos, sin, ws.dctx + sw * NS * 4 * d,
                           ws.dvc + sw * NS * d, ws.dglogx, ws.dkraw, ws.dvraw};
       hipLaunchKernelGGL((k_refine_bwd<T, DH>), dim3(cdiv((long)N * d / 2, 256)), dim3(256), 0, s, ra);
       // dv_in = dv_ctx . W_vctx (mult family)
       if (mult) {
-        EpiVinBwd<T> ev{g, N, c->ctx_mod, c->mult_res_lambda, ws.sv.save1 + sw * NS * 4 * d, L->sig,
+        EpiVinBwd<T> ev{g, N, c->ctx_mod, c->mult_res_lambda, sv.save1 + sw * NS * 4 * d, L->sig,
                         ws.dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
         launch_gemm<T, 64, 32, 4, 1, 8>(SrcRows<T>{ws.dvc + sw * NS * d, d, N},
                                         SrcRows<T>{(const T*)w->w_vctx_t, d, d}, N, d, d, ev, s);
       }
       // du = dctx . W_sweep (+ lam dv_in) -> RMS VJP inputs
       {
-        EpiDuBwd<T> eu{N, d, h, d / DU_TN, inv_d, c->rms_eps, mult ? ws.lamdv : nullptr, ws.sv.o + sw * NS * d,
-                       ws.sv.ssq + sw * NS * h, (const T*)w->norm_ctx_w, ws.gw, ws.rowdot, ws.dnw};
+        EpiDuBwd<T> eu{N, d, h, d / DU_TN, inv_d, c->rms_eps, mult ? ws.lamdv : nullptr, sv.o + sw * NS * d,
+                       sv.ssq + sw * NS * h, (const T*)w->norm_ctx_w, ws.gw, ws.rowdot, ws.dnw};
         launch_gemm<T, 64, 32, 4, 1, 8>(SrcRows<T>{ws.dctx + sw * NS * 4 * d, 4 * d, N},
                                         SrcRows<T>{(const T*)w->w_sweep_t, 4 * d, d}, N, d, 4 * d, eu, s);
       }
@@ -218,13 +232,13 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
       {
         const T* Kin; const T* Vin; long in_stride; int in_row0;
         if (sw == 0) { Kin = kself; Vin = vraw; in_stride = (long)T_ * DH; in_row0 = pos0; }
-        else { Kin = ws.sv.Kin + sw * slot; Vin = ws.sv.Vin + sw * slot; in_stride = (long)CMAX * DH; in_row0 = 0; }
+        else { Kin = sv.Kin + sw * slot; Vin = sv.Vin + sw * slot; in_stride = (long)CMAX * DH; in_row0 = 0; }
         float* dKo = sw == 0 ? nullptr : ((K - 1 - sw) % 2 == 0 ? ws.dKa : ws.dKb);
         float* dVo = sw == 0 ? nullptr : ((K - 1 - sw) % 2 == 0 ? ws.dVa : ws.dVb);
-        AttnBwdArgs<T> aa{g, qr, kself, vraw, Kin, Vin, in_stride, in_row0, ws.sv.o + sw * NS * d,
-                          ws.sv.ssq + sw * NS * h, ws.gw, ws.rowdot, d / DU_TN,
-                          sw == K - 1 ? ws.docat : nullptr, ws.sv.stat_m + sw * (size_t)BH * CMAX,
-                          ws.sv.stat_z + sw * (size_t)BH * CMAX, Mx, ws.G, ws.Dbar, sw == K - 1 ? 1 : 0,
+        AttnBwdArgs<T> aa{g, qr, kself, vraw, Kin, Vin, in_stride, in_row0, sv.o + sw * NS * d,
+                          sv.ssq + sw * NS * h, ws.gw, ws.rowdot, d / DU_TN,
+                          sw == K - 1 ? ws.docat : nullptr, sv.stat_m + sw * (size_t)BH * CMAX,
+                          sv.stat_z + sw * (size_t)BH * CMAX, Mx, ws.G, ws.Dbar, sw == K - 1 ? 1 : 0,
                           scale, inv_d, c->rms_eps, dKo, dVo, ws.dkself, ws.dvraw, ws.dq};
         const size_t lds = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
         hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(BH), dim3(256), lds, s, aa);
@@ -243,8 +257,9 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
                          (const float*)ws.dq_part, ws.dq);
     }
     // weight grads of the cell's sweeps: dW_sweep += dctx^T u ; dW_vctx += dv_ctx^T v_in
-    gemm_tn<T>(ws.dctx, 4 * d, ws.sv.u, d, ws.dWs, 4 * d, d, K * N, 1, ws.dctxT, ws.uT, s);
-    if (mult) gemm_tn<T>(ws.dvc, d, ws.sv.vin, d, gr->w_vctx, d, d, K * N, 1, ws.dvcT, ws.vinT, s);
+    gemm_tn_rms<T>(ws.dctx, 4 * d, sv.o, sv.ssq, h, (const T*)w->norm_ctx_w, inv_d, c->rms_eps, ws.dWs, 4 * d,
+                   d, K * N, 1, ws.dctxT, ws.uT, s);
+    if (mult) gemm_tn<T>(ws.dvc, d, sv.vin, d, gr->w_vctx, d, d, K * N, 1, ws.dvcT, ws.vinT, s);
   }
 
   // ---- projection VJP
@@ -318,6 +333,27 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   return DM_OK;
 }
 
+template <typename T>
+int layer_bwd_dispatch(const dm_config* c, const dm_packed* w, const void* x, const void* dy, void* dx,
+                       const float* cos, const float* sin, const dm_layer_bufs* L, const int32_t* sched,
+                       int n_cells, const void* Kc, const void* Vc, int cache_T, const void* ocat, const void* tape,
+                       size_t tape_bytes, const dm_grads* g, void* workspace, int kmax, hipStream_t s) {
+  std::vector<size_t> off;
+  if (tape != nullptr) {
+    off = tape_offsets<T>(c, sched, n_cells);
+    DM_REQUIRE(tape_bytes >= off[n_cells], DM_ERR_WORKSPACE, "tape %zu < %zu bytes", tape_bytes, off[n_cells]);
+    DM_REQUIRE(aligned16(tape), DM_ERR_INVALID, "tape must be 16-byte aligned");
+  }
+  const BwdWs<T> ws = carve_bwd<T>(c, L->T, cache_T, kmax, workspace);
+  auto run = [&](auto dh_tag) {
+    constexpr int DH = decltype(dh_tag)::value;
+    return run_layer_bwd<T, DH>(c, w, (const T*)x, (const T*)dy, (T*)dx, cos, sin, L, sched, n_cells, (const T*)Kc,
+                                (const T*)Vc, cache_T, (const T*)ocat, (const char*)tape,
+                                tape ? off.data() : nullptr, g, ws, s);
+  };
+  return c->dh == 64 ? run(std::integral_constant<int, 64>{}) : run(std::integral_constant<int, 128>{});
+}
+
 }  // namespace dm
 
 using namespace dm;
@@ -333,7 +369,8 @@ size_t dm_layer_bwd_workspace_bytes(const dm_config* c, int32_t T, int32_t cache
 int dm_layer_bwd(const dm_config* c, const dm_packed* w, const void* x, const void* dy, void* dx,
                  const float* cos, const float* sin, const dm_layer_bufs* L, const int32_t* sched,
                  int32_t n_cells, const void* K_cache, const void* V_cache, int32_t cache_T, const void* ocat,
-                 const dm_grads* g, void* workspace, size_t workspace_bytes, void* stream) {
+                 const void* tape, size_t tape_bytes, const dm_grads* g, void* workspace, size_t workspace_bytes,
+                 void* stream) {
   int rc = check_cfg(c);
   if (rc) return rc;
   if ((rc = check_packed(c, w)) || (rc = check_bufs(c, L))) return rc;
@@ -366,23 +403,10 @@ int dm_layer_bwd(const dm_config* c, const dm_packed* w, const void* x, const vo
   DM_REQUIRE(workspace && workspace_bytes >= need, DM_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes,
              need);
   hipStream_t s = S(stream);
-  if (c->dtype == DM_BF16) {
-    const BwdWs<bf16> ws = carve_bwd<bf16>(c, L->T, cache_T, kmax, workspace);
-    rc = c->dh == 64 ? run_layer_bwd<bf16, 64>(c, w, (const bf16*)x, (const bf16*)dy, (bf16*)dx, cos, sin, L, sched,
-                                               n_cells, (const bf16*)K_cache, (const bf16*)V_cache, cache_T,
-                                               (const bf16*)ocat, g, ws, s)
-                     : run_layer_bwd<bf16, 128>(c, w, (const bf16*)x, (const bf16*)dy, (bf16*)dx, cos, sin, L, sched,
-                                                n_cells, (const bf16*)K_cache, (const bf16*)V_cache, cache_T,
-                                                (const bf16*)ocat, g, ws, s);
-  } else {
-    const BwdWs<float> ws = carve_bwd<float>(c, L->T, cache_T, kmax, workspace);
-    rc = c->dh == 64 ? run_layer_bwd<float, 64>(c, w, (const float*)x, (const float*)dy, (float*)dx, cos, sin, L,
-                                                sched, n_cells, (const float*)K_cache, (const float*)V_cache, cache_T,
-                                                (const float*)ocat, g, ws, s)
-                     : run_layer_bwd<float, 128>(c, w, (const float*)x, (const float*)dy, (float*)dx, cos, sin, L,
-                                                 sched, n_cells, (const float*)K_cache, (const float*)V_cache,
-                                                 cache_T, (const float*)ocat, g, ws, s);
-  }
+  rc = c->dtype == DM_BF16 ? layer_bwd_dispatch<bf16>(c, w, x, dy, dx, cos, sin, L, sched, n_cells, K_cache, V_cache,
+                                                      cache_T, ocat, tape, tape_bytes, g, workspace, kmax, s)
+                           : layer_bwd_dispatch<float>(c, w, x, dy, dx, cos, sin, L, sched, n_cells, K_cache, V_cache,
+                                                       cache_T, ocat, tape, tape_bytes, g, workspace, kmax, s);
   if (rc) return rc;
   DM_HIP(hipGetLastError());
   return DM_OK;

@@ -182,4 +182,24 @@ template <> struct Mfma<float> {
 
 DM_DEV floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
 
+// ---- optional per-dispatch timing from the device clock ---------------------
+// A timed launch gets prof_ts = [PROF_SLOTS] earliest block starts followed by
+// [PROF_SLOTS] latest block ends (s_memrealtime ticks; block b folds into slot
+// b % PROF_SLOTS). The kernel's span is max(end) - min(start), the interval a
+// kernel-trace profiler reports. prof_ts is nullptr on every untimed launch.
+constexpr int PROF_SLOTS = 1024;
+
+DM_DEV uint64_t prof_begin(const uint64_t* prof_ts) { return prof_ts ? wall_clock64() : 0; }
+
+DM_DEV void prof_end(uint64_t* prof_ts, uint64_t t0) {
+  if (prof_ts == nullptr) return;   // uniform: a kernel argument
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int b = ((int)blockIdx.z * (int)gridDim.y + (int)blockIdx.y) * (int)gridDim.x + (int)blockIdx.x;
+    atomicMin(reinterpret_cast<unsigned long long*>(prof_ts + b % PROF_SLOTS), (unsigned long long)t0);
+    atomicMax(reinterpret_cast<unsigned long long*>(prof_ts + PROF_SLOTS + b % PROF_SLOTS),
+              (unsigned long long)wall_clock64());
+  }
+}
+
 }  // namespace dm

@@ -20,6 +20,7 @@ template <typename T> struct DecodeArgs {
   float* o;          // [B, d] fp32
   float* ssq;        // [B, h]
   T* o_cat;          // [B, d] storage dtype
+  uint64_t* prof_ts; // per-dispatch timing slots (nullptr: untimed)
 };
 
 template <typename T, int DH, int L>
@@ -29,6 +30,7 @@ __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs<T> a) {
   constexpr int KPP = 256 / LPK;         // keys per pass
   constexpr int NP = L / KPP;            // passes
   static_assert(L % KPP == 0, "split length");
+  const uint64_t t0 = prof_begin(a.prof_ts);
   __shared__ float red[4][DH + 2];
   const int s = blockIdx.x, bh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -105,6 +107,7 @@ __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs<T> a) {
   float* out = a.part + ((long)s * (a.B * a.h) + bh) * (DH + 2);
   for (int i = tid; i < DH + 1; i += 256) out[i] = red[0][i] + red[1][i] + red[2][i] + red[3][i];
   if (tid == 0) out[DH + 1] = M;
+  prof_end(a.prof_ts, t0);
 }
 
 // merge split partials + raw self column -> o, ssq, o_cat (one wave per (b, h))

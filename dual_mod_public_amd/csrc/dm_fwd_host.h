@@ -4,6 +4,8 @@
 // state in a CellSave instead of overwriting it in place).
 #pragma once
 
+#include <vector>
+
 #include "dm_host.h"
 
 namespace dm {
@@ -47,9 +49,45 @@ template <typename T> struct CellSave {
   float* save1;      // [K][N, 4d]     raw sweep GEMM 1 outputs
   float* save2;      // [K][N, d]      raw v_ctx (mult family)
   T* vin;            // [K][N, d]      v_in (mult family)
-  T* u;              // [K][N, d]      u = RMSNorm_ctx(o)
-  T* Kin; T* Vin;    // [K+1][BH, CMAX, DH]  intra rows read by sweep s (slot 0 unused: raw rows)
+  T* Kin; T* Vin;    // [K+1][BH, CMAX, DH]  intra rows read by sweep s (slot 0 unused: raw rows);
+                     //   with last_to_cache only [K] slots: the last sweep writes the cache rows
+  float* Mx;         // [BH, CMAX] committed row max (tape cells with pos0 > 0), else nullptr
+  bool last_to_cache;
 };
+
+// Layout of one cell's saved state for N = B*cc rows and K sweeps. `tape` cells
+// (forward-saved) drop the last K/V slot and add the committed row max.
+template <typename T>
+CellSave<T> carve_save(const dm_config* c, size_t N, int K, bool tape, bool has_comm, Carver& cv) {
+  CellSave<T> w{};
+  const size_t d = c->d, h = c->h, dh = c->dh, e = sizeof(T), BH = (size_t)c->B * c->h, k = K;
+  const bool mult = c->ctx_mod != DM_CTX_LINEAR;
+  w.o = cv.take<T>(k * N * d * e);
+  w.ssq = cv.take<float>(k * N * h * 4);
+  w.stat_m = cv.take<float>(k * BH * CMAX * 4);
+  w.stat_z = cv.take<float>(k * BH * CMAX * 4);
+  w.save1 = cv.take<float>(k * N * 4 * d * 4);
+  w.save2 = mult ? cv.take<float>(k * N * d * 4) : nullptr;
+  w.vin = mult ? cv.take<T>(k * N * d * e) : nullptr;
+  const size_t slots = tape ? k : k + 1;
+  w.Kin = cv.take<T>(slots * BH * CMAX * dh * e);
+  w.Vin = cv.take<T>(slots * BH * CMAX * dh * e);
+  w.Mx = (tape && has_comm) ? cv.take<float>(BH * CMAX * 4) : nullptr;
+  w.last_to_cache = tape;
+  return w;
+}
+
+// Byte offset of every cell's saved state in a layer tape (n_cells + 1 entries).
+template <typename T>
+std::vector<size_t> tape_offsets(const dm_config* c, const int32_t* sched, int n_cells) {
+  std::vector<size_t> off(n_cells + 1, 0);
+  for (int i = 0; i < n_cells; ++i) {
+    Carver cv(nullptr);
+    carve_save<T>(c, (size_t)c->B * sched[3 * i + 1], sched[3 * i + 2], true, sched[3 * i] > 0, cv);
+    off[i + 1] = off[i] + cv.off;
+  }
+  return off;
+}
 
 template <typename T, int DH>
 void run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int Tl, int Tbuf, int buf_t0,
@@ -60,11 +98,10 @@ void run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int 
                      qr, kraw, kself, vraw, glogx, sig};
   SrcRows<T> sa{xhat, c->d, M};
   SrcRows<T> sb{(const T*)w->w_proj, c->d, nseg * c->d};
-  ProfScope ps(PROF_PROJ, s);
   if constexpr (DH == 64)
-    launch_gemm<T, 128, 128, 2, 2, 4>(sa, sb, M, nseg * c->d, c->d, epi, s);
+    launch_gemm<T, 128, 128, 2, 2, 4>(sa, sb, M, nseg * c->d, c->d, epi, s, PROF_PROJ);
   else
-    launch_gemm<T, 128, 128, 4, 1, 4>(sa, sb, M, nseg * c->d, c->d, epi, s);
+    launch_gemm<T, 128, 128, 4, 1, 4>(sa, sb, M, nseg * c->d, c->d, epi, s, PROF_PROJ);
 }
 
 template <typename T>
@@ -83,22 +120,18 @@ template <typename T, int DH>
 void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N, const T* o, const float* ssq,
                 const T* kraw, const T* vraw, const float* glogx, const float* sig, const float* cos,
                 const float* sin, T* Kout, T* Vout, long out_stride, int out_row0, T* vin, float* gvu,
-                float* save1, float* save2, T* uout, hipStream_t s) {
+                float* save1, float* save2, hipStream_t s) {
   const T* normw = (const T*)w->norm_ctx_w;
-  SrcRms<T> sa{o, c->d, N, ssq, c->h, normw, 1.0f / (float)c->d, c->rms_eps, uout};
+  SrcRowsRs<T> sa{o, c->d, N, ssq, c->h, 1.0f / (float)c->d, c->rms_eps};
   SrcRows<T> sb{(const T*)w->w_sweep, c->d, 4 * c->d};
   EpiSweep1<T, DH> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
                       Kout, Vout, out_stride, out_row0, vin, gvu, save1};
-  {
-    ProfScope ps(PROF_SWEEP1, s);
-    launch_gemm<T, 64, 64, 4, 1, 4>(sa, sb, N, 4 * c->d, c->d, e1, s);
-  }
+  launch_gemm<T, 64, 64, 4, 1, 4>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
   if (c->ctx_mod != DM_CTX_LINEAR) {
     SrcRows<T> av{vin, c->d, N};
     SrcRows<T> bv{(const T*)w->w_vctx, c->d, c->d};
     EpiSweep2<T, DH> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2};
-    ProfScope ps(PROF_SWEEP2, s);
-    launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, c->d, c->d, e2, s);
+    launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, c->d, c->d, e2, s, PROF_SWEEP2);
   }
 }
 
@@ -112,8 +145,7 @@ int run_comm(const CellGeom& g, const T* qr, const T* Kc, const T* Vc, float sca
   const int BH = g.B * g.h;
   CommArgs<T> ca{g, qr, Kc, Vc, cp.split_len, scale, ws.Ap, ws.Zp, ws.Mp};
   if (cp.nsplit == 1) { ca.A = ws.A; ca.Z = ws.Z; ca.Mx = ws.M; }
-  ProfScope ps(PROF_COMM, s);
-  hipLaunchKernelGGL((k_comm_partial<T, DH>), dim3(cp.nsplit, BH), dim3(256), 0, s, ca);
+  launch_k(PROF_COMM, k_comm_partial<T, DH>, dim3(cp.nsplit, BH), dim3(256), 0, s, ca);
   return cp.nsplit;
 }
 
@@ -147,7 +179,7 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
     else { Kin = Kc; Vin = Vc; in_stride = cache_stride; in_row0 = pos0; }
     // rows written by this sweep's refine
     T* Kout; T* Vout; long out_stride; int out_row0;
-    if (sv) { Kout = sv->Kin + (sw + 1) * slot; Vout = sv->Vin + (sw + 1) * slot; out_stride = ws_stride; out_row0 = 0; }
+    if (sv && !(last && sv->last_to_cache)) { Kout = sv->Kin + (sw + 1) * slot; Vout = sv->Vin + (sw + 1) * slot; out_stride = ws_stride; out_row0 = 0; }
     else { Kout = Kc; Vout = Vc; out_stride = cache_stride; out_row0 = pos0; }
 
     T* o = sv ? sv->o + sw * NS * d : (T*)ws.o;
@@ -157,14 +189,11 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
                      scale, o, ssq, last ? ocat : nullptr, last ? o_last : nullptr,
                      sv ? sv->stat_m + sw * (size_t)BH * CMAX : nullptr,
                      sv ? sv->stat_z + sw * (size_t)BH * CMAX : nullptr};
-    {
-      ProfScope ps(PROF_ATTEND, s);
-      hipLaunchKernelGGL((k_attend<T, DH>), dim3(BH), dim3(256), 0, s, aa);
-    }
+    launch_k(PROF_ATTEND, k_attend<T, DH>, dim3(BH), dim3(256), 0, s, aa);
     T* vin = sv ? sv->vin + sw * NS * d : (T*)ws.vin;
     run_refine<T, DH>(c, w, g, N, o, ssq, kraw, vraw, L->glogx, L->sig, cos, sin, Kout, Vout, out_stride,
                       out_row0, vin, ws.gvu, sv ? sv->save1 + sw * NS * 4 * d : nullptr,
-                      sv ? sv->save2 + sw * NS * d : nullptr, sv ? sv->u + sw * NS * d : nullptr, s);
+                      sv ? sv->save2 + sw * NS * d : nullptr, s);
   }
 }
 

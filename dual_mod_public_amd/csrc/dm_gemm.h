@@ -9,7 +9,7 @@
 //
 // Operand sources describe a logical row-major [rows x K] operand:
 //   SrcRows   element (r, k) at p[r*ld + k]   (K contiguous; 16-byte vector loads along k)
-//   SrcRms    SrcRows scaled on the way into LDS: u = o * rs[r] * w[k]  (RMSNorm of o)
+//   SrcRowsRs SrcRows plus per-row RMS scales staged in LDS for the epilogue
 //   SrcKMajor element (r, k) at p[k*ld + r]   (rows contiguous; vectors along r,
 //                                              transposed on the way into LDS)
 // After the k-loop the epilogue functor receives the wave's accumulators:
@@ -17,6 +17,8 @@
 // wave tile, so head-aligned wave tiles keep RoPE pairs and gate/candidate
 // columns in one lane.
 #pragma once
+
+#include <type_traits>
 
 #include "dm_common.h"
 
@@ -48,50 +50,40 @@ template <typename T> struct SrcRows {
   DM_DEV uint4 xform(uint4 v, int, int, const float*, int) const { return v; }
 };
 
-constexpr int RMS_MAXR = 128;     // row-scale slots in LDS (>= BM of any RMS-sourced GEMM)
-constexpr int RMS_MAXK = 4096;    // norm-weight elements staged in LDS (>= K of any RMS-sourced GEMM)
+constexpr int RMS_MAXR = 128;     // row-scale slots in LDS (>= BM of any row-scaled GEMM)
+constexpr int RMS_MAXK = 4096;    // largest d_model the row scales are built for
 
-// u[r, k] = o[r, k] * rs[r] * w[k], rs = rsqrt(sum_p ssq[r, p] / d + eps); o in storage dtype.
-template <typename T> struct SrcRms {
+// Row-major operand whose rows carry an RMS scale for the epilogue:
+// rs[r] = rsqrt(sum_p ssq[r, p] * inv_d + eps) is staged in LDS before the k-loop
+// (prepare_load issues the ssq loads ahead of the operand ring, prepare_store
+// writes LDS) and handed to the epilogue. The operand itself is loaded unchanged:
+// RMSNorm(o) . W^T = rs * (o . (W diag(w))^T) with the norm weight w folded into
+// the packed weights.
+template <typename T> struct SrcRowsRs {
   static constexpr bool KMAJOR = false;
   const T* __restrict__ p;           // o [rows, ld]
   long ld;
   int rows;
   const float* __restrict__ ssq;     // [rows, nparts] partial sums of squares
   int nparts;
-  const T* __restrict__ w;           // norm weight [K]
   float inv_d, eps;
-  T* __restrict__ uout;              // optional: u rows [rows, ld] written by the blocks of column 0
-  // per-row scales of the tile's rows into rs_lds[0..R), the norm weight into w_lds[0..K)
-  template <int R> DM_DEV void prepare_rows(int r0, float* rs_lds, T* w_lds, int K) const {
-    for (int i = threadIdx.x; i < R; i += 256) {
-      const int r = r0 + i;
-      float s = 0.f;
-      if (r < rows)
-        for (int q = 0; q < nparts; ++q) s += ssq[(long)r * nparts + q];
-      rs_lds[i] = rsqrtf(s * inv_d + eps);
-    }
-    constexpr int V = GemmTraits<T>::VEC;
-    for (int i = threadIdx.x * V; i < K; i += 256 * V)
-      *reinterpret_cast<uint4*>(w_lds + i) = *reinterpret_cast<const uint4*>(w + i);
+  struct Pre {
+    float s;
+  };
+  template <int R> DM_DEV Pre prepare_load(int r0, int) const {
+    Pre pr;
+    pr.s = 0.f;
+    const int r = min(r0 + (int)(threadIdx.x % R), rows - 1);
+    for (int q = 0; q < nparts; ++q) pr.s += ssq[(long)r * nparts + q];
+    return pr;
+  }
+  template <int R> DM_DEV void prepare_store(const Pre& pr, float* rs_lds, T*, int) const {
+    if (threadIdx.x < R) rs_lds[threadIdx.x] = rsqrtf(pr.s * inv_d + eps);
   }
   DM_DEV uint4 load(int r, int k) const {
     return *reinterpret_cast<const uint4*>(p + (long)min(r, rows - 1) * ld + k);
   }
-  DM_DEV uint4 xform(uint4 v, int rloc, int k, const float* rs_lds, int r0) const {
-    constexpr int V = GemmTraits<T>::VEC;
-    float f[V], wf[V];
-    unpack16<T>(v, f);
-    const T* w_lds = reinterpret_cast<const T*>(rs_lds + RMS_MAXR);
-    unpack16<T>(*reinterpret_cast<const uint4*>(w_lds + k), wf);
-    const float r = rs_lds[rloc];
-#pragma unroll
-    for (int j = 0; j < V; ++j) f[j] = f[j] * r * wf[j];
-    const uint4 u = pack16<T>(f);
-    if (uout != nullptr && blockIdx.x == 0 && r0 + rloc < rows)
-      *reinterpret_cast<uint4*>(uout + (long)(r0 + rloc) * ld + k) = u;
-    return u;
-  }
+  DM_DEV uint4 xform(uint4 v, int, int, const float*, int) const { return v; }
 };
 
 template <typename T> struct SrcKMajor {
@@ -107,13 +99,21 @@ template <typename T> struct SrcKMajor {
 };
 
 template <class S> struct requires_prepare { static constexpr bool value = false; };
-template <typename T> struct requires_prepare<SrcRms<T>> { static constexpr bool value = true; };
+template <typename T> struct requires_prepare<SrcRowsRs<T>> { static constexpr bool value = true; };
+struct NoPre {};
+template <class S> struct PrepOf { using type = NoPre; };
+template <typename T> struct PrepOf<SrcRowsRs<T>> { using type = typename SrcRowsRs<T>::Pre; };
 
-// 2 operand stages + (RMS sources) row scales and the norm weight
+// Epilogues may prefetch their own global inputs before the k-loop: an EPI with a
+// member type Pre provides pre = epi.prefetch(row0, col0) and
+// epi.apply(acc, row0, col0, rs, pre); otherwise epi(acc, row0, col0, rs) is called.
+template <class E, class = void> struct has_prefetch { static constexpr bool value = false; };
+template <class E> struct has_prefetch<E, std::void_t<typename E::Pre>> { static constexpr bool value = true; };
+
+// 2 operand stages + the row scales
 template <typename T, int BM, int BN, bool RMS>
 constexpr int gemm_lds_bytes() {
-  return 2 * (BM + BN) * GemmTraits<T>::LDK * (int)sizeof(T) +
-         (RMS ? RMS_MAXR * 4 + RMS_MAXK * (int)sizeof(T) : BM * 4);
+  return 2 * (BM + BN) * GemmTraits<T>::LDK * (int)sizeof(T) + (RMS ? RMS_MAXR * 4 : BM * 4);
 }
 
 // Wave tile geometry of a (BM, BN, WM, WN) block.
@@ -223,6 +223,15 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
   };
 
   const int nk = (K + BK - 1) / BK;   // a partial last tile needs k-bounded sources
+  constexpr bool RMS = requires_prepare<SA>::value;
+  typename PrepOf<SA>::type pre{};
+  if constexpr (RMS) pre = sa.template prepare_load<BM>(m0, K);
+  auto prepare_store = [&]() {
+    if constexpr (RMS) {
+      sa.template prepare_store<BM>(pre, rs_lds, reinterpret_cast<T*>(rs_lds + RMS_MAXR), K);
+      __syncthreads();
+    }
+  };
   if (nk >= D && nk % D == 0) {
     // Software pipeline with no data-dependent branches around the loads: the
     // steady state always prefetches tile kt + D (it exists), the last D tiles run
@@ -230,6 +239,7 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
     // for the oldest ring slot.
 #pragma unroll
     for (int s = 0; s < D; ++s) gload(s, ra[s], rb[s]);
+    prepare_store();
     sstore(0, buf[0], ra[0], rb[0]);
     __syncthreads();
     for (int kt0 = 0; kt0 < nk - D; kt0 += D) {
@@ -253,6 +263,7 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
     // short or ragged K: one tile at a time
     for (int kt = 0; kt < nk; ++kt) {
       gload(kt, ra[0], rb[0]);
+      if (kt == 0) prepare_store();
       sstore(kt, buf[0], ra[0], rb[0]);
       __syncthreads();
       compute(buf[0]);
@@ -264,27 +275,31 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
 // Generic kernel: zero accumulators, k-loop, epilogue on the wave's registers.
 // epi(acc, row0, col0) with row0/col0 the global origin of the wave tile.
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
-__global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi) {
+__global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint64_t* prof_ts) {
+  const uint64_t t0 = prof_begin(prof_ts);
   using WT = WaveTile<BM, BN, WM, WN>;
   constexpr bool RMS = requires_prepare<SA>::value;
   __shared__ __attribute__((aligned(16))) char smem[gemm_lds_bytes<T, BM, BN, RMS>()];
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  if constexpr (RMS) {
-    static_assert(BM <= RMS_MAXR, "row-scale slots");
-    float* rs = reinterpret_cast<float*>(smem + 2 * (BM + BN) * GemmTraits<T>::LDK * sizeof(T));
-    sa.template prepare_rows<BM>(m0, rs, reinterpret_cast<T*>(rs + RMS_MAXR), K);
-    __syncthreads();
-  }
+  static_assert(!RMS || BM <= RMS_MAXR, "row-scale slots");
+  const int wave = threadIdx.x >> 6;
+  const int row0 = m0 + (wave / WN) * WT::TM, col0 = n0 + (wave % WN) * WT::TN;
+  const float* rs = reinterpret_cast<const float*>(smem + 2 * (BM + BN) * GemmTraits<T>::LDK * sizeof(T)) +
+                    (wave / WN) * WT::TM;
   floatx4 acc[WT::FM][WT::FN];
 #pragma unroll
   for (int i = 0; i < WT::FM; ++i)
 #pragma unroll
     for (int j = 0; j < WT::FN; ++j) acc[i][j] = zero4();
-  gemm_mainloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc);
-  const int wave = threadIdx.x >> 6;
-  epi(acc, m0 + (wave / WN) * WT::TM, n0 + (wave % WN) * WT::TN,
-      reinterpret_cast<const float*>(smem + 2 * (BM + BN) * GemmTraits<T>::LDK * sizeof(T)) +
-          (wave / WN) * WT::TM);
+  if constexpr (has_prefetch<EPI>::value) {
+    const typename EPI::Pre pre = epi.prefetch(row0, col0);
+    gemm_mainloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc);
+    epi.apply(acc, row0, col0, rs, pre);
+  } else {
+    gemm_mainloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc);
+    epi(acc, row0, col0, rs);
+  }
+  prof_end(prof_ts, t0);
 }
 
 }  // namespace dm

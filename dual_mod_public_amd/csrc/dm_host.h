@@ -109,9 +109,13 @@ struct Carver {
 
 // GEMM launch: grid (N/BN, ceil(M/BM)), 256 threads
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
-void launch_gemm(const SA& sa, const SB& sb, int M, int N, int K, const EPI& epi, hipStream_t s) {
+void launch_gemm(const SA& sa, const SB& sb, int M, int N, int K, const EPI& epi, hipStream_t s,
+                 int prof_cls = PROF_NONE) {
   dim3 grid(N / BN, cdiv(M, BM));
-  hipLaunchKernelGGL((k_gemm<T, BM, BN, WM, WN, D, SA, SB, EPI>), grid, dim3(256), 0, s, sa, sb, K, epi);
+  uint64_t* ts;
+  const int idx = prof_launch_begin(prof_cls, s, true, ts);
+  hipLaunchKernelGGL((k_gemm<T, BM, BN, WM, WN, D, SA, SB, EPI>), grid, dim3(256), 0, s, sa, sb, K, epi, ts);
+  prof_launch_end(idx, s);
 }
 
 }  // namespace dm

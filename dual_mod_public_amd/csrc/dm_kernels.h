@@ -95,6 +95,55 @@ static __global__ __launch_bounds__(256) void k_transpose16(const T* __restrict_
   }
 }
 
+// W[r, k] *= w[k] (in place)
+template <typename T>
+static __global__ __launch_bounds__(256) void k_scale_cols(T* __restrict__ W, const T* __restrict__ w, int rows,
+                                                           int cols) {
+  const long i = blockIdx.x * 256L + threadIdx.x;
+  if (i < (long)rows * cols) W[i] = from_f<T>(to_f(W[i]) * to_f(w[i % cols]));
+}
+
+// out[k, col0_out + r] = in[r, k] * rs[r] * w[k] with rs[r] = rsqrt(sum_p ssq[r, p] * inv_d + eps):
+// the transposed RMSNorm output u^T of the stacked sweeps (the weight-grad GEMM operand),
+// 64x64 tiles; output columns [rows, rows_pad) zero-filled.
+template <typename T>
+static __global__ __launch_bounds__(256) void k_transpose_rms16(const T* __restrict__ in, long ld_in, int rows,
+                                                                int cols, int rows_pad, const float* __restrict__ ssq,
+                                                                int nparts, const T* __restrict__ w, float inv_d,
+                                                                float eps, T* __restrict__ out, long ld_out) {
+  constexpr int V = 16 / (int)sizeof(T);
+  __shared__ float tile[64][64 + 1];
+  __shared__ float rs[64];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  if (threadIdx.x < 64) {
+    const int r = min(r0 + (int)threadIdx.x, rows - 1);
+    float s = 0.f;
+    for (int q = 0; q < nparts; ++q) s += ssq[(long)r * nparts + q];
+    rs[threadIdx.x] = rsqrtf(s * inv_d + eps);
+  }
+  __syncthreads();
+  for (int v = threadIdx.x; v < 64 * 64 / V; v += 256) {
+    const int r = v / (64 / V), cc = (v % (64 / V)) * V;
+    if (r0 + r < rows && c0 + cc < cols) {
+      float f[V], wf[V];
+      unpack16<T>(*reinterpret_cast<const uint4*>(in + (long)(r0 + r) * ld_in + c0 + cc), f);
+      unpack16<T>(*reinterpret_cast<const uint4*>(w + c0 + cc), wf);
+#pragma unroll
+      for (int j = 0; j < V; ++j) tile[r][cc + j] = f[j] * rs[r] * wf[j];
+    }
+  }
+  __syncthreads();
+  for (int v = threadIdx.x; v < 64 * 64 / V; v += 256) {
+    const int cc = v / (64 / V), r = (v % (64 / V)) * V;
+    if (r0 + r < rows_pad && c0 + cc < cols) {
+      float f[V];
+#pragma unroll
+      for (int j = 0; j < V; ++j) f[j] = (r0 + r + j < rows) ? tile[r + j][cc] : 0.f;
+      *reinterpret_cast<uint4*>(out + (long)(c0 + cc) * ld_out + r0 + r) = pack16<T>(f);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // row RMSNorm (attn_norm, models/dualmod/attention.py:74-83): one wave per row
 // ---------------------------------------------------------------------------
@@ -466,115 +515,124 @@ template <typename T, int DH> struct EpiSweep1 {
   T* __restrict__ vin; float* __restrict__ gvu;
   float* __restrict__ save;
 
-  // All global loads of the lane are issued before any store (gather, then
-  // compute + scatter): the outputs may alias nothing, but the compiler cannot
-  // know that, and interleaving would serialise a memory latency per element.
+  // The epilogue's global inputs are gathered first (prefetch), then combined with
+  // the accumulators and stored (apply): all loads precede all stores, so the
+  // compiler never serialises a memory latency per element on possible aliasing.
+  // (Gathering before the k-loop instead costs occupancy and was measured slower.)
+  struct PreData {
+    float f[4][10];   // per row q: K path gx_a, gx_b, kraw_a, kraw_b, cos, sin;
+                      //   linear V: gx x2, v_raw x2; v_map: sig x4, o x4, + norm weight x4 (f[..][8..])
+  };
+  DM_DEV PreData prefetch(int row0, int col0) const {
+    PreData pr;
+    const int lane = threadIdx.x & 63, lc = lane & 15;
+    const int d = g.d, h = g.h;
+    const int mq0 = row0 + 4 * (lane >> 4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int m = min(mq0 + q, M - 1);
+      const int b = m / g.c, p = m - b * g.c;
+      const int t = g.buf_t0 + p, pos = g.pos0 + p;
+      const long xrow = (long)b * g.Tbuf + t;
+      if (col0 < 2 * d) {
+        const int hd = col0 / (2 * DH), jj = 16 * ((col0 % (2 * DH)) / 64) + lc;
+        const float* gx = glogx + xrow * 2 * d + hd * DH;
+        const long lrow = (((long)b * h + hd) * g.Tbuf + t) * DH;
+        pr.f[q][0] = gx[jj];
+        pr.f[q][1] = gx[jj + DH / 2];
+        pr.f[q][2] = to_f(kraw[lrow + jj]);
+        pr.f[q][3] = to_f(kraw[lrow + jj + DH / 2]);
+        pr.f[q][4] = cos[(long)pos * (DH / 2) + jj];
+        pr.f[q][5] = sin[(long)pos * (DH / 2) + jj];
+      } else if (ctx_mod == 0) {
+        const int cl = col0 - 2 * d;
+        const int hd = cl / (2 * DH), e0 = 32 * ((cl % (2 * DH)) / 64);
+        const float* gx = glogx + xrow * 2 * d + d + hd * DH;
+        const long lrow = (((long)b * h + hd) * g.Tbuf + t) * DH;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          pr.f[q][j] = gx[e0 + 16 * j + lc];
+          pr.f[q][2 + j] = to_f(vraw[lrow + e0 + 16 * j + lc]);
+        }
+      } else if (col0 < 3 * d) {
+        const int c0 = col0 - 2 * d;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int col = c0 + 16 * j + lc;
+          pr.f[q][j] = sig[xrow * d + col];
+          pr.f[q][4 + j] = ctx_mod == 1 ? to_f(o[(long)m * d + col]) : 0.f;
+          pr.f[q][8 + (j & 1)] = 0.f;
+        }
+      }
+    }
+    if (col0 >= 2 * d && col0 < 3 * d && ctx_mod != 0) {   // norm weight of the 4 columns, in f[0][8..9], f[1][8..9]
+      const int c0 = col0 - 2 * d;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pr.f[j >> 1][8 + (j & 1)] = to_f(normw[c0 + 16 * j + lc]);
+    }
+    return pr;
+  }
+
   template <int FM, int FN>
   DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float* rs) const {
+    apply(acc, row0, col0, rs, prefetch(row0, col0));
+  }
+
+  template <int FM, int FN>
+  DM_DEV void apply(const floatx4 (&acc)[FM][FN], int row0, int col0, const float* rs, const PreData& pr) const {
     static_assert(FM == 1 && FN == 4, "sweep GEMM 1 wave tile is 16 x 64");
     const int lane = threadIdx.x & 63, lc = lane & 15;
     const int d = g.d, h = g.h;
     const int mq0 = row0 + 4 * (lane >> 4);
-    int bq[4], pq[4];
-    bool ok[4];
+    // the GEMM ran on o with norm_ctx.weight folded into W: u . W^T = rs * acc
+    floatx4 a[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int m = mq0 + q;
-      ok[q] = m < M;
-      bq[q] = ok[q] ? m / g.c : 0;
-      pq[q] = ok[q] ? m - bq[q] * g.c : 0;
-    }
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[j][q] = acc[0][j][q] * rs[4 * (lane >> 4) + q];
     if (save != nullptr) {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        if (ok[q])
+        if (mq0 + q < M)
 #pragma unroll
-          for (int j = 0; j < FN; ++j) save[(long)(mq0 + q) * 4 * d + col0 + 16 * j + lc] = acc[0][j][q];
+          for (int j = 0; j < FN; ++j) save[(long)(mq0 + q) * 4 * d + col0 + 16 * j + lc] = a[j][q];
     }
-    if (col0 < 2 * d) {
-      const int hd = col0 / (2 * DH), jj = 16 * ((col0 % (2 * DH)) / 64) + lc;
-      float gxa[4], gxb[4], kra[4], krb[4], cs[4], sn[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int t = g.buf_t0 + pq[q], pos = g.pos0 + pq[q];
-        const float* gx = glogx + ((long)bq[q] * g.Tbuf + t) * 2 * d + hd * DH;
-        const long lrow = (((long)bq[q] * h + hd) * g.Tbuf + t) * DH;
-        gxa[q] = gx[jj];
-        gxb[q] = gx[jj + DH / 2];
-        kra[q] = to_f(kraw[lrow + jj]);
-        krb[q] = to_f(kraw[lrow + jj + DH / 2]);
-        cs[q] = cos[(long)pos * (DH / 2) + jj];
-        sn[q] = sin[(long)pos * (DH / 2) + jj];
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (!ok[q]) continue;
-        const float ga = sigmoidf_(gxa[q] + acc[0][2][q]);
-        const float gb = sigmoidf_(gxb[q] + acc[0][3][q]);
-        const float k1 = ga * kra[q] + (1.f - ga) * acc[0][0][q];
-        const float k2 = gb * krb[q] + (1.f - gb) * acc[0][1][q];
-        const long crow = ((long)bq[q] * h + hd) * out_stride + (long)(out_row0 + pq[q]) * DH;
-        Kout[crow + jj] = from_f<T>(k1 * cs[q] - k2 * sn[q]);
-        Kout[crow + jj + DH / 2] = from_f<T>(k2 * cs[q] + k1 * sn[q]);
-      }
-    } else if (ctx_mod == 0) {
-      const int cl = col0 - 2 * d;
-      const int hd = cl / (2 * DH), e0 = 32 * ((cl % (2 * DH)) / 64);
-      float gxv[4][2], vr[4][2];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int t = g.buf_t0 + pq[q];
-        const float* gx = glogx + ((long)bq[q] * g.Tbuf + t) * 2 * d + d + hd * DH;
-        const long lrow = (((long)bq[q] * h + hd) * g.Tbuf + t) * DH;
+    for (int q = 0; q < 4; ++q) {
+      const int m = mq0 + q;
+      if (m >= M) continue;
+      const int b = m / g.c, p = m - b * g.c;
+      if (col0 < 2 * d) {
+        const int hd = col0 / (2 * DH), jj = 16 * ((col0 % (2 * DH)) / 64) + lc;
+        const float ga = sigmoidf_(pr.f[q][0] + a[2][q]);
+        const float gb = sigmoidf_(pr.f[q][1] + a[3][q]);
+        const float k1 = ga * pr.f[q][2] + (1.f - ga) * a[0][q];
+        const float k2 = gb * pr.f[q][3] + (1.f - gb) * a[1][q];
+        const long crow = ((long)b * h + hd) * out_stride + (long)(out_row0 + p) * DH;
+        Kout[crow + jj] = from_f<T>(k1 * pr.f[q][4] - k2 * pr.f[q][5]);
+        Kout[crow + jj + DH / 2] = from_f<T>(k2 * pr.f[q][4] + k1 * pr.f[q][5]);
+      } else if (ctx_mod == 0) {
+        const int cl = col0 - 2 * d;
+        const int hd = cl / (2 * DH), e0 = 32 * ((cl % (2 * DH)) / 64);
+        const long crow = ((long)b * h + hd) * out_stride + (long)(out_row0 + p) * DH;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          gxv[q][j] = gx[e0 + 16 * j + lc];
-          vr[q][j] = to_f(vraw[lrow + e0 + 16 * j + lc]);
+          const float gv = sigmoidf_(pr.f[q][j] + a[j + 2][q]);
+          Vout[crow + e0 + 16 * j + lc] = from_f<T>(gv * pr.f[q][2 + j] + (1.f - gv) * a[j][q]);
         }
-      }
+      } else if (col0 < 3 * d) {
+        const int c0 = col0 - 2 * d;
+        const float r = rs[4 * (lane >> 4) + q];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (!ok[q]) continue;
-        const long crow = ((long)bq[q] * h + hd) * out_stride + (long)(out_row0 + pq[q]) * DH;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const float gv = sigmoidf_(gxv[q][j] + acc[0][j + 2][q]);
-          Vout[crow + e0 + 16 * j + lc] = from_f<T>(gv * vr[q][j] + (1.f - gv) * acc[0][j][q]);
-        }
-      }
-    } else {
-      const int c0 = col0 - 2 * d;   // column in [0, 2d)
-      if (c0 < d) {
-        float sg[4][FN], ov[4][FN], nw[FN];
-#pragma unroll
-        for (int j = 0; j < FN; ++j) nw[j] = to_f(normw[c0 + 16 * j + lc]);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const long xrow = (long)bq[q] * g.Tbuf + g.buf_t0 + pq[q];
-#pragma unroll
-          for (int j = 0; j < FN; ++j) {
-            const int col = c0 + 16 * j + lc;
-            sg[q][j] = sig[xrow * d + col];
-            ov[q][j] = ctx_mod == 1 ? to_f(o[(long)(ok[q] ? mq0 + q : 0) * d + col]) : 0.f;
-          }
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (!ok[q]) continue;
-          const float r = rs[4 * (lane >> 4) + q];
-#pragma unroll
-          for (int j = 0; j < FN; ++j) {
-            float v = sg[q][j] * tanhf_(acc[0][j][q]);
-            if (ctx_mod == 1) v += lam * (ov[q][j] * r * nw[j]);
-            vin[(long)(mq0 + q) * d + c0 + 16 * j + lc] = from_f<T>(v);
-          }
+        for (int j = 0; j < FN; ++j) {
+          float v = pr.f[q][j] * tanhf_(a[j][q]);
+          if (ctx_mod == 1) v += lam * (pr.f[q][4 + j] * r * pr.f[j >> 1][8 + (j & 1)]);
+          vin[(long)m * d + c0 + 16 * j + lc] = from_f<T>(v);
         }
       } else {
+        const int c0 = col0 - 3 * d;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (ok[q])
-#pragma unroll
-            for (int j = 0; j < FN; ++j) gvu[(long)(mq0 + q) * d + c0 - d + 16 * j + lc] = acc[0][j][q];
+        for (int j = 0; j < FN; ++j) gvu[(long)m * d + c0 + 16 * j + lc] = a[j][q];
       }
     }
   }

@@ -105,7 +105,14 @@ int dm_pack_weights(const dm_config* c, const dm_params* p, const dm_packed* out
   };
   const int nproj = mult ? 6 : 5;
   tr(out->w_proj, out->w_proj_t, nproj * d, d);
-  tr(out->w_sweep, out->w_sweep_t, 4 * d, d);
+  tr(out->w_sweep, out->w_sweep_t, 4 * d, d);   // unscaled rows: the backward's du = dctx . W
+  // fold norm_ctx.weight into the forward's packed rows: W[:, k] *= w[k]
+  if (c->dtype == DM_BF16)
+    hipLaunchKernelGGL(k_scale_cols<bf16>, dim3(cdiv((long)4 * d * d, 256)), dim3(256), 0, s, (bf16*)out->w_sweep,
+                       (const bf16*)p->norm_ctx_w, 4 * d, d);
+  else
+    hipLaunchKernelGGL(k_scale_cols<float>, dim3(cdiv((long)4 * d * d, 256)), dim3(256), 0, s, (float*)out->w_sweep,
+                       (const float*)p->norm_ctx_w, 4 * d, d);
   if (mult) tr(p->w_vctx, out->w_vctx_t, d, d);
   tr(p->wo, out->wo_t, d, d);
   DM_HIP(hipGetLastError());
@@ -194,22 +201,58 @@ int dm_check_schedule(const int32_t* sched, int32_t n_cells, int32_t T) {
   return DM_OK;
 }
 
+size_t dm_layer_tape_bytes(const dm_config* c, const int32_t* sched, int32_t n_cells) {
+  if (check_cfg(c) != DM_OK || sched == nullptr || n_cells <= 0) return 0;
+  return c->dtype == DM_BF16 ? tape_offsets<bf16>(c, sched, n_cells)[n_cells]
+                             : tape_offsets<float>(c, sched, n_cells)[n_cells];
+}
+
 int dm_layer_fwd(const dm_config* c, const dm_packed* w, const void* x, void* y, const float* cos,
                  const float* sin, const dm_layer_bufs* L, const int32_t* sched, int32_t n_cells,
-                 void* K_cache, void* V_cache, int32_t cache_T, void* ocat, void* workspace,
-                 size_t workspace_bytes, void* stream) {
+                 void* K_cache, void* V_cache, int32_t cache_T, void* ocat, void* tape, size_t tape_bytes,
+                 void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_cfg(c);
   if (rc) return rc;
   if ((rc = check_packed(c, w)) || (rc = check_bufs(c, L))) return rc;
   DM_REQUIRE(x && y && ocat, DM_ERR_INVALID, "null x/y/ocat");
   if ((rc = dm_check_schedule(sched, n_cells, L->T))) return rc;
   DM_REQUIRE(L->T <= cache_T, DM_ERR_INVALID, "T=%d > cache_T=%d", L->T, cache_T);
+  if (tape != nullptr) {
+    DM_REQUIRE(tape_bytes >= dm_layer_tape_bytes(c, sched, n_cells), DM_ERR_WORKSPACE, "tape %zu < %zu bytes",
+               tape_bytes, dm_layer_tape_bytes(c, sched, n_cells));
+    DM_REQUIRE(aligned16(tape), DM_ERR_INVALID, "tape must be 16-byte aligned");
+  }
   ProfScope whole(PROF_LAYER, S(stream));
   if ((rc = dm_layer_proj(c, w, x, cos, sin, L, stream))) return rc;
-  for (int i = 0; i < n_cells; ++i) {
-    dm_cell_args a{sched[3 * i], sched[3 * i + 1], sched[3 * i + 2], cache_T, K_cache, V_cache, ocat,
-                   nullptr, workspace, workspace_bytes};
-    if ((rc = dm_cell_fwd(c, w, L, cos, sin, &a, stream))) return rc;
+  if (tape == nullptr) {
+    for (int i = 0; i < n_cells; ++i) {
+      dm_cell_args a{sched[3 * i], sched[3 * i + 1], sched[3 * i + 2], cache_T, K_cache, V_cache, ocat,
+                     nullptr, workspace, workspace_bytes};
+      if ((rc = dm_cell_fwd(c, w, L, cos, sin, &a, stream))) return rc;
+    }
+  } else {
+    DM_REQUIRE(K_cache && V_cache && aligned16(K_cache) && aligned16(V_cache), DM_ERR_INVALID,
+               "K/V cache must be non-null and 16-byte aligned");
+    const CellWs need = carve_cell(c, cache_T, nullptr);
+    DM_REQUIRE(workspace && workspace_bytes >= need.bytes, DM_ERR_WORKSPACE, "workspace %zu < %zu bytes",
+               workspace_bytes, need.bytes);
+    const CellWs ws = carve_cell(c, cache_T, workspace);
+    auto run = [&](auto tag) {
+      using T = decltype(tag);
+      const std::vector<size_t> off = tape_offsets<T>(c, sched, n_cells);
+      for (int i = 0; i < n_cells; ++i) {
+        const int pos0 = sched[3 * i], cc = sched[3 * i + 1], K = sched[3 * i + 2];
+        Carver cv(static_cast<char*>(tape) + off[i]);
+        const CellSave<T> sv = carve_save<T>(c, (size_t)c->B * cc, K, true, pos0 > 0, cv);
+        CellWs cws = ws;
+        if (sv.Mx) cws.M = sv.Mx;   // the committed row max is part of the saved state
+        run_cell_dispatch<T>(c, w, L, cos, sin, pos0, cc, K, pos0, L->T, K_cache, V_cache, cache_T, ocat,
+                             nullptr, cws, &sv, S(stream));
+      }
+    };
+    if (c->dtype == DM_BF16) run(bf16{});
+    else run(float{});
+    DM_HIP(hipGetLastError());
   }
   return dm_linear(c->dtype, ocat, w->wo, (c->flags & DM_FLAG_NO_RESIDUAL) ? nullptr : x, y, c->B * L->T,
                    c->d, c->d, stream);
@@ -260,22 +303,21 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
   const int nsplit = pos > lo ? cdiv(pos - lo, DEC_SPLIT) : 0;
   DecodeArgs<T> da{B, h, d, a->tape_T, pos, lo, DEC_SPLIT, nsplit, 1.0f / sqrtf((float)DH),
                    (const T*)ws.q, (const T*)ws.kself, (const T*)ws.vraw, (const T*)a->K_tape,
-                   (const T*)a->V_tape, ws.part, ws.o, ws.ssq, (T*)a->o_cat};
+                   (const T*)a->V_tape, ws.part, ws.o, ws.ssq, (T*)a->o_cat, nullptr};
   if (nsplit > 0) {
-    ProfScope ps(PROF_DEC_READ, s);
+    const int idx = prof_launch_begin(PROF_DEC_READ, s, true, da.prof_ts);
     hipLaunchKernelGGL((k_decode_partial<T, DH, DEC_SPLIT>), dim3(nsplit, B * h), dim3(256), 0, s, da);
+    prof_launch_end(idx, s);
+    da.prof_ts = nullptr;
   }
-  {
-    ProfScope ps(PROF_DEC_MERGE, s);
-    hipLaunchKernelGGL((k_decode_merge<T, DH>), dim3(B * h), dim3(64), 0, s, da);
-  }
+  launch_k(PROF_DEC_MERGE, k_decode_merge<T, DH>, dim3(B * h), dim3(64), 0, s, da);
 
   // refine_kv for the B rows (c = 1, position pos), write slot pos of the tape
   CellGeom g{B, 1, d, h, DH, pos, 0, 1, a->tape_T};
   ProfScope pr(PROF_DEC_REFINE, s);
   run_refine<T, DH>(c, w, g, B, (const T*)a->o_cat, ws.ssq, (const T*)ws.kraw, (const T*)ws.vraw, ws.glogx,
                     ws.sig, cos, sin, (T*)a->K_tape, (T*)a->V_tape, (long)a->tape_T * DH, pos, (T*)ws.vin,
-                    ws.gvu, nullptr, nullptr, nullptr, s);
+                    ws.gvu, nullptr, nullptr, s);
   if (a->y != nullptr) {
     SrcRows<T> ao{(const T*)a->o_cat, d, B};
     SrcRows<T> bo{(const T*)w->wo, d, d};
@@ -389,6 +431,11 @@ int dm_gemm(int32_t dtype, int32_t trans_a, int32_t trans_b, const void* A, cons
 }  // extern "C"
 
 // ---- optional per-kernel-class timing --------------------------------------------
+static __global__ void k_prof_init(uint64_t* ts, long n) {
+  const long i = blockIdx.x * 256L + threadIdx.x;
+  if (i < n) ts[i] = ((i / dm::PROF_SLOTS) % 2 == 0) ? ~0ull : 0ull;
+}
+
 extern "C" {
 
 int dm_prof_start(int32_t kernel_class, int32_t max_launches) {
@@ -402,6 +449,20 @@ int dm_prof_start(int32_t kernel_class, int32_t max_launches) {
     p.ev.resize(2 * (size_t)max_launches);
     for (size_t i = have; i < p.ev.size(); ++i) DM_HIP(hipEventCreate(&p.ev[i]));
   }
+  if (p.dts_cap < max_launches) {
+    if (p.dts) DM_HIP(hipFree(p.dts));
+    p.dts = nullptr;
+    p.dts_cap = 0;
+    DM_HIP(hipMalloc(&p.dts, (size_t)max_launches * 2 * PROF_SLOTS * sizeof(uint64_t)));
+    p.dts_cap = max_launches;
+  }
+  {   // starts: all ones (min-reduced), ends: zero (max-reduced)
+    const long n = (long)max_launches * 2 * PROF_SLOTS;
+    hipLaunchKernelGGL(k_prof_init, dim3(cdiv(n, 256)), dim3(256), 0, nullptr, p.dts, n);
+    DM_HIP(hipGetLastError());
+    DM_HIP(hipDeviceSynchronize());
+  }
+  p.dev_timed.assign(max_launches, 0);
   p.cap = max_launches;
   p.n = 0;
   p.armed = kernel_class;
@@ -409,6 +470,10 @@ int dm_prof_start(int32_t kernel_class, int32_t max_launches) {
 }
 
 int dm_prof_stop(float* total_ms, int32_t* n_launches) {
+  return dm_prof_stop2(total_ms, nullptr, n_launches);
+}
+
+int dm_prof_stop2(float* event_ms, float* device_ms, int32_t* n_launches) {
   ProfState& p = prof();
   DM_REQUIRE(p.armed != PROF_NONE, DM_ERR_INVALID, "timing not armed");
   p.armed = PROF_NONE;
@@ -419,7 +484,30 @@ int dm_prof_stop(float* total_ms, int32_t* n_launches) {
     DM_HIP(hipEventElapsedTime(&ms, p.ev[2 * i], p.ev[2 * i + 1]));
     tot += ms;
   }
-  if (total_ms) *total_ms = tot;
+  double dev_tot = -1.0;
+  int ndev = 0;
+  for (int i = 0; i < p.n; ++i) ndev += p.dev_timed[i];
+  if (ndev == p.n && p.n > 0) {
+    int dev = 0, khz = 0;
+    DM_HIP(hipGetDevice(&dev));
+    DM_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+    DM_REQUIRE(khz > 0, DM_ERR_HIP, "device wall clock rate unavailable");
+    std::vector<uint64_t> h((size_t)p.n * 2 * PROF_SLOTS);
+    DM_HIP(hipMemcpy(h.data(), p.dts, h.size() * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    dev_tot = 0.0;
+    for (int i = 0; i < p.n; ++i) {
+      const uint64_t* st = h.data() + (size_t)i * 2 * PROF_SLOTS;
+      uint64_t lo = ~0ull, hi = 0;
+      for (int k = 0; k < PROF_SLOTS; ++k) {
+        lo = std::min(lo, st[k]);
+        hi = std::max(hi, st[PROF_SLOTS + k]);
+      }
+      DM_REQUIRE(hi >= lo && lo != ~0ull, DM_ERR_HIP, "launch %d left no device timestamps", i);
+      dev_tot += (double)(hi - lo) / (double)khz;   // ticks / (ticks per ms)
+    }
+  }
+  if (event_ms) *event_ms = tot;
+  if (device_ms) *device_ms = (float)dev_tot;
   if (n_launches) *n_launches = p.n;
   return DM_OK;
 }

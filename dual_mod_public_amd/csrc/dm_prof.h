@@ -1,10 +1,15 @@
-// Optional per-kernel-class timing with HIP events (host side).
+// Optional per-kernel-class timing (host side).
 //
-// When a class is armed (dm_prof_start), every launch of that class records a
-// start and a stop event on the launch's own stream; dm_prof_stop waits for the
-// last event and returns the summed elapsed time and the launch count. Unarmed,
-// a ProfScope costs one integer compare. Used by bench.py to time the dominant
-// kernel inside its timed region; never armed on the product path.
+// When a class is armed (dm_prof_start), every launch of that class is timed:
+//  * the GEMM kernels and the decode tape read take their own span from the
+//    device clock (first block start to last block end, folded into
+//    PROF_SLOTS slots per launch; see prof_begin / prof_end), the interval a
+//    kernel-trace profiler reports;
+//  * every class also records a HIP start/stop event pair on the launch's own
+//    stream (kernel + queue overheads: an upper bound).
+// dm_prof_stop waits for the last event and returns the summed times and the
+// launch count. Unarmed, a launch costs one integer compare. Used by bench.py to
+// time the dominant kernel inside its timed region; never armed on the product path.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -34,6 +39,9 @@ struct ProfState {
   int cap = 0;
   int n = 0;
   std::vector<hipEvent_t> ev;   // 2 * cap events: start, stop
+  uint64_t* dts = nullptr;      // [cap][2 * PROF_SLOTS] device-clock slots
+  int dts_cap = 0;
+  std::vector<char> dev_timed;  // per launch: took device-clock slots
 };
 
 inline ProfState& prof() {
@@ -56,5 +64,32 @@ struct ProfScope {
     if (stop_ != nullptr) (void)hipEventRecord(stop_, s_);
   }
 };
+
+// Timing of one launch of class `cls`: when armed, records the start event now
+// and returns the launch index (else -1). `ts` receives the launch's device-clock
+// slots when the kernel supports them (dev_ts) — nullptr otherwise.
+inline int prof_launch_begin(int cls, hipStream_t s, bool dev_ts, uint64_t*& ts) {
+  ProfState& p = prof();
+  ts = nullptr;
+  if (p.armed != cls || cls == PROF_NONE || p.n >= p.cap) return -1;
+  (void)hipEventRecord(p.ev[2 * p.n], s);
+  if (dev_ts && p.dts != nullptr) {
+    ts = p.dts + (size_t)p.n * 2 * PROF_SLOTS;
+    p.dev_timed[p.n] = 1;
+  }
+  return p.n++;
+}
+inline void prof_launch_end(int idx, hipStream_t s) {
+  if (idx >= 0) (void)hipEventRecord(prof().ev[2 * idx + 1], s);
+}
+
+// hipLaunchKernelGGL with event timing for class `cls`.
+template <typename F, typename... Args>
+inline void launch_k(int cls, F kernel, dim3 grid, dim3 block, uint32_t shmem, hipStream_t s, Args... args) {
+  uint64_t* ts;
+  const int idx = prof_launch_begin(cls, s, false, ts);
+  hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
+  prof_launch_end(idx, s);
+}
 
 }  // namespace dm

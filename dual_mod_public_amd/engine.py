@@ -254,12 +254,25 @@ class HipSweepCell:
         c.flags = 0 if residual else L.DM_FLAG_NO_RESIDUAL
         return c
 
+    def tape_bytes(self, schedule):
+        """Bytes of the saved cell states of one layer forward over ``schedule``."""
+        n = L.lib().dm_layer_tape_bytes(ctypes.byref(self.conf), _sched(schedule), len(schedule))
+        if n == 0:
+            raise L.DMError("dm_layer_tape_bytes rejected the schedule")
+        return n
+
+    def new_tape(self, schedule):
+        """Device buffer for ``layer_forward(..., tape=)``: every sweep state of every
+        cell, so that ``layer_backward`` skips the per-cell recompute."""
+        return torch.empty(self.tape_bytes(schedule), device=self.device, dtype=torch.uint8)
+
     def layer_forward(self, x, y, cos, sin, schedule, K_cache, V_cache, ocat, bufs, normalize=True,
-                      residual=True):
+                      residual=True, tape=None):
         """Attention sublayer y = x + W_O DM(attn_norm(x)) over ``schedule``
         (model.py:123-124 with forward.py:95-113's chunk loop), one C call.
         normalize=False takes x as xhat (no attn_norm); residual=False drops the +x
-        (DualModAttention.forward, attention.py:438-447)."""
+        (DualModAttention.forward, attention.py:438-447). ``tape`` (from new_tape)
+        keeps every cell's sweep states for layer_backward."""
         sched = _sched(schedule)
         cos, sin = _f32(cos, self.device), _f32(sin, self.device)
         ws = self.w.struct(with_attn_norm=normalize)
@@ -268,8 +281,8 @@ class HipSweepCell:
         L.check(L.lib().dm_layer_fwd(
             ctypes.byref(conf), ctypes.byref(ws), L.ptr(x), L.ptr(y), L.ptr(cos), L.ptr(sin),
             ctypes.byref(b), sched, len(schedule), L.ptr(K_cache), L.ptr(V_cache),
-            K_cache.shape[2], L.ptr(ocat), L.ptr(self.workspace), self.workspace.numel(),
-            L.stream_ptr()))
+            K_cache.shape[2], L.ptr(ocat), L.ptr(tape), 0 if tape is None else tape.numel(),
+            L.ptr(self.workspace), self.workspace.numel(), L.stream_ptr()))
         return y
 
     def _bwd_workspace(self, T, cache_T, kmax):
@@ -283,10 +296,11 @@ class HipSweepCell:
         return self._bwd_ws
 
     def layer_backward(self, x, dy, dx, cos, sin, schedule, K_cache, V_cache, ocat, bufs, grads,
-                       normalize=True, residual=True):
-        """Reverse-scan backward of ``layer_forward`` with exact recompute
-        (engines/wavescan/engine/backward.py:92-123, fused_sweep.py:1557-1959):
-        writes dx and ADDS the parameter grads into ``grads`` (LayerGrads)."""
+                       normalize=True, residual=True, tape=None):
+        """Reverse-scan backward of ``layer_forward`` (engines/wavescan/engine/backward.py:92-123,
+        fused_sweep.py:1557-1959): writes dx and ADDS the parameter grads into
+        ``grads`` (LayerGrads). With the forward's ``tape`` the cell states are read
+        from it, else every cell is recomputed exactly (same values either way)."""
         sched = _sched(schedule)
         cos, sin = _f32(cos, self.device), _f32(sin, self.device)
         ws = self.w.struct(with_attn_norm=normalize)
@@ -298,8 +312,8 @@ class HipSweepCell:
         L.check(L.lib().dm_layer_bwd(
             ctypes.byref(conf), ctypes.byref(ws), L.ptr(x), L.ptr(dy), L.ptr(dx), L.ptr(cos),
             L.ptr(sin), ctypes.byref(b), sched, len(schedule), L.ptr(K_cache), L.ptr(V_cache),
-            K_cache.shape[2], L.ptr(ocat), ctypes.byref(g), L.ptr(work), work.numel(),
-            L.stream_ptr()))
+            K_cache.shape[2], L.ptr(ocat), L.ptr(tape), 0 if tape is None else tape.numel(),
+            ctypes.byref(g), L.ptr(work), work.numel(), L.stream_ptr()))
         return dx
 
 

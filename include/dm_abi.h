@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DM_ABI_VERSION 1
+#define DM_ABI_VERSION 2
 
 typedef enum dm_status {
   DM_OK = 0,
@@ -148,20 +148,30 @@ int dm_cell_fwd(const dm_config* cfg, const dm_packed* w, const dm_layer_bufs* b
  * Block attention sublayer (models/dualmod/model.py:123-124) run through the
  * chunk schedule (engines/wavescan/engine/forward.py:95-113, schedule.py:63-69):
  *   y = x + W_O . DM(RMSNorm(x)).  sched = n_cells triples (pos0, c, n_sweeps)
- * that tile [0, T) in order. Fills bufs, the caches and ocat [B, T, d]. */
+ * that tile [0, T) in order. Fills bufs, the caches and ocat [B, T, d].
+ *
+ * tape (may be NULL): device buffer of dm_layer_tape_bytes() bytes that receives
+ * every sweep state of every cell (o, RMS sums, softmax row stats, raw sweep GEMM
+ * outputs, v_in, the refined intra rows of sweeps 1..K-1, the committed row max).
+ * The reference rebuilds these in the backward by exact recompute
+ * (fused_sweep.py:1580-1659); with 288 GB of HBM per GPU this build can keep them
+ * instead (about 58 MB per 64-token cell at d=1024, B=8, K=4). Every kernel is
+ * deterministic, so the saved states equal the recomputed ones bit for bit. */
+size_t dm_layer_tape_bytes(const dm_config* cfg, const int32_t* sched, int32_t n_cells);
 int dm_layer_fwd(const dm_config* cfg, const dm_packed* w, const void* x, void* y,
                  const float* cos, const float* sin, const dm_layer_bufs* bufs,
                  const int32_t* sched, int32_t n_cells, void* K_cache, void* V_cache,
-                 int32_t cache_T, void* ocat, void* workspace, size_t workspace_bytes,
-                 void* stream);
+                 int32_t cache_T, void* ocat, void* tape, size_t tape_bytes, void* workspace,
+                 size_t workspace_bytes, void* stream);
 
 /* ---- whole layer backward ---------------------------------------------------------
- * Reverse-scan backward with exact recompute of the layer forward above
- * (engines/wavescan/engine/backward.py:92-123, FusedSweepCell.cell_backward
- * fused_sweep.py:1557-1850, layer_close :1873-1959): cells in reverse order; each
- * cell recomputes its n_sweeps sweeps from the forward's projections (bufs) and
- * final cache rows, then runs the sweeps backward; grads of the committed rows
- * it read accumulate in an fp32 grad cache consumed by the earlier cells.
+ * Reverse-scan backward of the layer forward above (engines/wavescan/engine/backward.py:92-123,
+ * FusedSweepCell.cell_backward fused_sweep.py:1557-1850, layer_close :1873-1959):
+ * cells in reverse order; each cell takes its n_sweeps sweep states from the
+ * forward's tape (non-NULL, same schedule) or recomputes them exactly from the
+ * forward's projections (bufs) and final cache rows (tape NULL, as the reference),
+ * then runs the sweeps backward; grads of the committed rows it read accumulate in
+ * an fp32 grad cache consumed by the earlier cells.
  * Inputs are exactly what dm_layer_fwd produced / consumed (x, bufs, caches, ocat)
  * plus dy [B, T, d]. Writes dx [B, T, d] (storage dtype) and ADDS the parameter
  * gradients into g (fp32, reference layout). Needs the *_t fields of w. */
@@ -178,8 +188,8 @@ size_t dm_layer_bwd_workspace_bytes(const dm_config* cfg, int32_t T, int32_t cac
 int dm_layer_bwd(const dm_config* cfg, const dm_packed* w, const void* x, const void* dy, void* dx,
                  const float* cos, const float* sin, const dm_layer_bufs* bufs, const int32_t* sched,
                  int32_t n_cells, const void* K_cache, const void* V_cache, int32_t cache_T,
-                 const void* ocat, const dm_grads* g, void* workspace, size_t workspace_bytes,
-                 void* stream);
+                 const void* ocat, const void* tape, size_t tape_bytes, const dm_grads* g,
+                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- decode ------------------------------------------------------------------
  * Replaces DualModAttention.decode_step (attention.py:564-588) on a static tape
@@ -222,13 +232,20 @@ int dm_check_schedule(const int32_t* sched, int32_t n_cells, int32_t T);
 /* ---- optional kernel timing (benchmarks) -------------------------------------
  * No reference counterpart (the reference times with ad-hoc torch events,
  * engines/wave3d/wave3d_x.py:28-33). Arms one kernel class; every later launch of
- * that class (up to max_launches) is bracketed by HIP events on its own stream.
- * dm_prof_stop waits for the recorded events and returns their summed duration.
+ * that class (up to max_launches) is bracketed by HIP events on its own stream, and
+ * the GEMM classes (1, 4, 5, 6) and the decode tape read (7) also time themselves
+ * from the device clock (first block start to last block end of each dispatch, the
+ * span a kernel-trace profiler reports; the event pair adds queue overheads).
+ * dm_prof_stop2 waits, then returns the summed event time, the summed device-clock
+ * time (-1 when some launch of the class has no device timing) and the launch
+ * count; dm_prof_stop returns the event time only. dm_prof_start allocates its
+ * timestamp buffer (2 * 1024 * 8 bytes per launch) and synchronizes the device.
  * Classes: 1 projection, 2 committed accumulator, 3 sweep attention, 4 sweep GEMM 1,
  * 5 sweep GEMM 2, 6 W_O, 7 decode tape read, 8 decode merge, 9 decode refine,
  * 10 backward, 11 whole entry-point call. */
 int dm_prof_start(int32_t kernel_class, int32_t max_launches);
 int dm_prof_stop(float* total_ms, int32_t* n_launches);
+int dm_prof_stop2(float* event_ms, float* device_ms, int32_t* n_launches);
 
 #ifdef __cplusplus
 }

@@ -50,7 +50,8 @@ def oracle_grads(cfg, sd, x, dy, cos, sin, sched, dtype=torch.float64, normalize
     return xg.grad, g
 
 
-def hip_grads(cfg, sd, x, dy, cos, sin, sched, dtype, normalize=True, residual=True):
+def hip_grads(cfg, sd, x, dy, cos, sin, sched, dtype, normalize=True, residual=True, tape=False,
+              full=False):
     B, T, d = x.shape
     cell = HipSweepCell(cfg, B, T, device=DEV, dtype=dtype)
     cell.pack({k: v.to(DEV, dtype) for k, v in sd.items()})
@@ -60,12 +61,16 @@ def hip_grads(cfg, sd, x, dy, cos, sin, sched, dtype, normalize=True, residual=T
     K = torch.empty(B, cfg.n_heads, T, cfg.head_dim, device=DEV, dtype=dtype)
     V = torch.empty_like(K)
     ocat = torch.empty_like(xd)
-    cell.layer_forward(xd, y, cos, sin, sched, K, V, ocat, bufs, normalize=normalize, residual=residual)
+    tp = cell.new_tape(sched) if tape else None
+    cell.layer_forward(xd, y, cos, sin, sched, K, V, ocat, bufs, normalize=normalize, residual=residual,
+                       tape=tp)
     grads = LayerGrads(cfg, DEV)
     dx = torch.empty_like(xd)
     cell.layer_backward(xd, dy.to(DEV, dtype).contiguous(), dx, cos, sin, sched, K, V, ocat, bufs, grads,
-                        normalize=normalize, residual=residual)
+                        normalize=normalize, residual=residual, tape=tp)
     torch.cuda.synchronize()
+    if full:
+        return y, dx, grads, (K, V, ocat)
     return y, dx, grads
 
 
@@ -95,6 +100,63 @@ def test_layer_grads_fp32(ctx_mod, c, k):
     _, dx, g = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.float32)
     dx_ref, g_ref = oracle_grads(cfg, sd, x, dy, c64, s64, sched)
     compare("fp32", dx, g, dx_ref, g_ref, FP32_TOL)
+
+
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear"])
+def test_layer_grads_tape_fp32(ctx_mod):
+    """Forward-saved tape instead of recompute: grads vs autograd through the oracle."""
+    say(f"bwd fp32 tape ctx_mod={ctx_mod}")
+    cfg = cfg_of(ctx_mod=ctx_mod)
+    B, T = 2, 64
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(98), dtype=torch.float64)
+    sched = uniform_chunks(T, 16, 4)
+    _, dx, g = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.float32, tape=True)
+    dx_ref, g_ref = oracle_grads(cfg, sd, x, dy, c64, s64, sched)
+    compare("fp32 tape", dx, g, dx_ref, g_ref, FP32_TOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "mult"])
+@pytest.mark.parametrize("sched", [[(0, 16, 3), (16, 16, 1), (32, 7, 2), (39, 25, 4)], [(0, 64, 1)],
+                                   [(0, 8, 8), (8, 56, 2)]])
+def test_tape_equals_recompute(dtype, ctx_mod, sched):
+    """Tape and exact recompute give bit-identical outputs, caches and gradients
+    (deterministic kernels): the tape changes where the sweep states come from, not
+    their values. Ragged, single-cell and K = c schedules."""
+    say(f"tape == recompute {dtype} {ctx_mod} {sched}")
+    cfg = cfg_of(ctx_mod=ctx_mod)
+    B, T = 2, 64
+    sd, x, _, (c32, s32) = setup(cfg, B, T)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(5), dtype=torch.float64)
+    y0, dx0, g0, st0 = hip_grads(cfg, sd, x, dy, c32, s32, sched, dtype, full=True)
+    y1, dx1, g1, st1 = hip_grads(cfg, sd, x, dy, c32, s32, sched, dtype, tape=True, full=True)
+    assert torch.equal(y0, y1)
+    for a, b in zip(st0, st1):
+        assert torch.equal(a, b)
+    assert torch.equal(dx0, dx1)
+    for name, t in g0.t.items():
+        assert torch.equal(t, g1[name]), name
+
+
+def test_tape_bytes_and_bounds():
+    """dm_layer_tape_bytes grows with the schedule; an undersized tape is rejected."""
+    cfg = cfg_of()
+    B, T = 2, 64
+    cell = HipSweepCell(cfg, B, T, device=DEV, dtype=torch.float32)
+    a = cell.tape_bytes(uniform_chunks(T, 16, 2))
+    b = cell.tape_bytes(uniform_chunks(T, 16, 4))
+    assert 0 < a < b
+    sd, x, _, (c32, s32) = setup(cfg, B, T)
+    cell.pack({k: v.to(DEV, torch.float32) for k, v in sd.items()})
+    bufs = cell.new_bufs(T)
+    xd = x.float().to(DEV)
+    y, ocat = torch.empty_like(xd), torch.empty_like(xd)
+    K = torch.empty(B, cfg.n_heads, T, cfg.head_dim, device=DEV)
+    V = torch.empty_like(K)
+    small = torch.empty(a, device=DEV, dtype=torch.uint8)
+    with pytest.raises(L.DMError, match="tape"):
+        cell.layer_forward(xd, y, c32, s32, uniform_chunks(T, 16, 4), K, V, ocat, bufs, tape=small)
 
 
 def test_layer_grads_no_norm_no_residual_fp32():
