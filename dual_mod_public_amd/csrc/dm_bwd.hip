@@ -27,8 +27,12 @@ template <typename T> struct BwdWs {
   float *lamdv, *gw, *rowdot;           // [N, d], [N, d], [N, NRD]
   float *G, *Dbar;                      // [B*h, CMAX, dh], [B*h, CMAX]
   float *dq_part;                       // [nsplit, B*h, CMAX, dh]
+  // weight grads of the sweeps, one GEMM per layer: the cells' transposed operands
+  // side by side, [4d | d, Rp] with Rp >= sum over cells of K*B*c (rounded to 64)
+  T *dctxT, *uT, *dvcT, *vinT;
+  long Rp;
+  float* kpart;                         // [KSPLIT, 4d, d] split-K partials
   // layer close
-  T *dctxT, *uT, *dvcT, *vinT;          // per-cell transposes [4d | d, K*N] for the weight-grad GEMMs
   T* dproj;                             // [B*T, nproj*d]
   T *tA, *tB;                           // layer-level transposes [max(nproj*d, d), B*T] and [d, B*T]
   float* dxhat;                         // [B*T, d]
@@ -40,6 +44,7 @@ template <typename T> struct BwdWs {
 constexpr int NSLOT_TM = 16;      // rows per norm_ctx-weight partial slot (du GEMM wave tile)
 constexpr int DU_TN = 32;         // columns per row-dot partial (du GEMM wave tile)
 constexpr int NCHUNK = 64;        // row chunks of the column sums
+constexpr int KSPLIT = 4;         // split-K slices of the layer's sweep weight-grad GEMMs
 
 template <typename T>
 BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base) {
@@ -73,14 +78,18 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.G = cv.take<float>(BH * CMAX * dh * 4);
   w.Dbar = cv.take<float>(BH * CMAX * 4);
   w.dq_part = cv.take<float>(comm_splits_max_bwd(cache_T) * BH * CMAX * dh * 4);
-  w.dctxT = cv.take<T>((kmax * N + 64) * 4 * d * e);
-  w.uT = cv.take<T>((kmax * N + 64) * d * e);
-  w.dvcT = cv.take<T>((kmax * N + 64) * d * e);
-  w.vinT = cv.take<T>((kmax * N + 64) * d * e);
+  // + 64: rows of the transposes a power of two apart would all map to the same HBM
+  // channels (the per-cell transposes write 64 rows at a stride of Rp elements)
+  w.Rp = (long)cdiv((long)kmax * B * T_, 64) * 64 + 64;
+  w.dctxT = cv.take<T>(w.Rp * 4 * d * e);
+  w.uT = cv.take<T>(w.Rp * d * e);
+  w.dvcT = cv.take<T>(w.Rp * d * e);
+  w.vinT = cv.take<T>(w.Rp * d * e);
+  w.kpart = cv.take<float>(KSPLIT * 4 * d * d * 4);
   // the attn_norm weight partials [B*T, d] fp32 reuse dproj once it is consumed
   w.dproj = cv.take<T>(std::max(BT * nproj * d * e, BT * d * 4));
-  w.tA = cv.take<T>((BT + 64) * nproj * d * e);
-  w.tB = cv.take<T>((BT + 64) * d * e);
+  w.tA = cv.take<T>((BT + 128) * nproj * d * e);
+  w.tB = cv.take<T>((BT + 128) * d * e);
   w.dxhat = cv.take<float>(BT * d * 4);
   w.dWp = cv.take<float>(nproj * d * d * 4);
   w.dWs = cv.take<float>(4 * d * d * 4);
@@ -129,23 +138,23 @@ template <typename T>
 void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N, int K, int accumulate, T* At,
              T* Bt, hipStream_t s) {
   const int Kp = cdiv(K, 64) * 64;   // zero-padded to whole k-tiles
-  transpose<T>(A, lda, K, M, Kp, At, Kp, 0, s);
-  transpose<T>(Bm, ldb, K, N, Kp, Bt, Kp, 0, s);
+  const long ld = Kp + 64;            // off a power of two: see BwdWs::Rp
+  transpose<T>(A, lda, K, M, Kp, At, ld, 0, s);
+  transpose<T>(Bm, ldb, K, N, Kp, Bt, ld, 0, s);
   EpiStoreF32 ep{M, N, accumulate, C};
-  launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{At, Kp, M}, SrcRows<T>{Bt, Kp, N}, M, N, Kp, ep, s);
+  launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{At, ld, M}, SrcRows<T>{Bt, ld, N}, M, N, Kp, ep, s);
 }
 
-// C [M, N] (+)= A^T . u for u = RMSNorm(o) [K, N] with the norm weight w: u^T is
-// formed from o, its partial sums of squares and w in the transpose pass.
+// C [M, N] += At [M, Kp] . Bt [N, Kp]^T (both K-contiguous, zero past the valid k):
+// split-K into `part`, then a deterministic sum of the slices into C.
 template <typename T>
-void gemm_tn_rms(const T* A, long lda, const T* o, const float* ssq, int nparts, const T* w, float inv_d, float eps,
-                 float* C, int M, int N, int K, int accumulate, T* At, T* Bt, hipStream_t s) {
-  const int Kp = cdiv(K, 64) * 64;
-  transpose<T>(A, lda, K, M, Kp, At, Kp, 0, s);
-  hipLaunchKernelGGL(k_transpose_rms16<T>, dim3(cdiv(N, 64), cdiv(Kp, 64)), dim3(256), 0, s, o, (long)N, K, N, Kp,
-                     ssq, nparts, w, inv_d, eps, Bt, (long)Kp);
-  EpiStoreF32 ep{M, N, accumulate, C};
-  launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{At, Kp, M}, SrcRows<T>{Bt, Kp, N}, M, N, Kp, ep, s);
+void gemm_wgrad(const T* At, const T* Bt, long ld, int Kp, int M, int N, float* part, float* C, hipStream_t s) {
+  int S = KSPLIT;
+  while (S > 1 && (Kp / 64) % S != 0) --S;
+  EpiStoreF32 ep{M, N, 0, part, (long)M * N};
+  launch_gemm_splitk<T, 128, 128, 2, 2, 4>(SrcRows<T>{At, ld, M}, SrcRows<T>{Bt, ld, N}, M, N, Kp, S, ep, s);
+  hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv((long)M * N, 256)), dim3(256), 0, s, S, M * N, M * N,
+                     (const float*)part, C);
 }
 
 template <typename T, int DH>
@@ -187,6 +196,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   const T* kraw = (const T*)L->kraw;
   const size_t slot = (size_t)BH * CMAX * DH;
 
+  long coff = 0;   // columns of the weight-grad operands filled so far
   for (int ci = n_cells - 1; ci >= 0; --ci) {
     const int pos0 = sched[3 * ci], cc = sched[3 * ci + 1], K = sched[3 * ci + 2];
     const int N = B * cc;
@@ -256,10 +266,28 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
       hipLaunchKernelGGL(k_dq_reduce, dim3(cdiv((long)BH * cc * DH, 256)), dim3(256), 0, s, g, cp.nsplit,
                          (const float*)ws.dq_part, ws.dq);
     }
-    // weight grads of the cell's sweeps: dW_sweep += dctx^T u ; dW_vctx += dv_ctx^T v_in
-    gemm_tn_rms<T>(ws.dctx, 4 * d, sv.o, sv.ssq, h, (const T*)w->norm_ctx_w, inv_d, c->rms_eps, ws.dWs, 4 * d,
-                   d, K * N, 1, ws.dctxT, ws.uT, s);
-    if (mult) gemm_tn<T>(ws.dvc, d, sv.vin, d, gr->w_vctx, d, d, K * N, 1, ws.dvcT, ws.vinT, s);
+    // operands of the sweep weight grads (dW_sweep = dctx^T u, dW_vctx = dv_ctx^T v_in):
+    // this cell's K*N rows become columns [coff, coff + K*N) of the layer's transposes;
+    // the zero fill up to the next multiple of 64 is overwritten by the next cell
+    {
+      const int rows = K * N;
+      const long end = coff + rows;
+      const int pad = (int)(cdiv(end, 64) * 64 - coff);
+      transpose<T>(ws.dctx, 4 * d, rows, 4 * d, pad, ws.dctxT, ws.Rp, coff, s);
+      hipLaunchKernelGGL(k_transpose_rms16<T>, dim3(cdiv(d, 64), cdiv(pad, 64)), dim3(256), 0, s, sv.o, (long)d,
+                         rows, d, pad, (const float*)sv.ssq, h, (const T*)w->norm_ctx_w, inv_d, c->rms_eps, ws.uT,
+                         ws.Rp, coff);
+      if (mult) {
+        transpose<T>(ws.dvc, d, rows, d, pad, ws.dvcT, ws.Rp, coff, s);
+        transpose<T>(sv.vin, d, rows, d, pad, ws.vinT, ws.Rp, coff, s);
+      }
+      coff = end;
+    }
+  }
+  {   // the layer's sweep weight grads, one GEMM each over all cells' rows
+    const int Kp = (int)(cdiv(coff, 64) * 64);
+    gemm_wgrad<T>(ws.dctxT, ws.uT, ws.Rp, Kp, 4 * d, d, ws.kpart, ws.dWs, s);
+    if (mult) gemm_wgrad<T>(ws.dvcT, ws.vinT, ws.Rp, Kp, d, d, ws.kpart, gr->w_vctx, s);
   }
 
   // ---- projection VJP

@@ -124,9 +124,11 @@ template <int BM, int BN, int WM, int WN> struct WaveTile {
 };
 
 // The k-loop. acc must be zero-initialised by the caller (or hold a C to add to).
+// Reduces k in [kbase, kbase + K).
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB>
 DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, char* smem,
-                          floatx4 (&acc)[WaveTile<BM, BN, WM, WN>::FM][WaveTile<BM, BN, WM, WN>::FN]) {
+                          floatx4 (&acc)[WaveTile<BM, BN, WM, WN>::FM][WaveTile<BM, BN, WM, WN>::FN],
+                          int kbase = 0) {
   using Tr = GemmTraits<T>;
   using MF = Mfma<T>;
   using WT = WaveTile<BM, BN, WM, WN>;
@@ -158,7 +160,7 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
 
   uint4 ra[D][NA], rb[D][NB];
   auto gload = [&](int kt, uint4 (&xa)[NA], uint4 (&xb)[NB]) {
-    const int k0 = kt * BK;
+    const int k0 = kbase + kt * BK;
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
       int r, kc;
@@ -173,7 +175,7 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
     }
   };
   auto sstore = [&](int kt, T* dst, const uint4 (&xa)[NA], const uint4 (&xb)[NB]) {
-    const int k0 = kt * BK;
+    const int k0 = kbase + kt * BK;
     T* As = dst;
     T* Bs = dst + BM * LDK;
 #pragma unroll
@@ -274,6 +276,8 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
 
 // Generic kernel: zero accumulators, k-loop, epilogue on the wave's registers.
 // epi(acc, row0, col0) with row0/col0 the global origin of the wave tile.
+// Split-K launches (gridDim.z > 1) reduce k in [z*K, (z+1)*K) in block z; their
+// epilogue tells the slices apart by blockIdx.z.
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
 __global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint64_t* prof_ts) {
   const uint64_t t0 = prof_begin(prof_ts);
@@ -293,10 +297,10 @@ __global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint
     for (int j = 0; j < WT::FN; ++j) acc[i][j] = zero4();
   if constexpr (has_prefetch<EPI>::value) {
     const typename EPI::Pre pre = epi.prefetch(row0, col0);
-    gemm_mainloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc);
+    gemm_mainloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, (int)blockIdx.z * K);
     epi.apply(acc, row0, col0, rs, pre);
   } else {
-    gemm_mainloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc);
+    gemm_mainloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, (int)blockIdx.z * K);
     epi(acc, row0, col0, rs);
   }
   prof_end(prof_ts, t0);

@@ -118,4 +118,15 @@ void launch_gemm(const SA& sa, const SB& sb, int M, int N, int K, const EPI& epi
   prof_launch_end(idx, s);
 }
 
+// Split-K: S slices of K/S each (K/S a multiple of the k-tile), slice z in grid.z.
+template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
+void launch_gemm_splitk(const SA& sa, const SB& sb, int M, int N, int K, int S, const EPI& epi, hipStream_t s,
+                        int prof_cls = PROF_NONE) {
+  dim3 grid(N / BN, cdiv(M, BM), S);
+  uint64_t* ts;
+  const int idx = prof_launch_begin(prof_cls, s, true, ts);
+  hipLaunchKernelGGL((k_gemm<T, BM, BN, WM, WN, D, SA, SB, EPI>), grid, dim3(256), 0, s, sa, sb, K / S, epi, ts);
+  prof_launch_end(idx, s);
+}
+
 }  // namespace dm

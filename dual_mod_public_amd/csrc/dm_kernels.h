@@ -64,33 +64,37 @@ static __global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ 
 
 // out[c, col0_out + r] = in[r, c] for a [rows, cols] row-major matrix (ld_in) into a
 // [cols, ld_out] matrix, with output columns [rows, rows_pad) zero-filled: 64x64 tiles
-// through LDS, 16-byte loads and stores. cols, rows_pad, ld_out and col0_out must be
-// multiples of 16 / sizeof(T).
+// through LDS, 16-byte loads and stores. cols and ld_out must be multiples of
+// 16 / sizeof(T); an unaligned col0_out (or rows_pad) falls back to element stores.
 template <typename T>
 static __global__ __launch_bounds__(256) void k_transpose16(const T* __restrict__ in, long ld_in, int rows, int cols,
                                                             int rows_pad, T* __restrict__ out, long ld_out,
                                                             long col0_out) {
   constexpr int V = 16 / (int)sizeof(T);
-  __shared__ T tile[64][64 + 1];
+  __shared__ float tile[64][64 + 1];   // 4-byte cells, odd row stride: conflict-free both ways
   const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
   for (int v = threadIdx.x; v < 64 * 64 / V; v += 256) {
     const int r = v / (64 / V), cc = (v % (64 / V)) * V;
     if (r0 + r < rows && c0 + cc < cols) {
-      const uint4 x = *reinterpret_cast<const uint4*>(in + (long)(r0 + r) * ld_in + c0 + cc);
-      const T* e = reinterpret_cast<const T*>(&x);
+      float f[V];
+      unpack16<T>(*reinterpret_cast<const uint4*>(in + (long)(r0 + r) * ld_in + c0 + cc), f);
 #pragma unroll
-      for (int j = 0; j < V; ++j) tile[r][cc + j] = e[j];
+      for (int j = 0; j < V; ++j) tile[r][cc + j] = f[j];
     }
   }
   __syncthreads();
   for (int v = threadIdx.x; v < 64 * 64 / V; v += 256) {
     const int cc = v / (64 / V), r = (v % (64 / V)) * V;
     if (r0 + r < rows_pad && c0 + cc < cols) {
-      uint4 x;
-      T* e = reinterpret_cast<T*>(&x);
+      float f[V];
 #pragma unroll
-      for (int j = 0; j < V; ++j) e[j] = (r0 + r + j < rows) ? tile[r + j][cc] : from_f<T>(0.f);
-      *reinterpret_cast<uint4*>(out + (long)(c0 + cc) * ld_out + col0_out + r0 + r) = x;
+      for (int j = 0; j < V; ++j) f[j] = (r0 + r + j < rows) ? tile[r + j][cc] : 0.f;
+      T* dst = out + (long)(c0 + cc) * ld_out + col0_out + r0 + r;
+      if (col0_out % V == 0 && r0 + r + V <= rows_pad) {
+        *reinterpret_cast<uint4*>(dst) = pack16<T>(f);
+      } else {
+        for (int j = 0; j < V && r0 + r + j < rows_pad; ++j) dst[j] = from_f<T>(f[j]);
+      }
     }
   }
 }
@@ -105,12 +109,13 @@ static __global__ __launch_bounds__(256) void k_scale_cols(T* __restrict__ W, co
 
 // out[k, col0_out + r] = in[r, k] * rs[r] * w[k] with rs[r] = rsqrt(sum_p ssq[r, p] * inv_d + eps):
 // the transposed RMSNorm output u^T of the stacked sweeps (the weight-grad GEMM operand),
-// 64x64 tiles; output columns [rows, rows_pad) zero-filled.
+// 64x64 tiles; output columns [rows, rows_pad) zero-filled (stores as in k_transpose16).
 template <typename T>
 static __global__ __launch_bounds__(256) void k_transpose_rms16(const T* __restrict__ in, long ld_in, int rows,
                                                                 int cols, int rows_pad, const float* __restrict__ ssq,
                                                                 int nparts, const T* __restrict__ w, float inv_d,
-                                                                float eps, T* __restrict__ out, long ld_out) {
+                                                                float eps, T* __restrict__ out, long ld_out,
+                                                                long col0_out) {
   constexpr int V = 16 / (int)sizeof(T);
   __shared__ float tile[64][64 + 1];
   __shared__ float rs[64];
@@ -139,7 +144,12 @@ static __global__ __launch_bounds__(256) void k_transpose_rms16(const T* __restr
       float f[V];
 #pragma unroll
       for (int j = 0; j < V; ++j) f[j] = (r0 + r + j < rows) ? tile[r + j][cc] : 0.f;
-      *reinterpret_cast<uint4*>(out + (long)(c0 + cc) * ld_out + r0 + r) = pack16<T>(f);
+      T* dst = out + (long)(c0 + cc) * ld_out + col0_out + r0 + r;
+      if (col0_out % V == 0 && r0 + r + V <= rows_pad) {
+        *reinterpret_cast<uint4*>(dst) = pack16<T>(f);
+      } else {
+        for (int j = 0; j < V && r0 + r + j < rows_pad; ++j) dst[j] = from_f<T>(f[j]);
+      }
     }
   }
 }
@@ -717,12 +727,15 @@ template <typename T> struct EpiResidual {
 };
 
 // C (fp32) = acc, or C += acc when accumulate != 0
+// C [M, N] fp32 (+)= acc; split-K slice z stores into C + z * zstride.
 struct EpiStoreF32 {
   int M, N, accumulate;
   float* __restrict__ C;
+  long zstride = 0;
   template <int FM, int FN>
   DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
     const int lane = threadIdx.x & 63, lc = lane & 15;
+    float* __restrict__ C = this->C + (long)blockIdx.z * zstride;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
