@@ -271,7 +271,10 @@ template <typename T> struct EpiDuBwd {
 };
 
 // ---------------------------------------------------------------------------
-// attention VJP of one sweep, one block per (b, h), 4 waves x 16 rows
+// attention VJP of one sweep, two blocks per (b, h), 4 waves x 16 rows each:
+// role 0 (blockIdx.x == 0) the query-major half (dQ, the committed grads G / Dbar,
+// the self column's dq), role 1 the key-major half (dK, dV, the self column's
+// dkself / dvraw). Each role writes its own arrays, so the halves run concurrently.
 // ---------------------------------------------------------------------------
 template <typename T> struct AttnBwdArgs {
   CellGeom g;
@@ -313,7 +316,8 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
   __shared__ float sM[64], sZ[64], sD[64];
 
   const CellGeom& g = a.g;
-  const int bh = blockIdx.x, b = bh / g.h, hh = bh - b * g.h;
+  const int role = blockIdx.x;
+  const int bh = blockIdx.y, b = bh / g.h, hh = bh - b * g.h;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g4 = lane >> 4, lc = lane & 15;
   const int d = g.d, c = g.c;
@@ -367,7 +371,7 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
     const float dss = ps * (dov - Dp);
     if (part == 0) { sM[i] = Mi; sZ[i] = Zi; sD[i] = Dp; }
     // committed part: alpha = exp(m_comm - M) / Z
-    if (a.Mx != nullptr && ok) {
+    if (role == 0 && a.Mx != nullptr && ok) {
       const float alpha = __expf(a.Mx[(long)bh * c + i] - Mi) / Zi;
       float* Gr = a.G + ((long)bh * CMAX + i) * DH + e0;
 #pragma unroll
@@ -376,19 +380,24 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
     }
     if (ok) {
       const long lr = (lrow0 + i) * DH + e0;
-      float a0[EPT], a1[EPT], a2[EPT];
-      load_vec<float, EPT>(a.dkself + lr, a0);
-      load_vec<float, EPT>(a.dvraw + lr, a1);
-      load_vec<float, EPT>(a.dq + lr, a2);
+      if (role == 0) {
+        float a2[EPT];
+        load_vec<float, EPT>(a.dq + lr, a2);
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        a0[e] += a.scale * dss * q[e];
-        a1[e] += ps * dO[e];
-        a2[e] += a.scale * dss * ks[e];
+        for (int e = 0; e < EPT; ++e) a2[e] += a.scale * dss * ks[e];
+        store_vec<float, EPT>(a.dq + lr, a2);
+      } else {
+        float a0[EPT], a1[EPT];
+        load_vec<float, EPT>(a.dkself + lr, a0);
+        load_vec<float, EPT>(a.dvraw + lr, a1);
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          a0[e] += a.scale * dss * q[e];
+          a1[e] += ps * dO[e];
+        }
+        store_vec<float, EPT>(a.dkself + lr, a0);
+        store_vec<float, EPT>(a.dvraw + lr, a1);
       }
-      store_vec<float, EPT>(a.dkself + lr, a0);
-      store_vec<float, EPT>(a.dvraw + lr, a1);
-      store_vec<float, EPT>(a.dq + lr, a2);
     } else {
 #pragma unroll
       for (int e = 0; e < EPT; ++e) { q[e] = 0.f; kv[e] = 0.f; vv[e] = 0.f; }
@@ -408,7 +417,7 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
   __syncthreads();
 
   // ---- phase 2: query-major (rows i = 16 wave + ..): dS, then dQ = dS . K
-  {
+  if (role == 0) {
     floatx4 S[4], dP[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) { S[t] = zero4(); dP[t] = zero4(); }
@@ -438,10 +447,8 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
       for (int t = 0; t < NDT; ++t) a.dq[(lrow0 + i) * DH + 16 * t + lc] += a.scale * dQ[t][r];
     }
   }
-  __syncthreads();
-
   // ---- phase 3: key-major (rows j = 16 wave + ..): P^T, dS^T -> dV = P^T dO, dK = dS^T Q
-  {
+  else {
     floatx4 St[4], dPt[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) { St[t] = zero4(); dPt[t] = zero4(); }
@@ -772,6 +779,16 @@ static __global__ __launch_bounds__(256) void k_colsum_partial(int M, int ncols,
 }
 
 // out[col] += sum_chunk part[chunk * ld + col], col < ncols
+// C[i] (+)= sum_z part[z * n + i], z = 0..S-1 in order (split-K slices)
+static __global__ __launch_bounds__(256) void k_sum_splits(int S, long n, const float* __restrict__ part,
+                                                           float* __restrict__ C, int accumulate) {
+  const long i = blockIdx.x * 256L + threadIdx.x;
+  if (i >= n) return;
+  float v = 0.f;
+  for (int z = 0; z < S; ++z) v += part[(long)z * n + i];
+  C[i] = accumulate ? C[i] + v : v;
+}
+
 static __global__ __launch_bounds__(256) void k_sum_rows_add(int nchunk, int ncols, int ld, const float* __restrict__ part,
                                                       float* __restrict__ out) {
   const int col = blockIdx.x * 256 + threadIdx.x;

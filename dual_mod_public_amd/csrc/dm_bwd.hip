@@ -31,7 +31,7 @@ template <typename T> struct BwdWs {
   // side by side, [4d | d, Rp] with Rp >= sum over cells of K*B*c (rounded to 64)
   T *dctxT, *uT, *dvcT, *vinT;
   long Rp;
-  float* kpart;                         // [KSPLIT, 4d, d] split-K partials
+  float* kpart;                         // [KSPLIT_ELEMS(d)] split-K partials
   // layer close
   T* dproj;                             // [B*T, nproj*d]
   T *tA, *tB;                           // layer-level transposes [max(nproj*d, d), B*T] and [d, B*T]
@@ -44,7 +44,8 @@ template <typename T> struct BwdWs {
 constexpr int NSLOT_TM = 16;      // rows per norm_ctx-weight partial slot (du GEMM wave tile)
 constexpr int DU_TN = 32;         // columns per row-dot partial (du GEMM wave tile)
 constexpr int NCHUNK = 64;        // row chunks of the column sums
-constexpr int KSPLIT = 4;         // split-K slices of the layer's sweep weight-grad GEMMs
+// fp32 elements of the split-K partial buffer of the weight-grad GEMMs ([S, M, N], N = d)
+constexpr long KSPLIT_ELEMS(long d) { return 16 * d * d; }
 
 template <typename T>
 BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base) {
@@ -85,7 +86,7 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.uT = cv.take<T>(w.Rp * d * e);
   w.dvcT = cv.take<T>(w.Rp * d * e);
   w.vinT = cv.take<T>(w.Rp * d * e);
-  w.kpart = cv.take<float>(KSPLIT * 4 * d * d * 4);
+  w.kpart = cv.take<float>(KSPLIT_ELEMS((long)d) * 4);
   // the attn_norm weight partials [B*T, d] fp32 reuse dproj once it is consumed
   w.dproj = cv.take<T>(std::max(BT * nproj * d * e, BT * d * 4));
   w.tA = cv.take<T>((BT + 128) * nproj * d * e);
@@ -131,30 +132,39 @@ void transpose(const T* in, long ld_in, int rows, int cols, int rows_pad, T* out
                      col0_out);
 }
 
+// C [M, N] (+)= At [M, Kp] . Bt [N, Kp]^T (both K-contiguous, zero past the valid k):
+// split-K over enough slices to give every CU several blocks, the slices stored
+// into `part` ([KSPLIT_ELEMS] fp32) and summed into C in a fixed order.
+template <typename T>
+void gemm_splitk_f32(const T* At, long lda, const T* Bt, long ldb, int Kp, int M, int N, int accumulate, float* part,
+                     float* C, hipStream_t s) {
+  const long blocks = (long)(M / 128) * (N / 128);
+  int S = 1;
+  while (S < 16 && blocks * S * 2 <= 1024 && (long)S * 2 * M * N <= KSPLIT_ELEMS((long)N) &&
+         (Kp / 64) % (S * 2) == 0)
+    S *= 2;
+  if (S == 1) {
+    EpiStoreF32 ep{M, N, accumulate, C};
+    launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{At, lda, M}, SrcRows<T>{Bt, ldb, N}, M, N, Kp, ep, s);
+    return;
+  }
+  EpiStoreF32 ep{M, N, 0, part, (long)M * N};
+  launch_gemm_splitk<T, 128, 128, 2, 2, 4>(SrcRows<T>{At, lda, M}, SrcRows<T>{Bt, ldb, N}, M, N, Kp, S, ep, s);
+  hipLaunchKernelGGL(k_sum_splits, dim3(cdiv((long)M * N, 256)), dim3(256), 0, s, S, (long)M * N,
+                     (const float*)part, C, accumulate);
+}
+
 // C [M, N] (+)= A^T . B for row-major A [K, M], B [K, N] (the weight-grad products
 // sum over rows): both operands are transposed into scratch first so the GEMM runs
 // with K-contiguous operands (16-byte LDS stores).
 template <typename T>
 void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N, int K, int accumulate, T* At,
-             T* Bt, hipStream_t s) {
+             T* Bt, float* part, hipStream_t s) {
   const int Kp = cdiv(K, 64) * 64;   // zero-padded to whole k-tiles
   const long ld = Kp + 64;            // off a power of two: see BwdWs::Rp
   transpose<T>(A, lda, K, M, Kp, At, ld, 0, s);
   transpose<T>(Bm, ldb, K, N, Kp, Bt, ld, 0, s);
-  EpiStoreF32 ep{M, N, accumulate, C};
-  launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{At, ld, M}, SrcRows<T>{Bt, ld, N}, M, N, Kp, ep, s);
-}
-
-// C [M, N] += At [M, Kp] . Bt [N, Kp]^T (both K-contiguous, zero past the valid k):
-// split-K into `part`, then a deterministic sum of the slices into C.
-template <typename T>
-void gemm_wgrad(const T* At, const T* Bt, long ld, int Kp, int M, int N, float* part, float* C, hipStream_t s) {
-  int S = KSPLIT;
-  while (S > 1 && (Kp / 64) % S != 0) --S;
-  EpiStoreF32 ep{M, N, 0, part, (long)M * N};
-  launch_gemm_splitk<T, 128, 128, 2, 2, 4>(SrcRows<T>{At, ld, M}, SrcRows<T>{Bt, ld, N}, M, N, Kp, S, ep, s);
-  hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv((long)M * N, 256)), dim3(256), 0, s, S, M * N, M * N,
-                     (const float*)part, C);
+  gemm_splitk_f32<T>(At, ld, Bt, ld, Kp, M, N, accumulate, part, C, s);
 }
 
 template <typename T, int DH>
@@ -187,7 +197,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   {
     EpiStoreF32 ep{BT, d, 0, ws.docat};
     launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{dy, d, BT}, SrcRows<T>{(const T*)w->wo_t, d, d}, BT, d, d, ep, s);
-    gemm_tn<T>(dy, d, ocat, d, gr->wo, d, d, BT, 1, ws.tA, ws.tB, s);
+    gemm_tn<T>(dy, d, ocat, d, gr->wo, d, d, BT, 1, ws.tA, ws.tB, ws.kpart, s);
   }
 
   const T* qr = (const T*)L->qr;
@@ -251,7 +261,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
                           sv.stat_z + sw * (size_t)BH * CMAX, Mx, ws.G, ws.Dbar, sw == K - 1 ? 1 : 0,
                           scale, inv_d, c->rms_eps, dKo, dVo, ws.dkself, ws.dvraw, ws.dq};
         const size_t lds = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
-        hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(BH), dim3(256), lds, s, aa);
+        hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(2, BH), dim3(256), lds, s, aa);
         dKn = dKo; dVn = dVo;
         dn_stride = (long)CMAX * DH;
         dn_row0 = 0;
@@ -286,8 +296,8 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   }
   {   // the layer's sweep weight grads, one GEMM each over all cells' rows
     const int Kp = (int)(cdiv(coff, 64) * 64);
-    gemm_wgrad<T>(ws.dctxT, ws.uT, ws.Rp, Kp, 4 * d, d, ws.kpart, ws.dWs, s);
-    if (mult) gemm_wgrad<T>(ws.dvcT, ws.vinT, ws.Rp, Kp, d, d, ws.kpart, gr->w_vctx, s);
+    gemm_splitk_f32<T>(ws.dctxT, ws.Rp, ws.uT, ws.Rp, Kp, 4 * d, d, 1, ws.kpart, ws.dWs, s);
+    if (mult) gemm_splitk_f32<T>(ws.dvcT, ws.Rp, ws.vinT, ws.Rp, Kp, d, d, 1, ws.kpart, gr->w_vctx, s);
   }
 
   // ---- projection VJP
@@ -308,7 +318,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   }
   const T* xhat = norm ? (const T*)L->xhat : x;
   // dW_proj = d_proj^T . xhat (packed rows), dxhat = d_proj . W_proj
-  gemm_tn<T>(ws.dproj, (long)nproj * d, xhat, d, ws.dWp, nproj * d, d, BT, 0, ws.tA, ws.tB, s);
+  gemm_tn<T>(ws.dproj, (long)nproj * d, xhat, d, ws.dWp, nproj * d, d, BT, 0, ws.tA, ws.tB, ws.kpart, s);
   {
     EpiStoreF32 ep{BT, d, 0, ws.dxhat};
     launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{ws.dproj, (long)nproj * d, BT},
