@@ -42,6 +42,7 @@ from dual_mod_public_amd.synthetic import make_input, make_state_dict  # noqa: E
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+COPY_CAL_BYTES = 256 << 20  # --copy-calibration: bytes read (and written) per copy dispatch
 TIMING_NOTE = ("avg_launch_ms: per-dispatch span from the device clock (s_memrealtime, first block "
                "start to last block end), recorded by the kernel itself in the timed region; "
                "avg_launch_ms_events: HIP event pair around each launch on its stream (adds queue time)")
@@ -183,6 +184,9 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=0)
     ap.add_argument("--kernel", default="sweep1", help="kernel class timed for the roofline")
     ap.add_argument("--workload", default="fwdbwd", choices=["fwdbwd", "fwd"])
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run a plain 256 MiB device copy 3x (the known-size kernel that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     ap.add_argument("--recompute", action="store_true",
                     help="headline without the forward tape (backward recomputes every cell)")
     args = ap.parse_args()
@@ -196,6 +200,13 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     L.load()
+    if args.copy_calibration:
+        src = torch.ones(COPY_CAL_BYTES // 2, device=dev, dtype=torch.bfloat16)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     B, T, d, h, c, K = C2["B"], C2["T"], C2["d"], C2["h"], C2["c"], C2["K"]
     cfg = DualModConfig(d_model=d, n_heads=h, ctx_mod="mult_res", max_seq_len=T, dtype="bf16")

@@ -231,8 +231,8 @@ template <typename T> struct EpiDuBwd {
       for (int q = 0; q < 4; ++q) {
         int m = row0 + 16 * i + 4 * (lane >> 4) + q;
         m = m < M ? m : 0;
-        float s = 0.f;
-        for (int p = 0; p < h; ++p) s += ssq[(long)m * h + p];
+        // the 16 lanes holding row m split its h partial sums
+        const float s = group16_sum(sum_strided<MAX_HEADS / 16>(ssq + (long)m * h, lc, h, 16));
         rr[i][q] = rsqrtf(s * inv_d + eps);
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
@@ -346,8 +346,8 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
       for (int e = 0; e < EPT; ++e) dc[e] = 0.f;
     }
     float ss = 0.f, dot = 0.f;
-    for (int p = part; p < g.h; p += 4) ss += a.ssq[n * g.h + p];
-    for (int p = part; p < a.nrd; p += 4) dot += a.rowdot[n * a.nrd + p];
+    ss = sum_strided<MAX_HEADS / 4>(a.ssq + n * g.h, part, g.h, 4);
+    dot = sum_strided<MAX_ROWDOT / 4>(a.rowdot + n * a.nrd, part, a.nrd, 4);
     ss += __shfl_xor(ss, 1, 64); ss += __shfl_xor(ss, 2, 64);
     dot += __shfl_xor(dot, 1, 64); dot += __shfl_xor(dot, 2, 64);
     const float r = rsqrtf(ss * a.inv_d + a.eps);

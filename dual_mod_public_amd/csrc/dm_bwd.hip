@@ -145,11 +145,12 @@ void gemm_splitk_f32(const T* At, long lda, const T* Bt, long ldb, int Kp, int M
     S *= 2;
   if (S == 1) {
     EpiStoreF32 ep{M, N, accumulate, C};
-    launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{At, lda, M}, SrcRows<T>{Bt, ldb, N}, M, N, Kp, ep, s);
+    launch_gemm_auto<T, 128, 128, 2, 2, 3, 4>(SrcRows<T>{At, lda, M}, SrcRows<T>{Bt, ldb, N}, M, N, Kp, ep, s);
     return;
   }
   EpiStoreF32 ep{M, N, 0, part, (long)M * N};
-  launch_gemm_splitk<T, 128, 128, 2, 2, 4>(SrcRows<T>{At, lda, M}, SrcRows<T>{Bt, ldb, N}, M, N, Kp, S, ep, s);
+  launch_gemm_splitk<T, 128, 128, 2, 2, sizeof(T) == 2 ? -3 : 4>(SrcRows<T>{At, lda, M}, SrcRows<T>{Bt, ldb, N}, M, N,
+                                                                   Kp, S, ep, s);
   hipLaunchKernelGGL(k_sum_splits, dim3(cdiv((long)M * N, 256)), dim3(256), 0, s, S, (long)M * N,
                      (const float*)part, C, accumulate);
 }
@@ -196,7 +197,8 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   // ---- W_O: do_cat = dy . W_O ; dW_O += dy^T . ocat
   {
     EpiStoreF32 ep{BT, d, 0, ws.docat};
-    launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{dy, d, BT}, SrcRows<T>{(const T*)w->wo_t, d, d}, BT, d, d, ep, s);
+    launch_gemm_auto<T, 128, 128, 2, 2, 3, 4>(SrcRows<T>{dy, d, BT}, SrcRows<T>{(const T*)w->wo_t, d, d}, BT, d, d,
+                                               ep, s);
     gemm_tn<T>(dy, d, ocat, d, gr->wo, d, d, BT, 1, ws.tA, ws.tB, ws.kpart, s);
   }
 
@@ -321,7 +323,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   gemm_tn<T>(ws.dproj, (long)nproj * d, xhat, d, ws.dWp, nproj * d, d, BT, 0, ws.tA, ws.tB, ws.kpart, s);
   {
     EpiStoreF32 ep{BT, d, 0, ws.dxhat};
-    launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{ws.dproj, (long)nproj * d, BT},
+    launch_gemm_auto<T, 128, 128, 2, 2, 3, 4>(SrcRows<T>{ws.dproj, (long)nproj * d, BT},
                                       SrcRows<T>{(const T*)w->w_proj_t, (long)nproj * d, d}, BT, d, nproj * d, ep, s);
   }
   // unpack the packed weight grads into the reference layout

@@ -182,6 +182,25 @@ template <> struct Mfma<float> {
 
 DM_DEV floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
 
+// sum of p[q] for q = q0, q0 + step, ... < n, given n <= q0 + MAXQ * step: every load
+// is issued before the first add (indices clamped in bounds, excess terms masked),
+// so a runtime-length reduction costs one memory latency rather than one per term.
+template <int MAXQ>
+DM_DEV float sum_strided(const float* __restrict__ p, int q0, int n, int step) {
+  float v[MAXQ];
+#pragma unroll
+  for (int i = 0; i < MAXQ; ++i) v[i] = p[min(q0 + i * step, n - 1)];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXQ; ++i) s += (q0 + i * step < n) ? v[i] : 0.f;
+  return s;
+}
+
+// The per-row partial sums of the sweep arrays: ssq holds h <= MAX_HEADS per-head
+// sums of squares per row, rowdot d / 32 <= MAX_ROWDOT partial dot products.
+constexpr int MAX_HEADS = 64;
+constexpr int MAX_ROWDOT = 128;
+
 // ---- optional per-dispatch timing from the device clock ---------------------
 // A timed launch gets prof_ts = [PROF_SLOTS] earliest block starts followed by
 // [PROF_SLOTS] latest block ends (s_memrealtime ticks; block b folds into slot

@@ -1,11 +1,17 @@
 // MFMA GEMM core: C[BM x BN] = A[BM x K] . B[BN x K]^T with fp32 accumulation.
 //
 // 256 threads = 4 waves arranged WM x WN; each wave owns a (BM/WM) x (BN/WN)
-// sub-tile of 16x16 MFMA tiles, kept in registers. Operands are staged through
-// two LDS buffers (one barrier per k-tile) and fed from a ring of D register
-// stages, so the global loads of k-tile kt+D are in flight while tiles
-// kt..kt+D-1 are consumed: the small-M sweep GEMMs (M = B*c rows) have little
-// compute per k-tile and are otherwise bound by load latency.
+// sub-tile of 16x16 MFMA tiles, kept in registers. Two k-loops, chosen by the
+// template parameter D:
+//  * D > 0 (register ring): operands are staged through two LDS buffers (one
+//    barrier per k-tile) and fed from a ring of D register stages, so the global
+//    loads of k-tile kt+D are in flight while tiles kt..kt+D-1 are consumed;
+//  * D < 0 (bf16, K-contiguous sources, K a multiple of 64): -D LDS stages filled
+//    straight from global memory (global_load_lds_dwordx4, no register round trip),
+//    rows of 128 bytes with the 16-byte chunks XOR-swizzled by row so the MFMA
+//    fragment reads are bank-conflict free; tiles kt+1..kt-D-1 in flight.
+// The small-M sweep GEMMs (M = B*c rows) have little compute per k-tile and are
+// otherwise bound by load latency.
 //
 // Operand sources describe a logical row-major [rows x K] operand:
 //   SrcRows   element (r, k) at p[r*ld + k]   (K contiguous; 16-byte vector loads along k)
@@ -44,9 +50,8 @@ template <typename T> struct SrcRows {
   const T* __restrict__ p;
   long ld;
   int rows;   // valid rows (global index bound)
-  DM_DEV uint4 load(int r, int k) const {
-    return *reinterpret_cast<const uint4*>(p + (long)min(r, rows - 1) * ld + k);
-  }
+  DM_DEV const T* ptr(int r, int k) const { return p + (long)min(r, rows - 1) * ld + k; }
+  DM_DEV uint4 load(int r, int k) const { return *reinterpret_cast<const uint4*>(ptr(r, k)); }
   DM_DEV uint4 xform(uint4 v, int, int, const float*, int) const { return v; }
 };
 
@@ -70,19 +75,24 @@ template <typename T> struct SrcRowsRs {
   struct Pre {
     float s;
   };
+  // 256 / R adjacent threads per row split its nparts (<= MAX_HEADS) partial sums
   template <int R> DM_DEV Pre prepare_load(int r0, int) const {
+    constexpr int P = 256 / R;
+    static_assert(256 % R == 0 && P <= 8, "rows per block");
+    const int r = min(r0 + (int)threadIdx.x / P, rows - 1), part = threadIdx.x % P;
     Pre pr;
-    pr.s = 0.f;
-    const int r = min(r0 + (int)(threadIdx.x % R), rows - 1);
-    for (int q = 0; q < nparts; ++q) pr.s += ssq[(long)r * nparts + q];
+    pr.s = sum_strided<MAX_HEADS / P>(ssq + (long)r * nparts, part, nparts, P);
     return pr;
   }
   template <int R> DM_DEV void prepare_store(const Pre& pr, float* rs_lds, T*, int) const {
-    if (threadIdx.x < R) rs_lds[threadIdx.x] = rsqrtf(pr.s * inv_d + eps);
+    constexpr int P = 256 / R;
+    float s = pr.s;
+#pragma unroll
+    for (int o = 1; o < P; o <<= 1) s += __shfl_xor(s, o, 64);
+    if (threadIdx.x % P == 0) rs_lds[threadIdx.x / P] = rsqrtf(s * inv_d + eps);
   }
-  DM_DEV uint4 load(int r, int k) const {
-    return *reinterpret_cast<const uint4*>(p + (long)min(r, rows - 1) * ld + k);
-  }
+  DM_DEV const T* ptr(int r, int k) const { return p + (long)min(r, rows - 1) * ld + k; }
+  DM_DEV uint4 load(int r, int k) const { return *reinterpret_cast<const uint4*>(ptr(r, k)); }
   DM_DEV uint4 xform(uint4 v, int, int, const float*, int) const { return v; }
 };
 
@@ -110,10 +120,14 @@ template <typename T> struct PrepOf<SrcRowsRs<T>> { using type = typename SrcRow
 template <class E, class = void> struct has_prefetch { static constexpr bool value = false; };
 template <class E> struct has_prefetch<E, std::void_t<typename E::Pre>> { static constexpr bool value = true; };
 
-// 2 operand stages + the row scales
-template <typename T, int BM, int BN, bool RMS>
+// operand stages, then the row scales
+template <typename T, int BM, int BN, int D>
+constexpr int gemm_stage_bytes() {
+  return D > 0 ? 2 * (BM + BN) * GemmTraits<T>::LDK * (int)sizeof(T) : (-D) * (BM + BN) * 128;
+}
+template <typename T, int BM, int BN, int D, bool RMS>
 constexpr int gemm_lds_bytes() {
-  return 2 * (BM + BN) * GemmTraits<T>::LDK * (int)sizeof(T) + (RMS ? RMS_MAXR * 4 : BM * 4);
+  return gemm_stage_bytes<T, BM, BN, D>() + (RMS ? RMS_MAXR * 4 : BM * 4);
 }
 
 // Wave tile geometry of a (BM, BN, WM, WN) block.
@@ -274,22 +288,130 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
   }
 }
 
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt in [3:0] and [15:14], expcnt
+// [6:4] left at 7 = no wait, lgkmcnt [11:8])
+template <int N> DM_DEV void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// The direct-to-LDS k-loop (D = -S < 0). Stage layout: BM then BN rows of 64 bf16
+// (128 bytes, no padding); 16-byte chunk c of row r is stored at chunk c ^ (r & 7).
+// One global_load_lds_dwordx4 per wave fills 8 rows (lane l: row l/8, stored chunk
+// l%8), each wave issues BM/32 + BN/32 of them per k-tile. Per k-tile: wait for
+// this wave's loads of tile kt (vmcnt), barrier (everyone's landed, and stage
+// (kt-1)%S is free), issue tile kt+S-1 into it, compute on stage kt%S.
+template <typename T, int BM, int BN, int WM, int WN, int S, class SA, class SB>
+DM_DEV void gemm_mainloop_dma(const SA& sa, const SB& sb, int K, int m0, int n0, char* smem,
+                              floatx4 (&acc)[WaveTile<BM, BN, WM, WN>::FM][WaveTile<BM, BN, WM, WN>::FN],
+                              int kbase) {
+  static_assert(sizeof(T) == 2 && !SA::KMAJOR && !SB::KMAJOR, "direct-to-LDS path: bf16, K-contiguous");
+  static_assert(S >= 2 && BM % 32 == 0 && BN % 32 == 0, "stages / tile rows");
+  using MF = Mfma<T>;
+  using WT = WaveTile<BM, BN, WM, WN>;
+  constexpr int FM = WT::FM, FN = WT::FN, TM = WT::TM, TN = WT::TN;
+  constexpr int STAGE = (BM + BN) * 128;
+  constexpr int LA = BM / 32, LB = BN / 32, L = LA + LB;   // wave load instructions per tile
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;   // rows of an 8-row group start at multiples of 8
+  float* rs_lds = reinterpret_cast<float*>(smem + S * STAGE);
+  constexpr bool RMS = requires_prepare<SA>::value;
+  typename PrepOf<SA>::type pre{};
+  if constexpr (RMS) pre = sa.template prepare_load<BM>(m0, K);
+
+  auto issue = [&](int kt, int st) {
+    char* base = smem + st * STAGE;
+    const int k = kbase + kt * 64 + lchunk * 8;
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+      const int r = (wave * LA + i) * 8;
+      __builtin_amdgcn_global_load_lds((const void*)sa.ptr(m0 + r + lrow, k), (lds_void_t*)(base + r * 128), 16,
+                                       0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+      const int r = (wave * LB + i) * 8;
+      __builtin_amdgcn_global_load_lds((const void*)sb.ptr(n0 + r + lrow, k),
+                                       (lds_void_t*)(base + (BM + r) * 128), 16, 0, 0);
+    }
+  };
+  auto compute = [&](const char* As) {
+    const char* Bs = As + BM * 128;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      typename MF::frag af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int r = wm * TM + i * 16 + (lane & 15);
+        af[i] = *reinterpret_cast<const typename MF::frag*>(As + r * 128 +
+                                                             (((kk * 4 + (lane >> 4)) ^ (r & 7)) << 4));
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int r = wn * TN + j * 16 + (lane & 15);
+        bfr[j] = *reinterpret_cast<const typename MF::frag*>(Bs + r * 128 +
+                                                              (((kk * 4 + (lane >> 4)) ^ (r & 7)) << 4));
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = MF::mma(af[i], bfr[j], acc[i][j]);
+    }
+  };
+
+  const int nk = K / 64;
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < nk) issue(st, st);
+  // the row scales go to LDS while the first tiles are in flight; the first
+  // iteration's lgkmcnt(0) + barrier publishes them
+  if constexpr (RMS) sa.template prepare_store<BM>(pre, rs_lds, nullptr, K);
+  for (int kt = 0; kt < nk; ++kt) {
+    // tiles issued after kt and possibly outstanding: min(S-2, nk-1-kt)
+    const int after = min(S - 2, nk - 1 - kt);
+    if constexpr (S >= 4) {
+      if (after >= 2) wait_vm_lgkm0<2 * L>();
+      else if (after == 1) wait_vm_lgkm0<L>();
+      else wait_vm_lgkm0<0>();
+    } else if constexpr (S == 3) {
+      if (after >= 1) wait_vm_lgkm0<L>();
+      else wait_vm_lgkm0<0>();
+    } else {
+      wait_vm_lgkm0<0>();
+    }
+    __builtin_amdgcn_s_barrier();
+    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+    compute(smem + (kt % S) * STAGE);
+  }
+  // every wave is done reading the stages before the epilogue may reuse LDS
+  __syncthreads();
+}
+
 // Generic kernel: zero accumulators, k-loop, epilogue on the wave's registers.
 // epi(acc, row0, col0) with row0/col0 the global origin of the wave tile.
 // Split-K launches (gridDim.z > 1) reduce k in [z*K, (z+1)*K) in block z; their
 // epilogue tells the slices apart by blockIdx.z.
+template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB>
+DM_DEV void gemm_kloop(const SA& sa, const SB& sb, int K, int m0, int n0, char* smem,
+                       floatx4 (&acc)[WaveTile<BM, BN, WM, WN>::FM][WaveTile<BM, BN, WM, WN>::FN], int kbase) {
+  if constexpr (D > 0) gemm_mainloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, kbase);
+  else gemm_mainloop_dma<T, BM, BN, WM, WN, -D>(sa, sb, K, m0, n0, smem, acc, kbase);
+}
+
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
 __global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint64_t* prof_ts) {
   const uint64_t t0 = prof_begin(prof_ts);
   using WT = WaveTile<BM, BN, WM, WN>;
   constexpr bool RMS = requires_prepare<SA>::value;
-  __shared__ __attribute__((aligned(16))) char smem[gemm_lds_bytes<T, BM, BN, RMS>()];
+  __shared__ __attribute__((aligned(1024))) char smem[gemm_lds_bytes<T, BM, BN, D, RMS>()];
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   static_assert(!RMS || BM <= RMS_MAXR, "row-scale slots");
   const int wave = threadIdx.x >> 6;
   const int row0 = m0 + (wave / WN) * WT::TM, col0 = n0 + (wave % WN) * WT::TN;
-  const float* rs = reinterpret_cast<const float*>(smem + 2 * (BM + BN) * GemmTraits<T>::LDK * sizeof(T)) +
-                    (wave / WN) * WT::TM;
+  const float* rs = reinterpret_cast<const float*>(smem + gemm_stage_bytes<T, BM, BN, D>()) + (wave / WN) * WT::TM;
   floatx4 acc[WT::FM][WT::FN];
 #pragma unroll
   for (int i = 0; i < WT::FM; ++i)
@@ -297,10 +419,10 @@ __global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint
     for (int j = 0; j < WT::FN; ++j) acc[i][j] = zero4();
   if constexpr (has_prefetch<EPI>::value) {
     const typename EPI::Pre pre = epi.prefetch(row0, col0);
-    gemm_mainloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, (int)blockIdx.z * K);
+    gemm_kloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, (int)blockIdx.z * K);
     epi.apply(acc, row0, col0, rs, pre);
   } else {
-    gemm_mainloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, (int)blockIdx.z * K);
+    gemm_kloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, (int)blockIdx.z * K);
     epi(acc, row0, col0, rs);
   }
   prof_end(prof_ts, t0);

@@ -59,6 +59,8 @@ inline int check_cfg(const dm_config* c) {
   DM_REQUIRE(c->d % (2 * c->dh) == 0 && c->d % 128 == 0, DM_ERR_UNSUPPORTED,
              "d_model %d must be a multiple of 128 and of 2*head_dim", c->d);
   DM_REQUIRE(c->d <= RMS_MAXK, DM_ERR_UNSUPPORTED, "d_model %d > %d", c->d, RMS_MAXK);
+  DM_REQUIRE(c->h <= MAX_HEADS && c->d / 32 <= MAX_ROWDOT, DM_ERR_UNSUPPORTED, "%d heads (at most %d)", c->h,
+             MAX_HEADS);
   DM_REQUIRE(c->ctx_mod >= 0 && c->ctx_mod <= 2, DM_ERR_UNSUPPORTED, "ctx_mod %d", c->ctx_mod);
   DM_REQUIRE(c->local_window >= 0, DM_ERR_INVALID, "local_window %d", c->local_window);
   return DM_OK;
@@ -116,6 +118,20 @@ void launch_gemm(const SA& sa, const SB& sb, int M, int N, int K, const EPI& epi
   const int idx = prof_launch_begin(prof_cls, s, true, ts);
   hipLaunchKernelGGL((k_gemm<T, BM, BN, WM, WN, D, SA, SB, EPI>), grid, dim3(256), 0, s, sa, sb, K, epi, ts);
   prof_launch_end(idx, s);
+}
+
+// bf16 with K-contiguous operands and K a multiple of 64: the direct-to-LDS k-loop
+// with S stages; otherwise the register-ring k-loop of depth D.
+template <typename T, int BM, int BN, int WM, int WN, int S, int D, class SA, class SB, class EPI>
+void launch_gemm_auto(const SA& sa, const SB& sb, int M, int N, int K, const EPI& epi, hipStream_t s,
+                      int prof_cls = PROF_NONE) {
+  if constexpr (sizeof(T) == 2 && !SA::KMAJOR && !SB::KMAJOR) {
+    if (K % 64 == 0) {
+      launch_gemm<T, BM, BN, WM, WN, -S>(sa, sb, M, N, K, epi, s, prof_cls);
+      return;
+    }
+  }
+  launch_gemm<T, BM, BN, WM, WN, D>(sa, sb, M, N, K, epi, s, prof_cls);
 }
 
 // Split-K: S slices of K/S each (K/S a multiple of the k-tile), slice z in grid.z.

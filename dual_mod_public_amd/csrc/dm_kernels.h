@@ -120,11 +120,12 @@ static __global__ __launch_bounds__(256) void k_transpose_rms16(const T* __restr
   __shared__ float tile[64][64 + 1];
   __shared__ float rs[64];
   const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
-  if (threadIdx.x < 64) {
-    const int r = min(r0 + (int)threadIdx.x, rows - 1);
-    float s = 0.f;
-    for (int q = 0; q < nparts; ++q) s += ssq[(long)r * nparts + q];
-    rs[threadIdx.x] = rsqrtf(s * inv_d + eps);
+  {   // 4 adjacent threads per row
+    const int r = min(r0 + (int)threadIdx.x / 4, rows - 1), part = threadIdx.x % 4;
+    float s = sum_strided<MAX_HEADS / 4>(ssq + (long)r * nparts, part, nparts, 4);
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if (part == 0) rs[threadIdx.x / 4] = rsqrtf(s * inv_d + eps);
   }
   __syncthreads();
   for (int v = threadIdx.x; v < 64 * 64 / V; v += 256) {

@@ -322,7 +322,7 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
     SrcRows<T> ao{(const T*)a->o_cat, d, B};
     SrcRows<T> bo{(const T*)w->wo, d, d};
     EpiResidual<T> ep{B, d, nullptr, (T*)a->y};
-    launch_gemm<T, 64, 128, 2, 2, 4>(ao, bo, B, d, d, ep, s);
+    launch_gemm_auto<T, 64, 128, 2, 2, 3, 4>(ao, bo, B, d, d, ep, s);
   }
   return DM_OK;
 }
@@ -376,7 +376,7 @@ int dm_linear(int32_t dtype, const void* x, const void* W, const void* r, void* 
     SrcRows<bf16> sa{(const bf16*)x, K, M};
     SrcRows<bf16> sb{(const bf16*)W, K, N};
     EpiResidual<bf16> ep{M, N, (const bf16*)r, (bf16*)y};
-    launch_gemm<bf16, 128, 128, 2, 2, 4>(sa, sb, M, N, K, ep, s);
+    launch_gemm_auto<bf16, 128, 128, 2, 2, 3, 4>(sa, sb, M, N, K, ep, s);
   } else if (dtype == DM_F32) {
     SrcRows<float> sa{(const float*)x, K, M};
     SrcRows<float> sb{(const float*)W, K, N};
@@ -399,7 +399,7 @@ void gemm_any(int ta, int tb, const void* A, const void* Bm, float* C, int M, in
   const T* a = (const T*)A;
   const T* b = (const T*)Bm;
   if (!ta && !tb)
-    launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{a, K, M}, SrcRows<T>{b, K, N}, M, N, K, ep, s);
+    launch_gemm_auto<T, 128, 128, 2, 2, 3, 4>(SrcRows<T>{a, K, M}, SrcRows<T>{b, K, N}, M, N, K, ep, s);
   else if (!ta && tb)
     launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{a, K, M}, SrcKMajor<T>{b, N, N}, M, N, K, ep, s);
   else if (ta && !tb)
