@@ -62,8 +62,8 @@ template <typename T> struct RefineBwdArgs {
   int N, ctx_mod;
   const float* dK; const float* dV;    // grads of the refined rows (rotated K, V)
   long dk_stride; int dk_row0;         //   (b,h) at bh*dk_stride, chunk row p at row dk_row0 + p
-  const float* save1;                  // [N, 4d] raw GEMM-1 outputs of this sweep
-  const float* save2;                  // [N, d] raw v_ctx (mult family)
+  const T* save1;                      // [N, 4d] raw GEMM-1 outputs of this sweep (storage dtype)
+  const T* save2;                      // [N, d] raw v_ctx (mult family)
   const float* glogx; const T* kraw; const T* vraw;
   const float* cos; const float* sin;
   T* dctx;                             // [N, 4d] (packed columns; v_map columns written by EpiVinBwd)
@@ -86,13 +86,13 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
   const long drow = bh * a.dk_stride + (long)(a.dk_row0 + p) * DH;
   const long lrow = (bh * g.Tbuf + t) * DH;
   const long xrow = (long)b * g.Tbuf + t;
-  const float* S1 = a.save1 + (long)m * 4 * d;
+  const T* S1 = a.save1 + (long)m * 4 * d;
   const float* gx = a.glogx + xrow * 2 * d;
   // ---- gather
   const float da = a.dK[drow + jj], db = a.dK[drow + jj + DH / 2];
   const float cs = a.cos[(long)pos * (DH / 2) + jj], sn = a.sin[(long)pos * (DH / 2) + jj];
-  const float kc1 = S1[col_k<DH>(hd, jj, 0)], kc2 = S1[col_k<DH>(hd, jj, 1)];
-  const float gu1 = S1[col_k<DH>(hd, jj, 2)], gu2 = S1[col_k<DH>(hd, jj, 3)];
+  const float kc1 = to_f(S1[col_k<DH>(hd, jj, 0)]), kc2 = to_f(S1[col_k<DH>(hd, jj, 1)]);
+  const float gu1 = to_f(S1[col_k<DH>(hd, jj, 2)]), gu2 = to_f(S1[col_k<DH>(hd, jj, 3)]);
   const float gx1 = gx[hd * DH + jj], gx2 = gx[hd * DH + jj + DH / 2];
   const float kr1 = to_f(a.kraw[lrow + jj]), kr2 = to_f(a.kraw[lrow + jj + DH / 2]);
   const float dv1 = a.dV[drow + jj], dv2 = a.dV[drow + jj + DH / 2];
@@ -104,11 +104,11 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
   if (a.ctx_mod == 0) {
     cv1 = col_vlin<DH>(d, hd, jj);
     cv2 = col_vlin<DH>(d, hd, jj + DH / 2);
-    vc1 = S1[cv1]; vc2 = S1[cv2];
-    gvu1 = S1[cv1 + 32]; gvu2 = S1[cv2 + 32];
+    vc1 = to_f(S1[cv1]); vc2 = to_f(S1[cv2]);
+    gvu1 = to_f(S1[cv1 + 32]); gvu2 = to_f(S1[cv2 + 32]);
   } else {
-    vc1 = a.save2[(long)m * d + c1]; vc2 = a.save2[(long)m * d + c2];
-    gvu1 = S1[3 * d + c1]; gvu2 = S1[3 * d + c2];
+    vc1 = to_f(a.save2[(long)m * d + c1]); vc2 = to_f(a.save2[(long)m * d + c2]);
+    gvu1 = to_f(S1[3 * d + c1]); gvu2 = to_f(S1[3 * d + c2]);
   }
   // ---- key: unrotate, then the convex blend k'' = g k_raw + (1 - g) k_ctx
   const float dk1 = da * cs + db * sn, dk2 = -da * sn + db * cs;
@@ -154,7 +154,7 @@ template <typename T> struct EpiVinBwd {
   CellGeom g;
   int M, ctx_mod;
   float lam;
-  const float* __restrict__ save1;   // [N, 4d]
+  const T* __restrict__ save1;       // [N, 4d]
   const float* __restrict__ sig;     // [B, Tbuf, d]
   T* __restrict__ dctx;              // [N, 4d]
   float* __restrict__ dsig;          // layer accumulator [B, Tbuf, d]
@@ -175,7 +175,7 @@ template <typename T> struct EpiVinBwd {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
           const int col = col0 + 16 * j + lc;
-          vm[i][q][j] = save1[(long)m * 4 * d + 2 * d + col];
+          vm[i][q][j] = to_f(save1[(long)m * 4 * d + 2 * d + col]);
           sg[i][q][j] = sig[xrow * d + col];
           ds[i][q][j] = dsig[xrow * d + col];
         }

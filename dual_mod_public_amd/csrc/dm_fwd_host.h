@@ -46,8 +46,8 @@ template <typename T> struct CellSave {
   float* ssq;        // [K][N, h]      per-head sums of squares of o
   float* stat_m;     // [K][BH, CMAX]  final row max of sweep s
   float* stat_z;     // [K][BH, CMAX]  final row sum of sweep s
-  float* save1;      // [K][N, 4d]     raw sweep GEMM 1 outputs
-  float* save2;      // [K][N, d]      raw v_ctx (mult family)
+  T* save1;          // [K][N, 4d]     raw sweep GEMM 1 outputs (rounded to the storage dtype,
+  T* save2;          // [K][N, d]      raw v_ctx (mult family)    as the reference's GEMM outputs)
   T* vin;            // [K][N, d]      v_in (mult family)
   T* Kin; T* Vin;    // [K+1][BH, CMAX, DH]  intra rows read by sweep s (slot 0 unused: raw rows);
                      //   with last_to_cache only [K] slots: the last sweep writes the cache rows
@@ -66,8 +66,8 @@ CellSave<T> carve_save(const dm_config* c, size_t N, int K, bool tape, bool has_
   w.ssq = cv.take<float>(k * N * h * 4);
   w.stat_m = cv.take<float>(k * BH * CMAX * 4);
   w.stat_z = cv.take<float>(k * BH * CMAX * 4);
-  w.save1 = cv.take<float>(k * N * 4 * d * 4);
-  w.save2 = mult ? cv.take<float>(k * N * d * 4) : nullptr;
+  w.save1 = cv.take<T>(k * N * 4 * d * e);
+  w.save2 = mult ? cv.take<T>(k * N * d * e) : nullptr;
   w.vin = mult ? cv.take<T>(k * N * d * e) : nullptr;
   const size_t slots = tape ? k : k + 1;
   w.Kin = cv.take<T>(slots * BH * CMAX * dh * e);
@@ -120,7 +120,7 @@ template <typename T, int DH>
 void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N, const T* o, const float* ssq,
                 const T* kraw, const T* vraw, const float* glogx, const float* sig, const float* cos,
                 const float* sin, T* Kout, T* Vout, long out_stride, int out_row0, T* vin, float* gvu,
-                float* save1, float* save2, hipStream_t s) {
+                T* save1, T* save2, hipStream_t s) {
   const T* normw = (const T*)w->norm_ctx_w;
   SrcRowsRs<T> sa{o, c->d, N, ssq, c->h, 1.0f / (float)c->d, c->rms_eps};
   SrcRows<T> sb{(const T*)w->w_sweep, c->d, 4 * c->d};

@@ -524,7 +524,7 @@ template <typename T, int DH> struct EpiSweep1 {
   T* __restrict__ Kout; T* __restrict__ Vout;             // refined rows: (b,h) at bh*out_stride,
   long out_stride; int out_row0;                          //   chunk row p at row out_row0 + p
   T* __restrict__ vin; float* __restrict__ gvu;
-  float* __restrict__ save;
+  T* __restrict__ save;
 
   // The epilogue's global inputs are gathered first (prefetch), then combined with
   // the accumulators and stored (apply): all loads precede all stores, so the
@@ -606,7 +606,7 @@ template <typename T, int DH> struct EpiSweep1 {
       for (int q = 0; q < 4; ++q)
         if (mq0 + q < M)
 #pragma unroll
-          for (int j = 0; j < FN; ++j) save[(long)(mq0 + q) * 4 * d + col0 + 16 * j + lc] = a[j][q];
+          for (int j = 0; j < FN; ++j) save[(long)(mq0 + q) * 4 * d + col0 + 16 * j + lc] = from_f<T>(a[j][q]);
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -659,7 +659,7 @@ template <typename T, int DH> struct EpiSweep2 {
   const float* __restrict__ gvu;
   T* __restrict__ Vout;
   long out_stride; int out_row0;
-  float* __restrict__ save2;
+  T* __restrict__ save2;
 
   template <int FM, int FN>
   DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
@@ -696,7 +696,7 @@ template <typename T, int DH> struct EpiSweep2 {
           const float gv = sigmoidf_(gx[i][q][j] + gu[i][q][j]);
           Vout[((long)b * g.h + hd) * out_stride + (long)(out_row0 + p) * DH + e] =
               from_f<T>(gv * vr[i][q][j] + (1.f - gv) * acc[i][j][q]);
-          if (save2 != nullptr) save2[(long)m * d + col] = acc[i][j][q];
+          if (save2 != nullptr) save2[(long)m * d + col] = from_f<T>(acc[i][j][q]);
         }
       }
   }
