@@ -43,6 +43,11 @@ from dual_mod_public_amd.synthetic import make_input, make_state_dict  # noqa: E
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 COPY_CAL_BYTES = 256 << 20  # --copy-calibration: bytes read (and written) per copy dispatch
+# HBM bytes per launch of the roofline kernels (read + written), from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE passes over this script (profiles/traffic_sweep1_decode.md has the commands and raw
+# readings), each scaled by what the counter reads for the 256 MiB --copy-calibration copy.
+# sweep1: tape-mode launches at C3; dec_read: launches at P = 32768..32783.
+TRAFFIC_BYTES = {"sweep1": 34.24e6, "dec_read": 8614.3e6}
 TIMING_NOTE = ("avg_launch_ms: per-dispatch span from the device clock (s_memrealtime, first block "
                "start to last block end), recorded by the kernel itself in the timed region; "
                "avg_launch_ms_events: HIP event pair around each launch on its stream (adds queue time)")
@@ -167,7 +172,7 @@ def bench_decode(dev, steps_override=None):
         "roofline": {"bound": "hbm", "achieved": read_bytes_per_launch / read_avg_s / 1e9,
                      "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": read_bytes_per_launch / read_avg_s / 1e9 / PEAK_HBM_GBS,
-                     "traffic": None, "kernel": "k_decode_partial",
+                     "traffic": TRAFFIC_BYTES["dec_read"], "kernel": "k_decode_partial",
                      "avg_launch_ms": read_avg_ms, "avg_launch_ms_events": kt.avg_ms,
                      "timing": TIMING_NOTE, "launches": kt.n},
         "path_frac_of_hbm_peak": total / wall / 1e9 / PEAK_HBM_GBS,
@@ -187,6 +192,8 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 256 MiB device copy 3x (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time only the headline mode (no forward-only / other-backward-mode lines)")
     ap.add_argument("--recompute", action="store_true",
                     help="headline without the forward tape (backward recomputes every cell)")
     args = ap.parse_args()
@@ -251,9 +258,10 @@ def main():
     with L.KernelTimer(args.kernel, max_launches=args.steps * per_step_launches * 2 + 64) as kt:
         dt = timed(step, args.steps)
     # forward alone, and the other backward mode (reported beside the headline)
-    dt_fwd = timed(step_fwd, args.steps)
-    dt_other = None
-    if fwdbwd:
+    dt_fwd = dt_other = None
+    if not args.headline_only:
+        dt_fwd = timed(step_fwd, args.steps)
+    if fwdbwd and not args.headline_only:
         other = make_step(not use_tape)
         other()
         dt_other = timed(other, args.steps)
@@ -284,17 +292,19 @@ def main():
                    "global_batch": B, "seq_len": T, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": (achieved / PEAK_BF16_TFLOPS) if achieved else None,
-                     "traffic": None, "kernel": kname, "flops_per_launch": per_launch,
+                     "traffic": TRAFFIC_BYTES.get(args.kernel), "kernel": kname, "flops_per_launch": per_launch,
                      "avg_launch_ms": avg_ms, "avg_launch_ms_events": kt.avg_ms,
                      "timing": TIMING_NOTE if kt.device_avg_ms is not None else "HIP event pairs",
                      "launches": kt.n},
         "path_roofline": {"flops_per_token": fpt, "achieved_tflops": fpt * tokens / dt / 1e12,
                           "frac": fpt * tokens / dt / 1e12 / PEAK_BF16_TFLOPS},
-        "forward_only": {"ms_per_step": dt_fwd * 1e3, "tokens_per_s": tokens / dt_fwd,
-                         "frac": fwd_flops_per_token(d, T, c, K) * tokens / dt_fwd / 1e12 / PEAK_BF16_TFLOPS},
     }
+    if dt_fwd is not None:
+        out["forward_only"] = {"ms_per_step": dt_fwd * 1e3, "tokens_per_s": tokens / dt_fwd,
+                               "frac": fwd_flops_per_token(d, T, c, K) * tokens / dt_fwd / 1e12 / PEAK_BF16_TFLOPS}
     if fwdbwd:
         out["tape_bytes"] = tape.numel()
+    if dt_other is not None:
         out["recompute" if use_tape else "tape"] = {"ms_per_step": dt_other * 1e3,
                                                     "tokens_per_s": tokens / dt_other}
     if not args.no_decode:
