@@ -54,6 +54,8 @@ TIMING_NOTE = ("avg_launch_ms: per-dispatch span from the device clock (s_memrea
 
 # BASELINE config 2 (forward) — the 340M-shape DM layer
 C2 = dict(B=8, T=2048, d=1024, h=16, c=64, K=4, wseed=1, xseed=2)
+# BASELINE config 4 — one layer of the 24-layer d=2048 trunk (16 heads x 128), K from --sweeps
+C4 = dict(B=4, T=4096, d=2048, h=16, c=64, K=4, wseed=1, xseed=2)
 # BASELINE config 5 — incremental decode
 C5 = dict(B=64, d=1024, h=16, P0=32768, steps=256, wseed=3, xseed=4, tseed=5)
 
@@ -188,7 +190,10 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=0)
     ap.add_argument("--kernel", default="sweep1", help="kernel class timed for the roofline")
-    ap.add_argument("--workload", default="fwdbwd", choices=["fwdbwd", "fwd"])
+    ap.add_argument("--workload", default="fwdbwd", choices=["fwdbwd", "fwd", "c4"],
+                    help="fwdbwd: C3 (340M-shape layer fwd+bwd, the headline); fwd: C2 forward; "
+                         "c4: one layer of the config-4 trunk (d=2048, 16x128, B=4, T=4096) fwd+bwd")
+    ap.add_argument("--sweeps", type=int, default=0, help="Jacobi sweeps K per chunk (default 4)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 256 MiB device copy 3x (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -215,7 +220,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    B, T, d, h, c, K = C2["B"], C2["T"], C2["d"], C2["h"], C2["c"], C2["K"]
+    shape = C4 if args.workload == "c4" else C2
+    B, T, d, h, c, K = shape["B"], shape["T"], shape["d"], shape["h"], shape["c"], shape["K"]
+    K = args.sweeps or K
     cfg = DualModConfig(d_model=d, n_heads=h, ctx_mod="mult_res", max_seq_len=T, dtype="bf16")
     sd, cell, x, cos, sin, bufs, Kc, Vc, ocat, y = build_layer(cfg, B, T, dev)
     sched = uniform_chunks(T, c, K)
@@ -224,7 +231,7 @@ def main():
     grads = LayerGrads(cfg, dev)
     dy = make_input((B, T, d), seed=C2["xseed"] + 100).to(dev, torch.bfloat16)
     dx = torch.empty_like(x)
-    fwdbwd = args.workload == "fwdbwd"
+    fwdbwd = args.workload in ("fwdbwd", "c4")
 
     use_tape = fwdbwd and not args.recompute
     tape = cell.new_tape(sched) if fwdbwd else None
@@ -279,16 +286,21 @@ def main():
         kname = args.kernel
     avg_ms = kt.device_avg_ms if kt.device_avg_ms is not None else kt.avg_ms
     achieved = per_launch / (avg_ms / 1e3) / 1e12 if kt.n else None
-    wl = ("C3: 340M-shape DM layer forward + reverse-scan backward (" +
-          ("exact recompute" if not use_tape else "sweep states from the forward's HBM tape") + ")"
-          if fwdbwd else "C2: 340M-shape DM layer forward")
+    mode = "exact recompute" if not use_tape else "sweep states from the forward's HBM tape"
+    if args.workload == "c4":
+        wl = f"C4: one layer of the d=2048 trunk, forward + reverse-scan backward ({mode})"
+    elif fwdbwd:
+        wl = f"C3: 340M-shape DM layer forward + reverse-scan backward ({mode})"
+    else:
+        wl = "C2: 340M-shape DM layer forward"
     out = {
-        "metric": "DM sweep tokens/s/GPU (fwd+bwd, c=64, K=4)" if fwdbwd else
-                  "DM sweep tokens/s/GPU (forward, c=64, K=4)",
+        "metric": f"DM sweep tokens/s/GPU ({'fwd+bwd' if fwdbwd else 'forward'}, c={c}, K={K})" +
+                  (" per layer, C4" if args.workload == "c4" else ""),
         "value": tokens / dt, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": dt * 1e3, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) x and dy, N(0,0.02) weights)",
-        "config": {"workload": wl + ", B=8 T=2048 d=1024 16x64 c=64 K=4, 32 chunks Gauss-Seidel",
+        "config": {"workload": wl + f", B={B} T={T} d={d} {h}x{d // h} c={c} K={K}, {T // c} chunks "
+                               "Gauss-Seidel",
                    "global_batch": B, "seq_len": T, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": (achieved / PEAK_BF16_TFLOPS) if achieved else None,
@@ -311,7 +323,7 @@ def main():
         del cell, bufs, Kc, Vc, ocat, y, x, dx, dy, grads, tape
         torch.cuda.empty_cache()
         out["decode"] = bench_decode(dev, args.decode_steps or None)
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.workload != "c4":
         out["cpu_baseline"] = cpu_baseline(cfg, sd, T, B, fwdbwd)
     print(json.dumps(out), flush=True)
 

@@ -259,7 +259,8 @@ def make_intra_mask(c, dtype=torch.float32):
 def chunk_attend(q_r, k_self_r, v_raw, K_comm, V_comm, K_intra, V_intra,
                  intra_mask, scale):
     """scan_cell_fwd.py:63-85 — [committed | intra (strict lower) | raw self]."""
-    s_intra = _hi(q_r @ K_intra.transpose(-1, -2) * scale) + intra_mask.to(_hi(q_r).dtype)
+    s_intra = _hi(q_r @ K_intra.transpose(-1, -2) * scale)
+    s_intra = s_intra + intra_mask.to(device=s_intra.device, dtype=s_intra.dtype)
     s_self = _hi((q_r * k_self_r).sum(-1, keepdim=True)) * scale
     if K_comm is not None and K_comm.shape[2] > 0:
         s_comm = _hi(q_r @ K_comm.transpose(-1, -2) * scale)

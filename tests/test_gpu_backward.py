@@ -32,20 +32,22 @@ def _gpu():
     L.load()
 
 
-def oracle_grads(cfg, sd, x, dy, cos, sin, sched, dtype=torch.float64, normalize=True, residual=True):
-    """dx and parameter grads of y = [x +] W_O DM([attn_norm](x)) by autograd through the oracle."""
-    sdg = {k: v.to(dtype).clone().requires_grad_(True) for k, v in sd.items()}
-    xg = x.to(dtype).clone().requires_grad_(True)
+def oracle_grads(cfg, sd, x, dy, cos, sin, sched, dtype=torch.float64, normalize=True, residual=True,
+                 device="cpu"):
+    """dx and parameter grads of y = [x +] W_O DM([attn_norm](x)) by autograd through the oracle
+    (on the CPU, or with device="cuda" the same torch code on the GPU for the large shapes)."""
+    sdg = {k: v.to(device, dtype).clone().requires_grad_(True) for k, v in sd.items()}
+    xg = x.to(device, dtype).clone().requires_grad_(True)
     with torch.enable_grad():
         if normalize:
             xh = O.rms_norm(xg, sdg["attn_norm.weight"], 1e-5)
         else:
             xh = xg
-        o = O.layer_forward(cfg, sdg, xh, cos.to(dtype), sin.to(dtype), sched)[0]
+        o = O.layer_forward(cfg, sdg, xh, cos.to(device, dtype), sin.to(device, dtype), sched)[0]
         y = O.dm_oracle._lin(o, sdg, "wo")
         if residual:
             y = y + xg
-        (y * dy.to(dtype)).sum().backward()
+        (y * dy.to(device, dtype)).sum().backward()
     g = {k: v.grad for k, v in sdg.items() if v.grad is not None}
     return xg.grad, g
 
@@ -227,6 +229,24 @@ def test_layer_grads_340m_shape_bf16():
     dx_ref, g_ref = oracle_grads(cfg, {k: v.float() for k, v in sd.items()}, x.float(), dy.float(),
                                  c32, s32, sched, dtype=torch.float32)
     compare("bf16 340m", dx, g, dx_ref, g_ref, BF16_TOL)
+
+
+def test_layer_grads_340m_shape_bf16_T2048():
+    """BASELINE config 3's bf16 leg: the bench shape itself (B=8, T=2048, d=1024, 16x64,
+    c=64, K=4), bf16 storage, forward tape, against autograd through the oracle's
+    chunked-Jacobi layer at the same K, run in fp32 torch on the GPU (the CPU would
+    take minutes at this size)."""
+    say("bwd bf16 d=1024 B=8 T=2048 c=64 K=4 (tape) vs fp32 oracle on the GPU")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    cfg = cfg_of(d=1024, h=16, T=2048)
+    B, T = 8, 2048
+    sd, x, _, (c32, s32) = setup(cfg, B, T)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(13), dtype=torch.float32)
+    sched = uniform_chunks(T, 64, 4)
+    _, dx, g = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.bfloat16, tape=True)
+    dx_ref, g_ref = oracle_grads(cfg, {k: v.float() for k, v in sd.items()}, x.float(), dy, c32, s32, sched,
+                                 dtype=torch.float32, device=DEV)
+    compare("bf16 340m T=2048", dx, g, dx_ref, g_ref, BF16_TOL)
 
 
 def test_module_autograd_matches_oracle():
