@@ -1,12 +1,12 @@
-// Kernels of the reverse-scan backward with exact recompute
+// Kernels of the reverse-scan backward
 // (engines/wavescan/cells/fused_sweep.py:1557-1850 semantics, own design).
 //
-// Per cell, sweeps run in reverse. For sweep s with recomputed state:
+// Per cell, sweeps run in reverse. For sweep s with its saved (or recomputed) state:
 //   k_refine_bwd  VJP of the blend/gate/RoPE epilogue of the sweep-s refine:
 //                 grads of the refined rows -> dctx (packed GEMM-1 column order),
 //                 dv_ctx, and the layer accumulators dglogx / dkraw / dvraw
 //   EpiVinBwd     epilogue of dv_in = dv_ctx . W_vctx: tanh / sigmoid VJP of v_in
-//   EpiDuBwd      epilogue of du = dctx . W_sweep (+ lam dv_in): g = du * w_ctx,
+//   k_du_epi      after the split-K GEMM du = dctx . W_sweep (+ lam dv_in): g = du * w_ctx,
 //                 per-row partial <g, o> for the RMS VJP, norm_ctx weight partials
 //   k_attn_bwd    attention VJP of sweep s per (b, h): intra rows (strict lower)
 //                 + raw self column; accumulates the committed part's G, Dbar
@@ -202,73 +202,59 @@ template <typename T> struct EpiVinBwd {
 };
 
 // ---------------------------------------------------------------------------
-// du = dctx . W_sweep (+ lam dv_in) epilogue: RMS VJP inputs
-//   gw = du * w (fp32), rowdot[m, col0 / TN] = sum over the wave's columns of gw * o,
-//   dnw[row0 / TM][col] += sum over the wave's rows of du * o * r   (norm_ctx.weight)
+// RMS-VJP inputs from the split-K slices of du = dctx . W_sweep (+ lam dv_in):
+//   gw = du * w (fp32), rowdot[m, chunk] = sum over the chunk's DU_EPI_TN columns of gw * o,
+//   dnw[m / 16][col] += sum over the 16 rows of du * o * r   (norm_ctx.weight)
+// One block per (16 rows, 64 columns): wave q takes rows 4q..4q+3, lane = column.
+// Slices are summed in order z = 0..S-1; every load is issued before the first add.
 // ---------------------------------------------------------------------------
-template <typename T> struct EpiDuBwd {
-  int M, d, h, nrd;
-  float inv_d, eps;
-  const float* __restrict__ lamdv;   // [M, d] or nullptr
-  const T* __restrict__ o;           // [M, d] this sweep's o
-  const float* __restrict__ ssq;     // [M, h]
-  const T* __restrict__ normw;       // [d]
-  float* __restrict__ gw;            // [M, d]
-  float* __restrict__ rowdot;        // [M, nrd]
-  float* __restrict__ dnw;           // [ceil(Mmax/TM), d] partials (+=)
-  template <int FM, int FN>
-  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
-    const int lane = threadIdx.x & 63, lc = lane & 15;
-    float ov[FM][4][FN], ld[FM][4][FN], rr[FM][4], wv[FN], dn[FN];
+constexpr int DU_EPI_TN = 64;
+template <typename T, int S>
+static __global__ __launch_bounds__(256) void k_du_epi(int M, int d, int h, float inv_d, float eps,
+                                                       const float* __restrict__ part,
+                                                       const float* __restrict__ lamdv, const T* __restrict__ o,
+                                                       const float* __restrict__ ssq, const T* __restrict__ normw,
+                                                       float* __restrict__ gw, float* __restrict__ rowdot,
+                                                       float* __restrict__ dnw) {
+  __shared__ float cs[4][DU_EPI_TN];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m0 = blockIdx.x * 16 + 4 * wave, col = blockIdx.y * DU_EPI_TN + lane;
+  const long n = (long)M * d;
+  float pv[S][4], lv[4], ov[4], ss[4];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      wv[j] = to_f(normw[col0 + 16 * j + lc]);
-      dn[j] = 0.f;
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int m = min(m0 + i, M - 1);
+    const long idx = (long)m * d + col;
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int z = 0; z < S; ++z) pv[z][i] = part[z * n + idx];
+    lv[i] = lamdv != nullptr ? lamdv[idx] : 0.f;
+    ov[i] = to_f(o[idx]);
+    // the row's h partial sums of squares, split over the wave's lanes
+    ss[i] = lane < h ? ssq[(long)m * h + lane] : 0.f;
+  }
+  const float w = to_f(normw[col]);
+  float dn = 0.f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        int m = row0 + 16 * i + 4 * (lane >> 4) + q;
-        m = m < M ? m : 0;
-        // the 16 lanes holding row m split its h partial sums
-        const float s = group16_sum(sum_strided<MAX_HEADS / 16>(ssq + (long)m * h, lc, h, 16));
-        rr[i][q] = rsqrtf(s * inv_d + eps);
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + i;
+    float du = pv[0][i];
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int col = col0 + 16 * j + lc;
-          ov[i][q][j] = to_f(o[(long)m * d + col]);
-          ld[i][q][j] = lamdv != nullptr ? lamdv[(long)m * d + col] : 0.f;
-        }
-      }
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
-        const bool ok = m < M;
-        float dot = 0.f;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const float du = ok ? acc[i][j][q] + ld[i][q][j] : 0.f;
-          const float gv = du * wv[j];
-          dot += gv * ov[i][q][j];
-          dn[j] += du * ov[i][q][j] * rr[i][q];
-          if (ok) gw[(long)m * d + col0 + 16 * j + lc] = gv;
-        }
-        dot = group16_sum(dot);
-        if (ok && lc == 0) rowdot[(long)m * nrd + col0 / (FN * 16)] = dot;
-      }
-    // column sums over the wave's rows: lanes l, l^16, l^32, l^48 share a column
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      float v = dn[j];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      if (lane < 16) dnw[(long)(row0 / (FM * 16)) * d + col0 + 16 * j + lc] += v;
+    for (int z = 1; z < S; ++z) du += pv[z][i];
+    du += lv[i];
+    const float r = rsqrtf(wave_sum(ss[i]) * inv_d + eps);
+    const float g = du * w;
+    const float dot = wave_sum(g * ov[i]);
+    if (m < M) {
+      gw[(long)m * d + col] = g;
+      dn += du * ov[i] * r;
+      if (lane == 0) rowdot[(long)m * (d / DU_EPI_TN) + blockIdx.y] = dot;
     }
   }
-};
+  cs[wave][lane] = dn;
+  __syncthreads();
+  if (wave == 0) dnw[(long)blockIdx.x * d + col] += cs[0][lane] + cs[1][lane] + cs[2][lane] + cs[3][lane];
+}
+
 
 // ---------------------------------------------------------------------------
 // attention VJP of one sweep, two blocks per (b, h), 4 waves x 16 rows each:
@@ -281,7 +267,7 @@ template <typename T> struct AttnBwdArgs {
   const T* qr; const T* kself; const T* vraw;          // layer buffers
   const T* Kin; const T* Vin; long in_stride; int in_row0;   // intra rows read by this sweep
   const T* o; const float* ssq;                        // this sweep's o [N, d], ssq [N, h]
-  const float* gw; const float* rowdot; int nrd;       // RMS VJP inputs (EpiDuBwd)
+  const float* gw; const float* rowdot; int nrd;       // RMS VJP inputs (k_du_epi)
   const float* docat;                                  // [B, Tbuf, d] upstream grad of o_cat, or nullptr
   const float* stat_m; const float* stat_z;            // [B*h, c] final row max / sum of the sweep
   const float* Mx;                                     // committed row max [B*h, c] or nullptr

@@ -24,7 +24,8 @@ template <typename T> struct BwdWs {
   CellSave<T> sv;                       // every sweep's state
   T *dctx, *dvc;                        // [K][N, 4d], [K][N, d]
   float *dKa, *dVa, *dKb, *dVb;         // [B*h, CMAX, dh] grads of the intra rows (ping-pong)
-  float *lamdv, *gw, *rowdot;           // [N, d], [N, d], [N, NRD]
+  float *lamdv, *gw, *rowdot;           // [N, d], [N, d], [N, d / DU_EPI_TN]
+  float *du_part;                       // [DU_SPLIT, N, d] split-K slices of du
   float *G, *Dbar;                      // [B*h, CMAX, dh], [B*h, CMAX]
   float *dq_part;                       // [nsplit, B*h, CMAX, dh]
   // weight grads of the sweeps, one GEMM per layer: the cells' transposed operands
@@ -41,8 +42,8 @@ template <typename T> struct BwdWs {
   size_t bytes;
 };
 
-constexpr int NSLOT_TM = 16;      // rows per norm_ctx-weight partial slot (du GEMM wave tile)
-constexpr int DU_TN = 32;         // columns per row-dot partial (du GEMM wave tile)
+constexpr int NSLOT_TM = 16;      // rows per norm_ctx-weight partial slot (k_du_epi block rows)
+constexpr int DU_SPLIT = 4;       // split-K slices of the du GEMM (K = 4d is long, M = B*c short)
 constexpr int NCHUNK = 64;        // row chunks of the column sums
 // fp32 elements of the split-K partial buffer of the weight-grad GEMMs ([S, M, N], N = d)
 constexpr long KSPLIT_ELEMS(long d) { return 16 * d * d; }
@@ -75,7 +76,8 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.dVb = cv.take<float>(BH * CMAX * dh * 4);
   w.lamdv = cv.take<float>(N * d * 4);
   w.gw = cv.take<float>(N * d * 4);
-  w.rowdot = cv.take<float>(N * (d / DU_TN) * 4);
+  w.rowdot = cv.take<float>(N * (d / DU_EPI_TN) * 4);
+  w.du_part = cv.take<float>(DU_SPLIT * N * d * 4);
   w.G = cv.take<float>(BH * CMAX * dh * 4);
   w.Dbar = cv.take<float>(BH * CMAX * 4);
   w.dq_part = cv.take<float>(comm_splits_max_bwd(cache_T) * BH * CMAX * dh * 4);
@@ -243,12 +245,18 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
         launch_gemm<T, 64, 32, 4, 1, 8>(SrcRows<T>{ws.dvc + sw * NS * d, d, N},
                                         SrcRows<T>{(const T*)w->w_vctx_t, d, d}, N, d, d, ev, s);
       }
-      // du = dctx . W_sweep (+ lam dv_in) -> RMS VJP inputs
+      // du = dctx . W_sweep (+ lam dv_in): split-K slices, then the RMS-VJP inputs
       {
-        EpiDuBwd<T> eu{N, d, h, d / DU_TN, inv_d, c->rms_eps, mult ? ws.lamdv : nullptr, sv.o + sw * NS * d,
-                       sv.ssq + sw * NS * h, (const T*)w->norm_ctx_w, ws.gw, ws.rowdot, ws.dnw};
-        launch_gemm<T, 64, 32, 4, 1, 8>(SrcRows<T>{ws.dctx + sw * NS * 4 * d, 4 * d, N},
-                                        SrcRows<T>{(const T*)w->w_sweep_t, 4 * d, d}, N, d, 4 * d, eu, s);
+        const int S = DU_SPLIT;
+        EpiStoreF32 ep{N, d, 0, ws.du_part, (long)N * d};
+        launch_gemm_splitk<T, 64, 64, 4, 1, sizeof(T) == 2 ? -3 : 4>(
+            SrcRows<T>{ws.dctx + sw * NS * 4 * d, 4 * d, N}, SrcRows<T>{(const T*)w->w_sweep_t, 4 * d, d}, N, d,
+            4 * d, S, ep, s);
+        hipLaunchKernelGGL((k_du_epi<T, DU_SPLIT>), dim3(cdiv(N, 16), d / DU_EPI_TN), dim3(256), 0, s, N, d, h,
+                           inv_d,
+                           c->rms_eps, (const float*)ws.du_part, mult ? (const float*)ws.lamdv : nullptr,
+                           (const T*)(sv.o + sw * NS * d), (const float*)(sv.ssq + sw * NS * h),
+                           (const T*)w->norm_ctx_w, ws.gw, ws.rowdot, ws.dnw);
       }
       // attention VJP of sweep sw
       {
@@ -258,7 +266,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
         float* dKo = sw == 0 ? nullptr : ((K - 1 - sw) % 2 == 0 ? ws.dKa : ws.dKb);
         float* dVo = sw == 0 ? nullptr : ((K - 1 - sw) % 2 == 0 ? ws.dVa : ws.dVb);
         AttnBwdArgs<T> aa{g, qr, kself, vraw, Kin, Vin, in_stride, in_row0, sv.o + sw * NS * d,
-                          sv.ssq + sw * NS * h, ws.gw, ws.rowdot, d / DU_TN,
+                          sv.ssq + sw * NS * h, ws.gw, ws.rowdot, d / DU_EPI_TN,
                           sw == K - 1 ? ws.docat : nullptr, sv.stat_m + sw * (size_t)BH * CMAX,
                           sv.stat_z + sw * (size_t)BH * CMAX, Mx, ws.G, ws.Dbar, sw == K - 1 ? 1 : 0,
                           scale, inv_d, c->rms_eps, dKo, dVo, ws.dkself, ws.dvraw, ws.dq};
