@@ -65,21 +65,21 @@ DM_DEV void load_q_frags(const T* qrow_ptr, bool valid, typename Mfma<T>::frag* 
 // loads can be in flight while the current tile is used). Consecutive lanes take
 // consecutive keys of one 16-byte column chunk, so the transposed V stores of a
 // wave land in one LDS row (no bank conflicts).
-template <typename T, int DH> struct KVRegs {
+template <typename T, int DH, int NT = 256> struct KVRegs {
   static constexpr int VPR = DH / AttnCfg<T, DH>::VEC;             // 16-byte vectors per row
-  static constexpr int NV = AttnCfg<T, DH>::KT * VPR / 256;        // vectors per thread
+  static constexpr int NV = AttnCfg<T, DH>::KT * VPR / NT;         // vectors per thread (NT threads)
   uint4 k[NV], v[NV];
 };
 
 // Load keys [0, nvalid) of a tile; rows >= nvalid become zeros (so 0-probability
 // columns multiply zeros).
-template <typename T, int DH>
+template <typename T, int DH, int NT = 256>
 DM_DEV void load_kv(const T* __restrict__ Kg, const T* __restrict__ Vg, long row_stride, int nvalid,
-                    KVRegs<T, DH>& r) {
-  using R = KVRegs<T, DH>;
+                    KVRegs<T, DH, NT>& r) {
+  using R = KVRegs<T, DH, NT>;
 #pragma unroll
   for (int i = 0; i < R::NV; ++i) {
-    const int v = threadIdx.x + 256 * i;
+    const int v = threadIdx.x + NT * i;
     const int k = v % AttnCfg<T, DH>::KT, c0 = (v / AttnCfg<T, DH>::KT) * AttnCfg<T, DH>::VEC;
     const bool ok = k < nvalid;
     const long off = (long)(ok ? k : 0) * row_stride + c0;
@@ -89,13 +89,13 @@ DM_DEV void load_kv(const T* __restrict__ Kg, const T* __restrict__ Vg, long row
 }
 
 // K rows -> Ks [key][dh], V rows transposed -> Vt [dh][key].
-template <typename T, int DH>
-DM_DEV void store_kv(const KVRegs<T, DH>& r, T* Ks, T* Vt) {
+template <typename T, int DH, int NT = 256>
+DM_DEV void store_kv(const KVRegs<T, DH, NT>& r, T* Ks, T* Vt) {
   using C = AttnCfg<T, DH>;
-  using R = KVRegs<T, DH>;
+  using R = KVRegs<T, DH, NT>;
 #pragma unroll
   for (int i = 0; i < R::NV; ++i) {
-    const int v = threadIdx.x + 256 * i;
+    const int v = threadIdx.x + NT * i;
     const int k = v % C::KT, c0 = (v / C::KT) * C::VEC;
     *reinterpret_cast<uint4*>(Ks + k * C::LDK + c0) = r.k[i];
     const T* ve = reinterpret_cast<const T*>(&r.v[i]);

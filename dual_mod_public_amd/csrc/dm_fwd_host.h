@@ -189,7 +189,10 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
                      scale, o, ssq, last ? ocat : nullptr, last ? o_last : nullptr,
                      sv ? sv->stat_m + sw * (size_t)BH * CMAX : nullptr,
                      sv ? sv->stat_z + sw * (size_t)BH * CMAX : nullptr};
-    launch_k(PROF_ATTEND, k_attend<T, DH>, dim3(BH), dim3(256), 0, s, aa);
+    // 16-row waves; the (b, h) blocks split by query rows until there are >= 256 blocks
+    if (BH >= 256) launch_k(PROF_ATTEND, k_attend<T, DH, 4>, dim3(BH, 1), dim3(256), 0, s, aa);
+    else if (BH >= 128) launch_k(PROF_ATTEND, k_attend<T, DH, 2>, dim3(BH, 2), dim3(128), 0, s, aa);
+    else launch_k(PROF_ATTEND, k_attend<T, DH, 1>, dim3(BH, 4), dim3(64), 0, s, aa);
     T* vin = sv ? sv->vin + sw * NS * d : (T*)ws.vin;
     run_refine<T, DH>(c, w, g, N, o, ssq, kraw, vraw, L->glogx, L->sig, cos, sin, Kout, Vout, out_stride,
                       out_row0, vin, ws.gvu, sv ? sv->save1 + sw * NS * 4 * d : nullptr,

@@ -281,8 +281,9 @@ struct KeyBound {
   int n;
   DM_DEV bool operator()(int, int key) const { return key < n; }
 };
-struct KeyStrictLower {
-  DM_DEV bool operator()(int q, int key) const { return key < q; }
+struct KeyStrictLower {   // q is block-relative; q0 = the block's first query row
+  int q0;
+  DM_DEV bool operator()(int q, int key) const { return key < q + q0; }
 };
 
 template <typename T, int DH>
@@ -360,8 +361,10 @@ template <typename T> struct AttendArgs {
   float* stat_z;    // [B*h, c] final row sum (or nullptr)
 };
 
-template <typename T, int DH>
-static __global__ __launch_bounds__(256) void k_attend(AttendArgs<T> a) {
+// NW waves per block, 16 query rows per wave: block y takes rows [16 NW y, 16 NW (y + 1)),
+// so a (b, h) spreads over 4 / NW blocks (more blocks when B*h alone underfills the GPU).
+template <typename T, int DH, int NW>
+static __global__ __launch_bounds__(64 * NW) void k_attend(AttendArgs<T> a) {
   using C = AttnCfg<T, DH>;
   __shared__ __attribute__((aligned(16))) T lds[C::LDS_ELEMS];
   T* Ks = lds;
@@ -372,13 +375,16 @@ static __global__ __launch_bounds__(256) void k_attend(AttendArgs<T> a) {
   const int b = bh / g.h, hh = bh - b * g.h;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g4 = lane >> 4, col = lane & 15;
-  const int qrow = 16 * wave + col;
+  const int q0 = 16 * NW * (int)blockIdx.y;   // the block's first query row
+  if (q0 >= g.c) return;                       // uniform: no rows in this block
+  const int wq = q0 + 16 * wave;               // the wave's first query row
+  const int qrow = wq + col;
   const long lrow0 = (long)bh * g.Tbuf + g.buf_t0;   // layer-buffer row of chunk row 0
   const int BH = g.B * g.h;
 
-  KVRegs<T, DH> kv;
-  load_kv<T, DH>(a.Kin + (long)bh * a.in_stride + (long)a.in_row0 * DH,
-                 a.Vin + (long)bh * a.in_stride + (long)a.in_row0 * DH, DH, g.c, kv);
+  KVRegs<T, DH, 64 * NW> kv;   // keys < the block's last row (strict lower)
+  load_kv<T, DH, 64 * NW>(a.Kin + (long)bh * a.in_stride + (long)a.in_row0 * DH,
+                          a.Vin + (long)bh * a.in_stride + (long)a.in_row0 * DH, DH, min(g.c, q0 + 16 * NW), kv);
   typename Mfma<T>::frag qf[C::NKS];
   load_q_frags<T, DH>(a.qr + (lrow0 + qrow) * DH, qrow < g.c, qf);
   FlashState<T, DH> st;
@@ -386,7 +392,7 @@ static __global__ __launch_bounds__(256) void k_attend(AttendArgs<T> a) {
   if (a.nsplit == 1) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int q = 16 * wave + 4 * g4 + r;
+      const int q = wq + 4 * g4 + r;
       if (q < g.c) {
         const long o = (long)bh * g.c + q;
         st.m[r] = a.Mx[o];
@@ -398,7 +404,7 @@ static __global__ __launch_bounds__(256) void k_attend(AttendArgs<T> a) {
   } else if (a.nsplit > 1) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int q = 16 * wave + 4 * g4 + r;
+      const int q = wq + 4 * g4 + r;
       if (q < g.c) {
         float M = NEG_INF;
         for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.Mp[((long)s * BH + bh) * g.c + q]);
@@ -435,7 +441,7 @@ static __global__ __launch_bounds__(256) void k_attend(AttendArgs<T> a) {
   float sdot[4], vself[4][C::NDT];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int qc = min(16 * wave + 4 * g4 + r, g.c - 1);
+    const int qc = min(wq + 4 * g4 + r, g.c - 1);
     const T* qp = a.qr + (lrow0 + qc) * DH + col * PER;
     const T* kp = a.kself + (lrow0 + qc) * DH + col * PER;
     float dot = 0.f;
@@ -446,9 +452,9 @@ static __global__ __launch_bounds__(256) void k_attend(AttendArgs<T> a) {
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt) vself[r][dt] = to_f(vp[col + 16 * dt]);
   }
-  store_kv<T, DH>(kv, Ks, Vt);
+  store_kv<T, DH, 64 * NW>(kv, Ks, Vt);
   __syncthreads();
-  flash_tile<T, DH>(qf, Ks, Vt, Ps + wave * 16 * C::LDP, a.scale, KeyStrictLower{}, st);
+  flash_tile<T, DH>(qf, Ks, Vt, Ps + wave * 16 * C::LDP, a.scale, KeyStrictLower{q0}, st);
 
   // raw self column: s_self = scale * <q_r, k_self_r> (fp32), value v_raw
 #pragma unroll
@@ -464,7 +470,7 @@ static __global__ __launch_bounds__(256) void k_attend(AttendArgs<T> a) {
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int q = 16 * wave + 4 * g4 + r;
+    const int q = wq + 4 * g4 + r;
     const float zt = group16_sum(st.z[r]);
     const float inv = 1.0f / zt;
     float sq = 0.f;
