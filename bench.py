@@ -49,8 +49,9 @@ COPY_CAL_BYTES = 256 << 20  # --copy-calibration: bytes read (and written) per c
 # sweep1: tape-mode launches at C3; dec_read: launches at P = 32768..32783.
 TRAFFIC_BYTES = {"sweep1": 34.24e6, "dec_read": 8614.3e6}
 TIMING_NOTE = ("avg_launch_ms: per-dispatch span from the device clock (s_memrealtime, first block "
-               "start to last block end), recorded by the kernel itself in the timed region; "
-               "avg_launch_ms_events: HIP event pair around each launch on its stream (adds queue time)")
+               "start to last block end), recorded by the kernel itself over a second pass of the timed "
+               "steps (instrumented_ms_per_step); avg_launch_ms_events: HIP event pair around each launch "
+               "on its stream (adds queue time)")
 
 # BASELINE config 2 (forward) — the 340M-shape DM layer
 C2 = dict(B=8, T=2048, d=1024, h=16, c=64, K=4, wseed=1, xseed=2)
@@ -153,11 +154,14 @@ def bench_decode(dev, steps_override=None):
     for t in range(4):
         tape.step(x[t], P0 + t, cos, sin, with_wo=True)
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run_all()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # the same steps again (rewriting the same tape slots) with the tape read's timing armed
     with L.KernelTimer("dec_read", max_launches=steps + 8) as kt:
-        t0 = time.perf_counter()
         run_all()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
     tape_bytes = sum(2.0 * B * h * (P0 + t) * dh * 2 for t in range(steps))
     weight_bytes = steps * 12.0 * d * d * 2
     write_bytes = steps * 2.0 * B * d * 2
@@ -262,8 +266,12 @@ def main():
     torch.cuda.synchronize()
     sweeps = sum(k for _, _, k in sched)
     per_step_launches = sweeps * (2 if fwdbwd else 1)
+    # the headline: the timed steps with nothing armed; then the same steps again with
+    # the roofline kernel's per-dispatch timing armed (its device-clock stamps and event
+    # pairs cost ~5% of the step, so they stay out of the headline's clock)
+    dt = timed(step, args.steps)
     with L.KernelTimer(args.kernel, max_launches=args.steps * per_step_launches * 2 + 64) as kt:
-        dt = timed(step, args.steps)
+        dt_instr = timed(step, args.steps)
     # forward alone, and the other backward mode (reported beside the headline)
     dt_fwd = dt_other = None
     if not args.headline_only:
@@ -307,7 +315,7 @@ def main():
                      "traffic": TRAFFIC_BYTES.get(args.kernel), "kernel": kname, "flops_per_launch": per_launch,
                      "avg_launch_ms": avg_ms, "avg_launch_ms_events": kt.avg_ms,
                      "timing": TIMING_NOTE if kt.device_avg_ms is not None else "HIP event pairs",
-                     "launches": kt.n},
+                     "launches": kt.n, "instrumented_ms_per_step": dt_instr * 1e3},
         "path_roofline": {"flops_per_token": fpt, "achieved_tflops": fpt * tokens / dt / 1e12,
                           "frac": fpt * tokens / dt / 1e12 / PEAK_BF16_TFLOPS},
     }
