@@ -46,7 +46,7 @@ constexpr int NSLOT_TM = 16;      // rows per norm_ctx-weight partial slot (k_du
 constexpr int DU_SPLIT = 4;       // split-K slices of the du GEMM (K = 4d is long, M = B*c short)
 constexpr int NCHUNK = 64;        // row chunks of the column sums
 // fp32 elements of the split-K partial buffer of the weight-grad GEMMs ([S, M, N], N = d)
-constexpr long KSPLIT_ELEMS(long d) { return 16 * d * d; }
+constexpr long KSPLIT_ELEMS(long d) { return 32 * d * d; }
 
 template <typename T>
 BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base) {
@@ -140,19 +140,24 @@ void transpose(const T* in, long ld_in, int rows, int cols, int rows_pad, T* out
 template <typename T>
 void gemm_splitk_f32(const T* At, long lda, const T* Bt, long ldb, int Kp, int M, int N, int accumulate, float* part,
                      float* C, hipStream_t s) {
-  const long blocks = (long)(M / 128) * (N / 128);
+  // bf16 with M, N multiples of 256: 256 x 256 blocks (one per CU), >= 256 blocks;
+  // otherwise 128 x 128 blocks, up to ~4 per CU
+  const bool big = sizeof(T) == 2 && M % 256 == 0 && N % 256 == 0;
+  const long blocks = big ? (long)(M / 256) * (N / 256) : (long)(M / 128) * (N / 128);
+  const long target = big ? 256 : 1024;
   int S = 1;
-  while (S < 16 && blocks * S * 2 <= 1024 && (long)S * 2 * M * N <= KSPLIT_ELEMS((long)N) &&
-         (Kp / 64) % (S * 2) == 0)
+  while (S < 16 && blocks * S * (big ? 1 : 2) < target + (big ? 0 : 1) &&
+         (long)S * 2 * M * N <= KSPLIT_ELEMS((long)N) && (Kp / 64) % (S * 2) == 0)
     S *= 2;
+  const SrcRows<T> sa{At, lda, M}, sb{Bt, ldb, N};
   if (S == 1) {
     EpiStoreF32 ep{M, N, accumulate, C};
-    launch_gemm_auto<T, 128, 128, 2, 2, 3, 4>(SrcRows<T>{At, lda, M}, SrcRows<T>{Bt, ldb, N}, M, N, Kp, ep, s);
+    launch_gemm_big<T>(sa, sb, M, N, Kp, ep, s);
     return;
   }
   EpiStoreF32 ep{M, N, 0, part, (long)M * N};
-  launch_gemm_splitk<T, 128, 128, 2, 2, sizeof(T) == 2 ? -3 : 4>(SrcRows<T>{At, lda, M}, SrcRows<T>{Bt, ldb, N}, M, N,
-                                                                   Kp, S, ep, s);
+  if (big) launch_gemm_splitk<T, 256, 256, 2, 2, (sizeof(T) == 2 ? -2 : 4)>(sa, sb, M, N, Kp, S, ep, s);
+  else launch_gemm_splitk<T, 128, 128, 2, 2, sizeof(T) == 2 ? -3 : 4>(sa, sb, M, N, Kp, S, ep, s);
   hipLaunchKernelGGL(k_sum_splits, dim3(cdiv((long)M * N, 256)), dim3(256), 0, s, S, (long)M * N,
                      (const float*)part, C, accumulate);
 }
@@ -199,7 +204,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   // ---- W_O: do_cat = dy . W_O ; dW_O += dy^T . ocat
   {
     EpiStoreF32 ep{BT, d, 0, ws.docat};
-    launch_gemm_auto<T, 128, 128, 2, 2, 3, 4>(SrcRows<T>{dy, d, BT}, SrcRows<T>{(const T*)w->wo_t, d, d}, BT, d, d,
+    launch_gemm_big<T>(SrcRows<T>{dy, d, BT}, SrcRows<T>{(const T*)w->wo_t, d, d}, BT, d, d,
                                                ep, s);
     gemm_tn<T>(dy, d, ocat, d, gr->wo, d, d, BT, 1, ws.tA, ws.tB, ws.kpart, s);
   }
@@ -331,7 +336,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   gemm_tn<T>(ws.dproj, (long)nproj * d, xhat, d, ws.dWp, nproj * d, d, BT, 0, ws.tA, ws.tB, ws.kpart, s);
   {
     EpiStoreF32 ep{BT, d, 0, ws.dxhat};
-    launch_gemm_auto<T, 128, 128, 2, 2, 3, 4>(SrcRows<T>{ws.dproj, (long)nproj * d, BT},
+    launch_gemm_big<T>(SrcRows<T>{ws.dproj, (long)nproj * d, BT},
                                       SrcRows<T>{(const T*)w->w_proj_t, (long)nproj * d, d}, BT, d, nproj * d, ep, s);
   }
   // unpack the packed weight grads into the reference layout

@@ -134,6 +134,21 @@ void launch_gemm_auto(const SA& sa, const SB& sb, int M, int N, int K, const EPI
   launch_gemm<T, BM, BN, WM, WN, D>(sa, sb, M, N, K, epi, s, prof_cls);
 }
 
+// Large GEMMs (M, N multiples of 256, bf16, K-contiguous, K a multiple of 64): 256 x 256
+// blocks of four 128 x 128 wave tiles with two 64 KB direct-to-LDS stages (a quarter of
+// the LDS traffic per MFMA of 64 x 64 wave tiles); otherwise 128 x 128.
+template <typename T, class SA, class SB, class EPI>
+void launch_gemm_big(const SA& sa, const SB& sb, int M, int N, int K, const EPI& epi, hipStream_t s,
+                     int prof_cls = PROF_NONE) {
+  if constexpr (sizeof(T) == 2 && !SA::KMAJOR && !SB::KMAJOR) {
+    if (M % 256 == 0 && N % 256 == 0 && K % 64 == 0) {
+      launch_gemm<T, 256, 256, 2, 2, -2>(sa, sb, M, N, K, epi, s, prof_cls);
+      return;
+    }
+  }
+  launch_gemm_auto<T, 128, 128, 2, 2, 3, 4>(sa, sb, M, N, K, epi, s, prof_cls);
+}
+
 // Split-K: S slices of K/S each (K/S a multiple of the k-tile), slice z in grid.z.
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
 void launch_gemm_splitk(const SA& sa, const SB& sb, int M, int N, int K, int S, const EPI& epi, hipStream_t s,

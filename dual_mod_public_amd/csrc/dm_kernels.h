@@ -194,13 +194,16 @@ template <typename T, int DH> struct EpiProj {
   T* __restrict__ qr; T* __restrict__ kraw; T* __restrict__ kself; T* __restrict__ vraw;
   float* __restrict__ glogx; float* __restrict__ sig;
 
+  // The wave tile spans whole heads (FN * 16 a multiple of DH); within each head
+  // columns j and j + DH/32 of the tile are the RoPE pair (jj, jj + DH/2).
   template <int FM, int FN>
   DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
-    static_assert(FN * 16 == DH, "projection wave tile must be one head wide");
-    constexpr int HF = FN / 2;
+    static_assert((FN * 16) % DH == 0, "projection wave tile must span whole heads");
+    constexpr int NHW = FN * 16 / DH;   // heads per wave tile
+    constexpr int FH = DH / 16;         // 16-column tiles per head
+    constexpr int HF = FH / 2;
     const int lane = threadIdx.x & 63, lc = lane & 15;
     const int seg = col0 / d, c0 = col0 - seg * d;
-    const int hh = c0 / DH;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -208,36 +211,41 @@ template <typename T, int DH> struct EpiProj {
         const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
         if (m >= M) continue;
         const int b = m / Tl, tl = m - b * Tl;
-        const long hrow = (((long)b * h + hh) * Tbuf + buf_t0 + tl) * DH;
         const long xrow = (long)b * Tbuf + buf_t0 + tl;
-        if (seg <= 1) {
-          const long rrow = (long)(rope_t0 + tl) * (DH / 2);
 #pragma unroll
-          for (int j = 0; j < HF; ++j) {
-            const int jj = 16 * j + lc;
-            const float a = acc[i][j][q], bb = acc[i][j + HF][q];
-            const float cs = cos[rrow + jj], sn = sin[rrow + jj];
-            if (seg == 0) {
-              qr[hrow + jj] = from_f<T>(a * cs - bb * sn);
-              qr[hrow + jj + DH / 2] = from_f<T>(bb * cs + a * sn);
-            } else {
-              kraw[hrow + jj] = from_f<T>(a);
-              kraw[hrow + jj + DH / 2] = from_f<T>(bb);
-              kself[hrow + jj] = from_f<T>(a * cs - bb * sn);
-              kself[hrow + jj + DH / 2] = from_f<T>(bb * cs + a * sn);
+        for (int hb = 0; hb < NHW; ++hb) {
+          const int hh = c0 / DH + hb;
+          const long hrow = (((long)b * h + hh) * Tbuf + buf_t0 + tl) * DH;
+          if (seg <= 1) {
+            const long rrow = (long)(rope_t0 + tl) * (DH / 2);
+#pragma unroll
+            for (int j = 0; j < HF; ++j) {
+              const int jj = 16 * j + lc;
+              const float a = acc[i][hb * FH + j][q], bb = acc[i][hb * FH + j + HF][q];
+              const float cs = cos[rrow + jj], sn = sin[rrow + jj];
+              if (seg == 0) {
+                qr[hrow + jj] = from_f<T>(a * cs - bb * sn);
+                qr[hrow + jj + DH / 2] = from_f<T>(bb * cs + a * sn);
+              } else {
+                kraw[hrow + jj] = from_f<T>(a);
+                kraw[hrow + jj + DH / 2] = from_f<T>(bb);
+                kself[hrow + jj] = from_f<T>(a * cs - bb * sn);
+                kself[hrow + jj + DH / 2] = from_f<T>(bb * cs + a * sn);
+              }
             }
-          }
-        } else if (seg == 2) {
+          } else if (seg == 2) {
 #pragma unroll
-          for (int j = 0; j < FN; ++j) vraw[hrow + 16 * j + lc] = from_f<T>(acc[i][j][q]);
-        } else if (seg <= 4) {
+            for (int j = 0; j < FH; ++j) vraw[hrow + 16 * j + lc] = from_f<T>(acc[i][hb * FH + j][q]);
+          }
+        }
+        if (seg == 3 || seg == 4) {
           const int gs = seg - 3;
 #pragma unroll
           for (int j = 0; j < FN; ++j) {
             const int col = c0 + 16 * j + lc;
             glogx[xrow * 2 * d + gs * d + col] = acc[i][j][q] + bias[gs * d + col];
           }
-        } else {
+        } else if (seg == 5) {
 #pragma unroll
           for (int j = 0; j < FN; ++j) {
             const int col = c0 + 16 * j + lc;

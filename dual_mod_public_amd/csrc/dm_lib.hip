@@ -399,7 +399,7 @@ void gemm_any(int ta, int tb, const void* A, const void* Bm, float* C, int M, in
   const T* a = (const T*)A;
   const T* b = (const T*)Bm;
   if (!ta && !tb)
-    launch_gemm_auto<T, 128, 128, 2, 2, 3, 4>(SrcRows<T>{a, K, M}, SrcRows<T>{b, K, N}, M, N, K, ep, s);
+    launch_gemm_big<T>(SrcRows<T>{a, K, M}, SrcRows<T>{b, K, N}, M, N, K, ep, s);
   else if (!ta && tb)
     launch_gemm<T, 128, 128, 2, 2, 4>(SrcRows<T>{a, K, M}, SrcKMajor<T>{b, N, N}, M, N, K, ep, s);
   else if (ta && !tb)
