@@ -110,6 +110,11 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
     vc1 = to_f(a.save2[(long)m * d + c1]); vc2 = to_f(a.save2[(long)m * d + c2]);
     gvu1 = to_f(S1[3 * d + c1]); gvu2 = to_f(S1[3 * d + c2]);
   }
+  // the accumulators' current values, loaded with the gather (one memory round trip)
+  float* dgx = a.dglogx + xrow * 2 * d;
+  const float ogx1 = dgx[c1], ogx2 = dgx[c2], ogxv1 = dgx[d + c1], ogxv2 = dgx[d + c2];
+  const float okr1 = a.dkraw[lrow + jj], okr2 = a.dkraw[lrow + jj + DH / 2];
+  const float ovr1 = a.dvraw[lrow + jj], ovr2 = a.dvraw[lrow + jj + DH / 2];
   // ---- key: unrotate, then the convex blend k'' = g k_raw + (1 - g) k_ctx
   const float dk1 = da * cs + db * sn, dk2 = -da * sn + db * cs;
   const float g1 = sigmoidf_(gx1 + gu1), g2 = sigmoidf_(gx2 + gu2);
@@ -120,11 +125,10 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
   D[col_k<DH>(hd, jj, 1)] = from_f<T>(dk2 * (1.f - g2));
   D[col_k<DH>(hd, jj, 2)] = from_f<T>(dl1);
   D[col_k<DH>(hd, jj, 3)] = from_f<T>(dl2);
-  float* dgx = a.dglogx + xrow * 2 * d;
-  dgx[c1] += dl1;
-  dgx[c2] += dl2;
-  a.dkraw[lrow + jj] += dk1 * g1;
-  a.dkraw[lrow + jj + DH / 2] += dk2 * g2;
+  dgx[c1] = ogx1 + dl1;
+  dgx[c2] = ogx2 + dl2;
+  a.dkraw[lrow + jj] = okr1 + dk1 * g1;
+  a.dkraw[lrow + jj + DH / 2] = okr2 + dk2 * g2;
   // ---- value: v'' = g_v v_raw + (1 - g_v) v_ctx
   const float gv1 = sigmoidf_(gxv1 + gvu1), gv2 = sigmoidf_(gxv2 + gvu2);
   const float dlv1 = dv1 * (vr1 - vc1) * gv1 * (1.f - gv1);
@@ -140,10 +144,10 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
     D[3 * d + c1] = from_f<T>(dlv1);
     D[3 * d + c2] = from_f<T>(dlv2);
   }
-  dgx[d + c1] += dlv1;
-  dgx[d + c2] += dlv2;
-  a.dvraw[lrow + jj] += dv1 * gv1;
-  a.dvraw[lrow + jj + DH / 2] += dv2 * gv2;
+  dgx[d + c1] = ogxv1 + dlv1;
+  dgx[d + c2] = ogxv2 + dlv2;
+  a.dvraw[lrow + jj] = ovr1 + dv1 * gv1;
+  a.dvraw[lrow + jj + DH / 2] = ovr2 + dv2 * gv2;
 }
 
 // ---------------------------------------------------------------------------
@@ -233,6 +237,7 @@ static __global__ __launch_bounds__(256) void k_du_epi(int M, int d, int h, floa
     ss[i] = lane < h ? ssq[(long)m * h + lane] : 0.f;
   }
   const float w = to_f(normw[col]);
+  const float dn_old = wave == 0 ? dnw[(long)blockIdx.x * d + col] : 0.f;
   float dn = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -252,7 +257,7 @@ static __global__ __launch_bounds__(256) void k_du_epi(int M, int d, int h, floa
   }
   cs[wave][lane] = dn;
   __syncthreads();
-  if (wave == 0) dnw[(long)blockIdx.x * d + col] += cs[0][lane] + cs[1][lane] + cs[2][lane] + cs[3][lane];
+  if (wave == 0) dnw[(long)blockIdx.x * d + col] = dn_old + (cs[0][lane] + cs[1][lane] + cs[2][lane] + cs[3][lane]);
 }
 
 
@@ -331,6 +336,21 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
 #pragma unroll
       for (int e = 0; e < EPT; ++e) dc[e] = 0.f;
     }
+    // the accumulators' current values, loaded with the inputs (one memory round trip)
+    const long lr = (lrow0 + ic) * DH + e0;
+    float acc0[EPT], acc1[EPT], gold[EPT];
+    float dbold = 0.f, mx = 0.f;
+    if (role == 0) {
+      load_vec<float, EPT>(a.dq + lr, acc0);
+      if (a.Mx != nullptr) {
+        mx = a.Mx[(long)bh * c + ic];
+        load_vec<float, EPT>(a.G + ((long)bh * CMAX + ic) * DH + e0, gold);
+        dbold = a.Dbar[(long)bh * CMAX + ic];
+      }
+    } else {
+      load_vec<float, EPT>(a.dkself + lr, acc0);
+      load_vec<float, EPT>(a.dvraw + lr, acc1);
+    }
     float ss = 0.f, dot = 0.f;
     ss = sum_strided<MAX_HEADS / 4>(a.ssq + n * g.h, part, g.h, 4);
     dot = sum_strided<MAX_ROWDOT / 4>(a.rowdot + n * a.nrd, part, a.nrd, 4);
@@ -358,31 +378,26 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
     if (part == 0) { sM[i] = Mi; sZ[i] = Zi; sD[i] = Dp; }
     // committed part: alpha = exp(m_comm - M) / Z
     if (role == 0 && a.Mx != nullptr && ok) {
-      const float alpha = __expf(a.Mx[(long)bh * c + i] - Mi) / Zi;
-      float* Gr = a.G + ((long)bh * CMAX + i) * DH + e0;
+      const float alpha = __expf(mx - Mi) / Zi;
+      float gn[EPT];
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) Gr[e] = (a.first ? 0.f : Gr[e]) + alpha * dO[e];
-      if (part == 0) a.Dbar[(long)bh * CMAX + i] = (a.first ? 0.f : a.Dbar[(long)bh * CMAX + i]) + alpha * Dp;
+      for (int e = 0; e < EPT; ++e) gn[e] = (a.first ? 0.f : gold[e]) + alpha * dO[e];
+      store_vec<float, EPT>(a.G + ((long)bh * CMAX + i) * DH + e0, gn);
+      if (part == 0) a.Dbar[(long)bh * CMAX + i] = (a.first ? 0.f : dbold) + alpha * Dp;
     }
     if (ok) {
-      const long lr = (lrow0 + i) * DH + e0;
       if (role == 0) {
-        float a2[EPT];
-        load_vec<float, EPT>(a.dq + lr, a2);
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) a2[e] += a.scale * dss * ks[e];
-        store_vec<float, EPT>(a.dq + lr, a2);
+        for (int e = 0; e < EPT; ++e) acc0[e] += a.scale * dss * ks[e];
+        store_vec<float, EPT>(a.dq + lr, acc0);
       } else {
-        float a0[EPT], a1[EPT];
-        load_vec<float, EPT>(a.dkself + lr, a0);
-        load_vec<float, EPT>(a.dvraw + lr, a1);
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
-          a0[e] += a.scale * dss * q[e];
-          a1[e] += ps * dO[e];
+          acc0[e] += a.scale * dss * q[e];
+          acc1[e] += ps * dO[e];
         }
-        store_vec<float, EPT>(a.dkself + lr, a0);
-        store_vec<float, EPT>(a.dvraw + lr, a1);
+        store_vec<float, EPT>(a.dkself + lr, acc0);
+        store_vec<float, EPT>(a.dvraw + lr, acc1);
       }
     } else {
 #pragma unroll
@@ -404,6 +419,13 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
 
   // ---- phase 2: query-major (rows i = 16 wave + ..): dS, then dQ = dS . K
   if (role == 0) {
+    float dqo[4][NDT];   // dq rows after phase 1, loaded before the products
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ic = min(16 * wave + 4 * g4 + r, c - 1);
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) dqo[r][t] = a.dq[(lrow0 + ic) * DH + 16 * t + lc];
+    }
     floatx4 S[4], dP[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) { S[t] = zero4(); dP[t] = zero4(); }
@@ -430,11 +452,24 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
       const int i = 16 * wave + 4 * g4 + r;
       if (i >= c) continue;
 #pragma unroll
-      for (int t = 0; t < NDT; ++t) a.dq[(lrow0 + i) * DH + 16 * t + lc] += a.scale * dQ[t][r];
+      for (int t = 0; t < NDT; ++t) a.dq[(lrow0 + i) * DH + 16 * t + lc] = dqo[r][t] + a.scale * dQ[t][r];
     }
   }
   // ---- phase 3: key-major (rows j = 16 wave + ..): P^T, dS^T -> dV = P^T dO, dK = dS^T Q
   else {
+    // sweep 0: the dkself / dvraw rows after phase 1, loaded before the products
+    float dko[4][NDT], dvo[4][NDT];
+    if (a.dKout == nullptr) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int jc = min(16 * wave + 4 * g4 + r, c - 1);
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) {
+          dko[r][t] = a.dkself[(lrow0 + jc) * DH + 16 * t + lc];
+          dvo[r][t] = a.dvraw[(lrow0 + jc) * DH + 16 * t + lc];
+        }
+      }
+    }
     floatx4 St[4], dPt[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) { St[t] = zero4(); dPt[t] = zero4(); }
@@ -478,8 +513,8 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
           a.dKout[((long)bh * CMAX + j) * DH + e] = a.scale * dK[t][r];
           a.dVout[((long)bh * CMAX + j) * DH + e] = dV[t][r];
         } else {
-          a.dkself[(lrow0 + j) * DH + e] += a.scale * dK[t][r];
-          a.dvraw[(lrow0 + j) * DH + e] += dV[t][r];
+          a.dkself[(lrow0 + j) * DH + e] = dko[r][t] + a.scale * dK[t][r];
+          a.dvraw[(lrow0 + j) * DH + e] = dvo[r][t] + dV[t][r];
         }
       }
     }
