@@ -141,7 +141,7 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
 template <typename T, int DH>
 int run_comm(const CellGeom& g, const T* qr, const T* Kc, const T* Vc, float scale, const CellWs& ws,
              hipStream_t s) {
-  const CommPlan cp = comm_plan(g.pos0);
+  const CommPlan cp = comm_plan(g.pos0, g.B * g.h);
   if (cp.nsplit == 0) return 0;
   const int BH = g.B * g.h;
   CommArgs<T> ca{g, qr, Kc, Vc, cp.split_len, scale, ws.Ap, ws.Zp, ws.Mp};

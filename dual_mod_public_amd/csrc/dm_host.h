@@ -70,10 +70,12 @@ inline int check_cfg(const dm_config* c) {
 struct CommPlan {
   int nsplit, split_len;
 };
-inline CommPlan comm_plan(int pos0) {
+// forward: enough splits for ~512 blocks over the B*h heads (the first sweep's
+// attention merges them, so no more than that)
+inline CommPlan comm_plan(int pos0, int BH) {
   if (pos0 <= 0) return CommPlan{0, 0};
   int nsplit = cdiv(pos0, COMM_SPLIT_MIN);
-  if (nsplit > COMM_MAX_SPLITS) nsplit = COMM_MAX_SPLITS;
+  nsplit = std::min(nsplit, std::max(1, std::min(COMM_MAX_SPLITS, cdiv(512, BH))));
   const int split_len = cdiv(cdiv(pos0, nsplit), 64) * 64;
   return CommPlan{cdiv(pos0, split_len), split_len};
 }
