@@ -19,6 +19,7 @@ namespace dm {
 
 constexpr int WAVE = 64;
 constexpr int CMAX = 64;   // max chunk length of one cell (rows of one attention block)
+constexpr int COMM_MAX_SPLITS = 8;   // committed-prefix splits of a cell's forward accumulator
 
 DM_DEV float to_f(float x) { return x; }
 DM_DEV float to_f(bf16 x) { return (float)x; }

@@ -47,7 +47,6 @@ inline int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 constexpr int COMM_SPLIT_MIN = 256;   // committed keys per split (lower bound)
-constexpr int COMM_MAX_SPLITS = 16;
 constexpr int DEC_SPLIT = 512;        // tape keys per decode split
 
 inline int check_cfg(const dm_config* c) {

@@ -410,37 +410,53 @@ static __global__ __launch_bounds__(64 * NW) void k_attend(AttendArgs<T> a) {
       }
     }
   } else if (a.nsplit > 1) {
+    // merge the split partials: per row, every split's loads are issued before the
+    // first use (indices clamped in bounds, splits >= nsplit masked); the merged state
+    // is stored only after all rows are merged
+    constexpr int MS = COMM_MAX_SPLITS;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {   // one row at a time (scheduling barrier below):
+                                    // MS * (2 + DH/16) loads in flight
+      const int qc = min(wq + 4 * g4 + r, g.c - 1);
+      float ms[MS], zs[MS], as[MS][C::NDT];
+#pragma unroll
+      for (int s = 0; s < MS; ++s) {
+        const long base = ((long)min(s, a.nsplit - 1) * BH + bh) * g.c + qc;
+        ms[s] = a.Mp[base];
+        zs[s] = a.Zp[base];
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; ++dt) as[s][dt] = a.Ap[base * DH + col + 16 * dt];
+      }
+      float M = NEG_INF;
+#pragma unroll
+      for (int s = 0; s < MS; ++s) M = (s < a.nsplit) ? fmaxf(M, ms[s]) : M;
+      float z = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt) st.O[dt][r] = 0.f;
+#pragma unroll
+      for (int s = 0; s < MS; ++s) {
+        const float w = (s < a.nsplit && ms[s] != NEG_INF) ? __expf(ms[s] - M) : 0.f;
+        z += w * zs[s];
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; ++dt) st.O[dt][r] += w * as[s][dt];
+      }
+      st.m[r] = M;
+      st.z[r] = z;   // the row total on every lane until stored below
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int q = wq + 4 * g4 + r;
       if (q < g.c) {
-        float M = NEG_INF;
-        for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.Mp[((long)s * BH + bh) * g.c + q]);
-        float z = 0.f;
-        float acc[C::NDT];
-#pragma unroll
-        for (int dt = 0; dt < C::NDT; ++dt) acc[dt] = 0.f;
-        for (int s = 0; s < a.nsplit; ++s) {
-          const long base = ((long)s * BH + bh) * g.c + q;
-          const float ms = a.Mp[base];
-          const float w = (ms == NEG_INF) ? 0.f : __expf(ms - M);
-          z += w * a.Zp[base];
-#pragma unroll
-          for (int dt = 0; dt < C::NDT; ++dt) acc[dt] += w * a.Ap[base * DH + col + 16 * dt];
-        }
         const long o = (long)bh * g.c + q;
-        st.m[r] = M;
-        st.z[r] = (col == 0) ? z : 0.f;
 #pragma unroll
-        for (int dt = 0; dt < C::NDT; ++dt) {
-          st.O[dt][r] = acc[dt];
-          a.A[o * DH + col + 16 * dt] = acc[dt];
-        }
+        for (int dt = 0; dt < C::NDT; ++dt) a.A[o * DH + col + 16 * dt] = st.O[dt][r];
         if (col == 0) {
-          a.Z[o] = z;
-          a.Mx[o] = M;
+          a.Z[o] = st.z[r];
+          a.Mx[o] = st.m[r];
         }
       }
+      st.z[r] = (col == 0) ? st.z[r] : 0.f;   // per-lane partial sums from here on
     }
   }
   // raw self column inputs, loaded before the barriers below: partial <q_r, k_self_r>
