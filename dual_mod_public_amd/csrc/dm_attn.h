@@ -149,7 +149,8 @@ DM_DEV void flash_tile(const typename Mfma<T>::frag* qf, const T* Ks, const T* V
       Pw[(4 * g + r) * C::LDP + col + 16 * t] = from_f<T>(p);
     }
   }
-  __syncthreads();   // P visible to the whole wave (all waves run in lockstep)
+  // P is the wave's own staging: LDS operations of one wave complete in order, so
+  // its lanes see each other's P without a workgroup barrier
 #pragma unroll
   for (int kb = 0; kb < C::NPS; ++kb) {
     typename MF::frag pf = MF::load(Pw + col * C::LDP + kb * MF::KSTEP + g * MF::KPL);

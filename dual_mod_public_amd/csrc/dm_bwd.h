@@ -313,6 +313,8 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
   const int g4 = lane >> 4, lc = lane & 15;
   const int d = g.d, c = g.c;
   const long lrow0 = (long)bh * g.Tbuf + g.buf_t0;
+  // the wave's own 16 rows of staging: written and read by that wave only (LDS
+  // operations of one wave complete in order, so no workgroup barrier is needed)
   T* W = Wst + wave * 16 * LDI;
 
   // ---- phase 1: 4 threads per row i build dO, D, stage Q / K / V / dO, self column
@@ -442,7 +444,6 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
         W[il * LDI + j] = from_f<T>(p * (dP[t][r] - Di));
       }
     }
-    __syncthreads();
     floatx4 dQ[NDT];
 #pragma unroll
     for (int t = 0; t < NDT; ++t) dQ[t] = zero4();
@@ -487,12 +488,10 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
         W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r]);
       }
     }
-    __syncthreads();
     floatx4 dV[NDT], dK[NDT];
 #pragma unroll
     for (int t = 0; t < NDT; ++t) { dV[t] = zero4(); dK[t] = zero4(); }
     wave_mma<T, 64, NDT>(W, LDI, dOt, LDI, dV);
-    __syncthreads();
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int i = 16 * t + lc;
@@ -500,7 +499,6 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r] * (dPt[t][r] - Di));
     }
-    __syncthreads();
     wave_mma<T, 64, NDT>(W, LDI, Qt, LDI, dK);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -557,30 +555,38 @@ static __global__ __launch_bounds__(256) void k_comm_bwd(CommBwdArgs<T> a) {
   const int g4 = lane >> 4, lc = lane & 15;
   const int c = g.c;
   const int k_begin = s * a.split_len, k_end = min(k_begin + a.split_len, g.pos0);
+  // the wave's own 16 rows of staging: written and read by that wave only (LDS
+  // operations of one wave complete in order, so no workgroup barrier is needed)
   T* W = Wst + wave * 16 * LDI;
   const long lrow0 = (long)bh * g.Tbuf + g.buf_t0;
   const T* Kb = a.Kc + (long)bh * g.cache_T * DH;
   const T* Vb = a.Vc + (long)bh * g.cache_T * DH;
 
   constexpr int EPT = DH / 4;            // elements per thread in the row-wise staging
+  constexpr int VT = 16 / (int)sizeof(T), NW = EPT / VT;   // 16-byte words per thread and row
   const int ri = tid >> 2, re0 = (tid & 3) * EPT;
-  // queries and committed grads of the block's 64 rows
+  // queries and committed grads of the block's 64 rows, row-wise and transposed
   {
     const bool ok = ri < c;
-    float q[EPT], gg[EPT];
-    load_vec<T, EPT>(a.qr + (lrow0 + (ok ? ri : 0)) * DH + re0, q);
-    load_vec<float, EPT>(a.G + ((long)bh * CMAX + (ok ? ri : 0)) * DH + re0, gg);
+    const int r = ok ? ri : 0;
+    float gg[EPT];
+    load_vec<float, EPT>(a.G + ((long)bh * CMAX + r) * DH + re0, gg);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint4 qv = keep_if(*reinterpret_cast<const uint4*>(a.qr + (lrow0 + r) * DH + re0 + w * VT), ok);
+      *reinterpret_cast<uint4*>(Qs + ri * LDE + re0 + w * VT) = qv;
+      float f[VT];
+      unpack16<T>(qv, f);
+#pragma unroll
+      for (int e = 0; e < VT; ++e) Qt[(re0 + w * VT + e) * LDI + ri] = from_f<T>(f[e]);
+    }
     if (!ok) {
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) { q[e] = 0.f; gg[e] = 0.f; }
+      for (int e = 0; e < EPT; ++e) gg[e] = 0.f;
     }
-    store_vec<T, EPT>(Qs + ri * LDE + re0, q);
     store_vec<T, EPT>(Gs + ri * LDE + re0, gg);
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      Qt[(re0 + e) * LDI + ri] = from_f<T>(q[e]);
-      Gt[(re0 + e) * LDI + ri] = from_f<T>(gg[e]);
-    }
+    for (int e = 0; e < EPT; ++e) Gt[(re0 + e) * LDI + ri] = from_f<T>(gg[e]);
     if ((tid & 3) == 0) {
       sM[ri] = ok ? a.Mx[(long)bh * c + ri] : 0.f;
       sD[ri] = ok ? a.Dbar[(long)bh * CMAX + ri] : 0.f;
@@ -590,13 +596,17 @@ static __global__ __launch_bounds__(256) void k_comm_bwd(CommBwdArgs<T> a) {
 #pragma unroll
   for (int t = 0; t < NDT; ++t) dQ[t] = zero4();
 
-  // key tiles: K / V of the next tile are loaded into registers while the current
-  // tile is used; the grad-cache rows a tile adds into are read at its start
-  float kreg[EPT], vreg[EPT];
+  // key tiles: K / V of the next tile are loaded into registers (raw words) while
+  // the current tile is used; the grad-cache rows a tile adds into are read at its start
+  uint4 kv[NW], vv[NW];
   auto load_tile = [&](int k0) {
     const int j = min(ri, k_end - k0 - 1);
-    load_vec<T, EPT>(Kb + (long)(k0 + j) * DH + re0, kreg);
-    load_vec<T, EPT>(Vb + (long)(k0 + j) * DH + re0, vreg);
+    const bool ok = ri < k_end - k0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      kv[w] = keep_if(*reinterpret_cast<const uint4*>(Kb + (long)(k0 + j) * DH + re0 + w * VT), ok);
+      vv[w] = keep_if(*reinterpret_cast<const uint4*>(Vb + (long)(k0 + j) * DH + re0 + w * VT), ok);
+    }
   };
   if (k_begin < k_end) load_tile(k_begin);
   for (int k0 = k_begin; k0 < k_end; k0 += 64) {
@@ -613,16 +623,15 @@ static __global__ __launch_bounds__(256) void k_comm_bwd(CommBwdArgs<T> a) {
         oldV[r][t] = a.dVgc[row + 16 * t + lc];
       }
     }
-    __syncthreads();
-    {
-      const bool ok = ri < nv;
+    __syncthreads();   // the previous tile's readers of the staged K / V are done
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        if (!ok) { kreg[e] = 0.f; vreg[e] = 0.f; }
-        Kt[(re0 + e) * LDI + ri] = from_f<T>(kreg[e]);
-      }
-      store_vec<T, EPT>(Ks + ri * LDE + re0, kreg);
-      store_vec<T, EPT>(Vs + ri * LDE + re0, vreg);
+    for (int w = 0; w < NW; ++w) {
+      *reinterpret_cast<uint4*>(Ks + ri * LDE + re0 + w * VT) = kv[w];
+      *reinterpret_cast<uint4*>(Vs + ri * LDE + re0 + w * VT) = vv[w];
+      float f[VT];
+      unpack16<T>(kv[w], f);
+#pragma unroll
+      for (int e = 0; e < VT; ++e) Kt[(re0 + w * VT + e) * LDI + ri] = from_f<T>(f[e]);
     }
     __syncthreads();
     if (k0 + 64 < k_end) load_tile(k0 + 64);
@@ -643,10 +652,8 @@ static __global__ __launch_bounds__(256) void k_comm_bwd(CommBwdArgs<T> a) {
           W[il * LDI + j] = from_f<T>(e * (dP[t][r] - sD[i]));
         }
       }
-      __syncthreads();
       wave_mma<T, 64, NDT>(W, LDI, Kt, LDI, dQ);
     }
-    __syncthreads();
     // key-major: E^T, dS^T -> dV = E^T G, dK = dS^T Q (rows j = 16 wave + ..)
     {
       floatx4 St[4], dPt[4];
@@ -665,19 +672,16 @@ static __global__ __launch_bounds__(256) void k_comm_bwd(CommBwdArgs<T> a) {
           W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[t][r]);
         }
       }
-      __syncthreads();
       floatx4 dV[NDT], dK[NDT];
 #pragma unroll
       for (int t = 0; t < NDT; ++t) { dV[t] = zero4(); dK[t] = zero4(); }
       wave_mma<T, 64, NDT>(W, LDI, Gt, LDI, dV);
-      __syncthreads();
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int i = 16 * t + lc;
 #pragma unroll
         for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[t][r] * (dPt[t][r] - sD[i]));
       }
-      __syncthreads();
       wave_mma<T, 64, NDT>(W, LDI, Qt, LDI, dK);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -701,18 +705,27 @@ static __global__ __launch_bounds__(256) void k_comm_bwd(CommBwdArgs<T> a) {
   }
 }
 
-// dq[b, h, buf_t0 + i] += sum_s dq_part[s, bh, i]
+// dq[b, h, buf_t0 + i] += sum_s dq_part[s, bh, i] (the partials of eight splits are
+// loaded together)
 static __global__ __launch_bounds__(256) void k_dq_reduce(CellGeom g, int nsplit, const float* __restrict__ dq_part,
                                                    float* __restrict__ dq) {
   const long BH = (long)g.B * g.h;
   const long n = BH * g.c * g.dh;
+  const long sstride = BH * CMAX * g.dh;   // one split
   for (long idx = blockIdx.x * 256L + threadIdx.x; idx < n; idx += (long)gridDim.x * 256) {
     const int e = idx % g.dh;
     const long r = idx / g.dh;
     const int i = r % g.c;
     const long bh = r / g.c;
+    const float* src = dq_part + (bh * CMAX + i) * g.dh + e;
     float s = 0.f;
-    for (int sp = 0; sp < nsplit; ++sp) s += dq_part[((sp * BH + bh) * CMAX + i) * g.dh + e];
+    for (int s0 = 0; s0 < nsplit; s0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = src[min(s0 + k, nsplit - 1) * sstride];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s += (s0 + k < nsplit) ? v[k] : 0.f;
+    }
     dq[(bh * g.Tbuf + g.buf_t0 + i) * g.dh + e] += s;
   }
 }
