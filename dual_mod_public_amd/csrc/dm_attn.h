@@ -69,22 +69,26 @@ template <typename T, int DH, int NT = 256> struct KVRegs {
   static constexpr int VPR = DH / AttnCfg<T, DH>::VEC;             // 16-byte vectors per row
   static constexpr int NV = AttnCfg<T, DH>::KT * VPR / NT;         // vectors per thread (NT threads)
   uint4 k[NV], v[NV];
+  int nvalid;                                                      // keys [0, nvalid) of the tile
 };
 
-// Load keys [0, nvalid) of a tile; rows >= nvalid become zeros (so 0-probability
-// columns multiply zeros).
+// Load keys [0, nvalid) of a tile; rows >= nvalid become zeros when stored (so
+// 0-probability columns multiply zeros). The mask is applied at the store, not
+// here: an operation on a loaded value right after its load would make the
+// compiler wait for the load there, and the next tile's loads would no longer
+// overlap the current tile's work.
 template <typename T, int DH, int NT = 256>
 DM_DEV void load_kv(const T* __restrict__ Kg, const T* __restrict__ Vg, long row_stride, int nvalid,
                     KVRegs<T, DH, NT>& r) {
   using R = KVRegs<T, DH, NT>;
+  r.nvalid = nvalid;
 #pragma unroll
   for (int i = 0; i < R::NV; ++i) {
     const int v = threadIdx.x + NT * i;
     const int k = v % AttnCfg<T, DH>::KT, c0 = (v / AttnCfg<T, DH>::KT) * AttnCfg<T, DH>::VEC;
-    const bool ok = k < nvalid;
-    const long off = (long)(ok ? k : 0) * row_stride + c0;
-    r.k[i] = keep_if(*reinterpret_cast<const uint4*>(Kg + off), ok);
-    r.v[i] = keep_if(*reinterpret_cast<const uint4*>(Vg + off), ok);
+    const long off = (long)(k < nvalid ? k : 0) * row_stride + c0;
+    r.k[i] = *reinterpret_cast<const uint4*>(Kg + off);
+    r.v[i] = *reinterpret_cast<const uint4*>(Vg + off);
   }
 }
 
@@ -97,8 +101,10 @@ DM_DEV void store_kv(const KVRegs<T, DH, NT>& r, T* Ks, T* Vt) {
   for (int i = 0; i < R::NV; ++i) {
     const int v = threadIdx.x + NT * i;
     const int k = v % C::KT, c0 = (v / C::KT) * C::VEC;
-    *reinterpret_cast<uint4*>(Ks + k * C::LDK + c0) = r.k[i];
-    const T* ve = reinterpret_cast<const T*>(&r.v[i]);
+    const bool ok = k < r.nvalid;
+    *reinterpret_cast<uint4*>(Ks + k * C::LDK + c0) = keep_if(r.k[i], ok);
+    const uint4 vm = keep_if(r.v[i], ok);
+    const T* ve = reinterpret_cast<const T*>(&vm);
 #pragma unroll
     for (int j = 0; j < C::VEC; ++j) Vt[(c0 + j) * C::LDV + k] = ve[j];
   }

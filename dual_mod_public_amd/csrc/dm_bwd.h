@@ -10,7 +10,7 @@
 //                 per-row partial <g, o> for the RMS VJP, norm_ctx weight partials
 //   k_attn_bwd    attention VJP of sweep s per (b, h): intra rows (strict lower)
 //                 + raw self column; accumulates the committed part's G, Dbar
-// After the sweeps, k_comm_bwd runs the committed-prefix VJP once per cell:
+// The committed-prefix part of every sweep is one VJP per row (k_comm_dkv, k_comm_dq):
 //   sum_s dS_comm^s = E o (G V^T - Dbar),  E = exp(S - m_comm),
 //   G = sum_s alpha_s dO_s, Dbar = sum_s alpha_s D_s, alpha_s = exp(m_comm - M_s) / Z_s,
 // which is exact because the committed scores are the same in every sweep.
@@ -60,8 +60,9 @@ template <int DH> DM_DEV int col_vlin(int d, int hd, int e) {
 template <typename T> struct RefineBwdArgs {
   CellGeom g;
   int N, ctx_mod;
-  const float* dK; const float* dV;    // grads of the refined rows (rotated K, V)
-  long dk_stride; int dk_row0;         //   (b,h) at bh*dk_stride, chunk row p at row dk_row0 + p
+  const float* dK; const float* dV;    // grads of the refined rows (rotated K, V): the sum of
+  long dk_stride; int dk_row0;         //   NS slices psum_stride apart, (b,h) at bh*dk_stride,
+  long psum_stride;                    //   chunk row p at row dk_row0 + p
   const T* save1;                      // [N, 4d] raw GEMM-1 outputs of this sweep (storage dtype)
   const T* save2;                      // [N, d] raw v_ctx (mult family)
   const float* glogx; const T* kraw; const T* vraw;
@@ -71,7 +72,7 @@ template <typename T> struct RefineBwdArgs {
   float* dglogx; float* dkraw; float* dvraw;   // layer accumulators (+=)
 };
 
-template <typename T, int DH>
+template <typename T, int DH, int NS>
 static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
   const CellGeom& g = a.g;
   const int d = g.d, h = g.h;
@@ -89,13 +90,18 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
   const T* S1 = a.save1 + (long)m * 4 * d;
   const float* gx = a.glogx + xrow * 2 * d;
   // ---- gather
-  const float da = a.dK[drow + jj], db = a.dK[drow + jj + DH / 2];
+  float da = 0.f, db = 0.f, dv1 = 0.f, dv2 = 0.f;
+#pragma unroll
+  for (int q = 0; q < NS; ++q) {
+    const long o = q * a.psum_stride + drow + jj;
+    da += a.dK[o]; db += a.dK[o + DH / 2];
+    dv1 += a.dV[o]; dv2 += a.dV[o + DH / 2];
+  }
   const float cs = a.cos[(long)pos * (DH / 2) + jj], sn = a.sin[(long)pos * (DH / 2) + jj];
   const float kc1 = to_f(S1[col_k<DH>(hd, jj, 0)]), kc2 = to_f(S1[col_k<DH>(hd, jj, 1)]);
   const float gu1 = to_f(S1[col_k<DH>(hd, jj, 2)]), gu2 = to_f(S1[col_k<DH>(hd, jj, 3)]);
   const float gx1 = gx[hd * DH + jj], gx2 = gx[hd * DH + jj + DH / 2];
   const float kr1 = to_f(a.kraw[lrow + jj]), kr2 = to_f(a.kraw[lrow + jj + DH / 2]);
-  const float dv1 = a.dV[drow + jj], dv2 = a.dV[drow + jj + DH / 2];
   const float vr1 = to_f(a.vraw[lrow + jj]), vr2 = to_f(a.vraw[lrow + jj + DH / 2]);
   const float gxv1 = gx[d + hd * DH + jj], gxv2 = gx[d + hd * DH + jj + DH / 2];
   const int c1 = hd * DH + jj, c2 = c1 + DH / 2;
@@ -276,7 +282,9 @@ template <typename T> struct AttnBwdArgs {
   const float* docat;                                  // [B, Tbuf, d] upstream grad of o_cat, or nullptr
   const float* stat_m; const float* stat_z;            // [B*h, c] final row max / sum of the sweep
   const float* Mx;                                     // committed row max [B*h, c] or nullptr
-  float* G; float* Dbar;                               // committed grads [B*h, CMAX, DH], [B*h, CMAX]
+  float* G; float* Dbar;                               // committed grads per layer-buffer row
+  float* Mrow; int* klim;                              //   [B*h, Tbuf, DH], [B*h, Tbuf]; row max [B*h, Tbuf],
+                                                       //   committed prefix length [Tbuf] (first sweep)
   int first;                                           // first reverse sweep: G / Dbar are written, else +=
   float scale, inv_d, eps;
   float* dKout; float* dVout;                          // [B*h, CMAX, DH] grads of the intra rows (sweep >= 1)
@@ -346,8 +354,8 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
       load_vec<float, EPT>(a.dq + lr, acc0);
       if (a.Mx != nullptr) {
         mx = a.Mx[(long)bh * c + ic];
-        load_vec<float, EPT>(a.G + ((long)bh * CMAX + ic) * DH + e0, gold);
-        dbold = a.Dbar[(long)bh * CMAX + ic];
+        load_vec<float, EPT>(a.G + lr, gold);
+        dbold = a.Dbar[lrow0 + ic];
       }
     } else {
       load_vec<float, EPT>(a.dkself + lr, acc0);
@@ -384,9 +392,13 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
       float gn[EPT];
 #pragma unroll
       for (int e = 0; e < EPT; ++e) gn[e] = (a.first ? 0.f : gold[e]) + alpha * dO[e];
-      store_vec<float, EPT>(a.G + ((long)bh * CMAX + i) * DH + e0, gn);
-      if (part == 0) a.Dbar[(long)bh * CMAX + i] = (a.first ? 0.f : dbold) + alpha * Dp;
+      store_vec<float, EPT>(a.G + lr, gn);
+      if (part == 0) {
+        a.Dbar[lrow0 + i] = (a.first ? 0.f : dbold) + alpha * Dp;
+        if (a.first) a.Mrow[lrow0 + i] = mx;
+      }
     }
+    if (role == 0 && a.first && bh == 0 && part == 0 && ok) a.klim[g.buf_t0 + i] = g.pos0;
     if (ok) {
       if (role == 0) {
 #pragma unroll
@@ -520,213 +532,265 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
 }
 
 // ---------------------------------------------------------------------------
-// committed-prefix VJP of a cell, one block per (split, b, h) over the split's
-// key tiles: dq partials, dK / dV of the committed rows into the grad cache.
+// committed-prefix VJP. Every query row i of a cell at pos0 > 0 attends the
+// committed keys j < klim_i = pos0 with E_ij = exp(scale q_i . k_j - Mx_i) and
+//   dS_ij = E_ij (G_i . v_j - Dbar_i),
+//   dq_i += scale sum_j dS_ij k_j,  dK_j += scale sum_i dS_ij q_i,  dV_j += sum_i E_ij G_i,
+// with G_i, Dbar_i, Mx_i kept per row by the attention VJP. The key side runs per
+// key cell right before that cell's sweep VJP (its rows are in the prefix of every
+// later row, so the sum is complete and is written once); the query side runs
+// once per layer after every cell.
 // ---------------------------------------------------------------------------
-template <typename T> struct CommBwdArgs {
-  CellGeom g;
-  int split_len;
-  const T* qr; const T* Kc; const T* Vc;   // layer buffer q_r; cache rows [0, pos0)
-  const float* Mx;                         // [B*h, c] committed row max (forward layout)
-  const float* G; const float* Dbar;       // [B*h, CMAX, DH], [B*h, CMAX]
+constexpr int COMM_NSQ = 4;   // query splits of the key side (partial slots summed by k_refine_bwd)
+
+template <typename T> struct CommKeyArgs {
+  int B, h, Tbuf, cache_T;
+  int k0, kc;                                  // key cell: cache rows [k0, k0 + kc)
+  int q_lo, q_hi;                              // query rows [q_lo, q_hi) of the layer buffers
+  const T* qr; const T* Kc; const T* Vc;       // layer buffer q_r; the cache rows
+  const float* G; const float* Dbar; const float* Mx;   // per layer-buffer row (see AttnBwdArgs)
   float scale;
-  float* dKgc; float* dVgc;                // grad cache [B, h, cache_T, DH] (+=)
-  float* dq_part;                          // [nsplit, B*h, CMAX, DH]
+  float* dKp; float* dVp;                      // [COMM_NSQ, B*h, CMAX, DH] partial sums per split
 };
 
+// One block per (query split s, b, h): the split's 64-row query tiles s, s + NSQ, ..;
+// wave w owns keys 16w .. 16w + 15 of the cell (key-major products, as in k_attn_bwd).
 template <typename T, int DH>
-static __global__ __launch_bounds__(256) void k_comm_bwd(CommBwdArgs<T> a) {
+static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
+  using C = AttnBwdCfg<T, DH>;
+  constexpr int LDE = C::LDE, LDI = C::LDI, NDT = DH / 16;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  T* Ks = reinterpret_cast<T*>(smem_raw);
+  T* Vs = Ks + 64 * LDE;
+  T* Qs = Vs + 64 * LDE;
+  T* Gs = Qs + 64 * LDE;
+  T* Qt = Gs + 64 * LDE;
+  T* Gt = Qt + DH * LDI;
+  T* Wst = Gt + DH * LDI;
+  __shared__ float sM[64], sD[64];
+
+  const int s = blockIdx.x, bh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g4 = lane >> 4, lc = lane & 15;
+  // the wave's own 16 rows of staging (LDS operations of one wave complete in order)
+  T* W = Wst + wave * 16 * LDI;
+  const long qrow0 = (long)bh * a.Tbuf;
+  constexpr int EPT = DH / 4;
+  constexpr int VT = 16 / (int)sizeof(T), NW = EPT / VT;   // 16-byte words per thread and row
+  const int ri = tid >> 2, re0 = (tid & 3) * EPT;
+  const int ntile = (a.q_hi - a.q_lo + 63) / 64;
+
+  // the cell's keys and values, row-wise (A operands of the key-major products)
+  {
+    const bool ok = ri < a.kc;
+    const long row = ((long)bh * a.cache_T + a.k0 + (ok ? ri : 0)) * DH + re0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      *reinterpret_cast<uint4*>(Ks + ri * LDE + re0 + w * VT) =
+          keep_if(*reinterpret_cast<const uint4*>(a.Kc + row + w * VT), ok);
+      *reinterpret_cast<uint4*>(Vs + ri * LDE + re0 + w * VT) =
+          keep_if(*reinterpret_cast<const uint4*>(a.Vc + row + w * VT), ok);
+    }
+  }
+  // query tile rows: q, G (raw words), row max, Dbar into registers, then LDS; rows
+  // past the end are zeroed when staged (a select on a loaded value right after
+  // its load would make the compiler wait for the load there)
+  constexpr int GW = EPT / 4;   // 16-byte words of a G row segment
+  uint4 qv[NW], gw[GW];
+  float mv, dv;
+  bool tok = false;
+  auto load_tile = [&](int t) {
+    const int i0 = a.q_lo + 64 * t;
+    tok = ri < a.q_hi - i0;
+    const long r = qrow0 + i0 + (tok ? ri : 0);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) qv[w] = *reinterpret_cast<const uint4*>(a.qr + r * DH + re0 + w * VT);
+#pragma unroll
+    for (int w = 0; w < GW; ++w) gw[w] = *reinterpret_cast<const uint4*>(a.G + r * DH + re0 + 4 * w);
+    mv = a.Mx[r];
+    dv = a.Dbar[r];
+  };
+  floatx4 dK[NDT], dV[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) { dK[t] = zero4(); dV[t] = zero4(); }
+  if (s < ntile) load_tile(s);
+  for (int t = s; t < ntile; t += COMM_NSQ) {
+    const int nq = min(64, a.q_hi - (a.q_lo + 64 * t));
+    __syncthreads();   // the previous tile's readers are done (first pass: publishes K / V)
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint4 q = keep_if(qv[w], tok);
+      *reinterpret_cast<uint4*>(Qs + ri * LDE + re0 + w * VT) = q;
+      float f[VT];
+      unpack16<T>(q, f);
+#pragma unroll
+      for (int e = 0; e < VT; ++e) Qt[(re0 + w * VT + e) * LDI + ri] = from_f<T>(f[e]);
+    }
+    {
+      float gv[EPT];
+#pragma unroll
+      for (int w = 0; w < GW; ++w) unpack16<float>(keep_if(gw[w], tok), gv + 4 * w);
+      store_vec<T, EPT>(Gs + ri * LDE + re0, gv);
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) Gt[(re0 + e) * LDI + ri] = from_f<T>(gv[e]);
+    }
+    if ((tid & 3) == 0) { sM[ri] = tok ? mv : 0.f; sD[ri] = tok ? dv : 0.f; }
+    __syncthreads();
+    if (t + COMM_NSQ < ntile) load_tile(t + COMM_NSQ);
+    // key-major: E^T, dS^T (rows j = 16 wave + .., columns i = queries) -> dV += E^T G, dK += dS^T Q
+    floatx4 St[4], dPt[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) { St[u] = zero4(); dPt[u] = zero4(); }
+    wave_mma<T, DH, 4>(Ks + 16 * wave * LDE, LDE, Qs, LDE, St);
+    wave_mma<T, DH, 4>(Vs + 16 * wave * LDE, LDE, Gs, LDE, dPt);
+    float Et[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = 16 * u + lc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * wave + 4 * g4 + r;
+        Et[u][r] = (j < a.kc && i < nq) ? __expf(St[u][r] * a.scale - sM[i]) : 0.f;
+        W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[u][r]);
+      }
+    }
+    wave_mma<T, 64, NDT>(W, LDI, Gt, LDI, dV);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = 16 * u + lc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[u][r] * (dPt[u][r] - sD[i]));
+    }
+    wave_mma<T, 64, NDT>(W, LDI, Qt, LDI, dK);
+  }
+  const long slot = ((long)s * a.B * a.h + bh) * CMAX;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int j = 16 * wave + 4 * g4 + r;
+    if (j >= a.kc) continue;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      a.dKp[(slot + j) * DH + 16 * t + lc] = a.scale * dK[t][r];
+      a.dVp[(slot + j) * DH + 16 * t + lc] = dV[t][r];
+    }
+  }
+}
+
+template <typename T> struct CommQueryArgs {
+  int B, h, Tbuf, cache_T, nrows;              // query rows [0, nrows)
+  const int* klim;                             // [Tbuf] committed prefix length of each row (0: none)
+  const T* qr; const T* Kc; const T* Vc;
+  const float* G; const float* Dbar; const float* Mx;   // per layer-buffer row (see AttnBwdArgs)
+  float scale;
+  float* dq;                                   // [B*h, Tbuf, DH] (+=)
+};
+
+// One block per (b, h, 64-row query tile), the tiles with the longest prefixes
+// first; wave w owns query rows 16w .. 16w + 15 (query-major products).
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
   using C = AttnBwdCfg<T, DH>;
   constexpr int LDE = C::LDE, LDI = C::LDI, NDT = DH / 16;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   T* Qs = reinterpret_cast<T*>(smem_raw);
-  T* Ks = Qs + 64 * LDE;
+  T* Gs = Qs + 64 * LDE;
+  T* Ks = Gs + 64 * LDE;
   T* Vs = Ks + 64 * LDE;
-  T* Gs = Vs + 64 * LDE;
-  T* Qt = Gs + 64 * LDE;
-  T* Kt = Qt + DH * LDI;
-  T* Gt = Kt + DH * LDI;
-  T* Wst = Gt + DH * LDI;
+  T* Kt = Vs + 64 * LDE;
+  T* Wst = Kt + DH * LDI;
   __shared__ float sM[64], sD[64];
+  __shared__ int sL[64];
 
-  const CellGeom& g = a.g;
-  const int s = blockIdx.x, bh = blockIdx.y;
+  const int bh = blockIdx.x;
+  const int i0 = 64 * ((int)gridDim.y - 1 - (int)blockIdx.y);
+  const int nq = min(64, a.nrows - i0);
+  const int k_end = a.klim[i0 + nq - 1];   // the prefix lengths do not decrease along the rows
+  if (k_end <= 0) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g4 = lane >> 4, lc = lane & 15;
-  const int c = g.c;
-  const int k_begin = s * a.split_len, k_end = min(k_begin + a.split_len, g.pos0);
-  // the wave's own 16 rows of staging: written and read by that wave only (LDS
-  // operations of one wave complete in order, so no workgroup barrier is needed)
-  T* W = Wst + wave * 16 * LDI;
-  const long lrow0 = (long)bh * g.Tbuf + g.buf_t0;
-  const T* Kb = a.Kc + (long)bh * g.cache_T * DH;
-  const T* Vb = a.Vc + (long)bh * g.cache_T * DH;
-
-  constexpr int EPT = DH / 4;            // elements per thread in the row-wise staging
-  constexpr int VT = 16 / (int)sizeof(T), NW = EPT / VT;   // 16-byte words per thread and row
+  T* W = Wst + wave * 16 * LDI;   // the wave's own rows (LDS operations of one wave complete in order)
+  const long qrow0 = (long)bh * a.Tbuf + i0;
+  const T* Kb = a.Kc + (long)bh * a.cache_T * DH;
+  const T* Vb = a.Vc + (long)bh * a.cache_T * DH;
+  constexpr int EPT = DH / 4;
+  constexpr int VT = 16 / (int)sizeof(T), NW = EPT / VT;
   const int ri = tid >> 2, re0 = (tid & 3) * EPT;
-  // queries and committed grads of the block's 64 rows, row-wise and transposed
   {
-    const bool ok = ri < c;
-    const int r = ok ? ri : 0;
+    const bool ok = ri < nq;
+    const long r = qrow0 + (ok ? ri : 0);
     float gg[EPT];
-    load_vec<float, EPT>(a.G + ((long)bh * CMAX + r) * DH + re0, gg);
+    load_vec<float, EPT>(a.G + r * DH + re0, gg);
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const uint4 qv = keep_if(*reinterpret_cast<const uint4*>(a.qr + (lrow0 + r) * DH + re0 + w * VT), ok);
-      *reinterpret_cast<uint4*>(Qs + ri * LDE + re0 + w * VT) = qv;
-      float f[VT];
-      unpack16<T>(qv, f);
-#pragma unroll
-      for (int e = 0; e < VT; ++e) Qt[(re0 + w * VT + e) * LDI + ri] = from_f<T>(f[e]);
-    }
-    if (!ok) {
+    for (int w = 0; w < NW; ++w)
+      *reinterpret_cast<uint4*>(Qs + ri * LDE + re0 + w * VT) =
+          keep_if(*reinterpret_cast<const uint4*>(a.qr + r * DH + re0 + w * VT), ok);
+    const int L = ok ? a.klim[i0 + ri] : 0;
+    if (L == 0) {   // no committed prefix (or past the end): contributes nothing
 #pragma unroll
       for (int e = 0; e < EPT; ++e) gg[e] = 0.f;
     }
     store_vec<T, EPT>(Gs + ri * LDE + re0, gg);
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) Gt[(re0 + e) * LDI + ri] = from_f<T>(gg[e]);
     if ((tid & 3) == 0) {
-      sM[ri] = ok ? a.Mx[(long)bh * c + ri] : 0.f;
-      sD[ri] = ok ? a.Dbar[(long)bh * CMAX + ri] : 0.f;
+      sM[ri] = L > 0 ? a.Mx[r] : 0.f;
+      sD[ri] = L > 0 ? a.Dbar[r] : 0.f;
+      sL[ri] = L;
     }
   }
   floatx4 dQ[NDT];
 #pragma unroll
   for (int t = 0; t < NDT; ++t) dQ[t] = zero4();
-
-  // key tiles: K / V of the next tile are loaded into registers (raw words) while
-  // the current tile is used; the grad-cache rows a tile adds into are read at its start
+  // the next key tile in registers (raw words; rows past the end zeroed when staged)
   uint4 kv[NW], vv[NW];
-  auto load_tile = [&](int k0) {
+  auto load_keys = [&](int k0) {
     const int j = min(ri, k_end - k0 - 1);
-    const bool ok = ri < k_end - k0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      kv[w] = keep_if(*reinterpret_cast<const uint4*>(Kb + (long)(k0 + j) * DH + re0 + w * VT), ok);
-      vv[w] = keep_if(*reinterpret_cast<const uint4*>(Vb + (long)(k0 + j) * DH + re0 + w * VT), ok);
+      kv[w] = *reinterpret_cast<const uint4*>(Kb + (long)(k0 + j) * DH + re0 + w * VT);
+      vv[w] = *reinterpret_cast<const uint4*>(Vb + (long)(k0 + j) * DH + re0 + w * VT);
     }
   };
-  if (k_begin < k_end) load_tile(k_begin);
-  for (int k0 = k_begin; k0 < k_end; k0 += 64) {
-    const int nv = min(64, k_end - k0);
-    // old grad-cache values of this tile's rows, in the C layout of dK / dV
-    float oldK[4][NDT], oldV[4][NDT];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int j = min(16 * wave + 4 * g4 + r, nv - 1);
-      const long row = ((long)bh * g.cache_T + k0 + j) * DH;
-#pragma unroll
-      for (int t = 0; t < NDT; ++t) {
-        oldK[r][t] = a.dKgc[row + 16 * t + lc];
-        oldV[r][t] = a.dVgc[row + 16 * t + lc];
-      }
-    }
-    __syncthreads();   // the previous tile's readers of the staged K / V are done
+  load_keys(0);
+  for (int k0 = 0; k0 < k_end; k0 += 64) {
+    const bool kok = ri < k_end - k0;
+    __syncthreads();   // the previous tile's readers are done (first pass: publishes Q / G)
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      *reinterpret_cast<uint4*>(Ks + ri * LDE + re0 + w * VT) = kv[w];
-      *reinterpret_cast<uint4*>(Vs + ri * LDE + re0 + w * VT) = vv[w];
+      const uint4 kw = keep_if(kv[w], kok);
+      *reinterpret_cast<uint4*>(Ks + ri * LDE + re0 + w * VT) = kw;
+      *reinterpret_cast<uint4*>(Vs + ri * LDE + re0 + w * VT) = keep_if(vv[w], kok);
       float f[VT];
-      unpack16<T>(kv[w], f);
+      unpack16<T>(kw, f);
 #pragma unroll
       for (int e = 0; e < VT; ++e) Kt[(re0 + w * VT + e) * LDI + ri] = from_f<T>(f[e]);
     }
     __syncthreads();
-    if (k0 + 64 < k_end) load_tile(k0 + 64);
-    // query-major: dS = E (G V^T - Dbar), dQ += dS K
-    {
-      floatx4 S[4], dP[4];
+    if (k0 + 64 < k_end) load_keys(k0 + 64);
+    floatx4 S[4], dP[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) { S[t] = zero4(); dP[t] = zero4(); }
-      wave_mma<T, DH, 4>(Qs + 16 * wave * LDE, LDE, Ks, LDE, S);
-      wave_mma<T, DH, 4>(Gs + 16 * wave * LDE, LDE, Vs, LDE, dP);
+    for (int t = 0; t < 4; ++t) { S[t] = zero4(); dP[t] = zero4(); }
+    wave_mma<T, DH, 4>(Qs + 16 * wave * LDE, LDE, Ks, LDE, S);
+    wave_mma<T, DH, 4>(Gs + 16 * wave * LDE, LDE, Vs, LDE, dP);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int il = 4 * g4 + r, i = 16 * wave + il;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int j = 16 * t + lc;
-          const float e = (j < nv && i < c) ? __expf(S[t][r] * a.scale - sM[i]) : 0.f;
-          W[il * LDI + j] = from_f<T>(e * (dP[t][r] - sD[i]));
-        }
-      }
-      wave_mma<T, 64, NDT>(W, LDI, Kt, LDI, dQ);
-    }
-    // key-major: E^T, dS^T -> dV = E^T G, dK = dS^T Q (rows j = 16 wave + ..)
-    {
-      floatx4 St[4], dPt[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) { St[t] = zero4(); dPt[t] = zero4(); }
-      wave_mma<T, DH, 4>(Ks + 16 * wave * LDE, LDE, Qs, LDE, St);
-      wave_mma<T, DH, 4>(Vs + 16 * wave * LDE, LDE, Gs, LDE, dPt);
-      float Et[4][4];
+    for (int r = 0; r < 4; ++r) {
+      const int il = 4 * g4 + r, i = 16 * wave + il;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const int i = 16 * t + lc;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = 16 * wave + 4 * g4 + r;
-          Et[t][r] = (j < nv && i < c) ? __expf(St[t][r] * a.scale - sM[i]) : 0.f;
-          W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[t][r]);
-        }
-      }
-      floatx4 dV[NDT], dK[NDT];
-#pragma unroll
-      for (int t = 0; t < NDT; ++t) { dV[t] = zero4(); dK[t] = zero4(); }
-      wave_mma<T, 64, NDT>(W, LDI, Gt, LDI, dV);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int i = 16 * t + lc;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[t][r] * (dPt[t][r] - sD[i]));
-      }
-      wave_mma<T, 64, NDT>(W, LDI, Qt, LDI, dK);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = 16 * wave + 4 * g4 + r;
-        if (j >= nv) continue;
-        const long row = ((long)bh * g.cache_T + k0 + j) * DH;
-#pragma unroll
-        for (int t = 0; t < NDT; ++t) {
-          a.dKgc[row + 16 * t + lc] = oldK[r][t] + a.scale * dK[t][r];
-          a.dVgc[row + 16 * t + lc] = oldV[r][t] + dV[t][r];
-        }
+        const int j = k0 + 16 * t + lc;
+        const float e = (j < sL[i]) ? __expf(S[t][r] * a.scale - sM[i]) : 0.f;
+        W[il * LDI + 16 * t + lc] = from_f<T>(e * (dP[t][r] - sD[i]));
       }
     }
+    wave_mma<T, 64, NDT>(W, LDI, Kt, LDI, dQ);
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int i = 16 * wave + 4 * g4 + r;
+    if (i >= nq || sL[i] == 0) continue;
 #pragma unroll
-    for (int t = 0; t < NDT; ++t)
-      a.dq_part[(((long)s * g.B * g.h + bh) * CMAX + i) * DH + 16 * t + lc] = a.scale * dQ[t][r];
-  }
-}
-
-// dq[b, h, buf_t0 + i] += sum_s dq_part[s, bh, i] (the partials of eight splits are
-// loaded together)
-static __global__ __launch_bounds__(256) void k_dq_reduce(CellGeom g, int nsplit, const float* __restrict__ dq_part,
-                                                   float* __restrict__ dq) {
-  const long BH = (long)g.B * g.h;
-  const long n = BH * g.c * g.dh;
-  const long sstride = BH * CMAX * g.dh;   // one split
-  for (long idx = blockIdx.x * 256L + threadIdx.x; idx < n; idx += (long)gridDim.x * 256) {
-    const int e = idx % g.dh;
-    const long r = idx / g.dh;
-    const int i = r % g.c;
-    const long bh = r / g.c;
-    const float* src = dq_part + (bh * CMAX + i) * g.dh + e;
-    float s = 0.f;
-    for (int s0 = 0; s0 < nsplit; s0 += 8) {
-      float v[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = src[min(s0 + k, nsplit - 1) * sstride];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) s += (s0 + k < nsplit) ? v[k] : 0.f;
+    for (int t = 0; t < NDT; ++t) {
+      float* p = a.dq + (qrow0 + i) * DH + 16 * t + lc;
+      *p += a.scale * dQ[t][r];
     }
-    dq[(bh * g.Tbuf + g.buf_t0 + i) * g.dh + e] += s;
   }
 }
 

@@ -14,7 +14,6 @@ namespace dm {
 template <typename T> struct BwdWs {
   // layer accumulators (fp32)
   float *dq, *dkraw, *dkself, *dvraw;   // [B, h, T, dh]
-  float *dKgc, *dVgc;                   // [B, h, cache_T, dh] grad cache of the refined rows
   float *dglogx;                        // [B, T, 2d]
   float *dsig;                          // [B, T, d]
   float *docat;                         // [B, T, d] = dy . W_O
@@ -26,8 +25,10 @@ template <typename T> struct BwdWs {
   float *dKa, *dVa, *dKb, *dVb;         // [B*h, CMAX, dh] grads of the intra rows (ping-pong)
   float *lamdv, *gw, *rowdot;           // [N, d], [N, d], [N, d / DU_EPI_TN]
   float *du_part;                       // [DU_SPLIT, N, d] split-K slices of du
-  float *G, *Dbar;                      // [B*h, CMAX, dh], [B*h, CMAX]
-  float *dq_part;                       // [nsplit, B*h, CMAX, dh]
+  // committed-prefix VJP: per-row state from the attention VJP, key-side partial sums
+  float *Grow, *Drow, *Mrow;            // [B*h, T, dh], [B*h, T], [B*h, T]
+  int* klim;                            // [T]
+  float *dKp, *dVp;                     // [COMM_NSQ, B*h, CMAX, dh]
   // weight grads of the sweeps, one GEMM per layer: the cells' transposed operands
   // side by side, [4d | d, Rp] with Rp >= sum over cells of K*B*c (rounded to 64)
   T *dctxT, *uT, *dvcT, *vinT;
@@ -59,8 +60,6 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.dkraw = cv.take<float>(BT * d * 4);
   w.dkself = cv.take<float>(BT * d * 4);
   w.dvraw = cv.take<float>(BT * d * 4);
-  w.dKgc = cv.take<float>(B * cache_T * d * 4);
-  w.dVgc = cv.take<float>(B * cache_T * d * 4);
   w.dglogx = cv.take<float>(BT * 2 * d * 4);
   w.dsig = cv.take<float>(BT * d * 4);
   w.docat = cv.take<float>(BT * d * 4);
@@ -78,9 +77,12 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.gw = cv.take<float>(N * d * 4);
   w.rowdot = cv.take<float>(N * (d / DU_EPI_TN) * 4);
   w.du_part = cv.take<float>(DU_SPLIT * N * d * 4);
-  w.G = cv.take<float>(BH * CMAX * dh * 4);
-  w.Dbar = cv.take<float>(BH * CMAX * 4);
-  w.dq_part = cv.take<float>(comm_splits_max_bwd(cache_T) * BH * CMAX * dh * 4);
+  w.Grow = cv.take<float>(BT * d * 4);
+  w.Drow = cv.take<float>(BH * T_ * 4);
+  w.Mrow = cv.take<float>(BH * T_ * 4);
+  w.klim = cv.take<int>(T_ * 4);
+  w.dKp = cv.take<float>(COMM_NSQ * BH * CMAX * dh * 4);
+  w.dVp = cv.take<float>(COMM_NSQ * BH * CMAX * dh * 4);
   // + 64: rows of the transposes a power of two apart would all map to the same HBM
   // channels (the per-cell transposes write 64 rows at a stride of Rp elements)
   w.Rp = (long)cdiv((long)kmax * B * T_, 64) * 64 + 64;
@@ -194,8 +196,6 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   fill0(ws.dkraw, (size_t)BT * d, s);
   fill0(ws.dkself, (size_t)BT * d, s);
   fill0(ws.dvraw, (size_t)BT * d, s);
-  fill0(ws.dKgc, (size_t)B * cache_T * d, s);
-  fill0(ws.dVgc, (size_t)B * cache_T * d, s);
   fill0(ws.dglogx, (size_t)BT * 2 * d, s);
   fill0(ws.dsig, (size_t)BT * d, s);
   fill0(ws.dnw, (size_t)cdiv(B * CMAX, NSLOT_TM) * d, s);
@@ -215,6 +215,8 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   const T* kraw = (const T*)L->kraw;
   const size_t slot = (size_t)BH * CMAX * DH;
 
+  const size_t lds_attn = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
+  const int t_end = sched[3 * (n_cells - 1)] + sched[3 * (n_cells - 1) + 1];   // rows of the schedule
   long coff = 0;   // columns of the weight-grad operands filled so far
   for (int ci = n_cells - 1; ci >= 0; --ci) {
     const int pos0 = sched[3 * ci], cc = sched[3 * ci + 1], K = sched[3 * ci + 2];
@@ -233,16 +235,24 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
                       &ws.sv, s);
       Mx = pos0 > 0 ? ws.fws.M : nullptr;
     }
-    const float* dKn = ws.dKgc;
-    const float* dVn = ws.dVgc;
-    long dn_stride = (long)cache_T * DH;
-    int dn_row0 = pos0;
+    // grads of the cell's final rows from the committed-prefix attention of every
+    // later row (their G / Dbar / row max are in place: those cells are done)
+    {
+      CommKeyArgs<T> ka{B, h, T_, cache_T, pos0, cc, pos0 + cc, t_end, qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow,
+                        scale, ws.dKp, ws.dVp};
+      hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(COMM_NSQ, BH), dim3(256), lds_attn, s, ka);
+    }
+    const float* dKn = ws.dKp;
+    const float* dVn = ws.dVp;
+    const long dn_stride = (long)CMAX * DH;
     for (int sw = K - 1; sw >= 0; --sw) {
-      // refine VJP of sweep sw
-      RefineBwdArgs<T> ra{g, N, c->ctx_mod, dKn, dVn, dn_stride, dn_row0, sv.save1 + sw * NS * 4 * d,
-                          mult ? sv.save2 + sw * NS * d : nullptr, L->glogx, kraw, vraw, cos, sin, ws.dctx + sw * NS * 4 * d,
-                          ws.dvc + sw * NS * d, ws.dglogx, ws.dkraw, ws.dvraw};
-      hipLaunchKernelGGL((k_refine_bwd<T, DH>), dim3(cdiv((long)N * d / 2, 256)), dim3(256), 0, s, ra);
+      // refine VJP of sweep sw (the last sweep's rows: the sum of the key-side splits)
+      RefineBwdArgs<T> ra{g, N, c->ctx_mod, dKn, dVn, dn_stride, 0, (long)BH * CMAX * DH,
+                          sv.save1 + sw * NS * 4 * d, mult ? sv.save2 + sw * NS * d : nullptr, L->glogx, kraw, vraw,
+                          cos, sin, ws.dctx + sw * NS * 4 * d, ws.dvc + sw * NS * d, ws.dglogx, ws.dkraw, ws.dvraw};
+      const dim3 rgrid(cdiv((long)N * d / 2, 256));
+      if (sw == K - 1) hipLaunchKernelGGL((k_refine_bwd<T, DH, COMM_NSQ>), rgrid, dim3(256), 0, s, ra);
+      else hipLaunchKernelGGL((k_refine_bwd<T, DH, 1>), rgrid, dim3(256), 0, s, ra);
       // dv_in = dv_ctx . W_vctx (mult family)
       if (mult) {
         EpiVinBwd<T> ev{g, N, c->ctx_mod, c->mult_res_lambda, sv.save1 + sw * NS * 4 * d, L->sig,
@@ -273,23 +283,12 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
         AttnBwdArgs<T> aa{g, qr, kself, vraw, Kin, Vin, in_stride, in_row0, sv.o + sw * NS * d,
                           sv.ssq + sw * NS * h, ws.gw, ws.rowdot, d / DU_EPI_TN,
                           sw == K - 1 ? ws.docat : nullptr, sv.stat_m + sw * (size_t)BH * CMAX,
-                          sv.stat_z + sw * (size_t)BH * CMAX, Mx, ws.G, ws.Dbar, sw == K - 1 ? 1 : 0,
+                          sv.stat_z + sw * (size_t)BH * CMAX, Mx, ws.Grow, ws.Drow, ws.Mrow, ws.klim,
+                          sw == K - 1 ? 1 : 0,
                           scale, inv_d, c->rms_eps, dKo, dVo, ws.dkself, ws.dvraw, ws.dq};
-        const size_t lds = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
-        hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(2, BH), dim3(256), lds, s, aa);
+        hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(2, BH), dim3(256), lds_attn, s, aa);
         dKn = dKo; dVn = dVo;
-        dn_stride = (long)CMAX * DH;
-        dn_row0 = 0;
       }
-    }
-    // committed-prefix VJP (once per cell) into the grad cache and dq
-    if (pos0 > 0) {
-      const CommPlan cp = comm_plan_bwd(pos0);
-      CommBwdArgs<T> ca{g, cp.split_len, qr, Kc, Vc, Mx, ws.G, ws.Dbar, scale, ws.dKgc, ws.dVgc, ws.dq_part};
-      const size_t lds = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
-      hipLaunchKernelGGL((k_comm_bwd<T, DH>), dim3(cp.nsplit, BH), dim3(256), lds, s, ca);
-      hipLaunchKernelGGL(k_dq_reduce, dim3(cdiv((long)BH * cc * DH, 256)), dim3(256), 0, s, g, cp.nsplit,
-                         (const float*)ws.dq_part, ws.dq);
     }
     // operands of the sweep weight grads (dW_sweep = dctx^T u, dW_vctx = dv_ctx^T v_in):
     // this cell's K*N rows become columns [coff, coff + K*N) of the layer's transposes;
@@ -313,6 +312,12 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
     const int Kp = (int)(cdiv(coff, 64) * 64);
     gemm_splitk_f32<T>(ws.dctxT, ws.Rp, ws.uT, ws.Rp, Kp, 4 * d, d, 1, ws.kpart, ws.dWs, s);
     if (mult) gemm_splitk_f32<T>(ws.dvcT, ws.Rp, ws.vinT, ws.Rp, Kp, d, d, 1, ws.kpart, gr->w_vctx, s);
+  }
+
+  // committed-prefix VJP, query side: every row with a committed prefix, into dq
+  {
+    CommQueryArgs<T> qa{B, h, T_, cache_T, t_end, ws.klim, qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow, scale, ws.dq};
+    hipLaunchKernelGGL((k_comm_dq<T, DH>), dim3(BH, cdiv(t_end, 64)), dim3(256), lds_attn, s, qa);
   }
 
   // ---- projection VJP

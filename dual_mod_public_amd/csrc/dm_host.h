@@ -78,21 +78,6 @@ inline CommPlan comm_plan(int pos0, int BH) {
   const int split_len = cdiv(cdiv(pos0, nsplit), 64) * 64;
   return CommPlan{cdiv(pos0, split_len), split_len};
 }
-// committed-prefix split plan of the backward: more, shorter splits (the VJP does
-// ~3x the forward's work per key and has no sweep loop to amortise over)
-constexpr int BWD_SPLIT_MIN = 128;
-constexpr int BWD_MAX_SPLITS = 32;
-inline CommPlan comm_plan_bwd(int pos0) {
-  if (pos0 <= 0) return CommPlan{0, 0};
-  int nsplit = cdiv(pos0, BWD_SPLIT_MIN);
-  if (nsplit > BWD_MAX_SPLITS) nsplit = BWD_MAX_SPLITS;
-  const int split_len = cdiv(cdiv(pos0, nsplit), 64) * 64;
-  return CommPlan{cdiv(pos0, split_len), split_len};
-}
-inline int comm_splits_max_bwd(int cache_T) {
-  int n = cdiv(cache_T, BWD_SPLIT_MIN);
-  return n < 1 ? 1 : (n > BWD_MAX_SPLITS ? BWD_MAX_SPLITS : n);
-}
 inline int comm_splits_max(int cache_T) {
   int n = cdiv(cache_T, COMM_SPLIT_MIN);
   return n < 1 ? 1 : (n > COMM_MAX_SPLITS ? COMM_MAX_SPLITS : n);
