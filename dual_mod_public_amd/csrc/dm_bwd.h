@@ -445,15 +445,22 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
     for (int t = 0; t < 4; ++t) { S[t] = zero4(); dP[t] = zero4(); }
     wave_mma<T, DH, 4>(Qs + 16 * wave * LDE, LDE, Ks, LDE, S);
     wave_mma<T, DH, 4>(dOs + 16 * wave * LDE, LDE, Vs, LDE, dP);
+    // exponentials for every element, then masked (a masked exponential would
+    // become a branch); 1 / Z once per row
+    float Mr[4], rZ[4], Dr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * wave + 4 * g4 + r;
+      Mr[r] = sM[i]; rZ[r] = 1.f / sZ[i]; Dr[r] = sD[i];
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int il = 4 * g4 + r, i = 16 * wave + il;
-      const float Mi = sM[i], Zi = sZ[i], Di = sD[i];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int j = 16 * t + lc;
-        const float p = (j < i && i < c) ? __expf(S[t][r] * a.scale - Mi) / Zi : 0.f;
-        W[il * LDI + j] = from_f<T>(p * (dP[t][r] - Di));
+        const float e = __expf(S[t][r] * a.scale - Mr[r]) * rZ[r];
+        W[il * LDI + j] = from_f<T>((j < i && i < c ? e : 0.f) * (dP[t][r] - Dr[r]));
       }
     }
     floatx4 dQ[NDT];
@@ -488,15 +495,21 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
     for (int t = 0; t < 4; ++t) { St[t] = zero4(); dPt[t] = zero4(); }
     wave_mma<T, DH, 4>(Ks + 16 * wave * LDE, LDE, Qs, LDE, St);
     wave_mma<T, DH, 4>(Vs + 16 * wave * LDE, LDE, dOs, LDE, dPt);
+    float Mq[4], rZq[4], Dq[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int i = 16 * t + lc;
+      Mq[t] = sM[i]; rZq[t] = 1.f / sZ[i]; Dq[t] = sD[i];
+    }
     float Pt[4][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int i = 16 * t + lc;
-      const float Mi = sM[i], Zi = sZ[i];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = 16 * wave + 4 * g4 + r;
-        Pt[t][r] = (j < i && i < c) ? __expf(St[t][r] * a.scale - Mi) / Zi : 0.f;
+        const float e = __expf(St[t][r] * a.scale - Mq[t]) * rZq[t];
+        Pt[t][r] = (j < i && i < c) ? e : 0.f;
         W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r]);
       }
     }
@@ -507,9 +520,8 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int i = 16 * t + lc;
-      const float Di = sD[i];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r] * (dPt[t][r] - Di));
+      for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r] * (dPt[t][r] - Dq[t]));
     }
     wave_mma<T, 64, NDT>(W, LDI, Qt, LDI, dK);
 #pragma unroll
@@ -643,6 +655,12 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
     for (int u = 0; u < 4; ++u) { St[u] = zero4(); dPt[u] = zero4(); }
     wave_mma<T, DH, 4>(Ks + 16 * wave * LDE, LDE, Qs, LDE, St);
     wave_mma<T, DH, 4>(Vs + 16 * wave * LDE, LDE, Gs, LDE, dPt);
+    // the row values are read before the exponentials, which are computed for every
+    // element and then masked (a masked exponential with its LDS read would become
+    // a branch that waits for that read)
+    float mq[4], dq[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) { mq[u] = sM[16 * u + lc]; dq[u] = sD[16 * u + lc]; }
     float Et[4][4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -650,7 +668,8 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = 16 * wave + 4 * g4 + r;
-        Et[u][r] = (j < a.kc && i < nq) ? __expf(St[u][r] * a.scale - sM[i]) : 0.f;
+        const float e = __expf(St[u][r] * a.scale - mq[u]);
+        Et[u][r] = (j < a.kc && i < nq) ? e : 0.f;
         W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[u][r]);
       }
     }
@@ -659,7 +678,7 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
     for (int u = 0; u < 4; ++u) {
       const int i = 16 * u + lc;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[u][r] * (dPt[u][r] - sD[i]));
+      for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[u][r] * (dPt[u][r] - dq[u]));
     }
     wave_mma<T, 64, NDT>(W, LDI, Qt, LDI, dK);
   }
@@ -739,6 +758,10 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
   floatx4 dQ[NDT];
 #pragma unroll
   for (int t = 0; t < NDT; ++t) dQ[t] = zero4();
+  // the lane's rows' prefix length, row max and Dbar, read once (published by the
+  // first tile's barrier)
+  int lq[4];
+  float mq[4], dq[4];
   // the next key tile in registers (raw words; rows past the end zeroed when staged)
   uint4 kv[NW], vv[NW];
   auto load_keys = [&](int k0) {
@@ -764,6 +787,13 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
       for (int e = 0; e < VT; ++e) Kt[(re0 + w * VT + e) * LDI + ri] = from_f<T>(f[e]);
     }
     __syncthreads();
+    if (k0 == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * wave + 4 * g4 + r;
+        lq[r] = sL[i]; mq[r] = sM[i]; dq[r] = sD[i];
+      }
+    }
     if (k0 + 64 < k_end) load_keys(k0 + 64);
     floatx4 S[4], dP[4];
 #pragma unroll
@@ -772,25 +802,30 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
     wave_mma<T, DH, 4>(Gs + 16 * wave * LDE, LDE, Vs, LDE, dP);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int il = 4 * g4 + r, i = 16 * wave + il;
+      const int il = 4 * g4 + r;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int j = k0 + 16 * t + lc;
-        const float e = (j < sL[i]) ? __expf(S[t][r] * a.scale - sM[i]) : 0.f;
-        W[il * LDI + 16 * t + lc] = from_f<T>(e * (dP[t][r] - sD[i]));
+        const float e = __expf(S[t][r] * a.scale - mq[r]);
+        W[il * LDI + 16 * t + lc] = from_f<T>((j < lq[r] ? e : 0.f) * (dP[t][r] - dq[r]));
       }
     }
     wave_mma<T, 64, NDT>(W, LDI, Kt, LDI, dQ);
   }
+  // dq rows: every current value loaded first, then the sums stored
+  float old[4][NDT];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int ic = min(16 * wave + 4 * g4 + r, nq - 1);
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) old[r][t] = a.dq[(qrow0 + ic) * DH + 16 * t + lc];
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int i = 16 * wave + 4 * g4 + r;
-    if (i >= nq || sL[i] == 0) continue;
+    if (i >= nq || lq[r] == 0) continue;
 #pragma unroll
-    for (int t = 0; t < NDT; ++t) {
-      float* p = a.dq + (qrow0 + i) * DH + 16 * t + lc;
-      *p += a.scale * dQ[t][r];
-    }
+    for (int t = 0; t < NDT; ++t) a.dq[(qrow0 + i) * DH + 16 * t + lc] = old[r][t] + a.scale * dQ[t][r];
   }
 }
 
