@@ -170,8 +170,10 @@ int dm_layer_fwd(const dm_config* cfg, const dm_packed* w, const void* x, void* 
  * cells in reverse order; each cell takes its n_sweeps sweep states from the
  * forward's tape (non-NULL, same schedule) or recomputes them exactly from the
  * forward's projections (bufs) and final cache rows (tape NULL, as the reference),
- * then runs the sweeps backward; grads of the committed rows it read accumulate in
- * an fp32 grad cache consumed by the earlier cells.
+ * then runs the sweeps backward. Before a cell's sweeps, the grads its final rows
+ * receive from the committed-prefix attention of every later row are summed (the
+ * reference's grad cache, backward.py:27-123, without a running fp32 buffer); the
+ * query side of that attention is computed for every row once, at the end.
  * Inputs are exactly what dm_layer_fwd produced / consumed (x, bufs, caches, ocat)
  * plus dy [B, T, d]. Writes dx [B, T, d] (storage dtype) and ADDS the parameter
  * gradients into g (fp32, reference layout). Needs the *_t fields of w. */
