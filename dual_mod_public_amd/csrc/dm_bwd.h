@@ -44,6 +44,21 @@ DM_DEV void wave_mma(const T* X, int ldx, const T* Y, int ldy, floatx4 (&acc)[NT
   }
 }
 
+// The same with the B operand read from the transposed view of a row-major LDS
+// matrix Z [KD rows][ldz]: acc[t] += X[16 rows, KD] . Z[:, 16 t + (0..15)] (no
+// transposed copy of Z is staged).
+template <typename T, int KD, int NT>
+DM_DEV void wave_mma_bt(const T* X, int ldx, const T* Z, int ldz, floatx4 (&acc)[NT]) {
+  using MF = Mfma<T>;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 0; k < KD; k += MF::KSTEP) {
+    const typename MF::frag a = MF::load(X + (lane & 15) * ldx + k + (lane >> 4) * MF::KPL);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = MF::mma(a, MF::load_tr(Z + (long)k * ldz + 16 * t, ldz), acc[t]);
+  }
+}
+
 // packed GEMM-1 column of the k_ctx / g_k(u) quads (see EpiSweep1)
 template <int DH> DM_DEV int col_k(int hd, int jj, int part) {
   return hd * 2 * DH + 64 * (jj / 16) + 16 * part + (jj % 16);
@@ -295,8 +310,8 @@ template <typename T, int DH> struct AttnBwdCfg {
   static constexpr int PAD = 16 / (int)sizeof(T);
   static constexpr int LDE = DH + PAD;     // rows over head_dim
   static constexpr int LDI = 64 + PAD;     // rows over the 64 queries / keys
-  // Qs, Ks, Vs, dOs [64][LDE]; Qt, Kt, dOt [DH][LDI]; per-wave stage [4][16][LDI]
-  static constexpr int LDS_ELEMS = 4 * 64 * LDE + 3 * DH * LDI + 4 * 16 * LDI;
+  // four [64][LDE] row-major tiles (Q, K, V, dO or G) + a per-wave stage [4][16][LDI]
+  static constexpr int LDS_ELEMS = 4 * 64 * LDE + 4 * 16 * LDI;
 };
 
 template <typename T, int DH>
@@ -308,10 +323,7 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
   T* Ks = Qs + 64 * LDE;
   T* Vs = Ks + 64 * LDE;
   T* dOs = Vs + 64 * LDE;
-  T* Qt = dOs + 64 * LDE;
-  T* Kt = Qt + DH * LDI;
-  T* dOt = Kt + DH * LDI;
-  T* Wst = dOt + DH * LDI;
+  T* Wst = dOs + 64 * LDE;
   __shared__ float sM[64], sZ[64], sD[64];
 
   const CellGeom& g = a.g;
@@ -421,13 +433,6 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
     store_vec<T, EPT>(Ks + i * LDE + e0, kv);
     store_vec<T, EPT>(Vs + i * LDE + e0, vv);
     store_vec<T, EPT>(dOs + i * LDE + e0, dO);
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const int col = e0 + e;
-      Qt[col * LDI + i] = from_f<T>(q[e]);
-      Kt[col * LDI + i] = from_f<T>(kv[e]);
-      dOt[col * LDI + i] = from_f<T>(dO[e]);
-    }
   }
   __syncthreads();
 
@@ -466,7 +471,7 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
     floatx4 dQ[NDT];
 #pragma unroll
     for (int t = 0; t < NDT; ++t) dQ[t] = zero4();
-    wave_mma<T, 64, NDT>(W, LDI, Kt, LDI, dQ);
+    wave_mma_bt<T, 64, NDT>(W, LDI, Ks, LDE, dQ);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = 16 * wave + 4 * g4 + r;
@@ -516,14 +521,14 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
     floatx4 dV[NDT], dK[NDT];
 #pragma unroll
     for (int t = 0; t < NDT; ++t) { dV[t] = zero4(); dK[t] = zero4(); }
-    wave_mma<T, 64, NDT>(W, LDI, dOt, LDI, dV);
+    wave_mma_bt<T, 64, NDT>(W, LDI, dOs, LDE, dV);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int i = 16 * t + lc;
 #pragma unroll
       for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r] * (dPt[t][r] - Dq[t]));
     }
-    wave_mma<T, 64, NDT>(W, LDI, Qt, LDI, dK);
+    wave_mma_bt<T, 64, NDT>(W, LDI, Qs, LDE, dK);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int j = 16 * wave + 4 * g4 + r;
@@ -576,9 +581,7 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
   T* Vs = Ks + 64 * LDE;
   T* Qs = Vs + 64 * LDE;
   T* Gs = Qs + 64 * LDE;
-  T* Qt = Gs + 64 * LDE;
-  T* Gt = Qt + DH * LDI;
-  T* Wst = Gt + DH * LDI;
+  T* Wst = Gs + 64 * LDE;
   __shared__ float sM[64], sD[64];
 
   const int s = blockIdx.x, bh = blockIdx.y;
@@ -630,21 +633,12 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
     const int nq = min(64, a.q_hi - (a.q_lo + 64 * t));
     __syncthreads();   // the previous tile's readers are done (first pass: publishes K / V)
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const uint4 q = keep_if(qv[w], tok);
-      *reinterpret_cast<uint4*>(Qs + ri * LDE + re0 + w * VT) = q;
-      float f[VT];
-      unpack16<T>(q, f);
-#pragma unroll
-      for (int e = 0; e < VT; ++e) Qt[(re0 + w * VT + e) * LDI + ri] = from_f<T>(f[e]);
-    }
+    for (int w = 0; w < NW; ++w) *reinterpret_cast<uint4*>(Qs + ri * LDE + re0 + w * VT) = keep_if(qv[w], tok);
     {
       float gv[EPT];
 #pragma unroll
       for (int w = 0; w < GW; ++w) unpack16<float>(keep_if(gw[w], tok), gv + 4 * w);
       store_vec<T, EPT>(Gs + ri * LDE + re0, gv);
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) Gt[(re0 + e) * LDI + ri] = from_f<T>(gv[e]);
     }
     if ((tid & 3) == 0) { sM[ri] = tok ? mv : 0.f; sD[ri] = tok ? dv : 0.f; }
     __syncthreads();
@@ -673,14 +667,14 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
         W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[u][r]);
       }
     }
-    wave_mma<T, 64, NDT>(W, LDI, Gt, LDI, dV);
+    wave_mma_bt<T, 64, NDT>(W, LDI, Gs, LDE, dV);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int i = 16 * u + lc;
 #pragma unroll
       for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[u][r] * (dPt[u][r] - dq[u]));
     }
-    wave_mma<T, 64, NDT>(W, LDI, Qt, LDI, dK);
+    wave_mma_bt<T, 64, NDT>(W, LDI, Qs, LDE, dK);
   }
   const long slot = ((long)s * a.B * a.h + bh) * CMAX;
 #pragma unroll
@@ -715,8 +709,7 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
   T* Gs = Qs + 64 * LDE;
   T* Ks = Gs + 64 * LDE;
   T* Vs = Ks + 64 * LDE;
-  T* Kt = Vs + 64 * LDE;
-  T* Wst = Kt + DH * LDI;
+  T* Wst = Vs + 64 * LDE;
   __shared__ float sM[64], sD[64];
   __shared__ int sL[64];
 
@@ -778,13 +771,8 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
     __syncthreads();   // the previous tile's readers are done (first pass: publishes Q / G)
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const uint4 kw = keep_if(kv[w], kok);
-      *reinterpret_cast<uint4*>(Ks + ri * LDE + re0 + w * VT) = kw;
+      *reinterpret_cast<uint4*>(Ks + ri * LDE + re0 + w * VT) = keep_if(kv[w], kok);
       *reinterpret_cast<uint4*>(Vs + ri * LDE + re0 + w * VT) = keep_if(vv[w], kok);
-      float f[VT];
-      unpack16<T>(kw, f);
-#pragma unroll
-      for (int e = 0; e < VT; ++e) Kt[(re0 + w * VT + e) * LDI + ri] = from_f<T>(f[e]);
     }
     __syncthreads();
     if (k0 == 0) {
@@ -810,7 +798,7 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
         W[il * LDI + 16 * t + lc] = from_f<T>((j < lq[r] ? e : 0.f) * (dP[t][r] - dq[r]));
       }
     }
-    wave_mma<T, 64, NDT>(W, LDI, Kt, LDI, dQ);
+    wave_mma_bt<T, 64, NDT>(W, LDI, Ks, LDE, dQ);
   }
   // dq rows: every current value loaded first, then the sums stored
   float old[4][NDT];

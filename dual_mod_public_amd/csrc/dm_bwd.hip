@@ -445,7 +445,7 @@ int dm_layer_bwd(const dm_config* c, const dm_packed* w, const void* x, const vo
              "attn_norm needs its gradient buffer and bufs->xhat");
   if ((rc = dm_check_schedule(sched, n_cells, L->T))) return rc;
   DM_REQUIRE(L->T <= cache_T, DM_ERR_INVALID, "T=%d > cache_T=%d", L->T, cache_T);
-  {   // the attention VJP keeps Q, K, V, dO and their transposes of a 64-row block in LDS
+  {   // the attention VJP keeps Q, K, V and dO of a 64-row block in LDS
     const size_t lds = c->dtype == DM_BF16
                            ? (c->dh == 64 ? AttnBwdCfg<bf16, 64>::LDS_ELEMS : AttnBwdCfg<bf16, 128>::LDS_ELEMS) * 2
                            : (c->dh == 64 ? AttnBwdCfg<float, 64>::LDS_ELEMS : AttnBwdCfg<float, 128>::LDS_ELEMS) * 4;

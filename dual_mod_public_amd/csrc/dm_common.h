@@ -13,6 +13,9 @@
 typedef __bf16 bf16;
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 
 namespace dm {
@@ -163,6 +166,20 @@ template <> struct Mfma<bf16> {
   }
   // load KPL consecutive elements starting at p (16-byte aligned)
   static DM_DEV frag load(const bf16* p) { return *reinterpret_cast<const frag*>(p); }
+  // The fragment of the transposed view of a row-major LDS matrix X (row stride ldx,
+  // 8-byte aligned rows): lane l gets X[8 (l / 16) + v][l % 16], v = 0..7, i.e. the
+  // B operand k = row, n = column. Two ds_read_b64_tr_b16: in each 16-lane group,
+  // lane s names the 8 bytes at row (s / 4), column 4 (s % 4) of a 4 x 16 block and
+  // receives that block's column s.
+  static DM_DEV frag load_tr(const bf16* X, int ldx) {
+    const int lane = threadIdx.x & 63, g = lane >> 4, s = lane & 15;
+    const bf16* p = X + (8 * g + (s >> 2)) * ldx + 4 * (s & 3);
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * ldx));
+    // whole-vector casts (element-wise inserts into a bf16 vector are mis-lowered)
+    const i16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(frag, both);
+  }
   static DM_DEV frag from_floats(const float* f) {
     frag r;
 #pragma unroll
@@ -178,6 +195,11 @@ template <> struct Mfma<float> {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
   }
   static DM_DEV frag load(const float* p) { return *p; }
+  // transposed view of a row-major LDS matrix X: lane l gets X[l / 16][l % 16]
+  static DM_DEV frag load_tr(const float* X, int ldx) {
+    const int lane = threadIdx.x & 63;
+    return X[(lane >> 4) * ldx + (lane & 15)];
+  }
   static DM_DEV frag from_floats(const float* f) { return f[0]; }
 };
 
