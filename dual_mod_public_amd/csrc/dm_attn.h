@@ -22,13 +22,12 @@ template <typename T, int DH> struct AttnCfg {
   static constexpr int KT = 64;                     // keys per tile
   static constexpr int PAD = 16 / (int)sizeof(T);
   static constexpr int LDK = DH + PAD;              // Ks row stride
-  static constexpr int LDV = KT + PAD;              // Vt row stride (keys)
   static constexpr int LDP = KT + PAD;              // Ps row stride (keys)
   static constexpr int NDT = DH / 16;               // 16-wide output column tiles
   static constexpr int NKS = DH / MF::KSTEP;        // k-steps over head_dim
   static constexpr int NPS = KT / MF::KSTEP;        // k-steps over keys
   static constexpr int VEC = 16 / (int)sizeof(T);   // elements per 16-byte load
-  static constexpr int LDS_ELEMS = KT * LDK + DH * LDV + 4 * 16 * LDP;
+  static constexpr int LDS_ELEMS = 2 * KT * LDK + 4 * 16 * LDP;   // Ks, Vs [key][dh] + per-wave P
 };
 
 template <typename T, int DH> struct FlashState {
@@ -63,8 +62,7 @@ DM_DEV void load_q_frags(const T* qrow_ptr, bool valid, typename Mfma<T>::frag* 
 
 // One key tile held in registers (global -> registers -> LDS, so the next tile's
 // loads can be in flight while the current tile is used). Consecutive lanes take
-// consecutive keys of one 16-byte column chunk, so the transposed V stores of a
-// wave land in one LDS row (no bank conflicts).
+// consecutive 16-byte chunks of a row (whole rows per load instruction).
 template <typename T, int DH, int NT = 256> struct KVRegs {
   static constexpr int VPR = DH / AttnCfg<T, DH>::VEC;             // 16-byte vectors per row
   static constexpr int NV = AttnCfg<T, DH>::KT * VPR / NT;         // vectors per thread (NT threads)
@@ -85,35 +83,33 @@ DM_DEV void load_kv(const T* __restrict__ Kg, const T* __restrict__ Vg, long row
 #pragma unroll
   for (int i = 0; i < R::NV; ++i) {
     const int v = threadIdx.x + NT * i;
-    const int k = v % AttnCfg<T, DH>::KT, c0 = (v / AttnCfg<T, DH>::KT) * AttnCfg<T, DH>::VEC;
+    const int k = v / R::VPR, c0 = (v % R::VPR) * AttnCfg<T, DH>::VEC;
     const long off = (long)(k < nvalid ? k : 0) * row_stride + c0;
     r.k[i] = *reinterpret_cast<const uint4*>(Kg + off);
     r.v[i] = *reinterpret_cast<const uint4*>(Vg + off);
   }
 }
 
-// K rows -> Ks [key][dh], V rows transposed -> Vt [dh][key].
+// K rows -> Ks [key][dh], V rows -> Vs [key][dh] (P V reads V through the
+// transposed-view fragment loads).
 template <typename T, int DH, int NT = 256>
-DM_DEV void store_kv(const KVRegs<T, DH, NT>& r, T* Ks, T* Vt) {
+DM_DEV void store_kv(const KVRegs<T, DH, NT>& r, T* Ks, T* Vs) {
   using C = AttnCfg<T, DH>;
   using R = KVRegs<T, DH, NT>;
 #pragma unroll
   for (int i = 0; i < R::NV; ++i) {
     const int v = threadIdx.x + NT * i;
-    const int k = v % C::KT, c0 = (v / C::KT) * C::VEC;
+    const int k = v / R::VPR, c0 = (v % R::VPR) * C::VEC;
     const bool ok = k < r.nvalid;
     *reinterpret_cast<uint4*>(Ks + k * C::LDK + c0) = keep_if(r.k[i], ok);
-    const uint4 vm = keep_if(r.v[i], ok);
-    const T* ve = reinterpret_cast<const T*>(&vm);
-#pragma unroll
-    for (int j = 0; j < C::VEC; ++j) Vt[(c0 + j) * C::LDV + k] = ve[j];
+    *reinterpret_cast<uint4*>(Vs + k * C::LDK + c0) = keep_if(r.v[i], ok);
   }
 }
 
 // One 64-key tile: S = Q K^T * scale, mask, online softmax update, O += P V.
 // mask(q, key) -> true if the score is kept; q is the wave-relative row + 16*wave.
 template <typename T, int DH, class MASK>
-DM_DEV void flash_tile(const typename Mfma<T>::frag* qf, const T* Ks, const T* Vt, T* Pw,
+DM_DEV void flash_tile(const typename Mfma<T>::frag* qf, const T* Ks, const T* Vs, T* Pw,
                        float scale, const MASK& keep, FlashState<T, DH>& st) {
   using C = AttnCfg<T, DH>;
   using MF = Mfma<T>;
@@ -162,7 +158,7 @@ DM_DEV void flash_tile(const typename Mfma<T>::frag* qf, const T* Ks, const T* V
     typename MF::frag pf = MF::load(Pw + col * C::LDP + kb * MF::KSTEP + g * MF::KPL);
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt) {
-      typename MF::frag vf = MF::load(Vt + (col + 16 * dt) * C::LDV + kb * MF::KSTEP + g * MF::KPL);
+      typename MF::frag vf = MF::load_tr(Vs + kb * MF::KSTEP * C::LDK + 16 * dt, C::LDK);
       st.O[dt] = MF::mma(pf, vf, st.O[dt]);
     }
   }

@@ -299,8 +299,8 @@ static __global__ __launch_bounds__(256) void k_comm_partial(CommArgs<T> a) {
   using C = AttnCfg<T, DH>;
   __shared__ __attribute__((aligned(16))) T lds[C::LDS_ELEMS];
   T* Ks = lds;
-  T* Vt = Ks + C::KT * C::LDK;
-  T* Ps = Vt + DH * C::LDV;
+  T* Vs = Ks + C::KT * C::LDK;
+  T* Ps = Vs + C::KT * C::LDK;
   const CellGeom& g = a.g;
   const int s = blockIdx.x, bh = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -321,11 +321,11 @@ static __global__ __launch_bounds__(256) void k_comm_partial(CommArgs<T> a) {
   for (int k0 = k_begin; k0 < k_end; k0 += C::KT) {
     const int nv = min(C::KT, k_end - k0);
     __syncthreads();
-    store_kv<T, DH>(kv, Ks, Vt);
+    store_kv<T, DH>(kv, Ks, Vs);
     __syncthreads();
     const int k1 = k0 + C::KT;
     if (k1 < k_end) load_kv<T, DH>(Kb + (long)k1 * DH, Vb + (long)k1 * DH, DH, min(C::KT, k_end - k1), kv);
-    flash_tile<T, DH>(qf, Ks, Vt, Ps + wave * 16 * C::LDP, a.scale, KeyBound{nv}, st);
+    flash_tile<T, DH>(qf, Ks, Vs, Ps + wave * 16 * C::LDP, a.scale, KeyBound{nv}, st);
   }
   const int g4 = lane >> 4, col = lane & 15;
 #pragma unroll
@@ -376,8 +376,8 @@ static __global__ __launch_bounds__(64 * NW) void k_attend(AttendArgs<T> a) {
   using C = AttnCfg<T, DH>;
   __shared__ __attribute__((aligned(16))) T lds[C::LDS_ELEMS];
   T* Ks = lds;
-  T* Vt = Ks + C::KT * C::LDK;
-  T* Ps = Vt + DH * C::LDV;
+  T* Vs = Ks + C::KT * C::LDK;
+  T* Ps = Vs + C::KT * C::LDK;
   const CellGeom& g = a.g;
   const int bh = blockIdx.x;
   const int b = bh / g.h, hh = bh - b * g.h;
@@ -476,9 +476,9 @@ static __global__ __launch_bounds__(64 * NW) void k_attend(AttendArgs<T> a) {
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt) vself[r][dt] = to_f(vp[col + 16 * dt]);
   }
-  store_kv<T, DH, 64 * NW>(kv, Ks, Vt);
+  store_kv<T, DH, 64 * NW>(kv, Ks, Vs);
   __syncthreads();
-  flash_tile<T, DH>(qf, Ks, Vt, Ps + wave * 16 * C::LDP, a.scale, KeyStrictLower{q0}, st);
+  flash_tile<T, DH>(qf, Ks, Vs, Ps + wave * 16 * C::LDP, a.scale, KeyStrictLower{q0}, st);
 
   // raw self column: s_self = scale * <q_r, k_self_r> (fp32), value v_raw
 #pragma unroll
