@@ -821,71 +821,64 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
 // projection VJP inputs: d_proj [B*T, nproj*d] in the w_proj row order
 //   q: unrotate dq_r; k: dkraw + unrotate(dkself); v: dvraw; gate x-halves: dglogx;
 //   v_gate: dsig * sig * (1 - sig)
+// and the bias gradients' column partials over the block's rows:
+//   bpart[chunk][0, d) = sum dglogx (b_gk), [d, 2d) = sum dglogx[d..] (b_gv),
+//   [2d, 3d) = sum dsig sig (1 - sig) (b_vgate).
+// One thread per RoPE column pair (jj, jj + DH/2) of a head, PROJ_ROWS rows per
+// block; each row's loads are issued before its stores.
 // ---------------------------------------------------------------------------
+constexpr int PROJ_ROWS = 64;
 template <typename T, int DH>
 static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, int h, int nproj,
                                                   const float* __restrict__ dq, const float* __restrict__ dkraw,
                                                   const float* __restrict__ dkself, const float* __restrict__ dvraw,
                                                   const float* __restrict__ dglogx, const float* __restrict__ dsig,
                                                   const float* __restrict__ sig, const float* __restrict__ cos,
-                                                  const float* __restrict__ sin, T* __restrict__ dproj) {
-  const long idx = blockIdx.x * 256L + threadIdx.x;
-  const int per_row = d / 2;
-  if (idx >= (long)M * per_row) return;
-  const int m = idx / per_row, rem = idx - (long)m * per_row;
-  const int hd = rem / (DH / 2), jj = rem - hd * (DH / 2);
-  const int b = m / T_, t = m - b * T_;
-  const long hr = (((long)b * h + hd) * T_ + t) * DH;
-  const float cs = cos[(long)t * (DH / 2) + jj], sn = sin[(long)t * (DH / 2) + jj];
+                                                  const float* __restrict__ sin, T* __restrict__ dproj,
+                                                  float* __restrict__ bpart) {
+  const int pidx = blockIdx.x * 256 + threadIdx.x;
+  if (pidx >= d / 2) return;
+  const int hd = pidx / (DH / 2), jj = pidx - hd * (DH / 2);
   const int c1 = hd * DH + jj, c2 = c1 + DH / 2;
-  T* D = dproj + (long)m * nproj * d;
-  // q
-  {
-    const float a1 = dq[hr + jj], a2 = dq[hr + jj + DH / 2];
-    D[c1] = from_f<T>(a1 * cs + a2 * sn);
-    D[c2] = from_f<T>(-a1 * sn + a2 * cs);
-  }
-  // k
-  {
-    const float a1 = dkself[hr + jj], a2 = dkself[hr + jj + DH / 2];
-    D[d + c1] = from_f<T>(dkraw[hr + jj] + a1 * cs + a2 * sn);
-    D[d + c2] = from_f<T>(dkraw[hr + jj + DH / 2] - a1 * sn + a2 * cs);
-  }
-  // v
-  D[2 * d + c1] = from_f<T>(dvraw[hr + jj]);
-  D[2 * d + c2] = from_f<T>(dvraw[hr + jj + DH / 2]);
-  // gate x-halves
-  const float* dg = dglogx + (long)m * 2 * d;
-  D[3 * d + c1] = from_f<T>(dg[c1]);
-  D[3 * d + c2] = from_f<T>(dg[c2]);
-  D[4 * d + c1] = from_f<T>(dg[d + c1]);
-  D[4 * d + c2] = from_f<T>(dg[d + c2]);
-  if (nproj == 6) {
-    const float s1 = sig[(long)m * d + c1], s2 = sig[(long)m * d + c2];
-    D[5 * d + c1] = from_f<T>(dsig[(long)m * d + c1] * s1 * (1.f - s1));
-    D[5 * d + c2] = from_f<T>(dsig[(long)m * d + c2] * s2 * (1.f - s2));
-  }
-}
-
-// Column sums of the bias gradients over the M rows, stage 1: part[chunk][col]
-//   cols [0, 2d): dglogx; cols [2d, 3d): dsig * sig * (1 - sig)
-static __global__ __launch_bounds__(256) void k_bias_partial(int M, int d, int ncols, int rows_per_chunk,
-                                                      const float* __restrict__ dglogx,
-                                                      const float* __restrict__ dsig,
-                                                      const float* __restrict__ sig, float* __restrict__ part) {
-  const int col = blockIdx.x * 256 + threadIdx.x;
-  if (col >= ncols) return;
-  const int r0 = blockIdx.y * rows_per_chunk, r1 = min(r0 + rows_per_chunk, M);
-  float s = 0.f;
+  const int r0 = blockIdx.y * PROJ_ROWS, r1 = min(r0 + PROJ_ROWS, M);
+  float bg[4] = {0.f, 0.f, 0.f, 0.f}, bv[2] = {0.f, 0.f};
   for (int m = r0; m < r1; ++m) {
-    if (col < 2 * d) {
-      s += dglogx[(long)m * 2 * d + col];
-    } else {
-      const float sg = sig[(long)m * d + col - 2 * d];
-      s += dsig[(long)m * d + col - 2 * d] * sg * (1.f - sg);
+    const int b = m / T_, t = m - b * T_;
+    const long hr = (((long)b * h + hd) * T_ + t) * DH;
+    const float* dg = dglogx + (long)m * 2 * d;
+    const float cs = cos[(long)t * (DH / 2) + jj], sn = sin[(long)t * (DH / 2) + jj];
+    const float q1 = dq[hr + jj], q2 = dq[hr + jj + DH / 2];
+    const float s1 = dkself[hr + jj], s2 = dkself[hr + jj + DH / 2];
+    const float k1 = dkraw[hr + jj], k2 = dkraw[hr + jj + DH / 2];
+    const float v1 = dvraw[hr + jj], v2 = dvraw[hr + jj + DH / 2];
+    const float g1 = dg[c1], g2 = dg[c2], g3 = dg[d + c1], g4 = dg[d + c2];
+    float z1 = 0.f, z2 = 0.f;
+    if (nproj == 6) {
+      const float sg1 = sig[(long)m * d + c1], sg2 = sig[(long)m * d + c2];
+      z1 = dsig[(long)m * d + c1] * sg1 * (1.f - sg1);
+      z2 = dsig[(long)m * d + c2] * sg2 * (1.f - sg2);
     }
+    T* D = dproj + (long)m * nproj * d;
+    D[c1] = from_f<T>(q1 * cs + q2 * sn);
+    D[c2] = from_f<T>(-q1 * sn + q2 * cs);
+    D[d + c1] = from_f<T>(k1 + s1 * cs + s2 * sn);
+    D[d + c2] = from_f<T>(k2 - s1 * sn + s2 * cs);
+    D[2 * d + c1] = from_f<T>(v1);
+    D[2 * d + c2] = from_f<T>(v2);
+    D[3 * d + c1] = from_f<T>(g1);
+    D[3 * d + c2] = from_f<T>(g2);
+    D[4 * d + c1] = from_f<T>(g3);
+    D[4 * d + c2] = from_f<T>(g4);
+    if (nproj == 6) {
+      D[5 * d + c1] = from_f<T>(z1);
+      D[5 * d + c2] = from_f<T>(z2);
+    }
+    bg[0] += g1; bg[1] += g2; bg[2] += g3; bg[3] += g4;
+    bv[0] += z1; bv[1] += z2;
   }
-  part[(long)blockIdx.y * ncols + col] = s;
+  float* P = bpart + (long)blockIdx.y * 3 * d;
+  P[c1] = bg[0]; P[c2] = bg[1]; P[d + c1] = bg[2]; P[d + c2] = bg[3];
+  P[2 * d + c1] = bv[0]; P[2 * d + c2] = bv[1];
 }
 
 // Column sums of a row-major fp32 matrix [M, ncols], stage 1: part[chunk][col]
@@ -895,7 +888,13 @@ static __global__ __launch_bounds__(256) void k_colsum_partial(int M, int ncols,
   if (col >= ncols) return;
   const int r0 = blockIdx.y * rows_per_chunk, r1 = min(r0 + rows_per_chunk, M);
   float s = 0.f;
-  for (int m = r0; m < r1; ++m) s += src[(long)m * ncols + col];
+  for (int m0 = r0; m0 < r1; m0 += 8) {   // eight rows' loads in flight at a time
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = src[(long)min(m0 + k, r1 - 1) * ncols + col];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += (m0 + k < r1) ? v[k] : 0.f;
+  }
   part[(long)blockIdx.y * ncols + col] = s;
 }
 
@@ -911,45 +910,73 @@ static __global__ __launch_bounds__(256) void k_sum_splits(int S, long n, const 
 }
 
 static __global__ __launch_bounds__(256) void k_sum_rows_add(int nchunk, int ncols, int ld, const float* __restrict__ part,
-                                                      float* __restrict__ out) {
-  const int col = blockIdx.x * 256 + threadIdx.x;
-  if (col >= ncols) return;
+                                                      float* __restrict__ out0, float* __restrict__ out1,
+                                                      float* __restrict__ out2, int seg) {
+  // out_i[c] += sum_k part[k * ld + i * seg + c]: 64 columns per block, four row
+  // groups (rows rg, rg + 4, ..) whose sums are added in LDS; eight loads in flight
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63, rg = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + lane;
+  const int cc = min(col, ncols - 1);
   float s = 0.f;
-  for (int k = 0; k < nchunk; ++k) s += part[(long)k * ld + col];
-  out[col] += s;
+  for (int k0 = rg; k0 < nchunk; k0 += 32) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = part[(long)min(k0 + 4 * k, nchunk - 1) * ld + cc];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += (k0 + 4 * k < nchunk) ? v[k] : 0.f;
+  }
+  red[rg][lane] = s;
+  __syncthreads();
+  if (rg == 0 && col < ncols) {
+    const int i = col / seg, c = col - i * seg;
+    float* out = i == 0 ? out0 : (i == 1 ? out1 : out2);
+    if (out != nullptr) out[c] += red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+  }
 }
 
 // ---------------------------------------------------------------------------
-// attn_norm VJP (attention.py:74-83) with the block residual, one wave per row:
-//   dx = dy + r w dxhat - x r^3 / d <w dxhat, x>; dwa_part[row / 4 group] over rows
+// attn_norm VJP (attention.py:74-83) with the block residual, one wave per row,
+// RMSN_ROWS rows per block:
+//   dx = dy + r w dxhat - x r^3 / d <w dxhat, x>;
+//   dwa_part[block][j] = sum over the block's rows of dxhat x r (the norm weight's
+//   gradient, summed over the blocks afterwards); each wave accumulates its rows in
+//   its own LDS row, the four are added at the end.
 // ---------------------------------------------------------------------------
+constexpr int RMSN_ROWS = 8;
 template <typename T>
 static __global__ __launch_bounds__(256) void k_rmsnorm_bwd(int M, int d, float eps, int residual,
                                                      const T* __restrict__ x, const T* __restrict__ w,
                                                      const float* __restrict__ dxhat, const T* __restrict__ dy,
                                                      T* __restrict__ dx, float* __restrict__ dwa_part) {
-  const int lane = threadIdx.x & 63;
-  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (m >= M) return;
-  const T* xr = x + (long)m * d;
-  const float* gr = dxhat + (long)m * d;
-  float ss = 0.f, dot = 0.f;
-  for (int j = lane; j < d; j += 64) {
-    const float xv = to_f(xr[j]);
-    ss += xv * xv;
-    dot += to_f(w[j]) * gr[j] * xv;
+  extern __shared__ float acc_lds[];   // [4][d]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float* acc = acc_lds + (long)wave * d;
+  for (int j = lane; j < d; j += 64) acc[j] = 0.f;
+  const int r0 = blockIdx.x * RMSN_ROWS, r1 = min(r0 + RMSN_ROWS, M);
+  for (int m = r0 + wave; m < r1; m += 4) {
+    const T* xr = x + (long)m * d;
+    const float* gr = dxhat + (long)m * d;
+    float ss = 0.f, dot = 0.f;
+    for (int j = lane; j < d; j += 64) {
+      const float xv = to_f(xr[j]);
+      ss += xv * xv;
+      dot += to_f(w[j]) * gr[j] * xv;
+    }
+    ss = wave_sum(ss);
+    dot = wave_sum(dot);
+    const float r = rsqrtf(ss / (float)d + eps);
+    const float c3 = r * r * r / (float)d * dot;
+    for (int j = lane; j < d; j += 64) {
+      const float xv = to_f(xr[j]), g = gr[j];
+      const float yv = residual ? to_f(dy[(long)m * d + j]) : 0.f;
+      dx[(long)m * d + j] = from_f<T>(r * to_f(w[j]) * g - xv * c3 + yv);
+      acc[j] += g * xv * r;
+    }
   }
-  ss = wave_sum(ss);
-  dot = wave_sum(dot);
-  const float r = rsqrtf(ss / (float)d + eps);
-  const float c3 = r * r * r / (float)d * dot;
-  for (int j = lane; j < d; j += 64) {
-    const float xv = to_f(xr[j]);
-    float v = r * to_f(w[j]) * gr[j] - xv * c3;
-    if (residual) v += to_f(dy[(long)m * d + j]);
-    dx[(long)m * d + j] = from_f<T>(v);
-    dwa_part[(long)m * d + j] = gr[j] * xv * r;   // summed over rows afterwards
-  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < d; j += 256)
+    dwa_part[(long)blockIdx.x * d + j] = acc_lds[j] + acc_lds[d + j] + acc_lds[2 * d + j] + acc_lds[3 * d + j];
 }
 
 // dx = dy + dxhat (no attn_norm) or dx = dxhat (no residual either)
@@ -987,7 +1014,20 @@ static __global__ __launch_bounds__(256) void k_unpack_add(UnpackArgs a) {
   const int r = row - acc;
   const float* src = a.src + (long)(sg.src_row + r) * a.ncols;
   float* dst = sg.dst + (long)r * sg.dst_ld + sg.dst_col;
-  for (int j = threadIdx.x; j < a.ncols; j += 256) dst[j] += src[j];
+  for (int j0 = 0; j0 < a.ncols; j0 += 4 * 256) {   // four elements' loads before their stores
+    float sv[4], dv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int j = min(j0 + k * 256 + (int)threadIdx.x, a.ncols - 1);
+      sv[k] = src[j];
+      dv[k] = dst[j];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int j = j0 + k * 256 + threadIdx.x;
+      if (j < a.ncols) dst[j] = dv[k] + sv[k];
+    }
+  }
 }
 
 }  // namespace dm

@@ -39,7 +39,7 @@ template <typename T> struct BwdWs {
   T *tA, *tB;                           // layer-level transposes [max(nproj*d, d), B*T] and [d, B*T]
   float* dxhat;                         // [B*T, d]
   float *dWp, *dWs;                     // packed weight-grad staging [nproj*d, d], [4d, d]
-  float* colpart;                       // [NCHUNK, 3d]
+  float* colpart;                       // [max(NCHUNK, B*T / PROJ_ROWS), 3d] column partials
   size_t bytes;
 };
 
@@ -98,7 +98,7 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.dxhat = cv.take<float>(BT * d * 4);
   w.dWp = cv.take<float>(nproj * d * d * 4);
   w.dWs = cv.take<float>(4 * d * d * 4);
-  w.colpart = cv.take<float>(NCHUNK * 3 * d * 4);
+  w.colpart = cv.take<float>((size_t)std::max<long>(NCHUNK, cdiv(BT, PROJ_ROWS)) * 3 * d * 4);
   w.bytes = cv.off;
   return w;
 }
@@ -112,7 +112,8 @@ inline void fill0(float* p, size_t n, hipStream_t s) {
 inline void colsum_add(const float* src, int M, int ncols, float* part, float* dst, hipStream_t s) {
   const int rpc = cdiv(M, NCHUNK);
   hipLaunchKernelGGL(k_colsum_partial, dim3(cdiv(ncols, 256), NCHUNK), dim3(256), 0, s, M, ncols, rpc, src, part);
-  hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(ncols, 256)), dim3(256), 0, s, NCHUNK, ncols, ncols, part, dst);
+  hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(ncols, 64)), dim3(256), 0, s, NCHUNK, ncols, ncols, part, dst,
+                     (float*)nullptr, (float*)nullptr, ncols);
 }
 
 inline void unpack(const std::vector<UnpackSeg>& segs, int ncols, const float* src, hipStream_t s) {
@@ -321,21 +322,15 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   }
 
   // ---- projection VJP
-  hipLaunchKernelGGL((k_proj_bwd<T, DH>), dim3(cdiv((long)BT * d / 2, 256)), dim3(256), 0, s, BT, T_, d, h,
-                     nproj, (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself,
-                     (const float*)ws.dvraw, (const float*)ws.dglogx, (const float*)ws.dsig, (const float*)L->sig,
-                     cos, sin, ws.dproj);
-  {   // bias grads: column sums of dglogx (b_gk | b_gv) and of dsig sig (1 - sig) (b_vgate)
-    const int ncols = mult ? 3 * d : 2 * d;
-    const int rpc = cdiv(BT, NCHUNK);
-    hipLaunchKernelGGL(k_bias_partial, dim3(cdiv(ncols, 256), NCHUNK), dim3(256), 0, s, BT, d, ncols, rpc,
-                       (const float*)ws.dglogx, (const float*)ws.dsig, (const float*)L->sig, ws.colpart);
-    float* dst[3] = {gr->b_gk, gr->b_gv, mult ? gr->b_vgate : nullptr};
-    for (int i = 0; i < 3; ++i)
-      if (dst[i])
-        hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(d, 256)), dim3(256), 0, s, NCHUNK, d, ncols,
-                           (const float*)(ws.colpart + i * d), dst[i]);
-  }
+  // (+ the bias grads' column partials: sums of dglogx (b_gk | b_gv) and of
+  // dsig sig (1 - sig) (b_vgate) over each block's rows)
+  const int pchunks = cdiv(BT, PROJ_ROWS);
+  hipLaunchKernelGGL((k_proj_bwd<T, DH>), dim3(cdiv(d / 2, 256), pchunks), dim3(256), 0, s, BT, T_, d, h, nproj,
+                     (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself, (const float*)ws.dvraw,
+                     (const float*)ws.dglogx, (const float*)ws.dsig, (const float*)L->sig, cos, sin, ws.dproj,
+                     ws.colpart);
+  hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks, 3 * d, 3 * d,
+                     (const float*)ws.colpart, gr->b_gk, gr->b_gv, mult ? gr->b_vgate : nullptr, d);
   const T* xhat = norm ? (const T*)L->xhat : x;
   // dW_proj = d_proj^T . xhat (packed rows), dxhat = d_proj . W_proj
   gemm_tn<T>(ws.dproj, (long)nproj * d, xhat, d, ws.dWp, nproj * d, d, BT, 0, ws.tA, ws.tB, ws.kpart, s);
@@ -381,9 +376,10 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   // attn_norm VJP + residual
   if (norm) {
     float* dwa_part = reinterpret_cast<float*>(ws.dproj);
-    hipLaunchKernelGGL(k_rmsnorm_bwd<T>, dim3(cdiv(BT, 4)), dim3(256), 0, s, BT, d, c->rms_eps, residual ? 1 : 0,
-                       x, (const T*)w->attn_norm_w, (const float*)ws.dxhat, dy, dx, dwa_part);
-    colsum_add(dwa_part, BT, d, ws.colpart, gr->attn_norm_w, s);
+    hipLaunchKernelGGL(k_rmsnorm_bwd<T>, dim3(cdiv(BT, RMSN_ROWS)), dim3(256), 4 * d * sizeof(float), s, BT, d,
+                       c->rms_eps, residual ? 1 : 0, x, (const T*)w->attn_norm_w, (const float*)ws.dxhat, dy, dx,
+                       dwa_part);
+    colsum_add(dwa_part, cdiv(BT, RMSN_ROWS), d, ws.colpart, gr->attn_norm_w, s);
   } else {
     hipLaunchKernelGGL(k_dx_plain<T>, dim3(std::min(cdiv((long)BT * d, 256), 4096)), dim3(256), 0, s,
                        (long)BT * d, residual ? 1 : 0, (const float*)ws.dxhat, dy, dx);

@@ -196,6 +196,8 @@ template <typename T, int DH> struct EpiProj {
 
   // The wave tile spans whole heads (FN * 16 a multiple of DH); within each head
   // columns j and j + DH/32 of the tile are the RoPE pair (jj, jj + DH/2).
+  // Every table value the tile needs is loaded before the first store (a load
+  // after a store that may alias it would wait for one memory latency per row).
   template <int FM, int FN>
   DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
     static_assert((FN * 16) % DH == 0, "projection wave tile must span whole heads");
@@ -204,6 +206,25 @@ template <typename T, int DH> struct EpiProj {
     constexpr int HF = FH / 2;
     const int lane = threadIdx.x & 63, lc = lane & 15;
     const int seg = col0 / d, c0 = col0 - seg * d;
+    float cs[FM][4][HF], sn[FM][4][HF], bs[FN];
+    if (seg <= 1) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int m = min(row0 + 16 * i + 4 * (lane >> 4) + q, M - 1);
+          const long rrow = (long)(rope_t0 + m % Tl) * (DH / 2);
+#pragma unroll
+          for (int j = 0; j < HF; ++j) {
+            cs[i][q][j] = cos[rrow + 16 * j + lc];
+            sn[i][q][j] = sin[rrow + 16 * j + lc];
+          }
+        }
+    } else if (seg >= 3) {
+      const int bo = (seg - 3) * d + c0;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bs[j] = bias[bo + 16 * j + lc];
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -217,20 +238,19 @@ template <typename T, int DH> struct EpiProj {
           const int hh = c0 / DH + hb;
           const long hrow = (((long)b * h + hh) * Tbuf + buf_t0 + tl) * DH;
           if (seg <= 1) {
-            const long rrow = (long)(rope_t0 + tl) * (DH / 2);
 #pragma unroll
             for (int j = 0; j < HF; ++j) {
               const int jj = 16 * j + lc;
               const float a = acc[i][hb * FH + j][q], bb = acc[i][hb * FH + j + HF][q];
-              const float cs = cos[rrow + jj], sn = sin[rrow + jj];
+              const float c = cs[i][q][j], sv = sn[i][q][j];
               if (seg == 0) {
-                qr[hrow + jj] = from_f<T>(a * cs - bb * sn);
-                qr[hrow + jj + DH / 2] = from_f<T>(bb * cs + a * sn);
+                qr[hrow + jj] = from_f<T>(a * c - bb * sv);
+                qr[hrow + jj + DH / 2] = from_f<T>(bb * c + a * sv);
               } else {
                 kraw[hrow + jj] = from_f<T>(a);
                 kraw[hrow + jj + DH / 2] = from_f<T>(bb);
-                kself[hrow + jj] = from_f<T>(a * cs - bb * sn);
-                kself[hrow + jj + DH / 2] = from_f<T>(bb * cs + a * sn);
+                kself[hrow + jj] = from_f<T>(a * c - bb * sv);
+                kself[hrow + jj + DH / 2] = from_f<T>(bb * c + a * sv);
               }
             }
           } else if (seg == 2) {
@@ -243,13 +263,13 @@ template <typename T, int DH> struct EpiProj {
 #pragma unroll
           for (int j = 0; j < FN; ++j) {
             const int col = c0 + 16 * j + lc;
-            glogx[xrow * 2 * d + gs * d + col] = acc[i][j][q] + bias[gs * d + col];
+            glogx[xrow * 2 * d + gs * d + col] = acc[i][j][q] + bs[j];
           }
         } else if (seg == 5) {
 #pragma unroll
           for (int j = 0; j < FN; ++j) {
             const int col = c0 + 16 * j + lc;
-            sig[xrow * d + col] = sigmoidf_(acc[i][j][q] + bias[2 * d + col]);
+            sig[xrow * d + col] = sigmoidf_(acc[i][j][q] + bs[j]);
           }
         }
       }
@@ -737,9 +757,19 @@ template <typename T> struct EpiResidual {
   int M, N;
   const T* __restrict__ x;
   T* __restrict__ y;
+  // the residual rows are loaded before the first store (y may alias x)
   template <int FM, int FN>
   DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
     const int lane = threadIdx.x & 63, lc = lane & 15;
+    float xv[FM][4][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = min(row0 + 16 * i + 4 * (lane >> 4) + q, M - 1);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) xv[i][q][j] = x != nullptr ? to_f(x[(long)m * N + col0 + 16 * j + lc]) : 0.f;
+      }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -747,12 +777,7 @@ template <typename T> struct EpiResidual {
         const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
         if (m >= M) continue;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const long idx = (long)m * N + col0 + 16 * j + lc;
-          float v = acc[i][j][q];
-          if (x != nullptr) v += to_f(x[idx]);
-          y[idx] = from_f<T>(v);
-        }
+        for (int j = 0; j < FN; ++j) y[(long)m * N + col0 + 16 * j + lc] = from_f<T>(acc[i][j][q] + xv[i][q][j]);
       }
   }
 };
@@ -763,10 +788,20 @@ struct EpiStoreF32 {
   int M, N, accumulate;
   float* __restrict__ C;
   long zstride = 0;
+  // with accumulate, every old value is loaded before the first store
   template <int FM, int FN>
   DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
     const int lane = threadIdx.x & 63, lc = lane & 15;
     float* __restrict__ C = this->C + (long)blockIdx.z * zstride;
+    float old[FM][4][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = min(row0 + 16 * i + 4 * (lane >> 4) + q, M - 1);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) old[i][q][j] = accumulate ? C[(long)m * N + col0 + 16 * j + lc] : 0.f;
+      }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -774,10 +809,7 @@ struct EpiStoreF32 {
         const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
         if (m >= M) continue;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const long idx = (long)m * N + col0 + 16 * j + lc;
-          C[idx] = accumulate ? C[idx] + acc[i][j][q] : acc[i][j][q];
-        }
+        for (int j = 0; j < FN; ++j) C[(long)m * N + col0 + 16 * j + lc] = old[i][q][j] + acc[i][j][q];
       }
   }
 };
