@@ -98,7 +98,14 @@ void run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int 
                      qr, kraw, kself, vraw, glogx, sig};
   SrcRows<T> sa{xhat, c->d, M};
   SrcRows<T> sb{(const T*)w->w_proj, c->d, nseg * c->d};
-  // (256 x 256 blocks measured slower here: the epilogue's scattered stores dominate)
+  // bf16, whole 256-row / 256-column tiles: 256 x 256 blocks (four 128 x 128 wave tiles,
+  // two direct-to-LDS stages); otherwise 128 x 128 with wave tiles spanning whole heads
+  if constexpr (sizeof(T) == 2) {
+    if (M % 256 == 0 && (nseg * c->d) % 256 == 0 && c->d % 64 == 0) {
+      launch_gemm<T, 256, 256, 2, 2, -2>(sa, sb, M, nseg * c->d, c->d, epi, s, PROF_PROJ);
+      return;
+    }
+  }
   if constexpr (DH == 64)
     launch_gemm_auto<T, 128, 128, 2, 2, 3, 4>(sa, sb, M, nseg * c->d, c->d, epi, s, PROF_PROJ);
   else

@@ -196,8 +196,9 @@ template <typename T, int DH> struct EpiProj {
 
   // The wave tile spans whole heads (FN * 16 a multiple of DH); within each head
   // columns j and j + DH/32 of the tile are the RoPE pair (jj, jj + DH/2).
-  // Every table value the tile needs is loaded before the first store (a load
-  // after a store that may alias it would wait for one memory latency per row).
+  // The RoPE table values of 16-row group i + 1 are loaded before group i is
+  // stored (a load after a store that may alias it would wait for one memory
+  // latency per group).
   template <int FM, int FN>
   DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
     static_assert((FN * 16) % DH == 0, "projection wave tile must span whole heads");
@@ -206,27 +207,29 @@ template <typename T, int DH> struct EpiProj {
     constexpr int HF = FH / 2;
     const int lane = threadIdx.x & 63, lc = lane & 15;
     const int seg = col0 / d, c0 = col0 - seg * d;
-    float cs[FM][4][HF], sn[FM][4][HF], bs[FN];
-    if (seg <= 1) {
+    float cs[2][4][HF], sn[2][4][HF], bs[FN];
+    auto load_rope = [&](int i, int buf) {
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+      for (int q = 0; q < 4; ++q) {
+        const int m = min(row0 + 16 * i + 4 * (lane >> 4) + q, M - 1);
+        const long rrow = (long)(rope_t0 + m % Tl) * (DH / 2);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int m = min(row0 + 16 * i + 4 * (lane >> 4) + q, M - 1);
-          const long rrow = (long)(rope_t0 + m % Tl) * (DH / 2);
-#pragma unroll
-          for (int j = 0; j < HF; ++j) {
-            cs[i][q][j] = cos[rrow + 16 * j + lc];
-            sn[i][q][j] = sin[rrow + 16 * j + lc];
-          }
+        for (int j = 0; j < HF; ++j) {
+          cs[buf][q][j] = cos[rrow + 16 * j + lc];
+          sn[buf][q][j] = sin[rrow + 16 * j + lc];
         }
-    } else if (seg >= 3) {
+      }
+    };
+    if (seg <= 1) load_rope(0, 0);
+    else if (seg >= 3) {
       const int bo = (seg - 3) * d + c0;
 #pragma unroll
       for (int j = 0; j < FN; ++j) bs[j] = bias[bo + 16 * j + lc];
     }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
+      const int cb = i & 1;
+      if (seg <= 1 && i + 1 < FM) load_rope(i + 1, cb ^ 1);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
@@ -242,7 +245,7 @@ template <typename T, int DH> struct EpiProj {
             for (int j = 0; j < HF; ++j) {
               const int jj = 16 * j + lc;
               const float a = acc[i][hb * FH + j][q], bb = acc[i][hb * FH + j + HF][q];
-              const float c = cs[i][q][j], sv = sn[i][q][j];
+              const float c = cs[cb][q][j], sv = sn[cb][q][j];
               if (seg == 0) {
                 qr[hrow + jj] = from_f<T>(a * c - bb * sv);
                 qr[hrow + jj + DH / 2] = from_f<T>(bb * c + a * sv);
@@ -757,28 +760,34 @@ template <typename T> struct EpiResidual {
   int M, N;
   const T* __restrict__ x;
   T* __restrict__ y;
-  // the residual rows are loaded before the first store (y may alias x)
+  // the residual rows of 16-row group i + 1 are loaded before group i is stored
+  // (y may alias x)
   template <int FM, int FN>
   DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
     const int lane = threadIdx.x & 63, lc = lane & 15;
-    float xv[FM][4][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
+    float xv[2][4][FN];
+    auto load_x = [&](int i, int buf) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = min(row0 + 16 * i + 4 * (lane >> 4) + q, M - 1);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) xv[i][q][j] = x != nullptr ? to_f(x[(long)m * N + col0 + 16 * j + lc]) : 0.f;
+        for (int j = 0; j < FN; ++j)
+          xv[buf][q][j] = x != nullptr ? to_f(x[(long)m * N + col0 + 16 * j + lc]) : 0.f;
       }
+    };
+    load_x(0, 0);
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i) {
+      const int cb = i & 1;
+      if (i + 1 < FM) load_x(i + 1, cb ^ 1);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
         if (m >= M) continue;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) y[(long)m * N + col0 + 16 * j + lc] = from_f<T>(acc[i][j][q] + xv[i][q][j]);
+        for (int j = 0; j < FN; ++j) y[(long)m * N + col0 + 16 * j + lc] = from_f<T>(acc[i][j][q] + xv[cb][q][j]);
       }
+    }
   }
 };
 

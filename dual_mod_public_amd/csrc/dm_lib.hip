@@ -376,7 +376,7 @@ int dm_linear(int32_t dtype, const void* x, const void* W, const void* r, void* 
     SrcRows<bf16> sa{(const bf16*)x, K, M};
     SrcRows<bf16> sb{(const bf16*)W, K, N};
     EpiResidual<bf16> ep{M, N, (const bf16*)r, (bf16*)y};
-    launch_gemm_auto<bf16, 128, 128, 2, 2, 3, 4>(sa, sb, M, N, K, ep, s);
+    launch_gemm_big<bf16>(sa, sb, M, N, K, ep, s);
   } else if (dtype == DM_F32) {
     SrcRows<float> sa{(const float*)x, K, M};
     SrcRows<float> sb{(const float*)W, K, N};
