@@ -21,7 +21,6 @@ template <typename T> struct BwdWs {
   // one cell
   CellWs fws;                           // forward scratch of the recompute
   CellSave<T> sv;                       // every sweep's state
-  T *dctx, *dvc;                        // [K][N, 4d], [K][N, d]
   float *dKa, *dVa, *dKb, *dVb;         // [B*h, CMAX, dh] grads of the intra rows (ping-pong)
   float *lamdv, *gw, *rowdot;           // [N, d], [N, d], [N, d / DU_EPI_TN]
   float *du_part;                       // [DU_SPLIT, N, d] split-K slices of du
@@ -30,13 +29,13 @@ template <typename T> struct BwdWs {
   int* klim;                            // [T]
   float *dKp, *dVp;                     // [COMM_NSQ, B*h, CMAX, dh]
   // weight grads of the sweeps, one GEMM per layer: the cells' transposed operands
-  // side by side, [4d | d, Rp] with Rp >= sum over cells of K*B*c (rounded to 64)
-  T *dctxT, *uT, *dvcT, *vinT;
+  // stacked row-major, [Rp, 4d | d] with Rp >= sum over cells of K*B*c (rounded to 64);
+  // a cell's sweeps write their dctx / dv_ctx rows in place, u and v_in are added per cell
+  T *dctxL, *uL, *dvcL, *vinL;
   long Rp;
   float* kpart;                         // [KSPLIT_ELEMS(d)] split-K partials
   // layer close
   T* dproj;                             // [B*T, nproj*d]
-  T *tA, *tB;                           // layer-level transposes [max(nproj*d, d), B*T] and [d, B*T]
   float* dxhat;                         // [B*T, d]
   float *dWp, *dWs;                     // packed weight-grad staging [nproj*d, d], [4d, d]
   float* colpart;                       // [max(NCHUNK, B*T / PROJ_ROWS), 3d] column partials
@@ -67,8 +66,6 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.fws = carve_cell(c, cache_T, cv.base ? cv.base + cv.off : nullptr);
   cv.off += align256(w.fws.bytes);
   w.sv = carve_save<T>(c, N, kmax, false, false, cv);
-  w.dctx = cv.take<T>(kmax * N * 4 * d * e);
-  w.dvc = cv.take<T>(kmax * N * d * e);
   w.dKa = cv.take<float>(BH * CMAX * dh * 4);
   w.dVa = cv.take<float>(BH * CMAX * dh * 4);
   w.dKb = cv.take<float>(BH * CMAX * dh * 4);
@@ -83,18 +80,14 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.klim = cv.take<int>(T_ * 4);
   w.dKp = cv.take<float>(COMM_NSQ * BH * CMAX * dh * 4);
   w.dVp = cv.take<float>(COMM_NSQ * BH * CMAX * dh * 4);
-  // + 64: rows of the transposes a power of two apart would all map to the same HBM
-  // channels (the per-cell transposes write 64 rows at a stride of Rp elements)
-  w.Rp = (long)cdiv((long)kmax * B * T_, 64) * 64 + 64;
-  w.dctxT = cv.take<T>(w.Rp * 4 * d * e);
-  w.uT = cv.take<T>(w.Rp * d * e);
-  w.dvcT = cv.take<T>(w.Rp * d * e);
-  w.vinT = cv.take<T>(w.Rp * d * e);
+  w.Rp = (long)cdiv((long)kmax * B * T_, 64) * 64;
+  w.dctxL = cv.take<T>(w.Rp * 4 * d * e);
+  w.uL = cv.take<T>(w.Rp * d * e);
+  w.dvcL = cv.take<T>(w.Rp * d * e);
+  w.vinL = cv.take<T>(w.Rp * d * e);
   w.kpart = cv.take<float>(KSPLIT_ELEMS((long)d) * 4);
   // the attn_norm weight partials [B*T, d] fp32 reuse dproj once it is consumed
   w.dproj = cv.take<T>(std::max(BT * nproj * d * e, BT * d * 4));
-  w.tA = cv.take<T>((BT + 128) * nproj * d * e);
-  w.tB = cv.take<T>((BT + 128) * d * e);
   w.dxhat = cv.take<float>(BT * d * 4);
   w.dWp = cv.take<float>(nproj * d * d * 4);
   w.dWs = cv.take<float>(4 * d * d * 4);
@@ -128,54 +121,40 @@ inline void unpack(const std::vector<UnpackSeg>& segs, int ncols, const float* s
   }
 }
 
-// out [cols, ld_out] (columns col0_out..) = in [rows, cols]^T
+// C [M, N] (+)= A^T . B for row-major A [K, M], B [K, N] (the weight-grad products
+// sum over rows): the operands are read K-major straight from the row-major buffers
+// (bf16 with whole tiles: direct-to-LDS k-loop with transposed-view fragment loads);
+// split-K over enough slices to give every CU a block, the slices stored into `part`
+// and summed into C in a fixed order.
 template <typename T>
-void transpose(const T* in, long ld_in, int rows, int cols, int rows_pad, T* out, long ld_out, long col0_out,
-               hipStream_t s) {
-  dim3 grid(cdiv(cols, 64), cdiv(rows_pad, 64));
-  hipLaunchKernelGGL(k_transpose16<T>, grid, dim3(256), 0, s, in, ld_in, rows, cols, rows_pad, out, ld_out,
-                     col0_out);
-}
-
-// C [M, N] (+)= At [M, Kp] . Bt [N, Kp]^T (both K-contiguous, zero past the valid k):
-// split-K over enough slices to give every CU several blocks, the slices stored
-// into `part` ([KSPLIT_ELEMS] fp32) and summed into C in a fixed order.
-template <typename T>
-void gemm_splitk_f32(const T* At, long lda, const T* Bt, long ldb, int Kp, int M, int N, int accumulate, float* part,
-                     float* C, hipStream_t s) {
-  // bf16 with M, N multiples of 256: 256 x 256 blocks (one per CU), >= 256 blocks;
-  // otherwise 128 x 128 blocks, up to ~4 per CU
-  const bool big = sizeof(T) == 2 && M % 256 == 0 && N % 256 == 0;
-  const long blocks = big ? (long)(M / 256) * (N / 256) : (long)(M / 128) * (N / 128);
+void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N, int K, int accumulate,
+             float* part, hipStream_t s) {
+  const bool dma = sizeof(T) == 2 && K % 64 == 0 && M % 128 == 0 && N % 128 == 0;
+  const bool big = dma && M % 256 == 0 && N % 256 == 0;
+  const long blocks = big ? (long)(M / 256) * (N / 256) : (long)cdiv(M, 128) * cdiv(N, 128);
   const long target = big ? 256 : 1024;
   int S = 1;
-  while (S < 16 && blocks * S * (big ? 1 : 2) < target + (big ? 0 : 1) &&
-         (long)S * 2 * M * N <= KSPLIT_ELEMS((long)N) && (Kp / 64) % (S * 2) == 0)
+  while (K % 64 == 0 && S < 16 && blocks * S * (big ? 1 : 2) < target + (big ? 0 : 1) &&
+         (long)S * 2 * M * N <= KSPLIT_ELEMS((long)N) && (K / 64) % (S * 2) == 0)
     S *= 2;
-  const SrcRows<T> sa{At, lda, M}, sb{Bt, ldb, N};
+  SrcKMajor<T> sa{A, lda, M}, sb{Bm, ldb, N};
+  sa.kmax = K;
+  sb.kmax = K;
   if (S == 1) {
     EpiStoreF32 ep{M, N, accumulate, C};
-    launch_gemm_big<T>(sa, sb, M, N, Kp, ep, s);
+    launch_gemm_kk<T>(sa, sb, M, N, K, ep, s);
     return;
   }
   EpiStoreF32 ep{M, N, 0, part, (long)M * N};
-  if (big) launch_gemm_splitk<T, 256, 256, 2, 2, (sizeof(T) == 2 ? -2 : 4)>(sa, sb, M, N, Kp, S, ep, s);
-  else launch_gemm_splitk<T, 128, 128, 2, 2, sizeof(T) == 2 ? -3 : 4>(sa, sb, M, N, Kp, S, ep, s);
+  if constexpr (sizeof(T) == 2) {
+    if (big) launch_gemm_splitk<T, 256, 256, 2, 2, -2>(sa, sb, M, N, K, S, ep, s);
+    else if (dma) launch_gemm_splitk<T, 128, 128, 2, 2, -3>(sa, sb, M, N, K, S, ep, s);
+    else launch_gemm_splitk<T, 128, 128, 2, 2, 4>(sa, sb, M, N, K, S, ep, s);
+  } else {
+    launch_gemm_splitk<T, 128, 128, 2, 2, 4>(sa, sb, M, N, K, S, ep, s);
+  }
   hipLaunchKernelGGL(k_sum_splits, dim3(cdiv((long)M * N, 256)), dim3(256), 0, s, S, (long)M * N,
                      (const float*)part, C, accumulate);
-}
-
-// C [M, N] (+)= A^T . B for row-major A [K, M], B [K, N] (the weight-grad products
-// sum over rows): both operands are transposed into scratch first so the GEMM runs
-// with K-contiguous operands (16-byte LDS stores).
-template <typename T>
-void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N, int K, int accumulate, T* At,
-             T* Bt, float* part, hipStream_t s) {
-  const int Kp = cdiv(K, 64) * 64;   // zero-padded to whole k-tiles
-  const long ld = Kp + 64;            // off a power of two: see BwdWs::Rp
-  transpose<T>(A, lda, K, M, Kp, At, ld, 0, s);
-  transpose<T>(Bm, ldb, K, N, Kp, Bt, ld, 0, s);
-  gemm_splitk_f32<T>(At, ld, Bt, ld, Kp, M, N, accumulate, part, C, s);
 }
 
 template <typename T, int DH>
@@ -207,7 +186,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
     EpiStoreF32 ep{BT, d, 0, ws.docat};
     launch_gemm_big<T>(SrcRows<T>{dy, d, BT}, SrcRows<T>{(const T*)w->wo_t, d, d}, BT, d, d,
                                                ep, s);
-    gemm_tn<T>(dy, d, ocat, d, gr->wo, d, d, BT, 1, ws.tA, ws.tB, ws.kpart, s);
+    gemm_tn<T>(dy, d, ocat, d, gr->wo, d, d, BT, 1, ws.kpart, s);
   }
 
   const T* qr = (const T*)L->qr;
@@ -243,6 +222,9 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
                         scale, ws.dKp, ws.dVp};
       hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(COMM_NSQ, BH), dim3(256), lds_attn, s, ka);
     }
+    // this cell's rows of the stacked weight-grad operands
+    T* dctx = ws.dctxL + coff * 4 * d;
+    T* dvc = ws.dvcL + coff * d;
     const float* dKn = ws.dKp;
     const float* dVn = ws.dVp;
     const long dn_stride = (long)CMAX * DH;
@@ -250,15 +232,15 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
       // refine VJP of sweep sw (the last sweep's rows: the sum of the key-side splits)
       RefineBwdArgs<T> ra{g, N, c->ctx_mod, dKn, dVn, dn_stride, 0, (long)BH * CMAX * DH,
                           sv.save1 + sw * NS * 4 * d, mult ? sv.save2 + sw * NS * d : nullptr, L->glogx, kraw, vraw,
-                          cos, sin, ws.dctx + sw * NS * 4 * d, ws.dvc + sw * NS * d, ws.dglogx, ws.dkraw, ws.dvraw};
+                          cos, sin, dctx + sw * NS * 4 * d, dvc + sw * NS * d, ws.dglogx, ws.dkraw, ws.dvraw};
       const dim3 rgrid(cdiv((long)N * d / 2, 256));
       if (sw == K - 1) hipLaunchKernelGGL((k_refine_bwd<T, DH, COMM_NSQ>), rgrid, dim3(256), 0, s, ra);
       else hipLaunchKernelGGL((k_refine_bwd<T, DH, 1>), rgrid, dim3(256), 0, s, ra);
       // dv_in = dv_ctx . W_vctx (mult family)
       if (mult) {
         EpiVinBwd<T> ev{g, N, c->ctx_mod, c->mult_res_lambda, sv.save1 + sw * NS * 4 * d, L->sig,
-                        ws.dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
-        launch_gemm<T, 64, 32, 4, 1, 8>(SrcRows<T>{ws.dvc + sw * NS * d, d, N},
+                        dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
+        launch_gemm<T, 64, 32, 4, 1, 8>(SrcRows<T>{dvc + sw * NS * d, d, N},
                                         SrcRows<T>{(const T*)w->w_vctx_t, d, d}, N, d, d, ev, s);
       }
       // du = dctx . W_sweep (+ lam dv_in): split-K slices, then the RMS-VJP inputs
@@ -266,7 +248,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
         const int S = DU_SPLIT;
         EpiStoreF32 ep{N, d, 0, ws.du_part, (long)N * d};
         launch_gemm_splitk<T, 64, 64, 4, 1, sizeof(T) == 2 ? -3 : 4>(
-            SrcRows<T>{ws.dctx + sw * NS * 4 * d, 4 * d, N}, SrcRows<T>{(const T*)w->w_sweep_t, 4 * d, d}, N, d,
+            SrcRows<T>{dctx + sw * NS * 4 * d, 4 * d, N}, SrcRows<T>{(const T*)w->w_sweep_t, 4 * d, d}, N, d,
             4 * d, S, ep, s);
         hipLaunchKernelGGL((k_du_epi<T, DU_SPLIT>), dim3(cdiv(N, 16), d / DU_EPI_TN), dim3(256), 0, s, N, d, h,
                            inv_d,
@@ -291,28 +273,32 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
         dKn = dKo; dVn = dVo;
       }
     }
-    // operands of the sweep weight grads (dW_sweep = dctx^T u, dW_vctx = dv_ctx^T v_in):
-    // this cell's K*N rows become columns [coff, coff + K*N) of the layer's transposes;
-    // the zero fill up to the next multiple of 64 is overwritten by the next cell
+    // the other operands of the sweep weight grads (dW_sweep = dctx^T u, dW_vctx =
+    // dv_ctx^T v_in): this cell's K*N rows of u = RMSNorm(o) and of v_in
     {
       const int rows = K * N;
-      const long end = coff + rows;
-      const int pad = (int)(cdiv(end, 64) * 64 - coff);
-      transpose<T>(ws.dctx, 4 * d, rows, 4 * d, pad, ws.dctxT, ws.Rp, coff, s);
-      hipLaunchKernelGGL(k_transpose_rms16<T>, dim3(cdiv(d, 64), cdiv(pad, 64)), dim3(256), 0, s, sv.o, (long)d,
-                         rows, d, pad, (const float*)sv.ssq, h, (const T*)w->norm_ctx_w, inv_d, c->rms_eps, ws.uT,
-                         ws.Rp, coff);
+      hipLaunchKernelGGL(k_rms_rows<T>, dim3(cdiv(rows, 4)), dim3(256), 0, s, (const T*)sv.o, rows, d,
+                         (const float*)sv.ssq, h, (const T*)w->norm_ctx_w, inv_d, c->rms_eps, ws.uL + coff * d);
       if (mult) {
-        transpose<T>(ws.dvc, d, rows, d, pad, ws.dvcT, ws.Rp, coff, s);
-        transpose<T>(sv.vin, d, rows, d, pad, ws.vinT, ws.Rp, coff, s);
+        const long n16 = (long)rows * d * (long)sizeof(T) / 16;
+        hipLaunchKernelGGL(k_copy16, dim3(std::min<long>(cdiv(n16, 256), 2048)), dim3(256), 0, s,
+                           reinterpret_cast<const uint4*>(sv.vin), n16, reinterpret_cast<uint4*>(ws.vinL + coff * d));
       }
-      coff = end;
+      coff += rows;
     }
   }
-  {   // the layer's sweep weight grads, one GEMM each over all cells' rows
+  {   // the layer's sweep weight grads, one GEMM each over all cells' stacked rows
+    // (zero rows up to a whole k-tile)
     const int Kp = (int)(cdiv(coff, 64) * 64);
-    gemm_splitk_f32<T>(ws.dctxT, ws.Rp, ws.uT, ws.Rp, Kp, 4 * d, d, 1, ws.kpart, ws.dWs, s);
-    if (mult) gemm_splitk_f32<T>(ws.dvcT, ws.Rp, ws.vinT, ws.Rp, Kp, d, d, 1, ws.kpart, gr->w_vctx, s);
+    if (Kp > coff) {
+      const size_t tail = (size_t)(Kp - coff) * sizeof(T) / 4;
+      fill0(reinterpret_cast<float*>(ws.dctxL + coff * 4 * d), tail * 4 * d, s);
+      fill0(reinterpret_cast<float*>(ws.uL + coff * d), tail * d, s);
+      fill0(reinterpret_cast<float*>(ws.dvcL + coff * d), tail * d, s);
+      fill0(reinterpret_cast<float*>(ws.vinL + coff * d), tail * d, s);
+    }
+    gemm_tn<T>(ws.dctxL, 4 * d, ws.uL, d, ws.dWs, 4 * d, d, Kp, 1, ws.kpart, s);
+    if (mult) gemm_tn<T>(ws.dvcL, d, ws.vinL, d, gr->w_vctx, d, d, Kp, 1, ws.kpart, s);
   }
 
   // committed-prefix VJP, query side: every row with a committed prefix, into dq
@@ -333,7 +319,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
                      (const float*)ws.colpart, gr->b_gk, gr->b_gv, mult ? gr->b_vgate : nullptr, d);
   const T* xhat = norm ? (const T*)L->xhat : x;
   // dW_proj = d_proj^T . xhat (packed rows), dxhat = d_proj . W_proj
-  gemm_tn<T>(ws.dproj, (long)nproj * d, xhat, d, ws.dWp, nproj * d, d, BT, 0, ws.tA, ws.tB, ws.kpart, s);
+  gemm_tn<T>(ws.dproj, (long)nproj * d, xhat, d, ws.dWp, nproj * d, d, BT, 0, ws.kpart, s);
   {
     EpiStoreF32 ep{BT, d, 0, ws.dxhat};
     launch_gemm_big<T>(SrcRows<T>{ws.dproj, (long)nproj * d, BT},

@@ -105,6 +105,8 @@ template <typename T> struct SrcKMajor {
   DM_DEV uint4 load(int r, int k) const {   // VEC consecutive rows r.. at column k
     return (r < rows && k < kmax) ? *reinterpret_cast<const uint4*>(p + (long)k * ld + r) : zero_u4();
   }
+  // direct-to-LDS path (whole tiles in range, K a multiple of the k-tile): row r of k-row k
+  DM_DEV const T* ptr_k(int k, int r) const { return p + (long)k * ld + r; }
   DM_DEV uint4 xform(uint4 v, int, int, const float*, int) const { return v; }
 };
 
@@ -390,6 +392,100 @@ DM_DEV void gemm_mainloop_dma(const SA& sa, const SB& sb, int K, int m0, int n0,
   __syncthreads();
 }
 
+// The direct-to-LDS k-loop for K-major operands (bf16, both operands K-major: the
+// weight-grad products C = A^T B summed over rows). A stage holds 64 k-rows of the
+// block's BM (then BN) columns, BM * 2 bytes per k-row, its 16-byte chunk c stored
+// at chunk c ^ (2 (k & 3)); one global_load_lds_dwordx4 per wave fills 1 KB (1024 /
+// (BM * 2) k-rows). MFMA fragments (8 consecutive k of one column per lane) come
+// from two ds_read_b64_tr_b16 each: in a 16-lane group, lane s names the 8 bytes
+// at k-row 8g + s / 4 (+ 4), columns 4 (s % 4) .. + 3 of the fragment's 16 columns,
+// and receives that 4 x 16 block's column s; the swizzle puts the four k-rows'
+// chunks in different banks.
+template <int ROW> DM_DEV bf16x8 frag_kmajor(const char* stage, int k0, int c0) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, s = lane & 15;
+  const int kr = k0 + 8 * g + (s >> 2);
+  const int col = c0 + 4 * (s & 3);
+  const char* p = stage + kr * ROW + ((((col >> 3) ^ (2 * (kr & 3))) << 4) | ((col & 7) << 1));
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * ROW));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int S, class SA, class SB>
+DM_DEV void gemm_mainloop_dma_kk(const SA& sa, const SB& sb, int K, int m0, int n0, char* smem,
+                                 floatx4 (&acc)[WaveTile<BM, BN, WM, WN>::FM][WaveTile<BM, BN, WM, WN>::FN],
+                                 int kbase) {
+  static_assert(sizeof(T) == 2 && SA::KMAJOR && SB::KMAJOR, "K-major direct-to-LDS path: bf16, both K-major");
+  static_assert(S >= 2 && (BM == 64 || BM == 128 || BM == 256) && (BN == 64 || BN == 128 || BN == 256),
+                "stages / tile columns");
+  using MF = Mfma<T>;
+  using WT = WaveTile<BM, BN, WM, WN>;
+  constexpr int FM = WT::FM, FN = WT::FN, TM = WT::TM, TN = WT::TN;
+  constexpr int ROWA = BM * 2, ROWB = BN * 2;              // bytes per k-row
+  constexpr int STAGE = 64 * (ROWA + ROWB);
+  constexpr int RPA = 1024 / ROWA, RPB = 1024 / ROWB;      // k-rows per wave load instruction
+  constexpr int LA = 64 / RPA / 4, LB = 64 / RPB / 4, L = LA + LB;
+  constexpr int CPA = ROWA / 16, CPB = ROWB / 16;          // 16-byte chunks per k-row
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  auto issue = [&](int kt, int st) {
+    char* base = smem + st * STAGE;
+    const int k = kbase + kt * 64;
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+      const int r0 = (wave * LA + i) * RPA, r = r0 + lane / CPA;
+      const int c = (lane % CPA) ^ (2 * (r & 3));
+      __builtin_amdgcn_global_load_lds((const void*)sa.ptr_k(k + r, m0 + 8 * c), (lds_void_t*)(base + r0 * ROWA),
+                                       16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+      const int r0 = (wave * LB + i) * RPB, r = r0 + lane / CPB;
+      const int c = (lane % CPB) ^ (2 * (r & 3));
+      __builtin_amdgcn_global_load_lds((const void*)sb.ptr_k(k + r, n0 + 8 * c),
+                                       (lds_void_t*)(base + 64 * ROWA + r0 * ROWB), 16, 0, 0);
+    }
+  };
+  auto compute = [&](const char* As) {
+    const char* Bs = As + 64 * ROWA;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      typename MF::frag af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[i] = frag_kmajor<ROWA>(As, 32 * kk, wm * TM + 16 * i);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bfr[j] = frag_kmajor<ROWB>(Bs, 32 * kk, wn * TN + 16 * j);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = MF::mma(af[i], bfr[j], acc[i][j]);
+    }
+  };
+
+  const int nk = K / 64;
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < nk) issue(st, st);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int after = min(S - 2, nk - 1 - kt);
+    if constexpr (S >= 4) {
+      if (after >= 2) wait_vm_lgkm0<2 * L>();
+      else if (after == 1) wait_vm_lgkm0<L>();
+      else wait_vm_lgkm0<0>();
+    } else if constexpr (S == 3) {
+      if (after >= 1) wait_vm_lgkm0<L>();
+      else wait_vm_lgkm0<0>();
+    } else {
+      wait_vm_lgkm0<0>();
+    }
+    __builtin_amdgcn_s_barrier();
+    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+    compute(smem + (kt % S) * STAGE);
+  }
+  __syncthreads();
+}
+
 // Generic kernel: zero accumulators, k-loop, epilogue on the wave's registers.
 // epi(acc, row0, col0) with row0/col0 the global origin of the wave tile.
 // Split-K launches (gridDim.z > 1) reduce k in [z*K, (z+1)*K) in block z; their
@@ -398,6 +494,7 @@ template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB>
 DM_DEV void gemm_kloop(const SA& sa, const SB& sb, int K, int m0, int n0, char* smem,
                        floatx4 (&acc)[WaveTile<BM, BN, WM, WN>::FM][WaveTile<BM, BN, WM, WN>::FN], int kbase) {
   if constexpr (D > 0) gemm_mainloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, kbase);
+  else if constexpr (SA::KMAJOR && SB::KMAJOR) gemm_mainloop_dma_kk<T, BM, BN, WM, WN, -D>(sa, sb, K, m0, n0, smem, acc, kbase);
   else gemm_mainloop_dma<T, BM, BN, WM, WN, -D>(sa, sb, K, m0, n0, smem, acc, kbase);
 }
 

@@ -135,6 +135,27 @@ void launch_gemm_big(const SA& sa, const SB& sb, int M, int N, int K, const EPI&
   launch_gemm_auto<T, 128, 128, 2, 2, 3, 4>(sa, sb, M, N, K, epi, s, prof_cls);
 }
 
+// K-major operands (C = A^T B summed over rows; element (r, k) at p[k * ld + r]):
+// bf16 whole tiles with K a multiple of 64 take the direct-to-LDS path (256 x 256
+// blocks where M and N allow), otherwise the register ring.
+template <typename T, class EPI>
+void launch_gemm_kk(const SrcKMajor<T>& sa, const SrcKMajor<T>& sb, int M, int N, int K, const EPI& epi,
+                    hipStream_t s, int prof_cls = PROF_NONE) {
+  if constexpr (sizeof(T) == 2) {
+    if (K % 64 == 0 && sa.kmax >= K && sb.kmax >= K) {
+      if (M % 256 == 0 && N % 256 == 0) {
+        launch_gemm<T, 256, 256, 2, 2, -2>(sa, sb, M, N, K, epi, s, prof_cls);
+        return;
+      }
+      if (M % 128 == 0 && N % 128 == 0) {
+        launch_gemm<T, 128, 128, 2, 2, -3>(sa, sb, M, N, K, epi, s, prof_cls);
+        return;
+      }
+    }
+  }
+  launch_gemm<T, 128, 128, 2, 2, 4>(sa, sb, M, N, K, epi, s, prof_cls);
+}
+
 // Split-K: S slices of K/S each (K/S a multiple of the k-tile), slice z in grid.z.
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
 void launch_gemm_splitk(const SA& sa, const SB& sb, int M, int N, int K, int S, const EPI& epi, hipStream_t s,

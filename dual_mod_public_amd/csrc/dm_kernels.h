@@ -62,42 +62,6 @@ static __global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ 
   }
 }
 
-// out[c, col0_out + r] = in[r, c] for a [rows, cols] row-major matrix (ld_in) into a
-// [cols, ld_out] matrix, with output columns [rows, rows_pad) zero-filled: 64x64 tiles
-// through LDS, 16-byte loads and stores. cols and ld_out must be multiples of
-// 16 / sizeof(T); an unaligned col0_out (or rows_pad) falls back to element stores.
-template <typename T>
-static __global__ __launch_bounds__(256) void k_transpose16(const T* __restrict__ in, long ld_in, int rows, int cols,
-                                                            int rows_pad, T* __restrict__ out, long ld_out,
-                                                            long col0_out) {
-  constexpr int V = 16 / (int)sizeof(T);
-  __shared__ float tile[64][64 + 1];   // 4-byte cells, odd row stride: conflict-free both ways
-  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
-  for (int v = threadIdx.x; v < 64 * 64 / V; v += 256) {
-    const int r = v / (64 / V), cc = (v % (64 / V)) * V;
-    if (r0 + r < rows && c0 + cc < cols) {
-      float f[V];
-      unpack16<T>(*reinterpret_cast<const uint4*>(in + (long)(r0 + r) * ld_in + c0 + cc), f);
-#pragma unroll
-      for (int j = 0; j < V; ++j) tile[r][cc + j] = f[j];
-    }
-  }
-  __syncthreads();
-  for (int v = threadIdx.x; v < 64 * 64 / V; v += 256) {
-    const int cc = v / (64 / V), r = (v % (64 / V)) * V;
-    if (r0 + r < rows_pad && c0 + cc < cols) {
-      float f[V];
-#pragma unroll
-      for (int j = 0; j < V; ++j) f[j] = (r0 + r + j < rows) ? tile[r + j][cc] : 0.f;
-      T* dst = out + (long)(c0 + cc) * ld_out + col0_out + r0 + r;
-      if (col0_out % V == 0 && r0 + r + V <= rows_pad) {
-        *reinterpret_cast<uint4*>(dst) = pack16<T>(f);
-      } else {
-        for (int j = 0; j < V && r0 + r + j < rows_pad; ++j) dst[j] = from_f<T>(f[j]);
-      }
-    }
-  }
-}
 
 // W[r, k] *= w[k] (in place)
 template <typename T>
@@ -107,53 +71,34 @@ static __global__ __launch_bounds__(256) void k_scale_cols(T* __restrict__ W, co
   if (i < (long)rows * cols) W[i] = from_f<T>(to_f(W[i]) * to_f(w[i % cols]));
 }
 
-// out[k, col0_out + r] = in[r, k] * rs[r] * w[k] with rs[r] = rsqrt(sum_p ssq[r, p] * inv_d + eps):
-// the transposed RMSNorm output u^T of the stacked sweeps (the weight-grad GEMM operand),
-// 64x64 tiles; output columns [rows, rows_pad) zero-filled (stores as in k_transpose16).
+// u rows of the sweep weight grads: out[r] = o[r] * rsqrt(sum_p ssq[r, p] * inv_d + eps) * w
+// (the RMSNorm the sweep GEMM applied), one wave per row, 16-byte vectors.
 template <typename T>
-static __global__ __launch_bounds__(256) void k_transpose_rms16(const T* __restrict__ in, long ld_in, int rows,
-                                                                int cols, int rows_pad, const float* __restrict__ ssq,
-                                                                int nparts, const T* __restrict__ w, float inv_d,
-                                                                float eps, T* __restrict__ out, long ld_out,
-                                                                long col0_out) {
+static __global__ __launch_bounds__(256) void k_rms_rows(const T* __restrict__ o, int rows, int cols,
+                                                         const float* __restrict__ ssq, int nparts,
+                                                         const T* __restrict__ w, float inv_d, float eps,
+                                                         T* __restrict__ out) {
   constexpr int V = 16 / (int)sizeof(T);
-  __shared__ float tile[64][64 + 1];
-  __shared__ float rs[64];
-  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
-  {   // 4 adjacent threads per row
-    const int r = min(r0 + (int)threadIdx.x / 4, rows - 1), part = threadIdx.x % 4;
-    float s = sum_strided<MAX_HEADS / 4>(ssq + (long)r * nparts, part, nparts, 4);
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    if (part == 0) rs[threadIdx.x / 4] = rsqrtf(s * inv_d + eps);
-  }
-  __syncthreads();
-  for (int v = threadIdx.x; v < 64 * 64 / V; v += 256) {
-    const int r = v / (64 / V), cc = (v % (64 / V)) * V;
-    if (r0 + r < rows && c0 + cc < cols) {
-      float f[V], wf[V];
-      unpack16<T>(*reinterpret_cast<const uint4*>(in + (long)(r0 + r) * ld_in + c0 + cc), f);
-      unpack16<T>(*reinterpret_cast<const uint4*>(w + c0 + cc), wf);
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float rs = rsqrtf(wave_sum(lane < nparts ? ssq[(long)r * nparts + lane] : 0.f) * inv_d + eps);
+  for (int c = lane * V; c < cols; c += 64 * V) {
+    float f[V], wf[V];
+    unpack16<T>(*reinterpret_cast<const uint4*>(o + (long)r * cols + c), f);
+    unpack16<T>(*reinterpret_cast<const uint4*>(w + c), wf);
 #pragma unroll
-      for (int j = 0; j < V; ++j) tile[r][cc + j] = f[j] * rs[r] * wf[j];
-    }
-  }
-  __syncthreads();
-  for (int v = threadIdx.x; v < 64 * 64 / V; v += 256) {
-    const int cc = v / (64 / V), r = (v % (64 / V)) * V;
-    if (r0 + r < rows_pad && c0 + cc < cols) {
-      float f[V];
-#pragma unroll
-      for (int j = 0; j < V; ++j) f[j] = (r0 + r + j < rows) ? tile[r + j][cc] : 0.f;
-      T* dst = out + (long)(c0 + cc) * ld_out + col0_out + r0 + r;
-      if (col0_out % V == 0 && r0 + r + V <= rows_pad) {
-        *reinterpret_cast<uint4*>(dst) = pack16<T>(f);
-      } else {
-        for (int j = 0; j < V && r0 + r + j < rows_pad; ++j) dst[j] = from_f<T>(f[j]);
-      }
-    }
+    for (int e = 0; e < V; ++e) f[e] *= rs * wf[e];
+    *reinterpret_cast<uint4*>(out + (long)r * cols + c) = pack16<T>(f);
   }
 }
+
+// dst[i] = src[i] for n 16-byte vectors
+static __global__ __launch_bounds__(256) void k_copy16(const uint4* __restrict__ src, long n, uint4* __restrict__ dst) {
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) dst[i] = src[i];
+}
+
+
 
 // ---------------------------------------------------------------------------
 // row RMSNorm (attn_norm, models/dualmod/attention.py:74-83): one wave per row

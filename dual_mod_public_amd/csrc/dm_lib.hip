@@ -405,7 +405,7 @@ void gemm_any(int ta, int tb, const void* A, const void* Bm, float* C, int M, in
   else if (ta && !tb)
     launch_gemm<T, 128, 128, 2, 2, 4>(SrcKMajor<T>{a, M, M}, SrcRows<T>{b, K, N}, M, N, K, ep, s);
   else
-    launch_gemm<T, 128, 128, 2, 2, 4>(SrcKMajor<T>{a, M, M}, SrcKMajor<T>{b, N, N}, M, N, K, ep, s);
+    launch_gemm_kk<T>(SrcKMajor<T>{a, M, M}, SrcKMajor<T>{b, N, N}, M, N, K, ep, s);
 }
 }  // namespace
 

@@ -29,7 +29,7 @@ def _gpu():
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (256, 384, 320), (128, 256, 1024)])
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (256, 384, 320), (128, 256, 1024), (512, 256, 192)])
 def test_gemm_matches_fp64(dtype, ta, tb, M, N, K):
     """dm_gemm: C = op(A) op(B)^T (+C) for the four operand layouts the backward uses."""
     say(f"gemm dtype={dtype} ta={ta} tb={tb} M={M} N={N} K={K}")
