@@ -196,6 +196,9 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   const size_t slot = (size_t)BH * CMAX * DH;
 
   const size_t lds_attn = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
+  // the stacked v_in of every cell: the tape's (saved by the forward in this order)
+  // or the workspace's (written by the recompute)
+  T* vinS = tape != nullptr ? (T*)(const_cast<char*>(tape) + tape_off[n_cells]) : ws.vinL;
   const int t_end = sched[3 * (n_cells - 1)] + sched[3 * (n_cells - 1) + 1];   // rows of the schedule
   long coff = 0;   // columns of the weight-grad operands filled so far
   for (int ci = n_cells - 1; ci >= 0; --ci) {
@@ -209,10 +212,12 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
     if (tape != nullptr) {
       Carver cv(const_cast<char*>(tape) + tape_off[ci]);
       sv = carve_save<T>(c, NS, K, true, pos0 > 0, cv);
+      if (mult) sv.vin = vinS + coff * d;
       Mx = sv.Mx;
     } else {
+      if (mult) sv.vin = vinS + coff * d;   // the recompute writes v_in into the stacked rows
       run_cell<T, DH>(c, w, L, cos, sin, pos0, cc, K, pos0, T_, (T*)Kc, (T*)Vc, cache_T, nullptr, nullptr, ws.fws,
-                      &ws.sv, s);
+                      &sv, s);
       Mx = pos0 > 0 ? ws.fws.M : nullptr;
     }
     // grads of the cell's final rows from the committed-prefix attention of every
@@ -273,17 +278,12 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
         dKn = dKo; dVn = dVo;
       }
     }
-    // the other operands of the sweep weight grads (dW_sweep = dctx^T u, dW_vctx =
-    // dv_ctx^T v_in): this cell's K*N rows of u = RMSNorm(o) and of v_in
+    // the other operand of dW_sweep = dctx^T u: this cell's K*N rows of u = RMSNorm(o)
+    // (dW_vctx = dv_ctx^T v_in reads the stacked v_in as it is)
     {
       const int rows = K * N;
       hipLaunchKernelGGL(k_rms_rows<T>, dim3(cdiv(rows, 4)), dim3(256), 0, s, (const T*)sv.o, rows, d,
                          (const float*)sv.ssq, h, (const T*)w->norm_ctx_w, inv_d, c->rms_eps, ws.uL + coff * d);
-      if (mult) {
-        const long n16 = (long)rows * d * (long)sizeof(T) / 16;
-        hipLaunchKernelGGL(k_copy16, dim3(std::min<long>(cdiv(n16, 256), 2048)), dim3(256), 0, s,
-                           reinterpret_cast<const uint4*>(sv.vin), n16, reinterpret_cast<uint4*>(ws.vinL + coff * d));
-      }
       coff += rows;
     }
   }
@@ -295,10 +295,10 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
       fill0(reinterpret_cast<float*>(ws.dctxL + coff * 4 * d), tail * 4 * d, s);
       fill0(reinterpret_cast<float*>(ws.uL + coff * d), tail * d, s);
       fill0(reinterpret_cast<float*>(ws.dvcL + coff * d), tail * d, s);
-      fill0(reinterpret_cast<float*>(ws.vinL + coff * d), tail * d, s);
+      if (mult) fill0(reinterpret_cast<float*>(vinS + coff * d), tail * d, s);
     }
     gemm_tn<T>(ws.dctxL, 4 * d, ws.uL, d, ws.dWs, 4 * d, d, Kp, 1, ws.kpart, s);
-    if (mult) gemm_tn<T>(ws.dvcL, d, ws.vinL, d, gr->w_vctx, d, d, Kp, 1, ws.kpart, s);
+    if (mult) gemm_tn<T>(ws.dvcL, d, vinS, d, gr->w_vctx, d, d, Kp, 1, ws.kpart, s);
   }
 
   // committed-prefix VJP, query side: every row with a committed prefix, into dq
@@ -381,7 +381,8 @@ int layer_bwd_dispatch(const dm_config* c, const dm_packed* w, const void* x, co
   std::vector<size_t> off;
   if (tape != nullptr) {
     off = tape_offsets<T>(c, sched, n_cells);
-    DM_REQUIRE(tape_bytes >= off[n_cells], DM_ERR_WORKSPACE, "tape %zu < %zu bytes", tape_bytes, off[n_cells]);
+    DM_REQUIRE(tape_bytes >= off[n_cells + 1], DM_ERR_WORKSPACE, "tape %zu < %zu bytes", tape_bytes,
+               off[n_cells + 1]);
     DM_REQUIRE(aligned16(tape), DM_ERR_INVALID, "tape must be 16-byte aligned");
   }
   const BwdWs<T> ws = carve_bwd<T>(c, L->T, cache_T, kmax, workspace);

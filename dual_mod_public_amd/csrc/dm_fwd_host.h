@@ -48,7 +48,8 @@ template <typename T> struct CellSave {
   float* stat_z;     // [K][BH, CMAX]  final row sum of sweep s
   T* save1;          // [K][N, 4d]     raw sweep GEMM 1 outputs (rounded to the storage dtype,
   T* save2;          // [K][N, d]      raw v_ctx (mult family)    as the reference's GEMM outputs)
-  T* vin;            // [K][N, d]      v_in (mult family)
+  T* vin;            // [K][N, d]      v_in (mult family): rows of the layer's stacked v_in
+                     //   (the backward's cell order), assigned by the caller
   T* Kin; T* Vin;    // [K+1][BH, CMAX, DH]  intra rows read by sweep s (slot 0 unused: raw rows);
                      //   with last_to_cache only [K] slots: the last sweep writes the cache rows
   float* Mx;         // [BH, CMAX] committed row max (tape cells with pos0 > 0), else nullptr
@@ -68,7 +69,7 @@ CellSave<T> carve_save(const dm_config* c, size_t N, int K, bool tape, bool has_
   w.stat_z = cv.take<float>(k * BH * CMAX * 4);
   w.save1 = cv.take<T>(k * N * 4 * d * e);
   w.save2 = mult ? cv.take<T>(k * N * d * e) : nullptr;
-  w.vin = mult ? cv.take<T>(k * N * d * e) : nullptr;
+  w.vin = nullptr;
   const size_t slots = tape ? k : k + 1;
   w.Kin = cv.take<T>(slots * BH * CMAX * dh * e);
   w.Vin = cv.take<T>(slots * BH * CMAX * dh * e);
@@ -77,15 +78,28 @@ CellSave<T> carve_save(const dm_config* c, size_t N, int K, bool tape, bool has_
   return w;
 }
 
-// Byte offset of every cell's saved state in a layer tape (n_cells + 1 entries).
+// Row of cell i's first v_in row in the layer's stacked v_in: the backward takes the
+// cells last first, so the rows of cells i+1.. precede cell i's.
+inline long vin_row(const dm_config* c, const int32_t* sched, int n_cells, int i) {
+  long r = 0;
+  for (int j = i + 1; j < n_cells; ++j) r += (long)sched[3 * j + 2] * c->B * sched[3 * j + 1];
+  return r;
+}
+
+// Layout of a layer tape (n_cells + 2 entries): off[i] = cell i's saved state,
+// off[n_cells] = the stacked v_in of every cell (mult family; rows in the backward's
+// cell order, rounded up to a whole 64-row k-tile), off[n_cells + 1] = total bytes.
 template <typename T>
 std::vector<size_t> tape_offsets(const dm_config* c, const int32_t* sched, int n_cells) {
-  std::vector<size_t> off(n_cells + 1, 0);
+  std::vector<size_t> off(n_cells + 2, 0);
   for (int i = 0; i < n_cells; ++i) {
     Carver cv(nullptr);
     carve_save<T>(c, (size_t)c->B * sched[3 * i + 1], sched[3 * i + 2], true, sched[3 * i] > 0, cv);
     off[i + 1] = off[i] + cv.off;
   }
+  const long rows = vin_row(c, sched, n_cells, -1);
+  const size_t vin_bytes = c->ctx_mod != DM_CTX_LINEAR ? (size_t)((rows + 63) / 64 * 64) * c->d * sizeof(T) : 0;
+  off[n_cells + 1] = off[n_cells] + align256(vin_bytes);
   return off;
 }
 

@@ -93,11 +93,6 @@ static __global__ __launch_bounds__(256) void k_rms_rows(const T* __restrict__ o
   }
 }
 
-// dst[i] = src[i] for n 16-byte vectors
-static __global__ __launch_bounds__(256) void k_copy16(const uint4* __restrict__ src, long n, uint4* __restrict__ dst) {
-  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) dst[i] = src[i];
-}
-
 
 
 // ---------------------------------------------------------------------------

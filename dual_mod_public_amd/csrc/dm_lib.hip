@@ -203,8 +203,8 @@ int dm_check_schedule(const int32_t* sched, int32_t n_cells, int32_t T) {
 
 size_t dm_layer_tape_bytes(const dm_config* c, const int32_t* sched, int32_t n_cells) {
   if (check_cfg(c) != DM_OK || sched == nullptr || n_cells <= 0) return 0;
-  return c->dtype == DM_BF16 ? tape_offsets<bf16>(c, sched, n_cells)[n_cells]
-                             : tape_offsets<float>(c, sched, n_cells)[n_cells];
+  return c->dtype == DM_BF16 ? tape_offsets<bf16>(c, sched, n_cells)[n_cells + 1]
+                             : tape_offsets<float>(c, sched, n_cells)[n_cells + 1];
 }
 
 int dm_layer_fwd(const dm_config* c, const dm_packed* w, const void* x, void* y, const float* cos,
@@ -243,7 +243,10 @@ int dm_layer_fwd(const dm_config* c, const dm_packed* w, const void* x, void* y,
       for (int i = 0; i < n_cells; ++i) {
         const int pos0 = sched[3 * i], cc = sched[3 * i + 1], K = sched[3 * i + 2];
         Carver cv(static_cast<char*>(tape) + off[i]);
-        const CellSave<T> sv = carve_save<T>(c, (size_t)c->B * cc, K, true, pos0 > 0, cv);
+        CellSave<T> sv = carve_save<T>(c, (size_t)c->B * cc, K, true, pos0 > 0, cv);
+        if (c->ctx_mod != DM_CTX_LINEAR)
+          sv.vin = reinterpret_cast<T*>(static_cast<char*>(tape) + off[n_cells]) +
+                   vin_row(c, sched, n_cells, i) * c->d;
         CellWs cws = ws;
         if (sv.Mx) cws.M = sv.Mx;   // the committed row max is part of the saved state
         run_cell_dispatch<T>(c, w, L, cos, sin, pos0, cc, K, pos0, L->T, K_cache, V_cache, cache_T, ocat,
