@@ -208,6 +208,14 @@ template <typename T> struct EpiVinBwd {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
+      for (int q = 0; q < 4; ++q) {   // every gathered value before the first store
+        settle(vm[i][q]);
+        settle(sg[i][q]);
+        settle(ds[i][q]);
+      }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
         if (m >= M) continue;

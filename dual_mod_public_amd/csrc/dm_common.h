@@ -94,6 +94,15 @@ DM_DEV void store_vec(T* p, const float* in) {
   for (int i = 0; i < N / V; ++i) *reinterpret_cast<uint4*>(p + i * V) = pack16<T>(in + i * V);
 }
 
+// Make every value of an array available here (one wait for all of them) before the
+// code that follows: on gfx9 the memory counter also counts stores, so a wait for a
+// loaded value issued after some stores also waits for those stores; consuming all
+// gathered values before the first store keeps store latency out of the chain.
+template <int N> DM_DEV void settle(const float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" ::"v"(v[i]));
+}
+
 // v if ok else 0, without a branch: the mask is made opaque to the optimizer so the
 // (unconditional) load that produced v is not sunk into a divergent branch (the
 // compiler then has to drain all outstanding loads at the join).

@@ -584,6 +584,8 @@ template <typename T, int DH> struct EpiSweep1 {
 
   template <int FM, int FN>
   DM_DEV void apply(const floatx4 (&acc)[FM][FN], int row0, int col0, const float* rs, const PreData& pr) const {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) settle(pr.f[q]);   // every gathered value before the first store
     static_assert(FM == 1 && FN == 4, "sweep GEMM 1 wave tile is 16 x 64");
     const int lane = threadIdx.x & 63, lc = lane & 15;
     const int d = g.d, h = g.h;
@@ -674,6 +676,14 @@ template <typename T, int DH> struct EpiSweep2 {
           gu[i][q][j] = gvu[(long)m * d + col];
           vr[i][q][j] = to_f(vraw[(((long)b * g.h + hd) * g.Tbuf + t) * DH + e]);
         }
+      }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {   // every gathered value before the first store
+        settle(gx[i][q]);
+        settle(gu[i][q]);
+        settle(vr[i][q]);
       }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
