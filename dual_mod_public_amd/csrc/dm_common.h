@@ -102,6 +102,55 @@ template <int N> DM_DEV void settle(const float (&v)[N]) {
 #pragma unroll
   for (int i = 0; i < N; ++i) asm volatile("" ::"v"(v[i]));
 }
+template <typename V> DM_DEV void settle_raw(const V& v) {
+  static_assert(sizeof(V) % 4 == 0, "whole dwords");
+  struct W { uint32_t w[sizeof(V) / 4]; };
+  const W x = __builtin_bit_cast(W, v);
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(V) / 4); ++i) asm volatile("" ::"v"(x.w[i]));
+}
+
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// A load through a pointer into global memory, typed as such: a generic (flat) load
+// would also count against the LDS counter that later LDS waits drain. V must be a
+// native vector or scalar type (HIP's struct vectors copy through a generic
+// reference, which loses the address space).
+template <typename V, typename P> DM_DEV V ld_global(const P* p) {
+  return *(const __attribute__((address_space(1))) V*)(p);
+}
+
+// 4 consecutive storage elements as one load / store: 8 bytes of bf16, 16 of fp32
+template <typename T> struct Raw4 { typedef u32x4 type; };
+template <> struct Raw4<bf16> { typedef u32x2 type; };
+template <typename T> DM_DEV void unpack4(const typename Raw4<T>::type& r, float* out) {
+  if constexpr (sizeof(T) == 2) {
+    out[0] = __uint_as_float(r[0] << 16);
+    out[1] = __uint_as_float(r[0] & 0xffff0000u);
+    out[2] = __uint_as_float(r[1] << 16);
+    out[3] = __uint_as_float(r[1] & 0xffff0000u);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = __uint_as_float(r[i]);
+  }
+}
+template <typename T> DM_DEV void st4(T* p, const float* in) {
+  if constexpr (sizeof(T) == 2) {
+    uint32_t w[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      w[i] = (uint32_t)__builtin_bit_cast(uint16_t, (bf16)in[2 * i]) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, (bf16)in[2 * i + 1]) << 16);
+    *reinterpret_cast<u32x2*>(p) = u32x2{w[0], w[1]};
+  } else {
+    *reinterpret_cast<floatx4*>(p) = floatx4{in[0], in[1], in[2], in[3]};
+  }
+}
+DM_DEV void unpackf4(const floatx4& v, float* out) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = v[i];
+}
 
 // v if ok else 0, without a branch: the mask is made opaque to the optimizer so the
 // (unconditional) load that produced v is not sunk into a divergent branch (the
@@ -113,7 +162,6 @@ DM_DEV uint4 keep_if(uint4 v, bool ok) {
   return v;
 }
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // streaming 16-byte load (non-temporal hint: the data is read once)
 template <typename T>
 DM_DEV uint4 ld_nt(const T* p) {

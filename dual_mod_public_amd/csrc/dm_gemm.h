@@ -73,20 +73,25 @@ template <typename T> struct SrcRowsRs {
   int nparts;
   float inv_d, eps;
   struct Pre {
-    float s;
+    float v[MAX_HEADS / 2];   // the loaded partials (summed in prepare_store, so no wait here)
   };
   // 256 / R adjacent threads per row split its nparts (<= MAX_HEADS) partial sums
   template <int R> DM_DEV Pre prepare_load(int r0, int) const {
-    constexpr int P = 256 / R;
-    static_assert(256 % R == 0 && P <= 8, "rows per block");
+    constexpr int P = 256 / R, Q = MAX_HEADS / P;
+    static_assert(256 % R == 0 && P >= 2 && P <= 8, "rows per block");
     const int r = min(r0 + (int)threadIdx.x / P, rows - 1), part = threadIdx.x % P;
+    const float* row = ssq + (long)r * nparts;
     Pre pr;
-    pr.s = sum_strided<MAX_HEADS / P>(ssq + (long)r * nparts, part, nparts, P);
+#pragma unroll
+    for (int i = 0; i < Q; ++i) pr.v[i] = row[min(part + i * P, nparts - 1)];
     return pr;
   }
   template <int R> DM_DEV void prepare_store(const Pre& pr, float* rs_lds, T*, int) const {
-    constexpr int P = 256 / R;
-    float s = pr.s;
+    constexpr int P = 256 / R, Q = MAX_HEADS / P;
+    const int part = threadIdx.x % P;
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < Q; ++i) s += part + i * P < nparts ? pr.v[i] : 0.f;
 #pragma unroll
     for (int o = 1; o < P; o <<= 1) s += __shfl_xor(s, o, 64);
     if (threadIdx.x % P == 0) rs_lds[threadIdx.x / P] = rsqrtf(s * inv_d + eps);
@@ -116,11 +121,15 @@ struct NoPre {};
 template <class S> struct PrepOf { using type = NoPre; };
 template <typename T> struct PrepOf<SrcRowsRs<T>> { using type = typename SrcRowsRs<T>::Pre; };
 
-// Epilogues may prefetch their own global inputs before the k-loop: an EPI with a
-// member type Pre provides pre = epi.prefetch(row0, col0) and
-// epi.apply(acc, row0, col0, rs, pre); otherwise epi(acc, row0, col0, rs) is called.
-template <class E, class = void> struct has_prefetch { static constexpr bool value = false; };
-template <class E> struct has_prefetch<E, std::void_t<typename E::Pre>> { static constexpr bool value = true; };
+// Tile epilogues: an EPI with a member type TilePre gathers its global inputs with
+// pre = epi.tile_prefetch(m0, n0) before the k-loop (the loads complete under it),
+// then sees the block's whole output tile, staged in LDS as fp32 rows of BN + 4
+// floats: epi.tile_apply<BM, BN, LDT>(tile, m0, n0, rs, pre), rs = the block's row
+// scales. Each thread then owns runs of consecutive columns (16-byte loads and
+// stores) instead of the MFMA fragment layout's one column per lane. Otherwise
+// epi(acc, row0, col0, rs) is called on each wave's fragments.
+template <class E, class = void> struct has_tile_epi { static constexpr bool value = false; };
+template <class E> struct has_tile_epi<E, std::void_t<typename E::TilePre>> { static constexpr bool value = true; };
 
 // operand stages, then the row scales
 template <typename T, int BM, int BN, int D>
@@ -144,7 +153,7 @@ template <int BM, int BN, int WM, int WN> struct WaveTile {
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB>
 DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, char* smem,
                           floatx4 (&acc)[WaveTile<BM, BN, WM, WN>::FM][WaveTile<BM, BN, WM, WN>::FN],
-                          int kbase = 0) {
+                          int kbase) {
   using Tr = GemmTraits<T>;
   using MF = Mfma<T>;
   using WT = WaveTile<BM, BN, WM, WN>;
@@ -241,15 +250,6 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
   };
 
   const int nk = (K + BK - 1) / BK;   // a partial last tile needs k-bounded sources
-  constexpr bool RMS = requires_prepare<SA>::value;
-  typename PrepOf<SA>::type pre{};
-  if constexpr (RMS) pre = sa.template prepare_load<BM>(m0, K);
-  auto prepare_store = [&]() {
-    if constexpr (RMS) {
-      sa.template prepare_store<BM>(pre, rs_lds, reinterpret_cast<T*>(rs_lds + RMS_MAXR), K);
-      __syncthreads();
-    }
-  };
   if (nk >= D && nk % D == 0) {
     // Software pipeline with no data-dependent branches around the loads: the
     // steady state always prefetches tile kt + D (it exists), the last D tiles run
@@ -257,7 +257,6 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
     // for the oldest ring slot.
 #pragma unroll
     for (int s = 0; s < D; ++s) gload(s, ra[s], rb[s]);
-    prepare_store();
     sstore(0, buf[0], ra[0], rb[0]);
     __syncthreads();
     for (int kt0 = 0; kt0 < nk - D; kt0 += D) {
@@ -281,7 +280,6 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
     // short or ragged K: one tile at a time
     for (int kt = 0; kt < nk; ++kt) {
       gload(kt, ra[0], rb[0]);
-      if (kt == 0) prepare_store();
       sstore(kt, buf[0], ra[0], rb[0]);
       __syncthreads();
       compute(buf[0]);
@@ -319,10 +317,6 @@ DM_DEV void gemm_mainloop_dma(const SA& sa, const SB& sb, int K, int m0, int n0,
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;   // rows of an 8-row group start at multiples of 8
-  float* rs_lds = reinterpret_cast<float*>(smem + S * STAGE);
-  constexpr bool RMS = requires_prepare<SA>::value;
-  typename PrepOf<SA>::type pre{};
-  if constexpr (RMS) pre = sa.template prepare_load<BM>(m0, K);
 
   auto issue = [&](int kt, int st) {
     char* base = smem + st * STAGE;
@@ -368,9 +362,6 @@ DM_DEV void gemm_mainloop_dma(const SA& sa, const SB& sb, int K, int m0, int n0,
 #pragma unroll
   for (int st = 0; st < S - 1; ++st)
     if (st < nk) issue(st, st);
-  // the row scales go to LDS while the first tiles are in flight; the first
-  // iteration's lgkmcnt(0) + barrier publishes them
-  if constexpr (RMS) sa.template prepare_store<BM>(pre, rs_lds, nullptr, K);
   for (int kt = 0; kt < nk; ++kt) {
     // tiles issued after kt and possibly outstanding: min(S-2, nk-1-kt)
     const int after = min(S - 2, nk - 1 - kt);
@@ -514,10 +505,32 @@ __global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint
   for (int i = 0; i < WT::FM; ++i)
 #pragma unroll
     for (int j = 0; j < WT::FN; ++j) acc[i][j] = zero4();
-  if constexpr (has_prefetch<EPI>::value) {
-    const typename EPI::Pre pre = epi.prefetch(row0, col0);
+  // Row scales (row-scaled operands feed tile epilogues only): their inputs are
+  // loaded first and the scales are staged in LDS after the k-loop, so no wait on
+  // them, or on the epilogue's gathers issued after them, precedes the k-loop.
+  static_assert(!RMS || has_tile_epi<EPI>::value, "row-scaled operands need a tile epilogue");
+  typename PrepOf<SA>::type pre_a{};
+  if constexpr (RMS) pre_a = sa.template prepare_load<BM>(m0, K);
+  if constexpr (has_tile_epi<EPI>::value) {
+    constexpr int LDT = BN + 4;
+    static_assert(BM * LDT * 4 <= gemm_stage_bytes<T, BM, BN, D>(), "output tile fits the stages");
+    const typename EPI::TilePre pre = epi.tile_prefetch(m0, n0);
     gemm_kloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, (int)blockIdx.z * K);
-    epi.apply(acc, row0, col0, rs, pre);
+    // the k-loop ends with a barrier: the stages are free for the output tile
+    float* tile = reinterpret_cast<float*>(smem);
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < WT::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < WT::FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          tile[(row0 - m0 + 16 * i + 4 * (lane >> 4) + q) * LDT + col0 - n0 + 16 * j + (lane & 15)] = acc[i][j][q];
+    if constexpr (RMS)
+      sa.template prepare_store<BM>(pre_a, reinterpret_cast<float*>(smem + gemm_stage_bytes<T, BM, BN, D>()), nullptr, K);
+    __syncthreads();
+    epi.template tile_apply<BM, BN, LDT>(tile, m0, n0,
+                                         reinterpret_cast<const float*>(smem + gemm_stage_bytes<T, BM, BN, D>()), pre);
   } else {
     gemm_kloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, (int)blockIdx.z * K);
     epi(acc, row0, col0, rs);

@@ -519,127 +519,160 @@ template <typename T, int DH> struct EpiSweep1 {
   T* __restrict__ vin; float* __restrict__ gvu;
   T* __restrict__ save;
 
-  // The epilogue's global inputs are gathered first (prefetch), then combined with
-  // the accumulators and stored (apply): all loads precede all stores, so the
-  // compiler never serialises a memory latency per element on possible aliasing.
-  // (Gathering before the k-loop instead costs occupancy and was measured slower.)
-  struct PreData {
-    float f[4][10];   // per row q: K path gx_a, gx_b, kraw_a, kraw_b, cos, sin;
-                      //   linear V: gx x2, v_raw x2; v_map: sig x4, o x4, + norm weight x4 (f[..][8..])
+  // Block tile 64 x 64 = one packed column group. Thread t owns row t / 4 and the
+  // column quad lc0 = 4 (t % 4) .. + 3 of each of the group's four 16-column
+  // sections, so its global inputs and outputs are runs of 4 consecutive elements.
+  // The inputs are gathered before the k-loop.
+  struct TilePre {
+    floatx4 f[4];                   // K: gx_a, gx_b, cos, sin; linear V: gx x2; v_map: sig x4
+    typename Raw4<T>::type h[8];    // K: kraw_a, kraw_b; linear V: v_raw x2; v_map: o x4, norm weight x4
   };
-  DM_DEV PreData prefetch(int row0, int col0) const {
-    PreData pr;
-    const int lane = threadIdx.x & 63, lc = lane & 15;
+  DM_DEV TilePre tile_prefetch(int m0, int n0) const {
+    const int r = threadIdx.x >> 2, lc0 = 4 * (threadIdx.x & 3);
     const int d = g.d, h = g.h;
-    const int mq0 = row0 + 4 * (lane >> 4);
+    const int m = min(m0 + r, M - 1);
+    const int b = m / g.c, p = m - b * g.c;
+    const int t = g.buf_t0 + p, pos = g.pos0 + p;
+    const long xrow = (long)b * g.Tbuf + t;
+    // The (block-uniform) branches only pick addresses; the loads follow them
+    // unconditionally (unused slots re-read a valid address), so no loaded value
+    // has to be merged, and waited for, where the branches join.
+    const float* fp[4];
+    const T* hp[8];
+    const float* f0 = glogx + xrow * 2 * d;
+    const T* h0 = kraw + ((long)b * h * g.Tbuf + t) * DH;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int m = min(mq0 + q, M - 1);
-      const int b = m / g.c, p = m - b * g.c;
-      const int t = g.buf_t0 + p, pos = g.pos0 + p;
-      const long xrow = (long)b * g.Tbuf + t;
-      if (col0 < 2 * d) {
-        const int hd = col0 / (2 * DH), jj = 16 * ((col0 % (2 * DH)) / 64) + lc;
-        const float* gx = glogx + xrow * 2 * d + hd * DH;
-        const long lrow = (((long)b * h + hd) * g.Tbuf + t) * DH;
-        pr.f[q][0] = gx[jj];
-        pr.f[q][1] = gx[jj + DH / 2];
-        pr.f[q][2] = to_f(kraw[lrow + jj]);
-        pr.f[q][3] = to_f(kraw[lrow + jj + DH / 2]);
-        pr.f[q][4] = cos[(long)pos * (DH / 2) + jj];
-        pr.f[q][5] = sin[(long)pos * (DH / 2) + jj];
-      } else if (ctx_mod == 0) {
-        const int cl = col0 - 2 * d;
-        const int hd = cl / (2 * DH), e0 = 32 * ((cl % (2 * DH)) / 64);
-        const float* gx = glogx + xrow * 2 * d + d + hd * DH;
-        const long lrow = (((long)b * h + hd) * g.Tbuf + t) * DH;
+    for (int k = 0; k < 4; ++k) fp[k] = f0;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          pr.f[q][j] = gx[e0 + 16 * j + lc];
-          pr.f[q][2 + j] = to_f(vraw[lrow + e0 + 16 * j + lc]);
-        }
-      } else if (col0 < 3 * d) {
-        const int c0 = col0 - 2 * d;
+    for (int k = 0; k < 8; ++k) hp[k] = h0;
+    if (n0 < 2 * d) {
+      const int hd = n0 / (2 * DH), jj = 16 * ((n0 % (2 * DH)) / 64) + lc0;
+      const long lrow = (((long)b * h + hd) * g.Tbuf + t) * DH + jj;
+      fp[0] = f0 + hd * DH + jj;
+      fp[1] = fp[0] + DH / 2;
+      fp[2] = cos + (long)pos * (DH / 2) + jj;
+      fp[3] = sin + (long)pos * (DH / 2) + jj;
+      hp[0] = kraw + lrow;
+      hp[1] = hp[0] + DH / 2;
+    } else if (ctx_mod == 0) {
+      const int cl = n0 - 2 * d;
+      const int hd = cl / (2 * DH), e = 32 * ((cl % (2 * DH)) / 64) + lc0;
+      const long lrow = (((long)b * h + hd) * g.Tbuf + t) * DH + e;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int col = c0 + 16 * j + lc;
-          pr.f[q][j] = sig[xrow * d + col];
-          pr.f[q][4 + j] = ctx_mod == 1 ? to_f(o[(long)m * d + col]) : 0.f;
-          pr.f[q][8 + (j & 1)] = 0.f;
+      for (int j = 0; j < 2; ++j) {
+        fp[j] = f0 + d + hd * DH + e + 16 * j;
+        hp[j] = vraw + lrow + 16 * j;
+      }
+    } else if (n0 < 3 * d) {
+      const int c0 = n0 - 2 * d + lc0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) fp[k] = sig + xrow * d + c0 + 16 * k;
+      if (ctx_mod == 1) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          hp[k] = o + (long)m * d + c0 + 16 * k;
+          hp[4 + k] = normw + c0 + 16 * k;
         }
       }
     }
-    if (col0 >= 2 * d && col0 < 3 * d && ctx_mod != 0) {   // norm weight of the 4 columns, in f[0][8..9], f[1][8..9]
-      const int c0 = col0 - 2 * d;
+    TilePre pr;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) pr.f[j >> 1][8 + (j & 1)] = to_f(normw[c0 + 16 * j + lc]);
-    }
+    for (int k = 0; k < 4; ++k) pr.f[k] = ld_global<floatx4>(fp[k]);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) pr.h[k] = ld_global<typename Raw4<T>::type>(hp[k]);
     return pr;
   }
 
-  template <int FM, int FN>
-  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float* rs) const {
-    apply(acc, row0, col0, rs, prefetch(row0, col0));
-  }
-
-  template <int FM, int FN>
-  DM_DEV void apply(const floatx4 (&acc)[FM][FN], int row0, int col0, const float* rs, const PreData& pr) const {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) settle(pr.f[q]);   // every gathered value before the first store
-    static_assert(FM == 1 && FN == 4, "sweep GEMM 1 wave tile is 16 x 64");
-    const int lane = threadIdx.x & 63, lc = lane & 15;
+  template <int BM, int BN, int LDT>
+  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float* rs, const TilePre& pr) const {
+    static_assert(BM == 64 && BN == 64, "sweep GEMM 1 block tile is one 64 x 64 column group");
+    const int r = threadIdx.x >> 2, lc0 = 4 * (threadIdx.x & 3);
     const int d = g.d, h = g.h;
-    const int mq0 = row0 + 4 * (lane >> 4);
+    const int m = m0 + r;
     // the GEMM ran on o with norm_ctx.weight folded into W: u . W^T = rs * acc
-    floatx4 a[4];
+    const float sc = rs[r];
+    float a[4][4];
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) a[j][q] = acc[0][j][q] * rs[4 * (lane >> 4) + q];
-    if (save != nullptr) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (mq0 + q < M)
-#pragma unroll
-          for (int j = 0; j < FN; ++j) save[(long)(mq0 + q) * 4 * d + col0 + 16 * j + lc] = from_f<T>(a[j][q]);
+    for (int k = 0; k < 4; ++k) {
+      const floatx4 v = *reinterpret_cast<const floatx4*>(tile + r * LDT + 16 * k + lc0);
+      a[k][0] = v.x * sc; a[k][1] = v.y * sc; a[k][2] = v.z * sc; a[k][3] = v.w * sc;
     }
+    // raw outputs for the tape: this thread's 16 consecutive columns of row r
+    float sv[16];
+    if (save != nullptr) {
+      const int cs0 = 16 * (threadIdx.x & 3);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int m = mq0 + q;
-      if (m >= M) continue;
-      const int b = m / g.c, p = m - b * g.c;
-      if (col0 < 2 * d) {
-        const int hd = col0 / (2 * DH), jj = 16 * ((col0 % (2 * DH)) / 64) + lc;
-        const float ga = sigmoidf_(pr.f[q][0] + a[2][q]);
-        const float gb = sigmoidf_(pr.f[q][1] + a[3][q]);
-        const float k1 = ga * pr.f[q][2] + (1.f - ga) * a[0][q];
-        const float k2 = gb * pr.f[q][3] + (1.f - gb) * a[1][q];
-        const long crow = ((long)b * h + hd) * out_stride + (long)(out_row0 + p) * DH;
-        Kout[crow + jj] = from_f<T>(k1 * pr.f[q][4] - k2 * pr.f[q][5]);
-        Kout[crow + jj + DH / 2] = from_f<T>(k2 * pr.f[q][4] + k1 * pr.f[q][5]);
-      } else if (ctx_mod == 0) {
-        const int cl = col0 - 2 * d;
-        const int hd = cl / (2 * DH), e0 = 32 * ((cl % (2 * DH)) / 64);
-        const long crow = ((long)b * h + hd) * out_stride + (long)(out_row0 + p) * DH;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const float gv = sigmoidf_(pr.f[q][j] + a[j + 2][q]);
-          Vout[crow + e0 + 16 * j + lc] = from_f<T>(gv * pr.f[q][2 + j] + (1.f - gv) * a[j][q]);
-        }
-      } else if (col0 < 3 * d) {
-        const int c0 = col0 - 2 * d;
-        const float r = rs[4 * (lane >> 4) + q];
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          float v = pr.f[q][j] * tanhf_(a[j][q]);
-          if (ctx_mod == 1) v += lam * (pr.f[q][4 + j] * r * pr.f[j >> 1][8 + (j & 1)]);
-          vin[(long)m * d + c0 + 16 * j + lc] = from_f<T>(v);
-        }
-      } else {
-        const int c0 = col0 - 3 * d;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) gvu[(long)m * d + c0 + 16 * j + lc] = a[j][q];
+      for (int k = 0; k < 4; ++k) {
+        const floatx4 v = *reinterpret_cast<const floatx4*>(tile + r * LDT + cs0 + 4 * k);
+        sv[4 * k] = v.x * sc; sv[4 * k + 1] = v.y * sc; sv[4 * k + 2] = v.z * sc; sv[4 * k + 3] = v.w * sc;
       }
+    }
+    if (m >= M) return;
+    const int b = m / g.c, p = m - b * g.c;
+    if (n0 < 2 * d) {
+      float gxa[4], gxb[4], cs[4], sn[4], ka[4], kb[4];
+      unpackf4(pr.f[0], gxa); unpackf4(pr.f[1], gxb); unpackf4(pr.f[2], cs); unpackf4(pr.f[3], sn);
+      unpack4<T>(pr.h[0], ka); unpack4<T>(pr.h[1], kb);
+      settle(gxa); settle(gxb); settle(cs); settle(sn); settle(ka); settle(kb);   // all loads before any store
+      if (save != nullptr) store_vec<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
+      const int hd = n0 / (2 * DH), jj = 16 * ((n0 % (2 * DH)) / 64) + lc0;
+      float o1[4], o2[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ga = sigmoidf_(gxa[i] + a[2][i]);
+        const float gb = sigmoidf_(gxb[i] + a[3][i]);
+        const float k1 = ga * ka[i] + (1.f - ga) * a[0][i];
+        const float k2 = gb * kb[i] + (1.f - gb) * a[1][i];
+        o1[i] = k1 * cs[i] - k2 * sn[i];
+        o2[i] = k2 * cs[i] + k1 * sn[i];
+      }
+      T* crow = Kout + ((long)b * h + hd) * out_stride + (long)(out_row0 + p) * DH + jj;
+      st4<T>(crow, o1);
+      st4<T>(crow + DH / 2, o2);
+    } else if (ctx_mod == 0) {
+      float gx[2][4], vr[2][4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) { unpackf4(pr.f[j], gx[j]); unpack4<T>(pr.h[j], vr[j]); settle(gx[j]); settle(vr[j]); }
+      if (save != nullptr) store_vec<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
+      const int cl = n0 - 2 * d;
+      const int hd = cl / (2 * DH), e = 32 * ((cl % (2 * DH)) / 64) + lc0;
+      T* crow = Vout + ((long)b * h + hd) * out_stride + (long)(out_row0 + p) * DH + e;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float gv = sigmoidf_(gx[j][i] + a[j + 2][i]);
+          v[i] = gv * vr[j][i] + (1.f - gv) * a[j][i];
+        }
+        st4<T>(crow + 16 * j, v);
+      }
+    } else if (n0 < 3 * d) {
+      float sg[4][4], ov[4][4], nw[4][4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        unpackf4(pr.f[k], sg[k]);
+        settle(sg[k]);
+        if (ctx_mod == 1) { unpack4<T>(pr.h[k], ov[k]); unpack4<T>(pr.h[4 + k], nw[k]); settle(ov[k]); settle(nw[k]); }
+      }
+      if (save != nullptr) store_vec<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
+      const int c0 = n0 - 2 * d + lc0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] = sg[k][i] * tanhf_(a[k][i]);
+          if (ctx_mod == 1) v[i] += lam * (ov[k][i] * sc * nw[k][i]);
+        }
+        st4<T>(vin + (long)m * d + c0 + 16 * k, v);
+      }
+    } else {
+      if (save != nullptr) store_vec<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
+      const int c0 = n0 - 3 * d + lc0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        *reinterpret_cast<floatx4*>(gvu + (long)m * d + c0 + 16 * k) = floatx4{a[k][0], a[k][1], a[k][2], a[k][3]};
     }
   }
 };
