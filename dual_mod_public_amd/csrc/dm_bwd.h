@@ -184,53 +184,59 @@ template <typename T> struct EpiVinBwd {
   T* __restrict__ dctx;              // [N, 4d]
   float* __restrict__ dsig;          // layer accumulator [B, Tbuf, d]
   float* __restrict__ lamdv;         // [N, d]
-  template <int FM, int FN>
-  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
-    const int lane = threadIdx.x & 63, lc = lane & 15;
+  // Block tile 64 x 32: thread t owns row t / 4, columns 8 (t % 4) .. + 7; its
+  // inputs (and the dsig values it will add to) are gathered before the k-loop.
+  struct TilePre {
+    floatx4 sg[2], ds[2];
+    Raw8<T> vm;
+  };
+  DM_DEV TilePre tile_prefetch(int m0, int n0) const {
+    const int r = threadIdx.x >> 2, col = n0 + 8 * (threadIdx.x & 3);
     const int d = g.d;
-    float vm[FM][4][FN], sg[FM][4][FN], ds[FM][4][FN];
+    const int m = min(m0 + r, M - 1);
+    const int b = m / g.c;
+    const long xrow = (long)b * g.Tbuf + g.buf_t0 + m - b * g.c;
+    TilePre pr;
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int k = 0; k < 2; ++k) {
+      pr.sg[k] = ld_global<floatx4>(sig + xrow * d + col + 4 * k);
+      pr.ds[k] = ld_global<floatx4>(dsig + xrow * d + col + 4 * k);
+    }
+    pr.vm = ld8_global(save1 + (long)m * 4 * d + 2 * d + col);
+    return pr;
+  }
+  template <int BM, int BN, int LDT>
+  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre& pr) const {
+    static_assert(BM == 64 && BN == 32, "dv_in GEMM block tile is 64 x 32");
+    const int r = threadIdx.x >> 2, c0 = 8 * (threadIdx.x & 3), col = n0 + c0;
+    const int d = g.d;
+    const int m = m0 + r;
+    float dv[8], sg[8], ds[8], vm[8];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        int m = row0 + 16 * i + 4 * (lane >> 4) + q;
-        m = m < M ? m : 0;
-        const int b = m / g.c;
-        const long xrow = (long)b * g.Tbuf + g.buf_t0 + m - b * g.c;
+    for (int k = 0; k < 2; ++k) {
+      unpackf4(*reinterpret_cast<const floatx4*>(tile + r * LDT + c0 + 4 * k), dv + 4 * k);
+      unpackf4(pr.sg[k], sg + 4 * k);
+      unpackf4(pr.ds[k], ds + 4 * k);
+    }
+    unpack8<T>(pr.vm, vm);
+    if (m >= M) return;
+    settle(sg); settle(ds); settle(vm);   // all loads before any store
+    const int b = m / g.c;
+    const long xrow = (long)b * g.Tbuf + g.buf_t0 + m - b * g.c;
+    float dso[8], dc[8], lv[8];
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int col = col0 + 16 * j + lc;
-          vm[i][q][j] = to_f(save1[(long)m * 4 * d + 2 * d + col]);
-          sg[i][q][j] = sig[xrow * d + col];
-          ds[i][q][j] = dsig[xrow * d + col];
-        }
-      }
+    for (int i = 0; i < 8; ++i) {
+      const float th = tanhf_(vm[i]);
+      dso[i] = ds[i] + dv[i] * th;
+      dc[i] = dv[i] * sg[i] * (1.f - th * th);
+      lv[i] = ctx_mod == 1 ? lam * dv[i] : 0.f;
+    }
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {   // every gathered value before the first store
-        settle(vm[i][q]);
-        settle(sg[i][q]);
-        settle(ds[i][q]);
-      }
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
-        if (m >= M) continue;
-        const int b = m / g.c;
-        const long xrow = (long)b * g.Tbuf + g.buf_t0 + m - b * g.c;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int col = col0 + 16 * j + lc;
-          const float dvi = acc[i][j][q];
-          const float th = tanhf_(vm[i][q][j]);
-          dsig[xrow * d + col] = ds[i][q][j] + dvi * th;
-          dctx[(long)m * 4 * d + 2 * d + col] = from_f<T>(dvi * sg[i][q][j] * (1.f - th * th));
-          lamdv[(long)m * d + col] = ctx_mod == 1 ? lam * dvi : 0.f;
-        }
-      }
+    for (int k = 0; k < 2; ++k) {
+      *reinterpret_cast<floatx4*>(dsig + xrow * d + col + 4 * k) = floatx4{dso[4 * k], dso[4 * k + 1], dso[4 * k + 2], dso[4 * k + 3]};
+      *reinterpret_cast<floatx4*>(lamdv + (long)m * d + col + 4 * k) = floatx4{lv[4 * k], lv[4 * k + 1], lv[4 * k + 2], lv[4 * k + 3]};
+    }
+    store_vec<T, 8>(dctx + (long)m * 4 * d + 2 * d + col, dc);
   }
 };
 

@@ -147,6 +147,28 @@ template <typename T> DM_DEV void st4(T* p, const float* in) {
     *reinterpret_cast<floatx4*>(p) = floatx4{in[0], in[1], in[2], in[3]};
   }
 }
+// 8 consecutive storage elements: one 16-byte load of bf16, two of fp32
+template <typename T> struct Raw8 {
+  u32x4 v[sizeof(T) / 2];
+};
+template <typename T> DM_DEV Raw8<T> ld8_global(const T* p) {
+  Raw8<T> r;
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 2); ++i) r.v[i] = ld_global<u32x4>(p + i * (16 / sizeof(T)));
+  return r;
+}
+template <typename T> DM_DEV void unpack8(const Raw8<T>& r, float* out) {
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = __uint_as_float(r.v[0][i] << 16);
+      out[2 * i + 1] = __uint_as_float(r.v[0][i] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = __uint_as_float(r.v[i >> 2][i & 3]);
+  }
+}
 DM_DEV void unpackf4(const floatx4& v, float* out) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) out[i] = v[i];

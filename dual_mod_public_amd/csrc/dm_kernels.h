@@ -679,6 +679,8 @@ template <typename T, int DH> struct EpiSweep1 {
 
 // sweep GEMM 2 (mult family): v_ctx = v_in . w_vctx^T ->
 // v'' = g_v v_raw + (1 - g_v) v_ctx -> V rows. save2 stores raw v_ctx [rows, d].
+// Block tile 64 x 32: thread t owns row t / 4, columns 8 (t % 4) .. + 7 (inputs
+// gathered before the k-loop).
 template <typename T, int DH> struct EpiSweep2 {
   CellGeom g;
   int M;
@@ -689,52 +691,51 @@ template <typename T, int DH> struct EpiSweep2 {
   long out_stride; int out_row0;
   T* __restrict__ save2;
 
-  template <int FM, int FN>
-  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
-    const int lane = threadIdx.x & 63, lc = lane & 15;
-    const int d = g.d;
-    float gx[FM][4][FN], gu[FM][4][FN], vr[FM][4][FN];
+  struct TilePre {
+    floatx4 gx[2], gu[2];
+    Raw8<T> vr;
+  };
+  DM_DEV TilePre tile_prefetch(int m0, int n0) const {
+    const int r = threadIdx.x >> 2, col = n0 + 8 * (threadIdx.x & 3);
+    const int m = min(m0 + r, M - 1);
+    const int b = m / g.c, t = g.buf_t0 + m - b * g.c;
+    const int hd = col / DH, e = col - hd * DH;
+    const float* gx = glogx + ((long)b * g.Tbuf + t) * 2 * g.d + g.d + col;
+    const float* gu = gvu + (long)m * g.d + col;
+    TilePre pr;
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int k = 0; k < 2; ++k) {
+      pr.gx[k] = ld_global<floatx4>(gx + 4 * k);
+      pr.gu[k] = ld_global<floatx4>(gu + 4 * k);
+    }
+    pr.vr = ld8_global(vraw + (((long)b * g.h + hd) * g.Tbuf + t) * DH + e);
+    return pr;
+  }
+  template <int BM, int BN, int LDT>
+  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre& pr) const {
+    static_assert(BM == 64 && BN == 32, "sweep GEMM 2 block tile is 64 x 32");
+    const int r = threadIdx.x >> 2, c0 = 8 * (threadIdx.x & 3), col = n0 + c0;
+    const int m = m0 + r;
+    float a[8], gx[8], gu[8], vr[8];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        int m = row0 + 16 * i + 4 * (lane >> 4) + q;
-        m = m < M ? m : 0;
-        const int b = m / g.c, t = g.buf_t0 + m - b * g.c;
+    for (int k = 0; k < 2; ++k) {
+      unpackf4(*reinterpret_cast<const floatx4*>(tile + r * LDT + c0 + 4 * k), a + 4 * k);
+      unpackf4(pr.gx[k], gx + 4 * k);
+      unpackf4(pr.gu[k], gu + 4 * k);
+    }
+    unpack8<T>(pr.vr, vr);
+    if (m >= M) return;
+    settle(gx); settle(gu); settle(vr);   // all loads before any store
+    const int b = m / g.c, p = m - b * g.c;
+    const int hd = col / DH, e = col - hd * DH;
+    float v[8];
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int col = col0 + 16 * j + lc;
-          const int hd = col / DH, e = col - hd * DH;
-          gx[i][q][j] = glogx[((long)b * g.Tbuf + t) * 2 * d + d + col];
-          gu[i][q][j] = gvu[(long)m * d + col];
-          vr[i][q][j] = to_f(vraw[(((long)b * g.h + hd) * g.Tbuf + t) * DH + e]);
-        }
-      }
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {   // every gathered value before the first store
-        settle(gx[i][q]);
-        settle(gu[i][q]);
-        settle(vr[i][q]);
-      }
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
-        if (m >= M) continue;
-        const int b = m / g.c, p = m - b * g.c;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int col = col0 + 16 * j + lc;
-          const int hd = col / DH, e = col - hd * DH;
-          const float gv = sigmoidf_(gx[i][q][j] + gu[i][q][j]);
-          Vout[((long)b * g.h + hd) * out_stride + (long)(out_row0 + p) * DH + e] =
-              from_f<T>(gv * vr[i][q][j] + (1.f - gv) * acc[i][j][q]);
-          if (save2 != nullptr) save2[(long)m * d + col] = from_f<T>(acc[i][j][q]);
-        }
-      }
+    for (int i = 0; i < 8; ++i) {
+      const float gv = sigmoidf_(gx[i] + gu[i]);
+      v[i] = gv * vr[i] + (1.f - gv) * a[i];
+    }
+    store_vec<T, 8>(Vout + ((long)b * g.h + hd) * out_stride + (long)(out_row0 + p) * DH + e, v);
+    if (save2 != nullptr) store_vec<T, 8>(save2 + (long)m * g.d + col, a);
   }
 };
 
