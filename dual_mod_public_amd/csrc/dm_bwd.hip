@@ -251,8 +251,8 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
       // du = dctx . W_sweep (+ lam dv_in): split-K slices, then the RMS-VJP inputs
       {
         const int S = DU_SPLIT;
-        EpiStoreF32 ep{N, d, 0, ws.du_part, (long)N * d};
-        launch_gemm_splitk<T, 64, 64, 4, 1, sizeof(T) == 2 ? -3 : 4>(
+        EpiStoreTileF32 ep{N, d, ws.du_part, (long)N * d};
+        launch_gemm_splitk<T, 64, 64, 2, 2, sizeof(T) == 2 ? -3 : 4>(
             SrcRows<T>{dctx + sw * NS * 4 * d, 4 * d, N}, SrcRows<T>{(const T*)w->w_sweep_t, 4 * d, d}, N, d,
             4 * d, S, ep, s);
         hipLaunchKernelGGL((k_du_epi<T, DU_SPLIT>), dim3(cdiv(N, 16), d / DU_EPI_TN), dim3(256), 0, s, N, d, h,

@@ -777,6 +777,28 @@ template <typename T> struct EpiResidual {
 
 // C (fp32) = acc, or C += acc when accumulate != 0
 // C [M, N] fp32 (+)= acc; split-K slice z stores into C + z * zstride.
+// fp32 output of a 64 x 64 block tile staged in LDS (split-K slice z at C + z * zstride):
+// each wave store instruction writes 4 whole 256-byte rows.
+struct EpiStoreTileF32 {
+  int M, N;
+  float* __restrict__ C;
+  long zstride;
+  struct TilePre {};
+  DM_DEV TilePre tile_prefetch(int, int) const { return TilePre{}; }
+  template <int BM, int BN, int LDT>
+  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre&) const {
+    static_assert(BM == 64 && BN == 64, "64 x 64 block tile");
+    float* __restrict__ C = this->C + (long)blockIdx.z * zstride;
+    const int c = 4 * (threadIdx.x & 15);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = 16 * k + (threadIdx.x >> 4);
+      const floatx4 v = *reinterpret_cast<const floatx4*>(tile + r * LDT + c);
+      if (m0 + r < M) *reinterpret_cast<floatx4*>(C + (long)(m0 + r) * N + n0 + c) = v;
+    }
+  }
+};
+
 struct EpiStoreF32 {
   int M, N, accumulate;
   float* __restrict__ C;
