@@ -206,7 +206,7 @@ template <typename T> struct EpiVinBwd {
     return pr;
   }
   template <int BM, int BN, int LDT>
-  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre& pr) const {
+  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre& pr, int) const {
     static_assert(BM == 64 && BN == 32, "dv_in GEMM block tile is 64 x 32");
     const int r = threadIdx.x >> 2, c0 = 8 * (threadIdx.x & 3), col = n0 + c0;
     const int d = g.d;

@@ -145,7 +145,7 @@ void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N
     launch_gemm_kk<T>(sa, sb, M, N, K, ep, s);
     return;
   }
-  EpiStoreF32 ep{M, N, 0, part, (long)M * N};
+  EpiStoreTileF32 ep{M, N, part, (long)M * N};
   if constexpr (sizeof(T) == 2) {
     if (big) launch_gemm_splitk<T, 256, 256, 2, 2, -2>(sa, sb, M, N, K, S, ep, s);
     else if (dma) launch_gemm_splitk<T, 128, 128, 2, 2, -3>(sa, sb, M, N, K, S, ep, s);
@@ -183,7 +183,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
 
   // ---- W_O: do_cat = dy . W_O ; dW_O += dy^T . ocat
   {
-    EpiStoreF32 ep{BT, d, 0, ws.docat};
+    EpiStoreTileF32 ep{BT, d, ws.docat, 0};
     launch_gemm_big<T>(SrcRows<T>{dy, d, BT}, SrcRows<T>{(const T*)w->wo_t, d, d}, BT, d, d,
                                                ep, s);
     gemm_tn<T>(dy, d, ocat, d, gr->wo, d, d, BT, 1, ws.kpart, s);
@@ -321,7 +321,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   // dW_proj = d_proj^T . xhat (packed rows), dxhat = d_proj . W_proj
   gemm_tn<T>(ws.dproj, (long)nproj * d, xhat, d, ws.dWp, nproj * d, d, BT, 0, ws.kpart, s);
   {
-    EpiStoreF32 ep{BT, d, 0, ws.dxhat};
+    EpiStoreTileF32 ep{BT, d, ws.dxhat, 0};
     launch_gemm_big<T>(SrcRows<T>{ws.dproj, (long)nproj * d, BT},
                                       SrcRows<T>{(const T*)w->w_proj_t, (long)nproj * d, d}, BT, d, nproj * d, ep, s);
   }

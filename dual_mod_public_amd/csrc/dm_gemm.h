@@ -128,17 +128,29 @@ template <typename T> struct PrepOf<SrcRowsRs<T>> { using type = typename SrcRow
 // scales. Each thread then owns runs of consecutive columns (16-byte loads and
 // stores) instead of the MFMA fragment layout's one column per lane. Otherwise
 // epi(acc, row0, col0, rs) is called on each wave's fragments.
+// An EPI with a static TILE_ROWS < BM sees the tile in chunks of TILE_ROWS rows
+// (tile_apply<TILE_ROWS, BN, LDT>(tile, m0 + chunk origin, ...)), so that blocks too
+// large for one LDS tile still store whole rows.
 template <class E, class = void> struct has_tile_epi { static constexpr bool value = false; };
 template <class E> struct has_tile_epi<E, std::void_t<typename E::TilePre>> { static constexpr bool value = true; };
+template <class E, class = void> struct tile_rows_of { static constexpr int value = 1 << 30; };
+template <class E> struct tile_rows_of<E, std::void_t<decltype(E::TILE_ROWS)>> { static constexpr int value = E::TILE_ROWS; };
+
+// k-rows per stage of the K-major direct-to-LDS k-loop: 32 for 256 x 256 blocks with
+// at least 4 stages (four 32 KB stages keep three in flight), else 64
+template <int BM, int BN, int S>
+constexpr int kk_stage_k() { return BM * BN >= 65536 && S >= 4 ? 32 : 64; }
 
 // operand stages, then the row scales
-template <typename T, int BM, int BN, int D>
+template <typename T, int BM, int BN, int D, bool KM = false>
 constexpr int gemm_stage_bytes() {
-  return D > 0 ? 2 * (BM + BN) * GemmTraits<T>::LDK * (int)sizeof(T) : (-D) * (BM + BN) * 128;
+  if constexpr (D > 0) return 2 * (BM + BN) * GemmTraits<T>::LDK * (int)sizeof(T);
+  else if constexpr (KM) return (-D) * kk_stage_k<BM, BN, -D>() * (BM + BN) * 2;
+  else return (-D) * (BM + BN) * 128;
 }
-template <typename T, int BM, int BN, int D, bool RMS>
+template <typename T, int BM, int BN, int D, bool RMS, bool KM = false>
 constexpr int gemm_lds_bytes() {
-  return gemm_stage_bytes<T, BM, BN, D>() + (RMS ? RMS_MAXR * 4 : BM * 4);
+  return gemm_stage_bytes<T, BM, BN, D, KM>() + (RMS ? RMS_MAXR * 4 : BM * 4);
 }
 
 // Wave tile geometry of a (BM, BN, WM, WN) block.
@@ -384,8 +396,8 @@ DM_DEV void gemm_mainloop_dma(const SA& sa, const SB& sb, int K, int m0, int n0,
 }
 
 // The direct-to-LDS k-loop for K-major operands (bf16, both operands K-major: the
-// weight-grad products C = A^T B summed over rows). A stage holds 64 k-rows of the
-// block's BM (then BN) columns, BM * 2 bytes per k-row, its 16-byte chunk c stored
+// weight-grad products C = A^T B summed over rows). A stage holds KS k-rows
+// (kk_stage_k) of the block's BM (then BN) columns, BM * 2 bytes per k-row, its 16-byte chunk c stored
 // at chunk c ^ (2 (k & 3)); one global_load_lds_dwordx4 per wave fills 1 KB (1024 /
 // (BM * 2) k-rows). MFMA fragments (8 consecutive k of one column per lane) come
 // from two ds_read_b64_tr_b16 each: in a 16-lane group, lane s names the 8 bytes
@@ -412,17 +424,19 @@ DM_DEV void gemm_mainloop_dma_kk(const SA& sa, const SB& sb, int K, int m0, int 
   using MF = Mfma<T>;
   using WT = WaveTile<BM, BN, WM, WN>;
   constexpr int FM = WT::FM, FN = WT::FN, TM = WT::TM, TN = WT::TN;
+  constexpr int KS = kk_stage_k<BM, BN, S>();             // k-rows per stage
   constexpr int ROWA = BM * 2, ROWB = BN * 2;              // bytes per k-row
-  constexpr int STAGE = 64 * (ROWA + ROWB);
+  constexpr int STAGE = KS * (ROWA + ROWB);
   constexpr int RPA = 1024 / ROWA, RPB = 1024 / ROWB;      // k-rows per wave load instruction
-  constexpr int LA = 64 / RPA / 4, LB = 64 / RPB / 4, L = LA + LB;
+  static_assert(KS % (4 * RPA) == 0 && KS % (4 * RPB) == 0, "whole wave loads per stage");
+  constexpr int LA = KS / RPA / 4, LB = KS / RPB / 4, L = LA + LB;
   constexpr int CPA = ROWA / 16, CPB = ROWB / 16;          // 16-byte chunks per k-row
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
   auto issue = [&](int kt, int st) {
     char* base = smem + st * STAGE;
-    const int k = kbase + kt * 64;
+    const int k = kbase + kt * KS;
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
       const int r0 = (wave * LA + i) * RPA, r = r0 + lane / CPA;
@@ -435,13 +449,13 @@ DM_DEV void gemm_mainloop_dma_kk(const SA& sa, const SB& sb, int K, int m0, int 
       const int r0 = (wave * LB + i) * RPB, r = r0 + lane / CPB;
       const int c = (lane % CPB) ^ (2 * (r & 3));
       __builtin_amdgcn_global_load_lds((const void*)sb.ptr_k(k + r, n0 + 8 * c),
-                                       (lds_void_t*)(base + 64 * ROWA + r0 * ROWB), 16, 0, 0);
+                                       (lds_void_t*)(base + KS * ROWA + r0 * ROWB), 16, 0, 0);
     }
   };
   auto compute = [&](const char* As) {
-    const char* Bs = As + 64 * ROWA;
+    const char* Bs = As + KS * ROWA;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
+    for (int kk = 0; kk < KS / 32; ++kk) {
       typename MF::frag af[FM], bfr[FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i) af[i] = frag_kmajor<ROWA>(As, 32 * kk, wm * TM + 16 * i);
@@ -454,7 +468,7 @@ DM_DEV void gemm_mainloop_dma_kk(const SA& sa, const SB& sb, int K, int m0, int 
     }
   };
 
-  const int nk = K / 64;
+  const int nk = K / KS;
 #pragma unroll
   for (int st = 0; st < S - 1; ++st)
     if (st < nk) issue(st, st);
@@ -480,7 +494,7 @@ DM_DEV void gemm_mainloop_dma_kk(const SA& sa, const SB& sb, int K, int m0, int 
 // Generic kernel: zero accumulators, k-loop, epilogue on the wave's registers.
 // epi(acc, row0, col0) with row0/col0 the global origin of the wave tile.
 // Split-K launches (gridDim.z > 1) reduce k in [z*K, (z+1)*K) in block z; their
-// epilogue tells the slices apart by blockIdx.z.
+// epilogue gets the slice index z.
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB>
 DM_DEV void gemm_kloop(const SA& sa, const SB& sb, int K, int m0, int n0, char* smem,
                        floatx4 (&acc)[WaveTile<BM, BN, WM, WN>::FM][WaveTile<BM, BN, WM, WN>::FN], int kbase) {
@@ -494,12 +508,28 @@ __global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint
   const uint64_t t0 = prof_begin(prof_ts);
   using WT = WaveTile<BM, BN, WM, WN>;
   constexpr bool RMS = requires_prepare<SA>::value;
-  __shared__ __attribute__((aligned(1024))) char smem[gemm_lds_bytes<T, BM, BN, D, RMS>()];
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  constexpr bool KM = SA::KMAJOR && SB::KMAJOR && D < 0;
+  __shared__ __attribute__((aligned(1024))) char smem[gemm_lds_bytes<T, BM, BN, D, RMS, KM>()];
+  // Blocks are dispatched round-robin over the 8 XCDs (each with its own L2). For
+  // the K-major (weight-grad) products every XCD gets a contiguous range of tiles
+  // instead (x fastest, then y, then the split-K slice), so tiles that share operand
+  // columns at the same k share an L2.
+  int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  if constexpr (KM) {
+    const int gx = gridDim.x, gy = gridDim.y, nb = gx * gy * (int)gridDim.z;
+    if (nb % 8 == 0) {
+      const int L = bx + gx * (by + gy * bz);
+      const int t = (L % 8) * (nb / 8) + L / 8;
+      bx = t % gx;
+      by = (t / gx) % gy;
+      bz = t / (gx * gy);
+    }
+  }
+  const int m0 = by * BM, n0 = bx * BN;
   static_assert(!RMS || BM <= RMS_MAXR, "row-scale slots");
   const int wave = threadIdx.x >> 6;
   const int row0 = m0 + (wave / WN) * WT::TM, col0 = n0 + (wave % WN) * WT::TN;
-  const float* rs = reinterpret_cast<const float*>(smem + gemm_stage_bytes<T, BM, BN, D>()) + (wave / WN) * WT::TM;
+  const float* rs = reinterpret_cast<const float*>(smem + gemm_stage_bytes<T, BM, BN, D, KM>()) + (wave / WN) * WT::TM;
   floatx4 acc[WT::FM][WT::FN];
 #pragma unroll
   for (int i = 0; i < WT::FM; ++i)
@@ -512,28 +542,37 @@ __global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint
   typename PrepOf<SA>::type pre_a{};
   if constexpr (RMS) pre_a = sa.template prepare_load<BM>(m0, K);
   if constexpr (has_tile_epi<EPI>::value) {
+    constexpr int TR = tile_rows_of<EPI>::value < BM ? tile_rows_of<EPI>::value : BM;   // rows per chunk
     constexpr int LDT = BN + 4;
-    static_assert(BM * LDT * 4 <= gemm_stage_bytes<T, BM, BN, D>(), "output tile fits the stages");
+    static_assert(BM % TR == 0 && TR % 16 == 0, "whole 16-row groups per chunk");
+    static_assert(TR * LDT * 4 <= gemm_stage_bytes<T, BM, BN, D, KM>(), "output chunk fits the stages");
     const typename EPI::TilePre pre = epi.tile_prefetch(m0, n0);
-    gemm_kloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, (int)blockIdx.z * K);
+    gemm_kloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, bz * K);
     // the k-loop ends with a barrier: the stages are free for the output tile
     float* tile = reinterpret_cast<float*>(smem);
+    const float* rs_lds = reinterpret_cast<const float*>(smem + gemm_stage_bytes<T, BM, BN, D, KM>());
     const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < WT::FM; ++i)
+    for (int c = 0; c < BM / TR; ++c) {
+      if (c > 0) __syncthreads();   // the previous chunk has been read
 #pragma unroll
-      for (int j = 0; j < WT::FN; ++j)
+      for (int i = 0; i < WT::FM; ++i) {
+        if ((row0 - m0 + 16 * i) / TR != c) continue;   // wave-uniform
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          tile[(row0 - m0 + 16 * i + 4 * (lane >> 4) + q) * LDT + col0 - n0 + 16 * j + (lane & 15)] = acc[i][j][q];
-    if constexpr (RMS)
-      sa.template prepare_store<BM>(pre_a, reinterpret_cast<float*>(smem + gemm_stage_bytes<T, BM, BN, D>()), nullptr, K);
-    __syncthreads();
-    epi.template tile_apply<BM, BN, LDT>(tile, m0, n0,
-                                         reinterpret_cast<const float*>(smem + gemm_stage_bytes<T, BM, BN, D>()), pre);
+        for (int j = 0; j < WT::FN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            tile[(row0 - m0 - c * TR + 16 * i + 4 * (lane >> 4) + q) * LDT + col0 - n0 + 16 * j + (lane & 15)] =
+                acc[i][j][q];
+      }
+      if constexpr (RMS)
+        if (c == 0) sa.template prepare_store<BM>(pre_a, const_cast<float*>(rs_lds), nullptr, K);
+      __syncthreads();
+      epi.template tile_apply<TR, BN, LDT>(tile, m0 + c * TR, n0, rs_lds + c * TR, pre, bz);
+    }
   } else {
-    gemm_kloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, (int)blockIdx.z * K);
-    epi(acc, row0, col0, rs);
+    gemm_kloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, bz * K);
+    epi(acc, row0, col0, rs, bz);
   }
   prof_end(prof_ts, t0);
 }

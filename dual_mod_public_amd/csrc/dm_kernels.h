@@ -140,7 +140,7 @@ template <typename T, int DH> struct EpiProj {
   // stored (a load after a store that may alias it would wait for one memory
   // latency per group).
   template <int FM, int FN>
-  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
+  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*, int) const {
     static_assert((FN * 16) % DH == 0, "projection wave tile must span whole heads");
     constexpr int NHW = FN * 16 / DH;   // heads per wave tile
     constexpr int FH = DH / 16;         // 16-column tiles per head
@@ -584,7 +584,7 @@ template <typename T, int DH> struct EpiSweep1 {
   }
 
   template <int BM, int BN, int LDT>
-  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float* rs, const TilePre& pr) const {
+  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float* rs, const TilePre& pr, int) const {
     static_assert(BM == 64 && BN == 64, "sweep GEMM 1 block tile is one 64 x 64 column group");
     const int r = threadIdx.x >> 2, lc0 = 4 * (threadIdx.x & 3);
     const int d = g.d, h = g.h;
@@ -712,7 +712,7 @@ template <typename T, int DH> struct EpiSweep2 {
     return pr;
   }
   template <int BM, int BN, int LDT>
-  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre& pr) const {
+  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre& pr, int) const {
     static_assert(BM == 64 && BN == 32, "sweep GEMM 2 block tile is 64 x 32");
     const int r = threadIdx.x >> 2, c0 = 8 * (threadIdx.x & 3), col = n0 + c0;
     const int m = m0 + r;
@@ -747,7 +747,7 @@ template <typename T> struct EpiResidual {
   // the residual rows of 16-row group i + 1 are loaded before group i is stored
   // (y may alias x)
   template <int FM, int FN>
-  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
+  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*, int) const {
     const int lane = threadIdx.x & 63, lc = lane & 15;
     float xv[2][4][FN];
     auto load_x = [&](int i, int buf) {
@@ -775,57 +775,59 @@ template <typename T> struct EpiResidual {
   }
 };
 
-// C (fp32) = acc, or C += acc when accumulate != 0
-// C [M, N] fp32 (+)= acc; split-K slice z stores into C + z * zstride.
-// fp32 output of a 64 x 64 block tile staged in LDS (split-K slice z at C + z * zstride):
-// each wave store instruction writes 4 whole 256-byte rows.
+// fp32 output of a block tile staged in LDS in chunks of up to 64 rows (split-K
+// slice z at C + z * zstride): each wave store instruction writes 64 consecutive
+// 16-byte pieces of a row (whole rows of up to 256 columns).
 struct EpiStoreTileF32 {
+  static constexpr int TILE_ROWS = 64;
   int M, N;
   float* __restrict__ C;
   long zstride;
   struct TilePre {};
   DM_DEV TilePre tile_prefetch(int, int) const { return TilePre{}; }
-  template <int BM, int BN, int LDT>
-  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre&) const {
-    static_assert(BM == 64 && BN == 64, "64 x 64 block tile");
-    float* __restrict__ C = this->C + (long)blockIdx.z * zstride;
-    const int c = 4 * (threadIdx.x & 15);
+  template <int TR, int BN, int LDT>
+  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre&, int z) const {
+    constexpr int C4 = BN / 4, NV = TR * C4;   // 16-byte pieces per row, per chunk
+    static_assert(NV % 256 == 0, "whole passes of the block");
+    float* __restrict__ C = this->C + (long)z * zstride;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int r = 16 * k + (threadIdx.x >> 4);
+    for (int it = 0; it < NV / 256; ++it) {
+      const int idx = it * 256 + threadIdx.x, r = idx / C4, c = 4 * (idx % C4);
       const floatx4 v = *reinterpret_cast<const floatx4*>(tile + r * LDT + c);
       if (m0 + r < M) *reinterpret_cast<floatx4*>(C + (long)(m0 + r) * N + n0 + c) = v;
     }
   }
 };
-
+// C (fp32) = acc, or C += acc when accumulate != 0
+// C [M, N] fp32 (+)= acc; split-K slice z stores into C + z * zstride.
 struct EpiStoreF32 {
   int M, N, accumulate;
   float* __restrict__ C;
   long zstride = 0;
-  // with accumulate, every old value is loaded before the first store
+  // With accumulate, each 16-row group's old values are loaded before its stores
+  // (one group at a time: a whole 128 x 128 wave tile of old values would not fit
+  // in registers next to the accumulators).
   template <int FM, int FN>
-  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*) const {
+  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*, int z) const {
     const int lane = threadIdx.x & 63, lc = lane & 15;
-    float* __restrict__ C = this->C + (long)blockIdx.z * zstride;
-    float old[FM][4][FN];
+    float* __restrict__ C = this->C + (long)z * zstride;
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i) {
+      float old[4][FN];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = min(row0 + 16 * i + 4 * (lane >> 4) + q, M - 1);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) old[i][q][j] = accumulate ? C[(long)m * N + col0 + 16 * j + lc] : 0.f;
+        for (int j = 0; j < FN; ++j) old[q][j] = accumulate ? C[(long)m * N + col0 + 16 * j + lc] : 0.f;
       }
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
         if (m >= M) continue;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) C[(long)m * N + col0 + 16 * j + lc] = old[i][q][j] + acc[i][j][q];
+        for (int j = 0; j < FN; ++j) C[(long)m * N + col0 + 16 * j + lc] = old[q][j] + acc[i][j][q];
       }
+    }
   }
 };
 
