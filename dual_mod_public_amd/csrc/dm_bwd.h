@@ -23,8 +23,24 @@ namespace dm {
 // ---------------------------------------------------------------------------
 // small helpers
 // ---------------------------------------------------------------------------
-static __global__ __launch_bounds__(256) void k_fill(float* __restrict__ p, long n, float v) {
-  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) p[i] = v;
+// zero up to FILL_MAX fp32 arrays, array blockIdx.y; 16-byte stores where the array allows
+constexpr int FILL_MAX = 12;
+struct FillList {
+  float* p[FILL_MAX];
+  long n[FILL_MAX];
+  int n_arr;
+};
+static __global__ __launch_bounds__(256) void k_fill_list(FillList fl) {
+  float* __restrict__ p = fl.p[blockIdx.y];
+  const long n = fl.n[blockIdx.y];
+  const long stride = (long)gridDim.x * 256;
+  const long i0 = blockIdx.x * 256L + threadIdx.x;
+  if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+    for (long i = i0; 4 * i + 3 < n; i += stride) *reinterpret_cast<floatx4*>(p + 4 * i) = zero4();
+    for (long j = (n / 4) * 4 + i0; j < n; j += stride) p[j] = 0.f;
+  } else {
+    for (long i = i0; i < n; i += stride) p[i] = 0.f;
+  }
 }
 
 // C-layout MFMA product for one wave: acc[t] += X[16 rows, KD] . Y[16 t + (0..15), KD]^T,

@@ -4,6 +4,8 @@
 //
 // Never allocates device memory and never synchronizes: every buffer is carved
 // from the caller's workspace; all launches go to the caller's stream.
+#include <initializer_list>
+#include <utility>
 #include <vector>
 
 #include "dm_bwd.h"
@@ -43,7 +45,7 @@ template <typename T> struct BwdWs {
 };
 
 constexpr int NSLOT_TM = 16;      // rows per norm_ctx-weight partial slot (k_du_epi block rows)
-constexpr int DU_SPLIT = 4;       // split-K slices of the du GEMM (K = 4d is long, M = B*c short)
+constexpr int DU_SPLIT = DM_DU_SPLIT;   // split-K slices of the du GEMM
 constexpr int NCHUNK = 64;        // row chunks of the column sums
 // fp32 elements of the split-K partial buffer of the weight-grad GEMMs ([S, M, N], N = d)
 constexpr long KSPLIT_ELEMS(long d) { return 32 * d * d; }
@@ -96,9 +98,20 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   return w;
 }
 
-inline void fill0(float* p, size_t n, hipStream_t s) {
-  const int blocks = (int)std::min<size_t>((n + 255) / 256, 4096);
-  hipLaunchKernelGGL(k_fill, dim3(blocks), dim3(256), 0, s, p, (long)n, 0.f);
+// zero several fp32 arrays in one launch (array i in grid row i)
+inline void fill0_list(std::initializer_list<std::pair<float*, size_t>> arrs, hipStream_t s) {
+  FillList fl{};
+  size_t most = 0;
+  for (const auto& a : arrs) {
+    if (a.second == 0) continue;
+    fl.p[fl.n_arr] = a.first;
+    fl.n[fl.n_arr] = (long)a.second;
+    ++fl.n_arr;
+    most = std::max(most, a.second);
+  }
+  if (fl.n_arr == 0) return;
+  const int blocks = (int)std::min<size_t>((most / 4 + 255) / 256, 1024);
+  hipLaunchKernelGGL(k_fill_list, dim3(blocks, fl.n_arr), dim3(256), 0, s, fl);
 }
 
 // out[chunk] column sums of a [M, ncols] fp32 matrix, added into dst[0..ncols)
@@ -172,14 +185,15 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   ProfScope whole(PROF_BWD, s);
 
   // ---- zero the accumulators
-  fill0(ws.dq, (size_t)BT * d, s);
-  fill0(ws.dkraw, (size_t)BT * d, s);
-  fill0(ws.dkself, (size_t)BT * d, s);
-  fill0(ws.dvraw, (size_t)BT * d, s);
-  fill0(ws.dglogx, (size_t)BT * 2 * d, s);
-  fill0(ws.dsig, (size_t)BT * d, s);
-  fill0(ws.dnw, (size_t)cdiv(B * CMAX, NSLOT_TM) * d, s);
-  fill0(ws.dWs, (size_t)4 * d * d, s);
+  fill0_list({{ws.dq, (size_t)BT * d},
+              {ws.dkraw, (size_t)BT * d},
+              {ws.dkself, (size_t)BT * d},
+              {ws.dvraw, (size_t)BT * d},
+              {ws.dglogx, (size_t)BT * 2 * d},
+              {ws.dsig, (size_t)BT * d},
+              {ws.dnw, (size_t)cdiv(B * CMAX, NSLOT_TM) * d},
+              {ws.dWs, (size_t)4 * d * d}},
+             s);
 
   // ---- W_O: do_cat = dy . W_O ; dW_O += dy^T . ocat
   {
@@ -201,6 +215,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   T* vinS = tape != nullptr ? (T*)(const_cast<char*>(tape) + tape_off[n_cells]) : ws.vinL;
   const int t_end = sched[3 * (n_cells - 1)] + sched[3 * (n_cells - 1) + 1];   // rows of the schedule
   long coff = 0;   // columns of the weight-grad operands filled so far
+  std::vector<RmsSeg> rms;   // tape mode: every cell's o rows, normalised after the cell loop
   for (int ci = n_cells - 1; ci >= 0; --ci) {
     const int pos0 = sched[3 * ci], cc = sched[3 * ci + 1], K = sched[3 * ci + 2];
     const int N = B * cc;
@@ -245,14 +260,15 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
       if (mult) {
         EpiVinBwd<T> ev{g, N, c->ctx_mod, c->mult_res_lambda, sv.save1 + sw * NS * 4 * d, L->sig,
                         dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
-        launch_gemm<T, 64, 32, 4, 1, 8>(SrcRows<T>{dvc + sw * NS * d, d, N},
-                                        SrcRows<T>{(const T*)w->w_vctx_t, d, d}, N, d, d, ev, s);
+        const SrcRows<T> av{dvc + sw * NS * d, d, N}, bv{(const T*)w->w_vctx_t, d, d};
+        if constexpr (SW2_STAGES > 0) launch_gemm_auto<T, 64, 32, 4, 1, SW2_STAGES, 8>(av, bv, N, d, d, ev, s);
+        else launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, d, d, ev, s);
       }
       // du = dctx . W_sweep (+ lam dv_in): split-K slices, then the RMS-VJP inputs
       {
         const int S = DU_SPLIT;
         EpiStoreTileF32 ep{N, d, ws.du_part, (long)N * d};
-        launch_gemm_splitk<T, 64, 64, 2, 2, sizeof(T) == 2 ? -3 : 4>(
+        launch_gemm_splitk<T, 64, 64, 2, 2, sizeof(T) == 2 ? -DU_STAGES : 4>(
             SrcRows<T>{dctx + sw * NS * 4 * d, 4 * d, N}, SrcRows<T>{(const T*)w->w_sweep_t, 4 * d, d}, N, d,
             4 * d, S, ep, s);
         hipLaunchKernelGGL((k_du_epi<T, DU_SPLIT>), dim3(cdiv(N, 16), d / DU_EPI_TN), dim3(256), 0, s, N, d, h,
@@ -279,23 +295,41 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
       }
     }
     // the other operand of dW_sweep = dctx^T u: this cell's K*N rows of u = RMSNorm(o)
-    // (dW_vctx = dv_ctx^T v_in reads the stacked v_in as it is)
+    // (dW_vctx = dv_ctx^T v_in reads the stacked v_in as it is). The tape keeps every
+    // cell's o: those rows are normalised after the cell loop, RMS_MAX_SEG cells per
+    // launch; a recomputed cell's o is overwritten by the next cell, so now.
     {
       const int rows = K * N;
-      hipLaunchKernelGGL(k_rms_rows<T>, dim3(cdiv(rows, 4)), dim3(256), 0, s, (const T*)sv.o, rows, d,
-                         (const float*)sv.ssq, h, (const T*)w->norm_ctx_w, inv_d, c->rms_eps, ws.uL + coff * d);
+      if (tape != nullptr) {
+        rms.push_back(RmsSeg{sv.o, sv.ssq, coff, rows});
+      } else {
+        hipLaunchKernelGGL(k_rms_rows<T>, dim3(cdiv(rows, 4)), dim3(256), 0, s, (const T*)sv.o, rows, d,
+                           (const float*)sv.ssq, h, (const T*)w->norm_ctx_w, inv_d, c->rms_eps, ws.uL + coff * d);
+      }
       coff += rows;
     }
+  }
+  for (size_t i0 = 0; i0 < rms.size(); i0 += RMS_MAX_SEG) {
+    RmsSegs ra{};
+    ra.nseg = (int)std::min<size_t>(RMS_MAX_SEG, rms.size() - i0);
+    int most = 0;
+    for (int i = 0; i < ra.nseg; ++i) {
+      ra.seg[i] = rms[i0 + i];
+      most = std::max(most, ra.seg[i].rows);
+    }
+    hipLaunchKernelGGL(k_rms_rows_multi<T>, dim3(cdiv(most, 4), ra.nseg), dim3(256), 0, s, ra, d, h,
+                       (const T*)w->norm_ctx_w, inv_d, c->rms_eps, ws.uL);
   }
   {   // the layer's sweep weight grads, one GEMM each over all cells' stacked rows
     // (zero rows up to a whole k-tile)
     const int Kp = (int)(cdiv(coff, 64) * 64);
     if (Kp > coff) {
       const size_t tail = (size_t)(Kp - coff) * sizeof(T) / 4;
-      fill0(reinterpret_cast<float*>(ws.dctxL + coff * 4 * d), tail * 4 * d, s);
-      fill0(reinterpret_cast<float*>(ws.uL + coff * d), tail * d, s);
-      fill0(reinterpret_cast<float*>(ws.dvcL + coff * d), tail * d, s);
-      if (mult) fill0(reinterpret_cast<float*>(vinS + coff * d), tail * d, s);
+      fill0_list({{reinterpret_cast<float*>(ws.dctxL + coff * 4 * d), tail * 4 * d},
+                  {reinterpret_cast<float*>(ws.uL + coff * d), tail * d},
+                  {reinterpret_cast<float*>(ws.dvcL + coff * d), tail * d},
+                  {reinterpret_cast<float*>(vinS + coff * d), mult ? tail * d : 0}},
+                 s);
     }
     gemm_tn<T>(ws.dctxL, 4 * d, ws.uL, d, ws.dWs, 4 * d, d, Kp, 1, ws.kpart, s);
     if (mult) gemm_tn<T>(ws.dvcL, d, vinS, d, gr->w_vctx, d, d, Kp, 1, ws.kpart, s);

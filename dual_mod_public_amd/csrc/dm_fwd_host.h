@@ -148,12 +148,15 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
   SrcRows<T> sb{(const T*)w->w_sweep, c->d, 4 * c->d};
   EpiSweep1<T, DH> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
                       Kout, Vout, out_stride, out_row0, vin, gvu, save1};
-  launch_gemm_auto<T, 64, 64, 2, 2, 3, 4>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
+  launch_gemm_auto<T, 64, 64, 2, 2, SW1_STAGES, 4>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
   if (c->ctx_mod != DM_CTX_LINEAR) {
     SrcRows<T> av{vin, c->d, N};
     SrcRows<T> bv{(const T*)w->w_vctx, c->d, c->d};
     EpiSweep2<T, DH> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2};
-    launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, c->d, c->d, e2, s, PROF_SWEEP2);
+    if constexpr (SW2_STAGES > 0)
+      launch_gemm_auto<T, 64, 32, 4, 1, SW2_STAGES, 8>(av, bv, N, c->d, c->d, e2, s, PROF_SWEEP2);
+    else
+      launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, c->d, c->d, e2, s, PROF_SWEEP2);
   }
 }
 

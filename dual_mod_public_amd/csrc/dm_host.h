@@ -13,6 +13,23 @@
 
 namespace dm {
 
+// Launch shapes of the per-sweep GEMMs (M = B*c rows). Their k-loops are bound by
+// load latency, so the number of k-tiles in flight per block sets their speed.
+// The defaults are the measured best on MI355X; -D overrides exist for tuning builds.
+#ifndef DM_SW1_STAGES
+#define DM_SW1_STAGES 3   // sweep GEMM 1: direct-to-LDS stages of the 64 x 64 blocks
+#endif
+#ifndef DM_SW2_STAGES
+#define DM_SW2_STAGES 0   // GEMM 2 / dv_in GEMM (64 x 32 blocks): 0 = register ring of depth 8
+#endif
+#ifndef DM_DU_STAGES
+#define DM_DU_STAGES 3    // du split-K GEMM: direct-to-LDS stages of the 64 x 64 blocks
+#endif
+#ifndef DM_DU_SPLIT
+#define DM_DU_SPLIT 4     // du split-K slices (K = 4d is long, M = B*c short)
+#endif
+constexpr int SW1_STAGES = DM_SW1_STAGES, SW2_STAGES = DM_SW2_STAGES, DU_STAGES = DM_DU_STAGES;
+
 inline std::string& last_error() {
   static thread_local std::string e;
   return e;

@@ -95,6 +95,41 @@ static __global__ __launch_bounds__(256) void k_rms_rows(const T* __restrict__ o
 
 
 
+// k_rms_rows over several row sets in one launch (set blockIdx.y): set i has `rows`
+// rows o / ssq and writes output rows out_row0.. of one stacked output.
+constexpr int RMS_MAX_SEG = 64;
+struct RmsSeg {
+  const void* o;
+  const float* ssq;
+  long out_row0;
+  int rows;
+};
+struct RmsSegs {
+  RmsSeg seg[RMS_MAX_SEG];
+  int nseg;
+};
+template <typename T>
+static __global__ __launch_bounds__(256) void k_rms_rows_multi(RmsSegs a, int cols, int nparts,
+                                                               const T* __restrict__ w, float inv_d, float eps,
+                                                               T* __restrict__ out) {
+  constexpr int V = 16 / (int)sizeof(T);
+  const RmsSeg& sg = a.seg[blockIdx.y];
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= sg.rows) return;
+  const T* __restrict__ o = reinterpret_cast<const T*>(sg.o);
+  T* __restrict__ dst = out + (sg.out_row0 + r) * (long)cols;
+  const float rs = rsqrtf(wave_sum(lane < nparts ? sg.ssq[(long)r * nparts + lane] : 0.f) * inv_d + eps);
+  for (int c = lane * V; c < cols; c += 64 * V) {
+    float f[V], wf[V];
+    unpack16<T>(*reinterpret_cast<const uint4*>(o + (long)r * cols + c), f);
+    unpack16<T>(*reinterpret_cast<const uint4*>(w + c), wf);
+#pragma unroll
+    for (int e = 0; e < V; ++e) f[e] *= rs * wf[e];
+    *reinterpret_cast<uint4*>(dst + c) = pack16<T>(f);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // row RMSNorm (attn_norm, models/dualmod/attention.py:74-83): one wave per row
 // ---------------------------------------------------------------------------
