@@ -15,6 +15,7 @@ import torch.nn as nn
 from . import _lib as L
 from .config import DualModConfig
 from .engine import HipSweepCell, check_supported, uniform_chunks
+from .lowrank import LoRAGate, LoRALinear
 
 
 class RMSNorm(nn.Module):
@@ -41,13 +42,25 @@ class DualModAttention(nn.Module):
         self.wk = nn.Linear(d, d, bias=False)
         self.wv = nn.Linear(d, d, bias=False)
         self.wo = nn.Linear(d, d, bias=False)
-        self.w_kctx = nn.Linear(d, d, bias=False)
-        self.w_gk = nn.Linear(2 * d, d, bias=True)
-        self.w_vctx = nn.Linear(d, d, bias=False)
-        self.w_gv = nn.Linear(2 * d, d, bias=True)
+        # ctx_rank / gate_rank > 0: factored operators with the reference's parameter
+        # names (attention.py:24-75, 125-152, 182-183); the kernels get their dense products
+        def ctx_mat(bias=False):
+            if cfg.ctx_rank > 0:
+                return LoRALinear(d, cfg.ctx_rank, d, bias=bias)
+            return nn.Linear(d, d, bias=bias)
+
+        def gate():
+            if cfg.gate_rank > 0:
+                return LoRAGate(2 * d, cfg.gate_rank, d)
+            return nn.Linear(2 * d, d, bias=True)
+
+        self.w_kctx = ctx_mat()
+        self.w_gk = gate()
+        self.w_vctx = ctx_mat()
+        self.w_gv = gate()
         if cfg.ctx_mod in ("mult", "mult_res"):
-            self.v_gate = nn.Linear(d, d, bias=True)
-            self.v_map = nn.Linear(d, d, bias=False)
+            self.v_gate = ctx_mat(bias=True)
+            self.v_map = ctx_mat()
         self.norm_ctx = RMSNorm(d)
         self._cells = {}
         self._packed_version = None

@@ -13,6 +13,7 @@ forward state kept in LayerBufs and caches).
 import torch
 
 from .engine import LayerGrads
+from .lowrank import factor_grads, is_factored
 
 
 class DMLayerFn(torch.autograd.Function):
@@ -31,6 +32,7 @@ class DMLayerFn(torch.autograd.Function):
                            residual=residual, tape=tape)
         ctx.cell, ctx.schedule, ctx.normalize, ctx.residual = cell, schedule, normalize, residual
         ctx.names = names
+        ctx.params = dict(zip(names, params)) if is_factored(dict.fromkeys(names)) else None
         ctx.state = (x, cos, sin, bufs, K, V, ocat, tape)
         ctx.param_dtypes = [p.dtype for p in params]
         return y
@@ -43,8 +45,9 @@ class DMLayerFn(torch.autograd.Function):
         dx = torch.empty_like(x)
         cell.layer_backward(x, dy.to(x.dtype).contiguous(), dx, cos, sin, ctx.schedule, K, V, ocat,
                             bufs, grads, normalize=ctx.normalize, residual=ctx.residual, tape=tape)
-        pgrads = [grads[n].to(dt) for n, dt in zip(ctx.names, ctx.param_dtypes)]
-        ctx.state = None
+        g = grads.t if ctx.params is None else factor_grads(ctx.params, grads.t, ctx.names)
+        pgrads = [g[n].to(dt) for n, dt in zip(ctx.names, ctx.param_dtypes)]
+        ctx.state = ctx.params = None
         return (dx, None, None, None, None, None, None, None, None, *pgrads)
 
 
@@ -52,7 +55,8 @@ def dm_layer(x, cell, params, cos, sin, schedule, normalize=True, residual=True,
     """Differentiable DM attention layer through the HIP path.
 
     params: {reference name: tensor} — the tensors ``cell`` was packed from; their
-    gradients come back through autograd. normalize/residual select the Block
+    gradients come back through autograd (factored gates / ctx operators, gate_rank /
+    ctx_rank > 0, get the dense gradients chained onto their factors). normalize/residual select the Block
     sublayer y = x + W_O DM(attn_norm(x)) (default) or DualModAttention.forward's
     W_O DM(xhat). save_tape keeps every cell's sweep states from the forward
     (``cell.tape_bytes(schedule)`` of device memory) so the backward does not

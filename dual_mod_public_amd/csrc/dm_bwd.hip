@@ -160,7 +160,7 @@ void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N
   }
   EpiStoreTileF32 ep{M, N, part, (long)M * N};
   if constexpr (sizeof(T) == 2) {
-    if (big) launch_gemm_splitk<T, 256, 256, 2, 2, -2>(sa, sb, M, N, K, S, ep, s);
+    if (big) launch_gemm_splitk<T, 256, 256, 2, 2, -KK_STAGES>(sa, sb, M, N, K, S, ep, s);
     else if (dma) launch_gemm_splitk<T, 128, 128, 2, 2, -3>(sa, sb, M, N, K, S, ep, s);
     else launch_gemm_splitk<T, 128, 128, 2, 2, 4>(sa, sb, M, N, K, S, ep, s);
   } else {

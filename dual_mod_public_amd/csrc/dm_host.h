@@ -28,7 +28,23 @@ namespace dm {
 #ifndef DM_DU_SPLIT
 #define DM_DU_SPLIT 4     // du split-K slices (K = 4d is long, M = B*c short)
 #endif
+// Layer-level GEMMs (M = B*T rows, outside the sweep chain): block tile and
+// direct-to-LDS stages of the K-contiguous products, stages of the K-major (weight-grad)
+// 256 x 256 products.
+#ifndef DM_BIG_BM
+#define DM_BIG_BM 256
+#endif
+#ifndef DM_BIG_BN
+#define DM_BIG_BN 256
+#endif
+#ifndef DM_BIG_STAGES
+#define DM_BIG_STAGES 2
+#endif
+#ifndef DM_KK_STAGES
+#define DM_KK_STAGES 2
+#endif
 constexpr int SW1_STAGES = DM_SW1_STAGES, SW2_STAGES = DM_SW2_STAGES, DU_STAGES = DM_DU_STAGES;
+constexpr int BIG_BM = DM_BIG_BM, BIG_BN = DM_BIG_BN, BIG_STAGES = DM_BIG_STAGES, KK_STAGES = DM_KK_STAGES;
 
 inline std::string& last_error() {
   static thread_local std::string e;
@@ -144,8 +160,8 @@ template <typename T, class SA, class SB, class EPI>
 void launch_gemm_big(const SA& sa, const SB& sb, int M, int N, int K, const EPI& epi, hipStream_t s,
                      int prof_cls = PROF_NONE) {
   if constexpr (sizeof(T) == 2 && !SA::KMAJOR && !SB::KMAJOR) {
-    if (M % 256 == 0 && N % 256 == 0 && K % 64 == 0) {
-      launch_gemm<T, 256, 256, 2, 2, -2>(sa, sb, M, N, K, epi, s, prof_cls);
+    if (M % BIG_BM == 0 && N % BIG_BN == 0 && K % 64 == 0) {
+      launch_gemm<T, BIG_BM, BIG_BN, 2, 2, -BIG_STAGES>(sa, sb, M, N, K, epi, s, prof_cls);
       return;
     }
   }
@@ -161,7 +177,7 @@ void launch_gemm_kk(const SrcKMajor<T>& sa, const SrcKMajor<T>& sb, int M, int N
   if constexpr (sizeof(T) == 2) {
     if (K % 64 == 0 && sa.kmax >= K && sb.kmax >= K) {
       if (M % 256 == 0 && N % 256 == 0) {
-        launch_gemm<T, 256, 256, 2, 2, -2>(sa, sb, M, N, K, epi, s, prof_cls);
+        launch_gemm<T, 256, 256, 2, 2, -KK_STAGES>(sa, sb, M, N, K, epi, s, prof_cls);
         return;
       }
       if (M % 128 == 0 && N % 128 == 0) {

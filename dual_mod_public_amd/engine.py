@@ -15,6 +15,7 @@ import ctypes
 import torch
 
 from . import _lib as L
+from .lowrank import dense_params
 
 
 def uniform_chunks(T, c, n_sweeps=None):
@@ -50,7 +51,7 @@ def check_supported(cfg):
     for knob, off in (("k_ctx_norm", "none"), ("v_ctx_norm", "none"), ("v_norm", "none")):
         if getattr(cfg, knob, off) != off:
             bad.append(f"{knob}={getattr(cfg, knob)}")
-    for knob in ("kmod_vraw_heads", "gate_rank", "ctx_rank", "attn_logn_ref"):
+    for knob in ("kmod_vraw_heads", "attn_logn_ref"):
         if getattr(cfg, knob, 0):
             bad.append(f"{knob}={getattr(cfg, knob)}")
     if getattr(cfg, "v_clamp_tau", 0.0):
@@ -103,6 +104,7 @@ class PackedWeights:
         a state dict or a DualModAttention's named parameters."""
         cfg = self.cfg
         keep = []
+        sd = dense_params(sd)   # factored gates / ctx operators (gate_rank, ctx_rank) -> dense
 
         def t(name):
             x = sd[name].detach().to(device=self.device, dtype=self.dtype).contiguous()

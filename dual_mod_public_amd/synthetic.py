@@ -9,6 +9,8 @@ golden-vector script and the GPU run all see identical numbers.
 Distribution (all configs): every matrix N(0, std=0.02), including w_kctx,
 w_vctx and v_map so the mult_res branch is live; gate biases and the v_gate
 bias N(0, 0.02) (gates open, sigma ~ 0.5); RMSNorm weights 1; per-head gains 1.
+Factored operators (gate_rank / ctx_rank > 0, attention.py:24-75) draw both factors
+N(0, sqrt(std / sqrt(r))), so their product has the dense weights' scale.
 """
 
 from collections import OrderedDict
@@ -26,19 +28,30 @@ def param_specs(cfg, with_attn_norm=True):
              ("wv.weight", (d, d), "w"), ("wo.weight", (d, d), "w")]
     if getattr(cfg, "v_norm", "none") == "rms":
         specs.append(("v_gain", (h,), "one"))
+    rc, rg = getattr(cfg, "ctx_rank", 0), getattr(cfg, "gate_rank", 0)
+
+    def ctx(name, bias=False):
+        if rc > 0:
+            out = [(f"{name}.down.weight", (rc, d), "f"), (f"{name}.up.weight", (d, rc), "f")]
+            return out + ([(f"{name}.up.bias", (d,), "b")] if bias else [])
+        return [(f"{name}.weight", (d, d), "w")] + ([(f"{name}.bias", (d,), "b")] if bias else [])
+
+    def gate(name):
+        if rg > 0:
+            return [(f"{name}.a.weight", (rg, 2 * d), "f"), (f"{name}.b.weight", (d, rg), "f"),
+                    (f"{name}.b.bias", (d,), "b")]
+        return [(f"{name}.weight", (d, 2 * d), "w"), (f"{name}.bias", (d,), "b")]
+
     if cfg.enable_key_mod:
-        specs += [("w_kctx.weight", (d, d), "w"), ("w_gk.weight", (d, 2 * d), "w"),
-                  ("w_gk.bias", (d,), "b")]
+        specs += ctx("w_kctx") + gate("w_gk")
         if getattr(cfg, "k_ctx_norm", "none") == "rms":
             specs.append(("k_gain", (h,), "one"))
     if cfg.enable_value_mod:
-        specs += [("w_vctx.weight", (d, d), "w"), ("w_gv.weight", (d, 2 * d), "w"),
-                  ("w_gv.bias", (d,), "b")]
+        specs += ctx("w_vctx") + gate("w_gv")
         if getattr(cfg, "v_ctx_norm", "none") == "rms":
             specs.append(("ctx_gain", (h,), "one"))
     if mod in ("mult", "mult_res"):
-        specs += [("v_gate.weight", (d, d), "w"), ("v_gate.bias", (d,), "b"),
-                  ("v_map.weight", (d, d), "w")]
+        specs += ctx("v_gate", bias=True) + ctx("v_map")
     if cfg.enable_key_mod or cfg.enable_value_mod:
         specs.append(("norm_ctx.weight", (d,), "one"))
     if with_attn_norm:
@@ -52,6 +65,8 @@ def make_state_dict(cfg, seed=0, std=0.02, dtype=torch.float32, with_attn_norm=T
     for name, shape, kind in param_specs(cfg, with_attn_norm):
         if kind == "one":
             a = np.ones(shape, dtype=np.float64)
+        elif kind == "f":   # one factor of a rank-r product: r is the smaller dimension
+            a = rng.normal(0.0, (std / min(shape) ** 0.5) ** 0.5, size=shape)
         else:
             a = rng.normal(0.0, std, size=shape)
         sd[name] = torch.from_numpy(a).to(dtype)
