@@ -25,7 +25,8 @@ c_fp = ctypes.c_void_p
 class dm_config(ctypes.Structure):
     _fields_ = [("dtype", c_i32), ("B", c_i32), ("d", c_i32), ("h", c_i32), ("dh", c_i32),
                 ("ctx_mod", c_i32), ("mult_res_lambda", ctypes.c_float), ("rms_eps", ctypes.c_float),
-                ("local_window", c_i32), ("flags", c_i32), ("reserved", c_i32 * 6)]
+                ("local_window", c_i32), ("flags", c_i32), ("kmod_vraw_heads", c_i32),
+                ("kmod_mode", c_i32), ("reserved", c_i32 * 4)]
 
 
 DM_FLAG_NO_RESIDUAL = 1
@@ -219,4 +220,10 @@ def make_config(cfg, B, dtype):
     c.mult_res_lambda = float(getattr(cfg, "mult_res_lambda", 1.0))
     c.rms_eps = 1e-5
     c.local_window = int(getattr(cfg, "local_window", 0) or 0)
+    # kmod heads (attention.py:362-384): 0 raw, 1 raw with the tanh bound, 2 gated_norm
+    c.kmod_vraw_heads = int(getattr(cfg, "kmod_vraw_heads", 0) or 0)
+    if getattr(cfg, "kmod_mode", "raw") == "gated_norm":
+        c.kmod_mode = 2
+    else:
+        c.kmod_mode = 1 if getattr(cfg, "kmod_vraw_bound", "none") == "tanh" else 0
     return c

@@ -166,25 +166,46 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
   dgx[c2] = ogx2 + dl2;
   a.dkraw[lrow + jj] = okr1 + dk1 * g1;
   a.dkraw[lrow + jj + DH / 2] = okr2 + dk2 * g2;
-  // ---- value: v'' = g_v v_raw + (1 - g_v) v_ctx
+  // ---- value: v'' = g_v v_raw + (1 - g_v) v_ctx; kmod heads (attention.py:362-384):
+  // raw v'' = v_raw (or tanh(v_raw)) takes no gate or v_ctx grad; gated_norm blends with
+  // v_ctx = 0 (live gate, no v_ctx grad)
   const float gv1 = sigmoidf_(gxv1 + gvu1), gv2 = sigmoidf_(gxv2 + gvu2);
-  const float dlv1 = dv1 * (vr1 - vc1) * gv1 * (1.f - gv1);
-  const float dlv2 = dv2 * (vr2 - vc2) * gv2 * (1.f - gv2);
+  float dlv1, dlv2, dvc1, dvc2, dvr1, dvr2;
+  if (c1 < g.kmod_cols) {
+    const bool gated = g.kmod_mode == DM_KMOD_GATED_NORM;
+    dlv1 = gated ? dv1 * vr1 * gv1 * (1.f - gv1) : 0.f;
+    dlv2 = gated ? dv2 * vr2 * gv2 * (1.f - gv2) : 0.f;
+    dvc1 = 0.f;
+    dvc2 = 0.f;
+    if (gated) { dvr1 = dv1 * gv1; dvr2 = dv2 * gv2; }
+    else if (g.kmod_mode == DM_KMOD_RAW_TANH) {
+      const float t1 = tanhf_(vr1), t2 = tanhf_(vr2);
+      dvr1 = dv1 * (1.f - t1 * t1);
+      dvr2 = dv2 * (1.f - t2 * t2);
+    } else { dvr1 = dv1; dvr2 = dv2; }
+  } else {
+    dlv1 = dv1 * (vr1 - vc1) * gv1 * (1.f - gv1);
+    dlv2 = dv2 * (vr2 - vc2) * gv2 * (1.f - gv2);
+    dvc1 = dv1 * (1.f - gv1);
+    dvc2 = dv2 * (1.f - gv2);
+    dvr1 = dv1 * gv1;
+    dvr2 = dv2 * gv2;
+  }
   if (a.ctx_mod == 0) {
-    D[cv1] = from_f<T>(dv1 * (1.f - gv1));
-    D[cv2] = from_f<T>(dv2 * (1.f - gv2));
+    D[cv1] = from_f<T>(dvc1);
+    D[cv2] = from_f<T>(dvc2);
     D[cv1 + 32] = from_f<T>(dlv1);
     D[cv2 + 32] = from_f<T>(dlv2);
   } else {
-    a.dvc[(long)m * d + c1] = from_f<T>(dv1 * (1.f - gv1));
-    a.dvc[(long)m * d + c2] = from_f<T>(dv2 * (1.f - gv2));
+    a.dvc[(long)m * d + c1] = from_f<T>(dvc1);
+    a.dvc[(long)m * d + c2] = from_f<T>(dvc2);
     D[3 * d + c1] = from_f<T>(dlv1);
     D[3 * d + c2] = from_f<T>(dlv2);
   }
   dgx[d + c1] = ogxv1 + dlv1;
   dgx[d + c2] = ogxv2 + dlv2;
-  a.dvraw[lrow + jj] = ovr1 + dv1 * gv1;
-  a.dvraw[lrow + jj + DH / 2] = ovr2 + dv2 * gv2;
+  a.dvraw[lrow + jj] = ovr1 + dvr1;
+  a.dvraw[lrow + jj + DH / 2] = ovr2 + dvr2;
 }
 
 // ---------------------------------------------------------------------------

@@ -183,6 +183,8 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
               const float* sin, int pos0, int cc, int n_sweeps, int buf_t0, int Tbuf, T* Kc, T* Vc,
               int cache_T, T* ocat, float* o_last, const CellWs& ws, const CellSave<T>* sv, hipStream_t s) {
   CellGeom g{c->B, cc, c->d, c->h, DH, pos0, buf_t0, Tbuf, cache_T};
+  g.kmod_cols = c->kmod_vraw_heads * DH;
+  g.kmod_mode = c->kmod_mode;
   const int BH = c->B * c->h;
   const int N = c->B * cc;
   const size_t NS = (size_t)N, d = c->d;   // per-sweep row stride of the saved arrays

@@ -1,6 +1,7 @@
 // Kernels of the DM forward cell and the layer projection pass.
 #pragma once
 
+#include "../../include/dm_abi.h"
 #include "dm_attn.h"
 #include "dm_gemm.h"
 
@@ -264,7 +265,20 @@ struct CellGeom {
   int buf_t0;      // row of chunk row 0 inside the layer buffers
   int Tbuf;        // T of the layer buffers (qr/kraw/kself/vraw/glogx/sig)
   int cache_T;     // T of the K/V cache
+  int kmod_cols = 0;   // value columns [0, kmod_cols) belong to kmod heads (kmod_vraw_heads * dh)
+  int kmod_mode = 0;   // dm_kmod_mode of those columns
 };
+
+// Value blend of column col (attention.py:362-384): v'' = g v_raw + (1 - g) v_ctx, except
+// for the kmod heads: raw (v_raw, or tanh(v_raw) with the tanh bound) or, gated_norm,
+// the blend with v_ctx = 0.
+DM_DEV float value_blend(const CellGeom& g, int col, float gv, float vr, float vc) {
+  if (col < g.kmod_cols) {
+    if (g.kmod_mode == DM_KMOD_GATED_NORM) return gv * vr;
+    return g.kmod_mode == DM_KMOD_RAW_TANH ? tanhf_(vr) : vr;
+  }
+  return gv * vr + (1.f - gv) * vc;
+}
 
 // ---------------------------------------------------------------------------
 // committed-prefix accumulator (scan_cell_fwd.py:119-129): per (split, b, h),
@@ -676,10 +690,8 @@ template <typename T, int DH> struct EpiSweep1 {
       for (int j = 0; j < 2; ++j) {
         float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float gv = sigmoidf_(gx[j][i] + a[j + 2][i]);
-          v[i] = gv * vr[j][i] + (1.f - gv) * a[j][i];
-        }
+        for (int i = 0; i < 4; ++i)
+          v[i] = value_blend(g, hd * DH + e + 16 * j + i, sigmoidf_(gx[j][i] + a[j + 2][i]), vr[j][i], a[j][i]);
         st4<T>(crow + 16 * j, v);
       }
     } else if (n0 < 3 * d) {
@@ -765,10 +777,7 @@ template <typename T, int DH> struct EpiSweep2 {
     const int hd = col / DH, e = col - hd * DH;
     float v[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float gv = sigmoidf_(gx[i] + gu[i]);
-      v[i] = gv * vr[i] + (1.f - gv) * a[i];
-    }
+    for (int i = 0; i < 8; ++i) v[i] = value_blend(g, col + i, sigmoidf_(gx[i] + gu[i]), vr[i], a[i]);
     store_vec<T, 8>(Vout + ((long)b * g.h + hd) * out_stride + (long)(out_row0 + p) * DH + e, v);
     if (save2 != nullptr) store_vec<T, 8>(save2 + (long)m * g.d + col, a);
   }

@@ -51,7 +51,7 @@ def check_supported(cfg):
     for knob, off in (("k_ctx_norm", "none"), ("v_ctx_norm", "none"), ("v_norm", "none")):
         if getattr(cfg, knob, off) != off:
             bad.append(f"{knob}={getattr(cfg, knob)}")
-    for knob in ("kmod_vraw_heads", "attn_logn_ref"):
+    for knob in ("attn_logn_ref",):
         if getattr(cfg, knob, 0):
             bad.append(f"{knob}={getattr(cfg, knob)}")
     if getattr(cfg, "v_clamp_tau", 0.0):

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DM_ABI_VERSION 2
+#define DM_ABI_VERSION 3
 
 typedef enum dm_status {
   DM_OK = 0,
@@ -59,8 +59,15 @@ typedef struct dm_config {
   float rms_eps;            /* RMSNorm eps of attn_norm / norm_ctx: 1e-5 */
   int32_t local_window;     /* decode only: W tokens incl. self, 0 = full */
   int32_t flags;            /* DM_FLAG_* */
-  int32_t reserved[6];
+  int32_t kmod_vraw_heads;  /* config.py kmod_vraw_heads: the first n heads keep raw values */
+  int32_t kmod_mode;        /* dm_kmod_mode (kmod_mode + kmod_vraw_bound), attention.py:362-384 */
+  int32_t reserved[4];
 } dm_config;
+
+/* kmod heads (value columns of heads < kmod_vraw_heads), attention.py:362-384:
+ * RAW v'' = v_raw; RAW_TANH v'' = tanh(v_raw) (kmod_vraw_bound="tanh");
+ * GATED_NORM v_ctx = 0 in the blend, v'' = g v_raw (kmod_mode="gated_norm"). */
+typedef enum dm_kmod_mode { DM_KMOD_RAW = 0, DM_KMOD_RAW_TANH = 1, DM_KMOD_GATED_NORM = 2 } dm_kmod_mode;
 
 /* dm_layer_fwd / dm_layer_bwd: without this flag y = x + W_O . DM(norm(x)) (the Block
  * attention sublayer, models/dualmod/model.py:123-124); with it y = W_O . DM(norm(x))

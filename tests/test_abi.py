@@ -30,7 +30,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 
 def test_abi_version():
-    assert L.load().dm_abi_version() == 2
+    assert L.load().dm_abi_version() == 3
 
 
 def _conf(**kw):
@@ -74,9 +74,25 @@ def test_workspace_query():
 
 def test_unsupported_knobs_raise():
     from dual_mod_public_amd.engine import check_supported
-    for kw in (dict(k_ctx_norm="rms"), dict(v_clamp_tau=1.0), dict(kmod_vraw_heads=1),
+    for kw in (dict(k_ctx_norm="rms"), dict(v_clamp_tau=1.0), dict(v_ctx_norm="rms"),
                dict(gate_type_v="independent"), dict(ctx_mod="fusion"), dict(attn_logn_ref=64)):
         cfg = DualModConfig(d_model=256, n_heads=4, **kw)
         with pytest.raises(NotImplementedError):
             check_supported(cfg)
     check_supported(DualModConfig(d_model=256, n_heads=4, ctx_mod="mult_res"))
+    # implemented knobs: kmod heads (every mode), factored gates / ctx operators
+    for kw in (dict(kmod_vraw_heads=1), dict(kmod_vraw_heads=2, kmod_vraw_bound="tanh"),
+               dict(kmod_vraw_heads=1, kmod_mode="gated_norm"), dict(gate_rank=8, ctx_rank=16)):
+        check_supported(DualModConfig(d_model=256, n_heads=4, ctx_mod="mult_res", **kw))
+
+
+def test_kmod_config_fields():
+    """The kmod knob reaches dm_config (and is validated by the library)."""
+    c = L.make_config(DualModConfig(d_model=256, n_heads=4, kmod_vraw_heads=2, kmod_mode="gated_norm"), 2,
+                      __import__("torch").float32)
+    assert (c.kmod_vraw_heads, c.kmod_mode) == (2, 2)
+    c = L.make_config(DualModConfig(d_model=256, n_heads=4, kmod_vraw_heads=1, kmod_vraw_bound="tanh"), 2,
+                      __import__("torch").float32)
+    assert (c.kmod_vraw_heads, c.kmod_mode) == (1, 1)
+    c.kmod_vraw_heads = 5   # more kmod heads than heads: rejected by the library
+    assert L.load().dm_cell_workspace_bytes(c, 64) == 0
