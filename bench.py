@@ -46,8 +46,8 @@ COPY_CAL_BYTES = 256 << 20  # --copy-calibration: bytes read (and written) per c
 # HBM bytes per launch of the roofline kernels (read + written), from rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE passes over this script (profiles/traffic_sweep1_decode.md has the commands and raw
 # readings), each scaled by what the counter reads for the 256 MiB --copy-calibration copy.
-# sweep1: tape-mode launches at C3; dec_read: launches at P = 32768..32783.
-TRAFFIC_BYTES = {"sweep1": 34.24e6, "dec_read": 8614.3e6}
+# sweep1: the N = B*c = 512-row launches at C3 (tape mode); dec_read: launches at P = 32768..32783.
+TRAFFIC_BYTES = {"sweep1": 34.96e6, "dec_read": 8613.0e6}
 TIMING_NOTE = ("avg_launch_ms: per-dispatch span from the device clock (s_memrealtime, first block "
                "start to last block end), recorded by the kernel itself over a second pass of the timed "
                "steps (instrumented_ms_per_step); avg_launch_ms_events: HIP event pair around each launch "
@@ -98,14 +98,14 @@ def build_layer(cfg, B, T, dev):
     return sd, cell, x, cos.contiguous(), sin.contiguous(), bufs, K, V, ocat, y
 
 
-def cpu_baseline(cfg, sd, T, B, fwdbwd):
+def cpu_baseline(cfg, sd, T, B, fwdbwd, cpu_T=0):
     """The oracle's chunked-Jacobi layer (same schedule, fp32 torch) on this host's cores:
-    forward only, or forward + autograd backward over a T-prefix sample (the same
-    per-token work at a shorter committed prefix: 512 positions = 8 chunks)."""
+    forward only, or forward + autograd backward, over the whole workload or, with
+    cpu_T < T, a T-prefix sample (the same per-token work at a shorter committed prefix)."""
     import oracle as O
     nthr = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(nthr)
-    Ts = T if not fwdbwd else min(T, 512)
+    Ts = min(T, cpu_T) if cpu_T else T
     x = make_input((B, Ts, cfg.d_model), seed=C2["xseed"])
     cos, sin = O.build_rope_cache(Ts, cfg.head_dim, cfg.rope_theta)
     sched = O.uniform_chunks(Ts, C2["c"], C2["K"])
@@ -117,7 +117,8 @@ def cpu_baseline(cfg, sd, T, B, fwdbwd):
         y = O.dm_layer(cfg, sdf, x, cos, sin, schedule=sched)
         (y * dy).sum().backward()
         dt = time.perf_counter() - t0
-        what = f"layer forward + autograd backward at B={B}, T={Ts} (T-prefix of 2048; c=64, K=4)"
+        span = "the whole workload" if Ts == T else f"T-prefix of {T}"
+        what = f"layer forward + autograd backward at B={B}, T={Ts} ({span}; c=64, K=4)"
     else:
         sdf = {k: v.float() for k, v in sd.items()}
         with torch.no_grad():
@@ -191,6 +192,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-T", type=int, default=0,
+                    help="CPU baseline over a T-prefix of the workload (default: the whole T)")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=0)
     ap.add_argument("--kernel", default="sweep1", help="kernel class timed for the roofline")
@@ -332,7 +335,7 @@ def main():
         torch.cuda.empty_cache()
         out["decode"] = bench_decode(dev, args.decode_steps or None)
     if not args.no_cpu_baseline and args.workload != "c4":
-        out["cpu_baseline"] = cpu_baseline(cfg, sd, T, B, fwdbwd)
+        out["cpu_baseline"] = cpu_baseline(cfg, sd, T, B, fwdbwd, args.cpu_T)
     print(json.dumps(out), flush=True)
 
 
