@@ -15,7 +15,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "libdm_hip.so")
 
 DM_F32, DM_BF16 = 0, 1
-CTX_MOD = {"linear": 0, "mult_res": 1, "mult": 2}
+CTX_MOD = {"linear": 0, "mult_res": 1, "mult": 2, "fusion": 3}
 
 c_i32 = ctypes.c_int32
 c_vp = ctypes.c_void_p
@@ -36,7 +36,8 @@ GRAD_FIELDS = (("wq", "wq.weight"), ("wk", "wk.weight"), ("wv", "wv.weight"), ("
                ("w_kctx", "w_kctx.weight"), ("w_vctx", "w_vctx.weight"), ("w_gk", "w_gk.weight"),
                ("w_gv", "w_gv.weight"), ("b_gk", "w_gk.bias"), ("b_gv", "w_gv.bias"),
                ("v_gate", "v_gate.weight"), ("b_vgate", "v_gate.bias"), ("v_map", "v_map.weight"),
-               ("norm_ctx_w", "norm_ctx.weight"), ("attn_norm_w", "attn_norm.weight"))
+               ("norm_ctx_w", "norm_ctx.weight"), ("attn_norm_w", "attn_norm.weight"),
+               ("v_pre", "v_pre.weight"))
 
 
 class dm_grads(ctypes.Structure):
@@ -46,7 +47,7 @@ class dm_grads(ctypes.Structure):
 class dm_params(ctypes.Structure):
     _fields_ = [(n, c_vp) for n in ("wq", "wk", "wv", "wo", "w_kctx", "w_vctx", "w_gk", "w_gv",
                                     "b_gk", "b_gv", "v_gate", "b_vgate", "v_map", "norm_ctx_w",
-                                    "attn_norm_w")]
+                                    "attn_norm_w", "v_pre")]
 
 
 class dm_packed(ctypes.Structure):

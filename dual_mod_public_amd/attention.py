@@ -61,6 +61,10 @@ class DualModAttention(nn.Module):
         if cfg.ctx_mod in ("mult", "mult_res"):
             self.v_gate = ctx_mat(bias=True)
             self.v_map = ctx_mat()
+        elif cfg.ctx_mod == "fusion":
+            # attention.py:173-174, 198-200: v_in = u + silu(v_pre([xhat, u])), zero-initialised
+            self.v_pre = nn.Linear(2 * d, d, bias=False)
+            nn.init.zeros_(self.v_pre.weight)
         self.norm_ctx = RMSNorm(d)
         self._cells = {}
         self._packed_version = None

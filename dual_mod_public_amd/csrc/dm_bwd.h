@@ -211,6 +211,7 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
 // ---------------------------------------------------------------------------
 // dv_in = dv_ctx . W_vctx epilogue (mult family): v_in = lam u + sig tanh(vm)
 //   dsig += dv_in tanh(vm); dctx[:, 2d + j] = dv_in sig (1 - tanh^2); lamdv = lam dv_in
+//   (fusion, v_in = u + silu(z), z = px + vm: dsig and dctx[:, 2d + j] += dv_in silu'(z), lamdv = dv_in)
 // ---------------------------------------------------------------------------
 template <typename T> struct EpiVinBwd {
   CellGeom g;
@@ -263,10 +264,18 @@ template <typename T> struct EpiVinBwd {
     float dso[8], dc[8], lv[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float th = tanhf_(vm[i]);
-      dso[i] = ds[i] + dv[i] * th;
-      dc[i] = dv[i] * sg[i] * (1.f - th * th);
-      lv[i] = ctx_mod == 1 ? lam * dv[i] : 0.f;
+      if (ctx_mod == 3) {   // fusion: v_in = u + silu(z), z = px + vm; silu' = s (1 + z (1 - s))
+        const float z = sg[i] + vm[i], s = sigmoidf_(z);
+        const float dz = dv[i] * s * (1.f + z * (1.f - s));
+        dso[i] = ds[i] + dz;
+        dc[i] = dz;
+        lv[i] = dv[i];
+      } else {
+        const float th = tanhf_(vm[i]);
+        dso[i] = ds[i] + dv[i] * th;
+        dc[i] = dv[i] * sg[i] * (1.f - th * th);
+        lv[i] = ctx_mod == 1 ? lam * dv[i] : 0.f;
+      }
     }
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -880,7 +889,7 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
 // ---------------------------------------------------------------------------
 constexpr int PROJ_ROWS = 64;
 template <typename T, int DH>
-static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, int h, int nproj,
+static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, int h, int nproj, int fusion,
                                                   const float* __restrict__ dq, const float* __restrict__ dkraw,
                                                   const float* __restrict__ dkself, const float* __restrict__ dvraw,
                                                   const float* __restrict__ dglogx, const float* __restrict__ dsig,
@@ -906,8 +915,9 @@ static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, i
     float z1 = 0.f, z2 = 0.f;
     if (nproj == 6) {
       const float sg1 = sig[(long)m * d + c1], sg2 = sig[(long)m * d + c2];
-      z1 = dsig[(long)m * d + c1] * sg1 * (1.f - sg1);
-      z2 = dsig[(long)m * d + c2] * sg2 * (1.f - sg2);
+      // fusion: dsig already holds the grad of the raw pre-activation (no sigmoid, no bias)
+      z1 = fusion ? dsig[(long)m * d + c1] : dsig[(long)m * d + c1] * sg1 * (1.f - sg1);
+      z2 = fusion ? dsig[(long)m * d + c2] : dsig[(long)m * d + c2] * sg2 * (1.f - sg2);
     }
     T* D = dproj + (long)m * nproj * d;
     D[c1] = from_f<T>(q1 * cs + q2 * sn);

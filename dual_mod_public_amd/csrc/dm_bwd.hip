@@ -347,12 +347,14 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
   // (+ the bias grads' column partials: sums of dglogx (b_gk | b_gv) and of
   // dsig sig (1 - sig) (b_vgate) over each block's rows)
   const int pchunks = cdiv(BT, PROJ_ROWS);
+  const bool fusion = c->ctx_mod == DM_CTX_FUSION;
   hipLaunchKernelGGL((k_proj_bwd<T, DH>), dim3(cdiv(d / 2, 256), pchunks), dim3(256), 0, s, BT, T_, d, h, nproj,
+                     fusion ? 1 : 0,
                      (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself, (const float*)ws.dvraw,
                      (const float*)ws.dglogx, (const float*)ws.dsig, (const float*)L->sig, cos, sin, ws.dproj,
                      ws.colpart);
   hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks, 3 * d, 3 * d,
-                     (const float*)ws.colpart, gr->b_gk, gr->b_gv, mult ? gr->b_vgate : nullptr, d);
+                     (const float*)ws.colpart, gr->b_gk, gr->b_gv, (mult && !fusion) ? gr->b_vgate : nullptr, d);
   const T* xhat = norm ? (const T*)L->xhat : x;
   // dW_proj = d_proj^T . xhat (packed rows), dxhat = d_proj . W_proj
   gemm_tn<T>(ws.dproj, (long)nproj * d, xhat, d, ws.dWp, nproj * d, d, BT, 0, ws.kpart, s);
@@ -369,7 +371,8 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
     u.push_back(UnpackSeg{gr->wv, d, 0, d, 2 * d, 0});
     u.push_back(UnpackSeg{gr->w_gk, 2 * d, 0, d, 3 * d, 0});
     u.push_back(UnpackSeg{gr->w_gv, 2 * d, 0, d, 4 * d, 0});
-    if (mult) u.push_back(UnpackSeg{gr->v_gate, d, 0, d, 5 * d, 0});
+    if (fusion) u.push_back(UnpackSeg{gr->v_pre, 2 * d, 0, d, 5 * d, 0});   // x-half of v_pre
+    else if (mult) u.push_back(UnpackSeg{gr->v_gate, d, 0, d, 5 * d, 0});
     unpack(u, d, ws.dWp, s);
     u.clear();
     for (int hd = 0; hd < h; ++hd)
@@ -381,7 +384,8 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
         u.push_back(UnpackSeg{gr->w_gk + (size_t)r1 * 2 * d, 2 * d, d, 16, base + 48, 0});
       }
     if (mult) {
-      u.push_back(UnpackSeg{gr->v_map, d, 0, d, 2 * d, 0});
+      if (fusion) u.push_back(UnpackSeg{gr->v_pre, 2 * d, d, d, 2 * d, 0});   // u-half of v_pre
+      else u.push_back(UnpackSeg{gr->v_map, d, 0, d, 2 * d, 0});
       u.push_back(UnpackSeg{gr->w_gv, 2 * d, d, d, 3 * d, 0});
     } else {
       for (int hd = 0; hd < h; ++hd)
@@ -459,7 +463,9 @@ int dm_layer_bwd(const dm_config* c, const dm_packed* w, const void* x, const vo
   DM_REQUIRE(g->wq && g->wk && g->wv && g->wo && g->w_kctx && g->w_vctx && g->w_gk && g->w_gv && g->b_gk &&
                  g->b_gv && g->norm_ctx_w,
              DM_ERR_INVALID, "null gradient buffer");
-  DM_REQUIRE(!mult || (g->v_gate && g->b_vgate && g->v_map), DM_ERR_INVALID, "mult family needs v_gate/v_map grads");
+  DM_REQUIRE(!mult || c->ctx_mod == DM_CTX_FUSION || (g->v_gate && g->b_vgate && g->v_map), DM_ERR_INVALID,
+             "mult family needs v_gate/v_map grads");
+  DM_REQUIRE(c->ctx_mod != DM_CTX_FUSION || g->v_pre, DM_ERR_INVALID, "ctx_mod fusion needs the v_pre grad");
   DM_REQUIRE(w->attn_norm_w == nullptr || (g->attn_norm_w && L->xhat), DM_ERR_INVALID,
              "attn_norm needs its gradient buffer and bufs->xhat");
   if ((rc = dm_check_schedule(sched, n_cells, L->T))) return rc;

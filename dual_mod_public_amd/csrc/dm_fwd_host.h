@@ -109,7 +109,7 @@ void run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int 
               float* glogx, float* sig, hipStream_t s) {
   const int nseg = (c->ctx_mod == DM_CTX_LINEAR) ? 5 : 6;
   EpiProj<T, DH> epi{M, c->d, c->h, Tl, Tbuf, buf_t0, rope_t0, cos, sin, w->b_proj,
-                     qr, kraw, kself, vraw, glogx, sig};
+                     qr, kraw, kself, vraw, glogx, sig, c->ctx_mod == DM_CTX_FUSION};
   SrcRows<T> sa{xhat, c->d, M};
   SrcRows<T> sb{(const T*)w->w_proj, c->d, nseg * c->d};
   // bf16, whole 256-row / 256-column tiles: 256 x 256 blocks (four 128 x 128 wave tiles,

@@ -93,7 +93,7 @@ inline int check_cfg(const dm_config* c) {
   DM_REQUIRE(c->d <= RMS_MAXK, DM_ERR_UNSUPPORTED, "d_model %d > %d", c->d, RMS_MAXK);
   DM_REQUIRE(c->h <= MAX_HEADS && c->d / 32 <= MAX_ROWDOT, DM_ERR_UNSUPPORTED, "%d heads (at most %d)", c->h,
              MAX_HEADS);
-  DM_REQUIRE(c->ctx_mod >= 0 && c->ctx_mod <= 2, DM_ERR_UNSUPPORTED, "ctx_mod %d", c->ctx_mod);
+  DM_REQUIRE(c->ctx_mod >= 0 && c->ctx_mod <= DM_CTX_FUSION, DM_ERR_UNSUPPORTED, "ctx_mod %d", c->ctx_mod);
   DM_REQUIRE(c->kmod_vraw_heads >= 0 && c->kmod_vraw_heads <= c->h && c->kmod_mode >= DM_KMOD_RAW &&
                  c->kmod_mode <= DM_KMOD_GATED_NORM,
              DM_ERR_UNSUPPORTED, "kmod_vraw_heads %d / kmod_mode %d", c->kmod_vraw_heads, c->kmod_mode);

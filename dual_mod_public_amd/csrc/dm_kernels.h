@@ -169,6 +169,7 @@ template <typename T, int DH> struct EpiProj {
   const float* __restrict__ bias;   // [3d] fp32
   T* __restrict__ qr; T* __restrict__ kraw; T* __restrict__ kself; T* __restrict__ vraw;
   float* __restrict__ glogx; float* __restrict__ sig;
+  int fusion;    // ctx_mod fusion: segment 5 is v_pre's x-half, stored as the raw pre-activation
 
   // The wave tile spans whole heads (FN * 16 a multiple of DH); within each head
   // columns j and j + DH/32 of the tile are the RoPE pair (jj, jj + DH/2).
@@ -248,7 +249,7 @@ template <typename T, int DH> struct EpiProj {
 #pragma unroll
           for (int j = 0; j < FN; ++j) {
             const int col = c0 + 16 * j + lc;
-            sig[xrow * d + col] = sigmoidf_(acc[i][j][q] + bs[j]);
+            sig[xrow * d + col] = fusion ? acc[i][j][q] : sigmoidf_(acc[i][j][q] + bs[j]);
           }
         }
       }
@@ -551,7 +552,8 @@ static __global__ __launch_bounds__(64 * NW) void k_attend(AttendArgs<T> a) {
 //            g_k(u) cols 16q.., g_k(u) cols DH/2+16q..  -> blend, RoPE, K rows
 //   linear [2d, 4d) per head g, group q < DH/32: v_ctx cols 32q.. | g_v(u) cols 32q..
 //            -> blend, V rows
-//   mult   [2d, 3d) v_map(u) -> v_in = lam*u + sig * tanh(.)
+//   mult   [2d, 3d) v_map(u) -> v_in = lam*u + sig * tanh(.)  (fusion: v_pre u-half ->
+//          v_in = u + silu(px + .), px = v_pre x-half from the projection in the sig buffer)
 //          [3d, 4d) g_v(u)   -> fp32 scratch for GEMM 2
 // save != nullptr stores the raw GEMM outputs [rows, 4d] in this packed order.
 // ---------------------------------------------------------------------------
@@ -616,7 +618,7 @@ template <typename T, int DH> struct EpiSweep1 {
       const int c0 = n0 - 2 * d + lc0;
 #pragma unroll
       for (int k = 0; k < 4; ++k) fp[k] = sig + xrow * d + c0 + 16 * k;
-      if (ctx_mod == 1) {
+      if (ctx_mod == 1 || ctx_mod == 3) {   // mult_res, fusion: v_in has a u term
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           hp[k] = o + (long)m * d + c0 + 16 * k;
@@ -700,7 +702,9 @@ template <typename T, int DH> struct EpiSweep1 {
       for (int k = 0; k < 4; ++k) {
         unpackf4(pr.f[k], sg[k]);
         settle(sg[k]);
-        if (ctx_mod == 1) { unpack4<T>(pr.h[k], ov[k]); unpack4<T>(pr.h[4 + k], nw[k]); settle(ov[k]); settle(nw[k]); }
+        if (ctx_mod == 1 || ctx_mod == 3) {
+          unpack4<T>(pr.h[k], ov[k]); unpack4<T>(pr.h[4 + k], nw[k]); settle(ov[k]); settle(nw[k]);
+        }
       }
       if (save != nullptr) store_vec<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
       const int c0 = n0 - 2 * d + lc0;
@@ -709,8 +713,13 @@ template <typename T, int DH> struct EpiSweep1 {
         float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          v[i] = sg[k][i] * tanhf_(a[k][i]);
-          if (ctx_mod == 1) v[i] += lam * (ov[k][i] * sc * nw[k][i]);
+          if (ctx_mod == 3) {   // fusion (attention.py:341-342): u + silu(v_pre x-half + u-half)
+            const float z = sg[k][i] + a[k][i];
+            v[i] = ov[k][i] * sc * nw[k][i] + z * sigmoidf_(z);
+          } else {
+            v[i] = sg[k][i] * tanhf_(a[k][i]);
+            if (ctx_mod == 1) v[i] += lam * (ov[k][i] * sc * nw[k][i]);
+          }
         }
         st4<T>(vin + (long)m * d + c0 + 16 * k, v);
       }

@@ -25,7 +25,10 @@ int dm_pack_weights(const dm_config* c, const dm_params* p, const dm_packed* out
   DM_REQUIRE(p->wq && p->wk && p->wv && p->wo && p->w_kctx && p->w_vctx && p->w_gk && p->w_gv && p->b_gk &&
                  p->b_gv && p->norm_ctx_w,
              DM_ERR_INVALID, "null parameter pointer");
-  DM_REQUIRE(!mult || (p->v_gate && p->b_vgate && p->v_map), DM_ERR_INVALID, "mult family needs v_gate/v_map");
+  const bool fusion = c->ctx_mod == DM_CTX_FUSION;
+  DM_REQUIRE(!mult || fusion || (p->v_gate && p->b_vgate && p->v_map), DM_ERR_INVALID,
+             "mult family needs v_gate/v_map");
+  DM_REQUIRE(!fusion || p->v_pre, DM_ERR_INVALID, "ctx_mod fusion needs v_pre");
   DM_REQUIRE(out->w_proj && out->b_proj && out->w_sweep && out->norm_ctx_w && out->wo, DM_ERR_INVALID,
              "null packed output");
   DM_REQUIRE(!mult || out->w_vctx, DM_ERR_INVALID, "mult family needs packed w_vctx");
@@ -53,7 +56,8 @@ int dm_pack_weights(const dm_config* c, const dm_params* p, const dm_packed* out
   segs.push_back(PackSeg{p->wv, d, 0, d, 2 * d, 0});
   segs.push_back(PackSeg{p->w_gk, 2 * d, 0, d, 3 * d, 0});
   segs.push_back(PackSeg{p->w_gv, 2 * d, 0, d, 4 * d, 0});
-  if (mult) segs.push_back(PackSeg{p->v_gate, d, 0, d, 5 * d, 0});
+  if (fusion) segs.push_back(PackSeg{p->v_pre, 2 * d, 0, d, 5 * d, 0});   // x-half of v_pre
+  else if (mult) segs.push_back(PackSeg{p->v_gate, d, 0, d, 5 * d, 0});
   run(segs.data(), (int)segs.size(), out->w_proj);
   // w_sweep, in the 64-row groups of the sweep GEMM 1 epilogue
   segs.clear();
@@ -67,7 +71,8 @@ int dm_pack_weights(const dm_config* c, const dm_params* p, const dm_packed* out
       segs.push_back(PackSeg{rows_of(p->w_gk, 2 * d, r1), 2 * d, d, 16, base + 48, 0});
     }
   if (mult) {
-    segs.push_back(PackSeg{p->v_map, d, 0, d, 2 * d, 0});
+    if (fusion) segs.push_back(PackSeg{p->v_pre, 2 * d, d, d, 2 * d, 0});   // u-half of v_pre
+    else segs.push_back(PackSeg{p->v_map, d, 0, d, 2 * d, 0});
     segs.push_back(PackSeg{p->w_gv, 2 * d, d, d, 3 * d, 0});
   } else {
     for (int g = 0; g < h; ++g)
@@ -85,7 +90,7 @@ int dm_pack_weights(const dm_config* c, const dm_params* p, const dm_packed* out
     DM_HIP(hipMemcpyAsync(out->attn_norm_w, p->attn_norm_w, (size_t)d * e, hipMemcpyDeviceToDevice, s));
   if (mult) DM_HIP(hipMemcpyAsync(out->w_vctx, p->w_vctx, (size_t)d * d * e, hipMemcpyDeviceToDevice, s));
   // biases -> fp32
-  const void* bsrc[3] = {p->b_gk, p->b_gv, mult ? p->b_vgate : nullptr};
+  const void* bsrc[3] = {p->b_gk, p->b_gv, (mult && !fusion) ? p->b_vgate : nullptr};
   for (int i = 0; i < 3; ++i) {
     if (!bsrc[i]) continue;
     if (c->dtype == DM_BF16)

@@ -117,7 +117,9 @@ class PackedWeights:
                      ("w_gk", "w_gk.weight"), ("w_gv", "w_gv.weight"), ("b_gk", "w_gk.bias"),
                      ("b_gv", "w_gv.bias"), ("norm_ctx_w", "norm_ctx.weight")):
             setattr(p, f, t(n))
-        if cfg.ctx_mod != "linear":
+        if cfg.ctx_mod == "fusion":
+            p.v_pre = t("v_pre.weight")
+        elif cfg.ctx_mod != "linear":
             p.v_gate, p.b_vgate, p.v_map = t("v_gate.weight"), t("v_gate.bias"), t("v_map.weight")
         if attn_norm_w is None and "attn_norm.weight" in sd:
             attn_norm_w = sd["attn_norm.weight"]
@@ -178,7 +180,9 @@ class LayerGrads:
                   "w_kctx.weight": (d, d), "w_vctx.weight": (d, d), "w_gk.weight": (d, 2 * d),
                   "w_gv.weight": (d, 2 * d), "w_gk.bias": (d,), "w_gv.bias": (d,),
                   "norm_ctx.weight": (d,), "attn_norm.weight": (d,)}
-        if mult:
+        if cfg.ctx_mod == "fusion":
+            shapes["v_pre.weight"] = (d, 2 * d)
+        elif mult:
             shapes.update({"v_gate.weight": (d, d), "v_gate.bias": (d,), "v_map.weight": (d, d)})
         self.t = {k: torch.zeros(v, device=device, dtype=torch.float32) for k, v in shapes.items()}
 

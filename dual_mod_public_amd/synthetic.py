@@ -52,6 +52,8 @@ def param_specs(cfg, with_attn_norm=True):
             specs.append(("ctx_gain", (h,), "one"))
     if mod in ("mult", "mult_res"):
         specs += ctx("v_gate", bias=True) + ctx("v_map")
+    elif mod == "fusion":
+        specs.append(("v_pre.weight", (d, 2 * d), "w"))
     if cfg.enable_key_mod or cfg.enable_value_mod:
         specs.append(("norm_ctx.weight", (d,), "one"))
     if with_attn_norm:

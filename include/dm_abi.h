@@ -48,7 +48,7 @@ typedef enum dm_status {
 typedef enum dm_dtype { DM_F32 = 0, DM_BF16 = 1 } dm_dtype;
 
 /* ctx_mod values (models/dualmod/config.py:61, attention.py:338-360) */
-typedef enum dm_ctx_mod { DM_CTX_LINEAR = 0, DM_CTX_MULT_RES = 1, DM_CTX_MULT = 2 } dm_ctx_mod;
+typedef enum dm_ctx_mod { DM_CTX_LINEAR = 0, DM_CTX_MULT_RES = 1, DM_CTX_MULT = 2, DM_CTX_FUSION = 3 } dm_ctx_mod;
 
 /* Shape + knob set shared by every call (DualModConfig subset). */
 typedef struct dm_config {
@@ -84,15 +84,17 @@ typedef struct dm_params {
   const void* v_gate; const void* b_vgate; const void* v_map;        /* [d,d],[d],[d,d]; mult family */
   const void* norm_ctx_w;                                            /* [d] */
   const void* attn_norm_w;                                           /* [d] (layer entry points) */
+  const void* v_pre;                                                 /* [d, 2d]; ctx_mod fusion (attention.py:341-342) */
 } dm_params;
 
 /* Packed weights (written by dm_pack_weights, read by every compute call).
  * The *_t fields are transposed copies used by the backward (may be NULL for
  * forward-only use; dm_layer_bwd requires them).
- *   w_proj  [6d, d]  rows: wq | wk | wv | w_gk[:, :d] | w_gv[:, :d] | v_gate   (linear: 5d rows)
+ *   w_proj  [6d, d]  rows: wq | wk | wv | w_gk[:, :d] | w_gv[:, :d] | v_gate (fusion: v_pre[:, :d])
+ *                    (linear: 5d rows)
  *   b_proj  [3d] fp32: b_gk | b_gv | b_vgate
  *   w_sweep [4d, d]  per head g: [w_kctx rows of g ; w_gk[:, d:] rows of g] (2*dh rows each),
- *                    then mult family: v_map (d rows), w_gv[:, d:] (d rows);
+ *                    then mult family: v_map (fusion: v_pre[:, d:]) (d rows), w_gv[:, d:] (d rows);
  *                    linear: per head g: [w_vctx rows of g ; w_gv[:, d:] rows of g]
  *   w_vctx  [d, d]   (mult family), norm_ctx_w [d], attn_norm_w [d], wo [d, d]: copies */
 typedef struct dm_packed {
@@ -192,6 +194,7 @@ typedef struct dm_grads {
   float* v_gate; float* b_vgate; float* v_map;       /* [d, d], [d], [d, d] (mult family) */
   float* norm_ctx_w;                                 /* [d] */
   float* attn_norm_w;                                /* [d] (when w->attn_norm_w != NULL) */
+  float* v_pre;                                      /* [d, 2d] (fusion) */
 } dm_grads;
 size_t dm_layer_bwd_workspace_bytes(const dm_config* cfg, int32_t T, int32_t cache_T, int32_t max_sweeps);
 int dm_layer_bwd(const dm_config* cfg, const dm_packed* w, const void* x, const void* dy, void* dx,

@@ -146,7 +146,7 @@ def refine_kv(cfg, sd, xhat, o_cat, k_raw, v_raw):
     """attention.py:314-387 — ctx norm, ctx projections, gates, convex blend.
 
     All inputs [B,t,d]. Returns (k'', v'') UNROTATED. Supports the knob set
-    the HIP path honours: ctx_mod in {linear, mult, mult_res}, mult_res_lambda,
+    the HIP path honours: ctx_mod in {linear, mult, mult_res, fusion}, mult_res_lambda,
     k_ctx_norm, v_ctx_norm, kmod_vraw_heads (raw / gated_norm), v_clamp_tau.
     """
     if not (cfg_get(cfg, "enable_key_mod", True) or cfg_get(cfg, "enable_value_mod", True)):
@@ -171,6 +171,8 @@ def refine_kv(cfg, sd, xhat, o_cat, k_raw, v_raw):
             lam = cfg_get(cfg, "mult_res_lambda", 1.0)
             v_in = lam * u + torch.sigmoid(_hi(_lin(xhat, sd, "v_gate", bias=True))).to(u.dtype) \
                 * torch.tanh(_lin(u, sd, "v_map"))
+        elif mod == "fusion":                                          # :341-342
+            v_in = u + F.silu(_lin(g_in, sd, "v_pre"))
         elif mod == "linear":
             v_in = u                                                   # :359-360
         else:

@@ -2,7 +2,7 @@
 
 Run in the build container only (the reference is not on the GPU box):
 
-    python tests/golden/make_golden.py /path/to/reference
+    python tests/golden/make_golden.py /path/to/reference [--only case ...]
 
 The reference's own tests never exercise ctx_mod="mult_res" and hold no stored
 vectors, so the absolute numerics of refine_kv / sequential_scan / the Jacobi
@@ -42,6 +42,9 @@ CASES = {
     "c1_linear": dict(cfg=dict(d_model=256, n_heads=4, ctx_mod="linear"),
                       B=2, T=64, c=16, K=4, wseed=21, xseed=22, dtype="float32",
                       full=False),
+    # ctx_mod fusion (attention.py:341-342), v_pre live (random, not the reference's zero init)
+    "c1_fusion": dict(cfg=dict(d_model=256, n_heads=4, ctx_mod="fusion"),
+                      B=2, T=64, c=16, K=4, wseed=51, xseed=52, dtype="float32"),
     # knob combo: lambda leak, K-norm, V-ctx-norm, kmod raw heads, clamp
     "knobs_mult_res": dict(cfg=dict(d_model=128, n_heads=4, ctx_mod="mult_res",
                                     mult_res_lambda=0.97, k_ctx_norm="rms",
@@ -82,11 +85,19 @@ def _build_attn(R, kw, wseed, T):
     return ref_cfg, attn, sd
 
 
-def main(ref_root):
+def main(ref_root, only=None):
+    """Write every case, or with ``only`` just those cases, merged into the existing
+    fixture (its other arrays are kept as they are)."""
     torch.set_grad_enabled(False)
     R = _ref_modules(ref_root)
     out = {}
+    path = os.path.join(HERE, "dm_golden.npz")
+    if only:
+        with np.load(path) as old:
+            out = {k: old[k] for k in old.files}
     for name, case in CASES.items():
+        if only and name not in only:
+            continue
         B, T, c, K = case["B"], case["T"], case["c"], case["K"]
         ref_cfg, attn, sd = _build_attn(R, case["cfg"], case["wseed"], T)
         d = ref_cfg.d_model
@@ -117,6 +128,10 @@ def main(ref_root):
         out[f"{name}/decode_y"] = torch.cat(ys, dim=1).numpy().astype(np.float32)
         assert torch.allclose(cache["K"], K_rows, rtol=1e-4, atol=1e-5)
 
+    if only:
+        np.savez_compressed(path, **out)
+        print(f"wrote {path}: {len(out)} arrays ({', '.join(only)} rewritten)")
+        return
     # gradients through the exact scan: y = x + wo(scan(attn_norm(x)))
     g = GRAD_CASE
     B, T = g["B"], g["T"]
@@ -137,10 +152,13 @@ def main(ref_root):
         out[f"grad/{pname}"] = p.grad.numpy().astype(np.float32)
     out["grad/attn_norm.weight"] = norm.weight.grad.numpy().astype(np.float32)
 
-    path = os.path.join(HERE, "dm_golden.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path}: {len(out)} arrays, {os.path.getsize(path) / 1024:.0f} KiB")
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    # python tests/golden/make_golden.py [/path/to/reference] [--only case ...]
+    args = sys.argv[1:]
+    only = args[args.index("--only") + 1:] if "--only" in args else None
+    pos = [a for a in (args[:args.index("--only")] if "--only" in args else args)]
+    main(pos[0] if pos else "/root/reference", only)

@@ -89,7 +89,7 @@ def compare(name, dx, g, dx_ref, g_ref, tol, skip=()):
         assert v < tol, f"{k}: relerr {v:.3e} >= {tol}"
 
 
-@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "mult"])
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "mult", "fusion"])
 @pytest.mark.parametrize("c,k", [(16, 16), (16, 4), (64, 4), (8, 3)])
 def test_layer_grads_fp32(ctx_mod, c, k):
     """dm_layer_bwd vs autograd through the oracle (fp64), config-1 shape, fp32 storage."""
@@ -104,7 +104,7 @@ def test_layer_grads_fp32(ctx_mod, c, k):
     compare("fp32", dx, g, dx_ref, g_ref, FP32_TOL)
 
 
-@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear"])
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "fusion"])
 def test_layer_grads_tape_fp32(ctx_mod):
     """Forward-saved tape instead of recompute: grads vs autograd through the oracle."""
     say(f"bwd fp32 tape ctx_mod={ctx_mod}")
@@ -119,7 +119,7 @@ def test_layer_grads_tape_fp32(ctx_mod):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "mult"])
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "mult", "fusion"])
 @pytest.mark.parametrize("sched", [[(0, 16, 3), (16, 16, 1), (32, 7, 2), (39, 25, 4)], [(0, 64, 1)],
                                    [(0, 8, 8), (8, 56, 2)]])
 def test_tape_equals_recompute(dtype, ctx_mod, sched):
@@ -202,7 +202,7 @@ def test_grads_accumulate():
         assert relerr(g2[name], 2 * t) < 1e-6, name
 
 
-@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear"])
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "fusion"])
 def test_layer_grads_340m_shape_fp32(ctx_mod):
     """340M layer shape (d=1024, 16x64), c=64, K=4, T=256, fp32 storage (
     fp32 leg) vs autograd through the oracle in fp64."""

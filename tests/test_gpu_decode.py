@@ -24,7 +24,7 @@ def _gpu():
     L.load()
 
 
-@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear"])
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "fusion"])
 def test_decode_equals_teacher_forced_fp32(ctx_mod):
     say(f"decode fp32 teacher-forced ctx_mod={ctx_mod}")
     cfg = cfg_of(ctx_mod=ctx_mod)

@@ -53,7 +53,7 @@ def _cell(cfg, B, cache_T, sd, dtype):
     return cell
 
 
-@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "mult"])
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "mult", "fusion"])
 def test_layer_proj_matches_oracle(ctx_mod):
     say(f"layer_proj fp32 ctx_mod={ctx_mod}")
     cfg = cfg_of(ctx_mod=ctx_mod)
@@ -73,7 +73,9 @@ def test_layer_proj_matches_oracle(ctx_mod):
     gx = torch.cat([xhat @ sd["w_gk.weight"][:, :cfg.d_model].T + sd["w_gk.bias"],
                     xhat @ sd["w_gv.weight"][:, :cfg.d_model].T + sd["w_gv.bias"]], -1)
     assert relerr(bufs.glogx, gx) < 1e-6
-    if ctx_mod != "linear":
+    if ctx_mod == "fusion":   # the x-half pre-activation of v_pre (no bias, no activation)
+        assert relerr(bufs.sig, xhat @ sd["v_pre.weight"][:, :cfg.d_model].T) < 1e-6
+    elif ctx_mod != "linear":
         assert relerr(bufs.sig, torch.sigmoid(xhat @ sd["v_gate.weight"].T + sd["v_gate.bias"])) < 1e-6
 
 
@@ -93,7 +95,7 @@ def _hip_layer(cfg, sd, x, cos, sin, schedule, dtype, cache_T=None, fill=0.0):
     return ocat, K, V
 
 
-@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "mult"])
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "mult", "fusion"])
 @pytest.mark.parametrize("c", [16, 64])
 def test_cell_exact_equals_scan_fp32(ctx_mod, c):
     """K = c Jacobi cells == the exact sequential scan (config 1 shape)."""
@@ -108,7 +110,7 @@ def test_cell_exact_equals_scan_fp32(ctx_mod, c):
     assert relerr(V, V_ref) < FP32_TOL
 
 
-@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear"])
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "fusion"])
 @pytest.mark.parametrize("c,k", [(16, 4), (16, 1), (64, 4), (8, 3)])
 def test_cell_jacobi_equals_oracle_fp32(ctx_mod, c, k):
     """K < c: the HIP cells reproduce the chunked Jacobi result at the same K."""
@@ -186,7 +188,7 @@ def test_layer_fwd_matches_oracle_fp32():
     assert relerr(y - xd, (y_ref - x)) < FP32_TOL
 
 
-@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear"])
+@pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "fusion"])
 def test_bf16_340m_shape_within_tolerance(ctx_mod):
     """bf16 storage, fp32 accumulate, 340M layer shape (d=1024, 16x64), c=64, K=4,
     against the fp32/fp64 oracle's Jacobi result at the same K (T=256)."""

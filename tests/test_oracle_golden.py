@@ -151,3 +151,22 @@ def test_planted_mult_res_without_lambda_fails_pin(golden):
 def test_scale_is_inverse_sqrt_head_dim():
     # closed form for the score scale used everywhere (attention.py:96)
     assert math.isclose(1.0 / math.sqrt(64), 0.125)
+
+
+def test_fusion_pin_catches_planted_mistakes(golden, monkeypatch):
+    """ctx_mod fusion: v_in = u + silu(v_pre([xhat, u])). Dropping the u term or using
+    another activation must break the pin."""
+    case = CASES["c1_fusion"]
+    cfg, sd, cos, sin, x = _setup(case, torch.float64)
+    ref = _g(golden, "c1_fusion/scan_o")
+    with torch.no_grad():
+        assert relerr(O.sequential_scan(cfg, sd, x, cos, sin), ref) < TOL
+        monkeypatch.setattr(O.dm_oracle.F, "silu", torch.tanh)
+        assert relerr(O.sequential_scan(cfg, sd, x, cos, sin), ref) > 100 * TOL
+        monkeypatch.undo()
+        # v_pre = 0 reduces fusion to the linear ctx_mod (v_in = u): a different output
+        sd0 = dict(sd, **{"v_pre.weight": torch.zeros_like(sd["v_pre.weight"])})
+        o0 = O.sequential_scan(cfg, sd0, x, cos, sin)
+        lin = DualModConfig(**{**cfg.to_dict(), "ctx_mod": "linear"})
+        assert relerr(o0, O.sequential_scan(lin, sd0, x, cos, sin)) < 1e-12
+        assert relerr(o0, ref) > 100 * TOL
