@@ -26,7 +26,7 @@ class dm_config(ctypes.Structure):
     _fields_ = [("dtype", c_i32), ("B", c_i32), ("d", c_i32), ("h", c_i32), ("dh", c_i32),
                 ("ctx_mod", c_i32), ("mult_res_lambda", ctypes.c_float), ("rms_eps", ctypes.c_float),
                 ("local_window", c_i32), ("flags", c_i32), ("kmod_vraw_heads", c_i32),
-                ("kmod_mode", c_i32), ("reserved", c_i32 * 4)]
+                ("kmod_mode", c_i32), ("v_clamp_tau", ctypes.c_float), ("reserved", c_i32 * 3)]
 
 
 DM_FLAG_NO_RESIDUAL = 1
@@ -227,4 +227,5 @@ def make_config(cfg, B, dtype):
         c.kmod_mode = 2
     else:
         c.kmod_mode = 1 if getattr(cfg, "kmod_vraw_bound", "none") == "tanh" else 0
+    c.v_clamp_tau = float(getattr(cfg, "v_clamp_tau", 0.0) or 0.0)
     return c

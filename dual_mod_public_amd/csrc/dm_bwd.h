@@ -170,6 +170,20 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
   // raw v'' = v_raw (or tanh(v_raw)) takes no gate or v_ctx grad; gated_norm blends with
   // v_ctx = 0 (live gate, no v_ctx grad)
   const float gv1 = sigmoidf_(gxv1 + gvu1), gv2 = sigmoidf_(gxv2 + gvu2);
+  if (g.v_clamp_tau > 0.f) {
+    // VJP of the norm clamp v = v'' min(1, tau / ||v''||) (attention.py:389-402) over the
+    // head's DH / 2 lanes (consecutive, a whole group of each wave): outside the radius
+    // dv'' = (tau / n) (dv - v'' <v'', dv> / n^2), n = ||v''||, else dv'' = dv
+    const float p1 = value_blend(g, c1, gv1, vr1, vc1), p2 = value_blend(g, c2, gv2, vr2, vc2);
+    const float ss = group_sum<DH / 2>(p1 * p1 + p2 * p2);
+    const float dt = group_sum<DH / 2>(p1 * dv1 + p2 * dv2);
+    const float n = sqrtf(ss);
+    if (n > g.v_clamp_tau) {
+      const float sc = g.v_clamp_tau / n, k = dt / ss;
+      dv1 = sc * (dv1 - p1 * k);
+      dv2 = sc * (dv2 - p2 * k);
+    }
+  }
   float dlv1, dlv2, dvc1, dvc2, dvr1, dvr2;
   if (c1 < g.kmod_cols) {
     const bool gated = g.kmod_mode == DM_KMOD_GATED_NORM;

@@ -223,6 +223,7 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
     CellGeom g{B, cc, d, h, DH, pos0, pos0, T_, cache_T};
     g.kmod_cols = c->kmod_vraw_heads * DH;
     g.kmod_mode = c->kmod_mode;
+    g.v_clamp_tau = c->v_clamp_tau;
     // every sweep's state of the cell: saved by the forward, or an exact recompute
     CellSave<T> sv = ws.sv;
     const float* Mx;

@@ -208,6 +208,13 @@ DM_DEV float tanhf_(float x) {
 }
 
 // ---- wave reductions (full 64-lane and within 16-lane groups) ----------------
+// sum over aligned groups of G consecutive lanes (G a power of two <= 64)
+template <int G> DM_DEV float group_sum(float v) {
+  static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "lane group");
+#pragma unroll
+  for (int o = 1; o < G; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
 DM_DEV float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -158,6 +158,10 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
     else
       launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, c->d, c->d, e2, s, PROF_SWEEP2);
   }
+  // v'' entry-norm clamp of the refined value rows (v_clamp_tau > 0 only)
+  if (g.v_clamp_tau > 0.f)
+    hipLaunchKernelGGL((k_clamp_v<T, DH>), dim3(cdiv((long)N * c->h, 4)), dim3(256), 0, s, g, Vout, out_stride,
+                       out_row0, N, g.v_clamp_tau);
 }
 
 // Committed accumulator of a cell: split partials (merged by the first sweep's
@@ -185,6 +189,7 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
   CellGeom g{c->B, cc, c->d, c->h, DH, pos0, buf_t0, Tbuf, cache_T};
   g.kmod_cols = c->kmod_vraw_heads * DH;
   g.kmod_mode = c->kmod_mode;
+  g.v_clamp_tau = c->v_clamp_tau;
   const int BH = c->B * c->h;
   const int N = c->B * cc;
   const size_t NS = (size_t)N, d = c->d;   // per-sweep row stride of the saved arrays

@@ -97,6 +97,7 @@ inline int check_cfg(const dm_config* c) {
   DM_REQUIRE(c->kmod_vraw_heads >= 0 && c->kmod_vraw_heads <= c->h && c->kmod_mode >= DM_KMOD_RAW &&
                  c->kmod_mode <= DM_KMOD_GATED_NORM,
              DM_ERR_UNSUPPORTED, "kmod_vraw_heads %d / kmod_mode %d", c->kmod_vraw_heads, c->kmod_mode);
+  DM_REQUIRE(c->v_clamp_tau >= 0.f, DM_ERR_INVALID, "v_clamp_tau %g", (double)c->v_clamp_tau);
   DM_REQUIRE(c->local_window >= 0, DM_ERR_INVALID, "local_window %d", c->local_window);
   return DM_OK;
 }

@@ -268,7 +268,40 @@ struct CellGeom {
   int cache_T;     // T of the K/V cache
   int kmod_cols = 0;   // value columns [0, kmod_cols) belong to kmod heads (kmod_vraw_heads * dh)
   int kmod_mode = 0;   // dm_kmod_mode of those columns
+  float v_clamp_tau = 0.f;   // v'' norm clamp radius per (row, head), 0 = off
 };
+
+// ---------------------------------------------------------------------------
+// v'' entry-norm clamp (attention.py:389-402): v <- v min(1, tau / ||v||) over each
+// (row, head) of the refined value rows, in place, fp32 norm of the stored values.
+// One wave per (row, head); the rows are (b, h) at bh * stride, chunk row p at row0 + p.
+// ---------------------------------------------------------------------------
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_clamp_v(CellGeom g, T* __restrict__ V, long stride, int row0,
+                                                        int N, float tau) {
+  constexpr int PER = (DH + 63) / 64;   // elements per lane
+  const int lane = threadIdx.x & 63;
+  const long w = blockIdx.x * 4L + (threadIdx.x >> 6);   // (row m, head hd) = (w / h, w % h)
+  if (w >= (long)N * g.h) return;
+  const int m = (int)(w / g.h), hd = (int)(w - (long)m * g.h);
+  const int b = m / g.c, p = m - b * g.c;
+  T* row = V + ((long)b * g.h + hd) * stride + (long)(row0 + p) * DH;
+  float v[PER], ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < DH ? to_f(row[e]) : 0.f;
+    ss += v[i] * v[i];
+  }
+  const float n = sqrtf(wave_sum(ss));
+  if (n <= tau) return;   // wave-uniform: identity inside the radius
+  const float sc = tau / fmaxf(n, 1e-20f);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    if (e < DH) row[e] = from_f<T>(v[i] * sc);
+  }
+}
 
 // Value blend of column col (attention.py:362-384): v'' = g v_raw + (1 - g) v_ctx, except
 // for the kmod heads: raw (v_raw, or tanh(v_raw) with the tanh bound) or, gated_norm,

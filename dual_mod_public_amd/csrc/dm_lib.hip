@@ -324,6 +324,7 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
   CellGeom g{B, 1, d, h, DH, pos, 0, 1, a->tape_T};
   g.kmod_cols = c->kmod_vraw_heads * DH;
   g.kmod_mode = c->kmod_mode;
+  g.v_clamp_tau = c->v_clamp_tau;
   ProfScope pr(PROF_DEC_REFINE, s);
   run_refine<T, DH>(c, w, g, B, (const T*)a->o_cat, ws.ssq, (const T*)ws.kraw, (const T*)ws.vraw, ws.glogx,
                     ws.sig, cos, sin, (T*)a->K_tape, (T*)a->V_tape, (long)a->tape_T * DH, pos, (T*)ws.vin,

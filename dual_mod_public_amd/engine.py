@@ -54,8 +54,6 @@ def check_supported(cfg):
     for knob in ("attn_logn_ref",):
         if getattr(cfg, knob, 0):
             bad.append(f"{knob}={getattr(cfg, knob)}")
-    if getattr(cfg, "v_clamp_tau", 0.0):
-        bad.append(f"v_clamp_tau={cfg.v_clamp_tau}")
     if cfg.head_dim not in (64, 128):
         bad.append(f"head_dim={cfg.head_dim} (64 or 128)")
     if cfg.d_model % 128:

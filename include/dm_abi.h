@@ -61,7 +61,9 @@ typedef struct dm_config {
   int32_t flags;            /* DM_FLAG_* */
   int32_t kmod_vraw_heads;  /* config.py kmod_vraw_heads: the first n heads keep raw values */
   int32_t kmod_mode;        /* dm_kmod_mode (kmod_mode + kmod_vraw_bound), attention.py:362-384 */
-  int32_t reserved[4];
+  float v_clamp_tau;        /* config.py v_clamp_tau: v'' <- v'' min(1, tau / ||v''||) per (position,
+                               head), attention.py:389-402; 0 = off */
+  int32_t reserved[3];
 } dm_config;
 
 /* kmod heads (value columns of heads < kmod_vraw_heads), attention.py:362-384:

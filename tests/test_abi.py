@@ -74,7 +74,7 @@ def test_workspace_query():
 
 def test_unsupported_knobs_raise():
     from dual_mod_public_amd.engine import check_supported
-    for kw in (dict(k_ctx_norm="rms"), dict(v_clamp_tau=1.0), dict(v_ctx_norm="rms"),
+    for kw in (dict(k_ctx_norm="rms"), dict(v_norm="rms"), dict(v_ctx_norm="rms"),
                dict(gate_type_v="independent"), dict(ctx_mod="vmlp"), dict(attn_logn_ref=64)):
         cfg = DualModConfig(d_model=256, n_heads=4, **kw)
         with pytest.raises(NotImplementedError):
@@ -85,6 +85,7 @@ def test_unsupported_knobs_raise():
                dict(kmod_vraw_heads=1, kmod_mode="gated_norm"), dict(gate_rank=8, ctx_rank=16)):
         check_supported(DualModConfig(d_model=256, n_heads=4, ctx_mod="mult_res", **kw))
     check_supported(DualModConfig(d_model=256, n_heads=4, ctx_mod="fusion"))
+    check_supported(DualModConfig(d_model=256, n_heads=4, ctx_mod="mult_res", v_clamp_tau=1.0))
 
 
 def test_kmod_config_fields():
