@@ -30,6 +30,8 @@ class dm_config(ctypes.Structure):
 
 
 DM_FLAG_NO_RESIDUAL = 1
+DM_FLAG_FUSED_ATTEND = 2
+DM_FLAG_UNFUSED_ATTEND = 4
 
 # dm_grads fields and the reference parameter each one accumulates
 GRAD_FIELDS = (("wq", "wq.weight"), ("wk", "wk.weight"), ("wv", "wv.weight"), ("wo", "wo.weight"),

@@ -90,6 +90,30 @@ DM_DEV void load_kv(const T* __restrict__ Kg, const T* __restrict__ Vg, long row
   }
 }
 
+// K rows only (the V rows are already in LDS)
+template <typename T, int DH, int NT = 256>
+DM_DEV void load_k(const T* __restrict__ Kg, long row_stride, int nvalid, KVRegs<T, DH, NT>& r) {
+  using R = KVRegs<T, DH, NT>;
+  r.nvalid = nvalid;
+#pragma unroll
+  for (int i = 0; i < R::NV; ++i) {
+    const int v = threadIdx.x + NT * i;
+    const int k = v / R::VPR, c0 = (v % R::VPR) * AttnCfg<T, DH>::VEC;
+    r.k[i] = *reinterpret_cast<const uint4*>(Kg + (long)(k < nvalid ? k : 0) * row_stride + c0);
+  }
+}
+template <typename T, int DH, int NT = 256>
+DM_DEV void store_k(const KVRegs<T, DH, NT>& r, T* Ks) {
+  using C = AttnCfg<T, DH>;
+  using R = KVRegs<T, DH, NT>;
+#pragma unroll
+  for (int i = 0; i < R::NV; ++i) {
+    const int v = threadIdx.x + NT * i;
+    const int k = v / R::VPR, c0 = (v % R::VPR) * C::VEC;
+    *reinterpret_cast<uint4*>(Ks + k * C::LDK + c0) = keep_if(r.k[i], k < r.nvalid);
+  }
+}
+
 // K rows -> Ks [key][dh], V rows -> Vs [key][dh] (P V reads V through the
 // transposed-view fragment loads).
 template <typename T, int DH, int NT = 256>

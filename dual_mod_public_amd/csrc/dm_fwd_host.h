@@ -142,13 +142,25 @@ template <typename T, int DH>
 void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N, const T* o, const float* ssq,
                 const T* kraw, const T* vraw, const float* glogx, const float* sig, const float* cos,
                 const float* sin, T* Kout, T* Vout, long out_stride, int out_row0, T* vin, float* gvu,
-                T* save1, T* save2, hipStream_t s) {
+                T* save1, T* save2, hipStream_t s, const AttendArgs<T>* next_attend = nullptr) {
   const T* normw = (const T*)w->norm_ctx_w;
   SrcRowsRs<T> sa{o, c->d, N, ssq, c->h, 1.0f / (float)c->d, c->rms_eps};
   SrcRows<T> sb{(const T*)w->w_sweep, c->d, 4 * c->d};
   EpiSweep1<T, DH> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
                       Kout, Vout, out_stride, out_row0, vin, gvu, save1};
   launch_gemm_auto<T, 64, 64, 2, 2, SW1_STAGES, 4>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
+  if (c->ctx_mod != DM_CTX_LINEAR && next_attend != nullptr) {
+    // GEMM 2 fused with the next sweep's attention (64-row cells; the clamp is in its epilogue)
+    SrcRows<T> av{vin, c->d, N};
+    SrcRows<T> bv{(const T*)w->w_vctx, c->d, c->d};
+    EpiSweep2Head<T, DH> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2};
+    uint64_t* ts;
+    const int idx = prof_launch_begin(PROF_SWEEP2, s, true, ts);
+    hipLaunchKernelGGL((k_sweep2_attend<T, DH>), dim3(c->h, N / CMAX), dim3(256), 0, s, av, bv, c->d, e2,
+                       *next_attend, ts);
+    prof_launch_end(idx, s);
+    return;
+  }
   if (c->ctx_mod != DM_CTX_LINEAR) {
     SrcRows<T> av{vin, c->d, N};
     SrcRows<T> bv{(const T*)w->w_vctx, c->d, c->d};
@@ -202,13 +214,31 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
   const long cache_stride = (long)cache_T * DH, ws_stride = (long)CMAX * DH;
   const size_t slot = (size_t)BH * CMAX * DH;
 
-  for (int sw = 0; sw < n_sweeps; ++sw) {
-    const bool last = sw == n_sweeps - 1;
-    // intra rows read by this sweep
-    const T* Kin; const T* Vin; long in_stride; int in_row0;
+  // sweep s + 1's attention runs inside sweep s's GEMM 2 launch (mult family, whole 64-row
+  // chunks) when B*h gives that kernel enough blocks, or when forced by the flags
+  const bool fuse = c->ctx_mod != DM_CTX_LINEAR && cc == CMAX && !(c->flags & DM_FLAG_UNFUSED_ATTEND) &&
+                    ((c->flags & DM_FLAG_FUSED_ATTEND) || BH >= 128);
+  // intra rows read by sweep sw (= the rows written by sweep sw - 1)
+  auto rows_in = [&](int sw, const T*& Kin, const T*& Vin, long& in_stride, int& in_row0) {
     if (sw == 0) { Kin = kself; Vin = vraw; in_stride = (long)Tbuf * DH; in_row0 = buf_t0; }
     else if (sv) { Kin = sv->Kin + sw * slot; Vin = sv->Vin + sw * slot; in_stride = ws_stride; in_row0 = 0; }
     else { Kin = Kc; Vin = Vc; in_stride = cache_stride; in_row0 = pos0; }
+  };
+  auto attend_args = [&](int sw) {
+    const bool last = sw == n_sweeps - 1;
+    const T* Kin; const T* Vin; long in_stride; int in_row0;
+    rows_in(sw, Kin, Vin, in_stride, in_row0);
+    T* o = sv ? sv->o + sw * NS * d : (T*)ws.o;
+    float* ssq = sv ? sv->ssq + sw * NS * c->h : ws.ssq;
+    return AttendArgs<T>{g, qr, kself, vraw, Kin, Vin, in_stride, in_row0,
+                         sw == 0 ? nsplit : (nsplit > 0 ? 1 : 0), ws.Ap, ws.Zp, ws.Mp, ws.A, ws.Z, ws.M,
+                         scale, o, ssq, last ? ocat : nullptr, last ? o_last : nullptr,
+                         sv ? sv->stat_m + sw * (size_t)BH * CMAX : nullptr,
+                         sv ? sv->stat_z + sw * (size_t)BH * CMAX : nullptr};
+  };
+
+  for (int sw = 0; sw < n_sweeps; ++sw) {
+    const bool last = sw == n_sweeps - 1;
     // rows written by this sweep's refine
     T* Kout; T* Vout; long out_stride; int out_row0;
     if (sv && !(last && sv->last_to_cache)) { Kout = sv->Kin + (sw + 1) * slot; Vout = sv->Vin + (sw + 1) * slot; out_stride = ws_stride; out_row0 = 0; }
@@ -216,19 +246,18 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
 
     T* o = sv ? sv->o + sw * NS * d : (T*)ws.o;
     float* ssq = sv ? sv->ssq + sw * NS * c->h : ws.ssq;
-    AttendArgs<T> aa{g, qr, kself, vraw, Kin, Vin, in_stride, in_row0,
-                     sw == 0 ? nsplit : (nsplit > 0 ? 1 : 0), ws.Ap, ws.Zp, ws.Mp, ws.A, ws.Z, ws.M,
-                     scale, o, ssq, last ? ocat : nullptr, last ? o_last : nullptr,
-                     sv ? sv->stat_m + sw * (size_t)BH * CMAX : nullptr,
-                     sv ? sv->stat_z + sw * (size_t)BH * CMAX : nullptr};
-    // 16-row waves; the (b, h) blocks split by query rows until there are >= 256 blocks
-    if (BH >= 256) launch_k(PROF_ATTEND, k_attend<T, DH, 4>, dim3(BH, 1), dim3(256), 0, s, aa);
-    else if (BH >= 128) launch_k(PROF_ATTEND, k_attend<T, DH, 2>, dim3(BH, 2), dim3(128), 0, s, aa);
-    else launch_k(PROF_ATTEND, k_attend<T, DH, 1>, dim3(BH, 4), dim3(64), 0, s, aa);
+    if (sw == 0 || !fuse) {   // else the previous sweep's GEMM 2 launch ran it
+      const AttendArgs<T> aa = attend_args(sw);
+      // 16-row waves; the (b, h) blocks split by query rows until there are >= 256 blocks
+      if (BH >= 256) launch_k(PROF_ATTEND, k_attend<T, DH, 4>, dim3(BH, 1), dim3(256), 0, s, aa);
+      else if (BH >= 128) launch_k(PROF_ATTEND, k_attend<T, DH, 2>, dim3(BH, 2), dim3(128), 0, s, aa);
+      else launch_k(PROF_ATTEND, k_attend<T, DH, 1>, dim3(BH, 4), dim3(64), 0, s, aa);
+    }
     T* vin = sv ? sv->vin + sw * NS * d : (T*)ws.vin;
+    const AttendArgs<T> next = attend_args(last ? sw : sw + 1);
     run_refine<T, DH>(c, w, g, N, o, ssq, kraw, vraw, L->glogx, L->sig, cos, sin, Kout, Vout, out_stride,
                       out_row0, vin, ws.gvu, sv ? sv->save1 + sw * NS * 4 * d : nullptr,
-                      sv ? sv->save2 + sw * NS * d : nullptr, s);
+                      sv ? sv->save2 + sw * NS * d : nullptr, s, (fuse && !last) ? &next : nullptr);
   }
 }
 

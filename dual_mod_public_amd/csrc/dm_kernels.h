@@ -415,30 +415,30 @@ template <typename T> struct AttendArgs {
   float* stat_z;    // [B*h, c] final row sum (or nullptr)
 };
 
-// NW waves per block, 16 query rows per wave: block y takes rows [16 NW y, 16 NW (y + 1)),
-// so a (b, h) spreads over 4 / NW blocks (more blocks when B*h alone underfills the GPU).
-template <typename T, int DH, int NW>
-static __global__ __launch_bounds__(64 * NW) void k_attend(AttendArgs<T> a) {
+// The attention of query rows [q0, q0 + 16 NW) of (b, h) = bh, NW waves of 16 rows. With
+// V_STAGED the block has already written the intra V rows [0, 16 NW) into Vs (the fused
+// GEMM 2 + attention kernel); otherwise K and V are both loaded here.
+template <typename T, int DH, int NW, bool V_STAGED>
+DM_DEV void attend_rows(const AttendArgs<T>& a, int bh, int q0, T* lds) {
   using C = AttnCfg<T, DH>;
-  __shared__ __attribute__((aligned(16))) T lds[C::LDS_ELEMS];
   T* Ks = lds;
   T* Vs = Ks + C::KT * C::LDK;
   T* Ps = Vs + C::KT * C::LDK;
   const CellGeom& g = a.g;
-  const int bh = blockIdx.x;
   const int b = bh / g.h, hh = bh - b * g.h;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g4 = lane >> 4, col = lane & 15;
-  const int q0 = 16 * NW * (int)blockIdx.y;   // the block's first query row
-  if (q0 >= g.c) return;                       // uniform: no rows in this block
   const int wq = q0 + 16 * wave;               // the wave's first query row
   const int qrow = wq + col;
   const long lrow0 = (long)bh * g.Tbuf + g.buf_t0;   // layer-buffer row of chunk row 0
   const int BH = g.B * g.h;
 
   KVRegs<T, DH, 64 * NW> kv;   // keys < the block's last row (strict lower)
-  load_kv<T, DH, 64 * NW>(a.Kin + (long)bh * a.in_stride + (long)a.in_row0 * DH,
-                          a.Vin + (long)bh * a.in_stride + (long)a.in_row0 * DH, DH, min(g.c, q0 + 16 * NW), kv);
+  if constexpr (V_STAGED)
+    load_k<T, DH, 64 * NW>(a.Kin + (long)bh * a.in_stride + (long)a.in_row0 * DH, DH, min(g.c, q0 + 16 * NW), kv);
+  else
+    load_kv<T, DH, 64 * NW>(a.Kin + (long)bh * a.in_stride + (long)a.in_row0 * DH,
+                            a.Vin + (long)bh * a.in_stride + (long)a.in_row0 * DH, DH, min(g.c, q0 + 16 * NW), kv);
   typename Mfma<T>::frag qf[C::NKS];
   load_q_frags<T, DH>(a.qr + (lrow0 + qrow) * DH, qrow < g.c, qf);
   FlashState<T, DH> st;
@@ -522,7 +522,8 @@ static __global__ __launch_bounds__(64 * NW) void k_attend(AttendArgs<T> a) {
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt) vself[r][dt] = to_f(vp[col + 16 * dt]);
   }
-  store_kv<T, DH, 64 * NW>(kv, Ks, Vs);
+  if constexpr (V_STAGED) store_k<T, DH, 64 * NW>(kv, Ks);
+  else store_kv<T, DH, 64 * NW>(kv, Ks, Vs);
   __syncthreads();
   flash_tile<T, DH>(qf, Ks, Vs, Ps + wave * 16 * C::LDP, a.scale, KeyStrictLower{q0}, st);
 
@@ -575,6 +576,16 @@ static __global__ __launch_bounds__(64 * NW) void k_attend(AttendArgs<T> a) {
       }
     }
   }
+}
+
+// NW waves per block, 16 query rows per wave: block y takes rows [16 NW y, 16 NW (y + 1)),
+// so a (b, h) spreads over 4 / NW blocks (more blocks when B*h alone underfills the GPU).
+template <typename T, int DH, int NW>
+static __global__ __launch_bounds__(64 * NW) void k_attend(AttendArgs<T> a) {
+  __shared__ __attribute__((aligned(16))) T lds[AttnCfg<T, DH>::LDS_ELEMS];
+  const int q0 = 16 * NW * (int)blockIdx.y;   // the block's first query row
+  if (q0 >= a.g.c) return;                     // uniform: no rows in this block
+  attend_rows<T, DH, NW, false>(a, blockIdx.x, q0, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -824,6 +835,127 @@ template <typename T, int DH> struct EpiSweep2 {
     if (save2 != nullptr) store_vec<T, 8>(save2 + (long)m * g.d + col, a);
   }
 };
+
+
+// ---------------------------------------------------------------------------
+// Sweep GEMM 2 of sweep s fused with the attention of sweep s + 1 (cells of c = 64 rows).
+// Block (hh, b) computes v_ctx = v_in . W_vctx^T for the 64 rows of batch b (its whole
+// chunk) and head hh's DH columns, blends the refined V rows (the value blend of
+// EpiSweep2, plus the norm clamp: the block holds whole heads) into Vout and into the
+// attention's LDS V tile, then runs sweep s + 1's attention of (b, hh): its intra V rows
+// are exactly the rows this block wrote, its K rows came from sweep s's GEMM 1 (the
+// previous launch). Nothing crosses blocks, one launch per sweep less.
+// Epilogue layout: thread t owns row t / 4 and columns (t % 4) DH / 4 .. + DH / 4 - 1.
+// ---------------------------------------------------------------------------
+template <typename T, int DH> struct EpiSweep2Head {
+  static constexpr int CW = DH / 4;   // columns per thread
+  CellGeom g;
+  int M;
+  const T* __restrict__ vraw;
+  const float* __restrict__ glogx;
+  const float* __restrict__ gvu;
+  T* __restrict__ Vout;
+  long out_stride; int out_row0;
+  T* __restrict__ save2;
+  struct TilePre {
+    floatx4 gx[CW / 4], gu[CW / 4];
+    Raw8<T> vr[CW / 8];
+  };
+  DM_DEV TilePre tile_prefetch(int m0, int n0) const {
+    const int r = threadIdx.x >> 2, e0 = CW * (threadIdx.x & 3), col = n0 + e0;
+    const int m = min(m0 + r, M - 1);
+    const int b = m / g.c, t = g.buf_t0 + m - b * g.c;
+    const int hd = n0 / DH;
+    const float* gx = glogx + ((long)b * g.Tbuf + t) * 2 * g.d + g.d + col;
+    const float* gu = gvu + (long)m * g.d + col;
+    const T* vr = vraw + (((long)b * g.h + hd) * g.Tbuf + t) * DH + e0;
+    TilePre pr;
+#pragma unroll
+    for (int k = 0; k < CW / 4; ++k) {
+      pr.gx[k] = ld_global<floatx4>(gx + 4 * k);
+      pr.gu[k] = ld_global<floatx4>(gu + 4 * k);
+    }
+#pragma unroll
+    for (int k = 0; k < CW / 8; ++k) pr.vr[k] = ld8_global(vr + 8 * k);
+    return pr;
+  }
+  // v'' of the thread's columns into Vout (and save2 = raw v_ctx) and into vs [64][ldv]
+  template <int LDT>
+  DM_DEV void apply(const float* tile, int m0, int n0, const TilePre& pr, T* vs, int ldv) const {
+    const int r = threadIdx.x >> 2, e0 = CW * (threadIdx.x & 3), col = n0 + e0;
+    const int m = min(m0 + r, M - 1);
+    float a[CW], gx[CW], gu[CW], vr[CW], v[CW];
+#pragma unroll
+    for (int k = 0; k < CW / 4; ++k) {
+      unpackf4(*reinterpret_cast<const floatx4*>(tile + r * LDT + e0 + 4 * k), a + 4 * k);
+      unpackf4(pr.gx[k], gx + 4 * k);
+      unpackf4(pr.gu[k], gu + 4 * k);
+    }
+#pragma unroll
+    for (int k = 0; k < CW / 8; ++k) unpack8<T>(pr.vr[k], vr + 8 * k);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < CW; ++i) {
+      v[i] = to_f(from_f<T>(value_blend(g, col + i, sigmoidf_(gx[i] + gu[i]), vr[i], a[i])));   // the stored value
+      ss += v[i] * v[i];
+    }
+    if (g.v_clamp_tau > 0.f) {   // norm clamp of the stored row (as k_clamp_v): the row's 4 threads
+      ss += __shfl_xor(ss, 1, 64);
+      ss += __shfl_xor(ss, 2, 64);
+      const float n = sqrtf(ss);
+      if (n > g.v_clamp_tau) {
+        const float sc = g.v_clamp_tau / fmaxf(n, 1e-20f);
+#pragma unroll
+        for (int i = 0; i < CW; ++i) v[i] = to_f(from_f<T>(v[i] * sc));
+      }
+    }
+    settle(gx); settle(gu); settle(vr);   // all loads before any store
+    store_vec<T, CW>(vs + r * ldv + e0, v);
+    if (m0 + r >= M) return;
+    const int b = m / g.c, p = m - b * g.c;
+    store_vec<T, CW>(Vout + ((long)b * g.h + n0 / DH) * out_stride + (long)(out_row0 + p) * DH + e0, v);
+    if (save2 != nullptr) store_vec<T, CW>(save2 + (long)m * g.d + col, a);
+  }
+};
+
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_sweep2_attend(SrcRows<T> sa, SrcRows<T> sb, int K,
+                                                              EpiSweep2Head<T, DH> epi, AttendArgs<T> aa,
+                                                              uint64_t* prof_ts) {
+  const uint64_t t0 = prof_begin(prof_ts);
+  constexpr int D = sizeof(T) == 2 ? -3 : 4;
+  constexpr int LDT = DH + 4;
+  using WT = WaveTile<64, DH, 2, 2>;
+  using C = AttnCfg<T, DH>;
+  __shared__ __attribute__((aligned(1024))) char smem[gemm_lds_bytes<T, 64, DH, D, false>()];
+  __shared__ __attribute__((aligned(16))) T alds[C::LDS_ELEMS];
+  static_assert(64 * LDT * 4 <= gemm_stage_bytes<T, 64, DH, D>(), "output tile fits the stages");
+  const int hh = blockIdx.x, b = blockIdx.y;
+  const int m0 = b * 64, n0 = hh * DH;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  floatx4 acc[WT::FM][WT::FN];
+#pragma unroll
+  for (int i = 0; i < WT::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < WT::FN; ++j) acc[i][j] = zero4();
+  const typename EpiSweep2Head<T, DH>::TilePre pre = epi.tile_prefetch(m0, n0);
+  gemm_kloop<T, 64, DH, 2, 2, D>(sa, sb, K, m0, n0, smem, acc, 0);
+  // the k-loop ends with a barrier: the stages are free for the output tile
+  float* tile = reinterpret_cast<float*>(smem);
+  const int r0 = (wave / 2) * WT::TM, c0 = (wave % 2) * WT::TN;
+#pragma unroll
+  for (int i = 0; i < WT::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < WT::FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        tile[(r0 + 16 * i + 4 * (lane >> 4) + q) * LDT + c0 + 16 * j + (lane & 15)] = acc[i][j][q];
+  __syncthreads();
+  epi.template apply<LDT>(tile, m0, n0, pre, alds + C::KT * C::LDK, C::LDK);
+  __syncthreads();   // the V tile is complete
+  attend_rows<T, DH, 4, true>(aa, b * aa.g.h + hh, 0, alds);
+  prof_end(prof_ts, t0);
+}
 
 // y = acc (+ x): the W_O projection with the block residual, or plain nn.Linear
 template <typename T> struct EpiResidual {

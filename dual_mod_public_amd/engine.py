@@ -208,12 +208,16 @@ class HipSweepCell:
     buffers, K/V caches (append-only, rows [0, pos0) committed) and outputs.
     """
 
-    def __init__(self, cfg, B, cache_T, device="cuda", dtype=torch.bfloat16):
+    def __init__(self, cfg, B, cache_T, device="cuda", dtype=torch.bfloat16, fused_attend=None):
+        """fused_attend: None lets the library run sweep s + 1's attention inside sweep s's
+        GEMM 2 launch when it pays (64-row cells, B*h >= 128); True / False force it."""
         check_supported(cfg)
         self.cfg, self.B, self.cache_T = cfg, B, cache_T
         self.device, self.dtype = torch.device(device), dtype
         self.w = PackedWeights(cfg, self.device, dtype)
+        self.fuse_flags = {None: 0, True: L.DM_FLAG_FUSED_ATTEND, False: L.DM_FLAG_UNFUSED_ATTEND}[fused_attend]
         self.conf = L.make_config(cfg, B, dtype)
+        self.conf.flags = self.fuse_flags
         nbytes = L.lib().dm_cell_workspace_bytes(ctypes.byref(self.conf), cache_T)
         if nbytes == 0:
             raise L.DMError("dm_cell_workspace_bytes rejected the configuration")
@@ -255,7 +259,7 @@ class HipSweepCell:
 
     def _conf(self, residual):
         c = L.make_config(self.cfg, self.B, self.dtype)
-        c.flags = 0 if residual else L.DM_FLAG_NO_RESIDUAL
+        c.flags = (0 if residual else L.DM_FLAG_NO_RESIDUAL) | self.fuse_flags
         return c
 
     def tape_bytes(self, schedule):

@@ -75,6 +75,11 @@ typedef enum dm_kmod_mode { DM_KMOD_RAW = 0, DM_KMOD_RAW_TANH = 1, DM_KMOD_GATED
  * attention sublayer, models/dualmod/model.py:123-124); with it y = W_O . DM(norm(x))
  * (DualModAttention.forward, attention.py:438-447). */
 #define DM_FLAG_NO_RESIDUAL 1
+/* Forward sweeps of 64-row cells run sweep s + 1's attention inside sweep s's GEMM 2 launch (one
+ * launch per sweep less) when B*h >= 128 (enough blocks); these force it on / off (results agree
+ * to rounding). */
+#define DM_FLAG_FUSED_ATTEND 2
+#define DM_FLAG_UNFUSED_ATTEND 4
 
 /* The reference parameters of one DualModAttention layer (attention.py:100-202),
  * each as stored by torch (nn.Linear weight = [out, in]). Storage dtype unless noted. */
