@@ -76,6 +76,7 @@ template <typename T> struct SrcRowsRs {
     float v[MAX_HEADS / 2];   // the loaded partials (summed in prepare_store, so no wait here)
   };
   // 256 / R adjacent threads per row split its nparts (<= MAX_HEADS) partial sums
+  template <int R> static constexpr int prepare_loads() { return MAX_HEADS / (256 / R); }
   template <int R> DM_DEV Pre prepare_load(int r0, int) const {
     constexpr int P = 256 / R, Q = MAX_HEADS / P;
     static_assert(256 % R == 0 && P >= 2 && P <= 8, "rows per block");
@@ -134,6 +135,12 @@ template <typename T> struct PrepOf<SrcRowsRs<T>> { using type = typename SrcRow
 template <class E, class = void> struct has_tile_epi { static constexpr bool value = false; };
 template <class E> struct has_tile_epi<E, std::void_t<typename E::TilePre>> { static constexpr bool value = true; };
 template <class E, class = void> struct tile_rows_of { static constexpr int value = 1 << 30; };
+// An EPI with a static LATE_GATHERS = the exact number of vector-memory load instructions its
+// tile_prefetch issues gets them issued late in the direct-to-LDS k-loop (gemm_mainloop_dma).
+template <class E, class = void> struct late_gathers_of { static constexpr int value = 0; };
+template <class E> struct late_gathers_of<E, std::void_t<decltype(E::LATE_GATHERS)>> {
+  static constexpr int value = E::LATE_GATHERS;
+};
 template <class E> struct tile_rows_of<E, std::void_t<decltype(E::TILE_ROWS)>> { static constexpr int value = E::TILE_ROWS; };
 
 // k-rows per stage of the K-major direct-to-LDS k-loop: 32 for 256 x 256 blocks with
@@ -315,10 +322,18 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // l%8), each wave issues BM/32 + BN/32 of them per k-tile. Per k-tile: wait for
 // this wave's loads of tile kt (vmcnt), barrier (everyone's landed, and stage
 // (kt-1)%S is free), issue tile kt+S-1 into it, compute on stage kt%S.
-template <typename T, int BM, int BN, int WM, int WN, int S, class SA, class SB>
+struct NoLate {
+  DM_DEV void operator()() const {}
+};
+
+// G > 0: late(), which issues exactly G vector-memory loads (the epilogue's gathers), is
+// called right after the last stage is issued, and the waits that follow leave those G
+// loads outstanding (vector loads complete in issue order, so they would otherwise gate
+// the next stage's wait); before the k-loop they would gate its first wait instead.
+template <typename T, int BM, int BN, int WM, int WN, int S, int G = 0, class SA, class SB, class LATE = NoLate>
 DM_DEV void gemm_mainloop_dma(const SA& sa, const SB& sb, int K, int m0, int n0, char* smem,
                               floatx4 (&acc)[WaveTile<BM, BN, WM, WN>::FM][WaveTile<BM, BN, WM, WN>::FN],
-                              int kbase) {
+                              int kbase, const LATE& late = LATE{}) {
   static_assert(sizeof(T) == 2 && !SA::KMAJOR && !SB::KMAJOR, "direct-to-LDS path: bf16, K-contiguous");
   static_assert(S >= 2 && BM % 32 == 0 && BN % 32 == 0, "stages / tile rows");
   using MF = Mfma<T>;
@@ -370,26 +385,46 @@ DM_DEV void gemm_mainloop_dma(const SA& sa, const SB& sb, int K, int m0, int n0,
     }
   };
 
+  static_assert(G >= 0 && 2 * L + G < 64, "vmcnt range");
   const int nk = K / 64;
 #pragma unroll
   for (int st = 0; st < S - 1; ++st)
     if (st < nk) issue(st, st);
-  for (int kt = 0; kt < nk; ++kt) {
+  // one k-tile: wait for this wave's loads of tile kt (lg: the G late loads, issued after
+  // every stage, may stay outstanding), barrier, issue tile kt + S - 1, compute on tile kt
+  auto step = [&](int kt, bool lg, bool with_late) {
     // tiles issued after kt and possibly outstanding: min(S-2, nk-1-kt)
     const int after = min(S - 2, nk - 1 - kt);
     if constexpr (S >= 4) {
-      if (after >= 2) wait_vm_lgkm0<2 * L>();
-      else if (after == 1) wait_vm_lgkm0<L>();
-      else wait_vm_lgkm0<0>();
+      if (after >= 2) { if (lg) wait_vm_lgkm0<2 * L + G>(); else wait_vm_lgkm0<2 * L>(); }
+      else if (after == 1) { if (lg) wait_vm_lgkm0<L + G>(); else wait_vm_lgkm0<L>(); }
+      else { if (lg) wait_vm_lgkm0<G>(); else wait_vm_lgkm0<0>(); }
     } else if constexpr (S == 3) {
-      if (after >= 1) wait_vm_lgkm0<L>();
-      else wait_vm_lgkm0<0>();
+      if (after >= 1) { if (lg) wait_vm_lgkm0<L + G>(); else wait_vm_lgkm0<L>(); }
+      else { if (lg) wait_vm_lgkm0<G>(); else wait_vm_lgkm0<0>(); }
     } else {
-      wait_vm_lgkm0<0>();
+      if (lg) wait_vm_lgkm0<G>(); else wait_vm_lgkm0<0>();
     }
     __builtin_amdgcn_s_barrier();
     if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+    if constexpr (G > 0)
+      if (with_late) late();
     compute(smem + (kt % S) * STAGE);
+  };
+  if constexpr (G > 0) {
+    // the late loads go out with the last stage (iteration nk - S), or after the prologue;
+    // that iteration is peeled so the loads sit in straight-line code between the loops
+    const int kg = nk - S;
+    if (kg < 0) {
+      late();
+      for (int kt = 0; kt < nk; ++kt) step(kt, true, false);
+    } else {
+      for (int kt = 0; kt < kg; ++kt) step(kt, false, false);
+      step(kg, false, true);
+      for (int kt = kg + 1; kt < nk; ++kt) step(kt, true, false);
+    }
+  } else {
+    for (int kt = 0; kt < nk; ++kt) step(kt, false, false);
   }
   // every wave is done reading the stages before the epilogue may reuse LDS
   __syncthreads();
@@ -540,14 +575,25 @@ __global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint
   // them, or on the epilogue's gathers issued after them, precedes the k-loop.
   static_assert(!RMS || has_tile_epi<EPI>::value, "row-scaled operands need a tile epilogue");
   typename PrepOf<SA>::type pre_a{};
-  if constexpr (RMS) pre_a = sa.template prepare_load<BM>(m0, K);
   if constexpr (has_tile_epi<EPI>::value) {
     constexpr int TR = tile_rows_of<EPI>::value < BM ? tile_rows_of<EPI>::value : BM;   // rows per chunk
     constexpr int LDT = BN + 4;
     static_assert(BM % TR == 0 && TR % 16 == 0, "whole 16-row groups per chunk");
     static_assert(TR * LDT * 4 <= gemm_stage_bytes<T, BM, BN, D, KM>(), "output chunk fits the stages");
-    const typename EPI::TilePre pre = epi.tile_prefetch(m0, n0);
-    gemm_kloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, bz * K);
+    typename EPI::TilePre pre;
+    if constexpr (late_gathers_of<EPI>::value > 0 && D < 0 && !KM) {
+      // the gathers (and row-scale loads) are issued with the k-loop's last stage
+      constexpr int G = late_gathers_of<EPI>::value + (RMS ? SA::template prepare_loads<BM>() : 0);
+      auto late = [&]() {
+        if constexpr (RMS) pre_a = sa.template prepare_load<BM>(m0, K);
+        pre = epi.tile_prefetch(m0, n0);
+      };
+      gemm_mainloop_dma<T, BM, BN, WM, WN, -D, G>(sa, sb, K, m0, n0, smem, acc, bz * K, late);
+    } else {
+      if constexpr (RMS) pre_a = sa.template prepare_load<BM>(m0, K);
+      pre = epi.tile_prefetch(m0, n0);
+      gemm_kloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, bz * K);
+    }
     // the k-loop ends with a barrier: the stages are free for the output tile
     float* tile = reinterpret_cast<float*>(smem);
     const float* rs_lds = reinterpret_cast<const float*>(smem + gemm_stage_bytes<T, BM, BN, D, KM>());

@@ -622,6 +622,8 @@ template <typename T, int DH> struct EpiSweep1 {
     floatx4 f[4];                   // K: gx_a, gx_b, cos, sin; linear V: gx x2; v_map: sig x4
     typename Raw4<T>::type h[8];    // K: kraw_a, kraw_b; linear V: v_raw x2; v_map: o x4, norm weight x4
   };
+  // tile_prefetch issues exactly these 12 loads (one per f / h slot, unconditionally)
+  static constexpr int LATE_GATHERS = 12;
   DM_DEV TilePre tile_prefetch(int m0, int n0) const {
     const int r = threadIdx.x >> 2, lc0 = 4 * (threadIdx.x & 3);
     const int d = g.d, h = g.h;
