@@ -863,6 +863,8 @@ template <typename T, int DH> struct EpiSweep2Head {
     floatx4 gx[CW / 4], gu[CW / 4];
     Raw8<T> vr[CW / 8];
   };
+  // vector-memory load instructions tile_prefetch issues (Raw8 = one 16-byte load in bf16)
+  static constexpr int LATE_GATHERS = 2 * (CW / 4) + (CW / 8) * (int)(sizeof(T) / 2);
   DM_DEV TilePre tile_prefetch(int m0, int n0) const {
     const int r = threadIdx.x >> 2, e0 = CW * (threadIdx.x & 3), col = n0 + e0;
     const int m = min(m0 + r, M - 1);
@@ -929,8 +931,11 @@ static __global__ __launch_bounds__(256) void k_sweep2_attend(SrcRows<T> sa, Src
   constexpr int LDT = DH + 4;
   using WT = WaveTile<64, DH, 2, 2>;
   using C = AttnCfg<T, DH>;
-  __shared__ __attribute__((aligned(1024))) char smem[gemm_lds_bytes<T, 64, DH, D, false>()];
-  __shared__ __attribute__((aligned(16))) T alds[C::LDS_ELEMS];
+  // one LDS object for both (a second __shared__ array makes the compiler guard every read of
+  // the direct-to-LDS stages with a full vmcnt wait, serialising the k-loop)
+  constexpr int GEMM_LDS = (gemm_lds_bytes<T, 64, DH, D, false>() + 15) / 16 * 16;
+  __shared__ __attribute__((aligned(1024))) char smem[GEMM_LDS + C::LDS_ELEMS * sizeof(T)];
+  T* alds = reinterpret_cast<T*>(smem + GEMM_LDS);
   static_assert(64 * LDT * 4 <= gemm_stage_bytes<T, 64, DH, D>(), "output tile fits the stages");
   const int hh = blockIdx.x, b = blockIdx.y;
   const int m0 = b * 64, n0 = hh * DH;
@@ -940,8 +945,15 @@ static __global__ __launch_bounds__(256) void k_sweep2_attend(SrcRows<T> sa, Src
   for (int i = 0; i < WT::FM; ++i)
 #pragma unroll
     for (int j = 0; j < WT::FN; ++j) acc[i][j] = zero4();
-  const typename EpiSweep2Head<T, DH>::TilePre pre = epi.tile_prefetch(m0, n0);
-  gemm_kloop<T, 64, DH, 2, 2, D>(sa, sb, K, m0, n0, smem, acc, 0);
+  typename EpiSweep2Head<T, DH>::TilePre pre;
+  if constexpr (D < 0) {   // gathers issued with the k-loop's last stage (see gemm_mainloop_dma)
+    auto late = [&]() { pre = epi.tile_prefetch(m0, n0); };
+    gemm_mainloop_dma<T, 64, DH, 2, 2, -D, EpiSweep2Head<T, DH>::LATE_GATHERS>(sa, sb, K, m0, n0, smem, acc, 0,
+                                                                               late);
+  } else {
+    pre = epi.tile_prefetch(m0, n0);
+    gemm_kloop<T, 64, DH, 2, 2, D>(sa, sb, K, m0, n0, smem, acc, 0);
+  }
   // the k-loop ends with a barrier: the stages are free for the output tile
   float* tile = reinterpret_cast<float*>(smem);
   const int r0 = (wave / 2) * WT::TM, c0 = (wave % 2) * WT::TN;
