@@ -242,6 +242,8 @@ template <typename T> struct EpiVinBwd {
     floatx4 sg[2], ds[2];
     Raw8<T> vm;
   };
+  // vector-memory load instructions tile_prefetch issues (Raw8 = one 16-byte load in bf16)
+  static constexpr int LATE_GATHERS = 4 + (int)(sizeof(T) / 2);
   DM_DEV TilePre tile_prefetch(int m0, int n0) const {
     const int r = threadIdx.x >> 2, col = n0 + 8 * (threadIdx.x & 3);
     const int d = g.d;

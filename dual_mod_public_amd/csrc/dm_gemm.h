@@ -120,6 +120,11 @@ template <class S> struct requires_prepare { static constexpr bool value = false
 template <typename T> struct requires_prepare<SrcRowsRs<T>> { static constexpr bool value = true; };
 struct NoPre {};
 template <class S> struct PrepOf { using type = NoPre; };
+// vector-memory loads of a source's prepare_load (row scales), 0 for plain sources
+template <class S, int BM> constexpr int prepare_loads_of() {
+  if constexpr (requires_prepare<S>::value) return S::template prepare_loads<BM>();
+  else return 0;
+}
 template <typename T> struct PrepOf<SrcRowsRs<T>> { using type = typename SrcRowsRs<T>::Pre; };
 
 // Tile epilogues: an EPI with a member type TilePre gathers its global inputs with
@@ -583,7 +588,7 @@ __global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint
     typename EPI::TilePre pre;
     if constexpr (late_gathers_of<EPI>::value > 0 && D < 0 && !KM) {
       // the gathers (and row-scale loads) are issued with the k-loop's last stage
-      constexpr int G = late_gathers_of<EPI>::value + (RMS ? SA::template prepare_loads<BM>() : 0);
+      constexpr int G = late_gathers_of<EPI>::value + prepare_loads_of<SA, BM>();
       auto late = [&]() {
         if constexpr (RMS) pre_a = sa.template prepare_load<BM>(m0, K);
         pre = epi.tile_prefetch(m0, n0);

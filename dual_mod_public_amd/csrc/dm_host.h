@@ -20,7 +20,7 @@ namespace dm {
 #define DM_SW1_STAGES 3   // sweep GEMM 1: direct-to-LDS stages of the 64 x 64 blocks
 #endif
 #ifndef DM_SW2_STAGES
-#define DM_SW2_STAGES 0   // GEMM 2 / dv_in GEMM (64 x 32 blocks): 0 = register ring of depth 8
+#define DM_SW2_STAGES 3   // GEMM 2 / dv_in GEMM (64 x 32 blocks): direct-to-LDS stages (0 = register ring of depth 8)
 #endif
 #ifndef DM_DU_STAGES
 #define DM_DU_STAGES 3    // du split-K GEMM: direct-to-LDS stages of the 64 x 64 blocks

@@ -797,6 +797,8 @@ template <typename T, int DH> struct EpiSweep2 {
     floatx4 gx[2], gu[2];
     Raw8<T> vr;
   };
+  // vector-memory load instructions tile_prefetch issues (Raw8 = one 16-byte load in bf16)
+  static constexpr int LATE_GATHERS = 4 + (int)(sizeof(T) / 2);
   DM_DEV TilePre tile_prefetch(int m0, int n0) const {
     const int r = threadIdx.x >> 2, col = n0 + 8 * (threadIdx.x & 3);
     const int m = min(m0 + r, M - 1);
