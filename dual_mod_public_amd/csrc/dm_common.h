@@ -197,14 +197,14 @@ DM_DEV float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 // Accurate to a few fp32 ulp away from 0; near 0 the odd Taylor series
 // x - x^3/3 + 2x^5/15 is used (its error is below fp32 resolution for |x| < 2^-4).
 DM_DEV float tanhf_(float x) {
-  float ax = fabsf(x);
-  if (ax < 0.0625f) {
-    float x2 = x * x;
-    return x * (1.0f + x2 * (-1.0f / 3.0f + x2 * (2.0f / 15.0f)));
-  }
-  float e = __expf(-2.0f * ax);
-  float t = (1.0f - e) / (1.0f + e);
-  return copysignf(t, x);
+  // both forms, then a select: a branch per element would diverge inside the wave (the
+  // epilogues call this on every element of a tile); each input keeps the same formula
+  const float ax = fabsf(x);
+  const float x2 = x * x;
+  const float series = x * (1.0f + x2 * (-1.0f / 3.0f + x2 * (2.0f / 15.0f)));
+  const float e = __expf(-2.0f * ax);
+  const float t = copysignf((1.0f - e) / (1.0f + e), x);
+  return ax < 0.0625f ? series : t;
 }
 
 // ---- wave reductions (full 64-lane and within 16-lane groups) ----------------
