@@ -26,20 +26,42 @@ def hipcc():
     return "hipcc"
 
 
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def _errs(r):
+    return [ln for ln in r.stderr.splitlines() if "packed-fp32-ops" not in ln]
+
+
 def build(verbose=False):
-    """Compile unconditionally (the driver's build check expects a fresh compile)."""
+    """Compile unconditionally (the driver's build check expects a fresh compile): each
+    translation unit to an object in parallel, then one link into libdm_hip.so."""
+    objs, procs = [], []
+    for src in SOURCES:
+        obj = os.path.join(CSRC, src + ".o")
+        cmd = [hipcc()] + FLAGS + ["-c", "-o", obj, os.path.join(CSRC, src)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        objs.append(obj)
+        procs.append(subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True))
+    failed = []
+    for p in procs:
+        out, err = p.communicate()
+        r = subprocess.CompletedProcess(p.args, p.returncode, out, err)
+        if r.returncode != 0:
+            failed.append("\n".join(_errs(r)))
+        elif verbose and _errs(r):
+            print("\n".join(_errs(r)))
+    if failed:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(failed))
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           "-o", tmp] + [os.path.join(CSRC, s) for s in SOURCES]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+    cmd = [hipcc()] + FLAGS + ["-shared", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
-    errs = [ln for ln in r.stderr.splitlines() if "packed-fp32-ops" not in ln]
     if r.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + "\n".join(errs))
-    if verbose and errs:
-        print("\n".join(errs))
+        raise RuntimeError("hipcc link failed:\n" + "\n".join(_errs(r)))
+    for o in objs:
+        os.remove(o)
     os.replace(tmp, LIB)
     return LIB
 

@@ -3,7 +3,7 @@
 Mirrors models/dualmod/config.py:7-226 field for field so a reference config
 (or its ``to_dict()``) constructs one of these unchanged. Validation follows
 config.py:164-199. Which knobs the HIP path honours is decided in
-``dual_mod_public_amd.cells.check_supported`` (NotImplementedError for the
+``dual_mod_public_amd.engine.check_supported`` (NotImplementedError for the
 rest — there is no fallback backend).
 """
 

@@ -176,7 +176,9 @@ DM_DEV void flash_tile(const typename Mfma<T>::frag* qf, const T* Ks, const T* V
     }
   }
   // P is the wave's own staging: LDS operations of one wave complete in order, so
-  // its lanes see each other's P without a workgroup barrier
+  // its lanes see each other's P without a workgroup barrier; the wave barrier keeps
+  // the compiler from moving the reads below above the writes above
+  __builtin_amdgcn_wave_barrier();
 #pragma unroll
   for (int kb = 0; kb < C::NPS; ++kb) {
     typename MF::frag pf = MF::load(Pw + col * C::LDP + kb * MF::KSTEP + g * MF::KPL);

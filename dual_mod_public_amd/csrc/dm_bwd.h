@@ -63,16 +63,21 @@ DM_DEV void wave_mma(const T* X, int ldx, const T* Y, int ldy, floatx4 (&acc)[NT
 // The same with the B operand read from the transposed view of a row-major LDS
 // matrix Z [KD rows][ldz]: acc[t] += X[16 rows, KD] . Z[:, 16 t + (0..15)] (no
 // transposed copy of Z is staged).
+// X is the calling wave's own LDS staging, written by its lanes just before: LDS operations
+// of one wave complete in order, and the wave barriers keep the compiler from moving these
+// reads above those writes, or the wave's next writes of X above these reads.
 template <typename T, int KD, int NT>
 DM_DEV void wave_mma_bt(const T* X, int ldx, const T* Z, int ldz, floatx4 (&acc)[NT]) {
   using MF = Mfma<T>;
   const int lane = threadIdx.x & 63;
+  __builtin_amdgcn_wave_barrier();
 #pragma unroll
   for (int k = 0; k < KD; k += MF::KSTEP) {
     const typename MF::frag a = MF::load(X + (lane & 15) * ldx + k + (lane >> 4) * MF::KPL);
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = MF::mma(a, MF::load_tr(Z + (long)k * ldz + 16 * t, ldz), acc[t]);
   }
+  __builtin_amdgcn_wave_barrier();
 }
 
 // packed GEMM-1 column of the k_ctx / g_k(u) quads (see EpiSweep1)

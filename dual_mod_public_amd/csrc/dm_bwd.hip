@@ -327,11 +327,14 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
     // (zero rows up to a whole k-tile)
     const int Kp = (int)(cdiv(coff, 64) * 64);
     if (Kp > coff) {
-      const size_t tail = (size_t)(Kp - coff) * sizeof(T) / 4;
-      fill0_list({{reinterpret_cast<float*>(ws.dctxL + coff * 4 * d), tail * 4 * d},
-                  {reinterpret_cast<float*>(ws.uL + coff * d), tail * d},
-                  {reinterpret_cast<float*>(ws.dvcL + coff * d), tail * d},
-                  {reinterpret_cast<float*>(vinS + coff * d), mult ? tail * d : 0}},
+      // fp32 words of the padding rows: rows * cols * sizeof(T) bytes, a whole number of words
+      // since d is a multiple of 128 (the byte count is formed before dividing: an odd row
+      // count of bf16 rows would otherwise round a row away)
+      auto words = [&](size_t cols) { return (size_t)(Kp - coff) * cols * sizeof(T) / 4; };
+      fill0_list({{reinterpret_cast<float*>(ws.dctxL + coff * 4 * d), words(4 * (size_t)d)},
+                  {reinterpret_cast<float*>(ws.uL + coff * d), words(d)},
+                  {reinterpret_cast<float*>(ws.dvcL + coff * d), words(d)},
+                  {reinterpret_cast<float*>(vinS + coff * d), mult ? words(d) : 0}},
                  s);
     }
     gemm_tn<T>(ws.dctxL, 4 * d, ws.uL, d, ws.dWs, 4 * d, d, Kp, 1, ws.kpart, s);
@@ -469,6 +472,7 @@ int dm_layer_bwd(const dm_config* c, const dm_packed* w, const void* x, const vo
   DM_REQUIRE(c->ctx_mod != DM_CTX_FUSION || g->v_pre, DM_ERR_INVALID, "ctx_mod fusion needs the v_pre grad");
   DM_REQUIRE(w->attn_norm_w == nullptr || (g->attn_norm_w && L->xhat), DM_ERR_INVALID,
              "attn_norm needs its gradient buffer and bufs->xhat");
+  DM_REQUIRE(c->local_window == 0, DM_ERR_UNSUPPORTED, "local_window is decode-only");
   if ((rc = dm_check_schedule(sched, n_cells, L->T))) return rc;
   DM_REQUIRE(L->T <= cache_T, DM_ERR_INVALID, "T=%d > cache_T=%d", L->T, cache_T);
   {   // the attention VJP keeps Q, K, V and dO of a 64-row block in LDS

@@ -220,6 +220,9 @@ int dm_layer_fwd(const dm_config* c, const dm_packed* w, const void* x, void* y,
   if (rc) return rc;
   if ((rc = check_packed(c, w)) || (rc = check_bufs(c, L))) return rc;
   DM_REQUIRE(x && y && ocat, DM_ERR_INVALID, "null x/y/ocat");
+  // the chunk cells read the whole committed prefix (the fused engine's training path,
+  // engines/wavescan/cells/fused_sweep.py); a sliding window is decode-only here
+  DM_REQUIRE(c->local_window == 0, DM_ERR_UNSUPPORTED, "local_window is decode-only");
   if ((rc = dm_check_schedule(sched, n_cells, L->T))) return rc;
   DM_REQUIRE(L->T <= cache_T, DM_ERR_INVALID, "T=%d > cache_T=%d", L->T, cache_T);
   if (tape != nullptr) {

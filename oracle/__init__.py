@@ -12,6 +12,13 @@ Pinning status of each function (what independent check fixes it):
   * refine_kv (linear, mult_res)    — golden vectors written by the reference
                                       itself (tests/golden/make_golden.py);
                                       special case v_map=0, lam=1 == linear
+  * refine_kv knob branches         — closed forms in tests/test_oracle_invariants.py:
+      mult                              mult == mult_res at lambda = 0 (and the
+                                        lambda term == (1 - g_v) w_vctx(u))
+      kmod gated_norm                   kmod heads' v'' == sigmoid(gate) * v_raw
+      kmod raw / tanh bound             kmod heads' v'' == v_raw / tanh(v_raw)
+      k_ctx_norm, v_ctx_norm, v_norm    per-head RMS written element by element
+  * attend_one local_window         — scalar softmax over the last W-1 rows + self
   * sequential_scan                 — golden vectors + T1/T2/T5 invariants
   * chunk_cell_forward (Jacobi)     — golden vectors at K<c + nilpotency K=c
                                       == scan + frontier property

@@ -12,6 +12,12 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a real MI355X (HIP device)")
 
 
+def pytest_sessionfinish(session, exitstatus):
+    mod = sys.modules.get("tests.hip_helpers")
+    if mod is not None:
+        mod.write_margins(REPO)
+
+
 def relerr(a, b):
     """||a-b|| / ||b|| (the reference tests' metric, test_k1_k9.py:48-49)."""
     a = a.double().cpu()

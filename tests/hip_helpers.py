@@ -1,5 +1,7 @@
 """Shared helpers for the GPU parity tests (HIP path vs the CPU oracle)."""
 
+import json
+import os
 import sys
 
 import torch
@@ -11,9 +13,28 @@ from dual_mod_public_amd.synthetic import make_input, make_state_dict
 DEV = "cuda"
 
 
+# measured parity errors of this session: (test, {quantity: relerr}, tolerance)
+MARGINS = []
+
+
 def say(msg):
     print(f"[gpu-test] {msg}", flush=True)
     sys.stdout.flush()
+
+
+def record(test, errs, tol):
+    """Keep a test's measured relative errors (written to gpurun_out/parity_margins.json
+    at the end of the session, so the margins of every run come back with it)."""
+    MARGINS.append({"test": test, "tol": tol, "relerr": {k: float(v) for k, v in errs.items()}})
+
+
+def write_margins(repo):
+    if not MARGINS:
+        return
+    out = os.path.join(repo, "gpurun_out")
+    os.makedirs(out, exist_ok=True)
+    with open(os.path.join(out, "parity_margins.json"), "w") as f:
+        json.dump(MARGINS, f, indent=1)
 
 
 def cfg_of(d=256, h=4, ctx_mod="mult_res", T=64, **kw):

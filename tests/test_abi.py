@@ -98,3 +98,31 @@ def test_kmod_config_fields():
     assert (c.kmod_vraw_heads, c.kmod_mode) == (1, 1)
     c.kmod_vraw_heads = 5   # more kmod heads than heads: rejected by the library
     assert L.load().dm_cell_workspace_bytes(c, 64) == 0
+
+
+def test_training_entry_points_reject_local_window():
+    """A sliding window is decode-only: dm_layer_fwd (tape and recompute forms) and
+    dm_layer_bwd reject it with DM_ERR_UNSUPPORTED before any launch (the checks run on
+    the host; the placeholder pointers below are never dereferenced)."""
+    lib = L.load()
+    c = _conf(local_window=8)
+    fake = ctypes.c_void_p(1 << 20)   # non-null, 16-byte aligned, never dereferenced
+    w = L.dm_packed()
+    for f in ("w_proj", "b_proj", "w_sweep", "w_vctx", "norm_ctx_w", "attn_norm_w", "wo", "w_proj_t",
+              "w_sweep_t", "w_vctx_t", "wo_t"):
+        setattr(w, f, fake.value)
+    b = L.dm_layer_bufs()
+    b.T = 64
+    for f in ("xhat", "qr", "kraw", "kself", "vraw", "glogx", "sig"):
+        setattr(b, f, fake.value)
+    sched = (ctypes.c_int32 * 3)(0, 64, 4)
+    g = L.dm_grads()
+    for f, _ in L.GRAD_FIELDS:
+        setattr(g, f, fake.value)
+    for tape in (None, fake):
+        rc = lib.dm_layer_fwd(ctypes.byref(c), ctypes.byref(w), fake, fake, fake, fake, ctypes.byref(b), sched, 1,
+                              fake, fake, 64, fake, tape, 1 << 30, fake, 1 << 30, None)
+        assert rc == -2 and b"local_window" in lib.dm_last_error()
+    rc = lib.dm_layer_bwd(ctypes.byref(c), ctypes.byref(w), fake, fake, fake, fake, fake, ctypes.byref(b), sched, 1,
+                          fake, fake, 64, fake, None, 0, ctypes.byref(g), fake, 1 << 30, None)
+    assert rc == -2 and b"local_window" in lib.dm_last_error()

@@ -17,12 +17,13 @@ import oracle as O
 from dual_mod_public_amd import _lib as L
 from dual_mod_public_amd.autograd import dm_layer
 from dual_mod_public_amd.engine import HipSweepCell, LayerGrads, uniform_chunks
-from tests.hip_helpers import DEV, cfg_of, relerr, say, setup
+from tests.hip_helpers import DEV, cfg_of, record, relerr, say, setup
 
 pytestmark = pytest.mark.gpu
 
 FP32_TOL = 1e-4
 BF16_TOL = 5e-2
+BF16_FWD_TOL = 2e-2   # bf16 forward bar of BASELINE.json (2e-2 relative)
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -33,9 +34,10 @@ def _gpu():
 
 
 def oracle_grads(cfg, sd, x, dy, cos, sin, sched, dtype=torch.float64, normalize=True, residual=True,
-                 device="cpu"):
+                 device="cpu", with_forward=False):
     """dx and parameter grads of y = [x +] W_O DM([attn_norm](x)) by autograd through the oracle
-    (on the CPU, or with device="cuda" the same torch code on the GPU for the large shapes)."""
+    (on the CPU, or with device="cuda" the same torch code on the GPU for the large shapes).
+    with_forward also returns the forward's (o_cat, K, V)."""
     sdg = {k: v.to(device, dtype).clone().requires_grad_(True) for k, v in sd.items()}
     xg = x.to(device, dtype).clone().requires_grad_(True)
     with torch.enable_grad():
@@ -43,12 +45,14 @@ def oracle_grads(cfg, sd, x, dy, cos, sin, sched, dtype=torch.float64, normalize
             xh = O.rms_norm(xg, sdg["attn_norm.weight"], 1e-5)
         else:
             xh = xg
-        o = O.layer_forward(cfg, sdg, xh, cos.to(device, dtype), sin.to(device, dtype), sched)[0]
+        o, K, V = O.layer_forward(cfg, sdg, xh, cos.to(device, dtype), sin.to(device, dtype), sched)
         y = O.dm_oracle._lin(o, sdg, "wo")
         if residual:
             y = y + xg
         (y * dy.to(device, dtype)).sum().backward()
     g = {k: v.grad for k, v in sdg.items() if v.grad is not None}
+    if with_forward:
+        return xg.grad, g, (o.detach(), K.detach(), V.detach())
     return xg.grad, g
 
 
@@ -85,8 +89,9 @@ def compare(name, dx, g, dx_ref, g_ref, tol, skip=()):
     worst = max(errs, key=errs.get)
     say(f"  {name}: worst {worst} {errs[worst]:.2e}; " +
         " ".join(f"{k.split('.')[0]}={v:.1e}" for k, v in errs.items()))
+    record(name, errs, tol)
     for k, v in errs.items():
-        assert v < tol, f"{k}: relerr {v:.3e} >= {tol}"
+        assert v < tol, f"{k}: relerr {v:.3e} >= {tol} (all: {errs})"
 
 
 @pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "mult", "fusion"])
@@ -243,10 +248,51 @@ def test_layer_grads_340m_shape_bf16_T2048():
     sd, x, _, (c32, s32) = setup(cfg, B, T)
     dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(13), dtype=torch.float32)
     sched = uniform_chunks(T, 64, 4)
-    _, dx, g = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.bfloat16, tape=True)
-    dx_ref, g_ref = oracle_grads(cfg, {k: v.float() for k, v in sd.items()}, x.float(), dy, c32, s32, sched,
-                                 dtype=torch.float32, device=DEV)
+    _, dx, g, (K, V, ocat) = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.bfloat16, tape=True, full=True)
+    dx_ref, g_ref, (o_ref, K_ref, V_ref) = oracle_grads(
+        cfg, {k: v.float() for k, v in sd.items()}, x.float(), dy, c32, s32, sched, dtype=torch.float32,
+        device=DEV, with_forward=True)
+    # the forward over the whole 32-chunk Gauss-Seidel chain (o_cat and the final K / V
+    # rows of every chunk), against the 2e-2 bf16 bar
+    fwd = {"o_cat": relerr(ocat, o_ref), "K": relerr(K, K_ref), "V": relerr(V, V_ref)}
+    say(f"  bf16 T=2048 forward relerr " + " ".join(f"{k}={v:.2e}" for k, v in fwd.items()))
+    record("bf16 340m T=2048 forward", fwd, BF16_FWD_TOL)
+    for k, v in fwd.items():
+        assert v < BF16_FWD_TOL, f"forward {k}: relerr {v:.3e} >= {BF16_FWD_TOL} (all: {fwd})"
     compare("bf16 340m T=2048", dx, g, dx_ref, g_ref, BF16_TOL)
+
+
+@pytest.mark.parametrize("taped", [False, True])
+def test_bf16_grads_odd_stacked_rows(taped):
+    """Batch 1 with a schedule whose stacked weight-grad rows B * sum(K c) = 256 + 105 = 361
+    are odd: the rows padding the stack to a whole k-tile must be zeroed also when their
+    count is odd. The backward workspace and the tape are filled with 0xFF (bf16 NaN)
+    beforehand, so a padding row left unzeroed turns the sweep weight grads into NaN."""
+    say(f"bwd bf16 B=1 odd stacked rows taped={taped}")
+    cfg = cfg_of(d=256, h=4, T=99)
+    B, T = 1, 99
+    sched = [(0, 64, 4), (64, 35, 3)]
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(17), dtype=torch.float64)
+    dt = torch.bfloat16
+    cell = HipSweepCell(cfg, B, T, device=DEV, dtype=dt)
+    cell.pack({k: v.to(DEV, dt) for k, v in sd.items()})
+    bufs = cell.new_bufs(T)
+    xd = x.to(DEV, dt).contiguous()
+    y, ocat = torch.empty_like(xd), torch.empty_like(xd)
+    K = torch.empty(B, cfg.n_heads, T, cfg.head_dim, device=DEV, dtype=dt)
+    V = torch.empty_like(K)
+    tp = cell.new_tape(sched).fill_(255) if taped else None
+    cell.layer_forward(xd, y, c32, s32, sched, K, V, ocat, bufs, tape=tp)
+    cell._bwd_workspace(T, T, max(k for _, _, k in sched)).fill_(255)
+    grads = LayerGrads(cfg, DEV)
+    dx = torch.empty_like(xd)
+    cell.layer_backward(xd, dy.to(DEV, dt).contiguous(), dx, c32, s32, sched, K, V, ocat, bufs, grads, tape=tp)
+    torch.cuda.synchronize()
+    for name, t in grads.t.items():
+        assert torch.isfinite(t).all(), name
+    dx_ref, g_ref = oracle_grads(cfg, sd, x, dy, c64, s64, sched)
+    compare("bf16 odd rows", dx, grads, dx_ref, g_ref, BF16_TOL)
 
 
 def test_module_autograd_matches_oracle():

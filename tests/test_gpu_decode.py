@@ -12,7 +12,7 @@ import torch
 import oracle as O
 from dual_mod_public_amd import _lib as L
 from dual_mod_public_amd.decode import StaticTape
-from tests.hip_helpers import DEV, cfg_of, relerr, say, setup, to_dev
+from tests.hip_helpers import DEV, cfg_of, record, relerr, say, setup, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -104,3 +104,70 @@ def test_attention_module_decode_matches_scan():
     y_ref = O.dm_oracle._lin(o_ref, sd, "wo")
     assert relerr(torch.cat(ys, 1), y_ref) < 1e-5
     assert relerr(cache["K"], K_ref) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("W", [0, 3001])
+def test_decode_many_splits(dtype, W):
+    """A pre-written N(0,1) tape of 4700 rows: 10 splits of the split-P read (more than
+    any smaller test) merged by k_decode_merge, with and without a window whose first row
+    falls inside a split (W = 3001: rows [pos - 3000, pos) + self). Against the oracle's
+    decode_step (attend_one applies the window, attention.py:291-293) in fp64."""
+    say(f"decode many splits {dtype} W={W}")
+    cfg = cfg_of(d=256, h=4, T=4708, local_window=W)
+    B, P0, steps = 2, 4700, 3
+    P = P0 + steps
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, P)
+    g = torch.Generator().manual_seed(21)
+    K0 = torch.randn(B, 4, P, 64, generator=g).to(dtype)
+    V0 = torch.randn(B, 4, P, 64, generator=g).to(dtype)
+    tape = StaticTape(cfg, B, P, DEV, dtype, sd=to_dev(sd, dtype))
+    tape.K.copy_(K0.to(DEV))
+    tape.V.copy_(V0.to(DEV))
+    cache = {"K": K0[:, :, :P0].double(), "V": V0[:, :, :P0].double()}
+    xs = x.to(dtype)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    errs = {}
+    for t in range(P0, P):
+        o, _ = tape.step(xs[:, t].to(DEV).contiguous(), t, c32, s32)
+        o_ref, _ = O.decode_step(cfg, sd, xs[:, t:t + 1].double(), t, cache, c64, s64)
+        torch.cuda.synchronize()
+        errs[f"o@{t}"] = relerr(o, o_ref[:, 0])
+    errs["K rows"] = relerr(tape.K[:, :, P0:P], cache["K"][:, :, P0:P])
+    errs["V rows"] = relerr(tape.V[:, :, P0:P], cache["V"][:, :, P0:P])
+    say("  " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+    record(f"decode 10 splits {dtype} W={W}", errs, tol)
+    assert max(errs.values()) < tol, errs
+
+
+def test_decode_config5_shape():
+    """BASELINE config 5 itself: B=64, d=1024 16x64, a pre-written N(0,1) bf16 tape of 32768
+    rows (64 splits per (b, h) merged by k_decode_merge), 3 steps; against the oracle's
+    static-tape decode (lm/eval/graph_decode.py:33-51) run in fp32 torch on the GPU."""
+    say("decode C5 shape: B=64 P0=32768 bf16 vs fp32 oracle on the GPU")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    cfg = cfg_of(d=1024, h=16, T=32776)
+    B, P0, steps = 64, 32768, 3
+    P = P0 + steps
+    sd = {k: v.float() for k, v in setup(cfg, 1, 8)[0].items()}
+    g = torch.Generator(device=DEV).manual_seed(5)
+    tape = StaticTape(cfg, B, P, DEV, torch.bfloat16, sd=to_dev(sd, torch.bfloat16))
+    tape.K.normal_(generator=g)
+    tape.V.normal_(generator=g)
+    x = torch.randn(B, steps, 1024, generator=g, device=DEV).to(torch.bfloat16)
+    cos, sin = O.build_rope_cache(P, 64, 10000.0)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    Kb, Vb = tape.K.float(), tape.V.float()
+    sdd = to_dev(sd, torch.float32)
+    errs = {}
+    for t in range(P0, P):
+        o, _ = tape.step(x[:, t - P0].contiguous(), t, cos, sin)
+        o_ref = O.static_decode_step(cfg, sdd, x[:, t - P0:t - P0 + 1].float(), t, Kb, Vb, cos, sin)
+        torch.cuda.synchronize()
+        errs[f"o@{t}"] = relerr(o, o_ref[:, 0])
+    errs["K rows"] = relerr(tape.K[:, :, P0:P], Kb[:, :, P0:P])
+    errs["V rows"] = relerr(tape.V[:, :, P0:P], Vb[:, :, P0:P])
+    say("  " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+    record("decode C5 shape bf16", errs, 2e-2)
+    assert max(errs.values()) < 2e-2, errs
+    del Kb, Vb

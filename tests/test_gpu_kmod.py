@@ -1,9 +1,11 @@
 """GPU parity of the kmod heads knob (config.py kmod_vraw_heads / kmod_mode /
 kmod_vraw_bound; models/dualmod/attention.py:362-384): the first n heads keep their
 raw value (raw, optionally tanh-bounded) or blend it with a zeroed v_ctx
-(gated_norm). Forward, gradients (autograd through the oracle, whose knob path is
-pinned by the reference's golden knob case) and decode. fp32 tolerances as the dense
-tests: 1e-5 forward / decode, 1e-4 grads."""
+(gated_norm). Forward, gradients (autograd through the oracle) and decode. The
+oracle's kmod branches are pinned by closed forms (tests/test_oracle_invariants.py:
+gated_norm heads' v'' == sigmoid(gate) v_raw, raw heads' v'' == v_raw or tanh(v_raw));
+the reference's golden knob case covers raw mode without the tanh bound. fp32
+tolerances as the dense tests: 1e-5 forward / decode, 1e-4 grads."""
 
 import pytest
 import torch

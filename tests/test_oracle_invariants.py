@@ -8,6 +8,8 @@ T-K3 nilpotency + frontier (:114-137), T-K9 RoPE pairing (:142-152), and the
 special case v_map = 0, lambda = 1 (mult_res reduces to linear).
 """
 
+import math
+
 import pytest
 import torch
 
@@ -197,3 +199,143 @@ def test_attend_one_brute_force():
     e = [math.exp(s - max(sc)) for s in sc]
     ref = sum(ei * v for ei, v in zip(e, vals)) / sum(e)
     assert torch.allclose(o, ref, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# pins of the knob branches that no golden vector covers (attention.py:291-293,
+# 338-384): each check is a closed form the reference's formulas fix, computed here
+# from the raw projections rather than by calling the branch under test
+# ---------------------------------------------------------------------------
+
+def _refine_inputs(cfg, seed=9, T=5):
+    sd, _, _, x = _setup(cfg, T=T, seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    o_cat = torch.randn(x.shape, generator=g, dtype=D)
+    k_raw = torch.randn(x.shape, generator=g, dtype=D)
+    v_raw = torch.randn(x.shape, generator=g, dtype=D)
+    return sd, x, o_cat, k_raw, v_raw
+
+
+def test_mult_equals_mult_res_at_zero_lambda():
+    """attention.py:347-353: mult's v_in = sigmoid(v_gate x) tanh(v_map u) is mult_res's with
+    lambda = 0. A dropped sigmoid / tanh or swapped v_gate, v_map in the mult branch fails."""
+    cfg_m = _cfg(ctx_mod="mult")
+    cfg_r = _cfg(ctx_mod="mult_res", mult_res_lambda=0.0)
+    sd, x, o_cat, k_raw, v_raw = _refine_inputs(cfg_m)
+    km, vm = O.refine_kv(cfg_m, sd, x, o_cat, k_raw, v_raw)
+    kr, vr = O.refine_kv(cfg_r, sd, x, o_cat, k_raw, v_raw)
+    assert torch.equal(km, kr) and relerr(vm, vr) < TOL
+    # and lambda matters: mult_res at lambda = 1 differs by (1 - g_v) w_vctx(u)
+    cfg_1 = _cfg(ctx_mod="mult_res", mult_res_lambda=1.0)
+    _, v1 = O.refine_kv(cfg_1, sd, x, o_cat, k_raw, v_raw)
+    u = O.rms_norm(o_cat, sd["norm_ctx.weight"], 1e-5)
+    gv = torch.sigmoid(torch.nn.functional.linear(torch.cat([x, u], -1), sd["w_gv.weight"], sd["w_gv.bias"]))
+    assert relerr(v1 - vm, (1 - gv) * torch.nn.functional.linear(u, sd["w_vctx.weight"])) < TOL
+
+
+def _value_gate(sd, x, o_cat):
+    u = O.rms_norm(o_cat, sd["norm_ctx.weight"], 1e-5)
+    return torch.sigmoid(torch.nn.functional.linear(torch.cat([x, u], -1), sd["w_gv.weight"], sd["w_gv.bias"]))
+
+
+@pytest.mark.parametrize("mod", ["mult_res", "linear"])
+def test_kmod_gated_norm_closed_form(mod):
+    """attention.py:364-372 (kmod_mode gated_norm): the kmod heads' v_ctx is zeroed before
+    the blend, so their v'' = g_v v_raw exactly; the other heads and k'' are untouched."""
+    nvr = 2
+    cfg = _cfg(ctx_mod=mod, kmod_vraw_heads=nvr, kmod_mode="gated_norm")
+    base = _cfg(ctx_mod=mod)
+    sd, x, o_cat, k_raw, v_raw = _refine_inputs(cfg)
+    k, v = O.refine_kv(cfg, sd, x, o_cat, k_raw, v_raw)
+    k0, v0 = O.refine_kv(base, sd, x, o_cat, k_raw, v_raw)
+    cut = nvr * cfg.head_dim
+    gv = _value_gate(sd, x, o_cat)
+    assert relerr(v[..., :cut], (gv * v_raw)[..., :cut]) < TOL
+    assert torch.equal(v[..., cut:], v0[..., cut:]) and torch.equal(k, k0)
+
+
+@pytest.mark.parametrize("bound", ["none", "tanh"])
+def test_kmod_raw_closed_form(bound):
+    """attention.py:373-383 (kmod_mode raw): the kmod heads keep v_raw (tanh(v_raw) with
+    kmod_vraw_bound tanh), no gate and no ctx term; the other heads are untouched."""
+    nvr = 1
+    cfg = _cfg(kmod_vraw_heads=nvr, kmod_vraw_bound=bound)
+    base = _cfg()
+    sd, x, o_cat, k_raw, v_raw = _refine_inputs(cfg)
+    v_raw = 3.0 * v_raw   # beyond tanh's linear range
+    _, v = O.refine_kv(cfg, sd, x, o_cat, k_raw, v_raw)
+    _, v0 = O.refine_kv(base, sd, x, o_cat, k_raw, v_raw)
+    cut = nvr * cfg.head_dim
+    want = torch.tanh(v_raw[..., :cut]) if bound == "tanh" else v_raw[..., :cut]
+    assert torch.equal(v[..., :cut], want)
+    assert torch.equal(v[..., cut:], v0[..., cut:])
+
+
+@pytest.mark.parametrize("W,P", [(3, 7), (5, 4), (8, 8)])
+def test_attend_one_local_window_brute_force(W, P):
+    """attention.py:291-293: with local_window W the read keeps the last W - 1 tape rows
+    plus the raw self column; written out as a scalar softmax per key."""
+    cfg = _cfg(local_window=W)
+    g = torch.Generator().manual_seed(W * 10 + P)
+    dh = 4
+    q = torch.randn(1, 1, 1, dh, generator=g, dtype=D)
+    ks = torch.randn(1, 1, 1, dh, generator=g, dtype=D)
+    vs = torch.randn(1, 1, 1, dh, generator=g, dtype=D)
+    K = torch.randn(1, 1, P, dh, generator=g, dtype=D)
+    V = torch.randn(1, 1, P, dh, generator=g, dtype=D)
+    o = O.attend_one(cfg, q, ks, vs, K, V)[0, 0, 0]
+    lo = max(0, P - (W - 1))
+    keys = [K[0, 0, i] for i in range(lo, P)] + [ks[0, 0, 0]]
+    vals = [V[0, 0, i] for i in range(lo, P)] + [vs[0, 0, 0]]
+    sc = [float((q[0, 0, 0] * k).sum()) / math.sqrt(dh) for k in keys]
+    e = [math.exp(s - max(sc)) for s in sc]
+    ref = sum(ei * v for ei, v in zip(e, vals)) / sum(e)
+    assert torch.allclose(o, ref, atol=1e-12)
+
+
+def _head_rms_ref(y, gain, h, eps=1e-6):
+    """Per-head RMS norm written element by element (attention.py:227-269)."""
+    out = torch.empty_like(y)
+    dh = y.shape[-1] // h
+    for idx in range(y.shape[0] * y.shape[1]):
+        b, t = divmod(idx, y.shape[1])
+        for hd in range(h):
+            seg = y[b, t, hd * dh:(hd + 1) * dh]
+            r = 1.0 / math.sqrt(float((seg * seg).sum()) / dh + eps)
+            out[b, t, hd * dh:(hd + 1) * dh] = seg * r * float(gain[hd])
+    return out
+
+
+
+def test_k_ctx_norm_closed_form():
+    """attention.py:257-269 (k_ctx_norm rms): k'' = g k_raw + (1 - g) N(w_kctx u) with N the
+    per-head RMS norm (eps 1e-6) times k_gain."""
+    cfg = _cfg(k_ctx_norm="rms")
+    sd, x, o_cat, k_raw, v_raw = _refine_inputs(cfg)
+    sd["k_gain"] = torch.tensor([1.75, 0.5, 2.0, 1.0], dtype=D)
+    k, _ = O.refine_kv(cfg, sd, x, o_cat, k_raw, v_raw)
+    u = O.rms_norm(o_cat, sd["norm_ctx.weight"], 1e-5)
+    kc = _head_rms_ref(torch.nn.functional.linear(u, sd["w_kctx.weight"]), sd["k_gain"], 4)
+    gk = torch.sigmoid(torch.nn.functional.linear(torch.cat([x, u], -1), sd["w_gk.weight"], sd["w_gk.bias"]))
+    assert relerr(k, gk * k_raw + (1 - gk) * kc) < TOL
+
+
+def test_v_ctx_norm_closed_form():
+    """attention.py:238-255 (v_ctx_norm rms): v_ctx = N(w_vctx v_in), per-head RMS x ctx_gain."""
+    cfg = _cfg(v_ctx_norm="rms", ctx_mod="linear")
+    sd, x, o_cat, k_raw, v_raw = _refine_inputs(cfg)
+    sd["ctx_gain"] = torch.tensor([0.5, 1.0, 1.5, 2.0], dtype=D)
+    _, v = O.refine_kv(cfg, sd, x, o_cat, k_raw, v_raw)
+    u = O.rms_norm(o_cat, sd["norm_ctx.weight"], 1e-5)
+    vc = _head_rms_ref(torch.nn.functional.linear(u, sd["w_vctx.weight"]), sd["ctx_gain"], 4)
+    gv = _value_gate(sd, x, o_cat)
+    assert relerr(v, gv * v_raw + (1 - gv) * vc) < TOL
+
+
+def test_v_norm_closed_form():
+    """attention.py:218-234 (v_norm rms): v_raw = N(wv x), per-head RMS x v_gain."""
+    cfg = _cfg(v_norm="rms")
+    sd, _, _, x = _setup(cfg, T=3)
+    sd["v_gain"] = torch.tensor([2.0, 1.0, 0.25, 1.0], dtype=D)
+    v = O.project_v(cfg, sd, x)
+    assert relerr(v, _head_rms_ref(torch.nn.functional.linear(x, sd["wv.weight"]), sd["v_gain"], 4)) < TOL
