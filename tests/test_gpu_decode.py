@@ -112,7 +112,11 @@ def test_decode_many_splits(dtype, W):
     """A pre-written N(0,1) tape of 4700 rows: 10 splits of the split-P read (more than
     any smaller test) merged by k_decode_merge, with and without a window whose first row
     falls inside a split (W = 3001: rows [pos - 3000, pos) + self). Against the oracle's
-    decode_step (attend_one applies the window, attention.py:291-293) in fp64."""
+    decode_step (attend_one applies the window, attention.py:291-293) in fp64.
+    fp32 bar 1e-4, not 1e-5: o sums ~4700 N(0,1) value rows with random signs, so its fp32
+    rounding error in any summation order is ~sqrt(P) eps relative to |o| (measured ~1e-5;
+    the refine's random-sign W u products double it in the K rows); a dropped or doubled
+    split, or a window offset off by a row, is an error of 1e-3 or more."""
     say(f"decode many splits {dtype} W={W}")
     cfg = cfg_of(d=256, h=4, T=4708, local_window=W)
     B, P0, steps = 2, 4700, 3
@@ -126,7 +130,7 @@ def test_decode_many_splits(dtype, W):
     tape.V.copy_(V0.to(DEV))
     cache = {"K": K0[:, :, :P0].double(), "V": V0[:, :, :P0].double()}
     xs = x.to(dtype)
-    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
     errs = {}
     for t in range(P0, P):
         o, _ = tape.step(xs[:, t].to(DEV).contiguous(), t, c32, s32)
