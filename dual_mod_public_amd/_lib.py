@@ -29,6 +29,7 @@ class dm_config(ctypes.Structure):
                 ("kmod_mode", c_i32), ("v_clamp_tau", ctypes.c_float), ("reserved", c_i32 * 3)]
 
 
+DM_DECODE_SCRATCH_MAX = 32 << 20   # include/dm_abi.h: static scratch of dm_decode_step_noalloc
 DM_FLAG_NO_RESIDUAL = 1
 DM_FLAG_FUSED_ATTEND = 2
 DM_FLAG_UNFUSED_ATTEND = 4
@@ -99,6 +100,8 @@ SIGNATURES = {
     "dm_decode_workspace_bytes": (ctypes.c_size_t, [P(dm_config), c_i32]),
     "dm_decode_step": (ctypes.c_int, [P(dm_config), P(dm_packed), c_fp, c_fp,
                                       P(dm_decode_args), c_vp]),
+    "dm_decode_step_noalloc": (ctypes.c_int, [P(dm_config), P(dm_packed), c_fp, c_fp,
+                                              P(dm_decode_args), c_vp]),
     "dm_linear": (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp]),
     "dm_gemm": (ctypes.c_int, [c_i32, c_i32, c_i32, c_vp, c_vp, c_fp, c_i32, c_i32, c_i32, c_i32,
                                c_vp]),

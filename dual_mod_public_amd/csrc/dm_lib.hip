@@ -6,6 +6,7 @@
 #include "dm_decode.h"
 #include "dm_fwd_host.h"
 
+#include <mutex>
 #include <vector>
 
 using namespace dm;
@@ -376,6 +377,57 @@ int dm_decode_step(const dm_config* c, const dm_packed* w, const float* cos, con
   if (rc) return rc;
   DM_HIP(hipGetLastError());
   return DM_OK;
+}
+
+}  // extern "C"
+
+// ---- decode without a workspace argument -------------------------------------------
+// The decode workspace (this step's projections, the split-P partials, the refine's
+// v_in and gate logits) lives in one file-scope device array instead. Host code never
+// passes `scratch` itself to a kernel (in host code the name is a host-side stand-in):
+// each device's address of it is looked up once, with that device current, and kept.
+namespace {
+constexpr size_t SCRATCH_BYTES = DM_DECODE_SCRATCH_MAX;
+__device__ __align__(256) char scratch[SCRATCH_BYTES];
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[SCRATCH_MAX_DEVICES] = {};
+
+int scratch_for_current_device(void** out) {
+  int dev = 0;
+  DM_HIP(hipGetDevice(&dev));
+  DM_REQUIRE(dev >= 0 && dev < SCRATCH_MAX_DEVICES, DM_ERR_UNSUPPORTED, "device %d (at most %d devices)", dev,
+             SCRATCH_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    DM_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    DM_REQUIRE(p != nullptr, DM_ERR_HIP, "no device address for the decode scratch array on device %d", dev);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DM_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int dm_decode_step_noalloc(const dm_config* c, const dm_packed* w, const float* cos, const float* sin,
+                           const dm_decode_args* a, void* stream) {
+  int rc = check_cfg(c);
+  if (rc) return rc;
+  DM_REQUIRE(a != nullptr, DM_ERR_INVALID, "null decode argument");
+  DM_REQUIRE(a->tape_T > 0, DM_ERR_INVALID, "tape_T=%d", a->tape_T);
+  const size_t need = carve_dec(c, a->tape_T, nullptr).bytes;
+  DM_REQUIRE(need <= SCRATCH_BYTES, DM_ERR_WORKSPACE,
+             "decode step needs %zu bytes of scratch (B=%d, d=%d, tape_T=%d); the static scratch holds %zu",
+             need, c->B, c->d, a->tape_T, SCRATCH_BYTES);
+  void* base = nullptr;
+  if ((rc = scratch_for_current_device(&base))) return rc;
+  dm_decode_args b = *a;
+  b.workspace = base;
+  b.workspace_bytes = SCRATCH_BYTES;
+  return dm_decode_step(c, w, cos, sin, &b, stream);
 }
 
 int dm_linear(int32_t dtype, const void* x, const void* W, const void* r, void* y, int32_t M, int32_t N,

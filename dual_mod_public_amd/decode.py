@@ -15,7 +15,11 @@ from .engine import PackedWeights, check_supported
 
 
 class StaticTape:
-    def __init__(self, attn_or_cfg, B, P_max, device="cuda", dtype=torch.bfloat16, sd=None):
+    """noalloc=True steps through dm_decode_step_noalloc: no workspace tensor, the
+    library's static scratch instead (for graph capture / serving loops); steps whose
+    scratch would exceed _lib.DM_DECODE_SCRATCH_MAX are refused at construction."""
+
+    def __init__(self, attn_or_cfg, B, P_max, device="cuda", dtype=torch.bfloat16, sd=None, noalloc=False):
         cfg = attn_or_cfg.cfg if hasattr(attn_or_cfg, "cfg") else attn_or_cfg
         check_supported(cfg)
         self.cfg, self.B, self.P = cfg, B, P_max
@@ -27,7 +31,13 @@ class StaticTape:
         nbytes = L.lib().dm_decode_workspace_bytes(ctypes.byref(self.conf), P_max)
         if nbytes == 0:
             raise L.DMError("dm_decode_workspace_bytes rejected the configuration")
-        self.workspace = torch.empty(nbytes, device=self.device, dtype=torch.uint8)
+        self.noalloc = noalloc
+        if noalloc:
+            if nbytes > L.DM_DECODE_SCRATCH_MAX:
+                raise L.DMError(f"decode scratch {nbytes} bytes > the static {L.DM_DECODE_SCRATCH_MAX}")
+            self.workspace = None
+        else:
+            self.workspace = torch.empty(nbytes, device=self.device, dtype=torch.uint8)
         self.o_cat = torch.empty(B, cfg.d_model, device=self.device, dtype=dtype)
         self.y = torch.empty(B, cfg.d_model, device=self.device, dtype=dtype)
         self.w = PackedWeights(cfg, self.device, dtype, with_transposes=False)
@@ -58,8 +68,12 @@ class StaticTape:
         a.xhat, a.K_tape, a.V_tape = L.ptr(xhat), L.ptr(self.K), L.ptr(self.V)
         a.o_cat = L.ptr(self.o_cat)
         a.y = L.ptr(self.y) if with_wo else None
-        a.workspace, a.workspace_bytes = L.ptr(self.workspace), self.workspace.numel()
         ws = self.w.struct(with_attn_norm=False)
-        L.check(L.lib().dm_decode_step(ctypes.byref(self.conf), ctypes.byref(ws), L.ptr(cos),
-                                       L.ptr(sin), ctypes.byref(a), L.stream_ptr()))
+        if self.noalloc:
+            L.check(L.lib().dm_decode_step_noalloc(ctypes.byref(self.conf), ctypes.byref(ws), L.ptr(cos),
+                                                   L.ptr(sin), ctypes.byref(a), L.stream_ptr()))
+        else:
+            a.workspace, a.workspace_bytes = L.ptr(self.workspace), self.workspace.numel()
+            L.check(L.lib().dm_decode_step(ctypes.byref(self.conf), ctypes.byref(ws), L.ptr(cos),
+                                           L.ptr(sin), ctypes.byref(a), L.stream_ptr()))
         return self.o_cat, (self.y if with_wo else None)

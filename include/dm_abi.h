@@ -228,6 +228,23 @@ size_t dm_decode_workspace_bytes(const dm_config* cfg, int32_t tape_T);
 int dm_decode_step(const dm_config* cfg, const dm_packed* w, const float* cos, const float* sin,
                    const dm_decode_args* a, void* stream);
 
+/* ---- decode step that allocates nothing ------------------------------------------
+ * No counterpart in the reference. For callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid it):
+ * dm_decode_step with its workspace taken from a static device array of
+ * DM_DECODE_SCRATCH_MAX bytes inside the library (one per GPU, held until the process
+ * ends) instead of a->workspace (ignored). Steps that need more scratch than that
+ * (dm_decode_workspace_bytes > DM_DECODE_SCRATCH_MAX, e.g. B = 64, d = 1024 with
+ * tape_T above ~56k) return DM_ERR_WORKSPACE. Calls no hipMalloc / hipFree; the
+ * first call on a device looks up that device's address of the array
+ * (hipGetSymbolAddress), so a caller that captures should make one call before
+ * capturing. Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (concurrent streams, threads) race. Nothing in it needs clearing between calls
+ * (every scratch value a step reads is written earlier in the same step). */
+#define DM_DECODE_SCRATCH_MAX ((size_t)32 << 20)
+int dm_decode_step_noalloc(const dm_config* cfg, const dm_packed* w, const float* cos, const float* sin,
+                           const dm_decode_args* a, void* stream);
+
 /* ---- linear layer -------------------------------------------------------------
  * y[M, N] = x[M, K] . W[N, K]^T (+ r[M, N] when r != NULL): nn.Linear without
  * bias (the W_O projection, attention.py:103), storage dtype, fp32 accumulate.
