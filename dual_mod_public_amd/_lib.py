@@ -70,6 +70,12 @@ class dm_cell_args(ctypes.Structure):
                 ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t)]
 
 
+class dm_cell_bwd_args(ctypes.Structure):
+    _fields_ = [("sched", ctypes.POINTER(c_i32)), ("n_cells", c_i32), ("cell", c_i32), ("cache_T", c_i32),
+                ("K_cache", c_vp), ("V_cache", c_vp), ("dK_gc", c_vp), ("dV_gc", c_vp), ("tape", c_vp),
+                ("tape_bytes", ctypes.c_size_t), ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t)]
+
+
 class dm_decode_args(ctypes.Structure):
     _fields_ = [("pos", c_i32), ("tape_T", c_i32), ("xhat", c_vp), ("K_tape", c_vp),
                 ("V_tape", c_vp), ("o_cat", c_vp), ("y", c_vp), ("workspace", c_vp),
@@ -97,6 +103,13 @@ SIGNATURES = {
                                     P(dm_layer_bufs), P(c_i32), c_i32, c_vp, c_vp, c_i32, c_vp,
                                     c_vp, ctypes.c_size_t, P(dm_grads), c_vp, ctypes.c_size_t,
                                     c_vp]),
+    "dm_layer_bwd_begin": (ctypes.c_int, [P(dm_config), P(dm_packed), c_vp, c_vp, P(dm_layer_bufs), P(c_i32),
+                                          c_i32, c_i32, P(dm_grads), c_vp, ctypes.c_size_t, c_vp]),
+    "dm_cell_bwd": (ctypes.c_int, [P(dm_config), P(dm_packed), P(dm_layer_bufs), c_fp, c_fp,
+                                   P(dm_cell_bwd_args), c_vp]),
+    "dm_layer_bwd_end": (ctypes.c_int, [P(dm_config), P(dm_packed), c_vp, c_vp, c_vp, c_fp, c_fp,
+                                        P(dm_layer_bufs), P(c_i32), c_i32, c_vp, c_vp, c_i32, c_vp,
+                                        ctypes.c_size_t, P(dm_grads), c_vp, ctypes.c_size_t, c_vp]),
     "dm_decode_workspace_bytes": (ctypes.c_size_t, [P(dm_config), c_i32]),
     "dm_decode_step": (ctypes.c_int, [P(dm_config), P(dm_packed), c_fp, c_fp,
                                       P(dm_decode_args), c_vp]),

@@ -649,10 +649,15 @@ template <typename T> struct CommKeyArgs {
   const float* G; const float* Dbar; const float* Mx;   // per layer-buffer row (see AttnBwdArgs)
   float scale;
   float* dKp; float* dVp;                      // [COMM_NSQ, B*h, CMAX, DH] partial sums per split
+  // grad-cache form (dKg != nullptr): block x takes keys [64 x, min(64 x + 64, k0)) of the committed
+  // prefix [0, k0) against every query row [q_lo, q_hi) and ADDS into the fp32 grad cache
+  // dKg / dVg [B*h, cache_T, DH] (engines/wavescan/engine/backward.py:116-119)
+  float* dKg = nullptr; float* dVg = nullptr;
 };
 
 // One block per (query split s, b, h): the split's 64-row query tiles s, s + NSQ, ..;
 // wave w owns keys 16w .. 16w + 15 of the cell (key-major products, as in k_attn_bwd).
+// In the grad-cache form one block per (64-key tile, b, h) takes every query tile.
 template <typename T, int DH>
 static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
   using C = AttnBwdCfg<T, DH>;
@@ -665,7 +670,11 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
   T* Wst = Gs + 64 * LDE;
   __shared__ float sM[64], sD[64];
 
-  const int s = blockIdx.x, bh = blockIdx.y;
+  const int bh = blockIdx.y;
+  const bool gcache = a.dKg != nullptr;   // uniform
+  const int s = gcache ? 0 : (int)blockIdx.x, nsq = gcache ? 1 : COMM_NSQ;
+  const int k0 = gcache ? 64 * (int)blockIdx.x : a.k0;
+  const int kc = gcache ? min(64, a.k0 - k0) : a.kc;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g4 = lane >> 4, lc = lane & 15;
   // the wave's own 16 rows of staging (LDS operations of one wave complete in order)
@@ -678,8 +687,8 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
 
   // the cell's keys and values, row-wise (A operands of the key-major products)
   {
-    const bool ok = ri < a.kc;
-    const long row = ((long)bh * a.cache_T + a.k0 + (ok ? ri : 0)) * DH + re0;
+    const bool ok = ri < kc;
+    const long row = ((long)bh * a.cache_T + k0 + (ok ? ri : 0)) * DH + re0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       *reinterpret_cast<uint4*>(Ks + ri * LDE + re0 + w * VT) =
@@ -710,7 +719,7 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
 #pragma unroll
   for (int t = 0; t < NDT; ++t) { dK[t] = zero4(); dV[t] = zero4(); }
   if (s < ntile) load_tile(s);
-  for (int t = s; t < ntile; t += COMM_NSQ) {
+  for (int t = s; t < ntile; t += nsq) {
     const int nq = min(64, a.q_hi - (a.q_lo + 64 * t));
     __syncthreads();   // the previous tile's readers are done (first pass: publishes K / V)
 #pragma unroll
@@ -723,7 +732,7 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
     }
     if ((tid & 3) == 0) { sM[ri] = tok ? mv : 0.f; sD[ri] = tok ? dv : 0.f; }
     __syncthreads();
-    if (t + COMM_NSQ < ntile) load_tile(t + COMM_NSQ);
+    if (t + nsq < ntile) load_tile(t + nsq);
     // key-major: E^T, dS^T (rows j = 16 wave + .., columns i = queries) -> dV += E^T G, dK += dS^T Q
     floatx4 St[4], dPt[4];
 #pragma unroll
@@ -744,7 +753,7 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
       for (int r = 0; r < 4; ++r) {
         const int j = 16 * wave + 4 * g4 + r;
         const float e = __expf(St[u][r] * a.scale - mq[u]);
-        Et[u][r] = (j < a.kc && i < nq) ? e : 0.f;
+        Et[u][r] = (j < kc && i < nq) ? e : 0.f;
         W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[u][r]);
       }
     }
@@ -757,11 +766,36 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
     }
     wave_mma_bt<T, 64, NDT>(W, LDI, Qs, LDE, dK);
   }
+  if (gcache) {
+    // add into the grad cache rows of the tile: every current value loaded first
+    const long grow = (long)bh * a.cache_T + k0;
+    float ok_[4][NDT], ov_[4][NDT];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int jc = min(16 * wave + 4 * g4 + r, kc - 1);
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        ok_[r][t] = a.dKg[(grow + jc) * DH + 16 * t + lc];
+        ov_[r][t] = a.dVg[(grow + jc) * DH + 16 * t + lc];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int j = 16 * wave + 4 * g4 + r;
+      if (j >= kc) continue;
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        a.dKg[(grow + j) * DH + 16 * t + lc] = ok_[r][t] + a.scale * dK[t][r];
+        a.dVg[(grow + j) * DH + 16 * t + lc] = ov_[r][t] + dV[t][r];
+      }
+    }
+    return;
+  }
   const long slot = ((long)s * a.B * a.h + bh) * CMAX;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int j = 16 * wave + 4 * g4 + r;
-    if (j >= a.kc) continue;
+    if (j >= kc) continue;
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
       a.dKp[(slot + j) * DH + 16 * t + lc] = a.scale * dK[t][r];
@@ -771,12 +805,13 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
 }
 
 template <typename T> struct CommQueryArgs {
-  int B, h, Tbuf, cache_T, nrows;              // query rows [0, nrows)
+  int B, h, Tbuf, cache_T, nrows;              // query rows [row0, nrows)
   const int* klim;                             // [Tbuf] committed prefix length of each row (0: none)
   const T* qr; const T* Kc; const T* Vc;
   const float* G; const float* Dbar; const float* Mx;   // per layer-buffer row (see AttnBwdArgs)
   float scale;
   float* dq;                                   // [B*h, Tbuf, DH] (+=)
+  int row0 = 0;                                // first query row (a multiple of 64 or one cell's start)
 };
 
 // One block per (b, h, 64-row query tile), the tiles with the longest prefixes
@@ -795,7 +830,7 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
   __shared__ int sL[64];
 
   const int bh = blockIdx.x;
-  const int i0 = 64 * ((int)gridDim.y - 1 - (int)blockIdx.y);
+  const int i0 = a.row0 + 64 * ((int)gridDim.y - 1 - (int)blockIdx.y);
   const int nq = min(64, a.nrows - i0);
   const int k_end = a.klim[i0 + nq - 1];   // the prefix lengths do not decrease along the rows
   if (k_end <= 0) return;

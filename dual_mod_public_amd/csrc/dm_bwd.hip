@@ -170,21 +170,29 @@ void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N
                      (const float*)part, C, accumulate);
 }
 
-template <typename T, int DH>
-int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T* dx, const float* cos,
-                  const float* sin, const dm_layer_bufs* L, const int32_t* sched, int n_cells, const T* Kc,
-                  const T* Vc, int cache_T, const T* ocat, const char* tape, const size_t* tape_off,
-                  const dm_grads* gr, const BwdWs<T>& ws, hipStream_t s) {
-  const int B = c->B, d = c->d, h = c->h, T_ = L->T, BT = B * T_, BH = B * h;
-  const bool mult = c->ctx_mod != DM_CTX_LINEAR;
-  const int nproj = mult ? 6 : 5;
-  const bool norm = w->attn_norm_w != nullptr;
-  const bool residual = !(c->flags & DM_FLAG_NO_RESIDUAL);
-  const float scale = 1.0f / sqrtf((float)DH);
-  const float inv_d = 1.0f / (float)d;
-  ProfScope whole(PROF_BWD, s);
+// The backward of one layer in three parts, as the reference's fused engine splits it
+// (FusedSweepCell.layer_blockmlp_bwd / cell_backward / layer_close, fused_sweep.py:1557-1959):
+//   bwd_begin  zero the layer accumulators; W_O VJP (do_cat = dy . W_O, dW_O += dy^T o_cat)
+//   bwd_cell   one cell, the cells last first: its sweep states (tape or exact recompute), then its
+//              sweeps backward; the weight-grad operands of its rows are stacked in the workspace
+//   bwd_end    the sweep weight grads (one GEMM per weight over every cell's stacked rows), the
+//              projection VJP, the attn_norm VJP and dx
+// The committed prefix a cell reads gets its grads one of two ways. Layer path (dm_layer_bwd): a
+// cell's final rows receive, right before its sweeps, the sum over every later row's committed
+// attention (k_comm_dkv from the per-row G / Dbar, complete once the later cells are done; no fp32
+// grad cache) and the query side runs once per layer. Grad-cache path (dm_cell_bwd, the
+// reference's protocol, engines/wavescan/engine/backward.py:92-123): the cell takes its own rows'
+// grads from the caller's fp32 cache dK_gc / dV_gc, and right after its sweeps ADDS the grads of
+// the committed rows it read into dK_gc / dV_gc[:, :, :pos0] and its query side into dq.
+struct GradCache {
+  float* dK = nullptr;   // [B, h, cache_T, dh] fp32, or nullptr: layer path
+  float* dV = nullptr;
+};
 
-  // ---- zero the accumulators
+template <typename T, int DH>
+void bwd_begin(const dm_config* c, const dm_packed* w, const T* dy, const T* ocat, int T_, const dm_grads* gr,
+               const BwdWs<T>& ws, hipStream_t s) {
+  const int B = c->B, d = c->d, BT = B * T_;
   fill0_list({{ws.dq, (size_t)BT * d},
               {ws.dkraw, (size_t)BT * d},
               {ws.dkself, (size_t)BT * d},
@@ -194,124 +202,164 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
               {ws.dnw, (size_t)cdiv(B * CMAX, NSLOT_TM) * d},
               {ws.dWs, (size_t)4 * d * d}},
              s);
+  // W_O: do_cat = dy . W_O ; dW_O += dy^T . ocat
+  EpiStoreTileF32 ep{BT, d, ws.docat, 0};
+  launch_gemm_big<T>(SrcRows<T>{dy, d, BT}, SrcRows<T>{(const T*)w->wo_t, d, d}, BT, d, d, ep, s);
+  gemm_tn<T>(dy, d, ocat, d, gr->wo, d, d, BT, 1, ws.kpart, s);
+}
 
-  // ---- W_O: do_cat = dy . W_O ; dW_O += dy^T . ocat
-  {
-    EpiStoreTileF32 ep{BT, d, ws.docat, 0};
-    launch_gemm_big<T>(SrcRows<T>{dy, d, BT}, SrcRows<T>{(const T*)w->wo_t, d, d}, BT, d, d,
-                                               ep, s);
-    gemm_tn<T>(dy, d, ocat, d, gr->wo, d, d, BT, 1, ws.kpart, s);
-  }
+// the stacked v_in of every cell: the tape's (saved by the forward in the backward's cell order)
+// or the workspace's (written by the recompute)
+template <typename T>
+T* stacked_vin(const char* tape, const size_t* tape_off, int n_cells, const BwdWs<T>& ws) {
+  return tape != nullptr ? (T*)(const_cast<char*>(tape) + tape_off[n_cells]) : ws.vinL;
+}
 
+// rms: tape cells' o rows to normalise after the cell loop (nullptr: now)
+template <typename T, int DH>
+void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const float* sin, const dm_layer_bufs* L,
+              const int32_t* sched, int n_cells, int ci, const T* Kc, const T* Vc, int cache_T, const char* tape,
+              const size_t* tape_off, const GradCache& gc, const BwdWs<T>& ws, std::vector<RmsSeg>* rms,
+              hipStream_t s) {
+  const int B = c->B, d = c->d, h = c->h, T_ = L->T, BH = B * h;
+  const bool mult = c->ctx_mod != DM_CTX_LINEAR;
+  const float scale = 1.0f / sqrtf((float)DH);
+  const float inv_d = 1.0f / (float)d;
   const T* qr = (const T*)L->qr;
   const T* kself = (const T*)L->kself;
   const T* vraw = (const T*)L->vraw;
   const T* kraw = (const T*)L->kraw;
   const size_t slot = (size_t)BH * CMAX * DH;
-
   const size_t lds_attn = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
-  // the stacked v_in of every cell: the tape's (saved by the forward in this order)
-  // or the workspace's (written by the recompute)
-  T* vinS = tape != nullptr ? (T*)(const_cast<char*>(tape) + tape_off[n_cells]) : ws.vinL;
+  T* vinS = stacked_vin<T>(tape, tape_off, n_cells, ws);
   const int t_end = sched[3 * (n_cells - 1)] + sched[3 * (n_cells - 1) + 1];   // rows of the schedule
-  long coff = 0;   // columns of the weight-grad operands filled so far
-  std::vector<RmsSeg> rms;   // tape mode: every cell's o rows, normalised after the cell loop
-  for (int ci = n_cells - 1; ci >= 0; --ci) {
-    const int pos0 = sched[3 * ci], cc = sched[3 * ci + 1], K = sched[3 * ci + 2];
-    const int N = B * cc;
-    const size_t NS = (size_t)N;
-    CellGeom g{B, cc, d, h, DH, pos0, pos0, T_, cache_T};
-    g.kmod_cols = c->kmod_vraw_heads * DH;
-    g.kmod_mode = c->kmod_mode;
-    g.v_clamp_tau = c->v_clamp_tau;
-    // every sweep's state of the cell: saved by the forward, or an exact recompute
-    CellSave<T> sv = ws.sv;
-    const float* Mx;
-    if (tape != nullptr) {
-      Carver cv(const_cast<char*>(tape) + tape_off[ci]);
-      sv = carve_save<T>(c, NS, K, true, pos0 > 0, cv);
-      if (mult) sv.vin = vinS + coff * d;
-      Mx = sv.Mx;
-    } else {
-      if (mult) sv.vin = vinS + coff * d;   // the recompute writes v_in into the stacked rows
-      run_cell<T, DH>(c, w, L, cos, sin, pos0, cc, K, pos0, T_, (T*)Kc, (T*)Vc, cache_T, nullptr, nullptr, ws.fws,
-                      &sv, s);
-      Mx = pos0 > 0 ? ws.fws.M : nullptr;
+  const long coff = vin_row(c, sched, n_cells, ci);   // rows of the cells after this one in the stacks
+
+  const int pos0 = sched[3 * ci], cc = sched[3 * ci + 1], K = sched[3 * ci + 2];
+  const int N = B * cc;
+  const size_t NS = (size_t)N;
+  CellGeom g{B, cc, d, h, DH, pos0, pos0, T_, cache_T};
+  g.kmod_cols = c->kmod_vraw_heads * DH;
+  g.kmod_mode = c->kmod_mode;
+  g.v_clamp_tau = c->v_clamp_tau;
+  // every sweep's state of the cell: saved by the forward, or an exact recompute
+  CellSave<T> sv = ws.sv;
+  const float* Mx;
+  if (tape != nullptr) {
+    Carver cv(const_cast<char*>(tape) + tape_off[ci]);
+    sv = carve_save<T>(c, NS, K, true, pos0 > 0, cv);
+    if (mult) sv.vin = vinS + coff * d;
+    Mx = sv.Mx;
+  } else {
+    if (mult) sv.vin = vinS + coff * d;   // the recompute writes v_in into the stacked rows
+    run_cell<T, DH>(c, w, L, cos, sin, pos0, cc, K, pos0, T_, (T*)Kc, (T*)Vc, cache_T, nullptr, nullptr, ws.fws,
+                    &sv, s);
+    Mx = pos0 > 0 ? ws.fws.M : nullptr;
+  }
+  // grads of the cell's final rows: layer path, the committed-prefix attention of every later
+  // row (their G / Dbar / row max are in place: those cells are done), in COMM_NSQ partial slots;
+  // grad-cache path, the cache rows [pos0, pos0 + cc)
+  const float* dKn;
+  const float* dVn;
+  long dn_stride, dn_psum;
+  int dn_row0;
+  if (gc.dK == nullptr) {
+    CommKeyArgs<T> ka{B, h, T_, cache_T, pos0, cc, pos0 + cc, t_end, qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow,
+                      scale, ws.dKp, ws.dVp};
+    hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(COMM_NSQ, BH), dim3(256), lds_attn, s, ka);
+    dKn = ws.dKp; dVn = ws.dVp; dn_stride = (long)CMAX * DH; dn_row0 = 0; dn_psum = (long)BH * CMAX * DH;
+  } else {
+    dKn = gc.dK; dVn = gc.dV; dn_stride = (long)cache_T * DH; dn_row0 = pos0; dn_psum = 0;
+  }
+  // this cell's rows of the stacked weight-grad operands
+  T* dctx = ws.dctxL + coff * 4 * d;
+  T* dvc = ws.dvcL + coff * d;
+  for (int sw = K - 1; sw >= 0; --sw) {
+    // refine VJP of sweep sw (the last sweep's rows: the final-row grads above)
+    RefineBwdArgs<T> ra{g, N, c->ctx_mod, dKn, dVn, dn_stride, dn_row0, dn_psum,
+                        sv.save1 + sw * NS * 4 * d, mult ? sv.save2 + sw * NS * d : nullptr, L->glogx, kraw, vraw,
+                        cos, sin, dctx + sw * NS * 4 * d, dvc + sw * NS * d, ws.dglogx, ws.dkraw, ws.dvraw};
+    const dim3 rgrid(cdiv((long)N * d / 2, 256));
+    if (sw == K - 1 && gc.dK == nullptr) hipLaunchKernelGGL((k_refine_bwd<T, DH, COMM_NSQ>), rgrid, dim3(256), 0, s, ra);
+    else hipLaunchKernelGGL((k_refine_bwd<T, DH, 1>), rgrid, dim3(256), 0, s, ra);
+    // dv_in = dv_ctx . W_vctx (mult family)
+    if (mult) {
+      EpiVinBwd<T> ev{g, N, c->ctx_mod, c->mult_res_lambda, sv.save1 + sw * NS * 4 * d, L->sig,
+                      dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
+      const SrcRows<T> av{dvc + sw * NS * d, d, N}, bv{(const T*)w->w_vctx_t, d, d};
+      if constexpr (SW2_STAGES > 0) launch_gemm_auto<T, 64, 32, 4, 1, SW2_STAGES, 8>(av, bv, N, d, d, ev, s);
+      else launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, d, d, ev, s);
     }
-    // grads of the cell's final rows from the committed-prefix attention of every
-    // later row (their G / Dbar / row max are in place: those cells are done)
+    // du = dctx . W_sweep (+ lam dv_in): split-K slices, then the RMS-VJP inputs
     {
-      CommKeyArgs<T> ka{B, h, T_, cache_T, pos0, cc, pos0 + cc, t_end, qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow,
-                        scale, ws.dKp, ws.dVp};
-      hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(COMM_NSQ, BH), dim3(256), lds_attn, s, ka);
+      const int S = DU_SPLIT;
+      EpiStoreTileF32 ep{N, d, ws.du_part, (long)N * d};
+      launch_gemm_splitk<T, 64, 64, 2, 2, sizeof(T) == 2 ? -DU_STAGES : 4>(
+          SrcRows<T>{dctx + sw * NS * 4 * d, 4 * d, N}, SrcRows<T>{(const T*)w->w_sweep_t, 4 * d, d}, N, d,
+          4 * d, S, ep, s);
+      hipLaunchKernelGGL((k_du_epi<T, DU_SPLIT>), dim3(cdiv(N, 16), d / DU_EPI_TN), dim3(256), 0, s, N, d, h,
+                         inv_d, c->rms_eps, (const float*)ws.du_part, mult ? (const float*)ws.lamdv : nullptr,
+                         (const T*)(sv.o + sw * NS * d), (const float*)(sv.ssq + sw * NS * h),
+                         (const T*)w->norm_ctx_w, ws.gw, ws.rowdot, ws.dnw);
     }
-    // this cell's rows of the stacked weight-grad operands
-    T* dctx = ws.dctxL + coff * 4 * d;
-    T* dvc = ws.dvcL + coff * d;
-    const float* dKn = ws.dKp;
-    const float* dVn = ws.dVp;
-    const long dn_stride = (long)CMAX * DH;
-    for (int sw = K - 1; sw >= 0; --sw) {
-      // refine VJP of sweep sw (the last sweep's rows: the sum of the key-side splits)
-      RefineBwdArgs<T> ra{g, N, c->ctx_mod, dKn, dVn, dn_stride, 0, (long)BH * CMAX * DH,
-                          sv.save1 + sw * NS * 4 * d, mult ? sv.save2 + sw * NS * d : nullptr, L->glogx, kraw, vraw,
-                          cos, sin, dctx + sw * NS * 4 * d, dvc + sw * NS * d, ws.dglogx, ws.dkraw, ws.dvraw};
-      const dim3 rgrid(cdiv((long)N * d / 2, 256));
-      if (sw == K - 1) hipLaunchKernelGGL((k_refine_bwd<T, DH, COMM_NSQ>), rgrid, dim3(256), 0, s, ra);
-      else hipLaunchKernelGGL((k_refine_bwd<T, DH, 1>), rgrid, dim3(256), 0, s, ra);
-      // dv_in = dv_ctx . W_vctx (mult family)
-      if (mult) {
-        EpiVinBwd<T> ev{g, N, c->ctx_mod, c->mult_res_lambda, sv.save1 + sw * NS * 4 * d, L->sig,
-                        dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
-        const SrcRows<T> av{dvc + sw * NS * d, d, N}, bv{(const T*)w->w_vctx_t, d, d};
-        if constexpr (SW2_STAGES > 0) launch_gemm_auto<T, 64, 32, 4, 1, SW2_STAGES, 8>(av, bv, N, d, d, ev, s);
-        else launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, d, d, ev, s);
-      }
-      // du = dctx . W_sweep (+ lam dv_in): split-K slices, then the RMS-VJP inputs
-      {
-        const int S = DU_SPLIT;
-        EpiStoreTileF32 ep{N, d, ws.du_part, (long)N * d};
-        launch_gemm_splitk<T, 64, 64, 2, 2, sizeof(T) == 2 ? -DU_STAGES : 4>(
-            SrcRows<T>{dctx + sw * NS * 4 * d, 4 * d, N}, SrcRows<T>{(const T*)w->w_sweep_t, 4 * d, d}, N, d,
-            4 * d, S, ep, s);
-        hipLaunchKernelGGL((k_du_epi<T, DU_SPLIT>), dim3(cdiv(N, 16), d / DU_EPI_TN), dim3(256), 0, s, N, d, h,
-                           inv_d,
-                           c->rms_eps, (const float*)ws.du_part, mult ? (const float*)ws.lamdv : nullptr,
-                           (const T*)(sv.o + sw * NS * d), (const float*)(sv.ssq + sw * NS * h),
-                           (const T*)w->norm_ctx_w, ws.gw, ws.rowdot, ws.dnw);
-      }
-      // attention VJP of sweep sw
-      {
-        const T* Kin; const T* Vin; long in_stride; int in_row0;
-        if (sw == 0) { Kin = kself; Vin = vraw; in_stride = (long)T_ * DH; in_row0 = pos0; }
-        else { Kin = sv.Kin + sw * slot; Vin = sv.Vin + sw * slot; in_stride = (long)CMAX * DH; in_row0 = 0; }
-        float* dKo = sw == 0 ? nullptr : ((K - 1 - sw) % 2 == 0 ? ws.dKa : ws.dKb);
-        float* dVo = sw == 0 ? nullptr : ((K - 1 - sw) % 2 == 0 ? ws.dVa : ws.dVb);
-        AttnBwdArgs<T> aa{g, qr, kself, vraw, Kin, Vin, in_stride, in_row0, sv.o + sw * NS * d,
-                          sv.ssq + sw * NS * h, ws.gw, ws.rowdot, d / DU_EPI_TN,
-                          sw == K - 1 ? ws.docat : nullptr, sv.stat_m + sw * (size_t)BH * CMAX,
-                          sv.stat_z + sw * (size_t)BH * CMAX, Mx, ws.Grow, ws.Drow, ws.Mrow, ws.klim,
-                          sw == K - 1 ? 1 : 0,
-                          scale, inv_d, c->rms_eps, dKo, dVo, ws.dkself, ws.dvraw, ws.dq};
-        hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(2, BH), dim3(256), lds_attn, s, aa);
-        dKn = dKo; dVn = dVo;
-      }
-    }
-    // the other operand of dW_sweep = dctx^T u: this cell's K*N rows of u = RMSNorm(o)
-    // (dW_vctx = dv_ctx^T v_in reads the stacked v_in as it is). The tape keeps every
-    // cell's o: those rows are normalised after the cell loop, RMS_MAX_SEG cells per
-    // launch; a recomputed cell's o is overwritten by the next cell, so now.
+    // attention VJP of sweep sw
     {
-      const int rows = K * N;
-      if (tape != nullptr) {
-        rms.push_back(RmsSeg{sv.o, sv.ssq, coff, rows});
-      } else {
-        hipLaunchKernelGGL(k_rms_rows<T>, dim3(cdiv(rows, 4)), dim3(256), 0, s, (const T*)sv.o, rows, d,
-                           (const float*)sv.ssq, h, (const T*)w->norm_ctx_w, inv_d, c->rms_eps, ws.uL + coff * d);
-      }
-      coff += rows;
+      const T* Kin; const T* Vin; long in_stride; int in_row0;
+      if (sw == 0) { Kin = kself; Vin = vraw; in_stride = (long)T_ * DH; in_row0 = pos0; }
+      else { Kin = sv.Kin + sw * slot; Vin = sv.Vin + sw * slot; in_stride = (long)CMAX * DH; in_row0 = 0; }
+      float* dKo = sw == 0 ? nullptr : ((K - 1 - sw) % 2 == 0 ? ws.dKa : ws.dKb);
+      float* dVo = sw == 0 ? nullptr : ((K - 1 - sw) % 2 == 0 ? ws.dVa : ws.dVb);
+      AttnBwdArgs<T> aa{g, qr, kself, vraw, Kin, Vin, in_stride, in_row0, sv.o + sw * NS * d,
+                        sv.ssq + sw * NS * h, ws.gw, ws.rowdot, d / DU_EPI_TN,
+                        sw == K - 1 ? ws.docat : nullptr, sv.stat_m + sw * (size_t)BH * CMAX,
+                        sv.stat_z + sw * (size_t)BH * CMAX, Mx, ws.Grow, ws.Drow, ws.Mrow, ws.klim,
+                        sw == K - 1 ? 1 : 0,
+                        scale, inv_d, c->rms_eps, dKo, dVo, ws.dkself, ws.dvraw, ws.dq};
+      hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(2, BH), dim3(256), lds_attn, s, aa);
+      dKn = dKo; dVn = dVo;
+      dn_stride = (long)CMAX * DH; dn_row0 = 0; dn_psum = (long)BH * CMAX * DH;
     }
   }
+  // the other operand of dW_sweep = dctx^T u: this cell's K*N rows of u = RMSNorm(o)
+  // (dW_vctx = dv_ctx^T v_in reads the stacked v_in as it is). On the layer path the tape's cells
+  // are normalised after the cell loop, RMS_MAX_SEG cells per launch; a recomputed cell's o is
+  // overwritten by the next cell, and a per-cell call has no later batch: those now.
+  const int rows = K * N;
+  if (tape != nullptr && rms != nullptr) {
+    rms->push_back(RmsSeg{sv.o, sv.ssq, coff, rows});
+  } else {
+    hipLaunchKernelGGL(k_rms_rows<T>, dim3(cdiv(rows, 4)), dim3(256), 0, s, (const T*)sv.o, rows, d,
+                       (const float*)sv.ssq, h, (const T*)w->norm_ctx_w, inv_d, c->rms_eps, ws.uL + coff * d);
+  }
+  // grad-cache path: the committed rows [0, pos0) this cell read get their grads now, key side
+  // into the cache, query side into dq
+  if (gc.dK != nullptr && pos0 > 0) {
+    CommKeyArgs<T> ka{B, h, T_, cache_T, pos0, 0, pos0, pos0 + cc, qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow,
+                      scale, nullptr, nullptr, gc.dK, gc.dV};
+    hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(cdiv(pos0, 64), BH), dim3(256), lds_attn, s, ka);
+    CommQueryArgs<T> qa{B, h, T_, cache_T, pos0 + cc, ws.klim, qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow, scale, ws.dq,
+                        pos0};
+    hipLaunchKernelGGL((k_comm_dq<T, DH>), dim3(BH, cdiv(cc, 64)), dim3(256), lds_attn, s, qa);
+  }
+}
+
+template <typename T, int DH>
+void bwd_end(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T* dx, const float* cos,
+             const float* sin, const dm_layer_bufs* L, const int32_t* sched, int n_cells, const T* Kc, const T* Vc,
+             int cache_T, const char* tape, const size_t* tape_off, bool layer_path, const std::vector<RmsSeg>& rms,
+             const dm_grads* gr, const BwdWs<T>& ws, hipStream_t s) {
+  const int B = c->B, d = c->d, h = c->h, T_ = L->T, BT = B * T_, BH = B * h;
+  const bool mult = c->ctx_mod != DM_CTX_LINEAR;
+  const int nproj = mult ? 6 : 5;
+  const bool norm = w->attn_norm_w != nullptr;
+  const bool residual = !(c->flags & DM_FLAG_NO_RESIDUAL);
+  const float scale = 1.0f / sqrtf((float)DH);
+  const float inv_d = 1.0f / (float)d;
+  const T* qr = (const T*)L->qr;
+  const size_t lds_attn = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
+  T* vinS = stacked_vin<T>(tape, tape_off, n_cells, ws);
+  const int t_end = sched[3 * (n_cells - 1)] + sched[3 * (n_cells - 1) + 1];
+  const long coff = vin_row(c, sched, n_cells, -1);   // every cell's rows
   for (size_t i0 = 0; i0 < rms.size(); i0 += RMS_MAX_SEG) {
     RmsSegs ra{};
     ra.nseg = (int)std::min<size_t>(RMS_MAX_SEG, rms.size() - i0);
@@ -341,12 +389,11 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
     if (mult) gemm_tn<T>(ws.dvcL, d, vinS, d, gr->w_vctx, d, d, Kp, 1, ws.kpart, s);
   }
 
-  // committed-prefix VJP, query side: every row with a committed prefix, into dq
-  {
+  // committed-prefix VJP, query side (layer path): every row with a committed prefix, into dq
+  if (layer_path) {
     CommQueryArgs<T> qa{B, h, T_, cache_T, t_end, ws.klim, qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow, scale, ws.dq};
     hipLaunchKernelGGL((k_comm_dq<T, DH>), dim3(BH, cdiv(t_end, 64)), dim3(256), lds_attn, s, qa);
   }
-
   // ---- projection VJP
   // (+ the bias grads' column partials: sums of dglogx (b_gk | b_gv) and of
   // dsig sig (1 - sig) (b_vgate) over each block's rows)
@@ -414,27 +461,57 @@ int run_layer_bwd(const dm_config* c, const dm_packed* w, const T* x, const T* d
     hipLaunchKernelGGL(k_dx_plain<T>, dim3(std::min(cdiv((long)BT * d, 256), 4096)), dim3(256), 0, s,
                        (long)BT * d, residual ? 1 : 0, (const float*)ws.dxhat, dy, dx);
   }
-  return DM_OK;
 }
 
+// which part of the layer backward an entry point runs
+enum BwdPart { BWD_LAYER = 0, BWD_BEGIN = 1, BWD_CELL = 2, BWD_END = 3 };
+struct BwdCall {
+  int part;
+  const void* x; const void* dy; void* dx; const void* ocat;
+  const float* cos; const float* sin; const dm_layer_bufs* L;
+  const int32_t* sched; int n_cells; int cell;
+  const void* Kc; const void* Vc; int cache_T;
+  const void* tape; size_t tape_bytes;
+  GradCache gc;
+  const dm_grads* g;
+  void* workspace; int kmax;
+};
+
 template <typename T>
-int layer_bwd_dispatch(const dm_config* c, const dm_packed* w, const void* x, const void* dy, void* dx,
-                       const float* cos, const float* sin, const dm_layer_bufs* L, const int32_t* sched,
-                       int n_cells, const void* Kc, const void* Vc, int cache_T, const void* ocat, const void* tape,
-                       size_t tape_bytes, const dm_grads* g, void* workspace, int kmax, hipStream_t s) {
+int bwd_dispatch(const dm_config* c, const dm_packed* w, const BwdCall& a, hipStream_t s) {
   std::vector<size_t> off;
-  if (tape != nullptr) {
-    off = tape_offsets<T>(c, sched, n_cells);
-    DM_REQUIRE(tape_bytes >= off[n_cells + 1], DM_ERR_WORKSPACE, "tape %zu < %zu bytes", tape_bytes,
-               off[n_cells + 1]);
-    DM_REQUIRE(aligned16(tape), DM_ERR_INVALID, "tape must be 16-byte aligned");
+  if (a.tape != nullptr) {
+    off = tape_offsets<T>(c, a.sched, a.n_cells);
+    DM_REQUIRE(a.tape_bytes >= off[a.n_cells + 1], DM_ERR_WORKSPACE, "tape %zu < %zu bytes", a.tape_bytes,
+               off[a.n_cells + 1]);
+    DM_REQUIRE(aligned16(a.tape), DM_ERR_INVALID, "tape must be 16-byte aligned");
   }
-  const BwdWs<T> ws = carve_bwd<T>(c, L->T, cache_T, kmax, workspace);
+  const BwdWs<T> ws = carve_bwd<T>(c, a.L->T, a.cache_T, a.kmax, a.workspace);
+  const char* tape = (const char*)a.tape;
+  const size_t* to = a.tape ? off.data() : nullptr;
+  const T* Kc = (const T*)a.Kc;
+  const T* Vc = (const T*)a.Vc;
   auto run = [&](auto dh_tag) {
     constexpr int DH = decltype(dh_tag)::value;
-    return run_layer_bwd<T, DH>(c, w, (const T*)x, (const T*)dy, (T*)dx, cos, sin, L, sched, n_cells, (const T*)Kc,
-                                (const T*)Vc, cache_T, (const T*)ocat, (const char*)tape,
-                                tape ? off.data() : nullptr, g, ws, s);
+    std::vector<RmsSeg> rms;
+    if (a.part == BWD_LAYER) {
+      ProfScope whole(PROF_BWD, s);
+      bwd_begin<T, DH>(c, w, (const T*)a.dy, (const T*)a.ocat, a.L->T, a.g, ws, s);
+      for (int ci = a.n_cells - 1; ci >= 0; --ci)
+        bwd_cell<T, DH>(c, w, a.cos, a.sin, a.L, a.sched, a.n_cells, ci, Kc, Vc, a.cache_T, tape, to, GradCache{}, ws,
+                        &rms, s);
+      bwd_end<T, DH>(c, w, (const T*)a.x, (const T*)a.dy, (T*)a.dx, a.cos, a.sin, a.L, a.sched, a.n_cells, Kc, Vc,
+                     a.cache_T, tape, to, true, rms, a.g, ws, s);
+    } else if (a.part == BWD_BEGIN) {
+      bwd_begin<T, DH>(c, w, (const T*)a.dy, (const T*)a.ocat, a.L->T, a.g, ws, s);
+    } else if (a.part == BWD_CELL) {
+      bwd_cell<T, DH>(c, w, a.cos, a.sin, a.L, a.sched, a.n_cells, a.cell, Kc, Vc, a.cache_T, tape, to, a.gc, ws,
+                      nullptr, s);
+    } else {
+      bwd_end<T, DH>(c, w, (const T*)a.x, (const T*)a.dy, (T*)a.dx, a.cos, a.sin, a.L, a.sched, a.n_cells, Kc, Vc,
+                     a.cache_T, tape, to, false, rms, a.g, ws, s);
+    }
+    return DM_OK;
   };
   return c->dh == 64 ? run(std::integral_constant<int, 64>{}) : run(std::integral_constant<int, 128>{});
 }
@@ -451,27 +528,19 @@ size_t dm_layer_bwd_workspace_bytes(const dm_config* c, int32_t T, int32_t cache
                              : carve_bwd<float>(c, T, cache_T, max_sweeps, nullptr).bytes;
 }
 
-int dm_layer_bwd(const dm_config* c, const dm_packed* w, const void* x, const void* dy, void* dx,
-                 const float* cos, const float* sin, const dm_layer_bufs* L, const int32_t* sched,
-                 int32_t n_cells, const void* K_cache, const void* V_cache, int32_t cache_T, const void* ocat,
-                 const void* tape, size_t tape_bytes, const dm_grads* g, void* workspace, size_t workspace_bytes,
-                 void* stream) {
+}  // extern "C"
+
+namespace dm {
+// Checks shared by the backward entry points; kmax = the most sweeps of any cell (the workspace
+// layout depends on it, so every part of one layer's backward is given the same schedule).
+int check_bwd_common(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const int32_t* sched,
+                     int n_cells, int cache_T, void* workspace, size_t workspace_bytes, int* kmax) {
   int rc = check_cfg(c);
   if (rc) return rc;
   if ((rc = check_packed(c, w)) || (rc = check_bufs(c, L))) return rc;
   const bool mult = c->ctx_mod != DM_CTX_LINEAR;
-  DM_REQUIRE(x && dy && dx && cos && sin && K_cache && V_cache && ocat && g, DM_ERR_INVALID,
-             "null backward argument");
   DM_REQUIRE(w->w_proj_t && w->w_sweep_t && w->wo_t && (!mult || w->w_vctx_t), DM_ERR_INVALID,
-             "dm_layer_bwd needs the transposed packed weights");
-  DM_REQUIRE(g->wq && g->wk && g->wv && g->wo && g->w_kctx && g->w_vctx && g->w_gk && g->w_gv && g->b_gk &&
-                 g->b_gv && g->norm_ctx_w,
-             DM_ERR_INVALID, "null gradient buffer");
-  DM_REQUIRE(!mult || c->ctx_mod == DM_CTX_FUSION || (g->v_gate && g->b_vgate && g->v_map), DM_ERR_INVALID,
-             "mult family needs v_gate/v_map grads");
-  DM_REQUIRE(c->ctx_mod != DM_CTX_FUSION || g->v_pre, DM_ERR_INVALID, "ctx_mod fusion needs the v_pre grad");
-  DM_REQUIRE(w->attn_norm_w == nullptr || (g->attn_norm_w && L->xhat), DM_ERR_INVALID,
-             "attn_norm needs its gradient buffer and bufs->xhat");
+             "the backward needs the transposed packed weights");
   DM_REQUIRE(c->local_window == 0, DM_ERR_UNSUPPORTED, "local_window is decode-only");
   if ((rc = dm_check_schedule(sched, n_cells, L->T))) return rc;
   DM_REQUIRE(L->T <= cache_T, DM_ERR_INVALID, "T=%d > cache_T=%d", L->T, cache_T);
@@ -485,19 +554,97 @@ int dm_layer_bwd(const dm_config* c, const dm_packed* w, const void* x, const vo
     DM_REQUIRE(lds + 1024 <= (size_t)lim, DM_ERR_UNSUPPORTED,
                "backward attention block needs %zu bytes of LDS, device allows %d (fp32 head_dim 128)", lds, lim);
   }
-  int kmax = 0;
-  for (int i = 0; i < n_cells; ++i) kmax = std::max(kmax, (int)sched[3 * i + 2]);
-  const size_t need = dm_layer_bwd_workspace_bytes(c, L->T, cache_T, kmax);
+  int km = 0;
+  for (int i = 0; i < n_cells; ++i) km = std::max(km, (int)sched[3 * i + 2]);
+  const size_t need = dm_layer_bwd_workspace_bytes(c, L->T, cache_T, km);
   DM_REQUIRE(workspace && workspace_bytes >= need, DM_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes,
              need);
+  *kmax = km;
+  return DM_OK;
+}
+
+int check_grads(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const dm_grads* g) {
+  const bool mult = c->ctx_mod != DM_CTX_LINEAR;
+  DM_REQUIRE(g != nullptr, DM_ERR_INVALID, "null gradient buffers");
+  DM_REQUIRE(g->wq && g->wk && g->wv && g->wo && g->w_kctx && g->w_vctx && g->w_gk && g->w_gv && g->b_gk &&
+                 g->b_gv && g->norm_ctx_w,
+             DM_ERR_INVALID, "null gradient buffer");
+  DM_REQUIRE(!mult || c->ctx_mod == DM_CTX_FUSION || (g->v_gate && g->b_vgate && g->v_map), DM_ERR_INVALID,
+             "mult family needs v_gate/v_map grads");
+  DM_REQUIRE(c->ctx_mod != DM_CTX_FUSION || g->v_pre, DM_ERR_INVALID, "ctx_mod fusion needs the v_pre grad");
+  DM_REQUIRE(w->attn_norm_w == nullptr || (g->attn_norm_w && L->xhat), DM_ERR_INVALID,
+             "attn_norm needs its gradient buffer and bufs->xhat");
+  return DM_OK;
+}
+
+int run_bwd(const dm_config* c, const dm_packed* w, const BwdCall& call, void* stream) {
   hipStream_t s = S(stream);
-  rc = c->dtype == DM_BF16 ? layer_bwd_dispatch<bf16>(c, w, x, dy, dx, cos, sin, L, sched, n_cells, K_cache, V_cache,
-                                                      cache_T, ocat, tape, tape_bytes, g, workspace, kmax, s)
-                           : layer_bwd_dispatch<float>(c, w, x, dy, dx, cos, sin, L, sched, n_cells, K_cache, V_cache,
-                                                       cache_T, ocat, tape, tape_bytes, g, workspace, kmax, s);
+  const int rc = c->dtype == DM_BF16 ? bwd_dispatch<bf16>(c, w, call, s) : bwd_dispatch<float>(c, w, call, s);
   if (rc) return rc;
   DM_HIP(hipGetLastError());
   return DM_OK;
+}
+}  // namespace dm
+
+extern "C" {
+
+int dm_layer_bwd(const dm_config* c, const dm_packed* w, const void* x, const void* dy, void* dx,
+                 const float* cos, const float* sin, const dm_layer_bufs* L, const int32_t* sched,
+                 int32_t n_cells, const void* K_cache, const void* V_cache, int32_t cache_T, const void* ocat,
+                 const void* tape, size_t tape_bytes, const dm_grads* g, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  int kmax = 0;
+  int rc = check_bwd_common(c, w, L, sched, n_cells, cache_T, workspace, workspace_bytes, &kmax);
+  if (rc) return rc;
+  DM_REQUIRE(x && dy && dx && cos && sin && K_cache && V_cache && ocat, DM_ERR_INVALID, "null backward argument");
+  if ((rc = check_grads(c, w, L, g))) return rc;
+  BwdCall call{BWD_LAYER, x, dy, dx, ocat, cos, sin, L, sched, n_cells, 0, K_cache, V_cache, cache_T, tape,
+               tape_bytes, GradCache{}, g, workspace, kmax};
+  return run_bwd(c, w, call, stream);
+}
+
+int dm_layer_bwd_begin(const dm_config* c, const dm_packed* w, const void* dy, const void* ocat,
+                       const dm_layer_bufs* L, const int32_t* sched, int32_t n_cells, int32_t cache_T,
+                       const dm_grads* g, void* workspace, size_t workspace_bytes, void* stream) {
+  int kmax = 0;
+  int rc = check_bwd_common(c, w, L, sched, n_cells, cache_T, workspace, workspace_bytes, &kmax);
+  if (rc) return rc;
+  DM_REQUIRE(dy && ocat, DM_ERR_INVALID, "null dy / ocat");
+  if ((rc = check_grads(c, w, L, g))) return rc;
+  BwdCall call{BWD_BEGIN, nullptr, dy, nullptr, ocat, nullptr, nullptr, L, sched, n_cells, 0, nullptr, nullptr,
+               cache_T, nullptr, 0, GradCache{}, g, workspace, kmax};
+  return run_bwd(c, w, call, stream);
+}
+
+int dm_cell_bwd(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const float* cos, const float* sin,
+                const dm_cell_bwd_args* a, void* stream) {
+  DM_REQUIRE(a != nullptr, DM_ERR_INVALID, "null cell backward arguments");
+  int kmax = 0;
+  int rc = check_bwd_common(c, w, L, a->sched, a->n_cells, a->cache_T, a->workspace, a->workspace_bytes, &kmax);
+  if (rc) return rc;
+  DM_REQUIRE(a->cell >= 0 && a->cell < a->n_cells, DM_ERR_INVALID, "cell %d of %d", a->cell, a->n_cells);
+  DM_REQUIRE(cos && sin && a->K_cache && a->V_cache && a->dK_gc && a->dV_gc, DM_ERR_INVALID,
+             "null cell backward argument");
+  DM_REQUIRE(aligned16(a->K_cache) && aligned16(a->V_cache) && aligned16(a->dK_gc) && aligned16(a->dV_gc),
+             DM_ERR_INVALID, "caches must be 16-byte aligned");
+  BwdCall call{BWD_CELL, nullptr, nullptr, nullptr, nullptr, cos, sin, L, a->sched, a->n_cells, a->cell, a->K_cache,
+               a->V_cache, a->cache_T, a->tape, a->tape_bytes, GradCache{a->dK_gc, a->dV_gc}, nullptr,
+               a->workspace, kmax};
+  return run_bwd(c, w, call, stream);
+}
+
+int dm_layer_bwd_end(const dm_config* c, const dm_packed* w, const void* x, const void* dy, void* dx,
+                     const float* cos, const float* sin, const dm_layer_bufs* L, const int32_t* sched,
+                     int32_t n_cells, const void* K_cache, const void* V_cache, int32_t cache_T, const void* tape,
+                     size_t tape_bytes, const dm_grads* g, void* workspace, size_t workspace_bytes, void* stream) {
+  int kmax = 0;
+  int rc = check_bwd_common(c, w, L, sched, n_cells, cache_T, workspace, workspace_bytes, &kmax);
+  if (rc) return rc;
+  DM_REQUIRE(x && dy && dx && cos && sin && K_cache && V_cache, DM_ERR_INVALID, "null backward argument");
+  if ((rc = check_grads(c, w, L, g))) return rc;
+  BwdCall call{BWD_END, x, dy, dx, nullptr, cos, sin, L, sched, n_cells, 0, K_cache, V_cache, cache_T, tape,
+               tape_bytes, GradCache{}, g, workspace, kmax};
+  return run_bwd(c, w, call, stream);
 }
 
 }  // extern "C"

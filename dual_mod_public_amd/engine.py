@@ -324,6 +324,73 @@ class HipSweepCell:
             ctypes.byref(g), L.ptr(work), work.numel(), L.stream_ptr()))
         return dx
 
+    # ---- the backward one cell at a time (the reference engine's protocol) -----------
+    # FusedSweepCell.layer_blockmlp_bwd / cell_backward / layer_close (fused_sweep.py:1557-1959)
+    # with the fp32 grad cache of engines/wavescan/engine/backward.py:92-123. Call
+    # layer_backward_begin, then cell_backward for every cell from the last to the first, then
+    # layer_backward_end, with the same schedule, caches, tape and grads; the results equal
+    # layer_backward's to fp32 rounding.
+
+    def layer_backward_begin(self, dy, ocat, bufs, schedule, K_cache, grads, normalize=True, residual=True):
+        """Zero the layer accumulators; W_O VJP (adds dW_O into ``grads``)."""
+        self._bw = dict(schedule=list(schedule), sched=_sched(schedule), conf=self._conf(residual),
+                        ws=self.w.struct(with_attn_norm=normalize), normalize=normalize,
+                        work=self._bwd_workspace(bufs.T, K_cache.shape[2], max(k for _, _, k in schedule)))
+        bw = self._bw
+        b = bufs.struct()
+        g = grads.struct(with_attn_norm=normalize)
+        L.check(L.lib().dm_layer_bwd_begin(
+            ctypes.byref(bw["conf"]), ctypes.byref(bw["ws"]), L.ptr(dy), L.ptr(ocat), ctypes.byref(b), bw["sched"],
+            len(bw["schedule"]), K_cache.shape[2], ctypes.byref(g), L.ptr(bw["work"]), bw["work"].numel(),
+            L.stream_ptr()))
+
+    def cell_backward(self, bufs, cos, sin, K_cache, V_cache, cell, dK_gc, dV_gc, tape=None):
+        """fused_sweep.py:1557 cell_backward: cell ``cell`` of the schedule given to
+        layer_backward_begin. Its final rows' grads are dK_gc / dV_gc[:, :, pos0:pos0+c] (fp32
+        [B, h, cache_T, dh], accumulated by the later cells); the grads of the committed rows it
+        read are ADDED into dK_gc / dV_gc[:, :, :pos0]."""
+        bw = self._bw
+        cos, sin = _f32(cos, self.device), _f32(sin, self.device)
+        assert dK_gc.dtype == torch.float32 and dK_gc.is_contiguous() and dV_gc.is_contiguous()
+        a = L.dm_cell_bwd_args()
+        a.sched, a.n_cells, a.cell, a.cache_T = bw["sched"], len(bw["schedule"]), cell, K_cache.shape[2]
+        a.K_cache, a.V_cache, a.dK_gc, a.dV_gc = L.ptr(K_cache), L.ptr(V_cache), L.ptr(dK_gc), L.ptr(dV_gc)
+        a.tape, a.tape_bytes = L.ptr(tape), 0 if tape is None else tape.numel()
+        a.workspace, a.workspace_bytes = L.ptr(bw["work"]), bw["work"].numel()
+        b = bufs.struct()
+        L.check(L.lib().dm_cell_bwd(ctypes.byref(bw["conf"]), ctypes.byref(bw["ws"]), ctypes.byref(b), L.ptr(cos),
+                                    L.ptr(sin), ctypes.byref(a), L.stream_ptr()))
+
+    def layer_backward_end(self, x, dy, dx, cos, sin, bufs, K_cache, V_cache, grads, tape=None):
+        """fused_sweep.py:1873-1959 layer_close: sweep weight grads, projection and attn_norm VJP;
+        writes dx and adds the remaining parameter grads into ``grads``."""
+        bw = self._bw
+        cos, sin = _f32(cos, self.device), _f32(sin, self.device)
+        b = bufs.struct()
+        g = grads.struct(with_attn_norm=bw["normalize"])
+        L.check(L.lib().dm_layer_bwd_end(
+            ctypes.byref(bw["conf"]), ctypes.byref(bw["ws"]), L.ptr(x), L.ptr(dy), L.ptr(dx), L.ptr(cos), L.ptr(sin),
+            ctypes.byref(b), bw["sched"], len(bw["schedule"]), L.ptr(K_cache), L.ptr(V_cache), K_cache.shape[2],
+            L.ptr(tape), 0 if tape is None else tape.numel(), ctypes.byref(g), L.ptr(bw["work"]),
+            bw["work"].numel(), L.stream_ptr()))
+        self._bw = None
+        return dx
+
+
+def layer_backward_cells(cell, x, dy, dx, cos, sin, schedule, K_cache, V_cache, ocat, bufs, grads, tape=None,
+                         normalize=True, residual=True):
+    """engines/wavescan/engine/backward.py:92-123 (layer_backward) on the HIP cells: the
+    reverse scan one cell at a time through a zeroed fp32 grad cache dK / dV [B, h, cache_T, dh],
+    which ends up holding every cache row's grad from the later rows that read it. Returns dx
+    and the grad cache."""
+    dK = torch.zeros(K_cache.shape, device=K_cache.device, dtype=torch.float32)
+    dV = torch.zeros_like(dK)
+    cell.layer_backward_begin(dy, ocat, bufs, schedule, K_cache, grads, normalize=normalize, residual=residual)
+    for ci in reversed(range(len(schedule))):
+        cell.cell_backward(bufs, cos, sin, K_cache, V_cache, ci, dK, dV, tape=tape)
+    cell.layer_backward_end(x, dy, dx, cos, sin, bufs, K_cache, V_cache, grads, tape=tape)
+    return dx, dK, dV
+
 
 def chunk_cell_forward(attn, xhat_c, cos_c, sin_c, K_comm, V_comm, n_sweeps, intra_mask=None):
     """scan_cell_fwd.py:88-116 signature: one chunk against a committed prefix.

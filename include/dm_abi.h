@@ -210,6 +210,45 @@ int dm_layer_bwd(const dm_config* cfg, const dm_packed* w, const void* x, const 
                  const void* ocat, const void* tape, size_t tape_bytes, const dm_grads* g,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- the same backward one cell at a time --------------------------------------------
+ * The reference's engine drives the backward per cell (FusedSweepCell.layer_blockmlp_bwd,
+ * cell_backward, layer_close: engines/wavescan/cells/fused_sweep.py:1557-1959, called from
+ * engines/wavescan/engine/graphs.py:373-389) with an fp32 grad cache over the K/V rows
+ * (engines/wavescan/engine/backward.py:92-123). These three calls do that:
+ *   dm_layer_bwd_begin  zero the layer accumulators in `workspace`; W_O VJP (do_cat, dW_O += into g)
+ *   dm_cell_bwd         one cell, called for cell = n_cells-1 .. 0 in that order: reads the grads of
+ *                       its final rows from dK_gc / dV_gc rows [pos0, pos0+c) (complete once every
+ *                       later cell ran), runs its sweeps backward (states from `tape`, or an exact
+ *                       recompute when tape == NULL), and ADDS the grads of the committed rows
+ *                       [0, pos0) it read into dK_gc / dV_gc; its rows' weight-grad operands and
+ *                       projection grads stay in `workspace`
+ *   dm_layer_bwd_end    sweep weight grads, projection VJP, attn_norm VJP: dx and the rest of g
+ * Same arguments and results as dm_layer_bwd (dx, the ADDED grads), with one workspace
+ * (dm_layer_bwd_workspace_bytes) and the same schedule / tape passed to all three. The caller
+ * zeroes dK_gc / dV_gc (fp32 [B, h, cache_T, dh]) before the first cell. dm_layer_bwd computes
+ * the committed-prefix grads without the running cache (per key cell, from every later row):
+ * the results agree to fp32 rounding; the per-cell form reads and writes the cache once per
+ * cell, O(T^2) bytes per layer. */
+typedef struct dm_cell_bwd_args {
+  const int32_t* sched; int32_t n_cells;  /* the layer's schedule (as given to dm_layer_fwd) */
+  int32_t cell;                           /* index of this cell in sched */
+  int32_t cache_T;
+  const void* K_cache; const void* V_cache;   /* the forward's final rows [B, h, cache_T, dh] */
+  float* dK_gc; float* dV_gc;             /* fp32 grad cache [B, h, cache_T, dh] */
+  const void* tape; size_t tape_bytes;    /* the layer forward's tape, or NULL (recompute) */
+  void* workspace; size_t workspace_bytes;
+} dm_cell_bwd_args;
+int dm_layer_bwd_begin(const dm_config* cfg, const dm_packed* w, const void* dy, const void* ocat,
+                       const dm_layer_bufs* bufs, const int32_t* sched, int32_t n_cells, int32_t cache_T,
+                       const dm_grads* g, void* workspace, size_t workspace_bytes, void* stream);
+int dm_cell_bwd(const dm_config* cfg, const dm_packed* w, const dm_layer_bufs* bufs, const float* cos,
+                const float* sin, const dm_cell_bwd_args* a, void* stream);
+int dm_layer_bwd_end(const dm_config* cfg, const dm_packed* w, const void* x, const void* dy, void* dx,
+                     const float* cos, const float* sin, const dm_layer_bufs* bufs, const int32_t* sched,
+                     int32_t n_cells, const void* K_cache, const void* V_cache, int32_t cache_T,
+                     const void* tape, size_t tape_bytes, const dm_grads* g, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
 /* ---- decode ------------------------------------------------------------------
  * Replaces DualModAttention.decode_step (attention.py:564-588) on a static tape
  * (lm/eval/graph_decode.py:33-51): one token per batch row at position pos.
