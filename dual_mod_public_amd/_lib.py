@@ -67,7 +67,8 @@ class dm_layer_bufs(ctypes.Structure):
 class dm_cell_args(ctypes.Structure):
     _fields_ = [("pos0", c_i32), ("c", c_i32), ("n_sweeps", c_i32), ("cache_T", c_i32),
                 ("K_cache", c_vp), ("V_cache", c_vp), ("ocat", c_vp), ("o_last", c_vp),
-                ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t), ("K_rows", c_vp),
+                ("V_rows", c_vp), ("rows_T", c_i32), ("reserved_", c_i32)]
 
 
 class dm_cell_bwd_args(ctypes.Structure):
@@ -115,6 +116,11 @@ SIGNATURES = {
                                       P(dm_decode_args), c_vp]),
     "dm_decode_step_noalloc": (ctypes.c_int, [P(dm_config), P(dm_packed), c_fp, c_fp,
                                               P(dm_decode_args), c_vp]),
+    "dm_attend_one": (ctypes.c_int, [P(dm_config), c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp,
+                                     ctypes.c_size_t, c_vp]),
+    "dm_refine_kv_workspace_bytes": (ctypes.c_size_t, [P(dm_config), c_i32]),
+    "dm_refine_kv": (ctypes.c_int, [P(dm_config), P(dm_packed), P(dm_layer_bufs), c_vp, c_fp, c_fp, c_vp, c_vp,
+                                    c_vp, ctypes.c_size_t, c_vp]),
     "dm_linear": (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp]),
     "dm_gemm": (ctypes.c_int, [c_i32, c_i32, c_i32, c_vp, c_vp, c_fp, c_i32, c_i32, c_i32, c_i32,
                                c_vp]),

@@ -108,6 +108,64 @@ class DualModAttention(nn.Module):
         return dm_layer(xhat, cell, params, cos[:T], sin[:T], uniform_chunks(T, self.CHUNK, n_sweeps),
                         normalize=False, residual=False)
 
+    # ---- the per-position step as two calls (attention.py:283-434) --------------
+    def attend_one(self, q_r, k_self_r, v_self, K_past, V_past, need_probs=False, collect=None):
+        """attention.py:283-312 on the HIP decode read (dm_attend_one): q_r, k_self_r, v_self
+        [B,h,1,dh]; K_past / V_past [B,h,P,dh] refined rows (None or empty for none; a
+        ``cache[:, :, :P]`` view of a contiguous cache is read in place). The config's
+        local_window keeps the last W-1 rows. Returns (o [B,h,1,dh], None)."""
+        if need_probs or collect is not None:
+            raise NotImplementedError("attention probabilities / telemetry are not materialised on the HIP path")
+        from .engine import _row_stride
+        B, h, _, dh = q_r.shape
+        dt = q_r.dtype
+        P = 0 if K_past is None else K_past.shape[2]
+        conf = L.make_config(self.cfg, B, dt)
+        q, ks, vs = (t.reshape(B, h, dh).contiguous() for t in (q_r, k_self_r, v_self))
+        past_T = P
+        if P:
+            past_T = _row_stride(K_past, P)
+            if _row_stride(V_past, P) != past_T:
+                raise ValueError("K_past and V_past must have the same layout")
+        o = torch.empty(B, h, dh, device=q_r.device, dtype=dt)
+        import ctypes
+        n = L.lib().dm_decode_workspace_bytes(ctypes.byref(conf), max(P, 1))
+        ws = torch.empty(n, device=q_r.device, dtype=torch.uint8)
+        L.check(L.lib().dm_attend_one(ctypes.byref(conf), L.ptr(q), L.ptr(ks), L.ptr(vs),
+                                      L.ptr(K_past) if P else None, L.ptr(V_past) if P else None, P, past_T,
+                                      L.ptr(o), L.ptr(ws), n, L.stream_ptr()))
+        return o.reshape(B, h, 1, dh), None
+
+    def refine_kv(self, xhat, o_cat, k_raw, v_raw, collect=None):
+        """attention.py:314-434 on the HIP sweep GEMMs and their epilogues (dm_refine_kv): all
+        inputs [B,t,d]; returns the UNROTATED (k'', v'') [B,t,d], as the reference (the caller
+        rotates at write)."""
+        if collect is not None:
+            raise NotImplementedError("telemetry collection is not supported on the HIP path")
+        import ctypes
+        B, t, d = xhat.shape
+        h, dh = self.n_heads, self.head_dim
+        dt, dev = xhat.dtype, xhat.device
+        cell = self._hip_cell(B, t, dt)
+        bufs = cell.new_bufs(t)
+        # identity RoPE tables: the projection's rotated q / k rows are not used here, and the
+        # refined key comes back unrotated
+        one = torch.ones(t, dh // 2, device=dev, dtype=torch.float32)
+        zero = torch.zeros_like(one)
+        cell.layer_proj(xhat.contiguous(), bufs, one, zero, normalize=False)
+        bufs.kraw.copy_(k_raw.reshape(B, t, h, dh).transpose(1, 2))
+        bufs.vraw.copy_(v_raw.reshape(B, t, h, dh).transpose(1, 2))
+        K = torch.empty(B, h, t, dh, device=dev, dtype=dt)
+        V = torch.empty_like(K)
+        conf = cell.conf
+        n = L.lib().dm_refine_kv_workspace_bytes(ctypes.byref(conf), t)
+        ws = torch.empty(n, device=dev, dtype=torch.uint8)
+        L.check(L.lib().dm_refine_kv(ctypes.byref(conf), ctypes.byref(cell.w.struct(with_attn_norm=False)),
+                                     ctypes.byref(bufs.struct()), L.ptr(o_cat.contiguous()), L.ptr(one),
+                                     L.ptr(zero), L.ptr(K), L.ptr(V), L.ptr(ws), n, L.stream_ptr()))
+        merge = lambda z: z.transpose(1, 2).reshape(B, t, d)   # noqa: E731
+        return merge(K), merge(V)
+
     # ---- incremental decode (attention.py:564-588) ------------------------------
     @torch.no_grad()
     def decode_step(self, xhat_j, pos, cache, cos, sin):

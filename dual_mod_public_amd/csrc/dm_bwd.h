@@ -118,7 +118,7 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
   const int m = idx / per_row, rem = idx - m * per_row;
   const int hd = rem / (DH / 2), jj = rem - hd * (DH / 2);
   const int b = m / g.c, p = m - b * g.c;
-  const int t = g.buf_t0 + p, pos = g.pos0 + p;
+  const int t = g.buf_t0 + p, pos = rope_row(g, p);
   const long bh = (long)b * h + hd;
   const long drow = bh * a.dk_stride + (long)(a.dk_row0 + p) * DH;
   const long lrow = (bh * g.Tbuf + t) * DH;

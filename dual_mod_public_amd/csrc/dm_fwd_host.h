@@ -190,18 +190,35 @@ int run_comm(const CellGeom& g, const T* qr, const T* Kc, const T* Vc, float sca
   return cp.nsplit;
 }
 
+// Where a cell without saved state keeps its intra rows: by default the chunk's own cache rows
+// [pos0, pos0 + cc) (refined in place, the last sweep leaving the final rows there); a caller
+// that holds the committed prefix apart from the new rows (chunk_cell_forward's K_comm / V_comm)
+// gives a separate row buffer.
+template <typename T> struct CellRows {
+  T* K = nullptr; T* V = nullptr;   // nullptr: the cache rows
+  long stride = 0;                  // elements between (b, h) row blocks
+  int row0 = 0;                     // row of chunk row 0
+  int rope_t0 = -1;                 // RoPE table row of chunk row 0 (-1: pos0)
+};
+
 // One chunk cell [pos0, pos0+cc) of the layer: n_sweeps Jacobi sweeps against the
 // committed rows [0, pos0) of the cache. Without `sv` the sweeps refine the
-// chunk's cache rows in place and the last sweep leaves the final rows there;
-// with `sv` every sweep's rows and state are kept in sv (cache rows untouched).
+// chunk's rows in place (the cache rows, or `rows`) and the last sweep leaves the final rows
+// there; with `sv` every sweep's rows and state are kept in sv (cache rows untouched).
 template <typename T, int DH>
 void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const float* cos,
               const float* sin, int pos0, int cc, int n_sweeps, int buf_t0, int Tbuf, T* Kc, T* Vc,
-              int cache_T, T* ocat, float* o_last, const CellWs& ws, const CellSave<T>* sv, hipStream_t s) {
+              int cache_T, T* ocat, float* o_last, const CellWs& ws, const CellSave<T>* sv, hipStream_t s,
+              const CellRows<T>& rows = CellRows<T>{}) {
   CellGeom g{c->B, cc, c->d, c->h, DH, pos0, buf_t0, Tbuf, cache_T};
   g.kmod_cols = c->kmod_vraw_heads * DH;
   g.kmod_mode = c->kmod_mode;
   g.v_clamp_tau = c->v_clamp_tau;
+  g.rope_t0 = rows.rope_t0;
+  T* Kr = rows.K ? rows.K : Kc;
+  T* Vr = rows.K ? rows.V : Vc;
+  const long rows_stride = rows.K ? rows.stride : (long)cache_T * DH;
+  const int rows_row0 = rows.K ? rows.row0 : pos0;
   const int BH = c->B * c->h;
   const int N = c->B * cc;
   const size_t NS = (size_t)N, d = c->d;   // per-sweep row stride of the saved arrays
@@ -222,7 +239,7 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
   auto rows_in = [&](int sw, const T*& Kin, const T*& Vin, long& in_stride, int& in_row0) {
     if (sw == 0) { Kin = kself; Vin = vraw; in_stride = (long)Tbuf * DH; in_row0 = buf_t0; }
     else if (sv) { Kin = sv->Kin + sw * slot; Vin = sv->Vin + sw * slot; in_stride = ws_stride; in_row0 = 0; }
-    else { Kin = Kc; Vin = Vc; in_stride = cache_stride; in_row0 = pos0; }
+    else { Kin = Kr; Vin = Vr; in_stride = rows_stride; in_row0 = rows_row0; }
   };
   auto attend_args = [&](int sw) {
     const bool last = sw == n_sweeps - 1;
@@ -242,7 +259,8 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
     // rows written by this sweep's refine
     T* Kout; T* Vout; long out_stride; int out_row0;
     if (sv && !(last && sv->last_to_cache)) { Kout = sv->Kin + (sw + 1) * slot; Vout = sv->Vin + (sw + 1) * slot; out_stride = ws_stride; out_row0 = 0; }
-    else { Kout = Kc; Vout = Vc; out_stride = cache_stride; out_row0 = pos0; }
+    else if (sv) { Kout = Kc; Vout = Vc; out_stride = cache_stride; out_row0 = pos0; }
+    else { Kout = Kr; Vout = Vr; out_stride = rows_stride; out_row0 = rows_row0; }
 
     T* o = sv ? sv->o + sw * NS * d : (T*)ws.o;
     float* ssq = sv ? sv->ssq + sw * NS * c->h : ws.ssq;
@@ -265,13 +283,13 @@ template <typename T>
 void run_cell_dispatch(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const float* cos,
                        const float* sin, int pos0, int cc, int n_sweeps, int buf_t0, int Tbuf, void* Kc,
                        void* Vc, int cache_T, void* ocat, float* o_last, const CellWs& ws,
-                       const CellSave<T>* sv, hipStream_t s) {
+                       const CellSave<T>* sv, hipStream_t s, const CellRows<T>& rows = CellRows<T>{}) {
   if (c->dh == 64)
     run_cell<T, 64>(c, w, L, cos, sin, pos0, cc, n_sweeps, buf_t0, Tbuf, (T*)Kc, (T*)Vc, cache_T, (T*)ocat,
-                    o_last, ws, sv, s);
+                    o_last, ws, sv, s, rows);
   else
     run_cell<T, 128>(c, w, L, cos, sin, pos0, cc, n_sweeps, buf_t0, Tbuf, (T*)Kc, (T*)Vc, cache_T, (T*)ocat,
-                     o_last, ws, sv, s);
+                     o_last, ws, sv, s, rows);
 }
 
 inline int check_bufs(const dm_config* c, const dm_layer_bufs* L) {

@@ -269,7 +269,10 @@ struct CellGeom {
   int kmod_cols = 0;   // value columns [0, kmod_cols) belong to kmod heads (kmod_vraw_heads * dh)
   int kmod_mode = 0;   // dm_kmod_mode of those columns
   float v_clamp_tau = 0.f;   // v'' norm clamp radius per (row, head), 0 = off
+  int rope_t0 = -1;    // RoPE table row of chunk row 0 (-1: pos0, tables indexed by position)
 };
+// RoPE table row of chunk row p
+DM_DEV int rope_row(const CellGeom& g, int p) { return (g.rope_t0 < 0 ? g.pos0 : g.rope_t0) + p; }
 
 // ---------------------------------------------------------------------------
 // v'' entry-norm clamp (attention.py:389-402): v <- v min(1, tau / ||v||) over each
@@ -629,7 +632,7 @@ template <typename T, int DH> struct EpiSweep1 {
     const int d = g.d, h = g.h;
     const int m = min(m0 + r, M - 1);
     const int b = m / g.c, p = m - b * g.c;
-    const int t = g.buf_t0 + p, pos = g.pos0 + p;
+    const int t = g.buf_t0 + p, pos = rope_row(g, p);
     const long xrow = (long)b * g.Tbuf + t;
     // The (block-uniform) branches only pick addresses; the loads follow them
     // unconditionally (unused slots re-read a valid address), so no loaded value

@@ -172,22 +172,48 @@ int dm_cell_fwd(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, 
   DM_REQUIRE(a != nullptr && cos && sin, DM_ERR_INVALID, "null cell args / rope tables");
   DM_REQUIRE(a->c >= 1 && a->c <= CMAX, DM_ERR_UNSUPPORTED, "chunk length c=%d (1..%d)", a->c, CMAX);
   DM_REQUIRE(a->n_sweeps >= 1, DM_ERR_INVALID, "n_sweeps=%d", a->n_sweeps);
-  DM_REQUIRE(a->pos0 >= 0 && a->pos0 + a->c <= L->T && L->T <= a->cache_T, DM_ERR_INVALID,
-             "pos0=%d c=%d T=%d cache_T=%d", a->pos0, a->c, L->T, a->cache_T);
-  DM_REQUIRE(a->K_cache && a->V_cache && aligned16(a->K_cache) && aligned16(a->V_cache), DM_ERR_INVALID,
-             "K/V cache must be non-null and 16-byte aligned");
   DM_REQUIRE(c->local_window == 0, DM_ERR_UNSUPPORTED, "local_window is decode-only");
-  const CellWs need = carve_cell(c, a->cache_T, nullptr);
+  const bool local = a->K_rows != nullptr;
+  if (local) {
+    // chunk-local form: layer buffer row p, RoPE table row p and ocat row p belong to chunk row p;
+    // the committed prefix is K_cache / V_cache rows [0, pos0); the rows go to K_rows / V_rows
+    DM_REQUIRE(a->pos0 >= 0 && a->c <= L->T && a->pos0 <= a->cache_T && a->c <= a->rows_T, DM_ERR_INVALID,
+               "pos0=%d c=%d T=%d cache_T=%d rows_T=%d", a->pos0, a->c, L->T, a->cache_T, a->rows_T);
+    DM_REQUIRE(a->pos0 == 0 || (a->K_cache && a->V_cache && aligned16(a->K_cache) && aligned16(a->V_cache)),
+               DM_ERR_INVALID, "committed K/V must be non-null and 16-byte aligned");
+    DM_REQUIRE(a->V_rows && aligned16(a->K_rows) && aligned16(a->V_rows), DM_ERR_INVALID,
+               "K/V rows must be non-null and 16-byte aligned");
+  } else {
+    DM_REQUIRE(a->pos0 >= 0 && a->pos0 + a->c <= L->T && L->T <= a->cache_T, DM_ERR_INVALID,
+               "pos0=%d c=%d T=%d cache_T=%d", a->pos0, a->c, L->T, a->cache_T);
+    DM_REQUIRE(a->K_cache && a->V_cache && aligned16(a->K_cache) && aligned16(a->V_cache), DM_ERR_INVALID,
+               "K/V cache must be non-null and 16-byte aligned");
+  }
+  const int cache_T = a->cache_T > 0 ? a->cache_T : 1;
+  // the committed-prefix splits scale with the committed rows (the chunk-local form's cache_T is
+  // only the stride of the caller's view); dm_cell_workspace_bytes(cfg, n) covers n >= pos0
+  const int carve_T = local ? std::max(a->pos0, 1) : cache_T;
+  const CellWs need = carve_cell(c, carve_T, nullptr);
   DM_REQUIRE(a->workspace && a->workspace_bytes >= need.bytes, DM_ERR_WORKSPACE,
              "workspace %zu < %zu bytes", a->workspace_bytes, need.bytes);
-  const CellWs ws = carve_cell(c, a->cache_T, a->workspace);
+  const CellWs ws = carve_cell(c, carve_T, a->workspace);
   hipStream_t s = S(stream);
-  if (c->dtype == DM_BF16)
-    run_cell_dispatch<bf16>(c, w, L, cos, sin, a->pos0, a->c, a->n_sweeps, a->pos0, L->T, a->K_cache,
-                            a->V_cache, a->cache_T, a->ocat, a->o_last, ws, nullptr, s);
-  else
-    run_cell_dispatch<float>(c, w, L, cos, sin, a->pos0, a->c, a->n_sweeps, a->pos0, L->T, a->K_cache,
-                             a->V_cache, a->cache_T, a->ocat, a->o_last, ws, nullptr, s);
+  const int buf_t0 = local ? 0 : a->pos0;
+  auto run = [&](auto tag) {
+    using T = decltype(tag);
+    CellRows<T> rows;
+    if (local) {
+      rows.K = (T*)a->K_rows;
+      rows.V = (T*)a->V_rows;
+      rows.stride = (long)a->rows_T * c->dh;
+      rows.row0 = 0;
+      rows.rope_t0 = 0;
+    }
+    run_cell_dispatch<T>(c, w, L, cos, sin, a->pos0, a->c, a->n_sweeps, buf_t0, L->T, a->K_cache, a->V_cache,
+                         cache_T, a->ocat, a->o_last, ws, nullptr, s, rows);
+  };
+  if (c->dtype == DM_BF16) run(bf16{});
+  else run(float{});
   DM_HIP(hipGetLastError());
   return DM_OK;
 }
@@ -375,6 +401,130 @@ int dm_decode_step(const dm_config* c, const dm_packed* w, const float* cos, con
   else
     rc = c->dh == 64 ? run_decode<float, 64>(c, w, cos, sin, a, ws, s) : run_decode<float, 128>(c, w, cos, sin, a, ws, s);
   if (rc) return rc;
+  DM_HIP(hipGetLastError());
+  return DM_OK;
+}
+
+}  // extern "C"
+
+// ---- attend_one / refine_kv as separate calls --------------------------------------
+namespace dm {
+
+// per-(row, head) sums of squares of stored rows o [N, h * DH] -> ssq [N, h]
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_head_ssq(const T* __restrict__ o, long nrh, float* __restrict__ ssq) {
+  constexpr int V = 16 / (int)sizeof(T);
+  const long i = blockIdx.x * 256L + threadIdx.x;
+  if (i >= nrh) return;
+  const T* p = o + i * DH;   // row i / h, head i % h: d = h * DH
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < DH; e += V) {
+    float f[V];
+    unpack16<T>(*reinterpret_cast<const uint4*>(p + e), f);
+#pragma unroll
+    for (int j = 0; j < V; ++j) s += f[j] * f[j];
+  }
+  ssq[i] = s;
+}
+
+struct RefineWs {
+  float* ssq; void* vin; float* gvu;
+  size_t bytes;
+};
+inline RefineWs carve_refine(const dm_config* c, int t, void* base) {
+  RefineWs w{};
+  const size_t N = (size_t)c->B * t;
+  Carver cv(base);
+  w.ssq = cv.take<float>(N * c->h * 4);
+  w.vin = cv.take<void>(N * c->d * esz(c->dtype));
+  w.gvu = cv.take<float>(N * c->d * 4);
+  w.bytes = cv.off;
+  return w;
+}
+
+template <typename T, int DH>
+void run_attend_one(const dm_config* c, const void* q, const void* ks, const void* vs, const void* Kp, const void* Vp,
+                    int P, int past_T, void* o, const DecWs& ws, hipStream_t s) {
+  const int B = c->B, h = c->h, d = c->d;
+  const int lo = (c->local_window > 0 && P > c->local_window - 1) ? P - (c->local_window - 1) : 0;
+  const int nsplit = P > lo ? cdiv(P - lo, DEC_SPLIT) : 0;
+  DecodeArgs<T> da{B, h, d, past_T, P, lo, DEC_SPLIT, nsplit, 1.0f / sqrtf((float)DH), (const T*)q, (const T*)ks,
+                   (const T*)vs, (const T*)Kp, (const T*)Vp, ws.part, ws.o, ws.ssq, (T*)o, nullptr};
+  if (nsplit > 0)
+    hipLaunchKernelGGL((k_decode_partial<T, DH, DEC_SPLIT>), dim3(nsplit, B * h), dim3(256), 0, s, da);
+  hipLaunchKernelGGL((k_decode_merge<T, DH>), dim3(B * h), dim3(64), 0, s, da);
+}
+
+template <typename T, int DH>
+void run_refine_kv(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const void* o_cat,
+                   const float* cos, const float* sin, void* K_out, void* V_out, const RefineWs& ws, hipStream_t s) {
+  const int t = L->T, N = c->B * t;
+  const long nrh = (long)N * c->h;
+  hipLaunchKernelGGL((k_head_ssq<T, DH>), dim3(cdiv(nrh, 256)), dim3(256), 0, s, (const T*)o_cat, nrh, ws.ssq);
+  CellGeom g{c->B, t, c->d, c->h, DH, 0, 0, t, t};
+  g.kmod_cols = c->kmod_vraw_heads * DH;
+  g.kmod_mode = c->kmod_mode;
+  g.v_clamp_tau = c->v_clamp_tau;
+  g.rope_t0 = 0;
+  run_refine<T, DH>(c, w, g, N, (const T*)o_cat, ws.ssq, (const T*)L->kraw, (const T*)L->vraw, L->glogx, L->sig,
+                    cos, sin, (T*)K_out, (T*)V_out, (long)t * DH, 0, (T*)ws.vin, ws.gvu, nullptr, nullptr, s);
+}
+
+}  // namespace dm
+
+extern "C" {
+
+int dm_attend_one(const dm_config* c, const void* q_r, const void* k_self_r, const void* v_self, const void* K_past,
+                  const void* V_past, int32_t P, int32_t past_T, void* o, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  int rc = check_cfg(c);
+  if (rc) return rc;
+  DM_REQUIRE(q_r && k_self_r && v_self && o, DM_ERR_INVALID, "null attend_one argument");
+  DM_REQUIRE(P >= 0 && past_T >= P, DM_ERR_INVALID, "P=%d past_T=%d", P, past_T);
+  DM_REQUIRE(P == 0 || (K_past && V_past && aligned16(K_past) && aligned16(V_past)), DM_ERR_INVALID,
+             "K_past / V_past must be non-null and 16-byte aligned");
+  DM_REQUIRE(aligned16(q_r) && aligned16(k_self_r) && aligned16(v_self), DM_ERR_INVALID,
+             "q_r / k_self_r / v_self must be 16-byte aligned");
+  const DecWs need = carve_dec(c, P > 0 ? P : 1, nullptr);
+  DM_REQUIRE(workspace && workspace_bytes >= need.bytes, DM_ERR_WORKSPACE, "workspace %zu < %zu bytes",
+             workspace_bytes, need.bytes);
+  const DecWs ws = carve_dec(c, P > 0 ? P : 1, workspace);
+  hipStream_t s = S(stream);
+  if (c->dtype == DM_BF16)
+    c->dh == 64 ? run_attend_one<bf16, 64>(c, q_r, k_self_r, v_self, K_past, V_past, P, past_T, o, ws, s)
+                : run_attend_one<bf16, 128>(c, q_r, k_self_r, v_self, K_past, V_past, P, past_T, o, ws, s);
+  else
+    c->dh == 64 ? run_attend_one<float, 64>(c, q_r, k_self_r, v_self, K_past, V_past, P, past_T, o, ws, s)
+                : run_attend_one<float, 128>(c, q_r, k_self_r, v_self, K_past, V_past, P, past_T, o, ws, s);
+  DM_HIP(hipGetLastError());
+  return DM_OK;
+}
+
+size_t dm_refine_kv_workspace_bytes(const dm_config* c, int32_t t) {
+  if (check_cfg(c) != DM_OK || t <= 0) return 0;
+  return carve_refine(c, t, nullptr).bytes;
+}
+
+int dm_refine_kv(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const void* o_cat, const float* cos,
+                 const float* sin, void* K_out, void* V_out, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_cfg(c);
+  if (rc) return rc;
+  if ((rc = check_packed(c, w)) || (rc = check_bufs(c, L))) return rc;
+  DM_REQUIRE(o_cat && cos && sin && K_out && V_out, DM_ERR_INVALID, "null refine_kv argument");
+  DM_REQUIRE(aligned16(o_cat) && aligned16(K_out) && aligned16(V_out), DM_ERR_INVALID,
+             "o_cat / K_out / V_out must be 16-byte aligned");
+  const RefineWs need = carve_refine(c, L->T, nullptr);
+  DM_REQUIRE(workspace && workspace_bytes >= need.bytes, DM_ERR_WORKSPACE, "workspace %zu < %zu bytes",
+             workspace_bytes, need.bytes);
+  const RefineWs ws = carve_refine(c, L->T, workspace);
+  hipStream_t s = S(stream);
+  if (c->dtype == DM_BF16)
+    c->dh == 64 ? run_refine_kv<bf16, 64>(c, w, L, o_cat, cos, sin, K_out, V_out, ws, s)
+                : run_refine_kv<bf16, 128>(c, w, L, o_cat, cos, sin, K_out, V_out, ws, s);
+  else
+    c->dh == 64 ? run_refine_kv<float, 64>(c, w, L, o_cat, cos, sin, K_out, V_out, ws, s)
+                : run_refine_kv<float, 128>(c, w, L, o_cat, cos, sin, K_out, V_out, ws, s);
   DM_HIP(hipGetLastError());
   return DM_OK;
 }

@@ -242,13 +242,26 @@ class HipSweepCell:
         return bufs
 
     def cell_forward(self, bufs, cos, sin, K_cache, V_cache, pos0, c, n_sweeps, ocat=None,
-                     o_last=None):
+                     o_last=None, K_rows=None, V_rows=None):
         """fused_sweep.py:1455-1553 — one chunk [pos0, pos0+c), n_sweeps Jacobi sweeps.
         Writes the chunk's final rows into K_cache/V_cache and (optionally) its
-        o_cat rows into ocat [B, T, d] / the fp32 o_last [B*c, d]."""
+        o_cat rows into ocat [B, T, d] / the fp32 o_last [B*c, d].
+
+        With K_rows / V_rows [B, h, >= c, dh] (chunk-local form, chunk_cell_forward's
+        K_comm / V_comm): bufs, cos / sin and ocat hold only the chunk, K_cache / V_cache
+        are the committed rows [0, pos0) (a [B, h, :pos0] view of a larger cache is read in
+        place; None when pos0 == 0) and the chunk's rows go to K_rows / V_rows."""
         cos, sin = _f32(cos, self.device), _f32(sin, self.device)
         a = L.dm_cell_args()
-        a.pos0, a.c, a.n_sweeps, a.cache_T = pos0, c, n_sweeps, K_cache.shape[2]
+        a.pos0, a.c, a.n_sweeps = pos0, c, n_sweeps
+        if K_rows is not None:
+            a.cache_T = _row_stride(K_cache, pos0) if K_cache is not None else 0
+            if V_cache is not None and _row_stride(V_cache, pos0) != a.cache_T:
+                raise ValueError("K_comm and V_comm must have the same layout")
+            a.K_rows, a.V_rows = L.ptr(K_rows), L.ptr(V_rows)
+            a.rows_T = _row_stride(K_rows, c)
+        else:
+            a.cache_T = K_cache.shape[2]
         a.K_cache, a.V_cache = L.ptr(K_cache), L.ptr(V_cache)
         a.ocat, a.o_last = L.ptr(ocat), L.ptr(o_last)
         a.workspace, a.workspace_bytes = L.ptr(self.workspace), self.workspace.numel()
@@ -392,35 +405,42 @@ def layer_backward_cells(cell, x, dy, dx, cos, sin, schedule, K_cache, V_cache, 
     return dx, dK, dV
 
 
+def _row_stride(t, rows):
+    """Rows per (b, h) block of a [B, h, rows, dh] tensor that is contiguous or a leading-rows
+    view ``cache[:, :, :rows]`` of a contiguous [B, h, T, dh] cache (returns T); the kernels
+    read such views in place."""
+    B, h, n, dh = t.shape
+    if n < rows:
+        raise ValueError(f"{n} rows < {rows}")
+    st = t.stride()
+    if st[3] != 1 or st[2] != dh or st[1] % dh or st[0] != st[1] * h or st[1] // dh < n:
+        raise ValueError("expected a [B, h, rows, dh] tensor or a leading-rows view of a contiguous cache")
+    return st[1] // dh
+
+
 def chunk_cell_forward(attn, xhat_c, cos_c, sin_c, K_comm, V_comm, n_sweeps, intra_mask=None):
     """scan_cell_fwd.py:88-116 signature: one chunk against a committed prefix.
 
     attn: a dual_mod_public_amd.attention.DualModAttention. xhat_c [B,c,d];
     cos_c/sin_c: RoPE rows of the chunk's positions; K_comm/V_comm [B,h,a,dh]
-    (None or 0-length for the first chunk). Returns (o_cat [B,c,d],
-    K_rows [B,h,c,dh] rotated, V_rows [B,h,c,dh]). ``intra_mask`` is accepted
-    for signature compatibility; the kernels apply the strict-lower mask.
-    """
+    (None or 0-length for the first chunk; a ``cache[:, :, :a]`` view of a larger
+    contiguous cache is read in place). Returns (o_cat [B,c,d], K_rows [B,h,c,dh]
+    rotated, V_rows [B,h,c,dh]). Only the chunk's rows are projected and the committed
+    prefix is not copied: the cost is the cell's own, not O(a). ``intra_mask`` is
+    accepted for signature compatibility; the kernels apply the strict-lower mask."""
     B, c, d = xhat_c.shape
     a = 0 if K_comm is None else K_comm.shape[2]
-    cell = attn._hip_cell(B, a + c, xhat_c.dtype)
+    cell = attn._hip_cell(B, max(a, c), xhat_c.dtype)
     dev, dt = xhat_c.device, xhat_c.dtype
     h, dh = attn.n_heads, attn.head_dim
-    T = a + c
-    x = torch.zeros(B, T, d, device=dev, dtype=dt)
-    x[:, a:] = xhat_c
-    cos = torch.zeros(T, dh // 2, device=dev, dtype=torch.float32)
-    sin = torch.zeros_like(cos)
-    cos[a:], sin[a:] = cos_c.float(), sin_c.float()
-    Kc = torch.zeros(B, h, T, dh, device=dev, dtype=dt)
-    Vc = torch.zeros_like(Kc)
-    if a:
-        Kc[:, :, :a], Vc[:, :, :a] = K_comm, V_comm
-    bufs = cell.new_bufs(T)
-    cell.layer_proj(x, bufs, cos, sin, normalize=False)
-    ocat = torch.empty(B, T, d, device=dev, dtype=dt)
-    cell.cell_forward(bufs, cos, sin, Kc, Vc, a, c, n_sweeps, ocat=ocat)
-    return ocat[:, a:], Kc[:, :, a:], Vc[:, :, a:]
+    bufs = cell.new_bufs(c)
+    cell.layer_proj(xhat_c.contiguous(), bufs, cos_c, sin_c, normalize=False)
+    ocat = torch.empty(B, c, d, device=dev, dtype=dt)
+    K_rows = torch.empty(B, h, c, dh, device=dev, dtype=dt)
+    V_rows = torch.empty_like(K_rows)
+    cell.cell_forward(bufs, cos_c, sin_c, K_comm if a else None, V_comm if a else None, a, c, n_sweeps,
+                      ocat=ocat, K_rows=K_rows, V_rows=V_rows)
+    return ocat, K_rows, V_rows
 
 
 def layer_forward(attn, xhat, cos, sin, schedule, K_cache, V_cache, masks=None, o_out=None):

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DM_ABI_VERSION 3
+#define DM_ABI_VERSION 4
 
 typedef enum dm_status {
   DM_OK = 0,
@@ -148,13 +148,21 @@ int dm_layer_proj(const dm_config* cfg, const dm_packed* w, const void* x, const
  * layer, n_sweeps Jacobi sweeps against the committed rows [0, pos0) of K/V
  * cache, writing the chunk's final refined rows into the cache (append-only)
  * and the last sweep's o_cat into ocat[:, pos0:pos0+c] (storage dtype, [B,T,d]).
- * Requires 1 <= c <= 64, pos0 + c <= bufs->T <= cache_T. */
+ * Requires 1 <= c <= 64, pos0 + c <= bufs->T <= cache_T.
+ * Chunk-local form (K_rows != NULL, chunk_cell_forward's K_comm / V_comm arguments): bufs,
+ * the cos / sin rows and ocat hold only the chunk (row p = chunk row p, c <= bufs->T),
+ * K_cache / V_cache are the committed rows [0, pos0) alone ([B, h, cache_T, dh], pos0 <=
+ * cache_T; NULL when pos0 == 0), and the chunk's rows (rotated K, V) go to K_rows / V_rows
+ * [B, h, rows_T, dh] rows [0, c) instead of the cache. */
 typedef struct dm_cell_args {
   int32_t pos0, c, n_sweeps, cache_T;
   void* K_cache; void* V_cache;        /* [B, h, cache_T, dh] */
   void* ocat;                          /* [B, bufs->T, d] or NULL */
   float* o_last;                       /* [B*c, d] fp32 copy of the last sweep's o, or NULL */
   void* workspace; size_t workspace_bytes;
+  void* K_rows; void* V_rows;          /* chunk-local form: [B, h, rows_T, dh], else NULL */
+  int32_t rows_T;
+  int32_t reserved_;
 } dm_cell_args;
 size_t dm_cell_workspace_bytes(const dm_config* cfg, int32_t cache_T);
 int dm_cell_fwd(const dm_config* cfg, const dm_packed* w, const dm_layer_bufs* bufs,
@@ -283,6 +291,28 @@ int dm_decode_step(const dm_config* cfg, const dm_packed* w, const float* cos, c
 #define DM_DECODE_SCRATCH_MAX ((size_t)32 << 20)
 int dm_decode_step_noalloc(const dm_config* cfg, const dm_packed* w, const float* cos, const float* sin,
                            const dm_decode_args* a, void* stream);
+
+/* ---- the per-position step as two calls ------------------------------------------
+ * dm_attend_one replaces DualModAttention.attend_one (models/dualmod/attention.py:283-312):
+ * each batch row's rotated query q_r against its refined tape rows K_past / V_past
+ * [B, h, past_T, dh] (rows [max(0, P-W+1), P) with the config's local_window W, all P rows
+ * when W == 0) plus its own raw self column (k_self_r, v_self), fp32 softmax; q_r, k_self_r,
+ * v_self and the output o are [B, h, dh] (storage dtype). Workspace:
+ * dm_decode_workspace_bytes(cfg, P) bytes. */
+int dm_attend_one(const dm_config* cfg, const void* q_r, const void* k_self_r, const void* v_self,
+                  const void* K_past, const void* V_past, int32_t P, int32_t past_T, void* o,
+                  void* workspace, size_t workspace_bytes, void* stream);
+/* dm_refine_kv replaces DualModAttention.refine_kv (attention.py:314-434) for t rows of every
+ * batch row: u = RMSNorm_ctx(o_cat), the ctx projections, gates, value candidate, convex blends
+ * (+ kmod heads, v'' clamp). bufs (T = t rows) hold the rows' gate x-halves and v_gate term
+ * (glogx, sig: dm_layer_proj of xhat) and their raw key / value (kraw, vraw, [B, h, t, dh]);
+ * o_cat [B, t, d]. Writes k'' and v'' to K_out / V_out [B, h, t, dh], the key rotated with the
+ * cos / sin rows [t, dh/2] (identity tables give the reference's unrotated k''). Workspace:
+ * dm_refine_kv_workspace_bytes(cfg, t). */
+size_t dm_refine_kv_workspace_bytes(const dm_config* cfg, int32_t t);
+int dm_refine_kv(const dm_config* cfg, const dm_packed* w, const dm_layer_bufs* bufs, const void* o_cat,
+                 const float* cos, const float* sin, void* K_out, void* V_out, void* workspace,
+                 size_t workspace_bytes, void* stream);
 
 /* ---- linear layer -------------------------------------------------------------
  * y[M, N] = x[M, K] . W[N, K]^T (+ r[M, N] when r != NULL): nn.Linear without

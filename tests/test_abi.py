@@ -30,7 +30,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 
 def test_abi_version():
-    assert L.load().dm_abi_version() == 3
+    assert L.load().dm_abi_version() == 4
 
 
 def _conf(**kw):
