@@ -1,7 +1,7 @@
 """Benchmark of the Dual-Mod attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload fwdbwd|fwd]
-                    [--no-cpu-baseline] [--no-decode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload fwdbwd|fwd|c4]
+                    [--no-cpu-baseline] [--no-decode] [--no-c4]
 
 One step = one DM attention layer of the 340M shape (B=8, T=2048, d=1024,
 16 heads x 64, c=64, K=4 Jacobi sweeps chained over 32 chunks, bf16 storage /
@@ -9,22 +9,27 @@ fp32 accumulate) through libdm_hip.so: the forward (attn_norm + projections,
 the 32 chunk cells = committed accumulator + 4 sweeps each, W_O with the
 residual) and, for the default fwdbwd workload, the
 reverse-scan backward producing dx and every parameter gradient for an upstream
-dy ~ N(0,1). The forward keeps every cell's sweep states in an HBM tape (1.9 GB
+dy ~ N(0,1). The forward keeps every cell's sweep states in an HBM tape (1.2 GB
 for this layer) that the backward reads instead of recomputing them; the
-reference's exact-recompute mode (same values bit for bit) is timed beside it
-(--recompute makes it the headline). Inputs (x, dy, weights, RoPE tables) are
-resident in HBM before timing starts.
+reference's exact-recompute mode (same values bit for bit) is timed beside it in
+the same run and reported with the same fields ("recompute"; --recompute makes it
+the headline). Inputs (x, dy, weights, RoPE tables) are resident in HBM before
+timing starts.
 
-Prints ONE JSON line (rank 0): the headline sweep throughput in tokens/s, the
-roofline of the dominant kernel timed with HIP events inside the timed region,
-the path-level roofline, the CPU baseline (the oracle's chunked-Jacobi layer
-forward timed on this host's cores on a bounded sample) and the decode
-sub-benchmark (batch 64, bf16 tape of 32768 positions, HBM GB/s).
+Prints ONE JSON line: the headline sweep throughput in tokens/s, the roofline of
+the dominant kernel (sweep GEMM 1) timed with HIP events on its own stream inside a
+second pass of the timed steps, the path-level roofline, the config-4 K ladder (one
+layer of the d=2048 trunk, fwd+bwd for K in {1, 2, 4, 8}), the decode sub-benchmark
+(batch 64, bf16 tape of 32768 positions, HBM GB/s) and the CPU
+baselines (the oracle on this host's cores over bounded samples, warm-up then the
+median of 3).
 """
 
 import argparse
 import json
 import os
+import re
+import statistics
 import sys
 import time
 
@@ -36,29 +41,52 @@ sys.path.insert(0, REPO)
 from dual_mod_public_amd import _lib as L  # noqa: E402
 from dual_mod_public_amd.config import DualModConfig  # noqa: E402
 from dual_mod_public_amd.decode import StaticTape  # noqa: E402
-from dual_mod_public_amd.engine import HipSweepCell, uniform_chunks  # noqa: E402
+from dual_mod_public_amd.engine import HipSweepCell, LayerGrads, uniform_chunks  # noqa: E402
 from dual_mod_public_amd.rope import build_rope_cache  # noqa: E402
 from dual_mod_public_amd.synthetic import make_input, make_state_dict  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 COPY_CAL_BYTES = 256 << 20  # --copy-calibration: bytes read (and written) per copy dispatch
-# HBM bytes per launch of the roofline kernels (read + written), from rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE passes over this script (profiles/traffic_sweep1_decode.md has the commands and raw
-# readings), each scaled by what the counter reads for the 256 MiB --copy-calibration copy.
-# sweep1: the N = B*c = 512-row launches at C3 (tape mode); dec_read: launches at P = 32768..32783.
-TRAFFIC_BYTES = {"sweep1": 34.96e6, "dec_read": 8613.0e6}
-TIMING_NOTE = ("avg_launch_ms: per-dispatch span from the device clock (s_memrealtime, first block "
-               "start to last block end), recorded by the kernel itself over a second pass of the timed "
-               "steps (instrumented_ms_per_step); avg_launch_ms_events: HIP event pair around each launch "
-               "on its stream (adds queue time)")
+# HBM bytes per launch of the roofline kernels are read from the committed counter summary
+# (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over this script, each scaled by what the
+# counter reads for the 256 MiB --copy-calibration copy; the file has the commands).
+TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "traffic_sweep1_decode.md")
+TIMING_NOTE = ("avg_launch_ms: HIP event pair around each launch of the kernel on its own stream, "
+               "over a second pass of the timed steps (instrumented_ms_per_step); it includes the "
+               "dispatch and drain a kernel-trace profiler also counts, and the event packets' own "
+               "time; avg_launch_ms_device: first block start to last block end on the device clock "
+               "(s_memrealtime), the kernel's execution alone")
 
 # BASELINE config 2 (forward) — the 340M-shape DM layer
 C2 = dict(B=8, T=2048, d=1024, h=16, c=64, K=4, wseed=1, xseed=2)
-# BASELINE config 4 — one layer of the 24-layer d=2048 trunk (16 heads x 128), K from --sweeps
-C4 = dict(B=4, T=4096, d=2048, h=16, c=64, K=4, wseed=1, xseed=2)
+# BASELINE config 4 — one layer of the 24-layer d=2048 trunk (16 heads x 128), K ladder
+C4 = dict(B=4, T=4096, d=2048, h=16, c=64, K=4, wseed=1, xseed=2, ladder=(1, 2, 4, 8))
 # BASELINE config 5 — incremental decode
 C5 = dict(B=64, d=1024, h=16, P0=32768, steps=256, wseed=3, xseed=4, tseed=5)
+
+
+def traffic_from_profile(kernel):
+    """HBM bytes per launch of a kernel row ("| sweep1 | ... | <MB/launch> |") of the committed
+    counter summary, or None when the file or the row is missing."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(r"^\|\s*" + re.escape(kernel) + r"\s*\|(?:[^|\n]*\|){5}\s*([0-9.]+)\s*\|", text, re.M)
+    return float(m.group(1)) * 1e6 if m else None
+
+
+def host_info():
+    model = None
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"host_cpus": os.cpu_count(), "cpu_model": model}
 
 
 def fwd_flops_per_token(d, T, c, K, ctx_mod="mult_res"):
@@ -84,11 +112,11 @@ def sweep1_flops(N, d):
     return 2.0 * N * d * 4 * d
 
 
-def build_layer(cfg, B, T, dev):
-    sd = make_state_dict(cfg, seed=C2["wseed"])
+def build_layer(cfg, B, T, dev, seeds=C2):
+    sd = make_state_dict(cfg, seed=seeds["wseed"])
     cell = HipSweepCell(cfg, B, T, device=dev, dtype=torch.bfloat16)
     cell.pack({k: v.to(dev) for k, v in sd.items()})
-    x = make_input((B, T, cfg.d_model), seed=C2["xseed"]).to(dev, torch.bfloat16)
+    x = make_input((B, T, cfg.d_model), seed=seeds["xseed"]).to(dev, torch.bfloat16)
     cos, sin = build_rope_cache(T, cfg.head_dim, cfg.rope_theta, device=dev)
     bufs = cell.new_bufs(T)
     K = torch.zeros(B, cfg.n_heads, T, cfg.head_dim, device=dev, dtype=torch.bfloat16)
@@ -98,39 +126,97 @@ def build_layer(cfg, B, T, dev):
     return sd, cell, x, cos.contiguous(), sin.contiguous(), bufs, K, V, ocat, y
 
 
-def cpu_baseline(cfg, sd, T, B, fwdbwd, cpu_T=0):
-    """The oracle's chunked-Jacobi layer (same schedule, fp32 torch) on this host's cores:
-    forward only, or forward + autograd backward, over the whole workload or, with
-    cpu_T < T, a T-prefix sample (the same per-token work at a shorter committed prefix)."""
+def timed(fn, steps):
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def median_wall(fn, reps=3, warmup=1):
+    """One untimed warm-up call, then the median wall time of `reps` calls (and all of them)."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), ts
+
+
+def cpu_threads():
+    """Threads of the CPU baselines: every host core, capped at the 16 a one-GPU share of the box has."""
+    return min(os.cpu_count() or 1, 16)
+
+
+def cpu_baseline(cfg, sd, T, B, fwdbwd, cpu_T):
+    """The oracle's chunked-Jacobi layer (same schedule, fp32 torch) on this host's cores over a
+    T-prefix of the workload (the same per-token GEMM work, a shorter committed prefix), forward
+    or forward + autograd backward: one warm-up, then the median of 3."""
     import oracle as O
-    nthr = min(os.cpu_count() or 1, 16)
+    nthr = cpu_threads()
     torch.set_num_threads(nthr)
     Ts = min(T, cpu_T) if cpu_T else T
     x = make_input((B, Ts, cfg.d_model), seed=C2["xseed"])
     cos, sin = O.build_rope_cache(Ts, cfg.head_dim, cfg.rope_theta)
     sched = O.uniform_chunks(Ts, C2["c"], C2["K"])
-    if fwdbwd:
-        sdf = {k: v.float().clone().requires_grad_(True) for k, v in sd.items()}
-        x.requires_grad_(True)
-        dy = make_input((B, Ts, cfg.d_model), seed=C2["xseed"] + 100)
-        t0 = time.perf_counter()
-        y = O.dm_layer(cfg, sdf, x, cos, sin, schedule=sched)
-        (y * dy).sum().backward()
-        dt = time.perf_counter() - t0
-        span = "the whole workload" if Ts == T else f"T-prefix of {T}"
-        what = f"layer forward + autograd backward at B={B}, T={Ts} ({span}; c=64, K=4)"
-    else:
-        sdf = {k: v.float() for k, v in sd.items()}
+    dy = make_input((B, Ts, cfg.d_model), seed=C2["xseed"] + 100)
+
+    def run():
+        if fwdbwd:
+            sdf = {k: v.float().clone().requires_grad_(True) for k, v in sd.items()}
+            xg = x.clone().requires_grad_(True)
+            y = O.dm_layer(cfg, sdf, xg, cos, sin, schedule=sched)
+            (y * dy).sum().backward()
+        else:
+            with torch.no_grad():
+                O.dm_layer(cfg, {k: v.float() for k, v in sd.items()}, x, cos, sin, schedule=sched)
+
+    med, ts = median_wall(run)
+    span = "the whole workload" if Ts == T else f"a T-prefix of the T={T} workload"
+    what = ("layer forward + autograd backward" if fwdbwd else "layer forward") + \
+        f" at B={B}, T={Ts} ({span}; c=64, K=4)"
+    return dict(value=B * Ts / med, unit="tokens/s", cores=nthr, kind="port",
+                sample=f"{what}, fp32 torch CPU oracle, median of 3 after a warm-up: "
+                       + ", ".join(f"{t:.2f}" for t in ts) + " s", **host_info())
+
+
+def cpu_decode_baseline(cfg, sd, rows=8, steps=3):
+    """The oracle's static-tape decode step (lm/eval/graph_decode.py:33-51 restated, fp32 torch)
+    on this host's cores for `rows` of the 64 batch rows of BASELINE config 5 (tape of 32768
+    positions): one warm-up step, then the median of `steps`; GB/s of the same algorithmic bytes
+    as the GPU figure (the bf16 tape rows read, the weights, the row writes)."""
+    import oracle as O
+    nthr = cpu_threads()
+    torch.set_num_threads(nthr)
+    P0, h, d = C5["P0"], C5["h"], C5["d"]
+    dh = d // h
+    P = P0 + steps + 1
+    g = torch.Generator().manual_seed(C5["tseed"])
+    Kb = torch.randn(rows, h, P, dh, generator=g).bfloat16().float()
+    Vb = torch.randn(rows, h, P, dh, generator=g).bfloat16().float()
+    x = torch.randn(steps + 1, rows, 1, d, generator=g).bfloat16().float()
+    cos, sin = O.build_rope_cache(P, dh, cfg.rope_theta)
+    sdf = {k: v.float() for k, v in sd.items()}
+    pos = [P0]
+
+    def run():
         with torch.no_grad():
-            t0 = time.perf_counter()
-            O.dm_layer(cfg, sdf, x, cos, sin, schedule=sched)
-            dt = time.perf_counter() - t0
-        what = f"layer forward at B={B}, T={Ts} (c=64, K=4)"
-    return dict(value=B * Ts / dt, unit="tokens/s", cores=nthr, kind="port",
-                sample=f"{what}, fp32 torch CPU oracle, {dt:.2f} s wall")
+            O.static_decode_step(cfg, sdf, x[pos[0] - P0], pos[0], Kb, Vb, cos, sin)
+        pos[0] += 1
+
+    med, ts = median_wall(run, reps=steps)
+    step_bytes = 2.0 * rows * h * (P0 + 2) * dh * 2 + 12.0 * d * d * 2 + 2.0 * rows * d * 2
+    return dict(value=step_bytes / med / 1e9, unit="GB/s", tokens_per_s=rows / med, cores=nthr, kind="port",
+                sample=f"static-tape decode steps of {rows} of the 64 batch rows at P = {P0}.., fp32 torch "
+                       "CPU oracle, median of 3 after a warm-up: " + ", ".join(f"{t * 1e3:.0f}" for t in ts) + " ms",
+                **host_info())
 
 
-def bench_decode(dev, steps_override=None):
+def bench_decode(dev, steps_override=None, with_cpu=True):
     cfg = DualModConfig(d_model=C5["d"], n_heads=C5["h"], ctx_mod="mult_res", max_seq_len=8,
                         dtype="bf16")
     B, P0 = C5["B"], C5["P0"]
@@ -151,7 +237,7 @@ def bench_decode(dev, steps_override=None):
         for t in range(steps):
             tape.step(x[t], P0 + t, cos, sin, with_wo=True)
 
-    # warm-up pass over the first few slots, then restore nothing (slots are rewritten)
+    # warm-up pass over the first few slots (the slots are rewritten by the timed pass)
     for t in range(4):
         tape.step(x[t], P0 + t, cos, sin, with_wo=True)
     torch.cuda.synchronize()
@@ -167,23 +253,69 @@ def bench_decode(dev, steps_override=None):
     weight_bytes = steps * 12.0 * d * d * 2
     write_bytes = steps * 2.0 * B * d * 2
     total = tape_bytes + weight_bytes + write_bytes
-    read_avg_ms = kt.device_avg_ms if kt.device_avg_ms is not None else kt.avg_ms
-    read_avg_s = read_avg_ms / 1e3
     read_bytes_per_launch = tape_bytes / steps
-    return {
+    ev_s = kt.avg_ms / 1e3
+    out = {
         "metric": "decode HBM GB/s (attend_one+refine_kv over the tape, append)",
         "value": total / wall / 1e9, "unit": "GB/s", "steps": steps, "ms_per_step": wall / steps * 1e3,
         "tokens_per_s": B * steps / wall,
         "config": {"workload": "C5 decode: B=64, bf16 tape 32768..33023 positions, d=1024, 16x64",
                    "algorithmic_bytes": total},
-        "roofline": {"bound": "hbm", "achieved": read_bytes_per_launch / read_avg_s / 1e9,
+        "roofline": {"bound": "hbm", "achieved": read_bytes_per_launch / ev_s / 1e9,
                      "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": read_bytes_per_launch / read_avg_s / 1e9 / PEAK_HBM_GBS,
-                     "traffic": TRAFFIC_BYTES["dec_read"], "kernel": "k_decode_partial",
-                     "avg_launch_ms": read_avg_ms, "avg_launch_ms_events": kt.avg_ms,
+                     "frac": read_bytes_per_launch / ev_s / 1e9 / PEAK_HBM_GBS,
+                     "traffic": traffic_from_profile("dec_read"), "kernel": "k_decode_partial",
+                     "bytes_per_launch": read_bytes_per_launch,
+                     "avg_launch_ms": kt.avg_ms, "avg_launch_ms_device": kt.device_avg_ms,
                      "timing": TIMING_NOTE, "launches": kt.n},
         "path_frac_of_hbm_peak": total / wall / 1e9 / PEAK_HBM_GBS,
     }
+    del tape
+    torch.cuda.empty_cache()
+    if with_cpu:
+        out["cpu_baseline"] = cpu_decode_baseline(cfg, sd)
+    return out
+
+
+def bench_c4_ladder(dev, steps=3, warmup=1):
+    """BASELINE config 4's workload: one layer of the d=2048, 16 x 128 trunk at B=4, T=4096, c=64,
+    forward (tape) + reverse-scan backward per K in the ladder (1, 2, 4, 8). The cell's algorithmic
+    FLOPs as in SURVEY (the trunk's SwiGLU MLP and tied head are outside the layer)."""
+    B, T, d, h, c = C4["B"], C4["T"], C4["d"], C4["h"], C4["c"]
+    cfg = DualModConfig(d_model=d, n_heads=h, ctx_mod="mult_res", max_seq_len=T, dtype="bf16")
+    sd, cell, x, cos, sin, bufs, Kc, Vc, ocat, y = build_layer(cfg, B, T, dev, seeds=C4)
+    grads = LayerGrads(cfg, dev)
+    dy = make_input((B, T, d), seed=C4["xseed"] + 100).to(dev, torch.bfloat16)
+    dx = torch.empty_like(x)
+    ladder = []
+    for K in C4["ladder"]:
+        sched = uniform_chunks(T, c, K)
+        tape = cell.new_tape(sched)
+
+        def step():
+            cell.layer_forward(x, y, cos, sin, sched, Kc, Vc, ocat, bufs, tape=tape)
+            cell.layer_backward(x, dy, dx, cos, sin, sched, Kc, Vc, ocat, bufs, grads, tape=tape)
+
+        def fwd():
+            cell.layer_forward(x, y, cos, sin, sched, Kc, Vc, ocat, bufs, tape=tape)
+
+        for _ in range(warmup):
+            step()
+        dt = timed(step, steps)
+        dtf = timed(fwd, steps)
+        fpt = fwd_flops_per_token(d, T, c, K)
+        ladder.append({"K": K, "ms_per_layer_fwdbwd": dt * 1e3, "tokens_per_s": B * T / dt,
+                       "fwd_mflop_per_token": fpt / 1e6,
+                       "frac_fwdbwd": 3 * fpt * B * T / dt / 1e12 / PEAK_BF16_TFLOPS,
+                       "ms_per_layer_fwd": dtf * 1e3, "frac_fwd": fpt * B * T / dtf / 1e12 / PEAK_BF16_TFLOPS,
+                       "tape_bytes": tape.numel()})
+        del tape
+        torch.cuda.empty_cache()
+    del cell, bufs, Kc, Vc, ocat, y, x, dx, dy, grads
+    torch.cuda.empty_cache()
+    return {"workload": f"C4: one layer of the d=2048 trunk (16x128), B={B} T={T} c={c}, forward (tape) + "
+                        "reverse-scan backward per K; the per-layer cell of the 24-layer trunk",
+            "steps": steps, "warmup": warmup, "ladder": ladder}
 
 
 def main():
@@ -193,8 +325,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-T", type=int, default=0,
-                    help="CPU baseline over a T-prefix of the workload (default: the whole T)")
+                    help="T-prefix of the CPU baseline sample (0: the whole T)")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-c4", action="store_true", help="skip the config-4 K ladder")
     ap.add_argument("--decode-steps", type=int, default=0)
     ap.add_argument("--kernel", default="sweep1", help="kernel class timed for the roofline")
     ap.add_argument("--workload", default="fwdbwd", choices=["fwdbwd", "fwd", "c4"],
@@ -231,12 +364,11 @@ def main():
     B, T, d, h, c, K = shape["B"], shape["T"], shape["d"], shape["h"], shape["c"], shape["K"]
     K = args.sweeps or K
     cfg = DualModConfig(d_model=d, n_heads=h, ctx_mod="mult_res", max_seq_len=T, dtype="bf16")
-    sd, cell, x, cos, sin, bufs, Kc, Vc, ocat, y = build_layer(cfg, B, T, dev)
+    sd, cell, x, cos, sin, bufs, Kc, Vc, ocat, y = build_layer(cfg, B, T, dev, seeds=shape)
     sched = uniform_chunks(T, c, K)
 
-    from dual_mod_public_amd.engine import LayerGrads
     grads = LayerGrads(cfg, dev)
-    dy = make_input((B, T, d), seed=C2["xseed"] + 100).to(dev, torch.bfloat16)
+    dy = make_input((B, T, d), seed=shape["xseed"] + 100).to(dev, torch.bfloat16)
     dx = torch.empty_like(x)
     fwdbwd = args.workload in ("fwdbwd", "c4")
 
@@ -255,14 +387,6 @@ def main():
                 cell.layer_backward(x, dy, dx, cos, sin, sched, Kc, Vc, ocat, bufs, grads, tape=tp)
         return step
 
-    def timed(fn, steps):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            fn()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) / steps
-
     step = make_step(use_tape)
     for _ in range(args.warmup):
         step()
@@ -270,8 +394,8 @@ def main():
     sweeps = sum(k for _, _, k in sched)
     per_step_launches = sweeps * (2 if fwdbwd else 1)
     # the headline: the timed steps with nothing armed; then the same steps again with
-    # the roofline kernel's per-dispatch timing armed (its device-clock stamps and event
-    # pairs cost ~5% of the step, so they stay out of the headline's clock)
+    # the roofline kernel's per-launch timing armed (its event pairs and device-clock stamps
+    # cost ~5% of the step, so they stay out of the headline's clock)
     dt = timed(step, args.steps)
     with L.KernelTimer(args.kernel, max_launches=args.steps * per_step_launches * 2 + 64) as kt:
         dt_instr = timed(step, args.steps)
@@ -295,7 +419,7 @@ def main():
     else:
         per_launch = float("nan")
         kname = args.kernel
-    avg_ms = kt.device_avg_ms if kt.device_avg_ms is not None else kt.avg_ms
+    avg_ms = kt.avg_ms
     achieved = per_launch / (avg_ms / 1e3) / 1e12 if kt.n else None
     mode = "exact recompute" if not use_tape else "sweep states from the forward's HBM tape"
     if args.workload == "c4":
@@ -315,10 +439,12 @@ def main():
                    "global_batch": B, "seq_len": T, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": (achieved / PEAK_BF16_TFLOPS) if achieved else None,
-                     "traffic": TRAFFIC_BYTES.get(args.kernel), "kernel": kname, "flops_per_launch": per_launch,
-                     "avg_launch_ms": avg_ms, "avg_launch_ms_events": kt.avg_ms,
-                     "timing": TIMING_NOTE if kt.device_avg_ms is not None else "HIP event pairs",
-                     "launches": kt.n, "instrumented_ms_per_step": dt_instr * 1e3},
+                     "traffic": traffic_from_profile(args.kernel), "kernel": kname,
+                     "flops_per_launch": per_launch, "avg_launch_ms": avg_ms,
+                     "avg_launch_ms_device": kt.device_avg_ms,
+                     "frac_device_span": (per_launch / (kt.device_avg_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS
+                                          if kt.device_avg_ms else None),
+                     "timing": TIMING_NOTE, "launches": kt.n, "instrumented_ms_per_step": dt_instr * 1e3},
         "path_roofline": {"flops_per_token": fpt, "achieved_tflops": fpt * tokens / dt / 1e12,
                           "frac": fpt * tokens / dt / 1e12 / PEAK_BF16_TFLOPS},
     }
@@ -328,12 +454,19 @@ def main():
     if fwdbwd:
         out["tape_bytes"] = tape.numel()
     if dt_other is not None:
-        out["recompute" if use_tape else "tape"] = {"ms_per_step": dt_other * 1e3,
-                                                    "tokens_per_s": tokens / dt_other}
+        # the other backward mode, with the headline's fields (C3 as BASELINE words it is the
+        # exact-recompute mode; the tape holds the same sweep states bit for bit)
+        out["recompute" if use_tape else "tape"] = {
+            "value": tokens / dt_other, "unit": "tokens/s", "ms_per_step": dt_other * 1e3,
+            "tokens_per_s": tokens / dt_other,
+            "path_frac": fpt * tokens / dt_other / 1e12 / PEAK_BF16_TFLOPS,
+            "workload": wl.replace(mode, "exact recompute" if use_tape else "sweep states from the forward's HBM tape")}
+    del cell, bufs, Kc, Vc, ocat, y, x, dx, dy, grads, tape
+    torch.cuda.empty_cache()
+    if not args.no_c4 and args.workload != "c4":
+        out["c4"] = bench_c4_ladder(dev)
     if not args.no_decode:
-        del cell, bufs, Kc, Vc, ocat, y, x, dx, dy, grads, tape
-        torch.cuda.empty_cache()
-        out["decode"] = bench_decode(dev, args.decode_steps or None)
+        out["decode"] = bench_decode(dev, args.decode_steps or None, with_cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline and args.workload != "c4":
         out["cpu_baseline"] = cpu_baseline(cfg, sd, T, B, fwdbwd, args.cpu_T)
     print(json.dumps(out), flush=True)
