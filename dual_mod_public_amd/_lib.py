@@ -26,13 +26,18 @@ class dm_config(ctypes.Structure):
     _fields_ = [("dtype", c_i32), ("B", c_i32), ("d", c_i32), ("h", c_i32), ("dh", c_i32),
                 ("ctx_mod", c_i32), ("mult_res_lambda", ctypes.c_float), ("rms_eps", ctypes.c_float),
                 ("local_window", c_i32), ("flags", c_i32), ("kmod_vraw_heads", c_i32),
-                ("kmod_mode", c_i32), ("v_clamp_tau", ctypes.c_float), ("reserved", c_i32 * 3)]
+                ("kmod_mode", c_i32), ("v_clamp_tau", ctypes.c_float), ("norms", c_i32),
+                ("reserved", c_i32 * 2)]
 
 
 DM_DECODE_SCRATCH_MAX = 32 << 20   # include/dm_abi.h: static scratch of dm_decode_step_noalloc
 DM_FLAG_NO_RESIDUAL = 1
 DM_FLAG_FUSED_ATTEND = 2
 DM_FLAG_UNFUSED_ATTEND = 4
+# per-head RMS norms (dm_config.norms bits) and the gain parameter of each (attention.py:113-166)
+DM_NORM_K_CTX, DM_NORM_V_CTX, DM_NORM_V = 1, 2, 4
+NORM_KNOBS = (("k_ctx_norm", DM_NORM_K_CTX, "k_gain"), ("v_ctx_norm", DM_NORM_V_CTX, "ctx_gain"),
+              ("v_norm", DM_NORM_V, "v_gain"))
 
 # dm_grads fields and the reference parameter each one accumulates
 GRAD_FIELDS = (("wq", "wq.weight"), ("wk", "wk.weight"), ("wv", "wv.weight"), ("wo", "wo.weight"),
@@ -40,7 +45,8 @@ GRAD_FIELDS = (("wq", "wq.weight"), ("wk", "wk.weight"), ("wv", "wv.weight"), ("
                ("w_gv", "w_gv.weight"), ("b_gk", "w_gk.bias"), ("b_gv", "w_gv.bias"),
                ("v_gate", "v_gate.weight"), ("b_vgate", "v_gate.bias"), ("v_map", "v_map.weight"),
                ("norm_ctx_w", "norm_ctx.weight"), ("attn_norm_w", "attn_norm.weight"),
-               ("v_pre", "v_pre.weight"))
+               ("v_pre", "v_pre.weight"), ("k_gain", "k_gain"), ("ctx_gain", "ctx_gain"),
+               ("v_gain", "v_gain"))
 
 
 class dm_grads(ctypes.Structure):
@@ -50,18 +56,18 @@ class dm_grads(ctypes.Structure):
 class dm_params(ctypes.Structure):
     _fields_ = [(n, c_vp) for n in ("wq", "wk", "wv", "wo", "w_kctx", "w_vctx", "w_gk", "w_gv",
                                     "b_gk", "b_gv", "v_gate", "b_vgate", "v_map", "norm_ctx_w",
-                                    "attn_norm_w", "v_pre")]
+                                    "attn_norm_w", "v_pre", "k_gain", "ctx_gain", "v_gain")]
 
 
 class dm_packed(ctypes.Structure):
     _fields_ = [(n, c_vp) for n in ("w_proj", "b_proj", "w_sweep", "w_vctx", "norm_ctx_w",
                                     "attn_norm_w", "wo", "w_proj_t", "w_sweep_t", "w_vctx_t",
-                                    "wo_t")]
+                                    "wo_t", "gains")]
 
 
 class dm_layer_bufs(ctypes.Structure):
     _fields_ = [("T", c_i32), ("xhat", c_vp), ("qr", c_vp), ("kraw", c_vp), ("kself", c_vp),
-                ("vraw", c_vp), ("glogx", c_vp), ("sig", c_vp)]
+                ("vraw", c_vp), ("glogx", c_vp), ("sig", c_vp), ("vpre", c_vp)]
 
 
 class dm_cell_args(ctypes.Structure):
@@ -252,4 +258,14 @@ def make_config(cfg, B, dtype):
     else:
         c.kmod_mode = 1 if getattr(cfg, "kmod_vraw_bound", "none") == "tanh" else 0
     c.v_clamp_tau = float(getattr(cfg, "v_clamp_tau", 0.0) or 0.0)
+    c.norms = norm_bits(cfg)
     return c
+
+
+def norm_bits(cfg):
+    """dm_config.norms of a config: the per-head RMS norms set to "rms"."""
+    bits = 0
+    for knob, bit, _ in NORM_KNOBS:
+        if getattr(cfg, knob, "none") == "rms":
+            bits |= bit
+    return bits

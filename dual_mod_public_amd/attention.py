@@ -66,6 +66,13 @@ class DualModAttention(nn.Module):
             self.v_pre = nn.Linear(2 * d, d, bias=False)
             nn.init.zeros_(self.v_pre.weight)
         self.norm_ctx = RMSNorm(d)
+        # per-head RMS-norm gains (attention.py:113-114, 145-148, 165-166)
+        if getattr(cfg, "v_norm", "none") == "rms":
+            self.v_gain = nn.Parameter(torch.ones(cfg.n_heads))
+        if getattr(cfg, "k_ctx_norm", "none") == "rms":
+            self.k_gain = nn.Parameter(torch.full((cfg.n_heads,), float(getattr(cfg, "k_gain_init", 1.75))))
+        if getattr(cfg, "v_ctx_norm", "none") == "rms":
+            self.ctx_gain = nn.Parameter(torch.ones(cfg.n_heads))
         self._cells = {}
         self._packed_version = None
 

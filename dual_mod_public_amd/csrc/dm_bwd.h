@@ -106,6 +106,10 @@ template <typename T> struct RefineBwdArgs {
   T* dctx;                             // [N, 4d] (packed columns; v_map columns written by EpiVinBwd)
   T* dvc;                              // [N, d] dv_ctx (mult family)
   float* dglogx; float* dkraw; float* dvraw;   // layer accumulators (+=)
+  // k_ctx / v_ctx norms (attention.py:238-269): gains [h] (nullptr = off) and the gains'
+  // per-row gradient partials [B*Tbuf, h] (+=)
+  const float* kgain = nullptr; const float* vgain = nullptr;
+  float* dkg = nullptr; float* dvg = nullptr;
 };
 
 template <typename T, int DH, int NS>
@@ -134,23 +138,38 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
     dv1 += a.dV[o]; dv2 += a.dV[o + DH / 2];
   }
   const float cs = a.cos[(long)pos * (DH / 2) + jj], sn = a.sin[(long)pos * (DH / 2) + jj];
-  const float kc1 = to_f(S1[col_k<DH>(hd, jj, 0)]), kc2 = to_f(S1[col_k<DH>(hd, jj, 1)]);
+  const float kx1 = to_f(S1[col_k<DH>(hd, jj, 0)]), kx2 = to_f(S1[col_k<DH>(hd, jj, 1)]);
   const float gu1 = to_f(S1[col_k<DH>(hd, jj, 2)]), gu2 = to_f(S1[col_k<DH>(hd, jj, 3)]);
   const float gx1 = gx[hd * DH + jj], gx2 = gx[hd * DH + jj + DH / 2];
   const float kr1 = to_f(a.kraw[lrow + jj]), kr2 = to_f(a.kraw[lrow + jj + DH / 2]);
   const float vr1 = to_f(a.vraw[lrow + jj]), vr2 = to_f(a.vraw[lrow + jj + DH / 2]);
   const float gxv1 = gx[d + hd * DH + jj], gxv2 = gx[d + hd * DH + jj + DH / 2];
   const int c1 = hd * DH + jj, c2 = c1 + DH / 2;
-  float vc1, vc2, gvu1, gvu2;
+  float vx1, vx2, gvu1, gvu2;
   int cv1 = 0, cv2 = 0;
   if (a.ctx_mod == 0) {
     cv1 = col_vlin<DH>(d, hd, jj);
     cv2 = col_vlin<DH>(d, hd, jj + DH / 2);
-    vc1 = to_f(S1[cv1]); vc2 = to_f(S1[cv2]);
+    vx1 = to_f(S1[cv1]); vx2 = to_f(S1[cv2]);
     gvu1 = to_f(S1[cv1 + 32]); gvu2 = to_f(S1[cv2 + 32]);
   } else {
-    vc1 = to_f(a.save2[(long)m * d + c1]); vc2 = to_f(a.save2[(long)m * d + c2]);
+    vx1 = to_f(a.save2[(long)m * d + c1]); vx2 = to_f(a.save2[(long)m * d + c2]);
     gvu1 = to_f(S1[3 * d + c1]); gvu2 = to_f(S1[3 * d + c2]);
+  }
+  // k_ctx / v_ctx as the blends took them: raw (kx, vx), or normed, (x r) gain from and to stored
+  // values, r over the head's DH / 2 lanes (consecutive, a whole group of each wave)
+  float kc1 = kx1, kc2 = kx2, vc1 = vx1, vc2 = vx2, rk = 0.f, gk = 0.f, rv = 0.f, gvn = 0.f;
+  if (a.kgain != nullptr) {
+    rk = head_norm_r(group_sum<DH / 2>(kx1 * kx1 + kx2 * kx2), 1.0f / DH);
+    gk = a.kgain[hd];
+    kc1 = stored<T>((kx1 * rk) * gk);
+    kc2 = stored<T>((kx2 * rk) * gk);
+  }
+  if (a.vgain != nullptr) {
+    rv = head_norm_r(group_sum<DH / 2>(vx1 * vx1 + vx2 * vx2), 1.0f / DH);
+    gvn = a.vgain[hd];
+    vc1 = stored<T>((vx1 * rv) * gvn);
+    vc2 = stored<T>((vx2 * rv) * gvn);
   }
   // the accumulators' current values, loaded with the gather (one memory round trip)
   float* dgx = a.dglogx + xrow * 2 * d;
@@ -163,8 +182,17 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
   const float dl1 = dk1 * (kr1 - kc1) * g1 * (1.f - g1);
   const float dl2 = dk2 * (kr2 - kc2) * g2 * (1.f - g2);
   T* D = a.dctx + (long)m * 4 * d;
-  D[col_k<DH>(hd, jj, 0)] = from_f<T>(dk1 * (1.f - g1));
-  D[col_k<DH>(hd, jj, 1)] = from_f<T>(dk2 * (1.f - g2));
+  float dkc1 = dk1 * (1.f - g1), dkc2 = dk2 * (1.f - g2);
+  if (a.kgain != nullptr) {
+    // norm VJP: dx = gain (r dy - r^3 x <dy, x> / DH); d gain += r <dy, x> (this row's partial)
+    const float sk = group_sum<DH / 2>(dkc1 * kx1 + dkc2 * kx2);
+    const float r3 = rk * rk * rk * sk * (1.0f / DH);
+    dkc1 = gk * (rk * dkc1 - r3 * kx1);
+    dkc2 = gk * (rk * dkc2 - r3 * kx2);
+    if (jj == 0) a.dkg[xrow * h + hd] += rk * sk;
+  }
+  D[col_k<DH>(hd, jj, 0)] = from_f<T>(dkc1);
+  D[col_k<DH>(hd, jj, 1)] = from_f<T>(dkc2);
   D[col_k<DH>(hd, jj, 2)] = from_f<T>(dl1);
   D[col_k<DH>(hd, jj, 3)] = from_f<T>(dl2);
   dgx[c1] = ogx1 + dl1;
@@ -209,6 +237,13 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
     dvc2 = dv2 * (1.f - gv2);
     dvr1 = dv1 * gv1;
     dvr2 = dv2 * gv2;
+  }
+  if (a.vgain != nullptr) {   // v_ctx norm VJP, as the key's (kmod heads: dvc = 0, so zero)
+    const float sv = group_sum<DH / 2>(dvc1 * vx1 + dvc2 * vx2);
+    const float r3 = rv * rv * rv * sv * (1.0f / DH);
+    dvc1 = gvn * (rv * dvc1 - r3 * vx1);
+    dvc2 = gvn * (rv * dvc2 - r3 * vx2);
+    if (jj == 0) a.dvg[xrow * h + hd] += rv * sv;
   }
   if (a.ctx_mod == 0) {
     D[cv1] = from_f<T>(dvc1);
@@ -940,6 +975,8 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
 // and the bias gradients' column partials over the block's rows:
 //   bpart[chunk][0, d) = sum dglogx (b_gk), [d, 2d) = sum dglogx[d..] (b_gv),
 //   [2d, 3d) = sum dsig sig (1 - sig) (b_vgate).
+// With the v_norm (vgain != nullptr) dvraw is the grad of the normed value: the v columns get
+// its VJP, from the kept pre-norm values vpre, and vgpart[chunk][head] the v_gain partials.
 // One thread per RoPE column pair (jj, jj + DH/2) of a head, PROJ_ROWS rows per
 // block; each row's loads are issued before its stores.
 // ---------------------------------------------------------------------------
@@ -951,13 +988,15 @@ static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, i
                                                   const float* __restrict__ dglogx, const float* __restrict__ dsig,
                                                   const float* __restrict__ sig, const float* __restrict__ cos,
                                                   const float* __restrict__ sin, T* __restrict__ dproj,
-                                                  float* __restrict__ bpart) {
+                                                  float* __restrict__ bpart, const T* __restrict__ vpre,
+                                                  const float* __restrict__ vgain, float* __restrict__ vgpart) {
   const int pidx = blockIdx.x * 256 + threadIdx.x;
   if (pidx >= d / 2) return;
   const int hd = pidx / (DH / 2), jj = pidx - hd * (DH / 2);
   const int c1 = hd * DH + jj, c2 = c1 + DH / 2;
   const int r0 = blockIdx.y * PROJ_ROWS, r1 = min(r0 + PROJ_ROWS, M);
-  float bg[4] = {0.f, 0.f, 0.f, 0.f}, bv[2] = {0.f, 0.f};
+  float bg[4] = {0.f, 0.f, 0.f, 0.f}, bv[2] = {0.f, 0.f}, vg = 0.f;
+  const float gvn = vgain != nullptr ? vgain[hd] : 0.f;
   for (int m = r0; m < r1; ++m) {
     const int b = m / T_, t = m - b * T_;
     const long hr = (((long)b * h + hd) * T_ + t) * DH;
@@ -966,8 +1005,17 @@ static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, i
     const float q1 = dq[hr + jj], q2 = dq[hr + jj + DH / 2];
     const float s1 = dkself[hr + jj], s2 = dkself[hr + jj + DH / 2];
     const float k1 = dkraw[hr + jj], k2 = dkraw[hr + jj + DH / 2];
-    const float v1 = dvraw[hr + jj], v2 = dvraw[hr + jj + DH / 2];
+    float v1 = dvraw[hr + jj], v2 = dvraw[hr + jj + DH / 2];
     const float g1 = dg[c1], g2 = dg[c2], g3 = dg[d + c1], g4 = dg[d + c2];
+    if (vgain != nullptr) {   // v_norm VJP over the head's DH / 2 lanes (a whole lane group)
+      const float x1 = to_f(vpre[hr + jj]), x2 = to_f(vpre[hr + jj + DH / 2]);
+      const float r = head_norm_r(group_sum<DH / 2>(x1 * x1 + x2 * x2), 1.0f / DH);
+      const float sv = group_sum<DH / 2>(v1 * x1 + v2 * x2);
+      const float r3 = r * r * r * sv * (1.0f / DH);
+      v1 = gvn * (r * v1 - r3 * x1);
+      v2 = gvn * (r * v2 - r3 * x2);
+      vg += r * sv;
+    }
     float z1 = 0.f, z2 = 0.f;
     if (nproj == 6) {
       const float sg1 = sig[(long)m * d + c1], sg2 = sig[(long)m * d + c2];
@@ -996,6 +1044,7 @@ static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, i
   float* P = bpart + (long)blockIdx.y * 3 * d;
   P[c1] = bg[0]; P[c2] = bg[1]; P[d + c1] = bg[2]; P[d + c2] = bg[3];
   P[2 * d + c1] = bv[0]; P[2 * d + c2] = bv[1];
+  if (vgain != nullptr && jj == 0) vgpart[(long)blockIdx.y * h + hd] = vg;
 }
 
 // Column sums of a row-major fp32 matrix [M, ncols], stage 1: part[chunk][col]

@@ -41,6 +41,9 @@ template <typename T> struct BwdWs {
   float* dxhat;                         // [B*T, d]
   float *dWp, *dWs;                     // packed weight-grad staging [nproj*d, d], [4d, d]
   float* colpart;                       // [max(NCHUNK, B*T / PROJ_ROWS), 3d] column partials
+  // head norms: per-row partials of the k_gain / ctx_gain grads [B*T, h], and the v_gain grad's
+  // per-chunk partials [B*T / PROJ_ROWS, h] (nullptr when that norm is off)
+  float *dkg, *dvg, *vgpart;
   size_t bytes;
 };
 
@@ -94,6 +97,9 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.dWp = cv.take<float>(nproj * d * d * 4);
   w.dWs = cv.take<float>(4 * d * d * 4);
   w.colpart = cv.take<float>((size_t)std::max<long>(NCHUNK, cdiv(BT, PROJ_ROWS)) * 3 * d * 4);
+  w.dkg = (c->norms & DM_NORM_K_CTX) ? cv.take<float>(BT * h * 4) : nullptr;
+  w.dvg = (c->norms & DM_NORM_V_CTX) ? cv.take<float>(BT * h * 4) : nullptr;
+  w.vgpart = (c->norms & DM_NORM_V) ? cv.take<float>((size_t)cdiv(BT, PROJ_ROWS) * h * 4) : nullptr;
   w.bytes = cv.off;
   return w;
 }
@@ -200,7 +206,9 @@ void bwd_begin(const dm_config* c, const dm_packed* w, const T* dy, const T* oca
               {ws.dglogx, (size_t)BT * 2 * d},
               {ws.dsig, (size_t)BT * d},
               {ws.dnw, (size_t)cdiv(B * CMAX, NSLOT_TM) * d},
-              {ws.dWs, (size_t)4 * d * d}},
+              {ws.dWs, (size_t)4 * d * d},
+              {ws.dkg, ws.dkg ? (size_t)BT * c->h : 0},
+              {ws.dvg, ws.dvg ? (size_t)BT * c->h : 0}},
              s);
   // W_O: do_cat = dy . W_O ; dW_O += dy^T . ocat
   EpiStoreTileF32 ep{BT, d, ws.docat, 0};
@@ -278,7 +286,8 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
     // refine VJP of sweep sw (the last sweep's rows: the final-row grads above)
     RefineBwdArgs<T> ra{g, N, c->ctx_mod, dKn, dVn, dn_stride, dn_row0, dn_psum,
                         sv.save1 + sw * NS * 4 * d, mult ? sv.save2 + sw * NS * d : nullptr, L->glogx, kraw, vraw,
-                        cos, sin, dctx + sw * NS * 4 * d, dvc + sw * NS * d, ws.dglogx, ws.dkraw, ws.dvraw};
+                        cos, sin, dctx + sw * NS * 4 * d, dvc + sw * NS * d, ws.dglogx, ws.dkraw, ws.dvraw,
+                        kctx_gain(c, w), vctx_gain(c, w), ws.dkg, ws.dvg};
     const dim3 rgrid(cdiv((long)N * d / 2, 256));
     if (sw == K - 1 && gc.dK == nullptr) hipLaunchKernelGGL((k_refine_bwd<T, DH, COMM_NSQ>), rgrid, dim3(256), 0, s, ra);
     else hipLaunchKernelGGL((k_refine_bwd<T, DH, 1>), rgrid, dim3(256), 0, s, ra);
@@ -403,9 +412,15 @@ void bwd_end(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T*
                      fusion ? 1 : 0,
                      (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself, (const float*)ws.dvraw,
                      (const float*)ws.dglogx, (const float*)ws.dsig, (const float*)L->sig, cos, sin, ws.dproj,
-                     ws.colpart);
+                     ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart);
   hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks, 3 * d, 3 * d,
                      (const float*)ws.colpart, gr->b_gk, gr->b_gv, (mult && !fusion) ? gr->b_vgate : nullptr, d);
+  // the head norms' gains: sums over rows of the partials
+  if (ws.vgpart)
+    hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(h, 64)), dim3(256), 0, s, pchunks, h, h, (const float*)ws.vgpart,
+                       gr->v_gain, (float*)nullptr, (float*)nullptr, h);
+  if (ws.dkg) colsum_add(ws.dkg, BT, h, ws.colpart, gr->k_gain, s);
+  if (ws.dvg) colsum_add(ws.dvg, BT, h, ws.colpart, gr->ctx_gain, s);
   const T* xhat = norm ? (const T*)L->xhat : x;
   // dW_proj = d_proj^T . xhat (packed rows), dxhat = d_proj . W_proj
   gemm_tn<T>(ws.dproj, (long)nproj * d, xhat, d, ws.dWp, nproj * d, d, BT, 0, ws.kpart, s);
@@ -574,6 +589,10 @@ int check_grads(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, 
   DM_REQUIRE(c->ctx_mod != DM_CTX_FUSION || g->v_pre, DM_ERR_INVALID, "ctx_mod fusion needs the v_pre grad");
   DM_REQUIRE(w->attn_norm_w == nullptr || (g->attn_norm_w && L->xhat), DM_ERR_INVALID,
              "attn_norm needs its gradient buffer and bufs->xhat");
+  DM_REQUIRE(!(c->norms & DM_NORM_K_CTX) || g->k_gain, DM_ERR_INVALID, "k_ctx norm needs the k_gain grad");
+  DM_REQUIRE(!(c->norms & DM_NORM_V_CTX) || g->ctx_gain, DM_ERR_INVALID, "v_ctx norm needs the ctx_gain grad");
+  DM_REQUIRE(!(c->norms & DM_NORM_V) || (g->v_gain && L->vpre), DM_ERR_INVALID,
+             "v_norm needs the v_gain grad and bufs->vpre");
   return DM_OK;
 }
 

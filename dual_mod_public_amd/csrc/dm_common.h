@@ -207,6 +207,13 @@ DM_DEV float tanhf_(float x) {
   return ax < 0.0625f ? series : t;
 }
 
+// the value as stored in dtype T (rounded to bf16; fp32 unchanged)
+template <typename T> DM_DEV float stored(float x) { return to_f(from_f<T>(x)); }
+
+// per-head RMS norm (attention.py:218-269): y = gain x r, r = rsqrt(sum of x^2 / dh + 1e-6)
+constexpr float HEAD_NORM_EPS = 1e-6f;
+DM_DEV float head_norm_r(float ss, float inv_dh) { return rsqrtf(ss * inv_dh + HEAD_NORM_EPS); }
+
 // ---- wave reductions (full 64-lane and within 16-lane groups) ----------------
 // sum over aligned groups of G consecutive lanes (G a power of two <= 64)
 template <int G> DM_DEV float group_sum(float v) {

@@ -103,13 +103,25 @@ std::vector<size_t> tape_offsets(const dm_config* c, const int32_t* sched, int n
   return off;
 }
 
+// per-head norm gains of the packed weights (nullptr: that norm is off)
+inline const float* kctx_gain(const dm_config* c, const dm_packed* w) {
+  return (c->norms & DM_NORM_K_CTX) ? w->gains : nullptr;
+}
+inline const float* vctx_gain(const dm_config* c, const dm_packed* w) {
+  return (c->norms & DM_NORM_V_CTX) ? w->gains + c->h : nullptr;
+}
+inline const float* v_gain(const dm_config* c, const dm_packed* w) {
+  return (c->norms & DM_NORM_V) ? w->gains + 2 * c->h : nullptr;
+}
+
+// vpre: v_raw before the v_norm (nullptr: not kept)
 template <typename T, int DH>
 void run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int Tl, int Tbuf, int buf_t0,
-              int rope_t0, const float* cos, const float* sin, T* qr, T* kraw, T* kself, T* vraw,
+              int rope_t0, const float* cos, const float* sin, T* qr, T* kraw, T* kself, T* vraw, T* vpre,
               float* glogx, float* sig, hipStream_t s) {
   const int nseg = (c->ctx_mod == DM_CTX_LINEAR) ? 5 : 6;
   EpiProj<T, DH> epi{M, c->d, c->h, Tl, Tbuf, buf_t0, rope_t0, cos, sin, w->b_proj,
-                     qr, kraw, kself, vraw, glogx, sig, c->ctx_mod == DM_CTX_FUSION};
+                     qr, kraw, kself, vraw, glogx, sig, c->ctx_mod == DM_CTX_FUSION, v_gain(c, w), vpre};
   SrcRows<T> sa{xhat, c->d, M};
   SrcRows<T> sb{(const T*)w->w_proj, c->d, nseg * c->d};
   // bf16, whole 256-row / 256-column tiles: 256 x 256 blocks (four 128 x 128 wave tiles,
@@ -129,11 +141,12 @@ void run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int 
 template <typename T>
 void run_proj_dispatch(const dm_config* c, const dm_packed* w, const T* xhat, int M, int Tl, int Tbuf,
                        int buf_t0, int rope_t0, const float* cos, const float* sin, T* qr, T* kraw, T* kself,
-                       T* vraw, float* glogx, float* sig, hipStream_t s) {
+                       T* vraw, T* vpre, float* glogx, float* sig, hipStream_t s) {
   if (c->dh == 64)
-    run_proj<T, 64>(c, w, xhat, M, Tl, Tbuf, buf_t0, rope_t0, cos, sin, qr, kraw, kself, vraw, glogx, sig, s);
+    run_proj<T, 64>(c, w, xhat, M, Tl, Tbuf, buf_t0, rope_t0, cos, sin, qr, kraw, kself, vraw, vpre, glogx, sig, s);
   else
-    run_proj<T, 128>(c, w, xhat, M, Tl, Tbuf, buf_t0, rope_t0, cos, sin, qr, kraw, kself, vraw, glogx, sig, s);
+    run_proj<T, 128>(c, w, xhat, M, Tl, Tbuf, buf_t0, rope_t0, cos, sin, qr, kraw, kself, vraw, vpre, glogx, sig,
+                     s);
 }
 
 // One sweep's refine: sweep GEMM 1 (+ GEMM 2 for the mult family) with the blend
@@ -146,14 +159,29 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
   const T* normw = (const T*)w->norm_ctx_w;
   SrcRowsRs<T> sa{o, c->d, N, ssq, c->h, 1.0f / (float)c->d, c->rms_eps};
   SrcRows<T> sb{(const T*)w->w_sweep, c->d, 4 * c->d};
-  EpiSweep1<T, DH> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
-                      Kout, Vout, out_stride, out_row0, vin, gvu, save1};
-  launch_gemm_auto<T, 64, 64, 2, 2, SW1_STAGES, 4>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
-  if (c->ctx_mod != DM_CTX_LINEAR && next_attend != nullptr) {
-    // GEMM 2 fused with the next sweep's attention (64-row cells; the clamp is in its epilogue)
+  const bool linear = c->ctx_mod == DM_CTX_LINEAR;
+  const float* kgain = kctx_gain(c, w);
+  const float* vgain = vctx_gain(c, w);
+  if (kgain != nullptr || (linear && vgain != nullptr)) {
+    // a norm of GEMM 1's k_ctx or (linear) v_ctx columns: blocks of one head's 2 DH packed columns
+    constexpr int NG = DH / 32;
+    EpiSweep1<T, DH, NG> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
+                            Kout, Vout, out_stride, out_row0, vin, gvu, save1, kgain, linear ? vgain : nullptr};
+    if constexpr (DH == 64)
+      launch_gemm_auto<T, 64, 2 * DH, 2, 2, SW1_STAGES, 4>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
+    else
+      launch_gemm_auto<T, 64, 2 * DH, 1, 4, SW1_STAGES, 2>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
+  } else {
+    EpiSweep1<T, DH> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
+                        Kout, Vout, out_stride, out_row0, vin, gvu, save1};
+    launch_gemm_auto<T, 64, 64, 2, 2, SW1_STAGES, 4>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
+  }
+  if (!linear && next_attend != nullptr) {
+    // GEMM 2 fused with the next sweep's attention (64-row cells; the clamp and the v_ctx norm
+    // are in its epilogue)
     SrcRows<T> av{vin, c->d, N};
     SrcRows<T> bv{(const T*)w->w_vctx, c->d, c->d};
-    EpiSweep2Head<T, DH> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2};
+    EpiSweep2Head<T, DH> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2, vgain};
     uint64_t* ts;
     const int idx = prof_launch_begin(PROF_SWEEP2, s, true, ts);
     hipLaunchKernelGGL((k_sweep2_attend<T, DH>), dim3(c->h, N / CMAX), dim3(256), 0, s, av, bv, c->d, e2,
@@ -161,7 +189,16 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
     prof_launch_end(idx, s);
     return;
   }
-  if (c->ctx_mod != DM_CTX_LINEAR) {
+  if (!linear && vgain != nullptr) {
+    // v_ctx norm: 64 x DH blocks hold whole heads (the clamp runs in the same epilogue)
+    SrcRows<T> av{vin, c->d, N};
+    SrcRows<T> bv{(const T*)w->w_vctx, c->d, c->d};
+    EpiSweep2Head<T, DH> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2, vgain};
+    constexpr int S2 = SW2_STAGES > 0 ? SW2_STAGES : 3;
+    launch_gemm_auto<T, 64, DH, 4, 1, S2, 4>(av, bv, N, c->d, c->d, e2, s, PROF_SWEEP2);
+    return;
+  }
+  if (!linear) {
     SrcRows<T> av{vin, c->d, N};
     SrcRows<T> bv{(const T*)w->w_vctx, c->d, c->d};
     EpiSweep2<T, DH> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2};
@@ -307,6 +344,7 @@ inline int check_packed(const dm_config* c, const dm_packed* w) {
   DM_REQUIRE(w != nullptr, DM_ERR_INVALID, "null packed weights");
   DM_REQUIRE(w->w_proj && w->b_proj && w->w_sweep && w->norm_ctx_w, DM_ERR_INVALID, "null packed weight");
   DM_REQUIRE(c->ctx_mod == DM_CTX_LINEAR || w->w_vctx, DM_ERR_INVALID, "mult family needs w_vctx");
+  DM_REQUIRE(c->norms == 0 || w->gains, DM_ERR_INVALID, "the head norms need the packed gains");
   DM_REQUIRE(aligned16(w->w_proj) && aligned16(w->w_sweep) && aligned16(w->norm_ctx_w) &&
                  (w->w_vctx == nullptr || aligned16(w->w_vctx)),
              DM_ERR_INVALID, "packed weights must be 16-byte aligned");

@@ -99,6 +99,8 @@ inline int check_cfg(const dm_config* c) {
              DM_ERR_UNSUPPORTED, "kmod_vraw_heads %d / kmod_mode %d", c->kmod_vraw_heads, c->kmod_mode);
   DM_REQUIRE(c->v_clamp_tau >= 0.f, DM_ERR_INVALID, "v_clamp_tau %g", (double)c->v_clamp_tau);
   DM_REQUIRE(c->local_window >= 0, DM_ERR_INVALID, "local_window %d", c->local_window);
+  DM_REQUIRE((c->norms & ~(DM_NORM_K_CTX | DM_NORM_V_CTX | DM_NORM_V)) == 0, DM_ERR_UNSUPPORTED, "norms bits 0x%x",
+             c->norms);
   return DM_OK;
 }
 

@@ -170,6 +170,10 @@ template <typename T, int DH> struct EpiProj {
   T* __restrict__ qr; T* __restrict__ kraw; T* __restrict__ kself; T* __restrict__ vraw;
   float* __restrict__ glogx; float* __restrict__ sig;
   int fusion;    // ctx_mod fusion: segment 5 is v_pre's x-half, stored as the raw pre-activation
+  // v_norm (attention.py:218-234): v_raw = (x r) gain per head, x the stored projection,
+  // r = rsqrt(mean x^2 + 1e-6); vgain [h] fp32 (nullptr = off); vpre keeps x (nullptr = not kept)
+  const float* __restrict__ vgain = nullptr;
+  T* __restrict__ vpre = nullptr;
 
   // The wave tile spans whole heads (FN * 16 a multiple of DH); within each head
   // columns j and j + DH/32 of the tile are the RoPE pair (jj, jj + DH/2).
@@ -234,8 +238,24 @@ template <typename T, int DH> struct EpiProj {
               }
             }
           } else if (seg == 2) {
+            if (vgain != nullptr) {
+              // the head's DH columns of row m: FH tiles x the 16 lanes that share lane >> 4
+              float x[FH], ss = 0.f;
 #pragma unroll
-            for (int j = 0; j < FH; ++j) vraw[hrow + 16 * j + lc] = from_f<T>(acc[i][hb * FH + j][q]);
+              for (int j = 0; j < FH; ++j) {
+                x[j] = stored<T>(acc[i][hb * FH + j][q]);
+                ss += x[j] * x[j];
+              }
+              const float nr = head_norm_r(group16_sum(ss), 1.0f / DH), ng = vgain[hh];
+#pragma unroll
+              for (int j = 0; j < FH; ++j) {
+                if (vpre != nullptr) vpre[hrow + 16 * j + lc] = from_f<T>(x[j]);
+                vraw[hrow + 16 * j + lc] = from_f<T>((x[j] * nr) * ng);
+              }
+            } else {
+#pragma unroll
+              for (int j = 0; j < FH; ++j) vraw[hrow + 16 * j + lc] = from_f<T>(acc[i][hb * FH + j][q]);
+            }
           }
         }
         if (seg == 3 || seg == 4) {
@@ -604,7 +624,7 @@ static __global__ __launch_bounds__(64 * NW) void k_attend(AttendArgs<T> a) {
 //          [3d, 4d) g_v(u)   -> fp32 scratch for GEMM 2
 // save != nullptr stores the raw GEMM outputs [rows, 4d] in this packed order.
 // ---------------------------------------------------------------------------
-template <typename T, int DH> struct EpiSweep1 {
+template <typename T, int DH, int NG = 1> struct EpiSweep1 {
   CellGeom g;
   int M, ctx_mod;
   float lam;
@@ -616,18 +636,28 @@ template <typename T, int DH> struct EpiSweep1 {
   long out_stride; int out_row0;                          //   chunk row p at row out_row0 + p
   T* __restrict__ vin; float* __restrict__ gvu;
   T* __restrict__ save;
+  // Per-head norms of the GEMM outputs (attention.py:238-269), fp32 gains [h], nullptr = off:
+  // kgain k_ctx (norm_kctx), vgain the linear ctx_mod's v_ctx (norm_vctx). Either needs block
+  // tiles of NG = DH / 32 column groups (BN = 2 DH: one head's k_ctx / g_k(u), or v_ctx / g_v(u),
+  // columns), so that the block holds whole heads.
+  const float* __restrict__ kgain = nullptr;
+  const float* __restrict__ vgain = nullptr;
 
-  // Block tile 64 x 64 = one packed column group. Thread t owns row t / 4 and the
-  // column quad lc0 = 4 (t % 4) .. + 3 of each of the group's four 16-column
-  // sections, so its global inputs and outputs are runs of 4 consecutive elements.
-  // The inputs are gathered before the k-loop.
+  // Block tile 64 x 64 NG: NG packed column groups of 64. Thread t owns row t / 4 and the
+  // column quad lc0 = 4 (t % 4) .. + 3 of each group's four 16-column sections, so its global
+  // inputs and outputs are runs of 4 consecutive elements. With one group the inputs are
+  // gathered during the k-loop's last stage; with several, at the start of the epilogue.
   struct TilePre {
     floatx4 f[4];                   // K: gx_a, gx_b, cos, sin; linear V: gx x2; v_map: sig x4
     typename Raw4<T>::type h[8];    // K: kraw_a, kraw_b; linear V: v_raw x2; v_map: o x4, norm weight x4
   };
   // tile_prefetch issues exactly these 12 loads (one per f / h slot, unconditionally)
-  static constexpr int LATE_GATHERS = 12;
+  static constexpr int LATE_GATHERS = NG == 1 ? 12 : 0;
   DM_DEV TilePre tile_prefetch(int m0, int n0) const {
+    if constexpr (NG == 1) return group_prefetch(m0, n0);
+    else return TilePre{};
+  }
+  DM_DEV TilePre group_prefetch(int m0, int n0) const {
     const int r = threadIdx.x >> 2, lc0 = 4 * (threadIdx.x & 3);
     const int d = g.d, h = g.h;
     const int m = min(m0 + r, M - 1);
@@ -685,12 +715,55 @@ template <typename T, int DH> struct EpiSweep1 {
 
   template <int BM, int BN, int LDT>
   DM_DEV void tile_apply(const float* tile, int m0, int n0, const float* rs, const TilePre& pr, int) const {
-    static_assert(BM == 64 && BN == 64, "sweep GEMM 1 block tile is one 64 x 64 column group");
+    static_assert(BM == 64 && BN == 64 * NG, "sweep GEMM 1 block tile is NG 64 x 64 column groups");
+    const float sc = rs[threadIdx.x >> 2];
+    if constexpr (NG == 1) {
+      group_apply<LDT>(tile, m0, n0, sc, pr, false, 0.f, 0.f);
+    } else {
+      TilePre pg[NG];
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) pg[gi] = group_prefetch(m0, n0 + 64 * gi);
+      // The block's NG groups are one head's k_ctx / g_k(u) (or linear v_ctx / g_v(u)) columns:
+      // the head's norm scale r * gain from sections 0 and 1 of every group (the k_ctx, v_ctx
+      // columns), over the row's 4 threads.
+      const int r = threadIdx.x >> 2, lc0 = 4 * (threadIdx.x & 3);
+      const int d = g.d;
+      const float* gain = nullptr;
+      int hd = 0;
+      if (n0 < 2 * d) { gain = kgain; hd = n0 / (2 * DH); }
+      else if (ctx_mod == 0) { gain = vgain; hd = (n0 - 2 * d) / (2 * DH); }
+      float nr = 0.f, ng = 0.f;
+      if (gain != nullptr) {
+        float ss = 0.f;
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi)
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const floatx4 v = *reinterpret_cast<const floatx4*>(tile + r * LDT + 64 * gi + 16 * k + lc0);
+            const float x0 = stored<T>(v.x * sc), x1 = stored<T>(v.y * sc);
+            const float x2 = stored<T>(v.z * sc), x3 = stored<T>(v.w * sc);
+            ss += x0 * x0 + x1 * x1 + x2 * x2 + x3 * x3;
+          }
+        ss += __shfl_xor(ss, 1, 64);
+        ss += __shfl_xor(ss, 2, 64);
+        nr = head_norm_r(ss, 1.0f / DH);
+        ng = gain[hd];
+      }
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi)
+        group_apply<LDT>(tile + 64 * gi, m0, n0 + 64 * gi, sc, pg[gi], gain != nullptr, nr, ng);
+    }
+  }
+
+  // One 64-column group of the tile (tile points at the group's first column). nrm: the group's
+  // k_ctx / v_ctx columns are normed, x -> (x nr) ng, from and to stored values.
+  template <int LDT>
+  DM_DEV void group_apply(const float* tile, int m0, int n0, float sc, const TilePre& pr, bool nrm, float nr,
+                          float ng) const {
     const int r = threadIdx.x >> 2, lc0 = 4 * (threadIdx.x & 3);
     const int d = g.d, h = g.h;
     const int m = m0 + r;
     // the GEMM ran on o with norm_ctx.weight folded into W: u . W^T = rs * acc
-    const float sc = rs[r];
     float a[4][4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -706,6 +779,12 @@ template <typename T, int DH> struct EpiSweep1 {
         const floatx4 v = *reinterpret_cast<const floatx4*>(tile + r * LDT + cs0 + 4 * k);
         sv[4 * k] = v.x * sc; sv[4 * k + 1] = v.y * sc; sv[4 * k + 2] = v.z * sc; sv[4 * k + 3] = v.w * sc;
       }
+    }
+    if (NG > 1 && nrm) {   // normed k_ctx / v_ctx (sections 0 and 1)
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[k][i] = stored<T>((stored<T>(a[k][i]) * nr) * ng);
     }
     if (m >= M) return;
     const int b = m / g.c, p = m - b * g.c;
@@ -853,6 +932,8 @@ template <typename T, int DH> struct EpiSweep2 {
 // are exactly the rows this block wrote, its K rows came from sweep s's GEMM 1 (the
 // previous launch). Nothing crosses blocks, one launch per sweep less.
 // Epilogue layout: thread t owns row t / 4 and columns (t % 4) DH / 4 .. + DH / 4 - 1.
+// As a GEMM tile epilogue (64 x DH blocks) it is GEMM 2 with whole heads per block, which the
+// v_ctx norm needs.
 // ---------------------------------------------------------------------------
 template <typename T, int DH> struct EpiSweep2Head {
   static constexpr int CW = DH / 4;   // columns per thread
@@ -864,6 +945,7 @@ template <typename T, int DH> struct EpiSweep2Head {
   T* __restrict__ Vout;
   long out_stride; int out_row0;
   T* __restrict__ save2;
+  const float* __restrict__ vgain = nullptr;   // v_ctx norm gains [h] (norm_vctx), nullptr = off
   struct TilePre {
     floatx4 gx[CW / 4], gu[CW / 4];
     Raw8<T> vr[CW / 8];
@@ -888,7 +970,12 @@ template <typename T, int DH> struct EpiSweep2Head {
     for (int k = 0; k < CW / 8; ++k) pr.vr[k] = ld8_global(vr + 8 * k);
     return pr;
   }
-  // v'' of the thread's columns into Vout (and save2 = raw v_ctx) and into vs [64][ldv]
+  template <int BM, int BN, int LDT>
+  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre& pr, int) const {
+    static_assert(BM == 64 && BN == DH, "GEMM 2 head tile is 64 x DH");
+    apply<LDT>(tile, m0, n0, pr, nullptr, 0);
+  }
+  // v'' of the thread's columns into Vout (and save2 = raw v_ctx) and into vs [64][ldv] (if given)
   template <int LDT>
   DM_DEV void apply(const float* tile, int m0, int n0, const TilePre& pr, T* vs, int ldv) const {
     const int r = threadIdx.x >> 2, e0 = CW * (threadIdx.x & 3), col = n0 + e0;
@@ -902,10 +989,26 @@ template <typename T, int DH> struct EpiSweep2Head {
     }
 #pragma unroll
     for (int k = 0; k < CW / 8; ++k) unpack8<T>(pr.vr[k], vr + 8 * k);
+    float vc[CW];   // v_ctx as the blend takes it: normed (from and to stored values) with the norm on
+#pragma unroll
+    for (int i = 0; i < CW; ++i) vc[i] = a[i];
+    if (vgain != nullptr) {
+      float sn = 0.f;
+#pragma unroll
+      for (int i = 0; i < CW; ++i) {
+        vc[i] = stored<T>(a[i]);
+        sn += vc[i] * vc[i];
+      }
+      sn += __shfl_xor(sn, 1, 64);
+      sn += __shfl_xor(sn, 2, 64);
+      const float nr = head_norm_r(sn, 1.0f / DH), ng = vgain[n0 / DH];
+#pragma unroll
+      for (int i = 0; i < CW; ++i) vc[i] = stored<T>((vc[i] * nr) * ng);
+    }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < CW; ++i) {
-      v[i] = to_f(from_f<T>(value_blend(g, col + i, sigmoidf_(gx[i] + gu[i]), vr[i], a[i])));   // the stored value
+      v[i] = to_f(from_f<T>(value_blend(g, col + i, sigmoidf_(gx[i] + gu[i]), vr[i], vc[i])));   // the stored value
       ss += v[i] * v[i];
     }
     if (g.v_clamp_tau > 0.f) {   // norm clamp of the stored row (as k_clamp_v): the row's 4 threads
@@ -919,7 +1022,7 @@ template <typename T, int DH> struct EpiSweep2Head {
       }
     }
     settle(gx); settle(gu); settle(vr);   // all loads before any store
-    store_vec<T, CW>(vs + r * ldv + e0, v);
+    if (vs != nullptr) store_vec<T, CW>(vs + r * ldv + e0, v);
     if (m0 + r >= M) return;
     const int b = m / g.c, p = m - b * g.c;
     store_vec<T, CW>(Vout + ((long)b * g.h + n0 / DH) * out_stride + (long)(out_row0 + p) * DH + e0, v);

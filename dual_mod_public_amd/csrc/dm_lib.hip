@@ -100,6 +100,18 @@ int dm_pack_weights(const dm_config* c, const dm_params* p, const dm_packed* out
     else
       DM_HIP(hipMemcpyAsync(out->b_proj + (size_t)i * d, bsrc[i], (size_t)d * 4, hipMemcpyDeviceToDevice, s));
   }
+  // per-head norm gains -> fp32 gains[k_gain | ctx_gain | v_gain]
+  const void* gsrc[3] = {p->k_gain, p->ctx_gain, p->v_gain};
+  const int gbit[3] = {DM_NORM_K_CTX, DM_NORM_V_CTX, DM_NORM_V};
+  for (int i = 0; i < 3; ++i) {
+    if (!(c->norms & gbit[i])) continue;
+    DM_REQUIRE(gsrc[i] != nullptr && out->gains != nullptr, DM_ERR_INVALID, "norm gain %d: null pointer", i);
+    if (c->dtype == DM_BF16)
+      hipLaunchKernelGGL(k_to_f32<bf16>, dim3(cdiv(h, 256)), dim3(256), 0, s, (const bf16*)gsrc[i],
+                         out->gains + (size_t)i * h, h);
+    else
+      DM_HIP(hipMemcpyAsync(out->gains + (size_t)i * h, gsrc[i], (size_t)h * 4, hipMemcpyDeviceToDevice, s));
+  }
   // transposed copies for the backward's NT GEMMs
   auto tr = [&](const void* src, void* dst, int rows, int cols) {
     if (dst == nullptr) return;
@@ -144,7 +156,7 @@ int dm_layer_proj(const dm_config* c, const dm_packed* w, const void* x, const f
       xin = (const bf16*)L->xhat;
     }
     run_proj_dispatch<bf16>(c, w, xin, M, L->T, L->T, 0, 0, cos, sin, (bf16*)L->qr, (bf16*)L->kraw,
-                            (bf16*)L->kself, (bf16*)L->vraw, L->glogx, L->sig, s);
+                            (bf16*)L->kself, (bf16*)L->vraw, (bf16*)L->vpre, L->glogx, L->sig, s);
   } else {
     const float* xin = (const float*)x;
     if (norm) {
@@ -153,7 +165,7 @@ int dm_layer_proj(const dm_config* c, const dm_packed* w, const void* x, const f
       xin = (const float*)L->xhat;
     }
     run_proj_dispatch<float>(c, w, xin, M, L->T, L->T, 0, 0, cos, sin, (float*)L->qr, (float*)L->kraw,
-                             (float*)L->kself, (float*)L->vraw, L->glogx, L->sig, s);
+                             (float*)L->kself, (float*)L->vraw, (float*)L->vpre, L->glogx, L->sig, s);
   }
   DM_HIP(hipGetLastError());
   return DM_OK;
@@ -337,7 +349,7 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
   const int pos = a->pos;
   const int lo = (c->local_window > 0 && pos > c->local_window - 1) ? pos - (c->local_window - 1) : 0;
   run_proj<T, DH>(c, w, (const T*)a->xhat, B, 1, 1, 0, pos, cos, sin, (T*)ws.q, (T*)ws.kraw, (T*)ws.kself,
-                  (T*)ws.vraw, ws.glogx, ws.sig, s);
+                  (T*)ws.vraw, nullptr, ws.glogx, ws.sig, s);
   const int nsplit = pos > lo ? cdiv(pos - lo, DEC_SPLIT) : 0;
   DecodeArgs<T> da{B, h, d, a->tape_T, pos, lo, DEC_SPLIT, nsplit, 1.0f / sqrtf((float)DH),
                    (const T*)ws.q, (const T*)ws.kself, (const T*)ws.vraw, (const T*)a->K_tape,

@@ -48,8 +48,8 @@ def check_supported(cfg):
         bad.append("rmsnorm_on_o=False")
     if cfg.ctx_mod not in L.CTX_MOD:
         bad.append(f"ctx_mod={cfg.ctx_mod}")
-    for knob, off in (("k_ctx_norm", "none"), ("v_ctx_norm", "none"), ("v_norm", "none")):
-        if getattr(cfg, knob, off) != off:
+    for knob, _, _ in L.NORM_KNOBS:
+        if getattr(cfg, knob, "none") not in ("none", "rms"):
             bad.append(f"{knob}={getattr(cfg, knob)}")
     for knob in ("attn_logn_ref",):
         if getattr(cfg, knob, 0):
@@ -84,6 +84,9 @@ class PackedWeights:
         self.w_sweep_t = torch.empty(d, 4 * d, **kw) if with_transposes else None
         self.w_vctx_t = torch.empty(d, d, **kw) if (with_transposes and mult) else None
         self.wo_t = torch.empty(d, d, **kw) if with_transposes else None
+        # per-head norm gains, fp32: k_gain | ctx_gain | v_gain
+        self.gains = (torch.ones(3 * cfg.n_heads, device=device, dtype=torch.float32)
+                      if L.norm_bits(cfg) else None)
         self.has_attn_norm = False
 
     def struct(self, with_attn_norm=None):
@@ -92,6 +95,7 @@ class PackedWeights:
         s.w_vctx, s.norm_ctx_w, s.wo = L.ptr(self.w_vctx), L.ptr(self.norm_ctx_w), L.ptr(self.wo)
         s.w_proj_t, s.w_sweep_t = L.ptr(self.w_proj_t), L.ptr(self.w_sweep_t)
         s.w_vctx_t, s.wo_t = L.ptr(self.w_vctx_t), L.ptr(self.wo_t)
+        s.gains = L.ptr(self.gains)
         use = self.has_attn_norm if with_attn_norm is None else with_attn_norm
         s.attn_norm_w = L.ptr(self.attn_norm_w) if use else None
         return s
@@ -119,6 +123,9 @@ class PackedWeights:
             p.v_pre = t("v_pre.weight")
         elif cfg.ctx_mod != "linear":
             p.v_gate, p.b_vgate, p.v_map = t("v_gate.weight"), t("v_gate.bias"), t("v_map.weight")
+        for knob, _, gname in L.NORM_KNOBS:   # per-head norm gains (attention.py:113-166)
+            if getattr(cfg, knob, "none") == "rms":
+                setattr(p, gname, t(gname))
         if attn_norm_w is None and "attn_norm.weight" in sd:
             attn_norm_w = sd["attn_norm.weight"]
         if attn_norm_w is not None:
@@ -150,11 +157,13 @@ class LayerBufs:
         self.glogx = torch.empty(B, T, 2 * d, device=device, dtype=torch.float32)
         self.sig = (torch.empty(B, T, d, device=device, dtype=torch.float32)
                     if cfg.ctx_mod != "linear" else None)
+        # v_raw before the v_norm, kept for the backward
+        self.vpre = torch.empty(B, h, T, dh, **kw) if getattr(cfg, "v_norm", "none") == "rms" else None
 
     def struct(self):
         s = L.dm_layer_bufs()
         s.T = self.T
-        for n in ("xhat", "qr", "kraw", "kself", "vraw", "glogx", "sig"):
+        for n in ("xhat", "qr", "kraw", "kself", "vraw", "glogx", "sig", "vpre"):
             setattr(s, n, L.ptr(getattr(self, n)))
         return s
 
@@ -182,7 +191,10 @@ class LayerGrads:
             shapes["v_pre.weight"] = (d, 2 * d)
         elif mult:
             shapes.update({"v_gate.weight": (d, d), "v_gate.bias": (d,), "v_map.weight": (d, d)})
-        self.t = {k: torch.zeros(v, device=device, dtype=torch.float32) for k, v in shapes.items()}
+        for knob, _, gname in L.NORM_KNOBS:
+            if getattr(cfg, knob, "none") == "rms":
+                shapes[gname] = (cfg.n_heads,)
+        self.t ={k: torch.zeros(v, device=device, dtype=torch.float32) for k, v in shapes.items()}
 
     def zero_(self):
         for v in self.t.values():

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DM_ABI_VERSION 4
+#define DM_ABI_VERSION 5
 
 typedef enum dm_status {
   DM_OK = 0,
@@ -63,8 +63,19 @@ typedef struct dm_config {
   int32_t kmod_mode;        /* dm_kmod_mode (kmod_mode + kmod_vraw_bound), attention.py:362-384 */
   float v_clamp_tau;        /* config.py v_clamp_tau: v'' <- v'' min(1, tau / ||v''||) per (position,
                                head), attention.py:389-402; 0 = off */
-  int32_t reserved[3];
+  int32_t norms;            /* DM_NORM_* bits: the per-head RMS norms that are on */
+  int32_t reserved[2];
 } dm_config;
+
+/* Per-head RMS norms with a learned per-head gain, fp32, eps 1e-6 (attention.py:218-269):
+ *   K_CTX  k_ctx_norm="rms": k_ctx = w_kctx(u) -> norm_kctx (gain k_gain), before the key blend
+ *   V_CTX  v_ctx_norm="rms": v_ctx = w_vctx(v_in) -> norm_vctx (gain ctx_gain), before the value blend
+ *   V      v_norm="rms": v_raw = wv(xhat) -> project_v's norm (gain v_gain)
+ * y = gain * x * rsqrt(mean over the head's dh columns of x^2 + 1e-6); x is the projection's output
+ * rounded to the storage dtype and y is rounded to it again, as the reference's eager path does. */
+#define DM_NORM_K_CTX 1
+#define DM_NORM_V_CTX 2
+#define DM_NORM_V 4
 
 /* kmod heads (value columns of heads < kmod_vraw_heads), attention.py:362-384:
  * RAW v'' = v_raw; RAW_TANH v'' = tanh(v_raw) (kmod_vraw_bound="tanh");
@@ -92,6 +103,8 @@ typedef struct dm_params {
   const void* norm_ctx_w;                                            /* [d] */
   const void* attn_norm_w;                                           /* [d] (layer entry points) */
   const void* v_pre;                                                 /* [d, 2d]; ctx_mod fusion (attention.py:341-342) */
+  const void* k_gain; const void* ctx_gain; const void* v_gain;      /* [h] norm gains (attention.py:113-166),
+                                                                        read when the DM_NORM_* bit is set */
 } dm_params;
 
 /* Packed weights (written by dm_pack_weights, read by every compute call).
@@ -111,6 +124,7 @@ typedef struct dm_packed {
   void* w_sweep_t;  /* [d, 4d] */
   void* w_vctx_t;   /* [d, d]  (mult family) */
   void* wo_t;       /* [d, d]  */
+  float* gains;     /* [3h] fp32: k_gain | ctx_gain | v_gain (required when cfg->norms != 0) */
 } dm_packed;
 
 /* Per-layer projection buffers (fused_sweep.py:1179-1215 LayerBufs, own layout). */
@@ -123,6 +137,8 @@ typedef struct dm_layer_bufs {
   void* vraw;               /* [B, h, T, dh] raw value */
   float* glogx;             /* [B, T, 2d] */
   float* sig;               /* [B, T, d] or NULL (linear) */
+  void* vpre;               /* [B, h, T, dh] v_raw before the v_norm (DM_NORM_V only, kept for the
+                               backward; may be NULL for forward-only use) */
 } dm_layer_bufs;
 
 /* ---- version / errors ------------------------------------------------------ */
@@ -210,6 +226,7 @@ typedef struct dm_grads {
   float* norm_ctx_w;                                 /* [d] */
   float* attn_norm_w;                                /* [d] (when w->attn_norm_w != NULL) */
   float* v_pre;                                      /* [d, 2d] (fusion) */
+  float* k_gain; float* ctx_gain; float* v_gain;     /* [h] (with the matching DM_NORM_* bit) */
 } dm_grads;
 size_t dm_layer_bwd_workspace_bytes(const dm_config* cfg, int32_t T, int32_t cache_T, int32_t max_sweeps);
 int dm_layer_bwd(const dm_config* cfg, const dm_packed* w, const void* x, const void* dy, void* dx,

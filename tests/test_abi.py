@@ -30,7 +30,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 
 def test_abi_version():
-    assert L.load().dm_abi_version() == 4
+    assert L.load().dm_abi_version() == 5
 
 
 def _conf(**kw):
@@ -74,8 +74,7 @@ def test_workspace_query():
 
 def test_unsupported_knobs_raise():
     from dual_mod_public_amd.engine import check_supported
-    for kw in (dict(k_ctx_norm="rms"), dict(v_norm="rms"), dict(v_ctx_norm="rms"),
-               dict(gate_type_v="independent"), dict(ctx_mod="vmlp"), dict(attn_logn_ref=64)):
+    for kw in (dict(gate_type_v="independent"), dict(ctx_mod="vmlp"), dict(attn_logn_ref=64)):
         cfg = DualModConfig(d_model=256, n_heads=4, **kw)
         with pytest.raises(NotImplementedError):
             check_supported(cfg)
@@ -86,6 +85,22 @@ def test_unsupported_knobs_raise():
         check_supported(DualModConfig(d_model=256, n_heads=4, ctx_mod="mult_res", **kw))
     check_supported(DualModConfig(d_model=256, n_heads=4, ctx_mod="fusion"))
     check_supported(DualModConfig(d_model=256, n_heads=4, ctx_mod="mult_res", v_clamp_tau=1.0))
+    # per-head RMS norms (attention.py:218-269)
+    for kw in (dict(k_ctx_norm="rms"), dict(v_norm="rms"), dict(v_ctx_norm="rms")):
+        check_supported(DualModConfig(d_model=256, n_heads=4, ctx_mod="mult_res", **kw))
+
+
+def test_norm_config_bits():
+    """The head-norm knobs reach dm_config.norms; the library rejects unknown bits."""
+    import torch
+    cfg = DualModConfig(d_model=256, n_heads=4, k_ctx_norm="rms", v_norm="rms")
+    c = L.make_config(cfg, 2, torch.float32)
+    assert c.norms == L.DM_NORM_K_CTX | L.DM_NORM_V
+    assert L.make_config(DualModConfig(d_model=256, n_heads=4), 2, torch.float32).norms == 0
+    lib = L.load()
+    assert lib.dm_cell_workspace_bytes(ctypes.byref(c), 64) > 0
+    c.norms = 8
+    assert lib.dm_cell_workspace_bytes(ctypes.byref(c), 64) == 0
 
 
 def test_kmod_config_fields():
