@@ -155,8 +155,11 @@ static __global__ __launch_bounds__(256) void k_rmsnorm_rows(const T* __restrict
 // ---------------------------------------------------------------------------
 // projection epilogue: xhat . [wq | wk | wv | w_gk_x | w_gv_x | v_gate]^T
 // (fused_sweep.py:1403-1436 hoists; rope.py:22-33 on q and the raw key).
-// Wave tiles are one head wide (TN == DH) so RoPE pairs (j, j + DH/2) sit in
-// accumulator tiles j and j + FN/2 of the same lane.
+// A tile epilogue: the accumulators are staged in LDS, TILE_ROWS rows at a time, so the
+// epilogue's registers do not compete with a 128 x 128 wave tile's. The block's columns are
+// taken one head (DH columns) at a time; a head never straddles a segment (d is a multiple of
+// DH). q / k / v heads: DH / 8 lanes per row, each with 4 consecutive RoPE pairs (jj, jj + DH/2);
+// gate / v_gate columns: DH / 4 lanes per row, 4 consecutive columns each.
 // ---------------------------------------------------------------------------
 template <typename T, int DH> struct EpiProj {
   int M, d, h;
@@ -175,103 +178,111 @@ template <typename T, int DH> struct EpiProj {
   const float* __restrict__ vgain = nullptr;
   T* __restrict__ vpre = nullptr;
 
-  // The wave tile spans whole heads (FN * 16 a multiple of DH); within each head
-  // columns j and j + DH/32 of the tile are the RoPE pair (jj, jj + DH/2).
-  // The RoPE table values of 16-row group i + 1 are loaded before group i is
-  // stored (a load after a store that may alias it would wait for one memory
-  // latency per group).
-  template <int FM, int FN>
-  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*, int) const {
-    static_assert((FN * 16) % DH == 0, "projection wave tile must span whole heads");
-    constexpr int NHW = FN * 16 / DH;   // heads per wave tile
-    constexpr int FH = DH / 16;         // 16-column tiles per head
-    constexpr int HF = FH / 2;
-    const int lane = threadIdx.x & 63, lc = lane & 15;
-    const int seg = col0 / d, c0 = col0 - seg * d;
-    float cs[2][4][HF], sn[2][4][HF], bs[FN];
-    auto load_rope = [&](int i, int buf) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = min(row0 + 16 * i + 4 * (lane >> 4) + q, M - 1);
-        const long rrow = (long)(rope_t0 + m % Tl) * (DH / 2);
-#pragma unroll
-        for (int j = 0; j < HF; ++j) {
-          cs[buf][q][j] = cos[rrow + 16 * j + lc];
-          sn[buf][q][j] = sin[rrow + 16 * j + lc];
-        }
-      }
-    };
-    if (seg <= 1) load_rope(0, 0);
-    else if (seg >= 3) {
-      const int bo = (seg - 3) * d + c0;
-#pragma unroll
-      for (int j = 0; j < FN; ++j) bs[j] = bias[bo + 16 * j + lc];
+  static constexpr int TILE_ROWS = 64;
+  struct TilePre {};
+  DM_DEV TilePre tile_prefetch(int, int) const { return TilePre{}; }
+
+  template <int TR, int BN, int LDT>
+  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre&, int) const {
+    static_assert(BN % DH == 0, "whole heads per block");
+#pragma unroll 1
+    for (int hu = 0; hu < BN / DH; ++hu) {
+      const int col0 = n0 + hu * DH;
+      const int seg = col0 / d, c0 = col0 - seg * d;
+      if (seg <= 2) head_unit<TR, LDT>(tile + hu * DH, m0, seg, c0 / DH);
+      else row_unit<TR, LDT>(tile + hu * DH, m0, seg, c0);
     }
+  }
+
+  // q (rotated), k (raw and rotated) or v (raw, or normed) of head hh for the chunk's rows
+  template <int TR, int LDT>
+  DM_DEV void head_unit(const float* tl, int m0, int seg, int hh) const {
+    constexpr int L = DH / 8;     // lanes per row
+    constexpr int RP = 256 / L;   // rows per pass
+    static_assert(TR % RP == 0, "whole passes");
+    const int jj = 4 * (threadIdx.x % L);
+    const float gn = (seg == 2 && vgain != nullptr) ? vgain[hh] : 0.f;
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int cb = i & 1;
-      if (seg <= 1 && i + 1 < FM) load_rope(i + 1, cb ^ 1);
+    for (int pass = 0; pass < TR / RP; ++pass) {
+      const int r = threadIdx.x / L + pass * RP, m = m0 + r;
+      const floatx4 av = *reinterpret_cast<const floatx4*>(tl + r * LDT + jj);
+      const floatx4 bv = *reinterpret_cast<const floatx4*>(tl + r * LDT + jj + DH / 2);
+      float a[4] = {av.x, av.y, av.z, av.w}, b[4] = {bv.x, bv.y, bv.z, bv.w};
+      float nr = 0.f;
+      if (seg == 2 && vgain != nullptr) {   // the head's sum of squares over the row's L lanes
+        float ss = 0.f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
-        if (m >= M) continue;
-        const int b = m / Tl, tl = m - b * Tl;
-        const long xrow = (long)b * Tbuf + buf_t0 + tl;
-#pragma unroll
-        for (int hb = 0; hb < NHW; ++hb) {
-          const int hh = c0 / DH + hb;
-          const long hrow = (((long)b * h + hh) * Tbuf + buf_t0 + tl) * DH;
-          if (seg <= 1) {
-#pragma unroll
-            for (int j = 0; j < HF; ++j) {
-              const int jj = 16 * j + lc;
-              const float a = acc[i][hb * FH + j][q], bb = acc[i][hb * FH + j + HF][q];
-              const float c = cs[cb][q][j], sv = sn[cb][q][j];
-              if (seg == 0) {
-                qr[hrow + jj] = from_f<T>(a * c - bb * sv);
-                qr[hrow + jj + DH / 2] = from_f<T>(bb * c + a * sv);
-              } else {
-                kraw[hrow + jj] = from_f<T>(a);
-                kraw[hrow + jj + DH / 2] = from_f<T>(bb);
-                kself[hrow + jj] = from_f<T>(a * c - bb * sv);
-                kself[hrow + jj + DH / 2] = from_f<T>(bb * c + a * sv);
-              }
-            }
-          } else if (seg == 2) {
-            if (vgain != nullptr) {
-              // the head's DH columns of row m: FH tiles x the 16 lanes that share lane >> 4
-              float x[FH], ss = 0.f;
-#pragma unroll
-              for (int j = 0; j < FH; ++j) {
-                x[j] = stored<T>(acc[i][hb * FH + j][q]);
-                ss += x[j] * x[j];
-              }
-              const float nr = head_norm_r(group16_sum(ss), 1.0f / DH), ng = vgain[hh];
-#pragma unroll
-              for (int j = 0; j < FH; ++j) {
-                if (vpre != nullptr) vpre[hrow + 16 * j + lc] = from_f<T>(x[j]);
-                vraw[hrow + 16 * j + lc] = from_f<T>((x[j] * nr) * ng);
-              }
-            } else {
-#pragma unroll
-              for (int j = 0; j < FH; ++j) vraw[hrow + 16 * j + lc] = from_f<T>(acc[i][hb * FH + j][q]);
-            }
-          }
+        for (int i = 0; i < 4; ++i) {
+          a[i] = stored<T>(a[i]);
+          b[i] = stored<T>(b[i]);
+          ss += a[i] * a[i] + b[i] * b[i];
         }
-        if (seg == 3 || seg == 4) {
-          const int gs = seg - 3;
+        nr = head_norm_r(group_sum<L>(ss), 1.0f / DH);
+      }
+      if (m >= M) continue;
+      const int bb = m / Tl, t = m - bb * Tl;
+      const long hrow = (((long)bb * h + hh) * Tbuf + buf_t0 + t) * DH + jj;
+      if (seg <= 1) {
+        const long rrow = (long)(rope_t0 + t) * (DH / 2) + jj;
+        float c[4], s[4], o1[4], o2[4];
+        unpackf4(ld_global<floatx4>(cos + rrow), c);
+        unpackf4(ld_global<floatx4>(sin + rrow), s);
 #pragma unroll
-          for (int j = 0; j < FN; ++j) {
-            const int col = c0 + 16 * j + lc;
-            glogx[xrow * 2 * d + gs * d + col] = acc[i][j][q] + bs[j];
-          }
-        } else if (seg == 5) {
-#pragma unroll
-          for (int j = 0; j < FN; ++j) {
-            const int col = c0 + 16 * j + lc;
-            sig[xrow * d + col] = fusion ? acc[i][j][q] : sigmoidf_(acc[i][j][q] + bs[j]);
-          }
+        for (int i = 0; i < 4; ++i) {
+          o1[i] = a[i] * c[i] - b[i] * s[i];
+          o2[i] = b[i] * c[i] + a[i] * s[i];
         }
+        if (seg == 0) {
+          st4<T>(qr + hrow, o1);
+          st4<T>(qr + hrow + DH / 2, o2);
+        } else {
+          st4<T>(kraw + hrow, a);
+          st4<T>(kraw + hrow + DH / 2, b);
+          st4<T>(kself + hrow, o1);
+          st4<T>(kself + hrow + DH / 2, o2);
+        }
+      } else if (vgain != nullptr) {
+        float ya[4], yb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ya[i] = (a[i] * nr) * gn;
+          yb[i] = (b[i] * nr) * gn;
+        }
+        st4<T>(vraw + hrow, ya);
+        st4<T>(vraw + hrow + DH / 2, yb);
+        if (vpre != nullptr) {
+          st4<T>(vpre + hrow, a);
+          st4<T>(vpre + hrow + DH / 2, b);
+        }
+      } else {
+        st4<T>(vraw + hrow, a);
+        st4<T>(vraw + hrow + DH / 2, b);
+      }
+    }
+  }
+
+  // gate logits (x-halves + bias, fp32) or sigma(v_gate) / fusion's raw v_pre x-half
+  template <int TR, int LDT>
+  DM_DEV void row_unit(const float* tl, int m0, int seg, int c0) const {
+    constexpr int L = DH / 4;
+    constexpr int RP = 256 / L;
+    static_assert(TR % RP == 0, "whole passes");
+    const int e = 4 * (threadIdx.x % L), col = c0 + e;
+    float bs[4] = {0.f, 0.f, 0.f, 0.f};
+    if (!(seg == 5 && fusion)) unpackf4(ld_global<floatx4>(bias + (seg - 3) * d + col), bs);
+#pragma unroll
+    for (int pass = 0; pass < TR / RP; ++pass) {
+      const int r = threadIdx.x / L + pass * RP, m = m0 + r;
+      if (m >= M) continue;
+      const floatx4 v = *reinterpret_cast<const floatx4*>(tl + r * LDT + e);
+      const int bb = m / Tl, t = m - bb * Tl;
+      const long xrow = (long)bb * Tbuf + buf_t0 + t;
+      floatx4 o = floatx4{v.x + bs[0], v.y + bs[1], v.z + bs[2], v.w + bs[3]};
+      if (seg <= 4) {
+        *reinterpret_cast<floatx4*>(glogx + xrow * 2 * d + (seg - 3) * d + col) = o;
+      } else {
+        if (!fusion) o = floatx4{sigmoidf_(o.x), sigmoidf_(o.y), sigmoidf_(o.z), sigmoidf_(o.w)};
+        *reinterpret_cast<floatx4*>(sig + xrow * d + col) = o;
       }
     }
   }
