@@ -90,15 +90,17 @@ template <int DH> DM_DEV int col_vlin(int d, int hd, int e) {
 }
 
 // ---------------------------------------------------------------------------
-// refine VJP of one sweep (attention.py:314-387 backward), one thread per
-// (row m, head hd, pair jj < DH/2): K pair (jj, jj + DH/2), V elements jj, jj + DH/2.
+// refine VJP of one sweep (attention.py:314-387 backward). One item = (row m, head hd,
+// 4 consecutive RoPE pairs jj..jj+3): K pairs (jj + i, jj + i + DH/2), V elements likewise.
+// The DH / 8 items of a (row, head) are consecutive lanes, which reduce the head-wide sums of
+// the k_ctx / v_ctx norms and of the v'' clamp.
 // ---------------------------------------------------------------------------
 template <typename T> struct RefineBwdArgs {
   CellGeom g;
   int N, ctx_mod;
   const float* dK; const float* dV;    // grads of the refined rows (rotated K, V): the sum of
   long dk_stride; int dk_row0;         //   NS slices psum_stride apart, (b,h) at bh*dk_stride,
-  long psum_stride;                    //   chunk row p at row dk_row0 + p
+  long psum_stride;                    //   chunk row p at row dk_row0 + p (standalone kernel)
   const T* save1;                      // [N, 4d] raw GEMM-1 outputs of this sweep (storage dtype)
   const T* save2;                      // [N, d] raw v_ctx (mult family)
   const float* glogx; const T* kraw; const T* vraw;
@@ -112,154 +114,284 @@ template <typename T> struct RefineBwdArgs {
   float* dkg = nullptr; float* dvg = nullptr;
 };
 
-template <typename T, int DH, int NS>
-static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
+// the grads of one item's refined values: K at columns jj.. (a) and jj + DH/2.. (b), V likewise
+struct RefineGrad4 {
+  float ka[4], kb[4], va[4], vb[4];
+};
+
+template <typename T> DM_DEV void ld4(const T* p, float* out) {
+  if constexpr (sizeof(T) == 2) unpack4<T>(ld_global<typename Raw4<T>::type>(p), out);
+  else unpackf4(ld_global<floatx4>(p), out);
+}
+
+// The gathered inputs of one item (the loads, issued together before any math)
+struct RefineIn {
+  float cs[4], sn[4], kx1[4], kx2[4], gu1[4], gu2[4], gx1[4], gx2[4], gxv1[4], gxv2[4];
+  float kr1[4], kr2[4], vr1[4], vr2[4], vx1[4], vx2[4], gvu1[4], gvu2[4];
+  float ogx1[4], ogx2[4], ogxv1[4], ogxv2[4], okr1[4], okr2[4], ovr1[4], ovr2[4];
+};
+
+template <typename T, int DH>
+DM_DEV RefineIn refine_gather(const RefineBwdArgs<T>& a, int m, int hd, int jj) {
   const CellGeom& g = a.g;
   const int d = g.d, h = g.h;
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  const int per_row = d / 2;
-  if (idx >= a.N * per_row) return;
-  const int m = idx / per_row, rem = idx - m * per_row;
-  const int hd = rem / (DH / 2), jj = rem - hd * (DH / 2);
   const int b = m / g.c, p = m - b * g.c;
   const int t = g.buf_t0 + p, pos = rope_row(g, p);
-  const long bh = (long)b * h + hd;
-  const long drow = bh * a.dk_stride + (long)(a.dk_row0 + p) * DH;
-  const long lrow = (bh * g.Tbuf + t) * DH;
+  const long lrow = (((long)b * h + hd) * g.Tbuf + t) * DH + jj;
   const long xrow = (long)b * g.Tbuf + t;
   const T* S1 = a.save1 + (long)m * 4 * d;
-  const float* gx = a.glogx + xrow * 2 * d;
-  // ---- gather
-  float da = 0.f, db = 0.f, dv1 = 0.f, dv2 = 0.f;
-#pragma unroll
-  for (int q = 0; q < NS; ++q) {
-    const long o = q * a.psum_stride + drow + jj;
-    da += a.dK[o]; db += a.dK[o + DH / 2];
-    dv1 += a.dV[o]; dv2 += a.dV[o + DH / 2];
-  }
-  const float cs = a.cos[(long)pos * (DH / 2) + jj], sn = a.sin[(long)pos * (DH / 2) + jj];
-  const float kx1 = to_f(S1[col_k<DH>(hd, jj, 0)]), kx2 = to_f(S1[col_k<DH>(hd, jj, 1)]);
-  const float gu1 = to_f(S1[col_k<DH>(hd, jj, 2)]), gu2 = to_f(S1[col_k<DH>(hd, jj, 3)]);
-  const float gx1 = gx[hd * DH + jj], gx2 = gx[hd * DH + jj + DH / 2];
-  const float kr1 = to_f(a.kraw[lrow + jj]), kr2 = to_f(a.kraw[lrow + jj + DH / 2]);
-  const float vr1 = to_f(a.vraw[lrow + jj]), vr2 = to_f(a.vraw[lrow + jj + DH / 2]);
-  const float gxv1 = gx[d + hd * DH + jj], gxv2 = gx[d + hd * DH + jj + DH / 2];
+  const float* gxr = a.glogx + xrow * 2 * d;
+  const float* dgx = a.dglogx + xrow * 2 * d;
   const int c1 = hd * DH + jj, c2 = c1 + DH / 2;
-  float vx1, vx2, gvu1, gvu2;
-  int cv1 = 0, cv2 = 0;
+  RefineIn in;
+  ld4<float>(a.cos + (long)pos * (DH / 2) + jj, in.cs);
+  ld4<float>(a.sin + (long)pos * (DH / 2) + jj, in.sn);
+  ld4<T>(S1 + col_k<DH>(hd, jj, 0), in.kx1);
+  ld4<T>(S1 + col_k<DH>(hd, jj, 1), in.kx2);
+  ld4<T>(S1 + col_k<DH>(hd, jj, 2), in.gu1);
+  ld4<T>(S1 + col_k<DH>(hd, jj, 3), in.gu2);
+  ld4<float>(gxr + c1, in.gx1);
+  ld4<float>(gxr + c2, in.gx2);
+  ld4<float>(gxr + d + c1, in.gxv1);
+  ld4<float>(gxr + d + c2, in.gxv2);
+  ld4<T>(a.kraw + lrow, in.kr1);
+  ld4<T>(a.kraw + lrow + DH / 2, in.kr2);
+  ld4<T>(a.vraw + lrow, in.vr1);
+  ld4<T>(a.vraw + lrow + DH / 2, in.vr2);
   if (a.ctx_mod == 0) {
-    cv1 = col_vlin<DH>(d, hd, jj);
-    cv2 = col_vlin<DH>(d, hd, jj + DH / 2);
-    vx1 = to_f(S1[cv1]); vx2 = to_f(S1[cv2]);
-    gvu1 = to_f(S1[cv1 + 32]); gvu2 = to_f(S1[cv2 + 32]);
+    const int cv1 = col_vlin<DH>(d, hd, jj), cv2 = col_vlin<DH>(d, hd, jj + DH / 2);
+    ld4<T>(S1 + cv1, in.vx1);
+    ld4<T>(S1 + cv2, in.vx2);
+    ld4<T>(S1 + cv1 + 32, in.gvu1);
+    ld4<T>(S1 + cv2 + 32, in.gvu2);
   } else {
-    vx1 = to_f(a.save2[(long)m * d + c1]); vx2 = to_f(a.save2[(long)m * d + c2]);
-    gvu1 = to_f(S1[3 * d + c1]); gvu2 = to_f(S1[3 * d + c2]);
+    ld4<T>(a.save2 + (long)m * d + c1, in.vx1);
+    ld4<T>(a.save2 + (long)m * d + c2, in.vx2);
+    ld4<T>(S1 + 3 * d + c1, in.gvu1);
+    ld4<T>(S1 + 3 * d + c2, in.gvu2);
   }
-  // k_ctx / v_ctx as the blends took them: raw (kx, vx), or normed, (x r) gain from and to stored
-  // values, r over the head's DH / 2 lanes (consecutive, a whole group of each wave)
-  float kc1 = kx1, kc2 = kx2, vc1 = vx1, vc2 = vx2, rk = 0.f, gk = 0.f, rv = 0.f, gvn = 0.f;
+  // the accumulators' current values, loaded with the inputs (one memory round trip)
+  ld4<float>(dgx + c1, in.ogx1);
+  ld4<float>(dgx + c2, in.ogx2);
+  ld4<float>(dgx + d + c1, in.ogxv1);
+  ld4<float>(dgx + d + c2, in.ogxv2);
+  ld4<float>(a.dkraw + lrow, in.okr1);
+  ld4<float>(a.dkraw + lrow + DH / 2, in.okr2);
+  ld4<float>(a.dvraw + lrow, in.ovr1);
+  ld4<float>(a.dvraw + lrow + DH / 2, in.ovr2);
+  return in;
+}
+
+template <typename T, int DH>
+DM_DEV void refine_apply(const RefineBwdArgs<T>& a, int m, int hd, int jj, const RefineIn& in,
+                         const RefineGrad4& gr) {
+  constexpr int L = DH / 8;   // lanes per (row, head)
+  const CellGeom& g = a.g;
+  const int d = g.d, h = g.h;
+  const int b = m / g.c, p = m - b * g.c;
+  const int t = g.buf_t0 + p;
+  const long lrow = (((long)b * h + hd) * g.Tbuf + t) * DH + jj;
+  const long xrow = (long)b * g.Tbuf + t;
+  float* dgx = a.dglogx + xrow * 2 * d;
+  const int c1 = hd * DH + jj, c2 = c1 + DH / 2;
+  // k_ctx / v_ctx as the blends took them: raw (kx, vx), or normed, (x r) gain from and to
+  // stored values, r over the head's L lanes
+  float kc1[4], kc2[4], vc1[4], vc2[4];
+  float rk = 0.f, gk = 0.f, rv = 0.f, gvn = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { kc1[i] = in.kx1[i]; kc2[i] = in.kx2[i]; vc1[i] = in.vx1[i]; vc2[i] = in.vx2[i]; }
   if (a.kgain != nullptr) {
-    rk = head_norm_r(group_sum<DH / 2>(kx1 * kx1 + kx2 * kx2), 1.0f / DH);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss += in.kx1[i] * in.kx1[i] + in.kx2[i] * in.kx2[i];
+    rk = head_norm_r(group_sum<L>(ss), 1.0f / DH);
     gk = a.kgain[hd];
-    kc1 = stored<T>((kx1 * rk) * gk);
-    kc2 = stored<T>((kx2 * rk) * gk);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { kc1[i] = stored<T>((in.kx1[i] * rk) * gk); kc2[i] = stored<T>((in.kx2[i] * rk) * gk); }
   }
   if (a.vgain != nullptr) {
-    rv = head_norm_r(group_sum<DH / 2>(vx1 * vx1 + vx2 * vx2), 1.0f / DH);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss += in.vx1[i] * in.vx1[i] + in.vx2[i] * in.vx2[i];
+    rv = head_norm_r(group_sum<L>(ss), 1.0f / DH);
     gvn = a.vgain[hd];
-    vc1 = stored<T>((vx1 * rv) * gvn);
-    vc2 = stored<T>((vx2 * rv) * gvn);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { vc1[i] = stored<T>((in.vx1[i] * rv) * gvn); vc2[i] = stored<T>((in.vx2[i] * rv) * gvn); }
   }
-  // the accumulators' current values, loaded with the gather (one memory round trip)
-  float* dgx = a.dglogx + xrow * 2 * d;
-  const float ogx1 = dgx[c1], ogx2 = dgx[c2], ogxv1 = dgx[d + c1], ogxv2 = dgx[d + c2];
-  const float okr1 = a.dkraw[lrow + jj], okr2 = a.dkraw[lrow + jj + DH / 2];
-  const float ovr1 = a.dvraw[lrow + jj], ovr2 = a.dvraw[lrow + jj + DH / 2];
   // ---- key: unrotate, then the convex blend k'' = g k_raw + (1 - g) k_ctx
-  const float dk1 = da * cs + db * sn, dk2 = -da * sn + db * cs;
-  const float g1 = sigmoidf_(gx1 + gu1), g2 = sigmoidf_(gx2 + gu2);
-  const float dl1 = dk1 * (kr1 - kc1) * g1 * (1.f - g1);
-  const float dl2 = dk2 * (kr2 - kc2) * g2 * (1.f - g2);
-  T* D = a.dctx + (long)m * 4 * d;
-  float dkc1 = dk1 * (1.f - g1), dkc2 = dk2 * (1.f - g2);
+  float dkc1[4], dkc2[4], dl1[4], dl2[4], nk1[4], nk2[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float dk1 = gr.ka[i] * in.cs[i] + gr.kb[i] * in.sn[i], dk2 = -gr.ka[i] * in.sn[i] + gr.kb[i] * in.cs[i];
+    const float g1 = sigmoidf_(in.gx1[i] + in.gu1[i]), g2 = sigmoidf_(in.gx2[i] + in.gu2[i]);
+    dl1[i] = dk1 * (in.kr1[i] - kc1[i]) * g1 * (1.f - g1);
+    dl2[i] = dk2 * (in.kr2[i] - kc2[i]) * g2 * (1.f - g2);
+    dkc1[i] = dk1 * (1.f - g1);
+    dkc2[i] = dk2 * (1.f - g2);
+    nk1[i] = in.okr1[i] + dk1 * g1;
+    nk2[i] = in.okr2[i] + dk2 * g2;
+  }
   if (a.kgain != nullptr) {
     // norm VJP: dx = gain (r dy - r^3 x <dy, x> / DH); d gain += r <dy, x> (this row's partial)
-    const float sk = group_sum<DH / 2>(dkc1 * kx1 + dkc2 * kx2);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s += dkc1[i] * in.kx1[i] + dkc2[i] * in.kx2[i];
+    const float sk = group_sum<L>(s);
     const float r3 = rk * rk * rk * sk * (1.0f / DH);
-    dkc1 = gk * (rk * dkc1 - r3 * kx1);
-    dkc2 = gk * (rk * dkc2 - r3 * kx2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      dkc1[i] = gk * (rk * dkc1[i] - r3 * in.kx1[i]);
+      dkc2[i] = gk * (rk * dkc2[i] - r3 * in.kx2[i]);
+    }
     if (jj == 0) a.dkg[xrow * h + hd] += rk * sk;
   }
-  D[col_k<DH>(hd, jj, 0)] = from_f<T>(dkc1);
-  D[col_k<DH>(hd, jj, 1)] = from_f<T>(dkc2);
-  D[col_k<DH>(hd, jj, 2)] = from_f<T>(dl1);
-  D[col_k<DH>(hd, jj, 3)] = from_f<T>(dl2);
-  dgx[c1] = ogx1 + dl1;
-  dgx[c2] = ogx2 + dl2;
-  a.dkraw[lrow + jj] = okr1 + dk1 * g1;
-  a.dkraw[lrow + jj + DH / 2] = okr2 + dk2 * g2;
   // ---- value: v'' = g_v v_raw + (1 - g_v) v_ctx; kmod heads (attention.py:362-384):
   // raw v'' = v_raw (or tanh(v_raw)) takes no gate or v_ctx grad; gated_norm blends with
   // v_ctx = 0 (live gate, no v_ctx grad)
-  const float gv1 = sigmoidf_(gxv1 + gvu1), gv2 = sigmoidf_(gxv2 + gvu2);
+  float dv1[4], dv2[4], gv1[4], gv2[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    dv1[i] = gr.va[i];
+    dv2[i] = gr.vb[i];
+    gv1[i] = sigmoidf_(in.gxv1[i] + in.gvu1[i]);
+    gv2[i] = sigmoidf_(in.gxv2[i] + in.gvu2[i]);
+  }
   if (g.v_clamp_tau > 0.f) {
-    // VJP of the norm clamp v = v'' min(1, tau / ||v''||) (attention.py:389-402) over the
-    // head's DH / 2 lanes (consecutive, a whole group of each wave): outside the radius
-    // dv'' = (tau / n) (dv - v'' <v'', dv> / n^2), n = ||v''||, else dv'' = dv
-    const float p1 = value_blend(g, c1, gv1, vr1, vc1), p2 = value_blend(g, c2, gv2, vr2, vc2);
-    const float ss = group_sum<DH / 2>(p1 * p1 + p2 * p2);
-    const float dt = group_sum<DH / 2>(p1 * dv1 + p2 * dv2);
+    // VJP of the norm clamp v = v'' min(1, tau / ||v''||) (attention.py:389-402): outside the
+    // radius dv'' = (tau / n) (dv - v'' <v'', dv> / n^2), n = ||v''||, else dv'' = dv
+    float p1[4], p2[4], ss = 0.f, dt = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p1[i] = value_blend(g, c1 + i, gv1[i], in.vr1[i], vc1[i]);
+      p2[i] = value_blend(g, c2 + i, gv2[i], in.vr2[i], vc2[i]);
+      ss += p1[i] * p1[i] + p2[i] * p2[i];
+      dt += p1[i] * dv1[i] + p2[i] * dv2[i];
+    }
+    ss = group_sum<L>(ss);
+    dt = group_sum<L>(dt);
     const float n = sqrtf(ss);
     if (n > g.v_clamp_tau) {
       const float sc = g.v_clamp_tau / n, k = dt / ss;
-      dv1 = sc * (dv1 - p1 * k);
-      dv2 = sc * (dv2 - p2 * k);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dv1[i] = sc * (dv1[i] - p1[i] * k);
+        dv2[i] = sc * (dv2[i] - p2[i] * k);
+      }
     }
   }
-  float dlv1, dlv2, dvc1, dvc2, dvr1, dvr2;
-  if (c1 < g.kmod_cols) {
-    const bool gated = g.kmod_mode == DM_KMOD_GATED_NORM;
-    dlv1 = gated ? dv1 * vr1 * gv1 * (1.f - gv1) : 0.f;
-    dlv2 = gated ? dv2 * vr2 * gv2 * (1.f - gv2) : 0.f;
-    dvc1 = 0.f;
-    dvc2 = 0.f;
-    if (gated) { dvr1 = dv1 * gv1; dvr2 = dv2 * gv2; }
-    else if (g.kmod_mode == DM_KMOD_RAW_TANH) {
-      const float t1 = tanhf_(vr1), t2 = tanhf_(vr2);
-      dvr1 = dv1 * (1.f - t1 * t1);
-      dvr2 = dv2 * (1.f - t2 * t2);
-    } else { dvr1 = dv1; dvr2 = dv2; }
-  } else {
-    dlv1 = dv1 * (vr1 - vc1) * gv1 * (1.f - gv1);
-    dlv2 = dv2 * (vr2 - vc2) * gv2 * (1.f - gv2);
-    dvc1 = dv1 * (1.f - gv1);
-    dvc2 = dv2 * (1.f - gv2);
-    dvr1 = dv1 * gv1;
-    dvr2 = dv2 * gv2;
+  float dlv1[4], dlv2[4], dvc1[4], dvc2[4], nv1[4], nv2[4];
+  const bool kmod = c1 < g.kmod_cols;   // whole heads: uniform over the item
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float dvr1, dvr2;
+    if (kmod) {
+      const bool gated = g.kmod_mode == DM_KMOD_GATED_NORM;
+      dlv1[i] = gated ? dv1[i] * in.vr1[i] * gv1[i] * (1.f - gv1[i]) : 0.f;
+      dlv2[i] = gated ? dv2[i] * in.vr2[i] * gv2[i] * (1.f - gv2[i]) : 0.f;
+      dvc1[i] = 0.f;
+      dvc2[i] = 0.f;
+      if (gated) { dvr1 = dv1[i] * gv1[i]; dvr2 = dv2[i] * gv2[i]; }
+      else if (g.kmod_mode == DM_KMOD_RAW_TANH) {
+        const float t1 = tanhf_(in.vr1[i]), t2 = tanhf_(in.vr2[i]);
+        dvr1 = dv1[i] * (1.f - t1 * t1);
+        dvr2 = dv2[i] * (1.f - t2 * t2);
+      } else { dvr1 = dv1[i]; dvr2 = dv2[i]; }
+    } else {
+      dlv1[i] = dv1[i] * (in.vr1[i] - vc1[i]) * gv1[i] * (1.f - gv1[i]);
+      dlv2[i] = dv2[i] * (in.vr2[i] - vc2[i]) * gv2[i] * (1.f - gv2[i]);
+      dvc1[i] = dv1[i] * (1.f - gv1[i]);
+      dvc2[i] = dv2[i] * (1.f - gv2[i]);
+      dvr1 = dv1[i] * gv1[i];
+      dvr2 = dv2[i] * gv2[i];
+    }
+    nv1[i] = in.ovr1[i] + dvr1;
+    nv2[i] = in.ovr2[i] + dvr2;
   }
   if (a.vgain != nullptr) {   // v_ctx norm VJP, as the key's (kmod heads: dvc = 0, so zero)
-    const float sv = group_sum<DH / 2>(dvc1 * vx1 + dvc2 * vx2);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s += dvc1[i] * in.vx1[i] + dvc2[i] * in.vx2[i];
+    const float sv = group_sum<L>(s);
     const float r3 = rv * rv * rv * sv * (1.0f / DH);
-    dvc1 = gvn * (rv * dvc1 - r3 * vx1);
-    dvc2 = gvn * (rv * dvc2 - r3 * vx2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      dvc1[i] = gvn * (rv * dvc1[i] - r3 * in.vx1[i]);
+      dvc2[i] = gvn * (rv * dvc2[i] - r3 * in.vx2[i]);
+    }
     if (jj == 0) a.dvg[xrow * h + hd] += rv * sv;
   }
+  // ---- stores
+  T* D = a.dctx + (long)m * 4 * d;
+  st4<T>(D + col_k<DH>(hd, jj, 0), dkc1);
+  st4<T>(D + col_k<DH>(hd, jj, 1), dkc2);
+  st4<T>(D + col_k<DH>(hd, jj, 2), dl1);
+  st4<T>(D + col_k<DH>(hd, jj, 3), dl2);
   if (a.ctx_mod == 0) {
-    D[cv1] = from_f<T>(dvc1);
-    D[cv2] = from_f<T>(dvc2);
-    D[cv1 + 32] = from_f<T>(dlv1);
-    D[cv2 + 32] = from_f<T>(dlv2);
+    const int cv1 = col_vlin<DH>(d, hd, jj), cv2 = col_vlin<DH>(d, hd, jj + DH / 2);
+    st4<T>(D + cv1, dvc1);
+    st4<T>(D + cv2, dvc2);
+    st4<T>(D + cv1 + 32, dlv1);
+    st4<T>(D + cv2 + 32, dlv2);
   } else {
-    a.dvc[(long)m * d + c1] = from_f<T>(dvc1);
-    a.dvc[(long)m * d + c2] = from_f<T>(dvc2);
-    D[3 * d + c1] = from_f<T>(dlv1);
-    D[3 * d + c2] = from_f<T>(dlv2);
+    st4<T>(a.dvc + (long)m * d + c1, dvc1);
+    st4<T>(a.dvc + (long)m * d + c2, dvc2);
+    st4<T>(D + 3 * d + c1, dlv1);
+    st4<T>(D + 3 * d + c2, dlv2);
   }
-  dgx[d + c1] = ogxv1 + dlv1;
-  dgx[d + c2] = ogxv2 + dlv2;
-  a.dvraw[lrow + jj] = ovr1 + dvr1;
-  a.dvraw[lrow + jj + DH / 2] = ovr2 + dvr2;
+  float ng[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ng[i] = in.ogx1[i] + dl1[i];
+  st4<float>(dgx + c1, ng);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ng[i] = in.ogx2[i] + dl2[i];
+  st4<float>(dgx + c2, ng);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ng[i] = in.ogxv1[i] + dlv1[i];
+  st4<float>(dgx + d + c1, ng);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ng[i] = in.ogxv2[i] + dlv2[i];
+  st4<float>(dgx + d + c2, ng);
+  st4<float>(a.dkraw + lrow, nk1);
+  st4<float>(a.dkraw + lrow + DH / 2, nk2);
+  st4<float>(a.dvraw + lrow, nv1);
+  st4<float>(a.dvraw + lrow + DH / 2, nv2);
+}
+
+
+template <typename T, int DH>
+DM_DEV void refine_vjp4(const RefineBwdArgs<T>& a, int m, int hd, int jj, const RefineGrad4& gr) {
+  const RefineIn in = refine_gather<T, DH>(a, m, hd, jj);
+  refine_apply<T, DH>(a, m, hd, jj, in, gr);
+}
+
+// The refine VJP as its own launch (the first reverse sweep of a cell, whose grads come from
+// the committed-prefix VJP or the grad cache): one thread per item, the grads read from the NS
+// slices.
+template <typename T, int DH, int NS>
+static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
+  constexpr int Q = DH / 8;   // items per (row, head)
+  const int per_row = a.g.d / 8;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= a.N * per_row) return;   // whole (row, head) lane groups: Q divides 256 and per_row
+  const int m = idx / per_row, rem = idx - m * per_row;
+  const int hd = rem / Q, jj = 4 * (rem - hd * Q);
+  const int b = m / a.g.c, p = m - b * a.g.c;
+  const long drow = ((long)b * a.g.h + hd) * a.dk_stride + (long)(a.dk_row0 + p) * DH + jj;
+  RefineGrad4 gr;
+  float t0[4], t1[4], t2[4], t3[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { gr.ka[i] = 0.f; gr.kb[i] = 0.f; gr.va[i] = 0.f; gr.vb[i] = 0.f; }
+#pragma unroll
+  for (int q = 0; q < NS; ++q) {
+    const long o = q * a.psum_stride + drow;
+    ld4<float>(a.dK + o, t0);
+    ld4<float>(a.dK + o + DH / 2, t1);
+    ld4<float>(a.dV + o, t2);
+    ld4<float>(a.dV + o + DH / 2, t3);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { gr.ka[i] += t0[i]; gr.kb[i] += t1[i]; gr.va[i] += t2[i]; gr.vb[i] += t3[i]; }
+  }
+  refine_vjp4<T, DH>(a, m, hd, jj, gr);
 }
 
 // ---------------------------------------------------------------------------
@@ -418,8 +550,12 @@ template <typename T> struct AttnBwdArgs {
                                                        //   committed prefix length [Tbuf] (first sweep)
   int first;                                           // first reverse sweep: G / Dbar are written, else +=
   float scale, inv_d, eps;
-  float* dKout; float* dVout;                          // [B*h, CMAX, DH] grads of the intra rows (sweep >= 1)
   float* dkself; float* dvraw; float* dq;              // layer accumulators [B, h, Tbuf, DH] (+=)
+  // sweep >= 1 (fuse_refine): the grads of the intra rows are those of the previous sweep's
+  // refined rows; the key-major blocks run that sweep's refine VJP on them (ref). Sweep 0:
+  // the intra rows are the raw rows, their grads go to dkself / dvraw.
+  int fuse_refine;
+  RefineBwdArgs<T> ref;
 };
 
 template <typename T, int DH> struct AttnBwdCfg {
@@ -600,7 +736,7 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
   else {
     // sweep 0: the dkself / dvraw rows after phase 1, loaded before the products
     float dko[4][NDT], dvo[4][NDT];
-    if (a.dKout == nullptr) {
+    if (!a.fuse_refine) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int jc = min(16 * wave + 4 * g4 + r, c - 1);
@@ -645,6 +781,52 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
       for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r] * (dPt[t][r] - Dq[t]));
     }
     wave_mma_bt<T, 64, NDT>(W, LDI, Qs, LDE, dK);
+    if (a.fuse_refine) {
+      // the grads stay on chip: staged in LDS over the Q / K / V / dO tiles once every wave is
+      // done with them, then one refine item (row, 4 RoPE pairs) per thread at a time
+      constexpr int LDF = DH + 4;
+      static_assert(2 * 64 * LDF * 4 <= C::LDS_ELEMS * (int)sizeof(T), "grad staging fits the tiles");
+      float* dKs = reinterpret_cast<float*>(smem_raw);
+      float* dVs = dKs + 64 * LDF;
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * wave + 4 * g4 + r;
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) {
+          dKs[j * LDF + 16 * t + lc] = a.scale * dK[t][r];
+          dVs[j * LDF + 16 * t + lc] = dV[t][r];
+        }
+      }
+      __syncthreads();
+      // Items it = tid + 256 k: row it / Q, pairs 4 (it % Q); a row's items are Q consecutive
+      // lanes. Two items per round, both gathered before either is applied (their loads in
+      // flight together).
+      constexpr int Q = DH / 8;
+      auto grads = [&](int j, int jj) {
+        const float* kr = dKs + j * LDF + jj;
+        const float* vr = dVs + j * LDF + jj;
+        RefineGrad4 gr;
+        unpackf4(*reinterpret_cast<const floatx4*>(kr), gr.ka);
+        unpackf4(*reinterpret_cast<const floatx4*>(kr + DH / 2), gr.kb);
+        unpackf4(*reinterpret_cast<const floatx4*>(vr), gr.va);
+        unpackf4(*reinterpret_cast<const floatx4*>(vr + DH / 2), gr.vb);
+        return gr;
+      };
+      const int n_items = c * Q;
+      for (int it = tid; it < n_items; it += 512) {
+        const int it2 = it + 256;
+        const bool two = it2 < n_items;   // uniform over a row's lanes (n_items is a multiple of Q)
+        const int j = it / Q, jj = 4 * (it - j * Q);
+        const int j2 = two ? it2 / Q : j, jj2 = two ? 4 * (it2 - j2 * Q) : jj;
+        const RefineIn in1 = refine_gather<T, DH>(a.ref, b * c + j, hh, jj);
+        RefineIn in2;
+        if (two) in2 = refine_gather<T, DH>(a.ref, b * c + j2, hh, jj2);
+        refine_apply<T, DH>(a.ref, b * c + j, hh, jj, in1, grads(j, jj));
+        if (two) refine_apply<T, DH>(a.ref, b * c + j2, hh, jj2, in2, grads(j2, jj2));
+      }
+      return;
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int j = 16 * wave + 4 * g4 + r;
@@ -652,13 +834,8 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
         const int e = 16 * t + lc;
-        if (a.dKout != nullptr) {
-          a.dKout[((long)bh * CMAX + j) * DH + e] = a.scale * dK[t][r];
-          a.dVout[((long)bh * CMAX + j) * DH + e] = dV[t][r];
-        } else {
-          a.dkself[(lrow0 + j) * DH + e] = dko[r][t] + a.scale * dK[t][r];
-          a.dvraw[(lrow0 + j) * DH + e] = dvo[r][t] + dV[t][r];
-        }
+        a.dkself[(lrow0 + j) * DH + e] = dko[r][t] + a.scale * dK[t][r];
+        a.dvraw[(lrow0 + j) * DH + e] = dvo[r][t] + dV[t][r];
       }
     }
   }

@@ -23,7 +23,6 @@ template <typename T> struct BwdWs {
   // one cell
   CellWs fws;                           // forward scratch of the recompute
   CellSave<T> sv;                       // every sweep's state
-  float *dKa, *dVa, *dKb, *dVb;         // [B*h, CMAX, dh] grads of the intra rows (ping-pong)
   float *lamdv, *gw, *rowdot;           // [N, d], [N, d], [N, d / DU_EPI_TN]
   float *du_part;                       // [DU_SPLIT, N, d] split-K slices of du
   // committed-prefix VJP: per-row state from the attention VJP, key-side partial sums
@@ -71,10 +70,6 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.fws = carve_cell(c, cache_T, cv.base ? cv.base + cv.off : nullptr);
   cv.off += align256(w.fws.bytes);
   w.sv = carve_save<T>(c, N, kmax, false, false, cv);
-  w.dKa = cv.take<float>(BH * CMAX * dh * 4);
-  w.dVa = cv.take<float>(BH * CMAX * dh * 4);
-  w.dKb = cv.take<float>(BH * CMAX * dh * 4);
-  w.dVb = cv.take<float>(BH * CMAX * dh * 4);
   w.lamdv = cv.take<float>(N * d * 4);
   w.gw = cv.take<float>(N * d * 4);
   w.rowdot = cv.take<float>(N * (d / DU_EPI_TN) * 4);
@@ -282,15 +277,22 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
   // this cell's rows of the stacked weight-grad operands
   T* dctx = ws.dctxL + coff * 4 * d;
   T* dvc = ws.dvcL + coff * d;
+  // refine VJP arguments of sweep sw (the grads of its refined rows: given by the caller)
+  auto refine_args = [&](int sw) {
+    return RefineBwdArgs<T>{g, N, c->ctx_mod, dKn, dVn, dn_stride, dn_row0, dn_psum,
+                            sv.save1 + sw * NS * 4 * d, mult ? sv.save2 + sw * NS * d : nullptr, L->glogx, kraw,
+                            vraw, cos, sin, dctx + sw * NS * 4 * d, dvc + sw * NS * d, ws.dglogx, ws.dkraw,
+                            ws.dvraw, kctx_gain(c, w), vctx_gain(c, w), ws.dkg, ws.dvg};
+  };
   for (int sw = K - 1; sw >= 0; --sw) {
-    // refine VJP of sweep sw (the last sweep's rows: the final-row grads above)
-    RefineBwdArgs<T> ra{g, N, c->ctx_mod, dKn, dVn, dn_stride, dn_row0, dn_psum,
-                        sv.save1 + sw * NS * 4 * d, mult ? sv.save2 + sw * NS * d : nullptr, L->glogx, kraw, vraw,
-                        cos, sin, dctx + sw * NS * 4 * d, dvc + sw * NS * d, ws.dglogx, ws.dkraw, ws.dvraw,
-                        kctx_gain(c, w), vctx_gain(c, w), ws.dkg, ws.dvg};
-    const dim3 rgrid(cdiv((long)N * d / 2, 256));
-    if (sw == K - 1 && gc.dK == nullptr) hipLaunchKernelGGL((k_refine_bwd<T, DH, COMM_NSQ>), rgrid, dim3(256), 0, s, ra);
-    else hipLaunchKernelGGL((k_refine_bwd<T, DH, 1>), rgrid, dim3(256), 0, s, ra);
+    // refine VJP of sweep sw: the last sweep's from the final-row grads above, in its own launch;
+    // the others run inside the attention VJP of the sweep after them (below)
+    if (sw == K - 1) {
+      const RefineBwdArgs<T> ra = refine_args(sw);
+      const dim3 rgrid(cdiv((long)N * d / 8, 256));
+      if (gc.dK == nullptr) hipLaunchKernelGGL((k_refine_bwd<T, DH, COMM_NSQ>), rgrid, dim3(256), 0, s, ra);
+      else hipLaunchKernelGGL((k_refine_bwd<T, DH, 1>), rgrid, dim3(256), 0, s, ra);
+    }
     // dv_in = dv_ctx . W_vctx (mult family)
     if (mult) {
       EpiVinBwd<T> ev{g, N, c->ctx_mod, c->mult_res_lambda, sv.save1 + sw * NS * 4 * d, L->sig,
@@ -316,17 +318,14 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
       const T* Kin; const T* Vin; long in_stride; int in_row0;
       if (sw == 0) { Kin = kself; Vin = vraw; in_stride = (long)T_ * DH; in_row0 = pos0; }
       else { Kin = sv.Kin + sw * slot; Vin = sv.Vin + sw * slot; in_stride = (long)CMAX * DH; in_row0 = 0; }
-      float* dKo = sw == 0 ? nullptr : ((K - 1 - sw) % 2 == 0 ? ws.dKa : ws.dKb);
-      float* dVo = sw == 0 ? nullptr : ((K - 1 - sw) % 2 == 0 ? ws.dVa : ws.dVb);
       AttnBwdArgs<T> aa{g, qr, kself, vraw, Kin, Vin, in_stride, in_row0, sv.o + sw * NS * d,
                         sv.ssq + sw * NS * h, ws.gw, ws.rowdot, d / DU_EPI_TN,
                         sw == K - 1 ? ws.docat : nullptr, sv.stat_m + sw * (size_t)BH * CMAX,
                         sv.stat_z + sw * (size_t)BH * CMAX, Mx, ws.Grow, ws.Drow, ws.Mrow, ws.klim,
                         sw == K - 1 ? 1 : 0,
-                        scale, inv_d, c->rms_eps, dKo, dVo, ws.dkself, ws.dvraw, ws.dq};
+                        scale, inv_d, c->rms_eps, ws.dkself, ws.dvraw, ws.dq, sw >= 1 ? 1 : 0,
+                        sw >= 1 ? refine_args(sw - 1) : RefineBwdArgs<T>{}};
       hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(2, BH), dim3(256), lds_attn, s, aa);
-      dKn = dKo; dVn = dVo;
-      dn_stride = (long)CMAX * DH; dn_row0 = 0; dn_psum = (long)BH * CMAX * DH;
     }
   }
   // the other operand of dW_sweep = dctx^T u: this cell's K*N rows of u = RMSNorm(o)

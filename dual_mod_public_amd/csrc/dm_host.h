@@ -13,9 +13,10 @@
 
 namespace dm {
 
-// Launch shapes of the per-sweep GEMMs (M = B*c rows). Their k-loops are bound by
-// load latency, so the number of k-tiles in flight per block sets their speed.
-// The defaults are the measured best on MI355X; -D overrides exist for tuning builds.
+// Launch shapes of the per-sweep GEMMs (M = B*c rows). Their k-loops are bound by LDS
+// traffic; two 64 x 64 blocks per CU let one block's epilogue overlap the other's k-loop
+// (64 x 128 blocks, one per CU, measured slower). The defaults are the measured best on
+// MI355X; -D overrides exist for tuning builds.
 #ifndef DM_SW1_STAGES
 #define DM_SW1_STAGES 3   // sweep GEMM 1: direct-to-LDS stages of the 64 x 64 blocks
 #endif

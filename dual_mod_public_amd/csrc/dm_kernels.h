@@ -656,19 +656,27 @@ template <typename T, int DH, int NG = 1> struct EpiSweep1 {
 
   // Block tile 64 x 64 NG: NG packed column groups of 64. Thread t owns row t / 4 and the
   // column quad lc0 = 4 (t % 4) .. + 3 of each group's four 16-column sections, so its global
-  // inputs and outputs are runs of 4 consecutive elements. With one group the inputs are
-  // gathered during the k-loop's last stage; with several, at the start of the epilogue.
-  struct TilePre {
+  // inputs and outputs are runs of 4 consecutive elements. With up to two groups the inputs
+  // are gathered during the k-loop's last stage; with more, at the start of the epilogue.
+  struct GroupPre {
     floatx4 f[4];                   // K: gx_a, gx_b, cos, sin; linear V: gx x2; v_map: sig x4
     typename Raw4<T>::type h[8];    // K: kraw_a, kraw_b; linear V: v_raw x2; v_map: o x4, norm weight x4
   };
-  // tile_prefetch issues exactly these 12 loads (one per f / h slot, unconditionally)
-  static constexpr int LATE_GATHERS = NG == 1 ? 12 : 0;
+  static constexpr bool LATE = NG <= 2;
+  struct TilePre {
+    GroupPre p[LATE ? NG : 1];
+  };
+  // tile_prefetch issues exactly 12 loads per group (one per f / h slot, unconditionally)
+  static constexpr int LATE_GATHERS = LATE ? 12 * NG : 0;
   DM_DEV TilePre tile_prefetch(int m0, int n0) const {
-    if constexpr (NG == 1) return group_prefetch(m0, n0);
-    else return TilePre{};
+    TilePre pr{};
+    if constexpr (LATE) {
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) pr.p[gi] = group_prefetch(m0, n0 + 64 * gi);
+    }
+    return pr;
   }
-  DM_DEV TilePre group_prefetch(int m0, int n0) const {
+  DM_DEV GroupPre group_prefetch(int m0, int n0) const {
     const int r = threadIdx.x >> 2, lc0 = 4 * (threadIdx.x & 3);
     const int d = g.d, h = g.h;
     const int m = min(m0 + r, M - 1);
@@ -716,7 +724,7 @@ template <typename T, int DH, int NG = 1> struct EpiSweep1 {
         }
       }
     }
-    TilePre pr;
+    GroupPre pr;
 #pragma unroll
     for (int k = 0; k < 4; ++k) pr.f[k] = ld_global<floatx4>(fp[k]);
 #pragma unroll
@@ -729,11 +737,14 @@ template <typename T, int DH, int NG = 1> struct EpiSweep1 {
     static_assert(BM == 64 && BN == 64 * NG, "sweep GEMM 1 block tile is NG 64 x 64 column groups");
     const float sc = rs[threadIdx.x >> 2];
     if constexpr (NG == 1) {
-      group_apply<LDT>(tile, m0, n0, sc, pr, false, 0.f, 0.f);
+      group_apply<LDT>(tile, m0, n0, sc, pr.p[0], false, 0.f, 0.f);
     } else {
-      TilePre pg[NG];
+      GroupPre pg[NG];
 #pragma unroll
-      for (int gi = 0; gi < NG; ++gi) pg[gi] = group_prefetch(m0, n0 + 64 * gi);
+      for (int gi = 0; gi < NG; ++gi) {
+        if constexpr (LATE) pg[gi] = pr.p[gi];
+        else pg[gi] = group_prefetch(m0, n0 + 64 * gi);
+      }
       // The block's NG groups are one head's k_ctx / g_k(u) (or linear v_ctx / g_v(u)) columns:
       // the head's norm scale r * gain from sections 0 and 1 of every group (the k_ctx, v_ctx
       // columns), over the row's 4 threads.
@@ -769,7 +780,7 @@ template <typename T, int DH, int NG = 1> struct EpiSweep1 {
   // One 64-column group of the tile (tile points at the group's first column). nrm: the group's
   // k_ctx / v_ctx columns are normed, x -> (x nr) ng, from and to stored values.
   template <int LDT>
-  DM_DEV void group_apply(const float* tile, int m0, int n0, float sc, const TilePre& pr, bool nrm, float nr,
+  DM_DEV void group_apply(const float* tile, int m0, int n0, float sc, const GroupPre& pr, bool nrm, float nr,
                           float ng) const {
     const int r = threadIdx.x >> 2, lc0 = 4 * (threadIdx.x & 3);
     const int d = g.d, h = g.h;
