@@ -366,27 +366,45 @@ DM_DEV void gemm_mainloop_dma(const SA& sa, const SB& sb, int K, int m0, int n0,
                                        (lds_void_t*)(base + (BM + r) * 128), 16, 0, 0);
     }
   };
+  // Both k-halves' fragments are read first, then the MFMAs run: the reads of the second half
+  // overlap the first half's MFMAs, and each MFMA waits only for its own operands (LDS reads
+  // complete in order). Left to itself the scheduler sinks every A fragment read to just before
+  // its MFMAs, reusing one register quad, which exposes the LDS latency FM times per half.
   auto compute = [&](const char* As) {
     const char* Bs = As + BM * 128;
+    typename MF::frag af[2][FM], bfr[2][FN];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      typename MF::frag af[FM], bfr[FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const int r = wm * TM + i * 16 + (lane & 15);
-        af[i] = *reinterpret_cast<const typename MF::frag*>(As + r * 128 +
-                                                             (((kk * 4 + (lane >> 4)) ^ (r & 7)) << 4));
+        af[kk][i] = *reinterpret_cast<const typename MF::frag*>(As + r * 128 +
+                                                                 (((kk * 4 + (lane >> 4)) ^ (r & 7)) << 4));
       }
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int r = wn * TN + j * 16 + (lane & 15);
-        bfr[j] = *reinterpret_cast<const typename MF::frag*>(Bs + r * 128 +
-                                                              (((kk * 4 + (lane >> 4)) ^ (r & 7)) << 4));
+        bfr[kk][j] = *reinterpret_cast<const typename MF::frag*>(Bs + r * 128 +
+                                                                  (((kk * 4 + (lane >> 4)) ^ (r & 7)) << 4));
       }
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = MF::mma(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < FN; ++j) acc[i][j] = MF::mma(af[kk][i], bfr[kk][j], acc[i][j]);
+    if constexpr (FM * FN >= 16) {
+      // the first half's reads; the second half's one per MFMA of the first half; the rest
+      // (at most 15 LDS reads are outstanding when an MFMA has to wait for its operands: the
+      // wait counter's range)
+      __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);
+#pragma unroll
+      for (int q = 0; q < FM + FN; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * FM * FN - (FM + FN), 0);
     }
   };
 
@@ -492,6 +510,8 @@ DM_DEV void gemm_mainloop_dma_kk(const SA& sa, const SB& sb, int K, int m0, int 
                                        (lds_void_t*)(base + KS * ROWA + r0 * ROWB), 16, 0, 0);
     }
   };
+  // Per 32-k step the step's fragment reads go first, then its MFMAs (the reads of one fragment
+  // otherwise sink to just before its MFMAs, each exposing the LDS latency).
   auto compute = [&](const char* As) {
     const char* Bs = As + KS * ROWA;
 #pragma unroll
@@ -505,6 +525,10 @@ DM_DEV void gemm_mainloop_dma_kk(const SA& sa, const SB& sb, int K, int m0, int 
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = MF::mma(af[i], bfr[j], acc[i][j]);
+      if constexpr (FM * FN >= 16) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * (FM + FN), 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);
+      }
     }
   };
 
