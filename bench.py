@@ -73,7 +73,7 @@ def traffic_from_profile(kernel):
         text = open(TRAFFIC_PROFILE).read()
     except OSError:
         return None
-    m = re.search(r"^\|\s*" + re.escape(kernel) + r"\s*\|(?:[^|\n]*\|){5}\s*([0-9.]+)\s*\|", text, re.M)
+    m = re.search(r"^\|\s*" + re.escape(kernel) + r"\s*\|.*\|\s*([0-9.]+)\s*\|\s*$", text, re.M)
     return float(m.group(1)) * 1e6 if m else None
 
 
