@@ -141,11 +141,17 @@ PROF = {"proj": 1, "comm": 2, "attend": 3, "sweep1": 4, "sweep2": 5, "wo": 6, "d
         "dec_merge": 8, "dec_refine": 9, "bwd": 10, "layer": 11}
 
 
-class KernelTimer:
-    """Times every launch of one kernel class with HIP events (dm_prof_*)."""
+DM_PROF_EVENTS_ONLY = 0x100
 
-    def __init__(self, kernel_class, max_launches=8192):
+
+class KernelTimer:
+    """Times every launch of one kernel class with HIP events stamped by the launches
+    (dm_prof_*); device_clock=False leaves the kernels' own device-clock stamps out."""
+
+    def __init__(self, kernel_class, max_launches=8192, device_clock=True):
         self.cls = PROF[kernel_class] if isinstance(kernel_class, str) else int(kernel_class)
+        if not device_clock:
+            self.cls |= DM_PROF_EVENTS_ONLY
         self.cap = max_launches
         self.total_ms, self.n, self.device_total_ms = 0.0, 0, None
 
@@ -162,7 +168,7 @@ class KernelTimer:
 
     @property
     def avg_ms(self):
-        """Mean per-launch time from the HIP event pairs (includes queue overheads)."""
+        """Mean per-launch time from the HIP event pairs (each dispatch's begin to end)."""
         return self.total_ms / max(self.n, 1)
 
     @property

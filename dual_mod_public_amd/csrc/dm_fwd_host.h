@@ -183,10 +183,9 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
     SrcRows<T> bv{(const T*)w->w_vctx, c->d, c->d};
     EpiSweep2Head<T, DH> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2, vgain};
     uint64_t* ts;
-    const int idx = prof_launch_begin(PROF_SWEEP2, s, true, ts);
-    hipLaunchKernelGGL((k_sweep2_attend<T, DH>), dim3(c->h, N / CMAX), dim3(256), 0, s, av, bv, c->d, e2,
-                       *next_attend, ts);
-    prof_launch_end(idx, s);
+    const int idx = prof_launch_begin(PROF_SWEEP2, true, ts);
+    launch_timed(idx, k_sweep2_attend<T, DH>, dim3(c->h, N / CMAX), dim3(256), 0, s, av, bv, c->d, e2,
+                 *next_attend, ts);
     return;
   }
   if (!linear && vgain != nullptr) {

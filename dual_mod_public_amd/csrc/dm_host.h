@@ -141,9 +141,8 @@ void launch_gemm(const SA& sa, const SB& sb, int M, int N, int K, const EPI& epi
                  int prof_cls = PROF_NONE) {
   dim3 grid(N / BN, cdiv(M, BM));
   uint64_t* ts;
-  const int idx = prof_launch_begin(prof_cls, s, true, ts);
-  hipLaunchKernelGGL((k_gemm<T, BM, BN, WM, WN, D, SA, SB, EPI>), grid, dim3(256), 0, s, sa, sb, K, epi, ts);
-  prof_launch_end(idx, s);
+  const int idx = prof_launch_begin(prof_cls, true, ts);
+  launch_timed(idx, k_gemm<T, BM, BN, WM, WN, D, SA, SB, EPI>, grid, dim3(256), 0, s, sa, sb, K, epi, ts);
 }
 
 // bf16 with K-contiguous operands and K a multiple of 64: the direct-to-LDS k-loop
@@ -202,9 +201,8 @@ void launch_gemm_splitk(const SA& sa, const SB& sb, int M, int N, int K, int S, 
                         int prof_cls = PROF_NONE) {
   dim3 grid(N / BN, cdiv(M, BM), S);
   uint64_t* ts;
-  const int idx = prof_launch_begin(prof_cls, s, true, ts);
-  hipLaunchKernelGGL((k_gemm<T, BM, BN, WM, WN, D, SA, SB, EPI>), grid, dim3(256), 0, s, sa, sb, K / S, epi, ts);
-  prof_launch_end(idx, s);
+  const int idx = prof_launch_begin(prof_cls, true, ts);
+  launch_timed(idx, k_gemm<T, BM, BN, WM, WN, D, SA, SB, EPI>, grid, dim3(256), 0, s, sa, sb, K / S, epi, ts);
 }
 
 }  // namespace dm

@@ -355,9 +355,8 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
                    (const T*)ws.q, (const T*)ws.kself, (const T*)ws.vraw, (const T*)a->K_tape,
                    (const T*)a->V_tape, ws.part, ws.o, ws.ssq, (T*)a->o_cat, nullptr};
   if (nsplit > 0) {
-    const int idx = prof_launch_begin(PROF_DEC_READ, s, true, da.prof_ts);
-    hipLaunchKernelGGL((k_decode_partial<T, DH, DEC_SPLIT>), dim3(nsplit, B * h), dim3(256), 0, s, da);
-    prof_launch_end(idx, s);
+    const int idx = prof_launch_begin(PROF_DEC_READ, true, da.prof_ts);
+    launch_timed(idx, k_decode_partial<T, DH, DEC_SPLIT>, dim3(nsplit, B * h), dim3(256), 0, s, da);
     da.prof_ts = nullptr;
   }
   launch_k(PROF_DEC_MERGE, k_decode_merge<T, DH>, dim3(B * h), dim3(64), 0, s, da);
@@ -669,6 +668,8 @@ extern "C" {
 int dm_prof_start(int32_t kernel_class, int32_t max_launches) {
   ProfState& p = prof();
   DM_REQUIRE(p.armed == PROF_NONE, DM_ERR_INVALID, "timing already armed for class %d", p.armed);
+  p.dev_clock = !(kernel_class & DM_PROF_EVENTS_ONLY);
+  kernel_class &= ~DM_PROF_EVENTS_ONLY;
   DM_REQUIRE(kernel_class > PROF_NONE && kernel_class < PROF_NCLASS, DM_ERR_INVALID, "kernel class %d",
              kernel_class);
   DM_REQUIRE(max_launches > 0 && max_launches <= (1 << 16), DM_ERR_INVALID, "max_launches %d", max_launches);

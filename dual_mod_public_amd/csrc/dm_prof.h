@@ -1,17 +1,18 @@
 // Optional per-kernel-class timing (host side).
 //
 // When a class is armed (dm_prof_start), every launch of that class is timed:
-//  * the GEMM kernels and the decode tape read take their own span from the
-//    device clock (first block start to last block end, folded into
-//    PROF_SLOTS slots per launch; see prof_begin / prof_end), the interval a
-//    kernel-trace profiler reports;
-//  * every class also records a HIP start/stop event pair on the launch's own
-//    stream (kernel + queue overheads: an upper bound).
+//  * a HIP start/stop event pair that the launch itself stamps (hipExtLaunchKernel: the
+//    kernel dispatch's own begin and end, the interval a kernel-trace profiler reports);
+//    launch groups (ProfScope) record ordinary events around the group instead;
+//  * the GEMM kernels and the decode tape read also take their span from the device
+//    clock (first block start to last block end, folded into PROF_SLOTS slots per
+//    launch; see prof_begin / prof_end): the execution without dispatch and drain.
 // dm_prof_stop waits for the last event and returns the summed times and the
 // launch count. Unarmed, a launch costs one integer compare. Used by bench.py to
 // time the dominant kernel inside its timed region; never armed on the product path.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <vector>
@@ -42,6 +43,7 @@ struct ProfState {
   uint64_t* dts = nullptr;      // [cap][2 * PROF_SLOTS] device-clock slots
   int dts_cap = 0;
   std::vector<char> dev_timed;  // per launch: took device-clock slots
+  bool dev_clock = true;        // false: events only (the kernels write no device-clock slots)
 };
 
 inline ProfState& prof() {
@@ -65,31 +67,35 @@ struct ProfScope {
   }
 };
 
-// Timing of one launch of class `cls`: when armed, records the start event now
-// and returns the launch index (else -1). `ts` receives the launch's device-clock
-// slots when the kernel supports them (dev_ts) — nullptr otherwise.
-inline int prof_launch_begin(int cls, hipStream_t s, bool dev_ts, uint64_t*& ts) {
+// Timing of one launch of class `cls`: when armed, reserves the launch's event pair and
+// returns its index (else -1). `ts` receives the launch's device-clock slots when the
+// kernel supports them (dev_ts) — nullptr otherwise.
+inline int prof_launch_begin(int cls, bool dev_ts, uint64_t*& ts) {
   ProfState& p = prof();
   ts = nullptr;
   if (p.armed != cls || cls == PROF_NONE || p.n >= p.cap) return -1;
-  (void)hipEventRecord(p.ev[2 * p.n], s);
-  if (dev_ts && p.dts != nullptr) {
+  if (dev_ts && p.dev_clock && p.dts != nullptr) {
     ts = p.dts + (size_t)p.n * 2 * PROF_SLOTS;
     p.dev_timed[p.n] = 1;
   }
   return p.n++;
 }
-inline void prof_launch_end(int idx, hipStream_t s) {
-  if (idx >= 0) (void)hipEventRecord(prof().ev[2 * idx + 1], s);
+
+// The launch: with a reserved event pair (idx >= 0) the dispatch stamps both events.
+template <typename F, typename... Args>
+inline void launch_timed(int idx, F kernel, dim3 grid, dim3 block, uint32_t shmem, hipStream_t s, Args... args) {
+  if (idx >= 0)
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, prof().ev[2 * idx], prof().ev[2 * idx + 1], 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
 }
 
-// hipLaunchKernelGGL with event timing for class `cls`.
+// a launch of class `cls` with event timing
 template <typename F, typename... Args>
 inline void launch_k(int cls, F kernel, dim3 grid, dim3 block, uint32_t shmem, hipStream_t s, Args... args) {
   uint64_t* ts;
-  const int idx = prof_launch_begin(cls, s, false, ts);
-  hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
-  prof_launch_end(idx, s);
+  const int idx = prof_launch_begin(cls, false, ts);
+  launch_timed(idx, kernel, grid, block, shmem, s, args...);
 }
 
 }  // namespace dm

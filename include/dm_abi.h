@@ -354,10 +354,12 @@ int dm_check_schedule(const int32_t* sched, int32_t n_cells, int32_t T);
 /* ---- optional kernel timing (benchmarks) -------------------------------------
  * No reference counterpart (the reference times with ad-hoc torch events,
  * engines/wave3d/wave3d_x.py:28-33). Arms one kernel class; every later launch of
- * that class (up to max_launches) is bracketed by HIP events on its own stream, and
+ * that class (up to max_launches) stamps a HIP start/stop event pair from its own
+ * dispatch (hipExtLaunchKernel: the interval a kernel-trace profiler reports), and
  * the GEMM classes (1, 4, 5, 6) and the decode tape read (7) also time themselves
- * from the device clock (first block start to last block end of each dispatch, the
- * span a kernel-trace profiler reports; the event pair adds queue overheads).
+ * from the device clock (first block start to last block end of each dispatch: the
+ * execution without dispatch and drain) unless kernel_class carries
+ * DM_PROF_EVENTS_ONLY (then the kernels write no timestamps and run unmodified).
  * dm_prof_stop2 waits, then returns the summed event time, the summed device-clock
  * time (-1 when some launch of the class has no device timing) and the launch
  * count; dm_prof_stop returns the event time only. dm_prof_start allocates its
@@ -365,6 +367,7 @@ int dm_check_schedule(const int32_t* sched, int32_t n_cells, int32_t T);
  * Classes: 1 projection, 2 committed accumulator, 3 sweep attention, 4 sweep GEMM 1,
  * 5 sweep GEMM 2, 6 W_O, 7 decode tape read, 8 decode merge, 9 decode refine,
  * 10 backward, 11 whole entry-point call. */
+#define DM_PROF_EVENTS_ONLY 0x100
 int dm_prof_start(int32_t kernel_class, int32_t max_launches);
 int dm_prof_stop(float* total_ms, int32_t* n_launches);
 int dm_prof_stop2(float* event_ms, float* device_ms, int32_t* n_launches);
