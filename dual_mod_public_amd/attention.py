@@ -27,6 +27,18 @@ class RMSNorm(nn.Module):
         self.eps = eps
 
 
+def _forward_only(name, module, *tensors):
+    """attend_one / refine_kv run the HIP kernels without an autograd graph: a call that would
+    need gradients (grad mode on, and an input or a parameter that requires them) raises instead
+    of returning a result that silently has none."""
+    if not torch.is_grad_enabled():
+        return
+    params = module.parameters() if module is not None else ()
+    if any(t is not None and t.requires_grad for t in tensors) or any(p.requires_grad for p in params):
+        raise NotImplementedError(f"{name} is forward-only on the HIP path (no autograd); "
+                                  "differentiate through forward() or call it under torch.no_grad()")
+
+
 class DualModAttention(nn.Module):
     CHUNK = 64   # chunk length of the exact forward (cells of K = c sweeps)
 
@@ -123,6 +135,7 @@ class DualModAttention(nn.Module):
         local_window keeps the last W-1 rows. Returns (o [B,h,1,dh], None)."""
         if need_probs or collect is not None:
             raise NotImplementedError("attention probabilities / telemetry are not materialised on the HIP path")
+        _forward_only("attend_one", None, q_r, k_self_r, v_self, K_past, V_past)   # no parameters involved
         from .engine import _row_stride
         B, h, _, dh = q_r.shape
         dt = q_r.dtype
@@ -149,6 +162,7 @@ class DualModAttention(nn.Module):
         rotates at write)."""
         if collect is not None:
             raise NotImplementedError("telemetry collection is not supported on the HIP path")
+        _forward_only("refine_kv", self, xhat, o_cat, k_raw, v_raw)
         import ctypes
         B, t, d = xhat.shape
         h, dh = self.n_heads, self.head_dim

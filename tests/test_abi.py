@@ -141,3 +141,18 @@ def test_training_entry_points_reject_local_window():
     rc = lib.dm_layer_bwd(ctypes.byref(c), ctypes.byref(w), fake, fake, fake, fake, fake, ctypes.byref(b), sched, 1,
                           fake, fake, 64, fake, None, 0, ctypes.byref(g), fake, 1 << 30, None)
     assert rc == -2 and b"local_window" in lib.dm_last_error()
+
+
+def test_attend_one_refine_kv_refuse_autograd():
+    """The HIP attend_one / refine_kv build no autograd graph: a call that would need gradients
+    raises (before any library call) instead of returning a result without them."""
+    import torch
+    from dual_mod_public_amd.attention import DualModAttention
+    cfg = DualModConfig(d_model=256, n_heads=4, ctx_mod="mult_res")
+    attn = DualModAttention(cfg)
+    q = torch.zeros(1, 4, 1, 64, requires_grad=True)
+    with pytest.raises(NotImplementedError, match="forward-only"):
+        attn.attend_one(q, q, q, None, None)
+    x = torch.zeros(1, 2, 256)
+    with pytest.raises(NotImplementedError, match="forward-only"):   # the module's parameters need grads
+        attn.refine_kv(x, x, x, x)

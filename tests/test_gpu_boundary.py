@@ -44,8 +44,9 @@ def test_attend_one(P, W):
     q, ks, vs = (torch.randn(B, h, 1, dh, generator=g, dtype=torch.float64) for _ in range(3))
     cache = torch.randn(2, B, h, T, dh, generator=g, dtype=torch.float64)
     Kd, Vd = cache[0].float().to(DEV), cache[1].float().to(DEV)
-    o, probs = attn.attend_one(q.float().to(DEV), ks.float().to(DEV), vs.float().to(DEV),
-                               Kd[:, :, :P] if P else None, Vd[:, :, :P] if P else None)
+    with torch.no_grad():
+        o, probs = attn.attend_one(q.float().to(DEV), ks.float().to(DEV), vs.float().to(DEV),
+                                   Kd[:, :, :P] if P else None, Vd[:, :, :P] if P else None)
     torch.cuda.synchronize()
     assert probs is None
     ref = O.attend_one(cfg, q, ks, vs, cache[0][:, :, :P] if P else None, cache[1][:, :, :P] if P else None)
@@ -66,7 +67,8 @@ def test_refine_kv(ctx_mod, kw, t):
     attn = _module(cfg, sd)
     g = torch.Generator().manual_seed(t)
     o_cat, k_raw, v_raw = (torch.randn(2, t, cfg.d_model, generator=g, dtype=torch.float64) for _ in range(3))
-    k, v = attn.refine_kv(*(z.float().to(DEV) for z in (x, o_cat, k_raw, v_raw)))
+    with torch.no_grad():
+        k, v = attn.refine_kv(*(z.float().to(DEV) for z in (x, o_cat, k_raw, v_raw)))
     torch.cuda.synchronize()
     k_ref, v_ref = O.refine_kv(cfg, sd, x, o_cat, k_raw, v_raw)
     errs = {"k": relerr(k, k_ref), "v": relerr(v, v_ref)}
