@@ -86,7 +86,7 @@ class dm_cell_bwd_args(ctypes.Structure):
 class dm_decode_args(ctypes.Structure):
     _fields_ = [("pos", c_i32), ("tape_T", c_i32), ("xhat", c_vp), ("K_tape", c_vp),
                 ("V_tape", c_vp), ("o_cat", c_vp), ("y", c_vp), ("workspace", c_vp),
-                ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace_bytes", ctypes.c_size_t), ("pos_dev", c_vp)]
 
 
 P = ctypes.POINTER
@@ -128,6 +128,8 @@ SIGNATURES = {
     "dm_refine_kv": (ctypes.c_int, [P(dm_config), P(dm_packed), P(dm_layer_bufs), c_vp, c_fp, c_fp, c_vp, c_vp,
                                     c_vp, ctypes.c_size_t, c_vp]),
     "dm_linear": (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp]),
+    "dm_argmax_rows": (ctypes.c_int, [c_i32, c_vp, c_i32, c_i32, ctypes.c_int64, c_vp, c_vp]),
+    "dm_residual_rmsnorm": (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, ctypes.c_float, c_vp]),
     "dm_gemm": (ctypes.c_int, [c_i32, c_i32, c_i32, c_vp, c_vp, c_fp, c_i32, c_i32, c_i32, c_i32,
                                c_vp]),
     "dm_check_schedule": (ctypes.c_int, [P(c_i32), c_i32, c_i32]),
@@ -243,6 +245,26 @@ def linear(x, W, residual=None, out=None):
     check(lib().dm_linear(dtype_code(x.dtype), ptr(x2), ptr(W), ptr(r), ptr(y), x2.shape[0], N, K,
                           stream_ptr()))
     return y
+
+
+def residual_rmsnorm(x, delta=None, w=None, dtype=torch.bfloat16, y=None, eps=1e-5):
+    """dm_residual_rmsnorm on contiguous device tensors: x (fp32 [.., d], updated in place)
+    += delta (``dtype``); returns y = rmsnorm(x) * w in ``dtype`` (a new tensor unless y is
+    given), or None when w is None."""
+    d = x.shape[-1]
+    M = x.numel() // d
+    assert x.dtype == torch.float32 and x.is_contiguous()
+    if delta is not None:
+        assert delta.dtype == dtype and delta.is_contiguous() and delta.numel() == x.numel()
+    if w is not None:
+        assert w.dtype == torch.float32 and w.is_contiguous() and w.numel() == d
+        if y is None:
+            y = torch.empty(x.shape, device=x.device, dtype=dtype)
+        assert y.dtype == dtype and y.is_contiguous() and y.numel() == x.numel()
+    check(lib().dm_residual_rmsnorm(dtype_code(dtype), ptr(x), ptr(delta) if delta is not None else None,
+                                    ptr(w) if w is not None else None, ptr(y) if w is not None else None, M, d,
+                                    float(eps), stream_ptr()))
+    return y if w is not None else None
 
 
 def make_config(cfg, B, dtype):

@@ -19,12 +19,18 @@ from .lowrank import LoRAGate, LoRALinear
 
 
 class RMSNorm(nn.Module):
-    """attention.py:74-83 (parameter container; the kernels apply it)."""
+    """attention.py:74-83. Inside the attention path the kernels apply it (norm_ctx); the
+    trunk's attn_norm / mlp_norm / norm_f call ``forward``: fp32 statistics, result in the
+    input's dtype."""
 
     def __init__(self, d, eps=1e-5):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(d))
         self.eps = eps
+
+    def forward(self, x):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps) * self.weight.float()).to(x.dtype)
 
 
 def _forward_only(name, module, *tensors):

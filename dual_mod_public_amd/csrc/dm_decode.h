@@ -8,6 +8,9 @@ namespace dm {
 // ---------------------------------------------------------------------------
 // decode: split-P read of the tape (attention.py:283-312 over a static tape)
 // grid (nsplit, B*h); keys [lo + s*L, min(lo + (s+1)*L, pos))
+// With pos_dev set, the position is read from device memory at run time (one launch
+// shape serves every position, as a captured graph needs): the grid covers the whole
+// tape, blocks past the position return, and (pos, lo, nsplit) follow from *pos_dev.
 // ---------------------------------------------------------------------------
 template <typename T> struct DecodeArgs {
   int B, h, d, tape_T, pos, lo, split_len, nsplit;
@@ -21,7 +24,24 @@ template <typename T> struct DecodeArgs {
   float* ssq;        // [B, h]
   T* o_cat;          // [B, d] storage dtype
   uint64_t* prof_ts; // per-dispatch timing slots (nullptr: untimed)
+  const int* pos_dev = nullptr;   // device position (nullptr: pos / lo / nsplit above)
+  int window = 0;                 // local_window (W tokens incl. self, 0 = full) for pos_dev
 };
+
+// a device position clamped into the tape (a caller's position past the tape reads and
+// writes inside it instead of out of bounds)
+DM_DEV int clamp_pos(int p, int tape_T) { return p < 0 ? 0 : (p >= tape_T ? tape_T - 1 : p); }
+DM_DEV int window_lo(int pos, int W) { return (W > 0 && pos > W - 1) ? pos - (W - 1) : 0; }
+template <typename T>
+DM_DEV void dec_geometry(const DecodeArgs<T>& a, int& pos, int& lo, int& nsplit) {
+  if (a.pos_dev == nullptr) {
+    pos = a.pos; lo = a.lo; nsplit = a.nsplit;
+    return;
+  }
+  pos = clamp_pos(*a.pos_dev, a.tape_T);
+  lo = window_lo(pos, a.window);
+  nsplit = pos > lo ? (pos - lo + a.split_len - 1) / a.split_len : 0;
+}
 
 template <typename T, int DH, int L>
 __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs<T> a) {
@@ -33,10 +53,13 @@ __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs<T> a) {
   const uint64_t t0 = prof_begin(a.prof_ts);
   __shared__ float red[4][DH + 2];
   const int s = blockIdx.x, bh = blockIdx.y;
+  int pos, lo, nsplit;
+  dec_geometry(a, pos, lo, nsplit);
+  if (s >= nsplit) return;   // whole block: past the position (device-position grids only)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kslot = tid / LPK, part = tid - kslot * LPK;
-  const int k_begin = a.lo + s * a.split_len;
-  const int k_end = min(k_begin + a.split_len, a.pos);
+  const int k_begin = lo + s * a.split_len;
+  const int k_end = min(k_begin + a.split_len, pos);
 
   float qv[VEC];
   unpack16<T>(*reinterpret_cast<const uint4*>(a.q + (long)bh * DH + part * VEC), qv);
@@ -116,19 +139,21 @@ __global__ __launch_bounds__(64) void k_decode_merge(DecodeArgs<T> a) {
   constexpr int PER = DH / 64;
   const int bh = blockIdx.x, lane = threadIdx.x;
   const int b = bh / a.h, hh = bh - b * a.h;
+  int pos, lo, nsplit;
+  dec_geometry(a, pos, lo, nsplit);
   float qk = 0.f;
 #pragma unroll
   for (int e = 0; e < PER; ++e)
     qk += to_f(a.q[(long)bh * DH + lane * PER + e]) * to_f(a.kself[(long)bh * DH + lane * PER + e]);
   const float ss = wave_sum(qk) * a.scale;
   float M = ss;
-  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part[((long)s * (a.B * a.h) + bh) * (DH + 2) + DH + 1]);
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.part[((long)s * (a.B * a.h) + bh) * (DH + 2) + DH + 1]);
   const float es = __expf(ss - M);
   float z = es;
   float acc[PER];
 #pragma unroll
   for (int e = 0; e < PER; ++e) acc[e] = es * to_f(a.vself[(long)bh * DH + lane * PER + e]);
-  for (int s = 0; s < a.nsplit; ++s) {
+  for (int s = 0; s < nsplit; ++s) {
     const float* pp = a.part + ((long)s * (a.B * a.h) + bh) * (DH + 2);
     const float w = (pp[DH + 1] == NEG_INF) ? 0.f : __expf(pp[DH + 1] - M);
     z += w * pp[DH];
@@ -146,6 +171,82 @@ __global__ __launch_bounds__(64) void k_decode_merge(DecodeArgs<T> a) {
   }
   sq = wave_sum(sq);
   if (lane == 0) a.ssq[(long)b * a.h + hh] = sq;
+}
+
+// device position: the RoPE rows of position *pos_dev -> rope[0, half) cos, rope[half, 2 half) sin
+__global__ __launch_bounds__(64) void k_decode_pos_rope(const int* pos_dev, int tape_T, const float* cos,
+                                                        const float* sin, int half, float* rope) {
+  const int pos = clamp_pos(*pos_dev, tape_T);
+  for (int i = threadIdx.x; i < half; i += 64) {
+    rope[i] = cos[(long)pos * half + i];
+    rope[half + i] = sin[(long)pos * half + i];
+  }
+}
+
+// device position: the refined rows [B*h, DH] staged by the refine -> tape slot *pos_dev
+template <typename T, int DH>
+__global__ __launch_bounds__(DH) void k_decode_commit(const int* pos_dev, int tape_T, const T* Kst, const T* Vst,
+                                                      T* Kt, T* Vt) {
+  const int pos = clamp_pos(*pos_dev, tape_T);
+  const long bh = blockIdx.x;
+  const long dst = (bh * tape_T + pos) * DH + threadIdx.x;
+  Kt[dst] = Kst[bh * DH + threadIdx.x];
+  Vt[dst] = Vst[bh * DH + threadIdx.x];
+}
+
+// the trunk's fp32 residual stream around a decode step (models/dualmod/model.py:127-130,
+// attention.py:74-83): x[r] += delta[r] (when delta), then y[r] = x[r] * rsqrt(mean(x[r]^2) + eps)
+// * w (when w), in the storage dtype. One block per row; each thread re-reads only the
+// elements it wrote itself.
+template <typename T>
+__global__ __launch_bounds__(256) void k_residual_rmsnorm(float* x, const T* delta, const float* w, T* y, int d,
+                                                         float eps) {
+  __shared__ float red[4];
+  float* xr = x + (long)blockIdx.x * d;
+  float ss = 0.f;
+  for (int j = threadIdx.x; j < d; j += 256) {
+    float v = xr[j];
+    if (delta != nullptr) {
+      v += to_f(delta[(long)blockIdx.x * d + j]);
+      xr[j] = v;
+    }
+    ss += v * v;
+  }
+  if (w == nullptr) return;
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float rs = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)d + eps);
+  T* yr = y + (long)blockIdx.x * d;
+  for (int j = threadIdx.x; j < d; j += 256) yr[j] = from_f<T>(xr[j] * rs * w[j]);
+}
+
+// row argmax of x [rows, cols] (first index of the maximum; one block per row)
+template <typename T>
+__global__ __launch_bounds__(256) void k_argmax_rows(const T* x, long ld, int cols, int64_t* out) {
+  __shared__ float bv[4];
+  __shared__ int bi[4];
+  const T* r = x + blockIdx.x * ld;
+  float v = NEG_INF;
+  int idx = 0x7fffffff;
+  for (int j = threadIdx.x; j < cols; j += 256) {
+    const float f = to_f(r[j]);
+    if (f > v) { v = f; idx = j; }   // strided scan: the first maximum of this lane's columns
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ov = __shfl_xor(v, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { bv[wave] = v; bi[wave] = idx; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w)
+      if (bv[w] > v || (bv[w] == v && bi[w] < idx)) { v = bv[w]; idx = bi[w]; }
+    out[blockIdx.x] = idx == 0x7fffffff ? 0 : idx;
+  }
 }
 
 }  // namespace dm

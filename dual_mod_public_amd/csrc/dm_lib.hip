@@ -317,6 +317,7 @@ struct DecWs {
   void* q; void* kraw; void* kself; void* vraw;
   float* glogx; float* sig; float* o; float* ssq; float* part;
   void* vin; float* gvu;
+  float* rope; void* kst; void* vst;   // device position: RoPE rows, refined rows before the tape write
   size_t bytes;
 };
 
@@ -338,6 +339,9 @@ DecWs carve_dec(const dm_config* c, int tape_T, void* base) {
   w.part = (float*)take((ns ? ns : 1) * B * c->h * (c->dh + 2) * 4);
   w.vin = take(B * d * e);
   w.gvu = (float*)take(B * d * 4);
+  w.rope = (float*)take(c->dh * 4);
+  w.kst = take(B * d * e);
+  w.vst = take(B * d * e);
   w.bytes = off;
   return w;
 }
@@ -346,14 +350,27 @@ template <typename T, int DH>
 int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const float* sin,
                const dm_decode_args* a, const DecWs& ws, hipStream_t s) {
   const int B = c->B, d = c->d, h = c->h;
-  const int pos = a->pos;
+  // device position (a->pos_dev): one launch shape for every position — the RoPE rows are
+  // gathered first, the split grid covers the whole tape, the refined pair is staged and
+  // written into the tape slot last; host position: the launches are sized to a->pos
+  const bool dev_pos = a->pos_dev != nullptr;
+  const int pos = dev_pos ? 0 : a->pos;
   const int lo = (c->local_window > 0 && pos > c->local_window - 1) ? pos - (c->local_window - 1) : 0;
-  run_proj<T, DH>(c, w, (const T*)a->xhat, B, 1, 1, 0, pos, cos, sin, (T*)ws.q, (T*)ws.kraw, (T*)ws.kself,
-                  (T*)ws.vraw, nullptr, ws.glogx, ws.sig, s);
-  const int nsplit = pos > lo ? cdiv(pos - lo, DEC_SPLIT) : 0;
+  const float* rc = cos;
+  const float* rs = sin;
+  if (dev_pos) {
+    hipLaunchKernelGGL(k_decode_pos_rope, dim3(1), dim3(64), 0, s, a->pos_dev, a->tape_T, cos, sin, DH / 2,
+                       ws.rope);
+    rc = ws.rope;
+    rs = ws.rope + DH / 2;
+  }
+  run_proj<T, DH>(c, w, (const T*)a->xhat, B, 1, 1, 0, dev_pos ? 0 : pos, rc, rs, (T*)ws.q, (T*)ws.kraw,
+                  (T*)ws.kself, (T*)ws.vraw, nullptr, ws.glogx, ws.sig, s);
+  const int nsplit = dev_pos ? cdiv(a->tape_T, DEC_SPLIT) : (pos > lo ? cdiv(pos - lo, DEC_SPLIT) : 0);
   DecodeArgs<T> da{B, h, d, a->tape_T, pos, lo, DEC_SPLIT, nsplit, 1.0f / sqrtf((float)DH),
                    (const T*)ws.q, (const T*)ws.kself, (const T*)ws.vraw, (const T*)a->K_tape,
-                   (const T*)a->V_tape, ws.part, ws.o, ws.ssq, (T*)a->o_cat, nullptr};
+                   (const T*)a->V_tape, ws.part, ws.o, ws.ssq, (T*)a->o_cat, nullptr,
+                   (const int*)a->pos_dev, c->local_window};
   if (nsplit > 0) {
     const int idx = prof_launch_begin(PROF_DEC_READ, true, da.prof_ts);
     launch_timed(idx, k_decode_partial<T, DH, DEC_SPLIT>, dim3(nsplit, B * h), dim3(256), 0, s, da);
@@ -361,15 +378,23 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
   }
   launch_k(PROF_DEC_MERGE, k_decode_merge<T, DH>, dim3(B * h), dim3(64), 0, s, da);
 
-  // refine_kv for the B rows (c = 1, position pos), write slot pos of the tape
-  CellGeom g{B, 1, d, h, DH, pos, 0, 1, a->tape_T};
+  // refine_kv for the B rows (c = 1, position pos), write slot pos of the tape (device
+  // position: a staging row, copied into the slot by k_decode_commit)
+  CellGeom g{B, 1, d, h, DH, pos, 0, 1, dev_pos ? 1 : a->tape_T};
   g.kmod_cols = c->kmod_vraw_heads * DH;
   g.kmod_mode = c->kmod_mode;
   g.v_clamp_tau = c->v_clamp_tau;
   ProfScope pr(PROF_DEC_REFINE, s);
-  run_refine<T, DH>(c, w, g, B, (const T*)a->o_cat, ws.ssq, (const T*)ws.kraw, (const T*)ws.vraw, ws.glogx,
-                    ws.sig, cos, sin, (T*)a->K_tape, (T*)a->V_tape, (long)a->tape_T * DH, pos, (T*)ws.vin,
-                    ws.gvu, nullptr, nullptr, s);
+  if (dev_pos) {
+    run_refine<T, DH>(c, w, g, B, (const T*)a->o_cat, ws.ssq, (const T*)ws.kraw, (const T*)ws.vraw, ws.glogx,
+                      ws.sig, rc, rs, (T*)ws.kst, (T*)ws.vst, (long)DH, 0, (T*)ws.vin, ws.gvu, nullptr, nullptr, s);
+    hipLaunchKernelGGL((k_decode_commit<T, DH>), dim3(B * h), dim3(DH), 0, s, (const int*)a->pos_dev, a->tape_T,
+                       (const T*)ws.kst, (const T*)ws.vst, (T*)a->K_tape, (T*)a->V_tape);
+  } else {
+    run_refine<T, DH>(c, w, g, B, (const T*)a->o_cat, ws.ssq, (const T*)ws.kraw, (const T*)ws.vraw, ws.glogx,
+                      ws.sig, cos, sin, (T*)a->K_tape, (T*)a->V_tape, (long)a->tape_T * DH, pos, (T*)ws.vin,
+                      ws.gvu, nullptr, nullptr, s);
+  }
   if (a->y != nullptr) {
     SrcRows<T> ao{(const T*)a->o_cat, d, B};
     SrcRows<T> bo{(const T*)w->wo, d, d};
@@ -397,8 +422,10 @@ int dm_decode_step(const dm_config* c, const dm_packed* w, const float* cos, con
   if ((rc = check_packed(c, w))) return rc;
   DM_REQUIRE(a && cos && sin && a->xhat && a->K_tape && a->V_tape && a->o_cat, DM_ERR_INVALID,
              "null decode argument");
-  DM_REQUIRE(a->pos >= 0 && a->pos < a->tape_T, DM_ERR_INVALID, "pos=%d outside tape of %d", a->pos,
-             a->tape_T);
+  DM_REQUIRE(a->pos_dev != nullptr || (a->pos >= 0 && a->pos < a->tape_T), DM_ERR_INVALID,
+             "pos=%d outside tape of %d", a->pos, a->tape_T);
+  DM_REQUIRE(a->pos_dev == nullptr || (reinterpret_cast<uintptr_t>(a->pos_dev) & 3) == 0, DM_ERR_INVALID,
+             "pos_dev must be 4-byte aligned");
   DM_REQUIRE(aligned16(a->K_tape) && aligned16(a->V_tape) && aligned16(a->xhat), DM_ERR_INVALID,
              "tape/xhat must be 16-byte aligned");
   const DecWs need = carve_dec(c, a->tape_T, nullptr);
@@ -612,6 +639,39 @@ int dm_linear(int32_t dtype, const void* x, const void* W, const void* r, void* 
   } else {
     return fail(DM_ERR_INVALID, "dtype %d", dtype);
   }
+  DM_HIP(hipGetLastError());
+  return DM_OK;
+}
+
+int dm_residual_rmsnorm(int32_t dtype, float* x, const void* delta, const float* w, void* y, int32_t M,
+                        int32_t d, float eps, void* stream) {
+  DM_REQUIRE(x != nullptr && (w == nullptr || y != nullptr), DM_ERR_INVALID, "null operand");
+  DM_REQUIRE(M > 0 && d > 0, DM_ERR_INVALID, "M=%d d=%d", M, d);
+  hipStream_t s = S(stream);
+  if (dtype == DM_BF16)
+    hipLaunchKernelGGL(k_residual_rmsnorm<bf16>, dim3(M), dim3(256), 0, s, x, (const bf16*)delta, w, (bf16*)y, d,
+                       eps);
+  else if (dtype == DM_F32)
+    hipLaunchKernelGGL(k_residual_rmsnorm<float>, dim3(M), dim3(256), 0, s, x, (const float*)delta, w, (float*)y,
+                       d, eps);
+  else
+    return fail(DM_ERR_INVALID, "dtype %d", dtype);
+  DM_HIP(hipGetLastError());
+  return DM_OK;
+}
+
+int dm_argmax_rows(int32_t dtype, const void* x, int32_t rows, int32_t cols, int64_t ld, int64_t* out,
+                   void* stream) {
+  DM_REQUIRE(x && out, DM_ERR_INVALID, "null operand");
+  DM_REQUIRE(rows > 0 && cols > 0 && ld >= cols, DM_ERR_INVALID, "rows=%d cols=%d ld=%lld", rows, cols,
+             (long long)ld);
+  hipStream_t s = S(stream);
+  if (dtype == DM_BF16)
+    hipLaunchKernelGGL(k_argmax_rows<bf16>, dim3(rows), dim3(256), 0, s, (const bf16*)x, (long)ld, cols, out);
+  else if (dtype == DM_F32)
+    hipLaunchKernelGGL(k_argmax_rows<float>, dim3(rows), dim3(256), 0, s, (const float*)x, (long)ld, cols, out);
+  else
+    return fail(DM_ERR_INVALID, "dtype %d", dtype);
   DM_HIP(hipGetLastError());
   return DM_OK;
 }

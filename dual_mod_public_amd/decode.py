@@ -55,16 +55,28 @@ class StaticTape:
             self._ver = ver
 
     def step(self, xhat, pos, cos, sin, with_wo=False):
-        """xhat [B, d] (pre-normed, storage dtype). Returns (o_cat [B,d], y or None)."""
+        """xhat [B, d] (pre-normed, storage dtype). Returns (o_cat [B,d], y or None).
+
+        pos: the absolute position (int), or a one-element int32 tensor on the device that
+        the kernels read at run time (lm/eval/graph_decode.py:24: one captured graph serves
+        every position); the caller keeps it inside [0, P_max)."""
         self._refresh()
         xhat = xhat.contiguous()
         assert xhat.dtype == self.dtype and xhat.shape == (self.B, self.cfg.d_model)
         cos = cos.to(device=self.device, dtype=torch.float32).contiguous()
         sin = sin.to(device=self.device, dtype=torch.float32).contiguous()
-        if cos.shape[0] <= pos:
-            raise ValueError(f"RoPE table has {cos.shape[0]} rows, pos={pos}")
         a = L.dm_decode_args()
-        a.pos, a.tape_T = pos, self.P
+        if isinstance(pos, torch.Tensor):
+            if pos.dtype != torch.int32 or pos.numel() != 1 or pos.device.type != self.device.type:
+                raise ValueError("a device position is a one-element int32 tensor on the tape's device")
+            if cos.shape[0] < self.P:
+                raise ValueError(f"RoPE table has {cos.shape[0]} rows; a device position needs {self.P}")
+            a.pos, a.pos_dev = 0, L.ptr(pos)
+        else:
+            if cos.shape[0] <= pos:
+                raise ValueError(f"RoPE table has {cos.shape[0]} rows, pos={pos}")
+            a.pos = pos
+        a.tape_T = self.P
         a.xhat, a.K_tape, a.V_tape = L.ptr(xhat), L.ptr(self.K), L.ptr(self.V)
         a.o_cat = L.ptr(self.o_cat)
         a.y = L.ptr(self.y) if with_wo else None

@@ -75,6 +75,30 @@ def make_state_dict(cfg, seed=0, std=0.02, dtype=torch.float32, with_attn_norm=T
     return sd
 
 
+def make_lm_state_dict(cfg, seed=0, std=0.02, dtype=torch.float32):
+    """A DualModLM state dict (models/dualmod/model.py:134-150 names): token embedding
+    N(0, std) (tied head: ``lm_head.weight`` is the same tensor), per layer the attention
+    parameters of ``make_state_dict`` (seed 1000 * seed + layer), SwiGLU matrices N(0, std),
+    RMSNorm weights 1."""
+    rng = np.random.default_rng(seed)
+    d, hid = cfg.d_model, cfg.mlp_hidden
+    t = lambda *shape: torch.from_numpy(rng.normal(0.0, std, size=shape)).to(dtype)   # noqa: E731
+    sd = OrderedDict()
+    sd["tok_emb.weight"] = t(cfg.vocab_size, d)
+    for l in range(cfg.n_layers):
+        pre = f"blocks.{l}."
+        sd[pre + "attn_norm.weight"] = torch.ones(d, dtype=dtype)
+        for k, v in make_state_dict(cfg, seed=1000 * seed + l, std=std, dtype=dtype, with_attn_norm=False).items():
+            sd[pre + "attn." + k] = v
+        sd[pre + "mlp_norm.weight"] = torch.ones(d, dtype=dtype)
+        sd[pre + "mlp.w1.weight"] = t(hid, d)
+        sd[pre + "mlp.w3.weight"] = t(hid, d)
+        sd[pre + "mlp.w2.weight"] = t(d, hid)
+    sd["norm_f.weight"] = torch.ones(d, dtype=dtype)
+    sd["lm_head.weight"] = sd["tok_emb.weight"] if cfg.tie_embeddings else t(cfg.vocab_size, d)
+    return sd
+
+
 def make_input(shape, seed=1, dtype=torch.float32, scale=1.0):
     """x ~ N(0, scale^2) of the given shape (float64 draw, cast)."""
     rng = np.random.default_rng(seed)

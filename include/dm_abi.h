@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DM_ABI_VERSION 5
+#define DM_ABI_VERSION 6
 
 typedef enum dm_status {
   DM_OK = 0,
@@ -287,6 +287,13 @@ typedef struct dm_decode_args {
   void* K_tape; void* V_tape;          /* [B, h, tape_T, dh] */
   void* o_cat; void* y;
   void* workspace; size_t workspace_bytes;
+  /* Device position (lm/eval/graph_decode.py:24,44: GraphDecoder's device-side counter):
+   * when non-NULL, pos is ignored and every kernel reads the position from this int32 in
+   * device memory at run time, so one captured graph of the step serves every position.
+   * The launch shapes then cover the whole tape (split blocks past the position return).
+   * The RoPE tables must hold tape_T rows; a device position outside [0, tape_T) is
+   * clamped into the tape (keeping it inside is the caller's job). */
+  const int32_t* pos_dev;
 } dm_decode_args;
 size_t dm_decode_workspace_bytes(const dm_config* cfg, int32_t tape_T);
 int dm_decode_step(const dm_config* cfg, const dm_packed* w, const float* cos, const float* sin,
@@ -337,6 +344,22 @@ int dm_refine_kv(const dm_config* cfg, const dm_packed* w, const dm_layer_bufs* 
  * N multiple of 128, K multiple of 64, any M. */
 int dm_linear(int32_t dtype, const void* x, const void* W, const void* r, void* y, int32_t M,
               int32_t N, int32_t K, void* stream);
+
+/* ---- residual stream of the trunk's decode step -------------------------------------
+ * The fp32 residual stream around one decode step of a Block (models/dualmod/model.py:
+ * 127-130) with its RMSNorm (attention.py:74-83) in one pass per row: x[M, d] (fp32, in
+ * place) += delta[M, d] (storage dtype; skipped when NULL), then, when w != NULL,
+ * y[M, d] (storage dtype) = x * rsqrt(mean(x^2) + eps) * w (w fp32 [d]). */
+int dm_residual_rmsnorm(int32_t dtype, float* x, const void* delta, const float* w, void* y, int32_t M,
+                        int32_t d, float eps, void* stream);
+
+/* ---- row argmax ------------------------------------------------------------------
+ * out[r] = the first index of the maximum of x[r, 0:cols) (row stride ld elements),
+ * storage dtype bf16 or fp32: the greedy pick of lm/eval/graph_decode.py:62
+ * (lg.argmax(-1)) as one block per row, with no multi-block reduction (nothing to
+ * clear between graph replays). NaNs are skipped, not taken as the maximum. */
+int dm_argmax_rows(int32_t dtype, const void* x, int32_t rows, int32_t cols, int64_t ld, int64_t* out,
+                   void* stream);
 
 /* ---- plain GEMM (test / utility) --------------------------------------------
  * C[M, N] (fp32) = op(A) . op(B)^T (+ C when accumulate != 0), storage dtype inputs,

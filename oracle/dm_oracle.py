@@ -25,7 +25,7 @@ __all__ = [
     "attend_one", "refine_kv", "project_v", "sequential_scan",
     "make_intra_mask", "chunk_attend", "chunk_cell_forward", "layer_forward",
     "uniform_chunks", "exact_sequential", "decode_step", "static_decode_step",
-    "vanilla_attention", "dm_layer", "cfg_get",
+    "vanilla_attention", "dm_layer", "cfg_get", "swiglu", "lm_forward", "lm_decode_step",
 ]
 
 
@@ -405,6 +405,55 @@ def static_decode_step(cfg, sd, xhat_j, pos, Kb, Vb, cos, sin):
     Kb[:, :, pos:pos + 1] = apply_rope(split_heads(kpp, h), cj, sj).to(Kb.dtype)
     Vb[:, :, pos:pos + 1] = split_heads(vpp, h).to(Vb.dtype)
     return o_cat
+
+
+# ---------------------------------------------------------------------------
+# the LLaMA-style trunk — models/dualmod/model.py:102-131, 267-291
+# ---------------------------------------------------------------------------
+
+def swiglu(sd, x, prefix="mlp."):
+    """model.py:111-112: w2(silu(w1 x) * w3 x)."""
+    def lin(t, n):
+        w = sd[prefix + n + ".weight"]
+        return t.to(w.dtype) @ w.t()
+    return lin(F.silu(lin(x, "w1")) * lin(x, "w3"), "w2")
+
+
+def _block_sd(sd, l):
+    pre = f"blocks.{l}."
+    return {k[len(pre):]: v for k, v in sd.items() if k.startswith(pre)}
+
+
+def _attn_sd(bsd):
+    return {k[len("attn."):]: v for k, v in bsd.items() if k.startswith("attn.")}
+
+
+def lm_forward(cfg, sd, idx, cos, sin):
+    """model.py:267-281 with the exact sequential scan per layer (Block.forward,
+    model.py:123-125): logits [B, T, V]. ``sd`` holds the LM's parameter names
+    (tok_emb.weight, blocks.{l}.attn.*, blocks.{l}.mlp.w1..., norm_f.weight, lm_head.weight)."""
+    x = sd["tok_emb.weight"][idx]
+    for l in range(cfg.n_layers):
+        b = _block_sd(sd, l)
+        xhat = rms_norm(x, b["attn_norm.weight"], 1e-5)
+        x = x + _lin(sequential_scan(cfg, _attn_sd(b), xhat, cos, sin), _attn_sd(b), "wo")
+        x = x + swiglu(b, rms_norm(x, b["mlp_norm.weight"], 1e-5))
+    w = sd.get("lm_head.weight", sd["tok_emb.weight"])
+    return rms_norm(x, sd["norm_f.weight"], 1e-5) @ w.t()
+
+
+def lm_decode_step(cfg, sd, idx_j, pos, caches, cos, sin):
+    """model.py:285-291 with Block.decode_step (model.py:127-130): one token per row at
+    position ``pos``; caches: one {"K", "V"} dict per layer (decode_step's cat cache).
+    Returns logits [B, 1, V]."""
+    x = sd["tok_emb.weight"][idx_j]
+    for l in range(cfg.n_layers):
+        b = _block_sd(sd, l)
+        xhat = rms_norm(x, b["attn_norm.weight"], 1e-5)
+        x = x + decode_step(cfg, _attn_sd(b), xhat, pos, caches[l], cos, sin)[1]
+        x = x + swiglu(b, rms_norm(x, b["mlp_norm.weight"], 1e-5))
+    w = sd.get("lm_head.weight", sd["tok_emb.weight"])
+    return rms_norm(x, sd["norm_f.weight"], 1e-5) @ w.t()
 
 
 # ---------------------------------------------------------------------------

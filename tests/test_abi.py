@@ -6,6 +6,7 @@ import os
 import re
 
 import pytest
+import torch
 
 from dual_mod_public_amd import _lib as L
 from dual_mod_public_amd.config import DualModConfig
@@ -30,7 +31,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 
 def test_abi_version():
-    assert L.load().dm_abi_version() == 5
+    assert L.load().dm_abi_version() == 6
 
 
 def _conf(**kw):
@@ -156,3 +157,20 @@ def test_attend_one_refine_kv_refuse_autograd():
     x = torch.zeros(1, 2, 256)
     with pytest.raises(NotImplementedError, match="forward-only"):   # the module's parameters need grads
         attn.refine_kv(x, x, x, x)
+
+
+def test_lm_state_dict_loads_into_model():
+    """DualModLM carries the reference's parameter names (models/dualmod/model.py:134-150):
+    a synthetic LM state dict loads strictly, the head is tied to the embedding, and every
+    attention parameter sits where DualModAttention reads it."""
+    from dual_mod_public_amd.model import DualModLM
+    from dual_mod_public_amd.synthetic import make_lm_state_dict
+    cfg = DualModConfig(d_model=128, n_heads=2, n_layers=2, vocab_size=64, max_seq_len=32,
+                        mlp_hidden_override=192, ctx_mod="mult_res", v_norm="rms")
+    sd = make_lm_state_dict(cfg, seed=1)
+    m = DualModLM(cfg)
+    m.load_state_dict(sd, strict=True)
+    assert m.lm_head.weight is m.tok_emb.weight
+    assert torch.equal(m.blocks[1].attn.w_gk.bias, sd["blocks.1.attn.w_gk.bias"])
+    assert torch.equal(m.blocks[0].mlp.w2.weight, sd["blocks.0.mlp.w2.weight"])
+    assert set(m.state_dict()) == set(sd)

@@ -339,3 +339,67 @@ def test_v_norm_closed_form():
     sd["v_gain"] = torch.tensor([2.0, 1.0, 0.25, 1.0], dtype=D)
     v = O.project_v(cfg, sd, x)
     assert relerr(v, _head_rms_ref(torch.nn.functional.linear(x, sd["wv.weight"]), sd["v_gain"], 4)) < TOL
+
+
+# ---- the trunk around the attention (models/dualmod/model.py:102-131, 267-291) -----------
+
+def _lm_cfg(**kw):
+    return _cfg(n_layers=2, vocab_size=40, mlp_hidden_override=96, **kw)
+
+
+def _lm_sd(cfg, seed=3):
+    from dual_mod_public_amd.synthetic import make_lm_state_dict
+    return {k: v.to(D) for k, v in make_lm_state_dict(cfg, seed=seed, std=0.05).items()}
+
+
+def test_swiglu_gate_and_linear_paths():
+    """silu gates the w1 path only: the output is linear in w3 and in w2 (scaling either by a
+    scales it by a) and not in w1 — a swap of w1 / w3 or a silu on the wrong product fails."""
+    g = torch.Generator().manual_seed(9)
+    sd = {f"mlp.{n}.weight": torch.randn(*s, generator=g, dtype=D)
+          for n, s in (("w1", (6, 4)), ("w3", (6, 4)), ("w2", (4, 6)))}
+    x = torch.randn(3, 4, generator=g, dtype=D)
+    y = O.swiglu(sd, x)
+    for n in ("w3", "w2"):
+        s2 = dict(sd)
+        s2[f"mlp.{n}.weight"] = 2.5 * sd[f"mlp.{n}.weight"]
+        assert relerr(O.swiglu(s2, x), 2.5 * y) < TOL
+    s2 = dict(sd)
+    s2["mlp.w1.weight"] = 2.5 * sd["mlp.w1.weight"]
+    assert relerr(O.swiglu(s2, x), 2.5 * y) > 1e-2
+    # w1 -> +inf-like scale: silu(z) -> z for z > 0, 0 for z < 0 (a ReLU gate)
+    s2 = dict(sd)
+    s2["mlp.w1.weight"] = 1e3 * sd["mlp.w1.weight"]
+    a, b = x @ s2["mlp.w1.weight"].t(), x @ sd["mlp.w3.weight"].t()
+    assert relerr(O.swiglu(s2, x), (a.clamp(min=0) * b) @ sd["mlp.w2.weight"].t()) < 1e-6
+
+
+def test_lm_identity_blocks_give_tied_head_of_normed_embedding():
+    """With every block's output projections zero (wo = w2 = 0) the blocks are the identity and
+    logits = rmsnorm(E[idx]) . E^T (tied head): pins the embedding gather, the final norm and
+    the head's operand."""
+    cfg = _lm_cfg()
+    sd = _lm_sd(cfg)
+    for l in range(cfg.n_layers):
+        sd[f"blocks.{l}.attn.wo.weight"] = torch.zeros_like(sd[f"blocks.{l}.attn.wo.weight"])
+        sd[f"blocks.{l}.mlp.w2.weight"] = torch.zeros_like(sd[f"blocks.{l}.mlp.w2.weight"])
+    E = sd["tok_emb.weight"]
+    idx = torch.tensor([[1, 7, 39, 0], [5, 5, 2, 11]])
+    cos, sin = O.build_rope_cache(4, cfg.head_dim, cfg.rope_theta, dtype=D)
+    e = E[idx]
+    ref = (e / e.pow(2).mean(-1, keepdim=True).add(1e-5).sqrt()) @ E.t()
+    assert relerr(O.lm_forward(cfg, sd, idx, cos, sin), ref) < TOL
+
+
+def test_lm_decode_is_teacher_forced():
+    """T3 at the model level (model.py:285-291 vs :267-281): decoding token by token through
+    the per-layer caches reproduces the teacher-forced forward (exact sequential scan)."""
+    cfg = _lm_cfg()
+    sd = _lm_sd(cfg)
+    B, T = 2, 12
+    idx = torch.randint(0, cfg.vocab_size, (B, T), generator=torch.Generator().manual_seed(2))
+    cos, sin = O.build_rope_cache(T, cfg.head_dim, cfg.rope_theta, dtype=D)
+    ref = O.lm_forward(cfg, sd, idx, cos, sin)
+    caches = [{"K": None, "V": None} for _ in range(cfg.n_layers)]
+    out = torch.cat([O.lm_decode_step(cfg, sd, idx[:, t:t + 1], t, caches, cos, sin) for t in range(T)], 1)
+    assert relerr(out, ref) < TOL
