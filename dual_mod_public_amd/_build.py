@@ -2,7 +2,8 @@
 
     python -m dual_mod_public_amd._build
 
-Compiles csrc/dm_lib.hip with hipcc into dual_mod_public_amd/libdm_hip.so.
+Compiles csrc/dm_lib.hip, dm_bwd.hip and dm_stack.hip with hipcc into
+dual_mod_public_amd/libdm_hip.so.
 Packed FP32 VALU ops are disabled for the device code (the host pass warns
 that it does not know the feature; harmless).
 """
@@ -14,8 +15,8 @@ import sys
 PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libdm_hip.so")
-SOURCES = ["dm_lib.hip", "dm_bwd.hip"]
-HEADERS = ["dm_common.h", "dm_gemm.h", "dm_attn.h", "dm_kernels.h", "dm_decode.h", "dm_bwd.h", "dm_host.h",
+SOURCES = ["dm_lib.hip", "dm_bwd.hip", "dm_stack.hip"]
+HEADERS = ["dm_common.h", "dm_group.h", "dm_gemm.h", "dm_attn.h", "dm_kernels.h", "dm_decode.h", "dm_bwd.h", "dm_host.h",
            "dm_fwd_host.h", "dm_prof.h", "../../include/dm_abi.h"]
 
 

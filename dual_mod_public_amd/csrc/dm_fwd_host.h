@@ -114,20 +114,21 @@ inline const float* v_gain(const dm_config* c, const dm_packed* w) {
   return (c->norms & DM_NORM_V) ? w->gains + 2 * c->h : nullptr;
 }
 
-// vpre: v_raw before the v_norm (nullptr: not kept)
-template <typename T, int DH>
-void run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int Tl, int Tbuf, int buf_t0,
-              int rope_t0, const float* cos, const float* sin, T* qr, T* kraw, T* kself, T* vraw, T* vpre,
-              float* glogx, float* sig, hipStream_t s) {
+// vpre: v_raw before the v_norm (nullptr: not kept); sa: the M input rows (x-hat);
+// small_tiles: 128 x 128 blocks even where 256 x 256 ones fit (more blocks for a short M; the
+// k-order of every output element, and so the result, is the same)
+template <typename T, int DH, class SA>
+void run_proj_src(const dm_config* c, const dm_packed* w, const SA& sa, int M, int Tl, int Tbuf, int buf_t0,
+                  int rope_t0, const float* cos, const float* sin, T* qr, T* kraw, T* kself, T* vraw, T* vpre,
+                  float* glogx, float* sig, hipStream_t s, bool small_tiles = false) {
   const int nseg = (c->ctx_mod == DM_CTX_LINEAR) ? 5 : 6;
   EpiProj<T, DH> epi{M, c->d, c->h, Tl, Tbuf, buf_t0, rope_t0, cos, sin, w->b_proj,
                      qr, kraw, kself, vraw, glogx, sig, c->ctx_mod == DM_CTX_FUSION, v_gain(c, w), vpre};
-  SrcRows<T> sa{xhat, c->d, M};
   SrcRows<T> sb{(const T*)w->w_proj, c->d, nseg * c->d};
   // bf16, whole 256-row / 256-column tiles: 256 x 256 blocks (four 128 x 128 wave tiles,
   // two direct-to-LDS stages); otherwise 128 x 128 with wave tiles spanning whole heads
   if constexpr (sizeof(T) == 2) {
-    if (M % 256 == 0 && (nseg * c->d) % 256 == 0 && c->d % 64 == 0) {
+    if (!small_tiles && M % 256 == 0 && (nseg * c->d) % 256 == 0 && c->d % 64 == 0) {
       launch_gemm<T, 256, 256, 2, 2, -2>(sa, sb, M, nseg * c->d, c->d, epi, s, PROF_PROJ);
       return;
     }
@@ -136,6 +137,14 @@ void run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int 
     launch_gemm_auto<T, 128, 128, 2, 2, 3, 4>(sa, sb, M, nseg * c->d, c->d, epi, s, PROF_PROJ);
   else
     launch_gemm_auto<T, 128, 128, 4, 1, 3, 4>(sa, sb, M, nseg * c->d, c->d, epi, s, PROF_PROJ);
+}
+
+template <typename T, int DH>
+void run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int Tl, int Tbuf, int buf_t0,
+              int rope_t0, const float* cos, const float* sin, T* qr, T* kraw, T* kself, T* vraw, T* vpre,
+              float* glogx, float* sig, hipStream_t s) {
+  run_proj_src<T, DH>(c, w, SrcRows<T>{xhat, c->d, M}, M, Tl, Tbuf, buf_t0, rope_t0, cos, sin, qr, kraw, kself, vraw,
+                      vpre, glogx, sig, s);
 }
 
 template <typename T>
@@ -182,6 +191,11 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
     SrcRows<T> av{vin, c->d, N};
     SrcRows<T> bv{(const T*)w->w_vctx, c->d, c->d};
     EpiSweep2Head<T, DH> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2, vgain};
+    if (launch_log() != nullptr) {
+      record_launch<Sweep2AttendBody<T, DH>>(dim3(c->h, N / CMAX), dim3(256),
+                                             typename Sweep2AttendBody<T, DH>::Args{av, bv, c->d, e2, *next_attend});
+      return;
+    }
     uint64_t* ts;
     const int idx = prof_launch_begin(PROF_SWEEP2, true, ts);
     launch_timed(idx, k_sweep2_attend<T, DH>, dim3(c->h, N / CMAX), dim3(256), 0, s, av, bv, c->d, e2,
@@ -207,9 +221,14 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
       launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, c->d, c->d, e2, s, PROF_SWEEP2);
   }
   // v'' entry-norm clamp of the refined value rows (v_clamp_tau > 0 only)
-  if (g.v_clamp_tau > 0.f)
-    hipLaunchKernelGGL((k_clamp_v<T, DH>), dim3(cdiv((long)N * c->h, 4)), dim3(256), 0, s, g, Vout, out_stride,
-                       out_row0, N, g.v_clamp_tau);
+  if (g.v_clamp_tau > 0.f) {
+    const dim3 grid(cdiv((long)N * c->h, 4));
+    if (launch_log() != nullptr)
+      record_launch<ClampBody<T, DH>>(grid, dim3(256),
+                                      typename ClampBody<T, DH>::Args{g, Vout, out_stride, out_row0, N, g.v_clamp_tau});
+    else
+      hipLaunchKernelGGL((k_clamp_v<T, DH>), grid, dim3(256), 0, s, g, Vout, out_stride, out_row0, N, g.v_clamp_tau);
+  }
 }
 
 // Committed accumulator of a cell: split partials (merged by the first sweep's
@@ -218,10 +237,17 @@ template <typename T, int DH>
 int run_comm(const CellGeom& g, const T* qr, const T* Kc, const T* Vc, float scale, const CellWs& ws,
              hipStream_t s) {
   const CommPlan cp = comm_plan(g.pos0, g.B * g.h);
-  if (cp.nsplit == 0) return 0;
   const int BH = g.B * g.h;
   CommArgs<T> ca{g, qr, Kc, Vc, cp.split_len, scale, ws.Ap, ws.Zp, ws.Mp};
+  ca.nsplit = cp.nsplit;
   if (cp.nsplit == 1) { ca.A = ws.A; ca.Z = ws.Z; ca.Mx = ws.M; }
+  if (launch_log() != nullptr) {
+    // recorded even without a committed prefix (grid x 0), so that every chunk of a layer
+    // records the same launch sequence
+    record_launch<CommBody<T, DH>>(dim3(cp.nsplit, BH), dim3(256), ca);
+    return cp.nsplit;
+  }
+  if (cp.nsplit == 0) return 0;
   launch_k(PROF_COMM, k_comm_partial<T, DH>, dim3(cp.nsplit, BH), dim3(256), 0, s, ca);
   return cp.nsplit;
 }
@@ -303,7 +329,11 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
     if (sw == 0 || !fuse) {   // else the previous sweep's GEMM 2 launch ran it
       const AttendArgs<T> aa = attend_args(sw);
       // 16-row waves; the (b, h) blocks split by query rows until there are >= 256 blocks
-      if (BH >= 256) launch_k(PROF_ATTEND, k_attend<T, DH, 4>, dim3(BH, 1), dim3(256), 0, s, aa);
+      if (launch_log() != nullptr) {
+        if (BH >= 256) record_launch<AttendBody<T, DH, 4>>(dim3(BH, 1), dim3(256), aa);
+        else if (BH >= 128) record_launch<AttendBody<T, DH, 2>>(dim3(BH, 2), dim3(128), aa);
+        else record_launch<AttendBody<T, DH, 1>>(dim3(BH, 4), dim3(64), aa);
+      } else if (BH >= 256) launch_k(PROF_ATTEND, k_attend<T, DH, 4>, dim3(BH, 1), dim3(256), 0, s, aa);
       else if (BH >= 128) launch_k(PROF_ATTEND, k_attend<T, DH, 2>, dim3(BH, 2), dim3(128), 0, s, aa);
       else launch_k(PROF_ATTEND, k_attend<T, DH, 1>, dim3(BH, 4), dim3(64), 0, s, aa);
     }

@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "dm_common.h"
+#include "dm_group.h"
 
 namespace dm {
 
@@ -51,6 +52,22 @@ template <typename T> struct SrcRows {
   long ld;
   int rows;   // valid rows (global index bound)
   DM_DEV const T* ptr(int r, int k) const { return p + (long)min(r, rows - 1) * ld + k; }
+  DM_DEV uint4 load(int r, int k) const { return *reinterpret_cast<const uint4*>(ptr(r, k)); }
+  DM_DEV uint4 xform(uint4 v, int, int, const float*, int) const { return v; }
+};
+
+// Row-major operand whose rows are the rows of one chunk of every batch element of a
+// [B, T, ld] tensor: row r = b * c + p is tensor row b * T + pos0 + p (c a power of two).
+template <typename T> struct SrcChunkRows {
+  static constexpr bool KMAJOR = false;
+  const T* __restrict__ p;
+  long ld;
+  int rows;         // B * c
+  int lc, Tr, pos0;  // log2(c), rows per batch element of the tensor, chunk start
+  DM_DEV const T* ptr(int r, int k) const {
+    r = min(r, rows - 1);
+    return p + ((long)(r >> lc) * Tr + pos0 + (r & ((1 << lc) - 1))) * ld + k;
+  }
   DM_DEV uint4 load(int r, int k) const { return *reinterpret_cast<const uint4*>(ptr(r, k)); }
   DM_DEV uint4 xform(uint4 v, int, int, const float*, int) const { return v; }
 };
@@ -567,28 +584,13 @@ DM_DEV void gemm_kloop(const SA& sa, const SB& sb, int K, int m0, int n0, char* 
   else gemm_mainloop_dma<T, BM, BN, WM, WN, -D>(sa, sb, K, m0, n0, smem, acc, kbase);
 }
 
+// One block tile (bx, by) of split-K slice bz.
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
-__global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint64_t* prof_ts) {
-  const uint64_t t0 = prof_begin(prof_ts);
+DM_DEV void gemm_block(const SA& sa, const SB& sb, int K, const EPI& epi, int bx, int by, int bz) {
   using WT = WaveTile<BM, BN, WM, WN>;
   constexpr bool RMS = requires_prepare<SA>::value;
   constexpr bool KM = SA::KMAJOR && SB::KMAJOR && D < 0;
   __shared__ __attribute__((aligned(1024))) char smem[gemm_lds_bytes<T, BM, BN, D, RMS, KM>()];
-  // Blocks are dispatched round-robin over the 8 XCDs (each with its own L2). For
-  // the K-major (weight-grad) products every XCD gets a contiguous range of tiles
-  // instead (x fastest, then y, then the split-K slice), so tiles that share operand
-  // columns at the same k share an L2.
-  int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
-  if constexpr (KM) {
-    const int gx = gridDim.x, gy = gridDim.y, nb = gx * gy * (int)gridDim.z;
-    if (nb % 8 == 0) {
-      const int L = bx + gx * (by + gy * bz);
-      const int t = (L % 8) * (nb / 8) + L / 8;
-      bx = t % gx;
-      by = (t / gx) % gy;
-      bz = t / (gx * gy);
-    }
-  }
   const int m0 = by * BM, n0 = bx * BN;
   static_assert(!RMS || BM <= RMS_MAXR, "row-scale slots");
   const int wave = threadIdx.x >> 6;
@@ -649,7 +651,43 @@ __global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint
     gemm_kloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, bz * K);
     epi(acc, row0, col0, rs, bz);
   }
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
+__global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint64_t* prof_ts) {
+  const uint64_t t0 = prof_begin(prof_ts);
+  // Blocks are dispatched round-robin over the 8 XCDs (each with its own L2). For
+  // the K-major (weight-grad) products every XCD gets a contiguous range of tiles
+  // instead (x fastest, then y, then the split-K slice), so tiles that share operand
+  // columns at the same k share an L2.
+  int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  if constexpr (SA::KMAJOR && SB::KMAJOR && D < 0) {
+    const int gx = gridDim.x, gy = gridDim.y, nb = gx * gy * (int)gridDim.z;
+    if (nb % 8 == 0) {
+      const int L = bx + gx * (by + gy * bz);
+      const int t = (L % 8) * (nb / 8) + L / 8;
+      bx = t % gx;
+      by = (t / gx) % gy;
+      bz = t / (gx * gy);
+    }
+  }
+  gemm_block<T, BM, BN, WM, WN, D, SA, SB, EPI>(sa, sb, K, epi, bx, by, bz);
   prof_end(prof_ts, t0);
 }
+
+// k_gemm as a grouped-launch body (one split-K slice)
+template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
+struct GemmBody {
+  static constexpr int THREADS = 256;
+  struct Args {
+    SA sa;
+    SB sb;
+    int K;
+    EPI epi;
+  };
+  static DM_DEV void run(const Args& a, int bx, int by) {
+    gemm_block<T, BM, BN, WM, WN, D, SA, SB, EPI>(a.sa, a.sb, a.K, a.epi, bx, by, 0);
+  }
+};
 
 }  // namespace dm

@@ -140,6 +140,11 @@ template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB,
 void launch_gemm(const SA& sa, const SB& sb, int M, int N, int K, const EPI& epi, hipStream_t s,
                  int prof_cls = PROF_NONE) {
   dim3 grid(N / BN, cdiv(M, BM));
+  if (launch_log() != nullptr) {
+    using Body = GemmBody<T, BM, BN, WM, WN, D, SA, SB, EPI>;
+    record_launch<Body>(grid, dim3(256), typename Body::Args{sa, sb, K, epi});
+    return;
+  }
   uint64_t* ts;
   const int idx = prof_launch_begin(prof_cls, true, ts);
   launch_timed(idx, k_gemm<T, BM, BN, WM, WN, D, SA, SB, EPI>, grid, dim3(256), 0, s, sa, sb, K, epi, ts);
@@ -200,6 +205,10 @@ template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB,
 void launch_gemm_splitk(const SA& sa, const SB& sb, int M, int N, int K, int S, const EPI& epi, hipStream_t s,
                         int prof_cls = PROF_NONE) {
   dim3 grid(N / BN, cdiv(M, BM), S);
+  if (launch_log() != nullptr) {   // split-K slices use grid z: no grouped form
+    launch_log()->unsupported = true;
+    return;
+  }
   uint64_t* ts;
   const int idx = prof_launch_begin(prof_cls, true, ts);
   launch_timed(idx, k_gemm<T, BM, BN, WM, WN, D, SA, SB, EPI>, grid, dim3(256), 0, s, sa, sb, K / S, epi, ts);

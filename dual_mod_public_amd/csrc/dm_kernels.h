@@ -134,13 +134,21 @@ static __global__ __launch_bounds__(256) void k_rms_rows_multi(RmsSegs a, int co
 // ---------------------------------------------------------------------------
 // row RMSNorm (attn_norm, models/dualmod/attention.py:74-83): one wave per row
 // ---------------------------------------------------------------------------
+// Row m of a launch -> tensor row: the identity (lc < 0), or the rows of one chunk of every
+// batch element of a [B, T, d] tensor (m = b * 2^lc + p -> b * T + pos0 + p).
+struct RowMap {
+  int lc = -1, T = 0, pos0 = 0;
+  DM_DEV long operator()(int m) const {
+    return lc < 0 ? (long)m : (long)(m >> lc) * T + pos0 + (m & ((1 << lc) - 1));
+  }
+};
+
+// one wave per row
 template <typename T>
-static __global__ __launch_bounds__(256) void k_rmsnorm_rows(const T* __restrict__ x, const T* __restrict__ w,
-                                                      T* __restrict__ y, int M, int d, float eps) {
+DM_DEV void rmsnorm_row(const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ y, long row, int d,
+                        float eps) {
   const int lane = threadIdx.x & 63;
-  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (m >= M) return;
-  const T* xr = x + (long)m * d;
+  const T* xr = x + row * d;
   float ss = 0.f;
   for (int j = lane; j < d; j += 64) {
     float v = to_f(xr[j]);
@@ -148,9 +156,33 @@ static __global__ __launch_bounds__(256) void k_rmsnorm_rows(const T* __restrict
   }
   ss = wave_sum(ss);
   const float rs = rsqrtf(ss / (float)d + eps);
-  T* yr = y + (long)m * d;
+  T* yr = y + row * d;
   for (int j = lane; j < d; j += 64) yr[j] = from_f<T>(to_f(xr[j]) * rs * to_f(w[j]));
 }
+
+template <typename T>
+static __global__ __launch_bounds__(256) void k_rmsnorm_rows(const T* __restrict__ x, const T* __restrict__ w,
+                                                      T* __restrict__ y, int M, int d, float eps) {
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  rmsnorm_row<T>(x, w, y, m, d, eps);
+}
+
+// the rows of one chunk (RowMap), as a grouped-launch body: grid (ceil(M / 4))
+template <typename T> struct RmsRowsBody {
+  static constexpr int THREADS = 256;
+  struct Args {
+    const T* x; const T* w; T* y;
+    int M, d;
+    float eps;
+    RowMap map;
+  };
+  static DM_DEV void run(const Args& a, int bx, int) {
+    const int m = bx * 4 + (threadIdx.x >> 6);
+    if (m >= a.M) return;
+    rmsnorm_row<T>(a.x, a.w, a.y, a.map(m), a.d, a.eps);
+  }
+};
 
 // ---------------------------------------------------------------------------
 // projection epilogue: xhat . [wq | wk | wv | w_gk_x | w_gv_x | v_gate]^T
@@ -311,11 +343,10 @@ DM_DEV int rope_row(const CellGeom& g, int p) { return (g.rope_t0 < 0 ? g.pos0 :
 // One wave per (row, head); the rows are (b, h) at bh * stride, chunk row p at row0 + p.
 // ---------------------------------------------------------------------------
 template <typename T, int DH>
-static __global__ __launch_bounds__(256) void k_clamp_v(CellGeom g, T* __restrict__ V, long stride, int row0,
-                                                        int N, float tau) {
+DM_DEV void clamp_v_block(const CellGeom& g, T* __restrict__ V, long stride, int row0, int N, float tau, int bx) {
   constexpr int PER = (DH + 63) / 64;   // elements per lane
   const int lane = threadIdx.x & 63;
-  const long w = blockIdx.x * 4L + (threadIdx.x >> 6);   // (row m, head hd) = (w / h, w % h)
+  const long w = bx * 4L + (threadIdx.x >> 6);   // (row m, head hd) = (w / h, w % h)
   if (w >= (long)N * g.h) return;
   const int m = (int)(w / g.h), hd = (int)(w - (long)m * g.h);
   const int b = m / g.c, p = m - b * g.c;
@@ -336,6 +367,24 @@ static __global__ __launch_bounds__(256) void k_clamp_v(CellGeom g, T* __restric
     if (e < DH) row[e] = from_f<T>(v[i] * sc);
   }
 }
+
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_clamp_v(CellGeom g, T* __restrict__ V, long stride, int row0,
+                                                        int N, float tau) {
+  clamp_v_block<T, DH>(g, V, stride, row0, N, tau, blockIdx.x);
+}
+
+template <typename T, int DH> struct ClampBody {
+  static constexpr int THREADS = 256;
+  struct Args {
+    CellGeom g;
+    T* V;
+    long stride;
+    int row0, N;
+    float tau;
+  };
+  static DM_DEV void run(const Args& a, int bx, int) { clamp_v_block<T, DH>(a.g, a.V, a.stride, a.row0, a.N, a.tau, bx); }
+};
 
 // Value blend of column col (attention.py:362-384): v'' = g v_raw + (1 - g) v_ctx, except
 // for the kmod heads: raw (v_raw, or tanh(v_raw) with the tanh bound) or, gated_norm,
@@ -363,6 +412,7 @@ template <typename T> struct CommArgs {
   float* A;    // [nsplit, B*h, c, dh]
   float* Z;    // [nsplit, B*h, c]
   float* Mx;   // [nsplit, B*h, c]
+  int nsplit = 0;   // splits of this cell (a grouped launch's grid covers the largest)
 };
 
 struct KeyBound {
@@ -375,14 +425,13 @@ struct KeyStrictLower {   // q is block-relative; q0 = the block's first query r
 };
 
 template <typename T, int DH>
-static __global__ __launch_bounds__(256) void k_comm_partial(CommArgs<T> a) {
+DM_DEV void comm_partial_block(const CommArgs<T>& a, int s, int bh) {
   using C = AttnCfg<T, DH>;
   __shared__ __attribute__((aligned(16))) T lds[C::LDS_ELEMS];
   T* Ks = lds;
   T* Vs = Ks + C::KT * C::LDK;
   T* Ps = Vs + C::KT * C::LDK;
   const CellGeom& g = a.g;
-  const int s = blockIdx.x, bh = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int BH = g.B * g.h;
   const int k_begin = s * a.split_len;
@@ -423,6 +472,20 @@ static __global__ __launch_bounds__(256) void k_comm_partial(CommArgs<T> a) {
     }
   }
 }
+
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_comm_partial(CommArgs<T> a) {
+  comm_partial_block<T, DH>(a, blockIdx.x, blockIdx.y);
+}
+
+template <typename T, int DH> struct CommBody {
+  static constexpr int THREADS = 256;
+  using Args = CommArgs<T>;
+  static DM_DEV void run(const Args& a, int bx, int by) {
+    if (bx >= a.nsplit) return;   // uniform: past this cell's splits
+    comm_partial_block<T, DH>(a, bx, by);
+  }
+};
 
 // ---------------------------------------------------------------------------
 // one sweep's read (scan_cell_fwd.py:63-85 / :132-149): intra rows (strict
@@ -621,6 +684,17 @@ static __global__ __launch_bounds__(64 * NW) void k_attend(AttendArgs<T> a) {
   if (q0 >= a.g.c) return;                     // uniform: no rows in this block
   attend_rows<T, DH, NW, false>(a, blockIdx.x, q0, lds);
 }
+
+template <typename T, int DH, int NW> struct AttendBody {
+  static constexpr int THREADS = 64 * NW;
+  using Args = AttendArgs<T>;
+  static DM_DEV void run(const Args& a, int bx, int by) {
+    __shared__ __attribute__((aligned(16))) T lds[AttnCfg<T, DH>::LDS_ELEMS];
+    const int q0 = 16 * NW * by;
+    if (q0 >= a.g.c) return;
+    attend_rows<T, DH, NW, false>(a, bx, q0, lds);
+  }
+};
 
 // ---------------------------------------------------------------------------
 // sweep GEMM 1: u . W_sweep^T (u = RMSNorm_ctx(o) on the A load)
@@ -1053,10 +1127,8 @@ template <typename T, int DH> struct EpiSweep2Head {
 };
 
 template <typename T, int DH>
-static __global__ __launch_bounds__(256) void k_sweep2_attend(SrcRows<T> sa, SrcRows<T> sb, int K,
-                                                              EpiSweep2Head<T, DH> epi, AttendArgs<T> aa,
-                                                              uint64_t* prof_ts) {
-  const uint64_t t0 = prof_begin(prof_ts);
+DM_DEV void sweep2_attend_block(const SrcRows<T>& sa, const SrcRows<T>& sb, int K, const EpiSweep2Head<T, DH>& epi,
+                                const AttendArgs<T>& aa, int hh, int b) {
   constexpr int D = sizeof(T) == 2 ? -3 : 4;
   constexpr int LDT = DH + 4;
   using WT = WaveTile<64, DH, 2, 2>;
@@ -1067,7 +1139,6 @@ static __global__ __launch_bounds__(256) void k_sweep2_attend(SrcRows<T> sa, Src
   __shared__ __attribute__((aligned(1024))) char smem[GEMM_LDS + C::LDS_ELEMS * sizeof(T)];
   T* alds = reinterpret_cast<T*>(smem + GEMM_LDS);
   static_assert(64 * LDT * 4 <= gemm_stage_bytes<T, 64, DH, D>(), "output tile fits the stages");
-  const int hh = blockIdx.x, b = blockIdx.y;
   const int m0 = b * 64, n0 = hh * DH;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   floatx4 acc[WT::FM][WT::FN];
@@ -1098,14 +1169,34 @@ static __global__ __launch_bounds__(256) void k_sweep2_attend(SrcRows<T> sa, Src
   epi.template apply<LDT>(tile, m0, n0, pre, alds + C::KT * C::LDK, C::LDK);
   __syncthreads();   // the V tile is complete
   attend_rows<T, DH, 4, true>(aa, b * aa.g.h + hh, 0, alds);
+}
+
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_sweep2_attend(SrcRows<T> sa, SrcRows<T> sb, int K,
+                                                              EpiSweep2Head<T, DH> epi, AttendArgs<T> aa,
+                                                              uint64_t* prof_ts) {
+  const uint64_t t0 = prof_begin(prof_ts);
+  sweep2_attend_block<T, DH>(sa, sb, K, epi, aa, blockIdx.x, blockIdx.y);
   prof_end(prof_ts, t0);
 }
+
+template <typename T, int DH> struct Sweep2AttendBody {
+  static constexpr int THREADS = 256;
+  struct Args {
+    SrcRows<T> sa, sb;
+    int K;
+    EpiSweep2Head<T, DH> epi;
+    AttendArgs<T> aa;
+  };
+  static DM_DEV void run(const Args& a, int bx, int by) { sweep2_attend_block<T, DH>(a.sa, a.sb, a.K, a.epi, a.aa, bx, by); }
+};
 
 // y = acc (+ x): the W_O projection with the block residual, or plain nn.Linear
 template <typename T> struct EpiResidual {
   int M, N;
   const T* __restrict__ x;
   T* __restrict__ y;
+  RowMap map = RowMap{};   // output / residual row of GEMM row m
   // the residual rows of 16-row group i + 1 are loaded before group i is stored
   // (y may alias x)
   template <int FM, int FN>
@@ -1115,10 +1206,10 @@ template <typename T> struct EpiResidual {
     auto load_x = [&](int i, int buf) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int m = min(row0 + 16 * i + 4 * (lane >> 4) + q, M - 1);
+        const long m = map(min(row0 + 16 * i + 4 * (lane >> 4) + q, M - 1));
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          xv[buf][q][j] = x != nullptr ? to_f(x[(long)m * N + col0 + 16 * j + lc]) : 0.f;
+          xv[buf][q][j] = x != nullptr ? to_f(x[m * N + col0 + 16 * j + lc]) : 0.f;
       }
     };
     load_x(0, 0);
@@ -1130,8 +1221,9 @@ template <typename T> struct EpiResidual {
       for (int q = 0; q < 4; ++q) {
         const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
         if (m >= M) continue;
+        const long my = map(m);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) y[(long)m * N + col0 + 16 * j + lc] = from_f<T>(acc[i][j][q] + xv[cb][q][j]);
+        for (int j = 0; j < FN; ++j) y[my * N + col0 + 16 * j + lc] = from_f<T>(acc[i][j][q] + xv[cb][q][j]);
       }
     }
   }

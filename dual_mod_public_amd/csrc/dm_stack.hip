@@ -1,0 +1,246 @@
+// libdm_hip.so — the layer-batched (wavefront) forward of a stack of DM attention sublayers
+// (dm_stack_fwd in include/dm_abi.h; the schedule of engines/wave3d/wave3d.py:1-47 applied
+// to the chained chunk cells).
+//
+// Layer l runs cell t - l at global step t. What one layer launches for one cell — the
+// chunk's attn_norm rows and projection, the committed-prefix partials, the K sweeps, W_O
+// with the residual — is recorded (launch_log) instead of launched, for every active layer;
+// the records of a step line up position by position (uniform schedule), and each position
+// becomes one grouped launch (k_grouped<Body>, grid z = active layer) whose argument table
+// lives in the caller's plan buffer.
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <vector>
+
+#include "dm_fwd_host.h"
+
+namespace dm {
+namespace {
+
+int log2_exact(int v) {
+  int l = 0;
+  while ((1 << l) < v) ++l;
+  return (1 << l) == v ? l : -1;
+}
+
+// One layer's cell i, recorded: the same kernels and arguments as dm_layer_fwd's projection,
+// cell and W_O, restricted to the chunk's rows.
+template <typename T, int DH>
+void record_chunk(const dm_config* c, const dm_stack_layer& ly, const float* cos, const float* sin,
+                  const int32_t* sched, int n_cells, int i, int cache_T, const std::vector<size_t>& toff) {
+  const dm_packed* w = ly.w;
+  const dm_layer_bufs* L = ly.bufs;
+  const int pos0 = sched[3 * i], cc = sched[3 * i + 1], K = sched[3 * i + 2];
+  const int M = c->B * cc, d = c->d;
+  const RowMap map{log2_exact(cc), L->T, pos0};
+  const T* x = (const T*)ly.x;
+  // attn_norm of the chunk's rows into the layer's x-hat rows, then the projections
+  SrcChunkRows<T> sx{x, d, M, map.lc, L->T, pos0};
+  if (w->attn_norm_w != nullptr) {
+    record_launch<RmsRowsBody<T>>(dim3(cdiv(M, 4)), dim3(256),
+                                  typename RmsRowsBody<T>::Args{x, (const T*)w->attn_norm_w, (T*)L->xhat, M, d,
+                                                                c->rms_eps, map});
+    sx.p = (const T*)L->xhat;
+  }
+  // (a chunk's M = B * c rows: 128 x 128 blocks, several per layer and CU)
+  run_proj_src<T, DH>(c, w, sx, M, cc, L->T, pos0, pos0, cos, sin, (T*)L->qr, (T*)L->kraw, (T*)L->kself,
+                      (T*)L->vraw, (T*)L->vpre, L->glogx, L->sig, nullptr, true);
+  // the cell (as dm_layer_fwd: with the tape its sweep states go there)
+  const CellWs ws = carve_cell(c, cache_T, ly.workspace);
+  const T* o_last;
+  if (ly.tape == nullptr) {
+    run_cell<T, DH>(c, w, L, cos, sin, pos0, cc, K, pos0, L->T, (T*)ly.K_cache, (T*)ly.V_cache, cache_T,
+                    (T*)ly.ocat, nullptr, ws, nullptr, nullptr);
+    o_last = (const T*)ws.o;
+  } else {
+    Carver cv(static_cast<char*>(ly.tape) + toff[i]);
+    CellSave<T> sv = carve_save<T>(c, (size_t)M, K, true, pos0 > 0, cv);
+    if (c->ctx_mod != DM_CTX_LINEAR)
+      sv.vin = reinterpret_cast<T*>(static_cast<char*>(ly.tape) + toff[n_cells]) + vin_row(c, sched, n_cells, i) * d;
+    CellWs cws = ws;
+    if (sv.Mx) cws.M = sv.Mx;
+    run_cell<T, DH>(c, w, L, cos, sin, pos0, cc, K, pos0, L->T, (T*)ly.K_cache, (T*)ly.V_cache, cache_T,
+                    (T*)ly.ocat, nullptr, cws, &sv, nullptr);
+    o_last = sv.o + (size_t)(K - 1) * M * d;
+  }
+  // W_O (+ the residual) of the chunk's rows: the last sweep's o holds the chunk's o_cat rows
+  EpiResidual<T> ep{M, d, (c->flags & DM_FLAG_NO_RESIDUAL) ? nullptr : x, (T*)ly.y, map};
+  SrcRows<T> ao{o_last, d, M};
+  SrcRows<T> bo{(const T*)w->wo, d, d};
+  // 64 x 64 blocks (the per-layer product's k-order, so its result)
+  if constexpr (sizeof(T) == 2)
+    launch_gemm_auto<T, 64, 64, 2, 2, 3, 4>(ao, bo, M, d, d, ep, nullptr);
+  else
+    launch_gemm<T, 64, 64, 2, 2, 4>(ao, bo, M, d, d, ep, nullptr);
+}
+
+struct GroupedLaunch {
+  const void* f;
+  dim3 grid, block;
+  size_t off;
+};
+
+// Records every step and lines the layers' launches up; fills `tab` (when non-null) with the
+// argument tables and returns the plan size in *bytes.
+int plan_stack(const dm_config* c, int nl, const dm_stack_layer* layers, const float* cos, const float* sin,
+               const int32_t* sched, int n_cells, int cache_T, std::vector<GroupedLaunch>& out,
+               std::vector<unsigned char>* tab, size_t* bytes) {
+  const std::vector<size_t> toff =
+      c->dtype == DM_BF16 ? tape_offsets<bf16>(c, sched, n_cells) : tape_offsets<float>(c, sched, n_cells);
+  size_t off = 0;
+  std::vector<LaunchLog> logs;
+  for (int t = 0; t < n_cells + nl - 1; ++t) {
+    const int la = std::max(0, t - n_cells + 1), lb = std::min(nl - 1, t);
+    logs.assign(lb - la + 1, LaunchLog{});
+    for (int l = la; l <= lb; ++l) {
+      launch_log() = &logs[l - la];
+      if (c->dtype == DM_BF16) {
+        if (c->dh == 64) record_chunk<bf16, 64>(c, layers[l], cos, sin, sched, n_cells, t - l, cache_T, toff);
+        else record_chunk<bf16, 128>(c, layers[l], cos, sin, sched, n_cells, t - l, cache_T, toff);
+      } else {
+        if (c->dh == 64) record_chunk<float, 64>(c, layers[l], cos, sin, sched, n_cells, t - l, cache_T, toff);
+        else record_chunk<float, 128>(c, layers[l], cos, sin, sched, n_cells, t - l, cache_T, toff);
+      }
+      launch_log() = nullptr;
+      DM_REQUIRE(!logs[l - la].unsupported, DM_ERR_UNSUPPORTED, "a launch of layer %d has no grouped form", l);
+    }
+    const size_t n = logs[0].recs.size();
+    for (const LaunchLog& lg : logs)
+      DM_REQUIRE(lg.recs.size() == n, DM_ERR_UNSUPPORTED, "step %d: layers record %zu and %zu launches", t,
+                 lg.recs.size(), n);
+    const int G = (int)logs.size();
+    for (size_t r = 0; r < n; ++r) {
+      const LaunchRec& r0 = logs[0].recs[r];
+      unsigned gx = 0;
+      for (const LaunchLog& lg : logs) {
+        const LaunchRec& x = lg.recs[r];
+        DM_REQUIRE(x.gfunc == r0.gfunc && x.grid.y == r0.grid.y && x.block.x == r0.block.x &&
+                       x.args_bytes == r0.args_bytes,
+                   DM_ERR_UNSUPPORTED, "step %d, launch %zu differs between layers", t, r);
+        gx = std::max(gx, x.grid.x);
+      }
+      if (gx == 0) continue;   // nothing to do for any layer (no committed prefix yet)
+      off = (off + 255) / 256 * 256;
+      out.push_back(GroupedLaunch{r0.gfunc, dim3(gx, r0.grid.y, G), r0.block, off});
+      if (tab != nullptr) {
+        tab->resize(off + (size_t)G * r0.args_bytes);
+        for (int g = 0; g < G; ++g)
+          std::memcpy(tab->data() + off + (size_t)g * r0.args_bytes, logs[g].recs[r].args.data(), r0.args_bytes);
+      }
+      off += (size_t)G * r0.args_bytes;
+    }
+  }
+  *bytes = off;
+  return DM_OK;
+}
+
+int check_stack(const dm_config* c, int nl, const dm_stack_layer* layers, const int32_t* sched, int n_cells,
+                int cache_T) {
+  int rc = check_cfg(c);
+  if (rc) return rc;
+  DM_REQUIRE(nl >= 1 && layers != nullptr, DM_ERR_INVALID, "n_layers=%d", nl);
+  DM_REQUIRE(c->local_window == 0, DM_ERR_UNSUPPORTED, "local_window is decode-only");
+  DM_REQUIRE(layers[0].bufs != nullptr, DM_ERR_INVALID, "null layer buffers");
+  const int T = layers[0].bufs->T;
+  if ((rc = dm_check_schedule(sched, n_cells, T))) return rc;
+  for (int i = 0; i < n_cells; ++i)
+    DM_REQUIRE(sched[3 * i + 1] == sched[1] && sched[3 * i + 2] == sched[2], DM_ERR_UNSUPPORTED,
+               "the layer-batched forward needs equal cells (cell %d: c=%d K=%d, cell 0: c=%d K=%d)", i,
+               sched[3 * i + 1], sched[3 * i + 2], sched[1], sched[2]);
+  DM_REQUIRE(log2_exact(sched[1]) >= 0, DM_ERR_UNSUPPORTED, "cell length %d is not a power of two", sched[1]);
+  DM_REQUIRE(T <= cache_T, DM_ERR_INVALID, "T=%d > cache_T=%d", T, cache_T);
+  const bool tape = layers[0].tape != nullptr;
+  const size_t need_ws = carve_cell(c, cache_T, nullptr).bytes;
+  for (int l = 0; l < nl; ++l) {
+    const dm_stack_layer& ly = layers[l];
+    if ((rc = check_packed(c, ly.w)) || (rc = check_bufs(c, ly.bufs))) return rc;
+    DM_REQUIRE(ly.bufs->T == T, DM_ERR_INVALID, "layer %d: T=%d, layer 0: T=%d", l, ly.bufs->T, T);
+    DM_REQUIRE(ly.w->attn_norm_w == nullptr || ly.bufs->xhat != nullptr, DM_ERR_INVALID,
+               "layer %d: attn_norm needs the xhat buffer", l);
+    DM_REQUIRE(ly.x && ly.y && ly.ocat && aligned16(ly.x) && aligned16(ly.y), DM_ERR_INVALID,
+               "layer %d: null/misaligned x, y or ocat", l);
+    DM_REQUIRE(ly.K_cache && ly.V_cache && aligned16(ly.K_cache) && aligned16(ly.V_cache), DM_ERR_INVALID,
+               "layer %d: K/V cache must be non-null and 16-byte aligned", l);
+    DM_REQUIRE(ly.workspace && ly.workspace_bytes >= need_ws && aligned16(ly.workspace), DM_ERR_WORKSPACE,
+               "layer %d: workspace %zu < %zu bytes", l, ly.workspace_bytes, need_ws);
+    DM_REQUIRE((ly.tape != nullptr) == tape, DM_ERR_INVALID, "layer %d: all layers with a tape or none", l);
+    if (tape) {
+      const size_t need = dm_layer_tape_bytes(c, sched, n_cells);
+      DM_REQUIRE(ly.tape_bytes >= need && aligned16(ly.tape), DM_ERR_WORKSPACE, "layer %d: tape %zu < %zu bytes",
+                 l, ly.tape_bytes, need);
+    }
+  }
+  return DM_OK;
+}
+
+// The launch list of every plan written by this process (keyed by the plan's device
+// address): a call with build == 0 replays it without recording the steps again.
+struct PlanCache {
+  std::mutex mu;
+  std::map<const void*, std::vector<GroupedLaunch>> lists;
+};
+PlanCache& plan_cache() {
+  static PlanCache c;
+  return c;
+}
+
+}  // namespace
+}  // namespace dm
+
+using namespace dm;
+
+extern "C" {
+
+size_t dm_stack_fwd_plan_bytes(const dm_config* c, int32_t n_layers, const dm_stack_layer* layers,
+                               const int32_t* sched, int32_t n_cells, int32_t cache_T) {
+  if (check_stack(c, n_layers, layers, sched, n_cells, cache_T) != DM_OK) return 0;
+  std::vector<GroupedLaunch> launches;
+  size_t bytes = 0;
+  if (plan_stack(c, n_layers, layers, nullptr, nullptr, sched, n_cells, cache_T, launches, nullptr, &bytes) != DM_OK)
+    return 0;
+  return bytes;
+}
+
+int dm_stack_fwd(const dm_config* c, int32_t n_layers, const dm_stack_layer* layers, const float* cos,
+                 const float* sin, const int32_t* sched, int32_t n_cells, int32_t cache_T, void* plan,
+                 size_t plan_bytes, int32_t build, void* stream) {
+  int rc = check_stack(c, n_layers, layers, sched, n_cells, cache_T);
+  if (rc) return rc;
+  DM_REQUIRE(cos && sin, DM_ERR_INVALID, "null rope tables");
+  DM_REQUIRE(plan != nullptr && (reinterpret_cast<uintptr_t>(plan) & 255) == 0, DM_ERR_INVALID,
+             "plan must be non-null and 256-byte aligned");
+  std::vector<GroupedLaunch> launches;
+  bool cached = false;
+  if (!build) {
+    PlanCache& pc = plan_cache();
+    std::lock_guard<std::mutex> lk(pc.mu);
+    auto it = pc.lists.find(plan);
+    if (it != pc.lists.end()) {
+      launches = it->second;
+      cached = true;
+    }
+  }
+  if (!cached) {
+    std::vector<unsigned char> tab;
+    size_t bytes = 0;
+    if ((rc = plan_stack(c, n_layers, layers, cos, sin, sched, n_cells, cache_T, launches, build ? &tab : nullptr,
+                         &bytes)))
+      return rc;
+    DM_REQUIRE(plan_bytes >= bytes, DM_ERR_WORKSPACE, "plan %zu < %zu bytes", plan_bytes, bytes);
+    if (build) DM_HIP(hipMemcpy(plan, tab.data(), bytes, hipMemcpyHostToDevice));
+    PlanCache& pc = plan_cache();
+    std::lock_guard<std::mutex> lk(pc.mu);
+    pc.lists[plan] = launches;
+  }
+  hipStream_t s = S(stream);
+  for (const GroupedLaunch& g : launches) {
+    void* p = static_cast<char*>(plan) + g.off;
+    void* args[] = {&p};
+    DM_HIP(hipLaunchKernel(g.f, g.grid, g.block, args, 0, s));
+  }
+  DM_HIP(hipGetLastError());
+  return DM_OK;
+}
+
+}  // extern "C"

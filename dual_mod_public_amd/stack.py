@@ -15,13 +15,22 @@ records a memset (the zeroing is a fill kernel). Weights live in the cells' pack
 buffers, repacked in place by ``load`` (outside the graph) after an optimizer step.
 """
 
+import ctypes
+
 import torch
 
-from .engine import HipSweepCell, LayerGrads, uniform_chunks
+from . import _lib as L
+from .engine import HipSweepCell, LayerGrads, _sched, uniform_chunks
 
 
 class HipLayerStack:
-    def __init__(self, cfg, n_layers, B, T, schedule=None, device="cuda", dtype=torch.bfloat16, tape=True):
+    """wavefront=True runs the forward layer-batched (dm_stack_fwd, the schedule of
+    engines/wave3d/wave3d.py:1-47 on the chained chunk cells): layer l works on cell t - l at
+    step t and each kernel of a step is one launch over every active layer. Same results as
+    the layer-by-layer forward, bit for bit; it needs a schedule of equal cells."""
+
+    def __init__(self, cfg, n_layers, B, T, schedule=None, device="cuda", dtype=torch.bfloat16, tape=True,
+                 wavefront=False):
         self.cfg, self.L, self.B, self.T = cfg, n_layers, B, T
         self.device, self.dtype = torch.device(device), dtype
         d, h, dh = cfg.d_model, cfg.n_heads, cfg.head_dim
@@ -48,6 +57,8 @@ class HipLayerStack:
                 off += sz
         self.cos = self.sin = None
         self.graph = None
+        self.wavefront = wavefront
+        self._plan = None
 
     def load(self, state_dicts, cos, sin):
         """Pack every layer's weights (reference names, incl. attn_norm.weight) and the RoPE
@@ -63,11 +74,48 @@ class HipLayerStack:
             self.sin.copy_(sin[:self.T])
         return self
 
+    def _stack_args(self):
+        """The dm_stack_layer array (and the structs it points to, kept alive here)."""
+        self._keep = []
+        arr = (L.dm_stack_layer * self.L)()
+        for l, cell in enumerate(self.cells):
+            w, b = cell.w.struct(with_attn_norm=True), self.bufs[l].struct()
+            self._keep += [w, b]
+            a = arr[l]
+            a.w, a.bufs = ctypes.addressof(w), ctypes.addressof(b)
+            a.x, a.y = L.ptr(self.xs[l]), L.ptr(self.xs[l + 1])
+            a.K_cache, a.V_cache, a.ocat = L.ptr(self.K[l]), L.ptr(self.V[l]), L.ptr(self.ocat[l])
+            a.tape = L.ptr(self.tapes[l])
+            a.tape_bytes = 0 if self.tapes[l] is None else self.tapes[l].numel()
+            a.workspace, a.workspace_bytes = L.ptr(cell.workspace), cell.workspace.numel()
+        return arr
+
+    def forward_wavefront(self):
+        """The layer-batched forward over the stack's buffers (xs[0] -> xs[L]). The first call
+        writes the launch plan (a blocking copy); later calls launch from it (graph-capturable)."""
+        conf = self.cells[0]._conf(True)
+        sched = _sched(self.schedule)
+        arr = self._stack_args()
+        build = 0
+        if self._plan is None:
+            n = L.lib().dm_stack_fwd_plan_bytes(ctypes.byref(conf), self.L, arr, sched, len(self.schedule), self.T)
+            if n == 0:
+                raise L.DMError("dm_stack_fwd_plan_bytes rejected the stack (equal cells of a power-of-two length "
+                                "are needed)")
+            self._plan = torch.empty(n, device=self.device, dtype=torch.uint8)
+            build = 1
+        L.check(L.lib().dm_stack_fwd(ctypes.byref(conf), self.L, arr, L.ptr(self.cos), L.ptr(self.sin), sched,
+                                     len(self.schedule), self.T, L.ptr(self._plan), self._plan.numel(), build,
+                                     L.stream_ptr()))
+
     def _run(self):
         self.flat.zero_()
-        for l, cell in enumerate(self.cells):
-            cell.layer_forward(self.xs[l], self.xs[l + 1], self.cos, self.sin, self.schedule, self.K[l], self.V[l],
-                               self.ocat[l], self.bufs[l], tape=self.tapes[l])
+        if self.wavefront:
+            self.forward_wavefront()
+        else:
+            for l, cell in enumerate(self.cells):
+                cell.layer_forward(self.xs[l], self.xs[l + 1], self.cos, self.sin, self.schedule, self.K[l],
+                                   self.V[l], self.ocat[l], self.bufs[l], tape=self.tapes[l])
         for l in reversed(range(self.L)):
             self.cells[l].layer_backward(self.xs[l], self.dxs[l + 1], self.dxs[l], self.cos, self.sin, self.schedule,
                                          self.K[l], self.V[l], self.ocat[l], self.bufs[l], self.grads[l],

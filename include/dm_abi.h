@@ -204,6 +204,39 @@ int dm_layer_fwd(const dm_config* cfg, const dm_packed* w, const void* x, void* 
                  int32_t cache_T, void* ocat, void* tape, size_t tape_bytes, void* workspace,
                  size_t workspace_bytes, void* stream);
 
+/* ---- layer-batched (wavefront) forward of a stack of layers --------------------------
+ * engines/wave3d/wave3d.py:1-47 (layer l at global step t works on step t - l, every active
+ * layer's work batched into the same launches), applied to the chunk schedule above: layer l
+ * runs cell t - l at global step t (its chunk's rows are final once that cell's K sweeps
+ * are done, so layer l + 1 takes them one step later), and each kernel of a step is ONE launch
+ * over all active layers (grid z = layer), its arguments read from `plan`. Per layer the
+ * result is dm_layer_fwd's, bit for bit: the same bufs, caches, ocat, tape and output y (the
+ * chunk's RMSNorm + projection, its cell, W_O + residual per chunk instead of per layer).
+ * Layer l reads layers[l].x and writes layers[l].y (layers[l + 1].x is normally
+ * layers[l].y). Every cell of the schedule has the same length c (a power of two <= 64) and
+ * the same n_sweeps. Each layer has its own workspace (dm_cell_workspace_bytes(cfg,
+ * cache_T)) and tape (optional, as dm_layer_fwd; all layers with or all without).
+ * plan: device memory of dm_stack_fwd_plan_bytes() bytes holding every launch's argument
+ * table. build != 0 writes it (a blocking host-to-device copy) before launching; build == 0
+ * launches from a plan written by an earlier call with the same arguments (e.g. under graph
+ * capture): the library keeps each written plan's launch list, keyed by the plan's address,
+ * so such a call only issues the launches. Kernel timing (dm_prof_start) does not cover this
+ * entry point. */
+typedef struct dm_stack_layer {
+  const dm_packed* w;
+  const dm_layer_bufs* bufs;
+  const void* x; void* y;              /* [B, T, d] layer input / output */
+  void* K_cache; void* V_cache;        /* [B, h, cache_T, dh] */
+  void* ocat;                          /* [B, T, d] */
+  void* tape; size_t tape_bytes;       /* NULL: no tape */
+  void* workspace; size_t workspace_bytes;
+} dm_stack_layer;
+size_t dm_stack_fwd_plan_bytes(const dm_config* cfg, int32_t n_layers, const dm_stack_layer* layers,
+                               const int32_t* sched, int32_t n_cells, int32_t cache_T);
+int dm_stack_fwd(const dm_config* cfg, int32_t n_layers, const dm_stack_layer* layers, const float* cos,
+                 const float* sin, const int32_t* sched, int32_t n_cells, int32_t cache_T, void* plan,
+                 size_t plan_bytes, int32_t build, void* stream);
+
 /* ---- whole layer backward ---------------------------------------------------------
  * Reverse-scan backward of the layer forward above (engines/wavescan/engine/backward.py:92-123,
  * FusedSweepCell.cell_backward fused_sweep.py:1557-1850, layer_close :1873-1959):

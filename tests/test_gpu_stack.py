@@ -2,7 +2,9 @@
 the single-GPU part of engines/wavescan/engine/graphs.py:36-792): L attention sublayers
 forward + backward with one flat fp32 gradient buffer; against autograd through the oracle's
 chained layers; the captured HIP graph's replays equal the eager step bit for bit (replayed
-several times with eager work in between); and the T-K8 determinism check
+several times with eager work in between); the layer-batched (wavefront) forward equals the
+layer-by-layer forward bit for bit (outputs, caches, layer buffers, tapes, and the gradients
+of the backward that follows); and the T-K8 determinism check
 (engines/wavescan/tests/test_k1_k9.py:346-373): two reruns of a short training loop give
 bit-identical losses and weights."""
 
@@ -32,10 +34,10 @@ def _digest(t):
     return hashlib.sha1(t.detach().contiguous().view(torch.uint8).cpu().numpy().tobytes()).hexdigest()[:12]
 
 
-def _stack(cfg, n, B, T, dtype, seeds, sched, graph=False):
+def _stack(cfg, n, B, T, dtype, seeds, sched, graph=False, wavefront=False, tape=True):
     sds = [make_state_dict(cfg, seed=s, std=0.02) for s in seeds]
     cos, sin = O.build_rope_cache(T, cfg.head_dim, cfg.rope_theta)
-    st = HipLayerStack(cfg, n, B, T, schedule=sched, device=DEV, dtype=dtype)
+    st = HipLayerStack(cfg, n, B, T, schedule=sched, device=DEV, dtype=dtype, wavefront=wavefront, tape=tape)
     st.load([{k: v.to(DEV) for k, v in sd.items()} for sd in sds], cos, sin)
     if graph:
         st.capture()
@@ -132,3 +134,79 @@ def test_k8_determinism_training_loop():
             assert torch.isfinite(a[k]).all(), k
             assert torch.equal(a[k], b[k]), (k, float((a[k] - b[k]).abs().max()))
     assert runs[0][0][-1] != runs[0][0][0]   # the weights did move
+
+
+def _bufs_equal(a, b):
+    for n in ("xhat", "qr", "kraw", "kself", "vraw", "glogx", "sig"):
+        ta, tb = getattr(a, n), getattr(b, n)
+        if ta is None and tb is None:
+            continue
+        if not torch.equal(ta, tb):
+            return n
+    return None
+
+
+@pytest.mark.parametrize("dtype,ctx_mod,n,B,T,c,K,d,h,tape", [
+    (torch.float32, "mult_res", 3, 2, 64, 16, 4, 256, 4, True),
+    (torch.bfloat16, "mult_res", 4, 2, 128, 32, 3, 256, 4, True),
+    (torch.bfloat16, "linear", 3, 2, 128, 64, 2, 256, 4, False),
+    (torch.bfloat16, "fusion", 3, 1, 128, 64, 4, 256, 2, True),
+    (torch.bfloat16, "mult_res", 5, 8, 512, 64, 4, 1024, 16, True),
+    (torch.bfloat16, "mult_res", 3, 2, 256, 64, 4, 2048, 16, True),
+])
+def test_wavefront_forward_equals_layer_by_layer(dtype, ctx_mod, n, B, T, c, K, d, h, tape):
+    say(f"wavefront forward vs layer by layer: {dtype} {ctx_mod} L={n} B={B} T={T} c={c} K={K} d={d} h={h} "
+        f"tape={tape}")
+    cfg = cfg_of(d=d, h=h, T=T, ctx_mod=ctx_mod)
+    sched = [(p, c, K) for p in range(0, T, c)]
+    seeds = tuple(70 + i for i in range(n))
+    st_w, _ = _stack(cfg, n, B, T, dtype, seeds, sched, wavefront=True, tape=tape)
+    st_l, _ = _stack(cfg, n, B, T, dtype, seeds, sched, tape=tape)
+    if tape:   # slots a cell shorter than 64 rows leaves unwritten compare equal too
+        for t in st_w.tapes + st_l.tapes:
+            t.zero_()
+    g = torch.Generator(device=DEV).manual_seed(8)
+    x = torch.randn(B, T, d, generator=g, device=DEV).to(dtype)
+    dy = torch.randn(B, T, d, generator=g, device=DEV).to(dtype)
+    for rep in range(2):   # the second step launches from the plan the first one wrote
+        y1, dx1, _ = st_w.step(x, dy)
+        torch.cuda.synchronize()
+        y2, dx2, _ = st_l.step(x, dy)
+        torch.cuda.synchronize()
+        for l in range(n):
+            assert torch.equal(st_w.xs[l + 1], st_l.xs[l + 1]), (rep, l, "y")
+            assert torch.equal(st_w.K[l], st_l.K[l]) and torch.equal(st_w.V[l], st_l.V[l]), (rep, l, "K/V")
+            assert torch.equal(st_w.ocat[l], st_l.ocat[l]), (rep, l, "ocat")
+            assert _bufs_equal(st_w.bufs[l], st_l.bufs[l]) is None, (rep, l, _bufs_equal(st_w.bufs[l], st_l.bufs[l]))
+            if tape:
+                assert torch.equal(st_w.tapes[l], st_l.tapes[l]), (rep, l, "tape")
+        assert torch.equal(dx1, dx2) and torch.equal(st_w.flat, st_l.flat), rep
+
+
+def test_wavefront_graph_replays_equal_eager():
+    """The wavefront step captured as a HIP graph: every replay equals the eager layer-by-layer
+    step bit for bit, with eager work between the replays."""
+    say("wavefront stack graph replay == eager layer-by-layer step")
+    cfg = cfg_of(T=128)
+    B, T, n = 2, 128, 3
+    sched = [(p, 32, 3) for p in range(0, T, 32)]
+    st_g, _ = _stack(cfg, n, B, T, torch.bfloat16, (81, 82, 83), sched, graph=True, wavefront=True)
+    st_e, _ = _stack(cfg, n, B, T, torch.bfloat16, (81, 82, 83), sched)
+    g = torch.Generator(device=DEV).manual_seed(3)
+    for rep in range(3):
+        x = torch.randn(B, T, cfg.d_model, generator=g, device=DEV).to(torch.bfloat16)
+        dy = torch.randn(B, T, cfg.d_model, generator=g, device=DEV).to(torch.bfloat16)
+        y1, dx1, _ = st_g.step(x, dy)
+        torch.cuda.synchronize()
+        y1, dx1, f1 = y1.clone(), dx1.clone(), st_g.flat.clone()
+        y2, dx2, _ = st_e.step(x, dy)
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2) and torch.equal(dx1, dx2) and torch.equal(f1, st_e.flat), rep
+        _ = (x.float() @ x.float().transpose(1, 2)).sum().item()
+
+
+def test_wavefront_rejects_unequal_cells():
+    cfg = cfg_of(T=64)
+    st, _ = _stack(cfg, 2, 2, 64, torch.bfloat16, (1, 2), [(0, 16, 4), (16, 48, 2)], wavefront=True)
+    with pytest.raises(L.DMError):
+        st.forward_wavefront()
