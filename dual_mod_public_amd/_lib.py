@@ -95,6 +95,12 @@ class dm_stack_layer(ctypes.Structure):
                 ("workspace_bytes", ctypes.c_size_t)]
 
 
+class dm_stack_bwd_layer(ctypes.Structure):
+    _fields_ = [("w", c_vp), ("bufs", c_vp), ("x", c_vp), ("dy", c_vp), ("dx", c_vp), ("K_cache", c_vp),
+                ("V_cache", c_vp), ("ocat", c_vp), ("tape", c_vp), ("tape_bytes", ctypes.c_size_t), ("grads", c_vp),
+                ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t)]
+
+
 P = ctypes.POINTER
 
 # name -> (restype, argtypes); every symbol include/dm_abi.h declares
@@ -137,6 +143,10 @@ SIGNATURES = {
     "dm_argmax_rows": (ctypes.c_int, [c_i32, c_vp, c_i32, c_i32, ctypes.c_int64, c_vp, c_vp]),
     "dm_stack_fwd_plan_bytes": (ctypes.c_size_t, [P(dm_config), c_i32, P(dm_stack_layer), P(c_i32), c_i32, c_i32]),
     "dm_stack_fwd": (ctypes.c_int, [P(dm_config), c_i32, P(dm_stack_layer), c_fp, c_fp, P(c_i32), c_i32, c_i32,
+                                    c_vp, ctypes.c_size_t, c_i32, c_vp]),
+    "dm_stack_bwd_plan_bytes": (ctypes.c_size_t, [P(dm_config), c_i32, P(dm_stack_bwd_layer), P(c_i32), c_i32,
+                                                  c_i32]),
+    "dm_stack_bwd": (ctypes.c_int, [P(dm_config), c_i32, P(dm_stack_bwd_layer), c_fp, c_fp, P(c_i32), c_i32, c_i32,
                                     c_vp, ctypes.c_size_t, c_i32, c_vp]),
     "dm_residual_rmsnorm": (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, ctypes.c_float, c_vp]),
     "dm_gemm": (ctypes.c_int, [c_i32, c_i32, c_i32, c_vp, c_vp, c_fp, c_i32, c_i32, c_i32, c_i32,

@@ -368,7 +368,7 @@ DM_DEV void refine_vjp4(const RefineBwdArgs<T>& a, int m, int hd, int jj, const 
 // the committed-prefix VJP or the grad cache): one thread per item, the grads read from the NS
 // slices.
 template <typename T, int DH, int NS>
-static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
+DM_DEV void refine_bwd_body(const RefineBwdArgs<T>& a) {
   constexpr int Q = DH / 8;   // items per (row, head)
   const int per_row = a.g.d / 8;
   const int idx = blockIdx.x * 256 + threadIdx.x;
@@ -392,6 +392,11 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
     for (int i = 0; i < 4; ++i) { gr.ka[i] += t0[i]; gr.kb[i] += t1[i]; gr.va[i] += t2[i]; gr.vb[i] += t3[i]; }
   }
   refine_vjp4<T, DH>(a, m, hd, jj, gr);
+}
+
+template <typename T, int DH, int NS>
+static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
+  refine_bwd_body<T, DH, NS>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -483,12 +488,12 @@ template <typename T> struct EpiVinBwd {
 // ---------------------------------------------------------------------------
 constexpr int DU_EPI_TN = 64;
 template <typename T, int S>
-static __global__ __launch_bounds__(256) void k_du_epi(int M, int d, int h, float inv_d, float eps,
-                                                       const float* __restrict__ part,
-                                                       const float* __restrict__ lamdv, const T* __restrict__ o,
-                                                       const float* __restrict__ ssq, const T* __restrict__ normw,
-                                                       float* __restrict__ gw, float* __restrict__ rowdot,
-                                                       float* __restrict__ dnw) {
+DM_DEV void du_epi_body(int M, int d, int h, float inv_d, float eps,
+                        const float* __restrict__ part,
+                        const float* __restrict__ lamdv, const T* __restrict__ o,
+                        const float* __restrict__ ssq, const T* __restrict__ normw,
+                        float* __restrict__ gw, float* __restrict__ rowdot,
+                        float* __restrict__ dnw){
   __shared__ float cs[4][DU_EPI_TN];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m0 = blockIdx.x * 16 + 4 * wave, col = blockIdx.y * DU_EPI_TN + lane;
@@ -529,6 +534,16 @@ static __global__ __launch_bounds__(256) void k_du_epi(int M, int d, int h, floa
   if (wave == 0) dnw[(long)blockIdx.x * d + col] = dn_old + (cs[0][lane] + cs[1][lane] + cs[2][lane] + cs[3][lane]);
 }
 
+template <typename T, int S>
+static __global__ __launch_bounds__(256) void k_du_epi(int M, int d, int h, float inv_d, float eps,
+                                                       const float* __restrict__ part,
+                                                       const float* __restrict__ lamdv, const T* __restrict__ o,
+                                                       const float* __restrict__ ssq, const T* __restrict__ normw,
+                                                       float* __restrict__ gw, float* __restrict__ rowdot,
+                                                       float* __restrict__ dnw) {
+  du_epi_body<T, S>(M, d, h, inv_d, eps, part, lamdv, o, ssq, normw, gw, rowdot, dnw);
+}
+
 
 // ---------------------------------------------------------------------------
 // attention VJP of one sweep, two blocks per (b, h), 4 waves x 16 rows each:
@@ -567,7 +582,7 @@ template <typename T, int DH> struct AttnBwdCfg {
 };
 
 template <typename T, int DH>
-static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
+DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
   using C = AttnBwdCfg<T, DH>;
   constexpr int LDE = C::LDE, LDI = C::LDI, NDT = DH / 16;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
@@ -800,8 +815,8 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
       }
       __syncthreads();
       // Items it = tid + 256 k: row it / Q, pairs 4 (it % Q); a row's items are Q consecutive
-      // lanes. Two items per round, both gathered before either is applied (their loads in
-      // flight together).
+      // lanes. One item per thread at a time: with two in flight the kernel needs more than 256
+      // registers a lane and a CU holds one block instead of two.
       constexpr int Q = DH / 8;
       auto grads = [&](int j, int jj) {
         const float* kr = dKs + j * LDF + jj;
@@ -814,16 +829,10 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
         return gr;
       };
       const int n_items = c * Q;
-      for (int it = tid; it < n_items; it += 512) {
-        const int it2 = it + 256;
-        const bool two = it2 < n_items;   // uniform over a row's lanes (n_items is a multiple of Q)
+      for (int it = tid; it < n_items; it += 256) {
         const int j = it / Q, jj = 4 * (it - j * Q);
-        const int j2 = two ? it2 / Q : j, jj2 = two ? 4 * (it2 - j2 * Q) : jj;
-        const RefineIn in1 = refine_gather<T, DH>(a.ref, b * c + j, hh, jj);
-        RefineIn in2;
-        if (two) in2 = refine_gather<T, DH>(a.ref, b * c + j2, hh, jj2);
-        refine_apply<T, DH>(a.ref, b * c + j, hh, jj, in1, grads(j, jj));
-        if (two) refine_apply<T, DH>(a.ref, b * c + j2, hh, jj2, in2, grads(j2, jj2));
+        const RefineIn in = refine_gather<T, DH>(a.ref, b * c + j, hh, jj);
+        refine_apply<T, DH>(a.ref, b * c + j, hh, jj, in, grads(j, jj));
       }
       return;
     }
@@ -839,6 +848,12 @@ static __global__ __launch_bounds__(256) void k_attn_bwd(AttnBwdArgs<T> a) {
       }
     }
   }
+}
+
+// head_dim 64: at most 256 registers a lane, two blocks per CU
+template <typename T, int DH>
+static __global__ __launch_bounds__(256, DH == 64 ? 2 : 1) void k_attn_bwd(AttnBwdArgs<T> a) {
+  attn_bwd_body<T, DH>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -871,7 +886,7 @@ template <typename T> struct CommKeyArgs {
 // wave w owns keys 16w .. 16w + 15 of the cell (key-major products, as in k_attn_bwd).
 // In the grad-cache form one block per (64-key tile, b, h) takes every query tile.
 template <typename T, int DH>
-static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
+DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
   using C = AttnBwdCfg<T, DH>;
   constexpr int LDE = C::LDE, LDI = C::LDI, NDT = DH / 16;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
@@ -1016,6 +1031,11 @@ static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
   }
 }
 
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
+  comm_dkv_body<T, DH>(a);
+}
+
 template <typename T> struct CommQueryArgs {
   int B, h, Tbuf, cache_T, nrows;              // query rows [row0, nrows)
   const int* klim;                             // [Tbuf] committed prefix length of each row (0: none)
@@ -1029,7 +1049,7 @@ template <typename T> struct CommQueryArgs {
 // One block per (b, h, 64-row query tile), the tiles with the longest prefixes
 // first; wave w owns query rows 16w .. 16w + 15 (query-major products).
 template <typename T, int DH>
-static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
+DM_DEV void comm_dq_body(const CommQueryArgs<T>& a) {
   using C = AttnBwdCfg<T, DH>;
   constexpr int LDE = C::LDE, LDI = C::LDI, NDT = DH / 16;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
@@ -1145,6 +1165,11 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
   }
 }
 
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
+  comm_dq_body<T, DH>(a);
+}
+
 // ---------------------------------------------------------------------------
 // projection VJP inputs: d_proj [B*T, nproj*d] in the w_proj row order
 //   q: unrotate dq_r; k: dkraw + unrotate(dkself); v: dvraw; gate x-halves: dglogx;
@@ -1158,26 +1183,29 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
 // block; each row's loads are issued before its stores.
 // ---------------------------------------------------------------------------
 constexpr int PROJ_ROWS = 64;
+// map: row m of this launch -> layer row (one chunk's rows, or the identity); flags: PROJ_ROWS_OUT
+// writes the dproj rows, PROJ_PARTIALS the column partials of the block (block index blockIdx.y)
+constexpr int PROJ_ROWS_OUT = 1, PROJ_PARTIALS = 2;
 template <typename T, int DH>
-static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, int h, int nproj, int fusion,
-                                                  const float* __restrict__ dq, const float* __restrict__ dkraw,
-                                                  const float* __restrict__ dkself, const float* __restrict__ dvraw,
-                                                  const float* __restrict__ dglogx, const float* __restrict__ dsig,
-                                                  const float* __restrict__ sig, const float* __restrict__ cos,
-                                                  const float* __restrict__ sin, T* __restrict__ dproj,
-                                                  float* __restrict__ bpart, const T* __restrict__ vpre,
-                                                  const float* __restrict__ vgain, float* __restrict__ vgpart) {
+DM_DEV void proj_bwd_body(int M, int T_, int d, int h, int nproj, int fusion, const float* __restrict__ dq,
+                          const float* __restrict__ dkraw, const float* __restrict__ dkself,
+                          const float* __restrict__ dvraw, const float* __restrict__ dglogx,
+                          const float* __restrict__ dsig, const float* __restrict__ sig,
+                          const float* __restrict__ cos, const float* __restrict__ sin, T* __restrict__ dproj,
+                          float* __restrict__ bpart, const T* __restrict__ vpre, const float* __restrict__ vgain,
+                          float* __restrict__ vgpart, RowMap map, int flags, int rpb) {
   const int pidx = blockIdx.x * 256 + threadIdx.x;
   if (pidx >= d / 2) return;
   const int hd = pidx / (DH / 2), jj = pidx - hd * (DH / 2);
   const int c1 = hd * DH + jj, c2 = c1 + DH / 2;
-  const int r0 = blockIdx.y * PROJ_ROWS, r1 = min(r0 + PROJ_ROWS, M);
+  const int r0 = blockIdx.y * rpb, r1 = min(r0 + rpb, M);
   float bg[4] = {0.f, 0.f, 0.f, 0.f}, bv[2] = {0.f, 0.f}, vg = 0.f;
   const float gvn = vgain != nullptr ? vgain[hd] : 0.f;
-  for (int m = r0; m < r1; ++m) {
-    const int b = m / T_, t = m - b * T_;
+  for (int mi = r0; mi < r1; ++mi) {
+    const long m = map(mi);
+    const int b = (int)(m / T_), t = (int)(m - (long)b * T_);
     const long hr = (((long)b * h + hd) * T_ + t) * DH;
-    const float* dg = dglogx + (long)m * 2 * d;
+    const float* dg = dglogx + m * 2 * d;
     const float cs = cos[(long)t * (DH / 2) + jj], sn = sin[(long)t * (DH / 2) + jj];
     const float q1 = dq[hr + jj], q2 = dq[hr + jj + DH / 2];
     const float s1 = dkself[hr + jj], s2 = dkself[hr + jj + DH / 2];
@@ -1195,34 +1223,72 @@ static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, i
     }
     float z1 = 0.f, z2 = 0.f;
     if (nproj == 6) {
-      const float sg1 = sig[(long)m * d + c1], sg2 = sig[(long)m * d + c2];
+      const float sg1 = sig[m * d + c1], sg2 = sig[m * d + c2];
       // fusion: dsig already holds the grad of the raw pre-activation (no sigmoid, no bias)
-      z1 = fusion ? dsig[(long)m * d + c1] : dsig[(long)m * d + c1] * sg1 * (1.f - sg1);
-      z2 = fusion ? dsig[(long)m * d + c2] : dsig[(long)m * d + c2] * sg2 * (1.f - sg2);
+      z1 = fusion ? dsig[m * d + c1] : dsig[m * d + c1] * sg1 * (1.f - sg1);
+      z2 = fusion ? dsig[m * d + c2] : dsig[m * d + c2] * sg2 * (1.f - sg2);
     }
-    T* D = dproj + (long)m * nproj * d;
-    D[c1] = from_f<T>(q1 * cs + q2 * sn);
-    D[c2] = from_f<T>(-q1 * sn + q2 * cs);
-    D[d + c1] = from_f<T>(k1 + s1 * cs + s2 * sn);
-    D[d + c2] = from_f<T>(k2 - s1 * sn + s2 * cs);
-    D[2 * d + c1] = from_f<T>(v1);
-    D[2 * d + c2] = from_f<T>(v2);
-    D[3 * d + c1] = from_f<T>(g1);
-    D[3 * d + c2] = from_f<T>(g2);
-    D[4 * d + c1] = from_f<T>(g3);
-    D[4 * d + c2] = from_f<T>(g4);
-    if (nproj == 6) {
-      D[5 * d + c1] = from_f<T>(z1);
-      D[5 * d + c2] = from_f<T>(z2);
+    if (flags & PROJ_ROWS_OUT) {
+      T* D = dproj + m * nproj * d;
+      D[c1] = from_f<T>(q1 * cs + q2 * sn);
+      D[c2] = from_f<T>(-q1 * sn + q2 * cs);
+      D[d + c1] = from_f<T>(k1 + s1 * cs + s2 * sn);
+      D[d + c2] = from_f<T>(k2 - s1 * sn + s2 * cs);
+      D[2 * d + c1] = from_f<T>(v1);
+      D[2 * d + c2] = from_f<T>(v2);
+      D[3 * d + c1] = from_f<T>(g1);
+      D[3 * d + c2] = from_f<T>(g2);
+      D[4 * d + c1] = from_f<T>(g3);
+      D[4 * d + c2] = from_f<T>(g4);
+      if (nproj == 6) {
+        D[5 * d + c1] = from_f<T>(z1);
+        D[5 * d + c2] = from_f<T>(z2);
+      }
     }
     bg[0] += g1; bg[1] += g2; bg[2] += g3; bg[3] += g4;
     bv[0] += z1; bv[1] += z2;
   }
+  if (!(flags & PROJ_PARTIALS)) return;
   float* P = bpart + (long)blockIdx.y * 3 * d;
   P[c1] = bg[0]; P[c2] = bg[1]; P[d + c1] = bg[2]; P[d + c2] = bg[3];
   P[2 * d + c1] = bv[0]; P[2 * d + c2] = bv[1];
   if (vgain != nullptr && jj == 0) vgpart[(long)blockIdx.y * h + hd] = vg;
 }
+
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, int h, int nproj, int fusion,
+                                                         const float* __restrict__ dq, const float* __restrict__ dkraw,
+                                                         const float* __restrict__ dkself,
+                                                         const float* __restrict__ dvraw,
+                                                         const float* __restrict__ dglogx,
+                                                         const float* __restrict__ dsig, const float* __restrict__ sig,
+                                                         const float* __restrict__ cos, const float* __restrict__ sin,
+                                                         T* __restrict__ dproj, float* __restrict__ bpart,
+                                                         const T* __restrict__ vpre, const float* __restrict__ vgain,
+                                                         float* __restrict__ vgpart, RowMap map, int flags) {
+  proj_bwd_body<T, DH>(M, T_, d, h, nproj, fusion, dq, dkraw, dkself, dvraw, dglogx, dsig, sig, cos, sin, dproj, bpart,
+                       vpre, vgain, vgpart, map, flags, PROJ_ROWS);
+}
+
+template <typename T, int DH> struct ProjBwdBody {
+  static constexpr int THREADS = 256;
+  struct Args {
+    int M, T_, d, h, nproj, fusion;
+    const float *dq, *dkraw, *dkself, *dvraw, *dglogx, *dsig, *sig, *cos, *sin;
+    T* dproj;
+    float* bpart;
+    const T* vpre;
+    const float* vgain;
+    float* vgpart;
+    RowMap map;
+    int flags;
+    int rpb;   // rows per block (PROJ_ROWS when the block partials are written)
+  };
+  static DM_DEV void run(const Args& a, int, int) {
+    proj_bwd_body<T, DH>(a.M, a.T_, a.d, a.h, a.nproj, a.fusion, a.dq, a.dkraw, a.dkself, a.dvraw, a.dglogx, a.dsig,
+                         a.sig, a.cos, a.sin, a.dproj, a.bpart, a.vpre, a.vgain, a.vgpart, a.map, a.flags, a.rpb);
+  }
+};
 
 // Column sums of a row-major fp32 matrix [M, ncols], stage 1: part[chunk][col]
 static __global__ __launch_bounds__(256) void k_colsum_partial(int M, int ncols, int rows_per_chunk,
@@ -1287,19 +1353,20 @@ static __global__ __launch_bounds__(256) void k_sum_rows_add(int nchunk, int nco
 //   its own LDS row, the four are added at the end.
 // ---------------------------------------------------------------------------
 constexpr int RMSN_ROWS = 8;
+// map: row m of this launch -> layer row; flags: 1 writes dx, 2 the weight-grad partials
 template <typename T>
-static __global__ __launch_bounds__(256) void k_rmsnorm_bwd(int M, int d, float eps, int residual,
-                                                     const T* __restrict__ x, const T* __restrict__ w,
-                                                     const float* __restrict__ dxhat, const T* __restrict__ dy,
-                                                     T* __restrict__ dx, float* __restrict__ dwa_part) {
+DM_DEV void rmsnorm_bwd_body(int M, int d, float eps, int residual, const T* __restrict__ x,
+                             const T* __restrict__ w, const float* __restrict__ dxhat, const T* __restrict__ dy,
+                             T* __restrict__ dx, float* __restrict__ dwa_part, RowMap map, int flags) {
   extern __shared__ float acc_lds[];   // [4][d]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float* acc = acc_lds + (long)wave * d;
   for (int j = lane; j < d; j += 64) acc[j] = 0.f;
   const int r0 = blockIdx.x * RMSN_ROWS, r1 = min(r0 + RMSN_ROWS, M);
-  for (int m = r0 + wave; m < r1; m += 4) {
-    const T* xr = x + (long)m * d;
-    const float* gr = dxhat + (long)m * d;
+  for (int mi = r0 + wave; mi < r1; mi += 4) {
+    const long m = map(mi);
+    const T* xr = x + m * d;
+    const float* gr = dxhat + m * d;
     float ss = 0.f, dot = 0.f;
     for (int j = lane; j < d; j += 64) {
       const float xv = to_f(xr[j]);
@@ -1312,15 +1379,46 @@ static __global__ __launch_bounds__(256) void k_rmsnorm_bwd(int M, int d, float 
     const float c3 = r * r * r / (float)d * dot;
     for (int j = lane; j < d; j += 64) {
       const float xv = to_f(xr[j]), g = gr[j];
-      const float yv = residual ? to_f(dy[(long)m * d + j]) : 0.f;
-      dx[(long)m * d + j] = from_f<T>(r * to_f(w[j]) * g - xv * c3 + yv);
+      if (flags & 1) {
+        const float yv = residual ? to_f(dy[m * d + j]) : 0.f;
+        dx[m * d + j] = from_f<T>(r * to_f(w[j]) * g - xv * c3 + yv);
+      }
       acc[j] += g * xv * r;
     }
   }
+  if (!(flags & 2)) return;
   __syncthreads();
   for (int j = threadIdx.x; j < d; j += 256)
     dwa_part[(long)blockIdx.x * d + j] = acc_lds[j] + acc_lds[d + j] + acc_lds[2 * d + j] + acc_lds[3 * d + j];
 }
+
+template <typename T>
+static __global__ __launch_bounds__(256) void k_rmsnorm_bwd(int M, int d, float eps, int residual,
+                                                     const T* __restrict__ x, const T* __restrict__ w,
+                                                     const float* __restrict__ dxhat, const T* __restrict__ dy,
+                                                     T* __restrict__ dx, float* __restrict__ dwa_part, RowMap map,
+                                                     int flags) {
+  rmsnorm_bwd_body<T>(M, d, eps, residual, x, w, dxhat, dy, dx, dwa_part, map, flags);
+}
+
+template <typename T> struct RmsnormBwdBody {
+  static constexpr int THREADS = 256;
+  struct Args {
+    int M, d;
+    float eps;
+    int residual;
+    const T *x, *w;
+    const float* dxhat;
+    const T* dy;
+    T* dx;
+    float* dwa_part;
+    RowMap map;
+    int flags;
+  };
+  static DM_DEV void run(const Args& a, int, int) {
+    rmsnorm_bwd_body<T>(a.M, a.d, a.eps, a.residual, a.x, a.w, a.dxhat, a.dy, a.dx, a.dwa_part, a.map, a.flags);
+  }
+};
 
 // dx = dy + dxhat (no attn_norm) or dx = dxhat (no residual either)
 template <typename T>
@@ -1372,5 +1470,43 @@ static __global__ __launch_bounds__(256) void k_unpack_add(UnpackArgs a) {
     }
   }
 }
+
+// ---- grouped-launch bodies of the backward's per-cell kernels (the layer-batched backward) ----
+template <typename T, int DH, int NS> struct RefineBwdBody {
+  static constexpr int THREADS = 256;
+  using Args = RefineBwdArgs<T>;
+  static DM_DEV void run(const Args& a, int, int) { refine_bwd_body<T, DH, NS>(a); }
+};
+template <typename T, int S> struct DuEpiBody {
+  static constexpr int THREADS = 256;
+  struct Args {
+    int M, d, h;
+    float inv_d, eps;
+    const float *part, *lamdv;
+    const T* o;
+    const float* ssq;
+    const T* normw;
+    float *gw, *rowdot, *dnw;
+  };
+  static DM_DEV void run(const Args& a, int, int) {
+    du_epi_body<T, S>(a.M, a.d, a.h, a.inv_d, a.eps, a.part, a.lamdv, a.o, a.ssq, a.normw, a.gw, a.rowdot, a.dnw);
+  }
+};
+template <typename T, int DH> struct AttnBwdBody {
+  static constexpr int THREADS = 256;
+  static constexpr int MIN_WAVES = DH == 64 ? 2 : 1;
+  using Args = AttnBwdArgs<T>;
+  static DM_DEV void run(const Args& a, int, int) { attn_bwd_body<T, DH>(a); }
+};
+template <typename T, int DH> struct CommDkvBody {
+  static constexpr int THREADS = 256;
+  using Args = CommKeyArgs<T>;
+  static DM_DEV void run(const Args& a, int, int) { comm_dkv_body<T, DH>(a); }
+};
+template <typename T, int DH> struct CommDqBody {
+  static constexpr int THREADS = 256;
+  using Args = CommQueryArgs<T>;
+  static DM_DEV void run(const Args& a, int, int) { comm_dq_body<T, DH>(a); }
+};
 
 }  // namespace dm

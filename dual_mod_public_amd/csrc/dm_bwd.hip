@@ -269,7 +269,10 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
   if (gc.dK == nullptr) {
     CommKeyArgs<T> ka{B, h, T_, cache_T, pos0, cc, pos0 + cc, t_end, qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow,
                       scale, ws.dKp, ws.dVp};
-    hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(COMM_NSQ, BH), dim3(256), lds_attn, s, ka);
+    if (launch_log() != nullptr)
+      record_launch<CommDkvBody<T, DH>>(dim3(COMM_NSQ, BH), dim3(256), ka, (unsigned)lds_attn);
+    else
+      hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(COMM_NSQ, BH), dim3(256), lds_attn, s, ka);
     dKn = ws.dKp; dVn = ws.dVp; dn_stride = (long)CMAX * DH; dn_row0 = 0; dn_psum = (long)BH * CMAX * DH;
   } else {
     dKn = gc.dK; dVn = gc.dV; dn_stride = (long)cache_T * DH; dn_row0 = pos0; dn_psum = 0;
@@ -290,8 +293,14 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
     if (sw == K - 1) {
       const RefineBwdArgs<T> ra = refine_args(sw);
       const dim3 rgrid(cdiv((long)N * d / 8, 256));
-      if (gc.dK == nullptr) hipLaunchKernelGGL((k_refine_bwd<T, DH, COMM_NSQ>), rgrid, dim3(256), 0, s, ra);
-      else hipLaunchKernelGGL((k_refine_bwd<T, DH, 1>), rgrid, dim3(256), 0, s, ra);
+      if (launch_log() != nullptr) {
+        if (gc.dK == nullptr) record_launch<RefineBwdBody<T, DH, COMM_NSQ>>(rgrid, dim3(256), ra);
+        else launch_log()->unsupported = true;
+      } else if (gc.dK == nullptr) {
+        hipLaunchKernelGGL((k_refine_bwd<T, DH, COMM_NSQ>), rgrid, dim3(256), 0, s, ra);
+      } else {
+        hipLaunchKernelGGL((k_refine_bwd<T, DH, 1>), rgrid, dim3(256), 0, s, ra);
+      }
     }
     // dv_in = dv_ctx . W_vctx (mult family)
     if (mult) {
@@ -308,10 +317,17 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
       launch_gemm_splitk<T, 64, 64, 2, 2, sizeof(T) == 2 ? -DU_STAGES : 4>(
           SrcRows<T>{dctx + sw * NS * 4 * d, 4 * d, N}, SrcRows<T>{(const T*)w->w_sweep_t, 4 * d, d}, N, d,
           4 * d, S, ep, s);
-      hipLaunchKernelGGL((k_du_epi<T, DU_SPLIT>), dim3(cdiv(N, 16), d / DU_EPI_TN), dim3(256), 0, s, N, d, h,
-                         inv_d, c->rms_eps, (const float*)ws.du_part, mult ? (const float*)ws.lamdv : nullptr,
-                         (const T*)(sv.o + sw * NS * d), (const float*)(sv.ssq + sw * NS * h),
-                         (const T*)w->norm_ctx_w, ws.gw, ws.rowdot, ws.dnw);
+      const typename DuEpiBody<T, DU_SPLIT>::Args ea{N, d, h, inv_d, c->rms_eps, (const float*)ws.du_part,
+                                                     mult ? (const float*)ws.lamdv : nullptr,
+                                                     (const T*)(sv.o + sw * NS * d),
+                                                     (const float*)(sv.ssq + sw * NS * h), (const T*)w->norm_ctx_w,
+                                                     ws.gw, ws.rowdot, ws.dnw};
+      const dim3 egrid(cdiv(N, 16), d / DU_EPI_TN);
+      if (launch_log() != nullptr)
+        record_launch<DuEpiBody<T, DU_SPLIT>>(egrid, dim3(256), ea);
+      else
+        hipLaunchKernelGGL((k_du_epi<T, DU_SPLIT>), egrid, dim3(256), 0, s, ea.M, ea.d, ea.h, ea.inv_d, ea.eps, ea.part,
+                           ea.lamdv, ea.o, ea.ssq, ea.normw, ea.gw, ea.rowdot, ea.dnw);
     }
     // attention VJP of sweep sw
     {
@@ -325,7 +341,10 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
                         sw == K - 1 ? 1 : 0,
                         scale, inv_d, c->rms_eps, ws.dkself, ws.dvraw, ws.dq, sw >= 1 ? 1 : 0,
                         sw >= 1 ? refine_args(sw - 1) : RefineBwdArgs<T>{}};
-      hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(2, BH), dim3(256), lds_attn, s, aa);
+      if (launch_log() != nullptr)
+        record_launch<AttnBwdBody<T, DH>>(dim3(2, BH), dim3(256), aa, (unsigned)lds_attn);
+      else
+        hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(2, BH), dim3(256), lds_attn, s, aa);
     }
   }
   // the other operand of dW_sweep = dctx^T u: this cell's K*N rows of u = RMSNorm(o)
@@ -335,13 +354,19 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
   const int rows = K * N;
   if (tape != nullptr && rms != nullptr) {
     rms->push_back(RmsSeg{sv.o, sv.ssq, coff, rows});
+  } else if (launch_log() != nullptr) {
+    record_launch<RmsRowsUBody<T>>(dim3(cdiv(rows, 4)), dim3(256),
+                                   typename RmsRowsUBody<T>::Args{(const T*)sv.o, rows, d, (const float*)sv.ssq, h,
+                                                                  (const T*)w->norm_ctx_w, inv_d, c->rms_eps,
+                                                                  ws.uL + coff * d});
   } else {
     hipLaunchKernelGGL(k_rms_rows<T>, dim3(cdiv(rows, 4)), dim3(256), 0, s, (const T*)sv.o, rows, d,
                        (const float*)sv.ssq, h, (const T*)w->norm_ctx_w, inv_d, c->rms_eps, ws.uL + coff * d);
   }
   // grad-cache path: the committed rows [0, pos0) this cell read get their grads now, key side
   // into the cache, query side into dq
-  if (gc.dK != nullptr && pos0 > 0) {
+  if (gc.dK != nullptr && pos0 > 0 && launch_log() != nullptr) launch_log()->unsupported = true;
+  else if (gc.dK != nullptr && pos0 > 0) {
     CommKeyArgs<T> ka{B, h, T_, cache_T, pos0, 0, pos0, pos0 + cc, qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow,
                       scale, nullptr, nullptr, gc.dK, gc.dV};
     hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(cdiv(pos0, 64), BH), dim3(256), lds_attn, s, ka);
@@ -350,6 +375,9 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
     hipLaunchKernelGGL((k_comm_dq<T, DH>), dim3(BH, cdiv(cc, 64)), dim3(256), lds_attn, s, qa);
   }
 }
+
+template <typename T, int DH>
+void unpack_grads(const dm_config* c, const dm_grads* gr, const BwdWs<T>& ws, hipStream_t s);
 
 template <typename T, int DH>
 void bwd_end(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T* dx, const float* cos,
@@ -411,7 +439,7 @@ void bwd_end(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T*
                      fusion ? 1 : 0,
                      (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself, (const float*)ws.dvraw,
                      (const float*)ws.dglogx, (const float*)ws.dsig, (const float*)L->sig, cos, sin, ws.dproj,
-                     ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart);
+                     ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, RowMap{}, PROJ_ROWS_OUT | PROJ_PARTIALS);
   hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks, 3 * d, 3 * d,
                      (const float*)ws.colpart, gr->b_gk, gr->b_gv, (mult && !fusion) ? gr->b_vgate : nullptr, d);
   // the head norms' gains: sums over rows of the partials
@@ -428,7 +456,28 @@ void bwd_end(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T*
     launch_gemm_big<T>(SrcRows<T>{ws.dproj, (long)nproj * d, BT},
                                       SrcRows<T>{(const T*)w->w_proj_t, (long)nproj * d, d}, BT, d, nproj * d, ep, s);
   }
-  // unpack the packed weight grads into the reference layout
+  unpack_grads<T, DH>(c, gr, ws, s);
+  // norm_ctx.weight
+  colsum_add(ws.dnw, cdiv(B * CMAX, NSLOT_TM), d, ws.colpart, gr->norm_ctx_w, s);
+  // attn_norm VJP + residual
+  if (norm) {
+    float* dwa_part = reinterpret_cast<float*>(ws.dproj);
+    hipLaunchKernelGGL(k_rmsnorm_bwd<T>, dim3(cdiv(BT, RMSN_ROWS)), dim3(256), 4 * d * sizeof(float), s, BT, d,
+                       c->rms_eps, residual ? 1 : 0, x, (const T*)w->attn_norm_w, (const float*)ws.dxhat, dy, dx,
+                       dwa_part, RowMap{}, 3);
+    colsum_add(dwa_part, cdiv(BT, RMSN_ROWS), d, ws.colpart, gr->attn_norm_w, s);
+  } else {
+    hipLaunchKernelGGL(k_dx_plain<T>, dim3(std::min(cdiv((long)BT * d, 256), 4096)), dim3(256), 0, s,
+                       (long)BT * d, residual ? 1 : 0, (const float*)ws.dxhat, dy, dx);
+  }
+}
+
+// the packed weight grads (dWp, dWs) added into the reference layout
+template <typename T, int DH>
+void unpack_grads(const dm_config* c, const dm_grads* gr, const BwdWs<T>& ws, hipStream_t s) {
+  const int d = c->d, h = c->h;
+  const bool mult = c->ctx_mod != DM_CTX_LINEAR;
+  const bool fusion = c->ctx_mod == DM_CTX_FUSION;
   {
     std::vector<UnpackSeg> u;
     u.push_back(UnpackSeg{gr->wq, d, 0, d, 0, 0});
@@ -462,19 +511,126 @@ void bwd_end(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T*
     }
     unpack(u, d, ws.dWs, s);
   }
-  // norm_ctx.weight
-  colsum_add(ws.dnw, cdiv(B * CMAX, NSLOT_TM), d, ws.colpart, gr->norm_ctx_w, s);
-  // attn_norm VJP + residual
-  if (norm) {
-    float* dwa_part = reinterpret_cast<float*>(ws.dproj);
-    hipLaunchKernelGGL(k_rmsnorm_bwd<T>, dim3(cdiv(BT, RMSN_ROWS)), dim3(256), 4 * d * sizeof(float), s, BT, d,
-                       c->rms_eps, residual ? 1 : 0, x, (const T*)w->attn_norm_w, (const float*)ws.dxhat, dy, dx,
-                       dwa_part);
-    colsum_add(dwa_part, cdiv(BT, RMSN_ROWS), d, ws.colpart, gr->attn_norm_w, s);
-  } else {
-    hipLaunchKernelGGL(k_dx_plain<T>, dim3(std::min(cdiv((long)BT * d, 256), 4096)), dim3(256), 0, s,
-                       (long)BT * d, residual ? 1 : 0, (const float*)ws.dxhat, dy, dx);
+}
+
+// ---- the layer-batched (wavefront) backward of a stack ---------------------------------------
+// Per layer and cell the same kernels as bwd_begin / bwd_cell / bwd_end, restricted to the cell's
+// rows: the cell's do_cat rows, its sweeps, then the tail that makes its dx rows final (the
+// committed-prefix query VJP of its rows, the projection VJP rows, dxhat, the attn_norm VJP with
+// the residual). A layer's sums over all rows (weight grads, bias / gain / norm-weight partials)
+// run once its last cell (cell 0) is done.
+
+constexpr int PROJ_ROWS_CHUNK = 8;   // rows per block of a cell's projection VJP rows (no partials)
+
+template <typename T, int DH>
+void record_bwd_chunk(const dm_config* c, const dm_stack_bwd_layer& ly, const float* cos, const float* sin,
+                      const int32_t* sched, int n_cells, int ci, int cache_T, const size_t* toff, const BwdWs<T>& ws,
+                      std::vector<RmsSeg>* rms) {
+  const dm_packed* w = ly.w;
+  const dm_layer_bufs* L = ly.bufs;
+  const int B = c->B, d = c->d, h = c->h, T_ = L->T, BH = B * h;
+  const int pos0 = sched[3 * ci], cc = sched[3 * ci + 1];
+  const int N = B * cc, lc = log2_exact(cc);
+  const RowMap map{lc, T_, pos0};
+  const int nproj = c->ctx_mod == DM_CTX_LINEAR ? 5 : 6;
+  const T* dy = (const T*)ly.dy;
+  const T* Kc = (const T*)ly.K_cache;
+  const T* Vc = (const T*)ly.V_cache;
+  // do_cat rows of the cell: dy . W_O
+  {
+    EpiStoreTileF32 ep{N, d, ws.docat, 0, map};
+    launch_gemm_auto<T, 64, 64, 2, 2, 3, 4>(SrcChunkRows<T>{dy, d, N, lc, T_, pos0},
+                                            SrcRows<T>{(const T*)w->wo_t, d, d}, N, d, d, ep, nullptr);
   }
+  bwd_cell<T, DH>(c, w, cos, sin, L, sched, n_cells, ci, Kc, Vc, cache_T, (const char*)ly.tape, toff, GradCache{}, ws,
+                  rms, nullptr);
+  // committed-prefix VJP, query side, of the cell's rows
+  const size_t lds_attn = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
+  const float scale = 1.0f / sqrtf((float)DH);
+  CommQueryArgs<T> qa{B, h, T_, cache_T, pos0 + cc, ws.klim, (const T*)L->qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow,
+                      scale, ws.dq, pos0};
+  record_launch<CommDqBody<T, DH>>(dim3(BH, cdiv(cc, 64)), dim3(256), qa, (unsigned)lds_attn);
+  // projection VJP of the cell's rows (the column partials come with the layer's close)
+  typename ProjBwdBody<T, DH>::Args pa{N, T_, d, h, nproj, c->ctx_mod == DM_CTX_FUSION ? 1 : 0, ws.dq, ws.dkraw,
+                                       ws.dkself, ws.dvraw, ws.dglogx, ws.dsig, L->sig, cos, sin, ws.dproj,
+                                       ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, map, PROJ_ROWS_OUT,
+                                       PROJ_ROWS_CHUNK};
+  record_launch<ProjBwdBody<T, DH>>(dim3(cdiv(d / 2, 256), cdiv(N, PROJ_ROWS_CHUNK)), dim3(256), pa);
+  // dxhat rows = d_proj rows . W_proj
+  {
+    EpiStoreTileF32 ex{N, d, ws.dxhat, 0, map};
+    launch_gemm_auto<T, 64, 64, 2, 2, 3, 4>(SrcChunkRows<T>{ws.dproj, (long)nproj * d, N, lc, T_, pos0},
+                                            SrcRows<T>{(const T*)w->w_proj_t, (long)nproj * d, d}, N, d, nproj * d,
+                                            ex, nullptr);
+  }
+  // attn_norm VJP + residual: the cell's dx rows (the norm weight's partials with the close)
+  typename RmsnormBwdBody<T>::Args ra{N, d, c->rms_eps, (c->flags & DM_FLAG_NO_RESIDUAL) ? 0 : 1, (const T*)ly.x,
+                                      (const T*)w->attn_norm_w, ws.dxhat, dy, (T*)ly.dx, nullptr, map, 1};
+  record_launch<RmsnormBwdBody<T>>(dim3(cdiv(N, RMSN_ROWS)), dim3(256), ra, (unsigned)(4 * d * sizeof(float)));
+}
+
+// The layer's close once every cell is done (direct launches): the sweep weight grads, dW_O, the
+// column sums of the bias / gain / norm-weight partials, dW_proj, the unpack into the reference
+// layout — bwd_begin's and bwd_end's all-row work, in bwd_end's order.
+template <typename T, int DH>
+void bwd_stack_close(const dm_config* c, const dm_stack_bwd_layer& ly, const float* cos, const float* sin,
+                     const int32_t* sched, int n_cells, const size_t* toff, const std::vector<RmsSeg>& rms,
+                     const BwdWs<T>& ws, hipStream_t s) {
+  const dm_packed* w = ly.w;
+  const dm_layer_bufs* L = ly.bufs;
+  const dm_grads* gr = ly.grads;
+  const int B = c->B, d = c->d, h = c->h, T_ = L->T, BT = B * T_;
+  const bool mult = c->ctx_mod != DM_CTX_LINEAR;
+  const int nproj = mult ? 6 : 5;
+  const float inv_d = 1.0f / (float)d;
+  T* vinS = stacked_vin<T>((const char*)ly.tape, toff, n_cells, ws);
+  const long coff = vin_row(c, sched, n_cells, -1);
+  gemm_tn<T>((const T*)ly.dy, d, (const T*)ly.ocat, d, gr->wo, d, d, BT, 1, ws.kpart, s);
+  for (size_t i0 = 0; i0 < rms.size(); i0 += RMS_MAX_SEG) {
+    RmsSegs ra{};
+    ra.nseg = (int)std::min<size_t>(RMS_MAX_SEG, rms.size() - i0);
+    int most = 0;
+    for (int i = 0; i < ra.nseg; ++i) {
+      ra.seg[i] = rms[i0 + i];
+      most = std::max(most, ra.seg[i].rows);
+    }
+    hipLaunchKernelGGL(k_rms_rows_multi<T>, dim3(cdiv(most, 4), ra.nseg), dim3(256), 0, s, ra, d, h,
+                       (const T*)w->norm_ctx_w, inv_d, c->rms_eps, ws.uL);
+  }
+  {
+    const int Kp = (int)(cdiv(coff, 64) * 64);
+    if (Kp > coff) {
+      auto words = [&](size_t cols) { return (size_t)(Kp - coff) * cols * sizeof(T) / 4; };
+      fill0_list({{reinterpret_cast<float*>(ws.dctxL + coff * 4 * d), words(4 * (size_t)d)},
+                  {reinterpret_cast<float*>(ws.uL + coff * d), words(d)},
+                  {reinterpret_cast<float*>(ws.dvcL + coff * d), words(d)},
+                  {reinterpret_cast<float*>(vinS + coff * d), mult ? words(d) : 0}},
+                 s);
+    }
+    gemm_tn<T>(ws.dctxL, 4 * d, ws.uL, d, ws.dWs, 4 * d, d, Kp, 1, ws.kpart, s);
+    if (mult) gemm_tn<T>(ws.dvcL, d, vinS, d, gr->w_vctx, d, d, Kp, 1, ws.kpart, s);
+  }
+  const int pchunks = cdiv(BT, PROJ_ROWS);
+  const bool fusion = c->ctx_mod == DM_CTX_FUSION;
+  hipLaunchKernelGGL((k_proj_bwd<T, DH>), dim3(cdiv(d / 2, 256), pchunks), dim3(256), 0, s, BT, T_, d, h, nproj,
+                     fusion ? 1 : 0, (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself,
+                     (const float*)ws.dvraw, (const float*)ws.dglogx, (const float*)ws.dsig, (const float*)L->sig, cos,
+                     sin, ws.dproj, ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, RowMap{}, PROJ_PARTIALS);
+  hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks, 3 * d, 3 * d,
+                     (const float*)ws.colpart, gr->b_gk, gr->b_gv, (mult && !fusion) ? gr->b_vgate : nullptr, d);
+  if (ws.vgpart)
+    hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(h, 64)), dim3(256), 0, s, pchunks, h, h, (const float*)ws.vgpart,
+                       gr->v_gain, (float*)nullptr, (float*)nullptr, h);
+  if (ws.dkg) colsum_add(ws.dkg, BT, h, ws.colpart, gr->k_gain, s);
+  if (ws.dvg) colsum_add(ws.dvg, BT, h, ws.colpart, gr->ctx_gain, s);
+  gemm_tn<T>(ws.dproj, (long)nproj * d, (const T*)L->xhat, d, ws.dWp, nproj * d, d, BT, 0, ws.kpart, s);
+  unpack_grads<T, DH>(c, gr, ws, s);
+  colsum_add(ws.dnw, cdiv(B * CMAX, NSLOT_TM), d, ws.colpart, gr->norm_ctx_w, s);
+  float* dwa_part = reinterpret_cast<float*>(ws.dproj);
+  hipLaunchKernelGGL(k_rmsnorm_bwd<T>, dim3(cdiv(BT, RMSN_ROWS)), dim3(256), 4 * d * sizeof(float), s, BT, d,
+                     c->rms_eps, 0, (const T*)ly.x, (const T*)w->attn_norm_w, (const float*)ws.dxhat, (const T*)nullptr,
+                     (T*)nullptr, dwa_part, RowMap{}, 2);
+  colsum_add(dwa_part, cdiv(BT, RMSN_ROWS), d, ws.colpart, gr->attn_norm_w, s);
 }
 
 // which part of the layer backward an entry point runs
@@ -602,6 +758,105 @@ int run_bwd(const dm_config* c, const dm_packed* w, const BwdCall& call, void* s
   DM_HIP(hipGetLastError());
   return DM_OK;
 }
+// The layer-batched backward: checks, then (bytes != nullptr) the plan size, or the run: the
+// accumulators of every layer zeroed, then per step the grouped launches of every active layer's
+// cell and the close of each layer whose cell 0 that step finished.
+int run_stack_bwd(const dm_config* c, int nl, const dm_stack_bwd_layer* layers, const float* cos, const float* sin,
+                  const int32_t* sched, int n_cells, int cache_T, void* plan, size_t plan_bytes, int build,
+                  void* stream, size_t* bytes) {
+  DM_REQUIRE(nl >= 1 && layers != nullptr, DM_ERR_INVALID, "n_layers=%d", nl);
+  int kmax = 0;
+  for (int l = 0; l < nl; ++l) {
+    const dm_stack_bwd_layer& ly = layers[l];
+    int rc = check_bwd_common(c, ly.w, ly.bufs, sched, n_cells, cache_T, ly.workspace, ly.workspace_bytes, &kmax);
+    if (rc) return rc;
+    if ((rc = check_grads(c, ly.w, ly.bufs, ly.grads))) return rc;
+    DM_REQUIRE(ly.x && ly.dy && ly.dx && ly.K_cache && ly.V_cache && ly.ocat, DM_ERR_INVALID,
+               "layer %d: null backward argument", l);
+    DM_REQUIRE(ly.w->attn_norm_w != nullptr, DM_ERR_UNSUPPORTED, "the layer-batched backward needs attn_norm");
+    DM_REQUIRE(ly.bufs->T == layers[0].bufs->T, DM_ERR_INVALID, "layer %d: T differs", l);
+    DM_REQUIRE((ly.tape != nullptr) == (layers[0].tape != nullptr), DM_ERR_INVALID,
+               "layer %d: all layers with a tape or none", l);
+  }
+  for (int i = 0; i < n_cells; ++i)
+    DM_REQUIRE(sched[3 * i + 1] == sched[1] && sched[3 * i + 2] == sched[2], DM_ERR_UNSUPPORTED,
+               "the layer-batched backward needs equal cells");
+  DM_REQUIRE(log2_exact(sched[1]) >= 0, DM_ERR_UNSUPPORTED, "cell length %d is not a power of two", sched[1]);
+  hipStream_t s = S(stream);
+  auto run = [&](auto tt, auto dh_tag) -> int {
+    using T = decltype(tt);
+    constexpr int DH = decltype(dh_tag)::value;
+    std::vector<size_t> toff;
+    const bool tape = layers[0].tape != nullptr;
+    if (tape) {
+      toff = tape_offsets<T>(c, sched, n_cells);
+      for (int l = 0; l < nl; ++l)
+        DM_REQUIRE(layers[l].tape_bytes >= toff[n_cells + 1] && aligned16(layers[l].tape), DM_ERR_WORKSPACE,
+                   "layer %d: tape %zu < %zu bytes", l, layers[l].tape_bytes, toff[n_cells + 1]);
+    }
+    const size_t* to = tape ? toff.data() : nullptr;
+    std::vector<BwdWs<T>> ws;
+    for (int l = 0; l < nl; ++l) ws.push_back(carve_bwd<T>(c, layers[l].bufs->T, cache_T, kmax, layers[l].workspace));
+    std::vector<std::vector<RmsSeg>> rms(nl);
+    std::vector<GroupedLaunch> prog;
+    std::vector<unsigned char> tab;
+    size_t off = 0;
+    std::vector<LaunchLog> logs;
+    // layer l takes cell n_cells - 1 - (t - (nl - 1 - l)) at step t (the top layer first)
+    for (int t = 0; t < n_cells + nl - 1; ++t) {
+      const int la = std::max(0, nl - 1 - t), lb = std::min(nl - 1, nl - 1 - t + n_cells - 1);
+      logs.assign(lb - la + 1, LaunchLog{});
+      for (int l = lb; l >= la; --l) {
+        const int ci = n_cells - 1 - (t - (nl - 1 - l));
+        launch_log() = &logs[lb - l];
+        record_bwd_chunk<T, DH>(c, layers[l], cos, sin, sched, n_cells, ci, cache_T, to, ws[l],
+                                tape ? &rms[l] : nullptr);
+        launch_log() = nullptr;
+      }
+      const int rc = merge_step(t, logs, prog, (build && bytes == nullptr) ? &tab : nullptr, off);
+      if (rc) return rc;
+      for (int l = lb; l >= la; --l)
+        if (n_cells - 1 - (t - (nl - 1 - l)) == 0) prog.push_back(GroupedLaunch{nullptr, dim3(), dim3(), 0, 0, l});
+    }
+    if (bytes != nullptr) {
+      *bytes = off;
+      return DM_OK;
+    }
+    DM_REQUIRE(plan_bytes >= off, DM_ERR_WORKSPACE, "plan %zu < %zu bytes", plan_bytes, off);
+    if (build) DM_HIP(hipMemcpy(plan, tab.data(), off, hipMemcpyHostToDevice));
+    // every layer's accumulators (as bwd_begin)
+    for (int l = 0; l < nl; ++l) {
+      const BwdWs<T>& w = ws[l];
+      const size_t BT = (size_t)c->B * layers[l].bufs->T, d = c->d;
+      fill0_list({{w.dq, BT * d},
+                  {w.dkraw, BT * d},
+                  {w.dkself, BT * d},
+                  {w.dvraw, BT * d},
+                  {w.dglogx, BT * 2 * d},
+                  {w.dsig, BT * d},
+                  {w.dnw, (size_t)cdiv(c->B * CMAX, NSLOT_TM) * d},
+                  {w.dWs, 4 * d * d},
+                  {w.dkg, w.dkg ? BT * c->h : 0},
+                  {w.dvg, w.dvg ? BT * c->h : 0}},
+                 s);
+    }
+    for (const GroupedLaunch& g : prog) {
+      if (g.layer_end >= 0) {
+        const int l = g.layer_end;
+        bwd_stack_close<T, DH>(c, layers[l], cos, sin, sched, n_cells, to, rms[l], ws[l], s);
+      } else {
+        const int rc = issue_grouped(g, plan, s);
+        if (rc) return rc;
+      }
+    }
+    DM_HIP(hipGetLastError());
+    return DM_OK;
+  };
+  if (c->dtype == DM_BF16)
+    return c->dh == 64 ? run(bf16{}, std::integral_constant<int, 64>{}) : run(bf16{}, std::integral_constant<int, 128>{});
+  return c->dh == 64 ? run(float{}, std::integral_constant<int, 64>{}) : run(float{}, std::integral_constant<int, 128>{});
+}
+
 }  // namespace dm
 
 extern "C" {
@@ -649,6 +904,24 @@ int dm_cell_bwd(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, 
                a->V_cache, a->cache_T, a->tape, a->tape_bytes, GradCache{a->dK_gc, a->dV_gc}, nullptr,
                a->workspace, kmax};
   return run_bwd(c, w, call, stream);
+}
+
+size_t dm_stack_bwd_plan_bytes(const dm_config* c, int32_t n_layers, const dm_stack_bwd_layer* layers,
+                               const int32_t* sched, int32_t n_cells, int32_t cache_T) {
+  size_t bytes = 0;
+  if (run_stack_bwd(c, n_layers, layers, nullptr, nullptr, sched, n_cells, cache_T, nullptr, 0, 0, nullptr, &bytes))
+    return 0;
+  return bytes;
+}
+
+int dm_stack_bwd(const dm_config* c, int32_t n_layers, const dm_stack_bwd_layer* layers, const float* cos,
+                 const float* sin, const int32_t* sched, int32_t n_cells, int32_t cache_T, void* plan,
+                 size_t plan_bytes, int32_t build, void* stream) {
+  DM_REQUIRE(cos && sin, DM_ERR_INVALID, "null rope tables");
+  DM_REQUIRE(plan != nullptr && (reinterpret_cast<uintptr_t>(plan) & 255) == 0, DM_ERR_INVALID,
+             "plan must be non-null and 256-byte aligned");
+  return run_stack_bwd(c, n_layers, layers, cos, sin, sched, n_cells, cache_T, plan, plan_bytes, build, stream,
+                       nullptr);
 }
 
 int dm_layer_bwd_end(const dm_config* c, const dm_packed* w, const void* x, const void* dy, void* dx,

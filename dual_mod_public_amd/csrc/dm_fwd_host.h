@@ -164,7 +164,8 @@ template <typename T, int DH>
 void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N, const T* o, const float* ssq,
                 const T* kraw, const T* vraw, const float* glogx, const float* sig, const float* cos,
                 const float* sin, T* Kout, T* Vout, long out_stride, int out_row0, T* vin, float* gvu,
-                T* save1, T* save2, hipStream_t s, const AttendArgs<T>* next_attend = nullptr) {
+                T* save1, T* save2, hipStream_t s, const AttendArgs<T>* next_attend = nullptr,
+                bool wide = false) {
   const T* normw = (const T*)w->norm_ctx_w;
   SrcRowsRs<T> sa{o, c->d, N, ssq, c->h, 1.0f / (float)c->d, c->rms_eps};
   SrcRows<T> sb{(const T*)w->w_sweep, c->d, 4 * c->d};
@@ -180,6 +181,12 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
       launch_gemm_auto<T, 64, 2 * DH, 2, 2, SW1_STAGES, 4>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
     else
       launch_gemm_auto<T, 64, 2 * DH, 1, 4, SW1_STAGES, 2>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
+  } else if (wide) {
+    // 64 x 128 blocks (two column groups each): a quarter less LDS traffic per MFMA and half the
+    // o re-reads, for launches that have blocks to spare (the layer-batched forward)
+    EpiSweep1<T, DH, 2> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
+                           Kout, Vout, out_stride, out_row0, vin, gvu, save1};
+    launch_gemm_auto<T, 64, 128, 2, 2, SW1_STAGES, 4>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
   } else {
     EpiSweep1<T, DH> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
                         Kout, Vout, out_stride, out_row0, vin, gvu, save1};
@@ -271,7 +278,7 @@ template <typename T, int DH>
 void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const float* cos,
               const float* sin, int pos0, int cc, int n_sweeps, int buf_t0, int Tbuf, T* Kc, T* Vc,
               int cache_T, T* ocat, float* o_last, const CellWs& ws, const CellSave<T>* sv, hipStream_t s,
-              const CellRows<T>& rows = CellRows<T>{}) {
+              const CellRows<T>& rows = CellRows<T>{}, bool wide = false) {
   CellGeom g{c->B, cc, c->d, c->h, DH, pos0, buf_t0, Tbuf, cache_T};
   g.kmod_cols = c->kmod_vraw_heads * DH;
   g.kmod_mode = c->kmod_mode;
@@ -341,7 +348,7 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
     const AttendArgs<T> next = attend_args(last ? sw : sw + 1);
     run_refine<T, DH>(c, w, g, N, o, ssq, kraw, vraw, L->glogx, L->sig, cos, sin, Kout, Vout, out_stride,
                       out_row0, vin, ws.gvu, sv ? sv->save1 + sw * NS * 4 * d : nullptr,
-                      sv ? sv->save2 + sw * NS * d : nullptr, s, (fuse && !last) ? &next : nullptr);
+                      sv ? sv->save2 + sw * NS * d : nullptr, s, (fuse && !last) ? &next : nullptr, wide);
   }
 }
 

@@ -675,6 +675,22 @@ __global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint
   prof_end(prof_ts, t0);
 }
 
+// a split-K k_gemm as a grouped-launch body: slice z of S in grid rows [z * mt, (z + 1) * mt)
+template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
+struct SplitGemmBody {
+  static constexpr int THREADS = 256;
+  struct Args {
+    SA sa;
+    SB sb;
+    int K;   // per slice
+    EPI epi;
+    int mt;  // row tiles
+  };
+  static DM_DEV void run(const Args& a, int bx, int by) {
+    gemm_block<T, BM, BN, WM, WN, D, SA, SB, EPI>(a.sa, a.sb, a.K, a.epi, bx, by % a.mt, by / a.mt);
+  }
+};
+
 // k_gemm as a grouped-launch body (one split-K slice)
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
 struct GemmBody {

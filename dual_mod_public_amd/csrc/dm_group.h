@@ -15,14 +15,24 @@
 
 namespace dm {
 
+// Body::MIN_WAVES (optional): the waves per SIMD the kernel is built for (register budget)
+template <class Body, class = void> struct min_waves_of {
+  static constexpr int value = 1;
+};
+template <class Body> struct min_waves_of<Body, decltype(void(Body::MIN_WAVES))> {
+  static constexpr int value = Body::MIN_WAVES;
+};
+
 template <class Body>
-__global__ __launch_bounds__(Body::THREADS) void k_grouped(const typename Body::Args* __restrict__ tab) {
+__global__ __launch_bounds__(Body::THREADS, min_waves_of<Body>::value) void k_grouped(
+    const typename Body::Args* __restrict__ tab) {
   Body::run(tab[blockIdx.z], (int)blockIdx.x, (int)blockIdx.y);
 }
 
 struct LaunchRec {
   const void* gfunc;   // k_grouped<Body>
   dim3 grid, block;    // grid.x of this argument set (0: nothing to do for it), grid.y, block
+  unsigned shmem;      // dynamic LDS bytes
   size_t args_bytes;
   std::vector<unsigned char> args;
 };
@@ -37,11 +47,12 @@ inline LaunchLog*& launch_log() {
 }
 
 template <class Body>
-inline void record_launch(dim3 grid, dim3 block, const typename Body::Args& a) {
+inline void record_launch(dim3 grid, dim3 block, const typename Body::Args& a, unsigned shmem = 0) {
   LaunchRec r;
   r.gfunc = reinterpret_cast<const void*>(&k_grouped<Body>);
   r.grid = grid;
   r.block = block;
+  r.shmem = shmem;
   r.args_bytes = sizeof(a);
   r.args.resize(sizeof(a));
   std::memcpy(r.args.data(), &a, sizeof(a));

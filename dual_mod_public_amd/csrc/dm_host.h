@@ -2,10 +2,12 @@
 // error reporting, argument checks, launch helpers, workspace carving.
 #pragma once
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "../../include/dm_abi.h"
 #include "dm_kernels.h"
@@ -135,6 +137,64 @@ struct Carver {
   }
 };
 
+// ---- grouped launches of the layer-batched stack passes ------------------------------
+// One grouped launch (argument table at plan + off), or the per-layer closing work of
+// layer `layer_end` (issued directly, not grouped).
+struct GroupedLaunch {
+  const void* f;
+  dim3 grid, block;
+  unsigned shmem;
+  size_t off;
+  int layer_end;
+};
+
+// Lines one step's per-layer records up position by position into grouped launches (their
+// argument tables appended to tab when non-null, at 256-byte aligned offsets from off).
+inline int merge_step(int t, const std::vector<LaunchLog>& logs, std::vector<GroupedLaunch>& out,
+                      std::vector<unsigned char>* tab, size_t& off) {
+  for (const LaunchLog& lg : logs)
+    DM_REQUIRE(!lg.unsupported, DM_ERR_UNSUPPORTED, "step %d: a launch has no grouped form", t);
+  const size_t n = logs[0].recs.size();
+  for (const LaunchLog& lg : logs)
+    DM_REQUIRE(lg.recs.size() == n, DM_ERR_UNSUPPORTED, "step %d: layers record %zu and %zu launches", t,
+               lg.recs.size(), n);
+  const int G = (int)logs.size();
+  for (size_t r = 0; r < n; ++r) {
+    const LaunchRec& r0 = logs[0].recs[r];
+    unsigned gx = 0;
+    for (const LaunchLog& lg : logs) {
+      const LaunchRec& x = lg.recs[r];
+      DM_REQUIRE(x.gfunc == r0.gfunc && x.grid.y == r0.grid.y && x.block.x == r0.block.x &&
+                     x.shmem == r0.shmem && x.args_bytes == r0.args_bytes,
+                 DM_ERR_UNSUPPORTED, "step %d, launch %zu differs between layers", t, r);
+      gx = std::max(gx, x.grid.x);
+    }
+    if (gx == 0) continue;   // nothing to do for any layer
+    off = (off + 255) / 256 * 256;
+    out.push_back(GroupedLaunch{r0.gfunc, dim3(gx, r0.grid.y, G), r0.block, r0.shmem, off, -1});
+    if (tab != nullptr) {
+      tab->resize(off + (size_t)G * r0.args_bytes);
+      for (int g = 0; g < G; ++g)
+        std::memcpy(tab->data() + off + (size_t)g * r0.args_bytes, logs[g].recs[r].args.data(), r0.args_bytes);
+    }
+    off += (size_t)G * r0.args_bytes;
+  }
+  return DM_OK;
+}
+
+inline int issue_grouped(const GroupedLaunch& g, void* plan, hipStream_t s) {
+  void* p = static_cast<char*>(plan) + g.off;
+  void* args[] = {&p};
+  DM_HIP(hipLaunchKernel(g.f, g.grid, g.block, args, g.shmem, s));
+  return DM_OK;
+}
+
+inline int log2_exact(int v) {
+  int l = 0;
+  while ((1 << l) < v) ++l;
+  return (1 << l) == v ? l : -1;
+}
+
 // GEMM launch: grid (N/BN, ceil(M/BM)), 256 threads
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
 void launch_gemm(const SA& sa, const SB& sb, int M, int N, int K, const EPI& epi, hipStream_t s,
@@ -205,8 +265,9 @@ template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB,
 void launch_gemm_splitk(const SA& sa, const SB& sb, int M, int N, int K, int S, const EPI& epi, hipStream_t s,
                         int prof_cls = PROF_NONE) {
   dim3 grid(N / BN, cdiv(M, BM), S);
-  if (launch_log() != nullptr) {   // split-K slices use grid z: no grouped form
-    launch_log()->unsupported = true;
+  if (launch_log() != nullptr) {   // grouped: the slices stacked along grid y
+    using Body = SplitGemmBody<T, BM, BN, WM, WN, D, SA, SB, EPI>;
+    record_launch<Body>(dim3(N / BN, cdiv(M, BM) * S), dim3(256), typename Body::Args{sa, sb, K / S, epi, cdiv(M, BM)});
     return;
   }
   uint64_t* ts;

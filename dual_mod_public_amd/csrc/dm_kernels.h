@@ -75,10 +75,8 @@ static __global__ __launch_bounds__(256) void k_scale_cols(T* __restrict__ W, co
 // u rows of the sweep weight grads: out[r] = o[r] * rsqrt(sum_p ssq[r, p] * inv_d + eps) * w
 // (the RMSNorm the sweep GEMM applied), one wave per row, 16-byte vectors.
 template <typename T>
-static __global__ __launch_bounds__(256) void k_rms_rows(const T* __restrict__ o, int rows, int cols,
-                                                         const float* __restrict__ ssq, int nparts,
-                                                         const T* __restrict__ w, float inv_d, float eps,
-                                                         T* __restrict__ out) {
+DM_DEV void rms_rows_body(const T* __restrict__ o, int rows, int cols, const float* __restrict__ ssq, int nparts,
+                          const T* __restrict__ w, float inv_d, float eps, T* __restrict__ out) {
   constexpr int V = 16 / (int)sizeof(T);
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -93,6 +91,30 @@ static __global__ __launch_bounds__(256) void k_rms_rows(const T* __restrict__ o
     *reinterpret_cast<uint4*>(out + (long)r * cols + c) = pack16<T>(f);
   }
 }
+
+template <typename T>
+static __global__ __launch_bounds__(256) void k_rms_rows(const T* __restrict__ o, int rows, int cols,
+                                                         const float* __restrict__ ssq, int nparts,
+                                                         const T* __restrict__ w, float inv_d, float eps,
+                                                         T* __restrict__ out) {
+  rms_rows_body<T>(o, rows, cols, ssq, nparts, w, inv_d, eps, out);
+}
+
+template <typename T> struct RmsRowsUBody {
+  static constexpr int THREADS = 256;
+  struct Args {
+    const T* o;
+    int rows, cols;
+    const float* ssq;
+    int nparts;
+    const T* w;
+    float inv_d, eps;
+    T* out;
+  };
+  static DM_DEV void run(const Args& a, int, int) {
+    rms_rows_body<T>(a.o, a.rows, a.cols, a.ssq, a.nparts, a.w, a.inv_d, a.eps, a.out);
+  }
+};
 
 
 
@@ -1237,6 +1259,7 @@ struct EpiStoreTileF32 {
   int M, N;
   float* __restrict__ C;
   long zstride;
+  RowMap map = RowMap{};   // output row of GEMM row m
   struct TilePre {};
   DM_DEV TilePre tile_prefetch(int, int) const { return TilePre{}; }
   template <int TR, int BN, int LDT>
@@ -1248,7 +1271,7 @@ struct EpiStoreTileF32 {
     for (int it = 0; it < NV / 256; ++it) {
       const int idx = it * 256 + threadIdx.x, r = idx / C4, c = 4 * (idx % C4);
       const floatx4 v = *reinterpret_cast<const floatx4*>(tile + r * LDT + c);
-      if (m0 + r < M) *reinterpret_cast<floatx4*>(C + (long)(m0 + r) * N + n0 + c) = v;
+      if (m0 + r < M) *reinterpret_cast<floatx4*>(C + map(m0 + r) * N + n0 + c) = v;
     }
   }
 };

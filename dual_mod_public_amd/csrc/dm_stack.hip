@@ -18,12 +18,6 @@
 namespace dm {
 namespace {
 
-int log2_exact(int v) {
-  int l = 0;
-  while ((1 << l) < v) ++l;
-  return (1 << l) == v ? l : -1;
-}
-
 // One layer's cell i, recorded: the same kernels and arguments as dm_layer_fwd's projection,
 // cell and W_O, restricted to the chunk's rows.
 template <typename T, int DH>
@@ -51,7 +45,7 @@ void record_chunk(const dm_config* c, const dm_stack_layer& ly, const float* cos
   const T* o_last;
   if (ly.tape == nullptr) {
     run_cell<T, DH>(c, w, L, cos, sin, pos0, cc, K, pos0, L->T, (T*)ly.K_cache, (T*)ly.V_cache, cache_T,
-                    (T*)ly.ocat, nullptr, ws, nullptr, nullptr);
+                    (T*)ly.ocat, nullptr, ws, nullptr, nullptr, CellRows<T>{}, true);
     o_last = (const T*)ws.o;
   } else {
     Carver cv(static_cast<char*>(ly.tape) + toff[i]);
@@ -61,7 +55,7 @@ void record_chunk(const dm_config* c, const dm_stack_layer& ly, const float* cos
     CellWs cws = ws;
     if (sv.Mx) cws.M = sv.Mx;
     run_cell<T, DH>(c, w, L, cos, sin, pos0, cc, K, pos0, L->T, (T*)ly.K_cache, (T*)ly.V_cache, cache_T,
-                    (T*)ly.ocat, nullptr, cws, &sv, nullptr);
+                    (T*)ly.ocat, nullptr, cws, &sv, nullptr, CellRows<T>{}, true);
     o_last = sv.o + (size_t)(K - 1) * M * d;
   }
   // W_O (+ the residual) of the chunk's rows: the last sweep's o holds the chunk's o_cat rows
@@ -74,12 +68,6 @@ void record_chunk(const dm_config* c, const dm_stack_layer& ly, const float* cos
   else
     launch_gemm<T, 64, 64, 2, 2, 4>(ao, bo, M, d, d, ep, nullptr);
 }
-
-struct GroupedLaunch {
-  const void* f;
-  dim3 grid, block;
-  size_t off;
-};
 
 // Records every step and lines the layers' launches up; fills `tab` (when non-null) with the
 // argument tables and returns the plan size in *bytes.
@@ -103,33 +91,9 @@ int plan_stack(const dm_config* c, int nl, const dm_stack_layer* layers, const f
         else record_chunk<float, 128>(c, layers[l], cos, sin, sched, n_cells, t - l, cache_T, toff);
       }
       launch_log() = nullptr;
-      DM_REQUIRE(!logs[l - la].unsupported, DM_ERR_UNSUPPORTED, "a launch of layer %d has no grouped form", l);
     }
-    const size_t n = logs[0].recs.size();
-    for (const LaunchLog& lg : logs)
-      DM_REQUIRE(lg.recs.size() == n, DM_ERR_UNSUPPORTED, "step %d: layers record %zu and %zu launches", t,
-                 lg.recs.size(), n);
-    const int G = (int)logs.size();
-    for (size_t r = 0; r < n; ++r) {
-      const LaunchRec& r0 = logs[0].recs[r];
-      unsigned gx = 0;
-      for (const LaunchLog& lg : logs) {
-        const LaunchRec& x = lg.recs[r];
-        DM_REQUIRE(x.gfunc == r0.gfunc && x.grid.y == r0.grid.y && x.block.x == r0.block.x &&
-                       x.args_bytes == r0.args_bytes,
-                   DM_ERR_UNSUPPORTED, "step %d, launch %zu differs between layers", t, r);
-        gx = std::max(gx, x.grid.x);
-      }
-      if (gx == 0) continue;   // nothing to do for any layer (no committed prefix yet)
-      off = (off + 255) / 256 * 256;
-      out.push_back(GroupedLaunch{r0.gfunc, dim3(gx, r0.grid.y, G), r0.block, off});
-      if (tab != nullptr) {
-        tab->resize(off + (size_t)G * r0.args_bytes);
-        for (int g = 0; g < G; ++g)
-          std::memcpy(tab->data() + off + (size_t)g * r0.args_bytes, logs[g].recs[r].args.data(), r0.args_bytes);
-      }
-      off += (size_t)G * r0.args_bytes;
-    }
+    const int rc = merge_step(t, logs, out, tab, off);
+    if (rc) return rc;
   }
   *bytes = off;
   return DM_OK;
@@ -234,11 +198,8 @@ int dm_stack_fwd(const dm_config* c, int32_t n_layers, const dm_stack_layer* lay
     pc.lists[plan] = launches;
   }
   hipStream_t s = S(stream);
-  for (const GroupedLaunch& g : launches) {
-    void* p = static_cast<char*>(plan) + g.off;
-    void* args[] = {&p};
-    DM_HIP(hipLaunchKernel(g.f, g.grid, g.block, args, 0, s));
-  }
+  for (const GroupedLaunch& g : launches)
+    if ((rc = issue_grouped(g, plan, s))) return rc;
   DM_HIP(hipGetLastError());
   return DM_OK;
 }

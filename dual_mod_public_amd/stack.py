@@ -24,10 +24,11 @@ from .engine import HipSweepCell, LayerGrads, _sched, uniform_chunks
 
 
 class HipLayerStack:
-    """wavefront=True runs the forward layer-batched (dm_stack_fwd, the schedule of
-    engines/wave3d/wave3d.py:1-47 on the chained chunk cells): layer l works on cell t - l at
-    step t and each kernel of a step is one launch over every active layer. Same results as
-    the layer-by-layer forward, bit for bit; it needs a schedule of equal cells."""
+    """wavefront=True runs the forward and the backward layer-batched (dm_stack_fwd /
+    dm_stack_bwd, the schedule of engines/wave3d/wave3d.py:1-47 on the chained chunk cells):
+    layer l works on cell t - l at step t (the backward: the top layer first, cells last
+    first) and each kernel of a step is one launch over every active layer. Same results as
+    the layer-by-layer step, bit for bit; it needs a schedule of equal cells."""
 
     def __init__(self, cfg, n_layers, B, T, schedule=None, device="cuda", dtype=torch.bfloat16, tape=True,
                  wavefront=False):
@@ -59,6 +60,7 @@ class HipLayerStack:
         self.graph = None
         self.wavefront = wavefront
         self._plan = None
+        self._bplan = None
 
     def load(self, state_dicts, cos, sin):
         """Pack every layer's weights (reference names, incl. attn_norm.weight) and the RoPE
@@ -108,14 +110,45 @@ class HipLayerStack:
                                      len(self.schedule), self.T, L.ptr(self._plan), self._plan.numel(), build,
                                      L.stream_ptr()))
 
+    def backward_wavefront(self):
+        """The layer-batched backward over the stack's buffers (dxs[L] -> dxs[0], the gradients
+        ADDED into the flat buffer); plan handling as forward_wavefront."""
+        conf = self.cells[0]._conf(True)
+        sched = _sched(self.schedule)
+        kmax = max(k for _, _, k in self.schedule)
+        self._bkeep = []
+        arr = (L.dm_stack_bwd_layer * self.L)()
+        for l, cell in enumerate(self.cells):
+            w, b, g = cell.w.struct(with_attn_norm=True), self.bufs[l].struct(), self.grads[l].struct()
+            self._bkeep += [w, b, g]
+            ws = cell._bwd_workspace(self.T, self.T, kmax)
+            a = arr[l]
+            a.w, a.bufs, a.grads = ctypes.addressof(w), ctypes.addressof(b), ctypes.addressof(g)
+            a.x, a.dy, a.dx = L.ptr(self.xs[l]), L.ptr(self.dxs[l + 1]), L.ptr(self.dxs[l])
+            a.K_cache, a.V_cache, a.ocat = L.ptr(self.K[l]), L.ptr(self.V[l]), L.ptr(self.ocat[l])
+            a.tape = L.ptr(self.tapes[l])
+            a.tape_bytes = 0 if self.tapes[l] is None else self.tapes[l].numel()
+            a.workspace, a.workspace_bytes = L.ptr(ws), ws.numel()
+        build = 0
+        if self._bplan is None:
+            n = L.lib().dm_stack_bwd_plan_bytes(ctypes.byref(conf), self.L, arr, sched, len(self.schedule), self.T)
+            if n == 0:
+                raise L.DMError("dm_stack_bwd_plan_bytes rejected the stack")
+            self._bplan = torch.empty(n, device=self.device, dtype=torch.uint8)
+            build = 1
+        L.check(L.lib().dm_stack_bwd(ctypes.byref(conf), self.L, arr, L.ptr(self.cos), L.ptr(self.sin), sched,
+                                     len(self.schedule), self.T, L.ptr(self._bplan), self._bplan.numel(), build,
+                                     L.stream_ptr()))
+
     def _run(self):
         self.flat.zero_()
         if self.wavefront:
             self.forward_wavefront()
-        else:
-            for l, cell in enumerate(self.cells):
-                cell.layer_forward(self.xs[l], self.xs[l + 1], self.cos, self.sin, self.schedule, self.K[l],
-                                   self.V[l], self.ocat[l], self.bufs[l], tape=self.tapes[l])
+            self.backward_wavefront()
+            return
+        for l, cell in enumerate(self.cells):
+            cell.layer_forward(self.xs[l], self.xs[l + 1], self.cos, self.sin, self.schedule, self.K[l],
+                               self.V[l], self.ocat[l], self.bufs[l], tape=self.tapes[l])
         for l in reversed(range(self.L)):
             self.cells[l].layer_backward(self.xs[l], self.dxs[l + 1], self.dxs[l], self.cos, self.sin, self.schedule,
                                          self.K[l], self.V[l], self.ocat[l], self.bufs[l], self.grads[l],

@@ -268,6 +268,33 @@ int dm_layer_bwd(const dm_config* cfg, const dm_packed* w, const void* x, const 
                  const void* ocat, const void* tape, size_t tape_bytes, const dm_grads* g,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- layer-batched (wavefront) backward of a stack ---------------------------------------
+ * The reverse of dm_stack_fwd: layer l takes its cells last first, the top layer leading, one
+ * cell per step (layer l's cell i needs dy rows of that cell, written by layer l + 1's cell i
+ * the step before); each kernel of a step is one launch over every active layer. Per layer the
+ * result is dm_layer_bwd's (tape or recompute as given), bit for bit: dx, and the gradients
+ * ADDED into grads. A cell's dx rows are made final right after its sweeps (its committed-prefix
+ * query VJP, projection VJP rows, dxhat rows, attn_norm VJP + residual); the sums over a layer's
+ * rows (weight grads, the bias / gain / norm-weight partials) run once its cell 0 is done.
+ * Layer l reads layers[l].dy (normally layers[l + 1].dx). Equal cells of a power-of-two length,
+ * attn_norm present. workspace: dm_layer_bwd_workspace_bytes(cfg, T, cache_T, n_sweeps) per
+ * layer. plan / build as dm_stack_fwd (the argument tables of the grouped launches). */
+typedef struct dm_stack_bwd_layer {
+  const dm_packed* w;
+  const dm_layer_bufs* bufs;
+  const void* x; const void* dy; void* dx;   /* [B, T, d] */
+  const void* K_cache; const void* V_cache;
+  const void* ocat;
+  const void* tape; size_t tape_bytes;
+  const dm_grads* grads;
+  void* workspace; size_t workspace_bytes;
+} dm_stack_bwd_layer;
+size_t dm_stack_bwd_plan_bytes(const dm_config* cfg, int32_t n_layers, const dm_stack_bwd_layer* layers,
+                               const int32_t* sched, int32_t n_cells, int32_t cache_T);
+int dm_stack_bwd(const dm_config* cfg, int32_t n_layers, const dm_stack_bwd_layer* layers, const float* cos,
+                 const float* sin, const int32_t* sched, int32_t n_cells, int32_t cache_T, void* plan,
+                 size_t plan_bytes, int32_t build, void* stream);
+
 /* ---- the same backward one cell at a time --------------------------------------------
  * The reference's engine drives the backward per cell (FusedSweepCell.layer_blockmlp_bwd,
  * cell_backward, layer_close: engines/wavescan/cells/fused_sweep.py:1557-1959, called from
