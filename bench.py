@@ -1,7 +1,7 @@
 """Benchmark of the Dual-Mod attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload fwdbwd|fwd|c4]
-                    [--no-cpu-baseline] [--no-decode] [--no-c4]
+                    [--no-cpu-baseline] [--no-decode] [--no-c4] [--no-stack] [--no-graph-decode]
 
 One step = one DM attention layer of the 340M shape (B=8, T=2048, d=1024,
 16 heads x 64, c=64, K=4 Jacobi sweeps chained over 32 chunks, bf16 storage /
@@ -19,7 +19,9 @@ timing starts.
 Prints ONE JSON line: the headline sweep throughput in tokens/s, the roofline of
 the dominant kernel (sweep GEMM 1) timed with HIP events stamped by its own launches inside a
 second pass of the timed steps, the path-level roofline, the config-4 K ladder (one
-layer of the d=2048 trunk, fwd+bwd for K in {1, 2, 4, 8}), the decode sub-benchmark
+layer of the d=2048 trunk, fwd+bwd for K in {1, 2, 4, 8}), an 8-layer stack of the same layer
+fwd+bwd layer by layer and layer-batched (wavefront), the 24-layer model's greedy decode
+through the one-graph-per-token decoder against the eager one, the decode sub-benchmark
 (batch 64, bf16 tape of 32768 positions, HBM GB/s) and the CPU
 baselines (the oracle on this host's cores over bounded samples, warm-up then the
 median of 3).
@@ -318,6 +320,74 @@ def bench_c4_ladder(dev, steps=3, warmup=1):
             "steps": steps, "warmup": warmup, "ladder": ladder}
 
 
+def bench_stack(dev, n_layers=8, steps=3, warmup=1):
+    """A stack of n_layers 340M-shape attention sublayers (BASELINE config 3's layer, one seed per
+    layer), forward (tape) + reverse-scan backward per step, layer by layer and layer-batched
+    (HipLayerStack(wavefront=True): each kernel of a wavefront step one launch over every active
+    layer; bit-identical results). Throughput in layer-tokens/s (B*T tokens through one layer)."""
+    from dual_mod_public_amd.stack import HipLayerStack
+    B, T, d, h, c, K = C2["B"], C2["T"], C2["d"], C2["h"], C2["c"], C2["K"]
+    cfg = DualModConfig(d_model=d, n_heads=h, ctx_mod="mult_res", max_seq_len=T, dtype="bf16")
+    sds = [{k: v.to(dev) for k, v in make_state_dict(cfg, seed=C2["wseed"] + l).items()} for l in range(n_layers)]
+    cos, sin = build_rope_cache(T, d // h, cfg.rope_theta)
+    st = HipLayerStack(cfg, n_layers, B, T, schedule=uniform_chunks(T, c, K), device=dev, tape=True)
+    st.load(sds, cos, sin)
+    x = make_input((B, T, d), seed=C2["xseed"]).to(dev, torch.bfloat16)
+    dy = make_input((B, T, d), seed=C2["xseed"] + 100).to(dev, torch.bfloat16)
+    out = {"workload": f"{n_layers} attention sublayers of the 340M shape (B={B} T={T} d={d} {h}x{d // h} c={c} "
+                       f"K={K}), forward (tape) + reverse-scan backward per step",
+           "n_layers": n_layers, "steps": steps, "warmup": warmup}
+    fpt = fwd_flops_per_token(d, T, c, K)
+    for mode in (False, True):
+        st.wavefront = mode
+        for _ in range(warmup):
+            st.step(x, dy)
+        dt = timed(lambda: st.step(x, dy), steps)
+        key = "wavefront" if mode else "layer_by_layer"
+        out[key] = {"ms_per_step": dt * 1e3, "ms_per_layer": dt * 1e3 / n_layers,
+                    "layer_tokens_per_s": B * T * n_layers / dt,
+                    "path_frac": 3 * fpt * B * T * n_layers / dt / 1e12 / PEAK_BF16_TFLOPS}
+    out["speedup"] = out["layer_by_layer"]["ms_per_step"] / out["wavefront"]["ms_per_step"]
+    del st
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_graph_decode(dev, B=8, n_layers=24, P_max=2048, steps=100, warmup=5):
+    """Greedy decode of a 24-layer 340M-shape DualModLM (vocab 32000, random weights) through the
+    one-graph-per-token GraphDecoder against the eager decode_step, ms per token at B rows."""
+    from dual_mod_public_amd.graph_decode import GraphDecoder
+    from dual_mod_public_amd.model import DualModLM
+    from dual_mod_public_amd.synthetic import make_lm_state_dict
+    cfg = DualModConfig(d_model=C2["d"], n_heads=C2["h"], n_layers=n_layers, vocab_size=32000, max_seq_len=P_max,
+                        ctx_mod="mult_res")
+    m = DualModLM(cfg).to(dev).eval()
+    m.load_state_dict({k: v.to(dev) for k, v in make_lm_state_dict(cfg, seed=C2["wseed"]).items()})
+    dec = GraphDecoder(m, B, P_max).capture()
+    tok = torch.randint(0, cfg.vocab_size, (B, 1), generator=torch.Generator().manual_seed(3)).to(dev)
+    dec.reset()
+    dec.tok.copy_(tok)
+    for _ in range(warmup):
+        dec.step()
+    dt_g = timed(dec.step, steps)
+    caches = m.decode_init()
+    with torch.no_grad():
+        for p in range(warmup):
+            m.decode_step(tok, p, caches)
+        pos = [warmup]
+
+        def eager():
+            m.decode_step(tok, pos[0], caches)
+            pos[0] += 1
+        dt_e = timed(eager, max(10, steps // 5))
+    del dec, caches, m
+    torch.cuda.empty_cache()
+    return {"workload": f"greedy decode, {n_layers}-layer 340M-shape DualModLM (vocab 32000), B={B}, "
+                        f"tape {P_max} rows, positions {warmup}..{warmup + steps}",
+            "graph_ms_per_token": dt_g * 1e3, "graph_tokens_per_s": B / dt_g,
+            "eager_ms_per_token": dt_e * 1e3, "speedup": dt_e / dt_g}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -328,6 +398,8 @@ def main():
                     help="T-prefix of the CPU baseline sample (0: the whole T)")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="skip the config-4 K ladder")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 8-layer stack (layer-batched) sub-benchmark")
+    ap.add_argument("--no-graph-decode", action="store_true", help="skip the model-level graph decode")
     ap.add_argument("--decode-steps", type=int, default=0)
     ap.add_argument("--kernel", default="sweep1", help="kernel class timed for the roofline")
     ap.add_argument("--workload", default="fwdbwd", choices=["fwdbwd", "fwd", "c4"],
@@ -469,6 +541,10 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_c4 and args.workload != "c4":
         out["c4"] = bench_c4_ladder(dev)
+    if not args.no_stack and args.workload != "c4":
+        out["stack"] = bench_stack(dev)
+    if not args.no_graph_decode and args.workload != "c4":
+        out["graph_decode"] = bench_graph_decode(dev)
     if not args.no_decode:
         out["decode"] = bench_decode(dev, args.decode_steps or None, with_cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline and args.workload != "c4":
