@@ -122,10 +122,11 @@ class DualModAttention(nn.Module):
         K. Differentiable: the backward is the HIP reverse scan with exact recompute."""
         if collect is not None:
             raise NotImplementedError("telemetry collection is not supported on the HIP path")
-        if getattr(self.cfg, "local_window", 0):
-            # the fused engine's chunk cells read the whole committed prefix; the window is
-            # honoured by decode_step only (the C entry points reject it for training)
-            raise NotImplementedError("local_window > 0 is decode-only on the HIP path")
+        W = getattr(self.cfg, "local_window", 0) or 0
+        if W and W <= self.CHUNK:
+            # the cells window their committed prefix only; every row of a cell reads all of the
+            # cell's earlier rows, so the window has to exceed the chunk
+            raise NotImplementedError(f"local_window {W} <= the chunk length {self.CHUNK} on the HIP path")
         from .autograd import dm_layer
         B, T, d = xhat.shape
         cell = self._hip_cell(B, T, xhat.dtype)

@@ -880,6 +880,7 @@ template <typename T> struct CommKeyArgs {
   // prefix [0, k0) against every query row [q_lo, q_hi) and ADDS into the fp32 grad cache
   // dKg / dVg [B*h, cache_T, DH] (engines/wavescan/engine/backward.py:116-119)
   float* dKg = nullptr; float* dVg = nullptr;
+  int window = 0;   // local_window W: query row i reads keys >= i - W + 1 (0: none)
 };
 
 // One block per (query split s, b, h): the split's 64-row query tiles s, s + NSQ, ..;
@@ -910,7 +911,10 @@ DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
   constexpr int EPT = DH / 4;
   constexpr int VT = 16 / (int)sizeof(T), NW = EPT / VT;   // 16-byte words per thread and row
   const int ri = tid >> 2, re0 = (tid & 3) * EPT;
-  const int ntile = (a.q_hi - a.q_lo + 63) / 64;
+  // with a window, query rows past k0 + kc + W - 2 see none of these keys
+  const int q_hi = a.window > 0 ? max(a.q_lo, min(a.q_hi, k0 + kc + a.window - 1)) : a.q_hi;
+  const int ntile = (q_hi - a.q_lo + 63) / 64;
+  const int wlim = a.window > 0 ? a.window - 1 : (1 << 30);   // largest query - key distance read
 
   // the cell's keys and values, row-wise (A operands of the key-major products)
   {
@@ -933,7 +937,7 @@ DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
   bool tok = false;
   auto load_tile = [&](int t) {
     const int i0 = a.q_lo + 64 * t;
-    tok = ri < a.q_hi - i0;
+    tok = ri < q_hi - i0;
     const long r = qrow0 + i0 + (tok ? ri : 0);
 #pragma unroll
     for (int w = 0; w < NW; ++w) qv[w] = *reinterpret_cast<const uint4*>(a.qr + r * DH + re0 + w * VT);
@@ -947,7 +951,8 @@ DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
   for (int t = 0; t < NDT; ++t) { dK[t] = zero4(); dV[t] = zero4(); }
   if (s < ntile) load_tile(s);
   for (int t = s; t < ntile; t += nsq) {
-    const int nq = min(64, a.q_hi - (a.q_lo + 64 * t));
+    const int nq = min(64, q_hi - (a.q_lo + 64 * t));
+    const int dqk = a.q_lo + 64 * t - k0;   // query row i - key row j = dqk + i - j
     __syncthreads();   // the previous tile's readers are done (first pass: publishes K / V)
 #pragma unroll
     for (int w = 0; w < NW; ++w) *reinterpret_cast<uint4*>(Qs + ri * LDE + re0 + w * VT) = keep_if(qv[w], tok);
@@ -980,7 +985,7 @@ DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
       for (int r = 0; r < 4; ++r) {
         const int j = 16 * wave + 4 * g4 + r;
         const float e = __expf(St[u][r] * a.scale - mq[u]);
-        Et[u][r] = (j < kc && i < nq) ? e : 0.f;
+        Et[u][r] = (j < kc && i < nq && dqk + i - j <= wlim) ? e : 0.f;
         W[(4 * g4 + r) * LDI + i] = from_f<T>(Et[u][r]);
       }
     }
@@ -1044,6 +1049,7 @@ template <typename T> struct CommQueryArgs {
   float scale;
   float* dq;                                   // [B*h, Tbuf, DH] (+=)
   int row0 = 0;                                // first query row (a multiple of 64 or one cell's start)
+  int window = 0;                              // local_window W: row i reads keys >= i - W + 1 (0: none)
 };
 
 // One block per (b, h, 64-row query tile), the tiles with the longest prefixes
@@ -1101,7 +1107,7 @@ DM_DEV void comm_dq_body(const CommQueryArgs<T>& a) {
   for (int t = 0; t < NDT; ++t) dQ[t] = zero4();
   // the lane's rows' prefix length, row max and Dbar, read once (published by the
   // first tile's barrier)
-  int lq[4];
+  int lq[4] = {0, 0, 0, 0};
   float mq[4], dq[4];
   // the next key tile in registers (raw words; rows past the end zeroed when staged)
   uint4 kv[NW], vv[NW];
@@ -1113,8 +1119,11 @@ DM_DEV void comm_dq_body(const CommQueryArgs<T>& a) {
       vv[w] = *reinterpret_cast<const uint4*>(Vb + (long)(k0 + j) * DH + re0 + w * VT);
     }
   };
-  load_keys(0);
-  for (int k0 = 0; k0 < k_end; k0 += 64) {
+  // with a window the tile's first row reads keys from i0 - W + 1 on (later rows masked below)
+  const int k_lo = a.window > 0 ? max(0, i0 - a.window + 1) : 0;
+  const int wlim = a.window > 0 ? a.window - 1 : (1 << 30);
+  load_keys(k_lo);
+  for (int k0 = k_lo; k0 < k_end; k0 += 64) {
     const bool kok = ri < k_end - k0;
     __syncthreads();   // the previous tile's readers are done (first pass: publishes Q / G)
 #pragma unroll
@@ -1123,7 +1132,7 @@ DM_DEV void comm_dq_body(const CommQueryArgs<T>& a) {
       *reinterpret_cast<uint4*>(Vs + ri * LDE + re0 + w * VT) = keep_if(vv[w], kok);
     }
     __syncthreads();
-    if (k0 == 0) {
+    if (k0 == k_lo) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * wave + 4 * g4 + r;
@@ -1143,7 +1152,8 @@ DM_DEV void comm_dq_body(const CommQueryArgs<T>& a) {
       for (int t = 0; t < 4; ++t) {
         const int j = k0 + 16 * t + lc;
         const float e = __expf(S[t][r] * a.scale - mq[r]);
-        W[il * LDI + 16 * t + lc] = from_f<T>((j < lq[r] ? e : 0.f) * (dP[t][r] - dq[r]));
+        const bool keep = j < lq[r] && i0 + 16 * wave + il - j <= wlim;
+        W[il * LDI + 16 * t + lc] = from_f<T>((keep ? e : 0.f) * (dP[t][r] - dq[r]));
       }
     }
     wave_mma_bt<T, 64, NDT>(W, LDI, Ks, LDE, dQ);

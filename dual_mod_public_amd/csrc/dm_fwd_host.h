@@ -243,10 +243,12 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
 template <typename T, int DH>
 int run_comm(const CellGeom& g, const T* qr, const T* Kc, const T* Vc, float scale, const CellWs& ws,
              hipStream_t s) {
-  const CommPlan cp = comm_plan(g.pos0, g.B * g.h);
+  const int kstart = comm_kstart(g.pos0, g.window);
+  const CommPlan cp = comm_plan(g.pos0 - kstart, g.B * g.h);
   const int BH = g.B * g.h;
   CommArgs<T> ca{g, qr, Kc, Vc, cp.split_len, scale, ws.Ap, ws.Zp, ws.Mp};
   ca.nsplit = cp.nsplit;
+  ca.kstart = kstart;
   if (cp.nsplit == 1) { ca.A = ws.A; ca.Z = ws.Z; ca.Mx = ws.M; }
   if (launch_log() != nullptr) {
     // recorded even without a committed prefix (grid x 0), so that every chunk of a layer
@@ -284,6 +286,7 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
   g.kmod_mode = c->kmod_mode;
   g.v_clamp_tau = c->v_clamp_tau;
   g.rope_t0 = rows.rope_t0;
+  g.window = c->local_window;
   T* Kr = rows.K ? rows.K : Kc;
   T* Vr = rows.K ? rows.V : Vc;
   const long rows_stride = rows.K ? rows.stride : (long)cache_T * DH;

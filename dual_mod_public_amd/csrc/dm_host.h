@@ -113,13 +113,27 @@ struct CommPlan {
 };
 // forward: enough splits for ~512 blocks over the B*h heads (the first sweep's
 // attention merges them, so no more than that)
-inline CommPlan comm_plan(int pos0, int BH) {
-  if (pos0 <= 0) return CommPlan{0, 0};
-  int nsplit = cdiv(pos0, COMM_SPLIT_MIN);
+// (n: the committed keys the cell reads, pos0 or, with a window, fewer)
+inline CommPlan comm_plan(int n, int BH) {
+  if (n <= 0) return CommPlan{0, 0};
+  int nsplit = cdiv(n, COMM_SPLIT_MIN);
   nsplit = std::min(nsplit, std::max(1, std::min(COMM_MAX_SPLITS, cdiv(512, BH))));
-  const int split_len = cdiv(cdiv(pos0, nsplit), 64) * 64;
-  return CommPlan{cdiv(pos0, split_len), split_len};
+  const int split_len = cdiv(cdiv(n, nsplit), 64) * 64;
+  return CommPlan{cdiv(n, split_len), split_len};
 }
+// A local window on the cells covers only their committed prefix (every row of a cell reads all
+// of the cell's earlier rows): the window must exceed the longest cell.
+inline int check_window(const dm_config* c, const int32_t* sched, int n_cells) {
+  int most = 0;
+  for (int i = 0; i < n_cells; ++i) most = std::max(most, (int)sched[3 * i + 1]);
+  DM_REQUIRE(c->local_window == 0 || c->local_window > most, DM_ERR_UNSUPPORTED,
+             "local_window %d must exceed the cell length %d (a cell's rows read all its earlier rows)",
+             c->local_window, most);
+  return DM_OK;
+}
+
+// first committed key a cell at pos0 reads (chunk row 0's window start)
+inline int comm_kstart(int pos0, int window) { return window > 0 ? std::max(0, pos0 - window + 1) : 0; }
 inline int comm_splits_max(int cache_T) {
   int n = cdiv(cache_T, COMM_SPLIT_MIN);
   return n < 1 ? 1 : (n > COMM_MAX_SPLITS ? COMM_MAX_SPLITS : n);

@@ -355,6 +355,8 @@ struct CellGeom {
   int kmod_mode = 0;   // dm_kmod_mode of those columns
   float v_clamp_tau = 0.f;   // v'' norm clamp radius per (row, head), 0 = off
   int rope_t0 = -1;    // RoPE table row of chunk row 0 (-1: pos0, tables indexed by position)
+  int window = 0;      // local_window W (a row at position i reads keys >= i - W + 1); 0 = none.
+                       // The cell kernels take W > c: only the committed prefix is windowed
 };
 // RoPE table row of chunk row p
 DM_DEV int rope_row(const CellGeom& g, int p) { return (g.rope_t0 < 0 ? g.pos0 : g.rope_t0) + p; }
@@ -435,6 +437,7 @@ template <typename T> struct CommArgs {
   float* Z;    // [nsplit, B*h, c]
   float* Mx;   // [nsplit, B*h, c]
   int nsplit = 0;   // splits of this cell (a grouped launch's grid covers the largest)
+  int kstart = 0;   // first committed key of split 0 (the window's start for chunk row 0)
 };
 
 struct KeyBound {
@@ -445,6 +448,13 @@ struct KeyStrictLower {   // q is block-relative; q0 = the block's first query r
   int q0;
   DM_DEV bool operator()(int q, int key) const { return key < q + q0; }
 };
+// committed keys of a tile starting at position k0: key < n, and inside chunk row q's window
+// (position k0 + key >= lo0 + q, lo0 = pos0 - W + 1; a very negative lo0 without a window)
+struct KeyWindow {
+  int n, k0, lo0;
+  DM_DEV bool operator()(int q, int key) const { return key < n && k0 + key >= lo0 + q; }
+};
+constexpr int NO_WINDOW_LO = -(1 << 30);
 
 template <typename T, int DH>
 DM_DEV void comm_partial_block(const CommArgs<T>& a, int s, int bh) {
@@ -456,9 +466,10 @@ DM_DEV void comm_partial_block(const CommArgs<T>& a, int s, int bh) {
   const CellGeom& g = a.g;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int BH = g.B * g.h;
-  const int k_begin = s * a.split_len;
+  const int k_begin = a.kstart + s * a.split_len;
   const int k_end = min(k_begin + a.split_len, g.pos0);
   const int qrow = 16 * wave + (lane & 15);
+  const int lo0 = g.window > 0 ? g.pos0 - g.window + 1 : NO_WINDOW_LO;
 
   const T* Kb = a.Kc + (long)bh * g.cache_T * DH;
   const T* Vb = a.Vc + (long)bh * g.cache_T * DH;
@@ -476,7 +487,7 @@ DM_DEV void comm_partial_block(const CommArgs<T>& a, int s, int bh) {
     __syncthreads();
     const int k1 = k0 + C::KT;
     if (k1 < k_end) load_kv<T, DH>(Kb + (long)k1 * DH, Vb + (long)k1 * DH, DH, min(C::KT, k_end - k1), kv);
-    flash_tile<T, DH>(qf, Ks, Vs, Ps + wave * 16 * C::LDP, a.scale, KeyBound{nv}, st);
+    flash_tile<T, DH>(qf, Ks, Vs, Ps + wave * 16 * C::LDP, a.scale, KeyWindow{nv, k0, lo0}, st);
   }
   const int g4 = lane >> 4, col = lane & 15;
 #pragma unroll

@@ -184,7 +184,10 @@ int dm_cell_fwd(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, 
   DM_REQUIRE(a != nullptr && cos && sin, DM_ERR_INVALID, "null cell args / rope tables");
   DM_REQUIRE(a->c >= 1 && a->c <= CMAX, DM_ERR_UNSUPPORTED, "chunk length c=%d (1..%d)", a->c, CMAX);
   DM_REQUIRE(a->n_sweeps >= 1, DM_ERR_INVALID, "n_sweeps=%d", a->n_sweeps);
-  DM_REQUIRE(c->local_window == 0, DM_ERR_UNSUPPORTED, "local_window is decode-only");
+  {
+    const int32_t one[3] = {a->pos0, a->c, a->n_sweeps};
+    if ((rc = check_window(c, one, 1))) return rc;
+  }
   const bool local = a->K_rows != nullptr;
   if (local) {
     // chunk-local form: layer buffer row p, RoPE table row p and ocat row p belong to chunk row p;
@@ -259,10 +262,8 @@ int dm_layer_fwd(const dm_config* c, const dm_packed* w, const void* x, void* y,
   if (rc) return rc;
   if ((rc = check_packed(c, w)) || (rc = check_bufs(c, L))) return rc;
   DM_REQUIRE(x && y && ocat, DM_ERR_INVALID, "null x/y/ocat");
-  // the chunk cells read the whole committed prefix (the fused engine's training path,
-  // engines/wavescan/cells/fused_sweep.py); a sliding window is decode-only here
-  DM_REQUIRE(c->local_window == 0, DM_ERR_UNSUPPORTED, "local_window is decode-only");
   if ((rc = dm_check_schedule(sched, n_cells, L->T))) return rc;
+  if ((rc = check_window(c, sched, n_cells))) return rc;
   DM_REQUIRE(L->T <= cache_T, DM_ERR_INVALID, "T=%d > cache_T=%d", L->T, cache_T);
   if (tape != nullptr) {
     DM_REQUIRE(tape_bytes >= dm_layer_tape_bytes(c, sched, n_cells), DM_ERR_WORKSPACE, "tape %zu < %zu bytes",

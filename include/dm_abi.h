@@ -57,7 +57,9 @@ typedef struct dm_config {
   int32_t ctx_mod;          /* dm_ctx_mod */
   float mult_res_lambda;    /* config.py:126 */
   float rms_eps;            /* RMSNorm eps of attn_norm / norm_ctx: 1e-5 */
-  int32_t local_window;     /* decode only: W tokens incl. self, 0 = full */
+  int32_t local_window;     /* W tokens incl. self (attention.py:291-293), 0 = full. Decode: any W;
+                               the chunk cells: W > the cell length (a cell's rows read all of
+                               its earlier rows, the committed prefix is windowed) */
   int32_t flags;            /* DM_FLAG_* */
   int32_t kmod_vraw_heads;  /* config.py kmod_vraw_heads: the first n heads keep raw values */
   int32_t kmod_mode;        /* dm_kmod_mode (kmod_mode + kmod_vraw_bound), attention.py:362-384 */

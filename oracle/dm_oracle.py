@@ -258,14 +258,36 @@ def make_intra_mask(c, dtype=torch.float32):
     return m.triu(0)
 
 
+def _window_masks(c, P, W, device, dtype):
+    """attend_one's window (attention.py:291-293: the last W-1 rows before a token, plus
+    itself) on a cell's reads: chunk row p (position P + p) keeps committed key j iff
+    j >= P + p - W + 1 and intra row j' iff p - j' <= W - 1. Additive masks [c, P], [c, c]."""
+    neg = torch.finfo(torch.float32).min
+    p = torch.arange(c, device=device)[:, None]
+    mc = torch.zeros(c, P, device=device, dtype=dtype)
+    mc = mc.masked_fill(torch.arange(P, device=device)[None, :] < P + p - W + 1, neg)
+    mi = torch.zeros(c, c, device=device, dtype=dtype)
+    mi = mi.masked_fill(p - torch.arange(c, device=device)[None, :] > W - 1, neg)
+    return mc, mi
+
+
 def chunk_attend(q_r, k_self_r, v_raw, K_comm, V_comm, K_intra, V_intra,
-                 intra_mask, scale):
-    """scan_cell_fwd.py:63-85 — [committed | intra (strict lower) | raw self]."""
+                 intra_mask, scale, window=0):
+    """scan_cell_fwd.py:63-85 — [committed | intra (strict lower) | raw self]. window > 0:
+    attend_one's local window on the committed and intra reads (_window_masks); with K = c
+    sweeps the cell then equals the windowed sequential scan (scan.py over attend_one)."""
+    c = q_r.shape[2]
+    P = 0 if K_comm is None else K_comm.shape[2]
     s_intra = _hi(q_r @ K_intra.transpose(-1, -2) * scale)
     s_intra = s_intra + intra_mask.to(device=s_intra.device, dtype=s_intra.dtype)
+    if window:
+        mc, mi = _window_masks(c, P, window, s_intra.device, s_intra.dtype)
+        s_intra = s_intra + mi
     s_self = _hi((q_r * k_self_r).sum(-1, keepdim=True)) * scale
     if K_comm is not None and K_comm.shape[2] > 0:
         s_comm = _hi(q_r @ K_comm.transpose(-1, -2) * scale)
+        if window:
+            s_comm = s_comm + mc
         scores = torch.cat([s_comm, s_intra, s_self], dim=-1)
     else:
         scores = torch.cat([s_intra, s_self], dim=-1)
@@ -295,9 +317,10 @@ def chunk_cell_forward(cfg, sd, xhat_c, cos_c, sin_c, K_comm, V_comm, n_sweeps):
     v_raw = split_heads(v_flat, h)
     K_intra, V_intra = k_self_r, v_raw
     o_cat = None
+    W = cfg_get(cfg, "local_window", 0) or 0
     for _ in range(n_sweeps):
         o = chunk_attend(q_r, k_self_r, v_raw, K_comm, V_comm, K_intra, V_intra,
-                         mask, 1.0 / math.sqrt(dh))
+                         mask, 1.0 / math.sqrt(dh), window=W)
         o_cat = merge_heads(o)
         kpp, vpp = refine_kv(cfg, sd, xhat_c, o_cat, k_flat, v_flat)
         K_intra = apply_rope(split_heads(kpp, h), cos_c, sin_c)

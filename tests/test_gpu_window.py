@@ -1,0 +1,138 @@
+"""GPU tests of the local window on the chunk cells (config local_window, attention.py:291-293:
+a token reads the last W - 1 rows before it and itself).
+
+The cells window their committed prefix (a window longer than the cell; every row of a cell
+reads all its earlier rows): with K = c sweeps the windowed layer equals the windowed
+sequential scan of the oracle (attend_one's window, pinned by brute force), with K < c it
+equals the oracle's windowed Jacobi cells (whose masks are pinned to the windowed scan at K = c
+in tests/test_oracle_invariants.py). The backward against autograd through the oracle, the
+windowed decode against the windowed teacher-forced layer, the layer-batched stack against the
+layer-by-layer one, and the rejection of windows no longer than a cell.
+"""
+
+import pytest
+import torch
+
+import oracle as O
+from dual_mod_public_amd import _lib as L
+from dual_mod_public_amd.decode import StaticTape
+from dual_mod_public_amd.engine import HipSweepCell, uniform_chunks
+from tests.hip_helpers import DEV, cfg_of, record, relerr, say, setup, to_dev
+from tests.test_gpu_backward import FP32_TOL, compare, hip_grads, oracle_grads
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    L.load()
+
+
+def _layer(cfg, sd, x, cos, sin, sched, dtype):
+    B, T, d = x.shape
+    cell = HipSweepCell(cfg, B, T, device=DEV, dtype=dtype)
+    cell.pack({k: v.to(DEV, dtype) for k, v in sd.items()})
+    bufs = cell.new_bufs(T)
+    xd = x.to(DEV, dtype).contiguous()
+    y = torch.empty_like(xd)
+    K = torch.empty(B, cfg.n_heads, T, cfg.head_dim, device=DEV, dtype=dtype)
+    V = torch.empty_like(K)
+    ocat = torch.empty_like(xd)
+    cell.layer_forward(xd, y, cos, sin, sched, K, V, ocat, bufs, normalize=False, residual=False)
+    torch.cuda.synchronize()
+    return ocat, K, V
+
+
+@pytest.mark.parametrize("W,T", [(65, 256), (100, 256), (300, 512), (2048, 256)])
+def test_windowed_exact_cells_equal_windowed_scan_fp32(W, T):
+    say(f"windowed cells K=c vs windowed sequential scan, W={W} T={T}")
+    cfg = cfg_of(T=T, local_window=W)
+    B = 2
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    o, K, V = _layer(cfg, sd, x, c32, s32, uniform_chunks(T, 64), torch.float32)
+    o_ref, K_ref, V_ref = O.sequential_scan(cfg, sd, x, c64, s64, return_cache=True)
+    errs = {"o": relerr(o, o_ref), "K": relerr(K, K_ref), "V": relerr(V, V_ref)}
+    record(f"window W={W} T={T} K=c", errs, 1e-5)
+    say(f"  {errs}")
+    assert max(errs.values()) < 1e-5
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_windowed_jacobi_cells_equal_oracle(dtype, tol):
+    say(f"windowed Jacobi cells K=3 vs the oracle, {dtype}")
+    W, T = 150, 320
+    cfg = cfg_of(T=T, local_window=W)
+    B = 2
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    sched = uniform_chunks(T, 64, 3)
+    o, K, V = _layer(cfg, sd, x, c32, s32, sched, dtype)
+    o_ref, K_ref, V_ref = O.layer_forward(cfg, sd, x, c64, s64, sched)
+    errs = {"o": relerr(o, o_ref), "K": relerr(K, K_ref), "V": relerr(V, V_ref)}
+    record(f"window Jacobi {dtype}", errs, tol)
+    assert max(errs.values()) < tol, errs
+
+
+@pytest.mark.parametrize("K,W", [(4, 90), (64, 130)])
+def test_windowed_backward_fp32(K, W):
+    say(f"windowed backward K={K} W={W} vs autograd through the oracle")
+    T = 192
+    cfg = cfg_of(T=T, local_window=W)
+    B = 2
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(3), dtype=torch.float64)
+    sched = uniform_chunks(T, 64, K)
+    dx_ref, g_ref = oracle_grads(cfg, sd, x, dy, c64, s64, sched)
+    for tape in (False, True):
+        _, dx, grads = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.float32, tape=tape)
+        compare(f"window bwd K={K} W={W} tape={tape}", dx, grads, dx_ref, g_ref, FP32_TOL)
+
+
+def test_windowed_decode_equals_teacher_forced():
+    """Two independent paths of the same windowed operator: token-by-token decode on the static
+    tape and the K = c windowed layer forward."""
+    say("windowed decode vs windowed teacher-forced layer")
+    W, T, B = 70, 160, 2
+    cfg = cfg_of(T=T, local_window=W)
+    sd, x, _, (c32, s32) = setup(cfg, B, T)
+    o_f, K_f, V_f = _layer(cfg, sd, x, c32, s32, uniform_chunks(T, 64), torch.float32)
+    tape = StaticTape(cfg, B, T, DEV, torch.float32, sd=to_dev(sd, torch.float32))
+    xd = x.float().to(DEV)
+    outs = [tape.step(xd[:, t].contiguous(), t, c32, s32)[0].clone() for t in range(T)]
+    torch.cuda.synchronize()
+    errs = {"o": relerr(torch.stack(outs, 1), o_f), "K": relerr(tape.K, K_f), "V": relerr(tape.V, V_f)}
+    record("window decode vs layer", errs, 1e-5)
+    assert max(errs.values()) < 1e-5, errs
+
+
+def test_windowed_stack_wavefront_equals_layer_by_layer():
+    from dual_mod_public_amd.stack import HipLayerStack
+    from dual_mod_public_amd.synthetic import make_state_dict
+    say("windowed stack: layer-batched vs layer by layer")
+    T, B, n = 256, 2, 3
+    cfg = cfg_of(T=T, local_window=100)
+    sds = [{k: v.to(DEV) for k, v in make_state_dict(cfg, seed=90 + i).items()} for i in range(n)]
+    cos, sin = O.build_rope_cache(T, cfg.head_dim, cfg.rope_theta)
+    sts = []
+    for wf in (True, False):
+        st = HipLayerStack(cfg, n, B, T, schedule=uniform_chunks(T, 64, 4), device=DEV, dtype=torch.bfloat16,
+                           wavefront=wf)
+        sts.append(st.load(sds, cos, sin))
+    g = torch.Generator(device=DEV).manual_seed(5)
+    x = torch.randn(B, T, cfg.d_model, generator=g, device=DEV).bfloat16()
+    dy = torch.randn(B, T, cfg.d_model, generator=g, device=DEV).bfloat16()
+    y1, dx1, _ = sts[0].step(x, dy)
+    torch.cuda.synchronize()
+    y1, dx1 = y1.clone(), dx1.clone()
+    y2, dx2, _ = sts[1].step(x, dy)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2) and torch.equal(dx1, dx2) and torch.equal(sts[0].flat, sts[1].flat)
+
+
+def test_window_no_longer_than_a_cell_is_refused():
+    cfg = cfg_of(T=128, local_window=64)
+    B, T = 2, 128
+    sd, x, _, (c32, s32) = setup(cfg, B, T)
+    with pytest.raises(L.DMError):
+        _layer(cfg, sd, x, c32, s32, uniform_chunks(T, 64), torch.float32)

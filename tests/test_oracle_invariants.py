@@ -403,3 +403,23 @@ def test_lm_decode_is_teacher_forced():
     caches = [{"K": None, "V": None} for _ in range(cfg.n_layers)]
     out = torch.cat([O.lm_decode_step(cfg, sd, idx[:, t:t + 1], t, caches, cos, sin) for t in range(T)], 1)
     assert relerr(out, ref) < TOL
+
+
+@pytest.mark.parametrize("W,c", [(5, 8), (9, 8), (20, 8), (3, 4)])
+def test_windowed_cells_equal_windowed_scan(W, c):
+    """The local window on the chunk cells (chunk_attend's window masks) with K = c sweeps
+    reproduces the windowed sequential scan (scan.py over attend_one, whose window is pinned by
+    the brute-force test above) — windows shorter and longer than the chunk."""
+    cfg = _cfg(local_window=W)
+    sd, cos, sin, x = _setup(cfg, T=24)
+    ref = O.sequential_scan(cfg, sd, x, cos, sin)
+    out = O.layer_forward(cfg, sd, x, cos, sin, O.uniform_chunks(24, c))[0]
+    assert relerr(out, ref) < TOL
+
+
+def test_window_changes_the_cells():
+    cfg_w = _cfg(local_window=6)
+    sd, cos, sin, x = _setup(cfg_w, T=24)
+    a = O.layer_forward(cfg_w, sd, x, cos, sin, O.uniform_chunks(24, 8, 3))[0]
+    b = O.layer_forward(_cfg(), sd, x, cos, sin, O.uniform_chunks(24, 8, 3))[0]
+    assert relerr(a[:, 6:], b[:, 6:]) > 1e-3 and relerr(a[:, :5], b[:, :5]) < TOL
