@@ -547,9 +547,9 @@ static __global__ __launch_bounds__(256) void k_du_epi(int M, int d, int h, floa
 
 // ---------------------------------------------------------------------------
 // attention VJP of one sweep, two blocks per (b, h), 4 waves x 16 rows each:
-// role 0 (blockIdx.x == 0) the query-major half (dQ, the committed grads G / Dbar,
-// the self column's dq), role 1 the key-major half (dK, dV, the self column's
-// dkself / dvraw). Each role writes its own arrays, so the halves run concurrently.
+// role 0 the query-major half (dQ, the committed grads G / Dbar, the self column's dS
+// summed into sdss), role 1 the key-major half (dK, dV, the self column's dvraw). Each
+// role writes its own arrays, so the halves run concurrently.
 // ---------------------------------------------------------------------------
 template <typename T> struct AttnBwdArgs {
   CellGeom g;
@@ -566,6 +566,10 @@ template <typename T> struct AttnBwdArgs {
   int first;                                           // first reverse sweep: G / Dbar are written, else +=
   float scale, inv_d, eps;
   float* dkself; float* dvraw; float* dq;              // layer accumulators [B, h, Tbuf, DH] (+=)
+  // [B*h, Tbuf] (+=): the self column's dS summed over the sweeps. Its dq and dkself terms,
+  // scale dS_self k_self and scale dS_self q, have the same k_self / q in every sweep, so the
+  // projection VJP applies them once from this sum (no per-sweep dq / dkself round trip).
+  float* sdss;
   // sweep >= 1 (fuse_refine): the grads of the intra rows are those of the previous sweep's
   // refined rows; the key-major blocks run that sweep's refine VJP on them (ref). Sweep 0:
   // the intra rows are the raw rows, their grads go to dkself / dvraw.
@@ -594,8 +598,21 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
   __shared__ float sM[64], sZ[64], sD[64];
 
   const CellGeom& g = a.g;
-  const int role = blockIdx.x;
-  const int bh = blockIdx.y, b = bh / g.h, hh = bh - b * g.h;
+  // The two roles of one (b, h) read the same inputs, so they get blocks on the same XCD (blocks
+  // go round-robin over the 8 XCDs by linear id, x fastest): in each run of 16 linear ids, ids
+  // k and k + 8 are the two roles of one (b, h); a last partial run pairs neighbours.
+  int role, bh;
+  {
+    const int L = (int)blockIdx.x + 2 * (int)blockIdx.y, full = ((int)gridDim.y / 8) * 16;
+    if (L < full) {
+      role = (L & 15) >> 3;
+      bh = 8 * (L >> 4) + (L & 7);
+    } else {
+      role = (L - full) & 1;
+      bh = (full >> 1) + ((L - full) >> 1);
+    }
+  }
+  const int b = bh / g.h, hh = bh - b * g.h;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g4 = lane >> 4, lc = lane & 15;
   const int d = g.d, c = g.c;
@@ -627,17 +644,16 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
     }
     // the accumulators' current values, loaded with the inputs (one memory round trip)
     const long lr = (lrow0 + ic) * DH + e0;
-    float acc0[EPT], acc1[EPT], gold[EPT];
-    float dbold = 0.f, mx = 0.f;
+    float acc1[EPT], gold[EPT];
+    float dbold = 0.f, mx = 0.f, sdold = 0.f;
     if (role == 0) {
-      load_vec<float, EPT>(a.dq + lr, acc0);
+      sdold = a.sdss[lrow0 + ic];
       if (a.Mx != nullptr) {
         mx = a.Mx[(long)bh * c + ic];
         load_vec<float, EPT>(a.G + lr, gold);
         dbold = a.Dbar[lrow0 + ic];
       }
     } else {
-      load_vec<float, EPT>(a.dkself + lr, acc0);
       load_vec<float, EPT>(a.dvraw + lr, acc1);
     }
     float ss = 0.f, dot = 0.f;
@@ -680,16 +696,10 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
     if (role == 0 && a.first && bh == 0 && part == 0 && ok) a.klim[g.buf_t0 + i] = g.pos0;
     if (ok) {
       if (role == 0) {
-#pragma unroll
-        for (int e = 0; e < EPT; ++e) acc0[e] += a.scale * dss * ks[e];
-        store_vec<float, EPT>(a.dq + lr, acc0);
+        if (part == 0) a.sdss[lrow0 + i] = sdold + dss;
       } else {
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) {
-          acc0[e] += a.scale * dss * q[e];
-          acc1[e] += ps * dO[e];
-        }
-        store_vec<float, EPT>(a.dkself + lr, acc0);
+        for (int e = 0; e < EPT; ++e) acc1[e] += ps * dO[e];
         store_vec<float, EPT>(a.dvraw + lr, acc1);
       }
     } else {
@@ -749,7 +759,7 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
   }
   // ---- phase 3: key-major (rows j = 16 wave + ..): P^T, dS^T -> dV = P^T dO, dK = dS^T Q
   else {
-    // sweep 0: the dkself / dvraw rows after phase 1, loaded before the products
+    // sweep 0: the dkself rows and the dvraw rows after phase 1, loaded before the products
     float dko[4][NDT], dvo[4][NDT];
     if (!a.fuse_refine) {
 #pragma unroll
@@ -1182,7 +1192,8 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
 
 // ---------------------------------------------------------------------------
 // projection VJP inputs: d_proj [B*T, nproj*d] in the w_proj row order
-//   q: unrotate dq_r; k: dkraw + unrotate(dkself); v: dvraw; gate x-halves: dglogx;
+//   q: unrotate(dq_r + scale S k_self); k: dkraw + unrotate(dkself + scale S q_r), S = sdss (the
+//   self column's dS summed over the sweeps); v: dvraw; gate x-halves: dglogx;
 //   v_gate: dsig * sig * (1 - sig)
 // and the bias gradients' column partials over the block's rows:
 //   bpart[chunk][0, d) = sum dglogx (b_gk), [d, 2d) = sum dglogx[d..] (b_gv),
@@ -1203,7 +1214,9 @@ DM_DEV void proj_bwd_body(int M, int T_, int d, int h, int nproj, int fusion, co
                           const float* __restrict__ dsig, const float* __restrict__ sig,
                           const float* __restrict__ cos, const float* __restrict__ sin, T* __restrict__ dproj,
                           float* __restrict__ bpart, const T* __restrict__ vpre, const float* __restrict__ vgain,
-                          float* __restrict__ vgpart, RowMap map, int flags, int rpb) {
+                          float* __restrict__ vgpart, const float* __restrict__ sdss,
+                          const T* __restrict__ qr, const T* __restrict__ kself, float scale, RowMap map,
+                          int flags, int rpb) {
   const int pidx = blockIdx.x * 256 + threadIdx.x;
   if (pidx >= d / 2) return;
   const int hd = pidx / (DH / 2), jj = pidx - hd * (DH / 2);
@@ -1239,11 +1252,15 @@ DM_DEV void proj_bwd_body(int M, int T_, int d, int h, int nproj, int fusion, co
       z2 = fusion ? dsig[m * d + c2] : dsig[m * d + c2] * sg2 * (1.f - sg2);
     }
     if (flags & PROJ_ROWS_OUT) {
+      // the self column's terms: dq += scale S k_self, dk_self += scale S q (both rotated)
+      const float S = scale * sdss[((long)b * h + hd) * T_ + t];
+      const float dq1 = q1 + S * to_f(kself[hr + jj]), dq2 = q2 + S * to_f(kself[hr + jj + DH / 2]);
+      const float ds1 = s1 + S * to_f(qr[hr + jj]), ds2 = s2 + S * to_f(qr[hr + jj + DH / 2]);
       T* D = dproj + m * nproj * d;
-      D[c1] = from_f<T>(q1 * cs + q2 * sn);
-      D[c2] = from_f<T>(-q1 * sn + q2 * cs);
-      D[d + c1] = from_f<T>(k1 + s1 * cs + s2 * sn);
-      D[d + c2] = from_f<T>(k2 - s1 * sn + s2 * cs);
+      D[c1] = from_f<T>(dq1 * cs + dq2 * sn);
+      D[c2] = from_f<T>(-dq1 * sn + dq2 * cs);
+      D[d + c1] = from_f<T>(k1 + ds1 * cs + ds2 * sn);
+      D[d + c2] = from_f<T>(k2 - ds1 * sn + ds2 * cs);
       D[2 * d + c1] = from_f<T>(v1);
       D[2 * d + c2] = from_f<T>(v2);
       D[3 * d + c1] = from_f<T>(g1);
@@ -1275,9 +1292,11 @@ static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, i
                                                          const float* __restrict__ cos, const float* __restrict__ sin,
                                                          T* __restrict__ dproj, float* __restrict__ bpart,
                                                          const T* __restrict__ vpre, const float* __restrict__ vgain,
-                                                         float* __restrict__ vgpart, RowMap map, int flags) {
+                                                         float* __restrict__ vgpart, const float* __restrict__ sdss,
+                                                         const T* __restrict__ qr, const T* __restrict__ kself,
+                                                         float scale, RowMap map, int flags) {
   proj_bwd_body<T, DH>(M, T_, d, h, nproj, fusion, dq, dkraw, dkself, dvraw, dglogx, dsig, sig, cos, sin, dproj, bpart,
-                       vpre, vgain, vgpart, map, flags, PROJ_ROWS);
+                       vpre, vgain, vgpart, sdss, qr, kself, scale, map, flags, PROJ_ROWS);
 }
 
 template <typename T, int DH> struct ProjBwdBody {
@@ -1290,13 +1309,17 @@ template <typename T, int DH> struct ProjBwdBody {
     const T* vpre;
     const float* vgain;
     float* vgpart;
+    const float* sdss;
+    const T *qr, *kself;
+    float scale;
     RowMap map;
     int flags;
     int rpb;   // rows per block (PROJ_ROWS when the block partials are written)
   };
   static DM_DEV void run(const Args& a, int, int) {
     proj_bwd_body<T, DH>(a.M, a.T_, a.d, a.h, a.nproj, a.fusion, a.dq, a.dkraw, a.dkself, a.dvraw, a.dglogx, a.dsig,
-                         a.sig, a.cos, a.sin, a.dproj, a.bpart, a.vpre, a.vgain, a.vgpart, a.map, a.flags, a.rpb);
+                         a.sig, a.cos, a.sin, a.dproj, a.bpart, a.vpre, a.vgain, a.vgpart, a.sdss, a.qr, a.kself,
+                         a.scale, a.map, a.flags, a.rpb);
   }
 };
 

@@ -27,6 +27,7 @@ template <typename T> struct BwdWs {
   float *du_part;                       // [DU_SPLIT, N, d] split-K slices of du
   // committed-prefix VJP: per-row state from the attention VJP, key-side partial sums
   float *Grow, *Drow, *Mrow;            // [B*h, T, dh], [B*h, T], [B*h, T]
+  float *sdss;                          // [B*h, T] the self column's dS summed over a cell's sweeps
   int* klim;                            // [T]
   float *dKp, *dVp;                     // [COMM_NSQ, B*h, CMAX, dh]
   // weight grads of the sweeps, one GEMM per layer: the cells' transposed operands
@@ -77,6 +78,7 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.Grow = cv.take<float>(BT * d * 4);
   w.Drow = cv.take<float>(BH * T_ * 4);
   w.Mrow = cv.take<float>(BH * T_ * 4);
+  w.sdss = cv.take<float>(BH * T_ * 4);
   w.klim = cv.take<int>(T_ * 4);
   w.dKp = cv.take<float>(COMM_NSQ * BH * CMAX * dh * 4);
   w.dVp = cv.take<float>(COMM_NSQ * BH * CMAX * dh * 4);
@@ -195,6 +197,7 @@ void bwd_begin(const dm_config* c, const dm_packed* w, const T* dy, const T* oca
                const BwdWs<T>& ws, hipStream_t s) {
   const int B = c->B, d = c->d, BT = B * T_;
   fill0_list({{ws.dq, (size_t)BT * d},
+              {ws.sdss, (size_t)BT * c->h},
               {ws.dkraw, (size_t)BT * d},
               {ws.dkself, (size_t)BT * d},
               {ws.dvraw, (size_t)BT * d},
@@ -340,7 +343,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
                         sw == K - 1 ? ws.docat : nullptr, sv.stat_m + sw * (size_t)BH * CMAX,
                         sv.stat_z + sw * (size_t)BH * CMAX, Mx, ws.Grow, ws.Drow, ws.Mrow, ws.klim,
                         sw == K - 1 ? 1 : 0,
-                        scale, inv_d, c->rms_eps, ws.dkself, ws.dvraw, ws.dq, sw >= 1 ? 1 : 0,
+                        scale, inv_d, c->rms_eps, ws.dkself, ws.dvraw, ws.dq, ws.sdss, sw >= 1 ? 1 : 0,
                         sw >= 1 ? refine_args(sw - 1) : RefineBwdArgs<T>{}};
       if (launch_log() != nullptr)
         record_launch<AttnBwdBody<T, DH>>(dim3(2, BH), dim3(256), aa, (unsigned)lds_attn);
@@ -443,7 +446,8 @@ void bwd_end(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T*
                      fusion ? 1 : 0,
                      (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself, (const float*)ws.dvraw,
                      (const float*)ws.dglogx, (const float*)ws.dsig, (const float*)L->sig, cos, sin, ws.dproj,
-                     ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, RowMap{}, PROJ_ROWS_OUT | PROJ_PARTIALS);
+                     ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, (const float*)ws.sdss, qr,
+                     (const T*)L->kself, scale, RowMap{}, PROJ_ROWS_OUT | PROJ_PARTIALS);
   hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks, 3 * d, 3 * d,
                      (const float*)ws.colpart, gr->b_gk, gr->b_gv, (mult && !fusion) ? gr->b_vgate : nullptr, d);
   // the head norms' gains: sums over rows of the partials
@@ -558,7 +562,8 @@ void record_bwd_chunk(const dm_config* c, const dm_stack_bwd_layer& ly, const fl
   // projection VJP of the cell's rows (the column partials come with the layer's close)
   typename ProjBwdBody<T, DH>::Args pa{N, T_, d, h, nproj, c->ctx_mod == DM_CTX_FUSION ? 1 : 0, ws.dq, ws.dkraw,
                                        ws.dkself, ws.dvraw, ws.dglogx, ws.dsig, L->sig, cos, sin, ws.dproj,
-                                       ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, map, PROJ_ROWS_OUT,
+                                       ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, ws.sdss,
+                                       (const T*)L->qr, (const T*)L->kself, scale, map, PROJ_ROWS_OUT,
                                        PROJ_ROWS_CHUNK};
   record_launch<ProjBwdBody<T, DH>>(dim3(cdiv(d / 2, 256), cdiv(N, PROJ_ROWS_CHUNK)), dim3(256), pa);
   // dxhat rows = d_proj rows . W_proj
@@ -620,7 +625,8 @@ void bwd_stack_close(const dm_config* c, const dm_stack_bwd_layer& ly, const flo
   hipLaunchKernelGGL((k_proj_bwd<T, DH>), dim3(cdiv(d / 2, 256), pchunks), dim3(256), 0, s, BT, T_, d, h, nproj,
                      fusion ? 1 : 0, (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself,
                      (const float*)ws.dvraw, (const float*)ws.dglogx, (const float*)ws.dsig, (const float*)L->sig, cos,
-                     sin, ws.dproj, ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, RowMap{}, PROJ_PARTIALS);
+                     sin, ws.dproj, ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, (const float*)ws.sdss,
+                     (const T*)L->qr, (const T*)L->kself, 1.0f / sqrtf((float)DH), RowMap{}, PROJ_PARTIALS);
   hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks, 3 * d, 3 * d,
                      (const float*)ws.colpart, gr->b_gk, gr->b_gv, (mult && !fusion) ? gr->b_vgate : nullptr, d);
   if (ws.vgpart)
@@ -834,6 +840,7 @@ int run_stack_bwd(const dm_config* c, int nl, const dm_stack_bwd_layer* layers, 
       const BwdWs<T>& w = ws[l];
       const size_t BT = (size_t)c->B * layers[l].bufs->T, d = c->d;
       fill0_list({{w.dq, BT * d},
+                  {w.sdss, BT * c->h},
                   {w.dkraw, BT * d},
                   {w.dkself, BT * d},
                   {w.dvraw, BT * d},

@@ -109,6 +109,20 @@ def test_layer_grads_fp32(ctx_mod, c, k):
     compare("fp32", dx, g, dx_ref, g_ref, FP32_TOL)
 
 
+@pytest.mark.parametrize("taped", [False, True])
+def test_layer_grads_fp32_batch3(taped):
+    """B * h = 12 (attention-VJP blocks: one whole run of 16 role pairs plus a partial run)."""
+    say(f"bwd fp32 B=3 taped={taped}")
+    cfg = cfg_of()
+    B, T = 3, 64
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(97), dtype=torch.float64)
+    sched = uniform_chunks(T, 16, 4)
+    _, dx, g = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.float32, tape=taped)
+    dx_ref, g_ref = oracle_grads(cfg, sd, x, dy, c64, s64, sched)
+    compare("fp32 B=3", dx, g, dx_ref, g_ref, FP32_TOL)
+
+
 @pytest.mark.parametrize("ctx_mod", ["mult_res", "linear", "fusion"])
 def test_layer_grads_tape_fp32(ctx_mod):
     """Forward-saved tape instead of recompute: grads vs autograd through the oracle."""
