@@ -4,7 +4,7 @@
 // Per cell, sweeps run in reverse. For sweep s with its saved (or recomputed) state:
 //   k_refine_bwd  VJP of the blend/gate/RoPE epilogue of the sweep-s refine:
 //                 grads of the refined rows -> dctx (packed GEMM-1 column order),
-//                 dv_ctx, and the layer accumulators dglogx / dkraw / dvraw
+//                 dv_ctx, and the layer accumulators dkraw / dvraw
 //   EpiVinBwd     epilogue of dv_in = dv_ctx . W_vctx: tanh / sigmoid VJP of v_in
 //   k_du_epi      after the split-K GEMM du = dctx . W_sweep (+ lam dv_in): g = du * w_ctx,
 //                 per-row partial <g, o> for the RMS VJP, norm_ctx weight partials
@@ -80,6 +80,14 @@ DM_DEV void wave_mma_bt(const T* X, int ldx, const T* Z, int ldz, floatx4 (&acc)
   __builtin_amdgcn_wave_barrier();
 }
 
+// The cell of a layer row, for the backward's per-row sums over a cell's sweeps: its first
+// row pos0, length c, sweeps K, and the row of the weight-grad stacks (dctx) that holds its
+// sweep 0, batch element 0, cell row 0 (sweep s, element b, cell row p at row0 + s B c + b c + p).
+// K = 0: the row is in no cell.
+struct CellRow {
+  int pos0, c, K, row0;
+};
+
 // packed GEMM-1 column of the k_ctx / g_k(u) quads (see EpiSweep1)
 template <int DH> DM_DEV int col_k(int hd, int jj, int part) {
   return hd * 2 * DH + 64 * (jj / 16) + 16 * part + (jj % 16);
@@ -107,7 +115,8 @@ template <typename T> struct RefineBwdArgs {
   const float* cos; const float* sin;
   T* dctx;                             // [N, 4d] (packed columns; v_map columns written by EpiVinBwd)
   T* dvc;                              // [N, d] dv_ctx (mult family)
-  float* dglogx; float* dkraw; float* dvraw;   // layer accumulators (+=)
+  float* dkraw; float* dvraw;          // layer accumulators (+=). The gate logits' grads dl go
+                                       //   to dctx only: the projection VJP sums them per row
   // k_ctx / v_ctx norms (attention.py:238-269): gains [h] (nullptr = off) and the gains'
   // per-row gradient partials [B*Tbuf, h] (+=)
   const float* kgain = nullptr; const float* vgain = nullptr;
@@ -128,7 +137,7 @@ template <typename T> DM_DEV void ld4(const T* p, float* out) {
 struct RefineIn {
   float cs[4], sn[4], kx1[4], kx2[4], gu1[4], gu2[4], gx1[4], gx2[4], gxv1[4], gxv2[4];
   float kr1[4], kr2[4], vr1[4], vr2[4], vx1[4], vx2[4], gvu1[4], gvu2[4];
-  float ogx1[4], ogx2[4], ogxv1[4], ogxv2[4], okr1[4], okr2[4], ovr1[4], ovr2[4];
+  float okr1[4], okr2[4], ovr1[4], ovr2[4];
 };
 
 template <typename T, int DH>
@@ -141,7 +150,6 @@ DM_DEV RefineIn refine_gather(const RefineBwdArgs<T>& a, int m, int hd, int jj) 
   const long xrow = (long)b * g.Tbuf + t;
   const T* S1 = a.save1 + (long)m * 4 * d;
   const float* gxr = a.glogx + xrow * 2 * d;
-  const float* dgx = a.dglogx + xrow * 2 * d;
   const int c1 = hd * DH + jj, c2 = c1 + DH / 2;
   RefineIn in;
   ld4<float>(a.cos + (long)pos * (DH / 2) + jj, in.cs);
@@ -171,10 +179,6 @@ DM_DEV RefineIn refine_gather(const RefineBwdArgs<T>& a, int m, int hd, int jj) 
     ld4<T>(S1 + 3 * d + c2, in.gvu2);
   }
   // the accumulators' current values, loaded with the inputs (one memory round trip)
-  ld4<float>(dgx + c1, in.ogx1);
-  ld4<float>(dgx + c2, in.ogx2);
-  ld4<float>(dgx + d + c1, in.ogxv1);
-  ld4<float>(dgx + d + c2, in.ogxv2);
   ld4<float>(a.dkraw + lrow, in.okr1);
   ld4<float>(a.dkraw + lrow + DH / 2, in.okr2);
   ld4<float>(a.dvraw + lrow, in.ovr1);
@@ -192,7 +196,6 @@ DM_DEV void refine_apply(const RefineBwdArgs<T>& a, int m, int hd, int jj, const
   const int t = g.buf_t0 + p;
   const long lrow = (((long)b * h + hd) * g.Tbuf + t) * DH + jj;
   const long xrow = (long)b * g.Tbuf + t;
-  float* dgx = a.dglogx + xrow * 2 * d;
   const int c1 = hd * DH + jj, c2 = c1 + DH / 2;
   // k_ctx / v_ctx as the blends took them: raw (kx, vx), or normed, (x r) gain from and to
   // stored values, r over the head's L lanes
@@ -338,19 +341,6 @@ DM_DEV void refine_apply(const RefineBwdArgs<T>& a, int m, int hd, int jj, const
     st4<T>(D + 3 * d + c1, dlv1);
     st4<T>(D + 3 * d + c2, dlv2);
   }
-  float ng[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ng[i] = in.ogx1[i] + dl1[i];
-  st4<float>(dgx + c1, ng);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ng[i] = in.ogx2[i] + dl2[i];
-  st4<float>(dgx + c2, ng);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ng[i] = in.ogxv1[i] + dlv1[i];
-  st4<float>(dgx + d + c1, ng);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ng[i] = in.ogxv2[i] + dlv2[i];
-  st4<float>(dgx + d + c2, ng);
   st4<float>(a.dkraw + lrow, nk1);
   st4<float>(a.dkraw + lrow + DH / 2, nk2);
   st4<float>(a.dvraw + lrow, nv1);
@@ -563,6 +553,7 @@ template <typename T> struct AttnBwdArgs {
   float* G; float* Dbar;                               // committed grads per layer-buffer row
   float* Mrow; int* klim;                              //   [B*h, Tbuf, DH], [B*h, Tbuf]; row max [B*h, Tbuf],
                                                        //   committed prefix length [Tbuf] (first sweep)
+  CellRow* cellrow; int stack_K, stack_row0;          // [Tbuf] this cell's rows (first sweep), K, stack row
   int first;                                           // first reverse sweep: G / Dbar are written, else +=
   float scale, inv_d, eps;
   float* dkself; float* dvraw; float* dq;              // layer accumulators [B, h, Tbuf, DH] (+=)
@@ -693,7 +684,10 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
         if (a.first) a.Mrow[lrow0 + i] = mx;
       }
     }
-    if (role == 0 && a.first && bh == 0 && part == 0 && ok) a.klim[g.buf_t0 + i] = g.pos0;
+    if (role == 0 && a.first && bh == 0 && part == 0 && ok) {
+      a.klim[g.buf_t0 + i] = g.pos0;
+      a.cellrow[g.buf_t0 + i] = CellRow{g.pos0, c, a.stack_K, a.stack_row0};
+    }
     if (ok) {
       if (role == 0) {
         if (part == 0) a.sdss[lrow0 + i] = sdold + dss;
@@ -1193,10 +1187,11 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
 // ---------------------------------------------------------------------------
 // projection VJP inputs: d_proj [B*T, nproj*d] in the w_proj row order
 //   q: unrotate(dq_r + scale S k_self); k: dkraw + unrotate(dkself + scale S q_r), S = sdss (the
-//   self column's dS summed over the sweeps); v: dvraw; gate x-halves: dglogx;
+//   self column's dS summed over the sweeps); v: dvraw; gate x-halves: the row's gate-logit
+//   grads summed over its cell's sweeps (their dctx columns);
 //   v_gate: dsig * sig * (1 - sig)
 // and the bias gradients' column partials over the block's rows:
-//   bpart[chunk][0, d) = sum dglogx (b_gk), [d, 2d) = sum dglogx[d..] (b_gv),
+//   bpart[chunk][0, d) = sum of the key gate's (b_gk), [d, 2d) the value gate's (b_gv),
 //   [2d, 3d) = sum dsig sig (1 - sig) (b_vgate).
 // With the v_norm (vgain != nullptr) dvraw is the grad of the normed value: the v columns get
 // its VJP, from the kept pre-norm values vpre, and vgpart[chunk][head] the v_gain partials.
@@ -1210,8 +1205,8 @@ constexpr int PROJ_ROWS_OUT = 1, PROJ_PARTIALS = 2;
 template <typename T, int DH>
 DM_DEV void proj_bwd_body(int M, int T_, int d, int h, int nproj, int fusion, const float* __restrict__ dq,
                           const float* __restrict__ dkraw, const float* __restrict__ dkself,
-                          const float* __restrict__ dvraw, const float* __restrict__ dglogx,
-                          const float* __restrict__ dsig, const float* __restrict__ sig,
+                          const float* __restrict__ dvraw, const T* __restrict__ dctxL,
+                          const CellRow* __restrict__ cellrow, int B, const float* __restrict__ dsig, const float* __restrict__ sig,
                           const float* __restrict__ cos, const float* __restrict__ sin, T* __restrict__ dproj,
                           float* __restrict__ bpart, const T* __restrict__ vpre, const float* __restrict__ vgain,
                           float* __restrict__ vgpart, const float* __restrict__ sdss,
@@ -1228,13 +1223,29 @@ DM_DEV void proj_bwd_body(int M, int T_, int d, int h, int nproj, int fusion, co
     const long m = map(mi);
     const int b = (int)(m / T_), t = (int)(m - (long)b * T_);
     const long hr = (((long)b * h + hd) * T_ + t) * DH;
-    const float* dg = dglogx + m * 2 * d;
     const float cs = cos[(long)t * (DH / 2) + jj], sn = sin[(long)t * (DH / 2) + jj];
     const float q1 = dq[hr + jj], q2 = dq[hr + jj + DH / 2];
     const float s1 = dkself[hr + jj], s2 = dkself[hr + jj + DH / 2];
     const float k1 = dkraw[hr + jj], k2 = dkraw[hr + jj + DH / 2];
     float v1 = dvraw[hr + jj], v2 = dvraw[hr + jj + DH / 2];
-    const float g1 = dg[c1], g2 = dg[c2], g3 = dg[d + c1], g4 = dg[d + c2];
+    // the gate logits' x-half grads: the sum of the row's dl columns in the stacked dctx rows
+    // of its cell's sweeps, last sweep first (the order their VJPs ran)
+    float g1 = 0.f, g2 = 0.f, g3 = 0.f, g4 = 0.f;
+    {
+      const CellRow cr = cellrow[t];
+      const long step = (long)B * cr.c * 4 * d;
+      const T* R = dctxL + ((long)cr.row0 + (long)b * cr.c + (t - cr.pos0)) * 4 * d;
+      const int ck1 = col_k<DH>(hd, jj, 2), ck2 = col_k<DH>(hd, jj, 3);
+      const int cv1 = nproj == 5 ? col_vlin<DH>(d, hd, jj) + 32 : 3 * d + c1;
+      const int cv2 = nproj == 5 ? col_vlin<DH>(d, hd, jj + DH / 2) + 32 : 3 * d + c2;
+      for (int sw = cr.K - 1; sw >= 0; --sw) {
+        const T* Rs = R + sw * step;
+        g1 += to_f(Rs[ck1]);
+        g2 += to_f(Rs[ck2]);
+        g3 += to_f(Rs[cv1]);
+        g4 += to_f(Rs[cv2]);
+      }
+    }
     if (vgain != nullptr) {   // v_norm VJP over the head's DH / 2 lanes (a whole lane group)
       const float x1 = to_f(vpre[hr + jj]), x2 = to_f(vpre[hr + jj + DH / 2]);
       const float r = head_norm_r(group_sum<DH / 2>(x1 * x1 + x2 * x2), 1.0f / DH);
@@ -1287,7 +1298,8 @@ static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, i
                                                          const float* __restrict__ dq, const float* __restrict__ dkraw,
                                                          const float* __restrict__ dkself,
                                                          const float* __restrict__ dvraw,
-                                                         const float* __restrict__ dglogx,
+                                                         const T* __restrict__ dctxL,
+                                                         const CellRow* __restrict__ cellrow, int B,
                                                          const float* __restrict__ dsig, const float* __restrict__ sig,
                                                          const float* __restrict__ cos, const float* __restrict__ sin,
                                                          T* __restrict__ dproj, float* __restrict__ bpart,
@@ -1295,7 +1307,8 @@ static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, i
                                                          float* __restrict__ vgpart, const float* __restrict__ sdss,
                                                          const T* __restrict__ qr, const T* __restrict__ kself,
                                                          float scale, RowMap map, int flags) {
-  proj_bwd_body<T, DH>(M, T_, d, h, nproj, fusion, dq, dkraw, dkself, dvraw, dglogx, dsig, sig, cos, sin, dproj, bpart,
+  proj_bwd_body<T, DH>(M, T_, d, h, nproj, fusion, dq, dkraw, dkself, dvraw, dctxL, cellrow, B, dsig, sig, cos, sin,
+                       dproj, bpart,
                        vpre, vgain, vgpart, sdss, qr, kself, scale, map, flags, PROJ_ROWS);
 }
 
@@ -1303,7 +1316,11 @@ template <typename T, int DH> struct ProjBwdBody {
   static constexpr int THREADS = 256;
   struct Args {
     int M, T_, d, h, nproj, fusion;
-    const float *dq, *dkraw, *dkself, *dvraw, *dglogx, *dsig, *sig, *cos, *sin;
+    const float *dq, *dkraw, *dkself, *dvraw;
+    const T* dctxL;
+    const CellRow* cellrow;
+    int B;
+    const float *dsig, *sig, *cos, *sin;
     T* dproj;
     float* bpart;
     const T* vpre;
@@ -1317,7 +1334,8 @@ template <typename T, int DH> struct ProjBwdBody {
     int rpb;   // rows per block (PROJ_ROWS when the block partials are written)
   };
   static DM_DEV void run(const Args& a, int, int) {
-    proj_bwd_body<T, DH>(a.M, a.T_, a.d, a.h, a.nproj, a.fusion, a.dq, a.dkraw, a.dkself, a.dvraw, a.dglogx, a.dsig,
+    proj_bwd_body<T, DH>(a.M, a.T_, a.d, a.h, a.nproj, a.fusion, a.dq, a.dkraw, a.dkself, a.dvraw, a.dctxL, a.cellrow,
+                         a.B, a.dsig,
                          a.sig, a.cos, a.sin, a.dproj, a.bpart, a.vpre, a.vgain, a.vgpart, a.sdss, a.qr, a.kself,
                          a.scale, a.map, a.flags, a.rpb);
   }

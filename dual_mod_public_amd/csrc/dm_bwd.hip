@@ -16,7 +16,7 @@ namespace dm {
 template <typename T> struct BwdWs {
   // layer accumulators (fp32)
   float *dq, *dkraw, *dkself, *dvraw;   // [B, h, T, dh]
-  float *dglogx;                        // [B, T, 2d]
+  CellRow* cellrow;                     // [T] the cell of each layer row (written by the attention VJP)
   float *dsig;                          // [B, T, d]
   float *docat;                         // [B, T, d] = dy . W_O
   float *dnw;                           // [NSLOT, d] norm_ctx.weight partials
@@ -64,7 +64,7 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.dkraw = cv.take<float>(BT * d * 4);
   w.dkself = cv.take<float>(BT * d * 4);
   w.dvraw = cv.take<float>(BT * d * 4);
-  w.dglogx = cv.take<float>(BT * 2 * d * 4);
+  w.cellrow = cv.take<CellRow>((size_t)T_ * sizeof(CellRow));
   w.dsig = cv.take<float>(BT * d * 4);
   w.docat = cv.take<float>(BT * d * 4);
   w.dnw = cv.take<float>(cdiv(N, NSLOT_TM) * d * 4);
@@ -201,7 +201,7 @@ void bwd_begin(const dm_config* c, const dm_packed* w, const T* dy, const T* oca
               {ws.dkraw, (size_t)BT * d},
               {ws.dkself, (size_t)BT * d},
               {ws.dvraw, (size_t)BT * d},
-              {ws.dglogx, (size_t)BT * 2 * d},
+              {reinterpret_cast<float*>(ws.cellrow), (size_t)T_ * sizeof(CellRow) / 4},
               {ws.dsig, (size_t)BT * d},
               {ws.dnw, (size_t)cdiv(B * CMAX, NSLOT_TM) * d},
               {ws.dWs, (size_t)4 * d * d},
@@ -288,7 +288,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
   auto refine_args = [&](int sw) {
     return RefineBwdArgs<T>{g, N, c->ctx_mod, dKn, dVn, dn_stride, dn_row0, dn_psum,
                             sv.save1 + sw * NS * 4 * d, mult ? sv.save2 + sw * NS * d : nullptr, L->glogx, kraw,
-                            vraw, cos, sin, dctx + sw * NS * 4 * d, dvc + sw * NS * d, ws.dglogx, ws.dkraw,
+                            vraw, cos, sin, dctx + sw * NS * 4 * d, dvc + sw * NS * d, ws.dkraw,
                             ws.dvraw, kctx_gain(c, w), vctx_gain(c, w), ws.dkg, ws.dvg};
   };
   for (int sw = K - 1; sw >= 0; --sw) {
@@ -342,7 +342,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
                         sv.ssq + sw * NS * h, ws.gw, ws.rowdot, d / DU_EPI_TN,
                         sw == K - 1 ? ws.docat : nullptr, sv.stat_m + sw * (size_t)BH * CMAX,
                         sv.stat_z + sw * (size_t)BH * CMAX, Mx, ws.Grow, ws.Drow, ws.Mrow, ws.klim,
-                        sw == K - 1 ? 1 : 0,
+                        ws.cellrow, K, (int)coff, sw == K - 1 ? 1 : 0,
                         scale, inv_d, c->rms_eps, ws.dkself, ws.dvraw, ws.dq, ws.sdss, sw >= 1 ? 1 : 0,
                         sw >= 1 ? refine_args(sw - 1) : RefineBwdArgs<T>{}};
       if (launch_log() != nullptr)
@@ -438,14 +438,15 @@ void bwd_end(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T*
     hipLaunchKernelGGL((k_comm_dq<T, DH>), dim3(BH, cdiv(t_end, 64)), dim3(256), lds_attn, s, qa);
   }
   // ---- projection VJP
-  // (+ the bias grads' column partials: sums of dglogx (b_gk | b_gv) and of
+  // (+ the bias grads' column partials: sums of the gate logits' grads (b_gk | b_gv) and of
   // dsig sig (1 - sig) (b_vgate) over each block's rows)
   const int pchunks = cdiv(BT, PROJ_ROWS);
   const bool fusion = c->ctx_mod == DM_CTX_FUSION;
   hipLaunchKernelGGL((k_proj_bwd<T, DH>), dim3(cdiv(d / 2, 256), pchunks), dim3(256), 0, s, BT, T_, d, h, nproj,
                      fusion ? 1 : 0,
                      (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself, (const float*)ws.dvraw,
-                     (const float*)ws.dglogx, (const float*)ws.dsig, (const float*)L->sig, cos, sin, ws.dproj,
+                     (const T*)ws.dctxL, (const CellRow*)ws.cellrow, B, (const float*)ws.dsig,
+                     (const float*)L->sig, cos, sin, ws.dproj,
                      ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, (const float*)ws.sdss, qr,
                      (const T*)L->kself, scale, RowMap{}, PROJ_ROWS_OUT | PROJ_PARTIALS);
   hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks, 3 * d, 3 * d,
@@ -561,7 +562,8 @@ void record_bwd_chunk(const dm_config* c, const dm_stack_bwd_layer& ly, const fl
   record_launch<CommDqBody<T, DH>>(dim3(BH, cdiv(cc, 64)), dim3(256), qa, (unsigned)lds_attn);
   // projection VJP of the cell's rows (the column partials come with the layer's close)
   typename ProjBwdBody<T, DH>::Args pa{N, T_, d, h, nproj, c->ctx_mod == DM_CTX_FUSION ? 1 : 0, ws.dq, ws.dkraw,
-                                       ws.dkself, ws.dvraw, ws.dglogx, ws.dsig, L->sig, cos, sin, ws.dproj,
+                                       ws.dkself, ws.dvraw, ws.dctxL, ws.cellrow, B, ws.dsig, L->sig, cos, sin,
+                                       ws.dproj,
                                        ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, ws.sdss,
                                        (const T*)L->qr, (const T*)L->kself, scale, map, PROJ_ROWS_OUT,
                                        PROJ_ROWS_CHUNK};
@@ -624,7 +626,8 @@ void bwd_stack_close(const dm_config* c, const dm_stack_bwd_layer& ly, const flo
   const bool fusion = c->ctx_mod == DM_CTX_FUSION;
   hipLaunchKernelGGL((k_proj_bwd<T, DH>), dim3(cdiv(d / 2, 256), pchunks), dim3(256), 0, s, BT, T_, d, h, nproj,
                      fusion ? 1 : 0, (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself,
-                     (const float*)ws.dvraw, (const float*)ws.dglogx, (const float*)ws.dsig, (const float*)L->sig, cos,
+                     (const float*)ws.dvraw, (const T*)ws.dctxL, (const CellRow*)ws.cellrow, c->B,
+                     (const float*)ws.dsig, (const float*)L->sig, cos,
                      sin, ws.dproj, ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, (const float*)ws.sdss,
                      (const T*)L->qr, (const T*)L->kself, 1.0f / sqrtf((float)DH), RowMap{}, PROJ_PARTIALS);
   hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks, 3 * d, 3 * d,
@@ -844,7 +847,7 @@ int run_stack_bwd(const dm_config* c, int nl, const dm_stack_bwd_layer* layers, 
                   {w.dkraw, BT * d},
                   {w.dkself, BT * d},
                   {w.dvraw, BT * d},
-                  {w.dglogx, BT * 2 * d},
+                  {reinterpret_cast<float*>(w.cellrow), (size_t)layers[l].bufs->T * sizeof(CellRow) / 4},
                   {w.dsig, BT * d},
                   {w.dnw, (size_t)cdiv(c->B * CMAX, NSLOT_TM) * d},
                   {w.dWs, 4 * d * d},
