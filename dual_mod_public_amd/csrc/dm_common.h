@@ -93,6 +93,19 @@ DM_DEV void store_vec(T* p, const float* in) {
 #pragma unroll
   for (int i = 0; i < N / V; ++i) *reinterpret_cast<uint4*>(p + i * V) = pack16<T>(in + i * V);
 }
+// store_vec with the non-temporal hint: for data no kernel of the same pass reads back (the
+// forward tape), so that it does not displace reused operands from the caches
+template <typename T, int N>
+DM_DEV void store_vec_nt(T* p, const float* in) {
+  constexpr int V = 16 / (int)sizeof(T);
+  typedef unsigned int w4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int i = 0; i < N / V; ++i) {
+    const uint4 r = pack16<T>(in + i * V);
+    const w4 w = {r.x, r.y, r.z, r.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<w4*>(p + i * V));
+  }
+}
 
 // Make every value of an array available here (one wait for all of them) before the
 // code that follows: on gfx9 the memory counter also counts stores, so a wait for a

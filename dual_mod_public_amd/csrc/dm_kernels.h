@@ -922,7 +922,7 @@ template <typename T, int DH, int NG = 1> struct EpiSweep1 {
       unpackf4(pr.f[0], gxa); unpackf4(pr.f[1], gxb); unpackf4(pr.f[2], cs); unpackf4(pr.f[3], sn);
       unpack4<T>(pr.h[0], ka); unpack4<T>(pr.h[1], kb);
       settle(gxa); settle(gxb); settle(cs); settle(sn); settle(ka); settle(kb);   // all loads before any store
-      if (save != nullptr) store_vec<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
+      if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
       const int hd = n0 / (2 * DH), jj = 16 * ((n0 % (2 * DH)) / 64) + lc0;
       float o1[4], o2[4];
 #pragma unroll
@@ -941,7 +941,7 @@ template <typename T, int DH, int NG = 1> struct EpiSweep1 {
       float gx[2][4], vr[2][4];
 #pragma unroll
       for (int j = 0; j < 2; ++j) { unpackf4(pr.f[j], gx[j]); unpack4<T>(pr.h[j], vr[j]); settle(gx[j]); settle(vr[j]); }
-      if (save != nullptr) store_vec<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
+      if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
       const int cl = n0 - 2 * d;
       const int hd = cl / (2 * DH), e = 32 * ((cl % (2 * DH)) / 64) + lc0;
       T* crow = Vout + ((long)b * h + hd) * out_stride + (long)(out_row0 + p) * DH + e;
@@ -963,7 +963,7 @@ template <typename T, int DH, int NG = 1> struct EpiSweep1 {
           unpack4<T>(pr.h[k], ov[k]); unpack4<T>(pr.h[4 + k], nw[k]); settle(ov[k]); settle(nw[k]);
         }
       }
-      if (save != nullptr) store_vec<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
+      if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
       const int c0 = n0 - 2 * d + lc0;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -981,7 +981,7 @@ template <typename T, int DH, int NG = 1> struct EpiSweep1 {
         st4<T>(vin + (long)m * d + c0 + 16 * k, v);
       }
     } else {
-      if (save != nullptr) store_vec<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
+      if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
       const int c0 = n0 - 3 * d + lc0;
 #pragma unroll
       for (int k = 0; k < 4; ++k)
@@ -1047,7 +1047,7 @@ template <typename T, int DH> struct EpiSweep2 {
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = value_blend(g, col + i, sigmoidf_(gx[i] + gu[i]), vr[i], a[i]);
     store_vec<T, 8>(Vout + ((long)b * g.h + hd) * out_stride + (long)(out_row0 + p) * DH + e, v);
-    if (save2 != nullptr) store_vec<T, 8>(save2 + (long)m * g.d + col, a);
+    if (save2 != nullptr) store_vec_nt<T, 8>(save2 + (long)m * g.d + col, a);
   }
 };
 
@@ -1155,7 +1155,7 @@ template <typename T, int DH> struct EpiSweep2Head {
     if (m0 + r >= M) return;
     const int b = m / g.c, p = m - b * g.c;
     store_vec<T, CW>(Vout + ((long)b * g.h + n0 / DH) * out_stride + (long)(out_row0 + p) * DH + e0, v);
-    if (save2 != nullptr) store_vec<T, CW>(save2 + (long)m * g.d + col, a);
+    if (save2 != nullptr) store_vec_nt<T, CW>(save2 + (long)m * g.d + col, a);
   }
 };
 
