@@ -1195,102 +1195,162 @@ static __global__ __launch_bounds__(256) void k_comm_dq(CommQueryArgs<T> a) {
 //   [2d, 3d) = sum dsig sig (1 - sig) (b_vgate).
 // With the v_norm (vgain != nullptr) dvraw is the grad of the normed value: the v columns get
 // its VJP, from the kept pre-norm values vpre, and vgpart[chunk][head] the v_gain partials.
-// One thread per RoPE column pair (jj, jj + DH/2) of a head, PROJ_ROWS rows per
-// block; each row's loads are issued before its stores.
+// One thread per item: head hd, RoPE pairs jj .. jj + 3 (jj a multiple of 4) and their partners
+// jj + DH/2 .. + 3, with 4-wide loads and stores. A row has d / 8 items; a block runs
+// proj_rows_in_flight(d) rows at a time (row lane sub = thread / (d / 8)), or, from d = 2048 up,
+// 256 items of one row (grid.x = d / 2048). rpb rows per block, each row's loads issued before
+// its stores. Column partials: one chunk per (block row, row lane), chunk blockIdx.y * rif + sub.
 // ---------------------------------------------------------------------------
-constexpr int PROJ_ROWS = 64;
+constexpr int PROJ_ROWS = 32;
+DM_HOST_DEV inline int proj_rows_in_flight(int d) { return d / 8 >= 256 ? 1 : 256 / (d / 8); }
+DM_HOST_DEV inline int proj_grid_x(int d) { return d / 8 > 256 ? (d / 8 + 255) / 256 : 1; }
 // map: row m of this launch -> layer row (one chunk's rows, or the identity); flags: PROJ_ROWS_OUT
-// writes the dproj rows, PROJ_PARTIALS the column partials of the block (block index blockIdx.y)
+// writes the dproj rows, PROJ_PARTIALS the column partials
 constexpr int PROJ_ROWS_OUT = 1, PROJ_PARTIALS = 2;
 template <typename T, int DH>
 DM_DEV void proj_bwd_body(int M, int T_, int d, int h, int nproj, int fusion, const float* __restrict__ dq,
                           const float* __restrict__ dkraw, const float* __restrict__ dkself,
                           const float* __restrict__ dvraw, const T* __restrict__ dctxL,
-                          const CellRow* __restrict__ cellrow, int B, const float* __restrict__ dsig, const float* __restrict__ sig,
-                          const float* __restrict__ cos, const float* __restrict__ sin, T* __restrict__ dproj,
-                          float* __restrict__ bpart, const T* __restrict__ vpre, const float* __restrict__ vgain,
+                          const CellRow* __restrict__ cellrow, int B, const float* __restrict__ dsig,
+                          const float* __restrict__ sig, const float* __restrict__ cos,
+                          const float* __restrict__ sin, T* __restrict__ dproj, float* __restrict__ bpart,
+                          const T* __restrict__ vpre, const float* __restrict__ vgain,
                           float* __restrict__ vgpart, const float* __restrict__ sdss,
                           const T* __restrict__ qr, const T* __restrict__ kself, float scale, RowMap map,
                           int flags, int rpb) {
-  const int pidx = blockIdx.x * 256 + threadIdx.x;
-  if (pidx >= d / 2) return;
-  const int hd = pidx / (DH / 2), jj = pidx - hd * (DH / 2);
+  constexpr int Q = DH / 8;   // items per head (consecutive lanes)
+  const int ipr = d / 8, rif = proj_rows_in_flight(d);
+  const int sub = ipr >= 256 ? 0 : (int)threadIdx.x / ipr;
+  const int item = ipr >= 256 ? (int)(blockIdx.x * 256 + threadIdx.x) : (int)threadIdx.x - sub * ipr;
+  if (sub >= rif || item >= ipr) return;   // whole heads (ipr is a multiple of Q)
+  const int hd = item / Q, jj = 4 * (item - hd * Q);
   const int c1 = hd * DH + jj, c2 = c1 + DH / 2;
+  const int ck1 = col_k<DH>(hd, jj, 2), ck2 = col_k<DH>(hd, jj, 3);
+  const int cv1 = nproj == 5 ? col_vlin<DH>(d, hd, jj) + 32 : 3 * d + c1;
+  const int cv2 = nproj == 5 ? col_vlin<DH>(d, hd, jj + DH / 2) + 32 : 3 * d + c2;
   const int r0 = blockIdx.y * rpb, r1 = min(r0 + rpb, M);
-  float bg[4] = {0.f, 0.f, 0.f, 0.f}, bv[2] = {0.f, 0.f}, vg = 0.f;
+  float bg[4][4] = {}, bv[2][4] = {}, vg = 0.f;
   const float gvn = vgain != nullptr ? vgain[hd] : 0.f;
-  for (int mi = r0; mi < r1; ++mi) {
+  for (int mi = r0 + sub; mi < r1; mi += rif) {
     const long m = map(mi);
     const int b = (int)(m / T_), t = (int)(m - (long)b * T_);
-    const long hr = (((long)b * h + hd) * T_ + t) * DH;
-    const float cs = cos[(long)t * (DH / 2) + jj], sn = sin[(long)t * (DH / 2) + jj];
-    const float q1 = dq[hr + jj], q2 = dq[hr + jj + DH / 2];
-    const float s1 = dkself[hr + jj], s2 = dkself[hr + jj + DH / 2];
-    const float k1 = dkraw[hr + jj], k2 = dkraw[hr + jj + DH / 2];
-    float v1 = dvraw[hr + jj], v2 = dvraw[hr + jj + DH / 2];
+    const long hr = (((long)b * h + hd) * T_ + t) * DH + jj;
+    float cs[4], sn[4], q1[4], q2[4], s1[4], s2[4], k1[4], k2[4], v1[4], v2[4];
+    ld4<float>(cos + (long)t * (DH / 2) + jj, cs);
+    ld4<float>(sin + (long)t * (DH / 2) + jj, sn);
+    ld4<float>(dq + hr, q1);
+    ld4<float>(dq + hr + DH / 2, q2);
+    ld4<float>(dkself + hr, s1);
+    ld4<float>(dkself + hr + DH / 2, s2);
+    ld4<float>(dkraw + hr, k1);
+    ld4<float>(dkraw + hr + DH / 2, k2);
+    ld4<float>(dvraw + hr, v1);
+    ld4<float>(dvraw + hr + DH / 2, v2);
     // the gate logits' x-half grads: the sum of the row's dl columns in the stacked dctx rows
     // of its cell's sweeps, last sweep first (the order their VJPs ran)
-    float g1 = 0.f, g2 = 0.f, g3 = 0.f, g4 = 0.f;
+    float g[4][4] = {};
     {
       const CellRow cr = cellrow[t];
       const long step = (long)B * cr.c * 4 * d;
       const T* R = dctxL + ((long)cr.row0 + (long)b * cr.c + (t - cr.pos0)) * 4 * d;
-      const int ck1 = col_k<DH>(hd, jj, 2), ck2 = col_k<DH>(hd, jj, 3);
-      const int cv1 = nproj == 5 ? col_vlin<DH>(d, hd, jj) + 32 : 3 * d + c1;
-      const int cv2 = nproj == 5 ? col_vlin<DH>(d, hd, jj + DH / 2) + 32 : 3 * d + c2;
       for (int sw = cr.K - 1; sw >= 0; --sw) {
         const T* Rs = R + sw * step;
-        g1 += to_f(Rs[ck1]);
-        g2 += to_f(Rs[ck2]);
-        g3 += to_f(Rs[cv1]);
-        g4 += to_f(Rs[cv2]);
+        float x[4][4];
+        ld4<T>(Rs + ck1, x[0]);
+        ld4<T>(Rs + ck2, x[1]);
+        ld4<T>(Rs + cv1, x[2]);
+        ld4<T>(Rs + cv2, x[3]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) g[u][i] += x[u][i];
       }
     }
-    if (vgain != nullptr) {   // v_norm VJP over the head's DH / 2 lanes (a whole lane group)
-      const float x1 = to_f(vpre[hr + jj]), x2 = to_f(vpre[hr + jj + DH / 2]);
-      const float r = head_norm_r(group_sum<DH / 2>(x1 * x1 + x2 * x2), 1.0f / DH);
-      const float sv = group_sum<DH / 2>(v1 * x1 + v2 * x2);
+    if (vgain != nullptr) {   // v_norm VJP over the head's Q lanes (a whole lane group)
+      float x1[4], x2[4], ss = 0.f, sv = 0.f;
+      ld4<T>(vpre + hr, x1);
+      ld4<T>(vpre + hr + DH / 2, x2);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ss += x1[i] * x1[i] + x2[i] * x2[i];
+        sv += v1[i] * x1[i] + v2[i] * x2[i];
+      }
+      const float r = head_norm_r(group_sum<Q>(ss), 1.0f / DH);
+      sv = group_sum<Q>(sv);
       const float r3 = r * r * r * sv * (1.0f / DH);
-      v1 = gvn * (r * v1 - r3 * x1);
-      v2 = gvn * (r * v2 - r3 * x2);
-      vg += r * sv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v1[i] = gvn * (r * v1[i] - r3 * x1[i]);
+        v2[i] = gvn * (r * v2[i] - r3 * x2[i]);
+      }
+      if (jj == 0) vg += r * sv;
     }
-    float z1 = 0.f, z2 = 0.f;
+    float z1[4] = {}, z2[4] = {};
     if (nproj == 6) {
-      const float sg1 = sig[m * d + c1], sg2 = sig[m * d + c2];
+      float sg1[4], sg2[4], ds1[4], ds2[4];
+      ld4<float>(sig + m * d + c1, sg1);
+      ld4<float>(sig + m * d + c2, sg2);
+      ld4<float>(dsig + m * d + c1, ds1);
+      ld4<float>(dsig + m * d + c2, ds2);
       // fusion: dsig already holds the grad of the raw pre-activation (no sigmoid, no bias)
-      z1 = fusion ? dsig[m * d + c1] : dsig[m * d + c1] * sg1 * (1.f - sg1);
-      z2 = fusion ? dsig[m * d + c2] : dsig[m * d + c2] * sg2 * (1.f - sg2);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        z1[i] = fusion ? ds1[i] : ds1[i] * sg1[i] * (1.f - sg1[i]);
+        z2[i] = fusion ? ds2[i] : ds2[i] * sg2[i] * (1.f - sg2[i]);
+      }
     }
     if (flags & PROJ_ROWS_OUT) {
       // the self column's terms: dq += scale S k_self, dk_self += scale S q (both rotated)
       const float S = scale * sdss[((long)b * h + hd) * T_ + t];
-      const float dq1 = q1 + S * to_f(kself[hr + jj]), dq2 = q2 + S * to_f(kself[hr + jj + DH / 2]);
-      const float ds1 = s1 + S * to_f(qr[hr + jj]), ds2 = s2 + S * to_f(qr[hr + jj + DH / 2]);
+      float ks1[4], ks2[4], qa[4], qb[4];
+      ld4<T>(kself + hr, ks1);
+      ld4<T>(kself + hr + DH / 2, ks2);
+      ld4<T>(qr + hr, qa);
+      ld4<T>(qr + hr + DH / 2, qb);
+      float o[12][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float dq1 = q1[i] + S * ks1[i], dq2 = q2[i] + S * ks2[i];
+        const float ds1 = s1[i] + S * qa[i], ds2 = s2[i] + S * qb[i];
+        o[0][i] = dq1 * cs[i] + dq2 * sn[i];
+        o[1][i] = -dq1 * sn[i] + dq2 * cs[i];
+        o[2][i] = k1[i] + ds1 * cs[i] + ds2 * sn[i];
+        o[3][i] = k2[i] - ds1 * sn[i] + ds2 * cs[i];
+        o[4][i] = v1[i];
+        o[5][i] = v2[i];
+        o[6][i] = g[0][i];
+        o[7][i] = g[1][i];
+        o[8][i] = g[2][i];
+        o[9][i] = g[3][i];
+        o[10][i] = z1[i];
+        o[11][i] = z2[i];
+      }
       T* D = dproj + m * nproj * d;
-      D[c1] = from_f<T>(dq1 * cs + dq2 * sn);
-      D[c2] = from_f<T>(-dq1 * sn + dq2 * cs);
-      D[d + c1] = from_f<T>(k1 + ds1 * cs + ds2 * sn);
-      D[d + c2] = from_f<T>(k2 - ds1 * sn + ds2 * cs);
-      D[2 * d + c1] = from_f<T>(v1);
-      D[2 * d + c2] = from_f<T>(v2);
-      D[3 * d + c1] = from_f<T>(g1);
-      D[3 * d + c2] = from_f<T>(g2);
-      D[4 * d + c1] = from_f<T>(g3);
-      D[4 * d + c2] = from_f<T>(g4);
-      if (nproj == 6) {
-        D[5 * d + c1] = from_f<T>(z1);
-        D[5 * d + c2] = from_f<T>(z2);
+#pragma unroll
+      for (int p = 0; p < 6; ++p) {
+        if (p == 5 && nproj != 6) break;
+        st4<T>(D + p * d + c1, o[2 * p]);
+        st4<T>(D + p * d + c2, o[2 * p + 1]);
       }
     }
-    bg[0] += g1; bg[1] += g2; bg[2] += g3; bg[3] += g4;
-    bv[0] += z1; bv[1] += z2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) bg[u][i] += g[u][i];
+      bv[0][i] += z1[i];
+      bv[1][i] += z2[i];
+    }
   }
   if (!(flags & PROJ_PARTIALS)) return;
-  float* P = bpart + (long)blockIdx.y * 3 * d;
-  P[c1] = bg[0]; P[c2] = bg[1]; P[d + c1] = bg[2]; P[d + c2] = bg[3];
-  P[2 * d + c1] = bv[0]; P[2 * d + c2] = bv[1];
-  if (vgain != nullptr && jj == 0) vgpart[(long)blockIdx.y * h + hd] = vg;
+  const int chunk = blockIdx.y * rif + sub;
+  float* P = bpart + (long)chunk * 3 * d;
+  st4<float>(P + c1, bg[0]);
+  st4<float>(P + c2, bg[1]);
+  st4<float>(P + d + c1, bg[2]);
+  st4<float>(P + d + c2, bg[3]);
+  st4<float>(P + 2 * d + c1, bv[0]);
+  st4<float>(P + 2 * d + c2, bv[1]);
+  if (vgain != nullptr && jj == 0) vgpart[(long)chunk * h + hd] = vg;
 }
 
 template <typename T, int DH>

@@ -40,9 +40,10 @@ template <typename T> struct BwdWs {
   T* dproj;                             // [B*T, nproj*d]
   float* dxhat;                         // [B*T, d]
   float *dWp, *dWs;                     // packed weight-grad staging [nproj*d, d], [4d, d]
-  float* colpart;                       // [max(NCHUNK, B*T / PROJ_ROWS), 3d] column partials
+  float* colpart;                       // [max(NCHUNK, projection VJP chunks), 3d] column partials
   // head norms: per-row partials of the k_gain / ctx_gain grads [B*T, h], and the v_gain grad's
-  // per-chunk partials [B*T / PROJ_ROWS, h] (nullptr when that norm is off)
+  // per-chunk partials [projection VJP chunks, h] (nullptr when that norm is off); the projection
+  // VJP writes B*T / PROJ_ROWS * proj_rows_in_flight(d) chunks
   float *dkg, *dvg, *vgpart;
   size_t bytes;
 };
@@ -93,10 +94,11 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.dxhat = cv.take<float>(BT * d * 4);
   w.dWp = cv.take<float>(nproj * d * d * 4);
   w.dWs = cv.take<float>(4 * d * d * 4);
-  w.colpart = cv.take<float>((size_t)std::max<long>(NCHUNK, cdiv(BT, PROJ_ROWS)) * 3 * d * 4);
+  const long pparts = cdiv(BT, PROJ_ROWS) * proj_rows_in_flight((int)d);   // projection VJP partial chunks
+  w.colpart = cv.take<float>((size_t)std::max<long>(NCHUNK, pparts) * 3 * d * 4);
   w.dkg = (c->norms & DM_NORM_K_CTX) ? cv.take<float>(BT * h * 4) : nullptr;
   w.dvg = (c->norms & DM_NORM_V_CTX) ? cv.take<float>(BT * h * 4) : nullptr;
-  w.vgpart = (c->norms & DM_NORM_V) ? cv.take<float>((size_t)cdiv(BT, PROJ_ROWS) * h * 4) : nullptr;
+  w.vgpart = (c->norms & DM_NORM_V) ? cv.take<float>((size_t)pparts * h * 4) : nullptr;
   w.bytes = cv.off;
   return w;
 }
@@ -442,18 +444,19 @@ void bwd_end(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T*
   // dsig sig (1 - sig) (b_vgate) over each block's rows)
   const int pchunks = cdiv(BT, PROJ_ROWS);
   const bool fusion = c->ctx_mod == DM_CTX_FUSION;
-  hipLaunchKernelGGL((k_proj_bwd<T, DH>), dim3(cdiv(d / 2, 256), pchunks), dim3(256), 0, s, BT, T_, d, h, nproj,
+  hipLaunchKernelGGL((k_proj_bwd<T, DH>), dim3(proj_grid_x(d), pchunks), dim3(256), 0, s, BT, T_, d, h, nproj,
                      fusion ? 1 : 0,
                      (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself, (const float*)ws.dvraw,
                      (const T*)ws.dctxL, (const CellRow*)ws.cellrow, B, (const float*)ws.dsig,
                      (const float*)L->sig, cos, sin, ws.dproj,
                      ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, (const float*)ws.sdss, qr,
                      (const T*)L->kself, scale, RowMap{}, PROJ_ROWS_OUT | PROJ_PARTIALS);
-  hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks, 3 * d, 3 * d,
+  hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks * proj_rows_in_flight(d), 3 * d, 3 * d,
                      (const float*)ws.colpart, gr->b_gk, gr->b_gv, (mult && !fusion) ? gr->b_vgate : nullptr, d);
   // the head norms' gains: sums over rows of the partials
   if (ws.vgpart)
-    hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(h, 64)), dim3(256), 0, s, pchunks, h, h, (const float*)ws.vgpart,
+    hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(h, 64)), dim3(256), 0, s, pchunks * proj_rows_in_flight(d), h, h,
+                       (const float*)ws.vgpart,
                        gr->v_gain, (float*)nullptr, (float*)nullptr, h);
   if (ws.dkg) colsum_add(ws.dkg, BT, h, ws.colpart, gr->k_gain, s);
   if (ws.dvg) colsum_add(ws.dvg, BT, h, ws.colpart, gr->ctx_gain, s);
@@ -567,7 +570,7 @@ void record_bwd_chunk(const dm_config* c, const dm_stack_bwd_layer& ly, const fl
                                        ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, ws.sdss,
                                        (const T*)L->qr, (const T*)L->kself, scale, map, PROJ_ROWS_OUT,
                                        PROJ_ROWS_CHUNK};
-  record_launch<ProjBwdBody<T, DH>>(dim3(cdiv(d / 2, 256), cdiv(N, PROJ_ROWS_CHUNK)), dim3(256), pa);
+  record_launch<ProjBwdBody<T, DH>>(dim3(proj_grid_x(d), cdiv(N, PROJ_ROWS_CHUNK)), dim3(256), pa);
   // dxhat rows = d_proj rows . W_proj
   {
     EpiStoreTileF32 ex{N, d, ws.dxhat, 0, map};
@@ -624,16 +627,17 @@ void bwd_stack_close(const dm_config* c, const dm_stack_bwd_layer& ly, const flo
   }
   const int pchunks = cdiv(BT, PROJ_ROWS);
   const bool fusion = c->ctx_mod == DM_CTX_FUSION;
-  hipLaunchKernelGGL((k_proj_bwd<T, DH>), dim3(cdiv(d / 2, 256), pchunks), dim3(256), 0, s, BT, T_, d, h, nproj,
+  hipLaunchKernelGGL((k_proj_bwd<T, DH>), dim3(proj_grid_x(d), pchunks), dim3(256), 0, s, BT, T_, d, h, nproj,
                      fusion ? 1 : 0, (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself,
                      (const float*)ws.dvraw, (const T*)ws.dctxL, (const CellRow*)ws.cellrow, c->B,
                      (const float*)ws.dsig, (const float*)L->sig, cos,
                      sin, ws.dproj, ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, (const float*)ws.sdss,
                      (const T*)L->qr, (const T*)L->kself, 1.0f / sqrtf((float)DH), RowMap{}, PROJ_PARTIALS);
-  hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks, 3 * d, 3 * d,
+  hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks * proj_rows_in_flight(d), 3 * d, 3 * d,
                      (const float*)ws.colpart, gr->b_gk, gr->b_gv, (mult && !fusion) ? gr->b_vgate : nullptr, d);
   if (ws.vgpart)
-    hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(h, 64)), dim3(256), 0, s, pchunks, h, h, (const float*)ws.vgpart,
+    hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(h, 64)), dim3(256), 0, s, pchunks * proj_rows_in_flight(d), h, h,
+                       (const float*)ws.vgpart,
                        gr->v_gain, (float*)nullptr, (float*)nullptr, h);
   if (ws.dkg) colsum_add(ws.dkg, BT, h, ws.colpart, gr->k_gain, s);
   if (ws.dvg) colsum_add(ws.dvg, BT, h, ws.colpart, gr->ctx_gain, s);

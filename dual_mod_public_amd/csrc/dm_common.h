@@ -9,6 +9,7 @@
 #include <stdint.h>
 
 #define DM_DEV __device__ __forceinline__
+#define DM_HOST_DEV __host__ __device__
 
 typedef __bf16 bf16;
 typedef float floatx4 __attribute__((ext_vector_type(4)));
