@@ -536,10 +536,11 @@ static __global__ __launch_bounds__(256) void k_du_epi(int M, int d, int h, floa
 
 
 // ---------------------------------------------------------------------------
-// attention VJP of one sweep, two blocks per (b, h), 4 waves x 16 rows each:
+// attention VJP of one sweep, ATTN_BWD_ROLES blocks per (b, h), 4 waves x 16 rows each:
 // role 0 the query-major half (dQ, the committed grads G / Dbar, the self column's dS
-// summed into sdss), role 1 the key-major half (dK, dV, the self column's dvraw). Each
-// role writes its own arrays, so the halves run concurrently.
+// summed into sdss), roles 1 and 2 the key-major half for one half of the keys each (dK, dV,
+// the self column's dvraw, the refine VJP of those rows). Each block writes its own rows, so
+// the blocks run concurrently.
 // ---------------------------------------------------------------------------
 template <typename T> struct AttnBwdArgs {
   CellGeom g;
@@ -568,6 +569,8 @@ template <typename T> struct AttnBwdArgs {
   RefineBwdArgs<T> ref;
 };
 
+constexpr int ATTN_BWD_ROLES = 3;   // blocks per (b, h) of the attention VJP (grid x)
+
 template <typename T, int DH> struct AttnBwdCfg {
   static constexpr int PAD = 16 / (int)sizeof(T);
   static constexpr int LDE = DH + PAD;     // rows over head_dim
@@ -589,20 +592,25 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
   __shared__ float sM[64], sZ[64], sD[64];
 
   const CellGeom& g = a.g;
-  // The two roles of one (b, h) read the same inputs, so they get blocks on the same XCD (blocks
-  // go round-robin over the 8 XCDs by linear id, x fastest): in each run of 16 linear ids, ids
-  // k and k + 8 are the two roles of one (b, h); a last partial run pairs neighbours.
+  // Three blocks per (b, h): role 0 the query-major half, roles 1 and 2 the key-major half for
+  // keys [0, 32) and [32, 64) (each stages every row, computes its keys' dK / dV and runs their
+  // refine VJP). The roles of one (b, h) read the same inputs, so they get blocks on the same XCD
+  // (blocks go round-robin over the 8 XCDs by linear id, x fastest): in each run of 24 linear
+  // ids, ids k, k + 8 and k + 16 are the roles of one (b, h); a last partial run takes them in
+  // turn.
   int role, bh;
   {
-    const int L = (int)blockIdx.x + 2 * (int)blockIdx.y, full = ((int)gridDim.y / 8) * 16;
+    const int L = (int)blockIdx.x + ATTN_BWD_ROLES * (int)blockIdx.y;
+    const int full = ((int)gridDim.y / 8) * 8 * ATTN_BWD_ROLES;
     if (L < full) {
-      role = (L & 15) >> 3;
-      bh = 8 * (L >> 4) + (L & 7);
+      role = (L % (8 * ATTN_BWD_ROLES)) >> 3;
+      bh = 8 * (L / (8 * ATTN_BWD_ROLES)) + (L & 7);
     } else {
-      role = (L - full) & 1;
-      bh = (full >> 1) + ((L - full) >> 1);
+      role = (L - full) % ATTN_BWD_ROLES;
+      bh = full / ATTN_BWD_ROLES + (L - full) / ATTN_BWD_ROLES;
     }
   }
+  const int kh = role - 1;   // key roles: the key half (rows 32 kh .. 32 kh + 31)
   const int b = bh / g.h, hh = bh - b * g.h;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g4 = lane >> 4, lc = lane & 15;
@@ -644,7 +652,7 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
         load_vec<float, EPT>(a.G + lr, gold);
         dbold = a.Dbar[lrow0 + ic];
       }
-    } else {
+    } else if ((i >> 5) == kh) {
       load_vec<float, EPT>(a.dvraw + lr, acc1);
     }
     float ss = 0.f, dot = 0.f;
@@ -691,7 +699,7 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
     if (ok) {
       if (role == 0) {
         if (part == 0) a.sdss[lrow0 + i] = sdold + dss;
-      } else {
+      } else if ((i >> 5) == kh) {
 #pragma unroll
         for (int e = 0; e < EPT; ++e) acc1[e] += ps * dO[e];
         store_vec<float, EPT>(a.dvraw + lr, acc1);
@@ -751,11 +759,14 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
       for (int t = 0; t < NDT; ++t) a.dq[(lrow0 + i) * DH + 16 * t + lc] = dqo[r][t] + a.scale * dQ[t][r];
     }
   }
-  // ---- phase 3: key-major (rows j = 16 wave + ..): P^T, dS^T -> dV = P^T dO, dK = dS^T Q
+  // ---- phase 3: key-major (rows j = 16 wave + ..): P^T, dS^T -> dV = P^T dO, dK = dS^T Q.
+  // The block's key half is waves 2 kh and 2 kh + 1 (wave-uniform); the other two waves only
+  // take part in the barriers and the refine items.
   else {
+    const bool mine = (wave >> 1) == kh;
     // sweep 0: the dkself rows and the dvraw rows after phase 1, loaded before the products
     float dko[4][NDT], dvo[4][NDT];
-    if (!a.fuse_refine) {
+    if (!a.fuse_refine && mine) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int jc = min(16 * wave + 4 * g4 + r, c - 1);
@@ -766,40 +777,42 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
         }
       }
     }
-    floatx4 St[4], dPt[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) { St[t] = zero4(); dPt[t] = zero4(); }
-    wave_mma<T, DH, 4>(Ks + 16 * wave * LDE, LDE, Qs, LDE, St);
-    wave_mma<T, DH, 4>(Vs + 16 * wave * LDE, LDE, dOs, LDE, dPt);
-    float Mq[4], rZq[4], Dq[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int i = 16 * t + lc;
-      Mq[t] = sM[i]; rZq[t] = 1.f / sZ[i]; Dq[t] = sD[i];
-    }
-    float Pt[4][4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int i = 16 * t + lc;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = 16 * wave + 4 * g4 + r;
-        const float e = __expf(St[t][r] * a.scale - Mq[t]) * rZq[t];
-        Pt[t][r] = (j < i && i < c) ? e : 0.f;
-        W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r]);
-      }
-    }
     floatx4 dV[NDT], dK[NDT];
 #pragma unroll
     for (int t = 0; t < NDT; ++t) { dV[t] = zero4(); dK[t] = zero4(); }
-    wave_mma_bt<T, 64, NDT>(W, LDI, dOs, LDE, dV);
+    if (mine) {
+      floatx4 St[4], dPt[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int i = 16 * t + lc;
+      for (int t = 0; t < 4; ++t) { St[t] = zero4(); dPt[t] = zero4(); }
+      wave_mma<T, DH, 4>(Ks + 16 * wave * LDE, LDE, Qs, LDE, St);
+      wave_mma<T, DH, 4>(Vs + 16 * wave * LDE, LDE, dOs, LDE, dPt);
+      float Mq[4], rZq[4], Dq[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r] * (dPt[t][r] - Dq[t]));
+      for (int t = 0; t < 4; ++t) {
+        const int i = 16 * t + lc;
+        Mq[t] = sM[i]; rZq[t] = 1.f / sZ[i]; Dq[t] = sD[i];
+      }
+      float Pt[4][4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int i = 16 * t + lc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * wave + 4 * g4 + r;
+          const float e = __expf(St[t][r] * a.scale - Mq[t]) * rZq[t];
+          Pt[t][r] = (j < i && i < c) ? e : 0.f;
+          W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r]);
+        }
+      }
+      wave_mma_bt<T, 64, NDT>(W, LDI, dOs, LDE, dV);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int i = 16 * t + lc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r] * (dPt[t][r] - Dq[t]));
+      }
+      wave_mma_bt<T, 64, NDT>(W, LDI, Qs, LDE, dK);
     }
-    wave_mma_bt<T, 64, NDT>(W, LDI, Qs, LDE, dK);
     if (a.fuse_refine) {
       // the grads stay on chip: staged in LDS over the Q / K / V / dO tiles once every wave is
       // done with them, then one refine item (row, 4 RoPE pairs) per thread at a time
@@ -808,19 +821,22 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
       float* dKs = reinterpret_cast<float*>(smem_raw);
       float* dVs = dKs + 64 * LDF;
       __syncthreads();
+      if (mine) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = 16 * wave + 4 * g4 + r;
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * wave + 4 * g4 + r;
 #pragma unroll
-        for (int t = 0; t < NDT; ++t) {
-          dKs[j * LDF + 16 * t + lc] = a.scale * dK[t][r];
-          dVs[j * LDF + 16 * t + lc] = dV[t][r];
+          for (int t = 0; t < NDT; ++t) {
+            dKs[j * LDF + 16 * t + lc] = a.scale * dK[t][r];
+            dVs[j * LDF + 16 * t + lc] = dV[t][r];
+          }
         }
       }
       __syncthreads();
-      // Items it = tid + 256 k: row it / Q, pairs 4 (it % Q); a row's items are Q consecutive
-      // lanes. One item per thread at a time: with two in flight the kernel needs more than 256
-      // registers a lane and a CU holds one block instead of two.
+      // Items it = tid + 256 k over the block's key rows: row 32 kh + it / Q, pairs 4 (it % Q);
+      // a row's items are Q consecutive lanes. One item per thread at a time: with two in
+      // flight the kernel needs more than 256 registers a lane and a CU holds one block
+      // instead of two.
       constexpr int Q = DH / 8;
       auto grads = [&](int j, int jj) {
         const float* kr = dKs + j * LDF + jj;
@@ -832,14 +848,15 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
         unpackf4(*reinterpret_cast<const floatx4*>(vr + DH / 2), gr.vb);
         return gr;
       };
-      const int n_items = c * Q;
+      const int n_items = max(0, min(c - 32 * kh, 32)) * Q;
       for (int it = tid; it < n_items; it += 256) {
-        const int j = it / Q, jj = 4 * (it - j * Q);
+        const int j = 32 * kh + it / Q, jj = 4 * (it % Q);
         const RefineIn in = refine_gather<T, DH>(a.ref, b * c + j, hh, jj);
         refine_apply<T, DH>(a.ref, b * c + j, hh, jj, in, grads(j, jj));
       }
       return;
     }
+    if (!mine) return;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int j = 16 * wave + 4 * g4 + r;

@@ -348,9 +348,9 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
                         scale, inv_d, c->rms_eps, ws.dkself, ws.dvraw, ws.dq, ws.sdss, sw >= 1 ? 1 : 0,
                         sw >= 1 ? refine_args(sw - 1) : RefineBwdArgs<T>{}};
       if (launch_log() != nullptr)
-        record_launch<AttnBwdBody<T, DH>>(dim3(2, BH), dim3(256), aa, (unsigned)lds_attn);
+        record_launch<AttnBwdBody<T, DH>>(dim3(ATTN_BWD_ROLES, BH), dim3(256), aa, (unsigned)lds_attn);
       else
-        hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(2, BH), dim3(256), lds_attn, s, aa);
+        hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(ATTN_BWD_ROLES, BH), dim3(256), lds_attn, s, aa);
     }
   }
   // the other operand of dW_sweep = dctx^T u: this cell's K*N rows of u = RMSNorm(o)
