@@ -1,7 +1,8 @@
 """Benchmark of the Dual-Mod attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload fwdbwd|fwd|c4]
-                    [--no-cpu-baseline] [--no-decode] [--no-c4] [--no-stack] [--no-graph-decode]
+                    [--no-cpu-baseline] [--no-decode] [--no-c4] [--no-stack] [--stack-layers L]
+                    [--no-graph-decode]
 
 One step = one DM attention layer of the 340M shape (B=8, T=2048, d=1024,
 16 heads x 64, c=64, K=4 Jacobi sweeps chained over 32 chunks, bf16 storage /
@@ -19,8 +20,9 @@ timing starts.
 Prints ONE JSON line: the headline sweep throughput in tokens/s, the roofline of
 the dominant kernel (sweep GEMM 1) timed with HIP events stamped by its own launches inside a
 second pass of the timed steps, the path-level roofline, the config-4 K ladder (one
-layer of the d=2048 trunk, fwd+bwd for K in {1, 2, 4, 8}), an 8-layer stack of the same layer
-fwd+bwd layer by layer and layer-batched (wavefront), the 24-layer model's greedy decode
+layer of the d=2048 trunk, fwd+bwd for K in {1, 2, 4, 8}), a stack of the same layer at the 340M
+model's depth (24 layers, --stack-layers) fwd+bwd layer by layer and layer-batched (wavefront),
+the 24-layer model's greedy decode
 through the one-graph-per-token decoder against the eager one, the decode sub-benchmark
 (batch 64, bf16 tape of 32768 positions, HBM GB/s) and the CPU
 baselines (the oracle on this host's cores over bounded samples, warm-up then the
@@ -398,7 +400,9 @@ def main():
                     help="T-prefix of the CPU baseline sample (0: the whole T)")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="skip the config-4 K ladder")
-    ap.add_argument("--no-stack", action="store_true", help="skip the 8-layer stack (layer-batched) sub-benchmark")
+    ap.add_argument("--no-stack", action="store_true", help="skip the layer-stack (layer-batched) sub-benchmark")
+    ap.add_argument("--stack-layers", type=int, default=24,
+                    help="layers of the stack sub-benchmark (24: the 340M model's depth)")
     ap.add_argument("--no-graph-decode", action="store_true", help="skip the model-level graph decode")
     ap.add_argument("--decode-steps", type=int, default=0)
     ap.add_argument("--kernel", default="sweep1", help="kernel class timed for the roofline")
@@ -542,7 +546,7 @@ def main():
     if not args.no_c4 and args.workload != "c4":
         out["c4"] = bench_c4_ladder(dev)
     if not args.no_stack and args.workload != "c4":
-        out["stack"] = bench_stack(dev)
+        out["stack"] = bench_stack(dev, n_layers=args.stack_layers)
     if not args.no_graph_decode and args.workload != "c4":
         out["graph_decode"] = bench_graph_decode(dev)
     if not args.no_decode:

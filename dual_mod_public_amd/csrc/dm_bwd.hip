@@ -320,9 +320,13 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
     {
       const int S = DU_SPLIT;
       EpiStoreTileF32 ep{N, d, ws.du_part, (long)N * d};
-      launch_gemm_splitk<T, 64, 64, 2, 2, sizeof(T) == 2 ? -DU_STAGES : 4>(
-          SrcRows<T>{dctx + sw * NS * 4 * d, 4 * d, N}, SrcRows<T>{(const T*)w->w_sweep_t, 4 * d, d}, N, d,
-          4 * d, S, ep, s);
+      const SrcRows<T> da{dctx + sw * NS * 4 * d, 4 * d, N}, db{(const T*)w->w_sweep_t, 4 * d, d};
+      // the layer-batched launch has blocks to spare: 128 x 128 tiles (half the LDS traffic per
+      // product; every element's k order is the same, so the results are too)
+      if (sizeof(T) == 2 && launch_log() != nullptr)
+        launch_gemm_splitk<T, 128, 128, 2, 2, sizeof(T) == 2 ? -3 : 4>(da, db, N, d, 4 * d, S, ep, s);
+      else
+        launch_gemm_splitk<T, 64, 64, 2, 2, sizeof(T) == 2 ? -DU_STAGES : 4>(da, db, N, d, 4 * d, S, ep, s);
       const typename DuEpiBody<T, DU_SPLIT>::Args ea{N, d, h, inv_d, c->rms_eps, (const float*)ws.du_part,
                                                      mult ? (const float*)ws.lamdv : nullptr,
                                                      (const T*)(sv.o + sw * NS * d),
