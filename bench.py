@@ -1,7 +1,8 @@
 """Benchmark of the Dual-Mod attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload fwdbwd|fwd|c4]
-                    [--no-cpu-baseline] [--no-decode] [--no-c4] [--no-stack] [--stack-layers L]
+                    [--no-cpu-baseline] [--no-decode] [--no-c4] [--c4-stack-layers L] [--no-stack]
+                    [--stack-layers L]
                     [--no-graph-decode]
 
 One step = one DM attention layer of the 340M shape (B=8, T=2048, d=1024,
@@ -20,7 +21,7 @@ timing starts.
 Prints ONE JSON line: the headline sweep throughput in tokens/s, the roofline of
 the dominant kernel (sweep GEMM 1) timed with HIP events stamped by its own launches inside a
 second pass of the timed steps, the path-level roofline, the config-4 K ladder (one
-layer of the d=2048 trunk, fwd+bwd for K in {1, 2, 4, 8}), a stack of the same layer at the 340M
+layer of the d=2048 trunk, fwd+bwd for K in {1, 2, 4, 8}; and 8 such layers layer-batched), a stack of the same layer at the 340M
 model's depth (24 layers, --stack-layers) fwd+bwd layer by layer and layer-batched (wavefront),
 the 24-layer model's greedy decode
 through the one-graph-per-token decoder against the eager one, the decode sub-benchmark
@@ -284,7 +285,7 @@ def bench_decode(dev, steps_override=None, with_cpu=True):
 def bench_c4_ladder(dev, steps=3, warmup=1):
     """BASELINE config 4's workload: one layer of the d=2048, 16 x 128 trunk at B=4, T=4096, c=64,
     forward (tape) + reverse-scan backward per K in the ladder (1, 2, 4, 8). The cell's algorithmic
-    FLOPs as in SURVEY (the trunk's SwiGLU MLP and tied head are outside the layer)."""
+    FLOPs (fwd_flops_per_token; the trunk's SwiGLU MLP and tied head are outside the layer)."""
     B, T, d, h, c = C4["B"], C4["T"], C4["d"], C4["h"], C4["c"]
     cfg = DualModConfig(d_model=d, n_heads=h, ctx_mod="mult_res", max_seq_len=T, dtype="bf16")
     sd, cell, x, cos, sin, bufs, Kc, Vc, ocat, y = build_layer(cfg, B, T, dev, seeds=C4)
@@ -320,6 +321,37 @@ def bench_c4_ladder(dev, steps=3, warmup=1):
     return {"workload": f"C4: one layer of the d=2048 trunk (16x128), B={B} T={T} c={c}, forward (tape) + "
                         "reverse-scan backward per K; the per-layer cell of the 24-layer trunk",
             "steps": steps, "warmup": warmup, "ladder": ladder}
+
+
+def bench_c4_wavefront(dev, n_layers=8, steps=2, warmup=1):
+    """Config 4's trunk attention sublayers as a layer-batched stack: n_layers d=2048, 16 x 128
+    sublayers (one weight set) at B=4, T=4096, c=64, forward (tape) + reverse-scan backward per
+    step, HipLayerStack(wavefront=True), per K in the ladder; ms per layer and the cell's MFMA
+    fraction. 8 layers by default: at K = 8 a layer holds ~12 GB (tape and backward workspace)."""
+    from dual_mod_public_amd.stack import HipLayerStack
+    B, T, d, h, c = C4["B"], C4["T"], C4["d"], C4["h"], C4["c"]
+    cfg = DualModConfig(d_model=d, n_heads=h, ctx_mod="mult_res", max_seq_len=T, dtype="bf16")
+    sd = {k: v.to(dev) for k, v in make_state_dict(cfg, seed=C4["wseed"]).items()}
+    cos, sin = build_rope_cache(T, d // h, cfg.rope_theta)
+    x = make_input((B, T, d), seed=C4["xseed"]).to(dev, torch.bfloat16)
+    dy = make_input((B, T, d), seed=C4["xseed"] + 100).to(dev, torch.bfloat16)
+    ladder = []
+    for K in C4["ladder"]:
+        st = HipLayerStack(cfg, n_layers, B, T, schedule=uniform_chunks(T, c, K), device=dev, tape=True,
+                           wavefront=True)
+        st.load([sd] * n_layers, cos, sin)
+        for _ in range(warmup):
+            st.step(x, dy)
+        dt = timed(lambda: st.step(x, dy), steps)
+        fpt = fwd_flops_per_token(d, T, c, K)
+        ladder.append({"K": K, "ms_per_layer_fwdbwd": dt * 1e3 / n_layers,
+                       "layer_tokens_per_s": B * T * n_layers / dt,
+                       "frac_fwdbwd": 3 * fpt * B * T * n_layers / dt / 1e12 / PEAK_BF16_TFLOPS})
+        del st
+        torch.cuda.empty_cache()
+    return {"workload": f"C4: {n_layers} attention sublayers of the d=2048 trunk (16x128), B={B} T={T} c={c}, "
+                        "layer-batched (wavefront) forward (tape) + reverse-scan backward per K",
+            "n_layers": n_layers, "steps": steps, "warmup": warmup, "ladder": ladder}
 
 
 def bench_stack(dev, n_layers=8, steps=3, warmup=1):
@@ -401,6 +433,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="skip the config-4 K ladder")
     ap.add_argument("--no-stack", action="store_true", help="skip the layer-stack (layer-batched) sub-benchmark")
+    ap.add_argument("--c4-stack-layers", type=int, default=8,
+                    help="layers of the config-4 layer-batched K ladder (0: skip)")
     ap.add_argument("--stack-layers", type=int, default=24,
                     help="layers of the stack sub-benchmark (24: the 340M model's depth)")
     ap.add_argument("--no-graph-decode", action="store_true", help="skip the model-level graph decode")
@@ -545,6 +579,8 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_c4 and args.workload != "c4":
         out["c4"] = bench_c4_ladder(dev)
+        if args.c4_stack_layers > 0:
+            out["c4"]["wavefront"] = bench_c4_wavefront(dev, n_layers=args.c4_stack_layers)
     if not args.no_stack and args.workload != "c4":
         out["stack"] = bench_stack(dev, n_layers=args.stack_layers)
     if not args.no_graph_decode and args.workload != "c4":

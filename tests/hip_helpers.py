@@ -23,15 +23,15 @@ def say(msg):
 
 
 def record(test, errs, tol):
-    """Keep a test's measured relative errors (written to gpurun_out/parity_margins.json
-    at the end of the session, so the margins of every run come back with it)."""
+    """Keep a test's measured relative errors (written to parity_margins.json in the run's
+    output folder at the end of the session)."""
     MARGINS.append({"test": test, "tol": tol, "relerr": {k: float(v) for k, v in errs.items()}})
 
 
 def write_margins(repo):
     if not MARGINS:
         return
-    out = os.path.join(repo, "gpurun_out")
+    out = os.path.join(repo, os.environ.get("DM_RESULTS_DIR", "gpurun_out"))
     os.makedirs(out, exist_ok=True)
     with open(os.path.join(out, "parity_margins.json"), "w") as f:
         json.dump(MARGINS, f, indent=1)
