@@ -940,11 +940,31 @@ size_t dm_stack_bwd_plan_bytes(const dm_config* c, int32_t n_layers, const dm_st
 int dm_stack_bwd(const dm_config* c, int32_t n_layers, const dm_stack_bwd_layer* layers, const float* cos,
                  const float* sin, const int32_t* sched, int32_t n_cells, int32_t cache_T, void* plan,
                  size_t plan_bytes, int32_t build, void* stream) {
+  if (const int crc = check_cfg(c)) return crc;
   DM_REQUIRE(cos && sin, DM_ERR_INVALID, "null rope tables");
   DM_REQUIRE(plan != nullptr && (reinterpret_cast<uintptr_t>(plan) & 255) == 0, DM_ERR_INVALID,
              "plan must be non-null and 256-byte aligned");
-  return run_stack_bwd(c, n_layers, layers, cos, sin, sched, n_cells, cache_T, plan, plan_bytes, build, stream,
-                       nullptr);
+  DM_REQUIRE(n_layers >= 1 && layers != nullptr && sched != nullptr && n_cells >= 1, DM_ERR_INVALID,
+             "n_layers=%d n_cells=%d", n_layers, n_cells);
+  ArgSig sig;
+  sig.val(*c); sig.val(n_layers); sig.val(cos); sig.val(sin); sig.val(n_cells); sig.val(cache_T);
+  sig.val(plan_bytes); sig.add(sched, sizeof(int32_t) * 3 * (size_t)n_cells);
+  for (int l = 0; l < n_layers; ++l) {
+    const dm_stack_bwd_layer& ly = layers[l];
+    DM_REQUIRE(ly.w && ly.bufs && ly.grads, DM_ERR_INVALID, "layer %d: null weights, buffers or grads", l);
+    sig.val(*ly.w); sig.bufs(ly.bufs); sig.val(*ly.grads);
+    sig.val(ly.x); sig.val(ly.dy); sig.val(ly.dx); sig.val(ly.K_cache); sig.val(ly.V_cache); sig.val(ly.ocat);
+    sig.val(ly.tape); sig.val(ly.tape_bytes); sig.val(ly.workspace); sig.val(ly.workspace_bytes);
+  }
+  if (!build)
+    DM_REQUIRE(plan_sig_matches(plan, sig.h), DM_ERR_INVALID,
+               "plan %p was not written for these arguments (call once with build != 0)", plan);
+  else
+    plan_sig_forget(plan);
+  const int rc = run_stack_bwd(c, n_layers, layers, cos, sin, sched, n_cells, cache_T, plan, plan_bytes, build,
+                               stream, nullptr);
+  if (rc == DM_OK && build) plan_sig_store(plan, sig.h);
+  return rc;
 }
 
 int dm_layer_bwd_end(const dm_config* c, const dm_packed* w, const void* x, const void* dy, void* dx,

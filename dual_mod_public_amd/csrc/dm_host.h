@@ -5,7 +5,10 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdint>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -201,6 +204,51 @@ inline int issue_grouped(const GroupedLaunch& g, void* plan, hipStream_t s) {
   void* args[] = {&p};
   DM_HIP(hipLaunchKernel(g.f, g.grid, g.block, args, g.shmem, s));
   return DM_OK;
+}
+
+// ---- plans of the layer-batched passes -----------------------------------------------------
+// A plan's device table holds the argument structs of a pass's grouped launches. The library
+// remembers, per plan address, a signature (FNV-1a) of every argument the table was written
+// for; a call that launches from a written plan (build == 0) must present the same arguments,
+// so a plan never written, overwritten by another pass, or written for other buffers is refused
+// instead of being launched.
+struct ArgSig {
+  uint64_t h = 1469598103934665603ull;
+  void add(const void* p, size_t n) {
+    const unsigned char* b = static_cast<const unsigned char*>(p);
+    for (size_t i = 0; i < n; ++i) {
+      h ^= b[i];
+      h *= 1099511628211ull;
+    }
+  }
+  template <class X> void val(const X& x) { add(&x, sizeof(x)); }
+  void bufs(const dm_layer_bufs* L) {   // field by field: the struct has padding after T
+    val(L->T); val(L->xhat); val(L->qr); val(L->kraw); val(L->kself); val(L->vraw); val(L->glogx);
+    val(L->sig); val(L->vpre);
+  }
+};
+inline std::mutex& plan_sig_mu() {
+  static std::mutex m;
+  return m;
+}
+inline std::map<const void*, uint64_t>& plan_sigs() {
+  static std::map<const void*, uint64_t> m;
+  return m;
+}
+// a build forgets the plan's signature first (a failed build leaves no usable plan) and stores it
+// once the pass has gone through
+inline void plan_sig_forget(const void* plan) {
+  std::lock_guard<std::mutex> lk(plan_sig_mu());
+  plan_sigs().erase(plan);
+}
+inline void plan_sig_store(const void* plan, uint64_t sig) {
+  std::lock_guard<std::mutex> lk(plan_sig_mu());
+  plan_sigs()[plan] = sig;
+}
+inline bool plan_sig_matches(const void* plan, uint64_t sig) {
+  std::lock_guard<std::mutex> lk(plan_sig_mu());
+  auto it = plan_sigs().find(plan);
+  return it != plan_sigs().end() && it->second == sig;
 }
 
 inline int log2_exact(int v) {

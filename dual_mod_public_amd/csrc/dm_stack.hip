@@ -174,28 +174,38 @@ int dm_stack_fwd(const dm_config* c, int32_t n_layers, const dm_stack_layer* lay
   DM_REQUIRE(cos && sin, DM_ERR_INVALID, "null rope tables");
   DM_REQUIRE(plan != nullptr && (reinterpret_cast<uintptr_t>(plan) & 255) == 0, DM_ERR_INVALID,
              "plan must be non-null and 256-byte aligned");
+  ArgSig sig;
+  sig.val(*c); sig.val(n_layers); sig.val(cos); sig.val(sin); sig.val(n_cells); sig.val(cache_T);
+  sig.val(plan_bytes); sig.add(sched, sizeof(int32_t) * 3 * (size_t)n_cells);
+  for (int l = 0; l < n_layers; ++l) {
+    const dm_stack_layer& ly = layers[l];
+    sig.val(*ly.w); sig.bufs(ly.bufs);
+    sig.val(ly.x); sig.val(ly.y); sig.val(ly.K_cache); sig.val(ly.V_cache); sig.val(ly.ocat);
+    sig.val(ly.tape); sig.val(ly.tape_bytes); sig.val(ly.workspace); sig.val(ly.workspace_bytes);
+  }
   std::vector<GroupedLaunch> launches;
-  bool cached = false;
   if (!build) {
+    DM_REQUIRE(plan_sig_matches(plan, sig.h), DM_ERR_INVALID,
+               "plan %p was not written for these arguments (call once with build != 0)", plan);
     PlanCache& pc = plan_cache();
     std::lock_guard<std::mutex> lk(pc.mu);
     auto it = pc.lists.find(plan);
-    if (it != pc.lists.end()) {
-      launches = it->second;
-      cached = true;
-    }
-  }
-  if (!cached) {
+    DM_REQUIRE(it != pc.lists.end(), DM_ERR_INVALID, "plan %p has no launch list", plan);
+    launches = it->second;
+  } else {
+    plan_sig_forget(plan);
     std::vector<unsigned char> tab;
     size_t bytes = 0;
-    if ((rc = plan_stack(c, n_layers, layers, cos, sin, sched, n_cells, cache_T, launches, build ? &tab : nullptr,
-                         &bytes)))
+    if ((rc = plan_stack(c, n_layers, layers, cos, sin, sched, n_cells, cache_T, launches, &tab, &bytes)))
       return rc;
     DM_REQUIRE(plan_bytes >= bytes, DM_ERR_WORKSPACE, "plan %zu < %zu bytes", plan_bytes, bytes);
-    if (build) DM_HIP(hipMemcpy(plan, tab.data(), bytes, hipMemcpyHostToDevice));
-    PlanCache& pc = plan_cache();
-    std::lock_guard<std::mutex> lk(pc.mu);
-    pc.lists[plan] = launches;
+    DM_HIP(hipMemcpy(plan, tab.data(), bytes, hipMemcpyHostToDevice));
+    {
+      PlanCache& pc = plan_cache();
+      std::lock_guard<std::mutex> lk(pc.mu);
+      pc.lists[plan] = launches;
+    }
+    plan_sig_store(plan, sig.h);
   }
   hipStream_t s = S(stream);
   for (const GroupedLaunch& g : launches)

@@ -221,8 +221,10 @@ int dm_layer_fwd(const dm_config* cfg, const dm_packed* w, const void* x, void* 
  * plan: device memory of dm_stack_fwd_plan_bytes() bytes holding every launch's argument
  * table. build != 0 writes it (a blocking host-to-device copy) before launching; build == 0
  * launches from a plan written by an earlier call with the same arguments (e.g. under graph
- * capture): the library keeps each written plan's launch list, keyed by the plan's address,
- * so such a call only issues the launches. Kernel timing (dm_prof_start) does not cover this
+ * capture): the library keeps each written plan's launch list and a signature of its arguments,
+ * keyed by the plan's address, so such a call only issues the launches; a build == 0 call whose
+ * arguments differ from the plan's last build (or on a plan never built) returns
+ * DM_ERR_INVALID and launches nothing. Kernel timing (dm_prof_start) does not cover this
  * entry point. */
 typedef struct dm_stack_layer {
   const dm_packed* w;

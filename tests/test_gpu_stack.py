@@ -210,3 +210,36 @@ def test_wavefront_rejects_unequal_cells():
     st, _ = _stack(cfg, 2, 2, 64, torch.bfloat16, (1, 2), [(0, 16, 4), (16, 48, 2)], wavefront=True)
     with pytest.raises(L.DMError):
         st.forward_wavefront()
+
+
+def test_wavefront_plan_refused_unless_built_for_the_arguments():
+    """dm_stack_fwd / dm_stack_bwd with build == 0 launch from a plan written earlier: a plan
+    never written, or written for other buffers, is refused (DM_ERR_INVALID, nothing launched);
+    the same arguments go through and give the same results."""
+    say("wavefront plans: build == 0 needs a plan written for the same arguments")
+    cfg = cfg_of(T=64)
+    B, T, n = 2, 64, 2
+    st, _ = _stack(cfg, n, B, T, torch.bfloat16, (5, 6), [(p, 16, 2) for p in range(0, T, 16)], wavefront=True)
+    g = torch.Generator(device=DEV).manual_seed(8)
+    x = torch.randn(B, T, cfg.d_model, generator=g, device=DEV).to(torch.bfloat16)
+    dy = torch.randn(B, T, cfg.d_model, generator=g, device=DEV).to(torch.bfloat16)
+    y0, dx0, _ = st.step(x, dy)          # writes both plans
+    torch.cuda.synchronize()
+    y0, dx0 = y0.clone(), dx0.clone()
+    plan, bplan = st._plan, st._bplan
+    st._plan = torch.empty_like(plan)    # never written
+    with pytest.raises(L.DMError):
+        st.forward_wavefront()
+    st._plan = plan
+    x_saved = st.xs[0]
+    st.xs[0] = x_saved.clone()            # another input buffer than the plan was written for
+    with pytest.raises(L.DMError):
+        st.forward_wavefront()
+    st.xs[0] = x_saved
+    st._bplan = torch.empty_like(bplan)
+    with pytest.raises(L.DMError):
+        st.backward_wavefront()
+    st._bplan = bplan
+    y1, dx1, _ = st.step(x, dy)          # the written plans, the same arguments
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y0) and torch.equal(dx1, dx0)
