@@ -45,6 +45,7 @@ class GraphDecoder:
         self._head = torch.empty_like(model.lm_head.weight, dtype=self.dt)
         self._ver = None
         self.graph = None
+        self._steps = 0
         self.refresh()
 
     def refresh(self):
@@ -105,15 +106,22 @@ class GraphDecoder:
 
     def reset(self):
         self.pos.zero_()
+        self._steps = 0
         for t in self.tapes:
             t.K.zero_()
             t.V.zero_()
 
     def step(self):
+        """One token: the graph replay (or the eager step). The position lives on the device;
+        the host counts the steps since reset() and refuses a step past the tape (the kernels
+        would clamp the position onto the last slot)."""
+        if self._steps >= self.P:
+            raise ValueError(f"the tape is full: {self.P} positions since reset()")
         if self.graph is not None:
             self.graph.replay()
         else:
             self._run_step()
+        self._steps += 1
 
     # ---- greedy generation (graph_decode.py:91-125) -----------------------------------
     @torch.no_grad()

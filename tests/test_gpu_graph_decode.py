@@ -206,3 +206,20 @@ def test_graph_decoder_bf16_vs_oracle():
         f"({int(decided.sum())} of {decided.numel()} positions decided by more than 2 max|dlogit|)")
     assert err < 2e-2
     assert bool(agree[decided].all())
+
+
+def test_graph_decoder_refuses_a_step_past_the_tape():
+    say("GraphDecoder: a step past P_max is refused")
+    cfg = _lm_cfg()
+    m, _ = _lm(cfg, torch.bfloat16)
+    dec = GraphDecoder(m, 2, 4).capture()
+    for _ in range(4):
+        dec.step()
+    with pytest.raises(ValueError):
+        dec.step()
+    torch.cuda.synchronize()
+    assert int(dec.pos.item()) == 4
+    dec.reset()
+    dec.step()
+    torch.cuda.synchronize()
+    assert int(dec.pos.item()) == 1
