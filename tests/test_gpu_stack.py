@@ -153,6 +153,8 @@ def _bufs_equal(a, b):
     (torch.bfloat16, "fusion", 3, 1, 128, 64, 4, 256, 2, True),
     (torch.bfloat16, "mult_res", 5, 8, 512, 64, 4, 1024, 16, True),
     (torch.bfloat16, "mult_res", 3, 2, 256, 64, 4, 2048, 16, True),
+    (torch.float32, "mult", 2, 2, 64, 64, 3, 256, 4, True),        # one cell
+    (torch.float32, "linear", 2, 2, 64, 8, 2, 256, 4, False),      # 8-row cells
 ])
 def test_wavefront_forward_equals_layer_by_layer(dtype, ctx_mod, n, B, T, c, K, d, h, tape):
     say(f"wavefront forward vs layer by layer: {dtype} {ctx_mod} L={n} B={B} T={T} c={c} K={K} d={d} h={h} "
