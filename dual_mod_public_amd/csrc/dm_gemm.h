@@ -478,7 +478,7 @@ DM_DEV void gemm_mainloop_dma(const SA& sa, const SB& sb, int K, int m0, int n0,
 // from two ds_read_b64_tr_b16 each: in a 16-lane group, lane s names the 8 bytes
 // at k-row 8g + s / 4 (+ 4), columns 4 (s % 4) .. + 3 of the fragment's 16 columns,
 // and receives that 4 x 16 block's column s; the swizzle puts the four k-rows'
-// chunks in different banks.
+// chunks in different banks (also separating k-rows 8 apart measured slower).
 template <int ROW> DM_DEV bf16x8 frag_kmajor(const char* stage, int k0, int c0) {
   const int lane = threadIdx.x & 63, g = lane >> 4, s = lane & 15;
   const int kr = k0 + 8 * g + (s >> 2);
@@ -527,6 +527,53 @@ DM_DEV void gemm_mainloop_dma_kk(const SA& sa, const SB& sb, int K, int m0, int 
                                        (lds_void_t*)(base + KS * ROWA + r0 * ROWB), 16, 0, 0);
     }
   };
+  if constexpr (S == 2 && KS == 64 && FM * FN >= 32) {
+    // Software-pipelined: the fragments of the next 32-k half are read while the MFMAs of the
+    // current half run (two register sets), across the stage boundary too, so the MFMAs never
+    // wait for LDS (the compiler's own interleaving of the reads and MFMAs: forced orders measured
+    // slower). Per stage kt: MFMAs of half 0 with the reads of half 1; then the wait for
+    // stage kt + 1's loads and for this wave's reads of stage kt, the barrier (stage kt free
+    // everywhere), the loads of stage kt + 2 into it; then MFMAs of half 1 with the reads of
+    // stage kt + 1's half 0. Each accumulator still sums its k in ascending order.
+    typename MF::frag a0[FM], b0[FN], a1[FM], b1[FN];
+    auto rd = [&](const char* st, int kk, typename MF::frag(&af)[FM], typename MF::frag(&bf)[FN]) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[i] = frag_kmajor<ROWA>(st, 32 * kk, wm * TM + 16 * i);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bf[j] = frag_kmajor<ROWB>(st + KS * ROWA, 32 * kk, wn * TN + 16 * j);
+    };
+    auto mm = [&](const typename MF::frag(&af)[FM], const typename MF::frag(&bf)[FN]) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = MF::mma(af[i], bf[j], acc[i][j]);
+    };
+    const int nk = K / KS;
+    if (nk <= 0) return;
+    issue(0, 0);
+    if (nk > 1) {
+      issue(1, 1);
+      wait_vm_lgkm0<L>();
+    } else {
+      wait_vm_lgkm0<0>();
+    }
+    __builtin_amdgcn_s_barrier();
+    rd(smem, 0, a0, b0);
+    for (int kt = 0; kt < nk - 1; ++kt) {
+      rd(smem + (kt & 1) * STAGE, 1, a1, b1);
+      mm(a0, b0);
+      wait_vm_lgkm0<0>();
+      __builtin_amdgcn_s_barrier();
+      if (kt + 2 < nk) issue(kt + 2, kt & 1);
+      rd(smem + ((kt + 1) & 1) * STAGE, 0, a0, b0);
+      mm(a1, b1);
+    }
+    rd(smem + ((nk - 1) & 1) * STAGE, 1, a1, b1);
+    mm(a0, b0);
+    mm(a1, b1);
+    __syncthreads();
+    return;
+  }
   // Per 32-k step the step's fragment reads go first, then its MFMAs (the reads of one fragment
   // otherwise sink to just before its MFMAs, each exposing the LDS latency).
   auto compute = [&](const char* As) {
