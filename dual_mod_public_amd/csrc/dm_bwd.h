@@ -1446,6 +1446,31 @@ static __global__ __launch_bounds__(256) void k_sum_splits(int S, long n, const 
   C[i] = accumulate ? C[i] + v : v;
 }
 
+// k_sum_splits on 4 consecutive elements per thread, the S slices' loads all in flight (the same
+// per-element order: 0 + slice 0 + slice 1 + ...)
+template <int S>
+static __global__ __launch_bounds__(256) void k_sum_splits4(long n4, const float4* __restrict__ part,
+                                                            float4* __restrict__ C, int accumulate) {
+  const long i = blockIdx.x * 256L + threadIdx.x;
+  if (i >= n4) return;
+  float4 p[S];
+#pragma unroll
+  for (int z = 0; z < S; ++z) p[z] = part[(long)z * n4 + i];
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int z = 0; z < S; ++z) {
+    v.x += p[z].x;
+    v.y += p[z].y;
+    v.z += p[z].z;
+    v.w += p[z].w;
+  }
+  if (accumulate) {
+    const float4 c = C[i];
+    v = make_float4(c.x + v.x, c.y + v.y, c.z + v.z, c.w + v.w);
+  }
+  C[i] = v;
+}
+
 static __global__ __launch_bounds__(256) void k_sum_rows_add(int nchunk, int ncols, int ld, const float* __restrict__ part,
                                                       float* __restrict__ out0, float* __restrict__ out1,
                                                       float* __restrict__ out2, int seg) {

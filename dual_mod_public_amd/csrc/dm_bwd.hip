@@ -51,8 +51,9 @@ template <typename T> struct BwdWs {
 constexpr int NSLOT_TM = 16;      // rows per norm_ctx-weight partial slot (k_du_epi block rows)
 constexpr int DU_SPLIT = DM_DU_SPLIT;   // split-K slices of the du GEMM
 constexpr int NCHUNK = 64;        // row chunks of the column sums
-// fp32 elements of the split-K partial buffer of the weight-grad GEMMs ([S, M, N], N = d)
-constexpr long KSPLIT_ELEMS(long d) { return 32 * d * d; }
+// fp32 elements of the split-K partial buffer of the weight-grad GEMMs ([S, M, N], N = d): eight
+// slices of the 6d x d projection product
+constexpr long KSPLIT_ELEMS(long d) { return 48 * d * d; }
 
 template <typename T>
 BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base) {
@@ -150,11 +151,26 @@ void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N
   const bool dma = sizeof(T) == 2 && K % 64 == 0 && M % 128 == 0 && N % 128 == 0;
   const bool big = dma && M % 256 == 0 && N % 256 == 0;
   const long blocks = big ? (long)(M / 256) * (N / 256) : (long)cdiv(M, 128) * cdiv(N, 128);
-  const long target = big ? 256 : 1024;
   int S = 1;
-  while (K % 64 == 0 && S < 16 && blocks * S * (big ? 1 : 2) < target + (big ? 0 : 1) &&
-         (long)S * 2 * M * N <= KSPLIT_ELEMS((long)N) && (K / 64) % (S * 2) == 0)
-    S *= 2;
+  if (big) {
+    // one 256 x 256 block per CU: a launch takes ceil(blocks S / 256) rounds of K / S each; take
+    // the fewest slices within 10% of the fewest rounds per unit of k (e.g. 384 tiles: 2 slices,
+    // 3 rounds of half the k instead of 2 rounds of all of it)
+    long num = cdiv(blocks, 256), den = 1;
+    for (int s2 = 2; s2 <= 16; s2 *= 2) {
+      if ((K / 64) % s2 != 0 || (long)s2 * M * N > KSPLIT_ELEMS((long)N)) break;
+      const long r = cdiv(blocks * s2, 256);
+      if (r * den * 10 < num * s2 * 9) {
+        num = r;
+        den = s2;
+      }
+    }
+    S = (int)den;
+  } else {
+    while (K % 64 == 0 && S < 16 && blocks * S * 2 < 1025 && (long)S * 2 * M * N <= KSPLIT_ELEMS((long)N) &&
+           (K / 64) % (S * 2) == 0)
+      S *= 2;
+  }
   SrcKMajor<T> sa{A, lda, M}, sb{Bm, ldb, N};
   sa.kmax = K;
   sb.kmax = K;
@@ -171,8 +187,20 @@ void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N
   } else {
     launch_gemm_splitk<T, 128, 128, 2, 2, 4>(sa, sb, M, N, K, S, ep, s);
   }
-  hipLaunchKernelGGL(k_sum_splits, dim3(cdiv((long)M * N, 256)), dim3(256), 0, s, S, (long)M * N,
-                     (const float*)part, C, accumulate);
+  const long n = (long)M * N;
+  if (n % 4 == 0 && reinterpret_cast<uintptr_t>(C) % 16 == 0 && reinterpret_cast<uintptr_t>(part) % 16 == 0 &&
+      (S == 2 || S == 4 || S == 8 || S == 16)) {
+    const long n4 = n / 4;
+    const dim3 g4(cdiv(n4, 256));
+    const float4* p4 = reinterpret_cast<const float4*>(part);
+    float4* c4 = reinterpret_cast<float4*>(C);
+    if (S == 2) hipLaunchKernelGGL(k_sum_splits4<2>, g4, dim3(256), 0, s, n4, p4, c4, accumulate);
+    else if (S == 4) hipLaunchKernelGGL(k_sum_splits4<4>, g4, dim3(256), 0, s, n4, p4, c4, accumulate);
+    else if (S == 8) hipLaunchKernelGGL(k_sum_splits4<8>, g4, dim3(256), 0, s, n4, p4, c4, accumulate);
+    else hipLaunchKernelGGL(k_sum_splits4<16>, g4, dim3(256), 0, s, n4, p4, c4, accumulate);
+  } else {
+    hipLaunchKernelGGL(k_sum_splits, dim3(cdiv(n, 256)), dim3(256), 0, s, S, n, (const float*)part, C, accumulate);
+  }
 }
 
 // The backward of one layer in three parts, as the reference's fused engine splits it
