@@ -133,6 +133,14 @@ void run_proj_src(const dm_config* c, const dm_packed* w, const SA& sa, int M, i
       return;
     }
   }
+  if (M <= 64) {
+    // a decode step's few rows: 64-row blocks, one head wide (twice the blocks of 128 x 128)
+    if constexpr (DH == 64)
+      launch_gemm_auto<T, 64, 64, 2, 2, 3, 4>(sa, sb, M, nseg * c->d, c->d, epi, s, PROF_PROJ);
+    else
+      launch_gemm_auto<T, 64, 128, 2, 2, 3, 4>(sa, sb, M, nseg * c->d, c->d, epi, s, PROF_PROJ);
+    return;
+  }
   if constexpr (DH == 64)
     launch_gemm_auto<T, 128, 128, 2, 2, 3, 4>(sa, sb, M, nseg * c->d, c->d, epi, s, PROF_PROJ);
   else

@@ -400,7 +400,9 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
     SrcRows<T> ao{(const T*)a->o_cat, d, B};
     SrcRows<T> bo{(const T*)w->wo, d, d};
     EpiResidual<T> ep{B, d, nullptr, (T*)a->y};
-    launch_gemm_auto<T, 64, 128, 2, 2, 3, 4>(ao, bo, B, d, d, ep, s);
+    // one row block: 64 x 32 tiles give d / 32 blocks
+    if (B <= 64) launch_gemm_auto<T, 64, 32, 4, 1, 3, 4>(ao, bo, B, d, d, ep, s);
+    else launch_gemm_auto<T, 64, 128, 2, 2, 3, 4>(ao, bo, B, d, d, ep, s);
   }
   return DM_OK;
 }
