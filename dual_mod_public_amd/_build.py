@@ -17,7 +17,7 @@ CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libdm_hip.so")
 SOURCES = ["dm_lib.hip", "dm_bwd.hip", "dm_stack.hip"]
 HEADERS = ["dm_common.h", "dm_group.h", "dm_gemm.h", "dm_attn.h", "dm_kernels.h", "dm_decode.h", "dm_bwd.h", "dm_host.h",
-           "dm_fwd_host.h", "dm_prof.h", "../../include/dm_abi.h"]
+           "dm_fwd_host.h", "dm_mlp.h", "dm_prof.h", "../../include/dm_abi.h"]
 
 
 def hipcc():

@@ -149,6 +149,7 @@ SIGNATURES = {
     "dm_stack_bwd": (ctypes.c_int, [P(dm_config), c_i32, P(dm_stack_bwd_layer), c_fp, c_fp, P(c_i32), c_i32, c_i32,
                                     c_vp, ctypes.c_size_t, c_i32, c_vp]),
     "dm_residual_rmsnorm": (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, ctypes.c_float, c_vp]),
+    "dm_swiglu_rows": (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp]),
     "dm_gemm": (ctypes.c_int, [c_i32, c_i32, c_i32, c_vp, c_vp, c_fp, c_i32, c_i32, c_i32, c_i32,
                                c_vp]),
     "dm_check_schedule": (ctypes.c_int, [P(c_i32), c_i32, c_i32]),
@@ -284,6 +285,38 @@ def residual_rmsnorm(x, delta=None, w=None, dtype=torch.bfloat16, y=None, eps=1e
                                     ptr(w) if w is not None else None, ptr(y) if w is not None else None, M, d,
                                     float(eps), stream_ptr()))
     return y if w is not None else None
+
+
+MLP_ROWS = 16   # rows dm_swiglu_rows takes per call
+
+
+def swiglu_rows_ok(x, w1, w2):
+    """Whether dm_swiglu_rows takes this product: bf16, at most MLP_ROWS rows, d a multiple of
+    128 and H of 32."""
+    d = x.shape[-1]
+    M = x.numel() // d
+    H = w1.shape[0]
+    return x.dtype == torch.bfloat16 and 1 <= M <= MLP_ROWS and d % 128 == 0 and H % 32 == 0
+
+
+def swiglu_rows(x, w1, w3, w2, act=None, out=None):
+    """(silu(x w1^T) * (x w3^T)) w2^T through dm_swiglu_rows (models/dualmod/model.py:102-112 on
+    a decode step's rows): x [.., d] bf16 with at most MLP_ROWS rows, w1 / w3 [H, d], w2 [d, H]
+    bf16 contiguous; act [M, H] / out (shape of x) optional preallocated buffers."""
+    d = x.shape[-1]
+    M = x.numel() // d
+    H = w1.shape[0]
+    assert x.is_contiguous() and w1.is_contiguous() and w3.is_contiguous() and w2.is_contiguous()
+    assert w1.shape == (H, d) and w3.shape == (H, d) and w2.shape == (d, H)
+    assert x.dtype == w1.dtype == w3.dtype == w2.dtype
+    if act is None:
+        act = torch.empty(M, H, device=x.device, dtype=x.dtype)
+    if out is None:
+        out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
+    assert act.is_contiguous() and act.numel() >= M * H and out.is_contiguous() and out.numel() == x.numel()
+    check(lib().dm_swiglu_rows(dtype_code(x.dtype), ptr(x), ptr(w1), ptr(w3), ptr(w2), ptr(act), ptr(out), M, d, H,
+                               stream_ptr()))
+    return out
 
 
 def make_config(cfg, B, dtype):

@@ -5,6 +5,7 @@
 // and launch sequencing. Never allocates device memory, never synchronizes.
 #include "dm_decode.h"
 #include "dm_fwd_host.h"
+#include "dm_mlp.h"
 
 #include <mutex>
 #include <vector>
@@ -642,6 +643,24 @@ int dm_linear(int32_t dtype, const void* x, const void* W, const void* r, void* 
   } else {
     return fail(DM_ERR_INVALID, "dtype %d", dtype);
   }
+  DM_HIP(hipGetLastError());
+  return DM_OK;
+}
+
+int dm_swiglu_rows(int32_t dtype, const void* x, const void* w1, const void* w3, const void* w2, void* act,
+                   void* out, int32_t M, int32_t d, int32_t H, void* stream) {
+  DM_REQUIRE(x && w1 && w3 && w2 && act && out, DM_ERR_INVALID, "null operand");
+  DM_REQUIRE(dtype == DM_BF16, DM_ERR_UNSUPPORTED, "dm_swiglu_rows: bf16 only (dtype %d)", dtype);
+  DM_REQUIRE(M >= 1 && M <= MLP_ROWS, DM_ERR_INVALID, "M=%d (1..%d rows)", M, MLP_ROWS);
+  DM_REQUIRE(d > 0 && H > 0 && d % 128 == 0 && H % 32 == 0, DM_ERR_INVALID,
+             "d=%d H=%d (d a multiple of 128, H of 32)", d, H);
+  DM_REQUIRE(aligned16(x) && aligned16(w1) && aligned16(w3) && aligned16(w2) && aligned16(act), DM_ERR_INVALID,
+             "operands must be 16-byte aligned");
+  hipStream_t s = S(stream);
+  hipLaunchKernelGGL(k_swiglu_up<bf16>, dim3(H / 16), dim3(256), 0, s, (const bf16*)x, (const bf16*)w1,
+                     (const bf16*)w3, (bf16*)act, M, d, H);
+  hipLaunchKernelGGL(k_swiglu_down<bf16>, dim3(d / 16), dim3(512), 0, s, (const bf16*)act, (const bf16*)w2,
+                     (bf16*)out, M, d, H);
   DM_HIP(hipGetLastError());
   return DM_OK;
 }

@@ -43,6 +43,9 @@ class GraphDecoder:
         self._mlp = [tuple(torch.empty_like(w, dtype=self.dt) for w in
                            (blk.mlp.w1.weight, blk.mlp.w3.weight, blk.mlp.w2.weight)) for blk in model.blocks]
         self._head = torch.empty_like(model.lm_head.weight, dtype=self.dt)
+        # the MLP's intermediate and output rows (dm_swiglu_rows), at fixed addresses
+        self._act = torch.empty(B, cfg.mlp_hidden, device=self.dev, dtype=self.dt)
+        self._mo = torch.empty(B, 1, cfg.d_model, device=self.dev, dtype=self.dt)
         self._ver = None
         self.graph = None
         self._steps = 0
@@ -71,10 +74,10 @@ class GraphDecoder:
         for l, (blk, tape, (w1, w3, w2)) in enumerate(zip(blocks, self.tapes, self._mlp)):
             _, y = tape.step(h.view(B, d), self.pos, self.cos, self.sin, with_wo=True)
             h = L.residual_rmsnorm(x, y, blk.mlp_norm.weight, dt, eps=blk.mlp_norm.eps)
-            mo = F.linear(F.silu(F.linear(h, w1)) * F.linear(h, w3), w2)
+            mo = blk.mlp.decode(h, (w1, w3, w2), act=self._act, out=self._mo)
             # the MLP's residual add fused with the next norm (the next block's attn_norm, or norm_f)
             nrm = blocks[l + 1].attn_norm if l + 1 < len(blocks) else m.norm_f
-            h = L.residual_rmsnorm(x, mo.contiguous(), nrm.weight, dt, eps=nrm.eps)
+            h = L.residual_rmsnorm(x, mo, nrm.weight, dt, eps=nrm.eps)
         lg = F.linear(h, self._head)                                    # [B, 1, V]
         self.logits.copy_(lg.float())
         L.check(L.lib().dm_argmax_rows(L.dtype_code(self.dt), L.ptr(lg), B, self.vocab, self.vocab,

@@ -37,6 +37,16 @@ class SwiGLU(nn.Module):
     def forward(self, x):
         return _lin(F.silu(_lin(x, self.w1.weight)) * _lin(x, self.w3.weight), self.w2.weight)
 
+    def decode(self, h, w=None, act=None, out=None):
+        """The MLP on a decode step's rows h [B, 1, d] (compute dtype, contiguous): dm_swiglu_rows
+        where it applies (bf16, B <= 16), else the forward's torch products. w = (w1, w3, w2) in
+        h's dtype (default: cast from the parameters); act / out optional static buffers."""
+        if w is None:
+            w = tuple(p.to(h.dtype).contiguous() for p in (self.w1.weight, self.w3.weight, self.w2.weight))
+        if L.swiglu_rows_ok(h, w[0], w[2]):
+            return L.swiglu_rows(h, w[0], w[1], w[2], act=act, out=out)
+        return F.linear(F.silu(F.linear(h, w[0])) * F.linear(h, w[1]), w[2]).contiguous()
+
 
 class Block(nn.Module):
     """model.py:115-131: x + attn(attn_norm x), then x + mlp(mlp_norm x)."""
@@ -60,7 +70,7 @@ class Block(nn.Module):
         h = L.residual_rmsnorm(x, None, self.attn_norm.weight, dtype, eps=self.attn_norm.eps)
         y = self.attn.decode_step(h, pos, cache, cos, sin)
         h = L.residual_rmsnorm(x, y, self.mlp_norm.weight, dtype, eps=self.mlp_norm.eps)
-        L.residual_rmsnorm(x, self.mlp(h).contiguous(), None, dtype)
+        L.residual_rmsnorm(x, self.mlp.decode(h), None, dtype)
         return x
 
 

@@ -417,6 +417,16 @@ int dm_linear(int32_t dtype, const void* x, const void* W, const void* r, void* 
 int dm_residual_rmsnorm(int32_t dtype, float* x, const void* delta, const float* w, void* y, int32_t M,
                         int32_t d, float eps, void* stream);
 
+/* ---- SwiGLU MLP of a decode step ---------------------------------------------------
+ * out[M, d] = (silu(x W1^T) * (x W3^T)) W2^T, the Block's MLP (models/dualmod/model.py:
+ * 102-112) on a decode step's rows (one token per sequence, M <= 16): bf16 x [M, d],
+ * w1 / w3 [H, d], w2 [d, H], act [M, H] the caller's intermediate buffer, out [M, d]. The
+ * products accumulate in fp32; act holds silu(g) * u rounded once to bf16. Deterministic
+ * (fixed-order in-block sums). d must be a multiple of 128, H of 32, the operands 16-byte
+ * aligned; DM_ERR_UNSUPPORTED for a dtype other than bf16. */
+int dm_swiglu_rows(int32_t dtype, const void* x, const void* w1, const void* w3, const void* w2, void* act,
+                   void* out, int32_t M, int32_t d, int32_t H, void* stream);
+
 /* ---- row argmax ------------------------------------------------------------------
  * out[r] = the first index of the maximum of x[r, 0:cols) (row stride ld elements),
  * storage dtype bf16 or fp32: the greedy pick of lm/eval/graph_decode.py:62

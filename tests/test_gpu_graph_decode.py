@@ -223,3 +223,25 @@ def test_graph_decoder_refuses_a_step_past_the_tape():
     dec.step()
     torch.cuda.synchronize()
     assert int(dec.pos.item()) == 1
+
+
+@pytest.mark.parametrize("M,d,H", [(1, 256, 512), (8, 1024, 2816), (16, 512, 1376), (5, 128, 96)])
+def test_swiglu_rows_matches_fp32_reference(M, d, H):
+    """dm_swiglu_rows (the decode step's MLP, models/dualmod/model.py:102-112) against the same
+    products in fp32 on the bf16 inputs: act rounded once to bf16, so the bound is bf16's."""
+    g = torch.Generator().manual_seed(M * 1000 + d + H)
+    x = torch.randn(M, 1, d, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(H, d, generator=g) * d ** -0.5).to(torch.bfloat16)
+    w3 = (torch.randn(H, d, generator=g) * d ** -0.5).to(torch.bfloat16)
+    w2 = (torch.randn(d, H, generator=g) * H ** -0.5).to(torch.bfloat16)
+    xf, w1f, w3f, w2f = (t.float() for t in (x, w1, w3, w2))
+    ref = (torch.nn.functional.silu(xf @ w1f.T) * (xf @ w3f.T)) @ w2f.T
+    act = torch.full((M, H), float("nan"), device=DEV, dtype=torch.bfloat16)
+    out = L.swiglu_rows(x.to(DEV), w1.to(DEV), w3.to(DEV), w2.to(DEV), act=act)
+    assert out.shape == x.shape and out.dtype == torch.bfloat16
+    err = relerr(out.float().cpu(), ref)
+    record(f"swiglu_rows M={M} d={d} H={H}", {"out": err}, 1e-2)
+    assert err < 1e-2, err
+    # deterministic: a second call gives the same bits
+    out2 = L.swiglu_rows(x.to(DEV), w1.to(DEV), w3.to(DEV), w2.to(DEV))
+    assert torch.equal(out, out2)
