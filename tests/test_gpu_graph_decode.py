@@ -137,12 +137,14 @@ def test_lm_decode_and_forward_match_oracle_fp32():
     assert e_dec < 1e-5 and e_fwd < 1e-5
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_graph_decoder_equals_eager(dtype):
-    say(f"GraphDecoder replays vs eager decode_step, {dtype}")
+# bf16 at B = 3 takes the MLP through dm_swiglu_rows, B = 17 (more rows than it takes) and fp32
+# through torch's products
+@pytest.mark.parametrize("dtype,B", [(torch.float32, 3), (torch.bfloat16, 3), (torch.bfloat16, 17)])
+def test_graph_decoder_equals_eager(dtype, B):
+    say(f"GraphDecoder replays vs eager decode_step, {dtype}, B={B}")
     cfg = _lm_cfg()
     m, _ = _lm(cfg, dtype)
-    B, T = 3, 40
+    T = 40
     idx = _tokens(cfg, B, T, seed=4).to(DEV)
     dec = GraphDecoder(m, B, 48).capture()
     caches = m.decode_init()
