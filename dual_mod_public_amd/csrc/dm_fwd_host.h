@@ -120,11 +120,22 @@ inline const float* v_gain(const dm_config* c, const dm_packed* w) {
 template <typename T, int DH, class SA>
 void run_proj_src(const dm_config* c, const dm_packed* w, const SA& sa, int M, int Tl, int Tbuf, int buf_t0,
                   int rope_t0, const float* cos, const float* sin, T* qr, T* kraw, T* kself, T* vraw, T* vpre,
-                  float* glogx, float* sig, hipStream_t s, bool small_tiles = false) {
+                  float* glogx, float* sig, hipStream_t s, bool small_tiles = false, const int* pos_dev = nullptr,
+                  int pos_cap = 0) {
   const int nseg = (c->ctx_mod == DM_CTX_LINEAR) ? 5 : 6;
+  SrcRows<T> sb{(const T*)w->w_proj, c->d, nseg * c->d};
+  if (pos_dev != nullptr) {
+    // a decode step at a device position (M <= 64 rows): the RoPE row read from device memory
+    EpiProj<T, DH, true> epi{M, c->d, c->h, Tl, Tbuf, buf_t0, 0, cos, sin, w->b_proj, qr, kraw, kself, vraw,
+                             glogx, sig, c->ctx_mod == DM_CTX_FUSION, v_gain(c, w), vpre, pos_dev, pos_cap};
+    if constexpr (DH == 64)
+      launch_gemm_auto<T, 64, 64, 2, 2, 3, 4>(sa, sb, M, nseg * c->d, c->d, epi, s, PROF_PROJ);
+    else
+      launch_gemm_auto<T, 64, 128, 2, 2, 3, 4>(sa, sb, M, nseg * c->d, c->d, epi, s, PROF_PROJ);
+    return;
+  }
   EpiProj<T, DH> epi{M, c->d, c->h, Tl, Tbuf, buf_t0, rope_t0, cos, sin, w->b_proj,
                      qr, kraw, kself, vraw, glogx, sig, c->ctx_mod == DM_CTX_FUSION, v_gain(c, w), vpre};
-  SrcRows<T> sb{(const T*)w->w_proj, c->d, nseg * c->d};
   // bf16, whole 256-row / 256-column tiles: 256 x 256 blocks (four 128 x 128 wave tiles,
   // two direct-to-LDS stages); otherwise 128 x 128 with wave tiles spanning whole heads
   if constexpr (sizeof(T) == 2) {
@@ -150,9 +161,9 @@ void run_proj_src(const dm_config* c, const dm_packed* w, const SA& sa, int M, i
 template <typename T, int DH>
 void run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int Tl, int Tbuf, int buf_t0,
               int rope_t0, const float* cos, const float* sin, T* qr, T* kraw, T* kself, T* vraw, T* vpre,
-              float* glogx, float* sig, hipStream_t s) {
+              float* glogx, float* sig, hipStream_t s, const int* pos_dev = nullptr, int pos_cap = 0) {
   run_proj_src<T, DH>(c, w, SrcRows<T>{xhat, c->d, M}, M, Tl, Tbuf, buf_t0, rope_t0, cos, sin, qr, kraw, kself, vraw,
-                      vpre, glogx, sig, s);
+                      vpre, glogx, sig, s, false, pos_dev, pos_cap);
 }
 
 template <typename T>
@@ -195,6 +206,11 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
     EpiSweep1<T, DH, 2> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
                            Kout, Vout, out_stride, out_row0, vin, gvu, save1};
     launch_gemm_auto<T, 64, 128, 2, 2, SW1_STAGES, 4>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
+  } else if (g.pos_dev != nullptr) {
+    // a decode step at a device position: RoPE row and output row read from device memory
+    EpiSweep1<T, DH, 1, true> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
+                                 Kout, Vout, out_stride, out_row0, vin, gvu, save1};
+    launch_gemm_auto<T, 64, 64, 2, 2, SW1_STAGES, 4>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
   } else {
     EpiSweep1<T, DH> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
                         Kout, Vout, out_stride, out_row0, vin, gvu, save1};
@@ -229,11 +245,19 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
   if (!linear) {
     SrcRows<T> av{vin, c->d, N};
     SrcRows<T> bv{(const T*)w->w_vctx, c->d, c->d};
-    EpiSweep2<T, DH> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2};
-    if constexpr (SW2_STAGES > 0)
-      launch_gemm_auto<T, 64, 32, 4, 1, SW2_STAGES, 8>(av, bv, N, c->d, c->d, e2, s, PROF_SWEEP2);
-    else
-      launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, c->d, c->d, e2, s, PROF_SWEEP2);
+    if (g.pos_dev != nullptr) {   // device position (see GEMM 1)
+      EpiSweep2<T, DH, true> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2};
+      if constexpr (SW2_STAGES > 0)
+        launch_gemm_auto<T, 64, 32, 4, 1, SW2_STAGES, 8>(av, bv, N, c->d, c->d, e2, s, PROF_SWEEP2);
+      else
+        launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, c->d, c->d, e2, s, PROF_SWEEP2);
+    } else {
+      EpiSweep2<T, DH> e2{g, N, vraw, glogx, gvu, Vout, out_stride, out_row0, save2};
+      if constexpr (SW2_STAGES > 0)
+        launch_gemm_auto<T, 64, 32, 4, 1, SW2_STAGES, 8>(av, bv, N, c->d, c->d, e2, s, PROF_SWEEP2);
+      else
+        launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, c->d, c->d, e2, s, PROF_SWEEP2);
+    }
   }
   // v'' entry-norm clamp of the refined value rows (v_clamp_tau > 0 only)
   if (g.v_clamp_tau > 0.f) {

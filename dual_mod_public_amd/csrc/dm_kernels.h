@@ -215,7 +215,13 @@ template <typename T> struct RmsRowsBody {
 // DH). q / k / v heads: DH / 8 lanes per row, each with 4 consecutive RoPE pairs (jj, jj + DH/2);
 // gate / v_gate columns: DH / 4 lanes per row, 4 consecutive columns each.
 // ---------------------------------------------------------------------------
-template <typename T, int DH> struct EpiProj {
+// a decode step's device position (graph replay), clamped to [0, cap) as the decode kernels do
+DM_DEV int dev_position(const int* pos_dev, int cap) {
+  const int p = *pos_dev;
+  return p < 0 ? 0 : (p >= cap ? cap - 1 : p);
+}
+
+template <typename T, int DH, bool DEVPOS = false> struct EpiProj {
   int M, d, h;
   int Tl;        // rows per batch element in this call
   int Tbuf;      // T of the destination head buffers
@@ -231,6 +237,8 @@ template <typename T, int DH> struct EpiProj {
   // r = rsqrt(mean x^2 + 1e-6); vgain [h] fp32 (nullptr = off); vpre keeps x (nullptr = not kept)
   const float* __restrict__ vgain = nullptr;
   T* __restrict__ vpre = nullptr;
+  const int* pos_dev = nullptr;   // DEVPOS: RoPE row of local row 0 = *pos_dev clamped to [0, pos_cap)
+  int pos_cap = 0;
 
   static constexpr int TILE_ROWS = 64;
   struct TilePre {};
@@ -277,7 +285,8 @@ template <typename T, int DH> struct EpiProj {
       const int bb = m / Tl, t = m - bb * Tl;
       const long hrow = (((long)bb * h + hh) * Tbuf + buf_t0 + t) * DH + jj;
       if (seg <= 1) {
-        const long rrow = (long)(rope_t0 + t) * (DH / 2) + jj;
+        const int r0 = DEVPOS ? dev_position(pos_dev, pos_cap) : rope_t0;
+        const long rrow = (long)(r0 + t) * (DH / 2) + jj;
         float c[4], s[4], o1[4], o2[4];
         unpackf4(ld_global<floatx4>(cos + rrow), c);
         unpackf4(ld_global<floatx4>(sin + rrow), s);
@@ -357,6 +366,10 @@ struct CellGeom {
   int rope_t0 = -1;    // RoPE table row of chunk row 0 (-1: pos0, tables indexed by position)
   int window = 0;      // local_window W (a row at position i reads keys >= i - W + 1); 0 = none.
                        // The cell kernels take W > c: only the committed prefix is windowed
+  // a decode step at a device position (graph replay): the epilogues instantiated for it read
+  // the position here, clamped to [0, pos_cap), as their RoPE row and output row
+  const int* pos_dev = nullptr;
+  int pos_cap = 0;
 };
 // RoPE table row of chunk row p
 DM_DEV int rope_row(const CellGeom& g, int p) { return (g.rope_t0 < 0 ? g.pos0 : g.rope_t0) + p; }
@@ -742,7 +755,7 @@ template <typename T, int DH, int NW> struct AttendBody {
 //          [3d, 4d) g_v(u)   -> fp32 scratch for GEMM 2
 // save != nullptr stores the raw GEMM outputs [rows, 4d] in this packed order.
 // ---------------------------------------------------------------------------
-template <typename T, int DH, int NG = 1> struct EpiSweep1 {
+template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 {
   CellGeom g;
   int M, ctx_mod;
   float lam;
@@ -788,7 +801,7 @@ template <typename T, int DH, int NG = 1> struct EpiSweep1 {
     const int d = g.d, h = g.h;
     const int m = min(m0 + r, M - 1);
     const int b = m / g.c, p = m - b * g.c;
-    const int t = g.buf_t0 + p, pos = rope_row(g, p);
+    const int t = g.buf_t0 + p, pos = DEVPOS ? dev_position(g.pos_dev, g.pos_cap) + p : rope_row(g, p);
     const long xrow = (long)b * g.Tbuf + t;
     // The (block-uniform) branches only pick addresses; the loads follow them
     // unconditionally (unused slots re-read a valid address), so no loaded value
@@ -917,6 +930,7 @@ template <typename T, int DH, int NG = 1> struct EpiSweep1 {
     }
     if (m >= M) return;
     const int b = m / g.c, p = m - b * g.c;
+    const int orow0 = DEVPOS ? dev_position(g.pos_dev, g.pos_cap) : out_row0;
     if (n0 < 2 * d) {
       float gxa[4], gxb[4], cs[4], sn[4], ka[4], kb[4];
       unpackf4(pr.f[0], gxa); unpackf4(pr.f[1], gxb); unpackf4(pr.f[2], cs); unpackf4(pr.f[3], sn);
@@ -934,7 +948,7 @@ template <typename T, int DH, int NG = 1> struct EpiSweep1 {
         o1[i] = k1 * cs[i] - k2 * sn[i];
         o2[i] = k2 * cs[i] + k1 * sn[i];
       }
-      T* crow = Kout + ((long)b * h + hd) * out_stride + (long)(out_row0 + p) * DH + jj;
+      T* crow = Kout + ((long)b * h + hd) * out_stride + (long)(orow0 + p) * DH + jj;
       st4<T>(crow, o1);
       st4<T>(crow + DH / 2, o2);
     } else if (ctx_mod == 0) {
@@ -944,7 +958,7 @@ template <typename T, int DH, int NG = 1> struct EpiSweep1 {
       if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
       const int cl = n0 - 2 * d;
       const int hd = cl / (2 * DH), e = 32 * ((cl % (2 * DH)) / 64) + lc0;
-      T* crow = Vout + ((long)b * h + hd) * out_stride + (long)(out_row0 + p) * DH + e;
+      T* crow = Vout + ((long)b * h + hd) * out_stride + (long)(orow0 + p) * DH + e;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         float v[4];
@@ -994,7 +1008,7 @@ template <typename T, int DH, int NG = 1> struct EpiSweep1 {
 // v'' = g_v v_raw + (1 - g_v) v_ctx -> V rows. save2 stores raw v_ctx [rows, d].
 // Block tile 64 x 32: thread t owns row t / 4, columns 8 (t % 4) .. + 7 (inputs
 // gathered before the k-loop).
-template <typename T, int DH> struct EpiSweep2 {
+template <typename T, int DH, bool DEVPOS = false> struct EpiSweep2 {
   CellGeom g;
   int M;
   const T* __restrict__ vraw;
@@ -1046,7 +1060,8 @@ template <typename T, int DH> struct EpiSweep2 {
     float v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = value_blend(g, col + i, sigmoidf_(gx[i] + gu[i]), vr[i], a[i]);
-    store_vec<T, 8>(Vout + ((long)b * g.h + hd) * out_stride + (long)(out_row0 + p) * DH + e, v);
+    const int orow0 = DEVPOS ? dev_position(g.pos_dev, g.pos_cap) : out_row0;
+    store_vec<T, 8>(Vout + ((long)b * g.h + hd) * out_stride + (long)(orow0 + p) * DH + e, v);
     if (save2 != nullptr) store_vec_nt<T, 8>(save2 + (long)m * g.d + col, a);
   }
 };

@@ -358,16 +358,22 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
   const bool dev_pos = a->pos_dev != nullptr;
   const int pos = dev_pos ? 0 : a->pos;
   const int lo = (c->local_window > 0 && pos > c->local_window - 1) ? pos - (c->local_window - 1) : 0;
+  // device position without per-head context norms or the v'' clamp: the projection and refine
+  // epilogues read the position themselves (RoPE rows of the full tables, the refined pair written
+  // straight into tape slot pos); otherwise the RoPE rows are gathered and the pair staged first
+  const bool dev_direct = dev_pos && kctx_gain(c, w) == nullptr && vctx_gain(c, w) == nullptr &&
+                          c->v_clamp_tau <= 0.f;
   const float* rc = cos;
   const float* rs = sin;
-  if (dev_pos) {
+  if (dev_pos && !dev_direct) {
     hipLaunchKernelGGL(k_decode_pos_rope, dim3(1), dim3(64), 0, s, a->pos_dev, a->tape_T, cos, sin, DH / 2,
                        ws.rope);
     rc = ws.rope;
     rs = ws.rope + DH / 2;
   }
   run_proj<T, DH>(c, w, (const T*)a->xhat, B, 1, 1, 0, dev_pos ? 0 : pos, rc, rs, (T*)ws.q, (T*)ws.kraw,
-                  (T*)ws.kself, (T*)ws.vraw, nullptr, ws.glogx, ws.sig, s);
+                  (T*)ws.kself, (T*)ws.vraw, nullptr, ws.glogx, ws.sig, s,
+                  dev_direct ? (const int*)a->pos_dev : nullptr, a->tape_T);
   const int nsplit = dev_pos ? cdiv(a->tape_T, DEC_SPLIT) : (pos > lo ? cdiv(pos - lo, DEC_SPLIT) : 0);
   DecodeArgs<T> da{B, h, d, a->tape_T, pos, lo, DEC_SPLIT, nsplit, 1.0f / sqrtf((float)DH),
                    (const T*)ws.q, (const T*)ws.kself, (const T*)ws.vraw, (const T*)a->K_tape,
@@ -387,7 +393,14 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
   g.kmod_mode = c->kmod_mode;
   g.v_clamp_tau = c->v_clamp_tau;
   ProfScope pr(PROF_DEC_REFINE, s);
-  if (dev_pos) {
+  if (dev_direct) {
+    g.pos_dev = (const int*)a->pos_dev;
+    g.pos_cap = a->tape_T;
+    g.cache_T = a->tape_T;
+    run_refine<T, DH>(c, w, g, B, (const T*)a->o_cat, ws.ssq, (const T*)ws.kraw, (const T*)ws.vraw, ws.glogx,
+                      ws.sig, cos, sin, (T*)a->K_tape, (T*)a->V_tape, (long)a->tape_T * DH, 0, (T*)ws.vin, ws.gvu,
+                      nullptr, nullptr, s);
+  } else if (dev_pos) {
     run_refine<T, DH>(c, w, g, B, (const T*)a->o_cat, ws.ssq, (const T*)ws.kraw, (const T*)ws.vraw, ws.glogx,
                       ws.sig, rc, rs, (T*)ws.kst, (T*)ws.vst, (long)DH, 0, (T*)ws.vin, ws.gvu, nullptr, nullptr, s);
     hipLaunchKernelGGL((k_decode_commit<T, DH>), dim3(B * h), dim3(DH), 0, s, (const int*)a->pos_dev, a->tape_T,
