@@ -54,11 +54,16 @@ def _tokens(cfg, B, T, seed=3):
     return torch.randint(0, cfg.vocab_size, (B, T), generator=torch.Generator().manual_seed(seed))
 
 
-@pytest.mark.parametrize("dtype,P0,W", [(torch.float32, 0, 0), (torch.bfloat16, 1500, 0), (torch.bfloat16, 700, 300),
-                                        (torch.float32, 40, 8)])
-def test_device_position_equals_host_position(dtype, P0, W):
-    say(f"device-position decode vs host position dtype={dtype} P0={P0} W={W}")
-    cfg = cfg_of(d=256, h=4, T=P0 + 8, local_window=W)
+# the knob cases: linear and fusion write V rows from other epilogue branches; a k_ctx norm or the
+# v'' clamp take the staged path (RoPE rows gathered, refined pair committed by its own kernel)
+@pytest.mark.parametrize("dtype,P0,W,knobs", [
+    (torch.float32, 0, 0, {}), (torch.bfloat16, 1500, 0, {}), (torch.bfloat16, 700, 300, {}),
+    (torch.float32, 40, 8, {}), (torch.bfloat16, 600, 0, {"ctx_mod": "linear"}),
+    (torch.bfloat16, 600, 0, {"ctx_mod": "fusion"}), (torch.bfloat16, 600, 0, {"k_ctx_norm": "rms"}),
+    (torch.float32, 40, 0, {"v_clamp_tau": 0.5})])
+def test_device_position_equals_host_position(dtype, P0, W, knobs):
+    say(f"device-position decode vs host position dtype={dtype} P0={P0} W={W} {knobs}")
+    cfg = cfg_of(d=256, h=4, T=P0 + 8, local_window=W, **knobs)
     B, steps = 3, 4
     P = P0 + steps
     sd, x, _, (c32, s32) = setup(cfg, B, P)
