@@ -287,7 +287,7 @@ def residual_rmsnorm(x, delta=None, w=None, dtype=torch.bfloat16, y=None, eps=1e
     return y if w is not None else None
 
 
-MLP_ROWS = 16   # rows dm_swiglu_rows takes per call
+MLP_ROWS = 64   # rows dm_swiglu_rows takes per call
 
 
 def swiglu_rows_ok(x, w1, w2):

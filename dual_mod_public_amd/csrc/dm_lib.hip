@@ -670,10 +670,18 @@ int dm_swiglu_rows(int32_t dtype, const void* x, const void* w1, const void* w3,
   DM_REQUIRE(aligned16(x) && aligned16(w1) && aligned16(w3) && aligned16(w2) && aligned16(act), DM_ERR_INVALID,
              "operands must be 16-byte aligned");
   hipStream_t s = S(stream);
-  hipLaunchKernelGGL(k_swiglu_up<bf16>, dim3(H / 16), dim3(256), 0, s, (const bf16*)x, (const bf16*)w1,
-                     (const bf16*)w3, (bf16*)act, M, d, H);
-  hipLaunchKernelGGL(k_swiglu_down<bf16>, dim3(d / 16), dim3(512), 0, s, (const bf16*)act, (const bf16*)w2,
-                     (bf16*)out, M, d, H);
+  auto run = [&](auto rt) {
+    constexpr int RT = decltype(rt)::value;
+    hipLaunchKernelGGL((k_swiglu_up<bf16, RT>), dim3(H / 16), dim3(256), 0, s, (const bf16*)x, (const bf16*)w1,
+                       (const bf16*)w3, (bf16*)act, M, d, H);
+    hipLaunchKernelGGL((k_swiglu_down<bf16, RT>), dim3(d / 16), dim3(512), 0, s, (const bf16*)act,
+                       (const bf16*)w2, (bf16*)out, M, d, H);
+  };
+  const int rts = (M + 15) / 16;
+  if (rts == 1) run(std::integral_constant<int, 1>{});
+  else if (rts == 2) run(std::integral_constant<int, 2>{});
+  else if (rts == 3) run(std::integral_constant<int, 3>{});
+  else run(std::integral_constant<int, 4>{});
   DM_HIP(hipGetLastError());
   return DM_OK;
 }

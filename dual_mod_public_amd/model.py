@@ -39,7 +39,7 @@ class SwiGLU(nn.Module):
 
     def decode(self, h, w=None, act=None, out=None):
         """The MLP on a decode step's rows h [B, 1, d] (compute dtype, contiguous): dm_swiglu_rows
-        where it applies (bf16, B <= 16), else the forward's torch products. w = (w1, w3, w2) in
+        where it applies (bf16, B <= 64), else the forward's torch products. w = (w1, w3, w2) in
         h's dtype (default: cast from the parameters); act / out optional static buffers."""
         if w is None:
             w = tuple(p.to(h.dtype).contiguous() for p in (self.w1.weight, self.w3.weight, self.w2.weight))

@@ -419,7 +419,7 @@ int dm_residual_rmsnorm(int32_t dtype, float* x, const void* delta, const float*
 
 /* ---- SwiGLU MLP of a decode step ---------------------------------------------------
  * out[M, d] = (silu(x W1^T) * (x W3^T)) W2^T, the Block's MLP (models/dualmod/model.py:
- * 102-112) on a decode step's rows (one token per sequence, M <= 16): bf16 x [M, d],
+ * 102-112) on a decode step's rows (one token per sequence, M <= 64): bf16 x [M, d],
  * w1 / w3 [H, d], w2 [d, H], act [M, H] the caller's intermediate buffer, out [M, d]. The
  * products accumulate in fp32; act holds silu(g) * u rounded once to bf16. Deterministic
  * (fixed-order in-block sums). d must be a multiple of 128, H of 32, the operands 16-byte

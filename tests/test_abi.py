@@ -62,9 +62,9 @@ def test_rejects_null_and_bad_shapes():
     assert rc == -1 and b"null packed" in lib.dm_last_error()
     assert lib.dm_gemm(0, 0, 0, None, None, None, 128, 128, 64, 0, None) == -1
     assert lib.dm_linear(0, 1, 1, None, 1, 64, 100, 64, None) == -1
-    # dm_swiglu_rows: null operands, more than 16 rows, d not a multiple of 128, fp32 (unsupported)
+    # dm_swiglu_rows: null operands, more than 64 rows, d not a multiple of 128, fp32 (unsupported)
     assert lib.dm_swiglu_rows(1, None, 16, 16, 16, 16, 16, 8, 1024, 2816, None) == -1
-    assert lib.dm_swiglu_rows(1, 16, 16, 16, 16, 16, 16, 17, 1024, 2816, None) == -1
+    assert lib.dm_swiglu_rows(1, 16, 16, 16, 16, 16, 16, 65, 1024, 2816, None) == -1
     assert lib.dm_swiglu_rows(1, 16, 16, 16, 16, 16, 16, 8, 1000, 2816, None) == -1
     assert lib.dm_swiglu_rows(0, 16, 16, 16, 16, 16, 16, 8, 1024, 2816, None) == -2
 

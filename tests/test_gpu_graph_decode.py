@@ -142,9 +142,10 @@ def test_lm_decode_and_forward_match_oracle_fp32():
     assert e_dec < 1e-5 and e_fwd < 1e-5
 
 
-# bf16 at B = 3 takes the MLP through dm_swiglu_rows, B = 17 (more rows than it takes) and fp32
-# through torch's products
-@pytest.mark.parametrize("dtype,B", [(torch.float32, 3), (torch.bfloat16, 3), (torch.bfloat16, 17)])
+# bf16 at B = 3 and 17 takes the MLP through dm_swiglu_rows (one and two row tiles), B = 65 (more
+# rows than it takes) and fp32 through torch's products
+@pytest.mark.parametrize("dtype,B", [(torch.float32, 3), (torch.bfloat16, 3), (torch.bfloat16, 17),
+                                     (torch.bfloat16, 65)])
 def test_graph_decoder_equals_eager(dtype, B):
     say(f"GraphDecoder replays vs eager decode_step, {dtype}, B={B}")
     cfg = _lm_cfg()
@@ -232,7 +233,8 @@ def test_graph_decoder_refuses_a_step_past_the_tape():
     assert int(dec.pos.item()) == 1
 
 
-@pytest.mark.parametrize("M,d,H", [(1, 256, 512), (8, 1024, 2816), (16, 512, 1376), (5, 128, 96)])
+@pytest.mark.parametrize("M,d,H", [(1, 256, 512), (8, 1024, 2816), (16, 512, 1376), (5, 128, 96), (17, 256, 512),
+                                   (40, 1024, 2816), (64, 512, 1376)])
 def test_swiglu_rows_matches_fp32_reference(M, d, H):
     """dm_swiglu_rows (the decode step's MLP, models/dualmod/model.py:102-112) against the same
     products in fp32 on the bf16 inputs: act rounded once to bf16, so the bound is bf16's."""
