@@ -249,4 +249,44 @@ __global__ __launch_bounds__(256) void k_argmax_rows(const T* x, long ld, int co
   }
 }
 
+// k_argmax_rows for 16-byte aligned rows (ld a multiple of the vector width): 1024 threads per row,
+// 16-byte loads. A lane visits its columns in increasing order (its vectors, then the tail columns,
+// which come last in the row), so a strict > keeps its first maximum; lanes and waves then merge
+// by value, the smaller index on ties. NaNs never compare greater and are skipped.
+template <typename T>
+__global__ __launch_bounds__(1024) void k_argmax_rows_vec(const T* x, long ld, int cols, int64_t* out) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  __shared__ float bv[16];
+  __shared__ int bi[16];
+  const T* r = x + blockIdx.x * ld;
+  const int nv = cols / VEC;
+  float v = NEG_INF;
+  int idx = 0x7fffffff;
+  for (int q = threadIdx.x; q < nv; q += 1024) {
+    float f[VEC];
+    unpack16<T>(*reinterpret_cast<const uint4*>(r + (long)q * VEC), f);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e)
+      if (f[e] > v) { v = f[e]; idx = q * VEC + e; }
+  }
+  for (int j = nv * VEC + threadIdx.x; j < cols; j += 1024) {
+    const float f = to_f(r[j]);
+    if (f > v) { v = f; idx = j; }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ov = __shfl_xor(v, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { bv[wave] = v; bi[wave] = idx; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 16; ++w)
+      if (bv[w] > v || (bv[w] == v && bi[w] < idx)) { v = bv[w]; idx = bi[w]; }
+    out[blockIdx.x] = idx == 0x7fffffff ? 0 : idx;
+  }
+}
+
 }  // namespace dm

@@ -709,12 +709,17 @@ int dm_argmax_rows(int32_t dtype, const void* x, int32_t rows, int32_t cols, int
   DM_REQUIRE(rows > 0 && cols > 0 && ld >= cols, DM_ERR_INVALID, "rows=%d cols=%d ld=%lld", rows, cols,
              (long long)ld);
   hipStream_t s = S(stream);
-  if (dtype == DM_BF16)
-    hipLaunchKernelGGL(k_argmax_rows<bf16>, dim3(rows), dim3(256), 0, s, (const bf16*)x, (long)ld, cols, out);
-  else if (dtype == DM_F32)
-    hipLaunchKernelGGL(k_argmax_rows<float>, dim3(rows), dim3(256), 0, s, (const float*)x, (long)ld, cols, out);
-  else
+  // 16-byte aligned rows: the vector-load kernel; otherwise the scalar scan
+  const bool vec = aligned16(x) && ld % (dtype == DM_BF16 ? 8 : 4) == 0;
+  if (dtype == DM_BF16) {
+    if (vec) hipLaunchKernelGGL(k_argmax_rows_vec<bf16>, dim3(rows), dim3(1024), 0, s, (const bf16*)x, (long)ld, cols, out);
+    else hipLaunchKernelGGL(k_argmax_rows<bf16>, dim3(rows), dim3(256), 0, s, (const bf16*)x, (long)ld, cols, out);
+  } else if (dtype == DM_F32) {
+    if (vec) hipLaunchKernelGGL(k_argmax_rows_vec<float>, dim3(rows), dim3(1024), 0, s, (const float*)x, (long)ld, cols, out);
+    else hipLaunchKernelGGL(k_argmax_rows<float>, dim3(rows), dim3(256), 0, s, (const float*)x, (long)ld, cols, out);
+  } else {
     return fail(DM_ERR_INVALID, "dtype %d", dtype);
+  }
   DM_HIP(hipGetLastError());
   return DM_OK;
 }

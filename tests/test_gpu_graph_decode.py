@@ -86,20 +86,25 @@ def test_device_position_equals_host_position(dtype, P0, W, knobs):
     assert torch.equal(tapes[0].K, tapes[1].K) and torch.equal(tapes[0].V, tapes[1].V)
 
 
+# aligned rows (the vector kernel, with and without a tail of columns) and an odd row stride (the
+# scalar scan)
+@pytest.mark.parametrize("cols,ld", [(32000, 32000), (31997, 32000), (31997, 31997)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_argmax_rows_matches_torch(dtype):
-    say(f"dm_argmax_rows {dtype}")
+def test_argmax_rows_matches_torch(dtype, cols, ld):
+    say(f"dm_argmax_rows {dtype} cols={cols} ld={ld}")
     g = torch.Generator().manual_seed(1)
-    x = torch.randn(37, 32000, generator=g).to(dtype)
-    x[3, 100] = x[3, 31999] = 50.0       # ties: the first index wins
+    x = torch.randn(37, ld, generator=g).to(dtype)
+    x[3, 100] = x[3, cols - 1] = 50.0     # ties: the first index wins
     x[4, :] = 0.0
     x[5, 0] = 9.0
+    x[6, cols - 1] = 60.0                 # the maximum in the last column (a tail column when cols % 8)
+    x[7, cols:] = 99.0                    # past cols: not part of the row
     xd = x.to(DEV)
     out = torch.empty(37, dtype=torch.long, device=DEV)
-    L.check(L.lib().dm_argmax_rows(L.dtype_code(dtype), L.ptr(xd), 37, 32000, 32000, L.ptr(out), L.stream_ptr()))
+    L.check(L.lib().dm_argmax_rows(L.dtype_code(dtype), L.ptr(xd), 37, cols, ld, L.ptr(out), L.stream_ptr()))
     torch.cuda.synchronize()
-    assert torch.equal(out.cpu(), x.float().argmax(-1))
-    assert out[3].item() == 100 and out[4].item() == 0 and out[5].item() == 0
+    assert torch.equal(out.cpu(), x[:, :cols].float().argmax(-1))
+    assert out[3].item() == 100 and out[4].item() == 0 and out[5].item() == 0 and out[6].item() == cols - 1
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
