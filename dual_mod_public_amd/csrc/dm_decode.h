@@ -249,6 +249,45 @@ __global__ __launch_bounds__(256) void k_argmax_rows(const T* x, long ld, int co
   }
 }
 
+// k_residual_rmsnorm with the row held in registers (d <= 256 NPT): every load (x, delta, w) is
+// issued before the reduction and nothing is re-read; the same per-element arithmetic and the same
+// order of the sums, so the same results.
+template <typename T, int NPT>
+__global__ __launch_bounds__(256) void k_residual_rmsnorm_reg(float* x, const T* delta, const float* w, T* y, int d,
+                                                             float eps) {
+  __shared__ float red[4];
+  float* xr = x + (long)blockIdx.x * d;
+  float v[NPT], wv[NPT];
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    const int j = threadIdx.x + 256 * i;
+    const int jc = j < d ? j : 0;
+    v[i] = xr[jc];
+    if (delta != nullptr) v[i] += to_f(delta[(long)blockIdx.x * d + jc]);
+    wv[i] = w != nullptr ? w[jc] : 0.f;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    const int j = threadIdx.x + 256 * i;
+    if (j < d) {
+      if (delta != nullptr) xr[j] = v[i];
+      ss += v[i] * v[i];
+    }
+  }
+  if (w == nullptr) return;
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float rs = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)d + eps);
+  T* yr = y + (long)blockIdx.x * d;
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    const int j = threadIdx.x + 256 * i;
+    if (j < d) yr[j] = from_f<T>(v[i] * rs * wv[i]);
+  }
+}
+
 // k_argmax_rows for 16-byte aligned rows (ld a multiple of the vector width): 1024 threads per row,
 // 16-byte loads. A lane visits its columns in increasing order (its vectors, then the tail columns,
 // which come last in the row), so a strict > keeps its first maximum; lanes and waves then merge

@@ -691,14 +691,19 @@ int dm_residual_rmsnorm(int32_t dtype, float* x, const void* delta, const float*
   DM_REQUIRE(x != nullptr && (w == nullptr || y != nullptr), DM_ERR_INVALID, "null operand");
   DM_REQUIRE(M > 0 && d > 0, DM_ERR_INVALID, "M=%d d=%d", M, d);
   hipStream_t s = S(stream);
-  if (dtype == DM_BF16)
-    hipLaunchKernelGGL(k_residual_rmsnorm<bf16>, dim3(M), dim3(256), 0, s, x, (const bf16*)delta, w, (bf16*)y, d,
-                       eps);
-  else if (dtype == DM_F32)
-    hipLaunchKernelGGL(k_residual_rmsnorm<float>, dim3(M), dim3(256), 0, s, x, (const float*)delta, w, (float*)y,
-                       d, eps);
-  else
-    return fail(DM_ERR_INVALID, "dtype %d", dtype);
+  DM_REQUIRE(dtype == DM_BF16 || dtype == DM_F32, DM_ERR_INVALID, "dtype %d", dtype);
+  // rows of up to 4096 held in registers; longer rows by the streaming kernel
+  auto run = [&](auto tag) {
+    using T = decltype(tag);
+    const T* dl = (const T*)delta;
+    T* yy = (T*)y;
+    if (d <= 1024) hipLaunchKernelGGL((k_residual_rmsnorm_reg<T, 4>), dim3(M), dim3(256), 0, s, x, dl, w, yy, d, eps);
+    else if (d <= 2048) hipLaunchKernelGGL((k_residual_rmsnorm_reg<T, 8>), dim3(M), dim3(256), 0, s, x, dl, w, yy, d, eps);
+    else if (d <= 4096) hipLaunchKernelGGL((k_residual_rmsnorm_reg<T, 16>), dim3(M), dim3(256), 0, s, x, dl, w, yy, d, eps);
+    else hipLaunchKernelGGL(k_residual_rmsnorm<T>, dim3(M), dim3(256), 0, s, x, dl, w, yy, d, eps);
+  };
+  if (dtype == DM_BF16) run(bf16{});
+  else run(float{});
   DM_HIP(hipGetLastError());
   return DM_OK;
 }

@@ -107,15 +107,18 @@ def test_argmax_rows_matches_torch(dtype, cols, ld):
     assert out[3].item() == 100 and out[4].item() == 0 and out[5].item() == 0 and out[6].item() == cols - 1
 
 
+# row lengths for the register-resident kernel (up to 4096: 4 and 16 values per thread) and the
+# streaming one (longer rows)
+@pytest.mark.parametrize("d", [1000, 3000, 5000])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_residual_rmsnorm(dtype):
+def test_residual_rmsnorm(dtype, d):
     """dm_residual_rmsnorm: the residual add is exact fp32 (x + delta), the norm matches the
     oracle's RMSNorm (attention.py:74-83) in fp64 up to the output dtype's rounding."""
-    say(f"dm_residual_rmsnorm {dtype}")
+    say(f"dm_residual_rmsnorm {dtype} d={d}")
     g = torch.Generator().manual_seed(2)
-    x = torch.randn(5, 1, 1000, generator=g) * 3
-    delta = torch.randn(5, 1, 1000, generator=g).to(dtype)
-    w = torch.rand(1000, generator=g) + 0.5
+    x = torch.randn(5, 1, d, generator=g) * 3
+    delta = torch.randn(5, 1, d, generator=g).to(dtype)
+    w = torch.rand(d, generator=g) + 0.5
     xd = x.to(DEV)
     y = L.residual_rmsnorm(xd, delta.to(DEV), w.to(DEV), dtype)
     torch.cuda.synchronize()
