@@ -414,9 +414,19 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
     SrcRows<T> ao{(const T*)a->o_cat, d, B};
     SrcRows<T> bo{(const T*)w->wo, d, d};
     EpiResidual<T> ep{B, d, nullptr, (T*)a->y};
-    // one row block: 64 x 32 tiles give d / 32 blocks
-    if (B <= 64) launch_gemm_auto<T, 64, 32, 4, 1, 3, 4>(ao, bo, B, d, d, ep, s);
-    else launch_gemm_auto<T, 64, 128, 2, 2, 3, 4>(ao, bo, B, d, d, ep, s);
+    bool done = false;
+    if constexpr (sizeof(T) == 2) {
+      if (B <= MLP_ROWS && d % 32 == 0 && aligned16(a->o_cat) && aligned16(w->wo)) {
+        // bf16, one token per row: the weight-streaming product
+        launch_rows_wt<T>((const T*)a->o_cat, (const T*)w->wo, (T*)a->y, B, d, d, s);
+        done = true;
+      }
+    }
+    if (!done) {
+      // one row block: 64 x 32 tiles give d / 32 blocks
+      if (B <= 64) launch_gemm_auto<T, 64, 32, 4, 1, 3, 4>(ao, bo, B, d, d, ep, s);
+      else launch_gemm_auto<T, 64, 128, 2, 2, 3, 4>(ao, bo, B, d, d, ep, s);
+    }
   }
   return DM_OK;
 }
@@ -670,18 +680,17 @@ int dm_swiglu_rows(int32_t dtype, const void* x, const void* w1, const void* w3,
   DM_REQUIRE(aligned16(x) && aligned16(w1) && aligned16(w3) && aligned16(w2) && aligned16(act), DM_ERR_INVALID,
              "operands must be 16-byte aligned");
   hipStream_t s = S(stream);
-  auto run = [&](auto rt) {
+  auto up = [&](auto rt) {
     constexpr int RT = decltype(rt)::value;
     hipLaunchKernelGGL((k_swiglu_up<bf16, RT>), dim3(H / 16), dim3(256), 0, s, (const bf16*)x, (const bf16*)w1,
                        (const bf16*)w3, (bf16*)act, M, d, H);
-    hipLaunchKernelGGL((k_swiglu_down<bf16, RT>), dim3(d / 16), dim3(512), 0, s, (const bf16*)act,
-                       (const bf16*)w2, (bf16*)out, M, d, H);
   };
   const int rts = (M + 15) / 16;
-  if (rts == 1) run(std::integral_constant<int, 1>{});
-  else if (rts == 2) run(std::integral_constant<int, 2>{});
-  else if (rts == 3) run(std::integral_constant<int, 3>{});
-  else run(std::integral_constant<int, 4>{});
+  if (rts == 1) up(std::integral_constant<int, 1>{});
+  else if (rts == 2) up(std::integral_constant<int, 2>{});
+  else if (rts == 3) up(std::integral_constant<int, 3>{});
+  else up(std::integral_constant<int, 4>{});
+  launch_rows_wt<bf16>((const bf16*)act, (const bf16*)w2, (bf16*)out, M, d, H, s);
   DM_HIP(hipGetLastError());
   return DM_OK;
 }

@@ -9,6 +9,8 @@
 // 8-element fragment is one 16-byte load.
 #pragma once
 
+#include <type_traits>
+
 #include "dm_common.h"
 
 namespace dm {
@@ -115,6 +117,21 @@ __global__ __launch_bounds__(512) void k_swiglu_down(const T* __restrict__ act, 
       out[(long)i * d + n0 + j] = from_f<T>(v);
     }
   }
+}
+
+// out[M, N] = a[M, K] W^T for M <= MLP_ROWS bf16 rows, W [N, K] K-contiguous (N a multiple of 16,
+// K of 32): k_swiglu_down's weight-streaming product (the MLP's down projection, a decode step's W_O)
+template <typename T>
+void launch_rows_wt(const T* a, const T* W, T* out, int M, int N, int K, hipStream_t s) {
+  auto run = [&](auto rt) {
+    constexpr int RT = decltype(rt)::value;
+    hipLaunchKernelGGL((k_swiglu_down<T, RT>), dim3(N / 16), dim3(512), 0, s, a, W, out, M, N, K);
+  };
+  const int rts = (M + 15) / 16;
+  if (rts == 1) run(std::integral_constant<int, 1>{});
+  else if (rts == 2) run(std::integral_constant<int, 2>{});
+  else if (rts == 3) run(std::integral_constant<int, 3>{});
+  else run(std::integral_constant<int, 4>{});
 }
 
 }  // namespace dm
