@@ -42,7 +42,14 @@ class SwiGLU(nn.Module):
         where it applies (bf16, B <= 64), else the forward's torch products. w = (w1, w3, w2) in
         h's dtype (default: cast from the parameters); act / out optional static buffers."""
         if w is None:
-            w = tuple(p.to(h.dtype).contiguous() for p in (self.w1.weight, self.w3.weight, self.w2.weight))
+            # the compute-dtype copies, re-cast only when a parameter changed (its storage or version)
+            ps = (self.w1.weight, self.w3.weight, self.w2.weight)
+            key = (h.dtype,) + tuple((p.data_ptr(), p._version) for p in ps)
+            cached = getattr(self, "_decode_w", None)
+            if cached is None or cached[0] != key:
+                cached = (key, tuple(p.detach().to(h.dtype).contiguous() for p in ps))
+                self._decode_w = cached
+            w = cached[1]
         if L.swiglu_rows_ok(h, w[0], w[2]):
             return L.swiglu_rows(h, w[0], w[1], w[2], act=act, out=out)
         return F.linear(F.silu(F.linear(h, w[0])) * F.linear(h, w[1]), w[2]).contiguous()
