@@ -79,7 +79,7 @@ class GraphDecoder:
             nrm = blocks[l + 1].attn_norm if l + 1 < len(blocks) else m.norm_f
             h = L.residual_rmsnorm(x, mo, nrm.weight, dt, eps=nrm.eps)
         lg = F.linear(h, self._head)                                    # [B, 1, V]
-        self.logits.copy_(lg.float())
+        self.logits.copy_(lg)                                           # exact bf16 -> fp32 in one copy
         L.check(L.lib().dm_argmax_rows(L.dtype_code(self.dt), L.ptr(lg), B, self.vocab, self.vocab,
                                        L.ptr(self.next), L.stream_ptr()))
         self.pos += 1
