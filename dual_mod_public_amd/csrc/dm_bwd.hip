@@ -873,7 +873,10 @@ int run_stack_bwd(const dm_config* c, int nl, const dm_stack_bwd_layer* layers, 
       return DM_OK;
     }
     DM_REQUIRE(plan_bytes >= off, DM_ERR_WORKSPACE, "plan %zu < %zu bytes", plan_bytes, off);
-    if (build) DM_HIP(hipMemcpy(plan, tab.data(), off, hipMemcpyHostToDevice));
+    if (build) {
+      const int wrc = write_plan(plan, tab.data(), off, S(stream));
+      if (wrc) return wrc;
+    }
     // every layer's accumulators (as bwd_begin)
     for (int l = 0; l < nl; ++l) {
       const BwdWs<T>& w = ws[l];

@@ -221,6 +221,17 @@ __global__ __launch_bounds__(256) void k_residual_rmsnorm(float* x, const T* del
   for (int j = threadIdx.x; j < d; j += 256) yr[j] = from_f<T>(xr[j] * rs * w[j]);
 }
 
+// torch.argmax's order: NaN is greater than every number (the first NaN wins), otherwise the
+// larger value, the smaller index on ties. argmax_takes: a lane's scan in increasing column
+// order replaces its pick only by a strictly greater value or by a first NaN.
+DM_DEV bool argmax_takes(float f, float v) { return f > v || (f != f && v == v); }
+DM_DEV bool argmax_better(float ov, int oi, float v, int idx) {
+  const bool on = ov != ov, vn = v != v;
+  if (on != vn) return on;
+  if (on) return oi < idx;
+  return ov > v || (ov == v && oi < idx);
+}
+
 // row argmax of x [rows, cols] (first index of the maximum; one block per row)
 template <typename T>
 __global__ __launch_bounds__(256) void k_argmax_rows(const T* x, long ld, int cols, int64_t* out) {
@@ -231,20 +242,20 @@ __global__ __launch_bounds__(256) void k_argmax_rows(const T* x, long ld, int co
   int idx = 0x7fffffff;
   for (int j = threadIdx.x; j < cols; j += 256) {
     const float f = to_f(r[j]);
-    if (f > v) { v = f; idx = j; }   // strided scan: the first maximum of this lane's columns
+    if (argmax_takes(f, v)) { v = f; idx = j; }   // strided scan: this lane's first maximum
   }
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     const float ov = __shfl_xor(v, o, 64);
     const int oi = __shfl_xor(idx, o, 64);
-    if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+    if (argmax_better(ov, oi, v, idx)) { v = ov; idx = oi; }
   }
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { bv[wave] = v; bi[wave] = idx; }
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w = 1; w < 4; ++w)
-      if (bv[w] > v || (bv[w] == v && bi[w] < idx)) { v = bv[w]; idx = bi[w]; }
+      if (argmax_better(bv[w], bi[w], v, idx)) { v = bv[w]; idx = bi[w]; }
     out[blockIdx.x] = idx == 0x7fffffff ? 0 : idx;
   }
 }
@@ -291,7 +302,7 @@ __global__ __launch_bounds__(256) void k_residual_rmsnorm_reg(float* x, const T*
 // k_argmax_rows for 16-byte aligned rows (ld a multiple of the vector width): 1024 threads per row,
 // 16-byte loads. A lane visits its columns in increasing order (its vectors, then the tail columns,
 // which come last in the row), so a strict > keeps its first maximum; lanes and waves then merge
-// by value, the smaller index on ties. NaNs never compare greater and are skipped.
+// by value, the smaller index on ties; a NaN is the maximum (the first NaN wins), as torch.argmax.
 template <typename T>
 __global__ __launch_bounds__(1024) void k_argmax_rows_vec(const T* x, long ld, int cols, int64_t* out) {
   constexpr int VEC = 16 / (int)sizeof(T);
@@ -306,24 +317,24 @@ __global__ __launch_bounds__(1024) void k_argmax_rows_vec(const T* x, long ld, i
     unpack16<T>(*reinterpret_cast<const uint4*>(r + (long)q * VEC), f);
 #pragma unroll
     for (int e = 0; e < VEC; ++e)
-      if (f[e] > v) { v = f[e]; idx = q * VEC + e; }
+      if (argmax_takes(f[e], v)) { v = f[e]; idx = q * VEC + e; }
   }
   for (int j = nv * VEC + threadIdx.x; j < cols; j += 1024) {
     const float f = to_f(r[j]);
-    if (f > v) { v = f; idx = j; }
+    if (argmax_takes(f, v)) { v = f; idx = j; }
   }
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     const float ov = __shfl_xor(v, o, 64);
     const int oi = __shfl_xor(idx, o, 64);
-    if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+    if (argmax_better(ov, oi, v, idx)) { v = ov; idx = oi; }
   }
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { bv[wave] = v; bi[wave] = idx; }
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w = 1; w < 16; ++w)
-      if (bv[w] > v || (bv[w] == v && bi[w] < idx)) { v = bv[w]; idx = bi[w]; }
+      if (argmax_better(bv[w], bi[w], v, idx)) { v = bv[w]; idx = bi[w]; }
     out[blockIdx.x] = idx == 0x7fffffff ? 0 : idx;
   }
 }

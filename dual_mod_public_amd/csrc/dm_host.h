@@ -250,6 +250,19 @@ inline bool plan_sig_matches(const void* plan, uint64_t sig) {
   auto it = plan_sigs().find(plan);
   return it != plan_sigs().end() && it->second == sig;
 }
+// Write a plan's argument table (host staging -> device) for the grouped launches that read it on
+// stream s. A build is a one-time set-up step and is refused while s is being captured; otherwise
+// s is drained first, so that no launch still in flight on s reads an earlier table at the same
+// address, and the blocking copy has landed before the new launches are issued.
+inline int write_plan(void* plan, const void* tab, size_t bytes, hipStream_t s) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  DM_HIP(hipStreamIsCapturing(s, &cs));
+  DM_REQUIRE(cs == hipStreamCaptureStatusNone, DM_ERR_INVALID,
+             "a plan cannot be built (build != 0) on a stream under capture: build it once before capturing");
+  DM_HIP(hipStreamSynchronize(s));
+  DM_HIP(hipMemcpy(plan, tab, bytes, hipMemcpyHostToDevice));
+  return DM_OK;
+}
 
 inline int log2_exact(int v) {
   int l = 0;

@@ -199,7 +199,7 @@ int dm_stack_fwd(const dm_config* c, int32_t n_layers, const dm_stack_layer* lay
     if ((rc = plan_stack(c, n_layers, layers, cos, sin, sched, n_cells, cache_T, launches, &tab, &bytes)))
       return rc;
     DM_REQUIRE(plan_bytes >= bytes, DM_ERR_WORKSPACE, "plan %zu < %zu bytes", plan_bytes, bytes);
-    DM_HIP(hipMemcpy(plan, tab.data(), bytes, hipMemcpyHostToDevice));
+    if ((rc = write_plan(plan, tab.data(), bytes, S(stream)))) return rc;
     {
       PlanCache& pc = plan_cache();
       std::lock_guard<std::mutex> lk(pc.mu);

@@ -9,8 +9,10 @@ embedding gather, every layer's attention and MLP, the residual adds with their 
 are recorded once and replayed per token.
 
 The graph reads compute-dtype copies of the MLP / head weights and the attention's packed
-buffers, all at fixed addresses: after changing the model's parameters call ``refresh()``
-(outside the graph) before the next step.
+buffers, all at fixed addresses. Every ``step()`` first compares the parameters' version
+stamps (storage address and in-place version counter) with those of the last copy and
+re-reads the weights when one changed (as the reference re-casts the live weights on every
+replay), so an optimizer step between tokens is picked up.
 """
 
 import torch
@@ -46,14 +48,16 @@ class GraphDecoder:
         # the MLP's intermediate and output rows (dm_swiglu_rows), at fixed addresses
         self._act = torch.empty(B, cfg.mlp_hidden, device=self.dev, dtype=self.dt)
         self._mo = torch.empty(B, 1, cfg.d_model, device=self.dev, dtype=self.dt)
+        self._params = list(model.parameters())
         self._ver = None
         self.graph = None
         self._steps = 0
         self.refresh()
 
     def refresh(self):
-        """Re-read the model's parameters into the static copies the graph uses."""
-        ver = tuple((p.data_ptr(), p._version) for p in self.m.parameters())
+        """Re-read the model's parameters into the static copies the graph uses (a no-op while
+        no parameter changed)."""
+        ver = tuple((p.data_ptr(), p._version) for p in self._params)
         if ver == self._ver:
             return
         with torch.no_grad():
@@ -115,11 +119,13 @@ class GraphDecoder:
             t.V.zero_()
 
     def step(self):
-        """One token: the graph replay (or the eager step). The position lives on the device;
-        the host counts the steps since reset() and refuses a step past the tape (the kernels
-        would clamp the position onto the last slot)."""
+        """One token: the graph replay (or the eager step), after re-reading the weights if a
+        parameter changed since the last step. The position lives on the device; the host
+        counts the steps since reset() and refuses a step past the tape (the kernels would
+        clamp the position onto the last slot)."""
         if self._steps >= self.P:
             raise ValueError(f"the tape is full: {self.P} positions since reset()")
+        self.refresh()
         if self.graph is not None:
             self.graph.replay()
         else:

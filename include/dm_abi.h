@@ -431,7 +431,8 @@ int dm_swiglu_rows(int32_t dtype, const void* x, const void* w1, const void* w3,
  * out[r] = the first index of the maximum of x[r, 0:cols) (row stride ld elements),
  * storage dtype bf16 or fp32: the greedy pick of lm/eval/graph_decode.py:62
  * (lg.argmax(-1)) as one block per row, with no multi-block reduction (nothing to
- * clear between graph replays). NaNs are skipped, not taken as the maximum. */
+ * clear between graph replays). A NaN counts as the maximum (the first NaN's index), as
+ * torch.argmax; a row of -inf gives 0. */
 int dm_argmax_rows(int32_t dtype, const void* x, int32_t rows, int32_t cols, int64_t ld, int64_t* out,
                    void* stream);
 

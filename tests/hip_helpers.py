@@ -25,16 +25,28 @@ def say(msg):
 def record(test, errs, tol):
     """Keep a test's measured relative errors (written to parity_margins.json in the run's
     output folder at the end of the session)."""
-    MARGINS.append({"test": test, "tol": tol, "relerr": {k: float(v) for k, v in errs.items()}})
+    node = os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0].split("::")[-1]
+    MARGINS.append({"test": test, "node": node, "tol": tol, "relerr": {k: float(v) for k, v in errs.items()}})
 
 
 def write_margins(repo):
+    """parity_margins.json (every recorded error) and parity_margins.md (one row per recorded
+    check: tolerance, worst relative error, the quantity it was measured on, worst / tolerance)."""
     if not MARGINS:
         return
     out = os.path.join(repo, os.environ.get("DM_RESULTS_DIR", "gpurun_out"))
     os.makedirs(out, exist_ok=True)
     with open(os.path.join(out, "parity_margins.json"), "w") as f:
         json.dump(MARGINS, f, indent=1)
+    rows = ["| test | check | tolerance | worst relerr | on | worst / tol |", "|---|---|---|---|---|---|"]
+    for m in MARGINS:
+        if not m["relerr"]:
+            continue
+        k = max(m["relerr"], key=m["relerr"].get)
+        v = m["relerr"][k]
+        rows.append(f"| {m.get('node', '')} | {m['test']} | {m['tol']:.0e} | {v:.2e} | {k} | {v / m['tol']:.2f} |")
+    with open(os.path.join(out, "parity_margins.md"), "w") as f:
+        f.write("\n".join(rows) + "\n")
 
 
 def cfg_of(d=256, h=4, ctx_mod="mult_res", T=64, **kw):

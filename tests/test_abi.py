@@ -121,10 +121,11 @@ def test_kmod_config_fields():
     assert L.load().dm_cell_workspace_bytes(c, 64) == 0
 
 
-def test_training_entry_points_reject_local_window():
-    """A sliding window is decode-only: dm_layer_fwd (tape and recompute forms) and
-    dm_layer_bwd reject it with DM_ERR_UNSUPPORTED before any launch (the checks run on
-    the host; the placeholder pointers below are never dereferenced)."""
+def test_training_entry_points_reject_window_within_a_cell():
+    """Training windows must exceed the cell length (a cell's rows read all its earlier rows):
+    dm_layer_fwd (tape and recompute forms) and dm_layer_bwd reject W = 8 with 64-row cells with
+    DM_ERR_UNSUPPORTED before any launch (the checks run on the host; the placeholder pointers
+    below are never dereferenced)."""
     lib = L.load()
     c = _conf(local_window=8)
     fake = ctypes.c_void_p(1 << 20)   # non-null, 16-byte aligned, never dereferenced
@@ -147,6 +148,34 @@ def test_training_entry_points_reject_local_window():
     rc = lib.dm_layer_bwd(ctypes.byref(c), ctypes.byref(w), fake, fake, fake, fake, fake, ctypes.byref(b), sched, 1,
                           fake, fake, 64, fake, None, 0, ctypes.byref(g), fake, 1 << 30, None)
     assert rc == -2 and b"local_window" in lib.dm_last_error()
+
+
+def test_training_window_longer_than_a_cell_passes_host_checks():
+    """W > c is a training configuration (the committed-prefix kernels mask keys below
+    i - W + 1): the layer-batched forward's plan query, which runs every host check of the
+    training entry points and launches nothing, accepts W = 100 with 64-row cells and refuses
+    W = 8 (the placeholder pointers are never dereferenced)."""
+    lib = L.load()
+    fake = ctypes.c_void_p(1 << 20)
+    w = L.dm_packed()
+    for f in ("w_proj", "b_proj", "w_sweep", "w_vctx", "norm_ctx_w", "attn_norm_w", "wo", "w_proj_t",
+              "w_sweep_t", "w_vctx_t", "wo_t"):
+        setattr(w, f, fake.value)
+    b = L.dm_layer_bufs()
+    b.T = 256
+    for f in ("xhat", "qr", "kraw", "kself", "vraw", "glogx", "sig"):
+        setattr(b, f, fake.value)
+    ly = (L.dm_stack_layer * 1)()
+    ly[0].w, ly[0].bufs = ctypes.addressof(w), ctypes.addressof(b)
+    for f in ("x", "y", "K_cache", "V_cache", "ocat", "workspace"):
+        setattr(ly[0], f, fake.value)
+    ly[0].workspace_bytes = 1 << 34
+    sched = (ctypes.c_int32 * 12)(0, 64, 4, 64, 64, 4, 128, 64, 4, 192, 64, 4)
+    ok = _conf(local_window=100)
+    assert lib.dm_stack_fwd_plan_bytes(ctypes.byref(ok), 1, ly, sched, 4, 256) > 0, lib.dm_last_error()
+    bad = _conf(local_window=8)
+    assert lib.dm_stack_fwd_plan_bytes(ctypes.byref(bad), 1, ly, sched, 4, 256) == 0
+    assert b"local_window" in lib.dm_last_error()
 
 
 def test_attend_one_refine_kv_refuse_autograd():

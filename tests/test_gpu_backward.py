@@ -5,9 +5,10 @@ The oracle's layer forward is written functionally (cat-grown caches), so torch
 autograd through it is the reference's own gradient oracle for K < c
 (engines/wavescan/tests/test_k1_k9.py:240-281) and, at K = c, autograd through the
 sequential scan (the oracle's scan grads are pinned to the reference's golden
-gradients in tests/test_oracle_golden.py). Tolerances: fp32 grads within 1e-4
-relative (the reference's T-K6 bar, test_k1_k9.py:212-237) — in practice ~1e-6;
-bf16 within 5e-2 relative of the fp32 oracle.
+gradients in tests/test_oracle_golden.py). Tolerances: fp32 grads within 1e-5
+relative (the reference's published exactness bar, README.md:203-204; measured
+~1e-6), bf16 grads within 2e-2 relative of the fp64 oracle (measured <= 1.4e-2 at
+the 340M shape, T=2048).
 """
 
 import pytest
@@ -21,8 +22,8 @@ from tests.hip_helpers import DEV, cfg_of, record, relerr, say, setup
 
 pytestmark = pytest.mark.gpu
 
-FP32_TOL = 1e-4
-BF16_TOL = 5e-2
+FP32_TOL = 1e-5
+BF16_TOL = 2e-2
 BF16_FWD_TOL = 2e-2   # bf16 forward bar of BASELINE.json (2e-2 relative)
 
 

@@ -99,12 +99,18 @@ def test_argmax_rows_matches_torch(dtype, cols, ld):
     x[5, 0] = 9.0
     x[6, cols - 1] = 60.0                 # the maximum in the last column (a tail column when cols % 8)
     x[7, cols:] = 99.0                    # past cols: not part of the row
+    x[8, 17] = x[8, 40] = float("nan")    # a NaN is the maximum, the first NaN wins (torch.argmax)
+    x[8, 5] = 80.0
+    x[9, :] = float("-inf")               # all -inf: index 0
+    x[10, cols - 2] = float("nan")        # a NaN in a late column beats a larger value earlier
+    x[10, 3] = 70.0
     xd = x.to(DEV)
     out = torch.empty(37, dtype=torch.long, device=DEV)
     L.check(L.lib().dm_argmax_rows(L.dtype_code(dtype), L.ptr(xd), 37, cols, ld, L.ptr(out), L.stream_ptr()))
     torch.cuda.synchronize()
     assert torch.equal(out.cpu(), x[:, :cols].float().argmax(-1))
     assert out[3].item() == 100 and out[4].item() == 0 and out[5].item() == 0 and out[6].item() == cols - 1
+    assert out[8].item() == 17 and out[9].item() == 0 and out[10].item() == cols - 2
 
 
 # row lengths for the register-resident kernel (up to 4096: 4 and 16 values per thread) and the
@@ -173,6 +179,29 @@ def test_graph_decoder_equals_eager(dtype, B):
     assert int(dec.pos.item()) == T
     for l in range(cfg.n_layers):
         assert torch.equal(dec.K[l][:, :, :T], caches[l]["K"]) and torch.equal(dec.V[l][:, :, :T], caches[l]["V"])
+
+
+def test_graph_decoder_follows_parameter_updates():
+    """An in-place parameter update between replays (an optimizer step) is picked up by the next
+    step: the graph's static weight copies are re-read when a parameter's version changes."""
+    say("GraphDecoder after in-place parameter updates vs eager decode_step, bf16")
+    cfg = _lm_cfg()
+    m, _ = _lm(cfg, torch.bfloat16)
+    B, T = 3, 12
+    idx = _tokens(cfg, B, T, seed=8).to(DEV)
+    dec = GraphDecoder(m, B, 16).capture()
+    caches = m.decode_init()
+    g = torch.Generator(device=DEV).manual_seed(9)
+    with torch.no_grad():
+        for p in range(T):
+            if p in (3, 7):   # MLP, head (tied embedding) and attention weights all change
+                for prm in (m.blocks[0].mlp.w2.weight, m.lm_head.weight, m.blocks[-1].attn.w_kctx.weight):
+                    prm.add_(0.05 * torch.randn(prm.shape, generator=g, device=DEV))
+            eag = m.decode_step(idx[:, p:p + 1], p, caches)
+            dec.tok.copy_(idx[:, p:p + 1])
+            dec.step()
+            torch.cuda.synchronize()
+            assert torch.equal(dec.logits, eag.float()), p
 
 
 def test_graph_generate_equals_eager_greedy():

@@ -5,7 +5,7 @@ raw value (raw, optionally tanh-bounded) or blend it with a zeroed v_ctx
 oracle's kmod branches are pinned by closed forms (tests/test_oracle_invariants.py:
 gated_norm heads' v'' == sigmoid(gate) v_raw, raw heads' v'' == v_raw or tanh(v_raw));
 the reference's golden knob case covers raw mode without the tanh bound. fp32
-tolerances as the dense tests: 1e-5 forward / decode, 1e-4 grads."""
+tolerances as the dense tests: 1e-5 forward / decode, 1e-5 grads."""
 
 import pytest
 import torch

@@ -6,7 +6,7 @@ Forward, gradients (the gains' included) and decode against the oracle, which th
 reference's golden knob case pins for k_ctx_norm and v_ctx_norm (tests/golden,
 knobs_mult_res) and closed forms pin for all three (tests/test_oracle_invariants.py).
 The gains are drawn away from 1 so a dropped gain or a wrong head index fails.
-fp32 bars as the dense tests: 1e-5 forward / decode, 1e-4 gradients; bf16 as
+fp32 bars as the dense tests: 1e-5 forward / decode, 1e-5 gradients; bf16 as
 tests/test_gpu_backward.py."""
 
 import pytest

@@ -66,8 +66,8 @@ def test_stack_matches_oracle_fp32():
     for l, sd in enumerate(sdg):
         for k, v in sd.items():
             errs[f"L{l}.{k}"] = relerr(grads[l][k], v.grad)
-    record("stack 3 layers fp32", errs, 1e-4)
-    assert max(errs.values()) < 1e-4, max(errs.items(), key=lambda kv: kv[1])
+    record("stack 3 layers fp32", errs, 1e-5)
+    assert max(errs.values()) < 1e-5, max(errs.items(), key=lambda kv: kv[1])
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
