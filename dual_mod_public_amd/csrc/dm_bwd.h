@@ -111,7 +111,7 @@ template <typename T> struct RefineBwdArgs {
   long psum_stride;                    //   chunk row p at row dk_row0 + p (standalone kernel)
   const T* save1;                      // [N, 4d] raw GEMM-1 outputs of this sweep (storage dtype)
   const T* save2;                      // [N, d] raw v_ctx (mult family)
-  const float* glogx; const T* kraw; const T* vraw;
+  const T* glogx; const T* kraw; const T* vraw;
   const float* cos; const float* sin;
   T* dctx;                             // [N, 4d] (packed columns; v_map columns written by EpiVinBwd)
   T* dvc;                              // [N, d] dv_ctx (mult family)
@@ -149,7 +149,7 @@ DM_DEV RefineIn refine_gather(const RefineBwdArgs<T>& a, int m, int hd, int jj) 
   const long lrow = (((long)b * h + hd) * g.Tbuf + t) * DH + jj;
   const long xrow = (long)b * g.Tbuf + t;
   const T* S1 = a.save1 + (long)m * 4 * d;
-  const float* gxr = a.glogx + xrow * 2 * d;
+  const T* gxr = a.glogx + xrow * 2 * d;
   const int c1 = hd * DH + jj, c2 = c1 + DH / 2;
   RefineIn in;
   ld4<float>(a.cos + (long)pos * (DH / 2) + jj, in.cs);
@@ -158,10 +158,10 @@ DM_DEV RefineIn refine_gather(const RefineBwdArgs<T>& a, int m, int hd, int jj) 
   ld4<T>(S1 + col_k<DH>(hd, jj, 1), in.kx2);
   ld4<T>(S1 + col_k<DH>(hd, jj, 2), in.gu1);
   ld4<T>(S1 + col_k<DH>(hd, jj, 3), in.gu2);
-  ld4<float>(gxr + c1, in.gx1);
-  ld4<float>(gxr + c2, in.gx2);
-  ld4<float>(gxr + d + c1, in.gxv1);
-  ld4<float>(gxr + d + c2, in.gxv2);
+  ld4<T>(gxr + c1, in.gx1);
+  ld4<T>(gxr + c2, in.gx2);
+  ld4<T>(gxr + d + c1, in.gxv1);
+  ld4<T>(gxr + d + c2, in.gxv2);
   ld4<T>(a.kraw + lrow, in.kr1);
   ld4<T>(a.kraw + lrow + DH / 2, in.kr2);
   ld4<T>(a.vraw + lrow, in.vr1);
@@ -399,18 +399,20 @@ template <typename T> struct EpiVinBwd {
   int M, ctx_mod;
   float lam;
   const T* __restrict__ save1;       // [N, 4d]
-  const float* __restrict__ sig;     // [B, Tbuf, d]
+  const T* __restrict__ sig;         // [B, Tbuf, d]
   T* __restrict__ dctx;              // [N, 4d]
   float* __restrict__ dsig;          // layer accumulator [B, Tbuf, d]
   float* __restrict__ lamdv;         // [N, d]
   // Block tile 64 x 32: thread t owns row t / 4, columns 8 (t % 4) .. + 7; its
   // inputs (and the dsig values it will add to) are gathered before the k-loop.
   struct TilePre {
-    floatx4 sg[2], ds[2];
+    Raw8<T> sg;
+    floatx4 ds[2];
     Raw8<T> vm;
   };
-  // vector-memory load instructions tile_prefetch issues (Raw8 = one 16-byte load in bf16)
-  static constexpr int LATE_GATHERS = 4 + (int)(sizeof(T) / 2);
+  // vector-memory load instructions tile_prefetch issues (Raw8 = one 16-byte load in bf16, two in
+  // fp32: 16-byte loads, which the compiler cannot merge into fewer)
+  static constexpr int LATE_GATHERS = 2 + 2 * (int)(sizeof(T) / 2);
   DM_DEV TilePre tile_prefetch(int m0, int n0) const {
     const int r = threadIdx.x >> 2, col = n0 + 8 * (threadIdx.x & 3);
     const int d = g.d;
@@ -418,11 +420,9 @@ template <typename T> struct EpiVinBwd {
     const int b = m / g.c;
     const long xrow = (long)b * g.Tbuf + g.buf_t0 + m - b * g.c;
     TilePre pr;
+    pr.sg = ld8_global(sig + xrow * d + col);
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      pr.sg[k] = ld_global<floatx4>(sig + xrow * d + col + 4 * k);
-      pr.ds[k] = ld_global<floatx4>(dsig + xrow * d + col + 4 * k);
-    }
+    for (int k = 0; k < 2; ++k) pr.ds[k] = ld_global<floatx4>(dsig + xrow * d + col + 4 * k);
     pr.vm = ld8_global(save1 + (long)m * 4 * d + 2 * d + col);
     return pr;
   }
@@ -436,9 +436,9 @@ template <typename T> struct EpiVinBwd {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       unpackf4(*reinterpret_cast<const floatx4*>(tile + r * LDT + c0 + 4 * k), dv + 4 * k);
-      unpackf4(pr.sg[k], sg + 4 * k);
       unpackf4(pr.ds[k], ds + 4 * k);
     }
+    unpack8<T>(pr.sg, sg);
     unpack8<T>(pr.vm, vm);
     if (m >= M) return;
     settle(sg); settle(ds); settle(vm);   // all loads before any store
@@ -1229,7 +1229,7 @@ DM_DEV void proj_bwd_body(int M, int T_, int d, int h, int nproj, int fusion, co
                           const float* __restrict__ dkraw, const float* __restrict__ dkself,
                           const float* __restrict__ dvraw, const T* __restrict__ dctxL,
                           const CellRow* __restrict__ cellrow, int B, const float* __restrict__ dsig,
-                          const float* __restrict__ sig, const float* __restrict__ cos,
+                          const T* __restrict__ sig, const float* __restrict__ cos,
                           const float* __restrict__ sin, T* __restrict__ dproj, float* __restrict__ bpart,
                           const T* __restrict__ vpre, const float* __restrict__ vgain,
                           float* __restrict__ vgpart, const float* __restrict__ sdss,
@@ -1305,8 +1305,8 @@ DM_DEV void proj_bwd_body(int M, int T_, int d, int h, int nproj, int fusion, co
     float z1[4] = {}, z2[4] = {};
     if (nproj == 6) {
       float sg1[4], sg2[4], ds1[4], ds2[4];
-      ld4<float>(sig + m * d + c1, sg1);
-      ld4<float>(sig + m * d + c2, sg2);
+      ld4<T>(sig + m * d + c1, sg1);
+      ld4<T>(sig + m * d + c2, sg2);
       ld4<float>(dsig + m * d + c1, ds1);
       ld4<float>(dsig + m * d + c2, ds2);
       // fusion: dsig already holds the grad of the raw pre-activation (no sigmoid, no bias)
@@ -1377,7 +1377,7 @@ static __global__ __launch_bounds__(256) void k_proj_bwd(int M, int T_, int d, i
                                                          const float* __restrict__ dvraw,
                                                          const T* __restrict__ dctxL,
                                                          const CellRow* __restrict__ cellrow, int B,
-                                                         const float* __restrict__ dsig, const float* __restrict__ sig,
+                                                         const float* __restrict__ dsig, const T* __restrict__ sig,
                                                          const float* __restrict__ cos, const float* __restrict__ sin,
                                                          T* __restrict__ dproj, float* __restrict__ bpart,
                                                          const T* __restrict__ vpre, const float* __restrict__ vgain,
@@ -1397,7 +1397,9 @@ template <typename T, int DH> struct ProjBwdBody {
     const T* dctxL;
     const CellRow* cellrow;
     int B;
-    const float *dsig, *sig, *cos, *sin;
+    const float* dsig;
+    const T* sig;
+    const float *cos, *sin;
     T* dproj;
     float* bpart;
     const T* vpre;

@@ -317,7 +317,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
   // refine VJP arguments of sweep sw (the grads of its refined rows: given by the caller)
   auto refine_args = [&](int sw) {
     return RefineBwdArgs<T>{g, N, c->ctx_mod, dKn, dVn, dn_stride, dn_row0, dn_psum,
-                            sv.save1 + sw * NS * 4 * d, mult ? sv.save2 + sw * NS * d : nullptr, L->glogx, kraw,
+                            sv.save1 + sw * NS * 4 * d, mult ? sv.save2 + sw * NS * d : nullptr, (const T*)L->glogx, kraw,
                             vraw, cos, sin, dctx + sw * NS * 4 * d, dvc + sw * NS * d, ws.dkraw,
                             ws.dvraw, kctx_gain(c, w), vctx_gain(c, w), ws.dkg, ws.dvg};
   };
@@ -338,7 +338,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
     }
     // dv_in = dv_ctx . W_vctx (mult family)
     if (mult) {
-      EpiVinBwd<T> ev{g, N, c->ctx_mod, c->mult_res_lambda, sv.save1 + sw * NS * 4 * d, L->sig,
+      EpiVinBwd<T> ev{g, N, c->ctx_mod, c->mult_res_lambda, sv.save1 + sw * NS * 4 * d, (const T*)L->sig,
                       dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
       const SrcRows<T> av{dvc + sw * NS * d, d, N}, bv{(const T*)w->w_vctx_t, d, d};
       if constexpr (SW2_STAGES > 0) launch_gemm_auto<T, 64, 32, 4, 1, SW2_STAGES, 8>(av, bv, N, d, d, ev, s);
@@ -480,7 +480,7 @@ void bwd_end(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T*
                      fusion ? 1 : 0,
                      (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself, (const float*)ws.dvraw,
                      (const T*)ws.dctxL, (const CellRow*)ws.cellrow, B, (const float*)ws.dsig,
-                     (const float*)L->sig, cos, sin, ws.dproj,
+                     (const T*)L->sig, cos, sin, ws.dproj,
                      ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, (const float*)ws.sdss, qr,
                      (const T*)L->kself, scale, RowMap{}, PROJ_ROWS_OUT | PROJ_PARTIALS);
   hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks * proj_rows_in_flight(d), 3 * d, 3 * d,
@@ -597,7 +597,7 @@ void record_bwd_chunk(const dm_config* c, const dm_stack_bwd_layer& ly, const fl
   record_launch<CommDqBody<T, DH>>(dim3(BH, cdiv(cc, 64)), dim3(256), qa, (unsigned)lds_attn);
   // projection VJP of the cell's rows (the column partials come with the layer's close)
   typename ProjBwdBody<T, DH>::Args pa{N, T_, d, h, nproj, c->ctx_mod == DM_CTX_FUSION ? 1 : 0, ws.dq, ws.dkraw,
-                                       ws.dkself, ws.dvraw, ws.dctxL, ws.cellrow, B, ws.dsig, L->sig, cos, sin,
+                                       ws.dkself, ws.dvraw, ws.dctxL, ws.cellrow, B, ws.dsig, (const T*)L->sig, cos, sin,
                                        ws.dproj,
                                        ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, ws.sdss,
                                        (const T*)L->qr, (const T*)L->kself, scale, map, PROJ_ROWS_OUT,
@@ -662,7 +662,7 @@ void bwd_stack_close(const dm_config* c, const dm_stack_bwd_layer& ly, const flo
   hipLaunchKernelGGL((k_proj_bwd<T, DH>), dim3(proj_grid_x(d), pchunks), dim3(256), 0, s, BT, T_, d, h, nproj,
                      fusion ? 1 : 0, (const float*)ws.dq, (const float*)ws.dkraw, (const float*)ws.dkself,
                      (const float*)ws.dvraw, (const T*)ws.dctxL, (const CellRow*)ws.cellrow, c->B,
-                     (const float*)ws.dsig, (const float*)L->sig, cos,
+                     (const float*)ws.dsig, (const T*)L->sig, cos,
                      sin, ws.dproj, ws.colpart, (const T*)L->vpre, v_gain(c, w), ws.vgpart, (const float*)ws.sdss,
                      (const T*)L->qr, (const T*)L->kself, 1.0f / sqrtf((float)DH), RowMap{}, PROJ_PARTIALS);
   hipLaunchKernelGGL(k_sum_rows_add, dim3(cdiv(3 * d, 64)), dim3(256), 0, s, pchunks * proj_rows_in_flight(d), 3 * d, 3 * d,

@@ -15,7 +15,7 @@ struct CellWs {
   void* o; float* ssq;
   float* Ap; float* Zp; float* Mp;   // committed split partials
   float* A; float* Z; float* M;      // merged committed accumulator
-  void* vin; float* gvu;
+  void* vin; void* gvu;              // v_in, g_v(u) [N, d] (storage dtype)
   size_t bytes;
 };
 
@@ -33,7 +33,7 @@ inline CellWs carve_cell(const dm_config* c, int cache_T, void* base) {
   w.Z = cv.take<float>(BH * CMAX * 4);
   w.M = cv.take<float>(BH * CMAX * 4);
   w.vin = cv.take<void>(N * c->d * esz(c->dtype));
-  w.gvu = cv.take<float>(N * c->d * 4);
+  w.gvu = cv.take<void>(N * c->d * esz(c->dtype));
   w.bytes = cv.off;
   return w;
 }
@@ -120,7 +120,7 @@ inline const float* v_gain(const dm_config* c, const dm_packed* w) {
 template <typename T, int DH, class SA>
 void run_proj_src(const dm_config* c, const dm_packed* w, const SA& sa, int M, int Tl, int Tbuf, int buf_t0,
                   int rope_t0, const float* cos, const float* sin, T* qr, T* kraw, T* kself, T* vraw, T* vpre,
-                  float* glogx, float* sig, hipStream_t s, bool small_tiles = false, const int* pos_dev = nullptr,
+                  T* glogx, T* sig, hipStream_t s, bool small_tiles = false, const int* pos_dev = nullptr,
                   int pos_cap = 0) {
   const int nseg = (c->ctx_mod == DM_CTX_LINEAR) ? 5 : 6;
   SrcRows<T> sb{(const T*)w->w_proj, c->d, nseg * c->d};
@@ -161,7 +161,7 @@ void run_proj_src(const dm_config* c, const dm_packed* w, const SA& sa, int M, i
 template <typename T, int DH>
 void run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int Tl, int Tbuf, int buf_t0,
               int rope_t0, const float* cos, const float* sin, T* qr, T* kraw, T* kself, T* vraw, T* vpre,
-              float* glogx, float* sig, hipStream_t s, const int* pos_dev = nullptr, int pos_cap = 0) {
+              T* glogx, T* sig, hipStream_t s, const int* pos_dev = nullptr, int pos_cap = 0) {
   run_proj_src<T, DH>(c, w, SrcRows<T>{xhat, c->d, M}, M, Tl, Tbuf, buf_t0, rope_t0, cos, sin, qr, kraw, kself, vraw,
                       vpre, glogx, sig, s, false, pos_dev, pos_cap);
 }
@@ -169,7 +169,7 @@ void run_proj(const dm_config* c, const dm_packed* w, const T* xhat, int M, int 
 template <typename T>
 void run_proj_dispatch(const dm_config* c, const dm_packed* w, const T* xhat, int M, int Tl, int Tbuf,
                        int buf_t0, int rope_t0, const float* cos, const float* sin, T* qr, T* kraw, T* kself,
-                       T* vraw, T* vpre, float* glogx, float* sig, hipStream_t s) {
+                       T* vraw, T* vpre, T* glogx, T* sig, hipStream_t s) {
   if (c->dh == 64)
     run_proj<T, 64>(c, w, xhat, M, Tl, Tbuf, buf_t0, rope_t0, cos, sin, qr, kraw, kself, vraw, vpre, glogx, sig, s);
   else
@@ -181,8 +181,8 @@ void run_proj_dispatch(const dm_config* c, const dm_packed* w, const T* xhat, in
 // epilogues, writing the refined rows to (Kout, Vout).
 template <typename T, int DH>
 void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N, const T* o, const float* ssq,
-                const T* kraw, const T* vraw, const float* glogx, const float* sig, const float* cos,
-                const float* sin, T* Kout, T* Vout, long out_stride, int out_row0, T* vin, float* gvu,
+                const T* kraw, const T* vraw, const T* glogx, const T* sig, const float* cos,
+                const float* sin, T* Kout, T* Vout, long out_stride, int out_row0, T* vin, T* gvu,
                 T* save1, T* save2, hipStream_t s, const AttendArgs<T>* next_attend = nullptr,
                 bool wide = false) {
   const T* normw = (const T*)w->norm_ctx_w;
@@ -381,8 +381,8 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
     }
     T* vin = sv ? sv->vin + sw * NS * d : (T*)ws.vin;
     const AttendArgs<T> next = attend_args(last ? sw : sw + 1);
-    run_refine<T, DH>(c, w, g, N, o, ssq, kraw, vraw, L->glogx, L->sig, cos, sin, Kout, Vout, out_stride,
-                      out_row0, vin, ws.gvu, sv ? sv->save1 + sw * NS * 4 * d : nullptr,
+    run_refine<T, DH>(c, w, g, N, o, ssq, kraw, vraw, (const T*)L->glogx, (const T*)L->sig, cos, sin, Kout, Vout,
+                      out_stride, out_row0, vin, (T*)ws.gvu, sv ? sv->save1 + sw * NS * 4 * d : nullptr,
                       sv ? sv->save2 + sw * NS * d : nullptr, s, (fuse && !last) ? &next : nullptr, wide);
   }
 }

@@ -231,7 +231,7 @@ template <typename T, int DH, bool DEVPOS = false> struct EpiProj {
   const float* __restrict__ sin;
   const float* __restrict__ bias;   // [3d] fp32
   T* __restrict__ qr; T* __restrict__ kraw; T* __restrict__ kself; T* __restrict__ vraw;
-  float* __restrict__ glogx; float* __restrict__ sig;
+  T* __restrict__ glogx; T* __restrict__ sig;   // storage dtype (as the reference's LayerBufs)
   int fusion;    // ctx_mod fusion: segment 5 is v_pre's x-half, stored as the raw pre-activation
   // v_norm (attention.py:218-234): v_raw = (x r) gain per head, x the stored projection,
   // r = rsqrt(mean x^2 + 1e-6); vgain [h] fp32 (nullptr = off); vpre keeps x (nullptr = not kept)
@@ -324,7 +324,8 @@ template <typename T, int DH, bool DEVPOS = false> struct EpiProj {
     }
   }
 
-  // gate logits (x-halves + bias, fp32) or sigma(v_gate) / fusion's raw v_pre x-half
+  // gate logits (x-halves + bias) or sigma(v_gate) / fusion's raw v_pre x-half, fp32 math, stored
+  // in the storage dtype
   template <int TR, int LDT>
   DM_DEV void row_unit(const float* tl, int m0, int seg, int c0) const {
     constexpr int L = DH / 4;
@@ -340,12 +341,15 @@ template <typename T, int DH, bool DEVPOS = false> struct EpiProj {
       const floatx4 v = *reinterpret_cast<const floatx4*>(tl + r * LDT + e);
       const int bb = m / Tl, t = m - bb * Tl;
       const long xrow = (long)bb * Tbuf + buf_t0 + t;
-      floatx4 o = floatx4{v.x + bs[0], v.y + bs[1], v.z + bs[2], v.w + bs[3]};
+      float o[4] = {v.x + bs[0], v.y + bs[1], v.z + bs[2], v.w + bs[3]};
       if (seg <= 4) {
-        *reinterpret_cast<floatx4*>(glogx + xrow * 2 * d + (seg - 3) * d + col) = o;
+        st4<T>(glogx + xrow * 2 * d + (seg - 3) * d + col, o);
       } else {
-        if (!fusion) o = floatx4{sigmoidf_(o.x), sigmoidf_(o.y), sigmoidf_(o.z), sigmoidf_(o.w)};
-        *reinterpret_cast<floatx4*>(sig + xrow * d + col) = o;
+        if (!fusion) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = sigmoidf_(o[i]);
+        }
+        st4<T>(sig + xrow * d + col, o);
       }
     }
   }
@@ -752,7 +756,7 @@ template <typename T, int DH, int NW> struct AttendBody {
 //            -> blend, V rows
 //   mult   [2d, 3d) v_map(u) -> v_in = lam*u + sig * tanh(.)  (fusion: v_pre u-half ->
 //          v_in = u + silu(px + .), px = v_pre x-half from the projection in the sig buffer)
-//          [3d, 4d) g_v(u)   -> fp32 scratch for GEMM 2
+//          [3d, 4d) g_v(u)   -> scratch for GEMM 2 (storage dtype, as the GEMM's raw outputs)
 // save != nullptr stores the raw GEMM outputs [rows, 4d] in this packed order.
 // ---------------------------------------------------------------------------
 template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 {
@@ -760,12 +764,12 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
   int M, ctx_mod;
   float lam;
   const T* __restrict__ kraw; const T* __restrict__ vraw;
-  const float* __restrict__ glogx; const float* __restrict__ sig;
+  const T* __restrict__ glogx; const T* __restrict__ sig;   // the projection's gate inputs
   const float* __restrict__ cos; const float* __restrict__ sin;
   const T* __restrict__ o; const T* __restrict__ normw;   // u = o * rs * w for v_in's lam*u term
   T* __restrict__ Kout; T* __restrict__ Vout;             // refined rows: (b,h) at bh*out_stride,
   long out_stride; int out_row0;                          //   chunk row p at row out_row0 + p
-  T* __restrict__ vin; float* __restrict__ gvu;
+  T* __restrict__ vin; T* __restrict__ gvu;               // v_in, g_v(u) for GEMM 2 (storage dtype)
   T* __restrict__ save;
   // Per-head norms of the GEMM outputs (attention.py:238-269), fp32 gains [h], nullptr = off:
   // kgain k_ctx (norm_kctx), vgain the linear ctx_mod's v_ctx (norm_vctx). Either needs block
@@ -779,15 +783,16 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
   // inputs and outputs are runs of 4 consecutive elements. With up to two groups the inputs
   // are gathered during the k-loop's last stage; with more, at the start of the epilogue.
   struct GroupPre {
-    floatx4 f[4];                   // K: gx_a, gx_b, cos, sin; linear V: gx x2; v_map: sig x4
+    typename Raw4<T>::type x[4];    // K: gx_a, gx_b; linear V: gx x2; v_map: sig x4 (storage dtype)
+    floatx4 f[2];                   // K: cos, sin
     typename Raw4<T>::type h[8];    // K: kraw_a, kraw_b; linear V: v_raw x2; v_map: o x4, norm weight x4
   };
   static constexpr bool LATE = NG <= 2;
   struct TilePre {
     GroupPre p[LATE ? NG : 1];
   };
-  // tile_prefetch issues exactly 12 loads per group (one per f / h slot, unconditionally)
-  static constexpr int LATE_GATHERS = LATE ? 12 * NG : 0;
+  // tile_prefetch issues exactly 14 loads per group (one per x / f / h slot, unconditionally)
+  static constexpr int LATE_GATHERS = LATE ? 14 * NG : 0;
   DM_DEV TilePre tile_prefetch(int m0, int n0) const {
     TilePre pr{};
     if constexpr (LATE) {
@@ -806,21 +811,24 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
     // The (block-uniform) branches only pick addresses; the loads follow them
     // unconditionally (unused slots re-read a valid address), so no loaded value
     // has to be merged, and waited for, where the branches join.
-    const float* fp[4];
+    const T* xp[4];
+    const float* fp[2];
     const T* hp[8];
-    const float* f0 = glogx + xrow * 2 * d;
+    const T* x0 = glogx + xrow * 2 * d;
     const T* h0 = kraw + ((long)b * h * g.Tbuf + t) * DH;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) fp[k] = f0;
+    for (int k = 0; k < 4; ++k) xp[k] = x0;
+    fp[0] = cos + (long)pos * (DH / 2);
+    fp[1] = sin + (long)pos * (DH / 2);
 #pragma unroll
     for (int k = 0; k < 8; ++k) hp[k] = h0;
     if (n0 < 2 * d) {
       const int hd = n0 / (2 * DH), jj = 16 * ((n0 % (2 * DH)) / 64) + lc0;
       const long lrow = (((long)b * h + hd) * g.Tbuf + t) * DH + jj;
-      fp[0] = f0 + hd * DH + jj;
-      fp[1] = fp[0] + DH / 2;
-      fp[2] = cos + (long)pos * (DH / 2) + jj;
-      fp[3] = sin + (long)pos * (DH / 2) + jj;
+      xp[0] = x0 + hd * DH + jj;
+      xp[1] = xp[0] + DH / 2;
+      fp[0] += jj;
+      fp[1] += jj;
       hp[0] = kraw + lrow;
       hp[1] = hp[0] + DH / 2;
     } else if (ctx_mod == 0) {
@@ -829,13 +837,13 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
       const long lrow = (((long)b * h + hd) * g.Tbuf + t) * DH + e;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        fp[j] = f0 + d + hd * DH + e + 16 * j;
+        xp[j] = x0 + d + hd * DH + e + 16 * j;
         hp[j] = vraw + lrow + 16 * j;
       }
     } else if (n0 < 3 * d) {
       const int c0 = n0 - 2 * d + lc0;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) fp[k] = sig + xrow * d + c0 + 16 * k;
+      for (int k = 0; k < 4; ++k) xp[k] = sig + xrow * d + c0 + 16 * k;
       if (ctx_mod == 1 || ctx_mod == 3) {   // mult_res, fusion: v_in has a u term
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -846,7 +854,9 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
     }
     GroupPre pr;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) pr.f[k] = ld_global<floatx4>(fp[k]);
+    for (int k = 0; k < 4; ++k) pr.x[k] = ld_global<typename Raw4<T>::type>(xp[k]);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) pr.f[k] = ld_global<floatx4>(fp[k]);
 #pragma unroll
     for (int k = 0; k < 8; ++k) pr.h[k] = ld_global<typename Raw4<T>::type>(hp[k]);
     return pr;
@@ -933,7 +943,7 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
     const int orow0 = DEVPOS ? dev_position(g.pos_dev, g.pos_cap) : out_row0;
     if (n0 < 2 * d) {
       float gxa[4], gxb[4], cs[4], sn[4], ka[4], kb[4];
-      unpackf4(pr.f[0], gxa); unpackf4(pr.f[1], gxb); unpackf4(pr.f[2], cs); unpackf4(pr.f[3], sn);
+      unpack4<T>(pr.x[0], gxa); unpack4<T>(pr.x[1], gxb); unpackf4(pr.f[0], cs); unpackf4(pr.f[1], sn);
       unpack4<T>(pr.h[0], ka); unpack4<T>(pr.h[1], kb);
       settle(gxa); settle(gxb); settle(cs); settle(sn); settle(ka); settle(kb);   // all loads before any store
       if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
@@ -954,7 +964,7 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
     } else if (ctx_mod == 0) {
       float gx[2][4], vr[2][4];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) { unpackf4(pr.f[j], gx[j]); unpack4<T>(pr.h[j], vr[j]); settle(gx[j]); settle(vr[j]); }
+      for (int j = 0; j < 2; ++j) { unpack4<T>(pr.x[j], gx[j]); unpack4<T>(pr.h[j], vr[j]); settle(gx[j]); settle(vr[j]); }
       if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
       const int cl = n0 - 2 * d;
       const int hd = cl / (2 * DH), e = 32 * ((cl % (2 * DH)) / 64) + lc0;
@@ -971,7 +981,7 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
       float sg[4][4], ov[4][4], nw[4][4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        unpackf4(pr.f[k], sg[k]);
+        unpack4<T>(pr.x[k], sg[k]);
         settle(sg[k]);
         if (ctx_mod == 1 || ctx_mod == 3) {
           unpack4<T>(pr.h[k], ov[k]); unpack4<T>(pr.h[4 + k], nw[k]); settle(ov[k]); settle(nw[k]);
@@ -998,8 +1008,7 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
       if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
       const int c0 = n0 - 3 * d + lc0;
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        *reinterpret_cast<floatx4*>(gvu + (long)m * d + c0 + 16 * k) = floatx4{a[k][0], a[k][1], a[k][2], a[k][3]};
+      for (int k = 0; k < 4; ++k) st4<T>(gvu + (long)m * d + c0 + 16 * k, a[k]);
     }
   }
 };
@@ -1012,31 +1021,28 @@ template <typename T, int DH, bool DEVPOS = false> struct EpiSweep2 {
   CellGeom g;
   int M;
   const T* __restrict__ vraw;
-  const float* __restrict__ glogx;
-  const float* __restrict__ gvu;
+  const T* __restrict__ glogx;
+  const T* __restrict__ gvu;
   T* __restrict__ Vout;
   long out_stride; int out_row0;
   T* __restrict__ save2;
 
   struct TilePre {
-    floatx4 gx[2], gu[2];
-    Raw8<T> vr;
+    Raw8<T> gx, gu, vr;
   };
-  // vector-memory load instructions tile_prefetch issues (Raw8 = one 16-byte load in bf16)
-  static constexpr int LATE_GATHERS = 4 + (int)(sizeof(T) / 2);
+  // vector-memory load instructions tile_prefetch issues (Raw8 = one 16-byte load in bf16, two in
+  // fp32: 16-byte loads, which the compiler cannot merge into fewer)
+  static constexpr int LATE_GATHERS = 3 * (int)(sizeof(T) / 2);
   DM_DEV TilePre tile_prefetch(int m0, int n0) const {
     const int r = threadIdx.x >> 2, col = n0 + 8 * (threadIdx.x & 3);
     const int m = min(m0 + r, M - 1);
     const int b = m / g.c, t = g.buf_t0 + m - b * g.c;
     const int hd = col / DH, e = col - hd * DH;
-    const float* gx = glogx + ((long)b * g.Tbuf + t) * 2 * g.d + g.d + col;
-    const float* gu = gvu + (long)m * g.d + col;
+    const T* gx = glogx + ((long)b * g.Tbuf + t) * 2 * g.d + g.d + col;
+    const T* gu = gvu + (long)m * g.d + col;
     TilePre pr;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      pr.gx[k] = ld_global<floatx4>(gx + 4 * k);
-      pr.gu[k] = ld_global<floatx4>(gu + 4 * k);
-    }
+    pr.gx = ld8_global(gx);
+    pr.gu = ld8_global(gu);
     pr.vr = ld8_global(vraw + (((long)b * g.h + hd) * g.Tbuf + t) * DH + e);
     return pr;
   }
@@ -1049,9 +1055,9 @@ template <typename T, int DH, bool DEVPOS = false> struct EpiSweep2 {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       unpackf4(*reinterpret_cast<const floatx4*>(tile + r * LDT + c0 + 4 * k), a + 4 * k);
-      unpackf4(pr.gx[k], gx + 4 * k);
-      unpackf4(pr.gu[k], gu + 4 * k);
     }
+    unpack8<T>(pr.gx, gx);
+    unpack8<T>(pr.gu, gu);
     unpack8<T>(pr.vr, vr);
     if (m >= M) return;
     settle(gx); settle(gu); settle(vr);   // all loads before any store
@@ -1084,34 +1090,33 @@ template <typename T, int DH> struct EpiSweep2Head {
   CellGeom g;
   int M;
   const T* __restrict__ vraw;
-  const float* __restrict__ glogx;
-  const float* __restrict__ gvu;
+  const T* __restrict__ glogx;
+  const T* __restrict__ gvu;
   T* __restrict__ Vout;
   long out_stride; int out_row0;
   T* __restrict__ save2;
   const float* __restrict__ vgain = nullptr;   // v_ctx norm gains [h] (norm_vctx), nullptr = off
   struct TilePre {
-    floatx4 gx[CW / 4], gu[CW / 4];
-    Raw8<T> vr[CW / 8];
+    Raw8<T> gx[CW / 8], gu[CW / 8], vr[CW / 8];
   };
-  // vector-memory load instructions tile_prefetch issues (Raw8 = one 16-byte load in bf16)
-  static constexpr int LATE_GATHERS = 2 * (CW / 4) + (CW / 8) * (int)(sizeof(T) / 2);
+  // vector-memory load instructions tile_prefetch issues (Raw8 = one 16-byte load in bf16, two in
+  // fp32: 16-byte loads, which the compiler cannot merge into fewer)
+  static constexpr int LATE_GATHERS = 3 * (CW / 8) * (int)(sizeof(T) / 2);
   DM_DEV TilePre tile_prefetch(int m0, int n0) const {
     const int r = threadIdx.x >> 2, e0 = CW * (threadIdx.x & 3), col = n0 + e0;
     const int m = min(m0 + r, M - 1);
     const int b = m / g.c, t = g.buf_t0 + m - b * g.c;
     const int hd = n0 / DH;
-    const float* gx = glogx + ((long)b * g.Tbuf + t) * 2 * g.d + g.d + col;
-    const float* gu = gvu + (long)m * g.d + col;
+    const T* gx = glogx + ((long)b * g.Tbuf + t) * 2 * g.d + g.d + col;
+    const T* gu = gvu + (long)m * g.d + col;
     const T* vr = vraw + (((long)b * g.h + hd) * g.Tbuf + t) * DH + e0;
     TilePre pr;
 #pragma unroll
-    for (int k = 0; k < CW / 4; ++k) {
-      pr.gx[k] = ld_global<floatx4>(gx + 4 * k);
-      pr.gu[k] = ld_global<floatx4>(gu + 4 * k);
+    for (int k = 0; k < CW / 8; ++k) {
+      pr.gx[k] = ld8_global(gx + 8 * k);
+      pr.gu[k] = ld8_global(gu + 8 * k);
+      pr.vr[k] = ld8_global(vr + 8 * k);
     }
-#pragma unroll
-    for (int k = 0; k < CW / 8; ++k) pr.vr[k] = ld8_global(vr + 8 * k);
     return pr;
   }
   template <int BM, int BN, int LDT>
@@ -1128,11 +1133,13 @@ template <typename T, int DH> struct EpiSweep2Head {
 #pragma unroll
     for (int k = 0; k < CW / 4; ++k) {
       unpackf4(*reinterpret_cast<const floatx4*>(tile + r * LDT + e0 + 4 * k), a + 4 * k);
-      unpackf4(pr.gx[k], gx + 4 * k);
-      unpackf4(pr.gu[k], gu + 4 * k);
     }
 #pragma unroll
-    for (int k = 0; k < CW / 8; ++k) unpack8<T>(pr.vr[k], vr + 8 * k);
+    for (int k = 0; k < CW / 8; ++k) {
+      unpack8<T>(pr.gx[k], gx + 8 * k);
+      unpack8<T>(pr.gu[k], gu + 8 * k);
+      unpack8<T>(pr.vr[k], vr + 8 * k);
+    }
     float vc[CW];   // v_ctx as the blend takes it: normed (from and to stored values) with the norm on
 #pragma unroll
     for (int i = 0; i < CW; ++i) vc[i] = a[i];

@@ -157,7 +157,7 @@ int dm_layer_proj(const dm_config* c, const dm_packed* w, const void* x, const f
       xin = (const bf16*)L->xhat;
     }
     run_proj_dispatch<bf16>(c, w, xin, M, L->T, L->T, 0, 0, cos, sin, (bf16*)L->qr, (bf16*)L->kraw,
-                            (bf16*)L->kself, (bf16*)L->vraw, (bf16*)L->vpre, L->glogx, L->sig, s);
+                            (bf16*)L->kself, (bf16*)L->vraw, (bf16*)L->vpre, (bf16*)L->glogx, (bf16*)L->sig, s);
   } else {
     const float* xin = (const float*)x;
     if (norm) {
@@ -166,7 +166,8 @@ int dm_layer_proj(const dm_config* c, const dm_packed* w, const void* x, const f
       xin = (const float*)L->xhat;
     }
     run_proj_dispatch<float>(c, w, xin, M, L->T, L->T, 0, 0, cos, sin, (float*)L->qr, (float*)L->kraw,
-                             (float*)L->kself, (float*)L->vraw, (float*)L->vpre, L->glogx, L->sig, s);
+                             (float*)L->kself, (float*)L->vraw, (float*)L->vpre, (float*)L->glogx, (float*)L->sig,
+                             s);
   }
   DM_HIP(hipGetLastError());
   return DM_OK;
@@ -317,8 +318,8 @@ namespace dm {
 
 struct DecWs {
   void* q; void* kraw; void* kself; void* vraw;
-  float* glogx; float* sig; float* o; float* ssq; float* part;
-  void* vin; float* gvu;
+  void* glogx; void* sig; float* o; float* ssq; float* part;   // glogx, sig: storage dtype
+  void* vin; void* gvu;
   float* rope; void* kst; void* vst;   // device position: RoPE rows, refined rows before the tape write
   size_t bytes;
 };
@@ -334,13 +335,13 @@ DecWs carve_dec(const dm_config* c, int tape_T, void* base) {
   w.kraw = take(B * d * e);
   w.kself = take(B * d * e);
   w.vraw = take(B * d * e);
-  w.glogx = (float*)take(B * 2 * d * 4);
-  w.sig = (float*)take(B * d * 4);
+  w.glogx = take(B * 2 * d * e);
+  w.sig = take(B * d * e);
   w.o = (float*)take(B * d * 4);
   w.ssq = (float*)take(B * c->h * 4);
   w.part = (float*)take((ns ? ns : 1) * B * c->h * (c->dh + 2) * 4);
   w.vin = take(B * d * e);
-  w.gvu = (float*)take(B * d * 4);
+  w.gvu = take(B * d * e);
   w.rope = (float*)take(c->dh * 4);
   w.kst = take(B * d * e);
   w.vst = take(B * d * e);
@@ -372,7 +373,7 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
     rs = ws.rope + DH / 2;
   }
   run_proj<T, DH>(c, w, (const T*)a->xhat, B, 1, 1, 0, dev_pos ? 0 : pos, rc, rs, (T*)ws.q, (T*)ws.kraw,
-                  (T*)ws.kself, (T*)ws.vraw, nullptr, ws.glogx, ws.sig, s,
+                  (T*)ws.kself, (T*)ws.vraw, nullptr, (T*)ws.glogx, (T*)ws.sig, s,
                   dev_direct ? (const int*)a->pos_dev : nullptr, a->tape_T);
   const int nsplit = dev_pos ? cdiv(a->tape_T, DEC_SPLIT) : (pos > lo ? cdiv(pos - lo, DEC_SPLIT) : 0);
   DecodeArgs<T> da{B, h, d, a->tape_T, pos, lo, DEC_SPLIT, nsplit, 1.0f / sqrtf((float)DH),
@@ -397,18 +398,19 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
     g.pos_dev = (const int*)a->pos_dev;
     g.pos_cap = a->tape_T;
     g.cache_T = a->tape_T;
-    run_refine<T, DH>(c, w, g, B, (const T*)a->o_cat, ws.ssq, (const T*)ws.kraw, (const T*)ws.vraw, ws.glogx,
-                      ws.sig, cos, sin, (T*)a->K_tape, (T*)a->V_tape, (long)a->tape_T * DH, 0, (T*)ws.vin, ws.gvu,
-                      nullptr, nullptr, s);
+    run_refine<T, DH>(c, w, g, B, (const T*)a->o_cat, ws.ssq, (const T*)ws.kraw, (const T*)ws.vraw,
+                      (const T*)ws.glogx, (const T*)ws.sig, cos, sin, (T*)a->K_tape, (T*)a->V_tape,
+                      (long)a->tape_T * DH, 0, (T*)ws.vin, (T*)ws.gvu, nullptr, nullptr, s);
   } else if (dev_pos) {
-    run_refine<T, DH>(c, w, g, B, (const T*)a->o_cat, ws.ssq, (const T*)ws.kraw, (const T*)ws.vraw, ws.glogx,
-                      ws.sig, rc, rs, (T*)ws.kst, (T*)ws.vst, (long)DH, 0, (T*)ws.vin, ws.gvu, nullptr, nullptr, s);
+    run_refine<T, DH>(c, w, g, B, (const T*)a->o_cat, ws.ssq, (const T*)ws.kraw, (const T*)ws.vraw,
+                      (const T*)ws.glogx, (const T*)ws.sig, rc, rs, (T*)ws.kst, (T*)ws.vst, (long)DH, 0, (T*)ws.vin,
+                      (T*)ws.gvu, nullptr, nullptr, s);
     hipLaunchKernelGGL((k_decode_commit<T, DH>), dim3(B * h), dim3(DH), 0, s, (const int*)a->pos_dev, a->tape_T,
                        (const T*)ws.kst, (const T*)ws.vst, (T*)a->K_tape, (T*)a->V_tape);
   } else {
-    run_refine<T, DH>(c, w, g, B, (const T*)a->o_cat, ws.ssq, (const T*)ws.kraw, (const T*)ws.vraw, ws.glogx,
-                      ws.sig, cos, sin, (T*)a->K_tape, (T*)a->V_tape, (long)a->tape_T * DH, pos, (T*)ws.vin,
-                      ws.gvu, nullptr, nullptr, s);
+    run_refine<T, DH>(c, w, g, B, (const T*)a->o_cat, ws.ssq, (const T*)ws.kraw, (const T*)ws.vraw,
+                      (const T*)ws.glogx, (const T*)ws.sig, cos, sin, (T*)a->K_tape, (T*)a->V_tape,
+                      (long)a->tape_T * DH, pos, (T*)ws.vin, (T*)ws.gvu, nullptr, nullptr, s);
   }
   if (a->y != nullptr) {
     SrcRows<T> ao{(const T*)a->o_cat, d, B};
@@ -494,7 +496,7 @@ static __global__ __launch_bounds__(256) void k_head_ssq(const T* __restrict__ o
 }
 
 struct RefineWs {
-  float* ssq; void* vin; float* gvu;
+  float* ssq; void* vin; void* gvu;
   size_t bytes;
 };
 inline RefineWs carve_refine(const dm_config* c, int t, void* base) {
@@ -503,7 +505,7 @@ inline RefineWs carve_refine(const dm_config* c, int t, void* base) {
   Carver cv(base);
   w.ssq = cv.take<float>(N * c->h * 4);
   w.vin = cv.take<void>(N * c->d * esz(c->dtype));
-  w.gvu = cv.take<float>(N * c->d * 4);
+  w.gvu = cv.take<void>(N * c->d * esz(c->dtype));
   w.bytes = cv.off;
   return w;
 }
@@ -532,8 +534,9 @@ void run_refine_kv(const dm_config* c, const dm_packed* w, const dm_layer_bufs* 
   g.kmod_mode = c->kmod_mode;
   g.v_clamp_tau = c->v_clamp_tau;
   g.rope_t0 = 0;
-  run_refine<T, DH>(c, w, g, N, (const T*)o_cat, ws.ssq, (const T*)L->kraw, (const T*)L->vraw, L->glogx, L->sig,
-                    cos, sin, (T*)K_out, (T*)V_out, (long)t * DH, 0, (T*)ws.vin, ws.gvu, nullptr, nullptr, s);
+  run_refine<T, DH>(c, w, g, N, (const T*)o_cat, ws.ssq, (const T*)L->kraw, (const T*)L->vraw, (const T*)L->glogx,
+                    (const T*)L->sig, cos, sin, (T*)K_out, (T*)V_out, (long)t * DH, 0, (T*)ws.vin, (T*)ws.gvu, nullptr,
+                    nullptr, s);
 }
 
 }  // namespace dm

@@ -39,7 +39,7 @@ void record_chunk(const dm_config* c, const dm_stack_layer& ly, const float* cos
   }
   // (a chunk's M = B * c rows: 128 x 128 blocks, several per layer and CU)
   run_proj_src<T, DH>(c, w, sx, M, cc, L->T, pos0, pos0, cos, sin, (T*)L->qr, (T*)L->kraw, (T*)L->kself,
-                      (T*)L->vraw, (T*)L->vpre, L->glogx, L->sig, nullptr, true);
+                      (T*)L->vraw, (T*)L->vpre, (T*)L->glogx, (T*)L->sig, nullptr, true);
   // the cell (as dm_layer_fwd: with the tape its sweep states go there)
   const CellWs ws = carve_cell(c, cache_T, ly.workspace);
   const T* o_last;

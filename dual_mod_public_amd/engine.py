@@ -154,9 +154,9 @@ class LayerBufs:
         self.kraw = torch.empty(B, h, T, dh, **kw)
         self.kself = torch.empty(B, h, T, dh, **kw)
         self.vraw = torch.empty(B, h, T, dh, **kw)
-        self.glogx = torch.empty(B, T, 2 * d, device=device, dtype=torch.float32)
-        self.sig = (torch.empty(B, T, d, device=device, dtype=torch.float32)
-                    if cfg.ctx_mod != "linear" else None)
+        # gate inputs in the storage dtype, as the reference's LayerBufs (fused_sweep.py:1189, 1207)
+        self.glogx = torch.empty(B, T, 2 * d, **kw)
+        self.sig = torch.empty(B, T, d, **kw) if cfg.ctx_mod != "linear" else None
         # v_raw before the v_norm, kept for the backward
         self.vpre = torch.empty(B, h, T, dh, **kw) if getattr(cfg, "v_norm", "none") == "rms" else None
 

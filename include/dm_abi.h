@@ -11,8 +11,8 @@
  *   x, y        [B, T, d]        storage dtype
  *   head bufs   [B, h, T, dh]    storage dtype (qr, kraw, kself, vraw)
  *   K/V cache   [B, h, Tc, dh]   storage dtype, rows [0, pos0) committed
- *   glogx       [B, T, 2d] fp32  x-half of the key|value gate logits + bias
- *   sig         [B, T, d]  fp32  sigmoid(v_gate(xhat)) (ctx_mod mult/mult_res)
+ *   glogx       [B, T, 2d] storage dtype  x-half of the key|value gate logits + bias
+ *   sig         [B, T, d]  storage dtype  sigmoid(v_gate(xhat)) (ctx_mod mult/mult_res)
  *   cos, sin    [Tc, dh/2] fp32  RoPE tables (models/dualmod/rope.py:13-19)
  *
  * Reference interface each entry point replaces (paths in Atom-101/dual_mod_public):
@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DM_ABI_VERSION 6
+#define DM_ABI_VERSION 7
 
 typedef enum dm_status {
   DM_OK = 0,
@@ -137,8 +137,8 @@ typedef struct dm_layer_bufs {
   void* kraw;               /* [B, h, T, dh] unrotated raw key (blend space) */
   void* kself;              /* [B, h, T, dh] rotated raw key (self column) */
   void* vraw;               /* [B, h, T, dh] raw value */
-  float* glogx;             /* [B, T, 2d] */
-  float* sig;               /* [B, T, d] or NULL (linear) */
+  void* glogx;              /* [B, T, 2d] storage dtype (LayerBufs.glog_x, fused_sweep.py:1189) */
+  void* sig;                /* [B, T, d] storage dtype, or NULL (linear) (fused_sweep.py:1207) */
   void* vpre;               /* [B, h, T, dh] v_raw before the v_norm (DM_NORM_V only, kept for the
                                backward; may be NULL for forward-only use) */
 } dm_layer_bufs;

@@ -31,7 +31,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 
 def test_abi_version():
-    assert L.load().dm_abi_version() == 6
+    assert L.load().dm_abi_version() == 7
 
 
 def _conf(**kw):
