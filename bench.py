@@ -323,6 +323,73 @@ def bench_c4_ladder(dev, steps=3, warmup=1):
             "steps": steps, "warmup": warmup, "ladder": ladder}
 
 
+def bench_c4_trunk(dev, n_layers=24, steps=2, warmup=1, reserve_gb=64.0):
+    """BASELINE config 4 as written: the 24-layer d=2048 trunk (16 x 128 heads, SwiGLU ffn 5632, tied
+    embeddings, vocab 32000) at B=4, T=4096, token ids uniform random, bf16, one training step (forward
+    + backward, trunk.HipTrunk captured as one HIP graph) per K in the ladder; the per-layer DM cell
+    timed inside the step (HIP events around each layer's attention forward and backward in an eager
+    step). Forward tapes for as many layers as fit beside ``reserve_gb`` of other state; the others
+    recompute their cells (same results)."""
+    from dual_mod_public_amd.model import DualModLM
+    from dual_mod_public_amd.trunk import CellTimer, HipTrunk
+    B, T, d, h, c = C4["B"], C4["T"], C4["d"], C4["h"], C4["c"]
+    cfg = DualModConfig(d_model=d, n_heads=h, n_layers=n_layers, vocab_size=32000, max_seq_len=T, ctx_mod="mult_res",
+                        mlp_hidden_override=5632, dtype="bf16")
+    torch.manual_seed(C4["wseed"])
+    with torch.device(dev):
+        m = DualModLM(cfg, dtype=torch.bfloat16)
+    with torch.no_grad():
+        m.tok_emb.weight.normal_(0.0, 0.02)   # model.py:187-195 init scale (nn.Embedding's default is N(0, 1))
+    n_params = sum(p.numel() for p in m.parameters())
+    g = torch.Generator(device=dev).manual_seed(C4["xseed"])
+    idx = torch.randint(0, cfg.vocab_size, (B, T), generator=g, device=dev)
+    tg = torch.randint(0, cfg.vocab_size, (B, T), generator=g, device=dev)
+    Fh = cfg.mlp_hidden
+    ladder = []
+    for K in C4["ladder"]:
+        sched = uniform_chunks(T, c, K)
+        torch.cuda.empty_cache()
+        free = torch.cuda.mem_get_info(dev)[0]
+        tr = HipTrunk(m, B, T, schedule=sched, tape_budget=max(0.0, free - reserve_gb * 1e9))
+        for _ in range(warmup):
+            tr.train_step(idx, tg)
+        tr.timer = CellTimer(n_layers)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        tr.train_step(idx, tg)                 # eager, the cells timed in place
+        torch.cuda.synchronize()
+        eager = time.perf_counter() - t0
+        cells = tr.timer.ms()
+        tr.timer = None
+        tr.capture()
+        dt = timed(lambda: tr.train_step(idx, tg), steps)
+        loss = float(tr.loss)
+        fpt = fwd_flops_per_token(d, T, c, K)
+        cell_ms = [f + b for f, b in cells]
+        mean_cell = sum(cell_ms) / n_layers
+        mlp_f, head_f = 2 * 3 * d * Fh, 2 * d * cfg.vocab_size
+        trunk_f = 3 * (n_layers * (fpt + mlp_f) + head_f)
+        ladder.append({"K": K, "step_ms": dt * 1e3, "tokens_per_s": B * T / dt, "loss": loss,
+                       "cell_ms_per_layer_fwdbwd": mean_cell,
+                       "cell_fwd_ms_per_layer": sum(f for f, _ in cells) / n_layers,
+                       "cell_bwd_ms_per_layer": sum(b for _, b in cells) / n_layers,
+                       "cell_frac": 3 * fpt * B * T / (mean_cell / 1e3) / 1e12 / PEAK_BF16_TFLOPS,
+                       "cells_share_of_eager_step": sum(cell_ms) / (eager * 1e3), "eager_step_ms": eager * 1e3,
+                       "trunk_frac": trunk_f * B * T / dt / 1e12 / PEAK_BF16_TFLOPS,
+                       "tape_layers": tr.n_tape})
+        del tr
+        torch.cuda.empty_cache()
+    del m
+    torch.cuda.empty_cache()
+    return {"workload": f"C4: {n_layers}-layer d={d} trunk ({h}x{d // h}, SwiGLU {Fh}, tied vocab 32000, "
+                        f"{n_params / 1e9:.2f}B params), B={B} T={T} c={c}, one training step (embedding, attention + "
+                        "MLP per layer, head + CE loss, full backward into a flat fp32 gradient buffer) per K, "
+                        "captured as one HIP graph; the DM cell timed per layer inside an eager step",
+            "flops": "cell: 3 x fwd_flops_per_token per layer; trunk_frac adds the MLP (3 x 6 d ffn) and head "
+                     "(3 x 2 d V) per token",
+            "steps": steps, "warmup": warmup, "ladder": ladder}
+
+
 def bench_c4_wavefront(dev, n_layers=8, steps=2, warmup=1):
     """Config 4's trunk attention sublayers as a layer-batched stack: n_layers d=2048, 16 x 128
     sublayers (one weight set) at B=4, T=4096, c=64, forward (tape) + reverse-scan backward per
@@ -433,6 +500,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="skip the config-4 K ladder")
     ap.add_argument("--no-stack", action="store_true", help="skip the layer-stack (layer-batched) sub-benchmark")
+    ap.add_argument("--c4-trunk-layers", type=int, default=24,
+                    help="layers of the config-4 trunk training step (0: skip)")
     ap.add_argument("--c4-stack-layers", type=int, default=8,
                     help="layers of the config-4 layer-batched K ladder (0: skip)")
     ap.add_argument("--stack-layers", type=int, default=24,
@@ -579,6 +648,8 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_c4 and args.workload != "c4":
         out["c4"] = bench_c4_ladder(dev)
+        if args.c4_trunk_layers > 0:
+            out["c4"]["trunk"] = bench_c4_trunk(dev, n_layers=args.c4_trunk_layers)
         if args.c4_stack_layers > 0:
             out["c4"]["wavefront"] = bench_c4_wavefront(dev, n_layers=args.c4_stack_layers)
     if not args.no_stack and args.workload != "c4":

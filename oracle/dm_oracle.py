@@ -451,15 +451,21 @@ def _attn_sd(bsd):
     return {k[len("attn."):]: v for k, v in bsd.items() if k.startswith("attn.")}
 
 
-def lm_forward(cfg, sd, idx, cos, sin):
+def lm_forward(cfg, sd, idx, cos, sin, schedule=None):
     """model.py:267-281 with the exact sequential scan per layer (Block.forward,
     model.py:123-125): logits [B, T, V]. ``sd`` holds the LM's parameter names
-    (tok_emb.weight, blocks.{l}.attn.*, blocks.{l}.mlp.w1..., norm_f.weight, lm_head.weight)."""
+    (tok_emb.weight, blocks.{l}.attn.*, blocks.{l}.mlp.w1..., norm_f.weight, lm_head.weight).
+    ``schedule`` runs each layer's attention as the chunked Jacobi layer instead (the
+    engine's forward, engines/wavescan/engine/forward.py:95-113)."""
     x = sd["tok_emb.weight"][idx]
     for l in range(cfg.n_layers):
         b = _block_sd(sd, l)
         xhat = rms_norm(x, b["attn_norm.weight"], 1e-5)
-        x = x + _lin(sequential_scan(cfg, _attn_sd(b), xhat, cos, sin), _attn_sd(b), "wo")
+        if schedule is None:
+            o = sequential_scan(cfg, _attn_sd(b), xhat, cos, sin)
+        else:
+            o = layer_forward(cfg, _attn_sd(b), xhat, cos, sin, schedule)[0]
+        x = x + _lin(o, _attn_sd(b), "wo")
         x = x + swiglu(b, rms_norm(x, b["mlp_norm.weight"], 1e-5))
     w = sd.get("lm_head.weight", sd["tok_emb.weight"])
     return rms_norm(x, sd["norm_f.weight"], 1e-5) @ w.t()

@@ -405,6 +405,19 @@ def test_lm_decode_is_teacher_forced():
     assert relerr(out, ref) < TOL
 
 
+def test_lm_chunked_schedule_exact_equals_scan_and_differs_below_c():
+    """lm_forward with a chunk schedule (the trunk step's oracle): K = c cells per layer give the
+    sequential-scan model (nilpotency, scan_cell_fwd.py:1-10), K < c a different one."""
+    cfg = _lm_cfg()
+    sd = _lm_sd(cfg)
+    B, T = 2, 16
+    idx = torch.randint(0, cfg.vocab_size, (B, T), generator=torch.Generator().manual_seed(4))
+    cos, sin = O.build_rope_cache(T, cfg.head_dim, cfg.rope_theta, dtype=D)
+    ref = O.lm_forward(cfg, sd, idx, cos, sin)
+    assert relerr(O.lm_forward(cfg, sd, idx, cos, sin, schedule=O.uniform_chunks(T, 8)), ref) < TOL
+    assert relerr(O.lm_forward(cfg, sd, idx, cos, sin, schedule=O.uniform_chunks(T, 8, 2)), ref) > 1e-6
+
+
 @pytest.mark.parametrize("W,c", [(5, 8), (9, 8), (20, 8), (3, 4)])
 def test_windowed_cells_equal_windowed_scan(W, c):
     """The local window on the chunk cells (chunk_attend's window masks) with K = c sweeps
