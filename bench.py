@@ -323,13 +323,13 @@ def bench_c4_ladder(dev, steps=3, warmup=1):
             "steps": steps, "warmup": warmup, "ladder": ladder}
 
 
-def bench_c4_trunk(dev, n_layers=24, steps=2, warmup=1, reserve_gb=64.0):
+def bench_c4_trunk(dev, n_layers=24, steps=2, warmup=1):
     """BASELINE config 4 as written: the 24-layer d=2048 trunk (16 x 128 heads, SwiGLU ffn 5632, tied
     embeddings, vocab 32000) at B=4, T=4096, token ids uniform random, bf16, one training step (forward
     + backward, trunk.HipTrunk captured as one HIP graph) per K in the ladder; the per-layer DM cell
     timed inside the step (HIP events around each layer's attention forward and backward in an eager
-    step). Forward tapes for as many layers as fit beside ``reserve_gb`` of other state; the others
-    recompute their cells (same results)."""
+    step). Forward tapes for as many layers as fit in the memory left (HipTrunk's tape_budget "auto");
+    the others recompute their cells (same results)."""
     from dual_mod_public_amd.model import DualModLM
     from dual_mod_public_amd.trunk import CellTimer, HipTrunk
     B, T, d, h, c = C4["B"], C4["T"], C4["d"], C4["h"], C4["c"]
@@ -349,8 +349,7 @@ def bench_c4_trunk(dev, n_layers=24, steps=2, warmup=1, reserve_gb=64.0):
     for K in C4["ladder"]:
         sched = uniform_chunks(T, c, K)
         torch.cuda.empty_cache()
-        free = torch.cuda.mem_get_info(dev)[0]
-        tr = HipTrunk(m, B, T, schedule=sched, tape_budget=max(0.0, free - reserve_gb * 1e9))
+        tr = HipTrunk(m, B, T, schedule=sched, tape_budget="auto")
         for _ in range(warmup):
             tr.train_step(idx, tg)
         tr.timer = CellTimer(n_layers)
@@ -379,6 +378,25 @@ def bench_c4_trunk(dev, n_layers=24, steps=2, warmup=1, reserve_gb=64.0):
                        "tape_layers": tr.n_tape})
         del tr
         torch.cuda.empty_cache()
+    # the same step layer-batched: every block (attention + its MLP tail) in the wavefront, the
+    # forward tapes kept when every layer's fits (else every cell recomputed in the backward)
+    wf = []
+    for K in C4["ladder"]:
+        sched = uniform_chunks(T, c, K)
+        torch.cuda.empty_cache()
+        tr = HipTrunk(m, B, T, schedule=sched, tape_budget="auto", wavefront=True)
+        for _ in range(warmup):
+            tr.train_step(idx, tg)
+        tr.capture()
+        dt = timed(lambda: tr.train_step(idx, tg), steps)
+        fpt = fwd_flops_per_token(d, T, c, K)
+        mlp_f, head_f = 2 * 3 * d * Fh, 2 * d * cfg.vocab_size
+        trunk_f = 3 * (n_layers * (fpt + mlp_f) + head_f)
+        wf.append({"K": K, "step_ms": dt * 1e3, "tokens_per_s": B * T / dt, "loss": float(tr.loss),
+                   "trunk_frac": trunk_f * B * T / dt / 1e12 / PEAK_BF16_TFLOPS, "tape_layers": tr.n_tape,
+                   "speedup_vs_layer_by_layer": next(e["step_ms"] for e in ladder if e["K"] == K) / (dt * 1e3)})
+        del tr
+        torch.cuda.empty_cache()
     del m
     torch.cuda.empty_cache()
     return {"workload": f"C4: {n_layers}-layer d={d} trunk ({h}x{d // h}, SwiGLU {Fh}, tied vocab 32000, "
@@ -387,7 +405,9 @@ def bench_c4_trunk(dev, n_layers=24, steps=2, warmup=1, reserve_gb=64.0):
                         "captured as one HIP graph; the DM cell timed per layer inside an eager step",
             "flops": "cell: 3 x fwd_flops_per_token per layer; trunk_frac adds the MLP (3 x 6 d ffn) and head "
                      "(3 x 2 d V) per token",
-            "steps": steps, "warmup": warmup, "ladder": ladder}
+            "steps": steps, "warmup": warmup, "ladder": ladder,
+            "wavefront": {"what": "the same step with the blocks layer-batched (dm_stack_fwd / dm_stack_bwd, "
+                                  "each block's MLP its tail; the same results bit for bit)", "ladder": wf}}
 
 
 def bench_c4_wavefront(dev, n_layers=8, steps=2, warmup=1):

@@ -89,16 +89,31 @@ class dm_decode_args(ctypes.Structure):
                 ("workspace_bytes", ctypes.c_size_t), ("pos_dev", c_vp)]
 
 
+class dm_mlp_packed(ctypes.Structure):
+    _fields_ = [(n, c_vp) for n in ("w13", "w2", "w13_t", "w2_t", "norm_w")]
+
+
+class dm_mlp_bufs(ctypes.Structure):
+    _fields_ = [(n, c_vp) for n in ("h", "ab", "mid", "dab", "dh")]
+
+
+class dm_mlp_grads(ctypes.Structure):
+    _fields_ = [(n, c_vp) for n in ("w1", "w3", "w2", "norm_w")]
+
+
 class dm_stack_layer(ctypes.Structure):
     _fields_ = [("w", c_vp), ("bufs", c_vp), ("x", c_vp), ("y", c_vp), ("K_cache", c_vp), ("V_cache", c_vp),
                 ("ocat", c_vp), ("tape", c_vp), ("tape_bytes", ctypes.c_size_t), ("workspace", c_vp),
-                ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace_bytes", ctypes.c_size_t), ("mlp_w", c_vp), ("mlp_bufs", c_vp), ("z", c_vp),
+                ("mlp_H", c_i32)]
 
 
 class dm_stack_bwd_layer(ctypes.Structure):
     _fields_ = [("w", c_vp), ("bufs", c_vp), ("x", c_vp), ("dy", c_vp), ("dx", c_vp), ("K_cache", c_vp),
                 ("V_cache", c_vp), ("ocat", c_vp), ("tape", c_vp), ("tape_bytes", ctypes.c_size_t), ("grads", c_vp),
-                ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t), ("mlp_w", c_vp), ("mlp_bufs", c_vp),
+                ("mlp_grads", c_vp), ("dz", c_vp), ("mlp_y", c_vp), ("mlp_H", c_i32), ("mlp_workspace", c_vp),
+                ("mlp_workspace_bytes", ctypes.c_size_t)]
 
 
 P = ctypes.POINTER
@@ -149,6 +164,12 @@ SIGNATURES = {
     "dm_stack_bwd": (ctypes.c_int, [P(dm_config), c_i32, P(dm_stack_bwd_layer), c_fp, c_fp, P(c_i32), c_i32, c_i32,
                                     c_vp, ctypes.c_size_t, c_i32, c_vp]),
     "dm_residual_rmsnorm": (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, ctypes.c_float, c_vp]),
+    "dm_pack_mlp": (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, P(dm_mlp_packed), c_vp]),
+    "dm_mlp_fwd": (ctypes.c_int, [c_i32, P(dm_mlp_packed), c_vp, c_vp, P(dm_mlp_bufs), c_i32, c_i32, c_i32,
+                                  ctypes.c_float, c_vp]),
+    "dm_mlp_workspace_bytes": (ctypes.c_size_t, [c_i32, c_i32, c_i32, c_i32]),
+    "dm_mlp_bwd": (ctypes.c_int, [c_i32, P(dm_mlp_packed), c_vp, c_vp, c_vp, P(dm_mlp_bufs), P(dm_mlp_grads), c_i32,
+                                  c_i32, c_i32, ctypes.c_float, c_vp, ctypes.c_size_t, c_vp]),
     "dm_swiglu_rows": (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp]),
     "dm_gemm": (ctypes.c_int, [c_i32, c_i32, c_i32, c_vp, c_vp, c_fp, c_i32, c_i32, c_i32, c_i32,
                                c_vp]),

@@ -8,6 +8,7 @@
 #include <utility>
 #include <vector>
 
+#include "dm_block.h"
 #include "dm_bwd.h"
 #include "dm_fwd_host.h"
 
@@ -201,6 +202,39 @@ void gemm_tn(const T* A, long lda, const T* Bm, long ldb, float* C, int M, int N
   } else {
     hipLaunchKernelGGL(k_sum_splits, dim3(cdiv(n, 256)), dim3(256), 0, s, S, n, (const float*)part, C, accumulate);
   }
+}
+
+// ---- the SwiGLU MLP sublayer's entry points and weight grads ----------------------------------
+struct MlpWs {
+  float* kpart;      // split-K partials of the two weight-grad products
+  float* stage;      // [2H, d] dw13 in w13's row order
+  float* dwa_part;   // [ceil(M / RMSN_ROWS), d] mlp_norm weight partials
+  float* colpart;    // [NCHUNK, d]
+  size_t bytes;
+};
+inline size_t mlp_kpart_elems(long d, long H) {
+  // gemm_tn's largest split (<= 16 slices, <= KSPLIT_ELEMS(N) elements) of dW2 [d, H] and dw13 [2H, d]
+  return (size_t)std::max(std::min(16 * d * H, KSPLIT_ELEMS(H)), std::min(16 * 2 * H * d, KSPLIT_ELEMS(d)));
+}
+inline MlpWs carve_mlp(int M, int d, int H, void* base) {
+  MlpWs w{};
+  Carver cv(base);
+  w.kpart = cv.take<float>(mlp_kpart_elems(d, H) * 4);
+  w.stage = cv.take<float>((size_t)2 * H * d * 4);
+  w.dwa_part = cv.take<float>((size_t)cdiv(M, RMSN_ROWS) * d * 4);
+  w.colpart = cv.take<float>((size_t)NCHUNK * d * 4);
+  w.bytes = cv.off;
+  return w;
+}
+// the weight grads over all M rows (after every row's VJP): dW2 += dz^T mid, dw13 = dab^T h unpacked
+// into W1 / W3, the mlp_norm weight from the per-8-row partials (in dwa_part)
+template <typename T>
+void mlp_wgrad(const dm_mlp_bufs* mb, const T* dz, int M, int d, int H, const dm_mlp_grads* g, const MlpWs& ws,
+               hipStream_t s) {
+  gemm_tn<T>(dz, d, (const T*)mb->mid, H, g->w2, d, H, M, 1, ws.kpart, s);
+  gemm_tn<T>((const T*)mb->dab, 2L * H, (const T*)mb->h, d, ws.stage, 2 * H, d, M, 0, ws.kpart, s);
+  hipLaunchKernelGGL(k_unpack_w13, dim3(2 * H), dim3(256), 0, s, (const float*)ws.stage, H, d, g->w1, g->w3);
+  colsum_add(ws.dwa_part, cdiv(M, RMSN_ROWS), d, ws.colpart, g->norm_w, s);
 }
 
 // The backward of one layer in three parts, as the reference's fused engine splits it
@@ -580,6 +614,10 @@ void record_bwd_chunk(const dm_config* c, const dm_stack_bwd_layer& ly, const fl
   const T* dy = (const T*)ly.dy;
   const T* Kc = (const T*)ly.K_cache;
   const T* Vc = (const T*)ly.V_cache;
+  // the block tail: the cell's rows of the MLP VJP, dz -> dy (the attention sublayer's output grad)
+  if (ly.mlp_w != nullptr)
+    mlp_bwd_rows<T>(ly.mlp_w, (const T*)ly.mlp_y, (const T*)ly.dz, (T*)ly.dy, ly.mlp_bufs, N, d, ly.mlp_H,
+                    c->rms_eps, lc, T_, pos0, 1, nullptr, nullptr);
   // do_cat rows of the cell: dy . W_O
   {
     EpiStoreTileF32 ep{N, d, ws.docat, 0, map};
@@ -681,6 +719,14 @@ void bwd_stack_close(const dm_config* c, const dm_stack_bwd_layer& ly, const flo
                      c->rms_eps, 0, (const T*)ly.x, (const T*)w->attn_norm_w, (const float*)ws.dxhat, (const T*)nullptr,
                      (T*)nullptr, dwa_part, RowMap{}, 2);
   colsum_add(dwa_part, cdiv(BT, RMSN_ROWS), d, ws.colpart, gr->attn_norm_w, s);
+  if (ly.mlp_w != nullptr) {
+    // the block tail's sums over all rows: the mlp_norm weight partials, then the weight grads
+    const MlpWs mw = carve_mlp(BT, d, ly.mlp_H, ly.mlp_workspace);
+    hipLaunchKernelGGL(k_rmsnorm_bwd<T>, dim3(cdiv(BT, RMSN_ROWS)), dim3(256), 4 * d * sizeof(float), s, BT, d,
+                       c->rms_eps, 0, (const T*)ly.mlp_y, (const T*)ly.mlp_w->norm_w,
+                       (const float*)ly.mlp_bufs->dh, (const T*)nullptr, (T*)nullptr, mw.dwa_part, RowMap{}, 2);
+    mlp_wgrad<T>(ly.mlp_bufs, (const T*)ly.dz, BT, d, ly.mlp_H, ly.mlp_grads, mw, s);
+  }
 }
 
 // which part of the layer backward an entry point runs
@@ -827,6 +873,16 @@ int run_stack_bwd(const dm_config* c, int nl, const dm_stack_bwd_layer* layers, 
     DM_REQUIRE(ly.bufs->T == layers[0].bufs->T, DM_ERR_INVALID, "layer %d: T differs", l);
     DM_REQUIRE((ly.tape != nullptr) == (layers[0].tape != nullptr), DM_ERR_INVALID,
                "layer %d: all layers with a tape or none", l);
+    if (ly.mlp_w != nullptr) {
+      if ((rc = check_mlp(c->dtype, ly.mlp_w, ly.mlp_bufs, c->B * ly.bufs->T, c->d, ly.mlp_H)) ||
+          (rc = check_mlp_bwd(ly.mlp_bufs, ly.mlp_grads)))
+        return rc;
+      DM_REQUIRE(ly.dz && ly.mlp_y && ly.dz != ly.dy, DM_ERR_INVALID, "layer %d: the block tail needs dz, mlp_y "
+                 "and a dy buffer of its own", l);
+      DM_REQUIRE(ly.mlp_workspace && aligned16(ly.mlp_workspace) &&
+                     ly.mlp_workspace_bytes >= carve_mlp(c->B * ly.bufs->T, c->d, ly.mlp_H, nullptr).bytes,
+                 DM_ERR_WORKSPACE, "layer %d: MLP workspace %zu bytes too small", l, ly.mlp_workspace_bytes);
+    }
   }
   for (int i = 0; i < n_cells; ++i)
     DM_REQUIRE(sched[3 * i + 1] == sched[1] && sched[3 * i + 2] == sched[2], DM_ERR_UNSUPPORTED,
@@ -986,6 +1042,9 @@ int dm_stack_bwd(const dm_config* c, int32_t n_layers, const dm_stack_bwd_layer*
     sig.val(*ly.w); sig.bufs(ly.bufs); sig.val(*ly.grads);
     sig.val(ly.x); sig.val(ly.dy); sig.val(ly.dx); sig.val(ly.K_cache); sig.val(ly.V_cache); sig.val(ly.ocat);
     sig.val(ly.tape); sig.val(ly.tape_bytes); sig.val(ly.workspace); sig.val(ly.workspace_bytes);
+    sig.val(ly.mlp_w); sig.val(ly.dz); sig.val(ly.mlp_y); sig.val(ly.mlp_H); sig.val(ly.mlp_workspace);
+    sig.val(ly.mlp_workspace_bytes);
+    if (ly.mlp_w != nullptr) { sig.val(*ly.mlp_w); sig.val(*ly.mlp_bufs); sig.val(*ly.mlp_grads); }
   }
   if (!build)
     DM_REQUIRE(plan_sig_matches(plan, sig.h), DM_ERR_INVALID,
@@ -1010,6 +1069,87 @@ int dm_layer_bwd_end(const dm_config* c, const dm_packed* w, const void* x, cons
   BwdCall call{BWD_END, x, dy, dx, nullptr, cos, sin, L, sched, n_cells, 0, K_cache, V_cache, cache_T, tape,
                tape_bytes, GradCache{}, g, workspace, kmax};
   return run_bwd(c, w, call, stream);
+}
+
+
+int dm_pack_mlp(int32_t dtype, const void* w1, const void* w3, const void* w2, const void* norm_w, int32_t d,
+                int32_t H, const dm_mlp_packed* out, void* stream) {
+  DM_REQUIRE(dtype == DM_F32 || dtype == DM_BF16, DM_ERR_INVALID, "dtype %d", dtype);
+  DM_REQUIRE(d > 0 && H > 0 && d % 128 == 0 && H % 128 == 0, DM_ERR_INVALID, "MLP d=%d H=%d (multiples of 128)", d, H);
+  DM_REQUIRE(w1 && w3 && w2 && norm_w && out, DM_ERR_INVALID, "null MLP weight");
+  DM_REQUIRE(out->w13 && out->w2 && out->w13_t && out->w2_t && out->norm_w, DM_ERR_INVALID, "null packed MLP output");
+  hipStream_t s = S(stream);
+  const int e = (int)esz(dtype);
+  // w13: W1 / W3 rows interleaved in groups of MLP_GROUP
+  std::vector<PackSeg> segs;
+  for (int g = 0; g < H / MLP_GROUP; ++g) {
+    segs.push_back(PackSeg{(const char*)w1 + (size_t)g * MLP_GROUP * d * e, d, 0, MLP_GROUP, 2 * MLP_GROUP * g, 0});
+    segs.push_back(PackSeg{(const char*)w3 + (size_t)g * MLP_GROUP * d * e, d, 0, MLP_GROUP,
+                           2 * MLP_GROUP * g + MLP_GROUP, 0});
+  }
+  for (size_t i0 = 0; i0 < segs.size(); i0 += PACK_MAX_SEG) {
+    PackArgs a{};
+    a.nseg = (int)std::min<size_t>(PACK_MAX_SEG, segs.size() - i0);
+    int rows = 0;
+    for (int i = 0; i < a.nseg; ++i) { a.seg[i] = segs[i0 + i]; rows += a.seg[i].nrows; }
+    a.ncols = d;
+    a.esz = e;
+    a.dst = out->w13;
+    hipLaunchKernelGGL(k_pack, dim3(rows), dim3(256), 0, s, a);
+  }
+  DM_HIP(hipMemcpyAsync(out->w2, w2, (size_t)d * H * e, hipMemcpyDeviceToDevice, s));
+  DM_HIP(hipMemcpyAsync(out->norm_w, norm_w, (size_t)d * e, hipMemcpyDeviceToDevice, s));
+  auto tr = [&](const void* src, void* dst, int rows, int cols) {
+    dim3 grid(cdiv(cols, 64), cdiv(rows, 64));
+    if (dtype == DM_BF16)
+      hipLaunchKernelGGL(k_transpose<bf16>, grid, dim3(256), 0, s, (const bf16*)src, (bf16*)dst, rows, cols);
+    else
+      hipLaunchKernelGGL(k_transpose<float>, grid, dim3(256), 0, s, (const float*)src, (float*)dst, rows, cols);
+  };
+  tr(out->w13, out->w13_t, 2 * H, d);
+  tr(w2, out->w2_t, d, H);
+  DM_HIP(hipGetLastError());
+  return DM_OK;
+}
+
+int dm_mlp_fwd(int32_t dtype, const dm_mlp_packed* w, const void* y, void* z, const dm_mlp_bufs* bufs, int32_t M,
+               int32_t d, int32_t H, float eps, void* stream) {
+  int rc = check_mlp(dtype, w, bufs, M, d, H);
+  if (rc) return rc;
+  DM_REQUIRE(y && z && y != z && aligned16(y) && aligned16(z), DM_ERR_INVALID, "y, z: distinct, 16-byte aligned");
+  hipStream_t s = S(stream);
+  if (dtype == DM_BF16) mlp_fwd_rows<bf16>(w, (const bf16*)y, (bf16*)z, bufs, M, d, H, eps, -1, 0, 0, s);
+  else mlp_fwd_rows<float>(w, (const float*)y, (float*)z, bufs, M, d, H, eps, -1, 0, 0, s);
+  DM_HIP(hipGetLastError());
+  return DM_OK;
+}
+
+size_t dm_mlp_workspace_bytes(int32_t dtype, int32_t M, int32_t d, int32_t H) {
+  if ((dtype != DM_F32 && dtype != DM_BF16) || M <= 0 || d <= 0 || H <= 0 || d % 128 || H % 128) return 0;
+  return carve_mlp(M, d, H, nullptr).bytes;
+}
+
+int dm_mlp_bwd(int32_t dtype, const dm_mlp_packed* w, const void* y, const void* dz, void* dy,
+               const dm_mlp_bufs* bufs, const dm_mlp_grads* g, int32_t M, int32_t d, int32_t H, float eps,
+               void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_mlp(dtype, w, bufs, M, d, H);
+  if (rc || (rc = check_mlp_bwd(bufs, g))) return rc;
+  DM_REQUIRE(y && dz && dy && dz != dy && aligned16(y) && aligned16(dz) && aligned16(dy), DM_ERR_INVALID,
+             "y, dz, dy: 16-byte aligned, dy not aliasing dz");
+  const MlpWs ws = carve_mlp(M, d, H, workspace);
+  DM_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= ws.bytes, DM_ERR_WORKSPACE,
+             "MLP workspace %zu < %zu bytes", workspace_bytes, ws.bytes);
+  hipStream_t s = S(stream);
+  if (dtype == DM_BF16) {
+    mlp_bwd_rows<bf16>(w, (const bf16*)y, (const bf16*)dz, (bf16*)dy, bufs, M, d, H, eps, -1, 0, 0, 3, ws.dwa_part, s);
+    mlp_wgrad<bf16>(bufs, (const bf16*)dz, M, d, H, g, ws, s);
+  } else {
+    mlp_bwd_rows<float>(w, (const float*)y, (const float*)dz, (float*)dy, bufs, M, d, H, eps, -1, 0, 0, 3,
+                        ws.dwa_part, s);
+    mlp_wgrad<float>(bufs, (const float*)dz, M, d, H, g, ws, s);
+  }
+  DM_HIP(hipGetLastError());
+  return DM_OK;
 }
 
 }  // extern "C"

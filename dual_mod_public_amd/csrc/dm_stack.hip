@@ -13,6 +13,7 @@
 #include <mutex>
 #include <vector>
 
+#include "dm_block.h"
 #include "dm_fwd_host.h"
 
 namespace dm {
@@ -67,6 +68,10 @@ void record_chunk(const dm_config* c, const dm_stack_layer& ly, const float* cos
     launch_gemm_auto<T, 64, 64, 2, 2, 3, 4>(ao, bo, M, d, d, ep, nullptr);
   else
     launch_gemm<T, 64, 64, 2, 2, 4>(ao, bo, M, d, d, ep, nullptr);
+  // the block tail (wave3d.py:26-28): the MLP sublayer of the chunk's rows, y -> z
+  if (ly.mlp_w != nullptr)
+    mlp_fwd_rows<T>(ly.mlp_w, (const T*)ly.y, (T*)ly.z, ly.mlp_bufs, M, d, ly.mlp_H, c->rms_eps, map.lc, L->T, pos0,
+                    nullptr);
 }
 
 // Records every step and lines the layers' launches up; fills `tab` (when non-null) with the
@@ -129,6 +134,11 @@ int check_stack(const dm_config* c, int nl, const dm_stack_layer* layers, const 
     DM_REQUIRE(ly.workspace && ly.workspace_bytes >= need_ws && aligned16(ly.workspace), DM_ERR_WORKSPACE,
                "layer %d: workspace %zu < %zu bytes", l, ly.workspace_bytes, need_ws);
     DM_REQUIRE((ly.tape != nullptr) == tape, DM_ERR_INVALID, "layer %d: all layers with a tape or none", l);
+    if (ly.mlp_w != nullptr) {
+      if ((rc = check_mlp(c->dtype, ly.mlp_w, ly.mlp_bufs, c->B * T, c->d, ly.mlp_H))) return rc;
+      DM_REQUIRE(ly.z && aligned16(ly.z) && ly.z != ly.y, DM_ERR_INVALID, "layer %d: the block tail needs its own "
+                 "16-byte aligned z", l);
+    }
     if (tape) {
       const size_t need = dm_layer_tape_bytes(c, sched, n_cells);
       DM_REQUIRE(ly.tape_bytes >= need && aligned16(ly.tape), DM_ERR_WORKSPACE, "layer %d: tape %zu < %zu bytes",
@@ -182,6 +192,8 @@ int dm_stack_fwd(const dm_config* c, int32_t n_layers, const dm_stack_layer* lay
     sig.val(*ly.w); sig.bufs(ly.bufs);
     sig.val(ly.x); sig.val(ly.y); sig.val(ly.K_cache); sig.val(ly.V_cache); sig.val(ly.ocat);
     sig.val(ly.tape); sig.val(ly.tape_bytes); sig.val(ly.workspace); sig.val(ly.workspace_bytes);
+    sig.val(ly.mlp_w); sig.val(ly.z); sig.val(ly.mlp_H);
+    if (ly.mlp_w != nullptr) { sig.val(*ly.mlp_w); sig.val(*ly.mlp_bufs); }
   }
   std::vector<GroupedLaunch> launches;
   if (!build) {

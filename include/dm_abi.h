@@ -206,6 +206,48 @@ int dm_layer_fwd(const dm_config* cfg, const dm_packed* w, const void* x, void* 
                  int32_t cache_T, void* ocat, void* tape, size_t tape_bytes, void* workspace,
                  size_t workspace_bytes, void* stream);
 
+/* ---- SwiGLU MLP sublayer of a Block ---------------------------------------------------
+ * z = y + W2 (silu(W1 h) * W3 h), h = mlp_norm(y) (models/dualmod/model.py:102-112, 127-128;
+ * RMSNorm attention.py:74-83), over M rows [M, d] of the storage dtype, and its VJP. The
+ * trunk's MLP in the reference engine's chunk body (engines/wavescan/engine/graphs.py:254-256,
+ * the layer_blockmlp_bwd VJP fused_sweep.py:1854-1869); here on the library's own GEMM tiles,
+ * so that the layer-by-layer trunk and the layer-batched stack (dm_stack_fwd / dm_stack_bwd
+ * with a block tail) compute the same bits. Numerics as the reference's bf16 autocast: every
+ * product with fp32 accumulation rounded to the storage dtype, silu(a) * b from the rounded
+ * products, RMS statistics in fp32. H (the hidden width) a multiple of 32, d of 64.
+ * dm_pack_mlp writes the packed weights from the reference's w1 / w3 [H, d], w2 [d, H] and
+ * mlp_norm.weight [d] (storage dtype). */
+typedef struct dm_mlp_packed {
+  void* w13;      /* [2H, d] W1 / W3 rows interleaved in groups of 32 (W1 rows 32g.., then W3 rows 32g..) */
+  void* w2;       /* [d, H] */
+  void* w13_t;    /* [d, 2H] w13 transposed */
+  void* w2_t;     /* [H, d] W2 transposed */
+  void* norm_w;   /* [d] mlp_norm.weight */
+} dm_mlp_packed;
+/* The forward's saved state and the backward's intermediates, rows laid out as y's. */
+typedef struct dm_mlp_bufs {
+  void* h;        /* [rows, d]  mlp_norm(y) */
+  void* ab;       /* [rows, 2H] W1 h | W3 h in w13's row order */
+  void* mid;      /* [rows, H]  silu(W1 h) * W3 h */
+  void* dab;      /* [rows, 2H] backward: the grads of ab */
+  float* dh;      /* [rows, d]  backward: the grad of h */
+} dm_mlp_bufs;
+typedef struct dm_mlp_grads {
+  float* w1; float* w3;   /* [H, d] */
+  float* w2;              /* [d, H] */
+  float* norm_w;          /* [d] */
+} dm_mlp_grads;
+int dm_pack_mlp(int32_t dtype, const void* w1, const void* w3, const void* w2, const void* norm_w, int32_t d,
+                int32_t H, const dm_mlp_packed* out, void* stream);
+int dm_mlp_fwd(int32_t dtype, const dm_mlp_packed* w, const void* y, void* z, const dm_mlp_bufs* bufs, int32_t M,
+               int32_t d, int32_t H, float eps, void* stream);
+/* dy = dz + the MLP branch's VJP (dy may not alias dz); the weight gradients are ADDED into g.
+ * workspace: dm_mlp_workspace_bytes(dtype, M, d, H). */
+size_t dm_mlp_workspace_bytes(int32_t dtype, int32_t M, int32_t d, int32_t H);
+int dm_mlp_bwd(int32_t dtype, const dm_mlp_packed* w, const void* y, const void* dz, void* dy,
+               const dm_mlp_bufs* bufs, const dm_mlp_grads* g, int32_t M, int32_t d, int32_t H, float eps,
+               void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- layer-batched (wavefront) forward of a stack of layers --------------------------
  * engines/wave3d/wave3d.py:1-47 (layer l at global step t works on step t - l, every active
  * layer's work batched into the same launches), applied to the chunk schedule above: layer l
@@ -229,11 +271,19 @@ int dm_layer_fwd(const dm_config* cfg, const dm_packed* w, const void* x, void* 
 typedef struct dm_stack_layer {
   const dm_packed* w;
   const dm_layer_bufs* bufs;
-  const void* x; void* y;              /* [B, T, d] layer input / output */
+  const void* x; void* y;              /* [B, T, d] layer input / attention sublayer output */
   void* K_cache; void* V_cache;        /* [B, h, cache_T, dh] */
   void* ocat;                          /* [B, T, d] */
   void* tape; size_t tape_bytes;       /* NULL: no tape */
   void* workspace; size_t workspace_bytes;
+  /* the block tail (engines/wave3d/wave3d.py:26-28: x + wo(o) + mlp(mlp_norm(.)) per step):
+   * NULL mlp_w: the layer is the attention sublayer alone, its output y; else each cell's rows
+   * also run the MLP sublayer (as dm_mlp_fwd) from y into z, the block output [B, T, d] (then
+   * layers[l + 1].x is normally layers[l].z), with the state the backward reads in mlp_bufs */
+  const dm_mlp_packed* mlp_w;
+  const dm_mlp_bufs* mlp_bufs;
+  void* z;
+  int32_t mlp_H;
 } dm_stack_layer;
 size_t dm_stack_fwd_plan_bytes(const dm_config* cfg, int32_t n_layers, const dm_stack_layer* layers,
                                const int32_t* sched, int32_t n_cells, int32_t cache_T);
@@ -292,6 +342,16 @@ typedef struct dm_stack_bwd_layer {
   const void* tape; size_t tape_bytes;
   const dm_grads* grads;
   void* workspace; size_t workspace_bytes;
+  /* the block tail (as dm_stack_layer): with mlp_w, dz [B, T, d] is the grad of the block output
+   * z, each cell's rows first run the MLP VJP (as dm_mlp_bwd) from dz into dy (then written, the
+   * grad of the attention sublayer's output y = mlp_y), and the layer's close adds the MLP
+   * weight grads into mlp_grads; mlp_workspace: dm_mlp_workspace_bytes(dtype, B T, d, mlp_H) */
+  const dm_mlp_packed* mlp_w;
+  const dm_mlp_bufs* mlp_bufs;
+  const dm_mlp_grads* mlp_grads;
+  const void* dz; const void* mlp_y;
+  int32_t mlp_H;
+  void* mlp_workspace; size_t mlp_workspace_bytes;
 } dm_stack_bwd_layer;
 size_t dm_stack_bwd_plan_bytes(const dm_config* cfg, int32_t n_layers, const dm_stack_bwd_layer* layers,
                                const int32_t* sched, int32_t n_cells, int32_t cache_T);

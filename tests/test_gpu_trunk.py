@@ -11,7 +11,11 @@ fp32 gradient buffer.
 * T-K8 (engines/wavescan/tests/test_k1_k9.py:346-373): two runs of 8 SGD steps from the same
   weights give the same bits (every kernel of the step, the library GEMMs included, is
   deterministic);
-* forward tapes and exact recompute give the same bits.
+* forward tapes and exact recompute give the same bits;
+* the layer-batched trunk (dm_stack_fwd / dm_stack_bwd with the MLP as each block's tail,
+  engines/wave3d/wave3d.py:26-28) equals the layer-by-layer trunk bit for bit;
+* the MLP sublayer alone (dm_mlp_fwd / dm_mlp_bwd): output and every gradient against autograd
+  through the oracle's fp64 SwiGLU and RMSNorm (models/dualmod/model.py:102-131).
 """
 
 import pytest
@@ -26,6 +30,7 @@ from dual_mod_public_amd.model import DualModLM
 from dual_mod_public_amd.synthetic import make_lm_state_dict
 from dual_mod_public_amd.trunk import HipTrunk
 from tests.hip_helpers import DEV, record, relerr, say
+from dual_mod_public_amd.trunk import MlpBufs, MlpWeights
 
 pytestmark = pytest.mark.gpu
 
@@ -208,3 +213,86 @@ def test_trunk_tk8_bitwise_determinism():
     assert all(torch.equal(x, y) for x, y in zip(runs[0][1], runs[1][1]))
     say(f"  losses {['%.4f' % v for v in runs[0][0]]}")
     assert runs[0][0][-1] < runs[0][0][0]   # the steps descend on the repeated batch
+
+
+@pytest.mark.parametrize("dtype,tape", [(torch.float32, True), (torch.bfloat16, True), (torch.bfloat16, False)])
+def test_trunk_wavefront_equals_layer_by_layer(dtype, tape):
+    """The blocks layer-batched, each block's MLP its tail, against the layer-by-layer step: loss,
+    every gradient, the trunk's output and dx, bit for bit (3 layers, 4 cells)."""
+    say(f"trunk wavefront vs layer by layer, {dtype}, tape={tape}")
+    cfg = _cfg(n_layers=3)
+    B, T = 2, 64
+    m, _ = _model(cfg, dtype)
+    sched = uniform_chunks(T, 16, 4)
+    budget = None if tape else 0
+    a = HipTrunk(m, B, T, schedule=sched, tape_budget=budget)
+    b = HipTrunk(m, B, T, schedule=sched, tape_budget=budget, wavefront=True)
+    assert b.n_tape == (cfg.n_layers if tape else 0)
+    for seed in (21, 22):
+        idx, tg = (t.to(DEV) for t in _batch(cfg, B, T, seed=seed))
+        a.train_step(idx, tg)
+        b.train_step(idx, tg)
+        torch.cuda.synchronize()
+        assert _same(_snapshot(a), _snapshot(b)), seed
+    b.capture()   # the captured layer-batched step replays the same bits
+    idx, tg = (t.to(DEV) for t in _batch(cfg, B, T, seed=23))
+    a.train_step(idx, tg)
+    b.train_step(idx, tg)
+    torch.cuda.synchronize()
+    assert _same(_snapshot(a), _snapshot(b))
+
+
+@pytest.mark.parametrize("dtype,tol,M", [(torch.float32, 1e-5, 128), (torch.float32, 1e-5, 100),
+                                         (torch.bfloat16, 2e-2, 300)])
+def test_mlp_sublayer_matches_oracle(dtype, tol, M):
+    """dm_mlp_fwd / dm_mlp_bwd on M rows (also a count that is no multiple of the tiles) against
+    autograd through the oracle's fp64 z = y + swiglu(rms_norm(y))."""
+    say(f"MLP sublayer {dtype} M={M}")
+    d, H = 256, 384
+    g = torch.Generator().manual_seed(31)
+    y = torch.randn(M, d, generator=g, dtype=torch.float64)
+    dz = torch.randn(M, d, generator=g, dtype=torch.float64)
+    sd = {"mlp.w1.weight": 0.05 * torch.randn(H, d, generator=g, dtype=torch.float64),
+          "mlp.w3.weight": 0.05 * torch.randn(H, d, generator=g, dtype=torch.float64),
+          "mlp.w2.weight": 0.05 * torch.randn(d, H, generator=g, dtype=torch.float64),
+          "mlp_norm.weight": 1.0 + 0.1 * torch.randn(d, generator=g, dtype=torch.float64)}
+
+    class _Blk:   # the module attributes MlpWeights.pack reads
+        pass
+    blk = _Blk()
+    blk.mlp = _Blk()
+    for n in ("w1", "w3", "w2"):
+        setattr(blk.mlp, n, _Blk())
+        getattr(blk.mlp, n).weight = sd[f"mlp.{n}.weight"].to(DEV, dtype)
+    blk.mlp_norm = _Blk()
+    blk.mlp_norm.weight = sd["mlp_norm.weight"].to(DEV, dtype)
+    mw = MlpWeights(d, H, DEV, dtype)
+    mw.pack(blk)
+    mb = MlpBufs(1, M, d, H, DEV, dtype)
+    yd, dzd = y.to(DEV, dtype).contiguous(), dz.to(DEV, dtype).contiguous()
+    z = torch.empty_like(yd)
+    dy = torch.empty_like(yd)
+    grads = {k: torch.zeros(v.shape, device=DEV, dtype=torch.float32) for k, v in sd.items()}
+    gs = L.dm_mlp_grads()
+    gs.w1, gs.w3, gs.w2 = (L.ptr(grads[f"mlp.{n}.weight"]) for n in ("w1", "w3", "w2"))
+    gs.norm_w = L.ptr(grads["mlp_norm.weight"])
+    code = L.dtype_code(dtype)
+    import ctypes
+    L.check(L.lib().dm_mlp_fwd(code, ctypes.byref(mw.s), L.ptr(yd), L.ptr(z), ctypes.byref(mb.s), M, d, H, 1e-5,
+                               L.stream_ptr()))
+    nb = L.lib().dm_mlp_workspace_bytes(code, M, d, H)
+    ws = torch.empty(nb, device=DEV, dtype=torch.uint8)
+    L.check(L.lib().dm_mlp_bwd(code, ctypes.byref(mw.s), L.ptr(yd), L.ptr(dzd), L.ptr(dy), ctypes.byref(mb.s),
+                               ctypes.byref(gs), M, d, H, 1e-5, L.ptr(ws), nb, L.stream_ptr()))
+    torch.cuda.synchronize()
+    leaves = {k: v.clone().requires_grad_(True) for k, v in sd.items()}
+    yl = y.clone().requires_grad_(True)
+    z_ref = yl + O.swiglu(leaves, O.rms_norm(yl, leaves["mlp_norm.weight"], 1e-5))
+    (z_ref * dz).sum().backward()
+    errs = {"z": relerr(z, z_ref.detach()), "dy": relerr(dy, yl.grad)}
+    for k, v in leaves.items():
+        errs[k] = relerr(grads[k], v.grad)
+    say("  " + " ".join(f"{k}={v:.1e}" for k, v in errs.items()))
+    record(f"mlp sublayer {dtype} M={M}", errs, tol)
+    for k, v in errs.items():
+        assert v < tol, f"{k}: relerr {v:.3e}"
