@@ -156,23 +156,24 @@ def test_layer_grads_dh128_fp32(ctx_mod, tape):
     compare("fp32 dh128", dx, g, dx_ref, g_ref, FP32_GRAD_TOL)
 
 
-def test_layer_grads_config4_shape_bf16():
-    """BASELINE config 4's layer shape (d=2048, 16 x 128), c=64, K=4, T=256, bf16 storage,
+@pytest.mark.parametrize("k", [1, 4, 8])
+def test_layer_grads_config4_shape_bf16(k):
+    """Config 4's layer shape (d=2048, 16 x 128), c=64, K=1 / 4 / 8, T=256, bf16 storage,
     forward tape: gradients and the forward against autograd through the oracle's
     chunked-Jacobi layer at the same K, run in fp32 torch on the GPU."""
-    say("bwd bf16 d=2048 16x128 T=256 c=64 K=4 vs fp32 oracle on the GPU")
+    say(f"bwd bf16 d=2048 16x128 T=256 c=64 K={k} vs fp32 oracle on the GPU")
     torch.backends.cuda.matmul.allow_tf32 = False
     cfg = cfg_of(d=2048, h=16, T=256)
     B, T = 2, 256
     sd, x, _, (c32, s32) = setup(cfg, B, T)
     dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(41), dtype=torch.float32)
-    sched = uniform_chunks(T, 64, 4)
+    sched = uniform_chunks(T, 64, k)
     _, dx, g, (K, V, ocat) = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.bfloat16, tape=True, full=True)
     dx_ref, g_ref, (o_ref, K_ref, V_ref) = oracle_grads(
         cfg, {k: v.float() for k, v in sd.items()}, x.float(), dy, c32, s32, sched, dtype=torch.float32,
         device=DEV, with_forward=True)
     fwd = {"o_cat": relerr(ocat, o_ref), "K": relerr(K, K_ref), "V": relerr(V, V_ref)}
     say("  forward relerr " + " ".join(f"{k}={v:.2e}" for k, v in fwd.items()))
-    record("bf16 C4 shape T=256 forward", fwd, BF16_TOL)
+    record(f"bf16 C4 shape T=256 K={k} forward", fwd, BF16_TOL)
     assert max(fwd.values()) < BF16_TOL, fwd
-    compare("bf16 C4 shape T=256", dx, g, dx_ref, g_ref, BF16_GRAD_TOL)
+    compare(f"bf16 C4 shape T=256 K={k}", dx, g, dx_ref, g_ref, BF16_GRAD_TOL)
