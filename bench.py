@@ -1,7 +1,7 @@
 """Benchmark of the Dual-Mod attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload fwdbwd|fwd|c4]
-                    [--no-cpu-baseline] [--no-decode] [--no-c4] [--c4-stack-layers L] [--no-stack]
+                    [--no-cpu-baseline] [--no-decode] [--no-c1] [--no-c4] [--c4-stack-layers L] [--no-stack]
                     [--stack-layers L]
                     [--no-graph-decode]
 
@@ -20,14 +20,17 @@ timing starts.
 
 Prints ONE JSON line: the headline sweep throughput in tokens/s, the roofline of
 the dominant kernel (sweep GEMM 1) timed with HIP events stamped by its own launches inside a
-second pass of the timed steps, the path-level roofline, the config-4 K ladder (one
-layer of the d=2048 trunk, fwd+bwd for K in {1, 2, 4, 8}; and 8 such layers layer-batched), a stack of the same layer at the 340M
-model's depth (24 layers, --stack-layers) fwd+bwd layer by layer and layer-batched (wavefront),
-the 24-layer model's greedy decode
+second pass of the timed steps, the path-level roofline, config 4 (one layer of the d=2048
+trunk, fwd+bwd for K in {1, 2, 4, 8}; the whole 24-layer trunk training step with SwiGLU MLPs and
+the tied 32000-token head, layer by layer and layer-batched, its per-layer cell timed inside it;
+8 attention layers layer-batched), a stack of the 340M layer at the model's depth (24 layers,
+--stack-layers) fwd+bwd layer by layer and layer-batched (wavefront), the 24-layer model's greedy
+decode
 through the one-graph-per-token decoder against the eager one, the decode sub-benchmark
-(batch 64, bf16 tape of 32768 positions, HBM GB/s) and the CPU
-baselines (the oracle on this host's cores over bounded samples, warm-up then the
-median of 3).
+(batch 64, bf16 tape of 32768 positions, HBM GB/s)
+whole (B=2, T=64, d=256, fp32, c=16, K=16) and the CPU baselines (the oracle on this host's
+cores, warm-up then the median of 3: C1 whole by the sequential scan, the C2 forward and the C3
+forward + backward over the whole workload, C5 over 8 of the 64 batch rows).
 """
 
 import argparse
@@ -219,6 +222,52 @@ def cpu_decode_baseline(cfg, sd, rows=8, steps=3):
                 sample=f"static-tape decode steps of {rows} of the 64 batch rows at P = {P0}.., fp32 torch "
                        "CPU oracle, median of 3 after a warm-up: " + ", ".join(f"{t * 1e3:.0f}" for t in ts) + " ms",
                 **host_info())
+
+
+def bench_c1(dev, steps=50, warmup=5, with_cpu=True):
+    """BASELINE config 1, whole: one DM layer at B=2, T=64, d=256, 4 x 64, fp32, c=16, K=16 (exact).
+    The HIP layer forward (dm_layer_fwd, one call) timed over `steps` calls, and beside it the
+    reference's CPU path for the same case, the oracle's sequential scan (scan.py:19-95 restated,
+    fp32 torch) on this host's cores over the whole workload: one warm-up, then the median of 3."""
+    B, T, d, h, c, K = 2, 64, 256, 4, 16, 16
+    cfg = DualModConfig(d_model=d, n_heads=h, ctx_mod="mult_res", max_seq_len=T, dtype="fp32")
+    sd = make_state_dict(cfg, seed=C2["wseed"])
+    cell = HipSweepCell(cfg, B, T, device=dev, dtype=torch.float32)
+    cell.pack({k: v.to(dev) for k, v in sd.items()})
+    x = make_input((B, T, d), seed=C2["xseed"]).to(dev, torch.float32)
+    cos, sin = build_rope_cache(T, cfg.head_dim, cfg.rope_theta, device=dev)
+    cos, sin = cos.contiguous(), sin.contiguous()
+    bufs = cell.new_bufs(T)
+    Kc = torch.zeros(B, h, T, cfg.head_dim, device=dev, dtype=torch.float32)
+    Vc, ocat, y = torch.zeros_like(Kc), torch.empty_like(x), torch.empty_like(x)
+    sched = uniform_chunks(T, c, K)
+
+    def step():
+        cell.layer_forward(x, y, cos, sin, sched, Kc, Vc, ocat, bufs)
+    for _ in range(warmup):
+        step()
+    dt = timed(step, steps)
+    out = {"workload": f"C1: one DM layer forward, B={B} T={T} d={d} {h}x{d // h}, fp32, c={c} K={K} (exact)",
+           "ms_per_step": dt * 1e3, "tokens_per_s": B * T / dt, "steps": steps}
+    if with_cpu:
+        import oracle as O
+        nthr = cpu_threads()
+        torch.set_num_threads(nthr)
+        xc = make_input((B, T, d), seed=C2["xseed"])
+        c32, s32 = O.build_rope_cache(T, cfg.head_dim, cfg.rope_theta)
+        sdf = {k: v.float() for k, v in sd.items()}
+
+        def run():
+            with torch.no_grad():
+                O.dm_layer(cfg, sdf, xc, c32, s32, schedule=None)
+        med, ts = median_wall(run)
+        out["cpu_baseline"] = dict(
+            value=B * T / med, unit="tokens/s", cores=nthr, kind="port",
+            sample=f"the whole C1 workload (B={B}, T={T}): the sequential scan (scan.py), fp32 torch CPU oracle, "
+                   "median of 3 after a warm-up: " + ", ".join(f"{t * 1e3:.1f}" for t in ts) + " ms",
+            **host_info())
+    del cell, bufs, Kc, Vc, ocat, y, x
+    return out
 
 
 def bench_decode(dev, steps_override=None, with_cpu=True):
@@ -518,6 +567,7 @@ def main():
     ap.add_argument("--cpu-T", type=int, default=0,
                     help="T-prefix of the CPU baseline sample (0: the whole T)")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-c1", action="store_true", help="skip BASELINE config 1 (the CPU-runnable layer)")
     ap.add_argument("--no-c4", action="store_true", help="skip the config-4 K ladder")
     ap.add_argument("--no-stack", action="store_true", help="skip the layer-stack (layer-batched) sub-benchmark")
     ap.add_argument("--c4-trunk-layers", type=int, default=24,
@@ -678,8 +728,13 @@ def main():
         out["graph_decode"] = bench_graph_decode(dev)
     if not args.no_decode:
         out["decode"] = bench_decode(dev, args.decode_steps or None, with_cpu=not args.no_cpu_baseline)
+    if not args.no_c1 and args.workload != "c4":
+        out["c1"] = bench_c1(dev, with_cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline and args.workload != "c4":
         out["cpu_baseline"] = cpu_baseline(cfg, sd, T, B, fwdbwd, args.cpu_T)
+        if fwdbwd and "forward_only" in out:
+            # BASELINE config 2 (the forward of the same layer) on the same cores
+            out["forward_only"]["cpu_baseline"] = cpu_baseline(cfg, sd, T, B, False, args.cpu_T)
     print(json.dumps(out), flush=True)
 
 
