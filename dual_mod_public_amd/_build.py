@@ -16,7 +16,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libdm_hip.so")
 SOURCES = ["dm_lib.hip", "dm_bwd.hip", "dm_stack.hip"]
-HEADERS = ["dm_common.h", "dm_group.h", "dm_gemm.h", "dm_attn.h", "dm_kernels.h", "dm_decode.h", "dm_bwd.h", "dm_host.h",
+HEADERS = ["dm_common.h", "dm_group.h", "dm_gemm.h", "dm_attn.h", "dm_kernels.h", "dm_decode.h", "dm_bwd.h", "dm_block.h", "dm_host.h",
            "dm_fwd_host.h", "dm_mlp.h", "dm_prof.h", "../../include/dm_abi.h"]
 
 
@@ -27,7 +27,11 @@ def hipcc():
     return "hipcc"
 
 
-FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
+# -ffp-contract=on: a multiply and an add are fused only inside one expression, so an epilogue
+# or body inlined into different kernels (one layer's launch, the layer-batched grouped launch)
+# rounds the same way in each (with "fast", fusion across statements follows each kernel's
+# instruction selection).
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=on",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 

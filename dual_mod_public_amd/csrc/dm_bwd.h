@@ -394,7 +394,7 @@ static __global__ __launch_bounds__(256) void k_refine_bwd(RefineBwdArgs<T> a) {
 //   dsig += dv_in tanh(vm); dctx[:, 2d + j] = dv_in sig (1 - tanh^2); lamdv = lam dv_in
 //   (fusion, v_in = u + silu(z), z = px + vm: dsig and dctx[:, 2d + j] += dv_in silu'(z), lamdv = dv_in)
 // ---------------------------------------------------------------------------
-template <typename T> struct EpiVinBwd {
+template <typename T, int BN = 32> struct EpiVinBwd {
   CellGeom g;
   int M, ctx_mod;
   float lam;
@@ -403,69 +403,83 @@ template <typename T> struct EpiVinBwd {
   T* __restrict__ dctx;              // [N, 4d]
   float* __restrict__ dsig;          // layer accumulator [B, Tbuf, d]
   float* __restrict__ lamdv;         // [N, d]
-  // Block tile 64 x 32: thread t owns row t / 4, columns 8 (t % 4) .. + 7; its
-  // inputs (and the dsig values it will add to) are gathered before the k-loop.
+  // Block tile 64 x BN: thread t owns row t / 4 and, in each 32-column group q, columns
+  // 32 q + 8 (t % 4) .. + 7; its inputs (and the dsig values it will add to) are gathered
+  // before the k-loop.
+  static constexpr int NQ = BN / 32;
   struct TilePre {
-    Raw8<T> sg;
-    floatx4 ds[2];
-    Raw8<T> vm;
+    Raw8<T> sg[NQ];
+    floatx4 ds[NQ][2];
+    Raw8<T> vm[NQ];
   };
   // vector-memory load instructions tile_prefetch issues (Raw8 = one 16-byte load in bf16, two in
   // fp32: 16-byte loads, which the compiler cannot merge into fewer)
-  static constexpr int LATE_GATHERS = 2 + 2 * (int)(sizeof(T) / 2);
+  static constexpr int LATE_GATHERS = NQ * (2 + 2 * (int)(sizeof(T) / 2));
   DM_DEV TilePre tile_prefetch(int m0, int n0) const {
-    const int r = threadIdx.x >> 2, col = n0 + 8 * (threadIdx.x & 3);
+    const int r = threadIdx.x >> 2, c0 = n0 + 8 * (threadIdx.x & 3);
     const int d = g.d;
     const int m = min(m0 + r, M - 1);
     const int b = m / g.c;
     const long xrow = (long)b * g.Tbuf + g.buf_t0 + m - b * g.c;
     TilePre pr;
-    pr.sg = ld8_global(sig + xrow * d + col);
 #pragma unroll
-    for (int k = 0; k < 2; ++k) pr.ds[k] = ld_global<floatx4>(dsig + xrow * d + col + 4 * k);
-    pr.vm = ld8_global(save1 + (long)m * 4 * d + 2 * d + col);
+    for (int q = 0; q < NQ; ++q) {
+      const int col = c0 + 32 * q;
+      pr.sg[q] = ld8_global(sig + xrow * d + col);
+#pragma unroll
+      for (int k = 0; k < 2; ++k) pr.ds[q][k] = ld_global<floatx4>(dsig + xrow * d + col + 4 * k);
+      pr.vm[q] = ld8_global(save1 + (long)m * 4 * d + 2 * d + col);
+    }
     return pr;
   }
-  template <int BM, int BN, int LDT>
+  template <int BM, int BN_, int LDT>
   DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre& pr, int) const {
-    static_assert(BM == 64 && BN == 32, "dv_in GEMM block tile is 64 x 32");
-    const int r = threadIdx.x >> 2, c0 = 8 * (threadIdx.x & 3), col = n0 + c0;
-    const int d = g.d;
+    static_assert(BM == 64 && BN_ == BN, "dv_in GEMM block tile is 64 x BN");
+    const int r = threadIdx.x >> 2, d = g.d;
     const int m = m0 + r;
-    float dv[8], sg[8], ds[8], vm[8];
+    float dv[NQ][8], sg[NQ][8], ds[NQ][8], vm[NQ][8];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      unpackf4(*reinterpret_cast<const floatx4*>(tile + r * LDT + c0 + 4 * k), dv + 4 * k);
-      unpackf4(pr.ds[k], ds + 4 * k);
+    for (int q = 0; q < NQ; ++q) {
+      const int c0 = 32 * q + 8 * (threadIdx.x & 3);
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        unpackf4(*reinterpret_cast<const floatx4*>(tile + r * LDT + c0 + 4 * k), dv[q] + 4 * k);
+        unpackf4(pr.ds[q][k], ds[q] + 4 * k);
+      }
+      unpack8<T>(pr.sg[q], sg[q]);
+      unpack8<T>(pr.vm[q], vm[q]);
     }
-    unpack8<T>(pr.sg, sg);
-    unpack8<T>(pr.vm, vm);
     if (m >= M) return;
-    settle(sg); settle(ds); settle(vm);   // all loads before any store
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) { settle(sg[q]); settle(ds[q]); settle(vm[q]); }   // all loads before any store
     const int b = m / g.c;
     const long xrow = (long)b * g.Tbuf + g.buf_t0 + m - b * g.c;
-    float dso[8], dc[8], lv[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (ctx_mod == 3) {   // fusion: v_in = u + silu(z), z = px + vm; silu' = s (1 + z (1 - s))
-        const float z = sg[i] + vm[i], s = sigmoidf_(z);
-        const float dz = dv[i] * s * (1.f + z * (1.f - s));
-        dso[i] = ds[i] + dz;
-        dc[i] = dz;
-        lv[i] = dv[i];
-      } else {
-        const float th = tanhf_(vm[i]);
-        dso[i] = ds[i] + dv[i] * th;
-        dc[i] = dv[i] * sg[i] * (1.f - th * th);
-        lv[i] = ctx_mod == 1 ? lam * dv[i] : 0.f;
+    for (int q = 0; q < NQ; ++q) {
+      const int col = n0 + 32 * q + 8 * (threadIdx.x & 3);
+      float dso[8], dc[8], lv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (ctx_mod == 3) {   // fusion: v_in = u + silu(z), z = px + vm; silu' = s (1 + z (1 - s))
+          const float z = sg[q][i] + vm[q][i], s = sigmoidf_(z);
+          const float dz = dv[q][i] * s * (1.f + z * (1.f - s));
+          dso[i] = ds[q][i] + dz;
+          dc[i] = dz;
+          lv[i] = dv[q][i];
+        } else {
+          const float th = tanhf_(vm[q][i]);
+          dso[i] = ds[q][i] + dv[q][i] * th;
+          dc[i] = dv[q][i] * sg[q][i] * (1.f - th * th);
+          lv[i] = ctx_mod == 1 ? lam * dv[q][i] : 0.f;
+        }
       }
-    }
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      *reinterpret_cast<floatx4*>(dsig + xrow * d + col + 4 * k) = floatx4{dso[4 * k], dso[4 * k + 1], dso[4 * k + 2], dso[4 * k + 3]};
-      *reinterpret_cast<floatx4*>(lamdv + (long)m * d + col + 4 * k) = floatx4{lv[4 * k], lv[4 * k + 1], lv[4 * k + 2], lv[4 * k + 3]};
+      for (int k = 0; k < 2; ++k) {
+        *reinterpret_cast<floatx4*>(dsig + xrow * d + col + 4 * k) = floatx4{dso[4 * k], dso[4 * k + 1], dso[4 * k + 2], dso[4 * k + 3]};
+        *reinterpret_cast<floatx4*>(lamdv + (long)m * d + col + 4 * k) = floatx4{lv[4 * k], lv[4 * k + 1], lv[4 * k + 2], lv[4 * k + 3]};
+      }
+      store_vec<T, 8>(dctx + (long)m * 4 * d + 2 * d + col, dc);
     }
-    store_vec<T, 8>(dctx + (long)m * 4 * d + 2 * d + col, dc);
   }
 };
 
@@ -523,6 +537,94 @@ DM_DEV void du_epi_body(int M, int d, int h, float inv_d, float eps,
   __syncthreads();
   if (wave == 0) dnw[(long)blockIdx.x * d + col] = dn_old + (cs[0][lane] + cs[1][lane] + cs[2][lane] + cs[3][lane]);
 }
+
+// The RMS-VJP inputs of du_epi_body as the tile epilogue of the GEMM of slice ZS (its accumulators
+// stand for that slice; the other slices come from part), so the last du launch computes them and
+// no separate pass over the slices is needed: du = slices summed in order z = 0..S-1, + lam dv_in;
+// gw = du * w; rowdot[m, chunk] = the row's sum of gw * o over a 64-column chunk; dnw[slot][col] +=
+// the sum over the slot's 16 rows, in row order, of du * o * r. Each thread takes 8 consecutive
+// columns of a row and the 8 threads of a 64-column chunk are 8 consecutive lanes: the row's sums
+// (of its head sums of squares, of gw * o) are a fixed xor-tree over those lanes, so every block
+// width gives the same bits.
+template <typename T, int S, int ZS> struct EpiDuFinal {
+  static constexpr int TILE_ROWS = 32;
+  int M, d, h;
+  float inv_d, eps;
+  const float* __restrict__ part;    // [S, M, d] split-K slices (slice ZS, this GEMM's, not read)
+  const float* __restrict__ lamdv;   // [M, d] or null
+  const T* __restrict__ o;           // [M, d]
+  const float* __restrict__ ssq;     // [M, h]
+  const T* __restrict__ normw;       // [d]
+  float* __restrict__ gw;
+  float* __restrict__ rowdot;
+  float* __restrict__ dnw;
+  struct TilePre {};
+  DM_DEV TilePre tile_prefetch(int, int) const { return TilePre{}; }
+  template <int TR, int BN, int LDT>
+  DM_DEV void tile_apply(const float* tile_in, int m0, int n0, const float*, const TilePre&, int) const {
+    constexpr int CPT = 8, LPC = DU_EPI_TN / CPT;   // columns per thread, lanes per 64-column chunk
+    constexpr int P = BN / CPT, RPP = 256 / P;       // threads per row, rows per pass
+    static_assert(BN % DU_EPI_TN == 0 && 256 % P == 0 && TR % RPP == 0 && TR % 16 == 0, "tile shape");
+    static_assert(MAX_HEADS % LPC == 0, "head sums split over a chunk's lanes");
+    float* tile = const_cast<float*>(tile_in);  // the block's own LDS chunk: reused for du o r
+    const int t = threadIdx.x, pt = t % P;
+    const int c0 = pt * CPT, col = n0 + c0;
+    const long n = (long)M * d;
+    float wv[CPT];
+    load_vec<T, CPT>(normw + col, wv);
+#pragma unroll 1
+    for (int r = t / P; r < TR; r += RPP) {
+      const int m = m0 + r, mc = min(m, M - 1);
+      const long idx = (long)mc * d + col;
+      float pv[S][CPT], lv[CPT], ov[CPT];
+#pragma unroll
+      for (int z = 0; z < S; ++z)
+        if (z != ZS) load_vec<float, CPT>(part + z * n + idx, pv[z]);
+      if (lamdv != nullptr) {
+        load_vec<float, CPT>(lamdv + idx, lv);
+      } else {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) lv[j] = 0.f;
+      }
+      load_vec<T, CPT>(o + idx, ov);
+      float ss = sum_strided<MAX_HEADS / LPC>(ssq + (long)mc * h, pt % LPC, h, LPC);
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) pv[ZS][j] = tile[r * LDT + c0 + j];
+#pragma unroll
+      for (int x = 1; x < LPC; x <<= 1) ss += __shfl_xor(ss, x, 64);
+      const float rr = rsqrtf(ss * inv_d + eps);
+      float g[CPT], dot = 0.f;
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        float du = pv[0][j];
+#pragma unroll
+        for (int z = 1; z < S; ++z) du += pv[z][j];
+        du += lv[j];
+        g[j] = du * wv[j];
+        dot += g[j] * ov[j];
+        tile[r * LDT + c0 + j] = m < M ? du * ov[j] * rr : 0.f;
+      }
+#pragma unroll
+      for (int x = 1; x < LPC; x <<= 1) dot += __shfl_xor(dot, x, 64);
+      if (m < M) {
+        store_vec<float, CPT>(gw + (long)m * d + col, g);
+        if (pt % LPC == 0) rowdot[(long)m * (d / DU_EPI_TN) + col / DU_EPI_TN] = dot;
+      }
+    }
+    __syncthreads();
+    // norm_ctx-weight partials: one thread per (16-row slot, column)
+#pragma unroll 1
+    for (int it = t; it < (TR / 16) * BN; it += 256) {
+      const int sl = it / BN, cc = it % BN;
+      if (m0 + 16 * sl >= M) continue;
+      float sum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sum += tile[(16 * sl + i) * LDT + cc];
+      float* dst = dnw + (long)((m0 + 16 * sl) / 16) * d + n0 + cc;
+      *dst = *dst + sum;
+    }
+  }
+};
 
 template <typename T, int S>
 static __global__ __launch_bounds__(256) void k_du_epi(int M, int d, int h, float inv_d, float eps,

@@ -51,6 +51,9 @@ template <typename T> struct BwdWs {
 
 constexpr int NSLOT_TM = 16;      // rows per norm_ctx-weight partial slot (k_du_epi block rows)
 constexpr int DU_SPLIT = DM_DU_SPLIT;   // split-K slices of the du GEMM
+constexpr int DV_BN = 64;               // dv_in GEMM block columns beside the du slices (64 x DV_BN blocks)
+constexpr int DUF_BM = 32;              // block rows of du's last slice with the RMS-VJP epilogue (DUF_BM x 64)
+constexpr int DUF_STAGES = 3;           // its direct-to-LDS stages
 constexpr int NCHUNK = 64;        // row chunks of the column sums
 // fp32 elements of the split-K partial buffer of the weight-grad GEMMs ([S, M, N], N = d): eight
 // slices of the 6d x d projection product
@@ -370,30 +373,55 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
         hipLaunchKernelGGL((k_refine_bwd<T, DH, 1>), rgrid, dim3(256), 0, s, ra);
       }
     }
-    // dv_in = dv_ctx . W_vctx (mult family)
+    // du = dctx . W_sweep (+ lam dv_in) in DU_SPLIT split-K slices of d columns, then the RMS-VJP
+    // inputs. Mult family: slice 2 is dctx's v_map columns, which the dv_in GEMM's epilogue writes
+    // (dv_in = dv_ctx . W_vctx), so dv_in and the other slices run as one launch and slice 2 follows
+    // with the RMS-VJP inputs in its epilogue (EpiDuFinal): two launches where dv_in, du and du_epi
+    // took three. Linear: all slices, then k_du_epi.
+    static_assert(DU_SPLIT == 4, "slice 2 of the du GEMM is the v_map column block");
+    const SrcRows<T> da{dctx + sw * NS * 4 * d, 4 * d, N}, db{(const T*)w->w_sweep_t, 4 * d, d};
+    const typename DuEpiBody<T, DU_SPLIT>::Args ea{N, d, h, inv_d, c->rms_eps, (const float*)ws.du_part,
+                                                   mult ? (const float*)ws.lamdv : nullptr,
+                                                   (const T*)(sv.o + sw * NS * d),
+                                                   (const float*)(sv.ssq + sw * NS * h), (const T*)w->norm_ctx_w,
+                                                   ws.gw, ws.rowdot, ws.dnw};
+    EpiStoreTileF32 ep{N, d, ws.du_part, (long)N * d};
     if (mult) {
-      EpiVinBwd<T> ev{g, N, c->ctx_mod, c->mult_res_lambda, sv.save1 + sw * NS * 4 * d, (const T*)L->sig,
-                      dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
       const SrcRows<T> av{dvc + sw * NS * d, d, N}, bv{(const T*)w->w_vctx_t, d, d};
-      if constexpr (SW2_STAGES > 0) launch_gemm_auto<T, 64, 32, 4, 1, SW2_STAGES, 8>(av, bv, N, d, d, ev, s);
-      else launch_gemm<T, 64, 32, 4, 1, 8>(av, bv, N, d, d, ev, s);
-    }
-    // du = dctx . W_sweep (+ lam dv_in): split-K slices, then the RMS-VJP inputs
-    {
-      const int S = DU_SPLIT;
-      EpiStoreTileF32 ep{N, d, ws.du_part, (long)N * d};
-      const SrcRows<T> da{dctx + sw * NS * 4 * d, 4 * d, N}, db{(const T*)w->w_sweep_t, 4 * d, d};
-      // the layer-batched launch has blocks to spare: 128 x 128 tiles (half the LDS traffic per
-      // product; every element's k order is the same, so the results are too)
+      const SrcRows<T> da2{dctx + sw * NS * 4 * d + 2 * d, 4 * d, N}, db2{(const T*)w->w_sweep_t + 2 * d, 4 * d, d};
+      const EpiDuFinal<T, DU_SPLIT, 2> ef{N, d, h, inv_d, c->rms_eps, ea.part, ea.lamdv, ea.o, ea.ssq, ea.normw,
+                                          ea.gw, ea.rowdot, ea.dnw};
+      bool grouped = false;
+      if constexpr (sizeof(T) == 2) {
+        if (launch_log() != nullptr) {
+          // the layer-batched launch has blocks to spare: du in 128 x 128 tiles (half the LDS
+          // traffic per product; every element's k order is the same, and EpiDuFinal's sums do not
+          // depend on the block width, so the results are too)
+          grouped = true;
+          using PDu = GemmPart<T, 128, 128, 2, 2, -3, SrcRows<T>, SrcRows<T>, EpiStoreTileF32>;
+          using PVin = GemmPart<T, 64, 32, 4, 1, -SW2_STAGES, SrcRows<T>, SrcRows<T>, EpiVinBwd<T, 32>>;
+          const EpiVinBwd<T, 32> ev{g, N, c->ctx_mod, c->mult_res_lambda, sv.save1 + sw * NS * 4 * d,
+                                    (const T*)L->sig, dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
+          launch_gemm_pair(PDu{da, db, d, ep, d / 128, cdiv(N, 128), DU_SPLIT - 1, 2},
+                           PVin{av, bv, d, ev, d / 32, cdiv(N, 64), 1, -1}, s);
+          launch_gemm<T, 128, 128, 2, 2, -3>(da2, db2, N, d, d, ef, s);
+        }
+      }
+      if (!grouped) {
+        constexpr int DD = sizeof(T) == 2 ? -DU_STAGES : 4;
+        using PDu = GemmPart<T, 64, 64, 2, 2, DD, SrcRows<T>, SrcRows<T>, EpiStoreTileF32>;
+        using PVin = GemmPart<T, 64, DV_BN, 2, 2, DD, SrcRows<T>, SrcRows<T>, EpiVinBwd<T, DV_BN>>;
+        const EpiVinBwd<T, DV_BN> ev{g, N, c->ctx_mod, c->mult_res_lambda, sv.save1 + sw * NS * 4 * d,
+                                     (const T*)L->sig, dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
+        launch_gemm_pair(PDu{da, db, d, ep, d / 64, cdiv(N, 64), DU_SPLIT - 1, 2},
+                         PVin{av, bv, d, ev, d / DV_BN, cdiv(N, 64), 1, -1}, s);
+        launch_gemm<T, DUF_BM, 64, 2, 2, sizeof(T) == 2 ? -DUF_STAGES : 4>(da2, db2, N, d, d, ef, s);
+      }
+    } else {
       if (sizeof(T) == 2 && launch_log() != nullptr)
-        launch_gemm_splitk<T, 128, 128, 2, 2, sizeof(T) == 2 ? -3 : 4>(da, db, N, d, 4 * d, S, ep, s);
+        launch_gemm_splitk<T, 128, 128, 2, 2, sizeof(T) == 2 ? -3 : 4>(da, db, N, d, 4 * d, DU_SPLIT, ep, s);
       else
-        launch_gemm_splitk<T, 64, 64, 2, 2, sizeof(T) == 2 ? -DU_STAGES : 4>(da, db, N, d, 4 * d, S, ep, s);
-      const typename DuEpiBody<T, DU_SPLIT>::Args ea{N, d, h, inv_d, c->rms_eps, (const float*)ws.du_part,
-                                                     mult ? (const float*)ws.lamdv : nullptr,
-                                                     (const T*)(sv.o + sw * NS * d),
-                                                     (const float*)(sv.ssq + sw * NS * h), (const T*)w->norm_ctx_w,
-                                                     ws.gw, ws.rowdot, ws.dnw};
+        launch_gemm_splitk<T, 64, 64, 2, 2, sizeof(T) == 2 ? -DU_STAGES : 4>(da, db, N, d, 4 * d, DU_SPLIT, ep, s);
       const dim3 egrid(cdiv(N, 16), d / DU_EPI_TN);
       if (launch_log() != nullptr)
         record_launch<DuEpiBody<T, DU_SPLIT>>(egrid, dim3(256), ea);

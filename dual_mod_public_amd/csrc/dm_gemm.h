@@ -631,13 +631,19 @@ DM_DEV void gemm_kloop(const SA& sa, const SB& sb, int K, int m0, int n0, char* 
   else gemm_mainloop_dma<T, BM, BN, WM, WN, -D>(sa, sb, K, m0, n0, smem, acc, kbase);
 }
 
-// One block tile (bx, by) of split-K slice bz.
+// LDS bytes of one block of a k_gemm configuration
+template <typename T, int BM, int BN, int D, class SA, class SB>
+constexpr int gemm_block_lds() {
+  return gemm_lds_bytes<T, BM, BN, D, requires_prepare<SA>::value, SA::KMAJOR && SB::KMAJOR && D < 0>();
+}
+
+// One block tile (bx, by) of split-K slice bz, in the LDS at smem (gemm_block_lds bytes,
+// 1024-byte aligned).
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
-DM_DEV void gemm_block(const SA& sa, const SB& sb, int K, const EPI& epi, int bx, int by, int bz) {
+DM_DEV void gemm_block_at(const SA& sa, const SB& sb, int K, const EPI& epi, int bx, int by, int bz, char* smem) {
   using WT = WaveTile<BM, BN, WM, WN>;
   constexpr bool RMS = requires_prepare<SA>::value;
   constexpr bool KM = SA::KMAJOR && SB::KMAJOR && D < 0;
-  __shared__ __attribute__((aligned(1024))) char smem[gemm_lds_bytes<T, BM, BN, D, RMS, KM>()];
   const int m0 = by * BM, n0 = bx * BN;
   static_assert(!RMS || BM <= RMS_MAXR, "row-scale slots");
   const int wave = threadIdx.x >> 6;
@@ -701,6 +707,12 @@ DM_DEV void gemm_block(const SA& sa, const SB& sb, int K, const EPI& epi, int bx
 }
 
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
+DM_DEV void gemm_block(const SA& sa, const SB& sb, int K, const EPI& epi, int bx, int by, int bz) {
+  __shared__ __attribute__((aligned(1024))) char smem[gemm_block_lds<T, BM, BN, D, SA, SB>()];
+  gemm_block_at<T, BM, BN, WM, WN, D, SA, SB, EPI>(sa, sb, K, epi, bx, by, bz, smem);
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
 __global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint64_t* prof_ts) {
   const uint64_t t0 = prof_begin(prof_ts);
   // Blocks are dispatched round-robin over the 8 XCDs (each with its own L2). For
@@ -752,5 +764,43 @@ struct GemmBody {
     gemm_block<T, BM, BN, WM, WN, D, SA, SB, EPI>(a.sa, a.sb, a.K, a.epi, bx, by, 0);
   }
 };
+
+// Two independent GEMMs in one launch (blocks [0, P1 blocks) the first, the rest the second),
+// sharing one LDS allocation: a GemmPart is one k_gemm configuration over a grid of
+// (gx, gy) tiles and nz split-K slices (slice skip_z >= 0 left out: its K range is another
+// launch's).
+template <typename T, int BM_, int BN_, int WM, int WN, int D, class SA, class SB, class EPI>
+struct GemmPart {
+  static constexpr int LDS = gemm_block_lds<T, BM_, BN_, D, SA, SB>();
+  SA sa;
+  SB sb;
+  int K;   // per slice
+  EPI epi;
+  int gx, gy, nz, skip_z;
+  DM_DEV int blocks() const { return gx * gy * nz; }
+  DM_DEV void run(int L, char* smem) const {
+    const int bx = L % gx, by = (L / gx) % gy, zi = L / (gx * gy);
+    const int bz = (skip_z >= 0 && zi >= skip_z) ? zi + 1 : zi;
+    gemm_block_at<T, BM_, BN_, WM, WN, D, SA, SB, EPI>(sa, sb, K, epi, bx, by, bz, smem);
+  }
+};
+template <class P1, class P2> struct GemmPairBody {
+  static constexpr int THREADS = 256;
+  static constexpr int LDS = P1::LDS > P2::LDS ? P1::LDS : P2::LDS;
+  struct Args {
+    P1 p1;
+    P2 p2;
+  };
+  static DM_DEV void run(const Args& a, int bx, int) {
+    __shared__ __attribute__((aligned(1024))) char smem[LDS];
+    const int n1 = a.p1.blocks();
+    if (bx < n1) a.p1.run(bx, smem);
+    else a.p2.run(bx - n1, smem);
+  }
+};
+template <class P1, class P2>
+__global__ __launch_bounds__(256) void k_gemm_pair(typename GemmPairBody<P1, P2>::Args a) {
+  GemmPairBody<P1, P2>::run(a, (int)blockIdx.x, 0);
+}
 
 }  // namespace dm

@@ -335,6 +335,19 @@ void launch_gemm_kk(const SrcKMajor<T>& sa, const SrcKMajor<T>& sb, int M, int N
   launch_gemm<T, 128, 128, 2, 2, 4>(sa, sb, M, N, K, epi, s, prof_cls);
 }
 
+// Two independent GEMMs (GemmPart) in one launch: the first's blocks, then the second's.
+template <class P1, class P2>
+void launch_gemm_pair(const P1& p1, const P2& p2, hipStream_t s) {
+  using Body = GemmPairBody<P1, P2>;
+  const int n = p1.gx * p1.gy * p1.nz + p2.gx * p2.gy * p2.nz;
+  const typename Body::Args a{p1, p2};
+  if (launch_log() != nullptr) {
+    record_launch<Body>(dim3(n), dim3(256), a);
+    return;
+  }
+  hipLaunchKernelGGL((k_gemm_pair<P1, P2>), dim3(n), dim3(256), 0, s, a);
+}
+
 // Split-K: S slices of K/S each (K/S a multiple of the k-tile), slice z in grid.z.
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
 void launch_gemm_splitk(const SA& sa, const SB& sb, int M, int N, int K, int S, const EPI& epi, hipStream_t s,
