@@ -679,6 +679,11 @@ template <typename T, int DH> struct AttnBwdCfg {
   static constexpr int LDI = 64 + PAD;     // rows over the 64 queries / keys
   // four [64][LDE] row-major tiles (Q, K, V, dO or G) + a per-wave stage [4][16][LDI]
   static constexpr int LDS_ELEMS = 4 * 64 * LDE + 4 * 16 * LDI;
+  // k_attn_bwd: + the self column's dv_raw terms of the block's 32 key rows, fp32 [32][DH], where
+  // that fits the 160 KB of LDS (all but fp32 at head_dim 128)
+  static constexpr size_t PD_BYTES = 32 * DH * 4;
+  static constexpr bool PD_LDS = (size_t)LDS_ELEMS * sizeof(T) + PD_BYTES <= 160 * 1024;
+  static constexpr size_t BWD_LDS_BYTES = (size_t)LDS_ELEMS * sizeof(T) + (PD_LDS ? PD_BYTES : 0);
 };
 
 template <typename T, int DH>
@@ -731,10 +736,18 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
     const long n = (long)b * c + ic;                      // row of the sweep arrays
     float q[EPT], kv[EPT], vv[EPT], ks[EPT], vr[EPT], ov[EPT], gwv[EPT], dc[EPT];
     load_vec<T, EPT>(a.qr + (lrow0 + ic) * DH + e0, q);
-    load_vec<T, EPT>(a.Kin + (long)bh * a.in_stride + (long)(a.in_row0 + ic) * DH + e0, kv);
-    load_vec<T, EPT>(a.Vin + (long)bh * a.in_stride + (long)(a.in_row0 + ic) * DH + e0, vv);
-    load_vec<T, EPT>(a.kself + (lrow0 + ic) * DH + e0, ks);
-    load_vec<T, EPT>(a.vraw + (lrow0 + ic) * DH + e0, vr);
+    // a key role reads K / V rows (its keys) and the raw self pair (its rows' self column) of its
+    // own key half only; a wave's 16 rows lie in one half, so this is uniform over the wave
+    const bool own = role == 0 || (i >> 5) == kh;
+    if (own) {
+      load_vec<T, EPT>(a.Kin + (long)bh * a.in_stride + (long)(a.in_row0 + ic) * DH + e0, kv);
+      load_vec<T, EPT>(a.Vin + (long)bh * a.in_stride + (long)(a.in_row0 + ic) * DH + e0, vv);
+      load_vec<T, EPT>(a.kself + (lrow0 + ic) * DH + e0, ks);
+      load_vec<T, EPT>(a.vraw + (lrow0 + ic) * DH + e0, vr);
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) { kv[e] = 0.f; vv[e] = 0.f; ks[e] = 0.f; vr[e] = 0.f; }
+    }
     load_vec<T, EPT>(a.o + n * d + hh * DH + e0, ov);
     load_vec<float, EPT>(a.gw + n * d + hh * DH + e0, gwv);
     if (a.docat != nullptr) {
@@ -754,12 +767,17 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
         load_vec<float, EPT>(a.G + lr, gold);
         dbold = a.Dbar[lrow0 + ic];
       }
-    } else if ((i >> 5) == kh) {
+    } else if ((i >> 5) == kh && !(C::PD_LDS && a.fuse_refine)) {
       load_vec<float, EPT>(a.dvraw + lr, acc1);
     }
     float ss = 0.f, dot = 0.f;
-    ss = sum_strided<MAX_HEADS / 4>(a.ssq + n * g.h, part, g.h, 4);
-    dot = sum_strided<MAX_ROWDOT / 4>(a.rowdot + n * a.nrd, part, a.nrd, 4);
+    if ((g.h & 15) == 0 && (a.nrd & 15) == 0) {   // 16-byte loads: a quarter of the load instructions
+      ss = sum_quads<MAX_HEADS / 16>(a.ssq + n * g.h, part, g.h);
+      dot = sum_quads<MAX_ROWDOT / 16>(a.rowdot + n * a.nrd, part, a.nrd);
+    } else {
+      ss = sum_strided<MAX_HEADS / 4>(a.ssq + n * g.h, part, g.h, 4);
+      dot = sum_strided<MAX_ROWDOT / 4>(a.rowdot + n * a.nrd, part, a.nrd, 4);
+    }
     ss += __shfl_xor(ss, 1, 64); ss += __shfl_xor(ss, 2, 64);
     dot += __shfl_xor(dot, 1, 64); dot += __shfl_xor(dot, 2, 64);
     const float r = rsqrtf(ss * a.inv_d + a.eps);
@@ -802,9 +820,17 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
       if (role == 0) {
         if (part == 0) a.sdss[lrow0 + i] = sdold + dss;
       } else if ((i >> 5) == kh) {
+        if (C::PD_LDS && a.fuse_refine) {
+          // the refine VJP of these rows adds to the same dv_raw rows: it takes this term from
+          // LDS, so dv_raw is read (early, with its other inputs) and written once
+          float* pd = reinterpret_cast<float*>(smem_raw + (size_t)C::LDS_ELEMS * sizeof(T)) + (i - 32 * kh) * DH + e0;
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) acc1[e] += ps * dO[e];
-        store_vec<float, EPT>(a.dvraw + lr, acc1);
+          for (int e = 0; e < EPT; ++e) pd[e] = ps * dO[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < EPT; ++e) acc1[e] += ps * dO[e];
+          store_vec<float, EPT>(a.dvraw + lr, acc1);
+        }
       }
     } else {
 #pragma unroll
@@ -866,6 +892,13 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
   // take part in the barriers and the refine items.
   else {
     const bool mine = (wave >> 1) == kh;
+    // sweep >= 1: the thread's first refine item's inputs (the forward state and the dk_raw /
+    // dv_raw accumulators, whose phase-1 writes, if any, are behind the barrier above), gathered
+    // before the products so their latency overlaps them
+    constexpr int Q = DH / 8;
+    const int n_items = a.fuse_refine ? max(0, min(c - 32 * kh, 32)) * Q : 0;
+    RefineIn in0;
+    if (tid < n_items) in0 = refine_gather<T, DH>(a.ref, b * c + 32 * kh + tid / Q, hh, 4 * (tid % Q));
     // sweep 0: the dkself rows and the dvraw rows after phase 1, loaded before the products
     float dko[4][NDT], dvo[4][NDT];
     if (!a.fuse_refine && mine) {
@@ -938,9 +971,10 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
       // Items it = tid + 256 k over the block's key rows: row 32 kh + it / Q, pairs 4 (it % Q);
       // a row's items are Q consecutive lanes. One item per thread at a time: with two in
       // flight the kernel needs more than 256 registers a lane and a CU holds one block
-      // instead of two.
-      constexpr int Q = DH / 8;
-      auto grads = [&](int j, int jj) {
+      // instead of two. The first item's inputs were gathered before the products.
+      const float* pds = reinterpret_cast<const float*>(smem_raw + (size_t)C::LDS_ELEMS * sizeof(T));
+      auto apply = [&](int it, RefineIn& in) {
+        const int j = 32 * kh + it / Q, jj = 4 * (it % Q);
         const float* kr = dKs + j * LDF + jj;
         const float* vr = dVs + j * LDF + jj;
         RefineGrad4 gr;
@@ -948,13 +982,20 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
         unpackf4(*reinterpret_cast<const floatx4*>(kr + DH / 2), gr.kb);
         unpackf4(*reinterpret_cast<const floatx4*>(vr), gr.va);
         unpackf4(*reinterpret_cast<const floatx4*>(vr + DH / 2), gr.vb);
-        return gr;
+        if constexpr (C::PD_LDS) {   // the self column's dv_raw term of the row (phase 1)
+          const float* pd = pds + (j - 32 * kh) * DH + jj;
+          float p1[4], p2[4];
+          unpackf4(*reinterpret_cast<const floatx4*>(pd), p1);
+          unpackf4(*reinterpret_cast<const floatx4*>(pd + DH / 2), p2);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { in.ovr1[e] += p1[e]; in.ovr2[e] += p2[e]; }
+        }
+        refine_apply<T, DH>(a.ref, b * c + j, hh, jj, in, gr);
       };
-      const int n_items = max(0, min(c - 32 * kh, 32)) * Q;
-      for (int it = tid; it < n_items; it += 256) {
-        const int j = 32 * kh + it / Q, jj = 4 * (it % Q);
-        const RefineIn in = refine_gather<T, DH>(a.ref, b * c + j, hh, jj);
-        refine_apply<T, DH>(a.ref, b * c + j, hh, jj, in, grads(j, jj));
+      if (tid < n_items) apply(tid, in0);
+      for (int it = tid + 256; it < n_items; it += 256) {
+        RefineIn in = refine_gather<T, DH>(a.ref, b * c + 32 * kh + it / Q, hh, 4 * (it % Q));
+        apply(it, in);
       }
       return;
     }

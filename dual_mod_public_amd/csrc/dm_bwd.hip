@@ -304,6 +304,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
   const T* kraw = (const T*)L->kraw;
   const size_t slot = (size_t)BH * CMAX * DH;
   const size_t lds_attn = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
+  const size_t lds_attn_bwd = AttnBwdCfg<T, DH>::BWD_LDS_BYTES;
   T* vinS = stacked_vin<T>(tape, tape_off, n_cells, ws);
   const int t_end = sched[3 * (n_cells - 1)] + sched[3 * (n_cells - 1) + 1];   // rows of the schedule
   const long coff = vin_row(c, sched, n_cells, ci);   // rows of the cells after this one in the stacks
@@ -442,9 +443,9 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
                         scale, inv_d, c->rms_eps, ws.dkself, ws.dvraw, ws.dq, ws.sdss, sw >= 1 ? 1 : 0,
                         sw >= 1 ? refine_args(sw - 1) : RefineBwdArgs<T>{}};
       if (launch_log() != nullptr)
-        record_launch<AttnBwdBody<T, DH>>(dim3(ATTN_BWD_ROLES, BH), dim3(256), aa, (unsigned)lds_attn);
+        record_launch<AttnBwdBody<T, DH>>(dim3(ATTN_BWD_ROLES, BH), dim3(256), aa, (unsigned)lds_attn_bwd);
       else
-        hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(ATTN_BWD_ROLES, BH), dim3(256), lds_attn, s, aa);
+        hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(ATTN_BWD_ROLES, BH), dim3(256), lds_attn_bwd, s, aa);
     }
   }
   // the other operand of dW_sweep = dctx^T u: this cell's K*N rows of u = RMSNorm(o)

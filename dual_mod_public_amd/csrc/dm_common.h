@@ -326,6 +326,20 @@ DM_DEV float sum_strided(const float* __restrict__ p, int q0, int n, int step) {
   return s;
 }
 
+// sum of p[q] for q = 4 part + 16 j + i (i < 4, j < n / 16), n a multiple of 16 and at most 16 MAXJ:
+// one 16-byte load per j, every load issued before the first add
+template <int MAXJ>
+DM_DEV float sum_quads(const float* __restrict__ p, int part, int n) {
+  const int nj = n >> 4;
+  floatx4 v[MAXJ];
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) v[j] = *reinterpret_cast<const floatx4*>(p + 4 * part + 16 * min(j, nj - 1));
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) s += j < nj ? (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]) : 0.f;
+  return s;
+}
+
 // The per-row partial sums of the sweep arrays: ssq holds h <= MAX_HEADS per-head
 // sums of squares per row, rowdot d / 32 <= MAX_ROWDOT partial dot products.
 constexpr int MAX_HEADS = 64;
