@@ -546,48 +546,96 @@ DM_DEV void du_epi_body(int M, int d, int h, float inv_d, float eps,
 // columns of a row and the 8 threads of a 64-column chunk are 8 consecutive lanes: the row's sums
 // (of its head sums of squares, of gw * o) are a fixed xor-tree over those lanes, so every block
 // width gives the same bits.
-template <typename T, int S, int ZS> struct EpiDuFinal {
+template <typename T, int S, int ZS, bool PRE = false> struct EpiDuFinal {
   static constexpr int TILE_ROWS = 32;
+  static constexpr int CPT = 8, LPC = DU_EPI_TN / CPT;   // columns per thread, lanes per 64-column chunk
+  static constexpr int NSS = MAX_HEADS / LPC;            // head-sum loads per thread
+  // PRE (32 x 64 block tiles: each thread one row of 8 columns, one pass): the row's inputs are
+  // gathered with the k-loop's last stage. The exact count of their load instructions (16-byte
+  // loads and the head sums' dwords, which the compiler cannot merge):
+  static constexpr int LATE_GATHERS = PRE ? 2 * (S - 1) + 2 + 2 * (int)(sizeof(T) / 2) + NSS : 0;
   int M, d, h;
   float inv_d, eps;
   const float* __restrict__ part;    // [S, M, d] split-K slices (slice ZS, this GEMM's, not read)
-  const float* __restrict__ lamdv;   // [M, d] or null
+  const float* __restrict__ lamdv;   // [M, d]
   const T* __restrict__ o;           // [M, d]
   const float* __restrict__ ssq;     // [M, h]
   const T* __restrict__ normw;       // [d]
   float* __restrict__ gw;
   float* __restrict__ rowdot;
   float* __restrict__ dnw;
-  struct TilePre {};
-  DM_DEV TilePre tile_prefetch(int, int) const { return TilePre{}; }
+  struct TilePre {
+    floatx4 pv[PRE ? S - 1 : 1][2], lv[2];
+    Raw8<T> ov, wv;
+    float ss[NSS];
+  };
+  DM_DEV TilePre tile_prefetch(int m0, int n0) const {
+    TilePre pr;
+    if constexpr (PRE) {
+      const int t = threadIdx.x, pt = t % (64 / CPT) , r = t / (64 / CPT);
+      const int mc = min(m0 + r, M - 1), col = n0 + pt * CPT;
+      const long n = (long)M * d, idx = (long)mc * d + col;
+      int zi = 0;
+#pragma unroll
+      for (int z = 0; z < S; ++z) {
+        if (z == ZS) continue;
+        pr.pv[zi][0] = ld_global<floatx4>(part + z * n + idx);
+        pr.pv[zi][1] = ld_global<floatx4>(part + z * n + idx + 4);
+        ++zi;
+      }
+      pr.lv[0] = ld_global<floatx4>(lamdv + idx);
+      pr.lv[1] = ld_global<floatx4>(lamdv + idx + 4);
+      pr.ov = ld8_global(o + idx);
+      pr.wv = ld8_global(normw + col);
+#pragma unroll
+      for (int i = 0; i < NSS; ++i) pr.ss[i] = ssq[(long)mc * h + min(pt % LPC + i * LPC, h - 1)];
+    }
+    return pr;
+  }
   template <int TR, int BN, int LDT>
-  DM_DEV void tile_apply(const float* tile_in, int m0, int n0, const float*, const TilePre&, int) const {
-    constexpr int CPT = 8, LPC = DU_EPI_TN / CPT;   // columns per thread, lanes per 64-column chunk
+  DM_DEV void tile_apply(const float* tile_in, int m0, int n0, const float*, const TilePre& pr, int) const {
     constexpr int P = BN / CPT, RPP = 256 / P;       // threads per row, rows per pass
     static_assert(BN % DU_EPI_TN == 0 && 256 % P == 0 && TR % RPP == 0 && TR % 16 == 0, "tile shape");
+    static_assert(!PRE || (BN == 64 && TR == 32), "the gathered inputs cover one 32 x 64 pass");
     static_assert(MAX_HEADS % LPC == 0, "head sums split over a chunk's lanes");
     float* tile = const_cast<float*>(tile_in);  // the block's own LDS chunk: reused for du o r
     const int t = threadIdx.x, pt = t % P;
     const int c0 = pt * CPT, col = n0 + c0;
     const long n = (long)M * d;
     float wv[CPT];
-    load_vec<T, CPT>(normw + col, wv);
+    if constexpr (PRE) unpack8<T>(pr.wv, wv);
+    else load_vec<T, CPT>(normw + col, wv);
 #pragma unroll 1
     for (int r = t / P; r < TR; r += RPP) {
       const int m = m0 + r, mc = min(m, M - 1);
       const long idx = (long)mc * d + col;
-      float pv[S][CPT], lv[CPT], ov[CPT];
+      float pv[S][CPT], lv[CPT], ov[CPT], ssv[NSS];
+      if constexpr (PRE) {
+        int zi = 0;
 #pragma unroll
-      for (int z = 0; z < S; ++z)
-        if (z != ZS) load_vec<float, CPT>(part + z * n + idx, pv[z]);
-      if (lamdv != nullptr) {
-        load_vec<float, CPT>(lamdv + idx, lv);
+        for (int z = 0; z < S; ++z) {
+          if (z == ZS) continue;
+          unpackf4(pr.pv[zi][0], pv[z]);
+          unpackf4(pr.pv[zi][1], pv[z] + 4);
+          ++zi;
+        }
+        unpackf4(pr.lv[0], lv);
+        unpackf4(pr.lv[1], lv + 4);
+        unpack8<T>(pr.ov, ov);
+#pragma unroll
+        for (int i = 0; i < NSS; ++i) ssv[i] = pr.ss[i];
       } else {
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) lv[j] = 0.f;
+        for (int z = 0; z < S; ++z)
+          if (z != ZS) load_vec<float, CPT>(part + z * n + idx, pv[z]);
+        load_vec<float, CPT>(lamdv + idx, lv);
+        load_vec<T, CPT>(o + idx, ov);
+#pragma unroll
+        for (int i = 0; i < NSS; ++i) ssv[i] = ssq[(long)mc * h + min(pt % LPC + i * LPC, h - 1)];
       }
-      load_vec<T, CPT>(o + idx, ov);
-      float ss = sum_strided<MAX_HEADS / LPC>(ssq + (long)mc * h, pt % LPC, h, LPC);
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < NSS; ++i) ss += (pt % LPC + i * LPC < h) ? ssv[i] : 0.f;
 #pragma unroll
       for (int j = 0; j < CPT; ++j) pv[ZS][j] = tile[r * LDT + c0 + j];
 #pragma unroll

@@ -392,6 +392,8 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
       const SrcRows<T> da2{dctx + sw * NS * 4 * d + 2 * d, 4 * d, N}, db2{(const T*)w->w_sweep_t + 2 * d, 4 * d, d};
       const EpiDuFinal<T, DU_SPLIT, 2> ef{N, d, h, inv_d, c->rms_eps, ea.part, ea.lamdv, ea.o, ea.ssq, ea.normw,
                                           ea.gw, ea.rowdot, ea.dnw};
+      const EpiDuFinal<T, DU_SPLIT, 2, DUF_BM == 32> efp{N, d, h, inv_d, c->rms_eps, ea.part, ea.lamdv, ea.o, ea.ssq,
+                                                         ea.normw, ea.gw, ea.rowdot, ea.dnw};
       bool grouped = false;
       if constexpr (sizeof(T) == 2) {
         if (launch_log() != nullptr) {
@@ -416,7 +418,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
                                      (const T*)L->sig, dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
         launch_gemm_pair(PDu{da, db, d, ep, d / 64, cdiv(N, 64), DU_SPLIT - 1, 2},
                          PVin{av, bv, d, ev, d / DV_BN, cdiv(N, 64), 1, -1}, s);
-        launch_gemm<T, DUF_BM, 64, 2, 2, sizeof(T) == 2 ? -DUF_STAGES : 4>(da2, db2, N, d, d, ef, s);
+        launch_gemm<T, DUF_BM, 64, 2, 2, sizeof(T) == 2 ? -DUF_STAGES : 4>(da2, db2, N, d, d, efp, s);
       }
     } else {
       if (sizeof(T) == 2 && launch_log() != nullptr)
