@@ -177,6 +177,13 @@ void run_proj_dispatch(const dm_config* c, const dm_packed* w, const T* xhat, in
                      s);
 }
 
+// Split partials of the next cell's committed prefix that one fused GEMM 2 + attention launch
+// computes as extra blocks (splits s0 .. s0 + ns - 1 of ca)
+template <typename T> struct AheadComm {
+  CommArgs<T> ca;
+  int s0 = 0, ns = 0;
+};
+
 // One sweep's refine: sweep GEMM 1 (+ GEMM 2 for the mult family) with the blend
 // epilogues, writing the refined rows to (Kout, Vout).
 template <typename T, int DH>
@@ -184,7 +191,7 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
                 const T* kraw, const T* vraw, const T* glogx, const T* sig, const float* cos,
                 const float* sin, T* Kout, T* Vout, long out_stride, int out_row0, T* vin, T* gvu,
                 T* save1, T* save2, hipStream_t s, const AttendArgs<T>* next_attend = nullptr,
-                bool wide = false) {
+                bool wide = false, const AheadComm<T>* ahead = nullptr) {
   const T* normw = (const T*)w->norm_ctx_w;
   SrcRowsRs<T> sa{o, c->d, N, ssq, c->h, 1.0f / (float)c->d, c->rms_eps};
   SrcRows<T> sb{(const T*)w->w_sweep, c->d, 4 * c->d};
@@ -229,8 +236,14 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
     }
     uint64_t* ts;
     const int idx = prof_launch_begin(PROF_SWEEP2, true, ts);
-    launch_timed(idx, k_sweep2_attend<T, DH>, dim3(c->h, N / CMAX), dim3(256), 0, s, av, bv, c->d, e2,
-                 *next_attend, ts);
+    if (ahead != nullptr && ahead->ns > 0) {
+      const int nfused = c->h * (N / CMAX);
+      launch_timed(idx, k_sweep2_attend_comm<T, DH>, dim3(nfused + ahead->ns * c->B * c->h), dim3(256), 0, s, av,
+                   bv, c->d, e2, *next_attend, ahead->ca, nfused, ahead->s0, ts);
+    } else {
+      launch_timed(idx, k_sweep2_attend<T, DH>, dim3(c->h, N / CMAX), dim3(256), 0, s, av, bv, c->d, e2,
+                   *next_attend, ts);
+    }
     return;
   }
   if (!linear && vgain != nullptr) {
@@ -270,18 +283,19 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
   }
 }
 
-// Committed accumulator of a cell: split partials (merged by the first sweep's
-// attention) or, with one split, the merged state directly.
+// Committed accumulator of a cell: split partials over its committed keys but the last ones
+// (comm_prev_lo), merged by the first sweep's attention, which adds those last keys itself.
 template <typename T, int DH>
 int run_comm(const CellGeom& g, const T* qr, const T* Kc, const T* Vc, float scale, const CellWs& ws,
              hipStream_t s) {
   const int kstart = comm_kstart(g.pos0, g.window);
-  const CommPlan cp = comm_plan(g.pos0 - kstart, g.B * g.h);
+  const int prev_lo = comm_prev_lo(g.pos0, kstart);
+  const CommPlan cp = comm_plan(prev_lo - kstart, g.B * g.h);
   const int BH = g.B * g.h;
   CommArgs<T> ca{g, qr, Kc, Vc, cp.split_len, scale, ws.Ap, ws.Zp, ws.Mp};
   ca.nsplit = cp.nsplit;
   ca.kstart = kstart;
-  if (cp.nsplit == 1) { ca.A = ws.A; ca.Z = ws.Z; ca.Mx = ws.M; }
+  ca.kend = prev_lo;
   if (launch_log() != nullptr) {
     // recorded even without a committed prefix (grid x 0), so that every chunk of a layer
     // records the same launch sequence
@@ -308,11 +322,17 @@ template <typename T> struct CellRows {
 // committed rows [0, pos0) of the cache. Without `sv` the sweeps refine the
 // chunk's rows in place (the cache rows, or `rows`) and the last sweep leaves the final rows
 // there; with `sv` every sweep's rows and state are kept in sv (cache rows untouched).
+// Layer loops hand committed-prefix work from one cell to the next: own_nsplit >= 0 says the
+// previous cell's launches already computed this cell's split partials (that many); next_pos0 >= 0
+// names the next cell (next_cc rows), whose split partials this cell computes inside its fused
+// GEMM 2 + attention launches where it has them. Returns how many it computed (-1: none, the next
+// cell runs its own). The partials are the same either way: same plan, same kernel body.
 template <typename T, int DH>
-void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const float* cos,
-              const float* sin, int pos0, int cc, int n_sweeps, int buf_t0, int Tbuf, T* Kc, T* Vc,
-              int cache_T, T* ocat, float* o_last, const CellWs& ws, const CellSave<T>* sv, hipStream_t s,
-              const CellRows<T>& rows = CellRows<T>{}, bool wide = false) {
+int run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const float* cos,
+             const float* sin, int pos0, int cc, int n_sweeps, int buf_t0, int Tbuf, T* Kc, T* Vc,
+             int cache_T, T* ocat, float* o_last, const CellWs& ws, const CellSave<T>* sv, hipStream_t s,
+             const CellRows<T>& rows = CellRows<T>{}, bool wide = false, int own_nsplit = -1, int next_pos0 = -1,
+             int next_cc = 0) {
   CellGeom g{c->B, cc, c->d, c->h, DH, pos0, buf_t0, Tbuf, cache_T};
   g.kmod_cols = c->kmod_vraw_heads * DH;
   g.kmod_mode = c->kmod_mode;
@@ -331,7 +351,9 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
   const T* kself = (const T*)L->kself;
   const T* vraw = (const T*)L->vraw;
   const T* kraw = (const T*)L->kraw;
-  const int nsplit = run_comm<T, DH>(g, qr, Kc, Vc, scale, ws, s);
+  const int nsplit = own_nsplit >= 0 ? own_nsplit : run_comm<T, DH>(g, qr, Kc, Vc, scale, ws, s);
+  const int prev_lo = comm_prev_lo(pos0, comm_kstart(pos0, g.window));
+  const bool committed = pos0 > comm_kstart(pos0, g.window);
   const long cache_stride = (long)cache_T * DH, ws_stride = (long)CMAX * DH;
   const size_t slot = (size_t)BH * CMAX * DH;
 
@@ -339,6 +361,31 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
   // chunks) when B*h gives that kernel enough blocks, or when forced by the flags
   const bool fuse = c->ctx_mod != DM_CTX_LINEAR && cc == CMAX && !(c->flags & DM_FLAG_UNFUSED_ATTEND) &&
                     ((c->flags & DM_FLAG_FUSED_ATTEND) || BH >= 128);
+  // the next cell's split partials, spread over this cell's fused launches (sweeps 0 .. K-2); they
+  // read only keys before this cell (the next cell's last 64 committed keys are its own attention's)
+  AheadComm<T> ahead;
+  int handed = -1;
+  if (next_pos0 >= 0 && fuse && n_sweeps >= 2 && launch_log() == nullptr) {
+    CellGeom gn = g;
+    gn.pos0 = next_pos0;
+    gn.c = next_cc;
+    gn.buf_t0 = buf_t0 + (next_pos0 - pos0);
+    const int kst = comm_kstart(next_pos0, g.window), plo = comm_prev_lo(next_pos0, kst);
+    const CommPlan cp = comm_plan(plo - kst, BH);
+    if (plo <= pos0) {
+      ahead.ca = CommArgs<T>{gn, qr, Kc, Vc, cp.split_len, scale, ws.Ap, ws.Zp, ws.Mp};
+      ahead.ca.nsplit = cp.nsplit;
+      ahead.ca.kstart = kst;
+      ahead.ca.kend = plo;
+      handed = cp.nsplit;
+    }
+  }
+  auto ahead_for = [&](int sw) -> const AheadComm<T>* {
+    if (handed <= 0) return nullptr;
+    ahead.s0 = handed * sw / (n_sweeps - 1);
+    ahead.ns = handed * (sw + 1) / (n_sweeps - 1) - ahead.s0;
+    return &ahead;
+  };
   // intra rows read by sweep sw (= the rows written by sweep sw - 1)
   auto rows_in = [&](int sw, const T*& Kin, const T*& Vin, long& in_stride, int& in_row0) {
     if (sw == 0) { Kin = kself; Vin = vraw; in_stride = (long)Tbuf * DH; in_row0 = buf_t0; }
@@ -352,10 +399,11 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
     T* o = sv ? sv->o + sw * NS * d : (T*)ws.o;
     float* ssq = sv ? sv->ssq + sw * NS * c->h : ws.ssq;
     return AttendArgs<T>{g, qr, kself, vraw, Kin, Vin, in_stride, in_row0,
-                         sw == 0 ? nsplit : (nsplit > 0 ? 1 : 0), ws.Ap, ws.Zp, ws.Mp, ws.A, ws.Z, ws.M,
+                         sw == 0 ? nsplit : 0, ws.Ap, ws.Zp, ws.Mp, ws.A, ws.Z, ws.M,
                          scale, o, ssq, last ? ocat : nullptr, last ? o_last : nullptr,
                          sv ? sv->stat_m + sw * (size_t)BH * CMAX : nullptr,
-                         sv ? sv->stat_z + sw * (size_t)BH * CMAX : nullptr};
+                         sv ? sv->stat_z + sw * (size_t)BH * CMAX : nullptr,
+                         sw > 0 && committed ? 1 : 0, Kc, Vc, sw == 0 ? prev_lo : pos0};
   };
 
   for (int sw = 0; sw < n_sweeps; ++sw) {
@@ -383,21 +431,23 @@ void run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, co
     const AttendArgs<T> next = attend_args(last ? sw : sw + 1);
     run_refine<T, DH>(c, w, g, N, o, ssq, kraw, vraw, (const T*)L->glogx, (const T*)L->sig, cos, sin, Kout, Vout,
                       out_stride, out_row0, vin, (T*)ws.gvu, sv ? sv->save1 + sw * NS * 4 * d : nullptr,
-                      sv ? sv->save2 + sw * NS * d : nullptr, s, (fuse && !last) ? &next : nullptr, wide);
+                      sv ? sv->save2 + sw * NS * d : nullptr, s, (fuse && !last) ? &next : nullptr, wide,
+                      (fuse && !last) ? ahead_for(sw) : nullptr);
   }
+  return handed;
 }
 
 template <typename T>
-void run_cell_dispatch(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const float* cos,
-                       const float* sin, int pos0, int cc, int n_sweeps, int buf_t0, int Tbuf, void* Kc,
-                       void* Vc, int cache_T, void* ocat, float* o_last, const CellWs& ws,
-                       const CellSave<T>* sv, hipStream_t s, const CellRows<T>& rows = CellRows<T>{}) {
+int run_cell_dispatch(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, const float* cos,
+                      const float* sin, int pos0, int cc, int n_sweeps, int buf_t0, int Tbuf, void* Kc,
+                      void* Vc, int cache_T, void* ocat, float* o_last, const CellWs& ws,
+                      const CellSave<T>* sv, hipStream_t s, const CellRows<T>& rows = CellRows<T>{},
+                      int own_nsplit = -1, int next_pos0 = -1, int next_cc = 0) {
   if (c->dh == 64)
-    run_cell<T, 64>(c, w, L, cos, sin, pos0, cc, n_sweeps, buf_t0, Tbuf, (T*)Kc, (T*)Vc, cache_T, (T*)ocat,
-                    o_last, ws, sv, s, rows);
-  else
-    run_cell<T, 128>(c, w, L, cos, sin, pos0, cc, n_sweeps, buf_t0, Tbuf, (T*)Kc, (T*)Vc, cache_T, (T*)ocat,
-                     o_last, ws, sv, s, rows);
+    return run_cell<T, 64>(c, w, L, cos, sin, pos0, cc, n_sweeps, buf_t0, Tbuf, (T*)Kc, (T*)Vc, cache_T, (T*)ocat,
+                           o_last, ws, sv, s, rows, false, own_nsplit, next_pos0, next_cc);
+  return run_cell<T, 128>(c, w, L, cos, sin, pos0, cc, n_sweeps, buf_t0, Tbuf, (T*)Kc, (T*)Vc, cache_T, (T*)ocat,
+                          o_last, ws, sv, s, rows, false, own_nsplit, next_pos0, next_cc);
 }
 
 inline int check_bufs(const dm_config* c, const dm_layer_bufs* L) {

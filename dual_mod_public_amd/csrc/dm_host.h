@@ -137,6 +137,9 @@ inline int check_window(const dm_config* c, const int32_t* sched, int n_cells) {
 
 // first committed key a cell at pos0 reads (chunk row 0's window start)
 inline int comm_kstart(int pos0, int window) { return window > 0 ? std::max(0, pos0 - window + 1) : 0; }
+// the cell's last committed keys [comm_prev_lo, pos0), at most one 64-key tile: its first sweep's
+// attention reads them itself; the split partials cover [kstart, comm_prev_lo)
+inline int comm_prev_lo(int pos0, int kstart) { return std::max(kstart, pos0 - 64); }
 inline int comm_splits_max(int cache_T) {
   int n = cdiv(cache_T, COMM_SPLIT_MIN);
   return n < 1 ? 1 : (n > COMM_MAX_SPLITS ? COMM_MAX_SPLITS : n);

@@ -455,6 +455,8 @@ template <typename T> struct CommArgs {
   float* Mx;   // [nsplit, B*h, c]
   int nsplit = 0;   // splits of this cell (a grouped launch's grid covers the largest)
   int kstart = 0;   // first committed key of split 0 (the window's start for chunk row 0)
+  int kend = 0;     // end of the keys the splits cover (the cell's last committed keys are the
+                    // first sweep's attention's: AttendArgs::prev_lo)
 };
 
 struct KeyBound {
@@ -473,10 +475,10 @@ struct KeyWindow {
 };
 constexpr int NO_WINDOW_LO = -(1 << 30);
 
+// in the LDS at lds (AttnCfg<T, DH>::LDS_ELEMS elements)
 template <typename T, int DH>
-DM_DEV void comm_partial_block(const CommArgs<T>& a, int s, int bh) {
+DM_DEV void comm_partial_block_at(const CommArgs<T>& a, int s, int bh, T* lds) {
   using C = AttnCfg<T, DH>;
-  __shared__ __attribute__((aligned(16))) T lds[C::LDS_ELEMS];
   T* Ks = lds;
   T* Vs = Ks + C::KT * C::LDK;
   T* Ps = Vs + C::KT * C::LDK;
@@ -484,7 +486,7 @@ DM_DEV void comm_partial_block(const CommArgs<T>& a, int s, int bh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int BH = g.B * g.h;
   const int k_begin = a.kstart + s * a.split_len;
-  const int k_end = min(k_begin + a.split_len, g.pos0);
+  const int k_end = min(k_begin + a.split_len, a.kend);
   const int qrow = 16 * wave + (lane & 15);
   const int lo0 = g.window > 0 ? g.pos0 - g.window + 1 : NO_WINDOW_LO;
 
@@ -524,6 +526,12 @@ DM_DEV void comm_partial_block(const CommArgs<T>& a, int s, int bh) {
 }
 
 template <typename T, int DH>
+DM_DEV void comm_partial_block(const CommArgs<T>& a, int s, int bh) {
+  __shared__ __attribute__((aligned(16))) T lds[AttnCfg<T, DH>::LDS_ELEMS];
+  comm_partial_block_at<T, DH>(a, s, bh, lds);
+}
+
+template <typename T, int DH>
 static __global__ __launch_bounds__(256) void k_comm_partial(CommArgs<T> a) {
   comm_partial_block<T, DH>(a, blockIdx.x, blockIdx.y);
 }
@@ -550,8 +558,11 @@ template <typename T> struct AttendArgs {
   const T* qr; const T* kself; const T* vraw;   // layer buffers
   const T* Kin; const T* Vin;                   // intra rows of this sweep: (b,h) at bh*in_stride,
   long in_stride; int in_row0;                  //   chunk row p at row in_row0 + p
-  int nsplit;                                   // committed partials to merge (0: none, 1: merged)
-  const float* Ap; const float* Zp; const float* Mp;   // partials [nsplit, B*h, c, ...] when nsplit > 1
+  // The committed prefix [kstart, pos0): merged_in, the merged state A / Z / Mx of the cell's first
+  // sweep (later sweeps); else the first sweep merges nsplit split partials (keys [kstart, prev_lo))
+  // and its last keys [prev_lo, pos0) (cache rows Kc / Vc) and stores the merged state.
+  int nsplit;                                   // split partials to merge
+  const float* Ap; const float* Zp; const float* Mp;   // partials [nsplit, B*h, c, ...]
   float* A; float* Z; float* Mx;                // merged committed state [B*h, c, ...]
   float scale;
   T* o;         // [B*c, d]
@@ -560,6 +571,10 @@ template <typename T> struct AttendArgs {
   float* o_last;    // [B*c, d] or nullptr
   float* stat_m;    // [B*h, c] final row max (or nullptr)
   float* stat_z;    // [B*h, c] final row sum (or nullptr)
+  int merged_in = 0;
+  const T* Kc = nullptr;   // the committed cache rows (row stride DH, (b, h) stride g.cache_T DH)
+  const T* Vc = nullptr;
+  int prev_lo = 0;         // first of the last committed keys (pos0: none)
 };
 
 // The attention of query rows [q0, q0 + 16 NW) of (b, h) = bh, NW waves of 16 rows. With
@@ -590,7 +605,17 @@ DM_DEV void attend_rows(const AttendArgs<T>& a, int bh, int q0, T* lds) {
   load_q_frags<T, DH>(a.qr + (lrow0 + qrow) * DH, qrow < g.c, qf);
   FlashState<T, DH> st;
   flash_init(st);
-  if (a.nsplit == 1) {
+  // the cell's last committed keys (first sweep), loaded with the intra rows where the registers
+  // allow (at most 8 16-byte vectors of each per thread), else right before their use
+  [[maybe_unused]] const bool prev = !V_STAGED && !a.merged_in && a.prev_lo < g.pos0;
+  [[maybe_unused]] KVRegs<T, DH, 64 * NW> pk;
+  [[maybe_unused]] const long pb = (long)bh * g.cache_T * DH + (long)a.prev_lo * DH;
+  constexpr bool PREV_EARLY = KVRegs<T, DH, 64 * NW>::NV <= 8;
+  if constexpr (!V_STAGED && PREV_EARLY) {
+    if (prev) load_kv<T, DH, 64 * NW>(a.Kc + pb, a.Vc + pb, DH, g.pos0 - a.prev_lo, pk);
+  }
+  bool store_merged = false;
+  if (a.merged_in) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int q = wq + 4 * g4 + r;
@@ -602,10 +627,9 @@ DM_DEV void attend_rows(const AttendArgs<T>& a, int bh, int q0, T* lds) {
         for (int dt = 0; dt < C::NDT; ++dt) st.O[dt][r] = a.A[o * DH + col + 16 * dt];
       }
     }
-  } else if (a.nsplit > 1) {
+  } else if (a.nsplit > 0) {
     // merge the split partials: per row, every split's loads are issued before the
-    // first use (indices clamped in bounds, splits >= nsplit masked); the merged state
-    // is stored only after all rows are merged
+    // first use (indices clamped in bounds, splits >= nsplit masked)
     constexpr int MS = COMM_MAX_SPLITS;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {   // one row at a time (scheduling barrier below):
@@ -634,22 +658,38 @@ DM_DEV void attend_rows(const AttendArgs<T>& a, int bh, int q0, T* lds) {
         for (int dt = 0; dt < C::NDT; ++dt) st.O[dt][r] += w * as[s][dt];
       }
       st.m[r] = M;
-      st.z[r] = z;   // the row total on every lane until stored below
+      st.z[r] = (col == 0) ? z : 0.f;   // per-lane partial sums
       __builtin_amdgcn_sched_barrier(0);
     }
+    store_merged = true;
+  }
+  if constexpr (!V_STAGED) {
+    if (prev) {
+      // keys [prev_lo, pos0), inside each row's window: lo0 + q0 + q for block row q
+      const int lo0 = g.window > 0 ? g.pos0 - g.window + 1 : NO_WINDOW_LO;
+      if constexpr (!PREV_EARLY) load_kv<T, DH, 64 * NW>(a.Kc + pb, a.Vc + pb, DH, g.pos0 - a.prev_lo, pk);
+      store_kv<T, DH, 64 * NW>(pk, Ks, Vs);
+      __syncthreads();
+      flash_tile<T, DH>(qf, Ks, Vs, Ps + wave * 16 * C::LDP, a.scale,
+                        KeyWindow{g.pos0 - a.prev_lo, a.prev_lo, lo0 == NO_WINDOW_LO ? lo0 : lo0 + q0}, st);
+      __syncthreads();   // Ks / Vs are free for the intra rows
+      store_merged = true;
+    }
+  }
+  if (store_merged) {   // the merged committed state, read by the cell's later sweeps
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int q = wq + 4 * g4 + r;
+      const float zt = group16_sum(st.z[r]);
       if (q < g.c) {
         const long o = (long)bh * g.c + q;
 #pragma unroll
         for (int dt = 0; dt < C::NDT; ++dt) a.A[o * DH + col + 16 * dt] = st.O[dt][r];
         if (col == 0) {
-          a.Z[o] = st.z[r];
+          a.Z[o] = zt;
           a.Mx[o] = st.m[r];
         }
       }
-      st.z[r] = (col == 0) ? st.z[r] : 0.f;   // per-lane partial sums from here on
     }
   }
   // raw self column inputs, loaded before the barriers below: partial <q_r, k_self_r>
@@ -1181,18 +1221,23 @@ template <typename T, int DH> struct EpiSweep2Head {
   }
 };
 
+// LDS of the fused GEMM 2 + attention block: the GEMM's stages, then the attention's tiles (one
+// LDS object for both: a second __shared__ array makes the compiler guard every read of the
+// direct-to-LDS stages with a full vmcnt wait, serialising the k-loop)
+template <typename T, int DH> struct Sweep2AttendLds {
+  static constexpr int D = sizeof(T) == 2 ? -3 : 4;
+  static constexpr int GEMM = (gemm_lds_bytes<T, 64, DH, D, false>() + 15) / 16 * 16;
+  static constexpr int BYTES = GEMM + AttnCfg<T, DH>::LDS_ELEMS * (int)sizeof(T);
+};
+
 template <typename T, int DH>
-DM_DEV void sweep2_attend_block(const SrcRows<T>& sa, const SrcRows<T>& sb, int K, const EpiSweep2Head<T, DH>& epi,
-                                const AttendArgs<T>& aa, int hh, int b) {
-  constexpr int D = sizeof(T) == 2 ? -3 : 4;
+DM_DEV void sweep2_attend_block_at(const SrcRows<T>& sa, const SrcRows<T>& sb, int K, const EpiSweep2Head<T, DH>& epi,
+                                   const AttendArgs<T>& aa, int hh, int b, char* smem) {
+  constexpr int D = Sweep2AttendLds<T, DH>::D;
   constexpr int LDT = DH + 4;
   using WT = WaveTile<64, DH, 2, 2>;
   using C = AttnCfg<T, DH>;
-  // one LDS object for both (a second __shared__ array makes the compiler guard every read of
-  // the direct-to-LDS stages with a full vmcnt wait, serialising the k-loop)
-  constexpr int GEMM_LDS = (gemm_lds_bytes<T, 64, DH, D, false>() + 15) / 16 * 16;
-  __shared__ __attribute__((aligned(1024))) char smem[GEMM_LDS + C::LDS_ELEMS * sizeof(T)];
-  T* alds = reinterpret_cast<T*>(smem + GEMM_LDS);
+  T* alds = reinterpret_cast<T*>(smem + Sweep2AttendLds<T, DH>::GEMM);
   static_assert(64 * LDT * 4 <= gemm_stage_bytes<T, 64, DH, D>(), "output tile fits the stages");
   const int m0 = b * 64, n0 = hh * DH;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1227,11 +1272,38 @@ DM_DEV void sweep2_attend_block(const SrcRows<T>& sa, const SrcRows<T>& sb, int 
 }
 
 template <typename T, int DH>
+DM_DEV void sweep2_attend_block(const SrcRows<T>& sa, const SrcRows<T>& sb, int K, const EpiSweep2Head<T, DH>& epi,
+                                const AttendArgs<T>& aa, int hh, int b) {
+  __shared__ __attribute__((aligned(1024))) char smem[Sweep2AttendLds<T, DH>::BYTES];
+  sweep2_attend_block_at<T, DH>(sa, sb, K, epi, aa, hh, b, smem);
+}
+
+template <typename T, int DH>
 static __global__ __launch_bounds__(256) void k_sweep2_attend(SrcRows<T> sa, SrcRows<T> sb, int K,
                                                               EpiSweep2Head<T, DH> epi, AttendArgs<T> aa,
                                                               uint64_t* prof_ts) {
   const uint64_t t0 = prof_begin(prof_ts);
   sweep2_attend_block<T, DH>(sa, sb, K, epi, aa, blockIdx.x, blockIdx.y);
+  prof_end(prof_ts, t0);
+}
+
+// The same launch with the next cell's committed-prefix split partials s0 .. (ca) as extra blocks
+// after the (h, rows / 64) fused ones: that launch holds one block per (b, h) and leaves CUs free,
+// and those partials read only rows that are final before this cell began.
+template <typename T, int DH>
+static __global__ __launch_bounds__(256) void k_sweep2_attend_comm(SrcRows<T> sa, SrcRows<T> sb, int K,
+                                                                   EpiSweep2Head<T, DH> epi, AttendArgs<T> aa,
+                                                                   CommArgs<T> ca, int nfused, int s0,
+                                                                   uint64_t* prof_ts) {
+  const uint64_t t0 = prof_begin(prof_ts);
+  __shared__ __attribute__((aligned(1024))) char smem[Sweep2AttendLds<T, DH>::BYTES];
+  const int L = blockIdx.x;
+  if (L < nfused) {
+    sweep2_attend_block_at<T, DH>(sa, sb, K, epi, aa, L % aa.g.h, L / aa.g.h, smem);
+  } else {
+    const int BH = ca.g.B * ca.g.h, j = L - nfused;
+    comm_partial_block_at<T, DH>(ca, s0 + j / BH, j % BH, reinterpret_cast<T*>(smem + Sweep2AttendLds<T, DH>::GEMM));
+  }
   prof_end(prof_ts, t0);
 }
 

@@ -274,39 +274,39 @@ int dm_layer_fwd(const dm_config* c, const dm_packed* w, const void* x, void* y,
   }
   ProfScope whole(PROF_LAYER, S(stream));
   if ((rc = dm_layer_proj(c, w, x, cos, sin, L, stream))) return rc;
-  if (tape == nullptr) {
+  DM_REQUIRE(K_cache && V_cache && aligned16(K_cache) && aligned16(V_cache), DM_ERR_INVALID,
+             "K/V cache must be non-null and 16-byte aligned");
+  const CellWs need = carve_cell(c, cache_T, nullptr);
+  DM_REQUIRE(workspace && workspace_bytes >= need.bytes, DM_ERR_WORKSPACE, "workspace %zu < %zu bytes",
+             workspace_bytes, need.bytes);
+  const CellWs ws = carve_cell(c, cache_T, workspace);
+  auto run = [&](auto tag) {
+    using T = decltype(tag);
+    std::vector<size_t> off;
+    if (tape != nullptr) off = tape_offsets<T>(c, sched, n_cells);
+    // each cell computes the next one's committed-prefix split partials where it can (run_cell)
+    int handed = -1;
     for (int i = 0; i < n_cells; ++i) {
-      dm_cell_args a{sched[3 * i], sched[3 * i + 1], sched[3 * i + 2], cache_T, K_cache, V_cache, ocat,
-                     nullptr, workspace, workspace_bytes};
-      if ((rc = dm_cell_fwd(c, w, L, cos, sin, &a, stream))) return rc;
-    }
-  } else {
-    DM_REQUIRE(K_cache && V_cache && aligned16(K_cache) && aligned16(V_cache), DM_ERR_INVALID,
-               "K/V cache must be non-null and 16-byte aligned");
-    const CellWs need = carve_cell(c, cache_T, nullptr);
-    DM_REQUIRE(workspace && workspace_bytes >= need.bytes, DM_ERR_WORKSPACE, "workspace %zu < %zu bytes",
-               workspace_bytes, need.bytes);
-    const CellWs ws = carve_cell(c, cache_T, workspace);
-    auto run = [&](auto tag) {
-      using T = decltype(tag);
-      const std::vector<size_t> off = tape_offsets<T>(c, sched, n_cells);
-      for (int i = 0; i < n_cells; ++i) {
-        const int pos0 = sched[3 * i], cc = sched[3 * i + 1], K = sched[3 * i + 2];
+      const int pos0 = sched[3 * i], cc = sched[3 * i + 1], K = sched[3 * i + 2];
+      CellSave<T> sv{};
+      CellWs cws = ws;
+      if (tape != nullptr) {
         Carver cv(static_cast<char*>(tape) + off[i]);
-        CellSave<T> sv = carve_save<T>(c, (size_t)c->B * cc, K, true, pos0 > 0, cv);
+        sv = carve_save<T>(c, (size_t)c->B * cc, K, true, pos0 > 0, cv);
         if (c->ctx_mod != DM_CTX_LINEAR)
           sv.vin = reinterpret_cast<T*>(static_cast<char*>(tape) + off[n_cells]) +
                    vin_row(c, sched, n_cells, i) * c->d;
-        CellWs cws = ws;
         if (sv.Mx) cws.M = sv.Mx;   // the committed row max is part of the saved state
-        run_cell_dispatch<T>(c, w, L, cos, sin, pos0, cc, K, pos0, L->T, K_cache, V_cache, cache_T, ocat,
-                             nullptr, cws, &sv, S(stream));
       }
-    };
-    if (c->dtype == DM_BF16) run(bf16{});
-    else run(float{});
-    DM_HIP(hipGetLastError());
-  }
+      const bool more = i + 1 < n_cells;
+      handed = run_cell_dispatch<T>(c, w, L, cos, sin, pos0, cc, K, pos0, L->T, K_cache, V_cache, cache_T, ocat,
+                                    nullptr, cws, tape != nullptr ? &sv : nullptr, S(stream), CellRows<T>{}, handed,
+                                    more ? sched[3 * (i + 1)] : -1, more ? sched[3 * (i + 1) + 1] : 0);
+    }
+  };
+  if (c->dtype == DM_BF16) run(bf16{});
+  else run(float{});
+  DM_HIP(hipGetLastError());
   return dm_linear(c->dtype, ocat, w->wo, (c->flags & DM_FLAG_NO_RESIDUAL) ? nullptr : x, y, c->B * L->T,
                    c->d, c->d, stream);
 }
