@@ -361,11 +361,16 @@ int run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, con
   // chunks) when B*h gives that kernel enough blocks, or when forced by the flags
   const bool fuse = c->ctx_mod != DM_CTX_LINEAR && cc == CMAX && !(c->flags & DM_FLAG_UNFUSED_ATTEND) &&
                     ((c->flags & DM_FLAG_FUSED_ATTEND) || BH >= 128);
-  // the next cell's split partials, spread over this cell's fused launches (sweeps 0 .. K-2); they
-  // read only keys before this cell (the next cell's last 64 committed keys are its own attention's)
+  // the next cell's split partials, spread over this cell's fused GEMM 2 + attention launches
+  // (sweeps 0 .. K-2: one block per (b, h), CUs to spare; as extra blocks of the plain 64 x 32 GEMM 2
+  // launches, which fill the chip, they cost more than their own launch); they read only keys
+  // before this cell (the next cell's last 64 committed keys are its own attention's)
+  auto hosts = [&](int sw) { return fuse && sw < n_sweeps - 1; };
+  int n_hosts = 0;
+  for (int sw = 0; sw < n_sweeps; ++sw) n_hosts += hosts(sw) ? 1 : 0;
   AheadComm<T> ahead;
   int handed = -1;
-  if (next_pos0 >= 0 && fuse && n_sweeps >= 2 && launch_log() == nullptr) {
+  if (next_pos0 >= 0 && n_hosts > 0 && launch_log() == nullptr) {
     CellGeom gn = g;
     gn.pos0 = next_pos0;
     gn.c = next_cc;
@@ -381,9 +386,11 @@ int run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, con
     }
   }
   auto ahead_for = [&](int sw) -> const AheadComm<T>* {
-    if (handed <= 0) return nullptr;
-    ahead.s0 = handed * sw / (n_sweeps - 1);
-    ahead.ns = handed * (sw + 1) / (n_sweeps - 1) - ahead.s0;
+    if (handed <= 0 || !hosts(sw)) return nullptr;
+    int j = 0;   // this launch's index among the hosting ones
+    for (int u = 0; u < sw; ++u) j += hosts(u) ? 1 : 0;
+    ahead.s0 = handed * j / n_hosts;
+    ahead.ns = handed * (j + 1) / n_hosts - ahead.s0;
     return &ahead;
   };
   // intra rows read by sweep sw (= the rows written by sweep sw - 1)
@@ -432,7 +439,7 @@ int run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, con
     run_refine<T, DH>(c, w, g, N, o, ssq, kraw, vraw, (const T*)L->glogx, (const T*)L->sig, cos, sin, Kout, Vout,
                       out_stride, out_row0, vin, (T*)ws.gvu, sv ? sv->save1 + sw * NS * 4 * d : nullptr,
                       sv ? sv->save2 + sw * NS * d : nullptr, s, (fuse && !last) ? &next : nullptr, wide,
-                      (fuse && !last) ? ahead_for(sw) : nullptr);
+                      ahead_for(sw));
   }
   return handed;
 }

@@ -536,6 +536,7 @@ static __global__ __launch_bounds__(256) void k_comm_partial(CommArgs<T> a) {
   comm_partial_block<T, DH>(a, blockIdx.x, blockIdx.y);
 }
 
+
 template <typename T, int DH> struct CommBody {
   static constexpr int THREADS = 256;
   using Args = CommArgs<T>;
