@@ -717,6 +717,9 @@ template <typename T> struct AttnBwdArgs {
   // the intra rows are the raw rows, their grads go to dkself / dvraw.
   int fuse_refine;
   RefineBwdArgs<T> ref;
+  // the cell's last reverse sweep: G is complete after it; the query-major blocks also store it
+  // rounded to the storage dtype, the committed VJPs' MFMA operand (nullptr: other sweeps)
+  T* Gb = nullptr;
 };
 
 constexpr int ATTN_BWD_ROLES = 3;   // blocks per (b, h) of the attention VJP (grid x)
@@ -855,6 +858,7 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
 #pragma unroll
       for (int e = 0; e < EPT; ++e) gn[e] = (a.first ? 0.f : gold[e]) + alpha * dO[e];
       store_vec<float, EPT>(a.G + lr, gn);
+      if (a.Gb != nullptr) store_vec<T, EPT>(a.Gb + lr, gn);
       if (part == 0) {
         a.Dbar[lrow0 + i] = (a.first ? 0.f : dbold) + alpha * Dp;
         if (a.first) a.Mrow[lrow0 + i] = mx;
@@ -1085,7 +1089,8 @@ template <typename T> struct CommKeyArgs {
   int k0, kc;                                  // key cell: cache rows [k0, k0 + kc)
   int q_lo, q_hi;                              // query rows [q_lo, q_hi) of the layer buffers
   const T* qr; const T* Kc; const T* Vc;       // layer buffer q_r; the cache rows
-  const float* G; const float* Dbar; const float* Mx;   // per layer-buffer row (see AttnBwdArgs)
+  const T* Gb; const float* Dbar; const float* Mx;   // per layer-buffer row (see AttnBwdArgs; G complete,
+                                                     // in the storage dtype)
   float scale;
   float* dKp; float* dVp;                      // [COMM_NSQ, B*h, CMAX, DH] partial sums per split
   // grad-cache form (dKg != nullptr): block x takes keys [64 x, min(64 x + 64, k0)) of the committed
@@ -1143,8 +1148,7 @@ DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
   // query tile rows: q, G (raw words), row max, Dbar into registers, then LDS; rows
   // past the end are zeroed when staged (a select on a loaded value right after
   // its load would make the compiler wait for the load there)
-  constexpr int GW = EPT / 4;   // 16-byte words of a G row segment
-  uint4 qv[NW], gw[GW];
+  uint4 qv[NW], gw[NW];
   float mv, dv;
   bool tok = false;
   auto load_tile = [&](int t) {
@@ -1154,7 +1158,7 @@ DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
 #pragma unroll
     for (int w = 0; w < NW; ++w) qv[w] = *reinterpret_cast<const uint4*>(a.qr + r * DH + re0 + w * VT);
 #pragma unroll
-    for (int w = 0; w < GW; ++w) gw[w] = *reinterpret_cast<const uint4*>(a.G + r * DH + re0 + 4 * w);
+    for (int w = 0; w < NW; ++w) gw[w] = *reinterpret_cast<const uint4*>(a.Gb + r * DH + re0 + w * VT);
     mv = a.Mx[r];
     dv = a.Dbar[r];
   };
@@ -1168,12 +1172,8 @@ DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
     __syncthreads();   // the previous tile's readers are done (first pass: publishes K / V)
 #pragma unroll
     for (int w = 0; w < NW; ++w) *reinterpret_cast<uint4*>(Qs + ri * LDE + re0 + w * VT) = keep_if(qv[w], tok);
-    {
-      float gv[EPT];
 #pragma unroll
-      for (int w = 0; w < GW; ++w) unpack16<float>(keep_if(gw[w], tok), gv + 4 * w);
-      store_vec<T, EPT>(Gs + ri * LDE + re0, gv);
-    }
+    for (int w = 0; w < NW; ++w) *reinterpret_cast<uint4*>(Gs + ri * LDE + re0 + w * VT) = keep_if(gw[w], tok);
     if ((tid & 3) == 0) { sM[ri] = tok ? mv : 0.f; sD[ri] = tok ? dv : 0.f; }
     __syncthreads();
     if (t + nsq < ntile) load_tile(t + nsq);
@@ -1257,7 +1257,7 @@ template <typename T> struct CommQueryArgs {
   int B, h, Tbuf, cache_T, nrows;              // query rows [row0, nrows)
   const int* klim;                             // [Tbuf] committed prefix length of each row (0: none)
   const T* qr; const T* Kc; const T* Vc;
-  const float* G; const float* Dbar; const float* Mx;   // per layer-buffer row (see AttnBwdArgs)
+  const T* Gb; const float* Dbar; const float* Mx;   // per layer-buffer row (see CommKeyArgs)
   float scale;
   float* dq;                                   // [B*h, Tbuf, DH] (+=)
   int row0 = 0;                                // first query row (a multiple of 64 or one cell's start)
@@ -1296,18 +1296,17 @@ DM_DEV void comm_dq_body(const CommQueryArgs<T>& a) {
   {
     const bool ok = ri < nq;
     const long r = qrow0 + (ok ? ri : 0);
-    float gg[EPT];
-    load_vec<float, EPT>(a.G + r * DH + re0, gg);
+    uint4 gg[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) gg[w] = *reinterpret_cast<const uint4*>(a.Gb + r * DH + re0 + w * VT);
 #pragma unroll
     for (int w = 0; w < NW; ++w)
       *reinterpret_cast<uint4*>(Qs + ri * LDE + re0 + w * VT) =
           keep_if(*reinterpret_cast<const uint4*>(a.qr + r * DH + re0 + w * VT), ok);
     const int L = ok ? a.klim[i0 + ri] : 0;
-    if (L == 0) {   // no committed prefix (or past the end): contributes nothing
+    // no committed prefix (or past the end): contributes nothing
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) gg[e] = 0.f;
-    }
-    store_vec<T, EPT>(Gs + ri * LDE + re0, gg);
+    for (int w = 0; w < NW; ++w) *reinterpret_cast<uint4*>(Gs + ri * LDE + re0 + w * VT) = keep_if(gg[w], L != 0);
     if ((tid & 3) == 0) {
       sM[ri] = L > 0 ? a.Mx[r] : 0.f;
       sD[ri] = L > 0 ? a.Dbar[r] : 0.f;

@@ -28,6 +28,8 @@ template <typename T> struct BwdWs {
   float *du_part;                       // [DU_SPLIT, N, d] split-K slices of du
   // committed-prefix VJP: per-row state from the attention VJP, key-side partial sums
   float *Grow, *Drow, *Mrow;            // [B*h, T, dh], [B*h, T], [B*h, T]
+  T* Gb;                                // [B*h, T, dh] G in the storage dtype once complete (the
+                                        // committed VJPs' MFMA operand)
   float *sdss;                          // [B*h, T] the self column's dS summed over a cell's sweeps
   int* klim;                            // [T]
   float *dKp, *dVp;                     // [COMM_NSQ, B*h, CMAX, dh]
@@ -82,6 +84,7 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.rowdot = cv.take<float>(N * (d / DU_EPI_TN) * 4);
   w.du_part = cv.take<float>(DU_SPLIT * N * d * 4);
   w.Grow = cv.take<float>(BT * d * 4);
+  w.Gb = cv.take<T>(BT * d * e);
   w.Drow = cv.take<float>(BH * T_ * 4);
   w.Mrow = cv.take<float>(BH * T_ * 4);
   w.sdss = cv.take<float>(BH * T_ * 4);
@@ -338,7 +341,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
   long dn_stride, dn_psum;
   int dn_row0;
   if (gc.dK == nullptr) {
-    CommKeyArgs<T> ka{B, h, T_, cache_T, pos0, cc, pos0 + cc, t_end, qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow,
+    CommKeyArgs<T> ka{B, h, T_, cache_T, pos0, cc, pos0 + cc, t_end, qr, Kc, Vc, ws.Gb, ws.Drow, ws.Mrow,
                       scale, ws.dKp, ws.dVp};
     ka.window = c->local_window;
     if (launch_log() != nullptr)
@@ -444,6 +447,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
                         ws.cellrow, K, (int)coff, sw == K - 1 ? 1 : 0,
                         scale, inv_d, c->rms_eps, ws.dkself, ws.dvraw, ws.dq, ws.sdss, sw >= 1 ? 1 : 0,
                         sw >= 1 ? refine_args(sw - 1) : RefineBwdArgs<T>{}};
+      aa.Gb = sw == 0 ? ws.Gb : nullptr;
       if (launch_log() != nullptr)
         record_launch<AttnBwdBody<T, DH>>(dim3(ATTN_BWD_ROLES, BH), dim3(256), aa, (unsigned)lds_attn_bwd);
       else
@@ -470,11 +474,11 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
   // into the cache, query side into dq
   if (gc.dK != nullptr && pos0 > 0 && launch_log() != nullptr) launch_log()->unsupported = true;
   else if (gc.dK != nullptr && pos0 > 0) {
-    CommKeyArgs<T> ka{B, h, T_, cache_T, pos0, 0, pos0, pos0 + cc, qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow,
+    CommKeyArgs<T> ka{B, h, T_, cache_T, pos0, 0, pos0, pos0 + cc, qr, Kc, Vc, ws.Gb, ws.Drow, ws.Mrow,
                       scale, nullptr, nullptr, gc.dK, gc.dV};
     ka.window = c->local_window;
     hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(cdiv(pos0, 64), BH), dim3(256), lds_attn, s, ka);
-    CommQueryArgs<T> qa{B, h, T_, cache_T, pos0 + cc, ws.klim, qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow, scale, ws.dq,
+    CommQueryArgs<T> qa{B, h, T_, cache_T, pos0 + cc, ws.klim, qr, Kc, Vc, ws.Gb, ws.Drow, ws.Mrow, scale, ws.dq,
                         pos0};
     qa.window = c->local_window;
     hipLaunchKernelGGL((k_comm_dq<T, DH>), dim3(BH, cdiv(cc, 64)), dim3(256), lds_attn, s, qa);
@@ -532,7 +536,7 @@ void bwd_end(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T*
 
   // committed-prefix VJP, query side (layer path): every row with a committed prefix, into dq
   if (layer_path) {
-    CommQueryArgs<T> qa{B, h, T_, cache_T, t_end, ws.klim, qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow, scale, ws.dq};
+    CommQueryArgs<T> qa{B, h, T_, cache_T, t_end, ws.klim, qr, Kc, Vc, ws.Gb, ws.Drow, ws.Mrow, scale, ws.dq};
     qa.window = c->local_window;
     hipLaunchKernelGGL((k_comm_dq<T, DH>), dim3(BH, cdiv(t_end, 64)), dim3(256), lds_attn, s, qa);
   }
@@ -660,7 +664,7 @@ void record_bwd_chunk(const dm_config* c, const dm_stack_bwd_layer& ly, const fl
   // committed-prefix VJP, query side, of the cell's rows
   const size_t lds_attn = AttnBwdCfg<T, DH>::LDS_ELEMS * sizeof(T);
   const float scale = 1.0f / sqrtf((float)DH);
-  CommQueryArgs<T> qa{B, h, T_, cache_T, pos0 + cc, ws.klim, (const T*)L->qr, Kc, Vc, ws.Grow, ws.Drow, ws.Mrow,
+  CommQueryArgs<T> qa{B, h, T_, cache_T, pos0 + cc, ws.klim, (const T*)L->qr, Kc, Vc, ws.Gb, ws.Drow, ws.Mrow,
                       scale, ws.dq, pos0};
   qa.window = c->local_window;
   record_launch<CommDqBody<T, DH>>(dim3(BH, cdiv(cc, 64)), dim3(256), qa, (unsigned)lds_attn);
