@@ -1082,7 +1082,9 @@ static __global__ __launch_bounds__(256, DH == 64 ? 2 : 1) void k_attn_bwd(AttnB
 // later row, so the sum is complete and is written once); the query side runs
 // once per layer after every cell.
 // ---------------------------------------------------------------------------
-constexpr int COMM_NSQ = 4;   // query splits of the key side (partial slots summed by k_refine_bwd)
+// query splits of the key side (partial slots summed by k_refine_bwd): 8 when B*h leaves the 4-split
+// grid at one block per CU (64 heads: 256 blocks), else 4
+inline int comm_nsq(int BH) { return BH <= 64 ? 8 : 4; }
 
 template <typename T> struct CommKeyArgs {
   int B, h, Tbuf, cache_T;
@@ -1092,12 +1094,13 @@ template <typename T> struct CommKeyArgs {
   const T* Gb; const float* Dbar; const float* Mx;   // per layer-buffer row (see AttnBwdArgs; G complete,
                                                      // in the storage dtype)
   float scale;
-  float* dKp; float* dVp;                      // [COMM_NSQ, B*h, CMAX, DH] partial sums per split
+  float* dKp; float* dVp;                      // [nsq, B*h, CMAX, DH] partial sums per split
   // grad-cache form (dKg != nullptr): block x takes keys [64 x, min(64 x + 64, k0)) of the committed
   // prefix [0, k0) against every query row [q_lo, q_hi) and ADDS into the fp32 grad cache
   // dKg / dVg [B*h, cache_T, DH] (engines/wavescan/engine/backward.py:116-119)
   float* dKg = nullptr; float* dVg = nullptr;
   int window = 0;   // local_window W: query row i reads keys >= i - W + 1 (0: none)
+  int nsq = 4;      // query splits (comm_nsq)
 };
 
 // One block per (query split s, b, h): the split's 64-row query tiles s, s + NSQ, ..;
@@ -1117,7 +1120,7 @@ DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
 
   const int bh = blockIdx.y;
   const bool gcache = a.dKg != nullptr;   // uniform
-  const int s = gcache ? 0 : (int)blockIdx.x, nsq = gcache ? 1 : COMM_NSQ;
+  const int s = gcache ? 0 : (int)blockIdx.x, nsq = gcache ? 1 : a.nsq;
   const int k0 = gcache ? 64 * (int)blockIdx.x : a.k0;
   const int kc = gcache ? min(64, a.k0 - k0) : a.kc;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

@@ -32,7 +32,7 @@ template <typename T> struct BwdWs {
                                         // committed VJPs' MFMA operand)
   float *sdss;                          // [B*h, T] the self column's dS summed over a cell's sweeps
   int* klim;                            // [T]
-  float *dKp, *dVp;                     // [COMM_NSQ, B*h, CMAX, dh]
+  float *dKp, *dVp;                     // [comm_nsq(B*h), B*h, CMAX, dh]
   // weight grads of the sweeps, one GEMM per layer: the cells' transposed operands
   // stacked row-major, [Rp, 4d | d] with Rp >= sum over cells of K*B*c (rounded to 64);
   // a cell's sweeps write their dctx / dv_ctx rows in place, u and v_in are added per cell
@@ -89,8 +89,8 @@ BwdWs<T> carve_bwd(const dm_config* c, int T_, int cache_T, int kmax, void* base
   w.Mrow = cv.take<float>(BH * T_ * 4);
   w.sdss = cv.take<float>(BH * T_ * 4);
   w.klim = cv.take<int>(T_ * 4);
-  w.dKp = cv.take<float>(COMM_NSQ * BH * CMAX * dh * 4);
-  w.dVp = cv.take<float>(COMM_NSQ * BH * CMAX * dh * 4);
+  w.dKp = cv.take<float>(comm_nsq((int)BH) * BH * CMAX * dh * 4);
+  w.dVp = cv.take<float>(comm_nsq((int)BH) * BH * CMAX * dh * 4);
   w.Rp = (long)cdiv((long)kmax * B * T_, 64) * 64;
   w.dctxL = cv.take<T>(w.Rp * 4 * d * e);
   w.uL = cv.take<T>(w.Rp * d * e);
@@ -334,7 +334,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
     Mx = pos0 > 0 ? ws.fws.M : nullptr;
   }
   // grads of the cell's final rows: layer path, the committed-prefix attention of every later
-  // row (their G / Dbar / row max are in place: those cells are done), in COMM_NSQ partial slots;
+  // row (their G / Dbar / row max are in place: those cells are done), in comm_nsq partial slots;
   // grad-cache path, the cache rows [pos0, pos0 + cc)
   const float* dKn;
   const float* dVn;
@@ -344,10 +344,11 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
     CommKeyArgs<T> ka{B, h, T_, cache_T, pos0, cc, pos0 + cc, t_end, qr, Kc, Vc, ws.Gb, ws.Drow, ws.Mrow,
                       scale, ws.dKp, ws.dVp};
     ka.window = c->local_window;
+    ka.nsq = comm_nsq(BH);
     if (launch_log() != nullptr)
-      record_launch<CommDkvBody<T, DH>>(dim3(COMM_NSQ, BH), dim3(256), ka, (unsigned)lds_attn);
+      record_launch<CommDkvBody<T, DH>>(dim3(ka.nsq, BH), dim3(256), ka, (unsigned)lds_attn);
     else
-      hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(COMM_NSQ, BH), dim3(256), lds_attn, s, ka);
+      hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(ka.nsq, BH), dim3(256), lds_attn, s, ka);
     dKn = ws.dKp; dVn = ws.dVp; dn_stride = (long)CMAX * DH; dn_row0 = 0; dn_psum = (long)BH * CMAX * DH;
   } else {
     dKn = gc.dK; dVn = gc.dV; dn_stride = (long)cache_T * DH; dn_row0 = pos0; dn_psum = 0;
@@ -369,10 +370,12 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
       const RefineBwdArgs<T> ra = refine_args(sw);
       const dim3 rgrid(cdiv((long)N * d / 8, 256));
       if (launch_log() != nullptr) {
-        if (gc.dK == nullptr) record_launch<RefineBwdBody<T, DH, COMM_NSQ>>(rgrid, dim3(256), ra);
+        if (gc.dK == nullptr && comm_nsq(BH) == 8) record_launch<RefineBwdBody<T, DH, 8>>(rgrid, dim3(256), ra);
+        else if (gc.dK == nullptr) record_launch<RefineBwdBody<T, DH, 4>>(rgrid, dim3(256), ra);
         else launch_log()->unsupported = true;
       } else if (gc.dK == nullptr) {
-        hipLaunchKernelGGL((k_refine_bwd<T, DH, COMM_NSQ>), rgrid, dim3(256), 0, s, ra);
+        if (comm_nsq(BH) == 8) hipLaunchKernelGGL((k_refine_bwd<T, DH, 8>), rgrid, dim3(256), 0, s, ra);
+        else hipLaunchKernelGGL((k_refine_bwd<T, DH, 4>), rgrid, dim3(256), 0, s, ra);
       } else {
         hipLaunchKernelGGL((k_refine_bwd<T, DH, 1>), rgrid, dim3(256), 0, s, ra);
       }
