@@ -737,8 +737,9 @@ template <typename T, int DH> struct AttnBwdCfg {
   static constexpr size_t BWD_LDS_BYTES = (size_t)LDS_ELEMS * sizeof(T) + (PD_LDS ? PD_BYTES : 0);
 };
 
+// L: the block's linear id in its grid of ATTN_BWD_ROLES x BH blocks
 template <typename T, int DH>
-DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
+DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a, int L, int nbh) {
   using C = AttnBwdCfg<T, DH>;
   constexpr int LDE = C::LDE, LDI = C::LDI, NDT = DH / 16;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
@@ -758,8 +759,7 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
   // turn.
   int role, bh;
   {
-    const int L = (int)blockIdx.x + ATTN_BWD_ROLES * (int)blockIdx.y;
-    const int full = ((int)gridDim.y / 8) * 8 * ATTN_BWD_ROLES;
+    const int full = (nbh / 8) * 8 * ATTN_BWD_ROLES;
     if (L < full) {
       role = (L % (8 * ATTN_BWD_ROLES)) >> 3;
       bh = 8 * (L / (8 * ATTN_BWD_ROLES)) + (L & 7);
@@ -1069,7 +1069,7 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a) {
 // head_dim 64: at most 256 registers a lane, two blocks per CU
 template <typename T, int DH>
 static __global__ __launch_bounds__(256, DH == 64 ? 2 : 1) void k_attn_bwd(AttnBwdArgs<T> a) {
-  attn_bwd_body<T, DH>(a);
+  attn_bwd_body<T, DH>(a, (int)blockIdx.x + ATTN_BWD_ROLES * (int)blockIdx.y, (int)gridDim.y);
 }
 
 // ---------------------------------------------------------------------------
@@ -1101,13 +1101,17 @@ template <typename T> struct CommKeyArgs {
   float* dKg = nullptr; float* dVg = nullptr;
   int window = 0;   // local_window W: query row i reads keys >= i - W + 1 (0: none)
   int nsq = 4;      // query splits (comm_nsq)
+  int s0 = 0;       // split of block x = 0 (a launch may cover some splits only)
 };
 
-// One block per (query split s, b, h): the split's 64-row query tiles s, s + NSQ, ..;
-// wave w owns keys 16w .. 16w + 15 of the cell (key-major products, as in k_attn_bwd).
-// In the grad-cache form one block per (64-key tile, b, h) takes every query tile.
+// One block per (query split s, b, h). Split 0 takes the first 64-row query tile (the rows right
+// after the key cell: the last to be complete in the reverse scan), split s >= 1 the tiles
+// s, s + (nsq - 1), .. (the rest, complete a cell earlier): a layer's backward can compute those
+// while the cell before is still running. Wave w owns keys 16w .. 16w + 15 of the cell
+// (key-major products, as in k_attn_bwd). In the grad-cache form one block per (64-key tile,
+// b, h) takes every query tile.
 template <typename T, int DH>
-DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
+DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a, int bx, int bh) {
   using C = AttnBwdCfg<T, DH>;
   constexpr int LDE = C::LDE, LDI = C::LDI, NDT = DH / 16;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
@@ -1118,10 +1122,9 @@ DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
   T* Wst = Gs + 64 * LDE;
   __shared__ float sM[64], sD[64];
 
-  const int bh = blockIdx.y;
   const bool gcache = a.dKg != nullptr;   // uniform
-  const int s = gcache ? 0 : (int)blockIdx.x, nsq = gcache ? 1 : a.nsq;
-  const int k0 = gcache ? 64 * (int)blockIdx.x : a.k0;
+  const int s = gcache ? 0 : a.s0 + bx;
+  const int k0 = gcache ? 64 * bx : a.k0;
   const int kc = gcache ? min(64, a.k0 - k0) : a.kc;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g4 = lane >> 4, lc = lane & 15;
@@ -1134,6 +1137,7 @@ DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
   // with a window, query rows past k0 + kc + W - 2 see none of these keys
   const int q_hi = a.window > 0 ? max(a.q_lo, min(a.q_hi, k0 + kc + a.window - 1)) : a.q_hi;
   const int ntile = (q_hi - a.q_lo + 63) / 64;
+  const int step = gcache ? 1 : (s == 0 ? ntile : a.nsq - 1);   // query tiles of this block: s, s + step, ..
   const int wlim = a.window > 0 ? a.window - 1 : (1 << 30);   // largest query - key distance read
 
   // the cell's keys and values, row-wise (A operands of the key-major products)
@@ -1169,7 +1173,7 @@ DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
 #pragma unroll
   for (int t = 0; t < NDT; ++t) { dK[t] = zero4(); dV[t] = zero4(); }
   if (s < ntile) load_tile(s);
-  for (int t = s; t < ntile; t += nsq) {
+  for (int t = s; t < ntile; t += step) {
     const int nq = min(64, q_hi - (a.q_lo + 64 * t));
     const int dqk = a.q_lo + 64 * t - k0;   // query row i - key row j = dqk + i - j
     __syncthreads();   // the previous tile's readers are done (first pass: publishes K / V)
@@ -1179,7 +1183,7 @@ DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
     for (int w = 0; w < NW; ++w) *reinterpret_cast<uint4*>(Gs + ri * LDE + re0 + w * VT) = keep_if(gw[w], tok);
     if ((tid & 3) == 0) { sM[ri] = tok ? mv : 0.f; sD[ri] = tok ? dv : 0.f; }
     __syncthreads();
-    if (t + nsq < ntile) load_tile(t + nsq);
+    if (t + step < ntile) load_tile(t + step);
     // key-major: E^T, dS^T (rows j = 16 wave + .., columns i = queries) -> dV += E^T G, dK += dS^T Q
     floatx4 St[4], dPt[4];
 #pragma unroll
@@ -1253,7 +1257,17 @@ DM_DEV void comm_dkv_body(const CommKeyArgs<T>& a) {
 
 template <typename T, int DH>
 static __global__ __launch_bounds__(256) void k_comm_dkv(CommKeyArgs<T> a) {
-  comm_dkv_body<T, DH>(a);
+  comm_dkv_body<T, DH>(a, blockIdx.x, blockIdx.y);
+}
+
+// The attention VJP launch (ATTN_BWD_ROLES x nbh blocks) with some key-side committed-VJP splits
+// of the cell before this one as extra blocks (ka.s0 .., nbh blocks each; one dynamic LDS object)
+template <typename T, int DH>
+static __global__ __launch_bounds__(256, DH == 64 ? 2 : 1) void k_attn_bwd_dkv(AttnBwdArgs<T> a, CommKeyArgs<T> ka,
+                                                                             int nbh) {
+  const int L = blockIdx.x, na = ATTN_BWD_ROLES * nbh;
+  if (L < na) attn_bwd_body<T, DH>(a, L, nbh);
+  else comm_dkv_body<T, DH>(ka, (L - na) / nbh, (L - na) % nbh);
 }
 
 template <typename T> struct CommQueryArgs {
@@ -1844,12 +1858,14 @@ template <typename T, int DH> struct AttnBwdBody {
   static constexpr int THREADS = 256;
   static constexpr int MIN_WAVES = DH == 64 ? 2 : 1;
   using Args = AttnBwdArgs<T>;
-  static DM_DEV void run(const Args& a, int, int) { attn_bwd_body<T, DH>(a); }
+  static DM_DEV void run(const Args& a, int bx, int by) {
+    attn_bwd_body<T, DH>(a, bx + ATTN_BWD_ROLES * by, (int)gridDim.y);
+  }
 };
 template <typename T, int DH> struct CommDkvBody {
   static constexpr int THREADS = 256;
   using Args = CommKeyArgs<T>;
-  static DM_DEV void run(const Args& a, int, int) { comm_dkv_body<T, DH>(a); }
+  static DM_DEV void run(const Args& a, int bx, int by) { comm_dkv_body<T, DH>(a, bx, by); }
 };
 template <typename T, int DH> struct CommDqBody {
   static constexpr int THREADS = 256;

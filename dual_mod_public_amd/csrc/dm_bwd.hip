@@ -292,11 +292,14 @@ T* stacked_vin(const char* tape, const size_t* tape_off, int n_cells, const BwdW
 }
 
 // rms: tape cells' o rows to normalise after the cell loop (nullptr: now)
+// far_done: the previous call (cell ci + 1 of a layer's reverse scan) computed this cell's
+// key-side committed-VJP splits 1 .. nsq-1 inside its attention-VJP launches, so only split 0
+// is left. Returns whether this call did the same for cell ci - 1.
 template <typename T, int DH>
-void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const float* sin, const dm_layer_bufs* L,
+bool bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const float* sin, const dm_layer_bufs* L,
               const int32_t* sched, int n_cells, int ci, const T* Kc, const T* Vc, int cache_T, const char* tape,
               const size_t* tape_off, const GradCache& gc, const BwdWs<T>& ws, std::vector<RmsSeg>* rms,
-              hipStream_t s) {
+              hipStream_t s, bool far_done = false) {
   const int B = c->B, d = c->d, h = c->h, T_ = L->T, BH = B * h;
   const bool mult = c->ctx_mod != DM_CTX_LINEAR;
   const float scale = 1.0f / sqrtf((float)DH);
@@ -345,13 +348,29 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
                       scale, ws.dKp, ws.dVp};
     ka.window = c->local_window;
     ka.nsq = comm_nsq(BH);
+    const int nlaunch = far_done ? 1 : ka.nsq;
     if (launch_log() != nullptr)
-      record_launch<CommDkvBody<T, DH>>(dim3(ka.nsq, BH), dim3(256), ka, (unsigned)lds_attn);
+      record_launch<CommDkvBody<T, DH>>(dim3(nlaunch, BH), dim3(256), ka, (unsigned)lds_attn);
     else
-      hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(ka.nsq, BH), dim3(256), lds_attn, s, ka);
+      hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(nlaunch, BH), dim3(256), lds_attn, s, ka);
     dKn = ws.dKp; dVn = ws.dVp; dn_stride = (long)CMAX * DH; dn_row0 = 0; dn_psum = (long)BH * CMAX * DH;
   } else {
     dKn = gc.dK; dVn = gc.dV; dn_stride = (long)cache_T * DH; dn_row0 = pos0; dn_psum = 0;
+  }
+  // The cell before this one (ci - 1): its key-side committed-VJP splits 1 .. nsq-1 read query rows
+  // from pos0 + 64 on, all of them complete (the cells after this one; this cell's rows are its
+  // split 0), so this cell's attention-VJP launches take them as extra blocks (head_dim 64: those
+  // launches leave a third of the CUs' block slots free; in a layer's own launches only).
+  CommKeyArgs<T> kprev{};
+  int host_splits = 0;
+  if constexpr (DH == 64) {
+    if (gc.dK == nullptr && launch_log() == nullptr && ci > 0 && t_end > pos0 + 64) {
+      kprev = CommKeyArgs<T>{B, h, T_, cache_T, sched[3 * (ci - 1)], sched[3 * (ci - 1) + 1], pos0, t_end, qr, Kc, Vc,
+                             ws.Gb, ws.Drow, ws.Mrow, scale, ws.dKp, ws.dVp};
+      kprev.window = c->local_window;
+      kprev.nsq = comm_nsq(BH);
+      host_splits = kprev.nsq - 1;
+    }
   }
   // this cell's rows of the stacked weight-grad operands
   T* dctx = ws.dctxL + coff * 4 * d;
@@ -451,10 +470,17 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
                         scale, inv_d, c->rms_eps, ws.dkself, ws.dvraw, ws.dq, ws.sdss, sw >= 1 ? 1 : 0,
                         sw >= 1 ? refine_args(sw - 1) : RefineBwdArgs<T>{}};
       aa.Gb = sw == 0 ? ws.Gb : nullptr;
-      if (launch_log() != nullptr)
+      // this launch's share of the cell before's hosted splits (launch j = K - 1 - sw of K)
+      const int j = K - 1 - sw, h0 = 1 + host_splits * j / K, h1 = 1 + host_splits * (j + 1) / K;
+      if (launch_log() != nullptr) {
         record_launch<AttnBwdBody<T, DH>>(dim3(ATTN_BWD_ROLES, BH), dim3(256), aa, (unsigned)lds_attn_bwd);
-      else
+      } else if (h1 > h0) {
+        kprev.s0 = h0;
+        hipLaunchKernelGGL((k_attn_bwd_dkv<T, DH>), dim3((ATTN_BWD_ROLES + h1 - h0) * BH), dim3(256), lds_attn_bwd, s,
+                           aa, kprev, BH);
+      } else {
         hipLaunchKernelGGL((k_attn_bwd<T, DH>), dim3(ATTN_BWD_ROLES, BH), dim3(256), lds_attn_bwd, s, aa);
+      }
     }
   }
   // the other operand of dW_sweep = dctx^T u: this cell's K*N rows of u = RMSNorm(o)
@@ -486,6 +512,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
     qa.window = c->local_window;
     hipLaunchKernelGGL((k_comm_dq<T, DH>), dim3(BH, cdiv(cc, 64)), dim3(256), lds_attn, s, qa);
   }
+  return host_splits > 0;
 }
 
 template <typename T, int DH>
@@ -801,9 +828,10 @@ int bwd_dispatch(const dm_config* c, const dm_packed* w, const BwdCall& a, hipSt
     if (a.part == BWD_LAYER) {
       ProfScope whole(PROF_BWD, s);
       bwd_begin<T, DH>(c, w, (const T*)a.dy, (const T*)a.ocat, a.L->T, a.g, ws, s);
+      bool far_done = false;   // each cell's far committed-VJP splits ride in the cell after's launches
       for (int ci = a.n_cells - 1; ci >= 0; --ci)
-        bwd_cell<T, DH>(c, w, a.cos, a.sin, a.L, a.sched, a.n_cells, ci, Kc, Vc, a.cache_T, tape, to, GradCache{}, ws,
-                        &rms, s);
+        far_done = bwd_cell<T, DH>(c, w, a.cos, a.sin, a.L, a.sched, a.n_cells, ci, Kc, Vc, a.cache_T, tape, to,
+                                   GradCache{}, ws, &rms, s, far_done);
       bwd_end<T, DH>(c, w, (const T*)a.x, (const T*)a.dy, (T*)a.dx, a.cos, a.sin, a.L, a.sched, a.n_cells, Kc, Vc,
                      a.cache_T, tape, to, true, rms, a.g, ws, s);
     } else if (a.part == BWD_BEGIN) {
