@@ -292,14 +292,21 @@ T* stacked_vin(const char* tape, const size_t* tape_off, int n_cells, const BwdW
 }
 
 // rms: tape cells' o rows to normalise after the cell loop (nullptr: now)
-// far_done: the previous call (cell ci + 1 of a layer's reverse scan) computed this cell's
-// key-side committed-VJP splits 1 .. nsq-1 inside its attention-VJP launches, so only split 0
-// is left. Returns whether this call did the same for cell ci - 1.
+// What one call of a layer's reverse scan leaves for the next (cell ci - 1): far_done, that cell's
+// key-side committed-VJP splits 1 .. nsq-1 were computed inside this call's attention-VJP launches
+// (only split 0 is left); comm_nsplit >= 0, its exact recompute's committed-prefix split partials
+// were computed inside this call's recompute (run_cell's handoff), that many.
+struct CellHandoff {
+  bool far_done = false;
+  int comm_nsplit = -1;
+};
+
 template <typename T, int DH>
-bool bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const float* sin, const dm_layer_bufs* L,
+void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const float* sin, const dm_layer_bufs* L,
               const int32_t* sched, int n_cells, int ci, const T* Kc, const T* Vc, int cache_T, const char* tape,
               const size_t* tape_off, const GradCache& gc, const BwdWs<T>& ws, std::vector<RmsSeg>* rms,
-              hipStream_t s, bool far_done = false) {
+              hipStream_t s, CellHandoff* ho = nullptr) {
+  const bool far_done = ho != nullptr && ho->far_done;
   const int B = c->B, d = c->d, h = c->h, T_ = L->T, BH = B * h;
   const bool mult = c->ctx_mod != DM_CTX_LINEAR;
   const float scale = 1.0f / sqrtf((float)DH);
@@ -332,8 +339,14 @@ bool bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
     Mx = sv.Mx;
   } else {
     if (mult) sv.vin = vinS + coff * d;   // the recompute writes v_in into the stacked rows
-    run_cell<T, DH>(c, w, L, cos, sin, pos0, cc, K, pos0, T_, (T*)Kc, (T*)Vc, cache_T, nullptr, nullptr, ws.fws,
-                    &sv, s);
+    // in a layer's reverse scan the recompute also computes the next cell's (ci - 1) committed-prefix
+    // partials inside its fused launches, as a layer's forward does for the cell after
+    const int own = ho != nullptr ? ho->comm_nsplit : -1;
+    const int handed = run_cell<T, DH>(c, w, L, cos, sin, pos0, cc, K, pos0, T_, (T*)Kc, (T*)Vc, cache_T, nullptr,
+                                       nullptr, ws.fws, &sv, s, CellRows<T>{}, false, own,
+                                       ho != nullptr && ci > 0 ? sched[3 * (ci - 1)] : -1,
+                                       ho != nullptr && ci > 0 ? sched[3 * (ci - 1) + 1] : 0);
+    if (ho != nullptr) ho->comm_nsplit = handed;
     Mx = pos0 > 0 ? ws.fws.M : nullptr;
   }
   // grads of the cell's final rows: layer path, the committed-prefix attention of every later
@@ -512,7 +525,7 @@ bool bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
     qa.window = c->local_window;
     hipLaunchKernelGGL((k_comm_dq<T, DH>), dim3(BH, cdiv(cc, 64)), dim3(256), lds_attn, s, qa);
   }
-  return host_splits > 0;
+  if (ho != nullptr) ho->far_done = host_splits > 0;
 }
 
 template <typename T, int DH>
@@ -828,10 +841,10 @@ int bwd_dispatch(const dm_config* c, const dm_packed* w, const BwdCall& a, hipSt
     if (a.part == BWD_LAYER) {
       ProfScope whole(PROF_BWD, s);
       bwd_begin<T, DH>(c, w, (const T*)a.dy, (const T*)a.ocat, a.L->T, a.g, ws, s);
-      bool far_done = false;   // each cell's far committed-VJP splits ride in the cell after's launches
+      CellHandoff ho;   // work each cell's launches do for the cell before it
       for (int ci = a.n_cells - 1; ci >= 0; --ci)
-        far_done = bwd_cell<T, DH>(c, w, a.cos, a.sin, a.L, a.sched, a.n_cells, ci, Kc, Vc, a.cache_T, tape, to,
-                                   GradCache{}, ws, &rms, s, far_done);
+        bwd_cell<T, DH>(c, w, a.cos, a.sin, a.L, a.sched, a.n_cells, ci, Kc, Vc, a.cache_T, tape, to, GradCache{}, ws,
+                        &rms, s, &ho);
       bwd_end<T, DH>(c, w, (const T*)a.x, (const T*)a.dy, (T*)a.dx, a.cos, a.sin, a.L, a.sched, a.n_cells, Kc, Vc,
                      a.cache_T, tape, to, true, rms, a.g, ws, s);
     } else if (a.part == BWD_BEGIN) {
