@@ -122,11 +122,6 @@ class DualModAttention(nn.Module):
         K. Differentiable: the backward is the HIP reverse scan with exact recompute."""
         if collect is not None:
             raise NotImplementedError("telemetry collection is not supported on the HIP path")
-        W = getattr(self.cfg, "local_window", 0) or 0
-        if W and W <= self.CHUNK:
-            # the cells window their committed prefix only; every row of a cell reads all of the
-            # cell's earlier rows, so the window has to exceed the chunk
-            raise NotImplementedError(f"local_window {W} <= the chunk length {self.CHUNK} on the HIP path")
         from .autograd import dm_layer
         B, T, d = xhat.shape
         cell = self._hip_cell(B, T, xhat.dtype)

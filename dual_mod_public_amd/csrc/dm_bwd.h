@@ -773,6 +773,7 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a, int L, int nbh) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g4 = lane >> 4, lc = lane & 15;
   const int d = g.d, c = g.c;
+  const int wl = intra_wlim(g.window);   // intra keys at most wl rows before the query
   const long lrow0 = (long)bh * g.Tbuf + g.buf_t0;
   // the wave's own 16 rows of staging: written and read by that wave only (LDS
   // operations of one wave complete in order, so no workgroup barrier is needed)
@@ -924,7 +925,7 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a, int L, int nbh) {
       for (int t = 0; t < 4; ++t) {
         const int j = 16 * t + lc;
         const float e = __expf(S[t][r] * a.scale - Mr[r]) * rZ[r];
-        W[il * LDI + j] = from_f<T>((j < i && i < c ? e : 0.f) * (dP[t][r] - Dr[r]));
+        W[il * LDI + j] = from_f<T>((j < i && i - j <= wl && i < c ? e : 0.f) * (dP[t][r] - Dr[r]));
       }
     }
     floatx4 dQ[NDT];
@@ -987,7 +988,7 @@ DM_DEV void attn_bwd_body(const AttnBwdArgs<T>& a, int L, int nbh) {
         for (int r = 0; r < 4; ++r) {
           const int j = 16 * wave + 4 * g4 + r;
           const float e = __expf(St[t][r] * a.scale - Mq[t]) * rZq[t];
-          Pt[t][r] = (j < i && i < c) ? e : 0.f;
+          Pt[t][r] = (j < i && i - j <= wl && i < c) ? e : 0.f;
           W[(4 * g4 + r) * LDI + i] = from_f<T>(Pt[t][r]);
         }
       }

@@ -326,6 +326,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
   const int N = B * cc;
   const size_t NS = (size_t)N;
   CellGeom g{B, cc, d, h, DH, pos0, pos0, T_, cache_T};
+  g.window = window_of(c);
   g.kmod_cols = c->kmod_vraw_heads * DH;
   g.kmod_mode = c->kmod_mode;
   g.v_clamp_tau = c->v_clamp_tau;
@@ -359,7 +360,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
   if (gc.dK == nullptr) {
     CommKeyArgs<T> ka{B, h, T_, cache_T, pos0, cc, pos0 + cc, t_end, qr, Kc, Vc, ws.Gb, ws.Drow, ws.Mrow,
                       scale, ws.dKp, ws.dVp};
-    ka.window = c->local_window;
+    ka.window = window_of(c);
     ka.nsq = comm_nsq(BH);
     const int nlaunch = far_done ? 1 : ka.nsq;
     if (launch_log() != nullptr)
@@ -380,7 +381,7 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
     if (gc.dK == nullptr && launch_log() == nullptr && ci > 0 && t_end > pos0 + 64) {
       kprev = CommKeyArgs<T>{B, h, T_, cache_T, sched[3 * (ci - 1)], sched[3 * (ci - 1) + 1], pos0, t_end, qr, Kc, Vc,
                              ws.Gb, ws.Drow, ws.Mrow, scale, ws.dKp, ws.dVp};
-      kprev.window = c->local_window;
+      kprev.window = window_of(c);
       kprev.nsq = comm_nsq(BH);
       host_splits = kprev.nsq - 1;
     }
@@ -518,11 +519,11 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
   else if (gc.dK != nullptr && pos0 > 0) {
     CommKeyArgs<T> ka{B, h, T_, cache_T, pos0, 0, pos0, pos0 + cc, qr, Kc, Vc, ws.Gb, ws.Drow, ws.Mrow,
                       scale, nullptr, nullptr, gc.dK, gc.dV};
-    ka.window = c->local_window;
+    ka.window = window_of(c);
     hipLaunchKernelGGL((k_comm_dkv<T, DH>), dim3(cdiv(pos0, 64), BH), dim3(256), lds_attn, s, ka);
     CommQueryArgs<T> qa{B, h, T_, cache_T, pos0 + cc, ws.klim, qr, Kc, Vc, ws.Gb, ws.Drow, ws.Mrow, scale, ws.dq,
                         pos0};
-    qa.window = c->local_window;
+    qa.window = window_of(c);
     hipLaunchKernelGGL((k_comm_dq<T, DH>), dim3(BH, cdiv(cc, 64)), dim3(256), lds_attn, s, qa);
   }
   if (ho != nullptr) ho->far_done = host_splits > 0;
@@ -580,7 +581,7 @@ void bwd_end(const dm_config* c, const dm_packed* w, const T* x, const T* dy, T*
   // committed-prefix VJP, query side (layer path): every row with a committed prefix, into dq
   if (layer_path) {
     CommQueryArgs<T> qa{B, h, T_, cache_T, t_end, ws.klim, qr, Kc, Vc, ws.Gb, ws.Drow, ws.Mrow, scale, ws.dq};
-    qa.window = c->local_window;
+    qa.window = window_of(c);
     hipLaunchKernelGGL((k_comm_dq<T, DH>), dim3(BH, cdiv(t_end, 64)), dim3(256), lds_attn, s, qa);
   }
   // ---- projection VJP
@@ -709,7 +710,7 @@ void record_bwd_chunk(const dm_config* c, const dm_stack_bwd_layer& ly, const fl
   const float scale = 1.0f / sqrtf((float)DH);
   CommQueryArgs<T> qa{B, h, T_, cache_T, pos0 + cc, ws.klim, (const T*)L->qr, Kc, Vc, ws.Gb, ws.Drow, ws.Mrow,
                       scale, ws.dq, pos0};
-  qa.window = c->local_window;
+  qa.window = window_of(c);
   record_launch<CommDqBody<T, DH>>(dim3(BH, cdiv(cc, 64)), dim3(256), qa, (unsigned)lds_attn);
   // projection VJP of the cell's rows (the column partials come with the layer's close)
   typename ProjBwdBody<T, DH>::Args pa{N, T_, d, h, nproj, c->ctx_mod == DM_CTX_FUSION ? 1 : 0, ws.dq, ws.dkraw,
@@ -887,7 +888,6 @@ int check_bwd_common(const dm_config* c, const dm_packed* w, const dm_layer_bufs
   DM_REQUIRE(w->w_proj_t && w->w_sweep_t && w->wo_t && (!mult || w->w_vctx_t), DM_ERR_INVALID,
              "the backward needs the transposed packed weights");
   if ((rc = dm_check_schedule(sched, n_cells, L->T))) return rc;
-  if ((rc = check_window(c, sched, n_cells))) return rc;
   DM_REQUIRE(L->T <= cache_T, DM_ERR_INVALID, "T=%d > cache_T=%d", L->T, cache_T);
   {   // the attention VJP keeps Q, K, V and dO of a 64-row block in LDS
     const size_t lds = c->dtype == DM_BF16

@@ -338,7 +338,7 @@ int run_cell(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, con
   g.kmod_mode = c->kmod_mode;
   g.v_clamp_tau = c->v_clamp_tau;
   g.rope_t0 = rows.rope_t0;
-  g.window = c->local_window;
+  g.window = window_of(c);
   T* Kr = rows.K ? rows.K : Kc;
   T* Vr = rows.K ? rows.V : Vc;
   const long rows_stride = rows.K ? rows.stride : (long)cache_T * DH;

@@ -124,16 +124,11 @@ inline CommPlan comm_plan(int n, int BH) {
   const int split_len = cdiv(cdiv(n, nsplit), 64) * 64;
   return CommPlan{cdiv(n, split_len), split_len};
 }
-// A local window on the cells covers only their committed prefix (every row of a cell reads all
-// of the cell's earlier rows): the window must exceed the longest cell.
-inline int check_window(const dm_config* c, const int32_t* sched, int n_cells) {
-  int most = 0;
-  for (int i = 0; i < n_cells; ++i) most = std::max(most, (int)sched[3 * i + 1]);
-  DM_REQUIRE(c->local_window == 0 || c->local_window > most, DM_ERR_UNSUPPORTED,
-             "local_window %d must exceed the cell length %d (a cell's rows read all its earlier rows)",
-             c->local_window, most);
-  return DM_OK;
-}
+// The window the kernels apply for local_window W (attention.py:291-293): a row at position i
+// reads keys >= i - W + 1, committed and intra (0 = none). W = 1 reads like no window, as the
+// reference's attend_one does: it keeps K_past[:, :, -(W - 1):], and for W = 1 that is
+// K_past[:, :, -0:], the whole past.
+inline int window_of(const dm_config* c) { return c->local_window > 1 ? c->local_window : 0; }
 
 // first committed key a cell at pos0 reads (chunk row 0's window start)
 inline int comm_kstart(int pos0, int window) { return window > 0 ? std::max(0, pos0 - window + 1) : 0; }

@@ -368,8 +368,7 @@ struct CellGeom {
   int kmod_mode = 0;   // dm_kmod_mode of those columns
   float v_clamp_tau = 0.f;   // v'' norm clamp radius per (row, head), 0 = off
   int rope_t0 = -1;    // RoPE table row of chunk row 0 (-1: pos0, tables indexed by position)
-  int window = 0;      // local_window W (a row at position i reads keys >= i - W + 1); 0 = none.
-                       // The cell kernels take W > c: only the committed prefix is windowed
+  int window = 0;      // local_window W (a row at position i reads keys >= i - W + 1); 0 = none
   // a decode step at a device position (graph replay): the epilogues instantiated for it read
   // the position here, clamped to [0, pos_cap), as their RoPE row and output row
   const int* pos_dev = nullptr;
@@ -463,10 +462,13 @@ struct KeyBound {
   int n;
   DM_DEV bool operator()(int, int key) const { return key < n; }
 };
+// intra keys of chunk row q0 + q: key < q0 + q, and at most wlim rows back (W - 1 with a
+// window, a huge value without)
 struct KeyStrictLower {   // q is block-relative; q0 = the block's first query row
-  int q0;
-  DM_DEV bool operator()(int q, int key) const { return key < q + q0; }
+  int q0, wlim;
+  DM_DEV bool operator()(int q, int key) const { return key < q + q0 && q + q0 - key <= wlim; }
 };
+DM_DEV int intra_wlim(int window) { return window > 0 ? window - 1 : (1 << 30); }
 // committed keys of a tile starting at position k0: key < n, and inside chunk row q's window
 // (position k0 + key >= lo0 + q, lo0 = pos0 - W + 1; a very negative lo0 without a window)
 struct KeyWindow {
@@ -713,7 +715,7 @@ DM_DEV void attend_rows(const AttendArgs<T>& a, int bh, int q0, T* lds) {
   if constexpr (V_STAGED) store_k<T, DH, 64 * NW>(kv, Ks);
   else store_kv<T, DH, 64 * NW>(kv, Ks, Vs);
   __syncthreads();
-  flash_tile<T, DH>(qf, Ks, Vs, Ps + wave * 16 * C::LDP, a.scale, KeyStrictLower{q0}, st);
+  flash_tile<T, DH>(qf, Ks, Vs, Ps + wave * 16 * C::LDP, a.scale, KeyStrictLower{q0, intra_wlim(g.window)}, st);
 
   // raw self column: s_self = scale * <q_r, k_self_r> (fp32), value v_raw
 #pragma unroll

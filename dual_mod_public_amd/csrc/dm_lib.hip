@@ -186,10 +186,6 @@ int dm_cell_fwd(const dm_config* c, const dm_packed* w, const dm_layer_bufs* L, 
   DM_REQUIRE(a != nullptr && cos && sin, DM_ERR_INVALID, "null cell args / rope tables");
   DM_REQUIRE(a->c >= 1 && a->c <= CMAX, DM_ERR_UNSUPPORTED, "chunk length c=%d (1..%d)", a->c, CMAX);
   DM_REQUIRE(a->n_sweeps >= 1, DM_ERR_INVALID, "n_sweeps=%d", a->n_sweeps);
-  {
-    const int32_t one[3] = {a->pos0, a->c, a->n_sweeps};
-    if ((rc = check_window(c, one, 1))) return rc;
-  }
   const bool local = a->K_rows != nullptr;
   if (local) {
     // chunk-local form: layer buffer row p, RoPE table row p and ocat row p belong to chunk row p;
@@ -265,7 +261,6 @@ int dm_layer_fwd(const dm_config* c, const dm_packed* w, const void* x, void* y,
   if ((rc = check_packed(c, w)) || (rc = check_bufs(c, L))) return rc;
   DM_REQUIRE(x && y && ocat, DM_ERR_INVALID, "null x/y/ocat");
   if ((rc = dm_check_schedule(sched, n_cells, L->T))) return rc;
-  if ((rc = check_window(c, sched, n_cells))) return rc;
   DM_REQUIRE(L->T <= cache_T, DM_ERR_INVALID, "T=%d > cache_T=%d", L->T, cache_T);
   if (tape != nullptr) {
     DM_REQUIRE(tape_bytes >= dm_layer_tape_bytes(c, sched, n_cells), DM_ERR_WORKSPACE, "tape %zu < %zu bytes",
@@ -358,7 +353,8 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
   // written into the tape slot last; host position: the launches are sized to a->pos
   const bool dev_pos = a->pos_dev != nullptr;
   const int pos = dev_pos ? 0 : a->pos;
-  const int lo = (c->local_window > 0 && pos > c->local_window - 1) ? pos - (c->local_window - 1) : 0;
+  const int W = window_of(c);
+  const int lo = (W > 0 && pos > W - 1) ? pos - (W - 1) : 0;
   // device position without per-head context norms or the v'' clamp: the projection and refine
   // epilogues read the position themselves (RoPE rows of the full tables, the refined pair written
   // straight into tape slot pos); otherwise the RoPE rows are gathered and the pair staged first
@@ -379,7 +375,7 @@ int run_decode(const dm_config* c, const dm_packed* w, const float* cos, const f
   DecodeArgs<T> da{B, h, d, a->tape_T, pos, lo, DEC_SPLIT, nsplit, 1.0f / sqrtf((float)DH),
                    (const T*)ws.q, (const T*)ws.kself, (const T*)ws.vraw, (const T*)a->K_tape,
                    (const T*)a->V_tape, ws.part, ws.o, ws.ssq, (T*)a->o_cat, nullptr,
-                   (const int*)a->pos_dev, c->local_window};
+                   (const int*)a->pos_dev, window_of(c)};
   if (nsplit > 0) {
     const int idx = prof_launch_begin(PROF_DEC_READ, true, da.prof_ts);
     launch_timed(idx, k_decode_partial<T, DH, DEC_SPLIT>, dim3(nsplit, B * h), dim3(256), 0, s, da);
@@ -514,7 +510,8 @@ template <typename T, int DH>
 void run_attend_one(const dm_config* c, const void* q, const void* ks, const void* vs, const void* Kp, const void* Vp,
                     int P, int past_T, void* o, const DecWs& ws, hipStream_t s) {
   const int B = c->B, h = c->h, d = c->d;
-  const int lo = (c->local_window > 0 && P > c->local_window - 1) ? P - (c->local_window - 1) : 0;
+  const int W = window_of(c);
+  const int lo = (W > 0 && P > W - 1) ? P - (W - 1) : 0;
   const int nsplit = P > lo ? cdiv(P - lo, DEC_SPLIT) : 0;
   DecodeArgs<T> da{B, h, d, past_T, P, lo, DEC_SPLIT, nsplit, 1.0f / sqrtf((float)DH), (const T*)q, (const T*)ks,
                    (const T*)vs, (const T*)Kp, (const T*)Vp, ws.part, ws.o, ws.ssq, (T*)o, nullptr};

@@ -112,7 +112,6 @@ int check_stack(const dm_config* c, int nl, const dm_stack_layer* layers, const 
   DM_REQUIRE(layers[0].bufs != nullptr, DM_ERR_INVALID, "null layer buffers");
   const int T = layers[0].bufs->T;
   if ((rc = dm_check_schedule(sched, n_cells, T))) return rc;
-  if ((rc = check_window(c, sched, n_cells))) return rc;
   for (int i = 0; i < n_cells; ++i)
     DM_REQUIRE(sched[3 * i + 1] == sched[1] && sched[3 * i + 2] == sched[2], DM_ERR_UNSUPPORTED,
                "the layer-batched forward needs equal cells (cell %d: c=%d K=%d, cell 0: c=%d K=%d)", i,

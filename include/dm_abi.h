@@ -57,9 +57,10 @@ typedef struct dm_config {
   int32_t ctx_mod;          /* dm_ctx_mod */
   float mult_res_lambda;    /* config.py:126 */
   float rms_eps;            /* RMSNorm eps of attn_norm / norm_ctx: 1e-5 */
-  int32_t local_window;     /* W tokens incl. self (attention.py:291-293), 0 = full. Decode: any W;
-                               the chunk cells: W > the cell length (a cell's rows read all of
-                               its earlier rows, the committed prefix is windowed) */
+  int32_t local_window;     /* W tokens incl. self (attention.py:291-293), 0 = full: a row at
+                               position i reads keys >= i - W + 1 of the committed prefix and of
+                               its own cell; W = 1 reads like 0, as attend_one's K_past[-(W-1):]
+                               does; < 0 is rejected (DM_ERR_INVALID) */
   int32_t flags;            /* DM_FLAG_* */
   int32_t kmod_vraw_heads;  /* config.py kmod_vraw_heads: the first n heads keep raw values */
   int32_t kmod_mode;        /* dm_kmod_mode (kmod_mode + kmod_vraw_bound), attention.py:362-384 */

@@ -273,20 +273,22 @@ def _window_masks(c, P, W, device, dtype):
 
 def chunk_attend(q_r, k_self_r, v_raw, K_comm, V_comm, K_intra, V_intra,
                  intra_mask, scale, window=0):
-    """scan_cell_fwd.py:63-85 — [committed | intra (strict lower) | raw self]. window > 0:
+    """scan_cell_fwd.py:63-85 — [committed | intra (strict lower) | raw self]. window > 1:
     attend_one's local window on the committed and intra reads (_window_masks); with K = c
-    sweeps the cell then equals the windowed sequential scan (scan.py over attend_one)."""
+    sweeps the cell then equals the windowed sequential scan (scan.py over attend_one).
+    window = 1 reads like no window, as attend_one does: its K_past[:, :, -(W - 1):] is
+    K_past[:, :, -0:], the whole past (attention.py:292-293)."""
     c = q_r.shape[2]
     P = 0 if K_comm is None else K_comm.shape[2]
     s_intra = _hi(q_r @ K_intra.transpose(-1, -2) * scale)
     s_intra = s_intra + intra_mask.to(device=s_intra.device, dtype=s_intra.dtype)
-    if window:
+    if window > 1:
         mc, mi = _window_masks(c, P, window, s_intra.device, s_intra.dtype)
         s_intra = s_intra + mi
     s_self = _hi((q_r * k_self_r).sum(-1, keepdim=True)) * scale
     if K_comm is not None and K_comm.shape[2] > 0:
         s_comm = _hi(q_r @ K_comm.transpose(-1, -2) * scale)
-        if window:
+        if window > 1:
             s_comm = s_comm + mc
         scores = torch.cat([s_comm, s_intra, s_self], dim=-1)
     else:

@@ -121,13 +121,12 @@ def test_kmod_config_fields():
     assert L.load().dm_cell_workspace_bytes(c, 64) == 0
 
 
-def test_training_entry_points_reject_window_within_a_cell():
-    """Training windows must exceed the cell length (a cell's rows read all its earlier rows):
-    dm_layer_fwd (tape and recompute forms) and dm_layer_bwd reject W = 8 with 64-row cells with
-    DM_ERR_UNSUPPORTED before any launch (the checks run on the host; the placeholder pointers
-    below are never dereferenced)."""
+def test_training_entry_points_reject_a_negative_window():
+    """dm_layer_fwd (tape and recompute forms) and dm_layer_bwd reject local_window < 0 with
+    DM_ERR_INVALID before any launch (the checks run on the host; the placeholder pointers below
+    are never dereferenced)."""
     lib = L.load()
-    c = _conf(local_window=8)
+    c = _conf(local_window=-1)
     fake = ctypes.c_void_p(1 << 20)   # non-null, 16-byte aligned, never dereferenced
     w = L.dm_packed()
     for f in ("w_proj", "b_proj", "w_sweep", "w_vctx", "norm_ctx_w", "attn_norm_w", "wo", "w_proj_t",
@@ -144,17 +143,17 @@ def test_training_entry_points_reject_window_within_a_cell():
     for tape in (None, fake):
         rc = lib.dm_layer_fwd(ctypes.byref(c), ctypes.byref(w), fake, fake, fake, fake, ctypes.byref(b), sched, 1,
                               fake, fake, 64, fake, tape, 1 << 30, fake, 1 << 30, None)
-        assert rc == -2 and b"local_window" in lib.dm_last_error()
+        assert rc == -1 and b"local_window" in lib.dm_last_error()
     rc = lib.dm_layer_bwd(ctypes.byref(c), ctypes.byref(w), fake, fake, fake, fake, fake, ctypes.byref(b), sched, 1,
                           fake, fake, 64, fake, None, 0, ctypes.byref(g), fake, 1 << 30, None)
-    assert rc == -2 and b"local_window" in lib.dm_last_error()
+    assert rc == -1 and b"local_window" in lib.dm_last_error()
 
 
-def test_training_window_longer_than_a_cell_passes_host_checks():
-    """W > c is a training configuration (the committed-prefix kernels mask keys below
-    i - W + 1): the layer-batched forward's plan query, which runs every host check of the
-    training entry points and launches nothing, accepts W = 100 with 64-row cells and refuses
-    W = 8 (the placeholder pointers are never dereferenced)."""
+def test_training_windows_pass_host_checks():
+    """Any W >= 1 is a training configuration (the committed-prefix and intra-cell attention mask
+    keys below i - W + 1): the layer-batched forward's plan query, which runs every host check of
+    the training entry points and launches nothing, accepts W = 1, 8 and 100 with 64-row cells and
+    refuses W = -1 (the placeholder pointers are never dereferenced)."""
     lib = L.load()
     fake = ctypes.c_void_p(1 << 20)
     w = L.dm_packed()
@@ -171,9 +170,10 @@ def test_training_window_longer_than_a_cell_passes_host_checks():
         setattr(ly[0], f, fake.value)
     ly[0].workspace_bytes = 1 << 34
     sched = (ctypes.c_int32 * 12)(0, 64, 4, 64, 64, 4, 128, 64, 4, 192, 64, 4)
-    ok = _conf(local_window=100)
-    assert lib.dm_stack_fwd_plan_bytes(ctypes.byref(ok), 1, ly, sched, 4, 256) > 0, lib.dm_last_error()
-    bad = _conf(local_window=8)
+    for W in (1, 8, 100):
+        ok = _conf(local_window=W)
+        assert lib.dm_stack_fwd_plan_bytes(ctypes.byref(ok), 1, ly, sched, 4, 256) > 0, lib.dm_last_error()
+    bad = _conf(local_window=-1)
     assert lib.dm_stack_fwd_plan_bytes(ctypes.byref(bad), 1, ly, sched, 4, 256) == 0
     assert b"local_window" in lib.dm_last_error()
 

@@ -1,13 +1,14 @@
 """GPU tests of the local window on the chunk cells (config local_window, attention.py:291-293:
 a token reads the last W - 1 rows before it and itself).
 
-The cells window their committed prefix (a window longer than the cell; every row of a cell
-reads all its earlier rows): with K = c sweeps the windowed layer equals the windowed
-sequential scan of the oracle (attend_one's window, pinned by brute force), with K < c it
-equals the oracle's windowed Jacobi cells (whose masks are pinned to the windowed scan at K = c
-in tests/test_oracle_invariants.py). The backward against autograd through the oracle, the
-windowed decode against the windowed teacher-forced layer, the layer-batched stack against the
-layer-by-layer one, and the rejection of windows no longer than a cell.
+The cells window their committed prefix and, for windows no longer than the cell, their intra
+rows (row p reads cell rows p - W + 1 .. p - 1): with K = c sweeps the windowed layer equals the
+windowed sequential scan of the oracle (attend_one's window, pinned by brute force), with K < c
+it equals the oracle's windowed Jacobi cells (whose masks are pinned to the windowed scan at
+K = c in tests/test_oracle_invariants.py). The backward against autograd through the oracle, the
+windowed decode against the windowed teacher-forced layer, and the layer-batched stack against
+the layer-by-layer one, each with windows longer and shorter than a cell (W = 1: the self
+column only).
 """
 
 import pytest
@@ -45,7 +46,7 @@ def _layer(cfg, sd, x, cos, sin, sched, dtype):
     return ocat, K, V
 
 
-@pytest.mark.parametrize("W,T", [(65, 256), (100, 256), (300, 512), (2048, 256)])
+@pytest.mark.parametrize("W,T", [(1, 192), (17, 256), (64, 256), (65, 256), (100, 256), (300, 512), (2048, 256)])
 def test_windowed_exact_cells_equal_windowed_scan_fp32(W, T):
     say(f"windowed cells K=c vs windowed sequential scan, W={W} T={T}")
     cfg = cfg_of(T=T, local_window=W)
@@ -59,10 +60,11 @@ def test_windowed_exact_cells_equal_windowed_scan_fp32(W, T):
     assert max(errs.values()) < 1e-5
 
 
+@pytest.mark.parametrize("W", [150, 40])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
-def test_windowed_jacobi_cells_equal_oracle(dtype, tol):
-    say(f"windowed Jacobi cells K=3 vs the oracle, {dtype}")
-    W, T = 150, 320
+def test_windowed_jacobi_cells_equal_oracle(dtype, tol, W):
+    say(f"windowed Jacobi cells K=3 W={W} vs the oracle, {dtype}")
+    T = 320
     cfg = cfg_of(T=T, local_window=W)
     B = 2
     sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
@@ -70,11 +72,11 @@ def test_windowed_jacobi_cells_equal_oracle(dtype, tol):
     o, K, V = _layer(cfg, sd, x, c32, s32, sched, dtype)
     o_ref, K_ref, V_ref = O.layer_forward(cfg, sd, x, c64, s64, sched)
     errs = {"o": relerr(o, o_ref), "K": relerr(K, K_ref), "V": relerr(V, V_ref)}
-    record(f"window Jacobi {dtype}", errs, tol)
+    record(f"window Jacobi W={W} {dtype}", errs, tol)
     assert max(errs.values()) < tol, errs
 
 
-@pytest.mark.parametrize("K,W", [(4, 90), (64, 130)])
+@pytest.mark.parametrize("K,W", [(4, 90), (64, 130), (4, 40), (64, 23), (3, 1)])
 def test_windowed_backward_fp32(K, W):
     say(f"windowed backward K={K} W={W} vs autograd through the oracle")
     T = 192
@@ -89,11 +91,12 @@ def test_windowed_backward_fp32(K, W):
         compare(f"window bwd K={K} W={W} tape={tape}", dx, grads, dx_ref, g_ref, FP32_TOL)
 
 
-def test_windowed_decode_equals_teacher_forced():
+@pytest.mark.parametrize("W", [70, 20])
+def test_windowed_decode_equals_teacher_forced(W):
     """Two independent paths of the same windowed operator: token-by-token decode on the static
     tape and the K = c windowed layer forward."""
-    say("windowed decode vs windowed teacher-forced layer")
-    W, T, B = 70, 160, 2
+    say(f"windowed decode vs windowed teacher-forced layer, W={W}")
+    T, B = 160, 2
     cfg = cfg_of(T=T, local_window=W)
     sd, x, _, (c32, s32) = setup(cfg, B, T)
     o_f, K_f, V_f = _layer(cfg, sd, x, c32, s32, uniform_chunks(T, 64), torch.float32)
@@ -102,16 +105,17 @@ def test_windowed_decode_equals_teacher_forced():
     outs = [tape.step(xd[:, t].contiguous(), t, c32, s32)[0].clone() for t in range(T)]
     torch.cuda.synchronize()
     errs = {"o": relerr(torch.stack(outs, 1), o_f), "K": relerr(tape.K, K_f), "V": relerr(tape.V, V_f)}
-    record("window decode vs layer", errs, 1e-5)
+    record(f"window decode vs layer W={W}", errs, 1e-5)
     assert max(errs.values()) < 1e-5, errs
 
 
-def test_windowed_stack_wavefront_equals_layer_by_layer():
+@pytest.mark.parametrize("W", [100, 30])
+def test_windowed_stack_wavefront_equals_layer_by_layer(W):
     from dual_mod_public_amd.stack import HipLayerStack
     from dual_mod_public_amd.synthetic import make_state_dict
-    say("windowed stack: layer-batched vs layer by layer")
+    say(f"windowed stack W={W}: layer-batched vs layer by layer")
     T, B, n = 256, 2, 3
-    cfg = cfg_of(T=T, local_window=100)
+    cfg = cfg_of(T=T, local_window=W)
     sds = [{k: v.to(DEV) for k, v in make_state_dict(cfg, seed=90 + i).items()} for i in range(n)]
     cos, sin = O.build_rope_cache(T, cfg.head_dim, cfg.rope_theta)
     sts = []
@@ -128,11 +132,3 @@ def test_windowed_stack_wavefront_equals_layer_by_layer():
     y2, dx2, _ = sts[1].step(x, dy)
     torch.cuda.synchronize()
     assert torch.equal(y1, y2) and torch.equal(dx1, dx2) and torch.equal(sts[0].flat, sts[1].flat)
-
-
-def test_window_no_longer_than_a_cell_is_refused():
-    cfg = cfg_of(T=128, local_window=64)
-    B, T = 2, 128
-    sd, x, _, (c32, s32) = setup(cfg, B, T)
-    with pytest.raises(L.DMError):
-        _layer(cfg, sd, x, c32, s32, uniform_chunks(T, 64), torch.float32)

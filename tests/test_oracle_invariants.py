@@ -418,16 +418,26 @@ def test_lm_chunked_schedule_exact_equals_scan_and_differs_below_c():
     assert relerr(O.lm_forward(cfg, sd, idx, cos, sin, schedule=O.uniform_chunks(T, 8, 2)), ref) > 1e-6
 
 
-@pytest.mark.parametrize("W,c", [(5, 8), (9, 8), (20, 8), (3, 4)])
+@pytest.mark.parametrize("W,c", [(5, 8), (9, 8), (20, 8), (3, 4), (2, 8), (1, 8)])
 def test_windowed_cells_equal_windowed_scan(W, c):
     """The local window on the chunk cells (chunk_attend's window masks) with K = c sweeps
     reproduces the windowed sequential scan (scan.py over attend_one, whose window is pinned by
-    the brute-force test above) — windows shorter and longer than the chunk."""
+    the brute-force test above) — windows shorter and longer than the chunk, and W = 1, which
+    attend_one reads as no window (its K_past[:, :, -(W - 1):] slices -0:, the whole past)."""
     cfg = _cfg(local_window=W)
     sd, cos, sin, x = _setup(cfg, T=24)
     ref = O.sequential_scan(cfg, sd, x, cos, sin)
     out = O.layer_forward(cfg, sd, x, cos, sin, O.uniform_chunks(24, c))[0]
     assert relerr(out, ref) < TOL
+
+
+def test_window_one_reads_the_whole_past():
+    """attention.py:292-293 at W = 1: the slice -(W - 1): is -0:, so attend_one keeps every past
+    row; the windowed scan then equals the unwindowed one (and W = 2 does not)."""
+    sd, cos, sin, x = _setup(_cfg(), T=12)
+    ref = O.sequential_scan(_cfg(), sd, x, cos, sin)
+    assert relerr(O.sequential_scan(_cfg(local_window=1), sd, x, cos, sin), ref) < TOL
+    assert relerr(O.sequential_scan(_cfg(local_window=2), sd, x, cos, sin), ref) > 1e-3
 
 
 def test_window_changes_the_cells():
