@@ -429,24 +429,26 @@ void bwd_cell(const dm_config* c, const dm_packed* w, const float* cos, const fl
     if (mult) {
       const SrcRows<T> av{dvc + sw * NS * d, d, N}, bv{(const T*)w->w_vctx_t, d, d};
       const SrcRows<T> da2{dctx + sw * NS * 4 * d + 2 * d, 4 * d, N}, db2{(const T*)w->w_sweep_t + 2 * d, 4 * d, d};
-      const EpiDuFinal<T, DU_SPLIT, 2> ef{N, d, h, inv_d, c->rms_eps, ea.part, ea.lamdv, ea.o, ea.ssq, ea.normw,
-                                          ea.gw, ea.rowdot, ea.dnw};
       const EpiDuFinal<T, DU_SPLIT, 2, DUF_BM == 32> efp{N, d, h, inv_d, c->rms_eps, ea.part, ea.lamdv, ea.o, ea.ssq,
                                                          ea.normw, ea.gw, ea.rowdot, ea.dnw};
       bool grouped = false;
       if constexpr (sizeof(T) == 2) {
         if (launch_log() != nullptr) {
-          // the layer-batched launch has blocks to spare: du in 128 x 128 tiles (half the LDS
-          // traffic per product; every element's k order is the same, and EpiDuFinal's sums do not
-          // depend on the block width, so the results are too)
+          // the layer-batched launch has blocks to spare: du's slices 0, 1, 3 in 128 x 128 tiles
+          // (half the LDS traffic per product; every element's k order is the same, so the results
+          // are too)
           grouped = true;
           using PDu = GemmPart<T, 128, 128, 2, 2, -3, SrcRows<T>, SrcRows<T>, EpiStoreTileF32>;
           using PVin = GemmPart<T, 64, 32, 4, 1, -SW2_STAGES, SrcRows<T>, SrcRows<T>, EpiVinBwd<T, 32>>;
           const EpiVinBwd<T, 32> ev{g, N, c->ctx_mod, c->mult_res_lambda, sv.save1 + sw * NS * 4 * d,
                                     (const T*)L->sig, dctx + sw * NS * 4 * d, ws.dsig, ws.lamdv};
-          launch_gemm_pair(PDu{da, db, d, ep, d / 128, cdiv(N, 128), DU_SPLIT - 1, 2},
-                           PVin{av, bv, d, ev, d / 32, cdiv(N, 64), 1, -1}, s);
-          launch_gemm<T, 128, 128, 2, 2, -3>(da2, db2, N, d, d, ef, s);
+          // dv_in and du's slices 0, 1, 3 as launches of their own (in one launch every dv_in block
+          // would hold the du blocks' LDS), then slice 2 as on the layer path
+          const PDu pdu{da, db, d, ep, d / 128, cdiv(N, 128), DU_SPLIT - 1, 2};
+          const PVin pvin{av, bv, d, ev, d / 32, cdiv(N, 64), 1, -1};
+          record_launch<GemmPartBody<PVin>>(dim3(pvin.gx * pvin.gy * pvin.nz), dim3(256), {pvin});
+          record_launch<GemmPartBody<PDu>>(dim3(pdu.gx * pdu.gy * pdu.nz), dim3(256), {pdu});
+          launch_gemm<T, DUF_BM, 64, 2, 2, -DUF_STAGES>(da2, db2, N, d, d, efp, s);
         }
       }
       if (!grouped) {

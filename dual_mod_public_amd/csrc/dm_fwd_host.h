@@ -207,7 +207,7 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
       launch_gemm_auto<T, 64, 2 * DH, 2, 2, SW1_STAGES, 4>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
     else
       launch_gemm_auto<T, 64, 2 * DH, 1, 4, SW1_STAGES, 2>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
-  } else if (wide) {
+  } else if (wide && DM_GROUPED_WIDE_SW1) {
     // 64 x 128 blocks (two column groups each): a quarter less LDS traffic per MFMA and half the
     // o re-reads, for launches that have blocks to spare (the layer-batched forward)
     EpiSweep1<T, DH, 2> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,

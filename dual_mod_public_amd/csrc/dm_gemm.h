@@ -798,6 +798,17 @@ template <class P1, class P2> struct GemmPairBody {
     else a.p2.run(bx - n1, smem);
   }
 };
+// one GemmPart as a grouped-launch body (its own LDS size)
+template <class P> struct GemmPartBody {
+  static constexpr int THREADS = 256;
+  struct Args {
+    P p;
+  };
+  static DM_DEV void run(const Args& a, int bx, int) {
+    __shared__ __attribute__((aligned(1024))) char smem[P::LDS];
+    a.p.run(bx, smem);
+  }
+};
 template <class P1, class P2>
 __global__ __launch_bounds__(256) void k_gemm_pair(typename GemmPairBody<P1, P2>::Args a) {
   GemmPairBody<P1, P2>::run(a, (int)blockIdx.x, 0);

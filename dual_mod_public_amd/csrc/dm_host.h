@@ -46,6 +46,9 @@ namespace dm {
 #ifndef DM_BIG_STAGES
 #define DM_BIG_STAGES 2
 #endif
+#ifndef DM_GROUPED_WIDE_SW1
+#define DM_GROUPED_WIDE_SW1 1  // layer-batched sweep GEMM 1 in 64 x 128 tiles
+#endif
 #ifndef DM_KK_STAGES
 #define DM_KK_STAGES 2
 #endif
