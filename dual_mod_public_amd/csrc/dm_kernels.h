@@ -247,6 +247,19 @@ template <typename T, int DH, bool DEVPOS = false> struct EpiProj {
   template <int TR, int BN, int LDT>
   DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre&, int) const {
     static_assert(BN % DH == 0, "whole heads per block");
+    const int seg0 = n0 / d;
+    if constexpr (BN > DH) {
+      if ((n0 + BN - 1) / d == seg0) {   // every unit of the block in one segment (uniform)
+        if (seg0 <= 1) {
+          rope_block<TR, BN, LDT>(tile, m0, n0, seg0);
+          return;
+        }
+        if (seg0 >= 3) {
+          row_block<TR, BN, LDT>(tile, m0, n0, seg0);
+          return;
+        }
+      }
+    }
 #pragma unroll 1
     for (int hu = 0; hu < BN / DH; ++hu) {
       const int col0 = n0 + hu * DH;
@@ -324,16 +337,89 @@ template <typename T, int DH, bool DEVPOS = false> struct EpiProj {
     }
   }
 
+  // q or k of the block's BN / DH heads (one segment): the RoPE angles depend on the row and the
+  // pair only, so each pass's cos / sin are loaded once for every head, all passes' before the first
+  // head (head_unit's arithmetic, the same values)
+  template <int TR, int BN, int LDT>
+  DM_DEV void rope_block(const float* tl, int m0, int n0, int seg) const {
+    constexpr int L = DH / 8, RP = 256 / L, NP = TR / RP;
+    static_assert(TR % RP == 0, "whole passes");
+    const int jj = 4 * (threadIdx.x % L);
+    const int r0 = DEVPOS ? dev_position(pos_dev, pos_cap) : rope_t0;
+    float cs[NP][4], sn[NP][4];
+#pragma unroll
+    for (int pass = 0; pass < NP; ++pass) {
+      const int m = min(m0 + (int)threadIdx.x / L + pass * RP, M - 1);
+      const int t = m - (m / Tl) * Tl;
+      const long rrow = (long)(r0 + t) * (DH / 2) + jj;
+      unpackf4(ld_global<floatx4>(cos + rrow), cs[pass]);
+      unpackf4(ld_global<floatx4>(sin + rrow), sn[pass]);
+    }
+#pragma unroll 1
+    for (int hu = 0; hu < BN / DH; ++hu) {
+      const int hh = (n0 + hu * DH - seg * d) / DH;
+      const float* tu = tl + hu * DH;
+#pragma unroll
+      for (int pass = 0; pass < NP; ++pass) {
+        const int r = threadIdx.x / L + pass * RP, m = m0 + r;
+        if (m >= M) continue;
+        const floatx4 av = *reinterpret_cast<const floatx4*>(tu + r * LDT + jj);
+        const floatx4 bv = *reinterpret_cast<const floatx4*>(tu + r * LDT + jj + DH / 2);
+        const float a[4] = {av.x, av.y, av.z, av.w}, b[4] = {bv.x, bv.y, bv.z, bv.w};
+        const int bb = m / Tl, t = m - bb * Tl;
+        const long hrow = (((long)bb * h + hh) * Tbuf + buf_t0 + t) * DH + jj;
+        float o1[4], o2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          o1[i] = a[i] * cs[pass][i] - b[i] * sn[pass][i];
+          o2[i] = b[i] * cs[pass][i] + a[i] * sn[pass][i];
+        }
+        if (seg == 0) {
+          st4<T>(qr + hrow, o1);
+          st4<T>(qr + hrow + DH / 2, o2);
+        } else {
+          st4<T>(kraw + hrow, a);
+          st4<T>(kraw + hrow + DH / 2, b);
+          st4<T>(kself + hrow, o1);
+          st4<T>(kself + hrow + DH / 2, o2);
+        }
+      }
+    }
+  }
+
+  // row units of the block's BN / DH column groups (one segment): every group's bias loaded
+  // before the first group
+  template <int TR, int BN, int LDT>
+  DM_DEV void row_block(const float* tl, int m0, int n0, int seg) const {
+    constexpr int NU = BN / DH, L = DH / 4;
+    const int e = 4 * (threadIdx.x % L);
+    float bs[NU][4];
+#pragma unroll
+    for (int hu = 0; hu < NU; ++hu) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bs[hu][i] = 0.f;
+      if (!(seg == 5 && fusion)) unpackf4(ld_global<floatx4>(bias + (seg - 3) * d + n0 + hu * DH - seg * d + e), bs[hu]);
+    }
+#pragma unroll 1
+    for (int hu = 0; hu < NU; ++hu) row_rows<TR, LDT>(tl + hu * DH, m0, seg, n0 + hu * DH - seg * d, bs[hu]);
+  }
+
   // gate logits (x-halves + bias) or sigma(v_gate) / fusion's raw v_pre x-half, fp32 math, stored
   // in the storage dtype
   template <int TR, int LDT>
   DM_DEV void row_unit(const float* tl, int m0, int seg, int c0) const {
     constexpr int L = DH / 4;
-    constexpr int RP = 256 / L;
-    static_assert(TR % RP == 0, "whole passes");
     const int e = 4 * (threadIdx.x % L), col = c0 + e;
     float bs[4] = {0.f, 0.f, 0.f, 0.f};
     if (!(seg == 5 && fusion)) unpackf4(ld_global<floatx4>(bias + (seg - 3) * d + col), bs);
+    row_rows<TR, LDT>(tl, m0, seg, c0, bs);
+  }
+  template <int TR, int LDT>
+  DM_DEV void row_rows(const float* tl, int m0, int seg, int c0, const float (&bs)[4]) const {
+    constexpr int L = DH / 4;
+    constexpr int RP = 256 / L;
+    static_assert(TR % RP == 0, "whole passes");
+    const int e = 4 * (threadIdx.x % L), col = c0 + e;
 #pragma unroll
     for (int pass = 0; pass < TR / RP; ++pass) {
       const int r = threadIdx.x / L + pass * RP, m = m0 + r;
