@@ -183,6 +183,19 @@ template <typename T> DM_DEV void unpack8(const Raw8<T>& r, float* out) {
     for (int i = 0; i < 8; ++i) out[i] = __uint_as_float(r.v[i >> 2][i & 3]);
   }
 }
+template <typename T> DM_DEV void st8(T* p, const float* in) {
+  if constexpr (sizeof(T) == 2) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (uint32_t)__builtin_bit_cast(uint16_t, (bf16)in[2 * i]) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, (bf16)in[2 * i + 1]) << 16);
+    *reinterpret_cast<u32x4*>(p) = u32x4{w[0], w[1], w[2], w[3]};
+  } else {
+    *reinterpret_cast<floatx4*>(p) = floatx4{in[0], in[1], in[2], in[3]};
+    *reinterpret_cast<floatx4*>(p + 4) = floatx4{in[4], in[5], in[6], in[7]};
+  }
+}
 DM_DEV void unpackf4(const floatx4& v, float* out) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) out[i] = v[i];

@@ -164,6 +164,12 @@ template <class E> struct late_gathers_of<E, std::void_t<decltype(E::LATE_GATHER
   static constexpr int value = E::LATE_GATHERS;
 };
 template <class E> struct tile_rows_of<E, std::void_t<decltype(E::TILE_ROWS)>> { static constexpr int value = E::TILE_ROWS; };
+// A tile EPI with a member type ChunkPre: chunk_prefetch<TR, BN>(chunk m0, n0) gathers a chunk's
+// inputs, issued for chunk c + 1 before chunk c is applied (tile_apply(..., cp) takes them)
+template <class E, class = void> struct has_chunk_pre { static constexpr bool value = false; };
+template <class E> struct has_chunk_pre<E, std::void_t<typename E::ChunkPre>> { static constexpr bool value = true; };
+template <class E, class = void> struct EPI_ChunkPre { typedef char type; };
+template <class E> struct EPI_ChunkPre<E, std::void_t<typename E::ChunkPre>> { typedef typename E::ChunkPre type; };
 
 // k-rows per stage of the K-major direct-to-LDS k-loop: 32 for 256 x 256 blocks with
 // at least 4 stages (four 32 KB stages keep three in flight), else 64
@@ -682,6 +688,9 @@ DM_DEV void gemm_block_at(const SA& sa, const SB& sb, int K, const EPI& epi, int
     float* tile = reinterpret_cast<float*>(smem);
     const float* rs_lds = reinterpret_cast<const float*>(smem + gemm_stage_bytes<T, BM, BN, D, KM>());
     const int lane = threadIdx.x & 63;
+    constexpr int NCP = has_chunk_pre<EPI>::value ? 2 : 0;
+    typename EPI_ChunkPre<EPI>::type cp[2];
+    if constexpr (NCP > 0) cp[0] = epi.template chunk_prefetch<TR, BN>(m0, n0);
 #pragma unroll
     for (int c = 0; c < BM / TR; ++c) {
       if (c > 0) __syncthreads();   // the previous chunk has been read
@@ -698,7 +707,12 @@ DM_DEV void gemm_block_at(const SA& sa, const SB& sb, int K, const EPI& epi, int
       if constexpr (RMS)
         if (c == 0) sa.template prepare_store<BM>(pre_a, const_cast<float*>(rs_lds), nullptr, K);
       __syncthreads();
-      epi.template tile_apply<TR, BN, LDT>(tile, m0 + c * TR, n0, rs_lds + c * TR, pre, bz);
+      if constexpr (NCP > 0) {
+        if (c + 1 < BM / TR) cp[(c + 1) & 1] = epi.template chunk_prefetch<TR, BN>(m0 + (c + 1) * TR, n0);
+        epi.template tile_apply<TR, BN, LDT>(tile, m0 + c * TR, n0, rs_lds + c * TR, pre, bz, cp[c & 1]);
+      } else {
+        epi.template tile_apply<TR, BN, LDT>(tile, m0 + c * TR, n0, rs_lds + c * TR, pre, bz);
+      }
     }
   } else {
     gemm_kloop<T, BM, BN, WM, WN, D>(sa, sb, K, m0, n0, smem, acc, bz * K);

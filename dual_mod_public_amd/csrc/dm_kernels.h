@@ -1408,39 +1408,51 @@ template <typename T, int DH> struct Sweep2AttendBody {
 };
 
 // y = acc (+ x): the W_O projection with the block residual, or plain nn.Linear
+// y = acc + x (x nullptr: no residual), row m of the GEMM at row map(m) of both; y may alias x.
+// A tile epilogue: each thread owns runs of 8 consecutive columns (16-byte bf16 loads and stores);
+// the residual runs of the next 64-row chunk are loaded before the current chunk is stored.
 template <typename T> struct EpiResidual {
   int M, N;
-  const T* __restrict__ x;
-  T* __restrict__ y;
+  const T* x;
+  T* y;
   RowMap map = RowMap{};   // output / residual row of GEMM row m
-  // the residual rows of 16-row group i + 1 are loaded before group i is stored
-  // (y may alias x)
-  template <int FM, int FN>
-  DM_DEV void operator()(const floatx4 (&acc)[FM][FN], int row0, int col0, const float*, int) const {
-    const int lane = threadIdx.x & 63, lc = lane & 15;
-    float xv[2][4][FN];
-    auto load_x = [&](int i, int buf) {
+  static constexpr int TILE_ROWS = 64;
+  static constexpr int VEC = 8, MAXP = 8;   // columns per run; runs per thread and chunk
+  struct TilePre {};
+  DM_DEV TilePre tile_prefetch(int, int) const { return TilePre{}; }
+  struct ChunkPre {
+    Raw8<T> v[MAXP];
+  };
+  template <int TR, int BN> struct Shape {
+    static constexpr int TPR = BN / VEC, RPP = 256 / TPR, NP = TR / RPP;
+    static_assert(BN % VEC == 0 && 256 % TPR == 0 && TR % RPP == 0 && NP <= MAXP, "runs of a chunk");
+  };
+  template <int TR, int BN> DM_DEV ChunkPre chunk_prefetch(int m0, int n0) const {
+    using S = Shape<TR, BN>;
+    ChunkPre cp;
+    if (x == nullptr) return cp;   // uniform
+    const int cg = threadIdx.x % S::TPR, r0 = threadIdx.x / S::TPR;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const long m = map(min(row0 + 16 * i + 4 * (lane >> 4) + q, M - 1));
+    for (int p = 0; p < S::NP; ++p)
+      cp.v[p] = ld8_global(x + map(min(m0 + r0 + p * S::RPP, M - 1)) * N + n0 + cg * VEC);
+    return cp;
+  }
+  template <int TR, int BN, int LDT>
+  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre&, int,
+                         const ChunkPre& cp) const {
+    using S = Shape<TR, BN>;
+    const int cg = threadIdx.x % S::TPR, r0 = threadIdx.x / S::TPR;
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-          xv[buf][q][j] = x != nullptr ? to_f(x[m * N + col0 + 16 * j + lc]) : 0.f;
-      }
-    };
-    load_x(0, 0);
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int cb = i & 1;
-      if (i + 1 < FM) load_x(i + 1, cb ^ 1);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = row0 + 16 * i + 4 * (lane >> 4) + q;
-        if (m >= M) continue;
-        const long my = map(m);
-#pragma unroll
-        for (int j = 0; j < FN; ++j) y[my * N + col0 + 16 * j + lc] = from_f<T>(acc[i][j][q] + xv[cb][q][j]);
-      }
+    for (int p = 0; p < S::NP; ++p) {
+      const int r = r0 + p * S::RPP, m = m0 + r;
+      if (m >= M) continue;
+      const floatx4 a0 = *reinterpret_cast<const floatx4*>(tile + r * LDT + cg * VEC);
+      const floatx4 a1 = *reinterpret_cast<const floatx4*>(tile + r * LDT + cg * VEC + 4);
+      float xv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (x != nullptr) unpack8(cp.v[p], xv);
+      const float o[8] = {a0.x + xv[0], a0.y + xv[1], a0.z + xv[2], a0.w + xv[3],
+                          a1.x + xv[4], a1.y + xv[5], a1.z + xv[6], a1.w + xv[7]};
+      st8<T>(y + map(m) * N + n0 + cg * VEC, o);
     }
   }
 };
