@@ -69,20 +69,43 @@ template <typename T> struct EpiSwiGLUBwd {
   RowMap map = RowMap{};
   struct TilePre {};
   DM_DEV TilePre tile_prefetch(int, int) const { return TilePre{}; }
-  template <int TR, int BN, int LDT>
-  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre&, int) const {
+  // a chunk's a, b runs, loaded before the chunk before it is applied
+  static constexpr int MAXI = 8;   // items per thread and chunk
+  struct ChunkPre {
+    Raw8<T> a[MAXI], b[MAXI];
+  };
+  template <int TR, int BN> struct Shape {
+    static constexpr int IPR = BN / 8, NI = TR * IPR / 256;   // items of 8 hidden units per row
     static_assert(BN % MLP_GROUP == 0, "whole 32-unit groups");
-    constexpr int IPR = BN / 8;   // items of 8 hidden units per row
-#pragma unroll 1
-    for (int it = threadIdx.x; it < TR * IPR; it += 256) {
-      const int r = it / IPR, u = n0 + 8 * (it % IPR);
+    static_assert((TR * IPR) % 256 == 0 && NI <= MAXI, "whole items per thread");
+  };
+  DM_DEV long item_col(int u) const { return 2L * MLP_GROUP * (u / MLP_GROUP) + u % MLP_GROUP; }
+  template <int TR, int BN> DM_DEV ChunkPre chunk_prefetch(int m0, int n0) const {
+    using S = Shape<TR, BN>;
+    ChunkPre cp;
+#pragma unroll
+    for (int i = 0; i < S::NI; ++i) {
+      const int it = threadIdx.x + 256 * i, r = it / S::IPR, u = n0 + 8 * (it % S::IPR);
+      const T* p = ab + map(min(m0 + r, M - 1)) * 2 * H + item_col(u);
+      cp.a[i] = ld8_global(p);
+      cp.b[i] = ld8_global(p + MLP_GROUP);
+    }
+    return cp;
+  }
+  template <int TR, int BN, int LDT>
+  DM_DEV void tile_apply(const float* tile, int m0, int n0, const float*, const TilePre&, int,
+                         const ChunkPre& cp) const {
+    using S = Shape<TR, BN>;
+#pragma unroll
+    for (int i = 0; i < S::NI; ++i) {
+      const int it = threadIdx.x + 256 * i, r = it / S::IPR, u = n0 + 8 * (it % S::IPR);
       const int m = m0 + r;
       if (m >= M) continue;
       const long row = map(m);
-      const long col = 2L * MLP_GROUP * (u / MLP_GROUP) + u % MLP_GROUP;
+      const long col = item_col(u);
       float a[8], b[8], dm[8], da[8], db[8];
-      unpack8<T>(ld8_global(ab + row * 2 * H + col), a);
-      unpack8<T>(ld8_global(ab + row * 2 * H + col + MLP_GROUP), b);
+      unpack8<T>(cp.a[i], a);
+      unpack8<T>(cp.b[i], b);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         dm[i] = tile[r * LDT + (u - n0) + i];
