@@ -1724,6 +1724,8 @@ DM_DEV void rmsnorm_bwd_body(int M, int d, float eps, int residual, const T* __r
   extern __shared__ float acc_lds[];   // [4][d]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float* acc = acc_lds + (long)wave * d;
+  // each lane owns runs of 8 consecutive columns (16-byte loads of bf16; d is a multiple of 8)
+  constexpr int V = 8;
   for (int j = lane; j < d; j += 64) acc[j] = 0.f;
   const int r0 = blockIdx.x * RMSN_ROWS, r1 = min(r0 + RMSN_ROWS, M);
   for (int mi = r0 + wave; mi < r1; mi += 4) {
@@ -1731,22 +1733,44 @@ DM_DEV void rmsnorm_bwd_body(int M, int d, float eps, int residual, const T* __r
     const T* xr = x + m * d;
     const float* gr = dxhat + m * d;
     float ss = 0.f, dot = 0.f;
-    for (int j = lane; j < d; j += 64) {
-      const float xv = to_f(xr[j]);
-      ss += xv * xv;
-      dot += to_f(w[j]) * gr[j] * xv;
+    for (int j0 = lane * V; j0 < d; j0 += 64 * V) {
+      float xv[V], wv[V], gv[V];
+      unpack8<T>(ld8_global(xr + j0), xv);
+      unpack8<T>(ld8_global(w + j0), wv);
+      unpackf4(ld_global<floatx4>(gr + j0), gv);
+      unpackf4(ld_global<floatx4>(gr + j0 + 4), gv + 4);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        ss += xv[i] * xv[i];
+        dot += wv[i] * gv[i] * xv[i];
+      }
     }
     ss = wave_sum(ss);
     dot = wave_sum(dot);
     const float r = rsqrtf(ss / (float)d + eps);
     const float c3 = r * r * r / (float)d * dot;
-    for (int j = lane; j < d; j += 64) {
-      const float xv = to_f(xr[j]), g = gr[j];
-      if (flags & 1) {
-        const float yv = residual ? to_f(dy[m * d + j]) : 0.f;
-        dx[m * d + j] = from_f<T>(r * to_f(w[j]) * g - xv * c3 + yv);
+    for (int j0 = lane * V; j0 < d; j0 += 64 * V) {
+      float xv[V], wv[V], gv[V], yv[V], o[V];
+      unpack8<T>(ld8_global(xr + j0), xv);
+      unpack8<T>(ld8_global(w + j0), wv);
+      unpackf4(ld_global<floatx4>(gr + j0), gv);
+      unpackf4(ld_global<floatx4>(gr + j0 + 4), gv + 4);
+      if ((flags & 1) && residual) unpack8<T>(ld8_global(dy + m * d + j0), yv);
+      else
+#pragma unroll
+        for (int i = 0; i < V; ++i) yv[i] = 0.f;
+      float* ar = acc + j0;
+      floatx4 a0 = *reinterpret_cast<floatx4*>(ar), a1 = *reinterpret_cast<floatx4*>(ar + 4);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        o[i] = r * wv[i] * gv[i] - xv[i] * c3 + yv[i];
+        const float t = gv[i] * xv[i] * r;
+        if (i < 4) a0[i] += t;
+        else a1[i - 4] += t;
       }
-      acc[j] += g * xv * r;
+      *reinterpret_cast<floatx4*>(ar) = a0;
+      *reinterpret_cast<floatx4*>(ar + 4) = a1;
+      if (flags & 1) st8<T>(dx + m * d + j0, o);
     }
   }
   if (!(flags & 2)) return;
