@@ -601,6 +601,11 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     L.load()
+    t_start = time.time()
+
+    def note(what):   # progress on stderr (stdout carries the one JSON line)
+        print(f"[bench] {what} done at {time.time() - t_start:.0f} s", file=sys.stderr, flush=True)
+
     if args.copy_calibration:
         src = torch.ones(COPY_CAL_BYTES // 2, device=dev, dtype=torch.bfloat16)
         dst = torch.empty_like(src)
@@ -716,20 +721,28 @@ def main():
             "workload": wl.replace(mode, "exact recompute" if use_tape else "sweep states from the forward's HBM tape")}
     del cell, bufs, Kc, Vc, ocat, y, x, dx, dy, grads, tape
     torch.cuda.empty_cache()
+    note("headline")
     if not args.no_c4 and args.workload != "c4":
         out["c4"] = bench_c4_ladder(dev)
+        note("c4 ladder")
         if args.c4_trunk_layers > 0:
             out["c4"]["trunk"] = bench_c4_trunk(dev, n_layers=args.c4_trunk_layers)
+            note("c4 trunk")
         if args.c4_stack_layers > 0:
             out["c4"]["wavefront"] = bench_c4_wavefront(dev, n_layers=args.c4_stack_layers)
+            note("c4 wavefront")
     if not args.no_stack and args.workload != "c4":
         out["stack"] = bench_stack(dev, n_layers=args.stack_layers)
+        note("stack")
     if not args.no_graph_decode and args.workload != "c4":
         out["graph_decode"] = bench_graph_decode(dev)
+        note("graph decode")
     if not args.no_decode:
         out["decode"] = bench_decode(dev, args.decode_steps or None, with_cpu=not args.no_cpu_baseline)
+        note("decode")
     if not args.no_c1 and args.workload != "c4":
         out["c1"] = bench_c1(dev, with_cpu=not args.no_cpu_baseline)
+        note("c1")
     if not args.no_cpu_baseline and args.workload != "c4":
         out["cpu_baseline"] = cpu_baseline(cfg, sd, T, B, fwdbwd, args.cpu_T)
         if fwdbwd and "forward_only" in out:
