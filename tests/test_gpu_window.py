@@ -132,3 +132,68 @@ def test_windowed_stack_wavefront_equals_layer_by_layer(W):
     y2, dx2, _ = sts[1].step(x, dy)
     torch.cuda.synchronize()
     assert torch.equal(y1, y2) and torch.equal(dx1, dx2) and torch.equal(sts[0].flat, sts[1].flat)
+
+
+@pytest.mark.parametrize("W", [40, 150])
+def test_windowed_backward_340m_shape_bf16(W):
+    """bf16 storage at the 340M layer shape (d=1024, 16x64, c=64, K=4, T=256), forward tape,
+    windows shorter and longer than the cell: gradients and the forward against autograd through
+    the oracle's windowed chunked-Jacobi layer at the same K, run in fp32 torch on the GPU."""
+    from tests.test_gpu_backward import BF16_TOL
+    say(f"windowed bwd bf16 d=1024 T=256 K=4 W={W} vs fp32 oracle on the GPU")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    T = 256
+    cfg = cfg_of(d=1024, h=16, T=T, local_window=W)
+    B = 2
+    sd, x, _, (c32, s32) = setup(cfg, B, T)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(17), dtype=torch.float32)
+    sched = uniform_chunks(T, 64, 4)
+    _, dx, g, (K, V, ocat) = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.bfloat16, tape=True, full=True)
+    dx_ref, g_ref, (o_ref, K_ref, V_ref) = oracle_grads(
+        cfg, {k: v.float() for k, v in sd.items()}, x.float(), dy, c32, s32, sched, dtype=torch.float32,
+        device=DEV, with_forward=True)
+    fwd = {"o_cat": relerr(ocat, o_ref), "K": relerr(K, K_ref), "V": relerr(V, V_ref)}
+    record(f"window bf16 W={W} forward", fwd, BF16_TOL)
+    assert max(fwd.values()) < BF16_TOL, fwd
+    compare(f"window bwd bf16 W={W}", dx, g, dx_ref, g_ref, BF16_TOL)
+
+
+@pytest.mark.parametrize("W", [1, 30, 100])
+def test_windowed_head_dim_128_fp32(W):
+    """head_dim 128 (d=256, 2 heads), windows shorter and longer than the 64-row cell, K = 3:
+    forward against the oracle's windowed cells and gradients against autograd through it."""
+    say(f"windowed dh=128 fp32 W={W}")
+    T = 192
+    cfg = cfg_of(d=256, h=2, T=T, local_window=W)
+    assert cfg.head_dim == 128
+    B = 2
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    sched = uniform_chunks(T, 64, 3)
+    o, K, V = _layer(cfg, sd, x, c32, s32, sched, torch.float32)
+    o_ref, K_ref, V_ref = O.layer_forward(cfg, sd, x, c64, s64, sched)
+    errs = {"o": relerr(o, o_ref), "K": relerr(K, K_ref), "V": relerr(V, V_ref)}
+    record(f"window dh128 W={W} forward", errs, 1e-5)
+    assert max(errs.values()) < 1e-5, errs
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(19), dtype=torch.float64)
+    dx_ref, g_ref = oracle_grads(cfg, sd, x, dy, c64, s64, sched)
+    _, dx, grads = hip_grads(cfg, sd, x, dy, c32, s32, sched, torch.float32, tape=True)
+    compare(f"window bwd dh128 W={W}", dx, grads, dx_ref, g_ref, FP32_TOL)
+
+
+def test_window_one_equals_no_window_on_the_gpu():
+    """W = 1 is read as no window (attend_one's K_past[:, :, -0:] is the whole past): the layer at
+    W = 1 and at W = 0 give the same bits, and the decode step too."""
+    say("W=1 layer and decode == no window")
+    T, B = 128, 2
+    outs = []
+    for W in (0, 1):
+        cfg = cfg_of(T=T, local_window=W)
+        sd, x, _, (c32, s32) = setup(cfg, B, T)
+        o, K, V = _layer(cfg, sd, x, c32, s32, uniform_chunks(T, 64, 3), torch.float32)
+        tape = StaticTape(cfg, B, T, DEV, torch.float32, sd=to_dev(sd, torch.float32))
+        xd = x.float().to(DEV)
+        dec = torch.stack([tape.step(xd[:, t].contiguous(), t, c32, s32)[0].clone() for t in range(T)], 1)
+        torch.cuda.synchronize()
+        outs.append((o, K, V, dec))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
