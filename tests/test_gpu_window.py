@@ -197,3 +197,26 @@ def test_window_one_equals_no_window_on_the_gpu():
         outs.append((o, K, V, dec))
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("W", [20, 90])
+def test_windowed_module_autograd_matches_oracle(W):
+    """DualModAttention (reference signature) with local_window W, forward + loss.backward()
+    through the HIP path, against autograd through the oracle's windowed cells (W = 20 inside a
+    64-row chunk, W = 90 across chunks)."""
+    from dual_mod_public_amd.attention import DualModAttention
+    say(f"DualModAttention autograd fp32, W={W}")
+    T, B = 128, 2
+    cfg = cfg_of(T=T, local_window=W)
+    sd, x, (c64, s64), (c32, s32) = setup(cfg, B, T)
+    attn = DualModAttention(cfg).to(DEV)
+    attn.load_state_dict({k: v.float() for k, v in sd.items() if k != "attn_norm.weight"})
+    xd = x.float().to(DEV).requires_grad_(True)
+    dy = torch.randn(B, T, cfg.d_model, generator=torch.Generator().manual_seed(23), dtype=torch.float64)
+    y = attn(xd, c32.to(DEV), s32.to(DEV), n_sweeps=4)
+    (y * dy.float().to(DEV)).sum().backward()
+    torch.cuda.synchronize()
+    sched = uniform_chunks(T, attn.CHUNK, 4)
+    dx_ref, g_ref = oracle_grads(cfg, sd, x, dy, c64, s64, sched, normalize=False, residual=False)
+    got = {n: p.grad for n, p in attn.named_parameters()}
+    compare(f"module W={W}", xd.grad, got, dx_ref, g_ref, FP32_TOL, skip=("attn_norm.weight",))
