@@ -296,3 +296,25 @@ def test_mlp_sublayer_matches_oracle(dtype, tol, M):
     record(f"mlp sublayer {dtype} M={M}", errs, tol)
     for k, v in errs.items():
         assert v < tol, f"{k}: relerr {v:.3e}"
+
+
+@pytest.mark.parametrize("W", [10, 24])
+def test_windowed_trunk_step_matches_oracle_fp32(W):
+    """local_window W (inside a 16-row cell, and across cells) on every layer of the trunk step:
+    the loss and every gradient against autograd through the oracle's windowed fp64 LM, K = 4;
+    the layer-batched step equals the layer-by-layer one bit for bit."""
+    say(f"windowed trunk step fp32 vs oracle autograd, W={W}")
+    cfg = _cfg(local_window=W)
+    B, T = 2, 64
+    m, sd = _model(cfg, torch.float32)
+    sched = uniform_chunks(T, 16, 4)
+    tr = HipTrunk(m, B, T, schedule=sched)
+    idx, tg = _batch(cfg, B, T)
+    tr.train_step(idx.to(DEV), tg.to(DEV))
+    torch.cuda.synchronize()
+    loss_ref, g_ref = _oracle(cfg, sd, idx, tg, T, sched)
+    _compare(f"trunk fp32 W={W}", tr, loss_ref, g_ref, 1e-5)
+    wf = HipTrunk(m, B, T, schedule=sched, wavefront=True)
+    wf.train_step(idx.to(DEV), tg.to(DEV))
+    torch.cuda.synchronize()
+    assert _same(_snapshot(tr), _snapshot(wf))
