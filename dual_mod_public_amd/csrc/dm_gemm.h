@@ -479,17 +479,29 @@ DM_DEV void gemm_mainloop_dma(const SA& sa, const SB& sb, int K, int m0, int n0,
 // The direct-to-LDS k-loop for K-major operands (bf16, both operands K-major: the
 // weight-grad products C = A^T B summed over rows). A stage holds KS k-rows
 // (kk_stage_k) of the block's BM (then BN) columns, BM * 2 bytes per k-row, its 16-byte chunk c stored
-// at chunk c ^ (2 (k & 3)); one global_load_lds_dwordx4 per wave fills 1 KB (1024 /
+// at chunk c ^ kk_swz<BM * 2>(k); one global_load_lds_dwordx4 per wave fills 1 KB (1024 /
 // (BM * 2) k-rows). MFMA fragments (8 consecutive k of one column per lane) come
 // from two ds_read_b64_tr_b16 each: in a 16-lane group, lane s names the 8 bytes
 // at k-row 8g + s / 4 (+ 4), columns 4 (s % 4) .. + 3 of the fragment's 16 columns,
-// and receives that 4 x 16 block's column s; the swizzle puts the four k-rows'
-// chunks in different banks (also separating k-rows 8 apart measured slower).
+// and receives that 4 x 16 block's column s.
+//
+// The swizzle: LDS serves a ds_read_b64_tr_b16 in two passes of 32 lanes over 64 four-byte
+// banks (256 bytes), so the 32-byte column pieces of the 8 k-rows one pass names (8 g + 0..3
+// for g = 0, 1; then 2, 3) must fill the 256 bytes without overlap. k-rows of 256 bytes or more
+// all start at bank 0: the piece moves by 2 (k & 3) chunks within a 128-byte half and by 8
+// chunks (the other half) for k-rows 8 apart. 128-byte k-rows pair up in a 256-byte span (odd
+// k-rows in the upper half): the piece moves by 2 ((k >> 1) & 1) + 4 ((k >> 3) & 1). Measured on
+// gfx950 with SQ_LDS_BANK_CONFLICT: 2.0 conflict cycles per read with 2 (k & 3) alone, 0 with these.
+template <int ROW> DM_DEV int kk_swz(int kr) {
+  static_assert(ROW == 128 || ROW == 256 || ROW == 512, "k-row bytes");
+  if constexpr (ROW == 128) return 2 * ((kr >> 1) & 1) + 4 * ((kr >> 3) & 1);
+  else return (2 * (kr & 3)) ^ (8 * ((kr >> 3) & 1));
+}
 template <int ROW> DM_DEV bf16x8 frag_kmajor(const char* stage, int k0, int c0) {
   const int lane = threadIdx.x & 63, g = lane >> 4, s = lane & 15;
   const int kr = k0 + 8 * g + (s >> 2);
   const int col = c0 + 4 * (s & 3);
-  const char* p = stage + kr * ROW + ((((col >> 3) ^ (2 * (kr & 3))) << 4) | ((col & 7) << 1));
+  const char* p = stage + kr * ROW + ((((col >> 3) ^ kk_swz<ROW>(kr)) << 4) | ((col & 7) << 1));
   const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
   const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * ROW));
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -521,14 +533,14 @@ DM_DEV void gemm_mainloop_dma_kk(const SA& sa, const SB& sb, int K, int m0, int 
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
       const int r0 = (wave * LA + i) * RPA, r = r0 + lane / CPA;
-      const int c = (lane % CPA) ^ (2 * (r & 3));
+      const int c = (lane % CPA) ^ kk_swz<ROWA>(r);
       __builtin_amdgcn_global_load_lds((const void*)sa.ptr_k(k + r, m0 + 8 * c), (lds_void_t*)(base + r0 * ROWA),
                                        16, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < LB; ++i) {
       const int r0 = (wave * LB + i) * RPB, r = r0 + lane / CPB;
-      const int c = (lane % CPB) ^ (2 * (r & 3));
+      const int c = (lane % CPB) ^ kk_swz<ROWB>(r);
       __builtin_amdgcn_global_load_lds((const void*)sb.ptr_k(k + r, n0 + 8 * c),
                                        (lds_void_t*)(base + KS * ROWA + r0 * ROWB), 16, 0, 0);
     }
