@@ -156,9 +156,9 @@ def test_layer_grads_dh128_fp32(ctx_mod, tape):
     compare("fp32 dh128", dx, g, dx_ref, g_ref, FP32_GRAD_TOL)
 
 
-@pytest.mark.parametrize("k", [1, 4, 8])
+@pytest.mark.parametrize("k", [1, 2, 4, 8])
 def test_layer_grads_config4_shape_bf16(k):
-    """Config 4's layer shape (d=2048, 16 x 128), c=64, K=1 / 4 / 8, T=256, bf16 storage,
+    """Config 4's layer shape (d=2048, 16 x 128), c=64, the ladder's K = 1 / 2 / 4 / 8, T=256, bf16 storage,
     forward tape: gradients and the forward against autograd through the oracle's
     chunked-Jacobi layer at the same K, run in fp32 torch on the GPU."""
     say(f"bwd bf16 d=2048 16x128 T=256 c=64 K={k} vs fp32 oracle on the GPU")
