@@ -218,6 +218,16 @@ void run_refine(const dm_config* c, const dm_packed* w, const CellGeom& g, int N
     EpiSweep1<T, DH, 1, true> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
                                  Kout, Vout, out_stride, out_row0, vin, gvu, save1};
     launch_gemm_auto<T, 64, 64, 2, 2, SW1_STAGES, 4>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
+  } else if (sizeof(T) == 2 && DM_SW1_EIGHT_WAVES && launch_log() == nullptr) {
+    // bf16: 64 x 128 blocks of eight waves (each 256-thread half one 64-column group; d is a
+    // multiple of 128, so the direct-to-LDS k-loop always applies): the two column groups share
+    // the block's o rows, so a k-step moves 24 KB into a CU's LDS instead of the 32 KB of two
+    // 64 x 64 blocks, still with eight waves per CU; the same per-element k order
+    if constexpr (sizeof(T) == 2) {
+      EpiSweep1<T, DH, 2, false, true> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o,
+                                          normw, Kout, Vout, out_stride, out_row0, vin, gvu, save1};
+      launch_gemm<T, 64, 128, 2, 4, -SW1_STAGES>(sa, sb, N, 4 * c->d, c->d, e1, s, PROF_SWEEP1);
+    }
   } else {
     EpiSweep1<T, DH> e1{g, N, c->ctx_mod, c->mult_res_lambda, kraw, vraw, glogx, sig, cos, sin, o, normw,
                         Kout, Vout, out_stride, out_row0, vin, gvu, save1};

@@ -191,7 +191,7 @@ constexpr int gemm_lds_bytes() {
 // Wave tile geometry of a (BM, BN, WM, WN) block.
 template <int BM, int BN, int WM, int WN> struct WaveTile {
   static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
-  static_assert(WM * WN == 4, "4 waves per block");
+  static_assert(WM * WN == 4 || WM * WN == 8, "4 or 8 waves per block");
   static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be whole 16x16 MFMA tiles");
 };
 
@@ -204,6 +204,7 @@ DM_DEV void gemm_mainloop(const SA& sa, const SB& sb, int K, int m0, int n0, cha
   using Tr = GemmTraits<T>;
   using MF = Mfma<T>;
   using WT = WaveTile<BM, BN, WM, WN>;
+  static_assert(WM * WN == 4, "register-ring k-loop: 4 waves");
   constexpr int BK = Tr::BK, LDK = Tr::LDK, VEC = Tr::VEC;
   constexpr int FM = WT::FM, FN = WT::FN, TM = WT::TM, TN = WT::TN;
   constexpr int NA = BM * BK / VEC / 256, NB = BN * BK / VEC / 256;
@@ -368,7 +369,9 @@ DM_DEV void gemm_mainloop_dma(const SA& sa, const SB& sb, int K, int m0, int n0,
   using WT = WaveTile<BM, BN, WM, WN>;
   constexpr int FM = WT::FM, FN = WT::FN, TM = WT::TM, TN = WT::TN;
   constexpr int STAGE = (BM + BN) * 128;
-  constexpr int LA = BM / 32, LB = BN / 32, L = LA + LB;   // wave load instructions per tile
+  // wave load instructions per tile: each fills 8 rows of 128 bytes, the block's waves in turn
+  constexpr int NWV = WM * WN, LA = BM / (8 * NWV), LB = BN / (8 * NWV), L = LA + LB;
+  static_assert(LA >= 1 && LB >= 1 && LA * 8 * NWV == BM && LB * 8 * NWV == BN, "whole 8-row loads per wave");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;   // rows of an 8-row group start at multiples of 8
@@ -516,6 +519,7 @@ DM_DEV void gemm_mainloop_dma_kk(const SA& sa, const SB& sb, int K, int m0, int 
                 "stages / tile columns");
   using MF = Mfma<T>;
   using WT = WaveTile<BM, BN, WM, WN>;
+  static_assert(WM * WN == 4, "K-major k-loop: 4 waves");
   constexpr int FM = WT::FM, FN = WT::FN, TM = WT::TM, TN = WT::TN;
   constexpr int KS = kk_stage_k<BM, BN, S>();             // k-rows per stage
   constexpr int ROWA = BM * 2, ROWB = BN * 2;              // bytes per k-row
@@ -739,7 +743,7 @@ DM_DEV void gemm_block(const SA& sa, const SB& sb, int K, const EPI& epi, int bx
 }
 
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
-__global__ __launch_bounds__(256) void k_gemm(SA sa, SB sb, int K, EPI epi, uint64_t* prof_ts) {
+__global__ __launch_bounds__(64 * WM * WN) void k_gemm(SA sa, SB sb, int K, EPI epi, uint64_t* prof_ts) {
   const uint64_t t0 = prof_begin(prof_ts);
   // Blocks are dispatched round-robin over the 8 XCDs (each with its own L2). For
   // the K-major (weight-grad) products every XCD gets a contiguous range of tiles

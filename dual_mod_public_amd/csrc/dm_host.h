@@ -49,6 +49,9 @@ namespace dm {
 #ifndef DM_GROUPED_WIDE_SW1
 #define DM_GROUPED_WIDE_SW1 1  // layer-batched sweep GEMM 1 in 64 x 128 tiles
 #endif
+#ifndef DM_SW1_EIGHT_WAVES
+#define DM_SW1_EIGHT_WAVES 1   // sweep GEMM 1 in 64 x 128 blocks of eight waves (one column group per half)
+#endif
 #ifndef DM_KK_STAGES
 #define DM_KK_STAGES 2
 #endif
@@ -271,19 +274,22 @@ inline int log2_exact(int v) {
   return (1 << l) == v ? l : -1;
 }
 
-// GEMM launch: grid (N/BN, ceil(M/BM)), 256 threads
+// GEMM launch: grid (N/BN, ceil(M/BM)), 64 WM WN threads (grouped-launch bodies: 4 waves only)
 template <typename T, int BM, int BN, int WM, int WN, int D, class SA, class SB, class EPI>
 void launch_gemm(const SA& sa, const SB& sb, int M, int N, int K, const EPI& epi, hipStream_t s,
                  int prof_cls = PROF_NONE) {
   dim3 grid(N / BN, cdiv(M, BM));
-  if (launch_log() != nullptr) {
-    using Body = GemmBody<T, BM, BN, WM, WN, D, SA, SB, EPI>;
-    record_launch<Body>(grid, dim3(256), typename Body::Args{sa, sb, K, epi});
-    return;
+  if constexpr (WM * WN == 4) {
+    if (launch_log() != nullptr) {
+      using Body = GemmBody<T, BM, BN, WM, WN, D, SA, SB, EPI>;
+      record_launch<Body>(grid, dim3(256), typename Body::Args{sa, sb, K, epi});
+      return;
+    }
   }
   uint64_t* ts;
   const int idx = prof_launch_begin(prof_cls, true, ts);
-  launch_timed(idx, k_gemm<T, BM, BN, WM, WN, D, SA, SB, EPI>, grid, dim3(256), 0, s, sa, sb, K, epi, ts);
+  launch_timed(idx, k_gemm<T, BM, BN, WM, WN, D, SA, SB, EPI>, grid, dim3(64 * WM * WN), 0, s, sa, sb, K, epi,
+               ts);
 }
 
 // bf16 with K-contiguous operands and K a multiple of 64: the direct-to-LDS k-loop

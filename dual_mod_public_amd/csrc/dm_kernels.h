@@ -888,7 +888,7 @@ template <typename T, int DH, int NW> struct AttendBody {
 //          [3d, 4d) g_v(u)   -> scratch for GEMM 2 (storage dtype, as the GEMM's raw outputs)
 // save != nullptr stores the raw GEMM outputs [rows, 4d] in this packed order.
 // ---------------------------------------------------------------------------
-template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 {
+template <typename T, int DH, int NG = 1, bool DEVPOS = false, bool SPLIT = false> struct EpiSweep1 {
   CellGeom g;
   int M, ctx_mod;
   float lam;
@@ -911,6 +911,13 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
   // column quad lc0 = 4 (t % 4) .. + 3 of each group's four 16-column sections, so its global
   // inputs and outputs are runs of 4 consecutive elements. With up to two groups the inputs
   // are gathered during the k-loop's last stage; with more, at the start of the epilogue.
+  // SPLIT: a 512-thread block of two groups (eight waves), each 256-thread half owning one
+  // group (threads t and t + 256 the same row and quad); no per-head norms.
+  static_assert(!SPLIT || NG == 2, "split: two groups, one per 256-thread half");
+  static constexpr int NGT = SPLIT ? 1 : NG;   // groups per thread
+  DM_DEV static int trow() { return (SPLIT ? (int)(threadIdx.x & 255) : (int)threadIdx.x) >> 2; }
+  DM_DEV static int tquad() { return threadIdx.x & 3; }
+  DM_DEV static int tgroup() { return SPLIT ? (int)(threadIdx.x >> 8) : 0; }
   struct GroupPre {
     typename Raw4<T>::type x[4];    // K: gx_a, gx_b; linear V: gx x2; v_map: sig x4 (storage dtype)
     floatx4 f[2];                   // K: cos, sin
@@ -918,20 +925,21 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
   };
   static constexpr bool LATE = NG <= 2;
   struct TilePre {
-    GroupPre p[LATE ? NG : 1];
+    GroupPre p[LATE ? NGT : 1];
   };
-  // tile_prefetch issues exactly 14 loads per group (one per x / f / h slot, unconditionally)
-  static constexpr int LATE_GATHERS = LATE ? 14 * NG : 0;
+  // tile_prefetch issues exactly 14 loads per group of the thread (one per x / f / h slot,
+  // unconditionally)
+  static constexpr int LATE_GATHERS = LATE ? 14 * NGT : 0;
   DM_DEV TilePre tile_prefetch(int m0, int n0) const {
     TilePre pr{};
     if constexpr (LATE) {
 #pragma unroll
-      for (int gi = 0; gi < NG; ++gi) pr.p[gi] = group_prefetch(m0, n0 + 64 * gi);
+      for (int gi = 0; gi < NGT; ++gi) pr.p[gi] = group_prefetch(m0, n0 + 64 * (gi + tgroup()));
     }
     return pr;
   }
   DM_DEV GroupPre group_prefetch(int m0, int n0) const {
-    const int r = threadIdx.x >> 2, lc0 = 4 * (threadIdx.x & 3);
+    const int r = trow(), lc0 = 4 * tquad();
     const int d = g.d, h = g.h;
     const int m = min(m0 + r, M - 1);
     const int b = m / g.c, p = m - b * g.c;
@@ -994,9 +1002,11 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
   template <int BM, int BN, int LDT>
   DM_DEV void tile_apply(const float* tile, int m0, int n0, const float* rs, const TilePre& pr, int) const {
     static_assert(BM == 64 && BN == 64 * NG, "sweep GEMM 1 block tile is NG 64 x 64 column groups");
-    const float sc = rs[threadIdx.x >> 2];
+    const float sc = rs[trow()];
     if constexpr (NG == 1) {
       group_apply<LDT>(tile, m0, n0, sc, pr.p[0], false, 0.f, 0.f);
+    } else if constexpr (SPLIT) {
+      group_apply<LDT>(tile + 64 * tgroup(), m0, n0 + 64 * tgroup(), sc, pr.p[0], false, 0.f, 0.f);
     } else {
       GroupPre pg[NG];
 #pragma unroll
@@ -1007,7 +1017,7 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
       // The block's NG groups are one head's k_ctx / g_k(u) (or linear v_ctx / g_v(u)) columns:
       // the head's norm scale r * gain from sections 0 and 1 of every group (the k_ctx, v_ctx
       // columns), over the row's 4 threads.
-      const int r = threadIdx.x >> 2, lc0 = 4 * (threadIdx.x & 3);
+      const int r = trow(), lc0 = 4 * tquad();
       const int d = g.d;
       const float* gain = nullptr;
       int hd = 0;
@@ -1041,7 +1051,7 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
   template <int LDT>
   DM_DEV void group_apply(const float* tile, int m0, int n0, float sc, const GroupPre& pr, bool nrm, float nr,
                           float ng) const {
-    const int r = threadIdx.x >> 2, lc0 = 4 * (threadIdx.x & 3);
+    const int r = trow(), lc0 = 4 * tquad();
     const int d = g.d, h = g.h;
     const int m = m0 + r;
     // the GEMM ran on o with norm_ctx.weight folded into W: u . W^T = rs * acc
@@ -1054,7 +1064,7 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
     // raw outputs for the tape: this thread's 16 consecutive columns of row r
     float sv[16];
     if (save != nullptr) {
-      const int cs0 = 16 * (threadIdx.x & 3);
+      const int cs0 = 16 * tquad();
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const floatx4 v = *reinterpret_cast<const floatx4*>(tile + r * LDT + cs0 + 4 * k);
@@ -1075,7 +1085,7 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
       unpack4<T>(pr.x[0], gxa); unpack4<T>(pr.x[1], gxb); unpackf4(pr.f[0], cs); unpackf4(pr.f[1], sn);
       unpack4<T>(pr.h[0], ka); unpack4<T>(pr.h[1], kb);
       settle(gxa); settle(gxb); settle(cs); settle(sn); settle(ka); settle(kb);   // all loads before any store
-      if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
+      if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * tquad(), sv);
       const int hd = n0 / (2 * DH), jj = 16 * ((n0 % (2 * DH)) / 64) + lc0;
       float o1[4], o2[4];
 #pragma unroll
@@ -1094,7 +1104,7 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
       float gx[2][4], vr[2][4];
 #pragma unroll
       for (int j = 0; j < 2; ++j) { unpack4<T>(pr.x[j], gx[j]); unpack4<T>(pr.h[j], vr[j]); settle(gx[j]); settle(vr[j]); }
-      if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
+      if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * tquad(), sv);
       const int cl = n0 - 2 * d;
       const int hd = cl / (2 * DH), e = 32 * ((cl % (2 * DH)) / 64) + lc0;
       T* crow = Vout + ((long)b * h + hd) * out_stride + (long)(orow0 + p) * DH + e;
@@ -1116,7 +1126,7 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
           unpack4<T>(pr.h[k], ov[k]); unpack4<T>(pr.h[4 + k], nw[k]); settle(ov[k]); settle(nw[k]);
         }
       }
-      if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
+      if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * tquad(), sv);
       const int c0 = n0 - 2 * d + lc0;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -1134,7 +1144,7 @@ template <typename T, int DH, int NG = 1, bool DEVPOS = false> struct EpiSweep1 
         st4<T>(vin + (long)m * d + c0 + 16 * k, v);
       }
     } else {
-      if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * (threadIdx.x & 3), sv);
+      if (save != nullptr) store_vec_nt<T, 16>(save + (long)m * 4 * d + n0 + 16 * tquad(), sv);
       const int c0 = n0 - 3 * d + lc0;
 #pragma unroll
       for (int k = 0; k < 4; ++k) st4<T>(gvu + (long)m * d + c0 + 16 * k, a[k]);
